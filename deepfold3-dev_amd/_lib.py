@@ -1,0 +1,110 @@
+"""ctypes binding of ``libpairformer_hip.so`` (the C ABI declared in include/pairformer_hip.h).
+
+The library is built in-tree by ``__graft_entry__.build()`` (``make -C
+deepfold3-dev_amd/csrc``). There is no fallback: if the library is missing or a
+call fails, this raises. Tensors cross the boundary as raw device pointers;
+the stream is torch's current HIP stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import torch
+
+from .inference_guard import NotActive
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpairformer_hip.so")
+HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "pairformer_hip.h")
+
+PF_F32 = 0
+PF_BF16 = 1
+
+_vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/pairformer_hip.h.
+SIGNATURES: dict[str, tuple] = {
+    "pf_version": (_i, []),
+    "pf_last_error": (ctypes.c_char_p, []),
+    "pf_last_error_code": (_i, []),
+    "pf_cast": (_i, [_vp, _i, _vp, _i, _sz, _vp]),
+    "pf_add": (_i, [_vp, _i, _vp, _i, _vp, _sz, _vp]),
+    "pf_layernorm_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, ctypes.c_long, _i, _vp]),
+    "pf_ln_transpose_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, _i, _i, _i, _i, _vp]),
+    "pf_trimul_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "pf_trimul_pack_weights": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp]),
+    "pf_trimul_fwd": (
+        _i,
+        [_vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
+    ),
+}
+
+_lib = None
+
+
+class PFError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        self.fn, self.code = fn, code
+        super().__init__(f"{fn} failed with status {code}: {msg}")
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises NotActive if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise NotActive("pairformer_hip", f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/pairformer_hip.h."""
+    with open(HEADER_PATH) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pf_[a-z0-9_]+)\s*\(", text)))
+
+
+def call(name: str, *args) -> int:
+    """Call ``name`` and raise PFError on a non-zero status."""
+    fn = getattr(lib(), name)
+    status = fn(*args)
+    if status != 0:
+        msg = lib().pf_last_error()
+        raise PFError(name, status, msg.decode() if msg else "")
+    return status
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return PF_F32
+    if dt == torch.bfloat16:
+        return PF_BF16
+    raise NotActive("pairformer_hip", f"dtype {dt} is not supported (fp32 or bf16 only)")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_device(name: str, *ts: torch.Tensor) -> None:
+    """Refuse (NotActive) unless every tensor is on a HIP device; there is no CPU path."""
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise NotActive(name, "tensors must be on a ROCm GPU; this build has no CPU path")

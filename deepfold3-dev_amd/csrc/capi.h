@@ -1,0 +1,37 @@
+// Host-side helpers shared by the C-ABI entry points: status codes, the
+// thread-local last-error message, and argument checks. No C++ exception ever
+// crosses the ABI: every entry point returns a PF_* status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/pairformer_hip.h"
+
+namespace pf {
+
+void set_error(int code, const char* fmt, ...);
+int ok();
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Returns PF_OK or records a launch error.
+int check_launch(const char* what);
+
+inline size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+// Token padding used by the pair-plane and attention buffers.
+inline int pad128(int n) { return (int)round_up((size_t)n, 128); }
+
+}  // namespace pf
+
+#define PF_REQUIRE(cond, code, ...)          \
+  do {                                       \
+    if (!(cond)) {                           \
+      pf::set_error((code), __VA_ARGS__);    \
+      return (code);                         \
+    }                                        \
+  } while (0)

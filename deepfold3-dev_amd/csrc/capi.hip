@@ -1,0 +1,100 @@
+// Library-wide C-ABI entry points: errors, version, dtype casts and the
+// elementwise residual add (the eval-mode dropout-add).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "capi.h"
+#include "common.h"
+
+namespace pf {
+
+static thread_local char g_err[512] = "";
+static thread_local int g_err_code = 0;
+
+void set_error(int code, const char* fmt, ...) {
+  g_err_code = code;
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int ok() {
+  g_err_code = 0;
+  g_err[0] = '\0';
+  return PF_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error(PF_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return PF_ERR_LAUNCH;
+  }
+  return ok();
+}
+
+}  // namespace pf
+
+template <class TS, class TD>
+__global__ void cast_kernel(const TS* __restrict__ src, TD* __restrict__ dst, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = from_f32<TD>(to_f32(src[i]));
+}
+
+// out[i] = res[i] + x[i], in the dtype of res (x may be another dtype).
+template <class TR, class TX>
+__global__ void add_kernel(const TR* __restrict__ res, const TX* __restrict__ x, TR* __restrict__ out, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    out[i] = from_f32<TR>(to_f32(res[i]) + to_f32(x[i]));
+}
+
+static unsigned grid_for(size_t n) {
+  size_t g = (n + 255) / 256;
+  return (unsigned)(g > 65536 ? 65536 : (g == 0 ? 1 : g));
+}
+
+extern "C" {
+
+const char* pf_last_error(void) { return pf::g_err; }
+int pf_last_error_code(void) { return pf::g_err_code; }
+int pf_version(void) { return PF_ABI_VERSION; }
+
+int pf_cast(const void* src, int src_dtype, void* dst, int dst_dtype, size_t n, void* stream) {
+  PF_REQUIRE(src && dst, PF_ERR_INVALID_ARG, "pf_cast: null pointer");
+  PF_REQUIRE((src_dtype == PF_F32 || src_dtype == PF_BF16) && (dst_dtype == PF_F32 || dst_dtype == PF_BF16),
+             PF_ERR_UNSUPPORTED, "pf_cast: dtype codes must be PF_F32 or PF_BF16");
+  if (n == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  unsigned g = grid_for(n);
+  if (src_dtype == PF_F32 && dst_dtype == PF_F32)
+    cast_kernel<float, float><<<g, 256, 0, s>>>((const float*)src, (float*)dst, n);
+  else if (src_dtype == PF_F32)
+    cast_kernel<float, bf16><<<g, 256, 0, s>>>((const float*)src, (bf16*)dst, n);
+  else if (dst_dtype == PF_F32)
+    cast_kernel<bf16, float><<<g, 256, 0, s>>>((const bf16*)src, (float*)dst, n);
+  else
+    cast_kernel<bf16, bf16><<<g, 256, 0, s>>>((const bf16*)src, (bf16*)dst, n);
+  return pf::check_launch("pf_cast");
+}
+
+int pf_add(const void* res, int res_dtype, const void* x, int x_dtype, void* out, size_t n, void* stream) {
+  PF_REQUIRE(res && x && out, PF_ERR_INVALID_ARG, "pf_add: null pointer");
+  PF_REQUIRE((res_dtype == PF_F32 || res_dtype == PF_BF16) && (x_dtype == PF_F32 || x_dtype == PF_BF16),
+             PF_ERR_UNSUPPORTED, "pf_add: dtype codes must be PF_F32 or PF_BF16");
+  if (n == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  unsigned g = grid_for(n);
+  if (res_dtype == PF_F32 && x_dtype == PF_F32)
+    add_kernel<float, float><<<g, 256, 0, s>>>((const float*)res, (const float*)x, (float*)out, n);
+  else if (res_dtype == PF_F32)
+    add_kernel<float, bf16><<<g, 256, 0, s>>>((const float*)res, (const bf16*)x, (float*)out, n);
+  else if (x_dtype == PF_F32)
+    add_kernel<bf16, float><<<g, 256, 0, s>>>((const bf16*)res, (const float*)x, (bf16*)out, n);
+  else
+    add_kernel<bf16, bf16><<<g, 256, 0, s>>>((const bf16*)res, (const bf16*)x, (bf16*)out, n);
+  return pf::check_launch("pf_add");
+}
+
+}  // extern "C"

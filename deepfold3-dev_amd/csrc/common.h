@@ -1,0 +1,299 @@
+// Shared device helpers for the PairFormer HIP kernels (gfx950 / CDNA4 only).
+//
+// Element types: activations are float or __bf16 ("TZ"); GEMM operands are
+// float or __bf16 ("TC"). bf16 operands run on v_mfma_f32_16x16x32_bf16 /
+// v_mfma_f32_32x32x16_bf16, fp32 operands on v_mfma_f32_16x16x4f32 /
+// v_mfma_f32_32x32x2f32; all accumulate in fp32.
+//
+// Fragment convention: every lane owns 16 bytes of an operand (8 bf16 or
+// 4 fp32). For the 16x16 tiles, lane l holds row/column (l & 15) and the KPL
+// consecutive k values starting at (l >> 4) * KPL; for the 32x32 tiles, row
+// (l & 31) and k from (l >> 5) * KPL. An fp32 fragment of 4 values feeds four
+// k=4 (or k=2) MFMAs, one per element, so the k order inside a fragment is a
+// permutation of the textbook one; A and B are always loaded with the same
+// convention, so the contraction is unchanged.
+//
+// Accumulator layout (CDNA): 16x16 -> lane l holds column (l & 15), rows
+// 4*(l>>4) + r, r = 0..3. 32x32 -> lane l holds column (l & 31), rows
+// 8*(r>>2) + 4*(l>>5) + (r&3), r = 0..15.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+#define PF_DEVICE __device__ __forceinline__
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------- conversions
+PF_DEVICE float to_f32(float x) { return x; }
+PF_DEVICE float to_f32(bf16 x) { return (float)x; }
+template <class T>
+PF_DEVICE T from_f32(float x);
+template <>
+PF_DEVICE float from_f32<float>(float x) { return x; }
+template <>
+PF_DEVICE bf16 from_f32<bf16>(float x) { return (bf16)x; }
+
+// 16-byte vector of T as an array of floats.
+template <class T>
+struct Vec16 {
+  static constexpr int N = 16 / sizeof(T);
+};
+
+template <class T>
+PF_DEVICE void load16(const T* p, float (&out)[16 / sizeof(T)]);
+template <>
+PF_DEVICE void load16<float>(const float* p, float (&out)[4]) {
+  f32x4 v = *reinterpret_cast<const f32x4*>(p);
+  out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+}
+template <>
+PF_DEVICE void load16<bf16>(const bf16* p, float (&out)[8]) {
+  bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = (float)v[e];
+}
+
+// Store VEC floats (VEC * sizeof(T) bytes: 4, 8 or 16) as T.
+template <class T, int VEC>
+PF_DEVICE void store_vec(T* p, const float* v) {
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) p[e] = from_f32<T>(v[e]);
+}
+template <>
+PF_DEVICE void store_vec<bf16, 8>(bf16* p, const float* v) {
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
+  *reinterpret_cast<bf16x8*>(p) = o;
+}
+template <>
+PF_DEVICE void store_vec<bf16, 4>(bf16* p, const float* v) {
+  bf16x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = (bf16)v[e];
+  *reinterpret_cast<bf16x4*>(p) = o;
+}
+template <>
+PF_DEVICE void store_vec<float, 4>(float* p, const float* v) {
+  f32x4 o = {v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<f32x4*>(p) = o;
+}
+
+// ---------------------------------------------------------------- math
+PF_DEVICE float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+PF_DEVICE float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+PF_DEVICE float sigmoidf_(float x) { return fast_rcp(1.0f + fast_exp(-x)); }
+PF_DEVICE float siluf_(float x) { return x * sigmoidf_(x); }
+
+// Sum over aligned groups of W lanes (W a power of two <= 64).
+template <int W>
+PF_DEVICE float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int W>
+PF_DEVICE float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+PF_DEVICE int lane_id() { return threadIdx.x & 63; }
+PF_DEVICE int wave_id() { return threadIdx.x >> 6; }
+
+// ---------------------------------------------------------------- MFMA
+template <class TC>
+struct Mfma;
+
+template <>
+struct Mfma<bf16> {
+  using Frag = bf16x8;
+  static constexpr int KPL = 8;        // k values per lane per fragment
+  static constexpr int K16 = 32;       // k covered by one 16x16 fragment step
+  static constexpr int K32 = 16;       // k covered by one 32x32 fragment step
+  PF_DEVICE static void mma16(f32x4& acc, const Frag& a, const Frag& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
+  PF_DEVICE static void mma32(f32x16& acc, const Frag& a, const Frag& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+  }
+  PF_DEVICE static Frag load(const bf16* p) { return *reinterpret_cast<const Frag*>(p); }
+  PF_DEVICE static Frag from_floats(const float* v) {
+    Frag f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (bf16)v[e];
+    return f;
+  }
+};
+
+template <>
+struct Mfma<float> {
+  using Frag = f32x4;
+  static constexpr int KPL = 4;
+  static constexpr int K16 = 16;
+  static constexpr int K32 = 8;
+  PF_DEVICE static void mma16(f32x4& acc, const Frag& a, const Frag& b) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc, 0, 0, 0);
+  }
+  PF_DEVICE static void mma32(f32x16& acc, const Frag& a, const Frag& b) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], b[e], acc, 0, 0, 0);
+  }
+  PF_DEVICE static Frag load(const float* p) { return *reinterpret_cast<const Frag*>(p); }
+  PF_DEVICE static Frag from_floats(const float* v) {
+    Frag f = {v[0], v[1], v[2], v[3]};
+    return f;
+  }
+};
+
+// Row padding (elements) for LDS operand tiles: 16 bytes.
+template <class T>
+constexpr int lds_pad() { return 16 / sizeof(T); }
+
+// acc[rb][cb] += A[rb*16 .. +16][0..K) * W[wrow(cb) .. +16][0..K)^T
+// A: LDS tile, row stride lda (elements). W: global weight rows, k contiguous,
+// row stride ldw; col block cb starts at weight row wrow0[cb].
+template <class TC, int K, int RB, int CB>
+PF_DEVICE void gemm16_lds_x_w(f32x4 (&acc)[RB][CB], const TC* A, int lda, int arow0, const TC* W, int ldw,
+                              const int (&wrow0)[CB]) {
+  using M = Mfma<TC>;
+  const int l = lane_id();
+  const int r = l & 15;
+  const int kq = (l >> 4) * M::KPL;
+#pragma unroll 2
+  for (int k0 = 0; k0 < K; k0 += M::K16) {
+    typename M::Frag bf[CB];
+#pragma unroll
+    for (int c = 0; c < CB; ++c) bf[c] = M::load(W + (size_t)(wrow0[c] + r) * ldw + k0 + kq);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      typename M::Frag af = M::load(A + (arow0 + rb * 16 + r) * lda + k0 + kq);
+#pragma unroll
+      for (int c = 0; c < CB; ++c) M::mma16(acc[rb][c], af, bf[c]);
+    }
+  }
+}
+
+template <int RB, int CB>
+PF_DEVICE void zero_acc(f32x4 (&acc)[RB][CB]) {
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// ---------------------------------------------------------------- LayerNorm tile
+// LayerNorm BM positions of C channels each and write them (as TC) into an LDS
+// tile lds[p * lda + c]. rowptr(p) returns the position's first element, or
+// nullptr for a padding position (written as zeros). Statistics are fp32 and
+// two-pass (mean, then mean of squared deviations), eps inside the rsqrt, as
+// torch.nn.functional.layer_norm. NT threads take part.
+template <class TZ, class TC, int C, int BM, int NT, class RowFn>
+PF_DEVICE void ln_tile_to_lds(RowFn rowptr, const float* __restrict__ w, const float* __restrict__ b, float eps,
+                              TC* lds, int lda) {
+  constexpr int VEC = 16 / sizeof(TZ);
+  constexpr int LPP = C / VEC;  // lanes per position
+  static_assert(C % VEC == 0 && 64 % LPP == 0, "channel count must tile a wave");
+  constexpr int PPI = NT / LPP;
+  static_assert(BM % PPI == 0, "tile rows must be a multiple of positions per pass");
+  const int tid = threadIdx.x;
+  const int sub = tid % LPP;
+  const int pp = tid / LPP;
+  float wv[VEC], bv[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    wv[e] = w[sub * VEC + e];
+    bv[e] = b[sub * VEC + e];
+  }
+#pragma unroll
+  for (int p0 = 0; p0 < BM; p0 += PPI) {
+    const int p = p0 + pp;
+    const TZ* src = rowptr(p);
+    float x[VEC];
+    if (src) {
+      load16<TZ>(src + sub * VEC, x);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = 0.f;
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) s += x[e];
+    const float mean = group_sum<LPP>(s) * (1.0f / C);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float d = x[e] - mean;
+      q += d * d;
+    }
+    const float rstd = rsqrtf(group_sum<LPP>(q) * (1.0f / C) + eps);
+    float y[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) y[e] = src ? (x[e] - mean) * rstd * wv[e] + bv[e] : 0.f;
+    store_vec<TC, VEC>(lds + p * lda + sub * VEC, y);
+  }
+}
+
+// Copy BM rows of C TZ elements into an LDS tile as TC without normalising.
+template <class TZ, class TC, int C, int BM, int NT, class RowFn>
+PF_DEVICE void copy_tile_to_lds(RowFn rowptr, TC* lds, int lda) {
+  constexpr int VEC = 16 / sizeof(TZ);
+  constexpr int LPP = C / VEC;
+  constexpr int PPI = NT / LPP;
+  const int tid = threadIdx.x;
+  const int sub = tid % LPP;
+  const int pp = tid / LPP;
+#pragma unroll
+  for (int p0 = 0; p0 < BM; p0 += PPI) {
+    const int p = p0 + pp;
+    const TZ* src = rowptr(p);
+    float x[VEC];
+    if (src) {
+      load16<TZ>(src + sub * VEC, x);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = 0.f;
+    }
+    store_vec<TC, VEC>(lds + p * lda + sub * VEC, x);
+  }
+}
+
+// dst(p)[c] = (accumulate ? dst(p)[c] : 0) + stage[p * lds_ld + c] for BM positions of
+// C channels; stage holds fp32. rowptr(p) returns nullptr for positions to skip.
+template <class TZ, int C, int BM, int NT, class RowFn>
+PF_DEVICE void store_tile_from_lds(RowFn rowptr, const float* stage, int lds_ld, bool accumulate) {
+  constexpr int VEC = 16 / sizeof(TZ);
+  constexpr int LPP = C / VEC;
+  constexpr int PPI = NT / LPP;
+  const int tid = threadIdx.x;
+  const int sub = tid % LPP;
+  const int pp = tid / LPP;
+#pragma unroll
+  for (int p0 = 0; p0 < BM; p0 += PPI) {
+    const int p = p0 + pp;
+    TZ* dst = const_cast<TZ*>(rowptr(p));
+    if (!dst) continue;
+    float x[VEC];
+    if (accumulate) {
+      load16<TZ>(dst + sub * VEC, x);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) x[e] += stage[p * lds_ld + sub * VEC + e];
+    store_vec<TZ, VEC>(dst + sub * VEC, x);
+  }
+}

@@ -1,0 +1,127 @@
+// Row LayerNorm and LayerNorm + transpose (HBM-bound).
+//
+//   pf_layernorm_fwd:    out[r] = LN(x[r]) over the last dim; fp32 statistics, output in
+//                        x's dtype (reference layer_norm, src/deepfold3/model/primitives.py:90-115).
+//   pf_ln_transpose_fwd: x [B,N1,N2,C] -> out [B,N2,N1,C] = LN(x).permute(0,2,1,3)
+//                        (reference FusedLayerNormTranspose, triton/layernorm_transpose.py:269-316).
+//
+// One wave per row; each lane owns C/128 chunks of two channels, so every load
+// instruction of a wave reads one 256-byte (bf16) or 512-byte (fp32) contiguous run.
+#include "capi.h"
+#include "common.h"
+
+namespace {
+
+template <class T>
+struct Pair;
+template <>
+struct Pair<float> {
+  using V = __attribute__((__vector_size__(2 * sizeof(float)))) float;
+};
+template <>
+struct Pair<bf16> {
+  using V = __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16;
+};
+
+// rows_per_wave rows per wave, each row C channels (C % 128 == 0).
+template <class T, int C>
+__global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* __restrict__ x, const float* __restrict__ w,
+                                                             const float* __restrict__ b, float eps,
+                                                             T* __restrict__ out, long M, int N1, int N2,
+                                                             int transpose) {
+  using V2 = typename Pair<T>::V;
+  constexpr int CH = C / 128;  // two-channel chunks per lane
+  const int l = lane_id();
+  const long row = (long)blockIdx.x * 4 + wave_id();
+  if (row >= M) return;
+  const T* src = x + row * C;
+  float v[CH][2];
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    V2 p = *reinterpret_cast<const V2*>(src + c * 128 + 2 * l);
+    v[c][0] = to_f32(p[0]);
+    v[c][1] = to_f32(p[1]);
+    s += v[c][0] + v[c][1];
+  }
+  const float mean = group_sum<64>(s) * (1.0f / C);
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const float d0 = v[c][0] - mean, d1 = v[c][1] - mean;
+    q += d0 * d0 + d1 * d1;
+  }
+  const float rstd = rsqrtf(group_sum<64>(q) * (1.0f / C) + eps);
+  long orow = row;
+  if (transpose) {
+    // row = (bb * N1 + i) * N2 + j  ->  (bb * N2 + j) * N1 + i
+    const long j = row % N2;
+    const long t = row / N2;
+    const long i = t % N1;
+    const long bb = t / N1;
+    orow = (bb * N2 + j) * N1 + i;
+  }
+  T* dst = out + orow * C;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = c * 128 + 2 * l;
+    V2 o;
+    o[0] = from_f32<T>((v[c][0] - mean) * rstd * w[ch] + b[ch]);
+    o[1] = from_f32<T>((v[c][1] - mean) * rstd * w[ch + 1] + b[ch + 1]);
+    *reinterpret_cast<V2*>(dst + ch) = o;
+  }
+}
+
+template <class T>
+int ln_dispatch(const void* x, const float* w, const float* b, float eps, void* out, long M, int C, int N1, int N2,
+                int transpose, hipStream_t s) {
+  dim3 grid((unsigned)((M + 3) / 4));
+  switch (C) {
+    case 128:
+      layernorm_rows_kernel<T, 128><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
+      break;
+    case 256:
+      layernorm_rows_kernel<T, 256><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
+      break;
+    case 384:
+      layernorm_rows_kernel<T, 384><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
+      break;
+    case 512:
+      layernorm_rows_kernel<T, 512><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
+      break;
+    default:
+      pf::set_error(PF_ERR_UNSUPPORTED, "layernorm: C=%d (built: 128, 256, 384, 512)", C);
+      return PF_ERR_UNSUPPORTED;
+  }
+  return pf::check_launch("layernorm");
+}
+
+}  // namespace
+
+extern "C" {
+
+int pf_layernorm_fwd(const void* x, int dtype, const float* w, const float* b, float eps, void* out, long M, int C,
+                     void* stream) {
+  PF_REQUIRE(x && w && b && out, PF_ERR_INVALID_ARG, "pf_layernorm_fwd: null pointer");
+  PF_REQUIRE(M >= 0, PF_ERR_INVALID_ARG, "pf_layernorm_fwd: M=%ld", M);
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_layernorm_fwd: dtype %d", dtype);
+  if (M == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  if (dtype == PF_F32) return ln_dispatch<float>(x, w, b, eps, out, M, C, 1, 1, 0, s);
+  return ln_dispatch<bf16>(x, w, b, eps, out, M, C, 1, 1, 0, s);
+}
+
+int pf_ln_transpose_fwd(const void* x, int dtype, const float* w, const float* b, float eps, void* out, int B, int N1,
+                        int N2, int C, int do_transpose, void* stream) {
+  PF_REQUIRE(x && w && b && out, PF_ERR_INVALID_ARG, "pf_ln_transpose_fwd: null pointer");
+  PF_REQUIRE(B >= 0 && N1 >= 0 && N2 >= 0, PF_ERR_INVALID_ARG, "pf_ln_transpose_fwd: bad shape");
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_ln_transpose_fwd: dtype %d", dtype);
+  PF_REQUIRE(x != out || !do_transpose, PF_ERR_INVALID_ARG, "pf_ln_transpose_fwd: cannot transpose in place");
+  const long M = (long)B * N1 * N2;
+  if (M == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  if (dtype == PF_F32) return ln_dispatch<float>(x, w, b, eps, out, M, C, N1, N2, do_transpose, s);
+  return ln_dispatch<bf16>(x, w, b, eps, out, M, C, N1, N2, do_transpose, s);
+}
+
+}  // extern "C"

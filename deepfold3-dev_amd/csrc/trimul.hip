@@ -1,0 +1,505 @@
+// Triangle multiplicative update (outgoing and incoming) in three launches:
+//
+//   K1 trimul_project:  x = LN_in(z); a, b = sigmoid(x Wg^T) * (x Wp^T) * mask,
+//                       stored channel-major as planes P, Q [B*C][Np][Np].
+//   K2 trimul_contract: X_c = P_c Q_c^T for every (batch, channel) plane.
+//   K3 trimul_output:   update = sigmoid(LN_in(z) Wog^T) * (LN_out(X) Wo^T),
+//                       written to `out` or added into it (fused residual).
+//
+// Reference semantics: TriangleMulOutgoing/Incoming (src/deepfold3/model/ops.py:412-473,
+// einsums ops.py:58-98) and the channel-major fused_trimul (triton/fused_trimul.py:264-366).
+//
+// Layout trick: the outgoing contraction X_ij = sum_k a_ik b_jk is P Q^T with P = a
+// stored [i][k] and Q = b stored [j][k]. For the incoming one, X_ij = sum_k a_kj b_ki,
+// K1 walks z along columns and stores the planes transposed (P = b^T as [i][k],
+// Q = a^T as [j][k]), so K2 is always the same k-contiguous "NT" GEMM.
+#include "capi.h"
+#include "common.h"
+
+namespace {
+
+template <class TC>
+constexpr int trimul_bm() { return sizeof(TC) == 2 ? 64 : 32; }
+
+// ------------------------------------------------------------------ K1
+// Packed weights w4 [4C][C]: for channel block j (16 channels), rows 64j + 16*kind + r,
+// kind 0 = a projection, 1 = a gate, 2 = b projection, 3 = b gate (channel 16j + r).
+template <class TZ, class TC, int C>
+__global__ __launch_bounds__(256) void trimul_project_kernel(const TZ* __restrict__ z, const float* __restrict__ mask,
+                                                             const float* __restrict__ lnw,
+                                                             const float* __restrict__ lnb, float eps,
+                                                             const TC* __restrict__ w4, TC* __restrict__ planes,
+                                                             int B, int N, int Np, int outgoing) {
+  constexpr int BM = trimul_bm<TC>();
+  constexpr int NT = 256;
+  constexpr int LDA = C + lds_pad<TC>();
+  constexpr int SLD = BM + lds_pad<TC>();
+  constexpr int RB = BM / 16;
+  constexpr int CBW = C / 16 / 4;  // channel blocks per wave
+  constexpr int A_BYTES = BM * LDA * (int)sizeof(TC);
+  constexpr int S_BYTES = 2 * C * SLD * (int)sizeof(TC);
+  __shared__ __attribute__((aligned(16))) char smem[(A_BYTES > S_BYTES ? A_BYTES : S_BYTES)];
+  __shared__ float mk[BM];
+  TC* A = reinterpret_cast<TC*>(smem);
+  TC* S = reinterpret_cast<TC*>(smem);
+
+  const int t0 = blockIdx.x * BM;
+  const int line = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const TZ* zb = z + (size_t)b * N * N * C;
+  auto pos_of = [&](int p) -> long {
+    const int t = t0 + p;
+    if (line >= N || t >= N) return -1;
+    return outgoing ? (long)line * N + t : (long)t * N + line;
+  };
+  auto rowptr = [&](int p) -> const TZ* {
+    const long pos = pos_of(p);
+    return pos < 0 ? nullptr : zb + pos * C;
+  };
+  ln_tile_to_lds<TZ, TC, C, BM, NT>(rowptr, lnw, lnb, eps, A, LDA);
+  if (tid < BM) {
+    const long pos = pos_of(tid);
+    mk[tid] = pos < 0 ? 0.f : mask[(size_t)b * N * N + pos];
+  }
+  __syncthreads();
+
+  const int w = wave_id();
+  const int l = lane_id();
+  f32x4 acc[RB][4 * CBW];
+  zero_acc(acc);
+  int wrow0[4 * CBW];
+#pragma unroll
+  for (int j = 0; j < 4 * CBW; ++j) wrow0[j] = (w * CBW + j / 4) * 64 + (j % 4) * 16;
+  gemm16_lds_x_w<TC, C, RB, 4 * CBW>(acc, A, LDA, 0, w4, C, wrow0);
+  __syncthreads();  // A is dead; its LDS becomes the staging tile S [2][C][SLD]
+
+#pragma unroll
+  for (int cbi = 0; cbi < CBW; ++cbi) {
+    const int ch = (w * CBW + cbi) * 16 + (l & 15);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p = rb * 16 + 4 * (l >> 4) + r;
+        const float m = mk[p];
+        av[r] = sigmoidf_(acc[rb][4 * cbi + 1][r]) * acc[rb][4 * cbi + 0][r] * m;
+        bv[r] = sigmoidf_(acc[rb][4 * cbi + 3][r]) * acc[rb][4 * cbi + 2][r] * m;
+      }
+      const int p0 = rb * 16 + 4 * (l >> 4);
+      store_vec<TC, 4>(S + ch * SLD + p0, av);
+      store_vec<TC, 4>(S + (C + ch) * SLD + p0, bv);
+    }
+  }
+  __syncthreads();
+
+  // Rows (plane, channel) of BM contiguous tokens.
+  constexpr int VEC = 16 / sizeof(TC);
+  constexpr int CPR = BM / VEC;  // 16-byte chunks per row
+  const size_t plane_elems = (size_t)Np * Np;
+  for (int idx = tid; idx < 2 * C * CPR; idx += NT) {
+    const int row = idx / CPR;
+    const int chunk = idx % CPR;
+    const int plane = row / C;
+    const int ch = row % C;
+    TC* dst = planes + ((size_t)plane * B * C + (size_t)b * C + ch) * plane_elems + (size_t)line * Np + t0 + chunk * VEC;
+    *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(S + row * SLD + chunk * VEC);
+  }
+}
+
+// ------------------------------------------------------------------ K2
+// X[g] = P[g] Q[g]^T, all [Np][Np] with k contiguous. 128x128 tile per block,
+// four waves in a 2x2 grid of 64x64, double-buffered LDS k-tiles.
+template <class TC>
+struct ContractCfg {
+  static constexpr int BMN = 128;
+  static constexpr int KT = sizeof(TC) == 2 ? 64 : 32;
+  static constexpr int LDK = KT + lds_pad<TC>();
+  static constexpr int TILE_ELEMS = BMN * LDK;
+  static constexpr int STAGE_BYTES = 2 * TILE_ELEMS * (int)sizeof(TC);
+  static constexpr int OUT_LD = BMN + lds_pad<TC>();
+  static constexpr int OUT_BYTES = BMN * OUT_LD * (int)sizeof(TC);
+  static constexpr int SMEM = (2 * STAGE_BYTES > OUT_BYTES) ? 2 * STAGE_BYTES : OUT_BYTES;
+};
+
+template <class TC>
+__global__ __launch_bounds__(256) void trimul_contract_kernel(const TC* __restrict__ P, const TC* __restrict__ Q,
+                                                              TC* __restrict__ X, int G, int Np, int xcd_remap) {
+  using Cfg = ContractCfg<TC>;
+  using M = Mfma<TC>;
+  constexpr int BMN = Cfg::BMN, KT = Cfg::KT, LDK = Cfg::LDK;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  TC* lds = reinterpret_cast<TC*>(smem);
+
+  const int tiles1 = Np / BMN;
+  const int tiles = tiles1 * tiles1;
+  // Block -> (plane, tile). Blocks are dispatched round-robin over the 8 XCDs; with
+  // the remap, XCD x walks planes x, x+8, ... one plane's tiles at a time, so a plane's
+  // operands are read from one L2.
+  int bid = blockIdx.x;
+  int g, tile;
+  if (xcd_remap) {
+    const int xcd = bid & 7;
+    const int u = bid >> 3;
+    g = xcd + 8 * (u / tiles);
+    tile = u % tiles;
+  } else {
+    g = bid / tiles;
+    tile = bid % tiles;
+  }
+  if (g >= G) return;
+  const int i0 = (tile / tiles1) * BMN;
+  const int j0 = (tile % tiles1) * BMN;
+  const size_t pe = (size_t)Np * Np;
+  const TC* Pg = P + (size_t)g * pe + (size_t)i0 * Np;
+  const TC* Qg = Q + (size_t)g * pe + (size_t)j0 * Np;
+
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const int wr = (w >> 1) * 64;  // wave's row offset in the tile
+  const int wc = (w & 1) * 64;   // wave's column offset
+
+  // Global -> LDS staging: each k-tile is 2 x BMN rows of KT elements.
+  constexpr int VEC = 16 / sizeof(TC);
+  constexpr int CPR = KT / VEC;                    // chunks per row
+  constexpr int LOADS = 2 * BMN * CPR / 256;       // 16-byte loads per thread per stage
+  static_assert((2 * BMN * CPR) % 256 == 0, "stage must split evenly");
+  u32x4 reg[LOADS];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < LOADS; ++q) {
+      const int idx = tid + q * 256;
+      const int row = idx / CPR;  // 0..2*BMN
+      const int chunk = idx % CPR;
+      const TC* src = row < BMN ? Pg + (size_t)row * Np : Qg + (size_t)(row - BMN) * Np;
+      reg[q] = *reinterpret_cast<const u32x4*>(src + k0 + chunk * VEC);
+    }
+  };
+  auto lstore = [&](int buf) {
+    TC* base = lds + buf * 2 * Cfg::TILE_ELEMS;
+#pragma unroll
+    for (int q = 0; q < LOADS; ++q) {
+      const int idx = tid + q * 256;
+      const int row = idx / CPR;
+      const int chunk = idx % CPR;
+      *reinterpret_cast<u32x4*>(base + row * LDK + chunk * VEC) = reg[q];
+    }
+  };
+
+  f32x4 acc[4][4];
+  zero_acc(acc);
+  const int nk = Np / KT;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int r = l & 15;
+  const int kq = (l >> 4) * M::KPL;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * KT);
+    const TC* As = lds + buf * 2 * Cfg::TILE_ELEMS;
+    const TC* Bs = As + Cfg::TILE_ELEMS;
+#pragma unroll
+    for (int kk = 0; kk < KT; kk += M::K16) {
+      typename M::Frag af[4], bfr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = M::load(As + (wr + i * 16 + r) * LDK + kk + kq);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfr[j] = M::load(Bs + (wc + j * 16 + r) * LDK + kk + kq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) M::mma16(acc[i][j], af[i], bfr[j]);
+    }
+    if (kt + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Stage the 128x128 output tile in LDS, then store 16-byte row chunks.
+  TC* O = lds;
+  constexpr int OLD = Cfg::OUT_LD;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) O[(wr + i * 16 + 4 * (l >> 4) + e) * OLD + wc + j * 16 + r] = from_f32<TC>(acc[i][j][e]);
+  __syncthreads();
+  constexpr int OCPR = BMN / VEC;
+  TC* Xg = X + (size_t)g * pe + (size_t)i0 * Np + j0;
+  for (int idx = tid; idx < BMN * OCPR; idx += 256) {
+    const int row = idx / OCPR;
+    const int chunk = idx % OCPR;
+    *reinterpret_cast<u32x4*>(Xg + (size_t)row * Np + chunk * VEC) =
+        *reinterpret_cast<const u32x4*>(O + row * OLD + chunk * VEC);
+  }
+}
+
+// ------------------------------------------------------------------ K3
+template <class TZ, class TC, int C>
+struct OutputCfg {
+  static constexpr int BM = trimul_bm<TC>();
+  static constexpr int XLD = BM + lds_pad<TC>();  // Xs [C][XLD]
+  static constexpr int ALD = C + lds_pad<TC>();   // A1, A2 [BM][ALD]
+  static constexpr int SLD = C + 4;               // fp32 stage [BM][SLD]
+  static constexpr int XS_BYTES = C * XLD * (int)sizeof(TC);
+  static constexpr int A_BYTES = BM * ALD * (int)sizeof(TC);
+  static constexpr int STAGE_BYTES = BM * SLD * 4;
+  static constexpr int NQ = 256 / BM;  // threads per position in the LN_out pass
+};
+
+template <class TZ, class TC, int C>
+__global__ __launch_bounds__(256) void trimul_output_kernel(
+    const TC* __restrict__ X, const TZ* __restrict__ z, TZ* __restrict__ out, const float* __restrict__ lniw,
+    const float* __restrict__ lnib, float eps_in, const float* __restrict__ lnow, const float* __restrict__ lnob,
+    float eps_out, const TC* __restrict__ Wo, const TC* __restrict__ Wog, int B, int N, int Np, int accumulate) {
+  using Cfg = OutputCfg<TZ, TC, C>;
+  constexpr int BM = Cfg::BM, XLD = Cfg::XLD, ALD = Cfg::ALD, SLD = Cfg::SLD, NQ = Cfg::NQ;
+  constexpr int NT = 256;
+  constexpr int RB = BM / 16;
+  constexpr int CBW = C / 16 / 4;
+  constexpr int SMEM1 = Cfg::XS_BYTES + 2 * Cfg::A_BYTES;
+  constexpr int SMEM = SMEM1 > Cfg::STAGE_BYTES ? SMEM1 : Cfg::STAGE_BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[SMEM];
+  __shared__ float red[NQ][BM];
+  __shared__ float stat_mean[BM];
+  TC* Xs = reinterpret_cast<TC*>(smem);
+  TC* A1 = reinterpret_cast<TC*>(smem + Cfg::XS_BYTES);
+  TC* A2 = reinterpret_cast<TC*>(smem + Cfg::XS_BYTES + Cfg::A_BYTES);
+  float* stage = reinterpret_cast<float*>(smem);
+
+  const int j0 = blockIdx.x * BM;
+  const int i = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const size_t pe = (size_t)Np * Np;
+
+  // 1) raw X tile, channel-major: Xs[c][p] = X[b*C + c][i][j0 + p]
+  {
+    constexpr int VEC = 16 / sizeof(TC);
+    constexpr int CPR = BM / VEC;
+    const TC* Xb = X + (size_t)b * C * pe + (size_t)i * Np + j0;
+    for (int idx = tid; idx < C * CPR; idx += NT) {
+      const int c = idx / CPR;
+      const int chunk = idx % CPR;
+      *reinterpret_cast<u32x4*>(Xs + c * XLD + chunk * VEC) =
+          *reinterpret_cast<const u32x4*>(Xb + (size_t)c * pe + chunk * VEC);
+    }
+  }
+  // 3) LN_in(z) tile (independent of Xs)
+  const TZ* zb = z + (size_t)b * N * N * C;
+  auto zrow = [&](int p) -> const TZ* {
+    const int j = j0 + p;
+    return j < N ? zb + ((size_t)i * N + j) * C : nullptr;
+  };
+  ln_tile_to_lds<TZ, TC, C, BM, NT>(zrow, lniw, lnib, eps_in, A2, ALD);
+  __syncthreads();
+
+  // 2) LN_out over channels of X, transposing into A1[p][c]
+  {
+    constexpr int CPQ = C / NQ;
+    const int p = tid % BM;
+    const int q = tid / BM;
+    float xv[CPQ];
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      xv[e] = to_f32(Xs[(q * CPQ + e) * XLD + p]);
+      s += xv[e];
+    }
+    red[q][p] = s;
+    __syncthreads();
+    if (q == 0) {
+      float t = 0.f;
+#pragma unroll
+      for (int k = 0; k < NQ; ++k) t += red[k][p];
+      stat_mean[p] = t * (1.0f / C);
+    }
+    __syncthreads();
+    const float mean = stat_mean[p];
+    float v = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      const float d = xv[e] - mean;
+      v += d * d;
+    }
+    __syncthreads();  // everyone has read stat_mean and red
+    red[q][p] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) t += red[k][p];
+    const float rstd = rsqrtf(t * (1.0f / C) + eps_out);
+    float y[CPQ];
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      const int c = q * CPQ + e;
+      y[e] = (xv[e] - mean) * rstd * lnow[c] + lnob[c];
+    }
+    constexpr int VEC = 16 / sizeof(TC);
+#pragma unroll
+    for (int e = 0; e < CPQ; e += VEC) store_vec<TC, VEC>(A1 + p * ALD + q * CPQ + e, y + e);
+  }
+  __syncthreads();
+
+  // 4) p = A1 Wo^T, g = A2 Wog^T
+  const int w = wave_id();
+  const int l = lane_id();
+  f32x4 accp[RB][CBW], accg[RB][CBW];
+  zero_acc(accp);
+  zero_acc(accg);
+  int wrow0[CBW];
+#pragma unroll
+  for (int j = 0; j < CBW; ++j) wrow0[j] = (w * CBW + j) * 16;
+  gemm16_lds_x_w<TC, C, RB, CBW>(accp, A1, ALD, 0, Wo, C, wrow0);
+  gemm16_lds_x_w<TC, C, RB, CBW>(accg, A2, ALD, 0, Wog, C, wrow0);
+  __syncthreads();  // A1/A2/Xs dead: reuse as the fp32 stage
+
+  // 5) update = sigmoid(g) * p, staged [p][c] in fp32, then stored / accumulated
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int j = 0; j < CBW; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p = rb * 16 + 4 * (l >> 4) + e;
+        const int c = (w * CBW + j) * 16 + (l & 15);
+        stage[p * SLD + c] = sigmoidf_(accg[rb][j][e]) * accp[rb][j][e];
+      }
+  __syncthreads();
+  TZ* ob = out + (size_t)b * N * N * C;
+  auto orow = [&](int p) -> TZ* {
+    const int j = j0 + p;
+    return j < N ? ob + ((size_t)i * N + j) * C : nullptr;
+  };
+  store_tile_from_lds<TZ, C, BM, NT>(orow, stage, SLD, accumulate != 0);
+}
+
+// ------------------------------------------------------------------ weight packing
+// w_proj, w_gate: [2C][C] in block order (rows 0..C-1 feed a, C..2C-1 feed b).
+template <class TS, class TD>
+__global__ void trimul_pack_kernel(const TS* __restrict__ wp, const TS* __restrict__ wg, TD* __restrict__ w4, int C) {
+  const int n = 4 * C * C;
+  for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += gridDim.x * blockDim.x) {
+    const int row = idx / C;
+    const int k = idx % C;
+    const int j = row / 64;
+    const int kind = (row % 64) / 16;
+    const int r = row % 16;
+    const int ch = j * 16 + r;
+    const TS* src = (kind & 1) ? wg : wp;
+    const int srow = (kind >= 2 ? C : 0) + ch;
+    w4[idx] = from_f32<TD>(to_f32(src[(size_t)srow * C + k]));
+  }
+}
+
+template <class TZ, class TC>
+int trimul_launch(const void* z, const float* mask, const float* lniw, const float* lnib, float eps_in,
+                  const void* w4, const float* lnow, const float* lnob, float eps_out, const void* wo,
+                  const void* wog, int B, int N, int outgoing, void* out, int accumulate, void* ws,
+                  hipStream_t s) {
+  constexpr int C = 128;
+  const int Np = pf::pad128(N);
+  const size_t pe = (size_t)Np * Np;
+  TC* planes = reinterpret_cast<TC*>(ws);
+  TC* P = planes;
+  TC* Q = planes + (size_t)B * C * pe;
+  TC* X = planes + (size_t)2 * B * C * pe;
+  {
+    constexpr int BM = trimul_bm<TC>();
+    dim3 grid(Np / BM, Np, B);
+    trimul_project_kernel<TZ, TC, C><<<grid, 256, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const TC*)w4,
+                                                          planes, B, N, Np, outgoing);
+    if (int e = pf::check_launch("trimul_project")) return e;
+  }
+  {
+    using Cfg = ContractCfg<TC>;
+    static bool attr_set = false;
+    if (!attr_set) {
+      hipError_t e = hipFuncSetAttribute((const void*)trimul_contract_kernel<TC>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::SMEM);
+      PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "trimul_contract: cannot reserve %d bytes of LDS: %s", Cfg::SMEM,
+                 hipGetErrorString(e));
+      attr_set = true;
+    }
+    const int G = B * C;
+    const int tiles = (Np / Cfg::BMN) * (Np / Cfg::BMN);
+    const int remap = (G % 8 == 0) ? 1 : 0;
+    dim3 grid((unsigned)(G * tiles));
+    trimul_contract_kernel<TC><<<grid, 256, Cfg::SMEM, s>>>(P, Q, X, G, Np, remap);
+    if (int e = pf::check_launch("trimul_contract")) return e;
+  }
+  {
+    constexpr int BM = trimul_bm<TC>();
+    dim3 grid((N + BM - 1) / BM, N, B);
+    trimul_output_kernel<TZ, TC, C><<<grid, 256, 0, s>>>(X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow, lnob,
+                                                         eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
+                                                         accumulate);
+    if (int e = pf::check_launch("trimul_output")) return e;
+  }
+  return pf::ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t pf_trimul_workspace_bytes(int B, int N, int C, int cdtype) {
+  if (B <= 0 || N <= 0 || C <= 0) return 0;
+  const size_t Np = (size_t)pf::pad128(N);
+  const size_t es = cdtype == PF_F32 ? 4 : 2;
+  return 3 * (size_t)B * C * Np * Np * es;
+}
+
+int pf_trimul_pack_weights(const void* w_proj, const void* w_gate, int wdtype, void* packed, int C, int cdtype,
+                           void* stream) {
+  PF_REQUIRE(w_proj && w_gate && packed, PF_ERR_INVALID_ARG, "pf_trimul_pack_weights: null pointer");
+  PF_REQUIRE(C == 128, PF_ERR_UNSUPPORTED, "pf_trimul_pack_weights: C=%d (only 128 is built)", C);
+  PF_REQUIRE((wdtype == PF_F32 || wdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16), PF_ERR_UNSUPPORTED,
+             "pf_trimul_pack_weights: bad dtype");
+  hipStream_t s = pf::as_stream(stream);
+  const int n = 4 * C * C;
+  dim3 grid((n + 255) / 256);
+  if (wdtype == PF_F32 && cdtype == PF_F32)
+    trimul_pack_kernel<float, float><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (float*)packed, C);
+  else if (wdtype == PF_F32)
+    trimul_pack_kernel<float, bf16><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (bf16*)packed, C);
+  else if (cdtype == PF_F32)
+    trimul_pack_kernel<bf16, float><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (float*)packed, C);
+  else
+    trimul_pack_kernel<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (bf16*)packed, C);
+  return pf::check_launch("pf_trimul_pack_weights");
+}
+
+int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const float* ln_in_b, float eps_in,
+                  const void* w_packed, const float* ln_out_w, const float* ln_out_b, float eps_out,
+                  const void* w_out, const void* w_out_gate, int B, int N, int C, int outgoing, int zdtype, int cdtype,
+                  void* out, int accumulate, void* workspace, size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(z && mask && ln_in_w && ln_in_b && w_packed && ln_out_w && ln_out_b && w_out && w_out_gate && out &&
+                 workspace,
+             PF_ERR_INVALID_ARG, "pf_trimul_fwd: null pointer");
+  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_trimul_fwd: B=%d N=%d", B, N);
+  PF_REQUIRE(C == 128, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: C=%d (only 128 is built)", C);
+  PF_REQUIRE(zdtype == PF_F32 || zdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: zdtype %d", zdtype);
+  PF_REQUIRE(cdtype == PF_F32 || cdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: cdtype %d", cdtype);
+  PF_REQUIRE(!(zdtype == PF_BF16 && cdtype == PF_F32), PF_ERR_UNSUPPORTED,
+             "pf_trimul_fwd: bf16 activations with fp32 GEMMs is not a supported regime");
+  PF_REQUIRE(pf::aligned16(z) && pf::aligned16(out) && pf::aligned16(workspace) && pf::aligned16(w_packed) &&
+                 pf::aligned16(w_out) && pf::aligned16(w_out_gate),
+             PF_ERR_ALIGNMENT, "pf_trimul_fwd: pointers must be 16-byte aligned");
+  PF_REQUIRE(workspace_bytes >= pf_trimul_workspace_bytes(B, N, C, cdtype), PF_ERR_WORKSPACE,
+             "pf_trimul_fwd: workspace %zu < %zu bytes", workspace_bytes, pf_trimul_workspace_bytes(B, N, C, cdtype));
+  hipStream_t s = pf::as_stream(stream);
+  if (zdtype == PF_F32 && cdtype == PF_F32)
+    return trimul_launch<float, float>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out, w_out,
+                                       w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+  if (zdtype == PF_F32)
+    return trimul_launch<float, bf16>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out, w_out,
+                                      w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+  return trimul_launch<bf16, bf16>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out, w_out,
+                                   w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+}
+
+}  // extern "C"

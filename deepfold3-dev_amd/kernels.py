@@ -1,0 +1,192 @@
+"""Functional HIP ops with the reference kernel layer's signatures (``src/deepfold3/model/triton/``).
+
+Each function here is a thin shim over one C-ABI entry point of
+``libpairformer_hip.so``: it checks devices and shapes, allocates the output
+and the workspace with torch's caching allocator, and launches on torch's
+current stream. There is no torch fallback; a call the kernels cannot serve
+raises :class:`NotActive`.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .inference_guard import NotActive, inference_only
+
+__all__ = [
+    "gemm_dtype_for",
+    "cast_weight",
+    "layer_norm",
+    "ln_transpose",
+    "pack_trimul_weights",
+    "trimul_forward",
+    "fused_trimul",
+    "residual_add",
+]
+
+
+def gemm_dtype_for(x: torch.Tensor) -> torch.dtype:
+    """GEMM operand dtype for activations ``x``.
+
+    bf16 when ``x`` is bf16 or when bf16 autocast is on for its device (the
+    reference's inference regime, ``scripts/inference.py:803-806``); fp32
+    otherwise (fp32 MFMA, the 1e-5 parity regime).
+    """
+    if x.dtype == torch.bfloat16:
+        return torch.bfloat16
+    dev = x.device.type
+    if torch.is_autocast_enabled(dev) and torch.get_autocast_dtype(dev) == torch.bfloat16:
+        return torch.bfloat16
+    return torch.float32
+
+
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().to(torch.float32).contiguous()
+
+
+def cast_weight(w: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """A contiguous ``dtype`` copy of ``w`` made by the HIP cast kernel."""
+    _lib.require_device("cast_weight", w)
+    src = w.detach().contiguous()
+    out = torch.empty(src.shape, dtype=dtype, device=src.device)
+    _lib.call(
+        "pf_cast", src.data_ptr(), _lib.dtype_code(src.dtype), out.data_ptr(), _lib.dtype_code(dtype), src.numel(),
+        _lib.stream_of(src),
+    )  # fmt: skip
+    return out
+
+
+def residual_add(res: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``res + x`` in ``res``'s dtype (eval-mode dropout-add, ``triton/dropout_add.py:221-265``)."""
+    _lib.require_device("residual_add", res, x)
+    if res.shape != x.shape:
+        raise NotActive("residual_add", f"shape mismatch {tuple(res.shape)} vs {tuple(x.shape)}")
+    res_c, x_c = res.contiguous(), x.contiguous()
+    out = torch.empty_like(res_c) if out is None else out
+    _lib.call(
+        "pf_add", res_c.data_ptr(), _lib.dtype_code(res_c.dtype), x_c.data_ptr(), _lib.dtype_code(x_c.dtype),
+        out.data_ptr(), res_c.numel(), _lib.stream_of(res_c),
+    )  # fmt: skip
+    return out
+
+
+def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """LayerNorm over the last dim with fp32 statistics, in x's dtype (``primitives.py:90-115``)."""
+    _lib.require_device("layer_norm", x)
+    C = x.shape[-1]
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    _lib.call(
+        "pf_layernorm_fwd", xc.data_ptr(), _lib.dtype_code(xc.dtype), _f32(weight).data_ptr(), _f32(bias).data_ptr(),
+        float(eps), out.data_ptr(), xc.numel() // C, C, _lib.stream_of(xc),
+    )  # fmt: skip
+    return out
+
+
+def ln_transpose(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float, do_transpose: bool):
+    """``LN(x).permute(0, 2, 1, 3)`` for x [B,N1,N2,C] (``triton/layernorm_transpose.py:269-316``)."""
+    _lib.require_device("ln_transpose", x)
+    if x.dim() != 4:
+        raise NotActive("ln_transpose", "input must be [B, N1, N2, C]")
+    B, N1, N2, C = x.shape
+    xc = x.contiguous()
+    out = torch.empty((B, N2, N1, C) if do_transpose else (B, N1, N2, C), dtype=x.dtype, device=x.device)
+    _lib.call(
+        "pf_ln_transpose_fwd", xc.data_ptr(), _lib.dtype_code(xc.dtype), _f32(weight).data_ptr(),
+        _f32(bias).data_ptr(), float(eps), out.data_ptr(), B, N1, N2, C, int(do_transpose), _lib.stream_of(xc),
+    )  # fmt: skip
+    return out
+
+
+# ---------------------------------------------------------------- triangle multiplication
+
+
+def pack_trimul_weights(w_proj: torch.Tensor, w_gate: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Pack block-ordered ``[2C, C]`` projection and gate weights into the ``[4C, C]`` K1 operand."""
+    _lib.require_device("pack_trimul_weights", w_proj, w_gate)
+    C = w_proj.shape[1]
+    if w_proj.shape != (2 * C, C) or w_gate.shape != (2 * C, C):
+        raise NotActive("fused_trimul", f"projection weights must be [2C, C], got {tuple(w_proj.shape)}")
+    wp, wg = w_proj.detach().contiguous(), w_gate.detach().to(w_proj.dtype).contiguous()
+    packed = torch.empty((4 * C, C), dtype=dtype, device=wp.device)
+    _lib.call(
+        "pf_trimul_pack_weights", wp.data_ptr(), wg.data_ptr(), _lib.dtype_code(wp.dtype), packed.data_ptr(), C,
+        _lib.dtype_code(dtype), _lib.stream_of(wp),
+    )  # fmt: skip
+    return packed
+
+
+def trimul_forward(
+    z: torch.Tensor,
+    mask: torch.Tensor,
+    ln_in_w: torch.Tensor,
+    ln_in_b: torch.Tensor,
+    eps_in: float,
+    w_packed: torch.Tensor,
+    ln_out_w: torch.Tensor,
+    ln_out_b: torch.Tensor,
+    eps_out: float,
+    w_out: torch.Tensor,
+    w_out_gate: torch.Tensor,
+    outgoing: bool,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """Launch K1, K2, K3 on prepared operands; returns ``out`` (the update, or z + update if accumulating)."""
+    _lib.require_device("fused_trimul", z, mask)
+    if z.dim() != 4 or z.shape[1] != z.shape[2]:
+        raise NotActive("fused_trimul", f"z must be [B, N, N, C], got {tuple(z.shape)}")
+    B, N, _, C = z.shape
+    if C != 128:
+        raise NotActive("fused_trimul", f"C={C}: only C=128 is built")
+    cdt = w_packed.dtype
+    if z.dtype == torch.bfloat16 and cdt == torch.float32:
+        raise NotActive("fused_trimul", "bf16 activations need bf16 GEMM operands")
+    zc = z.contiguous()
+    m = mask.to(torch.float32).contiguous()
+    if m.shape != (B, N, N):
+        raise NotActive("fused_trimul", f"mask must be [B, N, N], got {tuple(mask.shape)}")
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs an explicit out tensor")
+        out = torch.empty_like(zc)
+    elif not out.is_contiguous() or out.dtype != z.dtype or out.shape != z.shape:
+        raise NotActive("fused_trimul", "out must be a contiguous tensor like z")
+    code_c = _lib.dtype_code(cdt)
+    ws_bytes = _lib.lib().pf_trimul_workspace_bytes(B, N, C, code_c)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=z.device)
+    _lib.call(
+        "pf_trimul_fwd", zc.data_ptr(), m.data_ptr(), _f32(ln_in_w).data_ptr(), _f32(ln_in_b).data_ptr(),
+        float(eps_in), w_packed.data_ptr(), _f32(ln_out_w).data_ptr(), _f32(ln_out_b).data_ptr(), float(eps_out),
+        w_out.data_ptr(), w_out_gate.data_ptr(), B, N, C, int(outgoing), _lib.dtype_code(z.dtype), code_c,
+        out.data_ptr(), int(accumulate), ws.data_ptr(), ws_bytes, _lib.stream_of(zc),
+    )  # fmt: skip
+    return out
+
+
+@inference_only("fused_trimul")
+def fused_trimul(
+    z: torch.Tensor,
+    mask: torch.Tensor,
+    outgoing: bool,
+    norm_in: torch.nn.Module,
+    w_gate: torch.Tensor,
+    w_proj: torch.Tensor,
+    norm_out: torch.nn.Module,
+    w_out: torch.Tensor,
+    w_out_gate: torch.Tensor,
+) -> torch.Tensor:
+    """Triangle multiply in three HIP launches; same arguments as the reference's.
+
+    Reference: ``fused_trimul`` (``triton/fused_trimul.py:332-366``). ``w_gate`` and
+    ``w_proj`` are ``[2C, C]`` in block order (rows ``[a; b]``, the module's
+    ``_block_order``), ``w_out``/``w_out_gate`` are ``[C, C]``. Returns the update in
+    z's dtype. GEMM operands are bf16 for bf16 z or under bf16 autocast, else fp32.
+    """
+    cdt = gemm_dtype_for(z)
+    packed = pack_trimul_weights(w_proj, w_gate, cdt)
+    return trimul_forward(
+        z, mask, norm_in.weight, norm_in.bias, norm_in.eps, packed, norm_out.weight, norm_out.bias, norm_out.eps,
+        cast_weight(w_out, cdt), cast_weight(w_out_gate, cdt), outgoing,
+    )  # fmt: skip

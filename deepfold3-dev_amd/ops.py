@@ -1,0 +1,124 @@
+"""Triangle multiplicative update modules on the HIP kernels.
+
+``TriangleMulOutgoing`` / ``TriangleMulIncoming`` keep the reference's
+parameters, state-dict keys and ``forward(z, mask)`` signature
+(``src/deepfold3/model/ops.py:179-231``, ``:645-680``); the forward is the
+three-launch HIP triangle multiply (K1 project, K2 per-channel MFMA GEMM, K3
+output), see ``csrc/trimul.hip``. Multi-head routed (MHR) variants are not built
+and refuse at construction.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import kernel_census
+from .config import OptimConfig, require_hip
+from .inference_guard import NotActive, inference_only
+from .kernels import cast_weight, gemm_dtype_for, pack_trimul_weights, trimul_forward
+from .primitives import LayerNorm, LinearNoBias
+
+
+class WeightCache:
+    """Prepared (cast / packed) weight operands, rebuilt when a parameter changes.
+
+    The key is every parameter's storage pointer and in-place version counter plus
+    the operand dtype, so an optimizer step or ``load_state_dict`` invalidates it.
+    """
+
+    def __init__(self):
+        self._key = None
+        self._val = None
+
+    def get(self, params: list[torch.Tensor], dtype: torch.dtype, build):
+        key = (dtype, tuple((p.data_ptr(), p._version) for p in params))
+        if key != self._key:
+            self._val = build()
+            self._key = key
+        return self._val
+
+
+class _TriangleMulBase(nn.Module):
+    _outgoing: bool
+
+    def __init__(
+        self,
+        c_z: int,
+        optim: OptimConfig | None = None,
+        num_heads: int = 0,
+        head_norm: str = "channel",
+        router: bool = False,
+        router_kind: str = "softmax",
+    ):
+        super().__init__()
+        site = "TriangleMul"
+        if num_heads or head_norm != "channel" or router:
+            raise NotActive(site, "multi-head routed triangle multiplication is not built")
+        require_hip(site, optim)
+        self.norm_left = LayerNorm(c_z)
+        self.proj = LinearNoBias(c_z, c_z * 2)
+        self.gate = LinearNoBias(c_z, c_z * 2, initializer="zeros")
+        self.norm_center = LayerNorm(c_z)
+        self.out_proj = LinearNoBias(c_z, c_z, initializer="zeros")
+        self.out_gate = LinearNoBias(c_z, c_z, initializer="zeros")
+        even, odd = torch.arange(0, 2 * c_z, 2), torch.arange(1, 2 * c_z, 2)
+        # Interleaved a/b (ops.py:449-450) -> block order; incoming swaps a and b so the
+        # contraction stays P Q^T on transposed planes (ops.py:285-288).
+        self._block_order = torch.cat((even, odd)) if self._outgoing else torch.cat((odd, even))
+        self._cache = WeightCache()
+
+    def _operands(self, cdt: torch.dtype):
+        params = [
+            self.norm_left.weight, self.norm_left.bias, self.proj.weight, self.gate.weight,
+            self.norm_center.weight, self.norm_center.bias, self.out_proj.weight, self.out_gate.weight,
+        ]  # fmt: skip
+
+        def build():
+            order = self._block_order.to(self.proj.weight.device)
+            f32 = lambda t: t.detach().to(torch.float32).contiguous()  # noqa: E731
+            return dict(
+                packed=pack_trimul_weights(self.proj.weight[order], self.gate.weight[order], cdt),
+                w_out=cast_weight(self.out_proj.weight, cdt),
+                w_out_gate=cast_weight(self.out_gate.weight, cdt),
+                lniw=f32(self.norm_left.weight), lnib=f32(self.norm_left.bias),
+                lnow=f32(self.norm_center.weight), lnob=f32(self.norm_center.bias),
+            )  # fmt: skip
+
+        return self._cache.get(params, cdt, build)
+
+    def _run(self, z: torch.Tensor, mask: torch.Tensor, out: torch.Tensor | None, accumulate: bool) -> torch.Tensor:
+        kernel_census.record("TriangleMul", "hip_trimul")
+        op = self._operands(gemm_dtype_for(z))
+        return trimul_forward(
+            z, mask, op["lniw"], op["lnib"], self.norm_left.eps, op["packed"], op["lnow"], op["lnob"],
+            self.norm_center.eps, op["w_out"], op["w_out_gate"], self._outgoing, out=out, accumulate=accumulate,
+        )  # fmt: skip
+
+    @inference_only("TriangleMul")
+    def forward(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """The update for z [B?, N, N, C] and mask [B?, N, N] (not added to z)."""
+        has_batch = z.dim() == 4
+        if not has_batch:
+            z, mask = z.unsqueeze(0), mask.unsqueeze(0)
+        out = self._run(z, mask, None, False)
+        return out if has_batch else out.squeeze(0)
+
+    @inference_only("TriangleMul")
+    def forward_residual_(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """``z += update`` in place (fused into K3); z must be contiguous [B, N, N, C]."""
+        if not z.is_contiguous():
+            raise NotActive("TriangleMul", "in-place residual needs a contiguous z")
+        return self._run(z, mask, z, True)
+
+
+class TriangleMulOutgoing(_TriangleMulBase):
+    """Triangle multiplication, outgoing: ``X_ij = sum_k a_ik b_jk`` (``ops.py:665-671``)."""
+
+    _outgoing = True
+
+
+class TriangleMulIncoming(_TriangleMulBase):
+    """Triangle multiplication, incoming: ``X_ij = sum_k a_kj b_ki`` (``ops.py:674-680``)."""
+
+    _outgoing = False

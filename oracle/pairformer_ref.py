@@ -1,0 +1,244 @@
+"""CPU/GPU eager oracle for the DeepFold3 PairFormer block. TEST INFRASTRUCTURE ONLY.
+
+A functional PyTorch restatement of the reference's stock path
+(``OptimConfig.none()``, eval mode) that takes the block's state dict. Only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg use
+it, and only as the checker or as a timed baseline; the product path never calls
+it.
+
+Each function follows the reference file:line it cites, keeping its op order
+and rounding points: LayerNorm upcasts to fp32 and casts back to the input dtype,
+the a/b split of the triangle projection is interleaved (``0::2``/``1::2``), the
+attention masks are additive ``1e9 * (mask - 1)``, softmax runs on
+``logits.float()`` and casts back, GridSelfAttention post-scales ``QK^T`` and
+SingleAttention pre-scales ``q``.
+
+Pinning (what checks this restatement, beyond retyping it):
+  * ``tests/golden/*.npz``: fp32 outputs of the reference modules themselves,
+    imported on CPU by ``tests/golden/make_golden.py`` (block, every branch,
+    masked and unmasked).
+  * brute-force loops at tiny N for the triangle contraction, the per-row
+    attention and the column-attention transpose semantics
+    (``tests/test_oracle.py``).
+  * invariants: batch consistency, row-chunked == whole, fully masked rows
+    give the mean of V.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+__all__ = [
+    "layer_norm",
+    "tri_mul",
+    "grid_attention",
+    "transition",
+    "single_to_pair",
+    "single_attention",
+    "pairformer_block",
+    "pairformer_trunk",
+]
+
+
+def layer_norm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """fp32 LayerNorm over the last dim, cast back to x's dtype (``primitives.py:90-115``)."""
+    return F.layer_norm(x.float(), (x.shape[-1],), w.float(), b.float(), eps).to(x.dtype)
+
+
+def _sub(p: dict[str, torch.Tensor], prefix: str) -> dict[str, torch.Tensor]:
+    return {k[len(prefix) :]: v for k, v in p.items() if k.startswith(prefix)}
+
+
+def _triangle_matmul(a: torch.Tensor, b: torch.Tensor, outgoing: bool) -> torch.Tensor:
+    """``bikc,bjkc->bijc`` (outgoing) or ``bkjc,bkic->bijc`` (incoming), ``ops.py:58-98``."""
+    if outgoing:
+        return torch.matmul(a.permute(0, 3, 1, 2), b.permute(0, 3, 2, 1)).permute(0, 2, 3, 1)
+    return torch.matmul(a.permute(0, 3, 2, 1), b.permute(0, 3, 1, 2)).permute(0, 3, 2, 1)
+
+
+def tri_mul(z: torch.Tensor, mask: torch.Tensor, p: dict[str, torch.Tensor], outgoing: bool) -> torch.Tensor:
+    """Stock ``_TriangleMulBase._compute`` with plain heads (``ops.py:412-473``).
+
+    Args:
+        z: [B, N, N, C]; mask: [B, N, N]; p: keys ``norm_left.*``, ``proj.weight``,
+        ``gate.weight``, ``norm_center.*``, ``out_proj.weight``, ``out_gate.weight``.
+    Returns:
+        The update [B, N, N, C] (not added to z).
+    """
+    z0 = layer_norm(z, p["norm_left.weight"], p["norm_left.bias"])
+    proj = F.linear(z0, p["proj.weight"])
+    gate = torch.sigmoid(F.linear(z0, p["gate.weight"]))
+    out_gate = torch.sigmoid(F.linear(z0, p["out_gate.weight"]))
+    del z0
+    proj = proj * gate
+    a = proj[..., 0::2]
+    b = proj[..., 1::2]
+    m = mask.unsqueeze(-1)
+    a = (a * m).contiguous()
+    b = (b * m).contiguous()
+    act = _triangle_matmul(a, b, outgoing)
+    del a, b
+    act = layer_norm(act, p["norm_center.weight"], p["norm_center.bias"])
+    act = F.linear(act, p["out_proj.weight"])
+    return act * out_gate
+
+
+def _grid_attention_rows(
+    z_flat: torch.Tensor,
+    pb: torch.Tensor,
+    mask: torch.Tensor,
+    p: dict[str, torch.Tensor],
+    B: int,
+    N_rows: int,
+    N_cols: int,
+    H: int,
+    D: int,
+) -> torch.Tensor:
+    """``GridSelfAttention._compute_baseline`` (``attention.py:143-165``)."""
+    scale = D**-0.5
+    q = F.linear(z_flat, p["to_q.weight"]).view(B * N_rows, N_cols, H, D).permute(0, 2, 1, 3)
+    k = F.linear(z_flat, p["to_k.weight"]).view(B * N_rows, N_cols, H, D).permute(0, 2, 1, 3)
+    v = F.linear(z_flat, p["to_v.weight"]).view(B * N_rows, N_cols, H, D).permute(0, 2, 1, 3)
+    logits = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale
+    logits = logits.view(B, N_rows, H, N_cols, N_cols)
+    logits = logits + pb.unsqueeze(1)
+    logits = logits.reshape(B * N_rows, H, N_cols, N_cols)
+    mask_flat = mask.reshape(B * N_rows, N_cols)
+    logits = logits + 1e9 * (mask_flat.float() - 1.0).view(B * N_rows, 1, 1, N_cols)
+    w = F.softmax(logits.float(), dim=-1).to(z_flat.dtype)
+    del logits
+    out = torch.matmul(w, v)
+    out = out.permute(0, 2, 1, 3).reshape(B * N_rows, N_cols, H * D)
+    g = torch.sigmoid(F.linear(z_flat, p["to_g.weight"]))
+    return F.linear(out * g, p["out_proj.weight"])
+
+
+def grid_attention(
+    z: torch.Tensor,
+    mask: torch.Tensor,
+    p: dict[str, torch.Tensor],
+    transpose: bool,
+    num_heads: int = 4,
+    row_chunk: int = 0,
+) -> torch.Tensor:
+    """Stock ``GridSelfAttention.forward`` (``attention.py:167-269``, no fused kernels).
+
+    The pair bias comes from the un-transposed LN(z) (``attention.py:204-209``);
+    column mode transposes LN(z) and the mask, attends, and transposes back.
+    ``row_chunk`` evaluates that many rows at a time (rows are independent,
+    so it is exact) to bound the fp32 logits.
+    """
+    B, N, _, C = z.shape
+    H = num_heads
+    D = max(C // H, 16)
+    zn = layer_norm(z, p["norm.weight"], p["norm.bias"])
+    pb = F.linear(zn, p["pair_bias.weight"]).permute(0, 3, 1, 2)  # [B, H, N, N]
+    if transpose:
+        zn = zn.permute(0, 2, 1, 3)
+        mask = mask.permute(0, 2, 1)
+    N_rows, N_cols = zn.shape[1], zn.shape[2]
+    chunk = row_chunk if row_chunk > 0 else N_rows
+    outs = []
+    for r0 in range(0, N_rows, chunk):
+        r1 = min(N_rows, r0 + chunk)
+        rows = zn[:, r0:r1].reshape(B * (r1 - r0), N_cols, C)
+        o = _grid_attention_rows(rows, pb, mask[:, r0:r1], p, B, r1 - r0, N_cols, H, D)
+        outs.append(o.view(B, r1 - r0, N_cols, -1))
+    out = torch.cat(outs, dim=1) if len(outs) > 1 else outs[0]
+    if transpose:
+        out = out.permute(0, 2, 1, 3)
+    return out
+
+
+def transition(x: torch.Tensor, p: dict[str, torch.Tensor]) -> torch.Tensor:
+    """``TransitionBlock.forward`` (``primitives.py:193-251``): SwiGLU on contiguous halves."""
+    h = layer_norm(x, p["norm.weight"], p["norm.bias"])
+    h = F.linear(h, p["linear1.weight"])
+    a, b = h.chunk(2, dim=-1)
+    return F.linear(F.silu(a) * b, p["linear2.weight"])
+
+
+def single_to_pair(z: torch.Tensor, p: dict[str, torch.Tensor]) -> torch.Tensor:
+    """``single_to_pair(single_to_pair_norm(z)).movedim(-1, -3)`` (``evoformer.py:322-328``)."""
+    zn = layer_norm(z, p["single_to_pair_norm.weight"], p["single_to_pair_norm.bias"])
+    return F.linear(zn, p["single_to_pair.weight"]).movedim(-1, -3)
+
+
+def single_attention(
+    s: torch.Tensor, seq_mask: torch.Tensor, pair_logits: torch.Tensor, p: dict[str, torch.Tensor], num_heads: int = 16
+) -> torch.Tensor:
+    """``SingleAttention.forward`` (``attention.py:415-452``), no pair-bias gate."""
+    B, N, C = s.shape
+    H = num_heads
+    Dk = p["to_q.weight"].shape[0] // H
+    Dv = p["to_v.weight"].shape[0] // H
+    xn = layer_norm(s, p["norm.weight"], p["norm.bias"])
+    q = F.linear(xn, p["to_q.weight"], p["to_q.bias"]).view(B, N, H, Dk).permute(0, 2, 1, 3)
+    k = F.linear(xn, p["to_k.weight"]).view(B, N, H, Dk).permute(0, 2, 1, 3)
+    v = F.linear(xn, p["to_v.weight"]).view(B, N, H, Dv).permute(0, 2, 1, 3)
+    logits = torch.matmul(q * Dk**-0.5, k.transpose(-2, -1).contiguous())
+    logits = logits + pair_logits
+    logits = logits + (1e9 * (seq_mask.float() - 1.0)).view(B, 1, 1, N)
+    w = F.softmax(logits.float(), dim=-1).to(xn.dtype)
+    out = torch.matmul(w, v).permute(0, 2, 1, 3).reshape(B, N, H * Dv)
+    g = torch.sigmoid(F.linear(xn, p["to_g.weight"]))
+    return F.linear(out * g, p["out_proj.weight"])
+
+
+def pairformer_block(
+    pair: torch.Tensor,
+    single: torch.Tensor,
+    pair_mask: torch.Tensor,
+    seq_mask: torch.Tensor,
+    p: dict[str, torch.Tensor],
+    row_chunk: int = 0,
+    branches: dict[str, torch.Tensor] | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``PairFormerBlock.forward`` in eval mode (``evoformer.py:270-355``).
+
+    Identity branch scaler, ``residual_out_scale = 1``, eval dropout-add is a
+    plain add (``dropout_add.py:236-237``). If ``branches`` is a dict, each
+    branch output is stored in it under the reference submodule name.
+    """
+    tmo = tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True)
+    pair = pair + tmo
+    tmi = tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False)
+    pair = pair + tmi
+    row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
+    pair = pair + row
+    col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
+    pair = pair + col
+    pt = transition(pair, _sub(p, "pair_transition."))
+    pair = pair + pt
+    logits = single_to_pair(pair, p)
+    sa = single_attention(single, seq_mask, logits, _sub(p, "single_attn."))
+    single = single + sa
+    st = transition(single, _sub(p, "single_transition."))
+    single = single + st
+    if branches is not None:
+        branches.update(
+            tri_mul_out=tmo,
+            tri_mul_in=tmi,
+            pair_attn_row=row,
+            pair_attn_col=col,
+            pair_transition=pt,
+            pair_logits=logits,
+            single_attn=sa,
+            single_transition=st,
+        )
+    return pair, single
+
+
+def pairformer_trunk(
+    pair: torch.Tensor,
+    single: torch.Tensor,
+    pair_mask: torch.Tensor,
+    seq_mask: torch.Tensor,
+    blocks: list[dict[str, torch.Tensor]],
+    row_chunk: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The trunk loop (``evoformer.py:593-601``) without checkpointing or meters."""
+    for p in blocks:
+        pair, single = pairformer_block(pair, single, pair_mask, seq_mask, p, row_chunk=row_chunk)
+    return pair, single

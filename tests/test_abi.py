@@ -1,0 +1,56 @@
+"""CPU: the C-ABI library loads and exports every symbol include/pairformer_hip.h declares."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import pytest
+
+from tests._helpers import mod
+
+_lib = mod("_lib")
+
+
+def test_library_is_built():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build() first"
+
+
+def test_every_header_symbol_is_exported_and_bound():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    names = _lib.header_symbols()
+    assert len(names) >= 5
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    unbound = [n for n in names if n not in _lib.SIGNATURES]
+    assert not unbound, f"declared but missing from _lib.SIGNATURES: {unbound}"
+    extra = [n for n in _lib.SIGNATURES if n not in names]
+    assert not extra, f"bound but not declared in the header: {extra}"
+
+
+def test_version_and_error_reporting_without_gpu():
+    lib = _lib.lib()
+    assert lib.pf_version() == 1
+    # Argument validation runs before any device work, so it is testable on CPU.
+    nul = None
+    status = lib.pf_trimul_fwd(
+        nul, nul, nul, nul, 1e-5, nul, nul, nul, 1e-5, nul, nul, 1, 8, 128, 1, 0, 0, nul, 0, nul, 0, nul
+    )
+    assert status == 1  # PF_ERR_INVALID_ARG
+    assert b"null pointer" in lib.pf_last_error()
+    assert lib.pf_last_error_code() == 1
+
+
+def test_workspace_query():
+    lib = _lib.lib()
+    assert lib.pf_trimul_workspace_bytes(1, 768, 128, _lib.PF_BF16) == 3 * 128 * 768 * 768 * 2
+    assert lib.pf_trimul_workspace_bytes(1, 100, 128, _lib.PF_F32) == 3 * 128 * 128 * 128 * 4
+
+
+def test_cpu_tensors_are_refused():
+    import torch
+
+    k = mod("kernels")
+    NotActive = mod("inference_guard").NotActive
+    with pytest.raises(NotActive):
+        k.layer_norm(torch.randn(4, 128), torch.ones(128), torch.zeros(128))

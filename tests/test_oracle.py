@@ -1,0 +1,261 @@
+"""CPU: pin the oracle (oracle/pairformer_ref.py) to the reference and to independent forms.
+
+1. Golden vectors written by tests/golden/make_golden.py from the reference's own
+   PairFormerBlock (fp32, CPU): block outputs and every branch, masked.
+2. Brute force at tiny N: explicit loops for the triangle contractions, per-row
+   softmax attention, and the column-attention transpose semantics.
+3. Invariants: batch consistency, row chunking, fully masked rows = mean of V.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import pairformer_ref as R
+from tests._helpers import mod, rel_l2, sub
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+W = mod("weights")
+
+
+@pytest.fixture(autouse=True)
+def _highest_precision():
+    prev = torch.get_float32_matmul_precision()
+    torch.set_float32_matmul_precision("highest")
+    yield
+    torch.set_float32_matmul_precision(prev)
+
+
+def test_weight_generator_matches_golden_sha():
+    g = np.load(os.path.join(GOLDEN, "block_n24_masked.npz"))
+    assert str(g["weights_sha256"]) == W.state_dict_sha256(W.make_block_weights(7, perturb_affine=True))
+    g1 = np.load(os.path.join(GOLDEN, "block_n64_cfg1.npz"))
+    assert str(g1["weights_sha256"]) == W.state_dict_sha256(W.make_block_weights(0))
+
+
+def test_input_generator_matches_golden():
+    g = np.load(os.path.join(GOLDEN, "block_n24_masked.npz"))
+    inp = W.make_inputs(24, seed=10, pad_last=3)
+    for k in ("pair", "single", "pair_mask", "seq_mask"):
+        assert torch.equal(inp[k], torch.from_numpy(g["in_" + k])), k
+
+
+def test_block_and_branches_match_reference_golden():
+    g = np.load(os.path.join(GOLDEN, "block_n24_masked.npz"))
+    sd = W.make_block_weights(7, perturb_affine=True)
+    inp = {k: torch.from_numpy(g["in_" + k]) for k in ("pair", "single", "pair_mask", "seq_mask")}
+    br = {}
+    with torch.no_grad():
+        pair, single = R.pairformer_block(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], sd, branches=br)
+    assert rel_l2(pair, torch.from_numpy(g["out_pair"])) < 1e-6
+    assert rel_l2(single, torch.from_numpy(g["out_single"])) < 1e-6
+    for k in ("tri_mul_out", "tri_mul_in", "pair_attn_row", "pair_attn_col", "pair_transition", "single_attn",
+              "single_transition"):  # fmt: skip
+        assert rel_l2(br[k], torch.from_numpy(g["branch_" + k])) < 1e-6, k
+    s2p = br["pair_logits"].movedim(-3, -1)
+    assert rel_l2(s2p, torch.from_numpy(g["branch_single_to_pair"])) < 1e-6
+
+
+def test_config1_block_matches_reference_summary():
+    g = np.load(os.path.join(GOLDEN, "block_n64_cfg1.npz"))
+    sd = W.make_block_weights(0)
+    inp = W.make_inputs(64, seed=0)
+    with torch.no_grad():
+        pair, single = R.pairformer_block(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], sd)
+    assert rel_l2(single, torch.from_numpy(g["out_single"])) < 1e-6
+    got = pair.reshape(-1)[torch.from_numpy(g["pair_sample_idx"])]
+    assert rel_l2(got, torch.from_numpy(g["pair_sample_val"])) < 1e-6
+    p64 = pair.double()
+    assert abs(p64.sum().item() - float(g["pair_sum"])) <= 1e-6 * abs(float(g["pair_sumsq"])) ** 0.5 * 64
+    assert abs((p64 * p64).sum().item() / float(g["pair_sumsq"]) - 1.0) < 1e-6
+
+
+# ------------------------------------------------------------------ brute force
+
+
+def _tiny_trimul_params(c=8, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=gen) * 0.5  # noqa: E731
+    return {
+        "norm_left.weight": 1 + 0.1 * r(c), "norm_left.bias": 0.1 * r(c),
+        "proj.weight": r(2 * c, c), "gate.weight": r(2 * c, c),
+        "norm_center.weight": 1 + 0.1 * r(c), "norm_center.bias": 0.1 * r(c),
+        "out_proj.weight": r(c, c), "out_gate.weight": r(c, c),
+    }  # fmt: skip
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_trimul_against_explicit_loops(outgoing):
+    N, c = 5, 8
+    p = _tiny_trimul_params(c)
+    gen = torch.Generator().manual_seed(3)
+    z = torch.randn(1, N, N, c, generator=gen, dtype=torch.float64)
+    mask = (torch.rand(1, N, N, generator=gen) > 0.3).double()
+    p64 = {k: v.double() for k, v in p.items()}
+    out = R.tri_mul(z, mask, p64, outgoing)
+    # independent restatement with explicit index loops
+    zl = F.layer_norm(z, (c,), p64["norm_left.weight"], p64["norm_left.bias"])
+    pr = zl @ p64["proj.weight"].T
+    gt = torch.sigmoid(zl @ p64["gate.weight"].T)
+    ab = pr * gt
+    a = torch.zeros(N, N, c, dtype=torch.float64)
+    b = torch.zeros(N, N, c, dtype=torch.float64)
+    for i in range(N):
+        for j in range(N):
+            for ch in range(c):
+                a[i, j, ch] = ab[0, i, j, 2 * ch] * mask[0, i, j]
+                b[i, j, ch] = ab[0, i, j, 2 * ch + 1] * mask[0, i, j]
+    X = torch.zeros(N, N, c, dtype=torch.float64)
+    for i in range(N):
+        for j in range(N):
+            for k in range(N):
+                X[i, j] += a[i, k] * b[j, k] if outgoing else a[k, j] * b[k, i]
+    Xn = F.layer_norm(X, (c,), p64["norm_center.weight"], p64["norm_center.bias"])
+    ref = (Xn @ p64["out_proj.weight"].T) * torch.sigmoid(zl[0] @ p64["out_gate.weight"].T)
+    assert torch.allclose(out[0], ref, rtol=1e-5, atol=1e-6)  # LN runs in fp32 by design
+
+
+def _tiny_attn_params(c=8, H=2, seed=1):
+    gen = torch.Generator().manual_seed(seed)
+    D = max(c // H, 16)
+    r = lambda *s: torch.randn(*s, generator=gen) * 0.3  # noqa: E731
+    return {
+        "norm.weight": 1 + 0.1 * r(c), "norm.bias": 0.1 * r(c), "pair_bias.weight": r(H, c),
+        "to_q.weight": r(H * D, c), "to_k.weight": r(H * D, c), "to_v.weight": r(H * D, c),
+        "to_g.weight": r(H * D, c), "out_proj.weight": r(c, H * D),
+    }, H, D  # fmt: skip
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_grid_attention_against_loops(transpose):
+    N, c = 5, 8
+    p, H, D = _tiny_attn_params(c)
+    p = {k: v.double() for k, v in p.items()}
+    gen = torch.Generator().manual_seed(4)
+    z = torch.randn(1, N, N, c, generator=gen, dtype=torch.float64)
+    mask = torch.ones(1, N, N, dtype=torch.float64)
+    mask[0, 1, 3] = 0
+    mask[0, 2, :] = 0  # one fully masked row (and column entries)
+    out = R.grid_attention(z, mask, p, transpose=transpose, num_heads=H)
+    zn = F.layer_norm(z[0], (c,), p["norm.weight"], p["norm.bias"])
+    pb = torch.einsum("ijc,hc->hij", zn, p["pair_bias.weight"])  # bias from un-transposed LN(z)
+    ref = torch.zeros(N, N, c, dtype=torch.float64)
+    for line in range(N):
+        for qi in range(N):
+            # row mode: positions (line, .); column mode: positions (., line)
+            qpos = (line, qi) if not transpose else (qi, line)
+            o = torch.zeros(H * D, dtype=torch.float64)
+            for h in range(H):
+                sl = slice(h * D, (h + 1) * D)
+                q = zn[qpos] @ p["to_q.weight"][sl].T
+                logits = torch.zeros(N, dtype=torch.float64)
+                vs = torch.zeros(N, D, dtype=torch.float64)
+                for kj in range(N):
+                    kpos = (line, kj) if not transpose else (kj, line)
+                    k = zn[kpos] @ p["to_k.weight"][sl].T
+                    vs[kj] = zn[kpos] @ p["to_v.weight"][sl].T
+                    logits[kj] = q @ k * D**-0.5 + pb[h, qi, kj] + 1e9 * (mask[0][kpos] - 1.0)
+                # softmax on fp32 logits, as the reference (attention.py:160): this rounding
+                # point is what makes a fully masked row uniform
+                w = torch.softmax(logits.float(), 0).double()
+                o[sl] = w @ vs
+            g = torch.sigmoid(zn[qpos] @ p["to_g.weight"].T)
+            ref[qpos] = (o * g) @ p["out_proj.weight"].T
+    assert torch.allclose(out[0], ref, rtol=1e-5, atol=1e-6)  # LN runs in fp32 by design
+
+
+def test_fully_masked_row_is_mean_of_v():
+    """Eager semantics (attention.py:157-160): an all-masked row attends uniformly."""
+    N, c = 6, 8
+    p, H, D = _tiny_attn_params(c, seed=2)
+    z = torch.randn(1, N, N, c, generator=torch.Generator().manual_seed(5))
+    mask = torch.ones(1, N, N)
+    mask[0, 3, :] = 0
+    out = R.grid_attention(z, mask, p, transpose=False, num_heads=H)
+    zn = F.layer_norm(z[0], (c,), p["norm.weight"], p["norm.bias"])
+    v = zn[3] @ p["to_v.weight"].T  # [N, H*D]
+    o = v.mean(0, keepdim=True).expand(N, -1)
+    g = torch.sigmoid(zn[3] @ p["to_g.weight"].T)
+    ref = (o * g) @ p["out_proj.weight"].T
+    assert torch.allclose(out[0, 3], ref, rtol=1e-5, atol=1e-6)
+
+
+def test_single_attention_against_loops():
+    N, c, H = 5, 16, 4
+    gen = torch.Generator().manual_seed(6)
+    r = lambda *s: torch.randn(*s, generator=gen, dtype=torch.float64) * 0.3  # noqa: E731
+    p = {"norm.weight": 1 + r(c), "norm.bias": r(c), "to_q.weight": r(c, c), "to_q.bias": r(c),
+         "to_k.weight": r(c, c), "to_v.weight": r(c, c), "to_g.weight": r(c, c), "out_proj.weight": r(c, c)}  # fmt: skip
+    s = r(1, N, c)
+    seq = torch.tensor([[1.0, 1, 0, 1, 1]], dtype=torch.float64)
+    logits_pair = r(1, H, N, N)
+    out = R.single_attention(s, seq, logits_pair, p, num_heads=H)
+    D = c // H
+    xn = F.layer_norm(s[0], (c,), p["norm.weight"], p["norm.bias"])
+    ref = torch.zeros(N, c, dtype=torch.float64)
+    for i in range(N):
+        o = torch.zeros(c, dtype=torch.float64)
+        for h in range(H):
+            sl = slice(h * D, (h + 1) * D)
+            q = (xn[i] @ p["to_q.weight"][sl].T + p["to_q.bias"][sl]) * D**-0.5
+            lg = torch.stack([q @ (xn[j] @ p["to_k.weight"][sl].T) + logits_pair[0, h, i, j] + 1e9 * (seq[0, j] - 1)
+                              for j in range(N)])  # fmt: skip
+            w = torch.softmax(lg, 0)
+            o[sl] = sum(w[j] * (xn[j] @ p["to_v.weight"][sl].T) for j in range(N))
+        g = torch.sigmoid(xn[i] @ p["to_g.weight"].T)
+        ref[i] = (o * g) @ p["out_proj.weight"].T
+    assert torch.allclose(out[0], ref, rtol=1e-5, atol=1e-6)  # LN runs in fp32 by design
+
+
+def test_transition_swiglu_contiguous_halves():
+    c = 8
+    gen = torch.Generator().manual_seed(7)
+    p = {"norm.weight": torch.ones(c), "norm.bias": torch.zeros(c),
+         "linear1.weight": torch.randn(8 * c, c, generator=gen), "linear2.weight": torch.randn(c, 4 * c, generator=gen)}  # fmt: skip
+    x = torch.randn(3, c, generator=gen, dtype=torch.float64)
+    p = {k: v.double() for k, v in p.items()}
+    out = R.transition(x, p)
+    xn = F.layer_norm(x, (c,))
+    h = xn @ p["linear1.weight"].T
+    u = torch.stack([torch.stack([h[r, j] / (1 + torch.exp(-h[r, j])) * h[r, 4 * c + j] for j in range(4 * c)])
+                     for r in range(3)])  # fmt: skip
+    assert torch.allclose(out, u @ p["linear2.weight"].T, rtol=1e-5, atol=1e-6)  # LN runs in fp32 by design
+
+
+# ------------------------------------------------------------------ invariants
+
+
+def test_batch_consistency_and_row_chunking():
+    sd = W.make_block_weights(3, perturb_affine=True)
+    inp = W.make_inputs(12, seed=2, batch=2, pad_random=2)
+    with torch.no_grad():
+        pb, sb = R.pairformer_block(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], sd)
+        p1, s1 = R.pairformer_block(inp["pair"][1:], inp["single"][1:], inp["pair_mask"][1:], inp["seq_mask"][1:], sd)
+        pc, sc = R.pairformer_block(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], sd, row_chunk=5)
+    assert rel_l2(pb[1:], p1) < 1e-6 and rel_l2(sb[1:], s1) < 1e-6
+    assert rel_l2(pc, pb) < 1e-6 and rel_l2(sc, sb) < 1e-6
+
+
+def test_mask_changes_output():
+    sd = W.make_block_weights(4)
+    a = W.make_inputs(10, seed=1)
+    b = W.make_inputs(10, seed=1, pad_last=2)
+    with torch.no_grad():
+        pa, _ = R.pairformer_block(a["pair"], a["single"], a["pair_mask"], a["seq_mask"], sd)
+        pb, _ = R.pairformer_block(b["pair"], b["single"], b["pair_mask"], b["seq_mask"], sd)
+    assert rel_l2(pa, pb) > 1e-3
+
+
+def test_trunk_is_block_composition():
+    blocks = W.make_trunk_weights(9, 2)
+    inp = W.make_inputs(8, seed=3)
+    with torch.no_grad():
+        p, s = R.pairformer_trunk(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], blocks)
+        p1, s1 = R.pairformer_block(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], blocks[0])
+        p2, s2 = R.pairformer_block(p1, s1, inp["pair_mask"], inp["seq_mask"], blocks[1])
+    assert torch.equal(p, p2) and torch.equal(s, s2)
