@@ -22,7 +22,7 @@ HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__fil
 PF_F32 = 0
 PF_BF16 = 1
 
-_vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+_vp, _i, _f, _sz, _l = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_long
 
 # name -> (restype, argtypes); mirrors include/pairformer_hip.h.
 SIGNATURES: dict[str, tuple] = {
@@ -38,6 +38,26 @@ SIGNATURES: dict[str, tuple] = {
     "pf_trimul_fwd": (
         _i,
         [_vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
+    ),
+    "pf_grid_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "pf_grid_attn_fwd": (
+        _i,
+        [_vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
+    ),
+    "pf_pair_transition_fwd": (
+        _i,
+        [_vp, _vp, _vp, _f, _vp, _vp, _l, _i, _i, _i, _i, _vp, _i, _vp, _vp, _f, _vp, _vp, _l, _vp],
+    ),
+    "pf_single_to_pair_fwd": (_i, [_vp, _vp, _vp, _f, _vp, _l, _i, _i, _l, _i, _i, _vp, _vp]),
+    "pf_transition_workspace_bytes": (_sz, [_l, _i, _i, _i]),
+    "pf_transition_fwd": (
+        _i,
+        [_vp, _vp, _vp, _f, _vp, _vp, _l, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
+    ),
+    "pf_single_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "pf_single_attn_fwd": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
     ),
 }
 

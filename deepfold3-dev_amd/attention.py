@@ -1,0 +1,158 @@
+"""Triangle attention and single attention with pair bias on the HIP kernels.
+
+``GridSelfAttention`` (row: ``transpose=False``, starting node; column:
+``transpose=True``, ending node) and ``SingleAttention`` keep the reference's
+parameters, state-dict keys and ``forward`` signatures
+(``src/deepfold3/model/attention.py:56-104``, ``:344-452``). The forward is the
+three-launch HIP triangle attention (``csrc/attention.hip``: LN + fused q/k/v/g/pair-bias
+projection, flash attention with an online softmax, gated output projection) and the
+single-track kernels (``csrc/single.hip``).
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import kernel_census
+from .config import OptimConfig, require_hip
+from .inference_guard import NotActive, inference_only
+from .kernels import cast_weight, gemm_dtype_for, grid_attention_forward, pack_grid_attn_weights, single_attention_forward
+from .primitives import LayerNorm, LinearNoBias, WeightCache, f32
+
+
+class GridSelfAttention(nn.Module):
+    """Gated self-attention along rows (starting node) or columns (ending node) of z."""
+
+    def __init__(self, c: int, num_heads: int = 4, transpose: bool = False, optim: OptimConfig | None = None):
+        super().__init__()
+        assert c % num_heads == 0
+        require_hip("GridSelfAttention", optim)
+        self.num_heads = num_heads
+        self.head_dim = max(c // num_heads, 16)  # attention.py:67
+        self.transpose = transpose
+        self.scale = self.head_dim**-0.5
+        self.norm = LayerNorm(c)
+        self.pair_bias = LinearNoBias(c, num_heads)
+        self.to_q = LinearNoBias(c, num_heads * self.head_dim)
+        self.to_k = LinearNoBias(c, num_heads * self.head_dim)
+        self.to_v = LinearNoBias(c, num_heads * self.head_dim)
+        self.to_g = LinearNoBias(c, num_heads * self.head_dim, initializer="zeros")
+        self.out_proj = LinearNoBias(num_heads * self.head_dim, c, initializer="zeros")
+        self._cache = WeightCache()
+
+    def _operands(self, cdt: torch.dtype) -> dict:
+        params = [
+            self.norm.weight, self.norm.bias, self.pair_bias.weight, self.to_q.weight, self.to_k.weight,
+            self.to_v.weight, self.to_g.weight, self.out_proj.weight,
+        ]  # fmt: skip
+
+        def build():
+            return dict(
+                w5=pack_grid_attn_weights(
+                    self.to_q.weight, self.to_k.weight, self.to_v.weight, self.to_g.weight, self.pair_bias.weight, cdt
+                ),
+                w_out=cast_weight(self.out_proj.weight, cdt),
+                lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
+            )  # fmt: skip
+
+        return self._cache.get(params, cdt, build)
+
+    def _run(self, z, mask, out, accumulate):
+        kernel_census.record("GridSelfAttention.attention", "hip_tri_attn_col" if self.transpose else "hip_tri_attn_row")
+        op = self._operands(gemm_dtype_for(z))
+        return grid_attention_forward(
+            z, mask, op["lnw"], op["lnb"], self.norm.eps, op["w5"], op["w_out"], self.transpose,
+            num_heads=self.num_heads, out=out, accumulate=accumulate,
+        )  # fmt: skip
+
+    @inference_only("GridSelfAttention")
+    def forward(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """The update for z [B?, N, N, C], mask [B?, N, N] (not added to z)."""
+        has_batch = z.dim() == 4
+        if not has_batch:
+            z, mask = z.unsqueeze(0), mask.unsqueeze(0)
+        out = self._run(z, mask, None, False)
+        return out if has_batch else out.squeeze(0)
+
+    @inference_only("GridSelfAttention")
+    def forward_residual_(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """``z += update`` in place (fused into the output projection)."""
+        if not z.is_contiguous():
+            raise NotActive("GridSelfAttention", "in-place residual needs a contiguous z")
+        return self._run(z, mask, z, True)
+
+
+class SingleAttention(nn.Module):
+    """Self-attention on the single track with pair-logit bias (``attention.py:344-452``)."""
+
+    def __init__(
+        self,
+        c: int,
+        num_heads: int = 16,
+        key_dim: int = 384,
+        value_dim: int = 384,
+        optim: OptimConfig | None = None,
+        pair_bias_gate: bool = False,
+        pair_bias_gate_init_tau: float = 0.25,
+    ):
+        super().__init__()
+        require_hip("SingleAttention", optim)
+        if pair_bias_gate:
+            raise NotActive("SingleAttention", "the per-head pair-bias gate is not built")
+        if key_dim != value_dim or key_dim != c or key_dim // num_heads != 24:
+            raise NotActive("SingleAttention", "built for key_dim = value_dim = c with head dim 24")
+        self.num_heads = num_heads
+        self.key_dim_per_head = key_dim // num_heads
+        self.val_dim_per_head = value_dim // num_heads
+        self.scale = self.key_dim_per_head**-0.5
+        self.norm = LayerNorm(c)
+        self.register_parameter("pair_bias_gate_a", None)
+        self.to_q = nn.Linear(c, key_dim)
+        from .primitives import af3_linear_init_
+
+        af3_linear_init_(self.to_q.weight, "linear")
+        nn.init.zeros_(self.to_q.bias)
+        self.to_k = LinearNoBias(c, key_dim)
+        self.to_v = LinearNoBias(c, value_dim)
+        self.to_g = LinearNoBias(c, value_dim, initializer="zeros")
+        self.out_proj = LinearNoBias(value_dim, c, initializer="zeros")
+        self._cache = WeightCache()
+
+    def _operands(self, cdt: torch.dtype) -> dict:
+        params = [
+            self.norm.weight, self.norm.bias, self.to_q.weight, self.to_q.bias, self.to_k.weight, self.to_v.weight,
+            self.to_g.weight, self.out_proj.weight,
+        ]  # fmt: skip
+
+        def build():
+            w = torch.cat([self.to_q.weight, self.to_k.weight, self.to_v.weight, self.to_g.weight]).detach()
+            return dict(
+                wqkvg=cast_weight(w, cdt), w_out=cast_weight(self.out_proj.weight, cdt), qb=f32(self.to_q.bias),
+                lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
+            )  # fmt: skip
+
+        return self._cache.get(params, cdt, build)
+
+    def _run(self, x, mask, pair_logits, out, accumulate):
+        kernel_census.record("SingleAttention", "hip_single_attn")
+        op = self._operands(gemm_dtype_for(x))
+        return single_attention_forward(
+            x, mask, pair_logits, op["lnw"], op["lnb"], self.norm.eps, op["wqkvg"], op["qb"], op["w_out"],
+            self.num_heads, out=out, accumulate=accumulate,
+        )  # fmt: skip
+
+    @inference_only("SingleAttention")
+    def forward(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
+        """x [B?, N, c], mask [B?, N], pair_logits [B?, H, N, N] -> update [B?, N, c]."""
+        has_batch = x.dim() == 3
+        if not has_batch:
+            x, mask, pair_logits = x.unsqueeze(0), mask.unsqueeze(0), pair_logits.unsqueeze(0)
+        out = self._run(x, mask, pair_logits, None, False)
+        return out if has_batch else out.squeeze(0)
+
+    @inference_only("SingleAttention")
+    def forward_residual_(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
+        if not x.is_contiguous():
+            raise NotActive("SingleAttention", "in-place residual needs a contiguous x")
+        return self._run(x, mask, pair_logits, x, True)

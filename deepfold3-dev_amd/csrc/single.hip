@@ -1,0 +1,286 @@
+// Single-track kernels (tokens x 384): LayerNorm into the GEMM operand dtype, a row GEMM
+// with bias / SwiGLU / residual epilogues, and the attention-with-pair-bias core.
+//
+//   pf_single_attn_fwd: SingleAttention.forward (src/deepfold3/model/attention.py:415-452):
+//     xn = LN(s); q = xn Wq^T + bq; k, v, g = xn W^T; logits = (q d^-1/2) k^T + pair_logits
+//     + 1e9 (mask - 1); softmax in fp32; o = w v; out = (o * sigmoid(g)) Wout^T.
+//   pf_transition_fwd:  TransitionBlock.forward (primitives.py:193-251) for any C:
+//     LN -> W1 (SwiGLU on contiguous halves) -> W2, out = y or out += y.
+//
+// The single track is ~0.4 % of a PairFormer block's FLOPs; these kernels favour
+// simplicity: operands are read straight from global memory (they stay in L2).
+#include "capi.h"
+#include "common.h"
+
+namespace {
+
+// ------------------------------------------------------------------ LayerNorm rows -> TO
+template <class TI, class TO>
+__global__ __launch_bounds__(256) void ln_rows_kernel(const TI* __restrict__ x, const float* __restrict__ w,
+                                                      const float* __restrict__ b, float eps, TO* __restrict__ out,
+                                                      long M, int C) {
+  const long row = (long)blockIdx.x * 4 + wave_id();
+  if (row >= M) return;
+  const int l = lane_id();
+  const TI* src = x + row * C;
+  float s = 0.f;
+  for (int c = l; c < C; c += 64) s += to_f32(src[c]);
+  const float mean = group_sum<64>(s) / C;
+  float q = 0.f;
+  for (int c = l; c < C; c += 64) {
+    const float d = to_f32(src[c]) - mean;
+    q += d * d;
+  }
+  const float rstd = rsqrtf(group_sum<64>(q) / C + eps);
+  TO* dst = out + row * C;
+  for (int c = l; c < C; c += 64) dst[c] = from_f32<TO>((to_f32(src[c]) - mean) * rstd * w[c] + b[c]);
+}
+
+// ------------------------------------------------------------------ row GEMM
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2 };
+
+// out = epi(A W^T [+ bias]); A [M][K], W [Nw][K] (TC, k contiguous). One block computes a
+// 64-row x 64-column output tile, each wave one 16-column block over four row blocks.
+// EPI_SWIGLU: output column j is silu(h_j) * h_{F + j} with F = Nout (W has 2 Nout rows).
+// bias (fp32, may be null) applies to the first nbias output columns (EPI_STORE only).
+template <class TC, class TO, int EPI>
+__global__ __launch_bounds__(256) void rowgemm_kernel(const TC* __restrict__ A, const TC* __restrict__ W,
+                                                      const float* __restrict__ bias, int nbias, TO* __restrict__ out,
+                                                      long M, int Nout, int K) {
+  using MF = Mfma<TC>;
+  const int w = wave_id();
+  const int l = lane_id();
+  const long m0 = (long)blockIdx.x * 64;
+  const int n0 = blockIdx.y * 64 + w * 16;
+  if (n0 >= Nout) return;
+  const int r = l & 15;
+  const int kq = (l >> 4) * MF::KPL;
+  f32x4 acc[4], acc2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const TC* arow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    long m = m0 + i * 16 + r;
+    if (m >= M) m = M - 1;
+    arow[i] = A + m * K;
+  }
+  const TC* wrow = W + (size_t)(n0 + r) * K;
+  const TC* wrow2 = W + (size_t)(Nout + n0 + r) * K;
+  for (int k0 = 0; k0 < K; k0 += MF::K16) {
+    const typename MF::Frag bf = MF::load(wrow + k0 + kq);
+    typename MF::Frag bf2;
+    if (EPI == EPI_SWIGLU) bf2 = MF::load(wrow2 + k0 + kq);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const typename MF::Frag af = MF::load(arow[i] + k0 + kq);
+      MF::mma16(acc[i], af, bf);
+      if (EPI == EPI_SWIGLU) MF::mma16(acc2[i], af, bf2);
+    }
+  }
+  const int n = n0 + r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const long m = m0 + i * 16 + 4 * (l >> 4) + e;
+      if (m >= M) continue;
+      float y = acc[i][e];
+      TO* dst = out + m * Nout + n;
+      if (EPI == EPI_SWIGLU) {
+        y = siluf_(y) * acc2[i][e];
+        *dst = from_f32<TO>(y);
+      } else if (EPI == EPI_RESIDUAL) {
+        *dst = from_f32<TO>(to_f32(*dst) + y);
+      } else {
+        if (bias && n < nbias) y += bias[n];
+        *dst = from_f32<TO>(y);
+      }
+    }
+}
+
+// ------------------------------------------------------------------ attention core
+constexpr int kSHeadDim = 24;
+
+// One wave per (b, h, query i). qkvg [B*N][4*H*D] (TC): q | k | v | g (pre-sigmoid).
+// pair_logits fp32 [B][H][N][N]; seq_mask fp32 [B][N]. og [B*N][H*D] = o * sigmoid(g).
+// Dynamic LDS: 4 waves x N fp32 logits.
+template <class TC>
+__global__ __launch_bounds__(256) void single_attn_core_kernel(const TC* __restrict__ qkvg,
+                                                               const float* __restrict__ pl,
+                                                               const float* __restrict__ seq_mask,
+                                                               TC* __restrict__ og, int B, int N, int H) {
+  constexpr int D = kSHeadDim;
+  extern __shared__ float lg_all[];
+  const int w = wave_id();
+  const int l = lane_id();
+  const long task = (long)blockIdx.x * 4 + w;
+  if (task >= (long)B * H * N) return;
+  const int i = (int)(task % N);
+  const int h = (int)((task / N) % H);
+  const int b = (int)(task / ((long)N * H));
+  float* lg = lg_all + (size_t)w * N;
+  const int HD = H * D;
+  const int ld = 4 * HD;
+  const TC* base = qkvg + (size_t)b * N * ld;
+  const float scale = 1.0f / sqrtf((float)D);
+  float q[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) q[d] = to_f32(base[(size_t)i * ld + h * D + d]) * scale;
+  const float* plr = pl + (((size_t)b * H + h) * N + i) * N;
+  const float* mk = seq_mask + (size_t)b * N;
+  float mx = -INFINITY;
+  for (int j = l; j < N; j += 64) {
+    const TC* kr = base + (size_t)j * ld + HD + h * D;
+    float dot = 0.f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) dot += q[d] * to_f32(kr[d]);
+    const float v = dot + plr[j] + 1e9f * (mk[j] - 1.0f);
+    lg[j] = v;
+    mx = fmaxf(mx, v);
+  }
+  mx = group_max<64>(mx);
+  float sum = 0.f;
+  float o[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) o[d] = 0.f;
+  for (int j = l; j < N; j += 64) {
+    const float p = __expf(lg[j] - mx);
+    sum += p;
+    const TC* vr = base + (size_t)j * ld + 2 * HD + h * D;
+#pragma unroll
+    for (int d = 0; d < D; ++d) o[d] += p * to_f32(vr[d]);
+  }
+  sum = group_sum<64>(sum);
+#pragma unroll
+  for (int d = 0; d < D; ++d) o[d] = group_sum<64>(o[d]);
+  if (l < D) {
+    float od = 0.f;
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d == l) od = o[d];
+    const float g = to_f32(base[(size_t)i * ld + 3 * HD + h * D + l]);
+    og[((size_t)b * N + i) * HD + h * D + l] = from_f32<TC>(od / sum * sigmoidf_(g));
+  }
+}
+
+template <class TI, class TO>
+int ln_launch(const void* x, const float* w, const float* b, float eps, void* out, long M, int C, hipStream_t s) {
+  ln_rows_kernel<TI, TO><<<(unsigned)((M + 3) / 4), 256, 0, s>>>((const TI*)x, w, b, eps, (TO*)out, M, C);
+  return pf::check_launch("ln_rows");
+}
+
+template <class TC, class TO, int EPI>
+int rowgemm_launch(const void* A, const void* W, const float* bias, int nbias, void* out, long M, int Nout, int K,
+                   hipStream_t s) {
+  dim3 grid((unsigned)((M + 63) / 64), (unsigned)((Nout + 63) / 64));
+  rowgemm_kernel<TC, TO, EPI><<<grid, 256, 0, s>>>((const TC*)A, (const TC*)W, bias, nbias, (TO*)out, M, Nout, K);
+  return pf::check_launch("rowgemm");
+}
+
+size_t es_of(int dt) { return dt == PF_F32 ? 4 : 2; }
+
+template <class TZ, class TC>
+int single_attn_launch(const void* s_in, const float* seq_mask, const float* pair_logits, const float* lnw,
+                       const float* lnb, float eps, const void* wqkvg, const float* qbias, const void* wout, int B,
+                       int N, int C, int H, void* out, int accumulate, void* ws, hipStream_t st) {
+  const long M = (long)B * N;
+  const int HD = H * kSHeadDim;
+  char* p = reinterpret_cast<char*>(ws);
+  TC* xn = reinterpret_cast<TC*>(p);
+  p += pf::round_up((size_t)M * C * sizeof(TC), 256);
+  TC* qkvg = reinterpret_cast<TC*>(p);
+  p += pf::round_up((size_t)M * 4 * HD * sizeof(TC), 256);
+  TC* og = reinterpret_cast<TC*>(p);
+  if (int e = ln_launch<TZ, TC>(s_in, lnw, lnb, eps, xn, M, C, st)) return e;
+  if (int e = rowgemm_launch<TC, TC, EPI_STORE>(xn, wqkvg, qbias, HD, qkvg, M, 4 * HD, C, st)) return e;
+  {
+    const long tasks = (long)B * H * N;
+    const size_t lds = (size_t)4 * N * sizeof(float);
+    single_attn_core_kernel<TC><<<(unsigned)((tasks + 3) / 4), 256, lds, st>>>(qkvg, pair_logits, seq_mask, og, B,
+                                                                                N, H);
+    if (int e = pf::check_launch("single_attn_core")) return e;
+  }
+  if (accumulate) return rowgemm_launch<TC, TZ, EPI_RESIDUAL>(og, wout, nullptr, 0, out, M, C, HD, st);
+  return rowgemm_launch<TC, TZ, EPI_STORE>(og, wout, nullptr, 0, out, M, C, HD, st);
+}
+
+template <class TZ, class TC>
+int transition_generic_launch(const void* x, const float* lnw, const float* lnb, float eps, const void* w1,
+                              const void* w2, long M, int C, int F, void* out, int accumulate, void* ws,
+                              hipStream_t st) {
+  char* p = reinterpret_cast<char*>(ws);
+  TC* xn = reinterpret_cast<TC*>(p);
+  p += pf::round_up((size_t)M * C * sizeof(TC), 256);
+  TC* u = reinterpret_cast<TC*>(p);
+  if (int e = ln_launch<TZ, TC>(x, lnw, lnb, eps, xn, M, C, st)) return e;
+  if (int e = rowgemm_launch<TC, TC, EPI_SWIGLU>(xn, w1, nullptr, 0, u, M, F, C, st)) return e;
+  if (accumulate) return rowgemm_launch<TC, TZ, EPI_RESIDUAL>(u, w2, nullptr, 0, out, M, C, F, st);
+  return rowgemm_launch<TC, TZ, EPI_STORE>(u, w2, nullptr, 0, out, M, C, F, st);
+}
+
+#define PF_DISPATCH_ZC(zd, cd, FN, ...)                                                        \
+  ((zd) == PF_F32 && (cd) == PF_F32 ? FN<float, float>(__VA_ARGS__)                            \
+   : (zd) == PF_F32                 ? FN<float, bf16>(__VA_ARGS__)                             \
+                                    : FN<bf16, bf16>(__VA_ARGS__))
+
+bool dtype_pair_ok(int zd, int cd) {
+  return (zd == PF_F32 || zd == PF_BF16) && (cd == PF_F32 || cd == PF_BF16) && !(zd == PF_BF16 && cd == PF_F32);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t pf_single_attn_workspace_bytes(int B, int N, int C, int H, int cdtype) {
+  if (B <= 0 || N <= 0 || C <= 0 || H <= 0) return 0;
+  const size_t M = (size_t)B * N, es = es_of(cdtype), HD = (size_t)H * kSHeadDim;
+  return pf::round_up(M * C * es, 256) + pf::round_up(M * 4 * HD * es, 256) + pf::round_up(M * HD * es, 256);
+}
+
+int pf_single_attn_fwd(const void* s, const float* seq_mask, const float* pair_logits, const float* ln_w,
+                       const float* ln_b, float eps, const void* w_qkvg, const float* q_bias, const void* w_out, int B,
+                       int N, int C, int H, int zdtype, int cdtype, void* out, int accumulate, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(s && seq_mask && pair_logits && ln_w && ln_b && w_qkvg && q_bias && w_out && out && workspace,
+             PF_ERR_INVALID_ARG, "pf_single_attn_fwd: null pointer");
+  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_single_attn_fwd: B=%d N=%d", B, N);
+  PF_REQUIRE(H * kSHeadDim == C && C % 32 == 0, PF_ERR_UNSUPPORTED,
+             "pf_single_attn_fwd: C=%d H=%d (built: head dim 24, C a multiple of 32)", C, H);
+  PF_REQUIRE(N <= 4096, PF_ERR_UNSUPPORTED, "pf_single_attn_fwd: N=%d > 4096 (logits are staged in 64 KiB of LDS)", N);
+  PF_REQUIRE(dtype_pair_ok(zdtype, cdtype), PF_ERR_UNSUPPORTED, "pf_single_attn_fwd: dtype pair (%d, %d)", zdtype,
+             cdtype);
+  PF_REQUIRE(workspace_bytes >= pf_single_attn_workspace_bytes(B, N, C, H, cdtype), PF_ERR_WORKSPACE,
+             "pf_single_attn_fwd: workspace %zu < %zu bytes", workspace_bytes,
+             pf_single_attn_workspace_bytes(B, N, C, H, cdtype));
+  hipStream_t st = pf::as_stream(stream);
+  return PF_DISPATCH_ZC(zdtype, cdtype, single_attn_launch, s, seq_mask, pair_logits, ln_w, ln_b, eps, w_qkvg, q_bias,
+                        w_out, B, N, C, H, out, accumulate, workspace, st);
+}
+
+size_t pf_transition_workspace_bytes(long M, int C, int factor, int cdtype) {
+  if (M <= 0 || C <= 0 || factor <= 0) return 0;
+  const size_t es = es_of(cdtype);
+  return pf::round_up((size_t)M * C * es, 256) + pf::round_up((size_t)M * C * factor * es, 256);
+}
+
+int pf_transition_fwd(const void* x, const float* ln_w, const float* ln_b, float eps, const void* w1, const void* w2,
+                      long M, int C, int factor, int zdtype, int cdtype, void* out, int accumulate, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(x && ln_w && ln_b && w1 && w2 && out && workspace, PF_ERR_INVALID_ARG, "pf_transition_fwd: null pointer");
+  PF_REQUIRE(M >= 0 && C > 0 && factor > 0, PF_ERR_INVALID_ARG, "pf_transition_fwd: M=%ld C=%d factor=%d", M, C,
+             factor);
+  PF_REQUIRE(C % 32 == 0 && (C * factor) % 64 == 0, PF_ERR_UNSUPPORTED,
+             "pf_transition_fwd: C=%d factor=%d (C must be a multiple of 32, C*factor of 64)", C, factor);
+  PF_REQUIRE(dtype_pair_ok(zdtype, cdtype), PF_ERR_UNSUPPORTED, "pf_transition_fwd: dtype pair (%d, %d)", zdtype,
+             cdtype);
+  PF_REQUIRE(workspace_bytes >= pf_transition_workspace_bytes(M, C, factor, cdtype), PF_ERR_WORKSPACE,
+             "pf_transition_fwd: workspace %zu < %zu bytes", workspace_bytes,
+             pf_transition_workspace_bytes(M, C, factor, cdtype));
+  if (M == 0) return pf::ok();
+  hipStream_t st = pf::as_stream(stream);
+  return PF_DISPATCH_ZC(zdtype, cdtype, transition_generic_launch, x, ln_w, ln_b, eps, w1, w2, M, C, C * factor, out,
+                        accumulate, workspace, st);
+}
+
+}  // extern "C"

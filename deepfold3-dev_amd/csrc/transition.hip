@@ -1,0 +1,246 @@
+// Pair transition (SwiGLU MLP) with an optional fused single_to_pair epilogue, and the
+// standalone single_to_pair projection.
+//
+//   pair_transition: y = (silu(h_a) * h_b) W2^T with [h_a | h_b] = LN(x) W1^T, the halves
+//                    contiguous (reference TransitionBlock, src/deepfold3/model/primitives.py:193-251;
+//                    FusedTransitionBlock, triton/fused_transition.py:34-83). The hidden
+//                    activations never leave the chip: the hidden dim is walked in chunks of
+//                    128, each chunk's SwiGLU output goes through LDS straight into the second
+//                    GEMM, whose accumulators stay in registers. out = y or out += y.
+//   single_to_pair:  logits[b, h, i, j] = LN'(z[b, i, j]) Ws2p[h]^T (reference
+//                    evoformer.py:322-328, `.movedim(-1, -3)` materialised). When fused into
+//                    the transition, LN' reads the updated z (rounded to z's dtype first, as
+//                    the reference computes it from the stored residual stream).
+#include "capi.h"
+#include "common.h"
+
+namespace {
+
+constexpr int kC = 128;
+constexpr int kHidden = 512;  // factor 4: W1 [1024][128], W2 [128][512]
+constexpr int kS2pHeads = 16;
+
+template <class TC>
+constexpr int tr_bm() { return sizeof(TC) == 2 ? 64 : 32; }
+
+template <class TZ, class TC>
+struct TrCfg {
+  static constexpr int BM = tr_bm<TC>();
+  static constexpr int ALD = kC + lds_pad<TC>();
+  static constexpr int A_BYTES = BM * ALD * (int)sizeof(TC);
+  static constexpr int SLD = kC + 4;
+  static constexpr int S_BYTES = BM * SLD * 4;
+  // A | U | (stage aliases A+U once both are dead)
+  static constexpr int SMEM1 = 2 * A_BYTES;
+  static constexpr int SMEM = SMEM1 > S_BYTES ? SMEM1 : S_BYTES;
+};
+
+// LN'(rows) W^T for one 16-column block over BM rows held in an LDS tile A (already
+// normalised), written as logits[b][h][pos] for h < H. Row block rb is done by wave rb.
+template <class TC, int BM>
+PF_DEVICE void s2p_store(const TC* A, int ALD, const TC* __restrict__ Ws, float* __restrict__ logits, long m0, long M,
+                         long NN) {
+  constexpr int RB = BM / 16;
+  const int w = wave_id();
+  const int l = lane_id();
+  if (w >= RB) return;
+  f32x4 acc[1][1];
+  zero_acc(acc);
+  int wrow[1] = {0};
+  gemm16_lds_x_w<TC, kC, 1, 1>(acc, A, ALD, w * 16, Ws, kC, wrow);
+  const int h = l & 15;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const long m = m0 + w * 16 + 4 * (l >> 4) + e;
+    if (m >= M) continue;
+    const long b = m / NN;
+    const long pos = m % NN;
+    logits[(b * kS2pHeads + h) * NN + pos] = acc[0][0][e];
+  }
+}
+
+template <class TZ, class TC, bool S2P>
+__global__ __launch_bounds__(256) void pair_transition_kernel(
+    const TZ* __restrict__ x, TZ* __restrict__ out, const float* __restrict__ lnw, const float* __restrict__ lnb,
+    float eps, const TC* __restrict__ W1, const TC* __restrict__ W2, long M, int accumulate,
+    const float* __restrict__ s2p_w, const float* __restrict__ s2p_b, float s2p_eps, const TC* __restrict__ Ws2p,
+    float* __restrict__ logits, long NN) {
+  using Cfg = TrCfg<TZ, TC>;
+  constexpr int BM = Cfg::BM, ALD = Cfg::ALD, SLD = Cfg::SLD;
+  constexpr int NT = 256;
+  constexpr int RB = BM / 16;
+  __shared__ __attribute__((aligned(16))) char smem[Cfg::SMEM];
+  TC* A = reinterpret_cast<TC*>(smem);
+  TC* U = reinterpret_cast<TC*>(smem + Cfg::A_BYTES);
+  float* stage = reinterpret_cast<float*>(smem);
+
+  const long m0 = (long)blockIdx.x * BM;
+  const int w = wave_id();
+  const int l = lane_id();
+  auto xrow = [&](int p) -> const TZ* {
+    const long m = m0 + p;
+    return m < M ? x + m * kC : nullptr;
+  };
+  ln_tile_to_lds<TZ, TC, kC, BM, NT>(xrow, lnw, lnb, eps, A, ALD);
+  __syncthreads();
+
+  f32x4 acc_o[RB][2];
+  zero_acc(acc_o);
+  const int orow[2] = {w * 32, w * 32 + 16};
+#pragma unroll 1
+  for (int ch = 0; ch < kHidden / 128; ++ch) {
+    f32x4 acc_h[RB][4];
+    zero_acc(acc_h);
+    const int hrow[4] = {ch * 128 + w * 32, ch * 128 + w * 32 + 16, kHidden + ch * 128 + w * 32,
+                         kHidden + ch * 128 + w * 32 + 16};
+    gemm16_lds_x_w<TC, kC, RB, 4>(acc_h, A, ALD, 0, W1, kC, hrow);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int p = rb * 16 + 4 * (l >> 4) + e;
+          const int c = w * 32 + j * 16 + (l & 15);
+          U[p * ALD + c] = from_f32<TC>(siluf_(acc_h[rb][j][e]) * acc_h[rb][j + 2][e]);
+        }
+    __syncthreads();
+    gemm16_lds_x_w<TC, 128, RB, 2>(acc_o, U, ALD, 0, W2 + ch * 128, kHidden, orow);
+    __syncthreads();
+  }
+
+  // y -> fp32 stage [BM][SLD] (A and U are dead)
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        stage[(rb * 16 + 4 * (l >> 4) + e) * SLD + w * 32 + j * 16 + (l & 15)] = acc_o[rb][j][e];
+  __syncthreads();
+  {
+    constexpr int VEC = 16 / sizeof(TZ);
+    constexpr int LPP = kC / VEC;
+    constexpr int PPI = NT / LPP;
+    const int tid = threadIdx.x;
+    const int sub = tid % LPP;
+    const int pp = tid / LPP;
+#pragma unroll
+    for (int p0 = 0; p0 < BM; p0 += PPI) {
+      const int p = p0 + pp;
+      const long m = m0 + p;
+      if (m >= M) continue;
+      float v[VEC];
+      if (accumulate) {
+        load16<TZ>(out + m * kC + sub * VEC, v);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        v[e] = to_f32(from_f32<TZ>(v[e] + stage[p * SLD + sub * VEC + e]));
+        if (S2P) stage[p * SLD + sub * VEC + e] = v[e];
+      }
+      store_vec<TZ, VEC>(out + m * kC + sub * VEC, v);
+    }
+  }
+  if (S2P) {
+    // stage now holds the updated residual (as stored); LN' it into a TC tile placed after
+    // the stage, then project to the single-attention heads.
+    __syncthreads();
+    __shared__ __attribute__((aligned(16))) TC A2[BM * ALD];
+    auto srow = [&](int p) -> const float* { return m0 + p < M ? stage + p * SLD : nullptr; };
+    ln_tile_to_lds<float, TC, kC, BM, NT>(srow, s2p_w, s2p_b, s2p_eps, A2, ALD);
+    __syncthreads();
+    s2p_store<TC, BM>(A2, ALD, Ws2p, logits, m0, M, NN);
+  }
+}
+
+// Standalone single_to_pair: LN'(z) Ws2p^T -> logits [B][16][N][N].
+template <class TZ, class TC>
+__global__ __launch_bounds__(256) void single_to_pair_kernel(const TZ* __restrict__ z, const float* __restrict__ lnw,
+                                                             const float* __restrict__ lnb, float eps,
+                                                             const TC* __restrict__ Ws, float* __restrict__ logits,
+                                                             long M, long NN) {
+  constexpr int BM = tr_bm<TC>();
+  constexpr int ALD = kC + lds_pad<TC>();
+  __shared__ __attribute__((aligned(16))) TC A[BM * ALD];
+  const long m0 = (long)blockIdx.x * BM;
+  auto zrow = [&](int p) -> const TZ* { return m0 + p < M ? z + (m0 + p) * kC : nullptr; };
+  ln_tile_to_lds<TZ, TC, kC, BM, 256>(zrow, lnw, lnb, eps, A, ALD);
+  __syncthreads();
+  s2p_store<TC, BM>(A, ALD, Ws, logits, m0, M, NN);
+}
+
+template <class TZ, class TC>
+int transition_launch(const void* x, const float* lnw, const float* lnb, float eps, const void* w1, const void* w2,
+                      long M, void* out, int accumulate, const float* s2p_w, const float* s2p_b, float s2p_eps,
+                      const void* ws2p, float* logits, long NN, hipStream_t s) {
+  constexpr int BM = tr_bm<TC>();
+  dim3 grid((unsigned)((M + BM - 1) / BM));
+  if (logits)
+    pair_transition_kernel<TZ, TC, true><<<grid, 256, 0, s>>>((const TZ*)x, (TZ*)out, lnw, lnb, eps, (const TC*)w1,
+                                                             (const TC*)w2, M, accumulate, s2p_w, s2p_b, s2p_eps,
+                                                             (const TC*)ws2p, logits, NN);
+  else
+    pair_transition_kernel<TZ, TC, false><<<grid, 256, 0, s>>>((const TZ*)x, (TZ*)out, lnw, lnb, eps, (const TC*)w1,
+                                                              (const TC*)w2, M, accumulate, nullptr, nullptr, 0.f,
+                                                              nullptr, nullptr, NN);
+  return pf::check_launch("pair_transition");
+}
+
+template <class TZ, class TC>
+int s2p_launch(const void* z, const float* lnw, const float* lnb, float eps, const void* ws, float* logits, long M,
+               long NN, hipStream_t s) {
+  constexpr int BM = tr_bm<TC>();
+  dim3 grid((unsigned)((M + BM - 1) / BM));
+  single_to_pair_kernel<TZ, TC><<<grid, 256, 0, s>>>((const TZ*)z, lnw, lnb, eps, (const TC*)ws, logits, M, NN);
+  return pf::check_launch("single_to_pair");
+}
+
+#define PF_DISPATCH_ZC(zd, cd, FN, ...)                                                        \
+  ((zd) == PF_F32 && (cd) == PF_F32 ? FN<float, float>(__VA_ARGS__)                            \
+   : (zd) == PF_F32                 ? FN<float, bf16>(__VA_ARGS__)                             \
+                                    : FN<bf16, bf16>(__VA_ARGS__))
+
+}  // namespace
+
+extern "C" {
+
+int pf_pair_transition_fwd(const void* x, const float* ln_w, const float* ln_b, float eps, const void* w1,
+                           const void* w2, long M, int C, int factor, int zdtype, int cdtype, void* out, int accumulate,
+                           const float* s2p_ln_w, const float* s2p_ln_b, float s2p_eps, const void* w_s2p,
+                           float* pair_logits, long NN, void* stream) {
+  PF_REQUIRE(x && ln_w && ln_b && w1 && w2 && out, PF_ERR_INVALID_ARG, "pf_pair_transition_fwd: null pointer");
+  PF_REQUIRE(C == kC && factor == 4, PF_ERR_UNSUPPORTED,
+             "pf_pair_transition_fwd: C=%d factor=%d (built: C=128, factor 4)", C, factor);
+  PF_REQUIRE(M >= 0, PF_ERR_INVALID_ARG, "pf_pair_transition_fwd: M=%ld", M);
+  PF_REQUIRE((zdtype == PF_F32 || zdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16) &&
+                 !(zdtype == PF_BF16 && cdtype == PF_F32),
+             PF_ERR_UNSUPPORTED, "pf_pair_transition_fwd: dtype pair (%d, %d)", zdtype, cdtype);
+  PF_REQUIRE(!pair_logits || (s2p_ln_w && s2p_ln_b && w_s2p && NN > 0 && M % NN == 0), PF_ERR_INVALID_ARG,
+             "pf_pair_transition_fwd: fused single_to_pair needs its LN, weight and NN dividing M");
+  PF_REQUIRE(pf::aligned16(x) && pf::aligned16(out) && pf::aligned16(w1) && pf::aligned16(w2), PF_ERR_ALIGNMENT,
+             "pf_pair_transition_fwd: pointers must be 16-byte aligned");
+  if (M == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  return PF_DISPATCH_ZC(zdtype, cdtype, transition_launch, x, ln_w, ln_b, eps, w1, w2, M, out, accumulate, s2p_ln_w,
+                        s2p_ln_b, s2p_eps, w_s2p, pair_logits, NN, s);
+}
+
+int pf_single_to_pair_fwd(const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_s2p, long M,
+                          int C, int H, long NN, int zdtype, int cdtype, float* pair_logits, void* stream) {
+  PF_REQUIRE(z && ln_w && ln_b && w_s2p && pair_logits, PF_ERR_INVALID_ARG, "pf_single_to_pair_fwd: null pointer");
+  PF_REQUIRE(C == kC && H == kS2pHeads, PF_ERR_UNSUPPORTED, "pf_single_to_pair_fwd: C=%d H=%d (built: 128, 16)", C,
+             H);
+  PF_REQUIRE(NN > 0 && M >= 0 && M % NN == 0, PF_ERR_INVALID_ARG, "pf_single_to_pair_fwd: M=%ld NN=%ld", M, NN);
+  PF_REQUIRE((zdtype == PF_F32 || zdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16) &&
+                 !(zdtype == PF_BF16 && cdtype == PF_F32),
+             PF_ERR_UNSUPPORTED, "pf_single_to_pair_fwd: dtype pair (%d, %d)", zdtype, cdtype);
+  if (M == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  return PF_DISPATCH_ZC(zdtype, cdtype, s2p_launch, z, ln_w, ln_b, eps, w_s2p, pair_logits, M, NN, s);
+}
+
+}  // extern "C"

@@ -23,6 +23,12 @@ __all__ = [
     "trimul_forward",
     "fused_trimul",
     "residual_add",
+    "pack_grid_attn_weights",
+    "grid_attention_forward",
+    "pair_transition_forward",
+    "single_to_pair",
+    "transition_forward",
+    "single_attention_forward",
 ]
 
 
@@ -190,3 +196,193 @@ def fused_trimul(
         z, mask, norm_in.weight, norm_in.bias, norm_in.eps, packed, norm_out.weight, norm_out.bias, norm_out.eps,
         cast_weight(w_out, cdt), cast_weight(w_out_gate, cdt), outgoing,
     )  # fmt: skip
+
+
+# ---------------------------------------------------------------- triangle attention
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def pack_grid_attn_weights(to_q, to_k, to_v, to_g, pair_bias, dtype: torch.dtype) -> torch.Tensor:
+    """``[4C + 16, C]`` operand: rows to_q | to_k | to_v | to_g | pair_bias (H rows) | zeros."""
+    C = to_q.shape[1]
+    H = pair_bias.shape[0]
+    pad = torch.zeros(16 - H, C, dtype=to_q.dtype, device=to_q.device)
+    w = torch.cat([t.detach() for t in (to_q, to_k, to_v, to_g, pair_bias)] + [pad], dim=0)
+    return cast_weight(w, dtype)
+
+
+def grid_attention_forward(
+    z: torch.Tensor,
+    mask: torch.Tensor,
+    ln_w: torch.Tensor,
+    ln_b: torch.Tensor,
+    eps: float,
+    w_packed: torch.Tensor,
+    w_out: torch.Tensor,
+    transpose: bool,
+    num_heads: int = 4,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """GridSelfAttention on prepared operands (``attention.py:167-269``); returns ``out``."""
+    _lib.require_device("GridSelfAttention", z, mask)
+    if z.dim() != 4 or z.shape[1] != z.shape[2]:
+        raise NotActive("GridSelfAttention", f"z must be [B, N, N, C], got {tuple(z.shape)}")
+    B, N, _, C = z.shape
+    if C != 128 or num_heads != 4:
+        raise NotActive("GridSelfAttention", f"C={C}, heads={num_heads}: only C=128 with 4 heads x 32 is built")
+    cdt = w_packed.dtype
+    if z.dtype == torch.bfloat16 and cdt == torch.float32:
+        raise NotActive("GridSelfAttention", "bf16 activations need bf16 GEMM operands")
+    zc = z.contiguous()
+    m = mask.to(torch.float32).contiguous()
+    if m.shape != (B, N, N):
+        raise NotActive("GridSelfAttention", f"mask must be [B, N, N], got {tuple(mask.shape)}")
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs an explicit out tensor")
+        out = torch.empty_like(zc)
+    code_c = _lib.dtype_code(cdt)
+    ws_bytes = _lib.lib().pf_grid_attn_workspace_bytes(B, N, C, num_heads, code_c)
+    ws = _workspace(ws_bytes, z.device)
+    _lib.call(
+        "pf_grid_attn_fwd", zc.data_ptr(), m.data_ptr(), _f32(ln_w).data_ptr(), _f32(ln_b).data_ptr(), float(eps),
+        w_packed.data_ptr(), w_out.data_ptr(), B, N, C, num_heads, int(transpose), _lib.dtype_code(z.dtype), code_c,
+        out.data_ptr(), int(accumulate), ws.data_ptr(), ws_bytes, _lib.stream_of(zc),
+    )  # fmt: skip
+    return out
+
+
+# ---------------------------------------------------------------- transitions
+
+
+def pair_transition_forward(
+    x: torch.Tensor,
+    ln_w: torch.Tensor,
+    ln_b: torch.Tensor,
+    eps: float,
+    w1: torch.Tensor,
+    w2: torch.Tensor,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+    s2p: tuple | None = None,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Fused pair transition (C=128, factor 4); optionally also the single_to_pair logits.
+
+    ``s2p = (ln_w, ln_b, eps, w_s2p)`` computes ``pair_logits [B, 16, N, N]`` (fp32) from the
+    updated rows (``evoformer.py:322-328``). Returns ``(out, pair_logits or None)``.
+    """
+    _lib.require_device("FusedTransitionBlock", x)
+    C = x.shape[-1]
+    factor = w1.shape[0] // (2 * C)
+    xc = x.contiguous()
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs an explicit out tensor")
+        out = torch.empty_like(xc)
+    M = xc.numel() // C
+    logits = None
+    s2p_args = [None, None, 0.0, None, None, 0]
+    if s2p is not None:
+        if x.dim() != 4:
+            raise NotActive("single_to_pair", "fused single_to_pair needs x as [B, N, N, C]")
+        B, N = x.shape[0], x.shape[1]
+        logits = torch.empty((B, 16, N, N), dtype=torch.float32, device=x.device)
+        sw, sb, seps, ws2p = s2p
+        s2p_args = [_f32(sw).data_ptr(), _f32(sb).data_ptr(), float(seps), ws2p.data_ptr(), logits.data_ptr(), N * N]
+    _lib.call(
+        "pf_pair_transition_fwd", xc.data_ptr(), _f32(ln_w).data_ptr(), _f32(ln_b).data_ptr(), float(eps),
+        w1.data_ptr(), w2.data_ptr(), M, C, factor, _lib.dtype_code(x.dtype), _lib.dtype_code(w1.dtype),
+        out.data_ptr(), int(accumulate), *s2p_args, _lib.stream_of(xc),
+    )  # fmt: skip
+    return out, logits
+
+
+def single_to_pair(z: torch.Tensor, ln_w, ln_b, eps: float, w_s2p: torch.Tensor) -> torch.Tensor:
+    """``single_to_pair(single_to_pair_norm(z)).movedim(-1, -3)`` -> [B, H, N, N] fp32."""
+    _lib.require_device("single_to_pair", z)
+    B, N, _, C = z.shape
+    H = w_s2p.shape[0]
+    zc = z.contiguous()
+    logits = torch.empty((B, H, N, N), dtype=torch.float32, device=z.device)
+    _lib.call(
+        "pf_single_to_pair_fwd", zc.data_ptr(), _f32(ln_w).data_ptr(), _f32(ln_b).data_ptr(), float(eps),
+        w_s2p.data_ptr(), zc.numel() // C, C, H, N * N, _lib.dtype_code(z.dtype), _lib.dtype_code(w_s2p.dtype),
+        logits.data_ptr(), _lib.stream_of(zc),
+    )  # fmt: skip
+    return logits
+
+
+def transition_forward(
+    x: torch.Tensor,
+    ln_w: torch.Tensor,
+    ln_b: torch.Tensor,
+    eps: float,
+    w1: torch.Tensor,
+    w2: torch.Tensor,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """Generic TransitionBlock forward for any C (``primitives.py:193-251``)."""
+    _lib.require_device("TransitionBlock", x)
+    C = x.shape[-1]
+    factor = w1.shape[0] // (2 * C)
+    xc = x.contiguous()
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs an explicit out tensor")
+        out = torch.empty_like(xc)
+    M = xc.numel() // C
+    code_c = _lib.dtype_code(w1.dtype)
+    ws_bytes = _lib.lib().pf_transition_workspace_bytes(M, C, factor, code_c)
+    ws = _workspace(ws_bytes, x.device)
+    _lib.call(
+        "pf_transition_fwd", xc.data_ptr(), _f32(ln_w).data_ptr(), _f32(ln_b).data_ptr(), float(eps), w1.data_ptr(),
+        w2.data_ptr(), M, C, factor, _lib.dtype_code(x.dtype), code_c, out.data_ptr(), int(accumulate),
+        ws.data_ptr(), ws_bytes, _lib.stream_of(xc),
+    )  # fmt: skip
+    return out
+
+
+# ---------------------------------------------------------------- single attention
+
+
+def single_attention_forward(
+    s: torch.Tensor,
+    seq_mask: torch.Tensor,
+    pair_logits: torch.Tensor,
+    ln_w: torch.Tensor,
+    ln_b: torch.Tensor,
+    eps: float,
+    w_qkvg: torch.Tensor,
+    q_bias: torch.Tensor,
+    w_out: torch.Tensor,
+    num_heads: int,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """SingleAttention forward (``attention.py:415-452``) on prepared operands."""
+    _lib.require_device("SingleAttention", s, seq_mask, pair_logits)
+    B, N, C = s.shape
+    sc = s.contiguous()
+    m = seq_mask.to(torch.float32).contiguous()
+    pl = pair_logits.to(torch.float32).contiguous()
+    if pl.shape != (B, num_heads, N, N):
+        raise NotActive("SingleAttention", f"pair_logits must be [B, H, N, N], got {tuple(pl.shape)}")
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs an explicit out tensor")
+        out = torch.empty_like(sc)
+    code_c = _lib.dtype_code(w_qkvg.dtype)
+    ws_bytes = _lib.lib().pf_single_attn_workspace_bytes(B, N, C, num_heads, code_c)
+    ws = _workspace(ws_bytes, s.device)
+    _lib.call(
+        "pf_single_attn_fwd", sc.data_ptr(), m.data_ptr(), pl.data_ptr(), _f32(ln_w).data_ptr(),
+        _f32(ln_b).data_ptr(), float(eps), w_qkvg.data_ptr(), _f32(q_bias).data_ptr(), w_out.data_ptr(), B, N, C,
+        num_heads, _lib.dtype_code(s.dtype), code_c, out.data_ptr(), int(accumulate), ws.data_ptr(), ws_bytes,
+        _lib.stream_of(sc),
+    )  # fmt: skip
+    return out

@@ -17,26 +17,7 @@ from . import kernel_census
 from .config import OptimConfig, require_hip
 from .inference_guard import NotActive, inference_only
 from .kernels import cast_weight, gemm_dtype_for, pack_trimul_weights, trimul_forward
-from .primitives import LayerNorm, LinearNoBias
-
-
-class WeightCache:
-    """Prepared (cast / packed) weight operands, rebuilt when a parameter changes.
-
-    The key is every parameter's storage pointer and in-place version counter plus
-    the operand dtype, so an optimizer step or ``load_state_dict`` invalidates it.
-    """
-
-    def __init__(self):
-        self._key = None
-        self._val = None
-
-    def get(self, params: list[torch.Tensor], dtype: torch.dtype, build):
-        key = (dtype, tuple((p.data_ptr(), p._version) for p in params))
-        if key != self._key:
-            self._val = build()
-            self._key = key
-        return self._val
+from .primitives import LayerNorm, LinearNoBias, WeightCache
 
 
 class _TriangleMulBase(nn.Module):

@@ -38,6 +38,30 @@ class LinearNoBias(nn.Linear):
         af3_linear_init_(self.weight, initializer)
 
 
+class WeightCache:
+    """Prepared (cast / packed) weight operands, rebuilt when a parameter changes.
+
+    The key is every parameter's storage pointer and in-place version counter plus
+    the operand dtype, so an optimizer step or ``load_state_dict`` invalidates it.
+    """
+
+    def __init__(self):
+        self._key = None
+        self._val = None
+
+    def get(self, params: list[torch.Tensor], dtype: torch.dtype, build):
+        key = (dtype, tuple((p.data_ptr(), p._version) for p in params))
+        if key != self._key:
+            self._val = build()
+            self._key = key
+        return self._val
+
+
+def f32(t: torch.Tensor) -> torch.Tensor:
+    """A detached contiguous fp32 copy (LayerNorm affine and bias operands)."""
+    return t.detach().to(torch.float32).contiguous()
+
+
 class LayerNorm(nn.LayerNorm):
     """LayerNorm with fp32 statistics, output in the input dtype (``primitives.py:90-155``)."""
 
@@ -48,3 +72,74 @@ class LayerNorm(nn.LayerNorm):
         from .kernels import layer_norm
 
         return layer_norm(x, self.weight, self.bias, self.eps)
+
+
+class TransitionBlock(nn.Module):
+    """SwiGLU transition ``y = (silu(a) * b) W2^T`` with ``[a | b] = LN(x) W1^T`` (``primitives.py:193-251``).
+
+    Same parameters and state-dict keys as the reference (``norm.*``, ``linear1.weight``
+    ``[2 n C, C]``, ``linear2.weight`` ``[C, n C]``; ``fused_transition.py:63-65``). C=128 with
+    factor 4 runs the fused pair-transition kernel (hidden activations stay on chip); any
+    other shape runs LayerNorm + two MFMA row GEMMs.
+    """
+
+    def __init__(self, c: int, n: int = 4, optim=None, linear_out_init_gain: float | None = None):
+        super().__init__()
+        from .config import require_hip
+
+        require_hip("TransitionBlock", optim)
+        self.c, self.n = c, n
+        self.norm = LayerNorm(c)
+        self.linear1 = LinearNoBias(c, 2 * n * c)
+        self.linear2 = LinearNoBias(n * c, c, initializer="zeros")
+        if linear_out_init_gain is not None:
+            nn.init.normal_(self.linear2.weight, std=linear_out_init_gain / math.sqrt(n * c))
+        self._cache = WeightCache()
+
+    @property
+    def fused_pair(self) -> bool:
+        return self.c == 128 and self.n == 4
+
+    def operands(self, cdt: torch.dtype) -> dict:
+        from .kernels import cast_weight
+
+        params = [self.norm.weight, self.norm.bias, self.linear1.weight, self.linear2.weight]
+
+        def build():
+            return dict(
+                w1=cast_weight(self.linear1.weight, cdt), w2=cast_weight(self.linear2.weight, cdt),
+                lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
+            )  # fmt: skip
+
+        return self._cache.get(params, cdt, build)
+
+    def run(self, x: torch.Tensor, out=None, accumulate: bool = False, s2p=None):
+        from . import kernel_census
+        from .kernels import gemm_dtype_for, pair_transition_forward, transition_forward
+
+        op = self.operands(gemm_dtype_for(x))
+        if self.fused_pair:
+            kernel_census.record("TransitionBlock", "hip_pair_transition")
+            return pair_transition_forward(
+                x, op["lnw"], op["lnb"], self.norm.eps, op["w1"], op["w2"], out=out, accumulate=accumulate, s2p=s2p
+            )
+        if s2p is not None:
+            raise ValueError("the single_to_pair epilogue is fused only into the C=128 pair transition")
+        kernel_census.record("TransitionBlock", "hip_transition")
+        return transition_forward(x, op["lnw"], op["lnb"], self.norm.eps, op["w1"], op["w2"], out, accumulate), None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        from .inference_guard import InferenceOnlyKernelError
+
+        if torch.is_grad_enabled():
+            raise InferenceOnlyKernelError("TransitionBlock is forward-only: call it under torch.no_grad().")
+        return self.run(x)[0]
+
+    def forward_residual_(self, x: torch.Tensor, s2p=None):
+        """``x += transition(x)`` in place; returns ``(x, pair_logits or None)``."""
+        return self.run(x, out=x, accumulate=True, s2p=s2p)
+
+
+def make_transition_block(c: int, n: int = 4, config=None, linear_out_init_gain: float | None = None):
+    """Reference factory (``optim.py:50-105``): one implementation here, the HIP one."""
+    return TransitionBlock(c, n, optim=config, linear_out_init_gain=linear_out_init_gain)

@@ -84,6 +84,59 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
                   const void* w_out, const void* w_out_gate, int B, int N, int C, int outgoing, int zdtype, int cdtype,
                   void* out, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
 
+
+/* ---- triangle attention (starting / ending node) ------------------------ */
+/* Whole-module GridSelfAttention forward: replaces GridSelfAttention.forward
+ * (src/deepfold3/model/attention.py:167-269) with its kernel chain FusedPairBias
+ * (triton/fused_pair_bias.py:348-416) -> LN(+transpose) (triton/layernorm_transpose.py:269-316)
+ * -> q/k/v/g projections -> _EvoformerAttention.apply (triton/evo_attention.py:1198-1292)
+ * -> gate -> out_proj, and the dropout_add that consumes its output (eval: a plain add).
+ *
+ * z [B,N,N,C] (zdtype); mask [B,N,N] fp32 (pair mask, 1 keep / 0 pad); LN params fp32;
+ * w_qkvgb [4C+16, C] cdtype: rows to_q | to_k | to_v | to_g | pair_bias (H rows) | zeros;
+ * w_out [C, C] cdtype. transpose=0: starting node (rows), 1: ending node (columns).
+ * Writes the update to `out`, or adds it into `out` when accumulate != 0 (out == z is the
+ * fused residual). Masking follows the reference's eager path: keys with mask 0 get
+ * -1e9 added in fp32, so a fully masked line attends uniformly (mean of V); the Triton
+ * kernel's zero-output rule for such lines is not used. Built: C=128, H=4 (head dim 32). */
+size_t pf_grid_attn_workspace_bytes(int B, int N, int C, int H, int cdtype);
+int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const float* ln_b, float eps,
+                     const void* w_qkvgb, const void* w_out, int B, int N, int C, int H, int transpose, int zdtype,
+                     int cdtype, void* out, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- transitions ------------------------------------------------------- */
+/* Pair transition, C=128, factor 4: replaces FusedTransitionBlock / TransitionBlock.forward
+ * (triton/fused_transition.py:34-83, primitives.py:193-251; FusedLayerNormLinear
+ * triton/layernorm_linear.py:537-592 and FusedSwiGLU triton/swiglu.py:192-200 inside it).
+ * x [M, C] zdtype; w1 [2*factor*C, C], w2 [C, factor*C] cdtype. out = y or out += y.
+ * Optional fused single_to_pair (evoformer.py:322-328): when pair_logits != NULL, the
+ * updated rows are normalised with (s2p_ln_w, s2p_ln_b) and projected by w_s2p [16, C]
+ * into pair_logits [M/NN, 16, NN] fp32 (NN = N*N positions per batch item). */
+int pf_pair_transition_fwd(const void* x, const float* ln_w, const float* ln_b, float eps, const void* w1,
+                           const void* w2, long M, int C, int factor, int zdtype, int cdtype, void* out, int accumulate,
+                           const float* s2p_ln_w, const float* s2p_ln_b, float s2p_eps, const void* w_s2p,
+                           float* pair_logits, long NN, void* stream);
+/* single_to_pair(single_to_pair_norm(z)).movedim(-1, -3) (evoformer.py:322-328):
+ * z [M, C] -> pair_logits [M/NN, H, NN] fp32. Built: C=128, H=16. */
+int pf_single_to_pair_fwd(const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_s2p, long M,
+                          int C, int H, long NN, int zdtype, int cdtype, float* pair_logits, void* stream);
+/* Generic TransitionBlock.forward (primitives.py:193-251) for any C (the single
+ * transition, C=384): LN -> w1 [2fC, C] -> SwiGLU (contiguous halves) -> w2 [C, fC]. */
+size_t pf_transition_workspace_bytes(long M, int C, int factor, int cdtype);
+int pf_transition_fwd(const void* x, const float* ln_w, const float* ln_b, float eps, const void* w1, const void* w2,
+                      long M, int C, int factor, int zdtype, int cdtype, void* out, int accumulate, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* ---- single attention with pair bias ----------------------------------- */
+/* SingleAttention.forward (attention.py:344-452), pair_bias_gate off: s [B,N,C] zdtype;
+ * seq_mask [B,N] fp32; pair_logits [B,H,N,N] fp32; w_qkvg [4C, C] cdtype rows
+ * to_q | to_k | to_v | to_g; q_bias [C] fp32; w_out [C, C]. Head dim C/H must be 24. */
+size_t pf_single_attn_workspace_bytes(int B, int N, int C, int H, int cdtype);
+int pf_single_attn_fwd(const void* s, const float* seq_mask, const float* pair_logits, const float* ln_w,
+                       const float* ln_b, float eps, const void* w_qkvg, const float* q_bias, const void* w_out, int B,
+                       int N, int C, int H, int zdtype, int cdtype, void* out, int accumulate, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

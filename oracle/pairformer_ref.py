@@ -52,9 +52,11 @@ def _sub(p: dict[str, torch.Tensor], prefix: str) -> dict[str, torch.Tensor]:
 
 def _triangle_matmul(a: torch.Tensor, b: torch.Tensor, outgoing: bool) -> torch.Tensor:
     """``bikc,bjkc->bijc`` (outgoing) or ``bkjc,bkic->bijc`` (incoming), ``ops.py:58-98``."""
+    # Both operands are made contiguous before the batched product (same values; a
+    # transposed-view right operand of a bf16 batched matmul is avoided on ROCm).
     if outgoing:
-        return torch.matmul(a.permute(0, 3, 1, 2), b.permute(0, 3, 2, 1)).permute(0, 2, 3, 1)
-    return torch.matmul(a.permute(0, 3, 2, 1), b.permute(0, 3, 1, 2)).permute(0, 3, 2, 1)
+        return torch.matmul(a.permute(0, 3, 1, 2).contiguous(), b.permute(0, 3, 2, 1).contiguous()).permute(0, 2, 3, 1)
+    return torch.matmul(a.permute(0, 3, 2, 1).contiguous(), b.permute(0, 3, 1, 2).contiguous()).permute(0, 3, 2, 1)
 
 
 def tri_mul(z: torch.Tensor, mask: torch.Tensor, p: dict[str, torch.Tensor], outgoing: bool) -> torch.Tensor:
@@ -99,7 +101,7 @@ def _grid_attention_rows(
     scale = D**-0.5
     q = F.linear(z_flat, p["to_q.weight"]).view(B * N_rows, N_cols, H, D).permute(0, 2, 1, 3)
     k = F.linear(z_flat, p["to_k.weight"]).view(B * N_rows, N_cols, H, D).permute(0, 2, 1, 3)
-    v = F.linear(z_flat, p["to_v.weight"]).view(B * N_rows, N_cols, H, D).permute(0, 2, 1, 3)
+    v = F.linear(z_flat, p["to_v.weight"]).view(B * N_rows, N_cols, H, D).permute(0, 2, 1, 3).contiguous()
     logits = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale
     logits = logits.view(B, N_rows, H, N_cols, N_cols)
     logits = logits + pb.unsqueeze(1)
@@ -176,7 +178,7 @@ def single_attention(
     xn = layer_norm(s, p["norm.weight"], p["norm.bias"])
     q = F.linear(xn, p["to_q.weight"], p["to_q.bias"]).view(B, N, H, Dk).permute(0, 2, 1, 3)
     k = F.linear(xn, p["to_k.weight"]).view(B, N, H, Dk).permute(0, 2, 1, 3)
-    v = F.linear(xn, p["to_v.weight"]).view(B, N, H, Dv).permute(0, 2, 1, 3)
+    v = F.linear(xn, p["to_v.weight"]).view(B, N, H, Dv).permute(0, 2, 1, 3).contiguous()
     logits = torch.matmul(q * Dk**-0.5, k.transpose(-2, -1).contiguous())
     logits = logits + pair_logits
     logits = logits + (1e9 * (seq_mask.float() - 1.0)).view(B, 1, 1, N)
