@@ -29,6 +29,9 @@ SIGNATURES: dict[str, tuple] = {
     "pf_version": (_i, []),
     "pf_last_error": (ctypes.c_char_p, []),
     "pf_last_error_code": (_i, []),
+    "pf_kernel_timer_start": (_i, [ctypes.c_char_p]),
+    "pf_kernel_timer_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_long)]),
+    "pf_kernel_timer_stop": (_i, []),
     "pf_cast": (_i, [_vp, _i, _vp, _i, _sz, _vp]),
     "pf_add": (_i, [_vp, _i, _vp, _i, _vp, _sz, _vp]),
     "pf_layernorm_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, ctypes.c_long, _i, _vp]),
@@ -128,3 +131,19 @@ def require_device(name: str, *ts: torch.Tensor) -> None:
             continue
         if not t.is_cuda:
             raise NotActive(name, "tensors must be on a ROCm GPU; this build has no CPU path")
+
+
+def kernel_timer_start(kernel: str) -> None:
+    """Bracket every later launch of ``kernel`` with HIP events on its stream (totals reset)."""
+    call("pf_kernel_timer_start", kernel.encode())
+
+
+def kernel_timer_read() -> tuple[float, int]:
+    """(summed duration in ms, launch count) of the timed kernel so far; waits for its events."""
+    total, count = ctypes.c_double(0.0), ctypes.c_long(0)
+    call("pf_kernel_timer_read", ctypes.byref(total), ctypes.byref(count))
+    return total.value, count.value
+
+
+def kernel_timer_stop() -> None:
+    call("pf_kernel_timer_stop")

@@ -506,8 +506,10 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
   {
     constexpr int BM = proj_bm<TC>();
     dim3 grid(Np / BM, Np, B);
+    pf::KernelTimer timer_attn_project("attn_project", s);
     attn_project_kernel<TZ, TC><<<grid, 256, 0, s>>>((const TZ*)z, mask, lnw, lnb, eps, (const TC*)w5, Qb, Kb, Vb,
                                                      Gb, PBb, MAb, N, Np, transpose, qscale);
+    timer_attn_project.stop();
     if (int e = pf::check_launch("attn_project")) return e;
   }
   {
@@ -516,16 +518,20 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     const long total = (long)B * nlg * kHeads * nqb;
     const int remap = (total % 8 == 0) ? 1 : 0;
     dim3 grid((unsigned)total);
+    pf::KernelTimer timer("tri_attn", s);
     if (transpose)
       tri_attn_kernel<TC, true><<<grid, 256, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, remap);
     else
       tri_attn_kernel<TC, false><<<grid, 256, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, remap);
+    timer.stop();
     if (int e = pf::check_launch("tri_attn")) return e;
   }
   {
     constexpr int BM = proj_bm<TC>();
     dim3 grid((N + BM - 1) / BM, N, B);
+    pf::KernelTimer timer_attn_out("attn_out", s);
     attn_out_kernel<TZ, TC><<<grid, 256, 0, s>>>(Ob, Gb, (const TC*)wo, (TZ*)out, N, Np, transpose, accumulate);
+    timer_attn_out.stop();
     if (int e = pf::check_launch("attn_out")) return e;
   }
   return pf::ok();

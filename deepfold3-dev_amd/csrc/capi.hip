@@ -4,6 +4,11 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
+
 #include "capi.h"
 #include "common.h"
 
@@ -35,6 +40,42 @@ int check_launch(const char* what) {
   return ok();
 }
 
+// ---- kernel timer: events recorded around one selected launch site
+namespace {
+std::mutex g_timer_mu;
+std::string g_timer_name;  // empty: timing off
+std::vector<hipEvent_t> g_free_events;
+std::vector<std::pair<hipEvent_t, hipEvent_t>> g_pending;
+double g_timer_total_ms = 0.0;
+long g_timer_count = 0;
+
+hipEvent_t take_event() {
+  if (!g_free_events.empty()) {
+    hipEvent_t e = g_free_events.back();
+    g_free_events.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+}  // namespace
+
+KernelTimer::KernelTimer(const char* name, hipStream_t stream) : stream_(stream) {
+  std::lock_guard<std::mutex> lk(g_timer_mu);
+  if (g_timer_name.empty() || g_timer_name != name) return;
+  hipEvent_t e = take_event();
+  if (e && hipEventRecord(e, stream_) == hipSuccess) start_ = e;
+}
+
+void KernelTimer::stop() {
+  if (!start_) return;
+  std::lock_guard<std::mutex> lk(g_timer_mu);
+  hipEvent_t e = take_event();
+  if (e && hipEventRecord(e, stream_) == hipSuccess) g_pending.emplace_back((hipEvent_t)start_, e);
+  start_ = nullptr;
+}
+
 }  // namespace pf
 
 template <class TS, class TD>
@@ -58,6 +99,45 @@ static unsigned grid_for(size_t n) {
 extern "C" {
 
 const char* pf_last_error(void) { return pf::g_err; }
+
+int pf_kernel_timer_start(const char* kernel) {
+  PF_REQUIRE(kernel != nullptr, PF_ERR_INVALID_ARG, "pf_kernel_timer_start: null name");
+  std::lock_guard<std::mutex> lk(pf::g_timer_mu);
+  pf::g_timer_name = kernel;
+  pf::g_timer_total_ms = 0.0;
+  pf::g_timer_count = 0;
+  for (auto& pr : pf::g_pending) {
+    pf::g_free_events.push_back(pr.first);
+    pf::g_free_events.push_back(pr.second);
+  }
+  pf::g_pending.clear();
+  return pf::ok();
+}
+
+int pf_kernel_timer_read(double* total_ms, long* count) {
+  PF_REQUIRE(total_ms && count, PF_ERR_INVALID_ARG, "pf_kernel_timer_read: null pointer");
+  std::lock_guard<std::mutex> lk(pf::g_timer_mu);
+  for (auto& pr : pf::g_pending) {
+    float ms = 0.f;
+    hipError_t e = hipEventSynchronize(pr.second);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, pr.first, pr.second);
+    PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "pf_kernel_timer_read: %s", hipGetErrorString(e));
+    pf::g_timer_total_ms += ms;
+    pf::g_timer_count += 1;
+    pf::g_free_events.push_back(pr.first);
+    pf::g_free_events.push_back(pr.second);
+  }
+  pf::g_pending.clear();
+  *total_ms = pf::g_timer_total_ms;
+  *count = pf::g_timer_count;
+  return pf::ok();
+}
+
+int pf_kernel_timer_stop(void) {
+  std::lock_guard<std::mutex> lk(pf::g_timer_mu);
+  pf::g_timer_name.clear();
+  return pf::ok();
+}
 int pf_last_error_code(void) { return pf::g_err_code; }
 int pf_version(void) { return PF_ABI_VERSION; }
 

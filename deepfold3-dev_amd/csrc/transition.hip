@@ -179,6 +179,7 @@ int transition_launch(const void* x, const float* lnw, const float* lnb, float e
                       const void* ws2p, float* logits, long NN, hipStream_t s) {
   constexpr int BM = tr_bm<TC>();
   dim3 grid((unsigned)((M + BM - 1) / BM));
+  pf::KernelTimer timer("pair_transition", s);
   if (logits)
     pair_transition_kernel<TZ, TC, true><<<grid, 256, 0, s>>>((const TZ*)x, (TZ*)out, lnw, lnb, eps, (const TC*)w1,
                                                              (const TC*)w2, M, accumulate, s2p_w, s2p_b, s2p_eps,
@@ -187,6 +188,7 @@ int transition_launch(const void* x, const float* lnw, const float* lnb, float e
     pair_transition_kernel<TZ, TC, false><<<grid, 256, 0, s>>>((const TZ*)x, (TZ*)out, lnw, lnb, eps, (const TC*)w1,
                                                               (const TC*)w2, M, accumulate, nullptr, nullptr, 0.f,
                                                               nullptr, nullptr, NN);
+  timer.stop();
   return pf::check_launch("pair_transition");
 }
 

@@ -410,8 +410,10 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
   {
     constexpr int BM = trimul_bm<TC>();
     dim3 grid(Np / BM, Np, B);
+    pf::KernelTimer timer_trimul_project("trimul_project", s);
     trimul_project_kernel<TZ, TC, C><<<grid, 256, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const TC*)w4,
                                                           planes, B, N, Np, outgoing);
+    timer_trimul_project.stop();
     if (int e = pf::check_launch("trimul_project")) return e;
   }
   {
@@ -428,15 +430,19 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     const int tiles = (Np / Cfg::BMN) * (Np / Cfg::BMN);
     const int remap = (G % 8 == 0) ? 1 : 0;
     dim3 grid((unsigned)(G * tiles));
+    pf::KernelTimer timer_trimul_contract("trimul_contract", s);
     trimul_contract_kernel<TC><<<grid, 256, Cfg::SMEM, s>>>(P, Q, X, G, Np, remap);
+    timer_trimul_contract.stop();
     if (int e = pf::check_launch("trimul_contract")) return e;
   }
   {
     constexpr int BM = trimul_bm<TC>();
     dim3 grid((N + BM - 1) / BM, N, B);
+    pf::KernelTimer timer_trimul_output("trimul_output", s);
     trimul_output_kernel<TZ, TC, C><<<grid, 256, 0, s>>>(X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow, lnob,
                                                          eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
                                                          accumulate);
+    timer_trimul_output.stop();
     if (int e = pf::check_launch("trimul_output")) return e;
   }
   return pf::ok();

@@ -44,6 +44,17 @@ int pf_version(void);
 const char* pf_last_error(void);
 int pf_last_error_code(void);
 
+/* Kernel timer (no counterpart in the reference; the reference times kernels with CUDA
+ * events in benchmarks/utils.py:58-120). pf_kernel_timer_start(name) selects one launch
+ * site ("trimul_project", "trimul_contract", "trimul_output", "attn_project", "tri_attn",
+ * "attn_out", "pair_transition") and resets the totals; every later launch of that site
+ * is bracketed by HIP events recorded on its own stream. pf_kernel_timer_read waits for
+ * the recorded events and returns the summed duration and launch count so far;
+ * pf_kernel_timer_stop switches timing off. Host-side state, guarded by a mutex. */
+int pf_kernel_timer_start(const char* kernel);
+int pf_kernel_timer_read(double* total_ms, long* count);
+int pf_kernel_timer_stop(void);
+
 /* dst[i] = (dst dtype) src[i]. Used to cast weights once per module version. */
 int pf_cast(const void* src, int src_dtype, void* dst, int dst_dtype, size_t n, void* stream);
 
