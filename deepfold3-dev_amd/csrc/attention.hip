@@ -19,15 +19,18 @@
 // Frames. "line" is the attention row: i for the starting node (row mode), j for the
 // ending node (column mode). Keys and queries run along the other token index. The
 // projection kernel walks z along a line in both modes (column mode reads z down a column),
-// so every operand is written contiguously in the attention frame.
+// so every operand is written contiguously in the attention frame. The pair bias is
+// stored query-major [h][q][key slot] in row mode and key-major [h][key][q] in column mode
+// (again the order in which the projection produces it); the attention kernel stages it
+// through LDS either way.
 //
 // MFMA layout (v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x2f32). A wave owns 32 queries
 // per sub-block and computes S^T = K Q^T (keys are accumulator rows), so lane (q, h)
 // (q = lane & 31, h = lane >> 5) holds the logits of query q for keys
 // kappa(r, h) = 8 (r >> 2) + 4 h + (r & 3), r = 0..15. Those 16 probabilities are exactly
 // the B operand lane (q, h) must supply for O^T += V^T P^T when the keys of a 32-block are
-// stored in the order kappa (storage slot 16 h + r holds key kappa(r, h)): Vt, PB (row
-// mode) and MA are written in that order, so P never goes through LDS.
+// stored in the order kappa (storage slot 16 h + r holds key kappa(r, h)): Vt, PB and MA
+// use that order, so P never goes through LDS.
 #include "capi.h"
 #include "common.h"
 
@@ -36,26 +39,17 @@ namespace {
 constexpr int kHeads = 4;
 constexpr int kHeadDim = 32;
 constexpr int kC = 128;
+constexpr int kPad = 128;  // token padding of the attention frame
 
 // Storage slot -> key inside a 32-key block, and its inverse.
 PF_DEVICE int slot_key(int slot) { return 8 * ((slot & 15) >> 2) + 4 * (slot >> 4) + (slot & 3); }
 PF_DEVICE int key_slot(int key) { return 16 * ((key >> 2) & 1) + 4 * (key >> 3) + (key & 3); }
 
-template <class TC>
-constexpr int proj_bm() { return sizeof(TC) == 2 ? 64 : 32; }
-
 // ------------------------------------------------------------------ A1
 // w5 [4C + 16][C] (cdtype): rows q | k | v | g | pb (H rows) | zero padding.
-template <class TZ, class TC>
-struct ProjCfg {
-  static constexpr int BM = proj_bm<TC>();
-  static constexpr int ALD = kC + lds_pad<TC>();
-  static constexpr int SLD = kC + lds_pad<TC>();
-  static constexpr int A_BYTES = BM * ALD * (int)sizeof(TC);
-  static constexpr int S_BYTES = 4 * BM * SLD * (int)sizeof(TC);
-  static constexpr int SMEM = A_BYTES > S_BYTES ? A_BYTES : S_BYTES;
-};
-
+// Block: BM positions of one line; 4 waves in 2 x 2 (positions x channels), each 32x32
+// MFMA tiles. The four 128-row weight chunks go through one LDS buffer, which doubles as
+// the staging tile for the chunk's output.
 template <class TZ, class TC>
 __global__ __launch_bounds__(256) void attn_project_kernel(const TZ* __restrict__ z, const float* __restrict__ mask,
                                                            const float* __restrict__ lnw, const float* __restrict__ lnb,
@@ -64,15 +58,16 @@ __global__ __launch_bounds__(256) void attn_project_kernel(const TZ* __restrict_
                                                            TC* __restrict__ G, float* __restrict__ PB,
                                                            float* __restrict__ MA, int N, int Np, int transpose,
                                                            float qscale) {
-  using Cfg = ProjCfg<TZ, TC>;
-  constexpr int BM = Cfg::BM, ALD = Cfg::ALD, SLD = Cfg::SLD;
+  constexpr int BM = block_rows<TC>();
+  constexpr int LD = ld128<TC>();
   constexpr int NT = 256;
-  constexpr int RB = BM / 16;
+  constexpr int WM = BM / 2;  // positions per wave
+  constexpr int PT = WM / 32;
   constexpr int VEC = 16 / sizeof(TC);
-  __shared__ __attribute__((aligned(16))) char smem[Cfg::SMEM];
+  __shared__ __attribute__((aligned(16))) TC X[BM * LD];
+  __shared__ __attribute__((aligned(16))) TC WS[128 * LD];
   __shared__ float pbs[BM][kHeads];
   __shared__ float mks[BM];
-  TC* A = reinterpret_cast<TC*>(smem);
 
   const int t0 = blockIdx.x * BM;
   const int line = blockIdx.y;
@@ -80,121 +75,144 @@ __global__ __launch_bounds__(256) void attn_project_kernel(const TZ* __restrict_
   const int tid = threadIdx.x;
   const int w = wave_id();
   const int l = lane_id();
+  const int wr = w >> 1, wc = w & 1;
   const TZ* zb = z + (size_t)b * N * N * kC;
   auto pos_of = [&](int p) -> long {
     const int t = t0 + p;
     if (line >= N || t >= N) return -1;
     return transpose ? (long)t * N + line : (long)line * N + t;
   };
-  auto rowptr = [&](int p) -> const TZ* {
+  Rows128<TC, 128, NT> wpf;
+  wpf.load(w5, kC);
+  ln_tile_to_lds<TZ, TC, kC, BM, NT>([&](int p) -> const TZ* {
     const long pos = pos_of(p);
     return pos < 0 ? nullptr : zb + pos * kC;
-  };
-  ln_tile_to_lds<TZ, TC, kC, BM, NT>(rowptr, lnw, lnb, eps, A, ALD);
+  }, lnw, lnb, eps, X, LD);
   if (tid < BM) {
     const long pos = pos_of(tid);
     mks[tid] = pos < 0 ? 0.f : mask[(size_t)b * N * N + pos];
   }
-  __syncthreads();
+  const size_t lineq = (size_t)b * Np + line;  // [b][line] over the padded frame
 
-  // Wave w computes kind w (q, k, v, g) for all BM rows; the pair-bias block is split by
-  // row blocks over the waves.
-  f32x4 acc[RB][8];
-  zero_acc(acc);
-  int wrow0[8];
+#pragma unroll 1
+  for (int kind = 0; kind < 4; ++kind) {
+    __syncthreads();  // previous chunk's stage fully consumed
+    wpf.store(WS, LD);
+    __syncthreads();
+    if (kind < 3) wpf.load(w5 + (size_t)(kind + 1) * 128 * kC, kC);
+    if (kind != 2) {
+      // position-major output: acc^T = W X^T, lane holds 4 consecutive channels
+      f32x16 acc[2][PT];
+      zero_acc32(acc);
+      wave_mma32<TC, 2, PT, kC>(acc, WS, LD, wc * 64, X, LD, wr * WM);
+      __syncthreads();  // WS becomes the stage [pos][ch]
 #pragma unroll
-  for (int j = 0; j < 8; ++j) wrow0[j] = w * kC + j * 16;
-  gemm16_lds_x_w<TC, kC, RB, 8>(acc, A, ALD, 0, w5, kC, wrow0);
-  f32x4 accb[1][1];
-  zero_acc(accb);
-  const bool has_pb_rows = w < RB;
-  if (has_pb_rows) {
+      for (int ci = 0; ci < 2; ++ci)
+#pragma unroll
+        for (int pj = 0; pj < PT; ++pj)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float x = acc[ci][pj][4 * g4 + e];
+              if (kind == 0) x *= qscale;
+              if (kind == 3) x = sigmoidf_(x);
+              v[e] = x;
+            }
+            const int ch = wc * 64 + 32 * ci + acc32_row(4 * g4);
+            const int p = wr * WM + 32 * pj + (l & 31);
+            store_vec<TC, 4>(WS + p * LD + ch, v);
+          }
+    } else {
+      // channel-major output (Vt): acc = X W^T, lane holds 4 consecutive positions
+      f32x16 acc[PT][2];
+      zero_acc32(acc);
+      wave_mma32<TC, PT, 2, kC>(acc, X, LD, wr * WM, WS, LD, wc * 64);
+      __syncthreads();  // WS becomes the stage [ch][slot]
+#pragma unroll
+      for (int pi = 0; pi < PT; ++pi)
+#pragma unroll
+        for (int cj = 0; cj < 2; ++cj)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[pi][cj][4 * g4 + e];
+            const int p = wr * WM + 32 * pi + acc32_row(4 * g4);
+            const int ch = wc * 64 + 32 * cj + (l & 31);
+            store_vec<TC, 4>(WS + ch * LD + (p & ~31) + key_slot(p & 31), v);
+          }
+    }
+    __syncthreads();
+    if (kind == 0 || kind == 1) {
+      // Q / K: [b][line][h][t][d]; per head BM x D contiguous.
+      TC* dst = (kind == 0 ? Q : K) + lineq * kHeads * Np * kHeadDim;
+      constexpr int CPP = kHeadDim / VEC;  // chunks per (position, head)
+#pragma unroll
+      for (int it = 0; it < BM * kC / VEC / NT; ++it) {
+        const int idx = tid + it * NT;
+        const int hh = idx / (BM * CPP);
+        const int r = idx % (BM * CPP);
+        const int p = r / CPP;
+        const int d0 = (r % CPP) * VEC;
+        *reinterpret_cast<u32x4*>(dst + ((size_t)hh * Np + t0 + p) * kHeadDim + d0) =
+            *reinterpret_cast<const u32x4*>(WS + p * LD + hh * kHeadDim + d0);
+      }
+    } else if (kind == 2) {
+      // Vt: [b][line][h][d][slot]
+      TC* dst = Vt + lineq * kHeads * kHeadDim * Np + t0;
+      constexpr int CPR = BM / VEC;
+#pragma unroll
+      for (int it = 0; it < BM * kC / VEC / NT; ++it) {
+        const int idx = tid + it * NT;
+        const int c = idx / CPR;
+        const int s0 = (idx % CPR) * VEC;
+        *reinterpret_cast<u32x4*>(dst + (size_t)c * Np + s0) = *reinterpret_cast<const u32x4*>(WS + c * LD + s0);
+      }
+    } else {
+      // G = sigmoid(g): [b][line][t][C]
+      TC* dst = G + (lineq * Np + t0) * kC;
+      constexpr int CPR = kC / VEC;
+#pragma unroll
+      for (int it = 0; it < BM * kC / VEC / NT; ++it) {
+        const int idx = tid + it * NT;
+        const int p = idx / CPR;
+        const int c0 = (idx % CPR) * VEC;
+        *reinterpret_cast<u32x4*>(dst + (size_t)p * kC + c0) = *reinterpret_cast<const u32x4*>(WS + p * LD + c0);
+      }
+    }
+  }
+
+  // Pair bias: one 16-column block (H real columns) over BM rows, BM/4 rows per wave.
+  {
+    constexpr int RB = BM / 4 / 16;
+    f32x4 accb[RB][1];
+    zero_acc(accb);
     int prow[1] = {4 * kC};
-    gemm16_lds_x_w<TC, kC, 1, 1>(accb, A, ALD, w * 16, w5, kC, prow);
-  }
-  __syncthreads();  // A is dead: reuse as four per-kind stage tiles S[w] [BM][SLD]
-
-  TC* S = reinterpret_cast<TC*>(smem) + w * BM * SLD;
+    gemm16_lds_x_w<TC, kC, RB, 1>(accb, X, LD, w * (BM / 4), w5, kC, prow);
+    if ((l & 15) < kHeads) {
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int p = rb * 16 + 4 * (l >> 4) + e;
-        const int c = j * 16 + (l & 15);
-        float v = acc[rb][j][e];
-        if (w == 0) v *= qscale;
-        if (w == 3) v = sigmoidf_(v);
-        S[p * SLD + c] = from_f32<TC>(v);
-      }
-  if (has_pb_rows && (l & 15) < kHeads) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) pbs[w * 16 + 4 * (l >> 4) + e][l & 15] = accb[0][0][e] * kLog2e;
+        for (int e = 0; e < 4; ++e) pbs[w * (BM / 4) + rb * 16 + 4 * (l >> 4) + e][l & 15] = accb[rb][0][e] * kLog2e;
+    }
   }
   __syncthreads();
-
-  const size_t lineq = (size_t)b * Np + line;  // [b][line] index over the padded frame
   const bool line_ok = line < N;
-  if (w <= 1) {
-    // Q / K: [b][line][h][t][d]; per head BM x D contiguous.
-    TC* dst = (w == 0 ? Q : K) + lineq * kHeads * Np * kHeadDim;
-    constexpr int CPH = BM * kHeadDim / VEC;  // chunks per head
-    for (int idx = l; idx < kHeads * CPH; idx += 64) {
-      const int hh = idx / CPH;
-      const int r = idx % CPH;
-      const int p = r / (kHeadDim / VEC);
-      const int d0 = (r % (kHeadDim / VEC)) * VEC;
-      u32x4 v = *reinterpret_cast<const u32x4*>(S + p * SLD + hh * kHeadDim + d0);
-      if (!line_ok || t0 + p >= N) v = u32x4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4*>(dst + ((size_t)hh * Np + t0 + p) * kHeadDim + d0) = v;
-    }
-  } else if (w == 2) {
-    // Vt: [b][line][h][d][slot], keys permuted inside each 32-block.
-    TC* dst = Vt + lineq * kHeads * kHeadDim * Np;
-    constexpr int CPR = BM / VEC;  // chunks per (h, d) row
-    for (int idx = l; idx < kC * CPR; idx += 64) {
-      const int c = idx / CPR;
-      const int s0 = (idx % CPR) * VEC;  // slot offset inside the tile (tile is 32-aligned)
-      float v[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const int s = s0 + e;
-        const int p = (s & ~31) + slot_key(s & 31);
-        v[e] = (line_ok && t0 + p < N) ? to_f32(S[p * SLD + c]) : 0.f;
-      }
-      store_vec<TC, VEC>(dst + (size_t)c * Np + t0 + s0, v);
-    }
-  } else {
-    // G = sigmoid(g): [b][line][t][C]
-    TC* dst = G + lineq * Np * kC;
-    constexpr int CPR = kC / VEC;
-    for (int idx = l; idx < BM * CPR; idx += 64) {
-      const int p = idx / CPR;
-      const int c0 = (idx % CPR) * VEC;
-      *reinterpret_cast<u32x4*>(dst + (size_t)(t0 + p) * kC + c0) =
-          *reinterpret_cast<const u32x4*>(S + p * SLD + c0);
-    }
-  }
-  // Pair bias and key mask (tiny): one thread per (head, position).
   for (int idx = tid; idx < kHeads * BM; idx += NT) {
     const int hh = idx / BM;
     const int p = idx % BM;
     const int t = t0 + p;
-    const bool ok = line_ok && t < N;
-    const float v = ok ? pbs[p][hh] : 0.f;
-    if (transpose) {
-      // key-major [b][h][key = line][query = t]
+    const float v = (line_ok && t < N) ? pbs[p][hh] : 0.f;
+    if (transpose)  // key-major [b][h][key = line][query = t]
       PB[(((size_t)b * kHeads + hh) * Np + line) * Np + t] = v;
-    } else {
-      // query-major [b][h][query = line][slot(key = t)]
+    else  // query-major [b][h][query = line][slot(key = t)]
       PB[(((size_t)b * kHeads + hh) * Np + line) * Np + (t & ~31) + key_slot(t & 31)] = v;
-    }
   }
   if (tid < BM) {
     const int t = t0 + tid;
-    const float m = mks[tid];
-    const float v = t < N ? (m - 1.0f) * 1e9f * kLog2e : -INFINITY;
+    const float v = t < N ? (mks[tid] - 1.0f) * 1e9f * kLog2e : -INFINITY;
     MA[lineq * Np + (t & ~31) + key_slot(t & 31)] = v;
   }
 }
@@ -233,7 +251,7 @@ PF_DEVICE void mma32_16(f32x16& acc, const Frag16<float>& a, const Frag16<float>
 }
 
 // P^T as a B operand from 16 fp32 probabilities.
-PF_DEVICE Frag16<bf16> pack_p(const float (&p)[16], bf16) {
+PF_DEVICE Frag16<bf16> pack_p(const f32x16& p, bf16) {
   Frag16<bf16> f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -242,39 +260,53 @@ PF_DEVICE Frag16<bf16> pack_p(const float (&p)[16], bf16) {
   }
   return f;
 }
-PF_DEVICE Frag16<float> pack_p(const float (&p)[16], float) {
+PF_DEVICE Frag16<float> pack_p(const f32x16& p, float) {
   Frag16<float> f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) f.v[i] = f32x4{p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]};
   return f;
 }
 
-constexpr int kQSub = 2;                 // 32-query sub-blocks per wave
-constexpr int kQBlock = 32 * kQSub;      // queries per wave
-constexpr int kLinesPerBlock = 4;        // one line per wave
+template <class TC>
+constexpr int attn_qsub() { return sizeof(TC) == 2 ? 4 : 2; }  // 32-query sub-blocks per wave
+constexpr int kLinesPerBlock = 4;                                 // one line per wave
+constexpr int kBiasLd = 36;                                       // LDS row of 32 slots + pad (floats)
+// Rescale the running sums only when a block's maximum exceeds the running reference by
+// more than this (base-2 units): probabilities stay <= 2^8, far inside fp32 and bf16 range,
+// and the normalised result does not depend on the reference.
+constexpr float kRescaleSlack = 8.0f;
 
+// Block: 4 waves = 4 consecutive lines, one head, QB = 32 * QS queries. The pair-bias tile
+// (shared by the 4 lines) is staged through LDS, double-buffered; K and V are per line
+// and loaded straight into MFMA operand registers, one key block ahead.
 template <class TC, bool BIAS_KEY_MAJOR>
 __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__ Q, const TC* __restrict__ K,
                                                           const TC* __restrict__ Vt, const float* __restrict__ PB,
                                                           const float* __restrict__ MA, TC* __restrict__ O, int B,
                                                           int N, int Np, int xcd_remap) {
-  const int nqb = Np / kQBlock;
+  constexpr int QS = attn_qsub<TC>();
+  constexpr int QB = 32 * QS;
+  constexpr int NT = 256;
+  __shared__ __attribute__((aligned(16))) float bias_lds[2][QB * kBiasLd];
+
+  const int nqb = Np / QB;
   const int nlg = (N + kLinesPerBlock - 1) / kLinesPerBlock;
   const int total = B * nlg * kHeads * nqb;
   int bid = blockIdx.x;
   if (xcd_remap) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-  // task order: q-block fastest, then line group, then head, then batch, so that one XCD
-  // walks all q-blocks of a line group (K/V reuse) and many line groups of one head (bias reuse)
+  // q-block fastest, then line group, then head: one XCD walks all q-blocks of a line
+  // group (K/V reuse in its L2) and many line groups of one head (bias reuse).
   const int qb = bid % nqb;
   int rest = bid / nqb;
   const int lg = rest % nlg;
   rest /= nlg;
   const int h = rest % kHeads;
   const int b = rest / kHeads;
+  const int tid = threadIdx.x;
   const int w = wave_id();
   const int l = lane_id();
   const int line = lg * kLinesPerBlock + w;
-  if (b >= B || line >= N) return;
+  const bool active = line < N;  // inactive waves still stage the shared bias tiles
 
   const int lq = l & 31;
   const int hf = l >> 5;
@@ -284,92 +316,141 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__
   const TC* Vh = Vt + (lineq * kHeads + h) * (size_t)kHeadDim * Np;
   const float* PBh = PB + ((size_t)b * kHeads + h) * (size_t)Np * Np;
   const float* MAl = MA + lineq * Np;
-  const int q0 = qb * kQBlock;
+  const int q0 = qb * QB;
 
-  Frag16<TC> qf[kQSub];
+  // Bias tile staging: QB queries x 32 key slots per key block.
+  constexpr int BIAS_IT = QB * 32 / 4 / NT;
+  f32x4 bpf[BIAS_IT];
+  auto bias_load = [&](int k0) {
 #pragma unroll
-  for (int s = 0; s < kQSub; ++s) qf[s].load(Qh + (size_t)(q0 + 32 * s + lq) * kHeadDim + 16 * hf);
+    for (int it = 0; it < BIAS_IT; ++it) {
+      const int idx = tid + it * NT;
+      if (BIAS_KEY_MAJOR) {  // rows: 32 keys of QB queries
+        const int k = idx / (QB / 4);
+        const int qq = (idx % (QB / 4)) * 4;
+        bpf[it] = *reinterpret_cast<const f32x4*>(PBh + (size_t)(k0 + k) * Np + q0 + qq);
+      } else {  // rows: QB queries of 32 slots
+        const int qq = idx / 8;
+        const int s0 = (idx % 8) * 4;
+        bpf[it] = *reinterpret_cast<const f32x4*>(PBh + (size_t)(q0 + qq) * Np + k0 + s0);
+      }
+    }
+  };
+  auto bias_store = [&](int buf) {
+    float* dst = bias_lds[buf];
+#pragma unroll
+    for (int it = 0; it < BIAS_IT; ++it) {
+      const int idx = tid + it * NT;
+      if (BIAS_KEY_MAJOR) {
+        const int k = idx / (QB / 4);
+        const int qq = (idx % (QB / 4)) * 4;
+        const int s = key_slot(k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(qq + e) * kBiasLd + s] = bpf[it][e];
+      } else {
+        const int qq = idx / 8;
+        const int s0 = (idx % 8) * 4;
+        *reinterpret_cast<f32x4*>(dst + qq * kBiasLd + s0) = bpf[it];
+      }
+    }
+  };
 
-  // Does this line mask any real key? (wave-uniform)
+  Frag16<TC> qf[QS];
+  f32x16 o[QS];
+  float mref[QS], lrun[QS];
   bool masked = false;
-  for (int k = l; k < N; k += 64) masked |= MAl[(k & ~31) + key_slot(k & 31)] != 0.f;
-  masked = __any(masked);
-
-  f32x16 o[kQSub];
-  float mrun[kQSub], lrun[kQSub];
+  if (active) {
 #pragma unroll
-  for (int s = 0; s < kQSub; ++s) {
+    for (int s = 0; s < QS; ++s) qf[s].load(Qh + (size_t)(q0 + 32 * s + lq) * kHeadDim + 16 * hf);
+    for (int k = l; k < N; k += 64) masked |= MAl[(k & ~31) + key_slot(k & 31)] != 0.f;
+  }
+  masked = __any(masked);
+#pragma unroll
+  for (int s = 0; s < QS; ++s) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[s][r] = 0.f;
-    mrun[s] = -INFINITY;
+    mref[s] = 0.f;
     lrun[s] = 0.f;
   }
 
   const int nkb = (N + 31) / 32;
+  bias_load(0);
+  bias_store(0);
+  __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * 32;
+    const bool more = kb + 1 < nkb;
     Frag16<TC> kf, vf;
-    kf.load(Kh + (size_t)(k0 + lq) * kHeadDim + 16 * hf);
-    vf.load(Vh + (size_t)lq * Np + k0 + 16 * hf);
-    float madd[16];
-    if (masked) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f32x4 mv = *reinterpret_cast<const f32x4*>(MAl + k0 + 16 * hf + 4 * i);
-        madd[4 * i] = mv[0]; madd[4 * i + 1] = mv[1]; madd[4 * i + 2] = mv[2]; madd[4 * i + 3] = mv[3];
-      }
-    } else if (k0 + 32 > N) {
-      // padding keys of the last block still need -inf
-#pragma unroll
-      for (int r = 0; r < 16; ++r) madd[r] = (k0 + 8 * (r >> 2) + 4 * hf + (r & 3)) < N ? 0.f : -INFINITY;
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) madd[r] = 0.f;
+    if (active) {
+      kf.load(Kh + (size_t)(k0 + lq) * kHeadDim + 16 * hf);
+      vf.load(Vh + (size_t)lq * Np + k0 + 16 * hf);
     }
+    if (more) bias_load(k0 + 32);
+    if (active) {
+      // Additive key mask, applied after q k^T + pb as the reference orders the fp32 adds
+      // (a fully masked line then rounds every logit to the same -1e9 log2 e). The MA slots
+      // of padding keys hold -inf.
+      const bool use_madd = masked || k0 + 32 > N;
+      const float* mrow = MAl + k0 + 16 * hf;
+      const float* bl = bias_lds[kb & 1];
 #pragma unroll
-    for (int s = 0; s < kQSub; ++s) {
-      const int q = q0 + 32 * s + lq;
-      f32x16 sacc;
-      if (BIAS_KEY_MAJOR) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = PBh[(size_t)(k0 + 8 * (r >> 2) + 4 * hf + (r & 3)) * Np + q] + madd[r];
-      } else {
-        const float* pr = PBh + (size_t)q * Np + k0 + 16 * hf;
+      for (int s = 0; s < QS; ++s) {
+        f32x16 sacc;
+        const float* br = bl + (32 * s + lq) * kBiasLd + 16 * hf;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          f32x4 bv = *reinterpret_cast<const f32x4*>(pr + 4 * i);
-          sacc[4 * i] = bv[0] + madd[4 * i];
-          sacc[4 * i + 1] = bv[1] + madd[4 * i + 1];
-          sacc[4 * i + 2] = bv[2] + madd[4 * i + 2];
-          sacc[4 * i + 3] = bv[3] + madd[4 * i + 3];
+          const f32x4 bv = *reinterpret_cast<const f32x4*>(br + 4 * i);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sacc[4 * i + e] = bv[e];
         }
+        mma32_16(sacc, kf, qf[s]);  // log2-domain q k^T + pb
+        if (use_madd) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 mv = *reinterpret_cast<const f32x4*>(mrow + 4 * i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sacc[4 * i + e] = (sacc[4 * i + e] + mv[e]) - mref[s];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[r] -= mref[s];
+        }
+        float mx = fmaxf(fmaxf(sacc[0], sacc[1]), sacc[2]);
+#pragma unroll
+        for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sacc[r]), sacc[r + 1]);
+        mx = fmaxf(mx, sacc[15]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const bool first = kb == 0;
+        if (__any(first || mx > kRescaleSlack)) {
+          const float delta = (first || mx > kRescaleSlack) ? mx : 0.f;
+          const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(-delta);
+          mref[s] += delta;
+          lrun[s] *= alpha;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            o[s][r] *= alpha;
+            sacc[r] -= delta;
+          }
+        }
+        float ls = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sacc[r] = __builtin_amdgcn_exp2f(sacc[r]);
+          ls += sacc[r];
+        }
+        lrun[s] += ls;
+        mma32_16(o[s], vf, pack_p(sacc, TC{}));
       }
-      mma32_16(sacc, kf, qf[s]);
-      float mx = sacc[0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(mrun[s], mx);
-      const float alpha = __builtin_amdgcn_exp2f(mrun[s] - mnew);
-      mrun[s] = mnew;
-      float p[16];
-      float ls = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        p[r] = __builtin_amdgcn_exp2f(sacc[r] - mnew);
-        ls += p[r];
-      }
-      lrun[s] = lrun[s] * alpha + ls;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[s][r] *= alpha;
-      mma32_16(o[s], vf, pack_p(p, TC{}));
     }
+    if (more) bias_store((kb + 1) & 1);
+    __syncthreads();
   }
+  if (!active) return;
 
   // O^T lane (q, hf) holds d = 8 (r >> 2) + 4 hf + (r & 3).
   TC* Ol = O + lineq * (size_t)Np * kC;
 #pragma unroll
-  for (int s = 0; s < kQSub; ++s) {
+  for (int s = 0; s < QS; ++s) {
     const float lt = lrun[s] + __shfl_xor(lrun[s], 32, 64);
     const float inv = 1.0f / lt;
     const int q = q0 + 32 * s + lq;
@@ -386,40 +467,45 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__
 }
 
 // ------------------------------------------------------------------ A3
-template <class TZ, class TC>
-struct OutCfg {
-  static constexpr int BM = proj_bm<TC>();
-  static constexpr int ALD = kC + lds_pad<TC>();
-  static constexpr int SLD = kC + 4;
-  static constexpr int A_BYTES = BM * ALD * (int)sizeof(TC);
-  static constexpr int S_BYTES = BM * SLD * 4;
-  static constexpr int SMEM = A_BYTES > S_BYTES ? A_BYTES : S_BYTES;
-};
-
+// Block: BM positions of one line. A = O * G -> LDS; acc^T = Wout A^T; fp32 stage; the
+// update is stored (or added) at the z position of each attention-frame position.
 template <class TZ, class TC>
 __global__ __launch_bounds__(256) void attn_out_kernel(const TC* __restrict__ O, const TC* __restrict__ G,
                                                        const TC* __restrict__ Wo, TZ* __restrict__ out, int N, int Np,
                                                        int transpose, int accumulate) {
-  using Cfg = OutCfg<TZ, TC>;
-  constexpr int BM = Cfg::BM, ALD = Cfg::ALD, SLD = Cfg::SLD;
+  constexpr int BM = block_rows<TC>();
+  constexpr int LD = ld128<TC>();
+  constexpr int SLD = kC + 4;
   constexpr int NT = 256;
-  constexpr int RB = BM / 16;
-  constexpr int CBW = kC / 16 / 4;
+  constexpr int WM = BM / 2;
+  constexpr int PT = WM / 32;
   constexpr int VEC = 16 / sizeof(TC);
-  __shared__ __attribute__((aligned(16))) char smem[Cfg::SMEM];
+  constexpr int A_BYTES = BM * LD * (int)sizeof(TC);
+  constexpr int W_BYTES = 128 * LD * (int)sizeof(TC);
+  constexpr int S_BYTES = BM * SLD * 4;
+  static_assert(S_BYTES <= A_BYTES + W_BYTES, "stage must fit over the operand tiles");
+  __shared__ __attribute__((aligned(16))) char smem[A_BYTES + W_BYTES];
   TC* A = reinterpret_cast<TC*>(smem);
+  TC* Wl = reinterpret_cast<TC*>(smem + A_BYTES);
   float* stage = reinterpret_cast<float*>(smem);
 
   const int t0 = blockIdx.x * BM;
   const int line = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const int wr = w >> 1, wc = w & 1;
   const size_t lineq = (size_t)b * Np + line;
   {
+    Rows128<TC, 128, NT> wl;
+    wl.load(Wo, kC);
     const TC* Ol = O + (lineq * Np + t0) * kC;
     const TC* Gl = G + (lineq * Np + t0) * kC;
     constexpr int CPR = kC / VEC;
-    for (int idx = tid; idx < BM * CPR; idx += NT) {
+#pragma unroll
+    for (int it = 0; it < BM * CPR / NT; ++it) {
+      const int idx = tid + it * NT;
       const int p = idx / CPR;
       const int c0 = (idx % CPR) * VEC;
       float ov[VEC], gv[VEC], y[VEC];
@@ -432,26 +518,26 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const TC* __restrict__ O,
 #pragma unroll
         for (int e = 0; e < VEC; ++e) y[e] = 0.f;
       }
-      store_vec<TC, VEC>(A + p * ALD + c0, y);
+      store_vec<TC, VEC>(A + p * LD + c0, y);
     }
+    wl.store(Wl, LD);
   }
   __syncthreads();
-  const int w = wave_id();
-  const int l = lane_id();
-  f32x4 acc[RB][CBW];
-  zero_acc(acc);
-  int wrow0[CBW];
-#pragma unroll
-  for (int j = 0; j < CBW; ++j) wrow0[j] = (w * CBW + j) * 16;
-  gemm16_lds_x_w<TC, kC, RB, CBW>(acc, A, ALD, 0, Wo, kC, wrow0);
+  f32x16 acc[2][PT];
+  zero_acc32(acc);
+  wave_mma32<TC, 2, PT, kC>(acc, Wl, LD, wc * 64, A, LD, wr * WM);
   __syncthreads();
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int ci = 0; ci < 2; ++ci)
 #pragma unroll
-    for (int j = 0; j < CBW; ++j)
+    for (int pj = 0; pj < PT; ++pj)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        stage[(rb * 16 + 4 * (l >> 4) + e) * SLD + (w * CBW + j) * 16 + (l & 15)] = acc[rb][j][e];
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int ch = wc * 64 + 32 * ci + acc32_row(4 * g4);
+        const int p = wr * WM + 32 * pj + (l & 31);
+        *reinterpret_cast<f32x4*>(stage + p * SLD + ch) =
+            f32x4{acc[ci][pj][4 * g4], acc[ci][pj][4 * g4 + 1], acc[ci][pj][4 * g4 + 2], acc[ci][pj][4 * g4 + 3]};
+      }
   __syncthreads();
   TZ* ob = out + (size_t)b * N * N * kC;
   auto orow = [&](int p) -> TZ* {
@@ -468,7 +554,7 @@ struct AttnWs {
 };
 
 AttnWs attn_ws_layout(int B, int N, int cdtype) {
-  const size_t Np = (size_t)pf::round_up((size_t)N, kQBlock);
+  const size_t Np = pf::round_up((size_t)N, kPad);
   const size_t es = cdtype == PF_F32 ? 4 : 2;
   const size_t tok = (size_t)B * Np * Np * kC * es;  // one [B][Np][Np][C] operand
   AttnWs w;
@@ -492,7 +578,7 @@ AttnWs attn_ws_layout(int B, int N, int cdtype) {
 template <class TZ, class TC>
 int grid_attn_launch(const void* z, const float* mask, const float* lnw, const float* lnb, float eps, const void* w5,
                      const void* wo, int B, int N, int transpose, void* out, int accumulate, void* ws, hipStream_t s) {
-  const int Np = (int)pf::round_up((size_t)N, kQBlock);
+  const int Np = (int)pf::round_up((size_t)N, kPad);
   const AttnWs L = attn_ws_layout(B, N, sizeof(TC) == 4 ? PF_F32 : PF_BF16);
   char* base = reinterpret_cast<char*>(ws);
   TC* Qb = reinterpret_cast<TC*>(base + L.q);
@@ -503,17 +589,17 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
   float* PBb = reinterpret_cast<float*>(base + L.pb);
   float* MAb = reinterpret_cast<float*>(base + L.ma);
   const float qscale = (1.0f / sqrtf((float)kHeadDim)) * kLog2e;
+  constexpr int BM = block_rows<TC>();
   {
-    constexpr int BM = proj_bm<TC>();
     dim3 grid(Np / BM, Np, B);
-    pf::KernelTimer timer_attn_project("attn_project", s);
+    pf::KernelTimer timer("attn_project", s);
     attn_project_kernel<TZ, TC><<<grid, 256, 0, s>>>((const TZ*)z, mask, lnw, lnb, eps, (const TC*)w5, Qb, Kb, Vb,
                                                      Gb, PBb, MAb, N, Np, transpose, qscale);
-    timer_attn_project.stop();
+    timer.stop();
     if (int e = pf::check_launch("attn_project")) return e;
   }
   {
-    const int nqb = Np / kQBlock;
+    const int nqb = Np / (32 * attn_qsub<TC>());
     const int nlg = (N + kLinesPerBlock - 1) / kLinesPerBlock;
     const long total = (long)B * nlg * kHeads * nqb;
     const int remap = (total % 8 == 0) ? 1 : 0;
@@ -527,11 +613,10 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     if (int e = pf::check_launch("tri_attn")) return e;
   }
   {
-    constexpr int BM = proj_bm<TC>();
     dim3 grid((N + BM - 1) / BM, N, B);
-    pf::KernelTimer timer_attn_out("attn_out", s);
+    pf::KernelTimer timer("attn_out", s);
     attn_out_kernel<TZ, TC><<<grid, 256, 0, s>>>(Ob, Gb, (const TC*)wo, (TZ*)out, N, Np, transpose, accumulate);
-    timer_attn_out.stop();
+    timer.stop();
     if (int e = pf::check_launch("attn_out")) return e;
   }
   return pf::ok();

@@ -63,6 +63,21 @@ PF_DEVICE void load16<bf16>(const bf16* p, float (&out)[8]) {
   for (int e = 0; e < 8; ++e) out[e] = (float)v[e];
 }
 
+// 16 raw bytes (as loaded) -> floats.
+template <class T>
+PF_DEVICE void unpack16(const u32x4& r, float (&out)[16 / sizeof(T)]);
+template <>
+PF_DEVICE void unpack16<float>(const u32x4& r, float (&out)[4]) {
+  const f32x4 v = __builtin_bit_cast(f32x4, r);
+  out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+}
+template <>
+PF_DEVICE void unpack16<bf16>(const u32x4& r, float (&out)[8]) {
+  const bf16x8 v = __builtin_bit_cast(bf16x8, r);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = (float)v[e];
+}
+
 // Store VEC floats (VEC * sizeof(T) bytes: 4, 8 or 16) as T.
 template <class T, int VEC>
 PF_DEVICE void store_vec(T* p, const float* v) {
@@ -297,3 +312,131 @@ PF_DEVICE void store_tile_from_lds(RowFn rowptr, const float* stage, int lds_ld,
     store_vec<TZ, VEC>(dst + sub * VEC, x);
   }
 }
+
+// ---------------------------------------------------------------- 32x32 block tiles
+// Block GEMMs for the K = 128 contractions of the pair stack. Operands sit in LDS with
+// k contiguous and rows padded by 16 bytes; a wave computes 32x32 MFMA tiles, lane l
+// holding row (l & 31) and the KPL k values from (l >> 5) * KPL of each fragment.
+
+// Rows of positions per block tile: 128 with bf16 operands, 64 with fp32 (LDS budget).
+template <class TC>
+constexpr int block_rows() { return sizeof(TC) == 2 ? 128 : 64; }
+
+// LDS row stride (elements) of a 128-wide operand tile.
+template <class TC>
+constexpr int ld128() { return 128 + lds_pad<TC>(); }
+
+// R rows x 128 TC elements, global row stride ldg, staged through registers so the
+// global loads can be issued early (load) and written to LDS later (store).
+template <class TC, int R, int NT>
+struct Rows128 {
+  static constexpr int VEC = 16 / sizeof(TC);
+  static constexpr int CPR = 128 / VEC;
+  static constexpr int IT = R * CPR / NT;
+  static_assert((R * CPR) % NT == 0, "tile must split evenly over the block");
+  u32x4 v[IT];
+  PF_DEVICE void load(const TC* __restrict__ g, long ldg) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int idx = (int)threadIdx.x + it * NT;
+      v[it] = *reinterpret_cast<const u32x4*>(g + (long)(idx / CPR) * ldg + (idx % CPR) * VEC);
+    }
+  }
+  PF_DEVICE void store(TC* lds, int ld) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int idx = (int)threadIdx.x + it * NT;
+      *reinterpret_cast<u32x4*>(lds + (idx / CPR) * ld + (idx % CPR) * VEC) = v[it];
+    }
+  }
+};
+
+// acc[i][j] += A[arow0 + 32 i + .][0, K) * B[brow0 + 32 j + .][0, K)^T, A and B in LDS.
+template <class TC, int MI, int NJ, int K>
+PF_DEVICE void wave_mma32(f32x16 (&acc)[MI][NJ], const TC* A, int lda, int arow0, const TC* B, int ldb, int brow0) {
+  using M = Mfma<TC>;
+  const int l = lane_id();
+  const int r = l & 31;
+  const int kq = (l >> 5) * M::KPL;
+  // Two k-steps in flight: enough to cover LDS latency without hoisting every fragment.
+#pragma unroll 2
+  for (int kk = 0; kk < K; kk += M::K32) {
+    typename M::Frag a[MI], b[NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) a[i] = M::load(A + (arow0 + 32 * i + r) * lda + kk + kq);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) b[j] = M::load(B + (brow0 + 32 * j + r) * ldb + kk + kq);
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) M::mma32(acc[i][j], a[i], b[j]);
+  }
+}
+
+template <int MI, int NJ>
+PF_DEVICE void zero_acc32(f32x16 (&acc)[MI][NJ]) {
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+}
+
+// Row (inside a 32x32 tile) of accumulator element e of this lane; its column is lane & 31.
+// Elements 4g .. 4g+3 are four consecutive rows.
+PF_DEVICE int acc32_row(int e) { return 8 * (e >> 2) + 4 * (lane_id() >> 5) + (e & 3); }
+
+// Two-phase LayerNorm of BM rows: load() issues the global loads (so they can overlap
+// other work), store() normalises into an LDS tile with the same math as ln_tile_to_lds.
+template <class TZ, class TC, int C, int BM, int NT>
+struct LnTile {
+  static constexpr int VEC = 16 / sizeof(TZ);
+  static constexpr int LPP = C / VEC;
+  static constexpr int PPI = NT / LPP;
+  static constexpr int PASSES = BM / PPI;
+  static_assert(BM % PPI == 0 && 64 % LPP == 0, "tile must split evenly");
+  u32x4 raw[PASSES];
+  bool ok[PASSES];
+  template <class RowFn>
+  PF_DEVICE void load(RowFn rowptr) {
+    const int sub = threadIdx.x % LPP;
+    const int pp = threadIdx.x / LPP;
+#pragma unroll
+    for (int s = 0; s < PASSES; ++s) {
+      const TZ* src = rowptr(s * PPI + pp);
+      ok[s] = src != nullptr;
+      raw[s] = ok[s] ? *reinterpret_cast<const u32x4*>(src + sub * VEC) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  PF_DEVICE void store(const float* __restrict__ w, const float* __restrict__ b, float eps, TC* lds, int lda) const {
+    const int sub = threadIdx.x % LPP;
+    const int pp = threadIdx.x / LPP;
+    float wv[VEC], bv[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      wv[e] = w[sub * VEC + e];
+      bv[e] = b[sub * VEC + e];
+    }
+#pragma unroll
+    for (int s = 0; s < PASSES; ++s) {
+      float x[VEC];
+      unpack16<TZ>(raw[s], x);
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum += x[e];
+      const float mean = group_sum<LPP>(sum) * (1.0f / C);
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = x[e] - mean;
+        q += d * d;
+      }
+      const float rstd = rsqrtf(group_sum<LPP>(q) * (1.0f / C) + eps);
+      float y[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) y[e] = ok[s] ? (x[e] - mean) * rstd * wv[e] + bv[e] : 0.f;
+      store_vec<TC, VEC>(lds + (s * PPI + pp) * lda + sub * VEC, y);
+    }
+  }
+};

@@ -157,6 +157,131 @@ __global__ __launch_bounds__(256) void pair_transition_kernel(
   }
 }
 
+// bf16 path: 128 positions per block, 8 waves, 32x32x16 MFMAs on LDS operands. The block
+// walks the hidden dim in four chunks of 128: [h_a | h_b]^T = W1_chunk LN(x)^T (wave w:
+// hidden tile w & 3, positions 64 (w >> 2) ..), u = silu(h_a) h_b -> LDS, then
+// y^T += W2_chunk u^T (wave w: output tile w & 3). Weight chunks are prefetched into
+// registers one phase ahead. LDS: x | u | two weight buffers (136 KiB, one block per CU).
+template <class TZ, bool S2P>
+__global__ __launch_bounds__(512) void pair_transition32_kernel(
+    const TZ* __restrict__ x, TZ* __restrict__ out, const float* __restrict__ lnw, const float* __restrict__ lnb,
+    float eps, const bf16* __restrict__ W1, const bf16* __restrict__ W2, long M, int accumulate,
+    const float* __restrict__ s2p_w, const float* __restrict__ s2p_b, float s2p_eps, const bf16* __restrict__ Ws2p,
+    float* __restrict__ logits, long NN) {
+  constexpr int BM = 128;
+  constexpr int LD = ld128<bf16>();
+  constexpr int SLD = kC + 4;
+  constexpr int NT = 512;
+  constexpr int TILE = BM * LD * 2;
+  static_assert(BM * SLD * 4 <= 2 * TILE, "stage must fit over x and u");
+  __shared__ __attribute__((aligned(16))) char smem[4 * TILE];
+  bf16* X = reinterpret_cast<bf16*>(smem);
+  bf16* U = reinterpret_cast<bf16*>(smem + TILE);
+  bf16* Wa = reinterpret_cast<bf16*>(smem + 2 * TILE);
+  bf16* Wb = reinterpret_cast<bf16*>(smem + 3 * TILE);
+  float* stage = reinterpret_cast<float*>(smem);
+
+  const long m0 = (long)blockIdx.x * BM;
+  const int w = wave_id();
+  const int l = lane_id();
+  const int ht = w & 3;          // hidden / output tile of 32
+  const int pg = (w >> 2) * 64;  // first position of the wave's two position tiles
+
+  Rows128<bf16, 128, NT> pfa, pfb;
+  pfa.load(W1, kC);
+  pfb.load(W1 + (size_t)kHidden * kC, kC);
+  ln_tile_to_lds<TZ, bf16, kC, BM, NT>([&](int p) -> const TZ* {
+    const long m = m0 + p;
+    return m < M ? x + m * kC : nullptr;
+  }, lnw, lnb, eps, X, LD);
+  pfa.store(Wa, LD);
+  pfb.store(Wb, LD);
+  __syncthreads();
+
+  f32x16 acc_o[1][2];
+  zero_acc32(acc_o);
+#pragma unroll 1
+  for (int ch = 0; ch < kHidden / 128; ++ch) {
+    Rows128<bf16, 128, NT> pf2;
+    pf2.load(W2 + ch * 128, kHidden);
+    {
+      f32x16 acc_a[1][2], acc_b[1][2];
+      zero_acc32(acc_a);
+      zero_acc32(acc_b);
+      wave_mma32<bf16, 1, 2, kC>(acc_a, Wa, LD, 32 * ht, X, LD, pg);
+      wave_mma32<bf16, 1, 2, kC>(acc_b, Wb, LD, 32 * ht, X, LD, pg);
+#pragma unroll
+      for (int pj = 0; pj < 2; ++pj)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = siluf_(acc_a[0][pj][4 * g4 + e]) * acc_b[0][pj][4 * g4 + e];
+          store_vec<bf16, 4>(U + (pg + 32 * pj + (l & 31)) * LD + 32 * ht + acc32_row(4 * g4), v);
+        }
+    }
+    __syncthreads();  // u complete; the W1 buffers are free
+    pf2.store(Wa, LD);
+    if (ch + 1 < kHidden / 128) {
+      pfa.load(W1 + (size_t)(ch + 1) * 128 * kC, kC);
+      pfb.load(W1 + (size_t)(kHidden + (ch + 1) * 128) * kC, kC);
+    }
+    __syncthreads();
+    wave_mma32<bf16, 1, 2, 128>(acc_o, Wa, LD, 32 * ht, U, LD, pg);
+    __syncthreads();  // Wa and u free
+    if (ch + 1 < kHidden / 128) {
+      pfa.store(Wa, LD);
+      pfb.store(Wb, LD);
+      __syncthreads();
+    }
+  }
+
+  // y -> fp32 stage [pos][ch] over x and u
+#pragma unroll
+  for (int pj = 0; pj < 2; ++pj)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4)
+      *reinterpret_cast<f32x4*>(stage + (pg + 32 * pj + (l & 31)) * SLD + 32 * ht + acc32_row(4 * g4)) =
+          f32x4{acc_o[0][pj][4 * g4], acc_o[0][pj][4 * g4 + 1], acc_o[0][pj][4 * g4 + 2], acc_o[0][pj][4 * g4 + 3]};
+  __syncthreads();
+  {
+    constexpr int VEC = 16 / sizeof(TZ);
+    constexpr int LPP = kC / VEC;
+    constexpr int PPI = NT / LPP;
+    const int tid = threadIdx.x;
+    const int sub = tid % LPP;
+    const int pp = tid / LPP;
+#pragma unroll
+    for (int p0 = 0; p0 < BM; p0 += PPI) {
+      const int p = p0 + pp;
+      const long m = m0 + p;
+      if (m >= M) continue;
+      float v[VEC];
+      if (accumulate) {
+        load16<TZ>(out + m * kC + sub * VEC, v);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        v[e] = to_f32(from_f32<TZ>(v[e] + stage[p * SLD + sub * VEC + e]));
+        if (S2P) stage[p * SLD + sub * VEC + e] = v[e];
+      }
+      store_vec<TZ, VEC>(out + m * kC + sub * VEC, v);
+    }
+  }
+  if (S2P) {
+    __syncthreads();
+    bf16* A2 = Wa;
+    ln_tile_to_lds<float, bf16, kC, BM, NT>([&](int p) -> const float* {
+      return m0 + p < M ? stage + p * SLD : nullptr;
+    }, s2p_w, s2p_b, s2p_eps, A2, LD);
+    __syncthreads();
+    s2p_store<bf16, BM>(A2, LD, Ws2p, logits, m0, M, NN);
+  }
+}
+
 // Standalone single_to_pair: LN'(z) Ws2p^T -> logits [B][16][N][N].
 template <class TZ, class TC>
 __global__ __launch_bounds__(256) void single_to_pair_kernel(const TZ* __restrict__ z, const float* __restrict__ lnw,
@@ -177,9 +302,22 @@ template <class TZ, class TC>
 int transition_launch(const void* x, const float* lnw, const float* lnb, float eps, const void* w1, const void* w2,
                       long M, void* out, int accumulate, const float* s2p_w, const float* s2p_b, float s2p_eps,
                       const void* ws2p, float* logits, long NN, hipStream_t s) {
+  pf::KernelTimer timer("pair_transition", s);
+  if constexpr (sizeof(TC) == 2) {
+    dim3 grid((unsigned)((M + 127) / 128));
+    if (logits)
+      pair_transition32_kernel<TZ, true><<<grid, 512, 0, s>>>((const TZ*)x, (TZ*)out, lnw, lnb, eps, (const bf16*)w1,
+                                                             (const bf16*)w2, M, accumulate, s2p_w, s2p_b, s2p_eps,
+                                                             (const bf16*)ws2p, logits, NN);
+    else
+      pair_transition32_kernel<TZ, false><<<grid, 512, 0, s>>>((const TZ*)x, (TZ*)out, lnw, lnb, eps,
+                                                              (const bf16*)w1, (const bf16*)w2, M, accumulate,
+                                                              nullptr, nullptr, 0.f, nullptr, nullptr, NN);
+    timer.stop();
+    return pf::check_launch("pair_transition");
+  }
   constexpr int BM = tr_bm<TC>();
   dim3 grid((unsigned)((M + BM - 1) / BM));
-  pf::KernelTimer timer("pair_transition", s);
   if (logits)
     pair_transition_kernel<TZ, TC, true><<<grid, 256, 0, s>>>((const TZ*)x, (TZ*)out, lnw, lnb, eps, (const TC*)w1,
                                                              (const TC*)w2, M, accumulate, s2p_w, s2p_b, s2p_eps,

@@ -377,6 +377,223 @@ __global__ __launch_bounds__(256) void trimul_output_kernel(
   store_tile_from_lds<TZ, C, BM, NT>(orow, stage, SLD, accumulate != 0);
 }
 
+// ------------------------------------------------------------------ bf16 K1 / K3 (32x32 tiles)
+// The bf16 path runs K1 and K3 as 128- and 64-position block tiles on 32x32x16 MFMAs with
+// the weights staged through LDS; the fp32 parity path keeps the 16x16 kernels above.
+//
+// K1: packed weights in 32-channel chunks, row 128 j + 32 kind + r (kind 0 a proj, 1 a gate,
+// 2 b proj, 3 b gate; channel 32 j + r). Waves 2 x 2: positions x (a | b). Each wave's
+// accumulator pair (proj, gate) holds the same (position, channel) elements, so the gate is
+// applied in registers; the gated chunk is staged channel-major and written as 256-byte
+// plane rows.
+template <class TZ>
+__global__ __launch_bounds__(256) void trimul_project32_kernel(const TZ* __restrict__ z, const float* __restrict__ mask,
+                                                               const float* __restrict__ lnw,
+                                                               const float* __restrict__ lnb, float eps,
+                                                               const bf16* __restrict__ w4, bf16* __restrict__ planes,
+                                                               int B, int N, int Np, int outgoing) {
+  constexpr int C = 128;
+  constexpr int BM = 128;
+  constexpr int LD = ld128<bf16>();
+  constexpr int NT = 256;
+  constexpr int WM = 64;
+  constexpr int PT = 2;
+  constexpr int SLD = BM + 8;
+  __shared__ __attribute__((aligned(16))) bf16 X[BM * LD];
+  __shared__ __attribute__((aligned(16))) bf16 WS[128 * LD];
+  __shared__ float mk[BM];
+
+  const int t0 = blockIdx.x * BM;
+  const int line = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const int wr = w >> 1, wc = w & 1;
+  const TZ* zb = z + (size_t)b * N * N * C;
+  auto pos_of = [&](int p) -> long {
+    const int t = t0 + p;
+    if (line >= N || t >= N) return -1;
+    return outgoing ? (long)line * N + t : (long)t * N + line;
+  };
+  Rows128<bf16, 128, NT> wpf;
+  wpf.load(w4, C);
+  ln_tile_to_lds<TZ, bf16, C, BM, NT>([&](int p) -> const TZ* {
+    const long pos = pos_of(p);
+    return pos < 0 ? nullptr : zb + pos * C;
+  }, lnw, lnb, eps, X, LD);
+  if (tid < BM) {
+    const long pos = pos_of(tid);
+    mk[tid] = pos < 0 ? 0.f : mask[(size_t)b * N * N + pos];
+  }
+  const size_t pe = (size_t)Np * Np;
+#pragma unroll 1
+  for (int j = 0; j < C / 32; ++j) {
+    __syncthreads();
+    wpf.store(WS, LD);
+    __syncthreads();
+    if (j + 1 < C / 32) wpf.load(w4 + (size_t)(j + 1) * 128 * C, C);
+    f32x16 acc[PT][2];
+    zero_acc32(acc);
+    wave_mma32<bf16, PT, 2, C>(acc, X, LD, wr * WM, WS, LD, wc * 64);
+    __syncthreads();  // WS becomes the stage [plane * 32 + channel][position]
+#pragma unroll
+    for (int pi = 0; pi < PT; ++pi)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int p0 = wr * WM + 32 * pi + acc32_row(4 * g4);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = sigmoidf_(acc[pi][1][4 * g4 + e]) * acc[pi][0][4 * g4 + e] * mk[p0 + e];
+        store_vec<bf16, 4>(WS + (wc * 32 + (l & 31)) * SLD + p0, v);
+      }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 64 * BM / 8 / NT; ++it) {
+      const int idx = tid + it * NT;
+      const int row = idx / (BM / 8);
+      const int chunk = idx % (BM / 8);
+      const int plane = row / 32;
+      const int ch = 32 * j + (row % 32);
+      bf16* dst = planes + ((size_t)plane * B * C + (size_t)b * C + ch) * pe + (size_t)line * Np + t0 + chunk * 8;
+      *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(WS + row * SLD + chunk * 8);
+    }
+  }
+}
+
+// K3 on 64 positions of one row i: X tile (channel-major) -> LN_out -> A1 [pos][ch];
+// LN_in(z) -> A2; acc^T for g = Wog A2^T and p = Wo A1^T (wave w: channels 32 w, all 64
+// positions), update = sigmoid(g) p through an fp32 stage, stored or added.
+template <class TZ>
+__global__ __launch_bounds__(256) void trimul_output32_kernel(
+    const bf16* __restrict__ X, const TZ* __restrict__ z, TZ* __restrict__ out, const float* __restrict__ lniw,
+    const float* __restrict__ lnib, float eps_in, const float* __restrict__ lnow, const float* __restrict__ lnob,
+    float eps_out, const bf16* __restrict__ Wo, const bf16* __restrict__ Wog, int B, int N, int Np, int accumulate) {
+  constexpr int C = 128;
+  constexpr int BM = 64;
+  constexpr int LD = ld128<bf16>();
+  constexpr int XLD = BM + 8;
+  constexpr int SLD = C + 4;
+  constexpr int NT = 256;
+  constexpr int NQ = NT / BM;
+  constexpr int R0 = C * XLD * 2;  // Xs, later A2 and (with R1) the fp32 stage
+  constexpr int R1 = BM * LD * 2;  // A1
+  constexpr int R2 = 128 * LD * 2; // weights
+  static_assert(BM * LD * 2 <= R0 && BM * SLD * 4 <= R0 + R1, "LDS aliasing");
+  __shared__ __attribute__((aligned(16))) char smem[R0 + R1 + R2];
+  __shared__ float red[NQ][BM];
+  __shared__ float stat_mean[BM];
+  bf16* Xs = reinterpret_cast<bf16*>(smem);
+  bf16* A2 = reinterpret_cast<bf16*>(smem);
+  float* stage = reinterpret_cast<float*>(smem);
+  bf16* A1 = reinterpret_cast<bf16*>(smem + R0);
+  bf16* WS = reinterpret_cast<bf16*>(smem + R0 + R1);
+
+  const int j0 = blockIdx.x * BM;
+  const int i = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const size_t pe = (size_t)Np * Np;
+
+  Rows128<bf16, 128, NT> wpf;
+  wpf.load(Wog, C);
+  const TZ* zb = z + (size_t)b * N * N * C;
+  LnTile<TZ, bf16, C, BM, NT> zt;
+  zt.load([&](int p) -> const TZ* {
+    const int j = j0 + p;
+    return j < N ? zb + ((size_t)i * N + j) * C : nullptr;
+  });
+  {
+    const bf16* Xb = X + (size_t)b * C * pe + (size_t)i * Np + j0;
+#pragma unroll
+    for (int it = 0; it < C * BM / 8 / NT; ++it) {
+      const int idx = tid + it * NT;
+      const int c = idx / (BM / 8);
+      const int chunk = idx % (BM / 8);
+      *reinterpret_cast<u32x4*>(Xs + c * XLD + chunk * 8) =
+          *reinterpret_cast<const u32x4*>(Xb + (size_t)c * pe + chunk * 8);
+    }
+  }
+  __syncthreads();
+  {  // LN_out over the channels of each position, transposing into A1 [pos][ch]
+    constexpr int CPQ = C / NQ;
+    const int p = tid % BM;
+    const int q = tid / BM;
+    float xv[CPQ];
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      xv[e] = (float)Xs[(q * CPQ + e) * XLD + p];
+      s += xv[e];
+    }
+    red[q][p] = s;
+    __syncthreads();
+    if (q == 0) {
+      float t = 0.f;
+#pragma unroll
+      for (int k = 0; k < NQ; ++k) t += red[k][p];
+      stat_mean[p] = t * (1.0f / C);
+    }
+    __syncthreads();
+    const float mean = stat_mean[p];
+    float v = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      const float d = xv[e] - mean;
+      v += d * d;
+    }
+    __syncthreads();
+    red[q][p] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) t += red[k][p];
+    const float rstd = rsqrtf(t * (1.0f / C) + eps_out);
+    float y[CPQ];
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      const int c = q * CPQ + e;
+      y[e] = (xv[e] - mean) * rstd * lnow[c] + lnob[c];
+    }
+#pragma unroll
+    for (int e = 0; e < CPQ; e += 8) store_vec<bf16, 8>(A1 + p * LD + q * CPQ + e, y + e);
+  }
+  __syncthreads();  // Xs dead: A2 takes its place
+  zt.store(lniw, lnib, eps_in, A2, LD);
+  wpf.store(WS, LD);
+  __syncthreads();
+  wpf.load(Wo, C);
+  f32x16 accg[1][2], accp[1][2];
+  zero_acc32(accg);
+  zero_acc32(accp);
+  wave_mma32<bf16, 1, 2, C>(accg, WS, LD, 32 * w, A2, LD, 0);
+  __syncthreads();
+  wpf.store(WS, LD);
+  __syncthreads();
+  wave_mma32<bf16, 1, 2, C>(accp, WS, LD, 32 * w, A1, LD, 0);
+  __syncthreads();  // A1, A2 dead: fp32 stage [pos][ch]
+#pragma unroll
+  for (int pj = 0; pj < 2; ++pj)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int ch = 32 * w + acc32_row(4 * g4);
+      const int p = 32 * pj + (l & 31);
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = sigmoidf_(accg[0][pj][4 * g4 + e]) * accp[0][pj][4 * g4 + e];
+      *reinterpret_cast<f32x4*>(stage + p * SLD + ch) = v;
+    }
+  __syncthreads();
+  TZ* ob = out + (size_t)b * N * N * C;
+  auto orow = [&](int p) -> TZ* {
+    const int j = j0 + p;
+    return j < N ? ob + ((size_t)i * N + j) * C : nullptr;
+  };
+  store_tile_from_lds<TZ, C, BM, NT>(orow, stage, SLD, accumulate != 0);
+}
+
 // ------------------------------------------------------------------ weight packing
 // w_proj, w_gate: [2C][C] in block order (rows 0..C-1 feed a, C..2C-1 feed b).
 template <class TS, class TD>
@@ -385,10 +602,12 @@ __global__ void trimul_pack_kernel(const TS* __restrict__ wp, const TS* __restri
   for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += gridDim.x * blockDim.x) {
     const int row = idx / C;
     const int k = idx % C;
-    const int j = row / 64;
-    const int kind = (row % 64) / 16;
-    const int r = row % 16;
-    const int ch = j * 16 + r;
+    // bf16 operands: 32-channel chunks (K1 on 32x32 tiles); fp32: 16-channel blocks
+    constexpr int CB = sizeof(TD) == 2 ? 32 : 16;
+    const int j = row / (4 * CB);
+    const int kind = (row % (4 * CB)) / CB;
+    const int r = row % CB;
+    const int ch = j * CB + r;
     const TS* src = (kind & 1) ? wg : wp;
     const int srow = (kind >= 2 ? C : 0) + ch;
     w4[idx] = from_f32<TD>(to_f32(src[(size_t)srow * C + k]));
@@ -408,11 +627,16 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
   TC* Q = planes + (size_t)B * C * pe;
   TC* X = planes + (size_t)2 * B * C * pe;
   {
-    constexpr int BM = trimul_bm<TC>();
+    constexpr bool k32 = sizeof(TC) == 2;
+    constexpr int BM = k32 ? 128 : trimul_bm<TC>();
     dim3 grid(Np / BM, Np, B);
     pf::KernelTimer timer_trimul_project("trimul_project", s);
-    trimul_project_kernel<TZ, TC, C><<<grid, 256, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const TC*)w4,
-                                                          planes, B, N, Np, outgoing);
+    if constexpr (k32)
+      trimul_project32_kernel<TZ><<<grid, 256, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const bf16*)w4,
+                                                       (bf16*)planes, B, N, Np, outgoing);
+    else
+      trimul_project_kernel<TZ, TC, C><<<grid, 256, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const TC*)w4,
+                                                            planes, B, N, Np, outgoing);
     timer_trimul_project.stop();
     if (int e = pf::check_launch("trimul_project")) return e;
   }
@@ -436,12 +660,18 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     if (int e = pf::check_launch("trimul_contract")) return e;
   }
   {
-    constexpr int BM = trimul_bm<TC>();
+    constexpr bool k32 = sizeof(TC) == 2;
+    constexpr int BM = k32 ? 64 : trimul_bm<TC>();
     dim3 grid((N + BM - 1) / BM, N, B);
     pf::KernelTimer timer_trimul_output("trimul_output", s);
-    trimul_output_kernel<TZ, TC, C><<<grid, 256, 0, s>>>(X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow, lnob,
-                                                         eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
-                                                         accumulate);
+    if constexpr (k32)
+      trimul_output32_kernel<TZ><<<grid, 256, 0, s>>>((const bf16*)X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in,
+                                                      lnow, lnob, eps_out, (const bf16*)wo, (const bf16*)wog, B, N,
+                                                      Np, accumulate);
+    else
+      trimul_output_kernel<TZ, TC, C><<<grid, 256, 0, s>>>(X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow,
+                                                           lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
+                                                           accumulate);
     timer_trimul_output.stop();
     if (int e = pf::check_launch("trimul_output")) return e;
   }
