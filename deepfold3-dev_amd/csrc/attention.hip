@@ -40,6 +40,9 @@ constexpr int kHeads = 4;
 constexpr int kHeadDim = 32;
 constexpr int kC = 128;
 constexpr int kPad = 128;  // token padding of the attention frame
+#ifndef PF_ATTN_QS
+#define PF_ATTN_QS 2
+#endif
 
 // Storage slot -> key inside a 32-key block, and its inverse.
 PF_DEVICE int slot_key(int slot) { return 8 * ((slot & 15) >> 2) + 4 * (slot >> 4) + (slot & 3); }
@@ -268,26 +271,40 @@ PF_DEVICE Frag16<float> pack_p(const f32x16& p, float) {
 }
 
 template <class TC>
-constexpr int attn_qsub() { return sizeof(TC) == 2 ? 4 : 2; }  // 32-query sub-blocks per wave
-constexpr int kLinesPerBlock = 4;                                 // one line per wave
+constexpr int attn_qsub() { return sizeof(TC) == 2 ? PF_ATTN_QS : 2; }  // 32-query sub-blocks per wave
+#ifndef PF_ATTN_LPB
+#define PF_ATTN_LPB 4
+#endif
+constexpr int kLinesPerBlock = PF_ATTN_LPB;                       // one line per wave
 constexpr int kBiasLd = 36;                                       // LDS row of 32 slots + pad (floats)
-// Rescale the running sums only when a block's maximum exceeds the running reference by
-// more than this (base-2 units): probabilities stay <= 2^8, far inside fp32 and bf16 range,
-// and the normalised result does not depend on the reference.
-constexpr float kRescaleSlack = 8.0f;
+// Online-softmax reference. Probabilities are exp2(s - ref) with a per-query reference
+// that starts at 0 and is raised only when a key block's maximum exceeds it by more than
+// kRaise (base-2 units), so p <= 2^kRaise and a row sum <= N 2^kRaise stay far inside the
+// fp32 and bf16 exponent range; a first block whose maximum is below -kLower (a masked
+// start) sets the reference to it. The normalised result does not depend on the
+// reference, and while it is 0 -- the common case -- the per-logit subtraction is skipped.
+constexpr float kRaise = 32.0f;
+constexpr float kLower = 64.0f;
 
 // Block: 4 waves = 4 consecutive lines, one head, QB = 32 * QS queries. The pair-bias tile
-// (shared by the 4 lines) is staged through LDS, double-buffered; K and V are per line
-// and loaded straight into MFMA operand registers, one key block ahead.
-template <class TC, bool BIAS_KEY_MAJOR>
-__global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__ Q, const TC* __restrict__ K,
-                                                          const TC* __restrict__ Vt, const float* __restrict__ PB,
-                                                          const float* __restrict__ MA, TC* __restrict__ O, int B,
-                                                          int N, int Np, int xcd_remap) {
-  constexpr int QS = attn_qsub<TC>();
+// (shared by the 4 lines) is staged through LDS, double-buffered; Q is staged through LDS
+// once; K and V are per line and loaded straight into MFMA operand registers, one key
+// block ahead.
+template <class TC, bool BIAS_KEY_MAJOR, int QS>
+__global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2)) void tri_attn_kernel(const TC* __restrict__ Q,
+                                                                        const TC* __restrict__ K,
+                                                                        const TC* __restrict__ Vt,
+                                                                        const float* __restrict__ PB,
+                                                                        const float* __restrict__ MA,
+                                                                        TC* __restrict__ O, int B, int N, int Np,
+                                                                        int xcd_remap) {
   constexpr int QB = 32 * QS;
-  constexpr int NT = 256;
+  constexpr int NT = 64 * kLinesPerBlock;
+  constexpr int QLD = kHeadDim + lds_pad<TC>();
+  constexpr int QVEC = 16 / sizeof(TC);
   __shared__ __attribute__((aligned(16))) float bias_lds[2][QB * kBiasLd];
+  __shared__ __attribute__((aligned(16))) TC q_lds[kLinesPerBlock][QB * QLD];
+  __shared__ int same_mask[kLinesPerBlock];
 
   const int nqb = Np / QB;
   const int nlg = (N + kLinesPerBlock - 1) / kLinesPerBlock;
@@ -318,21 +335,36 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__
   const float* MAl = MA + lineq * Np;
   const int q0 = qb * QB;
 
-  // Bias tile staging: QB queries x 32 key slots per key block.
+  // Bias tile staging: QB queries x 32 key slots per key block. When every line of the
+  // block has the same key mask (the common case: pair masks are seq x seq, so all
+  // unpadded lines share one row), the mask row is added to the shared tile here once,
+  // instead of per wave and per logit. MA0 is the first line's mask row.
+  const float* MA0 = MA + ((size_t)b * Np + lg * kLinesPerBlock) * Np;
   constexpr int BIAS_IT = QB * 32 / 4 / NT;
   f32x4 bpf[BIAS_IT];
+  bool fold_mask = false;
   auto bias_load = [&](int k0) {
 #pragma unroll
     for (int it = 0; it < BIAS_IT; ++it) {
       const int idx = tid + it * NT;
-      if (BIAS_KEY_MAJOR) {  // rows: 32 keys of QB queries
-        const int k = idx / (QB / 4);
-        const int qq = (idx % (QB / 4)) * 4;
+      if (BIAS_KEY_MAJOR) {  // lanes run over the 32 keys, so the transposing LDS writes hit 32 banks
+        const int k = idx & 31;
+        const int qq = (idx >> 5) * 4;
         bpf[it] = *reinterpret_cast<const f32x4*>(PBh + (size_t)(k0 + k) * Np + q0 + qq);
+        if (fold_mask) {
+          const float m = MA0[k0 + key_slot(k)];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bpf[it][e] += m;
+        }
       } else {  // rows: QB queries of 32 slots
         const int qq = idx / 8;
         const int s0 = (idx % 8) * 4;
         bpf[it] = *reinterpret_cast<const f32x4*>(PBh + (size_t)(q0 + qq) * Np + k0 + s0);
+        if (fold_mask) {
+          const f32x4 m = *reinterpret_cast<const f32x4*>(MA0 + k0 + s0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bpf[it][e] += m[e];
+        }
       }
     }
   };
@@ -342,8 +374,8 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__
     for (int it = 0; it < BIAS_IT; ++it) {
       const int idx = tid + it * NT;
       if (BIAS_KEY_MAJOR) {
-        const int k = idx / (QB / 4);
-        const int qq = (idx % (QB / 4)) * 4;
+        const int k = idx & 31;
+        const int qq = (idx >> 5) * 4;
         const int s = key_slot(k);
 #pragma unroll
         for (int e = 0; e < 4; ++e) dst[(qq + e) * kBiasLd + s] = bpf[it][e];
@@ -355,16 +387,38 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__
     }
   };
 
-  Frag16<TC> qf[QS];
-  f32x16 o[QS];
-  float mref[QS], lrun[QS];
-  bool masked = false;
+  // Q of this wave's line -> LDS (rows of D elements, padded)
+  TC* qw = q_lds[w];
   if (active) {
 #pragma unroll
-    for (int s = 0; s < QS; ++s) qf[s].load(Qh + (size_t)(q0 + 32 * s + lq) * kHeadDim + 16 * hf);
-    for (int k = l; k < N; k += 64) masked |= MAl[(k & ~31) + key_slot(k & 31)] != 0.f;
+    for (int it = 0; it < QB * kHeadDim / QVEC / 64; ++it) {
+      const int idx = l + it * 64;
+      const int qq = idx / (kHeadDim / QVEC);
+      const int d0 = (idx % (kHeadDim / QVEC)) * QVEC;
+      *reinterpret_cast<u32x4*>(qw + qq * QLD + d0) =
+          *reinterpret_cast<const u32x4*>(Qh + (size_t)(q0 + qq) * kHeadDim + d0);
+    }
+  }
+  bool masked = false, same = true;
+  if (active) {
+    for (int k = l; k < N; k += 64) {
+      const int sl = (k & ~31) + key_slot(k & 31);
+      const float m = MAl[sl];
+      masked |= m != 0.f;
+      same &= m == MA0[sl];
+    }
   }
   masked = __any(masked);
+  same = __all(same);
+  if (l == 0) same_mask[w] = same ? 1 : 0;
+  __syncthreads();
+  fold_mask = true;
+#pragma unroll
+  for (int i = 0; i < kLinesPerBlock; ++i) fold_mask = fold_mask && same_mask[i];
+  if (fold_mask) masked = false;  // the tile carries the mask (and the padding keys' -inf)
+
+  f32x16 o[QS];
+  float mref[QS], lrun[QS];
 #pragma unroll
   for (int s = 0; s < QS; ++s) {
 #pragma unroll
@@ -374,23 +428,30 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__
   }
 
   const int nkb = (N + 31) / 32;
+  Frag16<TC> kf, vf;
+  if (active) {
+    kf.load(Kh + (size_t)lq * kHeadDim + 16 * hf);
+    vf.load(Vh + (size_t)lq * Np + 16 * hf);
+  }
   bias_load(0);
   bias_store(0);
   __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * 32;
     const bool more = kb + 1 < nkb;
-    Frag16<TC> kf, vf;
-    if (active) {
-      kf.load(Kh + (size_t)(k0 + lq) * kHeadDim + 16 * hf);
-      vf.load(Vh + (size_t)lq * Np + k0 + 16 * hf);
+    Frag16<TC> kn, vn;
+    if (more) {
+      bias_load(k0 + 32);
+      if (active) {
+        kn.load(Kh + (size_t)(k0 + 32 + lq) * kHeadDim + 16 * hf);
+        vn.load(Vh + (size_t)lq * Np + k0 + 32 + 16 * hf);
+      }
     }
-    if (more) bias_load(k0 + 32);
     if (active) {
       // Additive key mask, applied after q k^T + pb as the reference orders the fp32 adds
       // (a fully masked line then rounds every logit to the same -1e9 log2 e). The MA slots
       // of padding keys hold -inf.
-      const bool use_madd = masked || k0 + 32 > N;
+      const bool use_madd = masked || (!fold_mask && k0 + 32 > N);
       const float* mrow = MAl + k0 + 16 * hf;
       const float* bl = bias_lds[kb & 1];
 #pragma unroll
@@ -403,15 +464,18 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__
 #pragma unroll
           for (int e = 0; e < 4; ++e) sacc[4 * i + e] = bv[e];
         }
-        mma32_16(sacc, kf, qf[s]);  // log2-domain q k^T + pb
+        Frag16<TC> qf;
+        qf.load(qw + (32 * s + lq) * QLD + 16 * hf);
+        mma32_16(sacc, kf, qf);  // log2-domain q k^T + pb
         if (use_madd) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const f32x4 mv = *reinterpret_cast<const f32x4*>(mrow + 4 * i);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sacc[4 * i + e] = (sacc[4 * i + e] + mv[e]) - mref[s];
+            for (int e = 0; e < 4; ++e) sacc[4 * i + e] += mv[e];
           }
-        } else {
+        }
+        if (__any(mref[s] != 0.f)) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) sacc[r] -= mref[s];
         }
@@ -421,8 +485,9 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__
         mx = fmaxf(mx, sacc[15]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const bool first = kb == 0;
-        if (__any(first || mx > kRescaleSlack)) {
-          const float delta = (first || mx > kRescaleSlack) ? mx : 0.f;
+        const bool shift = mx > kRaise || (first && mx < -kLower);
+        if (__any(shift)) {
+          const float delta = shift ? mx : 0.f;
           const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(-delta);
           mref[s] += delta;
           lrun[s] *= alpha;
@@ -442,7 +507,11 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const TC* __restrict__
         mma32_16(o[s], vf, pack_p(sacc, TC{}));
       }
     }
-    if (more) bias_store((kb + 1) & 1);
+    if (more) {
+      bias_store((kb + 1) & 1);
+      kf = kn;
+      vf = vn;
+    }
     __syncthreads();
   }
   if (!active) return;
@@ -605,10 +674,12 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     const int remap = (total % 8 == 0) ? 1 : 0;
     dim3 grid((unsigned)total);
     pf::KernelTimer timer("tri_attn", s);
+    constexpr int QS = attn_qsub<TC>();
+    constexpr int NT = 64 * kLinesPerBlock;
     if (transpose)
-      tri_attn_kernel<TC, true><<<grid, 256, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, remap);
+      tri_attn_kernel<TC, true, QS><<<grid, NT, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, remap);
     else
-      tri_attn_kernel<TC, false><<<grid, 256, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, remap);
+      tri_attn_kernel<TC, false, QS><<<grid, NT, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, remap);
     timer.stop();
     if (int e = pf::check_launch("tri_attn")) return e;
   }

@@ -13,6 +13,8 @@
 // stored [i][k] and Q = b stored [j][k]. For the incoming one, X_ij = sum_k a_kj b_ki,
 // K1 walks z along columns and stores the planes transposed (P = b^T as [i][k],
 // Q = a^T as [j][k]), so K2 is always the same k-contiguous "NT" GEMM.
+#include <type_traits>
+
 #include "capi.h"
 #include "common.h"
 
@@ -235,6 +237,132 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(const TC* __restri
     *reinterpret_cast<u32x4*>(Xg + (size_t)row * Np + chunk * VEC) =
         *reinterpret_cast<const u32x4*>(O + row * OLD + chunk * VEC);
   }
+}
+
+// bf16 contraction on 256x256 tiles (used when Np is a multiple of 256). Eight waves in
+// 2 x 4, each owning a 128 (i) x 64 (j) block as 2 x 4 tiles of v_mfma_f32_32x32x16_bf16
+// (128 fp32 accumulators per lane); each LDS fragment feeds two or four MFMAs.
+// k-tiles of 64 flow through two LDS stages filled by global_load_lds_dwordx4 (global ->
+// LDS without registers): tile t + 1 is loaded while tile t is multiplied, one barrier per
+// tile. A wave's direct load writes 1 KiB lane-linearly (8 rows x 128 bytes), so the tiles
+// are unpadded and the 16-byte chunk c of row R is stored at chunk c ^ ((R >> 1) & 7).
+// LDS serves a 128-bit read for 16 lanes at a time over 64 four-byte banks; the 16 lanes
+// of a fragment read 16 consecutive rows at the same chunk, and the swizzle gives the 8
+// row pairs sharing a 256-byte bank window the 8 different chunk slots in it.
+// The waves compute X^T (A = Q rows j, B = P rows i): each lane holds four consecutive
+// output columns j of one row i, and lanes l, l + 32 together 16 contiguous bytes.
+struct Contract256 {
+  static constexpr int BT = 256;
+  static constexpr int KT = 64;
+  static constexpr int NT = 512;
+  static constexpr int TILE = BT * KT;       // elements of one operand k-tile
+  static constexpr int STAGE = 2 * TILE;     // P tile then Q tile
+  static constexpr int SMEM = 2 * STAGE * 2;
+};
+
+PF_DEVICE int k2_swz(int row) { return (row >> 1) & 7; }
+
+__global__ __launch_bounds__(512) void trimul_contract256_kernel(const bf16* __restrict__ P, const bf16* __restrict__ Q,
+                                                                 bf16* __restrict__ X, int G, int Np, int xcd_remap) {
+  using Cfg = Contract256;
+  constexpr int BT = Cfg::BT, KT = Cfg::KT;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  bf16* lds = reinterpret_cast<bf16*>(smem);
+
+  const int tiles1 = Np / BT;
+  const int tiles = tiles1 * tiles1;
+  int bid = blockIdx.x;
+  int g, tile;
+  if (xcd_remap) {  // XCD x walks planes x, x+8, ...: a plane's operands stay in one L2
+    const int xcd = bid & 7;
+    const int u = bid >> 3;
+    g = xcd + 8 * (u / tiles);
+    tile = u % tiles;
+  } else {
+    g = bid / tiles;
+    tile = bid % tiles;
+  }
+  if (g >= G) return;
+  const int i0 = (tile / tiles1) * BT;
+  const int j0 = (tile % tiles1) * BT;
+  const size_t pe = (size_t)Np * Np;
+  const bf16* Pg = P + (size_t)g * pe + (size_t)i0 * Np;
+  const bf16* Qg = Q + (size_t)g * pe + (size_t)j0 * Np;
+
+  const int w = wave_id();
+  const int l = lane_id();
+  const int wi = (w >> 2) * 128;  // wave's rows i in the tile
+  const int wj = (w & 3) * 64;    // wave's columns j
+
+  // Direct loads: a stage is 64 blocks of 8 rows (P blocks 0..31, Q blocks 32..63); wave w
+  // loads blocks 8w .. 8w + 7. Lane l writes row 8 blk + l / 8 at physical chunk l % 8,
+  // i.e. logical chunk (l % 8) ^ swz(row).
+  const int lrow = l >> 3;
+  const int lpc = l & 7;
+  auto issue = [&](int kt) {
+    bf16* st = lds + (kt & 1) * Cfg::STAGE;
+    const int k0 = kt * KT;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int blk = 8 * w + q;
+      const int op = blk >> 5;
+      const int row = (blk & 31) * 8 + lrow;
+      const int c = lpc ^ k2_swz(row);
+      const bf16* src = (op ? Qg : Pg) + (size_t)row * Np + k0 + 8 * c;
+      __builtin_amdgcn_global_load_lds(
+          (__attribute__((address_space(1))) const void*)src,
+          (__attribute__((address_space(3))) void*)(st + op * Cfg::TILE + (blk & 31) * 8 * KT), 16, 0, 0);
+    }
+  };
+
+  f32x16 acc[2][4];  // [j tile][i tile]
+  zero_acc32(acc);
+  const int nk = Np / KT;
+  const int r = l & 31;
+  const int hf = l >> 5;
+  issue(0);
+  for (int kt = 0; kt < nk; ++kt) {
+    // s_waitcnt vmcnt(0) (other counters untouched): this wave's loads of tile kt landed.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    // All waves' loads of tile kt visible; stage (kt + 1) & 1 no longer read. A bare
+    // s_barrier: __syncthreads() would add a full memory fence.
+    __builtin_amdgcn_s_barrier();
+    if (kt + 1 < nk) issue(kt + 1);
+    const bf16* Ps = lds + (kt & 1) * Cfg::STAGE;
+    const bf16* Qs = Ps + Cfg::TILE;
+#pragma unroll
+    for (int kk = 0; kk < KT; kk += 16) {
+      const int c = kk / 8 + hf;
+      bf16x8 af[2], bfr[4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int R = wj + 32 * t + r;
+        af[t] = *reinterpret_cast<const bf16x8*>(Qs + R * KT + 8 * (c ^ k2_swz(R)));
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int R = wi + 32 * t + r;
+        bfr[t] = *reinterpret_cast<const bf16x8*>(Ps + R * KT + 8 * (c ^ k2_swz(R)));
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+          acc[a][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[cc], acc[a][cc], 0, 0, 0);
+    }
+  }
+
+  // acc[a][c] element e: j = wj + 32 a + acc32_row(e), i = wi + 32 c + (lane & 31).
+  bf16* Xg = X + (size_t)g * pe + (size_t)i0 * Np + j0;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        float v[4] = {acc[a][cc][4 * g4], acc[a][cc][4 * g4 + 1], acc[a][cc][4 * g4 + 2], acc[a][cc][4 * g4 + 3]};
+        store_vec<bf16, 4>(Xg + (size_t)(wi + 32 * cc + r) * Np + wj + 32 * a + acc32_row(4 * g4), v);
+      }
 }
 
 // ------------------------------------------------------------------ K3
@@ -651,13 +779,36 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
       attr_set = true;
     }
     const int G = B * C;
-    const int tiles = (Np / Cfg::BMN) * (Np / Cfg::BMN);
     const int remap = (G % 8 == 0) ? 1 : 0;
-    dim3 grid((unsigned)(G * tiles));
-    pf::KernelTimer timer_trimul_contract("trimul_contract", s);
-    trimul_contract_kernel<TC><<<grid, 256, Cfg::SMEM, s>>>(P, Q, X, G, Np, remap);
-    timer_trimul_contract.stop();
-    if (int e = pf::check_launch("trimul_contract")) return e;
+    bool done = false;
+    if constexpr (sizeof(TC) == 2) {
+      if (Np % Contract256::BT == 0) {
+        static bool attr256 = false;
+        if (!attr256) {
+          hipError_t e = hipFuncSetAttribute((const void*)trimul_contract256_kernel,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, Contract256::SMEM);
+          PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "trimul_contract: cannot reserve %d bytes of LDS: %s",
+                     Contract256::SMEM, hipGetErrorString(e));
+          attr256 = true;
+        }
+        const int t1 = Np / Contract256::BT;
+        dim3 grid((unsigned)(G * t1 * t1));
+        pf::KernelTimer timer_trimul_contract("trimul_contract", s);
+        trimul_contract256_kernel<<<grid, Contract256::NT, Contract256::SMEM, s>>>((const bf16*)P, (const bf16*)Q,
+                                                                                   (bf16*)X, G, Np, remap);
+        timer_trimul_contract.stop();
+        if (int e = pf::check_launch("trimul_contract")) return e;
+        done = true;
+      }
+    }
+    if (!done) {
+      const int tiles = (Np / Cfg::BMN) * (Np / Cfg::BMN);
+      dim3 grid((unsigned)(G * tiles));
+      pf::KernelTimer timer_trimul_contract("trimul_contract", s);
+      trimul_contract_kernel<TC><<<grid, 256, Cfg::SMEM, s>>>(P, Q, X, G, Np, remap);
+      timer_trimul_contract.stop();
+      if (int e = pf::check_launch("trimul_contract")) return e;
+    }
   }
   {
     constexpr bool k32 = sizeof(TC) == 2;

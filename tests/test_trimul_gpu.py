@@ -41,8 +41,8 @@ def test_trimul_fp32_matches_oracle(dev, outgoing, n, pad):
 
 
 @pytest.mark.parametrize("outgoing", [True, False])
-def test_trimul_bf16_tolerance_rule(dev, outgoing):
-    n = 96
+@pytest.mark.parametrize("n", [96, 200, 500])  # padded 128 / 256 / 512: both contraction tilings
+def test_trimul_bf16_tolerance_rule(dev, outgoing, n):
     sd = W.make_block_weights(12, perturb_affine=True)
     p = sub(sd, "tri_mul_out." if outgoing else "tri_mul_in.")
     inp = W.make_inputs(n, seed=5, pad_random=6)
