@@ -70,6 +70,24 @@ def kernel_launch_flops(kernel: str, n: int) -> float:
     }[kernel]
 
 
+def profiled_traffic(kernel: str, n: int) -> float | None:
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter summary.
+
+    The summary (profiles/trunk_n768_bf16_hbm_traffic.md) holds FETCH_SIZE and WRITE_SIZE per
+    dispatch from two counter runs of this script, scaled by a 1 GiB copy measured in the same
+    runs; counters cannot be read live in the timed run.
+    """
+    path = os.path.join(ROOT, "profiles", f"trunk_n{n}_bf16_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    key = f"traffic_bytes_per_launch {kernel}:"
+    with open(path) as f:
+        for line in f:
+            if line.startswith(key):
+                return float(line.split(":", 1)[1])
+    return None
+
+
 def build_stack(evoformer, W, n_blocks: int, seed: int, dev, dtype):
     import torch
 
@@ -134,6 +152,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager-steps", type=int, default=1)
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--calibration-copy", action="store_true", help="run one 1 GiB copy (for PMC byte scaling)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -169,6 +188,15 @@ def main() -> int:
     single = inp["single"].to(dev, torch.bfloat16)
     pm, sm = inp["pair_mask"].to(dev), inp["seq_mask"].to(dev)
 
+    if args.calibration_copy:
+        # A plain 1 GiB device-to-device copy: under `rocprofv3 --pmc FETCH_SIZE` (or
+        # WRITE_SIZE) its counter value per byte scales the kernels' readings to bytes.
+        buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        buf.clone()
+        torch.cuda.synchronize()
+        del buf
+
+    out = None
     with torch.no_grad():
         for i in range(args.warmup):
             out = stack(pair, single, pm, sm)
@@ -241,7 +269,8 @@ def main() -> int:
             "avg_launch_ms": round(k_avg_ms, 4),
             "launches": k_count,
             "flops_per_launch": k_flops,
-            "traffic": None,
+            "traffic": profiled_traffic(args.roofline_kernel, n),
+            "traffic_source": "profiles/trunk_n768_bf16_hbm_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-scaled)",
         },
         "cpu_baseline": cpu,
         "gpu_eager": eager,
