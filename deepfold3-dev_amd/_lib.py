@@ -57,6 +57,12 @@ SIGNATURES: dict[str, tuple] = {
         _i,
         [_vp, _vp, _vp, _f, _vp, _vp, _l, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
     ),
+    "pf_evo_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "pf_evo_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "pf_pair_bias_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
+    "pf_layernorm_linear_workspace_bytes": (_sz, [_l, _i, _i]),
+    "pf_layernorm_linear_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, _vp, _l, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "pf_swiglu_fwd": (_i, [_vp, _i, _vp, _l, _i, _vp]),
     "pf_single_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "pf_single_attn_fwd": (
         _i,

@@ -290,13 +290,18 @@ constexpr float kLower = 64.0f;
 // (shared by the 4 lines) is staged through LDS, double-buffered; Q is staged through LDS
 // once; K and V are per line and loaded straight into MFMA operand registers, one key
 // block ahead.
-template <class TC, bool BIAS_KEY_MAJOR, int QS>
+// L lines per batch item (line stride Lp in the operand buffers). O_HEAD_MAJOR writes O as
+// [b][line][h][q][d] with q < N (the reference kernel's layout) instead of the frame's
+// [b][line][q][h d]; zero_masked_lines writes 0 for a line whose keys are all masked (the
+// reference kernel's rule) instead of the eager path's uniform average.
+template <class TC, bool BIAS_KEY_MAJOR, int QS, bool O_HEAD_MAJOR>
 __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2)) void tri_attn_kernel(const TC* __restrict__ Q,
                                                                         const TC* __restrict__ K,
                                                                         const TC* __restrict__ Vt,
                                                                         const float* __restrict__ PB,
                                                                         const float* __restrict__ MA,
                                                                         TC* __restrict__ O, int B, int N, int Np,
+                                                                        int L, int Lp, int zero_masked_lines,
                                                                         int xcd_remap) {
   constexpr int QB = 32 * QS;
   constexpr int NT = 64 * kLinesPerBlock;
@@ -307,7 +312,7 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   __shared__ int same_mask[kLinesPerBlock];
 
   const int nqb = Np / QB;
-  const int nlg = (N + kLinesPerBlock - 1) / kLinesPerBlock;
+  const int nlg = (L + kLinesPerBlock - 1) / kLinesPerBlock;
   const int total = B * nlg * kHeads * nqb;
   int bid = blockIdx.x;
   if (xcd_remap) bid = (bid & 7) * (total >> 3) + (bid >> 3);
@@ -323,11 +328,11 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   const int w = wave_id();
   const int l = lane_id();
   const int line = lg * kLinesPerBlock + w;
-  const bool active = line < N;  // inactive waves still stage the shared bias tiles
+  const bool active = line < L;  // inactive waves still stage the shared bias tiles
 
   const int lq = l & 31;
   const int hf = l >> 5;
-  const size_t lineq = (size_t)b * Np + line;
+  const size_t lineq = (size_t)b * Lp + line;
   const TC* Qh = Q + (lineq * kHeads + h) * (size_t)Np * kHeadDim;
   const TC* Kh = K + (lineq * kHeads + h) * (size_t)Np * kHeadDim;
   const TC* Vh = Vt + (lineq * kHeads + h) * (size_t)kHeadDim * Np;
@@ -339,7 +344,7 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   // block has the same key mask (the common case: pair masks are seq x seq, so all
   // unpadded lines share one row), the mask row is added to the shared tile here once,
   // instead of per wave and per logit. MA0 is the first line's mask row.
-  const float* MA0 = MA + ((size_t)b * Np + lg * kLinesPerBlock) * Np;
+  const float* MA0 = MA + ((size_t)b * Lp + lg * kLinesPerBlock) * Np;
   constexpr int BIAS_IT = QB * 32 / 4 / NT;
   f32x4 bpf[BIAS_IT];
   bool fold_mask = false;
@@ -399,17 +404,19 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
           *reinterpret_cast<const u32x4*>(Qh + (size_t)(q0 + qq) * kHeadDim + d0);
     }
   }
-  bool masked = false, same = true;
+  bool masked = false, same = true, all_masked = true;
   if (active) {
     for (int k = l; k < N; k += 64) {
       const int sl = (k & ~31) + key_slot(k & 31);
       const float m = MAl[sl];
       masked |= m != 0.f;
       same &= m == MA0[sl];
+      all_masked &= m < -1e8f;
     }
   }
   masked = __any(masked);
   same = __all(same);
+  all_masked = __all(all_masked);
   if (l == 0) same_mask[w] = same ? 1 : 0;
   __syncthreads();
   fold_mask = true;
@@ -517,14 +524,15 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   if (!active) return;
 
   // O^T lane (q, hf) holds d = 8 (r >> 2) + 4 hf + (r & 3).
-  TC* Ol = O + lineq * (size_t)Np * kC;
+  const bool write_zero = zero_masked_lines && all_masked;
 #pragma unroll
   for (int s = 0; s < QS; ++s) {
     const float lt = lrun[s] + __shfl_xor(lrun[s], 32, 64);
-    const float inv = 1.0f / lt;
+    const float inv = write_zero ? 0.f : 1.0f / lt;
     const int q = q0 + 32 * s + lq;
     if (q >= N) continue;
-    TC* dst = Ol + (size_t)q * kC + h * kHeadDim;
+    TC* dst = O_HEAD_MAJOR ? O + ((lineq * kHeads + h) * (size_t)N + q) * kHeadDim
+                           : O + (lineq * (size_t)Np + q) * kC + h * kHeadDim;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v[4];
@@ -677,9 +685,9 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     constexpr int QS = attn_qsub<TC>();
     constexpr int NT = 64 * kLinesPerBlock;
     if (transpose)
-      tri_attn_kernel<TC, true, QS><<<grid, NT, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, remap);
+      tri_attn_kernel<TC, true, QS, false><<<grid, NT, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap);
     else
-      tri_attn_kernel<TC, false, QS><<<grid, NT, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, remap);
+      tri_attn_kernel<TC, false, QS, false><<<grid, NT, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap);
     timer.stop();
     if (int e = pf::check_launch("tri_attn")) return e;
   }
@@ -691,6 +699,136 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     if (int e = pf::check_launch("attn_out")) return e;
   }
   return pf::ok();
+}
+
+// ------------------------------------------------------------------ kernel-level op
+// _EvoformerAttention.apply(Q, K, V, res_mask, pair_bias, pre_transposed=True)
+// (triton/evo_attention.py:1198-1292): O = softmax(Q K^T d^-1/2 + pair_bias + res_mask) V
+// per (batch, line, head) with Q, K, V, O as [B][S][H][N][D], res_mask additive [B][S][N],
+// pair_bias [B][H][N][N] fp32. The operands are repacked into the attention frame (padded
+// to Np, Q pre-scaled by d^-1/2 log2 e, V transposed with the key-slot order, bias and mask
+// times log2 e) and run through the same flash kernel. -inf mask entries become -1e9.
+template <class TC>
+__global__ __launch_bounds__(256) void evo_pack_qk_kernel(const TC* __restrict__ q, const TC* __restrict__ k,
+                                                          TC* __restrict__ Qw, TC* __restrict__ Kw, int N, int Np,
+                                                          float qscale) {
+  constexpr int VEC = 16 / sizeof(TC);
+  constexpr int CPT = kHeadDim / VEC;  // chunks per token
+  const size_t bsh = blockIdx.y;       // (b, s, h) flattened
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= Np * CPT) return;
+  const int t = idx / CPT;
+  const int d0 = (idx % CPT) * VEC;
+  float vq[VEC], vk[VEC];
+  if (t < N) {
+    load16<TC>(q + (bsh * N + t) * kHeadDim + d0, vq);
+    load16<TC>(k + (bsh * N + t) * kHeadDim + d0, vk);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) vq[e] *= qscale;
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) vq[e] = vk[e] = 0.f;
+  }
+  store_vec<TC, VEC>(Qw + (bsh * Np + t) * kHeadDim + d0, vq);
+  store_vec<TC, VEC>(Kw + (bsh * Np + t) * kHeadDim + d0, vk);
+}
+
+// One block per (32-key block, b s h): V[t][d] -> Vt[d][slot].
+template <class TC>
+__global__ __launch_bounds__(256) void evo_pack_v_kernel(const TC* __restrict__ v, TC* __restrict__ Vt, int N,
+                                                         int Np) {
+  __shared__ float tile[32][kHeadDim + 1];
+  const size_t bsh = blockIdx.y;
+  const int k0 = blockIdx.x * 32;
+  for (int i = threadIdx.x; i < 32 * kHeadDim; i += 256) {
+    const int t = i / kHeadDim, d = i % kHeadDim;
+    tile[t][d] = (k0 + t < N) ? to_f32(v[(bsh * N + k0 + t) * kHeadDim + d]) : 0.f;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 32 * kHeadDim; i += 256) {
+    const int d = i / 32, slot = i % 32;
+    Vt[(bsh * kHeadDim + d) * Np + k0 + slot] = from_f32<TC>(tile[slot_key(slot)][d]);
+  }
+}
+
+__global__ __launch_bounds__(256) void evo_pack_bias_kernel(const float* __restrict__ pb, float* __restrict__ PB,
+                                                            int N, int Np) {
+  const size_t bh = blockIdx.y;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)Np * Np) return;
+  const int qi = (int)(idx / Np);
+  const int sl = (int)(idx % Np);
+  const int kk = (sl & ~31) + slot_key(sl & 31);
+  PB[bh * Np * Np + idx] = (qi < N && kk < N) ? pb[(bh * N + qi) * N + kk] * kLog2e : 0.f;
+}
+
+__global__ __launch_bounds__(256) void evo_pack_mask_kernel(const float* __restrict__ rm, float* __restrict__ MA,
+                                                            int N, int Np) {
+  const size_t bs = blockIdx.y;
+  const int sl = blockIdx.x * 256 + threadIdx.x;
+  if (sl >= Np) return;
+  const int kk = (sl & ~31) + slot_key(sl & 31);
+  float v = -INFINITY;
+  if (kk < N) v = fmaxf(rm[bs * N + kk], -1e9f) * kLog2e;
+  MA[bs * Np + sl] = v;
+}
+
+struct EvoWs {
+  size_t q, k, v, pb, ma, total;
+};
+
+EvoWs evo_ws_layout(int B, int S, int N, int cdtype) {
+  const size_t Np = pf::round_up((size_t)N, kPad);
+  const size_t es = cdtype == PF_F32 ? 4 : 2;
+  const size_t tok = (size_t)B * S * kHeads * Np * kHeadDim * es;
+  EvoWs w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += pf::round_up(bytes, 256);
+    return at;
+  };
+  w.q = take(tok);
+  w.k = take(tok);
+  w.v = take(tok);
+  w.pb = take((size_t)B * kHeads * Np * Np * 4);
+  w.ma = take((size_t)B * S * Np * 4);
+  w.total = off;
+  return w;
+}
+
+template <class TC>
+int evo_attn_launch(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias, int B,
+                    int S, int N, int zero_rule, void* out, void* ws, hipStream_t s) {
+  const int Np = (int)pf::round_up((size_t)N, kPad);
+  const EvoWs L = evo_ws_layout(B, S, N, sizeof(TC) == 4 ? PF_F32 : PF_BF16);
+  char* base = reinterpret_cast<char*>(ws);
+  TC* Qw = reinterpret_cast<TC*>(base + L.q);
+  TC* Kw = reinterpret_cast<TC*>(base + L.k);
+  TC* Vw = reinterpret_cast<TC*>(base + L.v);
+  float* PBw = reinterpret_cast<float*>(base + L.pb);
+  float* MAw = reinterpret_cast<float*>(base + L.ma);
+  const float qscale = (1.0f / sqrtf((float)kHeadDim)) * kLog2e;
+  const unsigned bsh = (unsigned)(B * S * kHeads);
+  constexpr int VEC = 16 / sizeof(TC);
+  evo_pack_qk_kernel<TC><<<dim3((Np * (kHeadDim / VEC) + 255) / 256, bsh), 256, 0, s>>>(
+      (const TC*)q, (const TC*)k, Qw, Kw, N, Np, qscale);
+  evo_pack_v_kernel<TC><<<dim3(Np / 32, bsh), 256, 0, s>>>((const TC*)v, Vw, N, Np);
+  evo_pack_bias_kernel<<<dim3((unsigned)(((long)Np * Np + 255) / 256), B * kHeads), 256, 0, s>>>(pair_bias, PBw,
+                                                                                                   N, Np);
+  evo_pack_mask_kernel<<<dim3((Np + 255) / 256, B * S), 256, 0, s>>>(res_mask, MAw, N, Np);
+  if (int e = pf::check_launch("evo_attn pack")) return e;
+  constexpr int QS = attn_qsub<TC>();
+  constexpr int NT = 64 * kLinesPerBlock;
+  const int nqb = Np / (32 * QS);
+  const int nlg = (S + kLinesPerBlock - 1) / kLinesPerBlock;
+  const long total = (long)B * nlg * kHeads * nqb;
+  const int remap = (total % 8 == 0) ? 1 : 0;
+  pf::KernelTimer timer("evo_attn", s);
+  tri_attn_kernel<TC, false, QS, true><<<dim3((unsigned)total), NT, 0, s>>>(Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np,
+                                                                            S, S, zero_rule, remap);
+  timer.stop();
+  return pf::check_launch("evo_attn");
 }
 
 }  // namespace
@@ -728,6 +866,31 @@ int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const 
                                          workspace, s);
   return grid_attn_launch<bf16, bf16>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, transpose, out, accumulate,
                                       workspace, s);
+}
+
+size_t pf_evo_attn_workspace_bytes(int B, int S, int H, int N, int D, int dtype) {
+  if (B <= 0 || S <= 0 || N <= 0 || H != kHeads || D != kHeadDim) return 0;
+  return evo_ws_layout(B, S, N, dtype).total;
+}
+
+int pf_evo_attn_fwd(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias, int B,
+                    int S, int H, int N, int D, int dtype, int masked_rows_zero, void* out, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(q && k && v && res_mask && pair_bias && out && workspace, PF_ERR_INVALID_ARG,
+             "pf_evo_attn_fwd: null pointer");
+  PF_REQUIRE(B > 0 && S > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_evo_attn_fwd: B=%d S=%d N=%d", B, S, N);
+  PF_REQUIRE(H == kHeads && D == kHeadDim, PF_ERR_UNSUPPORTED, "pf_evo_attn_fwd: H=%d D=%d (built: H=4, D=32)", H,
+             D);
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_evo_attn_fwd: dtype %d", dtype);
+  PF_REQUIRE(pf::aligned16(q) && pf::aligned16(k) && pf::aligned16(v) && pf::aligned16(out) &&
+                 pf::aligned16(workspace),
+             PF_ERR_ALIGNMENT, "pf_evo_attn_fwd: pointers must be 16-byte aligned");
+  PF_REQUIRE(workspace_bytes >= evo_ws_layout(B, S, N, dtype).total, PF_ERR_WORKSPACE,
+             "pf_evo_attn_fwd: workspace %zu < %zu bytes", workspace_bytes, evo_ws_layout(B, S, N, dtype).total);
+  hipStream_t s = pf::as_stream(stream);
+  if (dtype == PF_F32)
+    return evo_attn_launch<float>(q, k, v, res_mask, pair_bias, B, S, N, masked_rows_zero, out, workspace, s);
+  return evo_attn_launch<bf16>(q, k, v, res_mask, pair_bias, B, S, N, masked_rows_zero, out, workspace, s);
 }
 
 }  // extern "C"

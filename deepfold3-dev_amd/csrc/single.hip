@@ -164,6 +164,19 @@ __global__ __launch_bounds__(256) void single_attn_core_kernel(const TC* __restr
   }
 }
 
+// y = silu(x[:, :D]) * x[:, D:] (FusedSwiGLU, triton/swiglu.py:30-58, :192-200).
+template <class T>
+__global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ x, T* __restrict__ y, long M, int D) {
+  const long n = M * D;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    const long r = i / D;
+    const int c = (int)(i % D);
+    const float a = to_f32(x[r * 2 * D + c]);
+    const float bb = to_f32(x[r * 2 * D + D + c]);
+    y[i] = from_f32<T>(siluf_(a) * bb);
+  }
+}
+
 template <class TI, class TO>
 int ln_launch(const void* x, const float* w, const float* b, float eps, void* out, long M, int C, hipStream_t s) {
   ln_rows_kernel<TI, TO><<<(unsigned)((M + 3) / 4), 256, 0, s>>>((const TI*)x, w, b, eps, (TO*)out, M, C);
@@ -256,6 +269,52 @@ int pf_single_attn_fwd(const void* s, const float* seq_mask, const float* pair_l
   hipStream_t st = pf::as_stream(stream);
   return PF_DISPATCH_ZC(zdtype, cdtype, single_attn_launch, s, seq_mask, pair_logits, ln_w, ln_b, eps, w_qkvg, q_bias,
                         w_out, B, N, C, H, out, accumulate, workspace, st);
+}
+
+int pf_swiglu_fwd(const void* x, int dtype, void* y, long M, int D, void* stream) {
+  PF_REQUIRE(x && y, PF_ERR_INVALID_ARG, "pf_swiglu_fwd: null pointer");
+  PF_REQUIRE(M >= 0 && D > 0, PF_ERR_INVALID_ARG, "pf_swiglu_fwd: M=%ld D=%d", M, D);
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_swiglu_fwd: dtype %d", dtype);
+  if (M == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  const long n = M * D;
+  const unsigned g = (unsigned)((n + 255) / 256 > 65536 ? 65536 : (n + 255) / 256);
+  if (dtype == PF_F32)
+    swiglu_kernel<float><<<g, 256, 0, s>>>((const float*)x, (float*)y, M, D);
+  else
+    swiglu_kernel<bf16><<<g, 256, 0, s>>>((const bf16*)x, (bf16*)y, M, D);
+  return pf::check_launch("swiglu");
+}
+
+size_t pf_layernorm_linear_workspace_bytes(long M, int K, int cdtype) {
+  if (M <= 0 || K <= 0) return 0;
+  return pf::round_up((size_t)M * K * es_of(cdtype), 256);
+}
+
+int pf_layernorm_linear_fwd(const void* x, int xdtype, const float* ln_w, const float* ln_b, float eps,
+                            const void* w_nk, const float* bias, long M, int K, int Nout, int cdtype, void* out,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(x && ln_w && ln_b && w_nk && out && workspace, PF_ERR_INVALID_ARG,
+             "pf_layernorm_linear_fwd: null pointer");
+  PF_REQUIRE(M >= 0 && K > 0 && Nout > 0, PF_ERR_INVALID_ARG, "pf_layernorm_linear_fwd: M=%ld K=%d N=%d", M, K, Nout);
+  PF_REQUIRE(K % 32 == 0 && Nout % 16 == 0, PF_ERR_UNSUPPORTED,
+             "pf_layernorm_linear_fwd: K=%d N=%d (K a multiple of 32, N of 16)", K, Nout);
+  PF_REQUIRE(dtype_pair_ok(xdtype, cdtype), PF_ERR_UNSUPPORTED, "pf_layernorm_linear_fwd: dtype pair (%d, %d)",
+             xdtype, cdtype);
+  PF_REQUIRE(workspace_bytes >= pf_layernorm_linear_workspace_bytes(M, K, cdtype), PF_ERR_WORKSPACE,
+             "pf_layernorm_linear_fwd: workspace too small");
+  if (M == 0) return pf::ok();
+  hipStream_t st = pf::as_stream(stream);
+  if (cdtype == PF_F32) {
+    if (int e = ln_launch<float, float>(x, ln_w, ln_b, eps, workspace, M, K, st)) return e;
+    return rowgemm_launch<float, float, EPI_STORE>(workspace, w_nk, bias, bias ? Nout : 0, out, M, Nout, K, st);
+  }
+  if (xdtype == PF_F32) {
+    if (int e = ln_launch<float, bf16>(x, ln_w, ln_b, eps, workspace, M, K, st)) return e;
+    return rowgemm_launch<bf16, float, EPI_STORE>(workspace, w_nk, bias, bias ? Nout : 0, out, M, Nout, K, st);
+  }
+  if (int e = ln_launch<bf16, bf16>(x, ln_w, ln_b, eps, workspace, M, K, st)) return e;
+  return rowgemm_launch<bf16, bf16, EPI_STORE>(workspace, w_nk, bias, bias ? Nout : 0, out, M, Nout, K, st);
 }
 
 size_t pf_transition_workspace_bytes(long M, int C, int factor, int cdtype) {

@@ -298,6 +298,43 @@ __global__ __launch_bounds__(256) void single_to_pair_kernel(const TZ* __restric
   s2p_store<TC, BM>(A, ALD, Ws, logits, m0, M, NN);
 }
 
+// FusedPairBias (triton/fused_pair_bias.py:348-416): LN(z) proj_w^T -> [B][H][N][N] in z's
+// dtype, plus (1 - mask[b][j]) * (-1e9) when a [B][N] mask is given. Computed in fp32 (the
+// reference's projection runs at fp32 accuracy, fused_pair_bias.py:198): the LN tile is
+// fp32 and the projection uses v_mfma_f32_16x16x4f32 against proj_w padded to 16 rows.
+template <class TZ>
+__global__ __launch_bounds__(256) void pair_bias_kernel(const TZ* __restrict__ z, const float* __restrict__ lnw,
+                                                        const float* __restrict__ lnb, float eps,
+                                                        const float* __restrict__ w16, const float* __restrict__ mask,
+                                                        TZ* __restrict__ out, int H, long M, long NN, int N) {
+  constexpr int BM = 32;
+  constexpr int ALD = kC + lds_pad<float>();
+  __shared__ __attribute__((aligned(16))) float A[BM * ALD];
+  const long m0 = (long)blockIdx.x * BM;
+  auto zrow = [&](int p) -> const TZ* { return m0 + p < M ? z + (m0 + p) * kC : nullptr; };
+  ln_tile_to_lds<TZ, float, kC, BM, 256>(zrow, lnw, lnb, eps, A, ALD);
+  __syncthreads();
+  const int w = wave_id();
+  const int l = lane_id();
+  if (w >= BM / 16) return;
+  f32x4 acc[1][1];
+  zero_acc(acc);
+  int wrow[1] = {0};
+  gemm16_lds_x_w<float, kC, 1, 1>(acc, A, ALD, w * 16, w16, kC, wrow);
+  const int h = l & 15;
+  if (h >= H) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const long m = m0 + w * 16 + 4 * (l >> 4) + e;
+    if (m >= M) continue;
+    const long b = m / NN;
+    const long pos = m % NN;
+    float v = acc[0][0][e];
+    if (mask) v += (1.0f - mask[b * N + pos % N]) * (-1e9f);
+    out[(b * H + h) * NN + pos] = from_f32<TZ>(v);
+  }
+}
+
 template <class TZ, class TC>
 int transition_launch(const void* x, const float* lnw, const float* lnb, float eps, const void* w1, const void* w2,
                       long M, void* out, int accumulate, const float* s2p_w, const float* s2p_b, float s2p_eps,
@@ -367,6 +404,26 @@ int pf_pair_transition_fwd(const void* x, const float* ln_w, const float* ln_b, 
   hipStream_t s = pf::as_stream(stream);
   return PF_DISPATCH_ZC(zdtype, cdtype, transition_launch, x, ln_w, ln_b, eps, w1, w2, M, out, accumulate, s2p_ln_w,
                         s2p_ln_b, s2p_eps, w_s2p, pair_logits, NN, s);
+}
+
+int pf_pair_bias_fwd(const void* z, int zdtype, const float* ln_w, const float* ln_b, float eps,
+                     const float* proj_w16, int H, const float* mask, void* out, int B, int N, int C, void* stream) {
+  PF_REQUIRE(z && ln_w && ln_b && proj_w16 && out, PF_ERR_INVALID_ARG, "pf_pair_bias_fwd: null pointer");
+  PF_REQUIRE(C == kC && H >= 1 && H <= 16, PF_ERR_UNSUPPORTED, "pf_pair_bias_fwd: C=%d H=%d (built: C=128, H<=16)",
+             C, H);
+  PF_REQUIRE(B >= 0 && N >= 0, PF_ERR_INVALID_ARG, "pf_pair_bias_fwd: B=%d N=%d", B, N);
+  PF_REQUIRE(zdtype == PF_F32 || zdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_pair_bias_fwd: zdtype %d", zdtype);
+  const long NN = (long)N * N, M = (long)B * NN;
+  if (M == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  dim3 grid((unsigned)((M + 31) / 32));
+  if (zdtype == PF_F32)
+    pair_bias_kernel<float><<<grid, 256, 0, s>>>((const float*)z, ln_w, ln_b, eps, proj_w16, mask, (float*)out, H, M,
+                                                 NN, N);
+  else
+    pair_bias_kernel<bf16><<<grid, 256, 0, s>>>((const bf16*)z, ln_w, ln_b, eps, proj_w16, mask, (bf16*)out, H, M,
+                                                NN, N);
+  return pf::check_launch("pair_bias");
 }
 
 int pf_single_to_pair_fwd(const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_s2p, long M,

@@ -1,0 +1,219 @@
+"""The reference's kernel-level operators (``src/deepfold3/model/triton/``) on the HIP library.
+
+Same class and function names, constructor arguments and call signatures as the
+reference, so call sites written against its Triton layer run unchanged:
+
+- ``_EvoformerAttention.apply`` / ``fused_evo_attention`` (``evo_attention.py:1198-1510``)
+- ``FusedPairBias`` (``fused_pair_bias.py:348-416``)
+- ``FusedLayerNormTranspose`` (``layernorm_transpose.py:269-316``)
+- ``FusedLayerNormLinear`` (``layernorm_linear.py:537-592``)
+- ``FusedSwiGLU`` (``swiglu.py:192-200``)
+- ``FusedTransitionBlock`` (``fused_transition.py:34-83``)
+- ``dropout_add_rowwise`` / ``dropout_add_columnwise`` (``dropout_add.py:221-265``)
+
+All are forward-only (inference): under grad they raise ``InferenceOnlyKernelError``;
+anything the kernels cannot serve raises ``NotActive``. There is no PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _lib, kernel_census
+from .inference_guard import NotActive, inference_only
+from .kernels import cast_weight, gemm_dtype_for, ln_transpose, residual_add
+from .primitives import TransitionBlock, f32
+
+__all__ = [
+    "_EvoformerAttention",
+    "fused_evo_attention",
+    "FusedPairBias",
+    "FusedLayerNormTranspose",
+    "FusedLayerNormLinear",
+    "FusedSwiGLU",
+    "FusedTransitionBlock",
+    "dropout_add_rowwise",
+    "dropout_add_columnwise",
+]
+
+
+def _ws(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+class _EvoformerAttention:
+    """Flash attention with pair bias and per-line key mask (``evo_attention.py:1198-1292``).
+
+    ``apply(Q, K, V, res_mask, pair_bias, pre_transposed=False, masked_rows="zero")``:
+    Q, K, V ``[B, N_seq, N_res, H, D]`` (or ``[B, N_seq, H, N_res, D]`` with
+    ``pre_transposed=True``), ``res_mask [B, N_seq, 1, 1, N_res]`` additive fp32,
+    ``pair_bias [B, 1, H, N_res, N_res]`` fp32. Returns O in the layout of Q.
+    ``masked_rows="zero"`` is the reference kernel's rule for a line whose keys are all
+    masked (output 0, ``evo_attention.py:307-318``); ``"eager"`` gives the stock path's
+    uniform average (``attention.py:157-160``). Built for H = 4, D = 32.
+    """
+
+    @staticmethod
+    @inference_only("evo_attention")
+    def apply(Q, K, V, res_mask, pair_bias, pre_transposed: bool = False, masked_rows: str = "zero"):
+        _lib.require_device("evo_attention", Q, K, V, res_mask, pair_bias)
+        if masked_rows not in ("zero", "eager"):
+            raise ValueError(f"masked_rows must be 'zero' or 'eager', got {masked_rows!r}")
+        if not pre_transposed:
+            Q, K, V = (t.transpose(-2, -3) for t in (Q, K, V))
+        Q, K, V = (t.contiguous() for t in (Q, K, V))
+        B, S, H, N, D = Q.shape
+        if K.shape != Q.shape or V.shape != Q.shape or K.dtype != Q.dtype or V.dtype != Q.dtype:
+            raise NotActive("evo_attention", "Q, K, V must share shape and dtype")
+        rm = res_mask.to(torch.float32).expand(B, S, 1, 1, N).reshape(B, S, N).contiguous()
+        pb = pair_bias.to(torch.float32).expand(B, 1, H, N, N).reshape(B, H, N, N).contiguous()
+        out = torch.empty_like(Q)
+        code = _lib.dtype_code(Q.dtype)
+        ws_bytes = _lib.lib().pf_evo_attn_workspace_bytes(B, S, H, N, D, code)
+        if ws_bytes == 0:
+            raise NotActive("evo_attention", f"H={H}, D={D}: built for H=4, D=32")
+        ws = _ws(ws_bytes, Q.device)
+        kernel_census.record("evo_attention", "hip_evo_attn")
+        _lib.call(
+            "pf_evo_attn_fwd", Q.data_ptr(), K.data_ptr(), V.data_ptr(), rm.data_ptr(), pb.data_ptr(), B, S, H, N, D,
+            code, int(masked_rows == "zero"), out.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(Q),
+        )  # fmt: skip
+        if not pre_transposed:
+            out = out.transpose(-2, -3).contiguous()
+        return out
+
+
+def fused_evo_attention(q, k, v, pair_bias, mask):
+    """Reference wrapper (``evo_attention.py:1475-1510``): q, k, v ``[B*N_rows, N_cols, H, D]``,
+    pair_bias ``[B or 1, H, N, N]``, mask ``[B*N_rows, N_cols]`` (1 keep, 0 drop)."""
+    BN, N_cols, H, D = q.shape
+    B = pair_bias.shape[0]
+    N_rows = BN // B
+    q5, k5, v5 = (t.view(B, N_rows, N_cols, H, D) for t in (q, k, v))
+    res_mask = mask.view(B, N_rows, 1, 1, N_cols).float()
+    res_mask = torch.where(res_mask > 0.5, 0.0, float("-inf"))
+    if pair_bias.dim() == 4:
+        pair_bias = pair_bias.unsqueeze(1)
+    o5 = _EvoformerAttention.apply(q5, k5, v5, res_mask, pair_bias.float())
+    return o5.view(BN, N_cols, H, D)
+
+
+class FusedPairBias(nn.Module):
+    """LN + ``[C -> H]`` projection + permute to ``[B, H, N, N]`` (stateless; ``fused_pair_bias.py:348-416``)."""
+
+    def __init__(self, c: int, num_heads: int, eps: float = 1e-5):
+        super().__init__()
+        self.c, self.num_heads, self.eps = c, num_heads, eps
+
+    @inference_only("FusedPairBias")
+    def forward(self, z, ln_weight, ln_bias, proj_weight, mask=None):
+        _lib.require_device("FusedPairBias", z)
+        B, N, _, C = z.shape
+        H = proj_weight.shape[0]
+        if C != self.c or H > 16:
+            raise NotActive("FusedPairBias", f"C={C}, H={H}: built for C=128, H<=16")
+        zc = z.contiguous()
+        w16 = torch.zeros(16, C, dtype=torch.float32, device=z.device)
+        w16[:H] = proj_weight.detach().float()
+        m = None if mask is None else mask.to(torch.float32).contiguous()
+        out = torch.empty((B, H, N, N), dtype=z.dtype, device=z.device)
+        kernel_census.record("GridSelfAttention.norm", "hip_pair_bias")
+        _lib.call(
+            "pf_pair_bias_fwd", zc.data_ptr(), _lib.dtype_code(z.dtype), f32(ln_weight).data_ptr(),
+            f32(ln_bias).data_ptr(), float(self.eps), w16.data_ptr(), H, _lib.ptr(m), out.data_ptr(), B, N, C,
+            _lib.stream_of(zc),
+        )  # fmt: skip
+        return out
+
+
+class FusedLayerNormTranspose(nn.Module):
+    """``LN(x).permute(0, 2, 1, 3)`` for x ``[B, N1, N2, C]`` (stateless; ``layernorm_transpose.py:269-316``)."""
+
+    def __init__(self, c: int, do_transpose: bool = True, eps: float = 1e-5):
+        super().__init__()
+        self.c, self.do_transpose, self.eps = c, do_transpose, eps
+
+    @inference_only("FusedLayerNormTranspose")
+    def forward(self, x, weight, bias):
+        kernel_census.record("GridSelfAttention.norm", "hip_ln_transpose")
+        return ln_transpose(x, weight, bias, self.eps, self.do_transpose)
+
+
+class FusedLayerNormLinear(nn.Module):
+    """``LN(X) W + b`` with W passed as ``[K, N]`` (stateless; ``layernorm_linear.py:537-592``)."""
+
+    def __init__(self, in_features: int, out_features: int, has_linear_bias: bool = False):
+        super().__init__()
+        self.in_features, self.out_features, self.has_linear_bias = in_features, out_features, has_linear_bias
+        self._wkey = None
+        self._wval = None
+
+    def _w_nk(self, W: torch.Tensor, cdt: torch.dtype) -> torch.Tensor:
+        key = (W.data_ptr(), W._version, tuple(W.shape), cdt)
+        if key != self._wkey:
+            self._wval = cast_weight(W.detach().t().contiguous(), cdt)
+            self._wkey = key
+        return self._wval
+
+    @inference_only("FusedLayerNormLinear")
+    def forward(self, X, ln_weight, ln_bias, linear_weight, linear_bias=None):
+        if linear_bias is not None and not self.has_linear_bias:
+            raise ValueError("linear_bias provided but module configured with has_linear_bias=False")
+        _lib.require_device("FusedLayerNormLinear", X)
+        K, N = self.in_features, self.out_features
+        if tuple(linear_weight.shape) != (K, N):
+            raise NotActive("FusedLayerNormLinear", f"weight must be [K, N] = [{K}, {N}]")
+        cdt = gemm_dtype_for(X)
+        Xc = X.contiguous()
+        M = Xc.numel() // K
+        out = torch.empty(Xc.shape[:-1] + (N,), dtype=X.dtype, device=X.device)
+        code_c = _lib.dtype_code(cdt)
+        ws_bytes = _lib.lib().pf_layernorm_linear_workspace_bytes(M, K, code_c)
+        ws = _ws(ws_bytes, X.device)
+        b = None if linear_bias is None else f32(linear_bias)
+        _lib.call(
+            "pf_layernorm_linear_fwd", Xc.data_ptr(), _lib.dtype_code(X.dtype), f32(ln_weight).data_ptr(),
+            f32(ln_bias).data_ptr(), 1e-5, self._w_nk(linear_weight, cdt).data_ptr(), _lib.ptr(b), M, K, N, code_c,
+            out.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(Xc),
+        )  # fmt: skip
+        return out
+
+
+class FusedSwiGLU(nn.Module):
+    """``silu(a) * b`` with ``[a, b] = split(x, 2, dim=-1)`` (``swiglu.py:192-200``)."""
+
+    @inference_only("FusedSwiGLU")
+    def forward(self, x):
+        _lib.require_device("FusedSwiGLU", x)
+        xc = x.contiguous()
+        D = xc.shape[-1] // 2
+        y = torch.empty(xc.shape[:-1] + (D,), dtype=x.dtype, device=x.device)
+        _lib.call("pf_swiglu_fwd", xc.data_ptr(), _lib.dtype_code(x.dtype), y.data_ptr(), xc.numel() // (2 * D), D,
+                  _lib.stream_of(xc))  # fmt: skip
+        return y
+
+
+class FusedTransitionBlock(TransitionBlock):
+    """The reference's fused pair transition (``fused_transition.py:34-83``): same keys, HIP kernels."""
+
+    def __init__(self, channels: int, num_intermediate_factor: int = 4, optim=None):
+        super().__init__(channels, num_intermediate_factor, optim=optim)
+        self.channels = channels
+
+
+def _dropout_add(residual, x, p_drop: float, training: bool, site: str):
+    if training and p_drop > 0.0:
+        raise NotActive(site, "training-mode dropout is not built (eval only)")
+    kernel_census.record(site, "hip_add")
+    return residual_add(residual, x)
+
+
+def dropout_add_rowwise(residual, x, p_drop: float, training: bool, use_fused: bool = True):
+    """Eval: ``residual + x`` (``dropout_add.py:221-242``); training dropout refuses."""
+    return _dropout_add(residual, x, p_drop, training, "dropout_add_rowwise")
+
+
+def dropout_add_columnwise(residual, x, p_drop: float, training: bool, use_fused: bool = True):
+    """Eval: ``residual + x`` (``dropout_add.py:245-265``); training dropout refuses."""
+    return _dropout_add(residual, x, p_drop, training, "dropout_add_columnwise")

@@ -148,6 +148,34 @@ int pf_single_attn_fwd(const void* s, const float* seq_mask, const float* pair_l
                        int N, int C, int H, int zdtype, int cdtype, void* out, int accumulate, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* ---- kernel-level operators of the reference's Triton layer -------------- */
+/* _EvoformerAttention.apply(Q, K, V, res_mask, pair_bias, pre_transposed=True)
+ * (triton/evo_attention.py:1198-1292): q, k, v, out [B,S,H,N,D] (dtype), res_mask [B,S,N]
+ * fp32 additive (0 / -1e9 or -inf; the contiguous view of [B,S,1,1,N]), pair_bias
+ * [B,H,N,N] fp32 (the view of [B,1,H,N,N]). out = softmax(q k^T D^-1/2 + pair_bias +
+ * res_mask) v. masked_rows_zero != 0 writes 0 for a line whose keys are all masked (the
+ * Triton kernel's rule, evo_attention.py:307-318); 0 gives the eager path's uniform
+ * average (attention.py:157-160). Built: H = 4, D = 32. */
+size_t pf_evo_attn_workspace_bytes(int B, int S, int H, int N, int D, int dtype);
+int pf_evo_attn_fwd(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias, int B,
+                    int S, int H, int N, int D, int dtype, int masked_rows_zero, void* out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+/* FusedPairBias(c, H)(z, ln_w, ln_b, proj_w, mask) (triton/fused_pair_bias.py:348-416):
+ * z [B,N,N,C] -> out [B,H,N,N] in z's dtype; proj_w16 [16, C] fp32 (proj_w padded with zero
+ * rows); mask [B,N] fp32 or NULL adds (1 - mask) * (-1e9) on the last axis. C = 128, H <= 16. */
+int pf_pair_bias_fwd(const void* z, int zdtype, const float* ln_w, const float* ln_b, float eps,
+                     const float* proj_w16, int H, const float* mask, void* out, int B, int N, int C, void* stream);
+/* FusedLayerNormLinear(K, N)(X, ln_w, ln_b, W, bias) (triton/layernorm_linear.py:537-592):
+ * out [M, N] (x's dtype) = LN(x [M, K]) W + bias, with W passed as w_nk [N, K] (cdtype; the
+ * reference's [K, N] argument transposed once by the caller), bias fp32 [N] or NULL.
+ * K a multiple of 32, N of 16. */
+size_t pf_layernorm_linear_workspace_bytes(long M, int K, int cdtype);
+int pf_layernorm_linear_fwd(const void* x, int xdtype, const float* ln_w, const float* ln_b, float eps,
+                            const void* w_nk, const float* bias, long M, int K, int Nout, int cdtype, void* out,
+                            void* workspace, size_t workspace_bytes, void* stream);
+/* FusedSwiGLU()(x) (triton/swiglu.py:192-200): y [M, D] = silu(x[:, :D]) * x[:, D:], x [M, 2D]. */
+int pf_swiglu_fwd(const void* x, int dtype, void* y, long M, int D, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
