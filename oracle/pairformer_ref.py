@@ -123,13 +123,16 @@ def grid_attention(
     transpose: bool,
     num_heads: int = 4,
     row_chunk: int = 0,
+    lines: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Stock ``GridSelfAttention.forward`` (``attention.py:167-269``, no fused kernels).
 
     The pair bias comes from the un-transposed LN(z) (``attention.py:204-209``);
     column mode transposes LN(z) and the mask, attends, and transposes back.
     ``row_chunk`` evaluates that many rows at a time (rows are independent,
-    so it is exact) to bound the fp32 logits.
+    so it is exact) to bound the fp32 logits. ``lines`` (indices into the
+    attended axis: rows of z, or columns when ``transpose``) evaluates only
+    those lines and returns ``[B, len(lines), N, C]`` in the attention frame.
     """
     B, N, _, C = z.shape
     H = num_heads
@@ -139,6 +142,9 @@ def grid_attention(
     if transpose:
         zn = zn.permute(0, 2, 1, 3)
         mask = mask.permute(0, 2, 1)
+    if lines is not None:
+        zn = zn[:, lines]
+        mask = mask[:, lines]
     N_rows, N_cols = zn.shape[1], zn.shape[2]
     chunk = row_chunk if row_chunk > 0 else N_rows
     outs = []
@@ -148,7 +154,7 @@ def grid_attention(
         o = _grid_attention_rows(rows, pb, mask[:, r0:r1], p, B, r1 - r0, N_cols, H, D)
         outs.append(o.view(B, r1 - r0, N_cols, -1))
     out = torch.cat(outs, dim=1) if len(outs) > 1 else outs[0]
-    if transpose:
+    if transpose and lines is None:
         out = out.permute(0, 2, 1, 3)
     return out
 

@@ -241,6 +241,20 @@ def test_batch_consistency_and_row_chunking():
     assert rel_l2(pc, pb) < 1e-6 and rel_l2(sc, sb) < 1e-6
 
 
+@pytest.mark.parametrize("transpose", [False, True])
+def test_grid_attention_line_subset_equals_whole(transpose):
+    """The sampled-line evaluation used at N=2048 picks the same lines out of the whole."""
+    sd = W.make_block_weights(6, perturb_affine=True)
+    p = sub(sd, "pair_attn_col." if transpose else "pair_attn_row.")
+    inp = W.make_inputs(20, seed=4, pad_random=3)
+    lines = torch.tensor([0, 7, 19])
+    with torch.no_grad():
+        whole = R.grid_attention(inp["pair"], inp["pair_mask"], p, transpose=transpose)
+        part = R.grid_attention(inp["pair"], inp["pair_mask"], p, transpose=transpose, lines=lines)
+    picked = whole[:, :, lines] if transpose else whole[:, lines]
+    assert rel_l2(part.transpose(1, 2) if transpose else part, picked) < 1e-6
+
+
 def test_mask_changes_output():
     sd = W.make_block_weights(4)
     a = W.make_inputs(10, seed=1)
