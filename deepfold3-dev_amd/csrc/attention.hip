@@ -20,9 +20,9 @@
 // ending node (column mode). Keys and queries run along the other token index. The
 // projection kernel walks z along a line in both modes (column mode reads z down a column),
 // so every operand is written contiguously in the attention frame. The pair bias is
-// stored query-major [h][q][key slot] in row mode and key-major [h][key][q] in column mode
-// (again the order in which the projection produces it); the attention kernel stages it
-// through LDS either way.
+// written query-major [h][q][key slot] in row mode and key-major [h][key][q] in column mode
+// (again the order in which the projection produces it); an in-place tile transpose turns
+// the latter query-major, the layout the attention kernel streams into LDS.
 //
 // MFMA layout (v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x2f32). A wave owns 32 queries
 // per sub-block and computes S^T = K Q^T (keys are accumulator rows), so lane (q, h)
@@ -270,13 +270,20 @@ PF_DEVICE Frag16<float> pack_p(const f32x16& p, float) {
   return f;
 }
 
+// max(x[l], x[l ^ 32]) over the wave's two 32-lane halves. v_permlane32_swap of x with
+// itself leaves (x[l], x[l + 32]) in the low half and (x[l - 32], x[l]) in the high half:
+// a VALU op, no LDS round trip.
+PF_DEVICE float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <class TC>
 constexpr int attn_qsub() { return sizeof(TC) == 2 ? PF_ATTN_QS : 2; }  // 32-query sub-blocks per wave
 #ifndef PF_ATTN_LPB
 #define PF_ATTN_LPB 4
 #endif
 constexpr int kLinesPerBlock = PF_ATTN_LPB;                       // one line per wave
-constexpr int kBiasLd = 36;                                       // LDS row of 32 slots + pad (floats)
 // Online-softmax reference. Probabilities are exp2(s - ref) with a per-query reference
 // that starts at 0 and is raised only when a key block's maximum exceeds it by more than
 // kRaise (base-2 units), so p <= 2^kRaise and a row sum <= N 2^kRaise stay far inside the
@@ -285,31 +292,63 @@ constexpr int kBiasLd = 36;                                       // LDS row of 
 // reference, and while it is 0 -- the common case -- the per-logit subtraction is skipped.
 constexpr float kRaise = 32.0f;
 constexpr float kLower = 64.0f;
+constexpr int kBiasStages = 3;  // LDS ring of pair-bias tiles, filled two key blocks ahead
+
+// XOR swizzle of the 16-byte chunks of a 128-byte bias row: the 16 lanes of a ds_read_b128
+// (rows R..R+15, one logical chunk) land on 16 distinct bank groups.
+PF_DEVICE int bias_swz(int row) { return (row >> 1) & 7; }
+
+// Dynamic LDS of the flash kernel: the bias ring, kBiasStages tiles of QB x 32 fp32.
+template <class TC>
+constexpr size_t attn_bias_lds_bytes() { return (size_t)kBiasStages * 32 * attn_qsub<TC>() * 32 * 4; }
+
+// Register sets for the K / V / mask-row prefetch ring (bf16: two key blocks ahead).
+template <class TC>
+constexpr int attn_kv_sets() { return sizeof(TC) == 2 ? 3 : 2; }
+
+// Mask operand: S^T += M 1^T, A = the line's additive key mask in k-column 0 (lanes of the
+// low half, key row lane & 31), B = ones in k-column 0. Keys are MFMA rows in natural
+// order, so lane l reads the mask slot key_slot(l & 31).
+PF_DEVICE void mma_mask(f32x16& acc, float m, bf16) {
+  const bool lo = (threadIdx.x & 32) == 0;
+  bf16x8 a = {}, one = {};
+  a[0] = lo ? (bf16)m : (bf16)0.f;
+  one[0] = lo ? (bf16)1.f : (bf16)0.f;
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, one, acc, 0, 0, 0);
+}
+PF_DEVICE void mma_mask(f32x16& acc, float m, float) {
+  const bool lo = (threadIdx.x & 32) == 0;
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(lo ? m : 0.f, lo ? 1.f : 0.f, acc, 0, 0, 0);
+}
 
 // Block: 4 waves = 4 consecutive lines, one head, QB = 32 * QS queries. The pair-bias tile
-// (shared by the 4 lines) is staged through LDS, double-buffered; Q is staged through LDS
-// once; K and V are per line and loaded straight into MFMA operand registers, one key
-// block ahead.
+// (query-major, shared by the 4 lines) streams through a 3-stage LDS ring filled by
+// global_load_lds_dwordx4 two key blocks ahead; Q is staged through LDS once; K, V and the
+// line's mask slot for the lane's key row are per line and go straight into registers
+// (bf16: two key blocks ahead, in three register sets the unrolled key loop rotates).
 // L lines per batch item (line stride Lp in the operand buffers). O_HEAD_MAJOR writes O as
 // [b][line][h][q][d] with q < N (the reference kernel's layout) instead of the frame's
 // [b][line][q][h d]; zero_masked_lines writes 0 for a line whose keys are all masked (the
 // reference kernel's rule) instead of the eager path's uniform average.
-template <class TC, bool BIAS_KEY_MAJOR, int QS, bool O_HEAD_MAJOR>
-__global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2)) void tri_attn_kernel(const TC* __restrict__ Q,
-                                                                        const TC* __restrict__ K,
-                                                                        const TC* __restrict__ Vt,
-                                                                        const float* __restrict__ PB,
-                                                                        const float* __restrict__ MA,
-                                                                        TC* __restrict__ O, int B, int N, int Np,
-                                                                        int L, int Lp, int zero_masked_lines,
-                                                                        int xcd_remap) {
+template <class TC, int QS, bool O_HEAD_MAJOR>
+__global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2)) void tri_attn_kernel(
+    const TC* __restrict__ Q, const TC* __restrict__ K, const TC* __restrict__ Vt, const float* __restrict__ PB,
+    const float* __restrict__ MA, TC* __restrict__ O, int B, int N, int Np, int L, int Lp, int zero_masked_lines,
+    int xcd_remap) {
   constexpr int QB = 32 * QS;
   constexpr int NT = 64 * kLinesPerBlock;
   constexpr int QLD = kHeadDim + lds_pad<TC>();
   constexpr int QVEC = 16 / sizeof(TC);
-  __shared__ __attribute__((aligned(16))) float bias_lds[2][QB * kBiasLd];
+  constexpr int TILE = QB * 32;                   // floats per bias stage: QB rows of 32 slots
+  constexpr int DL = TILE * 4 / (NT * 16);        // direct loads per lane per stage
+  static_assert(DL * NT * 16 == TILE * 4, "bias stage must split evenly over the block");
+  constexpr int NSET = attn_kv_sets<TC>();
+  // vmcnt budget: loads a lane issues per key block (bias stage + K + V + mask slot)
+  constexpr int KV_LOADS = (sizeof(TC) == 2 ? 4 : 8) + 1;
+  // The bias ring is dynamic LDS (attn_bias_lds_bytes at launch): the stage a step reads
+  // is never the one its direct loads fill, and the explicit vmcnt + barrier order them.
+  extern __shared__ __attribute__((aligned(16))) float bias_lds[];
   __shared__ __attribute__((aligned(16))) TC q_lds[kLinesPerBlock][QB * QLD];
-  __shared__ int same_mask[kLinesPerBlock];
 
   const int nqb = Np / QB;
   const int nlg = (L + kLinesPerBlock - 1) / kLinesPerBlock;
@@ -324,72 +363,44 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   rest /= nlg;
   const int h = rest % kHeads;
   const int b = rest / kHeads;
-  const int tid = threadIdx.x;
   const int w = wave_id();
   const int l = lane_id();
   const int line = lg * kLinesPerBlock + w;
-  const bool active = line < L;  // inactive waves still stage the shared bias tiles
+  const bool active = line < L;  // inactive waves still load their share of the bias tiles
 
   const int lq = l & 31;
   const int hf = l >> 5;
-  const size_t lineq = (size_t)b * Lp + line;
+  const size_t lineq = (size_t)b * Lp + (active ? line : lg * kLinesPerBlock);
   const TC* Qh = Q + (lineq * kHeads + h) * (size_t)Np * kHeadDim;
   const TC* Kh = K + (lineq * kHeads + h) * (size_t)Np * kHeadDim;
   const TC* Vh = Vt + (lineq * kHeads + h) * (size_t)kHeadDim * Np;
   const float* PBh = PB + ((size_t)b * kHeads + h) * (size_t)Np * Np;
   const float* MAl = MA + lineq * Np;
   const int q0 = qb * QB;
+  const int nkb = (N + 31) / 32;
 
-  // Bias tile staging: QB queries x 32 key slots per key block. When every line of the
-  // block has the same key mask (the common case: pair masks are seq x seq, so all
-  // unpadded lines share one row), the mask row is added to the shared tile here once,
-  // instead of per wave and per logit. MA0 is the first line's mask row.
-  const float* MA0 = MA + ((size_t)b * Lp + lg * kLinesPerBlock) * Np;
-  constexpr int BIAS_IT = QB * 32 / 4 / NT;
-  f32x4 bpf[BIAS_IT];
-  bool fold_mask = false;
-  auto bias_load = [&](int k0) {
+  // Bias stage of key block kb: DL instructions per lane, each 8 rows x 128 B; lane l
+  // writes row 8 blk + l / 8 at physical chunk l % 8 = logical chunk (l % 8) ^ swz(row).
+  // Past the last key block the last tile is loaded again into a stage nobody reads, so
+  // every iteration issues the same number of loads (the vmcnt budget below relies on it).
+  auto bias_issue = [&](int kb) {
+    float* st = bias_lds + (kb % kBiasStages) * TILE;
+    const int k0 = min(kb, nkb - 1) * 32;
 #pragma unroll
-    for (int it = 0; it < BIAS_IT; ++it) {
-      const int idx = tid + it * NT;
-      if (BIAS_KEY_MAJOR) {  // lanes run over the 32 keys, so the transposing LDS writes hit 32 banks
-        const int k = idx & 31;
-        const int qq = (idx >> 5) * 4;
-        bpf[it] = *reinterpret_cast<const f32x4*>(PBh + (size_t)(k0 + k) * Np + q0 + qq);
-        if (fold_mask) {
-          const float m = MA0[k0 + key_slot(k)];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bpf[it][e] += m;
-        }
-      } else {  // rows: QB queries of 32 slots
-        const int qq = idx / 8;
-        const int s0 = (idx % 8) * 4;
-        bpf[it] = *reinterpret_cast<const f32x4*>(PBh + (size_t)(q0 + qq) * Np + k0 + s0);
-        if (fold_mask) {
-          const f32x4 m = *reinterpret_cast<const f32x4*>(MA0 + k0 + s0);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bpf[it][e] += m[e];
-        }
-      }
+    for (int j = 0; j < DL; ++j) {
+      const int blk = w * DL + j;
+      const int row = blk * 8 + (l >> 3);
+      const int c = (l & 7) ^ bias_swz(row);
+      const float* src = PBh + (size_t)(q0 + row) * Np + k0 + 4 * c;
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) const void*)src,
+                                       (__attribute__((address_space(3))) void*)(st + blk * 8 * 32), 16, 0, 0);
     }
   };
-  auto bias_store = [&](int buf) {
-    float* dst = bias_lds[buf];
-#pragma unroll
-    for (int it = 0; it < BIAS_IT; ++it) {
-      const int idx = tid + it * NT;
-      if (BIAS_KEY_MAJOR) {
-        const int k = idx & 31;
-        const int qq = (idx >> 5) * 4;
-        const int s = key_slot(k);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(qq + e) * kBiasLd + s] = bpf[it][e];
-      } else {
-        const int qq = idx / 8;
-        const int s0 = (idx % 8) * 4;
-        *reinterpret_cast<f32x4*>(dst + qq * kBiasLd + s0) = bpf[it];
-      }
-    }
+  auto kv_load = [&](int kb, Frag16<TC>& kf, Frag16<TC>& vf, float& mf) {
+    const int k0 = min(kb, nkb - 1) * 32;
+    kf.load(Kh + (size_t)(k0 + lq) * kHeadDim + 16 * hf);
+    vf.load(Vh + (size_t)lq * Np + k0 + 16 * hf);
+    mf = MAl[k0 + key_slot(lq)];
   };
 
   // Q of this wave's line -> LDS (rows of D elements, padded)
@@ -404,25 +415,16 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
           *reinterpret_cast<const u32x4*>(Qh + (size_t)(q0 + qq) * kHeadDim + d0);
     }
   }
-  bool masked = false, same = true, all_masked = true;
+  bool masked = false, all_masked = true;
   if (active) {
     for (int k = l; k < N; k += 64) {
-      const int sl = (k & ~31) + key_slot(k & 31);
-      const float m = MAl[sl];
+      const float m = MAl[(k & ~31) + key_slot(k & 31)];
       masked |= m != 0.f;
-      same &= m == MA0[sl];
       all_masked &= m < -1e8f;
     }
   }
   masked = __any(masked);
-  same = __all(same);
   all_masked = __all(all_masked);
-  if (l == 0) same_mask[w] = same ? 1 : 0;
-  __syncthreads();
-  fold_mask = true;
-#pragma unroll
-  for (int i = 0; i < kLinesPerBlock; ++i) fold_mask = fold_mask && same_mask[i];
-  if (fold_mask) masked = false;  // the tile carries the mask (and the padding keys' -inf)
 
   f32x16 o[QS];
   float mref[QS], lrun[QS];
@@ -434,93 +436,119 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
     lrun[s] = 0.f;
   }
 
-  const int nkb = (N + 31) / 32;
-  Frag16<TC> kf, vf;
-  if (active) {
-    kf.load(Kh + (size_t)lq * kHeadDim + 16 * hf);
-    vf.load(Vh + (size_t)lq * Np + 16 * hf);
-  }
-  bias_load(0);
-  bias_store(0);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
+  __syncthreads();  // Q tiles
+
+  // Every key-block step issues K/V/mask (NSET - 1 blocks ahead) and then one bias stage
+  // (two blocks ahead); the prologue issues what steps -2 and -1 would have, so every
+  // lane -- inactive waves load their group's first line -- keeps the same load order.
+  Frag16<TC> kr[NSET], vr[NSET];
+  float mr[NSET];
+  if (NSET == 3) kv_load(0, kr[0], vr[0], mr[0]);
+  bias_issue(0);
+  kv_load(NSET - 2, kr[NSET - 2], vr[NSET - 2], mr[NSET - 2]);
+  bias_issue(1);
+
+  auto step = [&](int kb, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf, Frag16<TC>& kn, Frag16<TC>& vn,
+                  float& mn) {
     const int k0 = kb * 32;
-    const bool more = kb + 1 < nkb;
-    Frag16<TC> kn, vn;
-    if (more) {
-      bias_load(k0 + 32);
-      if (active) {
-        kn.load(Kh + (size_t)(k0 + 32 + lq) * kHeadDim + 16 * hf);
-        vn.load(Vh + (size_t)lq * Np + k0 + 32 + 16 * hf);
+    // This lane's loads of bias stage kb landed (and with them, in issue order, the K/V
+    // of block kb): after them it issued one step's K/V/mask loads and one bias stage.
+    constexpr int after = KV_LOADS + DL;
+    static_assert(after < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(after | (7 << 4) | (15 << 8));
+    // Every wave's stage kb is visible, and stage (kb + 2) % 3 (read at kb - 1) is free.
+    __builtin_amdgcn_s_barrier();
+    kv_load(kb + NSET - 1, kn, vn, mn);
+    bias_issue(kb + 2);
+    if (!active) return;
+
+    // Phases over the QS query sub-blocks, so the MFMAs of one sub-block overlap the
+    // softmax VALU work of the other: S tiles, the (rare, wave-uniform) reference paths,
+    // row maxima, exp2 and packing, then the P V products.
+    const float* bl = bias_lds + (kb % kBiasStages) * TILE;
+    const bool use_mask = masked || k0 + 32 > N;  // padding keys hold -inf in MA
+    const float mk = kb < nkb ? mf : -INFINITY;
+    f32x16 sacc[QS];
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      const int R = 32 * s + lq;
+      const float* br = bl + R * 32;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(br + 4 * ((4 * hf + i) ^ bias_swz(R)));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sacc[s][4 * i + e] = bv[e];
       }
+      // Additive key mask first, then q k^T: a fully masked line rounds every logit to
+      // the same -1e9 log2 e, as the reference's fp32 adds do.
+      if (use_mask) mma_mask(sacc[s], mk, TC{});
+      Frag16<TC> qf;
+      qf.load(qw + R * QLD + 16 * hf);
+      mma32_16(sacc[s], kf, qf);  // log2-domain q k^T + pb + mask
     }
-    if (active) {
-      // Additive key mask, applied after q k^T + pb as the reference orders the fp32 adds
-      // (a fully masked line then rounds every logit to the same -1e9 log2 e). The MA slots
-      // of padding keys hold -inf.
-      const bool use_madd = masked || (!fold_mask && k0 + 32 > N);
-      const float* mrow = MAl + k0 + 16 * hf;
-      const float* bl = bias_lds[kb & 1];
+    bool ref_set = false;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) ref_set |= mref[s] != 0.f;
+    if (__any(ref_set)) {
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[s][r] -= mref[s];
+    }
+    float mx[QS];
+    bool any_shift = false;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      float m = fmaxf(fmaxf(sacc[s][0], sacc[s][1]), sacc[s][2]);
+#pragma unroll
+      for (int r = 3; r < 15; r += 2) m = fmaxf(fmaxf(m, sacc[s][r]), sacc[s][r + 1]);
+      m = fmaxf(m, sacc[s][15]);
+      mx[s] = max_xor32(m);
+      any_shift |= mx[s] > kRaise || (kb == 0 && mx[s] < -kLower);
+    }
+    if (__any(any_shift)) {
 #pragma unroll
       for (int s = 0; s < QS; ++s) {
-        f32x16 sacc;
-        const float* br = bl + (32 * s + lq) * kBiasLd + 16 * hf;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f32x4 bv = *reinterpret_cast<const f32x4*>(br + 4 * i);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sacc[4 * i + e] = bv[e];
-        }
-        Frag16<TC> qf;
-        qf.load(qw + (32 * s + lq) * QLD + 16 * hf);
-        mma32_16(sacc, kf, qf);  // log2-domain q k^T + pb
-        if (use_madd) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const f32x4 mv = *reinterpret_cast<const f32x4*>(mrow + 4 * i);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sacc[4 * i + e] += mv[e];
-          }
-        }
-        if (__any(mref[s] != 0.f)) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sacc[r] -= mref[s];
-        }
-        float mx = fmaxf(fmaxf(sacc[0], sacc[1]), sacc[2]);
-#pragma unroll
-        for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sacc[r]), sacc[r + 1]);
-        mx = fmaxf(mx, sacc[15]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const bool first = kb == 0;
-        const bool shift = mx > kRaise || (first && mx < -kLower);
-        if (__any(shift)) {
-          const float delta = shift ? mx : 0.f;
-          const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(-delta);
-          mref[s] += delta;
-          lrun[s] *= alpha;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            o[s][r] *= alpha;
-            sacc[r] -= delta;
-          }
-        }
-        float ls = 0.f;
+        const bool shift = mx[s] > kRaise || (kb == 0 && mx[s] < -kLower);
+        const float delta = shift ? mx[s] : 0.f;
+        const float alpha = kb == 0 ? 0.f : __builtin_amdgcn_exp2f(-delta);
+        mref[s] += delta;
+        lrun[s] *= alpha;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          sacc[r] = __builtin_amdgcn_exp2f(sacc[r]);
-          ls += sacc[r];
+          o[s][r] *= alpha;
+          sacc[s][r] -= delta;
         }
-        lrun[s] += ls;
-        mma32_16(o[s], vf, pack_p(sacc, TC{}));
       }
     }
-    if (more) {
-      bias_store((kb + 1) & 1);
-      kf = kn;
-      vf = vn;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      float ls = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sacc[s][r] = __builtin_amdgcn_exp2f(sacc[s][r]);
+        ls += sacc[s][r];
+      }
+      lrun[s] += ls;
     }
-    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < QS; ++s) mma32_16(o[s], vf, pack_p(sacc[s], TC{}));
+  };
+
+  // Key loop unrolled over the register sets: key block kb uses set kb % NSET and refills
+  // set (kb - 1) % NSET, consumed one block earlier. Only whole rounds of NSET blocks run
+  // (no conditional step, so the compiler's wait counts stay exact): a step past the last
+  // key block sees every key masked to -inf and adds nothing.
+  for (int kb0 = 0; kb0 < nkb; kb0 += NSET) {
+#pragma unroll
+    for (int u = 0; u < NSET; ++u) {
+      const int nx = (u + NSET - 1) % NSET;
+      step(kb0 + u, kr[u], vr[u], mr[u], kr[nx], vr[nx], mr[nx]);
+    }
   }
+  // The last steps loaded repeat tiles into LDS; none may land after the block's LDS is
+  // handed to another block.
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
   if (!active) return;
 
   // O^T lane (q, hf) holds d = 8 (r >> 2) + 4 hf + (r & 3).
@@ -540,6 +568,33 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
       for (int e = 0; e < 4; ++e) v[e] = o[s][4 * j + e] * inv;
       store_vec<TC, 4>(dst + 8 * j + 4 * hf, v);
     }
+  }
+}
+
+// Column mode: the projection kernel writes the pair bias key-major [h][key][q]; the flash
+// kernel reads it query-major in key-slot order, out[q][slot] = in[slot_key(slot)][q]
+// within each 32-block. 32 x 32 tile (I, J) of the output depends only on tile (J, I) of
+// the input, so one block swaps a tile pair in place (I <= J; blockIdx.y = b h).
+__global__ __launch_bounds__(256) void pb_transpose_kernel(float* __restrict__ PB, int Np) {
+  __shared__ float ta[32][33], tb[32][33];
+  const int nt = Np / 32;
+  int p = blockIdx.x, I = 0;
+  while (p >= nt - I) {
+    p -= nt - I;
+    ++I;
+  }
+  const int J = I + p;
+  float* M = PB + (size_t)blockIdx.y * Np * Np;
+  for (int i = threadIdx.x; i < 1024; i += 256) {
+    const int r = i >> 5, c = i & 31;
+    ta[r][c] = M[(size_t)(32 * I + r) * Np + 32 * J + c];
+    tb[r][c] = M[(size_t)(32 * J + r) * Np + 32 * I + c];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 1024; i += 256) {
+    const int q = i >> 5, sl = i & 31;
+    M[(size_t)(32 * I + q) * Np + 32 * J + sl] = tb[slot_key(sl)][q];
+    M[(size_t)(32 * J + q) * Np + 32 * I + sl] = ta[slot_key(sl)][q];
   }
 }
 
@@ -675,6 +730,13 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     timer.stop();
     if (int e = pf::check_launch("attn_project")) return e;
   }
+  if (transpose) {
+    const int nt = Np / 32;
+    pf::KernelTimer timer("pb_transpose", s);
+    pb_transpose_kernel<<<dim3(nt * (nt + 1) / 2, B * kHeads), 256, 0, s>>>(PBb, Np);
+    timer.stop();
+    if (int e = pf::check_launch("pb_transpose")) return e;
+  }
   {
     const int nqb = Np / (32 * attn_qsub<TC>());
     const int nlg = (N + kLinesPerBlock - 1) / kLinesPerBlock;
@@ -684,10 +746,7 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     pf::KernelTimer timer("tri_attn", s);
     constexpr int QS = attn_qsub<TC>();
     constexpr int NT = 64 * kLinesPerBlock;
-    if (transpose)
-      tri_attn_kernel<TC, true, QS, false><<<grid, NT, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap);
-    else
-      tri_attn_kernel<TC, false, QS, false><<<grid, NT, 0, s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap);
+    tri_attn_kernel<TC, QS, false><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap);
     timer.stop();
     if (int e = pf::check_launch("tri_attn")) return e;
   }
@@ -825,7 +884,7 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   const long total = (long)B * nlg * kHeads * nqb;
   const int remap = (total % 8 == 0) ? 1 : 0;
   pf::KernelTimer timer("evo_attn", s);
-  tri_attn_kernel<TC, false, QS, true><<<dim3((unsigned)total), NT, 0, s>>>(Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np,
+  tri_attn_kernel<TC, QS, true><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np,
                                                                             S, S, zero_rule, remap);
   timer.stop();
   return pf::check_launch("evo_attn");
