@@ -26,6 +26,9 @@ inline size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
 // Token padding used by the pair-plane and attention buffers.
 inline int pad128(int n) { return (int)round_up((size_t)n, 128); }
 
+// Compute units of the current device (cached per device), for persistent grids.
+int cu_count();
+
 // Opt-in per-kernel timing with HIP events on the launch stream (pf_kernel_timer_*).
 // Construct before a launch site and call stop() after it; both are no-ops unless the
 // site's name is the one selected with pf_kernel_timer_start.

@@ -13,6 +13,7 @@
 // stored [i][k] and Q = b stored [j][k]. For the incoming one, X_ij = sum_k a_kj b_ki,
 // K1 walks z along columns and stores the planes transposed (P = b^T as [i][k],
 // Q = a^T as [j][k]), so K2 is always the same k-contiguous "NT" GEMM.
+#include <algorithm>
 #include <type_traits>
 
 #include "capi.h"
@@ -589,6 +590,164 @@ __global__ __launch_bounds__(256) void trimul_project32_kernel(const TZ* __restr
   }
 }
 
+// K1, persistent and weight-stationary (bf16 GEMMs). One 512-thread block per CU walks
+// tiles of 64 positions along a line. Wave w owns plane w >> 2 (a | b) and channels
+// 32 (w & 3) .. +32: its proj and gate weight rows (2 x 32 rows x 128 k, packed as above)
+// stay in MFMA A-operand registers for the whole kernel, so weights are read once per CU
+// instead of once per tile. Per tile: each wave LayerNorms 8 z rows into a double-buffered
+// LDS tile (the next tile's rows are loaded while this tile's MFMAs run); every wave then
+// computes acc^T[channel][position] for proj and gate (the same elements), gates in
+// registers, stages its 32 x 64 result channel-major in a private LDS region and writes
+// 128-byte plane rows.
+struct ProjectWs {
+  static constexpr int C = 128;
+  static constexpr int BP = 64;   // positions per tile
+  static constexpr int NW = 8;    // waves per block
+  static constexpr int NT = 64 * NW;
+  static constexpr int XLD = C + 8;   // 272-byte rows: conflict-free 16-byte B-operand reads
+  static constexpr int SLD = BP + 8;  // stage rows (bf16)
+};
+
+template <class TZ>
+__global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
+    const TZ* __restrict__ z, const float* __restrict__ mask, const float* __restrict__ lnw,
+    const float* __restrict__ lnb, float eps, const bf16* __restrict__ w4, bf16* __restrict__ planes, int B, int N,
+    int Np, int outgoing) {
+  using Cfg = ProjectWs;
+  constexpr int C = Cfg::C, BP = Cfg::BP, NW = Cfg::NW, XLD = Cfg::XLD, SLD = Cfg::SLD;
+  constexpr int VEC = 16 / sizeof(TZ);  // z elements per 16-byte load
+  constexpr int LPR = C / VEC;          // lanes per z row
+  constexpr int RPI = 64 / LPR;         // rows per wave-wide load
+  constexpr int RPW = BP / NW;          // z rows each wave normalises per tile
+  constexpr int NLD = RPW / RPI;        // 16-byte loads per lane per tile
+  __shared__ __attribute__((aligned(16))) bf16 xs[2][BP * XLD];
+  __shared__ __attribute__((aligned(16))) bf16 stage_all[NW][32 * SLD];
+
+  const int w = wave_id();
+  const int l = lane_id();
+  const int pl = w >> 2;  // 0: a (P), 1: b (Q)
+  const int cj = w & 3;   // 32-channel chunk
+  bf16* stg = stage_all[w];
+  const int tpl = Np / BP;
+  const long ntiles = (long)B * Np * tpl;
+  const size_t pe = (size_t)Np * Np;
+
+  // Weights -> A operands: lane l holds row l & 31, k = 16 ks + 8 (l >> 5) + e.
+  bf16x8 wp[C / 16], wg[C / 16];
+  {
+    const bf16* rp = w4 + (size_t)(128 * cj + 32 * (2 * pl) + (l & 31)) * C + 8 * (l >> 5);
+    const bf16* rg = rp + (size_t)32 * C;
+#pragma unroll
+    for (int ks = 0; ks < C / 16; ++ks) {
+      wp[ks] = *reinterpret_cast<const bf16x8*>(rp + 16 * ks);
+      wg[ks] = *reinterpret_cast<const bf16x8*>(rg + 16 * ks);
+    }
+  }
+  const int chunk = l % LPR;
+
+  auto tile_coords = [&](long tile, int& b, int& line, int& t0) {
+    b = (int)(tile / ((long)Np * tpl));
+    const long rem = tile % ((long)Np * tpl);
+    line = (int)(rem / tpl);
+    t0 = (int)(rem % tpl) * BP;
+  };
+  // Next tile's z rows (this wave's 8) and this lane's mask values, in registers.
+  u32x4 zr[NLD];
+  float mkn[2];
+  auto issue = [&](long tile) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
+    const TZ* zb = z + (size_t)b * N * N * C;
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      const int row = w * RPW + q * RPI + l / LPR;
+      const int t = t0 + row;
+      if (line < N && t < N) {
+        const size_t pos = outgoing ? (size_t)line * N + t : (size_t)t * N + line;
+        zr[q] = *reinterpret_cast<const u32x4*>(zb + pos * C + chunk * VEC);
+      } else {
+        zr[q] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int pt = 0; pt < 2; ++pt) {
+      const int t = t0 + 32 * pt + (l & 31);
+      const size_t pos = outgoing ? (size_t)line * N + t : (size_t)t * N + line;
+      mkn[pt] = (line < N && t < N) ? mask[(size_t)b * N * N + pos] : 0.f;
+    }
+  };
+
+  long tile = blockIdx.x;
+  if (tile < ntiles) issue(tile);
+  int buf = 0;
+  for (; tile < ntiles; tile += gridDim.x, buf ^= 1) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
+    // LayerNorm of this wave's rows (fp32 two-pass statistics) -> xs[buf] in bf16.
+    bf16* xb = xs[buf];
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      float v[VEC];
+      unpack16<TZ>(zr[q], v);
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum += v[e];
+      const float mean = group_sum<LPR>(sum) * (1.0f / C);
+      float sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = v[e] - mean;
+        sq += d * d;
+      }
+      const float rstd = rsqrtf(group_sum<LPR>(sq) * (1.0f / C) + eps);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[e] = (v[e] - mean) * rstd * lnw[chunk * VEC + e] + lnb[chunk * VEC + e];
+      const int row = w * RPW + q * RPI + l / LPR;
+      store_vec<bf16, VEC>(xb + row * XLD + chunk * VEC, v);
+    }
+    const float mk[2] = {mkn[0], mkn[1]};
+    const long next = tile + gridDim.x;
+    if (next < ntiles) issue(next);
+    __syncthreads();  // xs[buf] holds the whole tile
+
+    f32x16 acc[2][2];  // [proj | gate][position tile]
+    zero_acc32(acc);
+#pragma unroll
+    for (int ks = 0; ks < C / 16; ++ks) {
+      bf16x8 xf[2];
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt)
+        xf[pt] = *reinterpret_cast<const bf16x8*>(xb + (32 * pt + (l & 31)) * XLD + 16 * ks + 8 * (l >> 5));
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt) {
+        acc[0][pt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wp[ks], xf[pt], acc[0][pt], 0, 0, 0);
+        acc[1][pt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wg[ks], xf[pt], acc[1][pt], 0, 0, 0);
+      }
+    }
+    // Gate, mask, stage channel-major: lane (position p) holds channels acc32_row(e).
+#pragma unroll
+    for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = sigmoidf_(acc[1][pt][e]) * acc[0][pt][e] * mk[pt];
+        stg[acc32_row(e) * SLD + 32 * pt + (l & 31)] = (bf16)v;
+      }
+    // The stage is private to this wave: LDS operations of one wave complete in order.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    bf16* pb = planes + ((size_t)pl * B * C + (size_t)b * C + 32 * cj) * pe + (size_t)line * Np + t0;
+#pragma unroll
+    for (int it = 0; it < 32 * BP / 8 / 64; ++it) {
+      const int row = it * 8 + (l >> 3);
+      const int c8 = l & 7;
+      *reinterpret_cast<u32x4*>(pb + (size_t)row * pe + 8 * c8) =
+          *reinterpret_cast<const u32x4*>(stg + row * SLD + 8 * c8);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // K3 on 64 positions of one row i: X tile (channel-major) -> LN_out -> A1 [pos][ch];
 // LN_in(z) -> A2; acc^T for g = Wog A2^T and p = Wo A1^T (wave w: channels 32 w, all 64
 // positions), update = sigmoid(g) p through an fp32 stage, stored or added.
@@ -759,9 +918,14 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     constexpr int BM = k32 ? 128 : trimul_bm<TC>();
     dim3 grid(Np / BM, Np, B);
     pf::KernelTimer timer_trimul_project("trimul_project", s);
-    if constexpr (k32)
-      trimul_project32_kernel<TZ><<<grid, 256, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const bf16*)w4,
-                                                       (bf16*)planes, B, N, Np, outgoing);
+    if constexpr (k32) {
+      const long ntiles = (long)B * Np * (Np / ProjectWs::BP);
+      const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+      trimul_project_ws_kernel<TZ><<<nblk, ProjectWs::NT, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in,
+                                                                  (const bf16*)w4, (bf16*)planes, B, N, Np,
+                                                                  outgoing);
+      (void)grid;
+    }
     else
       trimul_project_kernel<TZ, TC, C><<<grid, 256, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const TC*)w4,
                                                             planes, B, N, Np, outgoing);
