@@ -31,6 +31,8 @@
 // the B operand lane (q, h) must supply for O^T += V^T P^T when the keys of a 32-block are
 // stored in the order kappa (storage slot 16 h + r holds key kappa(r, h)): Vt, PB and MA
 // use that order, so P never goes through LDS.
+#include <algorithm>
+
 #include "capi.h"
 #include "common.h"
 
@@ -217,6 +219,253 @@ __global__ __launch_bounds__(256) void attn_project_kernel(const TZ* __restrict_
     const int t = t0 + tid;
     const float v = t < N ? (mks[tid] - 1.0f) * 1e9f * kLog2e : -INFINITY;
     MA[lineq * Np + (t & ~31) + key_slot(t & 31)] = v;
+  }
+}
+
+// A1, persistent and weight-stationary (bf16 GEMMs). One 512-thread block per CU walks
+// tiles of 64 positions along a frame line. Wave w owns kind w >> 1 (q, k, v, g) and
+// heads 2 (w & 1), +1: those 64 weight rows stay in MFMA A-operand registers for the
+// whole kernel. Per tile: each wave LayerNorms 8 z rows into a double-buffered LDS tile
+// (the next tile's rows are loaded while this tile's MFMAs run); each wave computes
+// acc^T[channel][position] for its rows, stages the result in a private LDS region in the
+// layout of its output (Q, K: [h][t][d]; Vt: [h][d][slot]; G: [t][c]) and writes it with
+// 16-byte stores. Waves 0-3 also project the pair bias of 16 positions each (a 16x16x32
+// MFMA on the bias rows), wave 4 writes the line's additive mask slots.
+struct ProjectAttnWs {
+  static constexpr int BP = 64;
+  static constexpr int NW = 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int XLD = kC + 8;
+  static constexpr int QLD = kHeadDim + 8;  // Q/K stage rows [t][d]
+  static constexpr int VLD = BP + 8;        // Vt stage rows [d][slot], G stage rows [t][c]
+  static constexpr int STAGE = 2 * BP * QLD;
+};
+
+template <class TZ>
+__global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
+    const TZ* __restrict__ z, const float* __restrict__ mask, const float* __restrict__ lnw,
+    const float* __restrict__ lnb, float eps, const bf16* __restrict__ w5, bf16* __restrict__ Q,
+    bf16* __restrict__ K, bf16* __restrict__ Vt, bf16* __restrict__ G, float* __restrict__ PB,
+    float* __restrict__ MA, int B, int N, int Np, int transpose, float qscale) {
+  using Cfg = ProjectAttnWs;
+  constexpr int BP = Cfg::BP, NW = Cfg::NW, XLD = Cfg::XLD, QLD = Cfg::QLD, VLD = Cfg::VLD;
+  constexpr int VEC = 16 / sizeof(TZ);
+  constexpr int LPR = kC / VEC;
+  constexpr int RPI = 64 / LPR;
+  constexpr int RPW = BP / NW;
+  constexpr int NLD = RPW / RPI;
+  static_assert(2 * kHeadDim * VLD <= Cfg::STAGE && BP * VLD <= Cfg::STAGE, "stage size");
+  __shared__ __attribute__((aligned(16))) bf16 xs[2][BP * XLD];
+  __shared__ float lnp[2][kC];
+  __shared__ __attribute__((aligned(16))) bf16 stage_all[NW][Cfg::STAGE];
+
+  const int w = wave_id();
+  const int l = lane_id();
+  const int kind = w >> 1;
+  const int h0 = 2 * (w & 1);
+  bf16* stg = stage_all[w];
+  const int tpl = Np / BP;
+  const long ntiles = (long)B * Np * tpl;
+
+  // Weights -> A operands: rows kind * 128 + 32 (h0 + hi) + (l & 31), k = 16 ks + 8 (l >> 5).
+  bf16x8 wa[2][kC / 16];
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi) {
+    const bf16* rp = w5 + (size_t)(kind * kC + 32 * (h0 + hi) + (l & 31)) * kC + 8 * (l >> 5);
+#pragma unroll
+    for (int ks = 0; ks < kC / 16; ++ks) wa[hi][ks] = *reinterpret_cast<const bf16x8*>(rp + 16 * ks);
+  }
+  // Pair-bias rows (waves 0-3): 16x16x32 A operand, lane holds row l & 15, k = 32 ks + 8 (l >> 4).
+  bf16x8 wb[kC / 32];
+  if (w < 4) {
+    const bf16* rp = w5 + (size_t)(4 * kC + (l & 15)) * kC + 8 * (l >> 4);
+#pragma unroll
+    for (int ks = 0; ks < kC / 32; ++ks) wb[ks] = *reinterpret_cast<const bf16x8*>(rp + 32 * ks);
+  }
+  const int chunk = l % LPR;
+  for (int i = threadIdx.x; i < kC; i += blockDim.x) {
+    lnp[0][i] = lnw[i];
+    lnp[1][i] = lnb[i];
+  }
+  __syncthreads();
+
+  auto tile_coords = [&](long tile, int& b, int& line, int& t0) {
+    b = (int)(tile / ((long)Np * tpl));
+    const long rem = tile % ((long)Np * tpl);
+    line = (int)(rem / tpl);
+    t0 = (int)(rem % tpl) * BP;
+  };
+  u32x4 zr[NLD];
+  bool zok[NLD];
+  float mkn = 0.f;
+  auto issue = [&](long tile) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
+    const TZ* zb = z + (size_t)b * N * N * kC;
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      const int t = t0 + w * RPW + q * RPI + l / LPR;
+      zok[q] = line < N && t < N;
+      if (zok[q]) {
+        const size_t pos = transpose ? (size_t)t * N + line : (size_t)line * N + t;
+        zr[q] = *reinterpret_cast<const u32x4*>(zb + pos * kC + chunk * VEC);
+      } else {
+        zr[q] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    if (w == 4) {
+      const int t = t0 + l;
+      const size_t pos = transpose ? (size_t)t * N + line : (size_t)line * N + t;
+      mkn = (line < N && t < N) ? mask[(size_t)b * N * N + pos] : 0.f;
+    }
+  };
+
+  long tile = blockIdx.x;
+  if (tile < ntiles) issue(tile);
+  int buf = 0;
+  for (; tile < ntiles; tile += gridDim.x, buf ^= 1) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
+    const size_t lineq = (size_t)b * Np + line;
+    bf16* xb = xs[buf];
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      float v[VEC];
+      unpack16<TZ>(zr[q], v);
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum += v[e];
+      const float mean = row_group_sum<LPR>(sum) * (1.0f / kC);
+      float sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = v[e] - mean;
+        sq += d * d;
+      }
+      const float rstd = rsqrtf(row_group_sum<LPR>(sq) * (1.0f / kC) + eps);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float y = (v[e] - mean) * rstd * lnp[0][chunk * VEC + e] + lnp[1][chunk * VEC + e];
+        v[e] = zok[q] ? y : 0.f;
+      }
+      store_vec<bf16, VEC>(xb + (w * RPW + q * RPI + l / LPR) * XLD + chunk * VEC, v);
+    }
+    const float mk = mkn;
+    const long next = tile + gridDim.x;
+    if (next < ntiles) issue(next);
+    __syncthreads();  // xs[buf] holds the whole tile
+
+    f32x16 acc[2][2];  // [head][position tile]
+    zero_acc32(acc);
+#pragma unroll
+    for (int ks = 0; ks < kC / 16; ++ks) {
+      bf16x8 xf[2];
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt)
+        xf[pt] = *reinterpret_cast<const bf16x8*>(xb + (32 * pt + (l & 31)) * XLD + 16 * ks + 8 * (l >> 5));
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt)
+          acc[hi][pt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[hi][ks], xf[pt], acc[hi][pt], 0, 0, 0);
+    }
+    if (w < 4) {
+      // Pair bias of positions 16 w .. +16: lanes 0-15 hold heads 0-3 of position 16 w + l.
+      f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kC / 32; ++ks) {
+        const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xb + (16 * w + (l & 15)) * XLD + 32 * ks + 8 * (l >> 4));
+        pacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[ks], xf, pacc, 0, 0, 0);
+      }
+      if (l < 16) {
+        const int t = t0 + 16 * w + l;
+        const bool ok = line < N && t < N;
+#pragma unroll
+        for (int hh = 0; hh < kHeads; ++hh) {
+          const float v = ok ? pacc[hh] * kLog2e : 0.f;
+          float* dst = PB + (((size_t)b * kHeads + hh) * Np + line) * Np;
+          if (transpose)  // key-major [b][h][key = line][query = t]
+            dst[t] = v;
+          else  // query-major [b][h][query = line][slot(key = t)]
+            dst[(t & ~31) + key_slot(t & 31)] = v;
+        }
+      }
+    }
+    if (w == 4) {
+      const int t = t0 + l;
+      MA[lineq * Np + (t & ~31) + key_slot(t & 31)] = t < N ? (mk - 1.0f) * 1e9f * kLog2e : -INFINITY;
+    }
+
+    // Epilogue: stage in the output layout, then 16-byte stores.
+    if (kind <= 1) {  // Q (pre-scaled) or K: stage [hi][t][d]
+      const float sc = kind == 0 ? qscale : 1.0f;
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[hi][pt][4 * g4 + e] * sc;
+            store_vec<bf16, 4>(stg + (hi * BP + 32 * pt + (l & 31)) * QLD + acc32_row(4 * g4), v);
+          }
+    } else if (kind == 2) {  // Vt: stage [hi][d][slot]
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            stg[(hi * kHeadDim + acc32_row(e)) * VLD + 32 * pt + key_slot(l & 31)] = (bf16)acc[hi][pt][e];
+    } else {  // G = sigmoid(g): stage [t][64 channels]
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = sigmoidf_(acc[hi][pt][4 * g4 + e]);
+            store_vec<bf16, 4>(stg + (32 * pt + (l & 31)) * VLD + 32 * hi + acc32_row(4 * g4), v);
+          }
+    }
+    // The stage is private to this wave: LDS operations of one wave complete in order.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (kind <= 1) {
+      bf16* dst0 = (kind == 0 ? Q : K) + ((lineq * kHeads + h0) * Np + t0) * kHeadDim;
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int it = 0; it < BP * kHeadDim / 8 / 64; ++it) {
+          const int p = it * 16 + (l >> 2);
+          const int c = l & 3;
+          *reinterpret_cast<u32x4*>(dst0 + ((size_t)hi * Np + p) * kHeadDim + 8 * c) =
+              *reinterpret_cast<const u32x4*>(stg + (hi * BP + p) * QLD + 8 * c);
+        }
+    } else if (kind == 2) {
+      bf16* dst0 = Vt + ((lineq * kHeads + h0) * kHeadDim) * (size_t)Np + t0;
+#pragma unroll
+      for (int it = 0; it < 2 * kHeadDim * BP / 8 / 64; ++it) {
+        const int r = it * 8 + (l >> 3);  // hi * 32 + d
+        const int c = l & 7;
+        *reinterpret_cast<u32x4*>(dst0 + (size_t)r * Np + 8 * c) =
+            *reinterpret_cast<const u32x4*>(stg + r * VLD + 8 * c);
+      }
+    } else {
+      bf16* dst0 = G + (lineq * Np + t0) * kC + 64 * (w & 1);
+#pragma unroll
+      for (int it = 0; it < BP * 64 / 8 / 64; ++it) {
+        const int p = it * 8 + (l >> 3);
+        const int c = l & 7;
+        *reinterpret_cast<u32x4*>(dst0 + (size_t)p * kC + 8 * c) =
+            *reinterpret_cast<const u32x4*>(stg + p * VLD + 8 * c);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -725,8 +974,17 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
   {
     dim3 grid(Np / BM, Np, B);
     pf::KernelTimer timer("attn_project", s);
-    attn_project_kernel<TZ, TC><<<grid, 256, 0, s>>>((const TZ*)z, mask, lnw, lnb, eps, (const TC*)w5, Qb, Kb, Vb,
-                                                     Gb, PBb, MAb, N, Np, transpose, qscale);
+    if constexpr (sizeof(TC) == 2) {
+      const long ntiles = (long)B * Np * (Np / ProjectAttnWs::BP);
+      const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+      attn_project_ws_kernel<TZ><<<nblk, ProjectAttnWs::NT, 0, s>>>((const TZ*)z, mask, lnw, lnb, eps,
+                                                                    (const bf16*)w5, Qb, Kb, Vb, Gb, PBb, MAb, B,
+                                                                    N, Np, transpose, qscale);
+      (void)grid;
+    } else {
+      attn_project_kernel<TZ, TC><<<grid, 256, 0, s>>>((const TZ*)z, mask, lnw, lnb, eps, (const TC*)w5, Qb, Kb,
+                                                       Vb, Gb, PBb, MAb, N, Np, transpose, qscale);
+    }
     timer.stop();
     if (int e = pf::check_launch("attn_project")) return e;
   }

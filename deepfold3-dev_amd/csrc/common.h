@@ -124,6 +124,33 @@ PF_DEVICE float group_max(float v) {
   return v;
 }
 
+// Sum over each row of 16 lanes with DPP moves (no LDS round trip): quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror -- after each step every lane holds the
+// sum over twice as many lanes.
+PF_DEVICE float dpp_sum16(float v) {
+  auto dpp = [](float x, int ctrl) -> float {
+    switch (ctrl) {
+      case 0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+      case 1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+      case 2: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+      default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
+    }
+  };
+  v += dpp(v, 0);
+  v += dpp(v, 1);
+  v += dpp(v, 2);
+  v += dpp(v, 3);
+  return v;
+}
+// Sum over aligned groups of W lanes, W in {16, 32}: DPP inside rows, one swizzle across.
+template <int W>
+PF_DEVICE float row_group_sum(float v) {
+  static_assert(W == 16 || W == 32, "row groups of 16 or 32 lanes");
+  v = dpp_sum16(v);
+  if (W == 32) v += __shfl_xor(v, 16, 64);
+  return v;
+}
+
 PF_DEVICE int lane_id() { return threadIdx.x & 63; }
 PF_DEVICE int wave_id() { return threadIdx.x >> 6; }
 

@@ -644,6 +644,13 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
     }
   }
   const int chunk = l % LPR;
+  // LayerNorm parameters of this lane's channels, read once.
+  float lw[VEC], lb[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    lw[e] = lnw[chunk * VEC + e];
+    lb[e] = lnb[chunk * VEC + e];
+  }
 
   auto tile_coords = [&](long tile, int& b, int& line, int& t0) {
     b = (int)(tile / ((long)Np * tpl));
@@ -701,7 +708,7 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
       }
       const float rstd = rsqrtf(group_sum<LPR>(sq) * (1.0f / C) + eps);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) v[e] = (v[e] - mean) * rstd * lnw[chunk * VEC + e] + lnb[chunk * VEC + e];
+      for (int e = 0; e < VEC; ++e) v[e] = (v[e] - mean) * rstd * lw[e] + lb[e];
       const int row = w * RPW + q * RPI + l / LPR;
       store_vec<bf16, VEC>(xb + row * XLD + chunk * VEC, v);
     }
