@@ -755,6 +755,196 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
   }
 }
 
+// K3, persistent and weight-stationary (bf16 GEMMs). One 512-thread block per CU walks
+// tiles of 64 positions (i, j0 .. j0+63) of one row. Wave w owns output channels 16 w ..
+// +16: rows of out_proj and out_gate as 16x16x32 MFMA A operands, resident in registers;
+// the two accumulators share a layout, so the gate applies in registers. Per tile: the
+// X tile (channel-major, 128 x 64) is transposed through LDS for LN_out, the z tile is
+// normalised (LN_in) from registers that also keep it for the residual; after the MFMAs
+// each wave stages its fp32 update (16 channels x 64 positions) block-wide, and each wave
+// then adds the update to the 8 z rows it loaded and writes them. The next tile's X and z
+// are loaded during this tile's MFMAs.
+struct OutputWs {
+  static constexpr int C = 128;
+  static constexpr int BP = 64;
+  static constexpr int NW = 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int XLD = C + 8;   // bf16 operand rows [pos][ch]
+  static constexpr int TLD = BP + 8;  // bf16 X transpose rows [ch][pos]
+  static constexpr int SLD = C + 4;   // fp32 update stage rows [pos][ch]
+};
+
+template <class TZ>
+__global__ __launch_bounds__(OutputWs::NT) void trimul_output_ws_kernel(
+    const bf16* __restrict__ X, const TZ* __restrict__ z, TZ* __restrict__ out, const float* __restrict__ lniw,
+    const float* __restrict__ lnib, float eps_in, const float* __restrict__ lnow, const float* __restrict__ lnob,
+    float eps_out, const bf16* __restrict__ Wo, const bf16* __restrict__ Wog, int B, int N, int Np, int accumulate) {
+  using Cfg = OutputWs;
+  constexpr int C = Cfg::C, BP = Cfg::BP, NW = Cfg::NW, NT = Cfg::NT, XLD = Cfg::XLD, TLD = Cfg::TLD,
+                SLD = Cfg::SLD;
+  constexpr int VEC = 16 / sizeof(TZ);  // z elements per 16-byte load
+  constexpr int LPR = C / VEC;          // lanes per z row
+  constexpr int RPI = 64 / LPR;         // z rows per wave-wide load
+  constexpr int RPW = BP / NW;          // z rows per wave per tile
+  constexpr int NLD = RPW / RPI;        // z loads per lane per tile
+  constexpr int XLDS = C * BP / 8 / NT; // 16-byte X loads per lane per tile
+  __shared__ __attribute__((aligned(16))) bf16 xt[C * TLD];   // X tile [ch][pos]
+  __shared__ __attribute__((aligned(16))) bf16 xa[BP * XLD];  // LN_out(X) [pos][ch]
+  __shared__ __attribute__((aligned(16))) bf16 xb[BP * XLD];  // LN_in(z) [pos][ch]
+  __shared__ __attribute__((aligned(16))) float upd[BP * SLD];
+
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const size_t pe = (size_t)Np * Np;
+  const int tpr = (N + BP - 1) / BP;
+  const long ntiles = (long)B * N * tpr;
+
+  // Weights: lane holds row 16 w + (l & 15), k = 32 ks + 8 (l >> 4) + e.
+  bf16x8 wo[C / 32], wg[C / 32];
+#pragma unroll
+  for (int ks = 0; ks < C / 32; ++ks) {
+    wo[ks] = *reinterpret_cast<const bf16x8*>(Wo + (size_t)(16 * w + (l & 15)) * C + 32 * ks + 8 * (l >> 4));
+    wg[ks] = *reinterpret_cast<const bf16x8*>(Wog + (size_t)(16 * w + (l & 15)) * C + 32 * ks + 8 * (l >> 4));
+  }
+  const int chunk = l % LPR;
+  float liw[VEC], lib[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    liw[e] = lniw[chunk * VEC + e];
+    lib[e] = lnib[chunk * VEC + e];
+  }
+  // LN_out: thread (position p = tid / 8, part s = tid % 8) normalises channels 16 s .. +16.
+  const int op = tid >> 3, os = tid & 7;
+  float low[16], lob[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    low[c] = lnow[16 * os + c];
+    lob[c] = lnob[16 * os + c];
+  }
+
+  auto tile_coords = [&](long tile, int& b, int& i, int& j0) {
+    b = (int)(tile / ((long)N * tpr));
+    const long rem = tile % ((long)N * tpr);
+    i = (int)(rem / tpr);
+    j0 = (int)(rem % tpr) * BP;
+  };
+  u32x4 zr[NLD], xr[XLDS];
+  auto issue = [&](long tile) {
+    int b, i, j0;
+    tile_coords(tile, b, i, j0);
+    const TZ* zb = z + ((size_t)b * N + i) * N * C;
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      const int j = j0 + w * RPW + q * RPI + l / LPR;
+      zr[q] = j < N ? *reinterpret_cast<const u32x4*>(zb + (size_t)j * C + chunk * VEC) : u32x4{0u, 0u, 0u, 0u};
+    }
+    const bf16* Xb = X + (size_t)b * C * pe + (size_t)i * Np + j0;
+#pragma unroll
+    for (int q = 0; q < XLDS; ++q) {
+      const int c = (tid >> 3) + q * (NT / 8);
+      xr[q] = *reinterpret_cast<const u32x4*>(Xb + (size_t)c * pe + 8 * (tid & 7));
+    }
+  };
+
+  long tile = blockIdx.x;
+  if (tile < ntiles) issue(tile);
+  for (; tile < ntiles; tile += gridDim.x) {
+    int b, i, j0;
+    tile_coords(tile, b, i, j0);
+    // X tile -> LDS [ch][pos]; LN_in(z rows) -> xb (raw z stays in zr for the residual).
+#pragma unroll
+    for (int q = 0; q < XLDS; ++q) {
+      const int c = (tid >> 3) + q * (NT / 8);
+      *reinterpret_cast<u32x4*>(xt + c * TLD + 8 * (tid & 7)) = xr[q];
+    }
+    float zv[NLD][VEC];
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      unpack16<TZ>(zr[q], zv[q]);
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum += zv[q][e];
+      const float mean = group_sum<LPR>(sum) * (1.0f / C);
+      float sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = zv[q][e] - mean;
+        sq += d * d;
+      }
+      const float rstd = rsqrtf(group_sum<LPR>(sq) * (1.0f / C) + eps_in);
+      float y[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) y[e] = (zv[q][e] - mean) * rstd * liw[e] + lib[e];
+      store_vec<bf16, VEC>(xb + (w * RPW + q * RPI + l / LPR) * XLD + chunk * VEC, y);
+    }
+    const long next = tile + gridDim.x;
+    if (next < ntiles) issue(next);
+    __syncthreads();  // xt complete
+    {
+      float v[16];
+      float sum = 0.f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        v[c] = (float)xt[(16 * os + c) * TLD + op];
+        sum += v[c];
+      }
+      const float mean = group_sum<8>(sum) * (1.0f / C);
+      float sq = 0.f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const float d = v[c] - mean;
+        sq += d * d;
+      }
+      const float rstd = rsqrtf(group_sum<8>(sq) * (1.0f / C) + eps_out);
+#pragma unroll
+      for (int c = 0; c < 16; ++c) v[c] = (v[c] - mean) * rstd * low[c] + lob[c];
+      store_vec<bf16, 8>(xa + op * XLD + 16 * os, v);
+      store_vec<bf16, 8>(xa + op * XLD + 16 * os + 8, v + 8);
+    }
+    __syncthreads();  // xa, xb complete
+
+    f32x4 ao[4], ag[4];  // [position tile of 16]
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) ao[pt] = ag[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < C / 32; ++ks)
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) {
+        const int r = (16 * pt + (l & 15)) * XLD + 32 * ks + 8 * (l >> 4);
+        const bf16x8 fa = *reinterpret_cast<const bf16x8*>(xa + r);
+        const bf16x8 fb = *reinterpret_cast<const bf16x8*>(xb + r);
+        ao[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wo[ks], fa, ao[pt], 0, 0, 0);
+        ag[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wg[ks], fb, ag[pt], 0, 0, 0);
+      }
+    // update = sigmoid(gate) * out: lane holds channels 16 w + 4 (l >> 4) + e of position
+    // 16 pt + (l & 15).
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+      f32x4 u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) u[e] = sigmoidf_(ag[pt][e]) * ao[pt][e];
+      *reinterpret_cast<f32x4*>(upd + (16 * pt + (l & 15)) * SLD + 16 * w + 4 * (l >> 4)) = u;
+    }
+    __syncthreads();  // update tile complete
+    TZ* ob = out + ((size_t)b * N + i) * N * C;
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      const int p = w * RPW + q * RPI + l / LPR;
+      const int j = j0 + p;
+      if (j >= N) continue;
+      float y[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; e += 4) {
+        const f32x4 u = *reinterpret_cast<const f32x4*>(upd + p * SLD + chunk * VEC + e);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) y[e + k] = accumulate ? zv[q][e + k] + u[k] : u[k];
+      }
+      store_vec<TZ, VEC>(ob + (size_t)j * C + chunk * VEC, y);
+    }
+  }
+}
+
 // K3 on 64 positions of one row i: X tile (channel-major) -> LN_out -> A1 [pos][ch];
 // LN_in(z) -> A2; acc^T for g = Wog A2^T and p = Wo A1^T (wave w: channels 32 w, all 64
 // positions), update = sigmoid(g) p through an fp32 stage, stored or added.
@@ -986,11 +1176,14 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     constexpr int BM = k32 ? 64 : trimul_bm<TC>();
     dim3 grid((N + BM - 1) / BM, N, B);
     pf::KernelTimer timer_trimul_output("trimul_output", s);
-    if constexpr (k32)
-      trimul_output32_kernel<TZ><<<grid, 256, 0, s>>>((const bf16*)X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in,
-                                                      lnow, lnob, eps_out, (const bf16*)wo, (const bf16*)wog, B, N,
-                                                      Np, accumulate);
-    else
+    if constexpr (k32) {
+      const long ntiles = (long)B * N * ((N + OutputWs::BP - 1) / OutputWs::BP);
+      const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+      trimul_output_ws_kernel<TZ><<<nblk, OutputWs::NT, 0, s>>>((const bf16*)X, (const TZ*)z, (TZ*)out, lniw, lnib,
+                                                                eps_in, lnow, lnob, eps_out, (const bf16*)wo,
+                                                                (const bf16*)wog, B, N, Np, accumulate);
+      (void)grid;
+    } else
       trimul_output_kernel<TZ, TC, C><<<grid, 256, 0, s>>>(X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow,
                                                            lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
                                                            accumulate);
