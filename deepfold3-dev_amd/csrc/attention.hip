@@ -929,6 +929,129 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const TC* __restrict__ O,
   store_tile_from_lds<TZ, kC, BM, NT>(orow, stage, SLD, accumulate != 0);
 }
 
+// A3, persistent and weight-stationary (bf16 GEMMs). Blocks of 8 waves (two per CU) walk
+// tiles of 64 positions of a frame line. Wave w owns output channels 16 w .. +16 (W_out
+// rows as 16x16x32 MFMA A operands, resident in registers). Per tile: A = O * G (frame
+// rows) -> LDS; the MFMAs give acc^T[channel][position]; the fp32 update is staged
+// block-wide and each thread adds it to the z channels it loaded (the position's z row,
+// transposed back for columns) and stores them. The next tile's O, G and z are loaded
+// during this tile's MFMAs.
+struct OutAttnWs {
+  static constexpr int BP = 64;
+  static constexpr int NW = 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int ALD = kC + 8;  // bf16 operand rows [pos][ch]
+  static constexpr int SLD = kC + 4;  // fp32 update rows [pos][ch]
+};
+
+template <class TZ>
+__global__ __launch_bounds__(OutAttnWs::NT, 4) void attn_out_ws_kernel(
+    const bf16* __restrict__ O, const bf16* __restrict__ G, const bf16* __restrict__ Wo, const TZ* __restrict__ z,
+    TZ* __restrict__ out, int B, int N, int Np, int transpose, int accumulate) {
+  using Cfg = OutAttnWs;
+  constexpr int BP = Cfg::BP, ALD = Cfg::ALD, SLD = Cfg::SLD;
+  constexpr int ZV = 16 / sizeof(TZ);  // z elements per 16-byte load
+  constexpr int ZL = 16 / ZV;          // 16-byte z loads per thread (16 channels)
+  __shared__ __attribute__((aligned(16))) bf16 a_lds[BP * ALD];
+  __shared__ __attribute__((aligned(16))) float upd[BP * SLD];
+
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const int tpl = (N + BP - 1) / BP;
+  const long ntiles = (long)B * N * tpl;
+
+  bf16x8 wo[kC / 32];
+#pragma unroll
+  for (int ks = 0; ks < kC / 32; ++ks)
+    wo[ks] = *reinterpret_cast<const bf16x8*>(Wo + (size_t)(16 * w + (l & 15)) * kC + 32 * ks + 8 * (l >> 4));
+  // Thread (position p, part s) handles channels 16 s .. +16 of position p.
+  const int p = tid >> 3, sp = tid & 7;
+
+  auto tile_coords = [&](long tile, int& b, int& line, int& t0) {
+    b = (int)(tile / ((long)N * tpl));
+    const long rem = tile % ((long)N * tpl);
+    line = (int)(rem / tpl);
+    t0 = (int)(rem % tpl) * BP;
+  };
+  auto zpos = [&](int b, int line, int t) -> size_t {
+    return (size_t)b * N * N + (transpose ? (size_t)t * N + line : (size_t)line * N + t);
+  };
+  u32x4 orr[2], grr[2], zr[ZL];
+  auto issue = [&](long tile) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
+    const int t = t0 + p;
+    const size_t fr = (((size_t)b * Np + line) * Np + t) * kC + 16 * sp;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      orr[q] = *reinterpret_cast<const u32x4*>(O + fr + 8 * q);
+      grr[q] = *reinterpret_cast<const u32x4*>(G + fr + 8 * q);
+    }
+    if (accumulate && t < N) {
+      const TZ* zp = z + zpos(b, line, t) * kC + 16 * sp;
+#pragma unroll
+      for (int q = 0; q < ZL; ++q) zr[q] = *reinterpret_cast<const u32x4*>(zp + ZV * q);
+    }
+  };
+
+  long tile = blockIdx.x;
+  if (tile < ntiles) issue(tile);
+  for (; tile < ntiles; tile += gridDim.x) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
+    {
+      float a[16];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        float ov[8], gv[8];
+        unpack16<bf16>(orr[q], ov);
+        unpack16<bf16>(grr[q], gv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[8 * q + e] = ov[e] * gv[e];
+      }
+      store_vec<bf16, 8>(a_lds + p * ALD + 16 * sp, a);
+      store_vec<bf16, 8>(a_lds + p * ALD + 16 * sp + 8, a + 8);
+    }
+    float zv[16];
+#pragma unroll
+    for (int q = 0; q < ZL; ++q) unpack16<TZ>(zr[q], *reinterpret_cast<float(*)[ZV]>(zv + ZV * q));
+    const long next = tile + gridDim.x;
+    if (next < ntiles) issue(next);
+    __syncthreads();  // A tile complete
+
+    f32x4 acc[4];
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) acc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < kC / 32; ++ks)
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) {
+        const bf16x8 fa =
+            *reinterpret_cast<const bf16x8*>(a_lds + (16 * pt + (l & 15)) * ALD + 32 * ks + 8 * (l >> 4));
+        acc[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wo[ks], fa, acc[pt], 0, 0, 0);
+      }
+    // lane holds channels 16 w + 4 (l >> 4) + e of position 16 pt + (l & 15)
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt)
+      *reinterpret_cast<f32x4*>(upd + (16 * pt + (l & 15)) * SLD + 16 * w + 4 * (l >> 4)) = acc[pt];
+    __syncthreads();  // update tile complete
+    const int t = t0 + p;
+    if (t < N) {
+      float y[16];
+#pragma unroll
+      for (int e = 0; e < 16; e += 4) {
+        const f32x4 u = *reinterpret_cast<const f32x4*>(upd + p * SLD + 16 * sp + e);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) y[e + k] = accumulate ? zv[e + k] + u[k] : u[k];
+      }
+      TZ* op = out + zpos(b, line, t) * kC + 16 * sp;
+#pragma unroll
+      for (int q = 0; q < ZL; ++q) store_vec<TZ, ZV>(op + ZV * q, y + ZV * q);
+    }
+  }
+}
+
 // Offsets of the operand buffers inside the workspace (bytes, 256-aligned).
 struct AttnWs {
   size_t q, k, v, g, o, pb, ma, total;
@@ -1011,7 +1134,15 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
   {
     dim3 grid((N + BM - 1) / BM, N, B);
     pf::KernelTimer timer("attn_out", s);
-    attn_out_kernel<TZ, TC><<<grid, 256, 0, s>>>(Ob, Gb, (const TC*)wo, (TZ*)out, N, Np, transpose, accumulate);
+    if constexpr (sizeof(TC) == 2) {
+      const long ntiles = (long)B * N * ((N + OutAttnWs::BP - 1) / OutAttnWs::BP);
+      const int nblk = (int)std::min<long>(ntiles, 2L * pf::cu_count());
+      attn_out_ws_kernel<TZ><<<nblk, OutAttnWs::NT, 0, s>>>(Ob, Gb, (const bf16*)wo, (const TZ*)out, (TZ*)out, B, N,
+                                                            Np, transpose, accumulate);
+      (void)grid;
+    } else {
+      attn_out_kernel<TZ, TC><<<grid, 256, 0, s>>>(Ob, Gb, (const TC*)wo, (TZ*)out, N, Np, transpose, accumulate);
+    }
     timer.stop();
     if (int e = pf::check_launch("attn_out")) return e;
   }
