@@ -46,9 +46,6 @@ constexpr int kPad = 128;  // token padding of the attention frame
 #define PF_ATTN_QS 2
 #endif
 
-// Storage slot -> key inside a 32-key block, and its inverse.
-PF_DEVICE int slot_key(int slot) { return 8 * ((slot & 15) >> 2) + 4 * (slot >> 4) + (slot & 3); }
-PF_DEVICE int key_slot(int key) { return 16 * ((key >> 2) & 1) + 4 * (key >> 3) + (key & 3); }
 
 // ------------------------------------------------------------------ A1
 // w5 [4C + 16][C] (cdtype): rows q | k | v | g | pb (H rows) | zero padding.
@@ -470,63 +467,6 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
 }
 
 // ------------------------------------------------------------------ A2
-// 16 operand values per lane (bf16: 32 bytes; fp32: 64 bytes).
-template <class TC>
-struct Frag16;
-template <>
-struct Frag16<bf16> {
-  bf16x8 v[2];
-  PF_DEVICE void load(const bf16* p) {
-    v[0] = *reinterpret_cast<const bf16x8*>(p);
-    v[1] = *reinterpret_cast<const bf16x8*>(p + 8);
-  }
-};
-template <>
-struct Frag16<float> {
-  f32x4 v[4];
-  PF_DEVICE void load(const float* p) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const f32x4*>(p + 4 * i);
-  }
-};
-
-// acc += A B over the 16 k values the two lane halves hold (bf16: 2 MFMAs, fp32: 16).
-PF_DEVICE void mma32_16(f32x16& acc, const Frag16<bf16>& a, const Frag16<bf16>& b) {
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v[0], b.v[0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v[1], b.v[1], acc, 0, 0, 0);
-}
-PF_DEVICE void mma32_16(f32x16& acc, const Frag16<float>& a, const Frag16<float>& b) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.v[i][e], b.v[i][e], acc, 0, 0, 0);
-}
-
-// P^T as a B operand from 16 fp32 probabilities.
-PF_DEVICE Frag16<bf16> pack_p(const f32x16& p, bf16) {
-  Frag16<bf16> f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    f.v[0][e] = (bf16)p[e];
-    f.v[1][e] = (bf16)p[8 + e];
-  }
-  return f;
-}
-PF_DEVICE Frag16<float> pack_p(const f32x16& p, float) {
-  Frag16<float> f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) f.v[i] = f32x4{p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]};
-  return f;
-}
-
-// max(x[l], x[l ^ 32]) over the wave's two 32-lane halves. v_permlane32_swap of x with
-// itself leaves (x[l], x[l + 32]) in the low half and (x[l - 32], x[l]) in the high half:
-// a VALU op, no LDS round trip.
-PF_DEVICE float max_xor32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
 template <class TC>
 constexpr int attn_qsub() { return sizeof(TC) == 2 ? PF_ATTN_QS : 2; }  // 32-query sub-blocks per wave
 #ifndef PF_ATTN_LPB

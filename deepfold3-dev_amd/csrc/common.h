@@ -410,6 +410,73 @@ PF_DEVICE void zero_acc32(f32x16 (&acc)[MI][NJ]) {
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 }
 
+// ---------------------------------------------------------------- 16-value fragments
+// Key order of a 32-key block in flash-attention operands. With S^T = K Q^T on a 32x32
+// MFMA, lane (q, h) (q = lane & 31, h = lane >> 5) holds the logits of query q for keys
+// kappa(r, h) = 8 (r >> 2) + 4 h + (r & 3), r = 0..15; storing key kappa(r, h) at slot
+// 16 h + r makes those 16 probabilities the lane's B operand of O^T += V^T P^T directly.
+PF_DEVICE int slot_key(int slot) { return 8 * ((slot & 15) >> 2) + 4 * (slot >> 4) + (slot & 3); }
+PF_DEVICE int key_slot(int key) { return 16 * ((key >> 2) & 1) + 4 * (key >> 3) + (key & 3); }
+
+// Flash-attention operands: a lane holds 16 consecutive k values (k from 16 (lane >> 5)),
+// fed to two 32x32x16 bf16 MFMAs (or sixteen 32x32x2 fp32 MFMAs).
+// 16 operand values per lane (bf16: 32 bytes; fp32: 64 bytes).
+template <class TC>
+struct Frag16;
+template <>
+struct Frag16<bf16> {
+  bf16x8 v[2];
+  PF_DEVICE void load(const bf16* p) {
+    v[0] = *reinterpret_cast<const bf16x8*>(p);
+    v[1] = *reinterpret_cast<const bf16x8*>(p + 8);
+  }
+};
+template <>
+struct Frag16<float> {
+  f32x4 v[4];
+  PF_DEVICE void load(const float* p) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const f32x4*>(p + 4 * i);
+  }
+};
+
+// acc += A B over the 16 k values the two lane halves hold (bf16: 2 MFMAs, fp32: 16).
+PF_DEVICE void mma32_16(f32x16& acc, const Frag16<bf16>& a, const Frag16<bf16>& b) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v[0], b.v[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v[1], b.v[1], acc, 0, 0, 0);
+}
+PF_DEVICE void mma32_16(f32x16& acc, const Frag16<float>& a, const Frag16<float>& b) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.v[i][e], b.v[i][e], acc, 0, 0, 0);
+}
+
+// P^T as a B operand from 16 fp32 probabilities.
+PF_DEVICE Frag16<bf16> pack_p(const f32x16& p, bf16) {
+  Frag16<bf16> f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    f.v[0][e] = (bf16)p[e];
+    f.v[1][e] = (bf16)p[8 + e];
+  }
+  return f;
+}
+PF_DEVICE Frag16<float> pack_p(const f32x16& p, float) {
+  Frag16<float> f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f.v[i] = f32x4{p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]};
+  return f;
+}
+
+// max(x[l], x[l ^ 32]) over the wave's two 32-lane halves. v_permlane32_swap of x with
+// itself leaves (x[l], x[l + 32]) in the low half and (x[l - 32], x[l]) in the high half:
+// a VALU op, no LDS round trip.
+PF_DEVICE float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Row (inside a 32x32 tile) of accumulator element e of this lane; its column is lane & 31.
 // Elements 4g .. 4g+3 are four consecutive rows.
 PF_DEVICE int acc32_row(int e) { return 8 * (e >> 2) + 4 * (lane_id() >> 5) + (e & 3); }

@@ -7,8 +7,12 @@
 //   pf_transition_fwd:  TransitionBlock.forward (primitives.py:193-251) for any C:
 //     LN -> W1 (SwiGLU on contiguous halves) -> W2, out = y or out += y.
 //
-// The single track is ~0.4 % of a PairFormer block's FLOPs; these kernels favour
-// simplicity: operands are read straight from global memory (they stay in L2).
+// The single track is ~0.4 % of a PairFormer block's FLOPs. The row GEMMs read their
+// operands straight from global memory (they stay in L2); the attention core is a
+// flash kernel on 32x32 MFMAs (V transposed once into key-slot order by a pack kernel,
+// keys split over the four waves of a block and merged through LDS).
+#include <algorithm>
+
 #include "capi.h"
 #include "common.h"
 
@@ -102,65 +106,192 @@ __global__ __launch_bounds__(256) void rowgemm_kernel(const TC* __restrict__ A, 
 // ------------------------------------------------------------------ attention core
 constexpr int kSHeadDim = 24;
 
-// One wave per (b, h, query i). qkvg [B*N][4*H*D] (TC): q | k | v | g (pre-sigmoid).
-// pair_logits fp32 [B][H][N][N]; seq_mask fp32 [B][N]. og [B*N][H*D] = o * sigmoid(g).
-// Dynamic LDS: 4 waves x N fp32 logits.
+// Flash attention for the single track, head dim 24 padded to 32, on 32x32 MFMAs with the
+// same frame as the triangle-attention kernel: a wave owns 32 queries of one (b, h) and
+// computes S^T = K Q^T per 32-key block, so lane (q, h) = (lane & 31, lane >> 5) holds the
+// logits of query q for the 16 keys kappa(r, h) (key_slot / slot_key), which are the P^T
+// operand of O^T += V^T P^T once V^T is stored with keys in slot order.
+//
+// Pack: Vt [B][H][32][Np] (TC; slot order inside each 32-key block; d >= 24 and keys >= N
+// are zero) and the additive key mask MA [B][Np] fp32 in slot order, log2 e * 1e9 (m - 1)
+// for real keys (attention.py:429-430) and -inf for the padding keys.
 template <class TC>
-__global__ __launch_bounds__(256) void single_attn_core_kernel(const TC* __restrict__ qkvg,
-                                                               const float* __restrict__ pl,
+__global__ __launch_bounds__(256) void single_attn_pack_kernel(const TC* __restrict__ qkvg,
                                                                const float* __restrict__ seq_mask,
-                                                               TC* __restrict__ og, int B, int N, int H) {
+                                                               TC* __restrict__ Vt, float* __restrict__ MA, int B,
+                                                               int N, int Np, int H) {
+  const int HD = H * kSHeadDim;
+  const long nvt = (long)B * H * 32 * Np;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < nvt; i += (long)gridDim.x * 256) {
+    const int slot = (int)(i % Np);
+    const long r = i / Np;
+    const int d = (int)(r % 32);
+    const int h = (int)((r / 32) % H);
+    const int b = (int)(r / (32 * H));
+    const int key = (slot & ~31) + slot_key(slot & 31);
+    float v = 0.f;
+    if (d < kSHeadDim && key < N) v = to_f32(qkvg[((size_t)b * N + key) * 4 * HD + 2 * HD + h * kSHeadDim + d]);
+    Vt[i] = from_f32<TC>(v);
+    if (i < (long)B * Np) {
+      const int bb = (int)(i / Np);
+      MA[i] = key < N ? kLog2e * (1e9f * (seq_mask[(size_t)bb * N + key] - 1.0f)) : -INFINITY;
+    }
+  }
+}
+
+// 16 values of a 24-wide head row as a Frag16 (lane half hf: d 16 hf .. 16 hf + 15; d >= 24
+// is zero), each multiplied by `scale`.
+template <class TC>
+PF_DEVICE Frag16<TC> head_frag(const TC* row, int hf, float scale);
+template <>
+PF_DEVICE Frag16<bf16> head_frag<bf16>(const bf16* row, int hf, float scale) {
+  Frag16<bf16> f;
+  const bf16x8 a = *reinterpret_cast<const bf16x8*>(row + 16 * hf);
+  const bf16x8 c = *reinterpret_cast<const bf16x8*>(row + 8);  // d 8..15 (used by hf = 0)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    f.v[0][e] = scale == 1.0f ? a[e] : (bf16)((float)a[e] * scale);
+    f.v[1][e] = hf ? (bf16)0.f : (scale == 1.0f ? c[e] : (bf16)((float)c[e] * scale));
+  }
+  return f;
+}
+template <>
+PF_DEVICE Frag16<float> head_frag<float>(const float* row, int hf, float scale) {
+  Frag16<float> f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d0 = 16 * hf + 4 * i;
+    if (d0 < kSHeadDim) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(row + d0);
+      f.v[i] = f32x4{v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale};
+    } else {
+      f.v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  return f;
+}
+
+// One block per (b, h, 32 queries); its four waves split the key blocks (wave w takes
+// blocks w, w + 4, ...) and merge their partial softmax states through LDS at the end.
+// qkvg [B*N][4*H*24] (TC): q | k | v | g (pre-sigmoid); pair_logits pl fp32 [B][H][N][N];
+// og [B*N][H*24] = o * sigmoid(g). Softmax in fp32 with a running maximum (base 2); a fully
+// masked query row sees every logit shifted by the same -1e9 and attends uniformly, as the
+// reference's fp32 softmax does.
+template <class TC>
+__global__ __launch_bounds__(256) void single_attn_flash_kernel(const TC* __restrict__ qkvg, const TC* __restrict__ Vt,
+                                                                const float* __restrict__ MA,
+                                                                const float* __restrict__ pl, TC* __restrict__ og,
+                                                                int B, int N, int Np, int H) {
   constexpr int D = kSHeadDim;
-  extern __shared__ float lg_all[];
+  __shared__ float part[3][18][64];  // waves 1..3: running max, sum and 16 output values per lane
+  const int nqb = Np / 32;
+  const int qb = blockIdx.x % nqb;
+  const int h = (blockIdx.x / nqb) % H;
+  const int b = blockIdx.x / (nqb * H);
   const int w = wave_id();
   const int l = lane_id();
-  const long task = (long)blockIdx.x * 4 + w;
-  if (task >= (long)B * H * N) return;
-  const int i = (int)(task % N);
-  const int h = (int)((task / N) % H);
-  const int b = (int)(task / ((long)N * H));
-  float* lg = lg_all + (size_t)w * N;
+  const int lq = l & 31, hf = l >> 5;
   const int HD = H * D;
-  const int ld = 4 * HD;
+  const size_t ld = 4 * (size_t)HD;
   const TC* base = qkvg + (size_t)b * N * ld;
-  const float scale = 1.0f / sqrtf((float)D);
-  float q[D];
+  const int q = qb * 32 + lq;
+  const int qc = min(q, N - 1);
+  const Frag16<TC> qf = head_frag<TC>(base + qc * ld + h * D, hf, kLog2e / sqrtf((float)D));
+  const float* plr = pl + (((size_t)b * H + h) * N + qc) * N;
+  const TC* vt = Vt + (((size_t)b * H + h) * 32 + lq) * Np + 16 * hf;
+  const float* ma = MA + (size_t)b * Np + 16 * hf;
+  const bool vec_ok = (N & 3) == 0;
+
+  // Operands of one key block: K and V^T fragments, and the bias + mask logits.
+  struct Ops {
+    Frag16<TC> kf, vf;
+    f32x4 mk[4], pb[4];
+  };
+  auto load = [&](int kb, Ops& op) {
+    const int k0 = kb * 32;
+    op.kf = head_frag<TC>(base + min(k0 + lq, N - 1) * ld + HD + h * D, hf, 1.0f);
+    op.vf.load(vt + k0);
 #pragma unroll
-  for (int d = 0; d < D; ++d) q[d] = to_f32(base[(size_t)i * ld + h * D + d]) * scale;
-  const float* plr = pl + (((size_t)b * H + h) * N + i) * N;
-  const float* mk = seq_mask + (size_t)b * N;
-  float mx = -INFINITY;
-  for (int j = l; j < N; j += 64) {
-    const TC* kr = base + (size_t)j * ld + HD + h * D;
-    float dot = 0.f;
+    for (int g = 0; g < 4; ++g) {
+      op.mk[g] = *reinterpret_cast<const f32x4*>(ma + k0 + 4 * g);
+      const int kk = k0 + 8 * g + 4 * hf;  // keys kappa(4 g .. 4 g + 3, hf)
+      if (vec_ok && kk < N) {
+        op.pb[g] = *reinterpret_cast<const f32x4*>(plr + kk);
+      } else {
 #pragma unroll
-    for (int d = 0; d < D; ++d) dot += q[d] * to_f32(kr[d]);
-    const float v = dot + plr[j] + 1e9f * (mk[j] - 1.0f);
-    lg[j] = v;
-    mx = fmaxf(mx, v);
+        for (int e = 0; e < 4; ++e) op.pb[g][e] = kk + e < N ? plr[kk + e] : 0.f;
+      }
+    }
+  };
+
+  f32x16 o;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) o[r] = 0.f;
+  float mrun = -INFINITY, lrun = 0.f;
+  const int nkb = Np / 32;
+  Ops cur, nxt;
+  if (w < nkb) load(w, cur);
+  for (int kb = w; kb < nkb; kb += 4) {
+    if (kb + 4 < nkb) load(kb + 4, nxt);
+    f32x16 s;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[4 * g + e] = fmaf(cur.pb[g][e], kLog2e, cur.mk[g][e]);
+    mma32_16(s, cur.kf, qf);
+    float m = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) m = fmaxf(m, s[r]);
+    const float mnew = fmaxf(mrun, max_xor32(m));
+    const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+    mrun = mnew;
+    float ls = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = __builtin_amdgcn_exp2f(s[r] - mnew);
+      ls += s[r];
+      o[r] *= alpha;
+    }
+    lrun = lrun * alpha + ls;
+    mma32_16(o, cur.vf, pack_p(s, TC{}));
+    cur = nxt;
   }
-  mx = group_max<64>(mx);
-  float sum = 0.f;
-  float o[D];
+  if (w > 0) {
+    part[w - 1][0][l] = mrun;
+    part[w - 1][1][l] = lrun;
 #pragma unroll
-  for (int d = 0; d < D; ++d) o[d] = 0.f;
-  for (int j = l; j < N; j += 64) {
-    const float p = __expf(lg[j] - mx);
-    sum += p;
-    const TC* vr = base + (size_t)j * ld + 2 * HD + h * D;
-#pragma unroll
-    for (int d = 0; d < D; ++d) o[d] += p * to_f32(vr[d]);
+    for (int r = 0; r < 16; ++r) part[w - 1][2 + r][l] = o[r];
   }
-  sum = group_sum<64>(sum);
+  __syncthreads();
+  if (w > 0) return;
+  // Merge: wave 0 always holds key block 0 (a finite maximum), so mt is finite; a wave
+  // without key blocks has mrun = -inf and contributes 0.
+  float mt = mrun;
 #pragma unroll
-  for (int d = 0; d < D; ++d) o[d] = group_sum<64>(o[d]);
-  if (l < D) {
-    float od = 0.f;
+  for (int v = 0; v < 3; ++v) mt = fmaxf(mt, part[v][0][l]);
+  const float a0 = __builtin_amdgcn_exp2f(mrun - mt);
+  lrun *= a0;
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      if (d == l) od = o[d];
-    const float g = to_f32(base[(size_t)i * ld + 3 * HD + h * D + l]);
-    og[((size_t)b * N + i) * HD + h * D + l] = from_f32<TC>(od / sum * sigmoidf_(g));
+  for (int r = 0; r < 16; ++r) o[r] *= a0;
+#pragma unroll
+  for (int v = 0; v < 3; ++v) {
+    const float av = __builtin_amdgcn_exp2f(part[v][0][l] - mt);
+    lrun += av * part[v][1][l];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[r] += av * part[v][2 + r][l];
+  }
+  if (q >= N) return;
+  const float inv = 1.0f / (lrun + __shfl_xor(lrun, 32, 64));
+  // O^T lane (q, hf) holds d = 8 (r >> 2) + 4 hf + (r & 3); d < 24 for r < 12.
+  const TC* grow = base + q * ld + 3 * HD + h * D;
+  TC* dst = og + ((size_t)b * N + q) * HD + h * D;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int d0 = 8 * j + 4 * hf;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = o[4 * j + e] * inv * sigmoidf_(to_f32(grow[d0 + e]));
+    store_vec<TC, 4>(dst + d0, v);
   }
 }
 
@@ -208,10 +339,19 @@ int single_attn_launch(const void* s_in, const float* seq_mask, const float* pai
   if (int e = ln_launch<TZ, TC>(s_in, lnw, lnb, eps, xn, M, C, st)) return e;
   if (int e = rowgemm_launch<TC, TC, EPI_STORE>(xn, wqkvg, qbias, HD, qkvg, M, 4 * HD, C, st)) return e;
   {
-    const long tasks = (long)B * H * N;
-    const size_t lds = (size_t)4 * N * sizeof(float);
-    single_attn_core_kernel<TC><<<(unsigned)((tasks + 3) / 4), 256, lds, st>>>(qkvg, pair_logits, seq_mask, og, B,
-                                                                                N, H);
+    const int Np = (int)pf::round_up((size_t)N, 32);
+    p += pf::round_up((size_t)M * HD * sizeof(TC), 256);
+    TC* vt = reinterpret_cast<TC*>(p);
+    p += pf::round_up((size_t)B * H * 32 * Np * sizeof(TC), 256);
+    float* ma = reinterpret_cast<float*>(p);
+    const long nvt = (long)B * H * 32 * Np;
+    single_attn_pack_kernel<TC><<<(unsigned)std::min<long>((nvt + 255) / 256, 4096), 256, 0, st>>>(
+        qkvg, seq_mask, vt, ma, B, N, Np, H);
+    if (int e = pf::check_launch("single_attn_pack")) return e;
+    const long blocks = (long)B * H * (Np / 32);
+    pf::KernelTimer timer("single_attn_core", st);
+    single_attn_flash_kernel<TC><<<(unsigned)blocks, 256, 0, st>>>(qkvg, vt, ma, pair_logits, og, B, N, Np, H);
+    timer.stop();
     if (int e = pf::check_launch("single_attn_core")) return e;
   }
   if (accumulate) return rowgemm_launch<TC, TZ, EPI_RESIDUAL>(og, wout, nullptr, 0, out, M, C, HD, st);
@@ -248,7 +388,9 @@ extern "C" {
 size_t pf_single_attn_workspace_bytes(int B, int N, int C, int H, int cdtype) {
   if (B <= 0 || N <= 0 || C <= 0 || H <= 0) return 0;
   const size_t M = (size_t)B * N, es = es_of(cdtype), HD = (size_t)H * kSHeadDim;
-  return pf::round_up(M * C * es, 256) + pf::round_up(M * 4 * HD * es, 256) + pf::round_up(M * HD * es, 256);
+  const size_t Np = pf::round_up((size_t)N, 32);
+  return pf::round_up(M * C * es, 256) + pf::round_up(M * 4 * HD * es, 256) + pf::round_up(M * HD * es, 256) +
+         pf::round_up((size_t)B * H * 32 * Np * es, 256) + pf::round_up((size_t)B * Np * 4, 256);
 }
 
 int pf_single_attn_fwd(const void* s, const float* seq_mask, const float* pair_logits, const float* ln_w,
@@ -260,8 +402,7 @@ int pf_single_attn_fwd(const void* s, const float* seq_mask, const float* pair_l
   PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_single_attn_fwd: B=%d N=%d", B, N);
   PF_REQUIRE(H * kSHeadDim == C && C % 32 == 0, PF_ERR_UNSUPPORTED,
              "pf_single_attn_fwd: C=%d H=%d (built: head dim 24, C a multiple of 32)", C, H);
-  PF_REQUIRE(N <= 4096, PF_ERR_UNSUPPORTED, "pf_single_attn_fwd: N=%d > 4096 (logits are staged in 64 KiB of LDS)", N);
-  PF_REQUIRE(dtype_pair_ok(zdtype, cdtype), PF_ERR_UNSUPPORTED, "pf_single_attn_fwd: dtype pair (%d, %d)", zdtype,
+    PF_REQUIRE(dtype_pair_ok(zdtype, cdtype), PF_ERR_UNSUPPORTED, "pf_single_attn_fwd: dtype pair (%d, %d)", zdtype,
              cdtype);
   PF_REQUIRE(workspace_bytes >= pf_single_attn_workspace_bytes(B, N, C, H, cdtype), PF_ERR_WORKSPACE,
              "pf_single_attn_fwd: workspace %zu < %zu bytes", workspace_bytes,

@@ -134,6 +134,27 @@ def test_single_attention_and_transition_fp32(dev):
     assert_fp32_close(got_t.cpu(), R.transition(inp["single"], pt), what="single transition")
 
 
+@pytest.mark.parametrize("n,masked", [(37, "all"), (64, "none"), (130, "first")])
+def test_single_attention_masking_fp32(dev, n, masked):
+    """Key masks: every key masked (uniform attention, the eager rule), none, and a masked first
+    key block; N not a multiple of 32 (padding keys) and not of 4 (unaligned pair-logit rows)."""
+    sd = W.make_block_weights(27, perturb_affine=True)
+    inp = W.make_inputs(n, seed=9)
+    seq = torch.ones(1, n)
+    if masked == "all":
+        seq.zero_()
+    elif masked == "first":
+        seq[:, :40] = 0
+    pa = sub(sd, "single_attn.")
+    sa = attention.SingleAttention(384).to(dev)
+    sa.load_state_dict(pa)
+    pl = 3 * torch.randn(1, 16, n, n, generator=torch.Generator().manual_seed(10))
+    with torch.no_grad():
+        got = sa(inp["single"].to(dev), seq.to(dev), pl.to(dev))
+    ref = R.single_attention(inp["single"], seq, pl, pa)
+    assert_fp32_close(got.cpu(), ref, what=f"single attention mask={masked}")
+
+
 def _block(sd, dev, dtype=torch.float32):
     blk = evoformer.PairFormerBlock(128, 384).to(dev).eval()
     blk.load_state_dict(sd)
