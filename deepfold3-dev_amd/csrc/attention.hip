@@ -510,20 +510,61 @@ PF_DEVICE void mma_mask(f32x16& acc, float m, float) {
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(lo ? m : 0.f, lo ? 1.f : 0.f, acc, 0, 0, 0);
 }
 
+// Buffer resource over `bytes` bytes at `p` (raw buffer loads: SGPR base, 32-bit offsets,
+// out-of-range lanes read 0).
+PF_DEVICE __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// 16 bytes per lane from a buffer straight into LDS: lane l lands at lds + 16 l. (The host
+// compilation pass cannot type-check this builtin; kernels only run on the device.)
+PF_DEVICE void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+#endif
+}
+template <class TC>
+PF_DEVICE Frag16<TC> buf_frag16(__amdgpu_buffer_rsrc_t r, int voff, int soff);
+template <>
+PF_DEVICE Frag16<bf16> buf_frag16<bf16>(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  Frag16<bf16> f;
+  f.v[0] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  f.v[1] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0));
+  return f;
+}
+template <>
+PF_DEVICE Frag16<float> buf_frag16<float>(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  Frag16<float> f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    f.v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16 * i, soff, 0));
+  return f;
+}
+
 // Block: 4 waves = 4 consecutive lines, one head, QB = 32 * QS queries. The pair-bias tile
-// (query-major, shared by the 4 lines) streams through a 3-stage LDS ring filled by
-// global_load_lds_dwordx4 two key blocks ahead; Q is staged through LDS once; K, V and the
+// (query-major, shared by the 4 lines) streams through a 3-stage LDS ring filled by direct
+// buffer-to-LDS loads two key blocks ahead; Q is staged through LDS once; K, V and the
 // line's mask slot for the lane's key row are per line and go straight into registers
-// (bf16: two key blocks ahead, in three register sets the unrolled key loop rotates).
+// (bf16: two key blocks ahead, in three register sets the unrolled key loop rotates). All
+// global loads are raw buffer loads: a scalar base per operand, a fixed per-lane offset and
+// a scalar per-key-block offset, so the key loop does no vector address arithmetic.
 // L lines per batch item (line stride Lp in the operand buffers). O_HEAD_MAJOR writes O as
 // [b][line][h][q][d] with q < N (the reference kernel's layout) instead of the frame's
 // [b][line][q][h d]; zero_masked_lines writes 0 for a line whose keys are all masked (the
 // reference kernel's rule) instead of the eager path's uniform average.
-template <class TC, int QS, bool O_HEAD_MAJOR>
+//
+// Two modes share this kernel. FAST keeps the softmax reference at 0 for the whole key loop:
+// no running maximum, no rescaling, only exp2, the row sum and the P V products per logit
+// (the logits of LayerNorm-ed projections are small, so 2^s stays far inside fp32/bf16
+// range). A line whose keys are all masked takes the closed form of the eager rule (every
+// real key weighs 1). The wave then checks its result -- row sums in [2^-90, 3e38], all
+// outputs finite -- and writes a per-wave flag redo[blockIdx.x * 4 + wave]; a flagged block
+// is recomputed by the exact mode (FAST = false with `redo` set), which runs the lazy
+// running-maximum softmax below and skips every block whose flags are all 0.
+template <class TC, int QS, bool O_HEAD_MAJOR, bool FAST>
 __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2)) void tri_attn_kernel(
     const TC* __restrict__ Q, const TC* __restrict__ K, const TC* __restrict__ Vt, const float* __restrict__ PB,
     const float* __restrict__ MA, TC* __restrict__ O, int B, int N, int Np, int L, int Lp, int zero_masked_lines,
-    int xcd_remap) {
+    int xcd_remap, int* __restrict__ redo) {
   constexpr int QB = 32 * QS;
   constexpr int NT = 64 * kLinesPerBlock;
   constexpr int QLD = kHeadDim + lds_pad<TC>();
@@ -539,6 +580,12 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   extern __shared__ __attribute__((aligned(16))) float bias_lds[];
   __shared__ __attribute__((aligned(16))) TC q_lds[kLinesPerBlock][QB * QLD];
 
+  if (!FAST && redo != nullptr) {
+    int any = 0;
+#pragma unroll
+    for (int i = 0; i < kLinesPerBlock; ++i) any |= redo[(size_t)blockIdx.x * kLinesPerBlock + i];
+    if (!any) return;  // block-uniform: every wave leaves before the first barrier
+  }
   const int nqb = Np / QB;
   const int nlg = (L + kLinesPerBlock - 1) / kLinesPerBlock;
   const int total = B * nlg * kHeads * nqb;
@@ -568,28 +615,39 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   const int q0 = qb * QB;
   const int nkb = (N + 31) / 32;
 
-  // Bias stage of key block kb: DL instructions per lane, each 8 rows x 128 B; lane l
-  // writes row 8 blk + l / 8 at physical chunk l % 8 = logical chunk (l % 8) ^ swz(row).
+  const auto rk = buf_rsrc(Kh, (unsigned)(Np * kHeadDim * sizeof(TC)));
+  const auto rv = buf_rsrc(Vh, (unsigned)(kHeadDim * Np * sizeof(TC)));
+  const auto rm = buf_rsrc(MAl, (unsigned)(Np * sizeof(float)));
+  const auto rb = buf_rsrc(PBh, (unsigned)((size_t)Np * Np * sizeof(float)));
+  const int k_voff = (lq * kHeadDim + 16 * hf) * (int)sizeof(TC);
+  const int v_voff = (lq * Np + 16 * hf) * (int)sizeof(TC);
+  const int m_voff = key_slot(lq) * 4;
+  // Bias stage: DL loads per lane, each 8 rows x 128 B; lane l writes row 8 blk + l / 8 at
+  // physical chunk l % 8 = logical chunk (l % 8) ^ swz(row).
+  int b_voff[DL];
+#pragma unroll
+  for (int j = 0; j < DL; ++j) {
+    const int row = (w * DL + j) * 8 + (l >> 3);
+    b_voff[j] = ((q0 + row) * Np + 4 * ((l & 7) ^ bias_swz(row))) * 4;
+  }
+
   // Past the last key block the last tile is loaded again into a stage nobody reads, so
   // every iteration issues the same number of loads (the vmcnt budget below relies on it).
-  auto bias_issue = [&](int kb) {
-    float* st = bias_lds + (kb % kBiasStages) * TILE;
-    const int k0 = min(kb, nkb - 1) * 32;
+  // Bias ring stage of key block kb. The key loop runs whole rounds of NSET blocks from 0,
+  // so with NSET == kBiasStages the stage is the (compile-time) position u in the round.
+  // (u: the block's position in its round, or any value congruent to kb mod NSET).
+  auto stage_of = [&](int kb, int u) { return NSET == kBiasStages ? u % NSET : kb % kBiasStages; };
+  auto bias_issue = [&](int kb, int u) {
+    float* st = bias_lds + stage_of(kb, u) * TILE;
+    const int soff = min(kb, nkb - 1) * 32 * 4;
 #pragma unroll
-    for (int j = 0; j < DL; ++j) {
-      const int blk = w * DL + j;
-      const int row = blk * 8 + (l >> 3);
-      const int c = (l & 7) ^ bias_swz(row);
-      const float* src = PBh + (size_t)(q0 + row) * Np + k0 + 4 * c;
-      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) const void*)src,
-                                       (__attribute__((address_space(3))) void*)(st + blk * 8 * 32), 16, 0, 0);
-    }
+    for (int j = 0; j < DL; ++j) buf_load_lds16(rb, st + (w * DL + j) * 8 * 32, b_voff[j], soff);
   };
   auto kv_load = [&](int kb, Frag16<TC>& kf, Frag16<TC>& vf, float& mf) {
     const int k0 = min(kb, nkb - 1) * 32;
-    kf.load(Kh + (size_t)(k0 + lq) * kHeadDim + 16 * hf);
-    vf.load(Vh + (size_t)lq * Np + k0 + 16 * hf);
-    mf = MAl[k0 + key_slot(lq)];
+    kf = buf_frag16<TC>(rk, k_voff, k0 * kHeadDim * (int)sizeof(TC));
+    vf = buf_frag16<TC>(rv, v_voff, k0 * (int)sizeof(TC));
+    mf = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, m_voff, k0 * 4, 0));
   };
 
   // Q of this wave's line -> LDS (rows of D elements, padded)
@@ -624,6 +682,11 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
     mref[s] = 0.f;
     lrun[s] = 0.f;
   }
+  // FAST: row sums of P per sub-block, two partial sums each (bf16: v_dot2 over the packed
+  // probabilities the P V product consumes).
+  float lsum[QS][2];
+#pragma unroll
+  for (int s = 0; s < QS; ++s) lsum[s][0] = lsum[s][1] = 0.f;
 
   __syncthreads();  // Q tiles
 
@@ -633,48 +696,76 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   Frag16<TC> kr[NSET], vr[NSET];
   float mr[NSET];
   if (NSET == 3) kv_load(0, kr[0], vr[0], mr[0]);
-  bias_issue(0);
+  bias_issue(0, 0);
   kv_load(NSET - 2, kr[NSET - 2], vr[NSET - 2], mr[NSET - 2]);
-  bias_issue(1);
+  bias_issue(1, 1);
 
-  auto step = [&](int kb, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf, Frag16<TC>& kn, Frag16<TC>& vn,
-                  float& mn) {
-    const int k0 = kb * 32;
-    // This lane's loads of bias stage kb landed (and with them, in issue order, the K/V
-    // of block kb): after them it issued one step's K/V/mask loads and one bias stage.
+  // Start of step kb: this lane's loads of bias stage kb landed (and with them, in issue
+  // order, the K/V of block kb): after them it issued one step's K/V/mask loads and one bias
+  // stage. Then every wave's stage kb is visible, and stage (kb + 2) % 3 (read at kb - 1) is
+  // free for the next fill.
+  auto sync_issue = [&](int kb, int u, Frag16<TC>& kn, Frag16<TC>& vn, float& mn) {
     constexpr int after = KV_LOADS + DL;
     static_assert(after < 16, "vmcnt immediate");
     __builtin_amdgcn_s_waitcnt(after | (7 << 4) | (15 << 8));
-    // Every wave's stage kb is visible, and stage (kb + 2) % 3 (read at kb - 1) is free.
     __builtin_amdgcn_s_barrier();
     kv_load(kb + NSET - 1, kn, vn, mn);
-    bias_issue(kb + 2);
-    if (!active) return;
+    bias_issue(kb + 2, u + 2);
+  };
 
-    // Phases over the QS query sub-blocks, so the MFMAs of one sub-block overlap the
-    // softmax VALU work of the other: S tiles, the (rare, wave-uniform) reference paths,
-    // row maxima, exp2 and packing, then the P V products.
-    const float* bl = bias_lds + (kb % kBiasStages) * TILE;
+  // S^T tiles of key block kb: bias from the LDS stage, key mask, then q k^T (log2 domain).
+  auto logits = [&](int kb, int u, int s, const Frag16<TC>& kf, float mf, f32x16& sacc) {
+    const int k0 = kb * 32;
+    const float* bl = bias_lds + stage_of(kb, u) * TILE;
     const bool use_mask = masked || k0 + 32 > N;  // padding keys hold -inf in MA
     const float mk = kb < nkb ? mf : -INFINITY;
-    f32x16 sacc[QS];
+    const int R = 32 * s + lq;
+    const float* br = bl + R * 32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(br + 4 * ((4 * hf + i) ^ bias_swz(R)));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sacc[4 * i + e] = bv[e];
+    }
+    // Additive key mask first, then q k^T: a fully masked line rounds every logit to
+    // the same -1e9 log2 e, as the reference's fp32 adds do.
+    if (use_mask) mma_mask(sacc, mk, TC{});
+    Frag16<TC> qf;
+    qf.load(qw + R * QLD + 16 * hf);
+    mma32_16(sacc, kf, qf);
+  };
+
+  // FAST step: p = 2^s, row sums, O^T += V^T P^T.
+  // Sub-blocks one after the other: one S tile live at a time.
+  auto compute_fast = [&](int kb, int u, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf) {
 #pragma unroll
     for (int s = 0; s < QS; ++s) {
-      const int R = 32 * s + lq;
-      const float* br = bl + R * 32;
+      f32x16 sacc;
+      logits(kb, u, s, kf, mf, sacc);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 bv = *reinterpret_cast<const f32x4*>(br + 4 * ((4 * hf + i) ^ bias_swz(R)));
+      for (int r = 0; r < 16; ++r) sacc[r] = __builtin_amdgcn_exp2f(sacc[r]);
+      const Frag16<TC> pf = pack_p(sacc, TC{});
+      if constexpr (sizeof(TC) == 2) {
+        typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+        const bf16x2_t one2 = {(bf16)1.f, (bf16)1.f};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sacc[s][4 * i + e] = bv[e];
+        for (int j = 0; j < 8; ++j) {
+          const bf16x2_t pr = {pf.v[j >> 2][2 * (j & 3)], pf.v[j >> 2][2 * (j & 3) + 1]};
+          lsum[s][j & 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, lsum[s][j & 1], false);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) lsum[s][r & 1] += sacc[r];
       }
-      // Additive key mask first, then q k^T: a fully masked line rounds every logit to
-      // the same -1e9 log2 e, as the reference's fp32 adds do.
-      if (use_mask) mma_mask(sacc[s], mk, TC{});
-      Frag16<TC> qf;
-      qf.load(qw + R * QLD + 16 * hf);
-      mma32_16(sacc[s], kf, qf);  // log2-domain q k^T + pb + mask
+      mma32_16(o[s], vf, pf);
     }
+  };
+
+  // Exact step: lazy running maximum (see kRaise / kLower).
+  auto compute_exact = [&](int kb, int u, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf) {
+    f32x16 sacc[QS];
+#pragma unroll
+    for (int s = 0; s < QS; ++s) logits(kb, u, s, kf, mf, sacc[s]);
     bool ref_set = false;
 #pragma unroll
     for (int s = 0; s < QS; ++s) ref_set |= mref[s] != 0.f;
@@ -728,16 +819,65 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   // set (kb - 1) % NSET, consumed one block earlier. Only whole rounds of NSET blocks run
   // (no conditional step, so the compiler's wait counts stay exact): a step past the last
   // key block sees every key masked to -inf and adds nothing.
-  for (int kb0 = 0; kb0 < nkb; kb0 += NSET) {
-#pragma unroll
-    for (int u = 0; u < NSET; ++u) {
-      const int nx = (u + NSET - 1) % NSET;
-      step(kb0 + u, kr[u], vr[u], mr[u], kr[nx], vr[nx], mr[nx]);
-    }
+#define PF_TRI_ATTN_KEY_LOOP(COMPUTE)                         \
+  for (int kb0 = 0; kb0 < nkb; kb0 += NSET) {                 \
+    _Pragma("unroll") for (int u = 0; u < NSET; ++u) {        \
+      const int nx = (u + NSET - 1) % NSET;                   \
+      sync_issue(kb0 + u, u, kr[nx], vr[nx], mr[nx]);         \
+      if (active) COMPUTE(kb0 + u, u, kr[u], vr[u], mr[u]);   \
+    }                                                         \
   }
+  if constexpr (FAST) {
+    const bool live = active && !all_masked;  // wave-uniform
+    auto compute_live = [&](int kb, int u, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf) {
+      if (live) compute_fast(kb, u, kf, vf, mf);
+    };
+    PF_TRI_ATTN_KEY_LOOP(compute_live)
+    if (active && all_masked) {
+      // Fully masked line: every logit carries the same -1e9 shift, so each real key
+      // weighs 1 (the eager rule's uniform average); V is summed outside the bias ring.
+      for (int kb = 0; kb < nkb; ++kb) {
+        const int k0 = kb * 32;
+        const Frag16<TC> vf = buf_frag16<TC>(rv, v_voff, k0 * (int)sizeof(TC));
+        f32x16 pr;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pr[r] = k0 + 8 * (r >> 2) + 4 * hf + (r & 3) < N ? 1.f : 0.f;
+        float c = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) c += pr[r];
+        const Frag16<TC> pf = pack_p(pr, TC{});
+#pragma unroll
+        for (int s = 0; s < QS; ++s) {
+          lsum[s][0] += c;
+          mma32_16(o[s], vf, pf);
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < QS; ++s) lrun[s] = lsum[s][0] + lsum[s][1];
+  } else {
+    PF_TRI_ATTN_KEY_LOOP(compute_exact)
+  }
+#undef PF_TRI_ATTN_KEY_LOOP
   // The last steps loaded repeat tiles into LDS; none may land after the block's LDS is
   // handed to another block.
   __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+  if constexpr (FAST) {
+    bool bad = false;
+    if (active) {
+#pragma unroll
+      for (int s = 0; s < QS; ++s) {
+        const float lt = lrun[s] + __shfl_xor(lrun[s], 32, 64);
+        const bool real = q0 + 32 * s + lq < N;
+        bad |= real && !(lt >= 0x1p-90f && lt <= 3.0e38f);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bad |= real && !__builtin_isfinite(o[s][r]);
+      }
+    }
+    bad = __any(bad);
+    if (l == 0) redo[(size_t)blockIdx.x * kLinesPerBlock + w] = bad ? 1 : 0;
+    if (bad) return;
+  }
   if (!active) return;
 
   // O^T lane (q, hf) holds d = 8 (r >> 2) + 4 hf + (r & 3).
@@ -994,8 +1134,15 @@ __global__ __launch_bounds__(OutAttnWs::NT, 4) void attn_out_ws_kernel(
 
 // Offsets of the operand buffers inside the workspace (bytes, 256-aligned).
 struct AttnWs {
-  size_t q, k, v, g, o, pb, ma, total;
+  size_t q, k, v, g, o, pb, ma, redo, total;
 };
+
+// Redo flags of the flash kernel: one int per wave, an upper bound over the query-block
+// sizes (lines rounded up to whole blocks, 32-query blocks).
+size_t redo_flag_bytes(int B, int L, int Np) {
+  const size_t lines = pf::round_up((size_t)L, kLinesPerBlock);
+  return (size_t)B * lines * kHeads * (Np / 32) * sizeof(int);
+}
 
 AttnWs attn_ws_layout(int B, int N, int cdtype) {
   const size_t Np = pf::round_up((size_t)N, kPad);
@@ -1015,6 +1162,7 @@ AttnWs attn_ws_layout(int B, int N, int cdtype) {
   w.o = take(tok);
   w.pb = take((size_t)B * kHeads * Np * Np * 4);
   w.ma = take((size_t)B * Np * Np * 4);
+  w.redo = take(redo_flag_bytes(B, N, (int)Np));
   w.total = off;
   return w;
 }
@@ -1032,6 +1180,7 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
   TC* Ob = reinterpret_cast<TC*>(base + L.o);
   float* PBb = reinterpret_cast<float*>(base + L.pb);
   float* MAb = reinterpret_cast<float*>(base + L.ma);
+  int* redo = reinterpret_cast<int*>(base + L.redo);
   const float qscale = (1.0f / sqrtf((float)kHeadDim)) * kLog2e;
   constexpr int BM = block_rows<TC>();
   {
@@ -1067,9 +1216,15 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     pf::KernelTimer timer("tri_attn", s);
     constexpr int QS = attn_qsub<TC>();
     constexpr int NT = 64 * kLinesPerBlock;
-    tri_attn_kernel<TC, QS, false><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap);
+    tri_attn_kernel<TC, QS, false, true><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(
+        Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap, redo);
     timer.stop();
     if (int e = pf::check_launch("tri_attn")) return e;
+    pf::KernelTimer timer2("tri_attn_redo", s);
+    tri_attn_kernel<TC, QS, false, false><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(
+        Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap, redo);
+    timer2.stop();
+    if (int e = pf::check_launch("tri_attn_redo")) return e;
   }
   {
     dim3 grid((N + BM - 1) / BM, N, B);
@@ -1162,7 +1317,7 @@ __global__ __launch_bounds__(256) void evo_pack_mask_kernel(const float* __restr
 }
 
 struct EvoWs {
-  size_t q, k, v, pb, ma, total;
+  size_t q, k, v, pb, ma, redo, total;
 };
 
 EvoWs evo_ws_layout(int B, int S, int N, int cdtype) {
@@ -1181,6 +1336,7 @@ EvoWs evo_ws_layout(int B, int S, int N, int cdtype) {
   w.v = take(tok);
   w.pb = take((size_t)B * kHeads * Np * Np * 4);
   w.ma = take((size_t)B * S * Np * 4);
+  w.redo = take(redo_flag_bytes(B, S, (int)Np));
   w.total = off;
   return w;
 }
@@ -1196,6 +1352,7 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   TC* Vw = reinterpret_cast<TC*>(base + L.v);
   float* PBw = reinterpret_cast<float*>(base + L.pb);
   float* MAw = reinterpret_cast<float*>(base + L.ma);
+  int* redo = reinterpret_cast<int*>(base + L.redo);
   const float qscale = (1.0f / sqrtf((float)kHeadDim)) * kLog2e;
   const unsigned bsh = (unsigned)(B * S * kHeads);
   constexpr int VEC = 16 / sizeof(TC);
@@ -1213,10 +1370,13 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   const long total = (long)B * nlg * kHeads * nqb;
   const int remap = (total % 8 == 0) ? 1 : 0;
   pf::KernelTimer timer("evo_attn", s);
-  tri_attn_kernel<TC, QS, true><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np,
-                                                                            S, S, zero_rule, remap);
+  tri_attn_kernel<TC, QS, true, true><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
+      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo);
+  if (int e = pf::check_launch("evo_attn")) return e;
+  tri_attn_kernel<TC, QS, true, false><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
+      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo);
   timer.stop();
-  return pf::check_launch("evo_attn");
+  return pf::check_launch("evo_attn redo");
 }
 
 }  // namespace

@@ -152,7 +152,8 @@ PF_DEVICE float row_group_sum(float v) {
 }
 
 PF_DEVICE int lane_id() { return threadIdx.x & 63; }
-PF_DEVICE int wave_id() { return threadIdx.x >> 6; }
+// Wave index inside the block, as a wave-uniform (scalar) value.
+PF_DEVICE int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // ---------------------------------------------------------------- MFMA
 template <class TC>
