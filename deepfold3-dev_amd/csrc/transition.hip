@@ -11,6 +11,8 @@
 //                    evoformer.py:322-328, `.movedim(-1, -3)` materialised). When fused into
 //                    the transition, LN' reads the updated z (rounded to z's dtype first, as
 //                    the reference computes it from the stored residual stream).
+#include <algorithm>
+
 #include "capi.h"
 #include "common.h"
 
@@ -282,6 +284,353 @@ __global__ __launch_bounds__(512) void pair_transition32_kernel(
   }
 }
 
+// bf16 path, persistent and weight-streaming: one 8-wave block per CU (two waves per SIMD)
+// walks tiles of 256 positions, 32 per wave (one MFMA column tile). Per tile each wave
+// normalises its positions straight into registers as the B operands of W1 (fp32
+// statistics; a position's 128 channels live in lanes l and l ^ 32). The hidden dim is
+// walked in eight chunks of 64 (a rows 64 c .., b rows 512 + 64 c ..): the chunk's W1 rows
+// (32 KiB) and W2 columns (16 KiB) are streamed into a double-buffered LDS ring by direct
+// buffer-to-LDS loads one chunk ahead (16-byte chunks XOR-swizzled by row, so fragment
+// reads are conflict-free); [h_a | h_b]^T = W1_c LN(x)^T on 32x32x16 MFMAs, u = silu(h_a) h_b
+// goes through a per-wave LDS tile into y^T += W2_c u^T, whose accumulators stay in
+// registers for the whole tile. Epilogue: the residual add and the stores straight from the
+// accumulator layout (lane: one position, 4-channel groups), then the fused single_to_pair:
+// LN' of the updated rows (statistics via the lane-pair swap) and its [128 -> 16]
+// projection as 8 more MFMAs whose A operands (Ws2p, columns in the accumulator's channel
+// order) are built once per block in LDS. The next tile's rows are loaded before the
+// epilogue so their latency overlaps it.
+struct TransWs {
+  static constexpr int C = 128;
+  static constexpr int HC = 64;                      // hidden units per chunk
+  static constexpr int NCH = kHidden / HC;           // 8 chunks
+  static constexpr int NW = 8;                       // waves per block (two per SIMD)
+  static constexpr int NT = 64 * NW;
+  static constexpr int PW = 32;                      // positions per wave
+  static constexpr int BP = PW * NW;                 // positions per tile
+  static constexpr int W1_BYTES = 2 * HC * C * 2;    // 128 rows x 256 B
+  static constexpr int W2_BYTES = C * HC * 2;        // 128 rows x 128 B
+  static constexpr int STAGE = W1_BYTES + W2_BYTES;  // 48 KiB
+  static constexpr int U_BYTES = PW * HC * 2;        // per wave
+  static constexpr int DMA1 = W1_BYTES / 1024 / NW;  // W1 direct loads per wave per chunk
+  static constexpr int DMA2 = W2_BYTES / 1024 / NW;  // W2 direct loads per wave per chunk
+  static constexpr int S2P_BYTES = 8 * 64 * 16;      // Ws2p A fragments [k-step][lane]
+};
+
+constexpr size_t tr_ws_lds_bytes() {
+  return 2 * (size_t)TransWs::STAGE + (size_t)TransWs::NW * TransWs::U_BYTES + TransWs::S2P_BYTES +
+         4 * TransWs::C * sizeof(float);
+}
+
+// Byte offset of 16-byte chunk c of row r in an LDS tile of `row_bytes` rows whose chunks are
+// XOR-swizzled by (row & 7).
+PF_DEVICE int swz_off(int r, int c, int row_bytes) { return r * row_bytes + 16 * (c ^ (r & 7)); }
+
+PF_DEVICE void tr_lds_dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, int voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+#endif
+}
+
+// One position row of z as the raw 16-byte pieces the LayerNorm B operands need: channels
+// 16 ks + 8 hf .. +7 for ks = 0..7 (bf16: 8 pieces, fp32: 16).
+template <class TZ>
+struct ZRow {
+  static constexpr int NP = sizeof(TZ) == 2 ? 8 : 16;
+  u32x4 v[NP];
+  PF_DEVICE void load(const TZ* __restrict__ x, long m, long M, int hf) {
+    if (m < M) {
+      const TZ* row = x + m * TransWs::C + 8 * hf;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        if constexpr (sizeof(TZ) == 2) {
+          v[ks] = *reinterpret_cast<const u32x4*>(row + 16 * ks);
+        } else {
+          v[2 * ks] = *reinterpret_cast<const u32x4*>(row + 16 * ks);
+          v[2 * ks + 1] = *reinterpret_cast<const u32x4*>(row + 16 * ks + 4);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NP; ++i) v[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  PF_DEVICE void get(int ks, float (&o)[8]) const {
+    if constexpr (sizeof(TZ) == 2) {
+      const bf16x8 t = __builtin_bit_cast(bf16x8, v[ks]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (float)t[e];
+    } else {
+      const f32x4 a = __builtin_bit_cast(f32x4, v[2 * ks]), b = __builtin_bit_cast(f32x4, v[2 * ks + 1]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = a[e];
+        o[4 + e] = b[e];
+      }
+    }
+  }
+};
+
+template <class TZ, bool S2P>
+__global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
+    const TZ* __restrict__ x, TZ* __restrict__ out, const float* __restrict__ lnw, const float* __restrict__ lnb,
+    float eps, const bf16* __restrict__ W1, const bf16* __restrict__ W2, long M, int accumulate,
+    const float* __restrict__ s2p_w, const float* __restrict__ s2p_b, float s2p_eps, const bf16* __restrict__ Ws2p,
+    float* __restrict__ logits, long NN) {
+  using Cfg = TransWs;
+  constexpr int C = Cfg::C, HC = Cfg::HC, NCH = Cfg::NCH, PW = Cfg::PW, BP = Cfg::BP;
+  __shared__ __attribute__((aligned(16))) char smem[tr_ws_lds_bytes()];
+  char* stage0 = smem;                                      // [2][STAGE]
+  char* ubase = smem + 2 * Cfg::STAGE;                      // [NW][U_BYTES]
+  char* s2pa = ubase + Cfg::NW * Cfg::U_BYTES;              // [8][64] x 16 B
+  float* lnp = reinterpret_cast<float*>(s2pa + Cfg::S2P_BYTES);  // lnw | lnb | s2p_w | s2p_b
+
+  const int w = wave_id();
+  const int l = lane_id();
+  const int lq = l & 31, hf = l >> 5;
+  char* ub = ubase + w * Cfg::U_BYTES;
+  const long ntiles = (M + BP - 1) / BP;
+
+  for (int i = threadIdx.x; i < C; i += Cfg::NT) {
+    lnp[i] = lnw[i];
+    lnp[C + i] = lnb[i];
+    if (S2P) {
+      lnp[2 * C + i] = s2p_w[i];
+      lnp[3 * C + i] = s2p_b[i];
+    }
+  }
+  if (S2P && w == 0) {
+    // k-step ks = 2 o + mm takes channels 32 o + 8 (2 mm + t) + 4 hf + e at element 4 t + e
+    // (the y^T accumulator order); rows >= 16 are zero.
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      bf16x8 a;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          a[4 * t + e] = lq < kS2pHeads ? Ws2p[lq * C + 32 * (ks >> 1) + 8 * (2 * (ks & 1) + t) + 4 * hf + e]
+                                        : (bf16)0.f;
+      *reinterpret_cast<bf16x8*>(s2pa + (ks * 64 + l) * 16) = a;
+    }
+  }
+
+  // Weight chunk g (global chunk counter; weights of hidden chunk g % NCH) -> LDS stage g & 1.
+  const auto r1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(W1), (short)0, 2 * kHidden * C * 2, 0x00020000);
+  const auto r2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(W2), (short)0, C * kHidden * 2, 0x00020000);
+  auto issue_chunk = [&](long g) {
+    const int c = (int)(g % NCH);
+    char* st = stage0 + (g & 1) * Cfg::STAGE;
+#pragma unroll
+    for (int t = 0; t < Cfg::DMA1; ++t) {
+      const int ins = w * Cfg::DMA1 + t;  // 4 LDS rows of 256 B per instruction
+      const int row = 4 * ins + (l >> 4);
+      const int lc = (l & 15) ^ (row & 7);  // logical chunk this lane fetches
+      const int grow = row < HC ? HC * c + row : kHidden + HC * c + (row - HC);
+      tr_lds_dma16(r1, st + ins * 1024, (grow * C + 8 * lc) * 2, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < Cfg::DMA2; ++t) {
+      const int ins = w * Cfg::DMA2 + t;  // 8 LDS rows of 128 B per instruction
+      const int row = 8 * ins + (l >> 3);
+      const int lc = (l & 7) ^ (row & 7);
+      tr_lds_dma16(r2, st + Cfg::W1_BYTES + ins * 1024, (row * kHidden + HC * c + 8 * lc) * 2, 0);
+    }
+  };
+
+  long g = 0;  // chunks consumed so far
+  long tile = blockIdx.x;
+  ZRow<TZ> zr;
+  if (tile < ntiles) {
+    issue_chunk(0);
+    zr.load(x, tile * BP + w * PW + lq, M, hf);
+  }
+  __syncthreads();  // LN parameters, Ws2p fragments
+
+  for (; tile < ntiles; tile += gridDim.x) {
+    const long m = tile * BP + w * PW + lq;  // this lane's position
+
+    // ---- LN(x) -> B operands xf[ks]: lane (position lq, half hf) holds channels
+    // 16 ks + 8 hf .. +7.
+    bf16x8 xf[C / 16];
+    {
+      float s = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        zr.get(ks, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += v[e];
+      }
+      s += __shfl_xor(s, 32, 64);
+      const float mean = s * (1.0f / C);
+      float q = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        zr.get(ks, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[e] - mean;
+          q += d * d;
+        }
+      }
+      q += __shfl_xor(q, 32, 64);
+      const float rstd = rsqrtf(q * (1.0f / C) + eps);
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        zr.get(ks, v);
+        const float* pw = lnp + 16 * ks + 8 * hf;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[ks][e] = (bf16)((v[e] - mean) * rstd * pw[e] + pw[C + e]);
+      }
+    }
+
+    f32x16 y[4];  // y^T tiles [out rows 32 o ..][the wave's 32 positions]
+#pragma unroll
+    for (int o = 0; o < 4; ++o)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) y[o][e] = 0.f;
+
+#pragma unroll 1
+    for (int c = 0; c < NCH; ++c, ++g) {
+      // Chunk g landed (this lane's loads, then every wave's); stage (g + 1) & 1 was read
+      // by chunk g - 1, which every wave has finished.
+      __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+      __syncthreads();
+      if (c + 1 < NCH || tile + gridDim.x < ntiles) issue_chunk(g + 1);
+      const char* st = stage0 + (g & 1) * Cfg::STAGE;
+      const char* w2s = st + Cfg::W1_BYTES;
+
+#pragma unroll
+      for (int i = 0; i < HC / 32; ++i) {
+        f32x16 ha, hb;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ha[e] = hb[e] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < C / 16; ++ks) {
+          const bf16x8 wa = *reinterpret_cast<const bf16x8*>(st + swz_off(32 * i + lq, 2 * ks + hf, 256));
+          const bf16x8 wb = *reinterpret_cast<const bf16x8*>(st + swz_off(HC + 32 * i + lq, 2 * ks + hf, 256));
+          ha = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa, xf[ks], ha, 0, 0, 0);
+          hb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb, xf[ks], hb, 0, 0, 0);
+        }
+        // u[pos][hidden 32 i + 8 gq + 4 hf + e] = silu(h_a) h_b, 8-byte writes into the
+        // wave's swizzled [32 pos][64 hidden] tile (128-byte rows).
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          bf16x4 u4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) u4[e] = (bf16)(siluf_(ha[4 * gq + e]) * hb[4 * gq + e]);
+          *reinterpret_cast<bf16x4*>(ub + swz_off(lq, 4 * i + gq, 128) + 8 * hf) = u4;
+        }
+      }
+      // The u tile is private to this wave, and one wave's LDS operations complete in order.
+#pragma unroll
+      for (int ks = 0; ks < HC / 16; ++ks) {
+        const bf16x8 uf = *reinterpret_cast<const bf16x8*>(ub + swz_off(lq, 2 * ks + hf, 128));
+#pragma unroll
+        for (int o = 0; o < 4; ++o) {
+          const bf16x8 wf = *reinterpret_cast<const bf16x8*>(w2s + swz_off(32 * o + lq, 2 * ks + hf, 128));
+          y[o] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, uf, y[o], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();  // u reads issued before the next chunk's writes
+    }
+
+    // ---- next tile's rows (their latency overlaps this epilogue), then the residual
+    // operands, all issued before any of them is used.
+    if (tile + gridDim.x < ntiles) zr.load(x, (tile + gridDim.x) * BP + w * PW + lq, M, hf);
+    // Lane (position lq, half hf) holds channels 32 o + 8 gq + 4 hf + e of y[o][4 gq + e].
+    float res[4][16];
+    if (accumulate && m < M) {
+      const TZ* row = out + m * C;
+#pragma unroll
+      for (int o = 0; o < 4; ++o)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int ch = 32 * o + 8 * gq + 4 * hf;
+          if constexpr (sizeof(TZ) == 2) {
+            const bf16x4 t = *reinterpret_cast<const bf16x4*>(row + ch);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) res[o][4 * gq + e] = (float)t[e];
+          } else {
+            const f32x4 t = *reinterpret_cast<const f32x4*>(row + ch);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) res[o][4 * gq + e] = t[e];
+          }
+        }
+    } else {
+#pragma unroll
+      for (int o = 0; o < 4; ++o)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) res[o][e] = 0.f;
+    }
+    if (m < M) {
+      TZ* row = out + m * C;
+#pragma unroll
+      for (int o = 0; o < 4; ++o)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = to_f32(from_f32<TZ>(res[o][4 * gq + e] + y[o][4 * gq + e]));
+            y[o][4 * gq + e] = v[e];  // the updated row as stored (single_to_pair input)
+          }
+          store_vec<TZ, 4>(row + 32 * o + 8 * gq + 4 * hf, v);
+        }
+    }
+
+    if constexpr (S2P) {
+      // LN' of the updated row, then logits^T = Ws2p LN'^T on 32x32x16 MFMAs (heads 16..31
+      // of the A operand are zero).
+      float s = 0.f;
+#pragma unroll
+      for (int o = 0; o < 4; ++o)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s += y[o][e];
+      s += __shfl_xor(s, 32, 64);
+      const float mean = s * (1.0f / C);
+      float q = 0.f;
+#pragma unroll
+      for (int o = 0; o < 4; ++o)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float d = y[o][e] - mean;
+          q += d * d;
+        }
+      q += __shfl_xor(q, 32, 64);
+      const float rstd = rsqrtf(q * (1.0f / C) + s2p_eps);
+      f32x16 acc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const int o = ks >> 1, mm = ks & 1;
+        bf16x8 bfr;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int ch = 32 * o + 8 * (2 * mm + t) + 4 * hf + e;
+            bfr[4 * t + e] = (bf16)((y[o][4 * (2 * mm + t) + e] - mean) * rstd * lnp[2 * C + ch] + lnp[3 * C + ch]);
+          }
+        const bf16x8 afr = *reinterpret_cast<const bf16x8*>(s2pa + (ks * 64 + l) * 16);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr, bfr, acc, 0, 0, 0);
+      }
+      // acc: lane (position, half hf) holds heads 8 gq + 4 hf + e; heads < 16 for gq < 2.
+      if (m < M) {
+        const long b = m / NN, pos = m % NN;
+#pragma unroll
+        for (int gq = 0; gq < 2; ++gq)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) logits[(b * kS2pHeads + 8 * gq + 4 * hf + e) * NN + pos] = acc[4 * gq + e];
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // no direct load outlives the block
+}
+
 // Standalone single_to_pair: LN'(z) Ws2p^T -> logits [B][16][N][N].
 template <class TZ, class TC>
 __global__ __launch_bounds__(256) void single_to_pair_kernel(const TZ* __restrict__ z, const float* __restrict__ lnw,
@@ -341,15 +690,16 @@ int transition_launch(const void* x, const float* lnw, const float* lnb, float e
                       const void* ws2p, float* logits, long NN, hipStream_t s) {
   pf::KernelTimer timer("pair_transition", s);
   if constexpr (sizeof(TC) == 2) {
-    dim3 grid((unsigned)((M + 127) / 128));
+    const long ntiles = (M + TransWs::BP - 1) / TransWs::BP;
+    const unsigned nblk = (unsigned)std::min<long>(ntiles, pf::cu_count());
     if (logits)
-      pair_transition32_kernel<TZ, true><<<grid, 512, 0, s>>>((const TZ*)x, (TZ*)out, lnw, lnb, eps, (const bf16*)w1,
-                                                             (const bf16*)w2, M, accumulate, s2p_w, s2p_b, s2p_eps,
-                                                             (const bf16*)ws2p, logits, NN);
+      pair_transition_ws_kernel<TZ, true><<<nblk, TransWs::NT, 0, s>>>(
+          (const TZ*)x, (TZ*)out, lnw, lnb, eps, (const bf16*)w1, (const bf16*)w2, M, accumulate, s2p_w, s2p_b,
+          s2p_eps, (const bf16*)ws2p, logits, NN);
     else
-      pair_transition32_kernel<TZ, false><<<grid, 512, 0, s>>>((const TZ*)x, (TZ*)out, lnw, lnb, eps,
-                                                              (const bf16*)w1, (const bf16*)w2, M, accumulate,
-                                                              nullptr, nullptr, 0.f, nullptr, nullptr, NN);
+      pair_transition_ws_kernel<TZ, false><<<nblk, TransWs::NT, 0, s>>>(
+          (const TZ*)x, (TZ*)out, lnw, lnb, eps, (const bf16*)w1, (const bf16*)w2, M, accumulate, nullptr, nullptr,
+          0.f, nullptr, nullptr, NN);
     timer.stop();
     return pf::check_launch("pair_transition");
   }

@@ -95,6 +95,35 @@ def test_grid_attention_residual_in_place(dev):
     assert_fp32_close(z.cpu(), ref, what="fused residual, batch 2")
 
 
+@pytest.mark.parametrize("stream_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n", [24, 70, 130])
+def test_pair_transition_and_fused_single_to_pair_bf16_rule(dev, n, stream_dtype):
+    """bf16 GEMM kernel (persistent, 256-position tiles; N^2 not a multiple of the tile), the
+    residual it adds and the fused single_to_pair logits, by the bf16 rule against the fp32
+    oracle; bf16 residual stream or fp32 stream under autocast."""
+    print(f"[pair transition bf16 n={n} stream={stream_dtype}]", flush=True)
+    sd = W.make_block_weights(28, perturb_affine=True)
+    p = sub(sd, "pair_transition.")
+    inp = W.make_inputs(n, seed=12)
+    blk = primitives.TransitionBlock(128, 4).to(dev)
+    blk.load_state_dict(p)
+    blk = blk.to(stream_dtype)
+    x = inp["pair"].to(dev, stream_dtype).contiguous()
+    x0 = x.clone()
+    ks = ("single_to_pair_norm.weight", "single_to_pair_norm.bias", "single_to_pair.weight")
+    s2p = (sd[ks[0]].to(dev), sd[ks[1]].to(dev), 1e-5, sd[ks[2]].to(dev, torch.bfloat16))  # cast to the GEMM dtype
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        y = blk(x)
+        _, logits = blk.forward_residual_(x, s2p=s2p)
+        ey = R.transition(x0, to(p, dev, stream_dtype))
+        el = R.single_to_pair((x0 + ey).to(stream_dtype), to(sd, dev, stream_dtype))
+    ry = R.transition(x0.float().cpu(), p)
+    rl = R.single_to_pair(x0.float().cpu() + ry, sd)
+    print("  update", assert_bf16_rule(y.cpu(), ey.cpu(), ry, "pair transition bf16"), flush=True)
+    print("  residual", assert_bf16_rule(x.cpu(), (x0 + ey).cpu(), x0.float().cpu() + ry, "residual"), flush=True)
+    print("  s2p", assert_bf16_rule(logits.cpu(), el.cpu(), rl, "single_to_pair bf16"), flush=True)
+
+
 @pytest.mark.parametrize("n", [24, 70])
 def test_pair_transition_and_fused_single_to_pair_fp32(dev, n):
     sd = W.make_block_weights(25, perturb_affine=True)
