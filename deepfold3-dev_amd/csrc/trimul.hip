@@ -258,7 +258,10 @@ struct Contract256 {
   static constexpr int NT = 512;
   static constexpr int TILE = BT * KT;       // elements of one operand k-tile
   static constexpr int STAGE = 2 * TILE;     // P tile then Q tile
-  static constexpr int SMEM = 2 * STAGE * 2;
+  static constexpr int OLD = BT + 8;         // output staging rows (bf16): 528 bytes
+  static constexpr int RING = 2 * STAGE * 2;
+  static constexpr int OUT = BT * OLD * 2;
+  static constexpr int SMEM = RING > OUT ? RING : OUT;
 };
 
 PF_DEVICE int k2_swz(int row) { return (row >> 1) & 7; }
@@ -353,8 +356,10 @@ __global__ __launch_bounds__(512) void trimul_contract256_kernel(const bf16* __r
     }
   }
 
-  // acc[a][c] element e: j = wj + 32 a + acc32_row(e), i = wi + 32 c + (lane & 31).
-  bf16* Xg = X + (size_t)g * pe + (size_t)i0 * Np + j0;
+  // acc[a][c] element e: j = wj + 32 a + acc32_row(e), i = wi + 32 c + (lane & 31). The tile
+  // goes through LDS ([i][j], 528-byte rows) so the stores are whole 512-byte rows.
+  __syncthreads();  // every wave is done reading the ring
+  bf16* ot = lds;
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -362,8 +367,17 @@ __global__ __launch_bounds__(512) void trimul_contract256_kernel(const bf16* __r
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         float v[4] = {acc[a][cc][4 * g4], acc[a][cc][4 * g4 + 1], acc[a][cc][4 * g4 + 2], acc[a][cc][4 * g4 + 3]};
-        store_vec<bf16, 4>(Xg + (size_t)(wi + 32 * cc + r) * Np + wj + 32 * a + acc32_row(4 * g4), v);
+        store_vec<bf16, 4>(ot + (wi + 32 * cc + r) * Cfg::OLD + wj + 32 * a + acc32_row(4 * g4), v);
       }
+  __syncthreads();
+  bf16* Xg = X + (size_t)g * pe + (size_t)i0 * Np + j0;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < BT * BT / 8 / Cfg::NT; ++it) {
+    const int idx = tid + it * Cfg::NT;
+    const int row = idx / (BT / 8), ch = idx % (BT / 8);
+    *reinterpret_cast<u32x4*>(Xg + (size_t)row * Np + 8 * ch) = *reinterpret_cast<const u32x4*>(ot + row * Cfg::OLD + 8 * ch);
+  }
 }
 
 // ------------------------------------------------------------------ K3
