@@ -510,18 +510,6 @@ PF_DEVICE void mma_mask(f32x16& acc, float m, float) {
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(lo ? m : 0.f, lo ? 1.f : 0.f, acc, 0, 0, 0);
 }
 
-// Buffer resource over `bytes` bytes at `p` (raw buffer loads: SGPR base, 32-bit offsets,
-// out-of-range lanes read 0).
-PF_DEVICE __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-// 16 bytes per lane from a buffer straight into LDS: lane l lands at lds + 16 l. (The host
-// compilation pass cannot type-check this builtin; kernels only run on the device.)
-PF_DEVICE void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-#endif
-}
 template <class TC>
 PF_DEVICE Frag16<TC> buf_frag16(__amdgpu_buffer_rsrc_t r, int voff, int soff);
 template <>

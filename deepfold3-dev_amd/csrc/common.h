@@ -411,6 +411,21 @@ PF_DEVICE void zero_acc32(f32x16 (&acc)[MI][NJ]) {
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 }
 
+// ---------------------------------------------------------------- buffer loads
+// Buffer resource over `bytes` bytes at `p` (raw buffer loads: scalar base, 32-bit offsets;
+// out-of-range reads return 0).
+PF_DEVICE __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// 16 bytes per lane from a buffer straight into LDS: lane l lands at lds + 16 l (the LDS
+// address is taken from the wave's first lane). The host compilation pass cannot type-check
+// this builtin; kernels only run on the device.
+PF_DEVICE void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+#endif
+}
+
 // ---------------------------------------------------------------- 16-value fragments
 // Key order of a 32-key block in flash-attention operands. With S^T = K Q^T on a 32x32
 // MFMA, lane (q, h) (q = lane & 31, h = lane >> 5) holds the logits of query q for keys

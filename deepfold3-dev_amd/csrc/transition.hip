@@ -325,12 +325,6 @@ constexpr size_t tr_ws_lds_bytes() {
 // XOR-swizzled by (row & 7).
 PF_DEVICE int swz_off(int r, int c, int row_bytes) { return r * row_bytes + 16 * (c ^ (r & 7)); }
 
-PF_DEVICE void tr_lds_dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, int voff, int soff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-#endif
-}
-
 // One position row of z as the raw 16-byte pieces the LayerNorm B operands need: channels
 // 16 ks + 8 hf .. +7 for ks = 0..7 (bf16: 8 pieces, fp32: 16).
 template <class TZ>
@@ -415,8 +409,8 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
   }
 
   // Weight chunk g (global chunk counter; weights of hidden chunk g % NCH) -> LDS stage g & 1.
-  const auto r1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(W1), (short)0, 2 * kHidden * C * 2, 0x00020000);
-  const auto r2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(W2), (short)0, C * kHidden * 2, 0x00020000);
+  const auto r1 = buf_rsrc(W1, 2 * kHidden * C * 2);
+  const auto r2 = buf_rsrc(W2, C * kHidden * 2);
   auto issue_chunk = [&](long g) {
     const int c = (int)(g % NCH);
     char* st = stage0 + (g & 1) * Cfg::STAGE;
@@ -426,14 +420,14 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
       const int row = 4 * ins + (l >> 4);
       const int lc = (l & 15) ^ (row & 7);  // logical chunk this lane fetches
       const int grow = row < HC ? HC * c + row : kHidden + HC * c + (row - HC);
-      tr_lds_dma16(r1, st + ins * 1024, (grow * C + 8 * lc) * 2, 0);
+      buf_load_lds16(r1, st + ins * 1024, (grow * C + 8 * lc) * 2, 0);
     }
 #pragma unroll
     for (int t = 0; t < Cfg::DMA2; ++t) {
       const int ins = w * Cfg::DMA2 + t;  // 8 LDS rows of 128 B per instruction
       const int row = 8 * ins + (l >> 3);
       const int lc = (l & 7) ^ (row & 7);
-      tr_lds_dma16(r2, st + Cfg::W1_BYTES + ins * 1024, (row * kHidden + HC * c + 8 * lc) * 2, 0);
+      buf_load_lds16(r2, st + Cfg::W1_BYTES + ins * 1024, (row * kHidden + HC * c + 8 * lc) * 2, 0);
     }
   };
 
