@@ -17,8 +17,9 @@
 // -1e9 * log2(e) term swamps every logit by the same amount.
 //
 // Frames. "line" is the attention row: i for the starting node (row mode), j for the
-// ending node (column mode). Keys and queries run along the other token index. The
-// projection kernel walks z along a line in both modes (column mode reads z down a column),
+// ending node (column mode). Keys and queries run along the other token index. In bf16, K
+// and Vt are stored as 2 KB key-block tiles in the flash kernel's fragment order (kv_chunk).
+// The projection kernel walks z along a line in both modes (column mode reads z down a column),
 // so every operand is written contiguously in the attention frame. The pair bias is
 // written query-major [h][q][key slot] in row mode and key-major [h][key][q] in column mode
 // (again the order in which the projection produces it); an in-place tile transpose turns
@@ -45,6 +46,13 @@ constexpr int kPad = 128;  // token padding of the attention frame
 #ifndef PF_ATTN_QS
 #define PF_ATTN_QS 2
 #endif
+
+// bf16 K and Vt tiles. Per (line, head) each 32-key block is one 2 KB tile of 128 chunks of
+// 16 bytes: chunk 32 g + r holds row r, columns 8 c .. 8 c + 7 with g = 2 (c & 1) + (c >> 1)
+// (K: row = key, column = d; Vt: row = d, column = key slot). Lane (r, hf) of the flash
+// kernel needs columns 16 hf + 8 j .. +7 of row r for MFMA j, i.e. chunk 64 j + 32 hf + r =
+// 64 j + lane: each of its two loads reads one contiguous kilobyte.
+PF_DEVICE int kv_chunk(int row, int c) { return 32 * (2 * (c & 1) + (c >> 1)) + row; }
 
 
 // ------------------------------------------------------------------ A1
@@ -432,8 +440,8 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (kind <= 1) {
-      bf16* dst0 = (kind == 0 ? Q : K) + ((lineq * kHeads + h0) * Np + t0) * kHeadDim;
+    if (kind == 0) {
+      bf16* dst0 = Q + ((lineq * kHeads + h0) * Np + t0) * kHeadDim;
 #pragma unroll
       for (int hi = 0; hi < 2; ++hi)
 #pragma unroll
@@ -443,15 +451,23 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
           *reinterpret_cast<u32x4*>(dst0 + ((size_t)hi * Np + p) * kHeadDim + 8 * c) =
               *reinterpret_cast<const u32x4*>(stg + (hi * BP + p) * QLD + 8 * c);
         }
-    } else if (kind == 2) {
-      bf16* dst0 = Vt + ((lineq * kHeads + h0) * kHeadDim) * (size_t)Np + t0;
+    } else if (kind <= 2) {
+      // K / Vt key-block tiles (kv_chunk): lane-consecutive chunks, so each store
+      // instruction writes one contiguous kilobyte. The tile's BP / 32 key blocks of head
+      // h0 + hi follow each other in memory.
+      bf16* dst0 = (kind == 1 ? K : Vt) + ((lineq * kHeads + h0) * Np + t0) * kHeadDim;
 #pragma unroll
-      for (int it = 0; it < 2 * kHeadDim * BP / 8 / 64; ++it) {
-        const int r = it * 8 + (l >> 3);  // hi * 32 + d
-        const int c = l & 7;
-        *reinterpret_cast<u32x4*>(dst0 + (size_t)r * Np + 8 * c) =
-            *reinterpret_cast<const u32x4*>(stg + r * VLD + 8 * c);
-      }
+      for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int it = 0; it < BP * kHeadDim / 8 / 64; ++it) {
+          const int g = it * 64 + l;  // chunk of this head's BP / 32 tiles
+          const int kbl = g >> 7, grp = (g >> 5) & 3, r = g & 31;
+          const int c = 2 * (grp & 1) + (grp >> 1);
+          const bf16* src = kind == 1 ? stg + (hi * BP + 32 * kbl + r) * QLD + 8 * c
+                                      : stg + (hi * kHeadDim + r) * VLD + 32 * kbl + 8 * c;
+          *reinterpret_cast<u32x4*>(dst0 + (size_t)hi * Np * kHeadDim + 8 * g) =
+              *reinterpret_cast<const u32x4*>(src);
+        }
     } else {
       bf16* dst0 = G + (lineq * Np + t0) * kC + 64 * (w & 1);
 #pragma unroll
@@ -510,13 +526,16 @@ PF_DEVICE void mma_mask(f32x16& acc, float m, float) {
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(lo ? m : 0.f, lo ? 1.f : 0.f, acc, 0, 0, 0);
 }
 
+// K / Vt fragment loads. bf16: the 2 KB tile of a key block is stored fragment-native
+// (kv_chunk), so the two 16-byte loads of a wave are each one contiguous 1 KB run
+// (voff = 16 * lane, second load at +1 KB). fp32: rows of the plain layouts, 16 bytes apart.
 template <class TC>
 PF_DEVICE Frag16<TC> buf_frag16(__amdgpu_buffer_rsrc_t r, int voff, int soff);
 template <>
 PF_DEVICE Frag16<bf16> buf_frag16<bf16>(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
   Frag16<bf16> f;
   f.v[0] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-  f.v[1] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0));
+  f.v[1] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 1024, soff, 0));
   return f;
 }
 template <>
@@ -607,8 +626,11 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   const auto rv = buf_rsrc(Vh, (unsigned)(kHeadDim * Np * sizeof(TC)));
   const auto rm = buf_rsrc(MAl, (unsigned)(Np * sizeof(float)));
   const auto rb = buf_rsrc(PBh, (unsigned)((size_t)Np * Np * sizeof(float)));
-  const int k_voff = (lq * kHeadDim + 16 * hf) * (int)sizeof(TC);
-  const int v_voff = (lq * Np + 16 * hf) * (int)sizeof(TC);
+  // bf16: K and Vt in 2 KB fragment-native key-block tiles; fp32: K [key][d], Vt [d][slot].
+  constexpr bool kBlk = sizeof(TC) == 2;
+  const int k_voff = kBlk ? 16 * l : (lq * kHeadDim + 16 * hf) * (int)sizeof(TC);
+  const int v_voff = kBlk ? 16 * l : (lq * Np + 16 * hf) * (int)sizeof(TC);
+  const int v_kstride = kBlk ? kHeadDim * (int)sizeof(TC) : (int)sizeof(TC);  // bytes per key
   const int m_voff = key_slot(lq) * 4;
   // Bias stage: DL loads per lane, each 8 rows x 128 B; lane l writes row 8 blk + l / 8 at
   // physical chunk l % 8 = logical chunk (l % 8) ^ swz(row).
@@ -634,7 +656,7 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   auto kv_load = [&](int kb, Frag16<TC>& kf, Frag16<TC>& vf, float& mf) {
     const int k0 = min(kb, nkb - 1) * 32;
     kf = buf_frag16<TC>(rk, k_voff, k0 * kHeadDim * (int)sizeof(TC));
-    vf = buf_frag16<TC>(rv, v_voff, k0 * (int)sizeof(TC));
+    vf = buf_frag16<TC>(rv, v_voff, k0 * v_kstride);
     mf = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, m_voff, k0 * 4, 0));
   };
 
@@ -826,7 +848,7 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
       // weighs 1 (the eager rule's uniform average); V is summed outside the bias ring.
       for (int kb = 0; kb < nkb; ++kb) {
         const int k0 = kb * 32;
-        const Frag16<TC> vf = buf_frag16<TC>(rv, v_voff, k0 * (int)sizeof(TC));
+        const Frag16<TC> vf = buf_frag16<TC>(rv, v_voff, k0 * v_kstride);
         f32x16 pr;
 #pragma unroll
         for (int r = 0; r < 16; ++r) pr[r] = k0 + 8 * (r >> 2) + 4 * hf + (r & 3) < N ? 1.f : 0.f;
@@ -1261,10 +1283,13 @@ __global__ __launch_bounds__(256) void evo_pack_qk_kernel(const TC* __restrict__
     for (int e = 0; e < VEC; ++e) vq[e] = vk[e] = 0.f;
   }
   store_vec<TC, VEC>(Qw + (bsh * Np + t) * kHeadDim + d0, vq);
-  store_vec<TC, VEC>(Kw + (bsh * Np + t) * kHeadDim + d0, vk);
+  if constexpr (sizeof(TC) == 2)  // key-block tiles (kv_chunk)
+    store_vec<TC, VEC>(Kw + (bsh * Np + (t & ~31)) * kHeadDim + 8 * kv_chunk(t & 31, d0 / 8), vk);
+  else
+    store_vec<TC, VEC>(Kw + (bsh * Np + t) * kHeadDim + d0, vk);
 }
 
-// One block per (32-key block, b s h): V[t][d] -> Vt[d][slot].
+// One block per (32-key block, b s h): V[t][d] -> Vt[d][slot] (bf16: the key-block tile).
 template <class TC>
 __global__ __launch_bounds__(256) void evo_pack_v_kernel(const TC* __restrict__ v, TC* __restrict__ Vt, int N,
                                                          int Np) {
@@ -1278,7 +1303,11 @@ __global__ __launch_bounds__(256) void evo_pack_v_kernel(const TC* __restrict__ 
   __syncthreads();
   for (int i = threadIdx.x; i < 32 * kHeadDim; i += 256) {
     const int d = i / 32, slot = i % 32;
-    Vt[(bsh * kHeadDim + d) * Np + k0 + slot] = from_f32<TC>(tile[slot_key(slot)][d]);
+    const TC v = from_f32<TC>(tile[slot_key(slot)][d]);
+    if constexpr (sizeof(TC) == 2)
+      Vt[(bsh * Np + k0) * kHeadDim + 8 * kv_chunk(d, slot / 8) + slot % 8] = v;
+    else
+      Vt[(bsh * kHeadDim + d) * Np + k0 + slot] = v;
   }
 }
 
