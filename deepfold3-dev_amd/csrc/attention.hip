@@ -703,12 +703,19 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   // Every key-block step issues K/V/mask (NSET - 1 blocks ahead) and then one bias stage
   // (two blocks ahead); the prologue issues what steps -2 and -1 would have, so every
   // lane -- inactive waves load their group's first line -- keeps the same load order.
+  // The scheduling barriers keep the prologue's loads in the in-loop order (K/V/mask, then
+  // bias): the vmcnt budget counts them in that order, and so does the compiler's own wait
+  // insertion, which otherwise waits on the newest loads inside the first step of every round.
   Frag16<TC> kr[NSET], vr[NSET];
   float mr[NSET];
   if (NSET == 3) kv_load(0, kr[0], vr[0], mr[0]);
+  __builtin_amdgcn_sched_barrier(0);
   bias_issue(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
   kv_load(NSET - 2, kr[NSET - 2], vr[NSET - 2], mr[NSET - 2]);
+  __builtin_amdgcn_sched_barrier(0);
   bias_issue(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
 
   // Start of step kb: this lane's loads of bias stage kb landed (and with them, in issue
   // order, the K/V of block kb): after them it issued one step's K/V/mask loads and one bias
@@ -828,14 +835,19 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   // Key loop unrolled over the register sets: key block kb uses set kb % NSET and refills
   // set (kb - 1) % NSET, consumed one block earlier. Only whole rounds of NSET blocks run
   // (no conditional step, so the compiler's wait counts stay exact): a step past the last
-  // key block sees every key masked to -inf and adds nothing.
+  // key block sees every key masked to -inf and adds nothing. The loop is entered
+  // unconditionally (nkb >= 1): a zero-trip test in front of it lets the compiler sink the
+  // prologue's K/V loads behind the bias loads, and the reordered counts then make it wait
+  // on the next block's loads inside every first step.
 #define PF_TRI_ATTN_KEY_LOOP(COMPUTE)                         \
-  for (int kb0 = 0; kb0 < nkb; kb0 += NSET) {                 \
+  for (int kb0 = 0;;) {                                       \
     _Pragma("unroll") for (int u = 0; u < NSET; ++u) {        \
       const int nx = (u + NSET - 1) % NSET;                   \
       sync_issue(kb0 + u, u, kr[nx], vr[nx], mr[nx]);         \
       if (active) COMPUTE(kb0 + u, u, kr[u], vr[u], mr[u]);   \
     }                                                         \
+    kb0 += NSET;                                              \
+    if (kb0 >= nkb) break;                                    \
   }
   if constexpr (FAST) {
     const bool live = active && !all_masked;  // wave-uniform

@@ -770,23 +770,40 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
 }
 
 // K3, persistent and weight-stationary (bf16 GEMMs). One 512-thread block per CU walks
-// tiles of 64 positions (i, j0 .. j0+63) of one row. Wave w owns output channels 16 w ..
-// +16: rows of out_proj and out_gate as 16x16x32 MFMA A operands, resident in registers;
-// the two accumulators share a layout, so the gate applies in registers. Per tile: the
-// X tile (channel-major, 128 x 64) is transposed through LDS for LN_out, the z tile is
-// normalised (LN_in) from registers that also keep it for the residual; after the MFMAs
-// each wave stages its fp32 update (16 channels x 64 positions) block-wide, and each wave
-// then adds the update to the 8 z rows it loaded and writes them. The next tile's X and z
-// are loaded during this tile's MFMAs.
+// tiles of 64 positions (i, j0 .. j0+63) of one row. Wave w owns output channels
+// 32 (w & 3) .. +32 of positions 32 (w >> 2) .. +32: rows of out_proj and out_gate as
+// 32x32x16 MFMA A operands, resident in registers; the two accumulators share a layout, so
+// the gate applies in registers. Per tile: the X tile (channel-major, 128 x 64) goes to
+// LDS and is normalised (LN_out) by a pass whose reads run along positions (no bank
+// conflicts); the z tile is normalised (LN_in) from registers that also keep it for the
+// residual; after the MFMAs each wave stages its fp32 update block-wide, and each wave then
+// adds the update to the 8 z rows it loaded and writes them. The next tile's X and z are
+// loaded during this tile's MFMAs.
 struct OutputWs {
   static constexpr int C = 128;
   static constexpr int BP = 64;
   static constexpr int NW = 8;
   static constexpr int NT = 64 * NW;
   static constexpr int XLD = C + 8;   // bf16 operand rows [pos][ch]
-  static constexpr int TLD = BP + 8;  // bf16 X transpose rows [ch][pos]
+  static constexpr int TLD = BP + 8;  // bf16 X tile rows [ch][pos]
   static constexpr int SLD = C + 4;   // fp32 update stage rows [pos][ch]
 };
+
+// Sum over aligned groups of 8 lanes with DPP moves: quad_perm [1,0,3,2], quad_perm
+// [2,3,0,1], row_half_mirror.
+PF_DEVICE float dpp_sum8(float v) {
+  auto dpp = [](float x, int ctrl) -> float {
+    switch (ctrl) {
+      case 0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+      case 1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+      default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+    }
+  };
+  v += dpp(v, 0);
+  v += dpp(v, 1);
+  v += dpp(v, 2);
+  return v;
+}
 
 template <class TZ>
 __global__ __launch_bounds__(OutputWs::NT) void trimul_output_ws_kernel(
@@ -810,16 +827,18 @@ __global__ __launch_bounds__(OutputWs::NT) void trimul_output_ws_kernel(
   const int tid = threadIdx.x;
   const int w = wave_id();
   const int l = lane_id();
-  const size_t pe = (size_t)Np * Np;
+  const int pe = Np * Np;  // plane size (elements); Np <= 4096 keeps every offset below 2^31
   const int tpr = (N + BP - 1) / BP;
-  const long ntiles = (long)B * N * tpr;
+  const int ntiles = B * N * tpr;
+  const int cw = w & 3, pw = w >> 2;
 
-  // Weights: lane holds row 16 w + (l & 15), k = 32 ks + 8 (l >> 4) + e.
-  bf16x8 wo[C / 32], wg[C / 32];
+  // Weights: lane holds row 32 cw + (l & 31), k = 16 ks + 8 (l >> 5) + e.
+  bf16x8 wo[C / 16], wg[C / 16];
 #pragma unroll
-  for (int ks = 0; ks < C / 32; ++ks) {
-    wo[ks] = *reinterpret_cast<const bf16x8*>(Wo + (size_t)(16 * w + (l & 15)) * C + 32 * ks + 8 * (l >> 4));
-    wg[ks] = *reinterpret_cast<const bf16x8*>(Wog + (size_t)(16 * w + (l & 15)) * C + 32 * ks + 8 * (l >> 4));
+  for (int ks = 0; ks < C / 16; ++ks) {
+    const size_t r = (size_t)(32 * cw + (l & 31)) * C + 16 * ks + 8 * (l >> 5);
+    wo[ks] = *reinterpret_cast<const bf16x8*>(Wo + r);
+    wg[ks] = *reinterpret_cast<const bf16x8*>(Wog + r);
   }
   const int chunk = l % LPR;
   float liw[VEC], lib[VEC];
@@ -828,40 +847,46 @@ __global__ __launch_bounds__(OutputWs::NT) void trimul_output_ws_kernel(
     liw[e] = lniw[chunk * VEC + e];
     lib[e] = lnib[chunk * VEC + e];
   }
-  // LN_out: thread (position p = tid / 8, part s = tid % 8) normalises channels 16 s .. +16.
+  // LN_out: thread (position op = tid / 8, part os = tid % 8) normalises the channel pairs
+  // 16 k + 2 os + {0, 1}, k = 0..7: the 64 lanes of one read instruction touch 32 distinct
+  // dwords in 32 distinct banks (rows 2 os + 16 k, positions op).
   const int op = tid >> 3, os = tid & 7;
+  auto och = [&](int c) { return 16 * (c >> 1) + 2 * os + (c & 1); };
   float low[16], lob[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
-    low[c] = lnow[16 * os + c];
-    lob[c] = lnob[16 * os + c];
+    low[c] = lnow[och(c)];
+    lob[c] = lnob[och(c)];
   }
+  // Per-lane load offsets (elements): z rows of this lane, X rows (tid >> 3) + 64 q.
+  int zoff[NLD];
+#pragma unroll
+  for (int q = 0; q < NLD; ++q) zoff[q] = (w * RPW + q * RPI + l / LPR) * C + chunk * VEC;
+  const int xoff = (tid >> 3) * pe + 8 * (tid & 7);
 
-  auto tile_coords = [&](long tile, int& b, int& i, int& j0) {
-    b = (int)(tile / ((long)N * tpr));
-    const long rem = tile % ((long)N * tpr);
-    i = (int)(rem / tpr);
-    j0 = (int)(rem % tpr) * BP;
+  auto tile_coords = [&](int tile, int& b, int& i, int& j0) {
+    b = tile / (N * tpr);
+    const int rem = tile - b * (N * tpr);
+    i = rem / tpr;
+    j0 = (rem - i * tpr) * BP;
   };
   u32x4 zr[NLD], xr[XLDS];
-  auto issue = [&](long tile) {
+  auto issue = [&](int tile) {
     int b, i, j0;
     tile_coords(tile, b, i, j0);
-    const TZ* zb = z + ((size_t)b * N + i) * N * C;
+    const TZ* zb = z + (((size_t)b * N + i) * N + j0) * C;
 #pragma unroll
     for (int q = 0; q < NLD; ++q) {
       const int j = j0 + w * RPW + q * RPI + l / LPR;
-      zr[q] = j < N ? *reinterpret_cast<const u32x4*>(zb + (size_t)j * C + chunk * VEC) : u32x4{0u, 0u, 0u, 0u};
+      zr[q] = j < N ? *reinterpret_cast<const u32x4*>(zb + zoff[q]) : u32x4{0u, 0u, 0u, 0u};
     }
     const bf16* Xb = X + (size_t)b * C * pe + (size_t)i * Np + j0;
 #pragma unroll
-    for (int q = 0; q < XLDS; ++q) {
-      const int c = (tid >> 3) + q * (NT / 8);
-      xr[q] = *reinterpret_cast<const u32x4*>(Xb + (size_t)c * pe + 8 * (tid & 7));
-    }
+    for (int q = 0; q < XLDS; ++q)
+      xr[q] = *reinterpret_cast<const u32x4*>(Xb + (size_t)q * (NT / 8) * pe + xoff);
   };
 
-  long tile = blockIdx.x;
+  int tile = blockIdx.x;
   if (tile < ntiles) issue(tile);
   for (; tile < ntiles; tile += gridDim.x) {
     int b, i, j0;
@@ -879,20 +904,20 @@ __global__ __launch_bounds__(OutputWs::NT) void trimul_output_ws_kernel(
       float sum = 0.f;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) sum += zv[q][e];
-      const float mean = group_sum<LPR>(sum) * (1.0f / C);
+      const float mean = row_group_sum<LPR>(sum) * (1.0f / C);
       float sq = 0.f;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const float d = zv[q][e] - mean;
         sq += d * d;
       }
-      const float rstd = rsqrtf(group_sum<LPR>(sq) * (1.0f / C) + eps_in);
+      const float rstd = rsqrtf(row_group_sum<LPR>(sq) * (1.0f / C) + eps_in);
       float y[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) y[e] = (zv[q][e] - mean) * rstd * liw[e] + lib[e];
       store_vec<bf16, VEC>(xb + (w * RPW + q * RPI + l / LPR) * XLD + chunk * VEC, y);
     }
-    const long next = tile + gridDim.x;
+    const int next = tile + gridDim.x;
     if (next < ntiles) issue(next);
     __syncthreads();  // xt complete
     {
@@ -900,45 +925,43 @@ __global__ __launch_bounds__(OutputWs::NT) void trimul_output_ws_kernel(
       float sum = 0.f;
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
-        v[c] = (float)xt[(16 * os + c) * TLD + op];
+        v[c] = (float)xt[och(c) * TLD + op];
         sum += v[c];
       }
-      const float mean = group_sum<8>(sum) * (1.0f / C);
+      const float mean = dpp_sum8(sum) * (1.0f / C);
       float sq = 0.f;
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
         const float d = v[c] - mean;
         sq += d * d;
       }
-      const float rstd = rsqrtf(group_sum<8>(sq) * (1.0f / C) + eps_out);
+      const float rstd = rsqrtf(dpp_sum8(sq) * (1.0f / C) + eps_out);
 #pragma unroll
       for (int c = 0; c < 16; ++c) v[c] = (v[c] - mean) * rstd * low[c] + lob[c];
-      store_vec<bf16, 8>(xa + op * XLD + 16 * os, v);
-      store_vec<bf16, 8>(xa + op * XLD + 16 * os + 8, v + 8);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) store_vec<bf16, 2>(xa + op * XLD + och(2 * k), v + 2 * k);
     }
     __syncthreads();  // xa, xb complete
 
-    f32x4 ao[4], ag[4];  // [position tile of 16]
+    f32x16 ao, ag;
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) ao[pt] = ag[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < 16; ++r) ao[r] = ag[r] = 0.f;
+    const int brow = (32 * pw + (l & 31)) * XLD + 8 * (l >> 5);
 #pragma unroll
-    for (int ks = 0; ks < C / 32; ++ks)
+    for (int ks = 0; ks < C / 16; ++ks) {
+      const bf16x8 fa = *reinterpret_cast<const bf16x8*>(xa + brow + 16 * ks);
+      const bf16x8 fb = *reinterpret_cast<const bf16x8*>(xb + brow + 16 * ks);
+      ao = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wo[ks], fa, ao, 0, 0, 0);
+      ag = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wg[ks], fb, ag, 0, 0, 0);
+    }
+    // update = sigmoid(gate) * out: lane holds channels 32 cw + acc32_row(r) of position
+    // 32 pw + (l & 31).
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt) {
-        const int r = (16 * pt + (l & 15)) * XLD + 32 * ks + 8 * (l >> 4);
-        const bf16x8 fa = *reinterpret_cast<const bf16x8*>(xa + r);
-        const bf16x8 fb = *reinterpret_cast<const bf16x8*>(xb + r);
-        ao[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wo[ks], fa, ao[pt], 0, 0, 0);
-        ag[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wg[ks], fb, ag[pt], 0, 0, 0);
-      }
-    // update = sigmoid(gate) * out: lane holds channels 16 w + 4 (l >> 4) + e of position
-    // 16 pt + (l & 15).
-#pragma unroll
-    for (int pt = 0; pt < 4; ++pt) {
+    for (int g4 = 0; g4 < 4; ++g4) {
       f32x4 u;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) u[e] = sigmoidf_(ag[pt][e]) * ao[pt][e];
-      *reinterpret_cast<f32x4*>(upd + (16 * pt + (l & 15)) * SLD + 16 * w + 4 * (l >> 4)) = u;
+      for (int e = 0; e < 4; ++e) u[e] = sigmoidf_(ag[4 * g4 + e]) * ao[4 * g4 + e];
+      *reinterpret_cast<f32x4*>(upd + (32 * pw + (l & 31)) * SLD + 32 * cw + acc32_row(4 * g4)) = u;
     }
     __syncthreads();  // update tile complete
     TZ* ob = out + ((size_t)b * N + i) * N * C;
@@ -1192,6 +1215,8 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     pf::KernelTimer timer_trimul_output("trimul_output", s);
     if constexpr (k32) {
       const long ntiles = (long)B * N * ((N + OutputWs::BP - 1) / OutputWs::BP);
+      PF_REQUIRE(ntiles < (1L << 31) && (long)Np * Np * OutputWs::C < (1L << 31), PF_ERR_UNSUPPORTED,
+                 "trimul_output: N=%d B=%d (B N ceil(N/64) and 128 Np^2 must stay below 2^31)", N, B);
       const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
       trimul_output_ws_kernel<TZ><<<nblk, OutputWs::NT, 0, s>>>((const bf16*)X, (const TZ*)z, (TZ*)out, lniw, lnib,
                                                                 eps_in, lnow, lnob, eps_out, (const bf16*)wo,
