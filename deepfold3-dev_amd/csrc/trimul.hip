@@ -607,18 +607,22 @@ __global__ __launch_bounds__(256) void trimul_project32_kernel(const TZ* __restr
 // K1, persistent and weight-stationary (bf16 GEMMs). One 512-thread block per CU walks
 // tiles of 64 positions along a line. Wave w owns plane w >> 2 (a | b) and channels
 // 32 (w & 3) .. +32: its proj and gate weight rows (2 x 32 rows x 128 k, packed as above)
-// stay in MFMA A-operand registers for the whole kernel, so weights are read once per CU
-// instead of once per tile. Per tile: each wave LayerNorms 8 z rows into a double-buffered
-// LDS tile (the next tile's rows are loaded while this tile's MFMAs run); every wave then
-// computes acc^T[channel][position] for proj and gate (the same elements), gates in
-// registers, stages its 32 x 64 result channel-major in a private LDS region and writes
-// 128-byte plane rows.
+// stay in MFMA operand registers for the whole kernel, so weights are read once per CU
+// instead of once per tile. Every wave computes acc[position][channel] for proj and gate of
+// the current tile (the same elements), gates and masks in registers -- a lane holds four
+// consecutive positions of one channel -- stages its 32 x 64 result channel-major in a
+// private LDS region with 8-byte stores and writes 128-byte plane rows.
+// The two waves that share a SIMD (w, w + 4) work out of phase: waves 4-7 first LayerNorm
+// the NEXT tile (16 rows each, from z rows they loaded two tiles ahead) into the other half
+// of a double-buffered LDS tile, then run their GEMMs, while waves 0-3 start on their GEMMs
+// at once; the MFMAs of one wave thus overlap the LayerNorm and gating VALU work of the
+// other. One barrier per tile publishes the next tile's LayerNorm.
 struct ProjectWs {
   static constexpr int C = 128;
   static constexpr int BP = 64;   // positions per tile
   static constexpr int NW = 8;    // waves per block
   static constexpr int NT = 64 * NW;
-  static constexpr int XLD = C + 8;   // 272-byte rows: conflict-free 16-byte B-operand reads
+  static constexpr int XLD = C + 8;   // 272-byte rows: conflict-free 16-byte operand reads
   static constexpr int SLD = BP + 8;  // stage rows (bf16)
 };
 
@@ -628,25 +632,27 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
     const float* __restrict__ lnb, float eps, const bf16* __restrict__ w4, bf16* __restrict__ planes, int B, int N,
     int Np, int outgoing) {
   using Cfg = ProjectWs;
-  constexpr int C = Cfg::C, BP = Cfg::BP, NW = Cfg::NW, XLD = Cfg::XLD, SLD = Cfg::SLD;
+  constexpr int C = Cfg::C, BP = Cfg::BP, XLD = Cfg::XLD, SLD = Cfg::SLD;
   constexpr int VEC = 16 / sizeof(TZ);  // z elements per 16-byte load
   constexpr int LPR = C / VEC;          // lanes per z row
   constexpr int RPI = 64 / LPR;         // rows per wave-wide load
-  constexpr int RPW = BP / NW;          // z rows each wave normalises per tile
+  constexpr int RPW = BP / 4;           // z rows each LayerNorm wave (4..7) normalises per tile
   constexpr int NLD = RPW / RPI;        // 16-byte loads per lane per tile
   __shared__ __attribute__((aligned(16))) bf16 xs[2][BP * XLD];
-  __shared__ __attribute__((aligned(16))) bf16 stage_all[NW][32 * SLD];
+  __shared__ __attribute__((aligned(16))) float mks[2][BP];
+  __shared__ __attribute__((aligned(16))) bf16 stage_all[Cfg::NW][32 * SLD];
 
   const int w = wave_id();
   const int l = lane_id();
-  const int pl = w >> 2;  // 0: a (P), 1: b (Q)
-  const int cj = w & 3;   // 32-channel chunk
+  const int pl = w >> 2;  // 0: a (P), 1: b (Q); also 1 = the LayerNorm group
+  const int cj = w & 3;   // 32-channel chunk; also the LayerNorm wave's row block
   bf16* stg = stage_all[w];
   const int tpl = Np / BP;
-  const long ntiles = (long)B * Np * tpl;
+  const int ntiles = B * Np * tpl;  // < 2^31 (checked at launch)
+  const int G = gridDim.x;
   const size_t pe = (size_t)Np * Np;
 
-  // Weights -> A operands: lane l holds row l & 31, k = 16 ks + 8 (l >> 5) + e.
+  // Weights -> B operands: lane l holds column (channel) l & 31, k = 16 ks + 8 (l >> 5) + e.
   bf16x8 wp[C / 16], wg[C / 16];
   {
     const bf16* rp = w4 + (size_t)(128 * cj + 32 * (2 * pl) + (l & 31)) * C + 8 * (l >> 5);
@@ -666,71 +672,72 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
     lb[e] = lnb[chunk * VEC + e];
   }
 
-  auto tile_coords = [&](long tile, int& b, int& line, int& t0) {
-    b = (int)(tile / ((long)Np * tpl));
-    const long rem = tile % ((long)Np * tpl);
-    line = (int)(rem / tpl);
-    t0 = (int)(rem % tpl) * BP;
+  auto tile_coords = [&](int tile, int& b, int& line, int& t0) {
+    b = tile / (Np * tpl);
+    const int rem = tile - b * (Np * tpl);
+    line = rem / tpl;
+    t0 = (rem - line * tpl) * BP;
   };
-  // Next tile's z rows (this wave's 8) and this lane's mask values, in registers.
-  u32x4 zr[NLD];
-  float mkn[2];
-  auto issue = [&](long tile) {
+  // LayerNorm group: z rows and mask values of two tiles ahead, in two register sets. The
+  // loads are unconditional (a padding row reads a clamped real row; its mask becomes 0 when
+  // it is used), so the compiler's wait counts stay exact and the second set stays in flight.
+  u32x4 zr[2][NLD];
+  float mkn[2][NLD];
+  unsigned okb[2];
+  auto issue = [&](int tile, int set) __attribute__((always_inline)) {
     int b, line, t0;
     tile_coords(tile, b, line, t0);
     const TZ* zb = z + (size_t)b * N * N * C;
+    const float* mb = mask + (size_t)b * N * N;
+    const int lc = min(line, N - 1);
+    unsigned ok = 0;
 #pragma unroll
     for (int q = 0; q < NLD; ++q) {
-      const int row = w * RPW + q * RPI + l / LPR;
-      const int t = t0 + row;
-      if (line < N && t < N) {
-        const size_t pos = outgoing ? (size_t)line * N + t : (size_t)t * N + line;
-        zr[q] = *reinterpret_cast<const u32x4*>(zb + pos * C + chunk * VEC);
-      } else {
-        zr[q] = u32x4{0u, 0u, 0u, 0u};
-      }
+      const int t = t0 + cj * RPW + q * RPI + l / LPR;
+      ok |= (line < N && t < N) ? 1u << q : 0u;
+      const int tc = min(t, N - 1);
+      const size_t pos = outgoing ? (size_t)lc * N + tc : (size_t)tc * N + lc;
+      zr[set][q] = *reinterpret_cast<const u32x4*>(zb + pos * C + chunk * VEC);
+      mkn[set][q] = mb[pos];
     }
-#pragma unroll
-    for (int pt = 0; pt < 2; ++pt) {
-      const int t = t0 + 32 * pt + (l & 31);
-      const size_t pos = outgoing ? (size_t)line * N + t : (size_t)t * N + line;
-      mkn[pt] = (line < N && t < N) ? mask[(size_t)b * N * N + pos] : 0.f;
-    }
+    okb[set] = ok;
   };
-
-  long tile = blockIdx.x;
-  if (tile < ntiles) issue(tile);
-  int buf = 0;
-  for (; tile < ntiles; tile += gridDim.x, buf ^= 1) {
-    int b, line, t0;
-    tile_coords(tile, b, line, t0);
-    // LayerNorm of this wave's rows (fp32 two-pass statistics) -> xs[buf] in bf16.
-    bf16* xb = xs[buf];
+  // LayerNorm (fp32 two-pass statistics) of this wave's rows of a tile -> xs[buf] in bf16.
+  auto layer_norm = [&](int set, int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < NLD; ++q) {
       float v[VEC];
-      unpack16<TZ>(zr[q], v);
+      unpack16<TZ>(zr[set][q], v);
       float sum = 0.f;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) sum += v[e];
-      const float mean = group_sum<LPR>(sum) * (1.0f / C);
+      const float mean = row_group_sum<LPR>(sum) * (1.0f / C);
       float sq = 0.f;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const float d = v[e] - mean;
         sq += d * d;
       }
-      const float rstd = rsqrtf(group_sum<LPR>(sq) * (1.0f / C) + eps);
+      const float rstd = rsqrtf(row_group_sum<LPR>(sq) * (1.0f / C) + eps);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) v[e] = (v[e] - mean) * rstd * lw[e] + lb[e];
-      const int row = w * RPW + q * RPI + l / LPR;
-      store_vec<bf16, VEC>(xb + row * XLD + chunk * VEC, v);
+      const int row = cj * RPW + q * RPI + l / LPR;
+      store_vec<bf16, VEC>(xs[buf] + row * XLD + chunk * VEC, v);
+      if (chunk == 0) mks[buf][row] = (okb[set] >> q) & 1u ? mkn[set][q] : 0.f;
     }
-    const float mk[2] = {mkn[0], mkn[1]};
-    const long next = tile + gridDim.x;
-    if (next < ntiles) issue(next);
-    __syncthreads();  // xs[buf] holds the whole tile
-
+  };
+  // LayerNorm group, step for tile `tile`: normalise the next tile (register set `set`) into
+  // xs[buf] and refill the set with the tile after the one already in flight.
+  // Every issue is unconditional (a tile past the end reloads the last tile, unused), so all
+  // paths through the loop carry the same load counts.
+  auto prepare_next = [&](int tile, int set, int buf) __attribute__((always_inline)) {
+    if (tile + G < ntiles) layer_norm(set, buf);
+    issue(min(tile + 3 * G, ntiles - 1), set);
+  };
+  auto compute = [&](int tile, int buf) __attribute__((always_inline)) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
+    const bf16* xb = xs[buf];
     f32x16 acc[2][2];  // [proj | gate][position tile]
     zero_acc32(acc);
 #pragma unroll
@@ -741,17 +748,22 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
         xf[pt] = *reinterpret_cast<const bf16x8*>(xb + (32 * pt + (l & 31)) * XLD + 16 * ks + 8 * (l >> 5));
 #pragma unroll
       for (int pt = 0; pt < 2; ++pt) {
-        acc[0][pt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wp[ks], xf[pt], acc[0][pt], 0, 0, 0);
-        acc[1][pt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wg[ks], xf[pt], acc[1][pt], 0, 0, 0);
+        acc[0][pt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[pt], wp[ks], acc[0][pt], 0, 0, 0);
+        acc[1][pt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[pt], wg[ks], acc[1][pt], 0, 0, 0);
       }
     }
-    // Gate, mask, stage channel-major: lane (position p) holds channels acc32_row(e).
+    // Gate, mask, stage channel-major: lane (channel l & 31) holds positions
+    // 32 pt + acc32_row(4 g + e), four consecutive per g.
 #pragma unroll
     for (int pt = 0; pt < 2; ++pt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float v = sigmoidf_(acc[1][pt][e]) * acc[0][pt][e] * mk[pt];
-        stg[acc32_row(e) * SLD + 32 * pt + (l & 31)] = (bf16)v;
+      for (int g = 0; g < 4; ++g) {
+        const int p0 = 32 * pt + acc32_row(4 * g);
+        const f32x4 m4 = *reinterpret_cast<const f32x4*>(&mks[buf][p0]);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = sigmoidf_(acc[1][pt][4 * g + e]) * acc[0][pt][4 * g + e] * m4[e];
+        store_vec<bf16, 4>(stg + (l & 31) * SLD + p0, v);
       }
     // The stage is private to this wave: LDS operations of one wave complete in order.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -766,6 +778,30 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
           *reinterpret_cast<const u32x4*>(stg + row * SLD + 8 * c8);
     }
     __builtin_amdgcn_wave_barrier();
+  };
+
+  // Prologue: the LayerNorm group loads two tiles and normalises the first. The loop runs
+  // two tiles per trip so the register sets and LDS halves are compile-time indices; all
+  // barrier conditions are block-uniform. The weights and LayerNorm parameters are waited
+  // for here, once: the two wave groups take different load paths into the loop, and
+  // without this the compiler waits on every load in flight wherever it first reads them.
+  __builtin_amdgcn_s_waitcnt(0);
+  int tile = blockIdx.x;
+  if (pl == 1) {
+    issue(min(tile, ntiles - 1), 0);
+    issue(min(tile + G, ntiles - 1), 1);
+    if (tile < ntiles) layer_norm(0, 0);
+    issue(min(tile + 2 * G, ntiles - 1), 0);
+  }
+  __syncthreads();
+  for (; tile < ntiles; tile += 2 * G) {
+    if (pl == 1) prepare_next(tile, 1, 1);
+    compute(tile, 0);
+    __syncthreads();  // xs[1] holds tile + G; every wave is done with xs[0]
+    if (tile + G >= ntiles) break;
+    if (pl == 1) prepare_next(tile + G, 0, 0);
+    compute(tile + G, 1);
+    __syncthreads();  // xs[0] holds tile + 2 G; every wave is done with xs[1]
   }
 }
 
@@ -1154,6 +1190,8 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     pf::KernelTimer timer_trimul_project("trimul_project", s);
     if constexpr (k32) {
       const long ntiles = (long)B * Np * (Np / ProjectWs::BP);
+      PF_REQUIRE(ntiles < (1L << 31), PF_ERR_UNSUPPORTED, "trimul_project: B=%d N=%d (B Np Np/64 must stay below 2^31)",
+                 B, N);
       const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
       trimul_project_ws_kernel<TZ><<<nblk, ProjectWs::NT, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in,
                                                                   (const bf16*)w4, (bf16*)planes, B, N, Np,
