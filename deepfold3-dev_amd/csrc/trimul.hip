@@ -380,6 +380,150 @@ __global__ __launch_bounds__(512) void trimul_contract256_kernel(const bf16* __r
   }
 }
 
+// bf16 contraction on 256 (i) x 384 (j) tiles, used when Np is a multiple of 768 (then
+// B C (Np / 256) (Np / 384) blocks fill the CUs in whole rounds -- at N = 768, three -- and
+// each operand row block is read twice (P) or three times (Q) instead of three times each).
+// Eight waves in 2 x 4, each owning a 128 (i) x 96 (j) block as 4 x 3 tiles of
+// v_mfma_f32_32x32x16_bf16 (192 fp32 accumulators per lane): per k-step 7 fragment reads
+// feed 12 MFMAs. k-tiles of 64 (whole 128-byte lines per row) flow through two LDS stages
+// of 80 KiB -- the whole 160 KiB of a CU -- filled by global_load_lds_dwordx4 one tile
+// ahead, one barrier per tile, with the same 16-byte chunk swizzle as the 256 x 256 kernel.
+// The output tile leaves through the first stage in two passes of 128 rows i.
+struct Contract768 {
+  static constexpr int BI = 256;
+  static constexpr int BJ = 384;
+  static constexpr int KT = 64;
+  static constexpr int NT = 512;
+  static constexpr int PT = BI * KT;                 // elements of the P k-tile
+  static constexpr int STAGE = (BI + BJ) * KT;       // P tile then Q tile
+  static constexpr int BLKS = (BI + BJ) / 8;         // 1 KiB direct-load blocks per stage (80)
+  static constexpr int DMA = BLKS / (NT / 64);       // per wave (10)
+  static constexpr int OLD = BJ + 8;                 // output staging rows (bf16): 784 bytes
+  static constexpr int OROWS = 128;                  // output rows per staging pass
+  static constexpr int SMEM = 2 * STAGE * 2;         // 163840 bytes
+  static_assert(OROWS * OLD * 2 <= SMEM, "output pass fits the ring");
+};
+
+__global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __restrict__ P, const bf16* __restrict__ Q,
+                                                                 bf16* __restrict__ X, int G, int Np, int xcd_remap) {
+  using Cfg = Contract768;
+  constexpr int BI = Cfg::BI, BJ = Cfg::BJ, KT = Cfg::KT, DMA = Cfg::DMA;
+  static_assert(DMA * (Cfg::NT / 64) == Cfg::BLKS, "a stage splits evenly over the waves");
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  bf16* lds = reinterpret_cast<bf16*>(smem);
+
+  const int ti = Np / BI, tj = Np / BJ;
+  const int tiles = ti * tj;
+  int bid = blockIdx.x;
+  int g, tile;
+  if (xcd_remap) {  // XCD x walks planes x, x+8, ...: a plane's operands stay in one L2
+    const int xcd = bid & 7;
+    const int u = bid >> 3;
+    g = xcd + 8 * (u / tiles);
+    tile = u % tiles;
+  } else {
+    g = bid / tiles;
+    tile = bid % tiles;
+  }
+  if (g >= G) return;
+  const int i0 = (tile / tj) * BI;
+  const int j0 = (tile % tj) * BJ;
+  const size_t pe = (size_t)Np * Np;
+  const bf16* Pg = P + (size_t)g * pe + (size_t)i0 * Np;
+  const bf16* Qg = Q + (size_t)g * pe + (size_t)j0 * Np;
+
+  const int w = wave_id();
+  const int l = lane_id();
+  const int wi = (w >> 2) * 128;  // wave's rows i in the tile
+  const int wj = (w & 3) * 96;    // wave's columns j
+
+  // Direct loads: a stage is 80 blocks of 8 rows (P blocks 0..31, Q blocks 32..79); wave w
+  // loads blocks DMA w .. DMA w + DMA - 1. Lane l writes row 8 blk + l / 8 at physical
+  // chunk l % 8, i.e. logical chunk (l % 8) ^ swz(row). 32-bit per-lane offsets from a scalar
+  // base per operand (raw buffer loads).
+  const auto rsP = buf_rsrc(Pg, (unsigned)(BI * Np * 2));
+  const auto rsQ = buf_rsrc(Qg, (unsigned)(BJ * Np * 2));
+  int voff[DMA];
+#pragma unroll
+  for (int q = 0; q < DMA; ++q) {
+    const int blk = DMA * w + q;
+    const int row = (blk < BI / 8 ? blk : blk - BI / 8) * 8 + (l >> 3);
+    voff[q] = (row * Np + 8 * ((l & 7) ^ k2_swz(row))) * 2;
+  }
+  auto issue = [&](int kt) {
+    bf16* st = lds + (kt & 1) * Cfg::STAGE;
+#pragma unroll
+    for (int q = 0; q < DMA; ++q) {
+      const int blk = DMA * w + q;  // compile-time split per wave is not possible: w is uniform
+      buf_load_lds16(blk < BI / 8 ? rsP : rsQ, st + blk * 8 * KT, voff[q], kt * KT * 2);
+    }
+  };
+
+  f32x16 acc[3][4];  // [j tile][i tile]
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+  const int nk = Np / KT;
+  const int r = l & 31;
+  const int hf = l >> 5;
+  const int sw = k2_swz(r);  // rows wi + 32 t + r and wj + 32 t + r share the swizzle of r
+  issue(0);
+  for (int kt = 0; kt < nk; ++kt) {
+    // s_waitcnt vmcnt(0) (other counters untouched): this wave's loads of tile kt landed.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    // All waves' loads of tile kt visible; stage (kt + 1) & 1 no longer read.
+    __builtin_amdgcn_s_barrier();
+    if (kt + 1 < nk) issue(kt + 1);
+    const bf16* Ps = lds + (kt & 1) * Cfg::STAGE;
+    const bf16* Qs = Ps + Cfg::PT;
+#pragma unroll
+    for (int kk = 0; kk < KT; kk += 16) {
+      const int c8 = 8 * ((kk / 8 + hf) ^ sw);
+      bf16x8 af[3], bfr[4];
+#pragma unroll
+      for (int t = 0; t < 3; ++t) af[t] = *reinterpret_cast<const bf16x8*>(Qs + (wj + 32 * t + r) * KT + c8);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) bfr[t] = *reinterpret_cast<const bf16x8*>(Ps + (wi + 32 * t + r) * KT + c8);
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+          acc[a][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[cc], acc[a][cc], 0, 0, 0);
+    }
+  }
+
+  // acc[a][c] element e: j = wj + 32 a + acc32_row(e), i = wi + 32 c + (lane & 31). Two passes
+  // of 128 rows i through LDS ([i][j], 784-byte rows), stored as whole 768-byte rows.
+  bf16* Xg = X + (size_t)g * pe + (size_t)i0 * Np + j0;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int pass = 0; pass < BI / Cfg::OROWS; ++pass) {
+    __syncthreads();  // the ring (or the previous pass's stage) is no longer read
+    if (wi == pass * Cfg::OROWS) {
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            float v[4] = {acc[a][cc][4 * g4], acc[a][cc][4 * g4 + 1], acc[a][cc][4 * g4 + 2], acc[a][cc][4 * g4 + 3]};
+            store_vec<bf16, 4>(lds + (32 * cc + r) * Cfg::OLD + wj + 32 * a + acc32_row(4 * g4), v);
+          }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < Cfg::OROWS * BJ / 8 / Cfg::NT; ++it) {
+      const int idx = tid + it * Cfg::NT;
+      const int row = idx / (BJ / 8), ch = idx % (BJ / 8);
+      *reinterpret_cast<u32x4*>(Xg + (size_t)(pass * Cfg::OROWS + row) * Np + 8 * ch) =
+          *reinterpret_cast<const u32x4*>(lds + row * Cfg::OLD + 8 * ch);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ K3
 template <class TZ, class TC, int C>
 struct OutputCfg {
@@ -1218,7 +1362,23 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     const int remap = (G % 8 == 0) ? 1 : 0;
     bool done = false;
     if constexpr (sizeof(TC) == 2) {
-      if (Np % Contract256::BT == 0) {
+      if (Np % (Contract768::BI * 3) == 0) {
+        static bool attr768 = false;
+        if (!attr768) {
+          hipError_t e = hipFuncSetAttribute((const void*)trimul_contract768_kernel,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, Contract768::SMEM);
+          PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "trimul_contract: cannot reserve %d bytes of LDS: %s",
+                     Contract768::SMEM, hipGetErrorString(e));
+          attr768 = true;
+        }
+        dim3 grid((unsigned)(G * (Np / Contract768::BI) * (Np / Contract768::BJ)));
+        pf::KernelTimer timer_trimul_contract("trimul_contract", s);
+        trimul_contract768_kernel<<<grid, Contract768::NT, Contract768::SMEM, s>>>((const bf16*)P, (const bf16*)Q,
+                                                                                   (bf16*)X, G, Np, remap);
+        timer_trimul_contract.stop();
+        if (int e = pf::check_launch("trimul_contract")) return e;
+        done = true;
+      } else if (Np % Contract256::BT == 0) {
         static bool attr256 = false;
         if (!attr256) {
           hipError_t e = hipFuncSetAttribute((const void*)trimul_contract256_kernel,
