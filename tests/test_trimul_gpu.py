@@ -41,7 +41,8 @@ def test_trimul_fp32_matches_oracle(dev, outgoing, n, pad):
 
 
 @pytest.mark.parametrize("outgoing", [True, False])
-@pytest.mark.parametrize("n", [96, 200, 500])  # padded 128 / 256 / 512: both contraction tilings
+# padded 128 / 256 / 512 / 768: every contraction tiling (generic, 256 x 256, 256 x 384)
+@pytest.mark.parametrize("n", [96, 200, 500, 700])
 def test_trimul_bf16_tolerance_rule(dev, outgoing, n):
     sd = W.make_block_weights(12, perturb_affine=True)
     p = sub(sd, "tri_mul_out." if outgoing else "tri_mul_in.")
