@@ -321,6 +321,14 @@ constexpr size_t tr_ws_lds_bytes() {
          4 * TransWs::C * sizeof(float);
 }
 
+// v_permlane32_swap: lanes 32..63 of a trade values with lanes 0..31 of b. Written as inline
+// assembly with both operands read-write: the compiler builtin returned wrong lanes once
+// unrolled (both registers are rewritten, which its lowering did not model). The s_nop
+// covers the VALU-write -> cross-lane-read hazard the compiler cannot see through asm.
+PF_DEVICE void permlane32_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
 // Byte offset of 16-byte chunk c of row r in an LDS tile of `row_bytes` rows whose chunks are
 // XOR-swizzled by (row & 7).
 PF_DEVICE int swz_off(int r, int c, int row_bytes) { return r * row_bytes + 16 * (c ^ (r & 7)); }
@@ -393,17 +401,13 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
     }
   }
   if (S2P && w == 0) {
-    // k-step ks = 2 o + mm takes channels 32 o + 8 (2 mm + t) + 4 hf + e at element 4 t + e
-    // (the y^T accumulator order); rows >= 16 are zero.
+    // k-step ks takes channels 16 ks + 8 hf + e (the epilogue's lane-pair-swapped order);
+    // rows >= 16 are zero.
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       bf16x8 a;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          a[4 * t + e] = lq < kS2pHeads ? Ws2p[lq * C + 32 * (ks >> 1) + 8 * (2 * (ks & 1) + t) + 4 * hf + e]
-                                        : (bf16)0.f;
+      for (int e = 0; e < 8; ++e) a[e] = lq < kS2pHeads ? Ws2p[lq * C + 16 * ks + 8 * hf + e] : (bf16)0.f;
       *reinterpret_cast<bf16x8*>(s2pa + (ks * 64 + l) * 16) = a;
     }
   }
@@ -442,6 +446,7 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
 
   for (; tile < ntiles; tile += gridDim.x) {
     const long m = tile * BP + w * PW + lq;  // this lane's position
+    const long tb0 = S2P ? (tile * BP) / NN : 0, tp0 = S2P ? tile * BP - tb0 * NN : 0;
 
     // ---- LN(x) -> B operands xf[ks]: lane (position lq, half hf) holds channels
     // 16 ks + 8 hf .. +7.
@@ -535,22 +540,34 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
     // operands, all issued before any of them is used.
     if (tile + gridDim.x < ntiles) zr.load(x, (tile + gridDim.x) * BP + w * PW + lq, M, hf);
     // Lane (position lq, half hf) holds channels 32 o + 8 gq + 4 hf + e of y[o][4 gq + e].
+    // Swapping the (gq = 2 p, gq = 2 p + 1) registers between lanes l and l + 32 leaves lane
+    // hf with channels 32 o + 16 p + 8 hf + e, e = 0..7, in v[o][8 p + e]: 16-byte row
+    // accesses, and the natural k order for the single_to_pair MFMAs.
+    float v[4][16];
+#pragma unroll
+    for (int o = 0; o < 4; ++o)
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float a = y[o][8 * pp + e], b = y[o][8 * pp + 4 + e];
+          permlane32_swap(a, b);
+          v[o][8 * pp + e] = a;
+          v[o][8 * pp + 4 + e] = b;
+        }
     float res[4][16];
     if (accumulate && m < M) {
       const TZ* row = out + m * C;
 #pragma unroll
       for (int o = 0; o < 4; ++o)
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int ch = 32 * o + 8 * gq + 4 * hf;
+        for (int pp = 0; pp < 2; ++pp) {
+          const TZ* src = row + 32 * o + 16 * pp + 8 * hf;
           if constexpr (sizeof(TZ) == 2) {
-            const bf16x4 t = *reinterpret_cast<const bf16x4*>(row + ch);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) res[o][4 * gq + e] = (float)t[e];
+            load16<bf16>(src, *reinterpret_cast<float(*)[8]>(&res[o][8 * pp]));
           } else {
-            const f32x4 t = *reinterpret_cast<const f32x4*>(row + ch);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) res[o][4 * gq + e] = t[e];
+            load16<float>(src, *reinterpret_cast<float(*)[4]>(&res[o][8 * pp]));
+            load16<float>(src + 4, *reinterpret_cast<float(*)[4]>(&res[o][8 * pp + 4]));
           }
         }
     } else {
@@ -564,25 +581,27 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
 #pragma unroll
       for (int o = 0; o < 4; ++o)
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          float v[4];
+        for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            v[e] = to_f32(from_f32<TZ>(res[o][4 * gq + e] + y[o][4 * gq + e]));
-            y[o][4 * gq + e] = v[e];  // the updated row as stored (single_to_pair input)
+          for (int e = 0; e < 8; ++e)
+            v[o][8 * pp + e] = to_f32(from_f32<TZ>(res[o][8 * pp + e] + v[o][8 * pp + e]));  // as stored
+          if constexpr (sizeof(TZ) == 2) {
+            store_vec<bf16, 8>(row + 32 * o + 16 * pp + 8 * hf, &v[o][8 * pp]);
+          } else {
+            store_vec<float, 4>(row + 32 * o + 16 * pp + 8 * hf, &v[o][8 * pp]);
+            store_vec<float, 4>(row + 32 * o + 16 * pp + 8 * hf + 4, &v[o][8 * pp + 4]);
           }
-          store_vec<TZ, 4>(row + 32 * o + 8 * gq + 4 * hf, v);
         }
     }
 
     if constexpr (S2P) {
       // LN' of the updated row, then logits^T = Ws2p LN'^T on 32x32x16 MFMAs (heads 16..31
-      // of the A operand are zero).
+      // of the A operand are zero); k-step ks = 2 o + pp is channels 16 ks + 8 hf + e.
       float s = 0.f;
 #pragma unroll
       for (int o = 0; o < 4; ++o)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s += y[o][e];
+        for (int e = 0; e < 16; ++e) s += v[o][e];
       s += __shfl_xor(s, 32, 64);
       const float mean = s * (1.0f / C);
       float q = 0.f;
@@ -590,7 +609,7 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
       for (int o = 0; o < 4; ++o)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const float d = y[o][e] - mean;
+          const float d = v[o][e] - mean;
           q += d * d;
         }
       q += __shfl_xor(q, 32, 64);
@@ -600,21 +619,23 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
       for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        const int o = ks >> 1, mm = ks & 1;
         bf16x8 bfr;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int ch = 32 * o + 8 * (2 * mm + t) + 4 * hf + e;
-            bfr[4 * t + e] = (bf16)((y[o][4 * (2 * mm + t) + e] - mean) * rstd * lnp[2 * C + ch] + lnp[3 * C + ch]);
-          }
+        for (int e = 0; e < 8; ++e) {
+          const int ch = 16 * ks + 8 * hf + e;
+          bfr[e] = (bf16)((v[ks >> 1][8 * (ks & 1) + e] - mean) * rstd * lnp[2 * C + ch] + lnp[3 * C + ch]);
+        }
         const bf16x8 afr = *reinterpret_cast<const bf16x8*>(s2pa + (ks * 64 + l) * 16);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr, bfr, acc, 0, 0, 0);
       }
       // acc: lane (position, half hf) holds heads 8 gq + 4 hf + e; heads < 16 for gq < 2.
+      // Batch item and in-plane position from the tile's (scalar) start.
       if (m < M) {
-        const long b = m / NN, pos = m % NN;
+        long b = tb0, pos = tp0 + w * PW + lq;
+        while (pos >= NN) {
+          pos -= NN;
+          ++b;
+        }
 #pragma unroll
         for (int gq = 0; gq < 2; ++gq)
 #pragma unroll
