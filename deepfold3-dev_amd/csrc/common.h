@@ -151,6 +151,18 @@ PF_DEVICE float row_group_sum(float v) {
   return v;
 }
 
+// v_permlane32_swap: lanes 32..63 of a trade values with lanes 0..31 of b. Inline assembly
+// with both operands read-write (the compiler builtin returned wrong lanes once unrolled).
+// The compiler cannot see hazards through inline assembly, so the operands first pass
+// through an ordinary VALU add: the compiler gives that add the wait states an MFMA result
+// needs before a VALU read, and the s_nop covers the VALU-write -> cross-lane-read hazard.
+// (x + 0 turns -0 into +0; nothing downstream distinguishes them.)
+PF_DEVICE void permlane32_swap(float& a, float& b) {
+  a += 0.0f;
+  b += 0.0f;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
 PF_DEVICE int lane_id() { return threadIdx.x & 63; }
 // Wave index inside the block, as a wave-uniform (scalar) value.
 PF_DEVICE int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }

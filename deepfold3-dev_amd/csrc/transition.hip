@@ -321,14 +321,6 @@ constexpr size_t tr_ws_lds_bytes() {
          4 * TransWs::C * sizeof(float);
 }
 
-// v_permlane32_swap: lanes 32..63 of a trade values with lanes 0..31 of b. Written as inline
-// assembly with both operands read-write: the compiler builtin returned wrong lanes once
-// unrolled (both registers are rewritten, which its lowering did not model). The s_nop
-// covers the VALU-write -> cross-lane-read hazard the compiler cannot see through asm.
-PF_DEVICE void permlane32_swap(float& a, float& b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-
 // Byte offset of 16-byte chunk c of row r in an LDS tile of `row_bytes` rows whose chunks are
 // XOR-swizzled by (row & 7).
 PF_DEVICE int swz_off(int r, int c, int row_bytes) { return r * row_bytes + 16 * (c ^ (r & 7)); }
