@@ -99,15 +99,29 @@ class PairFormerBlock(nn.Module):
         if self.training:
             raise NotActive("PairFormerBlock", "training-mode dropout is not built (eval only)")
         kernel_census.record("PairFormerBlock", "hip_block")
+        pair_logits = self.pair_forward_(pair, pair_mask)
+        self.single_forward_(single, seq_mask, pair_logits)
+        return pair, single
+
+    def pair_forward_(self, pair: torch.Tensor, pair_mask: torch.Tensor) -> torch.Tensor:
+        """The pair half of the block, in place; returns the single track's pair logits.
+
+        The pair update reads only the pair representation (``evoformer.py:289-321``), so it
+        does not depend on the single half of the block.
+        """
         self.tri_mul_out.forward_residual_(pair, pair_mask)
         self.tri_mul_in.forward_residual_(pair, pair_mask)
         self.pair_attn_row.forward_residual_(pair, pair_mask)
         self.pair_attn_col.forward_residual_(pair, pair_mask)
         s2p = self._s2p_operands(gemm_dtype_for(pair))
         _, pair_logits = self.pair_transition.forward_residual_(pair, s2p=s2p)
+        return pair_logits
+
+    def single_forward_(self, single: torch.Tensor, seq_mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
+        """The single half of the block, in place (``evoformer.py:322-353``)."""
         self.single_attn.forward_residual_(single, seq_mask, pair_logits)
         self.single_transition.forward_residual_(single)
-        return pair, single
+        return single
 
     @inference_only("PairFormerBlock")
     def forward(
@@ -141,8 +155,35 @@ class PairFormerStack(nn.Module):
     def forward(
         self, pair: torch.Tensor, single: torch.Tensor, pair_mask: torch.Tensor, seq_mask: torch.Tensor
     ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Same result as applying the blocks in order. On the GPU the single half of block i
+        runs on a second stream, beside the pair half of block i + 1: the pair update never
+        reads the single representation, and the single half of block i needs only block i's
+        pair logits (an event orders it after them) and block i - 1's single half (same
+        stream). The streams join before returning."""
         pair = pair.contiguous().clone()
         single = single.contiguous().clone()
+        if not pair.is_cuda or len(self.blocks) == 0:
+            for blk in self.blocks:
+                blk.forward_(pair, single, pair_mask, seq_mask)
+            return pair, single
+        main = torch.cuda.current_stream(pair.device)
+        side = self._side_stream(pair.device)
+        side.wait_stream(main)  # single, masks and the clones above
         for blk in self.blocks:
-            blk.forward_(pair, single, pair_mask, seq_mask)
+            kernel_census.record("PairFormerBlock", "hip_block")
+            pair_logits = blk.pair_forward_(pair, pair_mask)
+            done = torch.cuda.Event()
+            done.record(main)
+            side.wait_event(done)
+            with torch.cuda.stream(side):
+                pair_logits.record_stream(side)  # freed on main, still read on side
+                blk.single_forward_(single, seq_mask, pair_logits)
+        main.wait_stream(side)
         return pair, single
+
+    def _side_stream(self, device) -> torch.cuda.Stream:
+        streams = self.__dict__.setdefault("_side_streams", {})
+        key = torch.device(device).index
+        if key not in streams:
+            streams[key] = torch.cuda.Stream(device=device)  # default priority
+        return streams[key]
