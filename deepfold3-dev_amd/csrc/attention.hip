@@ -734,7 +734,9 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   auto logits = [&](int kb, int u, int s, const Frag16<TC>& kf, float mf, f32x16& sacc) {
     const int k0 = kb * 32;
     const float* bl = bias_lds + stage_of(kb, u) * TILE;
-    const bool use_mask = masked || k0 + 32 > N;  // padding keys hold -inf in MA
+    // The mask MFMA only for key blocks that hold a masked (or padding, -inf) key: each
+    // lane holds the mask slot of one key row, so one wave-wide vote decides.
+    const bool use_mask = k0 + 32 > N || (masked && __any(mf != 0.f));
     const float mk = kb < nkb ? mf : -INFINITY;
     const int R = 32 * s + lq;
     const float* br = bl + R * 32;
