@@ -672,12 +672,25 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
           *reinterpret_cast<const u32x4*>(Qh + (size_t)(q0 + qq) * kHeadDim + d0);
     }
   }
+  // Scan of the line's mask slots: 16-byte loads, four per lane in flight before any is
+  // used (a load-then-test loop made one memory round trip per 64 keys). Padding slots
+  // (keys >= N, holding -inf) are skipped by their key index.
   bool masked = false, all_masked = true;
   if (active) {
-    for (int k = l; k < N; k += 64) {
-      const float m = MAl[(k & ~31) + key_slot(k & 31)];
-      masked |= m != 0.f;
-      all_masked &= m < -1e8f;
+    for (int s0 = 4 * l; s0 < Np; s0 += 1024) {
+      f32x4 m4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) m4[j] = *reinterpret_cast<const f32x4*>(MAl + min(s0 + 256 * j, Np - 4));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int sl = s0 + 256 * j + e;
+          if (sl < Np && (sl & ~31) + slot_key(sl & 31) < N) {
+            masked |= m4[j][e] != 0.f;
+            all_masked &= m4[j][e] < -1e8f;
+          }
+        }
     }
   }
   masked = __any(masked);
