@@ -321,9 +321,14 @@ constexpr size_t tr_ws_lds_bytes() {
          4 * TransWs::C * sizeof(float);
 }
 
-// Byte offset of 16-byte chunk c of row r in an LDS tile of `row_bytes` rows whose chunks are
-// XOR-swizzled by (row & 7).
-PF_DEVICE int swz_off(int r, int c, int row_bytes) { return r * row_bytes + 16 * (c ^ (r & 7)); }
+// XOR swizzle of the 16-byte chunks of LDS rows of 256 or 128 bytes. The LDS serves a
+// ds_read_b128 16 lanes at a time from 64 banks (256 bytes), and the 16 lanes of a fragment
+// read are 16 consecutive rows at one logical chunk: with 256-byte rows (r & 15) spreads them
+// over the 16 bank groups; with 128-byte rows a row pair spans the banks once, so pairs take
+// the XOR (r >> 1) & 7.
+PF_DEVICE int swz(int r, int row_bytes) { return row_bytes == 256 ? (r & 15) : ((r >> 1) & 7); }
+// Byte offset of logical 16-byte chunk c of row r.
+PF_DEVICE int swz_off(int r, int c, int row_bytes) { return r * row_bytes + 16 * (c ^ swz(r, row_bytes)); }
 
 // One position row of z as the raw 16-byte pieces the LayerNorm B operands need: channels
 // 16 ks + 8 hf .. +7 for ks = 0..7 (bf16: 8 pieces, fp32: 16).
@@ -414,7 +419,7 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
     for (int t = 0; t < Cfg::DMA1; ++t) {
       const int ins = w * Cfg::DMA1 + t;  // 4 LDS rows of 256 B per instruction
       const int row = 4 * ins + (l >> 4);
-      const int lc = (l & 15) ^ (row & 7);  // logical chunk this lane fetches
+      const int lc = (l & 15) ^ swz(row, 256);  // logical chunk this lane fetches
       const int grow = row < HC ? HC * c + row : kHidden + HC * c + (row - HC);
       buf_load_lds16(r1, st + ins * 1024, (grow * C + 8 * lc) * 2, 0);
     }
@@ -422,7 +427,7 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
     for (int t = 0; t < Cfg::DMA2; ++t) {
       const int ins = w * Cfg::DMA2 + t;  // 8 LDS rows of 128 B per instruction
       const int row = 8 * ins + (l >> 3);
-      const int lc = (l & 7) ^ (row & 7);
+      const int lc = (l & 7) ^ swz(row, 128);
       buf_load_lds16(r2, st + Cfg::W1_BYTES + ins * 1024, (row * kHidden + HC * c + 8 * lc) * 2, 0);
     }
   };

@@ -756,11 +756,11 @@ __global__ __launch_bounds__(256) void trimul_project32_kernel(const TZ* __restr
 // the current tile (the same elements), gates and masks in registers -- a lane holds four
 // consecutive positions of one channel -- stages its 32 x 64 result channel-major in a
 // private LDS region with 8-byte stores and writes 128-byte plane rows.
-// The two waves that share a SIMD (w, w + 4) work out of phase: waves 4-7 first LayerNorm
-// the NEXT tile (16 rows each, from z rows they loaded two tiles ahead) into the other half
-// of a double-buffered LDS tile, then run their GEMMs, while waves 0-3 start on their GEMMs
-// at once; the MFMAs of one wave thus overlap the LayerNorm and gating VALU work of the
-// other. One barrier per tile publishes the next tile's LayerNorm.
+// Every wave LayerNorms 8 rows of the NEXT tile (from z rows it loaded two tiles ahead) into
+// the other half of a double-buffered LDS tile. The two waves that share a SIMD (w, w + 4)
+// work out of phase: waves 4-7 LayerNorm first and then run their GEMMs, waves 0-3 run their
+// GEMMs first and LayerNorm after, so each wave's MFMAs overlap the other's LayerNorm and
+// gating VALU work. One barrier per tile publishes the next tile's LayerNorm.
 struct ProjectWs {
   static constexpr int C = 128;
   static constexpr int BP = 64;   // positions per tile
@@ -780,7 +780,7 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
   constexpr int VEC = 16 / sizeof(TZ);  // z elements per 16-byte load
   constexpr int LPR = C / VEC;          // lanes per z row
   constexpr int RPI = 64 / LPR;         // rows per wave-wide load
-  constexpr int RPW = BP / 4;           // z rows each LayerNorm wave (4..7) normalises per tile
+  constexpr int RPW = BP / Cfg::NW;     // z rows each wave normalises per tile
   constexpr int NLD = RPW / RPI;        // 16-byte loads per lane per tile
   __shared__ __attribute__((aligned(16))) bf16 xs[2][BP * XLD];
   __shared__ __attribute__((aligned(16))) float mks[2][BP];
@@ -788,8 +788,8 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
 
   const int w = wave_id();
   const int l = lane_id();
-  const int pl = w >> 2;  // 0: a (P), 1: b (Q); also 1 = the LayerNorm group
-  const int cj = w & 3;   // 32-channel chunk; also the LayerNorm wave's row block
+  const int pl = w >> 2;  // 0: a (P), 1: b (Q); also 1 = LayerNorm before the GEMMs
+  const int cj = w & 3;   // 32-channel chunk
   bf16* stg = stage_all[w];
   const int tpl = Np / BP;
   const int ntiles = B * Np * tpl;  // < 2^31 (checked at launch)
@@ -822,7 +822,7 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
     line = rem / tpl;
     t0 = (rem - line * tpl) * BP;
   };
-  // LayerNorm group: z rows and mask values of two tiles ahead, in two register sets. The
+  // z rows and mask values of two tiles ahead, in two register sets. The
   // loads are unconditional (a padding row reads a clamped real row; its mask becomes 0 when
   // it is used), so the compiler's wait counts stay exact and the second set stays in flight.
   u32x4 zr[2][NLD];
@@ -837,7 +837,7 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
     unsigned ok = 0;
 #pragma unroll
     for (int q = 0; q < NLD; ++q) {
-      const int t = t0 + cj * RPW + q * RPI + l / LPR;
+      const int t = t0 + w * RPW + q * RPI + l / LPR;
       ok |= (line < N && t < N) ? 1u << q : 0u;
       const int tc = min(t, N - 1);
       const size_t pos = outgoing ? (size_t)lc * N + tc : (size_t)tc * N + lc;
@@ -865,12 +865,12 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
       const float rstd = rsqrtf(row_group_sum<LPR>(sq) * (1.0f / C) + eps);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) v[e] = (v[e] - mean) * rstd * lw[e] + lb[e];
-      const int row = cj * RPW + q * RPI + l / LPR;
+      const int row = w * RPW + q * RPI + l / LPR;
       store_vec<bf16, VEC>(xs[buf] + row * XLD + chunk * VEC, v);
       if (chunk == 0) mks[buf][row] = (okb[set] >> q) & 1u ? mkn[set][q] : 0.f;
     }
   };
-  // LayerNorm group, step for tile `tile`: normalise the next tile (register set `set`) into
+  // Step for tile `tile`: normalise the next tile (register set `set`) into
   // xs[buf] and refill the set with the tile after the one already in flight.
   // Every issue is unconditional (a tile past the end reloads the last tile, unused), so all
   // paths through the loop carry the same load counts.
@@ -924,27 +924,27 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
     __builtin_amdgcn_wave_barrier();
   };
 
-  // Prologue: the LayerNorm group loads two tiles and normalises the first. The loop runs
-  // two tiles per trip so the register sets and LDS halves are compile-time indices; all
-  // barrier conditions are block-uniform. The weights and LayerNorm parameters are waited
-  // for here, once: the two wave groups take different load paths into the loop, and
+  // Prologue: every wave loads its rows of two tiles and normalises the first. The loop
+  // runs two tiles per trip so the register sets and LDS halves are compile-time indices;
+  // all barrier conditions are block-uniform. The weights and LayerNorm parameters are
+  // waited for here, once: the two wave groups take different load paths into the loop, and
   // without this the compiler waits on every load in flight wherever it first reads them.
   __builtin_amdgcn_s_waitcnt(0);
   int tile = blockIdx.x;
-  if (pl == 1) {
-    issue(min(tile, ntiles - 1), 0);
-    issue(min(tile + G, ntiles - 1), 1);
-    if (tile < ntiles) layer_norm(0, 0);
-    issue(min(tile + 2 * G, ntiles - 1), 0);
-  }
+  issue(min(tile, ntiles - 1), 0);
+  issue(min(tile + G, ntiles - 1), 1);
+  if (tile < ntiles) layer_norm(0, 0);
+  issue(min(tile + 2 * G, ntiles - 1), 0);
   __syncthreads();
   for (; tile < ntiles; tile += 2 * G) {
     if (pl == 1) prepare_next(tile, 1, 1);
     compute(tile, 0);
+    if (pl == 0) prepare_next(tile, 1, 1);
     __syncthreads();  // xs[1] holds tile + G; every wave is done with xs[0]
     if (tile + G >= ntiles) break;
     if (pl == 1) prepare_next(tile + G, 0, 0);
     compute(tile + G, 1);
+    if (pl == 0) prepare_next(tile + G, 0, 0);
     __syncthreads();  // xs[0] holds tile + 2 G; every wave is done with xs[1]
   }
 }
