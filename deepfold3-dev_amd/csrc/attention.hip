@@ -228,21 +228,22 @@ __global__ __launch_bounds__(256) void attn_project_kernel(const TZ* __restrict_
 }
 
 // A1, persistent and weight-stationary (bf16 GEMMs). One 512-thread block per CU walks
-// tiles of 64 positions along a frame line. Wave w owns kind w >> 1 (q, k, v, g) and
-// heads 2 (w & 1), +1: those 64 weight rows stay in MFMA A-operand registers for the
-// whole kernel. Per tile: each wave LayerNorms 8 z rows into a double-buffered LDS tile
-// (the next tile's rows are loaded while this tile's MFMAs run); each wave computes
-// acc^T[channel][position] for its rows, stages the result in a private LDS region in the
-// layout of its output (Q, K: [h][t][d]; Vt: [h][d][slot]; G: [t][c]) and writes it with
-// 16-byte stores. Waves 0-3 also project the pair bias of 16 positions each (a 16x16x32
-// MFMA on the bias rows), wave 4 writes the line's additive mask slots.
+// tiles of 64 positions along a frame line. Waves 0-5 own kind w >> 1 (q, k, v) and heads
+// 2 (w & 1), +1: those 64 weight rows stay in MFMA A-operand registers for the whole
+// kernel. Per tile: each wave LayerNorms 8 z rows into a double-buffered LDS tile (the next
+// tile's rows are loaded while this tile's MFMAs run); waves 0-5 compute their rows'
+// projections, stage the result in a private LDS region in the layout of the output
+// (Q, K: [h][t][d] via acc^T[channel][position]; Vt: [h][d][slot] via acc[position][channel])
+// and write it with 16-byte stores. Waves 6 and 7 project the pair bias of 32 positions
+// each (16x16x32 MFMAs on the bias rows); wave 7 writes the line's additive mask slots.
+// The gate projection is not made here: the output kernel computes it from z.
 struct ProjectAttnWs {
   static constexpr int BP = 64;
   static constexpr int NW = 8;
   static constexpr int NT = 64 * NW;
   static constexpr int XLD = kC + 8;
   static constexpr int QLD = kHeadDim + 8;  // Q/K stage rows [t][d]
-  static constexpr int VLD = BP + 8;        // Vt stage rows [d][slot], G stage rows [t][c]
+  static constexpr int VLD = BP + 8;        // Vt stage rows [d][slot]
   static constexpr int STAGE = 2 * BP * QLD;
 };
 
@@ -250,7 +251,7 @@ template <class TZ>
 __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
     const TZ* __restrict__ z, const float* __restrict__ mask, const float* __restrict__ lnw,
     const float* __restrict__ lnb, float eps, const bf16* __restrict__ w5, bf16* __restrict__ Q,
-    bf16* __restrict__ K, bf16* __restrict__ Vt, bf16* __restrict__ G, float* __restrict__ PB,
+    bf16* __restrict__ K, bf16* __restrict__ Vt, float* __restrict__ PB,
     float* __restrict__ MA, int B, int N, int Np, int transpose, float qscale) {
   using Cfg = ProjectAttnWs;
   constexpr int BP = Cfg::BP, NW = Cfg::NW, XLD = Cfg::XLD, QLD = Cfg::QLD, VLD = Cfg::VLD;
@@ -259,14 +260,13 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
   constexpr int RPI = 64 / LPR;
   constexpr int RPW = BP / NW;
   constexpr int NLD = RPW / RPI;
-  static_assert(2 * kHeadDim * VLD <= Cfg::STAGE && BP * VLD <= Cfg::STAGE, "stage size");
+  static_assert(2 * kHeadDim * VLD <= Cfg::STAGE, "stage size");
   __shared__ __attribute__((aligned(16))) bf16 xs[2][BP * XLD];
-  __shared__ float lnp[2][kC];
   __shared__ __attribute__((aligned(16))) bf16 stage_all[NW][Cfg::STAGE];
 
   const int w = wave_id();
   const int l = lane_id();
-  const int kind = w >> 1;
+  const int kind = w >> 1;  // 0 q, 1 k, 2 v, 3: pair bias and mask
   const int h0 = 2 * (w & 1);
   bf16* stg = stage_all[w];
   const int tpl = Np / BP;
@@ -276,21 +276,26 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
   bf16x8 wa[2][kC / 16];
 #pragma unroll
   for (int hi = 0; hi < 2; ++hi) {
-    const bf16* rp = w5 + (size_t)(kind * kC + 32 * (h0 + hi) + (l & 31)) * kC + 8 * (l >> 5);
+    const bf16* rp = w5 + (size_t)(min(kind, 2) * kC + 32 * (h0 + hi) + (l & 31)) * kC + 8 * (l >> 5);
 #pragma unroll
     for (int ks = 0; ks < kC / 16; ++ks) wa[hi][ks] = *reinterpret_cast<const bf16x8*>(rp + 16 * ks);
   }
-  // Pair-bias rows (waves 0-3): 16x16x32 A operand, lane holds row l & 15, k = 32 ks + 8 (l >> 4).
-  bf16x8 wb[kC / 32];
-  if (w < 4) {
+  // Pair-bias rows: 16x16x32 A operands (lane holds row l & 15, k = 32 ks + 8 (l >> 4)),
+  // kept in LDS as [ks][lane] fragments, which leaves the registers for the LayerNorm
+  // parameters (read from LDS per tile, their 32-byte-strided reads cost more bank-conflict
+  // cycles than the rest of the kernel's LDS traffic together).
+  __shared__ bf16x8 wbs[kC / 32][64];
+  if (w == 0) {
     const bf16* rp = w5 + (size_t)(4 * kC + (l & 15)) * kC + 8 * (l >> 4);
 #pragma unroll
-    for (int ks = 0; ks < kC / 32; ++ks) wb[ks] = *reinterpret_cast<const bf16x8*>(rp + 32 * ks);
+    for (int ks = 0; ks < kC / 32; ++ks) wbs[ks][l] = *reinterpret_cast<const bf16x8*>(rp + 32 * ks);
   }
   const int chunk = l % LPR;
-  for (int i = threadIdx.x; i < kC; i += blockDim.x) {
-    lnp[0][i] = lnw[i];
-    lnp[1][i] = lnb[i];
+  float lw[VEC], lb[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    lw[e] = lnw[chunk * VEC + e];
+    lb[e] = lnb[chunk * VEC + e];
   }
   __syncthreads();
 
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
         zr[q] = u32x4{0u, 0u, 0u, 0u};
       }
     }
-    if (w == 4) {
+    if (w == 7) {
       const int t = t0 + l;
       const size_t pos = transpose ? (size_t)t * N + line : (size_t)line * N + t;
       mkn = (line < N && t < N) ? mask[(size_t)b * N * N + pos] : 0.f;
@@ -350,7 +355,7 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
       const float rstd = rsqrtf(row_group_sum<LPR>(sq) * (1.0f / kC) + eps);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        const float y = (v[e] - mean) * rstd * lnp[0][chunk * VEC + e] + lnp[1][chunk * VEC + e];
+        const float y = (v[e] - mean) * rstd * lw[e] + lb[e];
         v[e] = zok[q] ? y : 0.f;
       }
       store_vec<bf16, VEC>(xb + (w * RPW + q * RPI + l / LPR) * XLD + chunk * VEC, v);
@@ -360,46 +365,63 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
     if (next < ntiles) issue(next);
     __syncthreads();  // xs[buf] holds the whole tile
 
-    f32x16 acc[2][2];  // [head][position tile]
-    zero_acc32(acc);
+    if (kind == 3) {
+      // Pair bias of positions 32 (w - 6) + 16 sb + l (lanes 0-15 hold heads 0-3).
 #pragma unroll
-    for (int ks = 0; ks < kC / 16; ++ks) {
-      bf16x8 xf[2];
+      for (int sb = 0; sb < 2; ++sb) {
+        const int pp = 32 * (w - 6) + 16 * sb;
+        f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int pt = 0; pt < 2; ++pt)
-        xf[pt] = *reinterpret_cast<const bf16x8*>(xb + (32 * pt + (l & 31)) * XLD + 16 * ks + 8 * (l >> 5));
+        for (int ks = 0; ks < kC / 32; ++ks) {
+          const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xb + (pp + (l & 15)) * XLD + 32 * ks + 8 * (l >> 4));
+          pacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wbs[ks][l], xf, pacc, 0, 0, 0);
+        }
+        if (l < 16) {
+          const int t = t0 + pp + l;
+          const bool ok = line < N && t < N;
 #pragma unroll
-      for (int hi = 0; hi < 2; ++hi)
-#pragma unroll
-        for (int pt = 0; pt < 2; ++pt)
-          acc[hi][pt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[hi][ks], xf[pt], acc[hi][pt], 0, 0, 0);
-    }
-    if (w < 4) {
-      // Pair bias of positions 16 w .. +16: lanes 0-15 hold heads 0-3 of position 16 w + l.
-      f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < kC / 32; ++ks) {
-        const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xb + (16 * w + (l & 15)) * XLD + 32 * ks + 8 * (l >> 4));
-        pacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[ks], xf, pacc, 0, 0, 0);
-      }
-      if (l < 16) {
-        const int t = t0 + 16 * w + l;
-        const bool ok = line < N && t < N;
-#pragma unroll
-        for (int hh = 0; hh < kHeads; ++hh) {
-          const float v = ok ? pacc[hh] * kLog2e : 0.f;
-          float* dst = PB + (((size_t)b * kHeads + hh) * Np + line) * Np;
-          if (transpose)  // key-major [b][h][key = line][query = t]
-            dst[t] = v;
-          else  // query-major [b][h][query = line][slot(key = t)]
-            dst[(t & ~31) + key_slot(t & 31)] = v;
+          for (int hh = 0; hh < kHeads; ++hh) {
+            const float v = ok ? pacc[hh] * kLog2e : 0.f;
+            float* dst = PB + (((size_t)b * kHeads + hh) * Np + line) * Np;
+            if (transpose)  // key-major [b][h][key = line][query = t]
+              dst[t] = v;
+            else  // query-major [b][h][query = line][slot(key = t)]
+              dst[(t & ~31) + key_slot(t & 31)] = v;
+          }
         }
       }
+      if (w == 7) {
+        const int t = t0 + l;
+        MA[lineq * Np + (t & ~31) + key_slot(t & 31)] = t < N ? (mk - 1.0f) * 1e9f * kLog2e : -INFINITY;
+      }
+      continue;  // block-uniform barriers only at the top of the loop
     }
-    if (w == 4) {
-      const int t = t0 + l;
-      MA[lineq * Np + (t & ~31) + key_slot(t & 31)] = t < N ? (mk - 1.0f) * 1e9f * kLog2e : -INFINITY;
-    }
+
+    // acc[head][position tile]: acc^T [channel][position] (a lane holds 16 channels of one
+    // position) for Q and K; acc [position][channel] for Vt, the operands swapped, so a lane
+    // holds 4 consecutive positions of a channel -- 4 consecutive key slots of its stage.
+    f32x16 acc[2][2];
+    zero_acc32(acc);
+    auto gemm = [&](auto positions_as_rows) __attribute__((always_inline)) {
+#pragma unroll
+      for (int ks = 0; ks < kC / 16; ++ks) {
+        bf16x8 xf[2];
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt)
+          xf[pt] = *reinterpret_cast<const bf16x8*>(xb + (32 * pt + (l & 31)) * XLD + 16 * ks + 8 * (l >> 5));
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+          for (int pt = 0; pt < 2; ++pt)
+            acc[hi][pt] = decltype(positions_as_rows)::value
+                              ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[pt], wa[hi][ks], acc[hi][pt], 0, 0, 0)
+                              : __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[hi][ks], xf[pt], acc[hi][pt], 0, 0, 0);
+      }
+    };
+    if (kind == 2)
+      gemm(std::true_type{});
+    else
+      gemm(std::false_type{});
 
     // Epilogue: stage in the output layout, then 16-byte stores.
     if (kind <= 1) {  // Q (pre-scaled) or K: stage [hi][t][d]
@@ -415,15 +437,7 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
             for (int e = 0; e < 4; ++e) v[e] = acc[hi][pt][4 * g4 + e] * sc;
             store_vec<bf16, 4>(stg + (hi * BP + 32 * pt + (l & 31)) * QLD + acc32_row(4 * g4), v);
           }
-    } else if (kind == 2) {  // Vt: stage [hi][d][slot]
-#pragma unroll
-      for (int hi = 0; hi < 2; ++hi)
-#pragma unroll
-        for (int pt = 0; pt < 2; ++pt)
-#pragma unroll
-          for (int e = 0; e < 16; ++e)
-            stg[(hi * kHeadDim + acc32_row(e)) * VLD + 32 * pt + key_slot(l & 31)] = (bf16)acc[hi][pt][e];
-    } else {  // G = sigmoid(g): stage [t][64 channels]
+    } else {  // Vt: stage [hi][d][slot]; positions 8 g4 + 4 hf + e are slots 16 hf + 4 g4 + e
 #pragma unroll
       for (int hi = 0; hi < 2; ++hi)
 #pragma unroll
@@ -432,8 +446,8 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
           for (int g4 = 0; g4 < 4; ++g4) {
             float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = sigmoidf_(acc[hi][pt][4 * g4 + e]);
-            store_vec<bf16, 4>(stg + (32 * pt + (l & 31)) * VLD + 32 * hi + acc32_row(4 * g4), v);
+            for (int e = 0; e < 4; ++e) v[e] = acc[hi][pt][4 * g4 + e];
+            store_vec<bf16, 4>(stg + (hi * kHeadDim + (l & 31)) * VLD + 32 * pt + key_slot(acc32_row(4 * g4)), v);
           }
     }
     // The stage is private to this wave: LDS operations of one wave complete in order.
@@ -451,7 +465,7 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
           *reinterpret_cast<u32x4*>(dst0 + ((size_t)hi * Np + p) * kHeadDim + 8 * c) =
               *reinterpret_cast<const u32x4*>(stg + (hi * BP + p) * QLD + 8 * c);
         }
-    } else if (kind <= 2) {
+    } else {
       // K / Vt key-block tiles (kv_chunk): lane-consecutive chunks, so each store
       // instruction writes one contiguous kilobyte. The tile's BP / 32 key blocks of head
       // h0 + hi follow each other in memory.
@@ -468,15 +482,6 @@ __global__ __launch_bounds__(ProjectAttnWs::NT) void attn_project_ws_kernel(
           *reinterpret_cast<u32x4*>(dst0 + (size_t)hi * Np * kHeadDim + 8 * g) =
               *reinterpret_cast<const u32x4*>(src);
         }
-    } else {
-      bf16* dst0 = G + (lineq * Np + t0) * kC + 64 * (w & 1);
-#pragma unroll
-      for (int it = 0; it < BP * 64 / 8 / 64; ++it) {
-        const int p = it * 8 + (l >> 3);
-        const int c = l & 7;
-        *reinterpret_cast<u32x4*>(dst0 + (size_t)p * kC + 8 * c) =
-            *reinterpret_cast<const u32x4*>(stg + p * VLD + 8 * c);
-      }
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -1046,13 +1051,17 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const TC* __restrict__ O,
   store_tile_from_lds<TZ, kC, BM, NT>(orow, stage, SLD, accumulate != 0);
 }
 
-// A3, persistent and weight-stationary (bf16 GEMMs). Blocks of 8 waves (two per CU) walk
-// tiles of 64 positions of a frame line. Wave w owns output channels 16 w .. +16 (W_out
-// rows as 16x16x32 MFMA A operands, resident in registers). Per tile: A = O * G (frame
-// rows) -> LDS; the MFMAs give acc^T[channel][position]; the fp32 update is staged
-// block-wide and each thread adds it to the z channels it loaded (the position's z row,
-// transposed back for columns) and stores them. The next tile's O, G and z are loaded
-// during this tile's MFMAs.
+// A3, persistent and weight-stationary (bf16 GEMMs), with the output gate. Blocks of 8
+// waves (two per CU) walk tiles of 64 positions of a frame line. Thread (position p, part
+// sp) loads channels 16 sp .. +16 of z at p; the 8 threads of a position LayerNorm the row
+// (statistics over DPP lane groups) into an LDS tile. Wave w owns channels 16 w .. +16 of
+// the gate and of the output projection (W_g and W_out rows as 16x16x32 MFMA A operands,
+// resident in registers): g^T = W_g LN(z)^T, then a = O * sigmoid(g) -- O read straight in
+// the accumulator layout -- into a second LDS tile, y^T = W_out a^T staged in fp32, and each
+// thread adds the update to the z channels it loaded and stores them. The next tile's z and
+// O are loaded during this tile's gate GEMM, and its LayerNorm runs before the residual.
+// Computing the gate here, from the z rows the residual needs anyway, saves A1 writing it
+// and this kernel reading it back.
 struct OutAttnWs {
   static constexpr int BP = 64;
   static constexpr int NW = 8;
@@ -1063,14 +1072,19 @@ struct OutAttnWs {
 
 template <class TZ>
 __global__ __launch_bounds__(OutAttnWs::NT, 4) void attn_out_ws_kernel(
-    const bf16* __restrict__ O, const bf16* __restrict__ G, const bf16* __restrict__ Wo, const TZ* __restrict__ z,
-    TZ* __restrict__ out, int B, int N, int Np, int transpose, int accumulate) {
+    const bf16* __restrict__ O, const bf16* __restrict__ Wg, const bf16* __restrict__ Wo, const TZ* z,
+    const float* __restrict__ lnw, const float* __restrict__ lnb, float eps, TZ* out, int B, int N, int Np,
+    int transpose, int accumulate, int res_is_z) {
   using Cfg = OutAttnWs;
   constexpr int BP = Cfg::BP, ALD = Cfg::ALD, SLD = Cfg::SLD;
   constexpr int ZV = 16 / sizeof(TZ);  // z elements per 16-byte load
   constexpr int ZL = 16 / ZV;          // 16-byte z loads per thread (16 channels)
-  __shared__ __attribute__((aligned(16))) bf16 a_lds[BP * ALD];
+  __shared__ __attribute__((aligned(16))) bf16 x_lds[BP * ALD];  // LN(z)
+  __shared__ __attribute__((aligned(16))) bf16 a_lds[BP * ALD];  // O * sigmoid(g)
   __shared__ __attribute__((aligned(16))) float upd[BP * SLD];
+  // LayerNorm weight | bias as [q][sp] groups of 4 channels (16 sp + 4 q ..): the 8 parts of
+  // a position read 8 consecutive 16-byte groups.
+  __shared__ f32x4 lnq[2][4][8];
 
   const int tid = threadIdx.x;
   const int w = wave_id();
@@ -1078,12 +1092,22 @@ __global__ __launch_bounds__(OutAttnWs::NT, 4) void attn_out_ws_kernel(
   const int tpl = (N + BP - 1) / BP;
   const long ntiles = (long)B * N * tpl;
 
-  bf16x8 wo[kC / 32];
+  bf16x8 wg[kC / 32], wo[kC / 32];
 #pragma unroll
-  for (int ks = 0; ks < kC / 32; ++ks)
-    wo[ks] = *reinterpret_cast<const bf16x8*>(Wo + (size_t)(16 * w + (l & 15)) * kC + 32 * ks + 8 * (l >> 4));
+  for (int ks = 0; ks < kC / 32; ++ks) {
+    const size_t at = (size_t)(16 * w + (l & 15)) * kC + 32 * ks + 8 * (l >> 4);
+    wg[ks] = *reinterpret_cast<const bf16x8*>(Wg + at);
+    wo[ks] = *reinterpret_cast<const bf16x8*>(Wo + at);
+  }
+  if (tid < 64) {
+    const int sp = tid & 7, q = (tid >> 3) & 3, wb = tid >> 5;
+    const float* src = (wb ? lnb : lnw) + 16 * sp + 4 * q;
+    lnq[wb][q][sp] = f32x4{src[0], src[1], src[2], src[3]};
+  }
   // Thread (position p, part s) handles channels 16 s .. +16 of position p.
   const int p = tid >> 3, sp = tid & 7;
+  // Accumulator lanes: channels 16 w + 4 (l >> 4) + e of position 16 pt + (l & 15).
+  const int cq = 16 * w + 4 * (l >> 4);
 
   auto tile_coords = [&](long tile, int& b, int& line, int& t0) {
     b = (int)(tile / ((long)N * tpl));
@@ -1094,48 +1118,98 @@ __global__ __launch_bounds__(OutAttnWs::NT, 4) void attn_out_ws_kernel(
   auto zpos = [&](int b, int line, int t) -> size_t {
     return (size_t)b * N * N + (transpose ? (size_t)t * N + line : (size_t)line * N + t);
   };
-  u32x4 orr[2], grr[2], zr[ZL];
+  // O tiles lie inside the padded frame (t0 + 63 < Np); z rows past N read as zeros.
+  u32x2 orr[4];
+  u32x4 zr[ZL];
   auto issue = [&](long tile) {
     int b, line, t0;
     tile_coords(tile, b, line, t0);
-    const int t = t0 + p;
-    const size_t fr = (((size_t)b * Np + line) * Np + t) * kC + 16 * sp;
+    const bf16* Ol = O + (((size_t)b * Np + line) * Np + t0) * kC + cq;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      orr[q] = *reinterpret_cast<const u32x4*>(O + fr + 8 * q);
-      grr[q] = *reinterpret_cast<const u32x4*>(G + fr + 8 * q);
-    }
-    if (accumulate && t < N) {
+    for (int pt = 0; pt < 4; ++pt) orr[pt] = *reinterpret_cast<const u32x2*>(Ol + (size_t)(16 * pt + (l & 15)) * kC);
+    const int t = t0 + p;
+    if (t < N) {
       const TZ* zp = z + zpos(b, line, t) * kC + 16 * sp;
 #pragma unroll
       for (int q = 0; q < ZL; ++q) zr[q] = *reinterpret_cast<const u32x4*>(zp + ZV * q);
+    } else {
+#pragma unroll
+      for (int q = 0; q < ZL; ++q) zr[q] = u32x4{0u, 0u, 0u, 0u};
     }
   };
 
-  long tile = blockIdx.x;
-  if (tile < ntiles) issue(tile);
-  for (; tile < ntiles; tile += gridDim.x) {
-    int b, line, t0;
-    tile_coords(tile, b, line, t0);
-    {
-      float a[16];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        float ov[8], gv[8];
-        unpack16<bf16>(orr[q], ov);
-        unpack16<bf16>(grr[q], gv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[8 * q + e] = ov[e] * gv[e];
-      }
-      store_vec<bf16, 8>(a_lds + p * ALD + 16 * sp, a);
-      store_vec<bf16, 8>(a_lds + p * ALD + 16 * sp + 8, a + 8);
-    }
+  // LayerNorm of a position's row (fp32 two-pass statistics over the 8 lanes of the
+  // position) -> x_lds.
+  auto layer_norm = [&](const u32x4 (&zz)[ZL]) __attribute__((always_inline)) {
     float zv[16];
 #pragma unroll
-    for (int q = 0; q < ZL; ++q) unpack16<TZ>(zr[q], *reinterpret_cast<float(*)[ZV]>(zv + ZV * q));
+    for (int q = 0; q < ZL; ++q) unpack16<TZ>(zz[q], *reinterpret_cast<float(*)[ZV]>(zv + ZV * q));
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sum += zv[e];
+    const float mean = dpp_sum8(sum) * (1.0f / kC);
+    float sq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float d = zv[e] - mean;
+      sq += d * d;
+    }
+    const float rstd = rsqrtf(dpp_sum8(sq) * (1.0f / kC) + eps);
+    float x[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 gw = lnq[0][q][sp], gb = lnq[1][q][sp];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * q + e] = (zv[4 * q + e] - mean) * rstd * gw[e] + gb[e];
+    }
+    store_vec<bf16, 8>(x_lds + p * ALD + 16 * sp, x);
+    store_vec<bf16, 8>(x_lds + p * ALD + 16 * sp + 8, x + 8);
+  };
+
+  // Two barriers per tile: the next tile's LayerNorm runs between the output GEMM and the
+  // residual, so one barrier publishes both it and the update. zc / oc: this tile's raw z
+  // rows and O; zr / orr: the next tile's, loaded during this tile's gate GEMM.
+  long tile = blockIdx.x;
+  if (tile >= ntiles) return;  // block-uniform
+  issue(tile);
+  __syncthreads();  // LayerNorm parameters
+  layer_norm(zr);
+  u32x4 zc[ZL];
+  u32x2 oc[4];
+#pragma unroll
+  for (int q = 0; q < ZL; ++q) zc[q] = zr[q];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) oc[pt] = orr[pt];
+  __syncthreads();  // x_lds complete
+  for (;;) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
     const long next = tile + gridDim.x;
     if (next < ntiles) issue(next);
-    __syncthreads();  // A tile complete
+
+    // g^T = W_g LN(z)^T; a = O * sigmoid(g) -> a_lds [pos][ch].
+    {
+      f32x4 gacc[4];
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) gacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kC / 32; ++ks)
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) {
+          const bf16x8 fx =
+              *reinterpret_cast<const bf16x8*>(x_lds + (16 * pt + (l & 15)) * ALD + 32 * ks + 8 * (l >> 4));
+          gacc[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wg[ks], fx, gacc[pt], 0, 0, 0);
+        }
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) {
+        const bf16x4 o4 = __builtin_bit_cast(bf16x4, oc[pt]);
+        float a[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[e] = (float)o4[e] * sigmoidf_(gacc[pt][e]);
+        store_vec<bf16, 4>(a_lds + (16 * pt + (l & 15)) * ALD + cq, a);
+      }
+    }
+    __syncthreads();  // a_lds complete; x_lds and the previous tile's update no longer read
 
     f32x4 acc[4];
 #pragma unroll
@@ -1148,13 +1222,22 @@ __global__ __launch_bounds__(OutAttnWs::NT, 4) void attn_out_ws_kernel(
             *reinterpret_cast<const bf16x8*>(a_lds + (16 * pt + (l & 15)) * ALD + 32 * ks + 8 * (l >> 4));
         acc[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wo[ks], fa, acc[pt], 0, 0, 0);
       }
-    // lane holds channels 16 w + 4 (l >> 4) + e of position 16 pt + (l & 15)
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt)
-      *reinterpret_cast<f32x4*>(upd + (16 * pt + (l & 15)) * SLD + 16 * w + 4 * (l >> 4)) = acc[pt];
-    __syncthreads();  // update tile complete
+    for (int pt = 0; pt < 4; ++pt) *reinterpret_cast<f32x4*>(upd + (16 * pt + (l & 15)) * SLD + cq) = acc[pt];
+    if (next < ntiles) layer_norm(zr);
+    __syncthreads();  // update and the next tile's x_lds complete; a_lds no longer read
+
     const int t = t0 + p;
     if (t < N) {
+      TZ* op = out + zpos(b, line, t) * kC + 16 * sp;
+      float zv[16];
+      if (accumulate && !res_is_z) {  // residual stream other than z: read it here
+#pragma unroll
+        for (int q = 0; q < ZL; ++q) load16<TZ>(op + ZV * q, *reinterpret_cast<float(*)[ZV]>(zv + ZV * q));
+      } else {
+#pragma unroll
+        for (int q = 0; q < ZL; ++q) unpack16<TZ>(zc[q], *reinterpret_cast<float(*)[ZV]>(zv + ZV * q));
+      }
       float y[16];
 #pragma unroll
       for (int e = 0; e < 16; e += 4) {
@@ -1162,10 +1245,15 @@ __global__ __launch_bounds__(OutAttnWs::NT, 4) void attn_out_ws_kernel(
 #pragma unroll
         for (int k = 0; k < 4; ++k) y[e + k] = accumulate ? zv[e + k] + u[k] : u[k];
       }
-      TZ* op = out + zpos(b, line, t) * kC + 16 * sp;
 #pragma unroll
       for (int q = 0; q < ZL; ++q) store_vec<TZ, ZV>(op + ZV * q, y + ZV * q);
     }
+    if (next >= ntiles) break;
+    tile = next;
+#pragma unroll
+    for (int q = 0; q < ZL; ++q) zc[q] = zr[q];
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) oc[pt] = orr[pt];
   }
 }
 
@@ -1195,7 +1283,7 @@ AttnWs attn_ws_layout(int B, int N, int cdtype) {
   w.q = take(tok);
   w.k = take(tok);
   w.v = take(tok);
-  w.g = take(tok);
+  w.g = cdtype == PF_F32 ? take(tok) : 0;  // the bf16 path computes the gate in the output kernel
   w.o = take(tok);
   w.pb = take((size_t)B * kHeads * Np * Np * 4);
   w.ma = take((size_t)B * Np * Np * 4);
@@ -1227,8 +1315,8 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
       const long ntiles = (long)B * Np * (Np / ProjectAttnWs::BP);
       const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
       attn_project_ws_kernel<TZ><<<nblk, ProjectAttnWs::NT, 0, s>>>((const TZ*)z, mask, lnw, lnb, eps,
-                                                                    (const bf16*)w5, Qb, Kb, Vb, Gb, PBb, MAb, B,
-                                                                    N, Np, transpose, qscale);
+                                                                    (const bf16*)w5, Qb, Kb, Vb, PBb, MAb, B, N,
+                                                                    Np, transpose, qscale);
       (void)grid;
     } else {
       attn_project_kernel<TZ, TC><<<grid, 256, 0, s>>>((const TZ*)z, mask, lnw, lnb, eps, (const TC*)w5, Qb, Kb,
@@ -1269,8 +1357,11 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     if constexpr (sizeof(TC) == 2) {
       const long ntiles = (long)B * N * ((N + OutAttnWs::BP - 1) / OutAttnWs::BP);
       const int nblk = (int)std::min<long>(ntiles, 2L * pf::cu_count());
-      attn_out_ws_kernel<TZ><<<nblk, OutAttnWs::NT, 0, s>>>(Ob, Gb, (const bf16*)wo, (const TZ*)out, (TZ*)out, B, N,
-                                                            Np, transpose, accumulate);
+      // The gate rows are kind 3 of the packed projection weights.
+      const bf16* wg = (const bf16*)w5 + (size_t)3 * kC * kC;
+      attn_out_ws_kernel<TZ><<<nblk, OutAttnWs::NT, 0, s>>>(Ob, wg, (const bf16*)wo, (const TZ*)z, lnw, lnb, eps,
+                                                            (TZ*)out, B, N, Np, transpose, accumulate,
+                                                            out == z ? 1 : 0);
       (void)grid;
     } else {
       attn_out_kernel<TZ, TC><<<grid, 256, 0, s>>>(Ob, Gb, (const TC*)wo, (TZ*)out, N, Np, transpose, accumulate);

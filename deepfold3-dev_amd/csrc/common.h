@@ -124,22 +124,23 @@ PF_DEVICE float group_max(float v) {
   return v;
 }
 
-// Sum over each row of 16 lanes with DPP moves (no LDS round trip): quad_perm [1,0,3,2],
-// quad_perm [2,3,0,1], row_half_mirror, row_mirror -- after each step every lane holds the
-// sum over twice as many lanes.
+// Row-local DPP move of a float (bound_ctrl off, all rows and banks).
+template <int CTRL>
+PF_DEVICE float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+// Sums over aligned groups of 8 / 16 lanes with DPP moves (no LDS round trip): quad_perm
+// [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror (8), then row_mirror (16) -- after each
+// step every lane holds the sum over twice as many lanes.
+PF_DEVICE float dpp_sum8(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  return v;
+}
 PF_DEVICE float dpp_sum16(float v) {
-  auto dpp = [](float x, int ctrl) -> float {
-    switch (ctrl) {
-      case 0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
-      case 1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
-      case 2: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
-      default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
-    }
-  };
-  v += dpp(v, 0);
-  v += dpp(v, 1);
-  v += dpp(v, 2);
-  v += dpp(v, 3);
+  v = dpp_sum8(v);
+  v += dpp_mov<0x140>(v);
   return v;
 }
 // Sum over aligned groups of W lanes, W in {16, 32}: DPP inside rows, one swizzle across.

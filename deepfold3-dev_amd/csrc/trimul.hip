@@ -969,22 +969,6 @@ struct OutputWs {
   static constexpr int SLD = C + 4;   // fp32 update stage rows [pos][ch]
 };
 
-// Sum over aligned groups of 8 lanes with DPP moves: quad_perm [1,0,3,2], quad_perm
-// [2,3,0,1], row_half_mirror.
-PF_DEVICE float dpp_sum8(float v) {
-  auto dpp = [](float x, int ctrl) -> float {
-    switch (ctrl) {
-      case 0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
-      case 1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
-      default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
-    }
-  };
-  v += dpp(v, 0);
-  v += dpp(v, 1);
-  v += dpp(v, 2);
-  return v;
-}
-
 template <class TZ>
 __global__ __launch_bounds__(OutputWs::NT) void trimul_output_ws_kernel(
     const bf16* __restrict__ X, const TZ* __restrict__ z, TZ* __restrict__ out, const float* __restrict__ lniw,
