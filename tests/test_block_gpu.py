@@ -95,6 +95,34 @@ def test_grid_attention_residual_in_place(dev):
     assert_fp32_close(z.cpu(), ref, what="fused residual, batch 2")
 
 
+@pytest.mark.parametrize("transpose", [False, True])
+def test_grid_attention_bf16_accumulate_into_other_stream(dev, transpose):
+    """bf16 path, out != z with accumulate: the output kernel adds the update to out's rows
+    (not z's), with the gate still taken from z; in place it adds to z. Both against the
+    plain update (accumulate off) plus the stream, within one bf16 rounding of the sum."""
+    n = 70
+    sd = W.make_block_weights(25, perturb_affine=True)
+    p = sub(sd, "pair_attn_col." if transpose else "pair_attn_row.")
+    inp = W.make_inputs(n, seed=8, batch=2, pad_random=5)
+    m = _grid(transpose, p, dev, torch.bfloat16)
+    z = inp["pair"].to(dev, torch.bfloat16).contiguous()
+    mask = inp["pair_mask"].to(dev)
+    gen = torch.Generator().manual_seed(9)
+    stream = torch.randn(z.shape, generator=gen).to(dev, torch.bfloat16)
+    print(f"[grid bf16 accumulate transpose={transpose}]", flush=True)
+    with torch.no_grad():
+        upd = m(z, mask).float()
+        other = stream.clone()
+        m._run(z, mask, other, True)
+        inplace = z.clone()
+        m.forward_residual_(inplace, mask)
+    for got, base, what in ((other, stream, "other stream"), (inplace, z, "in place")):
+        want = base.float() + upd
+        err = (got.float() - want).abs()
+        tol = 2.0 ** -7 * want.abs() + 2.0 ** -7 * upd.abs() + 1e-6
+        assert bool((err <= tol).all()), f"{what}: max err {err.max().item():.3e}"
+
+
 @pytest.mark.parametrize("stream_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("n", [24, 70, 130])
 def test_pair_transition_and_fused_single_to_pair_bf16_rule(dev, n, stream_dtype):
