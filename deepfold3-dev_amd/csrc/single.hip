@@ -73,8 +73,7 @@ __global__ __launch_bounds__(256) void rowgemm_kernel(const TC* __restrict__ A, 
   }
   const TC* wrow = W + (size_t)(n0 + r) * K;
   const TC* wrow2 = W + (size_t)(Nout + n0 + r) * K;
-#pragma unroll 4
-  for (int k0 = 0; k0 < K; k0 += MF::K16) {
+  auto kstep = [&](int k0) __attribute__((always_inline)) {
     const typename MF::Frag bf = MF::load(wrow + k0 + kq);
     typename MF::Frag bf2;
     if (EPI == EPI_SWIGLU) bf2 = MF::load(wrow2 + k0 + kq);
@@ -84,7 +83,14 @@ __global__ __launch_bounds__(256) void rowgemm_kernel(const TC* __restrict__ A, 
       MF::mma16(acc[i], af, bf);
       if (EPI == EPI_SWIGLU) MF::mma16(acc2[i], af, bf2);
     }
+  };
+  // Four k-steps per trip (their loads in flight together), then the remainder.
+  int k0 = 0;
+  for (; k0 + 4 * MF::K16 <= K; k0 += 4 * MF::K16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kstep(k0 + j * MF::K16);
   }
+  for (; k0 < K; k0 += MF::K16) kstep(k0);
   const int n = n0 + r;
 #pragma unroll
   for (int i = 0; i < RB; ++i)
