@@ -263,6 +263,25 @@ def test_block_bf16_rule(dev, stream_dtype):
     print("[block bf16 single]", assert_bf16_rule(single.cpu(), es.cpu(), rs, "block single"), flush=True)
 
 
+def test_block_bf16_batch_items_are_independent(dev):
+    """bf16 block on a batch of 2 (ragged N, padding) equals the block on each item alone,
+    bit for bit: every persistent kernel indexes batch items inside its flat tile walk
+    (tiles straddle the items when N^2 is not a multiple of the tile), so any batch-offset
+    mistake changes some position's result."""
+    n = 70
+    sd = W.make_block_weights(29, perturb_affine=True)
+    inp = W.make_inputs(n, seed=10, batch=2, pad_random=5)
+    blk = _block(sd, dev, torch.bfloat16)
+    x = [inp[k].to(dev, torch.bfloat16) if k in ("pair", "single") else inp[k].to(dev) for k in
+         ("pair", "single", "pair_mask", "seq_mask")]  # fmt: skip
+    with torch.no_grad():
+        pair, single = blk(*x)
+        for b in range(2):
+            pb, sb = blk(*(t[b : b + 1] for t in x))
+            assert torch.equal(pb[0], pair[b]), f"pair, item {b}: max |d| {(pb[0] - pair[b]).abs().max().item()}"
+            assert torch.equal(sb[0], single[b]), f"single, item {b}: max |d| {(sb[0] - single[b]).abs().max().item()}"
+
+
 def test_trunk_two_blocks_fp32(dev):
     blocks = W.make_trunk_weights(31, 2, perturb_affine=True)
     inp = W.make_inputs(32, seed=11, pad_random=3)
