@@ -380,15 +380,18 @@ __global__ __launch_bounds__(512) void trimul_contract256_kernel(const bf16* __r
   }
 }
 
-// bf16 contraction on 256 (i) x 384 (j) tiles, used when Np is a multiple of 768 (then
-// B C (Np / 256) (Np / 384) blocks fill the CUs in whole rounds -- at N = 768, three -- and
-// each operand row block is read twice (P) or three times (Q) instead of three times each).
-// Eight waves in 2 x 4, each owning a 128 (i) x 96 (j) block as 4 x 3 tiles of
+// bf16 contraction on 256 (i) x 384 (j) tiles, used when Np is a multiple of 768 (each
+// operand row block is then read twice (P) or three times (Q) instead of three times each).
+// Persistent: one block per CU walks tiles (at N = 768, B C 6 tiles: three per CU). Eight
+// waves in 2 x 4, each owning a 128 (i) x 96 (j) block as 4 x 3 tiles of
 // v_mfma_f32_32x32x16_bf16 (192 fp32 accumulators per lane): per k-step 7 fragment reads
 // feed 12 MFMAs. k-tiles of 64 (whole 128-byte lines per row) flow through two LDS stages
 // of 80 KiB -- the whole 160 KiB of a CU -- filled by global_load_lds_dwordx4 one tile
 // ahead, one barrier per tile, with the same 16-byte chunk swizzle as the 256 x 256 kernel.
-// The output tile leaves through the first stage in two passes of 128 rows i.
+// The last k-step of a tile issues the next tile's first k-tile into stage 0, so its
+// latency hides behind the last MFMAs and the output pass; the output tile leaves through
+// stage 1 in four passes of 64 rows i (the k-tile count is even: stage 1 holds the last
+// k-tile, whose readers the first pass's barrier waits for).
 struct Contract768 {
   static constexpr int BI = 256;
   static constexpr int BJ = 384;
@@ -399,9 +402,9 @@ struct Contract768 {
   static constexpr int BLKS = (BI + BJ) / 8;         // 1 KiB direct-load blocks per stage (80)
   static constexpr int DMA = BLKS / (NT / 64);       // per wave (10)
   static constexpr int OLD = BJ + 8;                 // output staging rows (bf16): 784 bytes
-  static constexpr int OROWS = 128;                  // output rows per staging pass
+  static constexpr int OROWS = 64;                   // output rows per staging pass
   static constexpr int SMEM = 2 * STAGE * 2;         // 163840 bytes
-  static_assert(OROWS * OLD * 2 <= SMEM, "output pass fits the ring");
+  static_assert(OROWS * OLD <= STAGE, "output pass fits stage 1");
 };
 
 __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __restrict__ P, const bf16* __restrict__ Q,
@@ -414,23 +417,24 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
 
   const int ti = Np / BI, tj = Np / BJ;
   const int tiles = ti * tj;
-  int bid = blockIdx.x;
-  int g, tile;
-  if (xcd_remap) {  // XCD x walks planes x, x+8, ...: a plane's operands stay in one L2
-    const int xcd = bid & 7;
-    const int u = bid >> 3;
-    g = xcd + 8 * (u / tiles);
-    tile = u % tiles;
-  } else {
-    g = bid / tiles;
-    tile = bid % tiles;
-  }
-  if (g >= G) return;
-  const int i0 = (tile / tj) * BI;
-  const int j0 = (tile % tj) * BJ;
+  const int total = G * tiles;
   const size_t pe = (size_t)Np * Np;
-  const bf16* Pg = P + (size_t)g * pe + (size_t)i0 * Np;
-  const bf16* Qg = Q + (size_t)g * pe + (size_t)j0 * Np;
+  // Virtual tile vt -> plane g and tile origin. With the XCD remap, XCD x (vt & 7: the grid
+  // is a multiple of 8 and vt steps by it) walks planes x, x + 8, ...: a plane's operands
+  // stay in one L2.
+  auto coords = [&](int vt, int& g, int& i0, int& j0) {
+    int tile;
+    if (xcd_remap) {
+      const int u = vt >> 3;
+      g = (vt & 7) + 8 * (u / tiles);
+      tile = u % tiles;
+    } else {
+      g = vt / tiles;
+      tile = vt % tiles;
+    }
+    i0 = (tile / tj) * BI;
+    j0 = (tile % tj) * BJ;
+  };
 
   const int w = wave_id();
   const int l = lane_id();
@@ -441,86 +445,118 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
   // loads blocks DMA w .. DMA w + DMA - 1. Lane l writes row 8 blk + l / 8 at physical
   // chunk l % 8, i.e. logical chunk (l % 8) ^ swz(row). 32-bit per-lane offsets from a scalar
   // base per operand (raw buffer loads).
-  const auto rsP = buf_rsrc(Pg, (unsigned)(BI * Np * 2));
-  const auto rsQ = buf_rsrc(Qg, (unsigned)(BJ * Np * 2));
-  int voff[DMA];
-#pragma unroll
-  for (int q = 0; q < DMA; ++q) {
-    const int blk = DMA * w + q;
-    const int row = (blk < BI / 8 ? blk : blk - BI / 8) * 8 + (l >> 3);
-    voff[q] = (row * Np + 8 * ((l & 7) ^ k2_swz(row))) * 2;
-  }
-  auto issue = [&](int kt) {
-    bf16* st = lds + (kt & 1) * Cfg::STAGE;
+  // The per-lane offsets are recomputed at each issue (a few VALU operations): the
+  // accumulators leave no registers to keep them in.
+  auto issue = [&](__amdgpu_buffer_rsrc_t rsP, __amdgpu_buffer_rsrc_t rsQ, int kt, int stage) {
+    bf16* st = lds + stage * Cfg::STAGE;
 #pragma unroll
     for (int q = 0; q < DMA; ++q) {
       const int blk = DMA * w + q;  // compile-time split per wave is not possible: w is uniform
-      buf_load_lds16(blk < BI / 8 ? rsP : rsQ, st + blk * 8 * KT, voff[q], kt * KT * 2);
+      const int row = (blk < BI / 8 ? blk : blk - BI / 8) * 8 + (l >> 3);
+      const int voff = (row * Np + 8 * ((l & 7) ^ k2_swz(row))) * 2;
+      buf_load_lds16(blk < BI / 8 ? rsP : rsQ, st + blk * 8 * KT, voff, kt * KT * 2);
     }
   };
+  auto rsrc_P = [&](int g, int i0) { return buf_rsrc(P + (size_t)g * pe + (size_t)i0 * Np, (unsigned)(BI * Np * 2)); };
+  auto rsrc_Q = [&](int g, int j0) { return buf_rsrc(Q + (size_t)g * pe + (size_t)j0 * Np, (unsigned)(BJ * Np * 2)); };
 
-  f32x16 acc[3][4];  // [j tile][i tile]
-#pragma unroll
-  for (int a = 0; a < 3; ++a)
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
-  const int nk = Np / KT;
+  const int nk = Np / KT;  // even (Np is a multiple of 768)
   const int r = l & 31;
   const int hf = l >> 5;
   const int sw = k2_swz(r);  // rows wi + 32 t + r and wj + 32 t + r share the swizzle of r
-  issue(0);
-  for (int kt = 0; kt < nk; ++kt) {
-    // s_waitcnt vmcnt(0) (other counters untouched): this wave's loads of tile kt landed.
-    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-    // All waves' loads of tile kt visible; stage (kt + 1) & 1 no longer read.
-    __builtin_amdgcn_s_barrier();
-    if (kt + 1 < nk) issue(kt + 1);
-    const bf16* Ps = lds + (kt & 1) * Cfg::STAGE;
-    const bf16* Qs = Ps + Cfg::PT;
-#pragma unroll
-    for (int kk = 0; kk < KT; kk += 16) {
-      const int c8 = 8 * ((kk / 8 + hf) ^ sw);
-      bf16x8 af[3], bfr[4];
-#pragma unroll
-      for (int t = 0; t < 3; ++t) af[t] = *reinterpret_cast<const bf16x8*>(Qs + (wj + 32 * t + r) * KT + c8);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) bfr[t] = *reinterpret_cast<const bf16x8*>(Ps + (wi + 32 * t + r) * KT + c8);
-#pragma unroll
-      for (int a = 0; a < 3; ++a)
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
-          acc[a][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[cc], acc[a][cc], 0, 0, 0);
-    }
-  }
-
-  // acc[a][c] element e: j = wj + 32 a + acc32_row(e), i = wi + 32 c + (lane & 31). Two passes
-  // of 128 rows i through LDS ([i][j], 784-byte rows), stored as whole 768-byte rows.
-  bf16* Xg = X + (size_t)g * pe + (size_t)i0 * Np + j0;
   const int tid = threadIdx.x;
+
+  int vt = blockIdx.x;
+  if (vt >= total) return;  // block-uniform
+  int g, i0, j0;
+  coords(vt, g, i0, j0);
+  auto rsP = rsrc_P(g, i0);
+  auto rsQ = rsrc_Q(g, j0);
+  issue(rsP, rsQ, 0, 0);
+  for (;;) {
+    const int nvt = vt + (int)gridDim.x;
+    const bool has_next = nvt < total;  // block-uniform
+    int ng = g, ni0 = i0, nj0 = j0;
+    if (has_next) coords(nvt, ng, ni0, nj0);
+    const auto nrsP = rsrc_P(ng, ni0);
+    const auto nrsQ = rsrc_Q(ng, nj0);
+
+    f32x16 acc[3][4];  // [j tile][i tile]
 #pragma unroll
-  for (int pass = 0; pass < BI / Cfg::OROWS; ++pass) {
-    __syncthreads();  // the ring (or the previous pass's stage) is no longer read
-    if (wi == pass * Cfg::OROWS) {
+    for (int a = 0; a < 3; ++a)
 #pragma unroll
-      for (int a = 0; a < 3; ++a)
+      for (int b = 0; b < 4; ++b)
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
+        for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+    for (int kt = 0; kt < nk; ++kt) {
+      // s_waitcnt vmcnt(0) (other counters untouched): this wave's loads of tile kt landed.
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+      // All waves' loads of tile kt visible; stage (kt + 1) & 1 no longer read.
+      __builtin_amdgcn_s_barrier();
+      if (kt + 1 < nk)
+        issue(rsP, rsQ, kt + 1, (kt + 1) & 1);
+      else if (has_next)
+        issue(nrsP, nrsQ, 0, 0);
+      const bf16* Ps = lds + (kt & 1) * Cfg::STAGE;
+      const bf16* Qs = Ps + Cfg::PT;
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            float v[4] = {acc[a][cc][4 * g4], acc[a][cc][4 * g4 + 1], acc[a][cc][4 * g4 + 2], acc[a][cc][4 * g4 + 3]};
-            store_vec<bf16, 4>(lds + (32 * cc + r) * Cfg::OLD + wj + 32 * a + acc32_row(4 * g4), v);
+      for (int kk = 0; kk < KT; kk += 16) {
+        const int c8 = 8 * ((kk / 8 + hf) ^ sw);
+        bf16x8 af[3], bfr[4];
+#pragma unroll
+        for (int t = 0; t < 3; ++t) af[t] = *reinterpret_cast<const bf16x8*>(Qs + (wj + 32 * t + r) * KT + c8);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bfr[t] = *reinterpret_cast<const bf16x8*>(Ps + (wi + 32 * t + r) * KT + c8);
+#pragma unroll
+        for (int a = 0; a < 3; ++a)
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc)
+            acc[a][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[cc], acc[a][cc], 0, 0, 0);
+      }
+    }
+
+    // acc[a][c] element e: j = wj + 32 a + acc32_row(e), i = wi + 32 c + (lane & 31). Four
+    // passes of 64 rows i through stage 1 ([i][j], 784-byte rows), stored as whole 768-byte
+    // rows; stage 0 is receiving the next tile's first k-tile meanwhile.
+    bf16* Xg = X + (size_t)g * pe + (size_t)i0 * Np + j0;
+    bf16* ost = lds + Cfg::STAGE;
+    // The store offsets are the same for every tile; the empty asm keeps the compiler from
+    // hoisting all 24 of them out of the tile loop (they would not fit in registers).
+    int t2 = tid;
+    asm volatile("" : "+v"(t2));
+#pragma unroll
+    for (int pass = 0; pass < BI / Cfg::OROWS; ++pass) {
+      __syncthreads();  // stage 1 (the last k-tile, or the previous pass) is no longer read
+      if (wi == (pass >> 1) * 128) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a)
+#pragma unroll
+          for (int c2 = 0; c2 < 2; ++c2) {
+            const int cc = 2 * (pass & 1) + c2;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              float v[4] = {acc[a][cc][4 * g4], acc[a][cc][4 * g4 + 1], acc[a][cc][4 * g4 + 2],
+                            acc[a][cc][4 * g4 + 3]};
+              store_vec<bf16, 4>(ost + (32 * c2 + r) * Cfg::OLD + wj + 32 * a + acc32_row(4 * g4), v);
+            }
           }
-    }
-    __syncthreads();
+      }
+      __syncthreads();
 #pragma unroll
-    for (int it = 0; it < Cfg::OROWS * BJ / 8 / Cfg::NT; ++it) {
-      const int idx = tid + it * Cfg::NT;
-      const int row = idx / (BJ / 8), ch = idx % (BJ / 8);
-      *reinterpret_cast<u32x4*>(Xg + (size_t)(pass * Cfg::OROWS + row) * Np + 8 * ch) =
-          *reinterpret_cast<const u32x4*>(lds + row * Cfg::OLD + 8 * ch);
+      for (int it = 0; it < Cfg::OROWS * BJ / 8 / Cfg::NT; ++it) {
+        const int idx = t2 + it * Cfg::NT;
+        const int row = idx / (BJ / 8), ch = idx % (BJ / 8);
+        *reinterpret_cast<u32x4*>(Xg + (pass * Cfg::OROWS + row) * Np + 8 * ch) =
+            *reinterpret_cast<const u32x4*>(ost + row * Cfg::OLD + 8 * ch);
+      }
     }
+    if (!has_next) break;
+    vt = nvt;
+    g = ng;
+    i0 = ni0;
+    j0 = nj0;
+    rsP = nrsP;
+    rsQ = nrsQ;
   }
 }
 
@@ -1355,7 +1391,12 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
                      Contract768::SMEM, hipGetErrorString(e));
           attr768 = true;
         }
-        dim3 grid((unsigned)(G * (Np / Contract768::BI) * (Np / Contract768::BJ)));
+        // Persistent: at most one block per CU, a multiple of 8 for the XCD remap.
+        const long total = (long)G * (Np / Contract768::BI) * (Np / Contract768::BJ);
+        PF_REQUIRE(total < (1L << 31), PF_ERR_UNSUPPORTED, "trimul_contract: B C = %d planes of Np = %d", G, Np);
+        long nblk = std::min<long>(total, pf::cu_count());
+        if (remap) nblk = std::max<long>(8, nblk & ~7L);
+        dim3 grid((unsigned)nblk);
         pf::KernelTimer timer_trimul_contract("trimul_contract", s);
         trimul_contract768_kernel<<<grid, Contract768::NT, Contract768::SMEM, s>>>((const bf16*)P, (const bf16*)Q,
                                                                                    (bf16*)X, G, Np, remap);
