@@ -67,8 +67,9 @@ def test_grid_attention_fully_masked_line_is_mean_of_v(dev):
 
 
 @pytest.mark.parametrize("transpose", [False, True])
-def test_grid_attention_bf16_rule(dev, transpose):
-    n = 96
+@pytest.mark.parametrize("n", [96, 130])
+def test_grid_attention_bf16_rule(dev, transpose, n):
+    print(f"[grid attn bf16 transpose={transpose} n={n}]", flush=True)
     sd = W.make_block_weights(23, perturb_affine=True)
     p = sub(sd, "pair_attn_col." if transpose else "pair_attn_row.")
     inp = W.make_inputs(n, seed=4, pad_random=6)
