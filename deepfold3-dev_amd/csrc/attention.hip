@@ -717,6 +717,13 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   for (int s = 0; s < QS; ++s) lsum[s][0] = lsum[s][1] = 0.f;
 
   __syncthreads();  // Q tiles
+  // bf16: this wave's Q fragments stay in registers for the whole key loop (16 VGPRs
+  // instead of four LDS reads per key block); fp32 reads them from LDS per block.
+  Frag16<TC> qreg[sizeof(TC) == 2 ? QS : 1];
+  if constexpr (sizeof(TC) == 2) {
+#pragma unroll
+    for (int s = 0; s < QS; ++s) qreg[s].load(qw + (32 * s + lq) * QLD + 16 * hf);
+  }
 
   // Every key-block step issues K/V/mask (NSET - 1 blocks ahead) and then one bias stage
   // (two blocks ahead); the prologue issues what steps -2 and -1 would have, so every
@@ -767,9 +774,13 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
     // Additive key mask first, then q k^T: a fully masked line rounds every logit to
     // the same -1e9 log2 e, as the reference's fp32 adds do.
     if (use_mask) mma_mask(sacc, mk, TC{});
-    Frag16<TC> qf;
-    qf.load(qw + R * QLD + 16 * hf);
-    mma32_16(sacc, kf, qf);
+    if constexpr (sizeof(TC) == 2) {
+      mma32_16(sacc, kf, qreg[s]);
+    } else {
+      Frag16<TC> qf;
+      qf.load(qw + R * QLD + 16 * hf);
+      mma32_16(sacc, kf, qf);
+    }
   };
 
   // FAST step: p = 2^s, row sums, O^T += V^T P^T.
