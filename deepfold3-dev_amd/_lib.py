@@ -59,6 +59,8 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "pf_evo_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "pf_evo_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "pf_grid_attn_redo_flags": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
+    "pf_evo_attn_redo_flags": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "pf_pair_bias_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
     "pf_layernorm_linear_workspace_bytes": (_sz, [_l, _i, _i]),
     "pf_layernorm_linear_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, _vp, _l, _i, _i, _i, _vp, _vp, _sz, _vp]),
@@ -153,3 +155,45 @@ def kernel_timer_read() -> tuple[float, int]:
 
 def kernel_timer_stop() -> None:
     call("pf_kernel_timer_stop")
+
+
+def check_out(name: str, out: torch.Tensor, like: torch.Tensor, shape=None, dtype=None) -> None:
+    """Refuse a caller-supplied ``out`` the kernels would write out of bounds of (or reinterpret)."""
+    shape = tuple(like.shape) if shape is None else tuple(shape)
+    dtype = like.dtype if dtype is None else dtype
+    if not out.is_contiguous() or out.dtype != dtype or tuple(out.shape) != shape or out.device != like.device:
+        raise NotActive(
+            name, f"out must be a contiguous {dtype} tensor of shape {shape} on {like.device}, "
+            f"got {out.dtype} {tuple(out.shape)} on {out.device} (contiguous={out.is_contiguous()})",
+        )  # fmt: skip
+
+
+# Redo bookkeeping of the flash-attention kernel (a test and debugging aid). While a
+# RedoRecorder is active, every attention call reads back its redo flags (one int32 per
+# wave of the fast pass; nonzero = recomputed by the exact running-maximum softmax) and
+# appends the number of flagged waves. Reading them synchronises the stream.
+_redo_log: list | None = None
+
+
+class RedoRecorder:
+    """``with RedoRecorder() as counts: ...`` collects one flagged-wave count per attention call."""
+
+    def __enter__(self) -> list:
+        global _redo_log
+        self._prev = _redo_log
+        _redo_log = []
+        return _redo_log
+
+    def __exit__(self, *exc) -> None:
+        global _redo_log
+        _redo_log = self._prev
+
+
+def note_redo(query: str, workspace: torch.Tensor, *sizes: int) -> None:
+    """Append the flagged-wave count of the call that just used ``workspace`` (if recording)."""
+    if _redo_log is None:
+        return
+    off, cnt = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    call(query, *sizes, ctypes.byref(off), ctypes.byref(cnt))
+    flags = workspace[off.value : off.value + 4 * cnt.value].view(torch.int32)
+    _redo_log.append(int((flags != 0).sum().item()))

@@ -562,7 +562,10 @@ PF_DEVICE Frag16<float> buf_frag16<float>(__amdgpu_buffer_rsrc_t r, int voff, in
 // L lines per batch item (line stride Lp in the operand buffers). O_HEAD_MAJOR writes O as
 // [b][line][h][q][d] with q < N (the reference kernel's layout) instead of the frame's
 // [b][line][q][h d]; zero_masked_lines writes 0 for a line whose keys are all masked (the
-// reference kernel's rule) instead of the eager path's uniform average.
+// reference kernel's rule) instead of the eager path's uniform average. POST_SCALE
+// multiplies the fp32 logit accumulator by `post_scale` after the q k^T products, so Q
+// reaches the MFMAs as given (no re-rounding of a pre-scaled Q to bf16) and the bias and
+// mask operands carry 1 / post_scale (the kernel-level op's fp32 post-scale).
 //
 // Two modes share this kernel. FAST keeps the softmax reference at 0 for the whole key loop:
 // no running maximum, no rescaling, only exp2, the row sum and the P V products per logit
@@ -572,11 +575,11 @@ PF_DEVICE Frag16<float> buf_frag16<float>(__amdgpu_buffer_rsrc_t r, int voff, in
 // outputs finite -- and writes a per-wave flag redo[blockIdx.x * 4 + wave]; a flagged block
 // is recomputed by the exact mode (FAST = false with `redo` set), which runs the lazy
 // running-maximum softmax below and skips every block whose flags are all 0.
-template <class TC, int QS, bool O_HEAD_MAJOR, bool FAST>
+template <class TC, int QS, bool O_HEAD_MAJOR, bool FAST, bool POST_SCALE = false>
 __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2)) void tri_attn_kernel(
     const TC* __restrict__ Q, const TC* __restrict__ K, const TC* __restrict__ Vt, const float* __restrict__ PB,
     const float* __restrict__ MA, TC* __restrict__ O, int B, int N, int Np, int L, int Lp, int zero_masked_lines,
-    int xcd_remap, int* __restrict__ redo) {
+    int xcd_remap, int* __restrict__ redo, float post_scale = 1.f) {
   constexpr int QB = 32 * QS;
   constexpr int NT = 64 * kLinesPerBlock;
   constexpr int QLD = kHeadDim + lds_pad<TC>();
@@ -765,21 +768,37 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
     const float mk = kb < nkb ? mf : -INFINITY;
     const int R = 32 * s + lq;
     const float* br = bl + R * 32;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x4 bv = *reinterpret_cast<const f32x4*>(br + 4 * ((4 * hf + i) ^ bias_swz(R)));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sacc[4 * i + e] = bv[e];
-    }
-    // Additive key mask first, then q k^T: a fully masked line rounds every logit to
-    // the same -1e9 log2 e, as the reference's fp32 adds do.
-    if (use_mask) mma_mask(sacc, mk, TC{});
     if constexpr (sizeof(TC) == 2) {
+      // bf16: the accumulator starts at the bias, then the key mask, then q k^T (two
+      // 32x32x16 steps, so the products meet the bias's magnitude twice).
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(br + 4 * ((4 * hf + i) ^ bias_swz(R)));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sacc[4 * i + e] = bv[e];
+      }
+      if (use_mask) mma_mask(sacc, mk, TC{});
       mma32_16(sacc, kf, qreg[s]);
     } else {
+      // fp32: q k^T from a zero accumulator (sixteen 32x32x2 steps), then the bias, then
+      // the key mask -- the eager order (q k^T scale + bias) + mask. Accumulating the
+      // sixteen partial products onto a large bias would round each at its magnitude.
       Frag16<TC> qf;
       qf.load(qw + R * QLD + 16 * hf);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
       mma32_16(sacc, kf, qf);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(br + 4 * ((4 * hf + i) ^ bias_swz(R)));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sacc[4 * i + e] += bv[e];
+      }
+      if (use_mask) mma_mask(sacc, mk, TC{});
+    }
+    if constexpr (POST_SCALE) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] *= post_scale;
     }
   };
 
@@ -809,20 +828,17 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
     }
   };
 
-  // Exact step: lazy running maximum (see kRaise / kLower).
+  // Exact step: lazy running maximum (see kRaise / kLower). The block maximum is taken
+  // over the raw logits and the reference is subtracted once, after it has been updated:
+  // a reference at the mask level (about -1.44e9, set by a first key block whose keys are
+  // all masked) subtracted from a real logit would round it to a multiple of 128, so it
+  // is never applied to a block that holds a real key -- that block's maximum exceeds it
+  // by far more than kRaise and replaces it first (alpha = 2^-1.44e9 = 0 then clears the
+  // masked keys' contributions).
   auto compute_exact = [&](int kb, int u, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf) {
     f32x16 sacc[QS];
 #pragma unroll
     for (int s = 0; s < QS; ++s) logits(kb, u, s, kf, mf, sacc[s]);
-    bool ref_set = false;
-#pragma unroll
-    for (int s = 0; s < QS; ++s) ref_set |= mref[s] != 0.f;
-    if (__any(ref_set)) {
-#pragma unroll
-      for (int s = 0; s < QS; ++s)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[s][r] -= mref[s];
-    }
     float mx[QS];
     bool any_shift = false;
 #pragma unroll
@@ -832,22 +848,29 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
       for (int r = 3; r < 15; r += 2) m = fmaxf(fmaxf(m, sacc[s][r]), sacc[s][r + 1]);
       m = fmaxf(m, sacc[s][15]);
       mx[s] = max_xor32(m);
-      any_shift |= mx[s] > kRaise || (kb == 0 && mx[s] < -kLower);
+      any_shift |= mx[s] - mref[s] > kRaise || (kb == 0 && mx[s] < -kLower);
     }
     if (__any(any_shift)) {
 #pragma unroll
       for (int s = 0; s < QS; ++s) {
-        const bool shift = mx[s] > kRaise || (kb == 0 && mx[s] < -kLower);
-        const float delta = shift ? mx[s] : 0.f;
-        const float alpha = kb == 0 ? 0.f : __builtin_amdgcn_exp2f(-delta);
-        mref[s] += delta;
+        const bool shift = mx[s] - mref[s] > kRaise || (kb == 0 && mx[s] < -kLower);
+        // kb == 0: nothing accumulated yet. Otherwise only raises reach here (mx - mref >
+        // kRaise), so the rescale factor is 2^(mref - mx) < 2^-kRaise.
+        const float alpha = !shift ? 1.f : (kb == 0 ? 0.f : __builtin_amdgcn_exp2f(mref[s] - mx[s]));
+        if (shift) mref[s] = mx[s];
         lrun[s] *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          o[s][r] *= alpha;
-          sacc[s][r] -= delta;
-        }
+        for (int r = 0; r < 16; ++r) o[s][r] *= alpha;
       }
+    }
+    bool ref_set = false;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) ref_set |= mref[s] != 0.f;
+    if (__any(ref_set)) {
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[s][r] -= mref[s];
     }
 #pragma unroll
     for (int s = 0; s < QS; ++s) {
@@ -880,38 +903,45 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
     kb0 += NSET;                                              \
     if (kb0 >= nkb) break;                                    \
   }
+  // Fully masked lines skip the key loop in both modes (closed form below), so the exact
+  // mode reproduces the fast mode's result for them bit for bit.
+  const bool live = active && !all_masked;  // wave-uniform
   if constexpr (FAST) {
-    const bool live = active && !all_masked;  // wave-uniform
     auto compute_live = [&](int kb, int u, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf) {
       if (live) compute_fast(kb, u, kf, vf, mf);
     };
     PF_TRI_ATTN_KEY_LOOP(compute_live)
-    if (active && all_masked) {
-      // Fully masked line: every logit carries the same -1e9 shift, so each real key
-      // weighs 1 (the eager rule's uniform average); V is summed outside the bias ring.
-      for (int kb = 0; kb < nkb; ++kb) {
-        const int k0 = kb * 32;
-        const Frag16<TC> vf = buf_frag16<TC>(rv, v_voff, k0 * v_kstride);
-        f32x16 pr;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) pr[r] = k0 + 8 * (r >> 2) + 4 * hf + (r & 3) < N ? 1.f : 0.f;
-        float c = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) c += pr[r];
-        const Frag16<TC> pf = pack_p(pr, TC{});
-#pragma unroll
-        for (int s = 0; s < QS; ++s) {
-          lsum[s][0] += c;
-          mma32_16(o[s], vf, pf);
-        }
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < QS; ++s) lrun[s] = lsum[s][0] + lsum[s][1];
   } else {
-    PF_TRI_ATTN_KEY_LOOP(compute_exact)
+    auto compute_live = [&](int kb, int u, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf) {
+      if (live) compute_exact(kb, u, kf, vf, mf);
+    };
+    PF_TRI_ATTN_KEY_LOOP(compute_live)
   }
 #undef PF_TRI_ATTN_KEY_LOOP
+  if (active && all_masked) {
+    // Fully masked line: every logit carries the same -1e9 shift, so each real key
+    // weighs 1 (the eager rule's uniform average); V is summed outside the bias ring.
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int k0 = kb * 32;
+      const Frag16<TC> vf = buf_frag16<TC>(rv, v_voff, k0 * v_kstride);
+      f32x16 pr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pr[r] = k0 + 8 * (r >> 2) + 4 * hf + (r & 3) < N ? 1.f : 0.f;
+      float c = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) c += pr[r];
+      const Frag16<TC> pf = pack_p(pr, TC{});
+#pragma unroll
+      for (int s = 0; s < QS; ++s) {
+        lsum[s][0] += c;
+        mma32_16(o[s], vf, pf);
+      }
+    }
+  }
+  // FAST: lrun is 0 here and lsum holds the row sums; exact: lsum is 0 except for a
+  // fully masked line.
+#pragma unroll
+  for (int s = 0; s < QS; ++s) lrun[s] += lsum[s][0] + lsum[s][1];
   // The last steps loaded repeat tiles into LDS; none may land after the block's LDS is
   // handed to another block.
   __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
@@ -1388,8 +1418,14 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
 // (triton/evo_attention.py:1198-1292): O = softmax(Q K^T d^-1/2 + pair_bias + res_mask) V
 // per (batch, line, head) with Q, K, V, O as [B][S][H][N][D], res_mask additive [B][S][N],
 // pair_bias [B][H][N][N] fp32. The operands are repacked into the attention frame (padded
-// to Np, Q pre-scaled by d^-1/2 log2 e, V transposed with the key-slot order, bias and mask
-// times log2 e) and run through the same flash kernel. -inf mask entries become -1e9.
+// to Np, V transposed with the key-slot order) and run through the same flash kernel. In
+// bf16 the kernel applies the fp32 post-scale the reference kernel uses
+// (evo_attention.py:100-109): Q is copied as given, the bias and mask are stored times
+// d^1/2, and the kernel multiplies the fp32 logit accumulator by d^-1/2 log2 e after the
+// q k^T products (a pre-scaled Q re-rounded to bf16 would perturb a logit by ~2^-9 of its
+// size). In fp32, Q is pre-scaled by d^-1/2 log2 e (one fp32 rounding) and the bias and mask
+// are stored times log2 e, which keeps large biases at their own fp32 precision.
+// -inf mask entries become -1e9.
 template <class TC>
 __global__ __launch_bounds__(256) void evo_pack_qk_kernel(const TC* __restrict__ q, const TC* __restrict__ k,
                                                           TC* __restrict__ Qw, TC* __restrict__ Kw, int N, int Np,
@@ -1441,24 +1477,24 @@ __global__ __launch_bounds__(256) void evo_pack_v_kernel(const TC* __restrict__ 
 }
 
 __global__ __launch_bounds__(256) void evo_pack_bias_kernel(const float* __restrict__ pb, float* __restrict__ PB,
-                                                            int N, int Np) {
+                                                            int N, int Np, float scale) {
   const size_t bh = blockIdx.y;
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (long)Np * Np) return;
   const int qi = (int)(idx / Np);
   const int sl = (int)(idx % Np);
   const int kk = (sl & ~31) + slot_key(sl & 31);
-  PB[bh * Np * Np + idx] = (qi < N && kk < N) ? pb[(bh * N + qi) * N + kk] * kLog2e : 0.f;
+  PB[bh * Np * Np + idx] = (qi < N && kk < N) ? pb[(bh * N + qi) * N + kk] * scale : 0.f;
 }
 
 __global__ __launch_bounds__(256) void evo_pack_mask_kernel(const float* __restrict__ rm, float* __restrict__ MA,
-                                                            int N, int Np) {
+                                                            int N, int Np, float scale) {
   const size_t bs = blockIdx.y;
   const int sl = blockIdx.x * 256 + threadIdx.x;
   if (sl >= Np) return;
   const int kk = (sl & ~31) + slot_key(sl & 31);
   float v = -INFINITY;
-  if (kk < N) v = fmaxf(rm[bs * N + kk], -1e9f) * kLog2e;
+  if (kk < N) v = fmaxf(rm[bs * N + kk], -1e9f) * scale;
   MA[bs * Np + sl] = v;
 }
 
@@ -1499,15 +1535,21 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   float* PBw = reinterpret_cast<float*>(base + L.pb);
   float* MAw = reinterpret_cast<float*>(base + L.ma);
   int* redo = reinterpret_cast<int*>(base + L.redo);
-  const float qscale = (1.0f / sqrtf((float)kHeadDim)) * kLog2e;
+  // logit (log2 units): bf16 post * (q k^T + (bias + mask) d^1/2) with post = d^-1/2 log2 e;
+  // fp32 (q d^-1/2 log2 e) k^T + (bias + mask) log2 e.
+  constexpr bool kPost = sizeof(TC) == 2;
+  const float softmax_scale = 1.0f / sqrtf((float)kHeadDim);
+  const float qscale = kPost ? 1.f : softmax_scale * kLog2e;
+  const float bscale = kPost ? 1.f / softmax_scale : kLog2e;
+  const float post = softmax_scale * kLog2e;
   const unsigned bsh = (unsigned)(B * S * kHeads);
   constexpr int VEC = 16 / sizeof(TC);
   evo_pack_qk_kernel<TC><<<dim3((Np * (kHeadDim / VEC) + 255) / 256, bsh), 256, 0, s>>>(
       (const TC*)q, (const TC*)k, Qw, Kw, N, Np, qscale);
   evo_pack_v_kernel<TC><<<dim3(Np / 32, bsh), 256, 0, s>>>((const TC*)v, Vw, N, Np);
   evo_pack_bias_kernel<<<dim3((unsigned)(((long)Np * Np + 255) / 256), B * kHeads), 256, 0, s>>>(pair_bias, PBw,
-                                                                                                   N, Np);
-  evo_pack_mask_kernel<<<dim3((Np + 255) / 256, B * S), 256, 0, s>>>(res_mask, MAw, N, Np);
+                                                                                                   N, Np, bscale);
+  evo_pack_mask_kernel<<<dim3((Np + 255) / 256, B * S), 256, 0, s>>>(res_mask, MAw, N, Np, bscale);
   if (int e = pf::check_launch("evo_attn pack")) return e;
   constexpr int QS = attn_qsub<TC>();
   constexpr int NT = 64 * kLinesPerBlock;
@@ -1516,11 +1558,11 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   const long total = (long)B * nlg * kHeads * nqb;
   const int remap = (total % 8 == 0) ? 1 : 0;
   pf::KernelTimer timer("evo_attn", s);
-  tri_attn_kernel<TC, QS, true, true><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
-      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo);
+  tri_attn_kernel<TC, QS, true, true, kPost><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
+      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post);
   if (int e = pf::check_launch("evo_attn")) return e;
-  tri_attn_kernel<TC, QS, true, false><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
-      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo);
+  tri_attn_kernel<TC, QS, true, false, kPost><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
+      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post);
   timer.stop();
   return pf::check_launch("evo_attn redo");
 }
@@ -1560,6 +1602,31 @@ int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const 
                                          workspace, s);
   return grid_attn_launch<bf16, bf16>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, transpose, out, accumulate,
                                       workspace, s);
+}
+
+// Number of redo flags the fast flash pass writes: one per wave of its grid.
+static size_t redo_flag_count(int B, int L, int Np, int cdtype) {
+  const int QS = cdtype == PF_F32 ? attn_qsub<float>() : attn_qsub<bf16>();
+  const size_t nlg = (size_t)(L + kLinesPerBlock - 1) / kLinesPerBlock;
+  return (size_t)B * nlg * kHeads * (size_t)(Np / (32 * QS)) * kLinesPerBlock;
+}
+
+int pf_grid_attn_redo_flags(int B, int N, int C, int H, int cdtype, size_t* offset, size_t* count) {
+  PF_REQUIRE(offset && count, PF_ERR_INVALID_ARG, "pf_grid_attn_redo_flags: null pointer");
+  PF_REQUIRE(B > 0 && N > 0 && C == kC && H == kHeads && (cdtype == PF_F32 || cdtype == PF_BF16),
+             PF_ERR_UNSUPPORTED, "pf_grid_attn_redo_flags: B=%d N=%d C=%d H=%d cdtype=%d", B, N, C, H, cdtype);
+  *offset = attn_ws_layout(B, N, cdtype).redo;
+  *count = redo_flag_count(B, N, pf::pad128(N), cdtype);
+  return pf::ok();
+}
+
+int pf_evo_attn_redo_flags(int B, int S, int H, int N, int D, int dtype, size_t* offset, size_t* count) {
+  PF_REQUIRE(offset && count, PF_ERR_INVALID_ARG, "pf_evo_attn_redo_flags: null pointer");
+  PF_REQUIRE(B > 0 && S > 0 && N > 0 && H == kHeads && D == kHeadDim && (dtype == PF_F32 || dtype == PF_BF16),
+             PF_ERR_UNSUPPORTED, "pf_evo_attn_redo_flags: B=%d S=%d N=%d H=%d D=%d dtype=%d", B, S, N, H, D, dtype);
+  *offset = evo_ws_layout(B, S, N, dtype).redo;
+  *count = redo_flag_count(B, S, pf::pad128(N), dtype);
+  return pf::ok();
 }
 
 size_t pf_evo_attn_workspace_bytes(int B, int S, int H, int N, int D, int dtype) {

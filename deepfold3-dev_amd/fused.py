@@ -79,6 +79,7 @@ class _EvoformerAttention:
             "pf_evo_attn_fwd", Q.data_ptr(), K.data_ptr(), V.data_ptr(), rm.data_ptr(), pb.data_ptr(), B, S, H, N, D,
             code, int(masked_rows == "zero"), out.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(Q),
         )  # fmt: skip
+        _lib.note_redo("pf_evo_attn_redo_flags", ws, B, S, H, N, D, code)
         if not pre_transposed:
             out = out.transpose(-2, -3).contiguous()
         return out

@@ -69,7 +69,10 @@ def residual_add(res: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = 
     if res.shape != x.shape:
         raise NotActive("residual_add", f"shape mismatch {tuple(res.shape)} vs {tuple(x.shape)}")
     res_c, x_c = res.contiguous(), x.contiguous()
-    out = torch.empty_like(res_c) if out is None else out
+    if out is None:
+        out = torch.empty_like(res_c)
+    else:
+        _lib.check_out("residual_add", out, res_c)
     _lib.call(
         "pf_add", res_c.data_ptr(), _lib.dtype_code(res_c.dtype), x_c.data_ptr(), _lib.dtype_code(x_c.dtype),
         out.data_ptr(), res_c.numel(), _lib.stream_of(res_c),
@@ -157,8 +160,8 @@ def trimul_forward(
         if accumulate:
             raise ValueError("accumulate=True needs an explicit out tensor")
         out = torch.empty_like(zc)
-    elif not out.is_contiguous() or out.dtype != z.dtype or out.shape != z.shape:
-        raise NotActive("fused_trimul", "out must be a contiguous tensor like z")
+    else:
+        _lib.check_out("fused_trimul", out, zc)
     code_c = _lib.dtype_code(cdt)
     ws_bytes = _lib.lib().pf_trimul_workspace_bytes(B, N, C, code_c)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=z.device)
@@ -245,6 +248,8 @@ def grid_attention_forward(
         if accumulate:
             raise ValueError("accumulate=True needs an explicit out tensor")
         out = torch.empty_like(zc)
+    else:
+        _lib.check_out("GridSelfAttention", out, zc)
     code_c = _lib.dtype_code(cdt)
     ws_bytes = _lib.lib().pf_grid_attn_workspace_bytes(B, N, C, num_heads, code_c)
     ws = _workspace(ws_bytes, z.device)
@@ -253,6 +258,7 @@ def grid_attention_forward(
         w_packed.data_ptr(), w_out.data_ptr(), B, N, C, num_heads, int(transpose), _lib.dtype_code(z.dtype), code_c,
         out.data_ptr(), int(accumulate), ws.data_ptr(), ws_bytes, _lib.stream_of(zc),
     )  # fmt: skip
+    _lib.note_redo("pf_grid_attn_redo_flags", ws, B, N, C, num_heads, code_c)
     return out
 
 
@@ -283,6 +289,8 @@ def pair_transition_forward(
         if accumulate:
             raise ValueError("accumulate=True needs an explicit out tensor")
         out = torch.empty_like(xc)
+    else:
+        _lib.check_out("FusedTransitionBlock", out, xc)
     M = xc.numel() // C
     logits = None
     s2p_args = [None, None, 0.0, None, None, 0]
@@ -335,6 +343,8 @@ def transition_forward(
         if accumulate:
             raise ValueError("accumulate=True needs an explicit out tensor")
         out = torch.empty_like(xc)
+    else:
+        _lib.check_out("TransitionBlock", out, xc)
     M = xc.numel() // C
     code_c = _lib.dtype_code(w1.dtype)
     ws_bytes = _lib.lib().pf_transition_workspace_bytes(M, C, factor, code_c)
@@ -376,6 +386,8 @@ def single_attention_forward(
         if accumulate:
             raise ValueError("accumulate=True needs an explicit out tensor")
         out = torch.empty_like(sc)
+    else:
+        _lib.check_out("SingleAttention", out, sc)
     code_c = _lib.dtype_code(w_qkvg.dtype)
     ws_bytes = _lib.lib().pf_single_attn_workspace_bytes(B, N, C, num_heads, code_c)
     ws = _workspace(ws_bytes, s.device)

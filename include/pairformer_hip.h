@@ -160,6 +160,14 @@ size_t pf_evo_attn_workspace_bytes(int B, int S, int H, int N, int D, int dtype)
 int pf_evo_attn_fwd(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias, int B,
                     int S, int H, int N, int D, int dtype, int masked_rows_zero, void* out, void* workspace,
                     size_t workspace_bytes, void* stream);
+/* Redo flags of the flash-attention kernel (no counterpart in the reference: a test and
+ * debugging aid). The kernel first runs a fast pass whose softmax keeps no running
+ * maximum; every wave checks its row sums and outputs and writes one int32 flag, and a
+ * nonzero flag makes the exact pass (running maximum) recompute that wave's block of
+ * lines. Once a pf_grid_attn_fwd / pf_evo_attn_fwd call with the same sizes has completed
+ * on its stream, its workspace holds *count such flags starting at byte *offset. */
+int pf_grid_attn_redo_flags(int B, int N, int C, int H, int cdtype, size_t* offset, size_t* count);
+int pf_evo_attn_redo_flags(int B, int S, int H, int N, int D, int dtype, size_t* offset, size_t* count);
 /* FusedPairBias(c, H)(z, ln_w, ln_b, proj_w, mask) (triton/fused_pair_bias.py:348-416):
  * z [B,N,N,C] -> out [B,H,N,N] in z's dtype; proj_w16 [16, C] fp32 (proj_w padded with zero
  * rows); mask [B,N] fp32 or NULL adds (1 - mask) * (-1e9) on the last axis. C = 128, H <= 16. */

@@ -121,6 +121,16 @@ def test_config4_trunk48_n768_bf16(dev):
     assert torch.isfinite(p).all() and torch.isfinite(s).all()
     _report("config 4 pair after 48 blocks", p, ep, rp)
     _report("config 4 single after 48 blocks", s, es, rs)
+    # The path bench.py times: PairFormerStack.forward runs block i's single half on a
+    # second stream beside block i + 1's pair half. It must give the block-by-block result
+    # bit for bit (the kernels have no atomics and a static tiling).
+    del ep, es, rp, rs
+    with torch.no_grad():
+        sp, ss = stack(x["pair"].to(BF), x["single"].to(BF), pm, sm)
+    torch.cuda.synchronize()
+    print("[config 4] two-stream stack vs block by block:", torch.equal(sp, p), torch.equal(ss, s), flush=True)
+    assert torch.equal(sp, p), f"pair differs, max {(sp.float() - p.float()).abs().max().item():.3e}"
+    assert torch.equal(ss, s), f"single differs, max {(ss.float() - s.float()).abs().max().item():.3e}"
 
 
 def _evo_inputs_n2048(dev):
