@@ -70,7 +70,14 @@ SIGNATURES: dict[str, tuple] = {
         _i,
         [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
     ),
+    "pf_single_attn_fwd_noalloc": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _vp],
+    ),
 }
+
+# Capacity of the library's static scratch array (PF_NOALLOC_SCRATCH_BYTES in the header).
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _lib = None
 

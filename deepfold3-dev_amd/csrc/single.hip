@@ -12,6 +12,7 @@
 // flash kernel on 32x32 MFMAs (V transposed once into key-slot order by a pack kernel,
 // keys split over the four waves of a block and merged through LDS).
 #include <algorithm>
+#include <mutex>
 
 #include "capi.h"
 #include "common.h"
@@ -396,6 +397,58 @@ bool dtype_pair_ok(int zd, int cd) {
   return (zd == PF_F32 || zd == PF_BF16) && (cd == PF_F32 || cd == PF_BF16) && !(zd == PF_BF16 && cd == PF_F32);
 }
 
+// Argument checks shared by pf_single_attn_fwd and its allocation-free variant.
+int single_attn_check(const char* fn, const void* s, const float* seq_mask, const float* pair_logits,
+                      const float* ln_w, const float* ln_b, const void* w_qkvg, const float* q_bias,
+                      const void* w_out, int B, int N, int C, int H, int zdtype, int cdtype, const void* out) {
+  PF_REQUIRE(s && seq_mask && pair_logits && ln_w && ln_b && w_qkvg && q_bias && w_out && out, PF_ERR_INVALID_ARG,
+             "%s: null pointer", fn);
+  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "%s: B=%d N=%d", fn, B, N);
+  PF_REQUIRE(H > 0 && H * kSHeadDim == C && C % 32 == 0, PF_ERR_UNSUPPORTED,
+             "%s: C=%d H=%d (built: head dim 24, C a multiple of 32)", fn, C, H);
+  PF_REQUIRE(dtype_pair_ok(zdtype, cdtype), PF_ERR_UNSUPPORTED, "%s: dtype pair (%d, %d)", fn, zdtype, cdtype);
+  return PF_OK;
+}
+
+// ---- scratch of the allocation-free entry point (pf_single_attn_fwd_noalloc)
+// One array per GPU, created with the code object when the library's kernels load on that
+// device and held until the process ends. In host code `scratch` names a host-side
+// stand-in, not device memory: kernels only ever receive the per-device address that
+// hipGetSymbolAddress returns for it (scratch_base below).
+static __device__ __align__(256) unsigned char scratch[PF_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_base[kMaxDevices] = {};
+
+// Address of `scratch` on the device that `stream` runs on, looked up once per device with
+// that device current.
+int scratch_base(hipStream_t stream, void** base) {
+  int dev = -1;
+  if (stream != nullptr) {
+    PF_REQUIRE(hipStreamGetDevice(stream, &dev) == hipSuccess, PF_ERR_LAUNCH,
+               "pf_single_attn_fwd_noalloc: hipStreamGetDevice failed");
+  } else {
+    PF_REQUIRE(hipGetDevice(&dev) == hipSuccess, PF_ERR_LAUNCH, "pf_single_attn_fwd_noalloc: hipGetDevice failed");
+  }
+  PF_REQUIRE(dev >= 0 && dev < kMaxDevices, PF_ERR_UNSUPPORTED, "pf_single_attn_fwd_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_base[dev] == nullptr) {
+    int cur = -1;
+    PF_REQUIRE(hipGetDevice(&cur) == hipSuccess, PF_ERR_LAUNCH, "pf_single_attn_fwd_noalloc: hipGetDevice failed");
+    if (cur != dev)
+      PF_REQUIRE(hipSetDevice(dev) == hipSuccess, PF_ERR_LAUNCH, "pf_single_attn_fwd_noalloc: hipSetDevice(%d)", dev);
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    PF_REQUIRE(e == hipSuccess && p != nullptr, PF_ERR_LAUNCH,
+               "pf_single_attn_fwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_base[dev] = p;
+  }
+  *base = g_scratch_base[dev];
+  return PF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -412,19 +465,38 @@ int pf_single_attn_fwd(const void* s, const float* seq_mask, const float* pair_l
                        const float* ln_b, float eps, const void* w_qkvg, const float* q_bias, const void* w_out, int B,
                        int N, int C, int H, int zdtype, int cdtype, void* out, int accumulate, void* workspace,
                        size_t workspace_bytes, void* stream) {
-  PF_REQUIRE(s && seq_mask && pair_logits && ln_w && ln_b && w_qkvg && q_bias && w_out && out && workspace,
-             PF_ERR_INVALID_ARG, "pf_single_attn_fwd: null pointer");
-  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_single_attn_fwd: B=%d N=%d", B, N);
-  PF_REQUIRE(H * kSHeadDim == C && C % 32 == 0, PF_ERR_UNSUPPORTED,
-             "pf_single_attn_fwd: C=%d H=%d (built: head dim 24, C a multiple of 32)", C, H);
-    PF_REQUIRE(dtype_pair_ok(zdtype, cdtype), PF_ERR_UNSUPPORTED, "pf_single_attn_fwd: dtype pair (%d, %d)", zdtype,
-             cdtype);
+  if (int e = single_attn_check("pf_single_attn_fwd", s, seq_mask, pair_logits, ln_w, ln_b, w_qkvg, q_bias, w_out, B,
+                                N, C, H, zdtype, cdtype, out))
+    return e;
+  PF_REQUIRE(workspace != nullptr, PF_ERR_INVALID_ARG, "pf_single_attn_fwd: null workspace");
   PF_REQUIRE(workspace_bytes >= pf_single_attn_workspace_bytes(B, N, C, H, cdtype), PF_ERR_WORKSPACE,
              "pf_single_attn_fwd: workspace %zu < %zu bytes", workspace_bytes,
              pf_single_attn_workspace_bytes(B, N, C, H, cdtype));
   hipStream_t st = pf::as_stream(stream);
   return PF_DISPATCH_ZC(zdtype, cdtype, single_attn_launch, s, seq_mask, pair_logits, ln_w, ln_b, eps, w_qkvg, q_bias,
                         w_out, B, N, C, H, out, accumulate, workspace, st);
+}
+
+int pf_single_attn_fwd_noalloc(const void* s, const float* seq_mask, const float* pair_logits, const float* ln_w,
+                               const float* ln_b, float eps, const void* w_qkvg, const float* q_bias, const void* w_out,
+                               int B, int N, int C, int H, int zdtype, int cdtype, void* out, int accumulate,
+                               void* stream) {
+  if (int e = single_attn_check("pf_single_attn_fwd_noalloc", s, seq_mask, pair_logits, ln_w, ln_b, w_qkvg, q_bias,
+                                w_out, B, N, C, H, zdtype, cdtype, out))
+    return e;
+  const size_t need = pf_single_attn_workspace_bytes(B, N, C, H, cdtype);
+  PF_REQUIRE(need <= PF_NOALLOC_SCRATCH_BYTES, PF_ERR_WORKSPACE,
+             "pf_single_attn_fwd_noalloc: B=%d N=%d C=%d needs %zu bytes of scratch, more than the %u-byte static "
+             "array; use pf_single_attn_fwd with a workspace",
+             B, N, C, need, (unsigned)PF_NOALLOC_SCRATCH_BYTES);
+  hipStream_t st = pf::as_stream(stream);
+  void* base = nullptr;
+  if (int e = scratch_base(st, &base)) return e;
+  // Every byte of the scratch a call reads is written earlier in the same call (LayerNorm
+  // rows, projections, the packed V^T and mask including their padding, the attention
+  // output), so nothing is cleared.
+  return PF_DISPATCH_ZC(zdtype, cdtype, single_attn_launch, s, seq_mask, pair_logits, ln_w, ln_b, eps, w_qkvg, q_bias,
+                        w_out, B, N, C, H, out, accumulate, base, st);
 }
 
 int pf_swiglu_fwd(const void* x, int dtype, void* y, long M, int D, void* stream) {

@@ -147,6 +147,20 @@ int pf_single_attn_fwd(const void* s, const float* seq_mask, const float* pair_l
                        const float* ln_b, float eps, const void* w_qkvg, const float* q_bias, const void* w_out, int B,
                        int N, int C, int H, int zdtype, int cdtype, void* out, int accumulate, void* workspace,
                        size_t workspace_bytes, void* stream);
+/* Allocation-free variant of pf_single_attn_fwd. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments and results as pf_single_attn_fwd
+ * without the workspace: the scratch lives in a library-owned static device array of
+ * PF_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load on that GPU until the
+ * process ends. Sizes whose pf_single_attn_workspace_bytes exceeds it return
+ * PF_ERR_WORKSPACE (bf16: about 5.6 KB per token, so B*N up to ~5900; fp32 ~2900). Every
+ * call on one GPU uses the same array: calls that overlap on one GPU (two streams, two
+ * threads) race. The call allocates and frees nothing. */
+#define PF_NOALLOC_SCRATCH_BYTES (32u << 20)
+int pf_single_attn_fwd_noalloc(const void* s, const float* seq_mask, const float* pair_logits, const float* ln_w,
+                               const float* ln_b, float eps, const void* w_qkvg, const float* q_bias, const void* w_out,
+                               int B, int N, int C, int H, int zdtype, int cdtype, void* out, int accumulate,
+                               void* stream);
 
 /* ---- kernel-level operators of the reference's Triton layer -------------- */
 /* _EvoformerAttention.apply(Q, K, V, res_mask, pair_bias, pre_transposed=True)

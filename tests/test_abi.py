@@ -54,3 +54,21 @@ def test_cpu_tensors_are_refused():
     NotActive = mod("inference_guard").NotActive
     with pytest.raises(NotActive):
         k.layer_norm(torch.randn(4, 128), torch.ones(128), torch.zeros(128))
+
+
+def test_noalloc_single_attention_refuses_oversize_without_gpu():
+    """The allocation-free entry point refuses sizes whose scratch exceeds its static array
+    before any device call (dummy non-null pointers; nothing is launched)."""
+    lib = _lib.lib()
+    C, H = 384, 16
+    per_item = lib.pf_single_attn_workspace_bytes(1, 200, C, H, _lib.PF_BF16)
+    B = _lib.NOALLOC_SCRATCH_BYTES // per_item + 1
+    assert lib.pf_single_attn_workspace_bytes(B, 200, C, H, _lib.PF_BF16) > _lib.NOALLOC_SCRATCH_BYTES
+    d = 16  # a non-null address the call must never dereference
+    status = lib.pf_single_attn_fwd_noalloc(
+        d, d, d, d, d, 1e-5, d, d, d, B, 200, C, H, _lib.PF_BF16, _lib.PF_BF16, d, 0, None
+    )
+    assert status == 3  # PF_ERR_WORKSPACE
+    assert b"static" in lib.pf_last_error()
+    with open(_lib.HEADER_PATH) as f:
+        assert f"#define PF_NOALLOC_SCRATCH_BYTES (32u << 20)" in f.read()
