@@ -1,77 +1,136 @@
-"""Which kernel each dispatch site ran.
+"""A per-process ledger of which kernel path each dispatch site took.
 
-Mirrors the reference's census (``src/deepfold3/model/kernel_census.py:45-135``):
-each dispatch site calls :func:`record` with the path it took, refusals are
-recorded as ``refused:<reason>``, and :func:`snapshot` returns the tally.
-Counts are per process and deliberately unsynchronised (a plain dict update),
-like the reference's.
+Public interface as in the reference's census (``src/deepfold3/model/kernel_census.py``;
+callers such as its ``scripts/inference.py:957-959`` write ``snapshot()``,
+``shadowed()`` and ``inactive()`` into run manifests):
+
+- ``record(site, path)``: one dispatch of ``site`` through ``path``; refusals use the
+  path ``"refused:<reason>"``.
+- ``requested(site, lever)``: a lever was enabled for ``site`` at construction.
+- ``shadowed()``: ``"site:lever"`` for every requested lever whose site has dispatched,
+  but never through that lever. A path ``"<lever>_<variant>"`` (``"hip_tri_attn_row"``
+  for the lever ``"hip"``) counts as the lever's.
+- ``inactive(lever, reason)``: a lever gated off at construction (logged once); with no
+  argument, the levers gated off so far.
+- ``snapshot()`` ``{site: {path: count}}``, ``format_census()`` a readable summary,
+  ``reset_counts()`` / ``reset()``, ``warn_once(key)``.
+
+Here the ledger is one object holding a ``Counter`` over ``(site, path)`` pairs, updated
+under a lock, so concurrent dispatch from several threads (the trunk's second stream is
+driven from the same thread, but callers may use more) keeps exact counts.
 """
 
 from __future__ import annotations
 
 import logging
-from collections import defaultdict
+import threading
+from collections import Counter
 
-__all__ = ["inactive", "record", "requested", "shadowed", "snapshot", "reset_counts", "reset", "format_census"]
+__all__ = [
+    "record",
+    "requested",
+    "inactive",
+    "snapshot",
+    "shadowed",
+    "warn_once",
+    "reset_counts",
+    "reset",
+    "format_census",
+]
 
-logger = logging.getLogger(__name__)
+_log = logging.getLogger(__name__)
 
-_counts: defaultdict[str, defaultdict[str, int]] = defaultdict(lambda: defaultdict(int))
-_requested: dict[str, str] = {}
-_inactive: dict[str, str] = {}
+
+class _Ledger:
+    def __init__(self) -> None:
+        self.lock = threading.Lock()
+        self.hits: Counter[tuple[str, str]] = Counter()
+        self.levers: set[tuple[str, str]] = set()  # (site, lever) enabled at construction
+        self.gated: dict[str, str] = {}  # lever -> reason, in the order first seen
+        self.warned: set[str] = set()
+
+    def paths_of(self, site: str) -> set[str]:
+        return {p for (s, p) in self.hits if s == site}
+
+
+_LEDGER = _Ledger()
 
 
 def record(site: str, path: str) -> None:
-    """Note that ``site`` dispatched to ``path`` once."""
-    _counts[site][path] += 1
+    """Count one dispatch of ``site`` through ``path``."""
+    with _LEDGER.lock:
+        _LEDGER.hits[(site, path)] += 1
 
 
 def requested(site: str, lever: str) -> None:
-    """Note at construction that ``lever`` is enabled for ``site``."""
-    _requested[f"{site}:{lever}"] = site
+    """Remember that ``lever`` is enabled for ``site`` (called at construction)."""
+    with _LEDGER.lock:
+        _LEDGER.levers.add((site, lever))
 
 
 def inactive(lever: str | None = None, reason: str = "") -> dict[str, str]:
-    """Note a lever gated off at construction; return all such levers."""
-    if lever is not None and lever not in _inactive:
-        _inactive[lever] = reason
-        logger.warning("NOT ACTIVE: %s: %s", lever, reason)
-    return dict(_inactive)
+    """Register ``lever`` as gated off for ``reason`` (first registration wins and is
+    logged); return every gated lever with its reason."""
+    with _LEDGER.lock:
+        new = lever is not None and lever not in _LEDGER.gated
+        if new:
+            _LEDGER.gated[lever] = reason
+        gated = dict(_LEDGER.gated)
+    if new:
+        _log.warning("kernel lever %s is gated off: %s", lever, reason)
+    return gated
 
 
 def snapshot() -> dict[str, dict[str, int]]:
-    """The tally so far, ``{site: {path: count}}``."""
-    return {site: dict(paths) for site, paths in sorted(_counts.items())}
-
-
-def shadowed() -> list[str]:
-    """Levers enabled at construction whose site dispatched, but never to them."""
-    out = []
-    for key, site in sorted(_requested.items()):
-        lever = key.split(":", 1)[1]
-        paths = _counts.get(site)
-        if paths and lever not in paths:
-            out.append(key)
+    """``{site: {path: count}}``, sites and paths in sorted order."""
+    with _LEDGER.lock:
+        items = sorted(_LEDGER.hits.items())
+    out: dict[str, dict[str, int]] = {}
+    for (site, path), n in items:
+        out.setdefault(site, {})[path] = n
     return out
 
 
+def shadowed() -> list[str]:
+    """Requested levers whose site dispatched but never through them, as ``site:lever``."""
+    with _LEDGER.lock:
+        levers = sorted(_LEDGER.levers)
+        taken = {site: _LEDGER.paths_of(site) for site, _ in levers}
+
+    def used(lever: str, paths: set[str]) -> bool:
+        return any(p == lever or p.startswith(lever + "_") for p in paths)
+
+    return [f"{site}:{lever}" for site, lever in levers if taken[site] and not used(lever, taken[site])]
+
+
+def warn_once(key: str) -> bool:
+    """True the first time ``key`` is seen in this process, False afterwards."""
+    with _LEDGER.lock:
+        if key in _LEDGER.warned:
+            return False
+        _LEDGER.warned.add(key)
+        return True
+
+
 def reset_counts() -> None:
-    """Clear the tally, keep the requested levers."""
-    _counts.clear()
+    """Forget the dispatch counts; keep requested and gated levers."""
+    with _LEDGER.lock:
+        _LEDGER.hits.clear()
 
 
 def reset() -> None:
-    """Clear everything (tests)."""
-    _counts.clear()
-    _requested.clear()
-    _inactive.clear()
+    """Forget everything (for tests)."""
+    with _LEDGER.lock:
+        _LEDGER.hits.clear()
+        _LEDGER.levers.clear()
+        _LEDGER.gated.clear()
+        _LEDGER.warned.clear()
 
 
 def format_census() -> str:
-    """One line per site, plus shadowed and inactive levers."""
-    lines = [f"{site}: " + ", ".join(f"{p}={n}" for p, n in sorted(paths.items())) for site, paths in snapshot().items()]
-    for key in shadowed():
-        lines.append(f"SHADOWED {key}")
-    for lever, reason in _inactive.items():
-        lines.append(f"NOT ACTIVE {lever} - {reason}")
-    return "\n".join(lines) if lines else "(no kernel dispatch recorded)"
+    """A summary: one ``site  path xN`` line per path, then shadowed and gated levers."""
+    snap = snapshot()
+    rows = [f"{site}  {path} x{n}" for site, paths in snap.items() for path, n in paths.items()]
+    rows += [f"shadowed lever: {key}" for key in shadowed()]
+    rows += [f"gated lever: {lever} ({why})" for lever, why in inactive().items()]
+    return "\n".join(rows) if rows else "no kernel dispatch recorded"

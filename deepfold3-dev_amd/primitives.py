@@ -83,17 +83,27 @@ class TransitionBlock(nn.Module):
     other shape runs LayerNorm + two MFMA row GEMMs.
     """
 
-    def __init__(self, c: int, n: int = 4, optim=None, linear_out_init_gain: float | None = None):
+    def __init__(
+        self,
+        channels: int,
+        num_intermediate_factor: int = 4,
+        optim=None,
+        linear_out_init_gain: float | None = None,
+    ):
         super().__init__()
         from .config import require_hip
 
         require_hip("TransitionBlock", optim)
+        c, n = channels, num_intermediate_factor
         self.c, self.n = c, n
         self.norm = LayerNorm(c)
-        self.linear1 = LinearNoBias(c, 2 * n * c)
+        # Default init as the reference's (primitives.py:219-238): linear1 ("linear_gate",
+        # feeding SwiGLU) with the AF3 "relu" scaling, linear2 zero, or, with
+        # linear_out_init_gain, a row-orthogonal linear2 scaled by that gain.
+        self.linear1 = LinearNoBias(c, 2 * n * c, initializer="relu")
         self.linear2 = LinearNoBias(n * c, c, initializer="zeros")
         if linear_out_init_gain is not None:
-            nn.init.normal_(self.linear2.weight, std=linear_out_init_gain / math.sqrt(n * c))
+            nn.init.orthogonal_(self.linear2.weight, gain=float(linear_out_init_gain))
         self._cache = WeightCache()
 
     @property
@@ -129,10 +139,9 @@ class TransitionBlock(nn.Module):
         return transition_forward(x, op["lnw"], op["lnb"], self.norm.eps, op["w1"], op["w2"], out, accumulate), None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        from .inference_guard import InferenceOnlyKernelError
+        from .inference_guard import require_no_grad
 
-        if torch.is_grad_enabled():
-            raise InferenceOnlyKernelError("TransitionBlock is forward-only: call it under torch.no_grad().")
+        require_no_grad("TransitionBlock")
         return self.run(x)[0]
 
     def forward_residual_(self, x: torch.Tensor, s2p=None):
@@ -140,6 +149,8 @@ class TransitionBlock(nn.Module):
         return self.run(x, out=x, accumulate=True, s2p=s2p)
 
 
-def make_transition_block(c: int, n: int = 4, config=None, linear_out_init_gain: float | None = None):
+def make_transition_block(
+    channels: int, num_intermediate_factor: int = 4, config=None, linear_out_init_gain: float | None = None
+):
     """Reference factory (``optim.py:50-105``): one implementation here, the HIP one."""
-    return TransitionBlock(c, n, optim=config, linear_out_init_gain=linear_out_init_gain)
+    return TransitionBlock(channels, num_intermediate_factor, optim=config, linear_out_init_gain=linear_out_init_gain)
