@@ -9,11 +9,19 @@ Besides the metric it reports:
   roofline      the dominant kernel's achieved rate from HIP events recorded around each
                 of its launches on its own stream inside the timed region (pf_kernel_timer_*),
                 against the MI355X dense bf16 MFMA peak (2.5 PFLOP/s);
+  block_ms      one PairFormer block (pair and single halves, one stream), median of 20;
+  trunk_fp32_stream_ms  the same trunk with an fp32 residual stream and bf16 GEMM operands
+                under bf16 autocast (the reference's inference regime, scripts/inference.py:803-806);
+  kernels       per-kernel figures at the configuration each is quoted on: the triangle
+                contraction K2 at BASELINE config 3 (N=1024) against the 50 % MFMA target, the
+                other trimul kernels there, LayerNorm+transpose at N=768 against 8 TB/s, and
+                the flash attention at config 5 (N=2048);
   gpu_eager     the same trunk as plain PyTorch eager ops (the oracle restatement of the
                 reference block) on the same GPU, bf16 weights and stream under bf16
-                autocast, timed like the reference harness (scripts/bench_kernels.py:107-127);
+                autocast, timed like the reference harness (scripts/bench_kernels.py:107-127:
+                warmup, then the median of the timed runs);
   cpu_baseline  the oracle in fp32 on the host cores: one block at N=768 (rows chunked),
-                extrapolated x48, reported as a baseline only.
+                one warmup and the median of three, extrapolated x48, reported as a baseline only.
 """
 
 from __future__ import annotations
@@ -64,10 +72,106 @@ def kernel_launch_flops(kernel: str, n: int) -> float:
         "trimul_contract": 2.0 * n**3 * c,
         "trimul_project": 2.0 * m * c * 4 * c,
         "trimul_output": 2.0 * 2 * m * c * c,
-        "attn_project": 2.0 * m * c * (4 * 128 + 4),
-        "attn_out": 2.0 * m * c * c,
+        # A1 projects q, k, v and the 4-head pair bias; the gate GEMM runs in A3 beside
+        # the output projection.
+        "attn_project": 2.0 * m * c * (3 * 128 + 4),
+        "attn_out": 2.0 * 2 * m * c * c,
         "pair_transition": 2.0 * m * c * 8 * c + 2.0 * m * 4 * c * c + 2.0 * m * c * 16,
     }[kernel]
+
+
+def time_site(_lib, site: str, run, iters: int) -> tuple[float, int]:
+    """Average duration (ms) of the launches of kernel site ``site`` over ``iters`` calls of
+    ``run`` (after one untimed call), from HIP events on each launch's own stream."""
+    import torch
+
+    run()
+    torch.cuda.synchronize()
+    _lib.kernel_timer_start(site)
+    for _ in range(iters):
+        run()
+    torch.cuda.synchronize()
+    total, count = _lib.kernel_timer_read()
+    _lib.kernel_timer_stop()
+    return total / max(count, 1), count
+
+
+def kernel_figures(_lib, W, ops, attention, kernels, dev) -> list[dict]:
+    """Standalone per-kernel timings at the configurations the targets are quoted on."""
+    import torch
+
+    out = []
+
+    def entry(kernel, config, avg_ms, count, work, unit, peak, work_unit):
+        rate = work / (avg_ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9) if count else 0.0
+        out.append({
+            "kernel": kernel, "config": config, "avg_launch_ms": round(avg_ms, 4), "launches": count,
+            work_unit: work, "achieved": round(rate, 1), "unit": unit, "peak": peak, "frac": round(rate / peak, 4),
+        })  # fmt: skip
+        log(f"kernel {kernel} [{config}]: {avg_ms * 1e3:.1f} us, {rate:.1f} {unit} ({rate / peak:.3f} of peak)")
+
+    # BASELINE config 3: triangle multiplication out then in, N=1024, bf16, full mask.
+    n = 1024
+    sd = W.make_block_weights(2)
+    mods = []
+    for prefix, cls in (("tri_mul_out.", ops.TriangleMulOutgoing), ("tri_mul_in.", ops.TriangleMulIncoming)):
+        m = cls(128).to(dev)
+        m.load_state_dict({k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)})
+        mods.append(m.to(torch.bfloat16))
+    z = torch.randn((1, n, n, 128), generator=torch.Generator().manual_seed(2)).to(dev, torch.bfloat16)
+    mask = torch.ones((1, n, n), device=dev)
+
+    def trimul():
+        for m in mods:
+            m.forward_residual_(z, mask)
+
+    with torch.no_grad():
+        for site in ("trimul_contract", "trimul_project", "trimul_output"):
+            avg, cnt = time_site(_lib, site, trimul, 5)
+            entry(site, "config 3: N=1024 bf16, out+in", avg, cnt, kernel_launch_flops(site, n), "TFLOP/s",
+                  MFMA_BF16_PEAK_TFLOPS, "flops_per_launch")  # fmt: skip
+    del z, mods
+    torch.cuda.empty_cache()
+
+    # LayerNorm + transpose at N=768 (FusedLayerNormTranspose): one read and one write of z.
+    n = 768
+    x = torch.randn((1, n, n, 128), generator=torch.Generator().manual_seed(3)).to(dev, torch.bfloat16)
+    w, b = torch.ones(128, device=dev), torch.zeros(128, device=dev)
+    with torch.no_grad():
+        avg, cnt = time_site(_lib, "ln_transpose", lambda: kernels.ln_transpose(x, w, b, 1e-5, True), 10)
+    entry("ln_transpose", "N=768 bf16", avg, cnt, 2.0 * n * n * 128 * 2, "GB/s", HBM_PEAK_GBS, "bytes_per_launch")
+    del x
+
+    # BASELINE config 5: triangle attention (row, then column) at N=2048, bf16, 10 % of keys masked.
+    n = 2048
+    sd = W.make_block_weights(4)
+    z = torch.randn((1, n, n, 128), generator=torch.Generator().manual_seed(4)).to(dev, torch.bfloat16)
+    keep = torch.ones(n, device=dev)
+    keep[torch.randperm(n, generator=torch.Generator().manual_seed(5))[: int(round(0.1 * n))].to(dev)] = 0.0
+    with torch.no_grad():
+        for transpose, prefix in ((False, "pair_attn_row."), (True, "pair_attn_col.")):
+            # 10 % of the keys of every attended line masked (keys run along rows in column mode)
+            mask = (keep[:, None].expand(n, n) if transpose else keep[None, :].expand(n, n)).contiguous()[None]
+            m = attention.GridSelfAttention(128, 4, transpose=transpose).to(dev)
+            m.load_state_dict({k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)})
+            m = m.to(torch.bfloat16)
+            avg, cnt = time_site(_lib, "tri_attn", lambda: m(z, mask), 2)
+            entry("tri_attn", f"config 5: N=2048 bf16, {'columns' if transpose else 'rows'}", avg, cnt,
+                  kernel_launch_flops("tri_attn", n), "TFLOP/s", MFMA_BF16_PEAK_TFLOPS, "flops_per_launch")  # fmt: skip
+    del z
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def profiled_traffic(kernel: str, n: int) -> float | None:
@@ -98,45 +202,67 @@ def build_stack(evoformer, W, n_blocks: int, seed: int, dev, dtype):
     return stack.to(dev).to(dtype), sds
 
 
-def time_cpu_baseline(R, W, sds, n: int, seed: int, n_blocks: int, threads: int) -> dict:
+def time_cpu_baseline(R, W, sds, n: int, seed: int, n_blocks: int, threads: int, runs: int) -> dict:
     import torch
 
     torch.set_num_threads(threads)
     inp = W.make_inputs(n, seed=seed, pad_random=int(0.05 * n))
+    times = []
     with torch.no_grad():
-        t0 = time.perf_counter()
-        R.pairformer_block(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], sds[0], row_chunk=32)
-        dt = time.perf_counter() - t0
+        for i in range(runs + 1):  # the first run is the warmup
+            t0 = time.perf_counter()
+            R.pairformer_block(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], sds[0], row_chunk=32)
+            if i:
+                times.append(time.perf_counter() - t0)
+            log(f"cpu block run {i}/{runs} ({'warmup' if i == 0 else 'timed'})")
+    times.sort()
+    dt = times[len(times) // 2]
     return {
         "value": round(dt * 1e3 * n_blocks, 1),
         "unit": "ms",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"1 of {n_blocks} blocks at N={n}, fp32 oracle on the host CPU "
-        f"(attention rows in chunks of 32), {dt:.2f} s, extrapolated x{n_blocks}",
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "sample": f"1 of {n_blocks} blocks at N={n}, fp32 oracle on the host CPU (attention rows in chunks "
+        f"of 32): one warmup, median of {runs} runs = {dt:.2f} s (runs {', '.join(f'{t:.2f}' for t in times)} s), "
+        f"extrapolated x{n_blocks}",
     }
 
 
-def time_gpu_eager(R, W, sds, inp, n_blocks: int, dev, steps: int) -> dict:
+def time_gpu_eager(R, W, sds, inp, n_blocks: int, dev, steps: int, block_iters: int) -> dict:
+    """Eager trunk: one warmup trunk, then the median of ``steps`` timed trunks; eager block:
+    the median of ``block_iters`` runs of block 0 (after the warm trunk)."""
     import torch
 
     blocks = [{k: v.to(dev, torch.bfloat16) for k, v in sd.items()} for sd in sds]
     pair = inp["pair"].to(dev, torch.bfloat16)
     single = inp["single"].to(dev, torch.bfloat16)
     pm, sm = inp["pair_mask"].to(dev), inp["seq_mask"].to(dev)
-    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
-        R.pairformer_block(pair, single, pm, sm, blocks[0])  # warmup
-        torch.cuda.synchronize()
+
+    def trunk():
+        p, s = pair, single
+        for blk in blocks:
+            p, s = R.pairformer_block(p, s, pm, sm, blk)
+        return p
+
+    def median_ms(fn, n):
         times = []
-        for _ in range(steps):
+        for _ in range(n):
             t0 = time.perf_counter()
-            p, s = pair, single
-            for blk in blocks:
-                p, s = R.pairformer_block(p, s, pm, sm, blk)
+            fn()
             torch.cuda.synchronize()
             times.append(time.perf_counter() - t0)
-    times.sort()
-    return {"ms": round(times[len(times) // 2] * 1e3, 2), "blocks_timed": n_blocks, "steps": steps}
+        times.sort()
+        return times[len(times) // 2] * 1e3
+
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        trunk()  # warmup
+        torch.cuda.synchronize()
+        trunk_ms = median_ms(trunk, steps)
+        block_ms = median_ms(lambda: R.pairformer_block(pair, single, pm, sm, blocks[0]), block_iters)
+    return {"ms": round(trunk_ms, 2), "blocks_timed": n_blocks, "warmup": 1, "steps": steps, "statistic": "median",
+            "block_ms": round(block_ms, 3), "block_iters": block_iters}
 
 
 def main() -> int:
@@ -150,8 +276,15 @@ def main() -> int:
     ap.add_argument("--roofline-kernel", default="tri_attn")
     ap.add_argument("--no-eager", action="store_true", help="skip the GPU eager baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--eager-steps", type=int, default=1)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--eager-steps", type=int, default=5, help="timed eager trunks (median)")
+    ap.add_argument("--eager-block-iters", type=int, default=20, help="timed eager blocks (median)")
+    ap.add_argument("--cpu-runs", type=int, default=3, help="timed CPU blocks after one warmup (median)")
+    ap.add_argument(
+        "--cpu-threads", type=int, default=0,
+        help="host threads for the CPU baseline (0: torch's default, which follows OMP_NUM_THREADS)",
+    )  # fmt: skip
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel figures")
+    ap.add_argument("--no-fp32-stream", action="store_true", help="skip the fp32-stream trunk")
     ap.add_argument("--calibration-copy", action="store_true", help="run one 1 GiB copy (for PMC byte scaling)")
     args = ap.parse_args()
 
@@ -174,6 +307,9 @@ def main() -> int:
 
     W = import_module("deepfold3_dev_amd.weights")
     evoformer = import_module("deepfold3_dev_amd.evoformer")
+    ops = import_module("deepfold3_dev_amd.ops")
+    attention = import_module("deepfold3_dev_amd.attention")
+    kernels = import_module("deepfold3_dev_amd.kernels")
     _lib = import_module("deepfold3_dev_amd._lib")
     if not torch.cuda.is_available():
         log("no GPU visible")
@@ -217,6 +353,49 @@ def main() -> int:
     log(f"timed {args.steps} steps: {ms:.2f} ms per trunk; outputs finite: {finite}")
     del out
 
+    # One block, pair and single halves on one stream (the median of 20 in-place runs).
+    with torch.no_grad():
+        p1, s1 = pair.clone(), single.clone()
+        blk = stack.blocks[0]
+
+        def one_block():
+            blk.forward_(p1, s1, pm, sm)
+
+        one_block()
+        torch.cuda.synchronize()
+        bt = []
+        for _ in range(20):
+            t_0 = time.perf_counter()
+            one_block()
+            torch.cuda.synchronize()
+            bt.append(time.perf_counter() - t_0)
+        bt.sort()
+        block_ms = bt[len(bt) // 2] * 1e3
+        del p1, s1
+    log(f"one block: {block_ms:.3f} ms (median of 20)")
+
+    fp32_stream = None
+    if not args.no_fp32_stream:
+        # The reference's inference regime: fp32 parameters and residual stream, bf16 GEMM
+        # operands under autocast (scripts/inference.py:803-806).
+        stack32, _ = build_stack(evoformer, W, nb, args.seed, dev, torch.float32)
+        p32, s32 = inp["pair"].to(dev), inp["single"].to(dev)
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            stack32(p32, s32, pm, sm)
+            torch.cuda.synchronize()
+            t_0 = time.perf_counter()
+            for _ in range(3):
+                o32 = stack32(p32, s32, pm, sm)
+            torch.cuda.synchronize()
+            fp32_stream = (time.perf_counter() - t_0) * 1e3 / 3
+        del stack32, p32, s32, o32
+        torch.cuda.empty_cache()
+        log(f"fp32-stream trunk (bf16 GEMM operands): {fp32_stream:.2f} ms")
+
+    kern = None
+    if not args.no_kernels:
+        kern = kernel_figures(_lib, W, ops, attention, kernels, dev)
+
     fl = block_flops(n)
     trunk_flops = nb * sum(fl.values())
     tflops = trunk_flops / (ms * 1e-3) / 1e12
@@ -227,14 +406,15 @@ def main() -> int:
     eager = None
     if not args.no_eager:
         log("timing the GPU eager baseline (oracle ops, bf16)")
-        eager = time_gpu_eager(R, W, sds, inp, nb, dev, args.eager_steps)
+        eager = time_gpu_eager(R, W, sds, inp, nb, dev, args.eager_steps, args.eager_block_iters)
         eager["speedup"] = round(eager["ms"] / ms, 2)
         log(f"gpu eager: {eager['ms']} ms per trunk, HIP speed-up x{eager['speedup']}")
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline (oracle, fp32, one block)")
-        cpu = time_cpu_baseline(R, W, sds, n, args.seed, nb, min(args.cpu_threads, os.cpu_count() or 1))
+        threads = args.cpu_threads if args.cpu_threads > 0 else torch.get_num_threads()
+        cpu = time_cpu_baseline(R, W, sds, n, args.seed, nb, threads, args.cpu_runs)
         log(f"cpu: {cpu['sample']}")
 
     line = {
@@ -257,6 +437,8 @@ def main() -> int:
             "blocks": nb,
             "batch": 1,
         },
+        "block_ms": round(block_ms, 3),
+        "trunk_fp32_stream_ms": None if fp32_stream is None else round(fp32_stream, 2),
         "tflops": round(tflops, 1),
         "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "roofline": {
@@ -272,6 +454,7 @@ def main() -> int:
             "traffic": profiled_traffic(args.roofline_kernel, n),
             "traffic_source": "profiles/trunk_n768_bf16_hbm_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-scaled)",
         },
+        "kernels": kern,
         "cpu_baseline": cpu,
         "gpu_eager": eager,
         "outputs_finite": finite,

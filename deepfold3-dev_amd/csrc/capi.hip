@@ -69,8 +69,11 @@ hipEvent_t take_event() {
     g_free_events.pop_back();
     return e;
   }
+  // Timing-only events: without the system-scope fence a recorded event would write back
+  // and invalidate the caches, and that cost lands inside the interval of the timed kernel
+  // (tens of microseconds after a kernel that leaves much dirty data in L2).
   hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
   return e;
 }
 }  // namespace

@@ -439,6 +439,14 @@ PF_DEVICE void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int
 #endif
 }
 
+// Workgroup barrier after this wave's LDS operations (s_waitcnt lgkmcnt(0); s_barrier),
+// without waiting for outstanding global or buffer-to-LDS loads (vmcnt), which
+// __syncthreads() would. Only for LDS data written by ds_* instructions.
+PF_DEVICE void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt at their maxima
+  __builtin_amdgcn_s_barrier();
+}
+
 // ---------------------------------------------------------------- 16-value fragments
 // Key order of a 32-key block in flash-attention operands. With S^T = K Q^T on a 32x32
 // MFMA, lane (q, h) (q = lane & 31, h = lane >> 5) holds the logits of query q for keys

@@ -76,6 +76,7 @@ template <class T>
 int ln_dispatch(const void* x, const float* w, const float* b, float eps, void* out, long M, int C, int N1, int N2,
                 int transpose, hipStream_t s) {
   dim3 grid((unsigned)((M + 3) / 4));
+  pf::KernelTimer timer(transpose ? "ln_transpose" : "layernorm", s);
   switch (C) {
     case 128:
       layernorm_rows_kernel<T, 128><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
@@ -93,6 +94,7 @@ int ln_dispatch(const void* x, const float* w, const float* b, float eps, void* 
       pf::set_error(PF_ERR_UNSUPPORTED, "layernorm: C=%d (built: 128, 256, 384, 512)", C);
       return PF_ERR_UNSUPPORTED;
   }
+  timer.stop();
   return pf::check_launch("layernorm");
 }
 

@@ -240,177 +240,54 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(const TC* __restri
   }
 }
 
-// bf16 contraction on 256x256 tiles (used when Np is a multiple of 256). Eight waves in
-// 2 x 4, each owning a 128 (i) x 64 (j) block as 2 x 4 tiles of v_mfma_f32_32x32x16_bf16
-// (128 fp32 accumulators per lane); each LDS fragment feeds two or four MFMAs.
-// k-tiles of 64 flow through two LDS stages filled by global_load_lds_dwordx4 (global ->
-// LDS without registers): tile t + 1 is loaded while tile t is multiplied, one barrier per
-// tile. A wave's direct load writes 1 KiB lane-linearly (8 rows x 128 bytes), so the tiles
-// are unpadded and the 16-byte chunk c of row R is stored at chunk c ^ ((R >> 1) & 7).
-// LDS serves a 128-bit read for 16 lanes at a time over 64 four-byte banks; the 16 lanes
-// of a fragment read 16 consecutive rows at the same chunk, and the swizzle gives the 8
-// row pairs sharing a 256-byte bank window the 8 different chunk slots in it.
-// The waves compute X^T (A = Q rows j, B = P rows i): each lane holds four consecutive
-// output columns j of one row i, and lanes l, l + 32 together 16 contiguous bytes.
-struct Contract256 {
-  static constexpr int BT = 256;
-  static constexpr int KT = 64;
-  static constexpr int NT = 512;
-  static constexpr int TILE = BT * KT;       // elements of one operand k-tile
-  static constexpr int STAGE = 2 * TILE;     // P tile then Q tile
-  static constexpr int OLD = BT + 8;         // output staging rows (bf16): 528 bytes
-  static constexpr int RING = 2 * STAGE * 2;
-  static constexpr int OUT = BT * OLD * 2;
-  static constexpr int SMEM = RING > OUT ? RING : OUT;
-};
-
+// 16-byte chunk swizzle of the contraction's LDS k-tiles (64 bf16 per row, unpadded): the
+// chunk c of row R is stored at chunk c ^ ((R >> 1) & 7). LDS serves a 128-bit read for 16
+// lanes at a time over 64 four-byte banks; the 16 lanes of a fragment read 16 consecutive
+// rows at the same chunk, and the swizzle gives the 8 row pairs sharing a 256-byte bank
+// window the 8 different chunk slots in it. A wave's direct load writes 1 KiB
+// lane-linearly (8 rows x 128 bytes), so lane l of a direct load fills row 8 blk + l / 8 at
+// physical chunk l % 8.
 PF_DEVICE int k2_swz(int row) { return (row >> 1) & 7; }
 
-__global__ __launch_bounds__(512) void trimul_contract256_kernel(const bf16* __restrict__ P, const bf16* __restrict__ Q,
-                                                                 bf16* __restrict__ X, int G, int Np, int xcd_remap) {
-  using Cfg = Contract256;
-  constexpr int BT = Cfg::BT, KT = Cfg::KT;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  bf16* lds = reinterpret_cast<bf16*>(smem);
-
-  const int tiles1 = Np / BT;
-  const int tiles = tiles1 * tiles1;
-  int bid = blockIdx.x;
-  int g, tile;
-  if (xcd_remap) {  // XCD x walks planes x, x+8, ...: a plane's operands stay in one L2
-    const int xcd = bid & 7;
-    const int u = bid >> 3;
-    g = xcd + 8 * (u / tiles);
-    tile = u % tiles;
-  } else {
-    g = bid / tiles;
-    tile = bid % tiles;
-  }
-  if (g >= G) return;
-  const int i0 = (tile / tiles1) * BT;
-  const int j0 = (tile % tiles1) * BT;
-  const size_t pe = (size_t)Np * Np;
-  const bf16* Pg = P + (size_t)g * pe + (size_t)i0 * Np;
-  const bf16* Qg = Q + (size_t)g * pe + (size_t)j0 * Np;
-
-  const int w = wave_id();
-  const int l = lane_id();
-  const int wi = (w >> 2) * 128;  // wave's rows i in the tile
-  const int wj = (w & 3) * 64;    // wave's columns j
-
-  // Direct loads: a stage is 64 blocks of 8 rows (P blocks 0..31, Q blocks 32..63); wave w
-  // loads blocks 8w .. 8w + 7. Lane l writes row 8 blk + l / 8 at physical chunk l % 8,
-  // i.e. logical chunk (l % 8) ^ swz(row).
-  const int lrow = l >> 3;
-  const int lpc = l & 7;
-  auto issue = [&](int kt) {
-    bf16* st = lds + (kt & 1) * Cfg::STAGE;
-    const int k0 = kt * KT;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int blk = 8 * w + q;
-      const int op = blk >> 5;
-      const int row = (blk & 31) * 8 + lrow;
-      const int c = lpc ^ k2_swz(row);
-      const bf16* src = (op ? Qg : Pg) + (size_t)row * Np + k0 + 8 * c;
-      __builtin_amdgcn_global_load_lds(
-          (__attribute__((address_space(1))) const void*)src,
-          (__attribute__((address_space(3))) void*)(st + op * Cfg::TILE + (blk & 31) * 8 * KT), 16, 0, 0);
-    }
-  };
-
-  f32x16 acc[2][4];  // [j tile][i tile]
-  zero_acc32(acc);
-  const int nk = Np / KT;
-  const int r = l & 31;
-  const int hf = l >> 5;
-  issue(0);
-  for (int kt = 0; kt < nk; ++kt) {
-    // s_waitcnt vmcnt(0) (other counters untouched): this wave's loads of tile kt landed.
-    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-    // All waves' loads of tile kt visible; stage (kt + 1) & 1 no longer read. A bare
-    // s_barrier: __syncthreads() would add a full memory fence.
-    __builtin_amdgcn_s_barrier();
-    if (kt + 1 < nk) issue(kt + 1);
-    const bf16* Ps = lds + (kt & 1) * Cfg::STAGE;
-    const bf16* Qs = Ps + Cfg::TILE;
-#pragma unroll
-    for (int kk = 0; kk < KT; kk += 16) {
-      const int c = kk / 8 + hf;
-      bf16x8 af[2], bfr[4];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int R = wj + 32 * t + r;
-        af[t] = *reinterpret_cast<const bf16x8*>(Qs + R * KT + 8 * (c ^ k2_swz(R)));
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int R = wi + 32 * t + r;
-        bfr[t] = *reinterpret_cast<const bf16x8*>(Ps + R * KT + 8 * (c ^ k2_swz(R)));
-      }
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
-          acc[a][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[cc], acc[a][cc], 0, 0, 0);
-    }
-  }
-
-  // acc[a][c] element e: j = wj + 32 a + acc32_row(e), i = wi + 32 c + (lane & 31). The tile
-  // goes through LDS ([i][j], 528-byte rows) so the stores are whole 512-byte rows.
-  __syncthreads();  // every wave is done reading the ring
-  bf16* ot = lds;
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        float v[4] = {acc[a][cc][4 * g4], acc[a][cc][4 * g4 + 1], acc[a][cc][4 * g4 + 2], acc[a][cc][4 * g4 + 3]};
-        store_vec<bf16, 4>(ot + (wi + 32 * cc + r) * Cfg::OLD + wj + 32 * a + acc32_row(4 * g4), v);
-      }
-  __syncthreads();
-  bf16* Xg = X + (size_t)g * pe + (size_t)i0 * Np + j0;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int it = 0; it < BT * BT / 8 / Cfg::NT; ++it) {
-    const int idx = tid + it * Cfg::NT;
-    const int row = idx / (BT / 8), ch = idx % (BT / 8);
-    *reinterpret_cast<u32x4*>(Xg + (size_t)row * Np + 8 * ch) = *reinterpret_cast<const u32x4*>(ot + row * Cfg::OLD + 8 * ch);
-  }
-}
-
-// bf16 contraction on 256 (i) x 384 (j) tiles, used when Np is a multiple of 768 (each
-// operand row block is then read twice (P) or three times (Q) instead of three times each).
-// Persistent: one block per CU walks tiles (at N = 768, B C 6 tiles: three per CU). Eight
-// waves in 2 x 4, each owning a 128 (i) x 96 (j) block as 4 x 3 tiles of
-// v_mfma_f32_32x32x16_bf16 (192 fp32 accumulators per lane): per k-step 7 fragment reads
-// feed 12 MFMAs. k-tiles of 64 (whole 128-byte lines per row) flow through two LDS stages
-// of 80 KiB -- the whole 160 KiB of a CU -- filled by global_load_lds_dwordx4 one tile
-// ahead, one barrier per tile, with the same 16-byte chunk swizzle as the 256 x 256 kernel.
-// The last k-step of a tile issues the next tile's first k-tile into stage 0, so its
-// latency hides behind the last MFMAs and the output pass; the output tile leaves through
-// stage 1 in four passes of 64 rows i (the k-tile count is even: stage 1 holds the last
-// k-tile, whose readers the first pass's barrier waits for).
-struct Contract768 {
+// Persistent bf16 contraction on 256 (i) x BJ (j) tiles, BJ = 384 when Np is a multiple
+// of 768 (each operand row block is then read twice (P) or three times (Q) instead of three
+// times each) and BJ = 256 for the other multiples of 256 (N = 1024: 16 tiles per plane).
+// One block per CU walks tiles (at N = 768, B C 6 tiles: three per CU). Eight waves in
+// 2 x 4, each owning a 128 (i) x BJ/4 (j) block as 4 x BJ/128 tiles of
+// v_mfma_f32_32x32x16_bf16 (BJ/2 fp32 accumulators per lane): per k-step 4 + BJ/128
+// fragment reads feed BJ/32 MFMAs. k-tiles of 64 (whole 128-byte lines per row) flow
+// through two LDS stages of (256 + BJ) x 128 bytes, filled by global_load_lds_dwordx4 one
+// tile ahead, one barrier per tile, with the same 16-byte chunk swizzle as the 256 x 256
+// kernel. The last k-step of a tile issues the next tile's first k-tile into stage 0, so
+// its latency hides behind the last MFMAs and the output pass; the output tile leaves
+// through stage 1 in four passes of 64 rows i (the k-tile count is even: stage 1 holds the
+// last k-tile, whose readers the first pass's barrier waits for).
+template <int BJ_>
+struct ContractP {
   static constexpr int BI = 256;
-  static constexpr int BJ = 384;
+  static constexpr int BJ = BJ_;
+  static constexpr int JT = BJ / 128;                // 32-wide j tiles per wave
   static constexpr int KT = 64;
   static constexpr int NT = 512;
   static constexpr int PT = BI * KT;                 // elements of the P k-tile
   static constexpr int STAGE = (BI + BJ) * KT;       // P tile then Q tile
-  static constexpr int BLKS = (BI + BJ) / 8;         // 1 KiB direct-load blocks per stage (80)
-  static constexpr int DMA = BLKS / (NT / 64);       // per wave (10)
-  static constexpr int OLD = BJ + 8;                 // output staging rows (bf16): 784 bytes
+  static constexpr int BLKS = (BI + BJ) / 8;         // 1 KiB direct-load blocks per stage
+  static constexpr int DMA = BLKS / (NT / 64);       // per wave
+  static constexpr int OLD = BJ + 8;                 // output staging rows (bf16)
   static constexpr int OROWS = 64;                   // output rows per staging pass
-  static constexpr int SMEM = 2 * STAGE * 2;         // 163840 bytes
+  static constexpr int SMEM = 2 * STAGE * 2;         // bytes (BJ 384: 163840, 256: 131072)
   static_assert(OROWS * OLD <= STAGE, "output pass fits stage 1");
 };
+using Contract768 = ContractP<384>;
+using Contract1024 = ContractP<256>;
 
-__global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __restrict__ P, const bf16* __restrict__ Q,
-                                                                 bf16* __restrict__ X, int G, int Np, int xcd_remap) {
-  using Cfg = Contract768;
-  constexpr int BI = Cfg::BI, BJ = Cfg::BJ, KT = Cfg::KT, DMA = Cfg::DMA;
+template <int BJ_>
+__global__ __launch_bounds__(512) void trimul_contract_persistent_kernel(const bf16* __restrict__ P,
+                                                                         const bf16* __restrict__ Q,
+                                                                         bf16* __restrict__ X, int G, int Np,
+                                                                         int xcd_remap) {
+  using Cfg = ContractP<BJ_>;
+  constexpr int BI = Cfg::BI, BJ = Cfg::BJ, KT = Cfg::KT, DMA = Cfg::DMA, JT = Cfg::JT;
   static_assert(DMA * (Cfg::NT / 64) == Cfg::BLKS, "a stage splits evenly over the waves");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* lds = reinterpret_cast<bf16*>(smem);
@@ -438,11 +315,11 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
 
   const int w = wave_id();
   const int l = lane_id();
-  const int wi = (w >> 2) * 128;  // wave's rows i in the tile
-  const int wj = (w & 3) * 96;    // wave's columns j
+  const int wi = (w >> 2) * 128;      // wave's rows i in the tile
+  const int wj = (w & 3) * (BJ / 4);  // wave's columns j
 
-  // Direct loads: a stage is 80 blocks of 8 rows (P blocks 0..31, Q blocks 32..79); wave w
-  // loads blocks DMA w .. DMA w + DMA - 1. Lane l writes row 8 blk + l / 8 at physical
+  // Direct loads: a stage is BLKS blocks of 8 rows (P blocks 0..31, then the Q blocks); wave
+  // w loads blocks DMA w .. DMA w + DMA - 1. Lane l writes row 8 blk + l / 8 at physical
   // chunk l % 8, i.e. logical chunk (l % 8) ^ swz(row). 32-bit per-lane offsets from a scalar
   // base per operand (raw buffer loads).
   // The per-lane offsets are recomputed at each issue (a few VALU operations): the
@@ -460,7 +337,7 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
   auto rsrc_P = [&](int g, int i0) { return buf_rsrc(P + (size_t)g * pe + (size_t)i0 * Np, (unsigned)(BI * Np * 2)); };
   auto rsrc_Q = [&](int g, int j0) { return buf_rsrc(Q + (size_t)g * pe + (size_t)j0 * Np, (unsigned)(BJ * Np * 2)); };
 
-  const int nk = Np / KT;  // even (Np is a multiple of 768)
+  const int nk = Np / KT;  // even (Np is a multiple of 256)
   const int r = l & 31;
   const int hf = l >> 5;
   const int sw = k2_swz(r);  // rows wi + 32 t + r and wj + 32 t + r share the swizzle of r
@@ -481,9 +358,9 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
     const auto nrsP = rsrc_P(ng, ni0);
     const auto nrsQ = rsrc_Q(ng, nj0);
 
-    f32x16 acc[3][4];  // [j tile][i tile]
+    f32x16 acc[JT][4];  // [j tile][i tile]
 #pragma unroll
-    for (int a = 0; a < 3; ++a)
+    for (int a = 0; a < JT; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
@@ -502,13 +379,13 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
 #pragma unroll
       for (int kk = 0; kk < KT; kk += 16) {
         const int c8 = 8 * ((kk / 8 + hf) ^ sw);
-        bf16x8 af[3], bfr[4];
+        bf16x8 af[JT], bfr[4];
 #pragma unroll
-        for (int t = 0; t < 3; ++t) af[t] = *reinterpret_cast<const bf16x8*>(Qs + (wj + 32 * t + r) * KT + c8);
+        for (int t = 0; t < JT; ++t) af[t] = *reinterpret_cast<const bf16x8*>(Qs + (wj + 32 * t + r) * KT + c8);
 #pragma unroll
         for (int t = 0; t < 4; ++t) bfr[t] = *reinterpret_cast<const bf16x8*>(Ps + (wi + 32 * t + r) * KT + c8);
 #pragma unroll
-        for (int a = 0; a < 3; ++a)
+        for (int a = 0; a < JT; ++a)
 #pragma unroll
           for (int cc = 0; cc < 4; ++cc)
             acc[a][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[cc], acc[a][cc], 0, 0, 0);
@@ -516,8 +393,8 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
     }
 
     // acc[a][c] element e: j = wj + 32 a + acc32_row(e), i = wi + 32 c + (lane & 31). Four
-    // passes of 64 rows i through stage 1 ([i][j], 784-byte rows), stored as whole 768-byte
-    // rows; stage 0 is receiving the next tile's first k-tile meanwhile.
+    // passes of 64 rows i through stage 1 ([i][j], (BJ + 8) x 2-byte rows), stored as whole
+    // 2 BJ-byte rows; stage 0 is receiving the next tile's first k-tile meanwhile.
     bf16* Xg = X + (size_t)g * pe + (size_t)i0 * Np + j0;
     bf16* ost = lds + Cfg::STAGE;
     // The store offsets are the same for every tile; the empty asm keeps the compiler from
@@ -526,10 +403,13 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
     asm volatile("" : "+v"(t2));
 #pragma unroll
     for (int pass = 0; pass < BI / Cfg::OROWS; ++pass) {
-      __syncthreads();  // stage 1 (the last k-tile, or the previous pass) is no longer read
+      // Stage 1 (the last k-tile, or the previous pass) is no longer read. A bare barrier
+      // after this wave's LDS operations: __syncthreads() would also wait for the next
+      // tile's buffer-to-LDS loads into stage 0, which are meant to overlap this pass.
+      lds_barrier();
       if (wi == (pass >> 1) * 128) {
 #pragma unroll
-        for (int a = 0; a < 3; ++a)
+        for (int a = 0; a < JT; ++a)
 #pragma unroll
           for (int c2 = 0; c2 < 2; ++c2) {
             const int cc = 2 * (pass & 1) + c2;
@@ -541,7 +421,7 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
             }
           }
       }
-      __syncthreads();
+      lds_barrier();
 #pragma unroll
       for (int it = 0; it < Cfg::OROWS * BJ / 8 / Cfg::NT; ++it) {
         const int idx = t2 + it * Cfg::NT;
@@ -558,6 +438,45 @@ __global__ __launch_bounds__(512) void trimul_contract768_kernel(const bf16* __r
     rsP = nrsP;
     rsQ = nrsQ;
   }
+  // No buffer-to-LDS load may land after the block's LDS is handed to another block.
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+}
+
+// Dynamic-LDS limits are set on every launch (a cheap host call): the attribute belongs to
+// the current device, and the library keeps no per-process flags.
+int reserve_lds(const void* fn, int bytes, const char* what) {
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "%s: cannot reserve %d bytes of LDS: %s", what, bytes,
+             hipGetErrorString(e));
+  return PF_OK;
+}
+
+template <int BJ>
+int contract_persistent_launch(const void* P, const void* Q, void* X, int G, int Np, int remap, hipStream_t s) {
+  using Cfg = ContractP<BJ>;
+  if (int e = reserve_lds((const void*)trimul_contract_persistent_kernel<BJ>, Cfg::SMEM, "trimul_contract")) return e;
+  // Persistent: at most one block per CU, a multiple of 8 for the XCD remap.
+  const long total = (long)G * (Np / Cfg::BI) * (Np / Cfg::BJ);
+  PF_REQUIRE(total < (1L << 31), PF_ERR_UNSUPPORTED, "trimul_contract: B C = %d planes of Np = %d", G, Np);
+  long nblk = std::min<long>(total, pf::cu_count());
+  if (remap) nblk = std::max<long>(8, nblk & ~7L);
+  pf::KernelTimer timer("trimul_contract", s);
+  trimul_contract_persistent_kernel<BJ><<<dim3((unsigned)nblk), Cfg::NT, Cfg::SMEM, s>>>(
+      (const bf16*)P, (const bf16*)Q, (bf16*)X, G, Np, remap);
+  timer.stop();
+  return pf::check_launch("trimul_contract");
+}
+
+template <class TC>
+int contract_generic_launch(const void* P, const void* Q, void* X, int G, int Np, int remap, hipStream_t s) {
+  using Cfg = ContractCfg<TC>;
+  if (int e = reserve_lds((const void*)trimul_contract_kernel<TC>, Cfg::SMEM, "trimul_contract")) return e;
+  const int tiles = (Np / Cfg::BMN) * (Np / Cfg::BMN);
+  pf::KernelTimer timer("trimul_contract", s);
+  trimul_contract_kernel<TC><<<dim3((unsigned)(G * tiles)), 256, Cfg::SMEM, s>>>((const TC*)P, (const TC*)Q,
+                                                                                  (TC*)X, G, Np, remap);
+  timer.stop();
+  return pf::check_launch("trimul_contract");
 }
 
 // ------------------------------------------------------------------ K3
@@ -1369,67 +1288,20 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     if (int e = pf::check_launch("trimul_project")) return e;
   }
   {
-    using Cfg = ContractCfg<TC>;
-    static bool attr_set = false;
-    if (!attr_set) {
-      hipError_t e = hipFuncSetAttribute((const void*)trimul_contract_kernel<TC>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::SMEM);
-      PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "trimul_contract: cannot reserve %d bytes of LDS: %s", Cfg::SMEM,
-                 hipGetErrorString(e));
-      attr_set = true;
-    }
     const int G = B * C;
     const int remap = (G % 8 == 0) ? 1 : 0;
-    bool done = false;
+    int e = PF_OK;
     if constexpr (sizeof(TC) == 2) {
-      if (Np % (Contract768::BI * 3) == 0) {
-        static bool attr768 = false;
-        if (!attr768) {
-          hipError_t e = hipFuncSetAttribute((const void*)trimul_contract768_kernel,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, Contract768::SMEM);
-          PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "trimul_contract: cannot reserve %d bytes of LDS: %s",
-                     Contract768::SMEM, hipGetErrorString(e));
-          attr768 = true;
-        }
-        // Persistent: at most one block per CU, a multiple of 8 for the XCD remap.
-        const long total = (long)G * (Np / Contract768::BI) * (Np / Contract768::BJ);
-        PF_REQUIRE(total < (1L << 31), PF_ERR_UNSUPPORTED, "trimul_contract: B C = %d planes of Np = %d", G, Np);
-        long nblk = std::min<long>(total, pf::cu_count());
-        if (remap) nblk = std::max<long>(8, nblk & ~7L);
-        dim3 grid((unsigned)nblk);
-        pf::KernelTimer timer_trimul_contract("trimul_contract", s);
-        trimul_contract768_kernel<<<grid, Contract768::NT, Contract768::SMEM, s>>>((const bf16*)P, (const bf16*)Q,
-                                                                                   (bf16*)X, G, Np, remap);
-        timer_trimul_contract.stop();
-        if (int e = pf::check_launch("trimul_contract")) return e;
-        done = true;
-      } else if (Np % Contract256::BT == 0) {
-        static bool attr256 = false;
-        if (!attr256) {
-          hipError_t e = hipFuncSetAttribute((const void*)trimul_contract256_kernel,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, Contract256::SMEM);
-          PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "trimul_contract: cannot reserve %d bytes of LDS: %s",
-                     Contract256::SMEM, hipGetErrorString(e));
-          attr256 = true;
-        }
-        const int t1 = Np / Contract256::BT;
-        dim3 grid((unsigned)(G * t1 * t1));
-        pf::KernelTimer timer_trimul_contract("trimul_contract", s);
-        trimul_contract256_kernel<<<grid, Contract256::NT, Contract256::SMEM, s>>>((const bf16*)P, (const bf16*)Q,
-                                                                                   (bf16*)X, G, Np, remap);
-        timer_trimul_contract.stop();
-        if (int e = pf::check_launch("trimul_contract")) return e;
-        done = true;
-      }
+      if (Np % 768 == 0)
+        e = contract_persistent_launch<384>(P, Q, X, G, Np, remap, s);
+      else if (Np % 256 == 0)
+        e = contract_persistent_launch<256>(P, Q, X, G, Np, remap, s);
+      else
+        e = contract_generic_launch<TC>(P, Q, X, G, Np, remap, s);
+    } else {
+      e = contract_generic_launch<TC>(P, Q, X, G, Np, remap, s);
     }
-    if (!done) {
-      const int tiles = (Np / Cfg::BMN) * (Np / Cfg::BMN);
-      dim3 grid((unsigned)(G * tiles));
-      pf::KernelTimer timer_trimul_contract("trimul_contract", s);
-      trimul_contract_kernel<TC><<<grid, 256, Cfg::SMEM, s>>>(P, Q, X, G, Np, remap);
-      timer_trimul_contract.stop();
-      if (int e = pf::check_launch("trimul_contract")) return e;
-    }
+    if (e) return e;
   }
   {
     constexpr bool k32 = sizeof(TC) == 2;

@@ -11,7 +11,8 @@
  *  - `stream` is a hipStream_t (pass torch.cuda.current_stream().cuda_stream).
  *    All work is enqueued on it; nothing synchronises the host.
  *  - The library never allocates device memory: scratch space is passed in as
- *    `workspace`, sized by the matching *_workspace_bytes query.
+ *    `workspace`, sized by the matching *_workspace_bytes query. The one exception is
+ *    pf_single_attn_fwd_noalloc, whose scratch is a static device array of the library.
  *  - Every entry point returns a PF_* status; on failure pf_last_error()
  *    returns a thread-local message. No C++ exception crosses this boundary.
  *
@@ -46,8 +47,9 @@ int pf_last_error_code(void);
 
 /* Kernel timer (no counterpart in the reference; the reference times kernels with CUDA
  * events in benchmarks/utils.py:58-120). pf_kernel_timer_start(name) selects one launch
- * site ("trimul_project", "trimul_contract", "trimul_output", "attn_project", "tri_attn",
- * "attn_out", "pair_transition") and resets the totals; every later launch of that site
+ * site ("trimul_project", "trimul_contract", "trimul_output", "attn_project", "pb_transpose",
+ * "tri_attn", "tri_attn_redo", "attn_out", "evo_attn", "pair_transition", "single_attn_core",
+ * "layernorm", "ln_transpose") and resets the totals; every later launch of that site
  * is bracketed by HIP events recorded on its own stream. pf_kernel_timer_read waits for
  * the recorded events and returns the summed duration and launch count so far;
  * pf_kernel_timer_stop switches timing off. Host-side state, guarded by a mutex. */
