@@ -5,7 +5,8 @@
 //   pf_ln_transpose_fwd: x [B,N1,N2,C] -> out [B,N2,N1,C] = LN(x).permute(0,2,1,3)
 //                        (reference FusedLayerNormTranspose, triton/layernorm_transpose.py:269-316).
 //
-// One wave per row; each lane owns C/128 chunks of two channels, so every load
+// C = 128 (the pair representation): 16 lanes per row, 16 rows per wave (layernorm128_kernel).
+// Other C: one wave per row; each lane owns C/128 chunks of two channels, so every load
 // instruction of a wave reads one 256-byte (bf16) or 512-byte (fp32) contiguous run.
 #include "capi.h"
 #include "common.h"
@@ -72,6 +73,73 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* __restrict
   }
 }
 
+// C = 128: 16 lanes per row, each owning 8 consecutive channels (one 16-byte load for
+// bf16, two for fp32), four rows per wave instruction and 16 rows per wave, with all of a
+// lane's loads issued before the first reduction (64 bytes in flight per lane for bf16
+// where the one-wave-per-row kernel has 4). Row statistics are two-pass fp32 sums over the
+// 16 lanes (DPP within the row of 16 lanes). Each output row is one contiguous 256- or
+// 512-byte store, whether or not it is transposed.
+template <class T>
+__global__ __launch_bounds__(256) void layernorm128_kernel(const T* __restrict__ x, const float* __restrict__ w,
+                                                           const float* __restrict__ b, float eps,
+                                                           T* __restrict__ out, long M, int N1, int N2,
+                                                           int transpose) {
+  constexpr int C = 128;
+  constexpr int R = 4;                     // rows per lane group
+  constexpr int LPR = 16;                  // lanes per row
+  constexpr int VL = 16 / sizeof(T);       // channels per 16-byte load
+  constexpr int NL = 8 / VL;               // loads per lane per row
+  const int l = lane_id();
+  const int grp = l / LPR, q = l % LPR;
+  const long row0 = ((long)blockIdx.x * 4 + wave_id()) * (R * 64 / LPR);
+  float wv[8], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; e += 4) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(w + 8 * q + e);
+    const f32x4 c = *reinterpret_cast<const f32x4*>(b + 8 * q + e);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wv[e + k] = a[k], bv[e + k] = c[k];
+  }
+  float v[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long row = min(row0 + 4 * r + grp, M - 1);  // rows past M recompute row M - 1, unstored
+#pragma unroll
+    for (int h = 0; h < NL; ++h) {
+      float t[VL];
+      load16<T>(x + row * C + 8 * q + VL * h, t);
+#pragma unroll
+      for (int e = 0; e < VL; ++e) v[r][VL * h + e] = t[e];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long row = row0 + 4 * r + grp;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += v[r][e];
+    const float mean = row_group_sum<LPR>(s) * (1.0f / C);
+    float qs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = v[r][e] - mean;
+      qs += d * d;
+    }
+    const float rstd = rsqrtf(row_group_sum<LPR>(qs) * (1.0f / C) + eps);
+    if (row >= M) continue;
+    long orow = row;
+    if (transpose) {  // (bb N1 + i) N2 + j -> (bb N2 + j) N1 + i
+      const long j = row % N2, t = row / N2;
+      orow = ((t / N1) * N2 + j) * N1 + t % N1;
+    }
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (v[r][e] - mean) * rstd * wv[e] + bv[e];
+#pragma unroll
+    for (int h = 0; h < NL; ++h) store_vec<T, VL>(out + orow * C + 8 * q + VL * h, o + VL * h);
+  }
+}
+
 template <class T>
 int ln_dispatch(const void* x, const float* w, const float* b, float eps, void* out, long M, int C, int N1, int N2,
                 int transpose, hipStream_t s) {
@@ -79,7 +147,8 @@ int ln_dispatch(const void* x, const float* w, const float* b, float eps, void* 
   pf::KernelTimer timer(transpose ? "ln_transpose" : "layernorm", s);
   switch (C) {
     case 128:
-      layernorm_rows_kernel<T, 128><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
+      layernorm128_kernel<T><<<dim3((unsigned)((M + 63) / 64)), 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1,
+                                                                            N2, transpose);
       break;
     case 256:
       layernorm_rows_kernel<T, 256><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);

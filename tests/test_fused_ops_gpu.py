@@ -157,3 +157,45 @@ def test_fused_transition_block_keys(dev):
     hh = xn @ blk.linear1.weight.double().T
     a, c = hh.chunk(2, dim=-1)
     assert_fp32_close(y.cpu(), ((F.silu(a) * c) @ blk.linear2.weight.double().T).float().cpu(), what="transition")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("C", [128, 256, 384, 512])
+def test_layer_norm_every_width(dev, dtype, C):
+    """LayerNorm.forward (primitives.py:90-115) at every built width: fp32 statistics and
+    affine, output in the input dtype. fp32 at 1e-5 against fp64; bf16 within one bf16
+    rounding of the fp64 result (|err| <= 2^-8 |ref| + 1e-6) with the input taken as given."""
+    g = torch.Generator().manual_seed(C)
+    M = 1001  # not a multiple of the 64 rows of a block
+    x = (3 * torch.randn(M, C, generator=g) + 0.5).to(dtype)
+    ln = mod("primitives").LayerNorm(C).to(dev)
+    with torch.no_grad():
+        ln.weight.copy_(1 + 0.1 * torch.randn(C, generator=g))
+        ln.bias.copy_(0.1 * torch.randn(C, generator=g))
+        got = ln(x.to(dev))
+    ref = F.layer_norm(x.double(), (C,), ln.weight.double().cpu(), ln.bias.double().cpu(), 1e-5)
+    assert got.dtype == dtype and got.shape == x.shape
+    if dtype == torch.float32:
+        assert_fp32_close(got.cpu(), ref.float(), what=f"layer_norm C={C}")
+    else:
+        err = (got.double().cpu() - ref).abs()
+        assert bool((err <= 2.0**-8 * ref.abs() + 1e-6).all()), f"C={C}: max err {err.max().item():.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ln_transpose_ragged(dev, dtype):
+    """FusedLayerNormTranspose at B=2, N1=37, N2=70 (rows not a multiple of a block), both dtypes."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 37, 70, 128, generator=g).to(dtype)
+    w, b = 1 + 0.1 * torch.randn(128, generator=g), 0.1 * torch.randn(128, generator=g)
+    with torch.no_grad():
+        got = fused.FusedLayerNormTranspose(128, True)(x.to(dev), w.to(dev), b.to(dev))
+        same = fused.FusedLayerNormTranspose(128, False)(x.to(dev), w.to(dev), b.to(dev))
+    ref = F.layer_norm(x.double(), (128,), w.double(), b.double())
+    assert got.shape == (2, 70, 37, 128) and same.shape == x.shape
+    assert torch.equal(got.cpu(), same.cpu().permute(0, 2, 1, 3))
+    if dtype == torch.float32:
+        assert_fp32_close(same.cpu(), ref.float(), what="LN transpose")
+    else:
+        err = (same.double().cpu() - ref).abs()
+        assert bool((err <= 2.0**-8 * ref.abs() + 1e-6).all()), f"max err {err.max().item():.3e}"
