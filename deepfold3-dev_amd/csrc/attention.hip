@@ -512,9 +512,11 @@ PF_DEVICE int bias_swz(int row) { return (row >> 1) & 7; }
 template <class TC>
 constexpr size_t attn_bias_lds_bytes() { return (size_t)kBiasStages * 32 * attn_qsub<TC>() * 32 * 4; }
 
-// Register sets for the K / V / mask-row prefetch ring (bf16: two key blocks ahead).
+// Register sets for the K / V / mask-row prefetch ring: loads one key block ahead. (Two
+// blocks ahead needs a third set, 16 more VGPRs, and costs the fourth wave per SIMD that
+// hides the same latency better: 487 -> 463 us at N=768 with one ahead and four waves.)
 template <class TC>
-constexpr int attn_kv_sets() { return sizeof(TC) == 2 ? 3 : 2; }
+constexpr int attn_kv_sets() { return 2; }
 
 // Mask operand: S^T += M 1^T, A = the line's additive key mask in k-column 0 (lanes of the
 // low half, key row lane & 31), B = ones in k-column 0. Keys are MFMA rows in natural
@@ -554,9 +556,12 @@ PF_DEVICE Frag16<float> buf_frag16<float>(__amdgpu_buffer_rsrc_t r, int voff, in
 
 // Block: 4 waves = 4 consecutive lines, one head, QB = 32 * QS queries. The pair-bias tile
 // (query-major, shared by the 4 lines) streams through a 3-stage LDS ring filled by direct
-// buffer-to-LDS loads two key blocks ahead; Q is staged through LDS once; K, V and the
-// line's mask slot for the lane's key row are per line and go straight into registers
-// (bf16: two key blocks ahead, in three register sets the unrolled key loop rotates). All
+// buffer-to-LDS loads two key blocks ahead; Q is staged through LDS once and its fragments
+// are read from there at every key block (bf16: unpadded 64-byte rows with a 16-byte chunk
+// swizzle, so a block takes 40 KB of LDS and four blocks fit a CU); K, V and the line's mask
+// slot for the lane's key row are per line and go straight into registers one key block
+// ahead, in two register sets the unrolled key loop alternates. The kernel fits 128 VGPRs:
+// four waves per SIMD. All
 // global loads are raw buffer loads: a scalar base per operand, a fixed per-lane offset and
 // a scalar per-key-block offset, so the key loop does no vector address arithmetic.
 // L lines per batch item (line stride Lp in the operand buffers). O_HEAD_MAJOR writes O as
@@ -576,14 +581,15 @@ PF_DEVICE Frag16<float> buf_frag16<float>(__amdgpu_buffer_rsrc_t r, int voff, in
 // is recomputed by the exact mode (FAST = false with `redo` set), which runs the lazy
 // running-maximum softmax below and skips every block whose flags are all 0.
 template <class TC, int QS, bool O_HEAD_MAJOR, bool FAST, bool POST_SCALE = false>
-__global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2)) void tri_attn_kernel(
+__global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2)) void tri_attn_kernel(
     const TC* __restrict__ Q, const TC* __restrict__ K, const TC* __restrict__ Vt, const float* __restrict__ PB,
     const float* __restrict__ MA, TC* __restrict__ O, int B, int N, int Np, int L, int Lp, int zero_masked_lines,
     int xcd_remap, int* __restrict__ redo, float post_scale = 1.f) {
   constexpr int QB = 32 * QS;
   constexpr int NT = 64 * kLinesPerBlock;
-  constexpr int QLD = kHeadDim + lds_pad<TC>();
+  constexpr int QLD = kHeadDim + (sizeof(TC) == 2 ? 0 : lds_pad<TC>());
   constexpr int QVEC = 16 / sizeof(TC);
+  auto qswz = [](int row) { return sizeof(TC) == 2 ? (row >> 2) & 3 : 0; };
   constexpr int TILE = QB * 32;                   // floats per bias stage: QB rows of 32 slots
   constexpr int DL = TILE * 4 / (NT * 16);        // direct loads per lane per stage
   static_assert(DL * NT * 16 == TILE * 4, "bias stage must split evenly over the block");
@@ -676,7 +682,7 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
       const int idx = l + it * 64;
       const int qq = idx / (kHeadDim / QVEC);
       const int d0 = (idx % (kHeadDim / QVEC)) * QVEC;
-      *reinterpret_cast<u32x4*>(qw + qq * QLD + d0) =
+      *reinterpret_cast<u32x4*>(qw + qq * QLD + QVEC * ((d0 / QVEC) ^ qswz(qq))) =
           *reinterpret_cast<const u32x4*>(Qh + (size_t)(q0 + qq) * kHeadDim + d0);
     }
   }
@@ -720,13 +726,6 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
   for (int s = 0; s < QS; ++s) lsum[s][0] = lsum[s][1] = 0.f;
 
   __syncthreads();  // Q tiles
-  // bf16: this wave's Q fragments stay in registers for the whole key loop (16 VGPRs
-  // instead of four LDS reads per key block); fp32 reads them from LDS per block.
-  Frag16<TC> qreg[sizeof(TC) == 2 ? QS : 1];
-  if constexpr (sizeof(TC) == 2) {
-#pragma unroll
-    for (int s = 0; s < QS; ++s) qreg[s].load(qw + (32 * s + lq) * QLD + 16 * hf);
-  }
 
   // Every key-block step issues K/V/mask (NSET - 1 blocks ahead) and then one bias stage
   // (two blocks ahead); the prologue issues what steps -2 and -1 would have, so every
@@ -778,7 +777,10 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 3 : 2
         for (int e = 0; e < 4; ++e) sacc[4 * i + e] = bv[e];
       }
       if (use_mask) mma_mask(sacc, mk, TC{});
-      mma32_16(sacc, kf, qreg[s]);
+      Frag16<TC> qf;
+      qf.v[0] = *reinterpret_cast<const bf16x8*>(qw + R * QLD + 8 * ((2 * hf) ^ qswz(R)));
+      qf.v[1] = *reinterpret_cast<const bf16x8*>(qw + R * QLD + 8 * ((2 * hf + 1) ^ qswz(R)));
+      mma32_16(sacc, kf, qf);
     } else {
       // fp32: q k^T from a zero accumulator (sixteen 32x32x2 steps), then the bias, then
       // the key mask -- the eager order (q k^T scale + bias) + mask. Accumulating the
