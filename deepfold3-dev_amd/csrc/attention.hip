@@ -757,14 +757,24 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
     bias_issue(kb + 2, u + 2);
   };
 
+  // Key mask of block kb, once per block for all sub-blocks: the mask MFMA only runs for
+  // key blocks that hold a masked (or padding, -inf) key; each lane holds the mask slot of
+  // one key row, so one wave-wide vote decides.
+  struct KeyMask {
+    bool use;
+    float m;
+  };
+  auto key_mask = [&](int kb, float mf) {
+    KeyMask km;
+    km.use = kb * 32 + 32 > N || (masked && __any(mf != 0.f));
+    km.m = kb < nkb ? mf : -INFINITY;
+    return km;
+  };
   // S^T tiles of key block kb: bias from the LDS stage, key mask, then q k^T (log2 domain).
-  auto logits = [&](int kb, int u, int s, const Frag16<TC>& kf, float mf, f32x16& sacc) {
-    const int k0 = kb * 32;
+  auto logits = [&](int kb, int u, int s, const Frag16<TC>& kf, const KeyMask& km, f32x16& sacc) {
     const float* bl = bias_lds + stage_of(kb, u) * TILE;
-    // The mask MFMA only for key blocks that hold a masked (or padding, -inf) key: each
-    // lane holds the mask slot of one key row, so one wave-wide vote decides.
-    const bool use_mask = k0 + 32 > N || (masked && __any(mf != 0.f));
-    const float mk = kb < nkb ? mf : -INFINITY;
+    const bool use_mask = km.use;
+    const float mk = km.m;
     const int R = 32 * s + lq;
     const float* br = bl + R * 32;
     if constexpr (sizeof(TC) == 2) {
@@ -807,10 +817,11 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
   // FAST step: p = 2^s, row sums, O^T += V^T P^T.
   // Sub-blocks one after the other: one S tile live at a time.
   auto compute_fast = [&](int kb, int u, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf) {
+    const KeyMask km = key_mask(kb, mf);
 #pragma unroll
     for (int s = 0; s < QS; ++s) {
       f32x16 sacc;
-      logits(kb, u, s, kf, mf, sacc);
+      logits(kb, u, s, kf, km, sacc);
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[r] = __builtin_amdgcn_exp2f(sacc[r]);
       const Frag16<TC> pf = pack_p(sacc, TC{});
@@ -839,8 +850,9 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
   // masked keys' contributions).
   auto compute_exact = [&](int kb, int u, const Frag16<TC>& kf, const Frag16<TC>& vf, float mf) {
     f32x16 sacc[QS];
+    const KeyMask km = key_mask(kb, mf);
 #pragma unroll
-    for (int s = 0; s < QS; ++s) logits(kb, u, s, kf, mf, sacc[s]);
+    for (int s = 0; s < QS; ++s) logits(kb, u, s, kf, km, sacc[s]);
     float mx[QS];
     bool any_shift = false;
 #pragma unroll

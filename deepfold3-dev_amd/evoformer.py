@@ -142,14 +142,23 @@ class PairFormerBlock(nn.Module):
 
 
 class PairFormerStack(nn.Module):
-    """The trunk loop over ``num_blocks`` PairFormer blocks (``evoformer.py:593-601``)."""
+    """The trunk loop over ``num_blocks`` PairFormer blocks (``evoformer.py:593-601``).
+
+    ``layer_attr`` names the ModuleList in the state dict (``blocks`` here; the confidence
+    head's stack uses the reference's ``layers``)."""
 
     def __init__(self, num_blocks: int, c_pair: int = 128, c_single: int = 384, optim: OptimConfig | None = None,
-                 **block_kwargs):  # fmt: skip
+                 layer_attr: str = "blocks", **block_kwargs):  # fmt: skip
         super().__init__()
-        self.blocks = nn.ModuleList(
-            [PairFormerBlock(c_pair, c_single, optim=optim, **block_kwargs) for _ in range(num_blocks)]
-        )
+        self._layer_attr = layer_attr
+        setattr(
+            self, layer_attr,
+            nn.ModuleList([PairFormerBlock(c_pair, c_single, optim=optim, **block_kwargs) for _ in range(num_blocks)]),
+        )  # fmt: skip
+
+    @property
+    def blocks(self) -> nn.ModuleList:
+        return self._modules[self._layer_attr]
 
     @inference_only("PairFormerStack")
     def forward(
@@ -187,3 +196,70 @@ class PairFormerStack(nn.Module):
         if key not in streams:
             streams[key] = torch.cuda.Stream(device=device)  # default priority
         return streams[key]
+
+
+class ConfidencePairFormer(PairFormerStack):
+    """The PairFormer layers of the confidence head (``confidence.py:88-117``, run in order
+    at ``:304-308``): ``num_layer`` blocks of the trunk's shape (``ConfidenceConfig``,
+    ``config.py:578-589``: 4 layers, c_pair 128, c_single 384, 4 pair and 16 single heads),
+    state-dict keys ``layers.{i}.*`` as in the reference's ``ConfidenceHead``. The feature
+    embedding before the layers and the logit heads after them are outside the hot path."""
+
+    def __init__(self, num_layer: int = 4, c_pair: int = 128, c_single: int = 384, num_pair_heads: int = 4,
+                 num_single_heads: int = 16, optim: OptimConfig | None = None, **block_kwargs):  # fmt: skip
+        super().__init__(
+            num_layer, c_pair, c_single, optim=optim, layer_attr="layers", num_pair_heads=num_pair_heads,
+            num_single_heads=num_single_heads, single_key_dim=c_single, single_value_dim=c_single, **block_kwargs,
+        )  # fmt: skip
+
+
+class TemplatePairFormerBlock(nn.Module):
+    """Pair-only PairFormer block of the template embedding (``template_embedding.py:180-241``):
+    triangle multiplications, row and column attention, and a transition with a smaller
+    intermediate factor; same submodule names and ``forward(pair, pair_mask)``.
+
+    Built for num_channels = 128 (every pair kernel here is); the reference's template
+    stack runs at 64 channels (``TemplatePairFormerConfig``, ``config.py:636-650``), which
+    refuses by name at construction."""
+
+    def __init__(self, num_channels: int, num_heads: int = 4, num_intermediate_factor: int = 2,
+                 pair_dropout: float = 0.25, optim: OptimConfig | None = None, residual_out_scale: float = 1.0):  # fmt: skip
+        super().__init__()
+        require_hip("TemplatePairFormerBlock", optim)
+        if num_channels != 128 or num_heads != 4:
+            raise NotActive(
+                "TemplatePairFormerBlock",
+                f"num_channels={num_channels}, num_heads={num_heads}: the pair kernels are built for 128 channels "
+                "and 4 heads of 32",
+            )  # fmt: skip
+        if residual_out_scale != 1.0:
+            raise NotActive("TemplatePairFormerBlock", "only a unit residual scale is built")
+        self.tri_mul_out = TriangleMulOutgoing(num_channels, optim=optim)
+        self.tri_mul_in = TriangleMulIncoming(num_channels, optim=optim)
+        self.pair_attn_row = GridSelfAttention(num_channels, num_heads=num_heads, transpose=False, optim=optim)
+        self.pair_attn_col = GridSelfAttention(num_channels, num_heads=num_heads, transpose=True, optim=optim)
+        self.pair_transition = make_transition_block(num_channels, num_intermediate_factor, config=optim)
+        self.num_intermediate_factor = num_intermediate_factor
+        self.pair_dropout = pair_dropout
+        self.residual_out_scale = 1.0
+
+    def forward_(self, pair: torch.Tensor, pair_mask: torch.Tensor) -> torch.Tensor:
+        """In place: ``pair`` [B, N, N, C] contiguous (``template_embedding.py:230-240``, eval)."""
+        if self.training and self.pair_dropout > 0.0:
+            raise NotActive("TemplatePairFormerBlock", "training-mode dropout is not built (eval only)")
+        kernel_census.record("TemplatePairFormerBlock", "hip_block")
+        self.tri_mul_out.forward_residual_(pair, pair_mask)
+        self.tri_mul_in.forward_residual_(pair, pair_mask)
+        self.pair_attn_row.forward_residual_(pair, pair_mask)
+        self.pair_attn_col.forward_residual_(pair, pair_mask)
+        self.pair_transition.forward_residual_(pair)
+        return pair
+
+    @inference_only("TemplatePairFormerBlock")
+    def forward(self, pair: torch.Tensor, pair_mask: torch.Tensor) -> torch.Tensor:
+        """Reference signature: ``pair`` [B?, N, N, C], ``pair_mask`` [B?, N, N] -> new pair."""
+        has_batch = pair.dim() == 4
+        if not has_batch:
+            pair, pair_mask = pair.unsqueeze(0), pair_mask.unsqueeze(0)
+        out = self.forward_(pair.contiguous().clone(), pair_mask)
+        return out if has_batch else out.squeeze(0)

@@ -37,6 +37,7 @@ __all__ = [
     "single_to_pair",
     "single_attention",
     "pairformer_block",
+    "template_pairformer_block",
     "pairformer_trunk",
 ]
 
@@ -236,6 +237,19 @@ def pairformer_block(
             single_transition=st,
         )
     return pair, single
+
+
+def template_pairformer_block(
+    pair: torch.Tensor, pair_mask: torch.Tensor, p: dict[str, torch.Tensor], row_chunk: int = 0
+) -> torch.Tensor:
+    """``TemplatePairFormerBlock.forward`` in eval mode (``template_embedding.py:220-240``):
+    the five pair branches of the PairFormer block in the same order, the transition with
+    its own intermediate factor (read from the weights), residual_out_scale 1."""
+    pair = pair + tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True)
+    pair = pair + tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False)
+    pair = pair + grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
+    pair = pair + grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
+    return pair + transition(pair, _sub(p, "pair_transition."))
 
 
 def pairformer_trunk(

@@ -133,3 +133,20 @@ def test_transition_block_out_gain_is_row_orthogonal():
     blk = primitives.make_transition_block(384, 4, linear_out_init_gain=gain)
     w = blk.linear2.weight.double()
     assert torch.allclose(w @ w.T, gain**2 * torch.eye(384, dtype=torch.float64), atol=1e-9)
+
+
+def test_template_block_refuses_unbuilt_widths():
+    evoformer = mod("evoformer")
+    assert sorted({k.split(".")[0] for k in evoformer.TemplatePairFormerBlock(128).state_dict()}) == [
+        "pair_attn_col", "pair_attn_row", "pair_transition", "tri_mul_in", "tri_mul_out",
+    ]  # fmt: skip
+    with pytest.raises(guard.NotActive) as ei:
+        evoformer.TemplatePairFormerBlock(64)  # the reference's template width (config.py:636-650)
+    assert ei.value.lever == "TemplatePairFormerBlock"
+
+
+def test_confidence_layers_keys():
+    evoformer = mod("evoformer")
+    keys = list(evoformer.ConfidencePairFormer().state_dict())
+    assert keys[0].startswith("layers.0.") and any(k.startswith("layers.3.") for k in keys)
+    assert not any(k.startswith("layers.4.") for k in keys)

@@ -273,3 +273,21 @@ def test_trunk_is_block_composition():
         p1, s1 = R.pairformer_block(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], blocks[0])
         p2, s2 = R.pairformer_block(p1, s1, inp["pair_mask"], inp["seq_mask"], blocks[1])
     assert torch.equal(p, p2) and torch.equal(s, s2)
+
+
+def test_template_block_is_the_pair_half_of_the_block():
+    """TemplatePairFormerBlock (template_embedding.py:220-240) runs the PairFormer block's
+    five pair branches in the same order (evoformer.py:298-321): with the same weights its
+    output equals the pinned block's pair output; with a factor-2 transition it differs."""
+    sd = W.make_block_weights(13, perturb_affine=True)
+    inp = W.make_inputs(12, seed=4, pad_last=2)
+    pair_keys = ("tri_mul_out.", "tri_mul_in.", "pair_attn_row.", "pair_attn_col.", "pair_transition.")
+    sub = {k: v for k, v in sd.items() if k.startswith(pair_keys)}
+    with torch.no_grad():
+        want, _ = R.pairformer_block(inp["pair"], inp["single"], inp["pair_mask"], inp["seq_mask"], sd)
+        got = R.template_pairformer_block(inp["pair"], inp["pair_mask"], sub)
+        sd2 = W.make_block_weights(13, perturb_affine=True, factor=2)
+        got2 = R.template_pairformer_block(inp["pair"], inp["pair_mask"], {k: sd2[k] for k in sub})
+    assert torch.equal(got, want)
+    assert sd2["pair_transition.linear1.weight"].shape == (512, 128)
+    assert rel_l2(got2, want) > 1e-3
