@@ -286,6 +286,10 @@ def main() -> int:
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel figures")
     ap.add_argument("--no-fp32-stream", action="store_true", help="skip the fp32-stream trunk")
     ap.add_argument("--calibration-copy", action="store_true", help="run one 1 GiB copy (for PMC byte scaling)")
+    ap.add_argument(
+        "--kernels-only", action="store_true",
+        help="run only the per-kernel figures (no trunk) and print them as one JSON line, for profiling",
+    )  # fmt: skip
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -317,6 +321,21 @@ def main() -> int:
     dev = torch.device("cuda:0")
     n, nb = args.n, args.blocks
 
+    def calibration_copy():
+        # A plain 1 GiB device-to-device copy: under `rocprofv3 --pmc FETCH_SIZE` (or
+        # WRITE_SIZE) its counter value per byte scales the kernels' readings to bytes.
+        buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        buf.clone()
+        torch.cuda.synchronize()
+        del buf
+
+    if args.kernels_only:
+        if args.calibration_copy:
+            calibration_copy()
+        kern = kernel_figures(_lib, W, ops, attention, kernels, dev)
+        print(json.dumps({"kernels": kern}), flush=True)
+        return 0
+
     log(f"building {nb} blocks (seed {args.seed}) and inputs N={n}")
     stack, sds = build_stack(evoformer, W, nb, args.seed, dev, torch.bfloat16)
     inp = W.make_inputs(n, seed=args.seed, pad_random=int(0.05 * n))
@@ -325,12 +344,7 @@ def main() -> int:
     pm, sm = inp["pair_mask"].to(dev), inp["seq_mask"].to(dev)
 
     if args.calibration_copy:
-        # A plain 1 GiB device-to-device copy: under `rocprofv3 --pmc FETCH_SIZE` (or
-        # WRITE_SIZE) its counter value per byte scales the kernels' readings to bytes.
-        buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-        buf.clone()
-        torch.cuda.synchronize()
-        del buf
+        calibration_copy()
 
     out = None
     with torch.no_grad():
