@@ -2,7 +2,8 @@
 //
 //   A1 attn_project:  x = LN(z); q, k, v, g = x W{q,k,v,g}^T; pb = x Wpb^T. Writes the
 //                     attention-frame operands Q, K (token-major), Vt (key-contiguous,
-//                     keys permuted inside 32-blocks), G = sigmoid(g), the pair bias PB and
+//                     keys permuted inside 32-blocks), G = sigmoid(g) (fp32 only; in bf16
+//                     A3 computes the gate from the z rows it reads), the pair bias PB and
 //                     the additive key mask MA (both pre-multiplied by log2 e).
 //   A2 tri_attn:      flash attention over keys with an online base-2 softmax; the
 //                     N^3*H logits never leave registers. Writes O (normalised, ungated).
