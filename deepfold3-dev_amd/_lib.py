@@ -57,6 +57,8 @@ SIGNATURES: dict[str, tuple] = {
         _i,
         [_vp, _vp, _vp, _f, _vp, _vp, _l, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
     ),
+    "pf_recycle_embed_workspace_bytes": (_sz, [_l, _i, _i]),
+    "pf_recycle_embed_fwd": (_i, [_vp, _vp, _vp, _f, _vp, _l, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "pf_evo_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "pf_evo_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "pf_grid_attn_redo_flags": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),

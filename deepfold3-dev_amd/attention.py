@@ -17,7 +17,14 @@ import torch.nn as nn
 from . import kernel_census
 from .config import OptimConfig, require_hip
 from .inference_guard import NotActive, inference_only
-from .kernels import cast_weight, gemm_dtype_for, grid_attention_forward, pack_grid_attn_weights, single_attention_forward
+from .kernels import (
+    cast_weight,
+    gemm_dtype_for,
+    grid_attention_forward,
+    pack_grid_attn_weights,
+    scaled_weight,
+    single_attention_forward,
+)
 from .primitives import LayerNorm, LinearNoBias, WeightCache, f32
 
 
@@ -40,6 +47,8 @@ class GridSelfAttention(nn.Module):
         self.to_g = LinearNoBias(c, num_heads * self.head_dim, initializer="zeros")
         self.out_proj = LinearNoBias(num_heads * self.head_dim, c, initializer="zeros")
         self._cache = WeightCache()
+        # Residual scale of this branch (the block's ``s_ros``), folded into out_proj.
+        self.branch_scale = 1.0
 
     def _operands(self, cdt: torch.dtype) -> dict:
         params = [
@@ -52,11 +61,11 @@ class GridSelfAttention(nn.Module):
                 w5=pack_grid_attn_weights(
                     self.to_q.weight, self.to_k.weight, self.to_v.weight, self.to_g.weight, self.pair_bias.weight, cdt
                 ),
-                w_out=cast_weight(self.out_proj.weight, cdt),
+                w_out=scaled_weight(self.out_proj.weight, self.branch_scale, cdt),
                 lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
             )  # fmt: skip
 
-        return self._cache.get(params, cdt, build)
+        return self._cache.get(params, cdt, build, tag=self.branch_scale)
 
     def _run(self, z, mask, out, accumulate):
         kernel_census.record("GridSelfAttention.attention", "hip_tri_attn_col" if self.transpose else "hip_tri_attn_row")
@@ -118,6 +127,8 @@ class SingleAttention(nn.Module):
         self.to_g = LinearNoBias(c, value_dim, initializer="zeros")
         self.out_proj = LinearNoBias(value_dim, c, initializer="zeros")
         self._cache = WeightCache()
+        # Residual scale of this branch (the block's ``s_ros``), folded into out_proj.
+        self.branch_scale = 1.0
 
     def _operands(self, cdt: torch.dtype) -> dict:
         params = [
@@ -128,11 +139,11 @@ class SingleAttention(nn.Module):
         def build():
             w = torch.cat([self.to_q.weight, self.to_k.weight, self.to_v.weight, self.to_g.weight]).detach()
             return dict(
-                wqkvg=cast_weight(w, cdt), w_out=cast_weight(self.out_proj.weight, cdt), qb=f32(self.to_q.bias),
-                lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
+                wqkvg=cast_weight(w, cdt), w_out=scaled_weight(self.out_proj.weight, self.branch_scale, cdt),
+                qb=f32(self.to_q.bias), lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
             )  # fmt: skip
 
-        return self._cache.get(params, cdt, build)
+        return self._cache.get(params, cdt, build, tag=self.branch_scale)
 
     def _run(self, x, mask, pair_logits, out, accumulate):
         kernel_census.record("SingleAttention", "hip_single_attn")

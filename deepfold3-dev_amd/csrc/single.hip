@@ -374,6 +374,15 @@ int single_attn_launch(const void* s_in, const float* seq_mask, const float* pai
   return rowgemm_launch<TC, TZ, EPI_STORE>(og, wout, nullptr, 0, out, M, C, HD, st);
 }
 
+// out += LN(prev) W^T: LayerNorm into the workspace, then the row GEMM whose epilogue adds
+// into `out` (one rounding of the sum, as the reference's `pair + prev_embedding(...)`).
+template <class TZ, class TC>
+int recycle_embed_launch(const void* prev, const float* lnw, const float* lnb, float eps, const void* w, long M,
+                         int C, void* out, void* ws, hipStream_t st) {
+  if (int e = ln_launch<TZ, TC>(prev, lnw, lnb, eps, ws, M, C, st)) return e;
+  return rowgemm_launch<TC, TZ, EPI_RESIDUAL>(ws, w, nullptr, 0, out, M, C, C, st);
+}
+
 template <class TZ, class TC>
 int transition_generic_launch(const void* x, const float* lnw, const float* lnb, float eps, const void* w1,
                               const void* w2, long M, int C, int F, void* out, int accumulate, void* ws,
@@ -568,6 +577,29 @@ int pf_transition_fwd(const void* x, const float* ln_w, const float* ln_b, float
   hipStream_t st = pf::as_stream(stream);
   return PF_DISPATCH_ZC(zdtype, cdtype, transition_generic_launch, x, ln_w, ln_b, eps, w1, w2, M, C, C * factor, out,
                         accumulate, workspace, st);
+}
+
+size_t pf_recycle_embed_workspace_bytes(long M, int C, int cdtype) {
+  if (M <= 0 || C <= 0) return 0;
+  return pf::round_up((size_t)M * C * es_of(cdtype), 256);
+}
+
+int pf_recycle_embed_fwd(const void* prev, const float* ln_w, const float* ln_b, float eps, const void* w, long M,
+                         int C, int zdtype, int cdtype, void* out, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  PF_REQUIRE(prev && ln_w && ln_b && w && out && workspace, PF_ERR_INVALID_ARG,
+             "pf_recycle_embed_fwd: null pointer");
+  PF_REQUIRE(M >= 0 && C > 0, PF_ERR_INVALID_ARG, "pf_recycle_embed_fwd: M=%ld C=%d", M, C);
+  PF_REQUIRE(C % 64 == 0, PF_ERR_UNSUPPORTED, "pf_recycle_embed_fwd: C=%d (a multiple of 64)", C);
+  PF_REQUIRE(dtype_pair_ok(zdtype, cdtype), PF_ERR_UNSUPPORTED, "pf_recycle_embed_fwd: dtype pair (%d, %d)", zdtype,
+             cdtype);
+  PF_REQUIRE(prev != out, PF_ERR_INVALID_ARG, "pf_recycle_embed_fwd: prev and out must not alias");
+  PF_REQUIRE(workspace_bytes >= pf_recycle_embed_workspace_bytes(M, C, cdtype), PF_ERR_WORKSPACE,
+             "pf_recycle_embed_fwd: workspace %zu < %zu bytes", workspace_bytes,
+             pf_recycle_embed_workspace_bytes(M, C, cdtype));
+  if (M == 0) return pf::ok();
+  hipStream_t st = pf::as_stream(stream);
+  return PF_DISPATCH_ZC(zdtype, cdtype, recycle_embed_launch, prev, ln_w, ln_b, eps, w, M, C, out, workspace, st);
 }
 
 }  // extern "C"

@@ -3,9 +3,10 @@
 ``PairFormerBlock`` keeps the reference's constructor arguments, submodule names
 (so state dicts load unchanged) and ``forward(pair, single, pair_mask, seq_mask)``
 signature (``src/deepfold3/model/evoformer.py:178-355``). Eval-mode semantics: the
-branch scaler is the identity, ``residual_out_scale`` is 1 and dropout-add is a plain
-add (``triton/dropout_add.py:236-237``), so every residual add is fused into the
-epilogue of the kernel that produces the branch. ``single_to_pair`` is fused into the
+branch scaler is the identity, ``residual_out_scale`` and the transitions' residual gains
+are folded into each branch's output projection, and dropout-add is a plain add
+(``triton/dropout_add.py:236-237``), so every residual add is fused into the epilogue of
+the kernel that produces the branch. ``single_to_pair`` is fused into the
 pair transition's epilogue (it normalises the updated pair rows).
 
 ``PairFormerStack`` is the trunk loop (``evoformer.py:593-601``): it copies the inputs
@@ -52,9 +53,8 @@ class PairFormerBlock(nn.Module):
     ):
         super().__init__()
         require_hip("PairFormerBlock", optim)
-        gains = (single_transition_residual_gain, pair_transition_residual_gain)
-        if residual_out_scale != 1.0 or any(g not in (None, 1.0) for g in gains) or branch_scaler != "identity":
-            raise NotActive("PairFormerBlock", "only unit residual scales and the identity branch scaler are built")
+        if branch_scaler != "identity":
+            raise NotActive("PairFormerBlock", f"branch_scaler={branch_scaler!r}: only the identity scaler is built")
         if not use_triangle_attention or not use_single_track:
             raise NotActive("PairFormerBlock", "the triangle-attention and single-track branches are always built")
         tk = trimul_kwargs or {}
@@ -74,7 +74,23 @@ class PairFormerBlock(nn.Module):
         self.single_transition = make_transition_block(
             c_single, config=optim, linear_out_init_gain=single_transition_linear_out_init_gain
         )
-        self.residual_out_scale = 1.0
+        # Residual scales (evoformer.py:207-217, applied at :282-353): every branch's output
+        # is multiplied by s_ros, the two transitions' also by their residual gain (None = 1).
+        # Each branch ends in a bias-free output projection, so the scale is folded into
+        # that weight when its operands are prepared.
+        self.residual_out_scale = float(residual_out_scale)
+        self.single_transition_residual_gain = (
+            1.0 if single_transition_residual_gain is None else float(single_transition_residual_gain)
+        )
+        self.pair_transition_residual_gain = (
+            1.0 if pair_transition_residual_gain is None else float(pair_transition_residual_gain)
+        )
+        self.branch_scaler_kind = "identity"
+        s_ros = self.residual_out_scale
+        for m in (self.tri_mul_out, self.tri_mul_in, self.pair_attn_row, self.pair_attn_col, self.single_attn):
+            m.branch_scale = s_ros
+        self.pair_transition.branch_scale = s_ros * self.pair_transition_residual_gain
+        self.single_transition.branch_scale = s_ros * self.single_transition_residual_gain
         self.pair_dropout = pair_dropout
         self._s2p_cache = WeightCache()
 
@@ -145,16 +161,22 @@ class PairFormerStack(nn.Module):
     """The trunk loop over ``num_blocks`` PairFormer blocks (``evoformer.py:593-601``).
 
     ``layer_attr`` names the ModuleList in the state dict (``blocks`` here; the confidence
-    head's stack uses the reference's ``layers``)."""
+    head's stack uses the reference's ``layers``). ``layer_kwargs(i)``, when given, returns
+    the constructor arguments that differ per layer (the reference's per-layer residual
+    scales, ``evoformer.py:459-489``); they override ``block_kwargs``."""
 
     def __init__(self, num_blocks: int, c_pair: int = 128, c_single: int = 384, optim: OptimConfig | None = None,
-                 layer_attr: str = "blocks", **block_kwargs):  # fmt: skip
+                 layer_attr: str = "blocks", layer_kwargs=None, **block_kwargs):  # fmt: skip
         super().__init__()
         self._layer_attr = layer_attr
-        setattr(
-            self, layer_attr,
-            nn.ModuleList([PairFormerBlock(c_pair, c_single, optim=optim, **block_kwargs) for _ in range(num_blocks)]),
-        )  # fmt: skip
+
+        def block(i: int) -> PairFormerBlock:
+            kw = dict(block_kwargs)
+            if layer_kwargs is not None:
+                kw.update(layer_kwargs(i))
+            return PairFormerBlock(c_pair, c_single, optim=optim, **kw)
+
+        setattr(self, layer_attr, nn.ModuleList([block(i) for i in range(num_blocks)]))
 
     @property
     def blocks(self) -> nn.ModuleList:
@@ -232,8 +254,6 @@ class TemplatePairFormerBlock(nn.Module):
                 f"num_channels={num_channels}, num_heads={num_heads}: the pair kernels are built for 128 channels "
                 "and 4 heads of 32",
             )  # fmt: skip
-        if residual_out_scale != 1.0:
-            raise NotActive("TemplatePairFormerBlock", "only a unit residual scale is built")
         self.tri_mul_out = TriangleMulOutgoing(num_channels, optim=optim)
         self.tri_mul_in = TriangleMulIncoming(num_channels, optim=optim)
         self.pair_attn_row = GridSelfAttention(num_channels, num_heads=num_heads, transpose=False, optim=optim)
@@ -241,7 +261,11 @@ class TemplatePairFormerBlock(nn.Module):
         self.pair_transition = make_transition_block(num_channels, num_intermediate_factor, config=optim)
         self.num_intermediate_factor = num_intermediate_factor
         self.pair_dropout = pair_dropout
-        self.residual_out_scale = 1.0
+        # Every branch is output-scaled by residual_out_scale (template_embedding.py:233-240),
+        # folded into each branch's output projection.
+        self.residual_out_scale = float(residual_out_scale)
+        for m in (self.tri_mul_out, self.tri_mul_in, self.pair_attn_row, self.pair_attn_col, self.pair_transition):
+            m.branch_scale = self.residual_out_scale
 
     def forward_(self, pair: torch.Tensor, pair_mask: torch.Tensor) -> torch.Tensor:
         """In place: ``pair`` [B, N, N, C] contiguous (``template_embedding.py:230-240``, eval)."""
@@ -263,3 +287,94 @@ class TemplatePairFormerBlock(nn.Module):
             pair, pair_mask = pair.unsqueeze(0), pair_mask.unsqueeze(0)
         out = self.forward_(pair.contiguous().clone(), pair_mask)
         return out if has_batch else out.squeeze(0)
+
+
+class TrunkRecycler(nn.Module):
+    """The recycling embeddings around the trunk (``evoformer.py:400-412``; applied at
+    ``:520-526`` and ``:558-561``): ``pair = pair_init + prev_embedding(LN(prev_pair))`` and,
+    with the single track, ``single = single_init + prev_single_embedding(LN(prev_single))``.
+    Submodule names as in the reference's ``Evoformer`` (``prev_embedding_layer_norm``,
+    ``prev_embedding``, ``prev_single_embedding_layer_norm``, ``prev_single_embedding``), so
+    the ``evoformer.prev_*`` keys of a checkpoint load unchanged. Both projections start at
+    zero (AF3 final init)."""
+
+    def __init__(self, c_pair: int = 128, c_single: int = 384, use_single_track: bool = True,
+                 optim: OptimConfig | None = None):  # fmt: skip
+        super().__init__()
+        require_hip("TrunkRecycler", optim)
+        self.prev_embedding_layer_norm = LayerNorm(c_pair)
+        self.prev_embedding = LinearNoBias(c_pair, c_pair, initializer="zeros")
+        self.use_single_track = bool(use_single_track)
+        if self.use_single_track:
+            self.prev_single_embedding_layer_norm = LayerNorm(c_single)
+            self.prev_single_embedding = LinearNoBias(c_single, c_single, initializer="zeros")
+        self._cache = WeightCache()
+
+    def _operands(self, cdt: torch.dtype) -> dict:
+        from .kernels import cast_weight
+
+        mods = [(self.prev_embedding_layer_norm, self.prev_embedding)]
+        if self.use_single_track:
+            mods.append((self.prev_single_embedding_layer_norm, self.prev_single_embedding))
+        params = [p for ln, lin in mods for p in (ln.weight, ln.bias, lin.weight)]
+
+        def build():
+            return [(f32(ln.weight), f32(ln.bias), ln.eps, cast_weight(lin.weight, cdt)) for ln, lin in mods]
+
+        return self._cache.get(params, cdt, build)
+
+    @inference_only("TrunkRecycler")
+    def forward_(
+        self, pair: torch.Tensor, single: torch.Tensor, prev_pair: torch.Tensor, prev_single: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """In place: ``pair += prev_embedding(LN(prev_pair))`` (and the single track)."""
+        from .kernels import recycle_embed_
+
+        kernel_census.record("TrunkRecycler", "hip_recycle_embed")
+        ops = self._operands(gemm_dtype_for(pair))
+        recycle_embed_(pair, prev_pair, *ops[0])
+        if self.use_single_track:
+            recycle_embed_(single, prev_single, *ops[1])
+        return pair, single
+
+    @inference_only("TrunkRecycler")
+    def forward(
+        self, pair_init: torch.Tensor, single_init: torch.Tensor, prev_pair: torch.Tensor, prev_single: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """New ``(pair, single)``: the initial embeddings plus the recycling embeddings."""
+        return self.forward_(
+            pair_init.contiguous().clone(), single_init.contiguous().clone(), prev_pair, prev_single
+        )
+
+
+def run_recycles(
+    recycler: TrunkRecycler,
+    trunk: PairFormerStack,
+    pair_init: torch.Tensor,
+    single_init: torch.Tensor,
+    pair_mask: torch.Tensor,
+    seq_mask: torch.Tensor,
+    num_recycles: int,
+    between=None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The recycle loop around the trunk (``model.py:385-470``), inference form.
+
+    The previous outputs start at zero (``model.py:311-319``). Each of the
+    ``num_recycles + 1`` passes adds the recycling embeddings of the previous pass's outputs
+    to the initial embeddings, runs ``between(pair, single)`` -- the stages the reference
+    runs between the recycling embedding and the trunk (template embedding, MSA stack;
+    outside this build, skipped when None) -- and the trunk; its outputs feed the next pass
+    (``model.py:468-470``). Returns the last pass's ``(pair, single)``.
+    """
+    if num_recycles < 0:
+        raise ValueError(f"num_recycles={num_recycles} must be >= 0")
+    prev_pair = torch.zeros_like(pair_init)
+    prev_single = torch.zeros_like(single_init)
+    pair = single = None
+    for _ in range(num_recycles + 1):
+        pair, single = recycler(pair_init, single_init, prev_pair, prev_single)
+        if between is not None:
+            pair, single = between(pair, single)
+        pair, single = trunk(pair, single, pair_mask, seq_mask)
+        prev_pair, prev_single = pair, single
+    return pair, single

@@ -63,6 +63,15 @@ def cast_weight(w: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return out
 
 
+def scaled_weight(w: torch.Tensor, scale: float, dtype: torch.dtype) -> torch.Tensor:
+    """``cast_weight(scale * w)``: a residual branch's output projection with the branch's
+    residual scale folded in. Every scaled branch ends in this bias-free linear map, so
+    ``x + s F(x)`` is ``x + F'(x)`` with ``W_out' = s W_out`` (``evoformer.py:282-321``)."""
+    if scale == 1.0:
+        return cast_weight(w, dtype)
+    return cast_weight(w.detach().to(torch.float32) * float(scale), dtype)
+
+
 def residual_add(res: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``res + x`` in ``res``'s dtype (eval-mode dropout-add, ``triton/dropout_add.py:221-265``)."""
     _lib.require_device("residual_add", res, x)
@@ -353,6 +362,29 @@ def transition_forward(
         "pf_transition_fwd", xc.data_ptr(), _f32(ln_w).data_ptr(), _f32(ln_b).data_ptr(), float(eps), w1.data_ptr(),
         w2.data_ptr(), M, C, factor, _lib.dtype_code(x.dtype), code_c, out.data_ptr(), int(accumulate),
         ws.data_ptr(), ws_bytes, _lib.stream_of(xc),
+    )  # fmt: skip
+    return out
+
+
+def recycle_embed_(
+    out: torch.Tensor, prev: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor, eps: float, w: torch.Tensor
+) -> torch.Tensor:
+    """``out += LN(prev) w^T`` in place (the recycling embedding, ``evoformer.py:520-526``,
+    ``:558-561``); ``w`` [C, C] in the GEMM operand dtype."""
+    _lib.require_device("recycle_embed", prev, out)
+    C = prev.shape[-1]
+    _lib.check_out("recycle_embed", out, prev)
+    if tuple(w.shape) != (C, C):
+        raise NotActive("recycle_embed", f"weight shape {tuple(w.shape)} is not ({C}, {C})")
+    prev_c = prev.contiguous()
+    M = prev_c.numel() // C
+    code_c = _lib.dtype_code(w.dtype)
+    ws_bytes = _lib.lib().pf_recycle_embed_workspace_bytes(M, C, code_c)
+    ws = _workspace(ws_bytes, prev.device)
+    _lib.call(
+        "pf_recycle_embed_fwd", prev_c.data_ptr(), _f32(ln_w).data_ptr(), _f32(ln_b).data_ptr(), float(eps),
+        w.data_ptr(), M, C, _lib.dtype_code(prev.dtype), code_c, out.data_ptr(), ws.data_ptr(), ws_bytes,
+        _lib.stream_of(prev_c),
     )  # fmt: skip
     return out
 

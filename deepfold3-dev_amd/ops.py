@@ -16,7 +16,7 @@ import torch.nn as nn
 from . import kernel_census
 from .config import OptimConfig, require_hip
 from .inference_guard import NotActive, inference_only
-from .kernels import cast_weight, gemm_dtype_for, pack_trimul_weights, trimul_forward
+from .kernels import cast_weight, gemm_dtype_for, pack_trimul_weights, scaled_weight, trimul_forward
 from .primitives import LayerNorm, LinearNoBias, WeightCache
 
 
@@ -48,6 +48,8 @@ class _TriangleMulBase(nn.Module):
         # contraction stays P Q^T on transposed planes (ops.py:285-288).
         self._block_order = torch.cat((even, odd)) if self._outgoing else torch.cat((odd, even))
         self._cache = WeightCache()
+        # Residual scale of this branch (the block's ``s_ros``), folded into out_proj.
+        self.branch_scale = 1.0
 
     def _operands(self, cdt: torch.dtype):
         params = [
@@ -60,13 +62,13 @@ class _TriangleMulBase(nn.Module):
             f32 = lambda t: t.detach().to(torch.float32).contiguous()  # noqa: E731
             return dict(
                 packed=pack_trimul_weights(self.proj.weight[order], self.gate.weight[order], cdt),
-                w_out=cast_weight(self.out_proj.weight, cdt),
+                w_out=scaled_weight(self.out_proj.weight, self.branch_scale, cdt),
                 w_out_gate=cast_weight(self.out_gate.weight, cdt),
                 lniw=f32(self.norm_left.weight), lnib=f32(self.norm_left.bias),
                 lnow=f32(self.norm_center.weight), lnob=f32(self.norm_center.bias),
             )  # fmt: skip
 
-        return self._cache.get(params, cdt, build)
+        return self._cache.get(params, cdt, build, tag=self.branch_scale)
 
     def _run(self, z: torch.Tensor, mask: torch.Tensor, out: torch.Tensor | None, accumulate: bool) -> torch.Tensor:
         kernel_census.record("TriangleMul", "hip_trimul")

@@ -42,15 +42,16 @@ class WeightCache:
     """Prepared (cast / packed) weight operands, rebuilt when a parameter changes.
 
     The key is every parameter's storage pointer and in-place version counter plus
-    the operand dtype, so an optimizer step or ``load_state_dict`` invalidates it.
+    the operand dtype and a caller tag (a folded residual scale), so an optimizer step,
+    ``load_state_dict`` or a new scale invalidates it.
     """
 
     def __init__(self):
         self._key = None
         self._val = None
 
-    def get(self, params: list[torch.Tensor], dtype: torch.dtype, build):
-        key = (dtype, tuple((p.data_ptr(), p._version) for p in params))
+    def get(self, params: list[torch.Tensor], dtype: torch.dtype, build, tag=None):
+        key = (dtype, tag, tuple((p.data_ptr(), p._version) for p in params))
         if key != self._key:
             self._val = build()
             self._key = key
@@ -105,23 +106,27 @@ class TransitionBlock(nn.Module):
         if linear_out_init_gain is not None:
             nn.init.orthogonal_(self.linear2.weight, gain=float(linear_out_init_gain))
         self._cache = WeightCache()
+        # Residual scale of this branch (s_ros times the transition's residual gain),
+        # folded into linear2.
+        self.branch_scale = 1.0
 
     @property
     def fused_pair(self) -> bool:
         return self.c == 128 and self.n == 4
 
     def operands(self, cdt: torch.dtype) -> dict:
-        from .kernels import cast_weight
+        from .kernels import cast_weight, scaled_weight
 
         params = [self.norm.weight, self.norm.bias, self.linear1.weight, self.linear2.weight]
 
         def build():
             return dict(
-                w1=cast_weight(self.linear1.weight, cdt), w2=cast_weight(self.linear2.weight, cdt),
+                w1=cast_weight(self.linear1.weight, cdt),
+                w2=scaled_weight(self.linear2.weight, self.branch_scale, cdt),
                 lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
             )  # fmt: skip
 
-        return self._cache.get(params, cdt, build)
+        return self._cache.get(params, cdt, build, tag=self.branch_scale)
 
     def run(self, x: torch.Tensor, out=None, accumulate: bool = False, s2p=None):
         from . import kernel_census

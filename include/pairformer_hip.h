@@ -140,6 +140,15 @@ int pf_transition_fwd(const void* x, const float* ln_w, const float* ln_b, float
                       long M, int C, int factor, int zdtype, int cdtype, void* out, int accumulate, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* Recycling embedding around the trunk (evoformer.py:520-526 for the pair,
+ * :558-561 for the single track): out += prev_embedding(prev_embedding_layer_norm(prev)),
+ * prev and out [M, C] zdtype (not aliased), w [C, C] cdtype (the LinearNoBias weight, rows =
+ * output channels). C a multiple of 64. */
+size_t pf_recycle_embed_workspace_bytes(long M, int C, int cdtype);
+int pf_recycle_embed_fwd(const void* prev, const float* ln_w, const float* ln_b, float eps, const void* w, long M,
+                         int C, int zdtype, int cdtype, void* out, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
 /* ---- single attention with pair bias ----------------------------------- */
 /* SingleAttention.forward (attention.py:344-452), pair_bias_gate off: s [B,N,C] zdtype;
  * seq_mask [B,N] fp32; pair_logits [B,H,N,N] fp32; w_qkvg [4C, C] cdtype rows

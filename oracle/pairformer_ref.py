@@ -22,6 +22,11 @@ Pinning (what checks this restatement, beyond retyping it):
     (``tests/test_oracle.py``).
   * invariants: batch consistency, row-chunked == whole, fully masked rows
     give the mean of V.
+  * residual scales: a scale s on every branch equals the unscaled block with each
+    branch's bias-free output projection multiplied by s (every branch is linear in
+    it); a zero transition gain equals a zeroed ``linear2``; s = 0 returns the inputs.
+  * recycling embedding: zero previous outputs give ``init + b W^T`` (LN of a zero row
+    is its bias b); LayerNorm's invariance to per-row shifts; linearity in W.
 """
 
 from __future__ import annotations
@@ -39,6 +44,8 @@ __all__ = [
     "pairformer_block",
     "template_pairformer_block",
     "pairformer_trunk",
+    "recycle_embed",
+    "recycled_trunk",
 ]
 
 
@@ -195,6 +202,11 @@ def single_attention(
     return F.linear(out * g, p["out_proj.weight"])
 
 
+def _scaled(x: torch.Tensor, s: float) -> torch.Tensor:
+    """``s * x``; a unit scale returns ``x`` itself (the same values, one pass fewer)."""
+    return x if s == 1.0 else s * x
+
+
 def pairformer_block(
     pair: torch.Tensor,
     single: torch.Tensor,
@@ -203,28 +215,38 @@ def pairformer_block(
     p: dict[str, torch.Tensor],
     row_chunk: int = 0,
     branches: dict[str, torch.Tensor] | None = None,
+    scales: dict | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``PairFormerBlock.forward`` in eval mode (``evoformer.py:270-355``).
 
-    Identity branch scaler, ``residual_out_scale = 1``, eval dropout-add is a
-    plain add (``dropout_add.py:236-237``). If ``branches`` is a dict, each
-    branch output is stored in it under the reference submodule name.
+    Identity branch scaler, eval dropout-add is a plain add (``dropout_add.py:236-237``).
+    ``scales`` may hold ``residual_out_scale`` (s_ros, every branch) and
+    ``pair_transition_residual_gain`` / ``single_transition_residual_gain`` (None = 1, the
+    transitions' extra factor), applied to each branch output as at ``evoformer.py:282-353``.
+    If ``branches`` is a dict, each unscaled branch output is stored in it under the
+    reference submodule name.
     """
+    sc = scales or {}
+    s_ros = float(sc.get("residual_out_scale", 1.0))
+    g_pf = sc.get("pair_transition_residual_gain")
+    g_sf = sc.get("single_transition_residual_gain")
+    s_pf = s_ros * (1.0 if g_pf is None else float(g_pf))
+    s_sf = s_ros * (1.0 if g_sf is None else float(g_sf))
     tmo = tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True)
-    pair = pair + tmo
+    pair = pair + _scaled(tmo, s_ros)
     tmi = tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False)
-    pair = pair + tmi
+    pair = pair + _scaled(tmi, s_ros)
     row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
-    pair = pair + row
+    pair = pair + _scaled(row, s_ros)
     col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
-    pair = pair + col
+    pair = pair + _scaled(col, s_ros)
     pt = transition(pair, _sub(p, "pair_transition."))
-    pair = pair + pt
+    pair = pair + _scaled(pt, s_pf)
     logits = single_to_pair(pair, p)
     sa = single_attention(single, seq_mask, logits, _sub(p, "single_attn."))
-    single = single + sa
+    single = single + _scaled(sa, s_ros)
     st = transition(single, _sub(p, "single_transition."))
-    single = single + st
+    single = single + _scaled(st, s_sf)
     if branches is not None:
         branches.update(
             tri_mul_out=tmo,
@@ -240,16 +262,24 @@ def pairformer_block(
 
 
 def template_pairformer_block(
-    pair: torch.Tensor, pair_mask: torch.Tensor, p: dict[str, torch.Tensor], row_chunk: int = 0
+    pair: torch.Tensor,
+    pair_mask: torch.Tensor,
+    p: dict[str, torch.Tensor],
+    row_chunk: int = 0,
+    residual_out_scale: float = 1.0,
 ) -> torch.Tensor:
     """``TemplatePairFormerBlock.forward`` in eval mode (``template_embedding.py:220-240``):
     the five pair branches of the PairFormer block in the same order, the transition with
-    its own intermediate factor (read from the weights), residual_out_scale 1."""
-    pair = pair + tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True)
-    pair = pair + tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False)
-    pair = pair + grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
-    pair = pair + grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
-    return pair + transition(pair, _sub(p, "pair_transition."))
+    its own intermediate factor (read from the weights), every branch output-scaled by
+    ``residual_out_scale``."""
+    s = float(residual_out_scale)
+    pair = pair + _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True), s)
+    pair = pair + _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False), s)
+    row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
+    pair = pair + _scaled(row, s)
+    col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
+    pair = pair + _scaled(col, s)
+    return pair + _scaled(transition(pair, _sub(p, "pair_transition.")), s)
 
 
 def pairformer_trunk(
@@ -259,8 +289,60 @@ def pairformer_trunk(
     seq_mask: torch.Tensor,
     blocks: list[dict[str, torch.Tensor]],
     row_chunk: int = 0,
+    scales: list[dict] | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """The trunk loop (``evoformer.py:593-601``) without checkpointing or meters."""
-    for p in blocks:
-        pair, single = pairformer_block(pair, single, pair_mask, seq_mask, p, row_chunk=row_chunk)
+    """The trunk loop (``evoformer.py:593-601``) without checkpointing or meters;
+    ``scales[i]`` are block i's residual scales (see ``pairformer_block``)."""
+    for i, p in enumerate(blocks):
+        sc = None if scales is None else scales[i]
+        pair, single = pairformer_block(pair, single, pair_mask, seq_mask, p, row_chunk=row_chunk, scales=sc)
+    return pair, single
+
+
+def recycle_embed(
+    pair_init: torch.Tensor,
+    single_init: torch.Tensor,
+    prev_pair: torch.Tensor,
+    prev_single: torch.Tensor,
+    p: dict[str, torch.Tensor],
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The recycling embeddings (``evoformer.py:520-526`` and ``:558-561``):
+    ``pair_init + LinearNoBias(LN(prev_pair))`` with keys ``prev_embedding_layer_norm.*`` /
+    ``prev_embedding.weight``; the single track likewise with ``prev_single_embedding*``
+    when those keys are present (``use_single_track``)."""
+    pair = pair_init + F.linear(
+        layer_norm(prev_pair, p["prev_embedding_layer_norm.weight"], p["prev_embedding_layer_norm.bias"]),
+        p["prev_embedding.weight"],
+    )
+    single = single_init
+    if "prev_single_embedding.weight" in p:
+        single = single_init + F.linear(
+            layer_norm(
+                prev_single, p["prev_single_embedding_layer_norm.weight"], p["prev_single_embedding_layer_norm.bias"]
+            ),
+            p["prev_single_embedding.weight"],
+        )
+    return pair, single
+
+
+def recycled_trunk(
+    pair_init: torch.Tensor,
+    single_init: torch.Tensor,
+    pair_mask: torch.Tensor,
+    seq_mask: torch.Tensor,
+    recycle_p: dict[str, torch.Tensor],
+    blocks: list[dict[str, torch.Tensor]],
+    num_recycles: int,
+    scales: list[dict] | None = None,
+    row_chunk: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The recycle loop around the trunk (``model.py:385-470``) with the stages between the
+    recycling embedding and the trunk left out: previous outputs start at zero
+    (``model.py:315-319``) and feed the next pass (``:468-470``)."""
+    prev_pair, prev_single = torch.zeros_like(pair_init), torch.zeros_like(single_init)
+    pair = single = None
+    for _ in range(num_recycles + 1):
+        pair, single = recycle_embed(pair_init, single_init, prev_pair, prev_single, recycle_p)
+        pair, single = pairformer_trunk(pair, single, pair_mask, seq_mask, blocks, row_chunk=row_chunk, scales=scales)
+        prev_pair, prev_single = pair, single
     return pair, single

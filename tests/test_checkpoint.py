@@ -1,0 +1,178 @@
+"""CPU: reference-format checkpoints (safetensors with the embedded ModelConfig JSON).
+
+The file is written here in the reference's layout: the trunk under
+``evoformer.trunk_pairformer.{i}.``, the recycling embeddings under ``evoformer.prev_*``, the
+confidence head's layers under ``confidence_head.layers.{i}.``, next to keys of parts this
+build does not have, and ``model_cfg_json`` in the metadata (``config.py:1895-1958``). The
+tests check the architecture mapping against the reference's closed forms
+(``primitives.py:20-44``, ``evoformer.py:66-82``), that every tensor lands where its key
+says, strictness, and refusal by name of what is not built. The forward passes of loaded
+stacks are compared with the oracle in ``tests/test_checkpoint_gpu.py``.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+
+import pytest
+import torch
+
+from tests._helpers import mod
+
+W = mod("weights")
+ck = mod("checkpoint")
+guard = mod("inference_guard")
+
+
+def _recycle(seed: int) -> dict:
+    g = torch.Generator().manual_seed(seed)
+    return {
+        "prev_embedding_layer_norm.weight": 1.0 + 0.2 * torch.randn(128, generator=g),
+        "prev_embedding_layer_norm.bias": 0.3 * torch.randn(128, generator=g),
+        "prev_embedding.weight": torch.randn(128, 128, generator=g) / 128**0.5,
+        "prev_single_embedding_layer_norm.weight": 1.0 + 0.2 * torch.randn(384, generator=g),
+        "prev_single_embedding_layer_norm.bias": 0.3 * torch.randn(384, generator=g),
+        "prev_single_embedding.weight": torch.randn(384, 384, generator=g) / 384**0.5,
+    }
+
+
+def write_checkpoint(path, model_cfg: dict | None, trunk_layers: int = 2, conf_layers: int = 2, seed: int = 40):
+    """A reference-layout checkpoint; returns the tensors written, by key."""
+    from safetensors.torch import save_file
+
+    sd = {}
+    for i, blk in enumerate(W.make_trunk_weights(seed, trunk_layers, perturb_affine=True)):
+        sd.update({f"evoformer.trunk_pairformer.{i}.{k}": v for k, v in blk.items()})
+    sd.update({f"evoformer.{k}": v for k, v in _recycle(seed + 1).items()})
+    for i, blk in enumerate(W.make_trunk_weights(seed + 2, conf_layers, perturb_affine=True)):
+        sd.update({f"confidence_head.layers.{i}.{k}": v for k, v in blk.items()})
+    # parts outside the hot path, which the loaders must leave alone
+    sd["evoformer.position_activations.weight"] = torch.randn(128, 139)
+    sd["evoformer.msa_stack.0.msa_transition.linear1.weight"] = torch.randn(512, 64)
+    sd["confidence_head.pae_logits.weight"] = torch.randn(64, 128)
+    sd["diffusion.conditioning.weight"] = torch.randn(8, 8)
+    sd = {k: v.contiguous() for k, v in sd.items()}
+    meta = None if model_cfg is None else {ck.MODEL_CFG_KEY: json.dumps(model_cfg)}
+    save_file(sd, str(path), metadata=meta)
+    return sd
+
+
+CFG = {
+    "pairformer": {
+        "num_layer": 2,
+        "pair_channel": 128,
+        "pair_attention": {"num_head": 4, "a_future_field": 3},
+        "residual_output_scaling": True,
+        "pair_transition_residual_gain": 0.5,
+        "single_transition_residual_per_layer_extra": True,
+        "a_field_from_a_later_revision": "ignored",
+    },
+    "confidence": {"num_layer": 2, "uniform_residual_scale": True},
+    "evoformer": {"num_layer": 4},
+    "optim": {"use_fused_triangle_mul": True},
+}
+
+
+def test_residual_scale_rules_match_reference_closed_forms():
+    for i in range(5):
+        assert ck.block_residual_scale(i, 48, True, False) == pytest.approx(1 / math.sqrt(i + 1), abs=0)
+        assert ck.block_residual_scale(i, 48, False, True) == pytest.approx(1 / math.sqrt(48), abs=0)
+        assert ck.block_residual_scale(i, 48, False, False) == 1.0
+        assert ck.branch_residual_gain(i, None, False) is None
+        assert ck.branch_residual_gain(i, 0.25, False) == 0.25
+        assert ck.branch_residual_gain(i, None, True) == pytest.approx(1 / math.sqrt(i + 1))
+        assert ck.branch_residual_gain(i, 0.25, True) == pytest.approx(0.25 / math.sqrt(i + 1))
+    with pytest.raises(ValueError, match="mutually exclusive"):
+        ck.block_residual_scale(0, 4, True, True)
+
+
+def test_config_sections_defaults_and_unknown_fields():
+    pf = ck.trunk_config(CFG)
+    assert pf["num_layer"] == 2 and pf["residual_output_scaling"] is True
+    assert pf["pair_attention"] == {"num_head": 4}
+    assert "a_field_from_a_later_revision" not in pf
+    assert pf["seq_channel"] == 384 and pf["use_single_track"] is True  # defaults where silent
+    assert ck.trunk_config(None) == ck.PAIRFORMER_DEFAULTS
+    assert ck.confidence_config(CFG)["uniform_residual_scale"] is True
+    assert ck.confidence_config(None)["num_layer"] == 4
+
+
+def test_trunk_block_kwargs_per_layer():
+    pf = ck.trunk_config(CFG)
+    for i in range(2):
+        kw = ck.trunk_block_kwargs(pf, i)
+        assert kw["residual_out_scale"] == pytest.approx(1 / math.sqrt(i + 1))
+        assert kw["pair_transition_residual_gain"] == 0.5
+        assert kw["single_transition_residual_gain"] == pytest.approx(1 / math.sqrt(i + 1))
+        assert kw["trimul_kwargs"]["num_heads"] == 0 and kw["num_pair_heads"] == 4
+
+
+def test_read_model_cfg(tmp_path):
+    write_checkpoint(tmp_path / "a.safetensors", CFG)
+    assert ck.read_model_cfg(tmp_path / "a.safetensors") == CFG
+    write_checkpoint(tmp_path / "b.safetensors", None)
+    assert ck.read_model_cfg(tmp_path / "b.safetensors") is None
+
+
+def test_load_trunk_recycler_and_confidence(tmp_path):
+    path = tmp_path / "ckpt.safetensors"
+    sd = write_checkpoint(path, CFG)
+    stack, cfg = ck.load_trunk(path)
+    assert cfg == CFG and len(stack.blocks) == 2
+    for i, blk in enumerate(stack.blocks):
+        for k, v in blk.state_dict().items():
+            assert torch.equal(v, sd[f"evoformer.trunk_pairformer.{i}.{k}"]), (i, k)
+        s = 1 / math.sqrt(i + 1)
+        assert blk.residual_out_scale == pytest.approx(s)
+        assert blk.tri_mul_in.branch_scale == pytest.approx(s)
+        assert blk.pair_attn_col.branch_scale == pytest.approx(s)
+        assert blk.pair_transition.branch_scale == pytest.approx(0.5 * s)
+        assert blk.single_transition.branch_scale == pytest.approx(s * s)
+        assert not blk.training
+    rec = ck.load_recycler(path)
+    for k, v in rec.state_dict().items():
+        assert torch.equal(v, sd["evoformer." + k]), k
+    conf = ck.load_confidence_pairformer(path)
+    assert len(conf.layers) == 2
+    for i, blk in enumerate(conf.layers):
+        assert blk.residual_out_scale == pytest.approx(1 / math.sqrt(2))
+        for k, v in blk.state_dict().items():
+            assert torch.equal(v, sd[f"confidence_head.layers.{i}.{k}"]), (i, k)
+    st2, _ = ck.load_trunk(path, dtype=torch.bfloat16)
+    assert all(p.dtype == torch.bfloat16 for p in st2.parameters())
+
+
+def test_loading_is_strict(tmp_path):
+    from safetensors.torch import save_file
+
+    path = tmp_path / "c.safetensors"
+    sd = write_checkpoint(path, CFG)
+    missing = {k: v for k, v in sd.items() if k != "evoformer.trunk_pairformer.1.pair_attn_row.to_q.weight"}
+    save_file(missing, str(tmp_path / "missing.safetensors"), metadata={ck.MODEL_CFG_KEY: json.dumps(CFG)})
+    with pytest.raises(KeyError, match="1.pair_attn_row.to_q.weight"):
+        ck.load_trunk(tmp_path / "missing.safetensors")
+    extra = dict(sd, **{"evoformer.trunk_pairformer.2.tri_mul_out.proj.weight": torch.zeros(256, 128)})
+    save_file(extra, str(tmp_path / "extra.safetensors"), metadata={ck.MODEL_CFG_KEY: json.dumps(CFG)})
+    with pytest.raises(KeyError, match="2.tri_mul_out.proj.weight"):
+        ck.load_trunk(tmp_path / "extra.safetensors")
+    extra_prev = dict(sd, **{"evoformer.prev_pos_embedding.weight": torch.zeros(4, 4)})
+    save_file(extra_prev, str(tmp_path / "prev.safetensors"))
+    with pytest.raises(KeyError, match="prev_pos_embedding"):
+        ck.load_recycler(tmp_path / "prev.safetensors")
+
+
+@pytest.mark.parametrize(
+    "field,value,needle",
+    [
+        ("pair_bias_gate", True, "pair-bias gate"),
+        ("branch_scaler", "rmsnorm", "branch_scaler"),
+        ("trimul_num_heads", 2, "multi-head"),
+        ("use_triangle_attention", False, "triangle-attention"),
+        ("use_single_track", False, "single-track"),
+    ],
+)
+def test_unbuilt_architectures_refuse_by_name(field, value, needle):
+    cfg = {"pairformer": {"num_layer": 1, field: value}}
+    with pytest.raises(guard.NotActive, match=needle):
+        ck.build_trunk(cfg)

@@ -291,3 +291,125 @@ def test_template_block_is_the_pair_half_of_the_block():
     assert torch.equal(got, want)
     assert sd2["pair_transition.linear1.weight"].shape == (512, 128)
     assert rel_l2(got2, want) > 1e-3
+
+
+# Every residual branch ends in a bias-free output projection, so each branch output is
+# linear in that weight: the block with a residual scale s on a branch equals the unscaled
+# block with that projection's weight multiplied by s.
+_OUT_PROJ = {
+    "tri_mul_out.out_proj.weight": "ros",
+    "tri_mul_in.out_proj.weight": "ros",
+    "pair_attn_row.out_proj.weight": "ros",
+    "pair_attn_col.out_proj.weight": "ros",
+    "pair_transition.linear2.weight": "pair",
+    "single_attn.out_proj.weight": "ros",
+    "single_transition.linear2.weight": "single",
+}
+
+
+def _f64(d: dict) -> dict:
+    return {k: (v.double() if v.is_floating_point() else v) for k, v in d.items()}
+
+
+def test_residual_scales_equal_scaled_output_projections():
+    sd = _f64(W.make_block_weights(21, perturb_affine=True))
+    x = _f64(W.make_inputs(10, seed=8, pad_last=2))
+    sc = dict(residual_out_scale=0.6, pair_transition_residual_gain=0.5, single_transition_residual_gain=1.7)
+    factor = {"ros": 0.6, "pair": 0.6 * 0.5, "single": 0.6 * 1.7}
+    scaled = {k: (v * factor[_OUT_PROJ[k]] if k in _OUT_PROJ else v) for k, v in sd.items()}
+    with torch.no_grad():
+        p, s = R.pairformer_block(x["pair"], x["single"], x["pair_mask"], x["seq_mask"], sd, scales=sc)
+        p2, s2 = R.pairformer_block(x["pair"], x["single"], x["pair_mask"], x["seq_mask"], scaled)
+        p1, s1 = R.pairformer_block(x["pair"], x["single"], x["pair_mask"], x["seq_mask"], sd)
+    assert rel_l2(p, p2) < 1e-12 and rel_l2(s, s2) < 1e-12
+    assert rel_l2(p, p1) > 1e-3 and rel_l2(s, s1) > 1e-3  # the scales do act
+
+
+def test_zero_scales():
+    """s_ros = 0 leaves both tracks unchanged; a zero transition gain equals a zeroed linear2
+    of that transition only."""
+    sd = W.make_block_weights(22, perturb_affine=True)
+    x = W.make_inputs(9, seed=2, pad_last=1)
+    args = (x["pair"], x["single"], x["pair_mask"], x["seq_mask"])
+    with torch.no_grad():
+        p0, s0 = R.pairformer_block(*args, sd, scales=dict(residual_out_scale=0.0))
+        pz, sz = R.pairformer_block(*args, sd, scales=dict(pair_transition_residual_gain=0.0))
+        pw, sw = R.pairformer_block(*args, {**sd, "pair_transition.linear2.weight": torch.zeros(128, 512)})
+        qz, tz = R.pairformer_block(*args, sd, scales=dict(single_transition_residual_gain=0.0))
+        qw, tw = R.pairformer_block(*args, {**sd, "single_transition.linear2.weight": torch.zeros(384, 1536)})
+    assert torch.equal(p0, x["pair"]) and torch.equal(s0, x["single"])
+    assert torch.equal(pz, pw) and torch.equal(sz, sw)
+    assert torch.equal(qz, qw) and torch.equal(tz, tw)
+
+
+def test_template_residual_scale_equals_scaled_output_projections():
+    sd = _f64(W.make_block_weights(23, perturb_affine=True, factor=2))
+    p = {k: v for k, v in sd.items() if k.startswith(("tri_mul_", "pair_attn_", "pair_transition."))}
+    x = _f64(W.make_inputs(8, seed=4, pad_last=1))
+    scaled = {k: (v * 0.3 if k in _OUT_PROJ else v) for k, v in p.items()}
+    with torch.no_grad():
+        got = R.template_pairformer_block(x["pair"], x["pair_mask"], p, residual_out_scale=0.3)
+        want = R.template_pairformer_block(x["pair"], x["pair_mask"], scaled)
+    assert rel_l2(got, want) < 1e-12
+
+
+def _recycle_weights(seed: int, c: int = 128, cs: int = 384, single: bool = True) -> dict:
+    g = torch.Generator().manual_seed(seed)
+    p = {
+        "prev_embedding_layer_norm.weight": 1.0 + 0.2 * torch.randn(c, generator=g),
+        "prev_embedding_layer_norm.bias": 0.5 * torch.randn(c, generator=g),
+        "prev_embedding.weight": torch.randn(c, c, generator=g) / c**0.5,
+    }
+    if single:
+        p.update({
+            "prev_single_embedding_layer_norm.weight": 1.0 + 0.2 * torch.randn(cs, generator=g),
+            "prev_single_embedding_layer_norm.bias": 0.5 * torch.randn(cs, generator=g),
+            "prev_single_embedding.weight": torch.randn(cs, cs, generator=g) / cs**0.5,
+        })  # fmt: skip
+    return p
+
+
+def test_recycle_embed_zero_prev_is_bias_projection():
+    """LayerNorm of a zero row is its bias b, so zero previous outputs add b W^T (W not
+    symmetric: a transposed operand would fail)."""
+    p = _f64(_recycle_weights(3))
+    g = torch.Generator().manual_seed(4)
+    zp, zs = torch.randn(1, 6, 6, 128, generator=g).double(), torch.randn(1, 6, 384, generator=g).double()
+    pair, single = R.recycle_embed(zp, zs, torch.zeros_like(zp), torch.zeros_like(zs), p)
+    wp = p["prev_embedding_layer_norm.bias"] @ p["prev_embedding.weight"].T
+    ws = p["prev_single_embedding_layer_norm.bias"] @ p["prev_single_embedding.weight"].T
+    assert rel_l2(pair, zp + wp) < 1e-13 and rel_l2(single, zs + ws) < 1e-13
+    assert rel_l2(pair, zp + p["prev_embedding_layer_norm.bias"] @ p["prev_embedding.weight"]) > 1e-2
+
+
+def test_recycle_embed_invariants():
+    """LayerNorm removes a per-row shift of the previous outputs; the embedding is linear in
+    the projection weight; without the single-track keys the single track passes through."""
+    p = _f64(_recycle_weights(5))
+    g = torch.Generator().manual_seed(6)
+    zp, zs = torch.randn(1, 5, 5, 128, generator=g).double(), torch.randn(1, 5, 384, generator=g).double()
+    pp, ps = torch.randn(1, 5, 5, 128, generator=g).double(), torch.randn(1, 5, 384, generator=g).double()
+    a, b = R.recycle_embed(zp, zs, pp, ps, p)
+    a2, b2 = R.recycle_embed(zp, zs, pp + 3.0 * torch.randn(1, 5, 5, 1, generator=g).double(),
+                             ps - 2.0 * torch.randn(1, 5, 1, generator=g).double(), p)  # fmt: skip
+    # the oracle's LayerNorm computes in fp32 (primitives.py:90-115), so the shift cancels to fp32 precision
+    assert rel_l2(a, a2) < 1e-6 and rel_l2(b, b2) < 1e-6
+    p2 = dict(p, **{"prev_embedding.weight": 2.0 * p["prev_embedding.weight"]})
+    c, _ = R.recycle_embed(zp, zs, pp, ps, p2)
+    assert rel_l2(c - zp, 2.0 * (a - zp)) < 1e-13
+    pair_only = {k: v for k, v in p.items() if not k.startswith("prev_single")}
+    _, same = R.recycle_embed(zp, zs, pp, ps, pair_only)
+    assert same is zs
+
+
+def test_recycled_trunk_is_recycle_then_trunk():
+    blocks = W.make_trunk_weights(31, 2)
+    rp = _recycle_weights(7)
+    x = W.make_inputs(8, seed=5, pad_last=1)
+    args = (x["pair_mask"], x["seq_mask"])
+    with torch.no_grad():
+        got = R.recycled_trunk(x["pair"], x["single"], *args, rp, blocks, num_recycles=1)
+        zp, zs = torch.zeros_like(x["pair"]), torch.zeros_like(x["single"])
+        p, s = R.pairformer_trunk(*R.recycle_embed(x["pair"], x["single"], zp, zs, rp), *args, blocks)
+        p, s = R.pairformer_trunk(*R.recycle_embed(x["pair"], x["single"], p, s, rp), *args, blocks)
+    assert torch.equal(got[0], p) and torch.equal(got[1], s)
