@@ -45,7 +45,7 @@ SIGNATURES: dict[str, tuple] = {
     "pf_grid_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "pf_grid_attn_fwd": (
         _i,
-        [_vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
+        [_vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _vp, _sz, _vp],
     ),
     "pf_pair_transition_fwd": (
         _i,
@@ -61,6 +61,7 @@ SIGNATURES: dict[str, tuple] = {
     "pf_recycle_embed_fwd": (_i, [_vp, _vp, _vp, _f, _vp, _l, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "pf_evo_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "pf_evo_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "pf_pair_mask_outer": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "pf_grid_attn_redo_flags": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "pf_evo_attn_redo_flags": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "pf_pair_bias_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),

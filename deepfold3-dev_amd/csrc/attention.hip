@@ -55,6 +55,15 @@ constexpr int kPad = 128;  // token padding of the attention frame
 // 64 j + lane: each of its two loads reads one contiguous kilobyte.
 PF_DEVICE int kv_chunk(int row, int c) { return 32 * (2 * (c & 1) + (c >> 1)) + row; }
 
+// For a pair mask that is the outer product of its binary diagonal (m[i][k] = m[i][i]
+// m[k][k], the trunk's seq_mask x seq_mask) every line with m[i][i] = 1 masks the same keys,
+// so their additive key mask km[b][k] = 1e9 (m[k][k] - 1) is added to the shared pair bias
+// once and the flash kernel needs no per-line mask (a line with m[i][i] = 0 has every key
+// masked and takes the closed form). In the log2 domain; padding keys (key >= N) get -inf.
+PF_DEVICE float folded_key_mask(const float* km, int N, int key) {
+  return key < N ? km[key] * kLog2e : -INFINITY;
+}
+
 
 // ------------------------------------------------------------------ A1
 // w5 [4C + 16][C] (cdtype): rows q | k | v | g | pb (H rows) | zero padding.
@@ -581,7 +590,7 @@ PF_DEVICE Frag16<float> buf_frag16<float>(__amdgpu_buffer_rsrc_t r, int voff, in
 // outputs finite -- and writes a per-wave flag redo[blockIdx.x * 4 + wave]; a flagged block
 // is recomputed by the exact mode (FAST = false with `redo` set), which runs the lazy
 // running-maximum softmax below and skips every block whose flags are all 0.
-template <class TC, int QS, bool O_HEAD_MAJOR, bool FAST, bool POST_SCALE = false>
+template <class TC, int QS, bool O_HEAD_MAJOR, bool FAST, bool POST_SCALE = false, bool KMASK = true>
 __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2)) void tri_attn_kernel(
     const TC* __restrict__ Q, const TC* __restrict__ K, const TC* __restrict__ Vt, const float* __restrict__ PB,
     const float* __restrict__ MA, TC* __restrict__ O, int B, int N, int Np, int L, int Lp, int zero_masked_lines,
@@ -595,8 +604,8 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
   constexpr int DL = TILE * 4 / (NT * 16);        // direct loads per lane per stage
   static_assert(DL * NT * 16 == TILE * 4, "bias stage must split evenly over the block");
   constexpr int NSET = attn_kv_sets<TC>();
-  // vmcnt budget: loads a lane issues per key block (bias stage + K + V + mask slot)
-  constexpr int KV_LOADS = (sizeof(TC) == 2 ? 4 : 8) + 1;
+  // vmcnt budget: loads a lane issues per key block (bias stage + K + V [+ mask slot])
+  constexpr int KV_LOADS = (sizeof(TC) == 2 ? 4 : 8) + (KMASK ? 1 : 0);
   // The bias ring is dynamic LDS (attn_bias_lds_bytes at launch): the stage a step reads
   // is never the one its direct loads fill, and the explicit vmcnt + barrier order them.
   extern __shared__ __attribute__((aligned(16))) float bias_lds[];
@@ -636,6 +645,11 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
   const float* MAl = MA + lineq * Np;
   const int q0 = qb * QB;
   const int nkb = (N + 31) / 32;
+  // Last key block a load may address. With the key mask applied here (KMASK), steps past
+  // nkb reload block nkb - 1 and the mask sends them to -inf; without it (the mask is in
+  // the bias, which is -inf at every padding key), such steps read the padding blocks up to
+  // Np (K and V zero there), which add nothing.
+  const int kb_last = KMASK ? nkb - 1 : Np / 32 - 1;
 
   const auto rk = buf_rsrc(Kh, (unsigned)(Np * kHeadDim * sizeof(TC)));
   const auto rv = buf_rsrc(Vh, (unsigned)(kHeadDim * Np * sizeof(TC)));
@@ -664,15 +678,18 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
   auto stage_of = [&](int kb, int u) { return NSET == kBiasStages ? u % NSET : kb % kBiasStages; };
   auto bias_issue = [&](int kb, int u) {
     float* st = bias_lds + stage_of(kb, u) * TILE;
-    const int soff = min(kb, nkb - 1) * 32 * 4;
+    const int soff = min(kb, kb_last) * 32 * 4;
 #pragma unroll
     for (int j = 0; j < DL; ++j) buf_load_lds16(rb, st + (w * DL + j) * 8 * 32, b_voff[j], soff);
   };
   auto kv_load = [&](int kb, Frag16<TC>& kf, Frag16<TC>& vf, float& mf) {
-    const int k0 = min(kb, nkb - 1) * 32;
+    const int k0 = min(kb, kb_last) * 32;
     kf = buf_frag16<TC>(rk, k_voff, k0 * kHeadDim * (int)sizeof(TC));
     vf = buf_frag16<TC>(rv, v_voff, k0 * v_kstride);
-    mf = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, m_voff, k0 * 4, 0));
+    if constexpr (KMASK)
+      mf = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, m_voff, k0 * 4, 0));
+    else
+      mf = 0.f;
   };
 
   // Q of this wave's line -> LDS (rows of D elements, padded)
@@ -772,7 +789,7 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
 #pragma unroll
         for (int e = 0; e < 4; ++e) sacc[4 * i + e] = bv[e];
       }
-      mma_mask(sacc, mk, TC{});
+      if constexpr (KMASK) mma_mask(sacc, mk, TC{});
       Frag16<TC> qf;
       qf.v[0] = *reinterpret_cast<const bf16x8*>(qw + R * QLD + 8 * ((2 * hf) ^ qswz(R)));
       qf.v[1] = *reinterpret_cast<const bf16x8*>(qw + R * QLD + 8 * ((2 * hf + 1) ^ qswz(R)));
@@ -792,7 +809,7 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
 #pragma unroll
         for (int e = 0; e < 4; ++e) sacc[4 * i + e] += bv[e];
       }
-      mma_mask(sacc, mk, TC{});
+      if constexpr (KMASK) mma_mask(sacc, mk, TC{});
     }
     if constexpr (POST_SCALE) {
 #pragma unroll
@@ -986,8 +1003,10 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
 // Column mode: the projection kernel writes the pair bias key-major [h][key][q]; the flash
 // kernel reads it query-major in key-slot order, out[q][slot] = in[slot_key(slot)][q]
 // within each 32-block. 32 x 32 tile (I, J) of the output depends only on tile (J, I) of
-// the input, so one block swaps a tile pair in place (I <= J; blockIdx.y = b h).
-__global__ __launch_bounds__(256) void pb_transpose_kernel(float* __restrict__ PB, int Np) {
+// the input, so one block swaps a tile pair in place (I <= J; blockIdx.y = b h). With an
+// outer-product key mask `km` [b][N] its folded value is added on the way.
+__global__ __launch_bounds__(256) void pb_transpose_kernel(float* __restrict__ PB, int Np,
+                                                           const float* __restrict__ km, int N) {
   __shared__ float ta[32][33], tb[32][33];
   const int nt = Np / 32;
   int p = blockIdx.x, I = 0;
@@ -1003,10 +1022,36 @@ __global__ __launch_bounds__(256) void pb_transpose_kernel(float* __restrict__ P
     tb[r][c] = M[(size_t)(32 * J + r) * Np + 32 * I + c];
   }
   __syncthreads();
+  const float* kb = km ? km + (size_t)(blockIdx.y / kHeads) * N : nullptr;
   for (int i = threadIdx.x; i < 1024; i += 256) {
     const int q = i >> 5, sl = i & 31;
-    M[(size_t)(32 * I + q) * Np + 32 * J + sl] = tb[slot_key(sl)][q];
-    M[(size_t)(32 * J + q) * Np + 32 * I + sl] = ta[slot_key(sl)][q];
+    float x = tb[slot_key(sl)][q], y = ta[slot_key(sl)][q];
+    if (kb) {
+      x += folded_key_mask(kb, N, 32 * J + slot_key(sl));
+      y += folded_key_mask(kb, N, 32 * I + slot_key(sl));
+    }
+    M[(size_t)(32 * I + q) * Np + 32 * J + sl] = x;
+    M[(size_t)(32 * J + q) * Np + 32 * I + sl] = y;
+  }
+}
+
+// Row mode: the folded outer-product key mask km [b][N] added to the query-major pair bias
+// [b][h][q][slot] (key = slot_key of the slot inside its 32-block), four slots per thread.
+__global__ __launch_bounds__(256) void pb_fold_kernel(float* __restrict__ PB, const float* __restrict__ km, int N,
+                                                      int Np) {
+  const size_t bh = blockIdx.y;
+  const float* kb = km + (bh / kHeads) * N;
+  f32x4* M = reinterpret_cast<f32x4*>(PB + bh * Np * Np);
+  const size_t n4 = (size_t)Np * Np / 4;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+    const int slot0 = (int)((4 * i) % Np);
+    f32x4 v = M[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int sl = slot0 + e;
+      v[e] += folded_key_mask(kb, N, (sl & ~31) + slot_key(sl & 31));
+    }
+    M[i] = v;
   }
 }
 
@@ -1335,7 +1380,8 @@ AttnWs attn_ws_layout(int B, int N, int cdtype) {
 
 template <class TZ, class TC>
 int grid_attn_launch(const void* z, const float* mask, const float* lnw, const float* lnb, float eps, const void* w5,
-                     const void* wo, int B, int N, int transpose, void* out, int accumulate, void* ws, hipStream_t s) {
+                     const void* wo, int B, int N, int transpose, void* out, int accumulate, const float* key_mask,
+                     void* ws, hipStream_t s) {
   const int Np = (int)pf::round_up((size_t)N, kPad);
   const AttnWs L = attn_ws_layout(B, N, sizeof(TC) == 4 ? PF_F32 : PF_BF16);
   char* base = reinterpret_cast<char*>(ws);
@@ -1366,10 +1412,19 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     timer.stop();
     if (int e = pf::check_launch("attn_project")) return e;
   }
+  // Outer-product mask: its key mask goes into the pair bias (rows: a pass over the bias;
+  // columns: inside the transpose).
+  const bool mask_outer = key_mask != nullptr;
+  if (mask_outer && !transpose) {
+    const long n4 = (long)Np * Np / 4;
+    const int gx = (int)std::min<long>((n4 + 255) / 256, (4L * pf::cu_count() + B * kHeads - 1) / (B * kHeads));
+    pb_fold_kernel<<<dim3(std::max(gx, 1), B * kHeads), 256, 0, s>>>(PBb, key_mask, N, Np);
+    if (int e = pf::check_launch("pb_fold")) return e;
+  }
   if (transpose) {
     const int nt = Np / 32;
     pf::KernelTimer timer("pb_transpose", s);
-    pb_transpose_kernel<<<dim3(nt * (nt + 1) / 2, B * kHeads), 256, 0, s>>>(PBb, Np);
+    pb_transpose_kernel<<<dim3(nt * (nt + 1) / 2, B * kHeads), 256, 0, s>>>(PBb, Np, key_mask, N);
     timer.stop();
     if (int e = pf::check_launch("pb_transpose")) return e;
   }
@@ -1382,13 +1437,23 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     pf::KernelTimer timer("tri_attn", s);
     constexpr int QS = attn_qsub<TC>();
     constexpr int NT = 64 * kLinesPerBlock;
-    tri_attn_kernel<TC, QS, false, true><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(
-        Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap, redo);
+    // With an outer-product mask the key mask is in the bias: no per-line key-mask MFMA or
+    // mask loads.
+    if (mask_outer)
+      tri_attn_kernel<TC, QS, false, true, false, false><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(
+          Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap, redo);
+    else
+      tri_attn_kernel<TC, QS, false, true><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(
+          Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap, redo);
     timer.stop();
     if (int e = pf::check_launch("tri_attn")) return e;
     pf::KernelTimer timer2("tri_attn_redo", s);
-    tri_attn_kernel<TC, QS, false, false><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(
-        Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap, redo);
+    if (mask_outer)
+      tri_attn_kernel<TC, QS, false, false, false, false><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(
+          Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap, redo);
+    else
+      tri_attn_kernel<TC, QS, false, false><<<grid, NT, attn_bias_lds_bytes<TC>(), s>>>(
+          Qb, Kb, Vb, PBb, MAb, Ob, B, N, Np, N, Np, 0, remap, redo);
     timer2.stop();
     if (int e = pf::check_launch("tri_attn_redo")) return e;
   }
@@ -1411,6 +1476,35 @@ int grid_attn_launch(const void* z, const float* mask, const float* lnw, const f
     if (int e = pf::check_launch("attn_out")) return e;
   }
   return pf::ok();
+}
+
+// Whether every pair mask [b][N][N] is the outer product of its binary diagonal (the
+// case folded_key_mask serves): the flag starts at 1 and any element that breaks
+// m[i][k] = m[i][i] m[k][k] with m in {0, 1} clears it (every writer stores the same 0).
+// The init pass also writes the additive key mask of the diagonal, km[b][k] = 1e9 (m[k][k] - 1).
+__global__ __launch_bounds__(256) void mask_outer_init_kernel(const float* __restrict__ mask, int B, int N,
+                                                              int* __restrict__ flag, float* __restrict__ km) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx == 0) flag[0] = 1;
+  if (idx < B * N) {
+    const int b = idx / N, k = idx % N;
+    km[idx] = (mask[((size_t)b * N + k) * N + k] - 1.0f) * 1e9f;
+  }
+}
+
+__global__ __launch_bounds__(256) void mask_outer_check_kernel(const float* __restrict__ mask, int B, int N,
+                                                               int* __restrict__ flag) {
+  const long total = (long)B * N * N;
+  for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (long)gridDim.x * 256) {
+    const long b = idx / ((long)N * N);
+    const long rem = idx - b * N * N;
+    const long i = rem / N, k = rem - i * N;
+    const float* mb = mask + b * N * N;
+    const float m = mb[idx - b * N * N];
+    const float di = mb[i * N + i], dk = mb[k * N + k];
+    const bool ok = (m == 0.f || m == 1.f) && m == di * dk;
+    if (!ok) flag[0] = 0;
+  }
 }
 
 // ------------------------------------------------------------------ kernel-level op
@@ -1578,7 +1672,8 @@ size_t pf_grid_attn_workspace_bytes(int B, int N, int C, int H, int cdtype) {
 
 int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const float* ln_b, float eps,
                      const void* w_qkvgb, const void* w_out, int B, int N, int C, int H, int transpose, int zdtype,
-                     int cdtype, void* out, int accumulate, void* workspace, size_t workspace_bytes, void* stream) {
+                     int cdtype, void* out, int accumulate, const float* key_mask, void* workspace,
+                     size_t workspace_bytes, void* stream) {
   PF_REQUIRE(z && mask && ln_w && ln_b && w_qkvgb && w_out && out && workspace, PF_ERR_INVALID_ARG,
              "pf_grid_attn_fwd: null pointer");
   PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_grid_attn_fwd: B=%d N=%d", B, N);
@@ -1596,12 +1691,24 @@ int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const 
   hipStream_t s = pf::as_stream(stream);
   if (zdtype == PF_F32 && cdtype == PF_F32)
     return grid_attn_launch<float, float>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, transpose, out, accumulate,
-                                          workspace, s);
+                                          key_mask, workspace, s);
   if (zdtype == PF_F32)
     return grid_attn_launch<float, bf16>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, transpose, out, accumulate,
-                                         workspace, s);
+                                         key_mask, workspace, s);
   return grid_attn_launch<bf16, bf16>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, transpose, out, accumulate,
-                                      workspace, s);
+                                      key_mask, workspace, s);
+}
+
+int pf_pair_mask_outer(const float* mask, int B, int N, int* flag, float* key_mask, void* stream) {
+  PF_REQUIRE(mask && flag && key_mask, PF_ERR_INVALID_ARG, "pf_pair_mask_outer: null pointer");
+  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_pair_mask_outer: B=%d N=%d", B, N);
+  hipStream_t s = pf::as_stream(stream);
+  mask_outer_init_kernel<<<(unsigned)((B * N + 255) / 256), 256, 0, s>>>(mask, B, N, flag, key_mask);
+  if (int e = pf::check_launch("mask_outer_init")) return e;
+  const long total = (long)B * N * N;
+  const int nblk = (int)std::min<long>((total + 255) / 256, 4L * pf::cu_count());
+  mask_outer_check_kernel<<<nblk, 256, 0, s>>>(mask, B, N, flag);
+  return pf::check_launch("mask_outer_check");
 }
 
 // Number of redo flags the fast flash pass writes: one per wave of its grid.

@@ -193,6 +193,9 @@ class PairFormerStack(nn.Module):
         stream). The streams join before returning."""
         pair = pair.contiguous().clone()
         single = single.contiguous().clone()
+        # One fp32 mask object for every block: the attention kernels' outer-product check
+        # of the mask is cached per tensor object, so the trunk checks it once.
+        pair_mask = pair_mask.to(torch.float32).contiguous()
         if not pair.is_cuda or len(self.blocks) == 0:
             for blk in self.blocks:
                 blk.forward_(pair, single, pair_mask, seq_mask)

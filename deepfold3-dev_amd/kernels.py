@@ -9,6 +9,8 @@ raises :class:`NotActive`.
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import _lib
@@ -226,6 +228,36 @@ def pack_grid_attn_weights(to_q, to_k, to_v, to_g, pair_bias, dtype: torch.dtype
     return cast_weight(w, dtype)
 
 
+# Outer-product checks of pair masks: (weak reference to the mask, its in-place version,
+# key mask or None) for the last few masks, so a trunk that passes one mask to every block
+# checks it (and synchronises its stream) once.
+_OUTER_SEEN: list = []
+
+
+def outer_key_mask(mask: torch.Tensor) -> torch.Tensor | None:
+    """For an fp32 contiguous pair mask [B, N, N] that is the outer product of its diagonal
+    with values in {0, 1} (the trunk's ``seq_mask x seq_mask``, ``featurizer.py:520``), the
+    diagonal's additive key mask ``1e9 (m[k][k] - 1)`` [B, N]; None for any other mask
+    (``pf_pair_mask_outer``). Cached per tensor object and version; the first check of a
+    mask reads the result back from the device."""
+    for ref, ver, km in _OUTER_SEEN:
+        if ref() is mask and ver == mask._version:
+            return km
+    B, N, _ = mask.shape
+    flag = torch.empty(1, dtype=torch.int32, device=mask.device)
+    km = torch.empty((B, N), dtype=torch.float32, device=mask.device)
+    _lib.call("pf_pair_mask_outer", mask.data_ptr(), B, N, flag.data_ptr(), km.data_ptr(), _lib.stream_of(mask))
+    km = km if bool(flag.item()) else None
+    live = [e for e in _OUTER_SEEN if e[0]() is not None][-7:]
+    _OUTER_SEEN[:] = live + [(weakref.ref(mask), mask._version, km)]
+    return km
+
+
+def pair_mask_is_outer(mask: torch.Tensor) -> bool:
+    """Whether ``outer_key_mask(mask)`` applies."""
+    return outer_key_mask(mask) is not None
+
+
 def grid_attention_forward(
     z: torch.Tensor,
     mask: torch.Tensor,
@@ -238,8 +270,14 @@ def grid_attention_forward(
     num_heads: int = 4,
     out: torch.Tensor | None = None,
     accumulate: bool = False,
+    mask_outer: bool | None = None,
 ) -> torch.Tensor:
-    """GridSelfAttention on prepared operands (``attention.py:167-269``); returns ``out``."""
+    """GridSelfAttention on prepared operands (``attention.py:167-269``); returns ``out``.
+
+    ``mask_outer`` selects the kernel path for the mask: True when the mask is the outer
+    product of its binary diagonal (checked; the key mask then lives in the pair bias),
+    False for the per-line key masks, None for the first when it applies
+    (``outer_key_mask``). Both give the same result."""
     _lib.require_device("GridSelfAttention", z, mask)
     if z.dim() != 4 or z.shape[1] != z.shape[2]:
         raise NotActive("GridSelfAttention", f"z must be [B, N, N, C], got {tuple(z.shape)}")
@@ -259,13 +297,17 @@ def grid_attention_forward(
         out = torch.empty_like(zc)
     else:
         _lib.check_out("GridSelfAttention", out, zc)
+    km = outer_key_mask(m) if mask_outer is None or mask_outer else None
+    if mask_outer and km is None:
+        raise NotActive("GridSelfAttention", "mask_outer=True needs a mask that is the outer product of its diagonal")
     code_c = _lib.dtype_code(cdt)
     ws_bytes = _lib.lib().pf_grid_attn_workspace_bytes(B, N, C, num_heads, code_c)
     ws = _workspace(ws_bytes, z.device)
     _lib.call(
         "pf_grid_attn_fwd", zc.data_ptr(), m.data_ptr(), _f32(ln_w).data_ptr(), _f32(ln_b).data_ptr(), float(eps),
         w_packed.data_ptr(), w_out.data_ptr(), B, N, C, num_heads, int(transpose), _lib.dtype_code(z.dtype), code_c,
-        out.data_ptr(), int(accumulate), ws.data_ptr(), ws_bytes, _lib.stream_of(zc),
+        out.data_ptr(), int(accumulate), 0 if km is None else km.data_ptr(), ws.data_ptr(), ws_bytes,
+        _lib.stream_of(zc),
     )  # fmt: skip
     _lib.note_redo("pf_grid_attn_redo_flags", ws, B, N, C, num_heads, code_c)
     return out

@@ -111,11 +111,24 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
  * Writes the update to `out`, or adds it into `out` when accumulate != 0 (out == z is the
  * fused residual). Masking follows the reference's eager path: keys with mask 0 get
  * -1e9 added in fp32, so a fully masked line attends uniformly (mean of V); the Triton
- * kernel's zero-output rule for such lines is not used. Built: C=128, H=4 (head dim 32). */
+ * kernel's zero-output rule for such lines is not used. Built: C=128, H=4 (head dim 32).
+ * key_mask: NULL, or the caller's assertion that every mask[b] is the outer product of its
+ * binary diagonal (m[i][k] = m[i][i] m[k][k], m in {0, 1}: the trunk's seq_mask x seq_mask),
+ * given as that diagonal's additive key mask key_mask [B,N] fp32 = 1e9 (m[k][k] - 1) (both
+ * from pf_pair_mask_outer). The key mask is then added to the pair bias once and the flash
+ * kernel runs without per-line key masks; the result is the same. A mask that is not of that
+ * form gives wrong results with key_mask set. */
 size_t pf_grid_attn_workspace_bytes(int B, int N, int C, int H, int cdtype);
 int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const float* ln_b, float eps,
                      const void* w_qkvgb, const void* w_out, int B, int N, int C, int H, int transpose, int zdtype,
-                     int cdtype, void* out, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+                     int cdtype, void* out, int accumulate, const float* key_mask, void* workspace,
+                     size_t workspace_bytes, void* stream);
+/* Whether pair masks are outer products (no reference counterpart: it selects
+ * pf_grid_attn_fwd's key_mask path; the pair mask of featurizer.py:520 is seq x seq).
+ * Writes flag[0] (device int) = 1 if every mask[b] [N,N] fp32 equals the outer product of
+ * its diagonal with values in {0, 1}, else 0, and key_mask [B,N] fp32 = 1e9 (m[b][k][k] - 1).
+ * Stream-ordered; the caller reads the flag. */
+int pf_pair_mask_outer(const float* mask, int B, int N, int* flag, float* key_mask, void* stream);
 
 /* ---- transitions ------------------------------------------------------- */
 /* Pair transition, C=128, factor 4: replaces FusedTransitionBlock / TransitionBlock.forward
