@@ -37,6 +37,7 @@
 
 #include "capi.h"
 #include "common.h"
+#include "rowops.h"
 
 namespace {
 
@@ -1617,9 +1618,12 @@ EvoWs evo_ws_layout(int B, int S, int N, int cdtype) {
   return w;
 }
 
+// softmax_scale multiplies q k^T (the reference's d^-1/2; a caller whose heads are zero-padded
+// to 32 dimensions passes its own head dimension's).
 template <class TC>
 int evo_attn_launch(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias, int B,
-                    int S, int N, int zero_rule, void* out, void* ws, hipStream_t s) {
+                    int S, int N, int zero_rule, void* out, void* ws, hipStream_t s,
+                    float softmax_scale = 1.0f / sqrtf((float)kHeadDim)) {
   const int Np = (int)pf::round_up((size_t)N, kPad);
   const EvoWs L = evo_ws_layout(B, S, N, sizeof(TC) == 4 ? PF_F32 : PF_BF16);
   char* base = reinterpret_cast<char*>(ws);
@@ -1632,7 +1636,6 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   // logit (log2 units): bf16 post * (q k^T + (bias + mask) d^1/2) with post = d^-1/2 log2 e;
   // fp32 (q d^-1/2 log2 e) k^T + (bias + mask) log2 e.
   constexpr bool kPost = sizeof(TC) == 2;
-  const float softmax_scale = 1.0f / sqrtf((float)kHeadDim);
   const float qscale = kPost ? 1.f : softmax_scale * kLog2e;
   const float bscale = kPost ? 1.f / softmax_scale : kLog2e;
   const float post = softmax_scale * kLog2e;
@@ -1661,13 +1664,148 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   return pf::check_launch("evo_attn redo");
 }
 
+// ------------------------------------------------------------------ generic channels / heads
+// GridSelfAttention for (C, H) other than (128, 4): the template stack's 64 channels in 4
+// heads of 16 and the 256-channel trunk's 8 heads of 32 (attention.py:56-269, head dim
+// max(C / H, 16), at most 32 here). Composed from the row kernels and the flash kernel:
+// LN(z) -> [q | k | v | g | pair bias] projection -> pack into groups of four heads, the head
+// dimension zero-padded to 32 (the logits and outputs are those of the real dimensions),
+// the line mask 1e9 (m - 1) and the pair bias [h][q][k] of the un-transposed positions ->
+// the flash kernel per group with the real head dimension's softmax scale (eager masked-line
+// rule) -> o * sigmoid(g) back in z order -> out_proj, stored or added into `out`.
+struct GridGenWs {
+  size_t xn, proj, q, k, v, pb, ma, o, og, evo, total;
+};
+
+int grid_gen_head_dim(int C, int H) { return std::max(C / H, 16); }
+
+GridGenWs grid_gen_layout(int B, int N, int C, int H, int cdtype) {
+  const size_t es = cdtype == PF_F32 ? 4 : 2;
+  const int d = grid_gen_head_dim(C, H);
+  const int H4 = (H + 3) / 4 * 4;
+  const size_t M = (size_t)B * N * N;
+  const size_t heads = (size_t)B * N * H4 * N * kHeadDim * es;  // [group][b][line][4][N][32]
+  GridGenWs w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += pf::round_up(bytes, 256);
+    return at;
+  };
+  w.xn = take(M * C * es);
+  w.proj = take(M * (size_t)(4 * H * d + 16) * es);
+  w.q = take(heads);
+  w.k = take(heads);
+  w.v = take(heads);
+  w.pb = take((size_t)B * H4 * N * N * 4);
+  w.ma = take((size_t)B * N * N * 4);
+  w.o = take(heads);
+  w.og = take(M * (size_t)H * d * es);
+  w.evo = take(evo_ws_layout(B, N, N, cdtype).total);
+  w.total = off;
+  return w;
+}
+
+// One thread per (position, head) with the head count padded to a multiple of four (the
+// padding heads are zero). Position (b, x, y) of z: row mode line x, token y; column mode
+// line y, token x. The pair bias is that of position (x, y) in both modes (attention.py:204-209).
+template <class TC>
+__global__ __launch_bounds__(256) void grid_gen_pack_kernel(const TC* __restrict__ proj, const float* __restrict__ mask,
+                                                            TC* __restrict__ Q, TC* __restrict__ K, TC* __restrict__ V,
+                                                            float* __restrict__ PB, float* __restrict__ MA, int B, int N,
+                                                            int H, int H4, int d, int PW, int transpose) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const long M = (long)B * N * N;
+  if (idx >= M * H4) return;
+  const int h = (int)(idx % H4);
+  const long pos = idx / H4;
+  const int b = (int)(pos / ((long)N * N));
+  const int x = (int)((pos / N) % N), y = (int)(pos % N);
+  const int line = transpose ? y : x, tok = transpose ? x : y;
+  const int g = h / 4, hh = h % 4;
+  const size_t head = (((((size_t)g * B + b) * N + line) * 4 + hh) * N + tok) * kHeadDim;
+  const TC* row = proj + pos * PW;
+  const int HD = H * d;
+  for (int e = 0; e < kHeadDim; ++e) {
+    const bool real = h < H && e < d;
+    Q[head + e] = real ? row[h * d + e] : from_f32<TC>(0.f);
+    K[head + e] = real ? row[HD + h * d + e] : from_f32<TC>(0.f);
+    V[head + e] = real ? row[2 * HD + h * d + e] : from_f32<TC>(0.f);
+  }
+  PB[(((size_t)g * B + b) * 4 + hh) * N * N + (size_t)x * N + y] = h < H ? to_f32(row[4 * HD + h]) : 0.f;
+  if (h == 0) MA[((size_t)b * N + line) * N + tok] = (mask[pos] - 1.0f) * 1e9f;
+}
+
+// og[pos][h d + e] = o * sigmoid(g) for the real heads and dimensions, in z position order.
+template <class TC>
+__global__ __launch_bounds__(256) void grid_gen_gate_kernel(const TC* __restrict__ O, const TC* __restrict__ proj,
+                                                            TC* __restrict__ og, int B, int N, int H, int d, int PW,
+                                                            int transpose) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const int HD = H * d;
+  if (idx >= (long)B * N * N * HD) return;
+  const int e = (int)(idx % d);
+  const int h = (int)((idx / d) % H);
+  const long pos = idx / HD;
+  const int b = (int)(pos / ((long)N * N));
+  const int x = (int)((pos / N) % N), y = (int)(pos % N);
+  const int line = transpose ? y : x, tok = transpose ? x : y;
+  const size_t head = (((((size_t)(h / 4) * B + b) * N + line) * 4 + h % 4) * N + tok) * kHeadDim;
+  const float gate = sigmoidf_(to_f32(proj[pos * PW + 3 * HD + h * d + e]));
+  og[pos * HD + h * d + e] = from_f32<TC>(to_f32(O[head + e]) * gate);
+}
+
+template <class TZ, class TC>
+int grid_attn_generic_launch(const void* z, const float* mask, const float* lnw, const float* lnb, float eps,
+                             const void* w5, const void* wo, int B, int N, int C, int H, int transpose, void* out,
+                             int accumulate, void* ws, hipStream_t s) {
+  const int cd = sizeof(TC) == 4 ? PF_F32 : PF_BF16;
+  const GridGenWs L = grid_gen_layout(B, N, C, H, cd);
+  const int d = grid_gen_head_dim(C, H);
+  const int H4 = (H + 3) / 4 * 4;
+  const int PW = 4 * H * d + 16;
+  const long M = (long)B * N * N;
+  char* base = reinterpret_cast<char*>(ws);
+  TC* xn = reinterpret_cast<TC*>(base + L.xn);
+  TC* proj = reinterpret_cast<TC*>(base + L.proj);
+  TC* Q = reinterpret_cast<TC*>(base + L.q);
+  TC* K = reinterpret_cast<TC*>(base + L.k);
+  TC* V = reinterpret_cast<TC*>(base + L.v);
+  float* PB = reinterpret_cast<float*>(base + L.pb);
+  float* MA = reinterpret_cast<float*>(base + L.ma);
+  TC* O = reinterpret_cast<TC*>(base + L.o);
+  TC* og = reinterpret_cast<TC*>(base + L.og);
+  if (int e = ln_launch<TZ, TC>(z, lnw, lnb, eps, xn, M, C, s)) return e;
+  if (int e = rowgemm_launch<TC, TC, EPI_STORE>(xn, w5, nullptr, 0, proj, M, PW, C, s)) return e;
+  grid_gen_pack_kernel<TC><<<(unsigned)((M * H4 + 255) / 256), 256, 0, s>>>(proj, mask, Q, K, V, PB, MA, B, N, H, H4, d,
+                                                                            PW, transpose);
+  if (int e = pf::check_launch("grid_gen_pack")) return e;
+  const size_t group = (size_t)B * N * 4 * N * kHeadDim;  // elements of one four-head group
+  for (int g = 0; g < H4 / 4; ++g) {
+    if (int e = evo_attn_launch<TC>(Q + g * group, K + g * group, V + g * group, MA, PB + (size_t)g * B * 4 * N * N,
+                                    B, N, N, 0, O + g * group, base + L.evo, s, 1.0f / sqrtf((float)d)))
+      return e;
+  }
+  grid_gen_gate_kernel<TC><<<(unsigned)((M * H * d + 255) / 256), 256, 0, s>>>(O, proj, og, B, N, H, d, PW, transpose);
+  if (int e = pf::check_launch("grid_gen_gate")) return e;
+  if (accumulate) return rowgemm_launch<TC, TZ, EPI_RESIDUAL>(og, wo, nullptr, 0, out, M, C, H * d, s);
+  return rowgemm_launch<TC, TZ, EPI_STORE>(og, wo, nullptr, 0, out, M, C, H * d, s);
+}
+
+bool grid_gen_supported(int C, int H) {
+  return H >= 1 && H <= 16 && C % 32 == 0 && C % H == 0 && grid_gen_head_dim(C, H) <= kHeadDim &&
+         (grid_gen_head_dim(C, H) * H) % 16 == 0;
+}
+
+
 }  // namespace
 
 extern "C" {
 
 size_t pf_grid_attn_workspace_bytes(int B, int N, int C, int H, int cdtype) {
-  if (B <= 0 || N <= 0 || C != kC || H != kHeads) return 0;
-  return attn_ws_layout(B, N, cdtype).total;
+  if (B <= 0 || N <= 0) return 0;
+  if (C == kC && H == kHeads) return attn_ws_layout(B, N, cdtype).total;
+  return grid_gen_supported(C, H) ? grid_gen_layout(B, N, C, H, cdtype).total : 0;
 }
 
 int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const float* ln_b, float eps,
@@ -1677,8 +1815,11 @@ int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const 
   PF_REQUIRE(z && mask && ln_w && ln_b && w_qkvgb && w_out && out && workspace, PF_ERR_INVALID_ARG,
              "pf_grid_attn_fwd: null pointer");
   PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_grid_attn_fwd: B=%d N=%d", B, N);
-  PF_REQUIRE(C == kC && H == kHeads, PF_ERR_UNSUPPORTED, "pf_grid_attn_fwd: C=%d H=%d (built: C=128, H=4, d=32)", C,
-             H);
+  const bool fused = C == kC && H == kHeads;
+  PF_REQUIRE(fused || grid_gen_supported(C, H), PF_ERR_UNSUPPORTED,
+             "pf_grid_attn_fwd: C=%d H=%d (built: C=128 with 4 heads, or C a multiple of 32 with 1-16 heads of "
+             "dimension max(C/H, 16) <= 32)",
+             C, H);
   PF_REQUIRE(zdtype == PF_F32 || zdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_grid_attn_fwd: zdtype %d", zdtype);
   PF_REQUIRE(cdtype == PF_F32 || cdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_grid_attn_fwd: cdtype %d", cdtype);
   PF_REQUIRE(!(zdtype == PF_BF16 && cdtype == PF_F32), PF_ERR_UNSUPPORTED,
@@ -1686,9 +1827,20 @@ int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const 
   PF_REQUIRE(pf::aligned16(z) && pf::aligned16(out) && pf::aligned16(workspace) && pf::aligned16(w_qkvgb) &&
                  pf::aligned16(w_out),
              PF_ERR_ALIGNMENT, "pf_grid_attn_fwd: pointers must be 16-byte aligned");
-  PF_REQUIRE(workspace_bytes >= attn_ws_layout(B, N, cdtype).total, PF_ERR_WORKSPACE,
-             "pf_grid_attn_fwd: workspace %zu < %zu bytes", workspace_bytes, attn_ws_layout(B, N, cdtype).total);
+  PF_REQUIRE(workspace_bytes >= pf_grid_attn_workspace_bytes(B, N, C, H, cdtype), PF_ERR_WORKSPACE,
+             "pf_grid_attn_fwd: workspace %zu < %zu bytes", workspace_bytes,
+             pf_grid_attn_workspace_bytes(B, N, C, H, cdtype));
   hipStream_t s = pf::as_stream(stream);
+  if (!fused) {  // the generic path takes the per-line mask (key_mask is not used)
+    if (zdtype == PF_F32 && cdtype == PF_F32)
+      return grid_attn_generic_launch<float, float>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, C, H, transpose,
+                                                    out, accumulate, workspace, s);
+    if (zdtype == PF_F32)
+      return grid_attn_generic_launch<float, bf16>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, C, H, transpose,
+                                                   out, accumulate, workspace, s);
+    return grid_attn_generic_launch<bf16, bf16>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, C, H, transpose, out,
+                                                accumulate, workspace, s);
+  }
   if (zdtype == PF_F32 && cdtype == PF_F32)
     return grid_attn_launch<float, float>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, transpose, out, accumulate,
                                           key_mask, workspace, s);
@@ -1720,9 +1872,12 @@ static size_t redo_flag_count(int B, int L, int Np, int cdtype) {
 
 int pf_grid_attn_redo_flags(int B, int N, int C, int H, int cdtype, size_t* offset, size_t* count) {
   PF_REQUIRE(offset && count, PF_ERR_INVALID_ARG, "pf_grid_attn_redo_flags: null pointer");
-  PF_REQUIRE(B > 0 && N > 0 && C == kC && H == kHeads && (cdtype == PF_F32 || cdtype == PF_BF16),
+  const bool fused = C == kC && H == kHeads;
+  PF_REQUIRE(B > 0 && N > 0 && (fused || grid_gen_supported(C, H)) && (cdtype == PF_F32 || cdtype == PF_BF16),
              PF_ERR_UNSUPPORTED, "pf_grid_attn_redo_flags: B=%d N=%d C=%d H=%d cdtype=%d", B, N, C, H, cdtype);
-  *offset = attn_ws_layout(B, N, cdtype).redo;
+  // generic channels: the flags of the last group of four heads
+  *offset = fused ? attn_ws_layout(B, N, cdtype).redo
+                  : grid_gen_layout(B, N, C, H, cdtype).evo + evo_ws_layout(B, N, N, cdtype).redo;
   *count = redo_flag_count(B, N, pf::pad128(N), cdtype);
   return pf::ok();
 }

@@ -738,6 +738,53 @@ int s2p_launch(const void* z, const float* lnw, const float* lnb, float eps, con
   return pf::check_launch("single_to_pair");
 }
 
+// single_to_pair for other channel counts (a multiple of 64; the 256-channel trunk): one wave
+// per position, fp32 LayerNorm statistics, the normalised row rounded to the GEMM operand
+// dtype (the reference's LN output under autocast), 16 fp32 dot products reduced over the wave.
+template <class TZ, class TC>
+__global__ __launch_bounds__(256) void single_to_pair_generic_kernel(const TZ* __restrict__ z,
+                                                                     const float* __restrict__ lnw,
+                                                                     const float* __restrict__ lnb, float eps,
+                                                                     const TC* __restrict__ w, float* __restrict__ logits,
+                                                                     long M, long NN, int C) {
+  const long row = (long)blockIdx.x * 4 + wave_id();
+  if (row >= M) return;
+  const int l = lane_id();
+  const TZ* x = z + row * C;
+  float s = 0.f;
+  for (int c = l; c < C; c += 64) s += to_f32(x[c]);
+  const float mean = group_sum<64>(s) / C;
+  float q = 0.f;
+  for (int c = l; c < C; c += 64) {
+    const float d = to_f32(x[c]) - mean;
+    q += d * d;
+  }
+  const float rstd = rsqrtf(group_sum<64>(q) / C + eps);
+  float acc[kS2pHeads];
+#pragma unroll
+  for (int h = 0; h < kS2pHeads; ++h) acc[h] = 0.f;
+  for (int c = l; c < C; c += 64) {
+    const float xn = to_f32(from_f32<TC>((to_f32(x[c]) - mean) * rstd * lnw[c] + lnb[c]));
+#pragma unroll
+    for (int h = 0; h < kS2pHeads; ++h) acc[h] += xn * to_f32(w[(size_t)h * C + c]);
+  }
+  float mine = 0.f;
+#pragma unroll
+  for (int h = 0; h < kS2pHeads; ++h) {
+    const float t = group_sum<64>(acc[h]);
+    if (l == h) mine = t;
+  }
+  if (l < kS2pHeads) logits[((row / NN) * kS2pHeads + l) * NN + row % NN] = mine;
+}
+
+template <class TZ, class TC>
+int s2p_generic_launch(const void* z, const float* lnw, const float* lnb, float eps, const void* w, float* logits,
+                       long M, long NN, int C, hipStream_t s) {
+  single_to_pair_generic_kernel<TZ, TC><<<(unsigned)((M + 3) / 4), 256, 0, s>>>((const TZ*)z, lnw, lnb, eps,
+                                                                                 (const TC*)w, logits, M, NN, C);
+  return pf::check_launch("single_to_pair");
+}
+
 #define PF_DISPATCH_ZC(zd, cd, FN, ...)                                                        \
   ((zd) == PF_F32 && (cd) == PF_F32 ? FN<float, float>(__VA_ARGS__)                            \
    : (zd) == PF_F32                 ? FN<float, bf16>(__VA_ARGS__)                             \
@@ -791,14 +838,16 @@ int pf_pair_bias_fwd(const void* z, int zdtype, const float* ln_w, const float* 
 int pf_single_to_pair_fwd(const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_s2p, long M,
                           int C, int H, long NN, int zdtype, int cdtype, float* pair_logits, void* stream) {
   PF_REQUIRE(z && ln_w && ln_b && w_s2p && pair_logits, PF_ERR_INVALID_ARG, "pf_single_to_pair_fwd: null pointer");
-  PF_REQUIRE(C == kC && H == kS2pHeads, PF_ERR_UNSUPPORTED, "pf_single_to_pair_fwd: C=%d H=%d (built: 128, 16)", C,
-             H);
+  PF_REQUIRE(H == kS2pHeads && (C == kC || (C > 0 && C % 64 == 0)), PF_ERR_UNSUPPORTED,
+             "pf_single_to_pair_fwd: C=%d H=%d (built: H=16, C a multiple of 64)", C, H);
   PF_REQUIRE(NN > 0 && M >= 0 && M % NN == 0, PF_ERR_INVALID_ARG, "pf_single_to_pair_fwd: M=%ld NN=%ld", M, NN);
   PF_REQUIRE((zdtype == PF_F32 || zdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16) &&
                  !(zdtype == PF_BF16 && cdtype == PF_F32),
              PF_ERR_UNSUPPORTED, "pf_single_to_pair_fwd: dtype pair (%d, %d)", zdtype, cdtype);
   if (M == 0) return pf::ok();
   hipStream_t s = pf::as_stream(stream);
+  if (C != kC)
+    return PF_DISPATCH_ZC(zdtype, cdtype, s2p_generic_launch, z, ln_w, ln_b, eps, w_s2p, pair_logits, M, NN, C, s);
   return PF_DISPATCH_ZC(zdtype, cdtype, s2p_launch, z, ln_w, ln_b, eps, w_s2p, pair_logits, M, NN, s);
 }
 

@@ -1236,14 +1236,15 @@ __global__ __launch_bounds__(256) void trimul_output32_kernel(
 
 // ------------------------------------------------------------------ weight packing
 // w_proj, w_gate: [2C][C] in block order (rows 0..C-1 feed a, C..2C-1 feed b).
+// CB: channels per block of the packed order -- 32 for the persistent bf16 K1 (C = 128, its
+// 32x32 tiles), 16 for the generic K1 (every other dtype / channel count).
 template <class TS, class TD>
-__global__ void trimul_pack_kernel(const TS* __restrict__ wp, const TS* __restrict__ wg, TD* __restrict__ w4, int C) {
+__global__ void trimul_pack_kernel(const TS* __restrict__ wp, const TS* __restrict__ wg, TD* __restrict__ w4, int C,
+                                   int CB) {
   const int n = 4 * C * C;
   for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += gridDim.x * blockDim.x) {
     const int row = idx / C;
     const int k = idx % C;
-    // bf16 operands: 32-channel chunks (K1 on 32x32 tiles); fp32: 16-channel blocks
-    constexpr int CB = sizeof(TD) == 2 ? 32 : 16;
     const int j = row / (4 * CB);
     const int kind = (row % (4 * CB)) / CB;
     const int r = row % CB;
@@ -1254,12 +1255,14 @@ __global__ void trimul_pack_kernel(const TS* __restrict__ wp, const TS* __restri
   }
 }
 
-template <class TZ, class TC>
+// C = 128 in bf16 runs the persistent weight-stationary K1/K3; fp32 and the other channel
+// counts (the template stack's 64, the 256-channel trunk) run the generic tile kernels.
+template <class TZ, class TC, int C>
 int trimul_launch(const void* z, const float* mask, const float* lniw, const float* lnib, float eps_in,
                   const void* w4, const float* lnow, const float* lnob, float eps_out, const void* wo,
                   const void* wog, int B, int N, int outgoing, void* out, int accumulate, void* ws,
                   hipStream_t s) {
-  constexpr int C = 128;
+  constexpr bool kWs = sizeof(TC) == 2 && C == 128;
   const int Np = pf::pad128(N);
   const size_t pe = (size_t)Np * Np;
   TC* planes = reinterpret_cast<TC*>(ws);
@@ -1267,11 +1270,10 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
   TC* Q = planes + (size_t)B * C * pe;
   TC* X = planes + (size_t)2 * B * C * pe;
   {
-    constexpr bool k32 = sizeof(TC) == 2;
-    constexpr int BM = k32 ? 128 : trimul_bm<TC>();
+    constexpr int BM = kWs ? 128 : trimul_bm<TC>();
     dim3 grid(Np / BM, Np, B);
     pf::KernelTimer timer_trimul_project("trimul_project", s);
-    if constexpr (k32) {
+    if constexpr (kWs) {
       const long ntiles = (long)B * Np * (Np / ProjectWs::BP);
       PF_REQUIRE(ntiles < (1L << 31), PF_ERR_UNSUPPORTED, "trimul_project: B=%d N=%d (B Np Np/64 must stay below 2^31)",
                  B, N);
@@ -1304,11 +1306,10 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     if (e) return e;
   }
   {
-    constexpr bool k32 = sizeof(TC) == 2;
-    constexpr int BM = k32 ? 64 : trimul_bm<TC>();
+    constexpr int BM = kWs ? 64 : trimul_bm<TC>();
     dim3 grid((N + BM - 1) / BM, N, B);
     pf::KernelTimer timer_trimul_output("trimul_output", s);
-    if constexpr (k32) {
+    if constexpr (kWs) {
       const long ntiles = (long)B * N * ((N + OutputWs::BP - 1) / OutputWs::BP);
       PF_REQUIRE(ntiles < (1L << 31) && (long)Np * Np * OutputWs::C < (1L << 31), PF_ERR_UNSUPPORTED,
                  "trimul_output: N=%d B=%d (B N ceil(N/64) and 128 Np^2 must stay below 2^31)", N, B);
@@ -1341,20 +1342,22 @@ size_t pf_trimul_workspace_bytes(int B, int N, int C, int cdtype) {
 int pf_trimul_pack_weights(const void* w_proj, const void* w_gate, int wdtype, void* packed, int C, int cdtype,
                            void* stream) {
   PF_REQUIRE(w_proj && w_gate && packed, PF_ERR_INVALID_ARG, "pf_trimul_pack_weights: null pointer");
-  PF_REQUIRE(C == 128, PF_ERR_UNSUPPORTED, "pf_trimul_pack_weights: C=%d (only 128 is built)", C);
+  PF_REQUIRE(C == 64 || C == 128 || C == 256, PF_ERR_UNSUPPORTED, "pf_trimul_pack_weights: C=%d (built: 64, 128, 256)",
+             C);
+  const int cb = (cdtype == PF_BF16 && C == 128) ? 32 : 16;  // the K1 that will read them (trimul_launch)
   PF_REQUIRE((wdtype == PF_F32 || wdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16), PF_ERR_UNSUPPORTED,
              "pf_trimul_pack_weights: bad dtype");
   hipStream_t s = pf::as_stream(stream);
   const int n = 4 * C * C;
   dim3 grid((n + 255) / 256);
   if (wdtype == PF_F32 && cdtype == PF_F32)
-    trimul_pack_kernel<float, float><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (float*)packed, C);
+    trimul_pack_kernel<float, float><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (float*)packed, C, cb);
   else if (wdtype == PF_F32)
-    trimul_pack_kernel<float, bf16><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (bf16*)packed, C);
+    trimul_pack_kernel<float, bf16><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (bf16*)packed, C, cb);
   else if (cdtype == PF_F32)
-    trimul_pack_kernel<bf16, float><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (float*)packed, C);
+    trimul_pack_kernel<bf16, float><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (float*)packed, C, cb);
   else
-    trimul_pack_kernel<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (bf16*)packed, C);
+    trimul_pack_kernel<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (bf16*)packed, C, cb);
   return pf::check_launch("pf_trimul_pack_weights");
 }
 
@@ -1366,7 +1369,7 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
                  workspace,
              PF_ERR_INVALID_ARG, "pf_trimul_fwd: null pointer");
   PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_trimul_fwd: B=%d N=%d", B, N);
-  PF_REQUIRE(C == 128, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: C=%d (only 128 is built)", C);
+  PF_REQUIRE(C == 64 || C == 128 || C == 256, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: C=%d (built: 64, 128, 256)", C);
   PF_REQUIRE(zdtype == PF_F32 || zdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: zdtype %d", zdtype);
   PF_REQUIRE(cdtype == PF_F32 || cdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: cdtype %d", cdtype);
   PF_REQUIRE(!(zdtype == PF_BF16 && cdtype == PF_F32), PF_ERR_UNSUPPORTED,
@@ -1377,14 +1380,20 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
   PF_REQUIRE(workspace_bytes >= pf_trimul_workspace_bytes(B, N, C, cdtype), PF_ERR_WORKSPACE,
              "pf_trimul_fwd: workspace %zu < %zu bytes", workspace_bytes, pf_trimul_workspace_bytes(B, N, C, cdtype));
   hipStream_t s = pf::as_stream(stream);
-  if (zdtype == PF_F32 && cdtype == PF_F32)
-    return trimul_launch<float, float>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out, w_out,
-                                       w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
-  if (zdtype == PF_F32)
-    return trimul_launch<float, bf16>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out, w_out,
-                                      w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
-  return trimul_launch<bf16, bf16>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out, w_out,
-                                   w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+  auto run = [&](auto cc) {
+    constexpr int CC = decltype(cc)::value;
+    if (zdtype == PF_F32 && cdtype == PF_F32)
+      return trimul_launch<float, float, CC>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out,
+                                             w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+    if (zdtype == PF_F32)
+      return trimul_launch<float, bf16, CC>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out,
+                                            w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+    return trimul_launch<bf16, bf16, CC>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out,
+                                         w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+  };
+  if (C == 64) return run(std::integral_constant<int, 64>{});
+  if (C == 256) return run(std::integral_constant<int, 256>{});
+  return run(std::integral_constant<int, 128>{});
 }
 
 }  // extern "C"

@@ -129,9 +129,13 @@ class PairFormerBlock(nn.Module):
         self.tri_mul_in.forward_residual_(pair, pair_mask)
         self.pair_attn_row.forward_residual_(pair, pair_mask)
         self.pair_attn_col.forward_residual_(pair, pair_mask)
-        s2p = self._s2p_operands(gemm_dtype_for(pair))
-        _, pair_logits = self.pair_transition.forward_residual_(pair, s2p=s2p)
-        return pair_logits
+        if self.pair_transition.fused_pair:
+            s2p = self._s2p_operands(gemm_dtype_for(pair))
+            _, pair_logits = self.pair_transition.forward_residual_(pair, s2p=s2p)
+            return pair_logits
+        # other channel counts: the generic transition, then single_to_pair on its own
+        self.pair_transition.forward_residual_(pair)
+        return self.pair_logits(pair)
 
     def single_forward_(self, single: torch.Tensor, seq_mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
         """The single half of the block, in place (``evoformer.py:322-353``)."""
@@ -243,19 +247,22 @@ class TemplatePairFormerBlock(nn.Module):
     triangle multiplications, row and column attention, and a transition with a smaller
     intermediate factor; same submodule names and ``forward(pair, pair_mask)``.
 
-    Built for num_channels = 128 (every pair kernel here is); the reference's template
-    stack runs at 64 channels (``TemplatePairFormerConfig``, ``config.py:636-650``), which
-    refuses by name at construction."""
+    Built for num_channels in 64 (the reference's template stack, ``TemplatePairFormerConfig``,
+    ``config.py:636-650``: 4 heads of 16), 128 and 256; the triangle attention runs the
+    generic-channel path for anything but 128 channels in 4 heads."""
 
     def __init__(self, num_channels: int, num_heads: int = 4, num_intermediate_factor: int = 2,
                  pair_dropout: float = 0.25, optim: OptimConfig | None = None, residual_out_scale: float = 1.0):  # fmt: skip
         super().__init__()
         require_hip("TemplatePairFormerBlock", optim)
-        if num_channels != 128 or num_heads != 4:
+        from .kernels import TRIMUL_CHANNELS
+
+        head_dim = max(num_channels // num_heads, 16)
+        if num_channels not in TRIMUL_CHANNELS or num_channels % num_heads or head_dim > 32 or num_heads > 16:
             raise NotActive(
                 "TemplatePairFormerBlock",
-                f"num_channels={num_channels}, num_heads={num_heads}: the pair kernels are built for 128 channels "
-                "and 4 heads of 32",
+                f"num_channels={num_channels}, num_heads={num_heads}: built for {TRIMUL_CHANNELS} channels in at "
+                "most 16 heads of dimension max(C/H, 16) <= 32",
             )  # fmt: skip
         self.tri_mul_out = TriangleMulOutgoing(num_channels, optim=optim)
         self.tri_mul_in = TriangleMulIncoming(num_channels, optim=optim)

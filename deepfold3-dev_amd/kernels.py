@@ -121,6 +121,10 @@ def ln_transpose(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps:
 
 # ---------------------------------------------------------------- triangle multiplication
 
+# Channel counts of the triangle-multiplication kernels: 128 (trunk, confidence head; fused
+# persistent K1/K3 in bf16), 64 (template stack), 256 (the 256-channel trunk).
+TRIMUL_CHANNELS = (64, 128, 256)
+
 
 def pack_trimul_weights(w_proj: torch.Tensor, w_gate: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     """Pack block-ordered ``[2C, C]`` projection and gate weights into the ``[4C, C]`` K1 operand."""
@@ -158,8 +162,8 @@ def trimul_forward(
     if z.dim() != 4 or z.shape[1] != z.shape[2]:
         raise NotActive("fused_trimul", f"z must be [B, N, N, C], got {tuple(z.shape)}")
     B, N, _, C = z.shape
-    if C != 128:
-        raise NotActive("fused_trimul", f"C={C}: only C=128 is built")
+    if C not in TRIMUL_CHANNELS:
+        raise NotActive("fused_trimul", f"C={C}: built for C in {TRIMUL_CHANNELS}")
     cdt = w_packed.dtype
     if z.dtype == torch.bfloat16 and cdt == torch.float32:
         raise NotActive("fused_trimul", "bf16 activations need bf16 GEMM operands")
@@ -282,8 +286,13 @@ def grid_attention_forward(
     if z.dim() != 4 or z.shape[1] != z.shape[2]:
         raise NotActive("GridSelfAttention", f"z must be [B, N, N, C], got {tuple(z.shape)}")
     B, N, _, C = z.shape
-    if C != 128 or num_heads != 4:
-        raise NotActive("GridSelfAttention", f"C={C}, heads={num_heads}: only C=128 with 4 heads x 32 is built")
+    fused = C == 128 and num_heads == 4
+    code_c = _lib.dtype_code(w_packed.dtype)
+    if not fused and _lib.lib().pf_grid_attn_workspace_bytes(1, 1, C, num_heads, code_c) == 0:
+        raise NotActive(
+            "GridSelfAttention", f"C={C}, heads={num_heads}: built for C=128 with 4 heads, or C a multiple of 32 with "
+            "1-16 heads of dimension max(C/H, 16) <= 32",
+        )  # fmt: skip
     cdt = w_packed.dtype
     if z.dtype == torch.bfloat16 and cdt == torch.float32:
         raise NotActive("GridSelfAttention", "bf16 activations need bf16 GEMM operands")
@@ -297,10 +306,10 @@ def grid_attention_forward(
         out = torch.empty_like(zc)
     else:
         _lib.check_out("GridSelfAttention", out, zc)
-    km = outer_key_mask(m) if mask_outer is None or mask_outer else None
+    # the outer-product path belongs to the fused 128-channel kernels
+    km = outer_key_mask(m) if fused and (mask_outer is None or mask_outer) else None
     if mask_outer and km is None:
         raise NotActive("GridSelfAttention", "mask_outer=True needs a mask that is the outer product of its diagonal")
-    code_c = _lib.dtype_code(cdt)
     ws_bytes = _lib.lib().pf_grid_attn_workspace_bytes(B, N, C, num_heads, code_c)
     ws = _workspace(ws_bytes, z.device)
     _lib.call(

@@ -83,12 +83,14 @@ int pf_ln_transpose_fwd(const void* x, int dtype, const float* w, const float* b
  * pf_trimul_pack_weights: w_proj, w_gate are [2C, C] (wdtype) in the fused
  * kernel's *block order* (rows 0..C-1 feed a, C..2C-1 feed b; the module's
  * `_block_order`, ops.py:285-288: (even, odd) outgoing, (odd, even) incoming).
- * Writes the packed [4C, C] cdtype operand `packed` consumed by pf_trimul_fwd.
+ * Writes the packed [4C, C] cdtype operand `packed` consumed by pf_trimul_fwd with the
+ * same C and cdtype (the packed order follows the kernel that reads it).
  *
  * pf_trimul_fwd: z [B,N,N,C] (zdtype); mask [B,N,N] fp32; w_out, w_out_gate
  * [C,C] cdtype. Writes the update to `out` [B,N,N,C] (zdtype), or adds it into
  * `out` when accumulate != 0 (out == z gives the fused residual z += update).
- * workspace >= pf_trimul_workspace_bytes(B, N, C, cdtype). Only C = 128. */
+ * workspace >= pf_trimul_workspace_bytes(B, N, C, cdtype). C = 64, 128 or 256 (128 in
+ * bf16 runs the persistent kernels, the rest the generic tile kernels). */
 size_t pf_trimul_workspace_bytes(int B, int N, int C, int cdtype);
 int pf_trimul_pack_weights(const void* w_proj, const void* w_gate, int wdtype, void* packed, int C, int cdtype,
                            void* stream);

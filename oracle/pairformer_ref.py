@@ -129,7 +129,7 @@ def grid_attention(
     mask: torch.Tensor,
     p: dict[str, torch.Tensor],
     transpose: bool,
-    num_heads: int = 4,
+    num_heads: int | None = None,
     row_chunk: int = 0,
     lines: torch.Tensor | None = None,
 ) -> torch.Tensor:
@@ -141,9 +141,10 @@ def grid_attention(
     so it is exact) to bound the fp32 logits. ``lines`` (indices into the
     attended axis: rows of z, or columns when ``transpose``) evaluates only
     those lines and returns ``[B, len(lines), N, C]`` in the attention frame.
+    The head count defaults to the rows of the pair-bias weight (one per head).
     """
     B, N, _, C = z.shape
-    H = num_heads
+    H = num_heads if num_heads is not None else p["pair_bias.weight"].shape[0]  # one bias row per head
     D = max(C // H, 16)
     zn = layer_norm(z, p["norm.weight"], p["norm.bias"])
     pb = F.linear(zn, p["pair_bias.weight"]).permute(0, 3, 1, 2)  # [B, H, N, N]

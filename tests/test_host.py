@@ -135,14 +135,20 @@ def test_transition_block_out_gain_is_row_orthogonal():
     assert torch.allclose(w @ w.T, gain**2 * torch.eye(384, dtype=torch.float64), atol=1e-9)
 
 
-def test_template_block_refuses_unbuilt_widths():
+def test_template_block_widths():
+    """Built at the reference's template width (64 channels in 4 heads of 16,
+    config.py:636-650), at 128 and 256; other widths and heads wider than 32 refuse by name."""
     evoformer = mod("evoformer")
-    assert sorted({k.split(".")[0] for k in evoformer.TemplatePairFormerBlock(128).state_dict()}) == [
-        "pair_attn_col", "pair_attn_row", "pair_transition", "tri_mul_in", "tri_mul_out",
-    ]  # fmt: skip
-    with pytest.raises(guard.NotActive) as ei:
-        evoformer.TemplatePairFormerBlock(64)  # the reference's template width (config.py:636-650)
-    assert ei.value.lever == "TemplatePairFormerBlock"
+    for c in (64, 128):
+        assert sorted({k.split(".")[0] for k in evoformer.TemplatePairFormerBlock(c).state_dict()}) == [
+            "pair_attn_col", "pair_attn_row", "pair_transition", "tri_mul_in", "tri_mul_out",
+        ]  # fmt: skip
+    blk = evoformer.TemplatePairFormerBlock(64)
+    assert blk.pair_attn_row.head_dim == 16 and blk.pair_transition.linear1.weight.shape == (256, 64)
+    for c, h in ((96, 4), (128, 2)):
+        with pytest.raises(guard.NotActive) as ei:
+            evoformer.TemplatePairFormerBlock(c, num_heads=h)
+        assert ei.value.lever == "TemplatePairFormerBlock"
 
 
 def test_confidence_layers_keys():

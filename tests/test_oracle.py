@@ -131,17 +131,19 @@ def _tiny_attn_params(c=8, H=2, seed=1):
     }, H, D  # fmt: skip
 
 
+@pytest.mark.parametrize("c,heads", [(8, 2), (64, 4)])  # head dim 16: floored (8 / 2), exact (64 / 4)
 @pytest.mark.parametrize("transpose", [False, True])
-def test_grid_attention_against_loops(transpose):
-    N, c = 5, 8
-    p, H, D = _tiny_attn_params(c)
+def test_grid_attention_against_loops(transpose, c, heads):
+    N = 5
+    p, H, D = _tiny_attn_params(c, H=heads)
     p = {k: v.double() for k, v in p.items()}
     gen = torch.Generator().manual_seed(4)
     z = torch.randn(1, N, N, c, generator=gen, dtype=torch.float64)
     mask = torch.ones(1, N, N, dtype=torch.float64)
     mask[0, 1, 3] = 0
     mask[0, 2, :] = 0  # one fully masked row (and column entries)
-    out = R.grid_attention(z, mask, p, transpose=transpose, num_heads=H)
+    # the head count is given, or (64 channels) taken from the pair-bias rows
+    out = R.grid_attention(z, mask, p, transpose=transpose, num_heads=H if c == 8 else None)
     zn = F.layer_norm(z[0], (c,), p["norm.weight"], p["norm.bias"])
     pb = torch.einsum("ijc,hc->hij", zn, p["pair_bias.weight"])  # bias from un-transposed LN(z)
     ref = torch.zeros(N, N, c, dtype=torch.float64)
@@ -166,7 +168,8 @@ def test_grid_attention_against_loops(transpose):
                 o[sl] = w @ vs
             g = torch.sigmoid(zn[qpos] @ p["to_g.weight"].T)
             ref[qpos] = (o * g) @ p["out_proj.weight"].T
-    assert torch.allclose(out[0], ref, rtol=1e-5, atol=1e-6)  # LN runs in fp32 by design
+    # LN runs in fp32 by design (primitives.py:90-115): fp32 rounding relative to the output scale
+    assert (out[0] - ref).abs().max() <= 1e-6 * ref.abs().max()
 
 
 def test_fully_masked_row_is_mean_of_v():
