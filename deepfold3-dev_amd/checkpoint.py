@@ -14,9 +14,9 @@ the weights by state-dict key. This module does the same for the parts built her
 
 Tensors are read one key at a time through safetensors' ``safe_open`` (nothing in the file
 is executed, and only the keys under the requested prefix are read). A configuration this
-build cannot serve (another channel count, MHR trimul, the pair-bias gate, an RMSNorm
-branch scaler, a stack without triangle attention or the single track) refuses by name
-when the stack is constructed. Loading is strict within the prefix: a missing or unexpected
+build cannot serve (pair channels other than 64, 128 or 256, pair heads wider than 32, MHR
+trimul, the pair-bias gate, an RMSNorm branch scaler, a stack without triangle attention or
+the single track) refuses by name when the stack is constructed or first run. Loading is strict within the prefix: a missing or unexpected
 key raises.
 """
 
