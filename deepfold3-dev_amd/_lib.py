@@ -59,6 +59,17 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "pf_recycle_embed_workspace_bytes": (_sz, [_l, _i, _i]),
     "pf_recycle_embed_fwd": (_i, [_vp, _vp, _vp, _f, _vp, _l, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "pf_outer_product_mean_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
+    "pf_outer_product_mean_fwd": (
+        _i,
+        [_vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],
+    ),
+    "pf_msa_pair_avg_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
+    "pf_msa_pair_avg_fwd": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz,
+         _vp],
+    ),  # fmt: skip
     "pf_evo_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "pf_evo_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "pf_pair_mask_outer": (_i, [_vp, _i, _i, _vp, _vp, _vp]),

@@ -92,6 +92,76 @@ class GridSelfAttention(nn.Module):
         return self._run(z, mask, z, True)
 
 
+class MSAAttention(nn.Module):
+    """MSA row update of the Evoformer block, AF3's pair-weighted averaging
+    (``attention.py:272-341``): weights ``softmax_k(LN(pair) W_h + 1e9 (colmask_k - 1))``
+    shared by every MSA row (colmask: any sequence holds residue k), values ``to_v(LN(msa))``,
+    gate ``sigmoid(to_g(LN(msa)))``, then ``out_proj``. Same parameter names as the reference."""
+
+    def __init__(self, c_msa: int, c_pair: int, num_heads: int = 8, optim: OptimConfig | None = None):
+        super().__init__()
+        require_hip("MSAAttention", optim)
+        assert c_msa % num_heads == 0
+        if num_heads > 16:
+            raise NotActive("MSAAttention", f"num_heads={num_heads}: at most 16 heads are built")
+        self.num_heads = num_heads
+        self.head_dim = c_msa // num_heads
+        self.norm = LayerNorm(c_msa)
+        self.pair_norm = LayerNorm(c_pair)
+        self.pair_logits = LinearNoBias(c_pair, num_heads)
+        self.to_v = LinearNoBias(c_msa, num_heads * self.head_dim)
+        self.to_g = LinearNoBias(c_msa, num_heads * self.head_dim, initializer="zeros")
+        self.out_proj = LinearNoBias(num_heads * self.head_dim, c_msa, initializer="zeros")
+        self._cache = WeightCache()
+        # Residual scale of this branch (the block's s_ros), folded into out_proj.
+        self.branch_scale = 1.0
+
+    def _operands(self, cdt: torch.dtype) -> dict:
+        params = [
+            self.norm.weight, self.norm.bias, self.pair_norm.weight, self.pair_norm.bias, self.pair_logits.weight,
+            self.to_v.weight, self.to_g.weight, self.out_proj.weight,
+        ]  # fmt: skip
+
+        def build():
+            w_lg = self.pair_logits.weight.detach()
+            pad = torch.zeros(16 - w_lg.shape[0], w_lg.shape[1], dtype=w_lg.dtype, device=w_lg.device)
+            return dict(
+                w_lg=cast_weight(torch.cat([w_lg, pad]), cdt),
+                w_vg=cast_weight(torch.cat([self.to_v.weight, self.to_g.weight]).detach(), cdt),
+                w_out=scaled_weight(self.out_proj.weight, self.branch_scale, cdt),
+                lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
+                plnw=f32(self.pair_norm.weight), plnb=f32(self.pair_norm.bias),
+            )  # fmt: skip
+
+        return self._cache.get(params, cdt, build, tag=self.branch_scale)
+
+    def _run(self, msa, mask, pair, out, accumulate):
+        from .kernels import msa_pair_avg_forward
+
+        kernel_census.record("MSAAttention", "hip_msa_pair_avg")
+        op = self._operands(gemm_dtype_for(msa))
+        return msa_pair_avg_forward(
+            msa, mask, pair, op["lnw"], op["lnb"], self.norm.eps, op["plnw"], op["plnb"], self.pair_norm.eps,
+            op["w_lg"], op["w_vg"], op["w_out"], self.num_heads, out=out, accumulate=accumulate,
+        )  # fmt: skip
+
+    @inference_only("MSAAttention")
+    def forward(self, msa: torch.Tensor, mask: torch.Tensor, pair: torch.Tensor) -> torch.Tensor:
+        """msa [B?, S, N, c_msa], mask [B?, S, N], pair [B?, N, N, c_pair] -> the msa update."""
+        has_batch = msa.dim() == 4
+        if not has_batch:
+            msa, mask, pair = msa.unsqueeze(0), mask.unsqueeze(0), pair.unsqueeze(0)
+        out = self._run(msa, mask, pair, None, False)
+        return out if has_batch else out.squeeze(0)
+
+    @inference_only("MSAAttention")
+    def forward_residual_(self, msa: torch.Tensor, mask: torch.Tensor, pair: torch.Tensor) -> torch.Tensor:
+        """``msa += update`` in place; msa contiguous [B, S, N, c_msa]."""
+        if not msa.is_contiguous():
+            raise NotActive("MSAAttention", "in-place residual needs a contiguous msa")
+        return self._run(msa, mask, pair, msa, True)
+
+
 class SingleAttention(nn.Module):
     """Self-attention on the single track with pair-logit bias (``attention.py:344-452``)."""
 

@@ -1,0 +1,139 @@
+// Batched NT GEMM on MFMA tiles (see gemm.h): 128 x 128 output tile per 256-thread block,
+// four waves in a 2 x 2 grid of 64 x 64, k-tiles double-buffered through LDS. Rows past M or
+// N load the last valid row (their results are not stored), so any M, N work; K is a
+// multiple of the k-tile. Serves the generic paths (outer product mean, MSA pair-weighted
+// averaging), where M, N and K follow the sequence and residue counts.
+#include <algorithm>
+
+#include "capi.h"
+#include "common.h"
+#include "gemm.h"
+
+namespace {
+
+template <class TC>
+struct BgemmCfg {
+  static constexpr int BMN = 128;
+  static constexpr int KT = sizeof(TC) == 2 ? 64 : 32;
+  static constexpr int LDK = KT + lds_pad<TC>();
+  static constexpr int TILE_ELEMS = BMN * LDK;
+  static constexpr int SMEM = 2 * 2 * TILE_ELEMS * (int)sizeof(TC);
+};
+
+template <class TC, class TO>
+__global__ __launch_bounds__(256) void bgemm_nt_kernel(const TC* __restrict__ A, const TC* __restrict__ Bm,
+                                                       TO* __restrict__ Cm, int M, int N, int K, long lda, long ldb,
+                                                       long ldc, long sA, long sB, long sC) {
+  using Cfg = BgemmCfg<TC>;
+  using MF = Mfma<TC>;
+  constexpr int BMN = Cfg::BMN, KT = Cfg::KT, LDK = Cfg::LDK;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  TC* lds = reinterpret_cast<TC*>(smem);
+
+  const int tn = (N + BMN - 1) / BMN;
+  const int i0 = (blockIdx.x / tn) * BMN;
+  const int j0 = (blockIdx.x % tn) * BMN;
+  const TC* Ab = A + (size_t)blockIdx.y * sA;
+  const TC* Bb = Bm + (size_t)blockIdx.y * sB;
+  TO* Cb = Cm + (size_t)blockIdx.y * sC;
+
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const int wr = (w >> 1) * 64;
+  const int wc = (w & 1) * 64;
+
+  constexpr int VEC = 16 / sizeof(TC);
+  constexpr int CPR = KT / VEC;
+  constexpr int LOADS = 2 * BMN * CPR / 256;
+  static_assert((2 * BMN * CPR) % 256 == 0, "stage must split evenly");
+  u32x4 reg[LOADS];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < LOADS; ++q) {
+      const int idx = tid + q * 256;
+      const int row = idx / CPR;
+      const int chunk = idx % CPR;
+      const TC* src = row < BMN ? Ab + (size_t)min(i0 + row, M - 1) * lda
+                                : Bb + (size_t)min(j0 + row - BMN, N - 1) * ldb;
+      reg[q] = *reinterpret_cast<const u32x4*>(src + k0 + chunk * VEC);
+    }
+  };
+  auto lstore = [&](int buf) {
+    TC* base = lds + buf * 2 * Cfg::TILE_ELEMS;
+#pragma unroll
+    for (int q = 0; q < LOADS; ++q) {
+      const int idx = tid + q * 256;
+      const int row = idx / CPR;
+      const int chunk = idx % CPR;
+      *reinterpret_cast<u32x4*>(base + row * LDK + chunk * VEC) = reg[q];
+    }
+  };
+
+  f32x4 acc[4][4];
+  zero_acc(acc);
+  const int nk = K / KT;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int r = l & 15;
+  const int kq = (l >> 4) * MF::KPL;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * KT);
+    const TC* As = lds + buf * 2 * Cfg::TILE_ELEMS;
+    const TC* Bs = As + Cfg::TILE_ELEMS;
+#pragma unroll
+    for (int kk = 0; kk < KT; kk += MF::K16) {
+      typename MF::Frag af[4], bfr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = MF::load(As + (wr + i * 16 + r) * LDK + kk + kq);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfr[j] = MF::load(Bs + (wc + j * 16 + r) * LDK + kk + kq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) MF::mma16(acc[i][j], af[i], bfr[j]);
+    }
+    if (kt + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+  // acc[i][j][e]: row wr + 16 i + 4 (l >> 4) + e, column wc + 16 j + (l & 15)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = j0 + wc + j * 16 + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = i0 + wr + i * 16 + 4 * (l >> 4) + e;
+        if (m < M && n < N) Cb[(size_t)m * ldc + n] = from_f32<TO>(acc[i][j][e]);
+      }
+    }
+}
+
+template <class TC, class TO>
+int bgemm_launch(const void* A, const void* B, void* C, int M, int N, int K, long lda, long ldb, long ldc, long sA,
+                 long sB, long sC, int batch, hipStream_t s) {
+  using Cfg = BgemmCfg<TC>;
+  const hipError_t e = hipFuncSetAttribute((const void*)bgemm_nt_kernel<TC, TO>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::SMEM);
+  PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "bgemm: cannot reserve %d bytes of LDS: %s", Cfg::SMEM,
+             hipGetErrorString(e));
+  const long tiles = (long)((M + Cfg::BMN - 1) / Cfg::BMN) * ((N + Cfg::BMN - 1) / Cfg::BMN);
+  PF_REQUIRE(tiles < (1L << 31) && batch < 65536, PF_ERR_UNSUPPORTED, "bgemm: M=%d N=%d batch=%d", M, N, batch);
+  bgemm_nt_kernel<TC, TO><<<dim3((unsigned)tiles, (unsigned)batch), 256, Cfg::SMEM, s>>>(
+      (const TC*)A, (const TC*)B, (TO*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
+  return pf::check_launch("bgemm");
+}
+
+}  // namespace
+
+int bgemm_nt(const void* A, const void* B, void* C, int M, int N, int K, long lda, long ldb, long ldc, long sA,
+             long sB, long sC, int batch, int tc_dtype, int out_dtype, hipStream_t s) {
+  PF_REQUIRE(M > 0 && N > 0 && K > 0 && K % kBgemmK == 0 && batch > 0, PF_ERR_INVALID_ARG,
+             "bgemm: M=%d N=%d K=%d (a multiple of %d) batch=%d", M, N, K, kBgemmK, batch);
+  if (tc_dtype == PF_F32) return bgemm_launch<float, float>(A, B, C, M, N, K, lda, ldb, ldc, sA, sB, sC, batch, s);
+  if (out_dtype == PF_F32) return bgemm_launch<bf16, float>(A, B, C, M, N, K, lda, ldb, ldc, sA, sB, sC, batch, s);
+  return bgemm_launch<bf16, bf16>(A, B, C, M, N, K, lda, ldb, ldc, sA, sB, sC, batch, s);
+}

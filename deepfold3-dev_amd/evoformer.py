@@ -388,3 +388,109 @@ def run_recycles(
         pair, single = trunk(pair, single, pair_mask, seq_mask)
         prev_pair, prev_single = pair, single
     return pair, single
+
+
+class EvoformerBlock(nn.Module):
+    """One block of the Evoformer MSA stack (``evoformer.py:100-175``): ``pair +=
+    OuterProductMean(msa)``, ``msa += MSAAttention(msa, pair)`` (pair-weighted averaging),
+    ``msa += msa_transition(msa)``, then the pair half of the PairFormer block (triangle
+    multiplications, row and column attention, pair transition). Every branch is
+    output-scaled by ``residual_out_scale`` (folded into its output projection). Same
+    constructor arguments, submodule names and ``forward(msa, pair, msa_mask, pair_mask)``."""
+
+    def __init__(
+        self,
+        c_msa: int,
+        c_pair: int,
+        num_msa_heads: int = 8,
+        num_pair_heads: int = 4,
+        outer_product_hidden: int = 32,
+        msa_dropout: float = 0.15,
+        pair_dropout: float = 0.25,
+        optim: OptimConfig | None = None,
+        residual_out_scale: float = 1.0,
+        use_triangle_attention: bool = True,
+        trimul_kwargs: dict | None = None,
+    ):
+        super().__init__()
+        from .attention import MSAAttention
+        from .ops import OuterProductMean
+
+        require_hip("EvoformerBlock", optim)
+        if not use_triangle_attention:
+            raise NotActive("EvoformerBlock", "the triangle-attention branches are always built")
+        tk = trimul_kwargs or {}
+        self.row_attn = MSAAttention(c_msa, c_pair, num_heads=num_msa_heads, optim=optim)
+        self.outer_product = OuterProductMean(c_msa, c_pair, c_hidden=outer_product_hidden, optim=optim)
+        self.tri_mul_out = TriangleMulOutgoing(c_pair, optim=optim, **tk)
+        self.tri_mul_in = TriangleMulIncoming(c_pair, optim=optim, **tk)
+        self.use_triangle_attention = True
+        self.pair_attn_row = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=False, optim=optim)
+        self.pair_attn_col = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=True, optim=optim)
+        self.pair_transition = make_transition_block(c_pair, config=optim)
+        self.msa_transition = make_transition_block(c_msa, config=optim)
+        self.msa_dropout = msa_dropout
+        self.pair_dropout = pair_dropout
+        self.residual_out_scale = float(residual_out_scale)
+        for m in (self.row_attn, self.outer_product, self.tri_mul_out, self.tri_mul_in, self.pair_attn_row,
+                  self.pair_attn_col, self.pair_transition, self.msa_transition):  # fmt: skip
+            m.branch_scale = self.residual_out_scale
+
+    @inference_only("EvoformerBlock")
+    def forward_(
+        self, msa: torch.Tensor, pair: torch.Tensor, msa_mask: torch.Tensor, pair_mask: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """In place on contiguous ``msa`` [B, S, N, c_msa] and ``pair`` [B, N, N, c_pair]."""
+        if self.training:
+            raise NotActive("EvoformerBlock", "training-mode dropout is not built (eval only)")
+        kernel_census.record("EvoformerBlock", "hip_block")
+        self.outer_product.forward_residual_(pair, msa, msa_mask)
+        self.row_attn.forward_residual_(msa, msa_mask, pair)
+        self.msa_transition.forward_residual_(msa)
+        self.tri_mul_out.forward_residual_(pair, pair_mask)
+        self.tri_mul_in.forward_residual_(pair, pair_mask)
+        self.pair_attn_row.forward_residual_(pair, pair_mask)
+        self.pair_attn_col.forward_residual_(pair, pair_mask)
+        self.pair_transition.forward_residual_(pair)
+        return msa, pair
+
+    @inference_only("EvoformerBlock")
+    def forward(
+        self, msa: torch.Tensor, pair: torch.Tensor, msa_mask: torch.Tensor, pair_mask: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Reference signature: msa [B?, S, N, c_msa], pair [B?, N, N, c_pair] -> new (msa, pair)."""
+        has_batch = msa.dim() == 4
+        if not has_batch:
+            msa, pair = msa.unsqueeze(0), pair.unsqueeze(0)
+            msa_mask, pair_mask = msa_mask.unsqueeze(0), pair_mask.unsqueeze(0)
+        m, p = self.forward_(msa.contiguous().clone(), pair.contiguous().clone(), msa_mask, pair_mask)
+        return (m, p) if has_batch else (m.squeeze(0), p.squeeze(0))
+
+
+class EvoformerStack(nn.Module):
+    """The MSA stack (``evoformer.py:433-455``, run at ``:575-580``): ``num_layer``
+    EvoformerBlocks under the reference's ``msa_stack.{i}`` keys; ``layer_kwargs(i)`` gives
+    per-layer constructor arguments (residual scales)."""
+
+    def __init__(self, num_layer: int, c_msa: int = 64, c_pair: int = 128, optim: OptimConfig | None = None,
+                 layer_kwargs=None, **block_kwargs):  # fmt: skip
+        super().__init__()
+
+        def block(i: int) -> EvoformerBlock:
+            kw = dict(block_kwargs)
+            if layer_kwargs is not None:
+                kw.update(layer_kwargs(i))
+            return EvoformerBlock(c_msa, c_pair, optim=optim, **kw)
+
+        self.msa_stack = nn.ModuleList([block(i) for i in range(num_layer)])
+
+    @inference_only("EvoformerStack")
+    def forward(
+        self, msa: torch.Tensor, pair: torch.Tensor, msa_mask: torch.Tensor, pair_mask: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """msa [B, S, N, c_msa], pair [B, N, N, c_pair] -> new (msa, pair) after every block."""
+        msa, pair = msa.contiguous().clone(), pair.contiguous().clone()
+        pair_mask = pair_mask.to(torch.float32).contiguous()
+        for blk in self.msa_stack:
+            blk.forward_(msa, pair, msa_mask, pair_mask)
+        return msa, pair

@@ -440,6 +440,99 @@ def recycle_embed_(
     return out
 
 
+# ---------------------------------------------------------------- MSA stack
+
+
+def outer_product_mean_forward(
+    msa: torch.Tensor,
+    mask: torch.Tensor,
+    ln_w: torch.Tensor,
+    ln_b: torch.Tensor,
+    eps: float,
+    w_ab: torch.Tensor,
+    w_out: torch.Tensor,
+    b_out: torch.Tensor,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """OuterProductMean on prepared operands (``ops.py:683-785``): msa [B, S, N, Cm], mask
+    [B, S, N]; returns (or adds into ``out``) the [B, N, N, Cz] update."""
+    _lib.require_device("OuterProductMean", msa, mask)
+    if msa.dim() != 4:
+        raise NotActive("OuterProductMean", f"msa must be [B, S, N, C], got {tuple(msa.shape)}")
+    B, S, N, Cm = msa.shape
+    CH = w_ab.shape[0] // 2
+    Cz = w_out.shape[0]
+    mc = msa.contiguous()
+    m = mask.to(torch.float32).contiguous()
+    if m.shape != (B, S, N):
+        raise NotActive("OuterProductMean", f"mask must be [B, S, N], got {tuple(mask.shape)}")
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs an explicit out tensor")
+        out = torch.empty((B, N, N, Cz), dtype=msa.dtype, device=msa.device)
+    else:
+        _lib.check_out("OuterProductMean", out, mc, shape=(B, N, N, Cz))
+    code_c = _lib.dtype_code(w_ab.dtype)
+    ws_bytes = _lib.lib().pf_outer_product_mean_workspace_bytes(B, S, N, Cm, CH, Cz, code_c)
+    ws = _workspace(ws_bytes, msa.device)
+    _lib.call(
+        "pf_outer_product_mean_fwd", mc.data_ptr(), m.data_ptr(), _f32(ln_w).data_ptr(), _f32(ln_b).data_ptr(),
+        float(eps), w_ab.data_ptr(), w_out.data_ptr(), _f32(b_out).data_ptr(), B, S, N, Cm, CH, Cz,
+        _lib.dtype_code(msa.dtype), _lib.dtype_code(out.dtype), code_c, out.data_ptr(), int(accumulate),
+        ws.data_ptr(), ws_bytes, _lib.stream_of(mc),
+    )  # fmt: skip
+    return out
+
+
+def msa_pair_avg_forward(
+    msa: torch.Tensor,
+    mask: torch.Tensor,
+    pair: torch.Tensor,
+    ln_w: torch.Tensor,
+    ln_b: torch.Tensor,
+    eps: float,
+    pair_ln_w: torch.Tensor,
+    pair_ln_b: torch.Tensor,
+    pair_eps: float,
+    w_logits16: torch.Tensor,
+    w_vg: torch.Tensor,
+    w_out: torch.Tensor,
+    num_heads: int,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """MSAAttention (pair-weighted averaging, ``attention.py:272-341``) on prepared operands:
+    msa [B, S, N, Cm], mask [B, S, N], pair [B, N, N, Cz] (msa's dtype); returns (or adds into
+    ``out``) the [B, S, N, Cm] update."""
+    _lib.require_device("MSAAttention", msa, mask, pair)
+    if msa.dim() != 4 or pair.dim() != 4:
+        raise NotActive("MSAAttention", f"msa [B, S, N, C] and pair [B, N, N, C] expected, got {tuple(msa.shape)}")
+    B, S, N, Cm = msa.shape
+    Cz = pair.shape[-1]
+    if pair.shape[:3] != (B, N, N) or pair.dtype != msa.dtype:
+        raise NotActive("MSAAttention", f"pair {tuple(pair.shape)} {pair.dtype} does not match msa {tuple(msa.shape)}")
+    mc, pc = msa.contiguous(), pair.contiguous()
+    m = mask.to(torch.float32).contiguous()
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs an explicit out tensor")
+        out = torch.empty_like(mc)
+    else:
+        _lib.check_out("MSAAttention", out, mc)
+    code_c = _lib.dtype_code(w_vg.dtype)
+    ws_bytes = _lib.lib().pf_msa_pair_avg_workspace_bytes(B, S, N, Cm, Cz, num_heads, code_c)
+    ws = _workspace(ws_bytes, msa.device)
+    _lib.call(
+        "pf_msa_pair_avg_fwd", mc.data_ptr(), m.data_ptr(), pc.data_ptr(), _f32(ln_w).data_ptr(),
+        _f32(ln_b).data_ptr(), float(eps), _f32(pair_ln_w).data_ptr(), _f32(pair_ln_b).data_ptr(), float(pair_eps),
+        w_logits16.data_ptr(), w_vg.data_ptr(), w_out.data_ptr(), B, S, N, Cm, Cz, num_heads,
+        _lib.dtype_code(msa.dtype), code_c, out.data_ptr(), int(accumulate), ws.data_ptr(), ws_bytes,
+        _lib.stream_of(mc),
+    )  # fmt: skip
+    return out
+
+
 # ---------------------------------------------------------------- single attention
 
 

@@ -105,3 +105,67 @@ class TriangleMulIncoming(_TriangleMulBase):
     """Triangle multiplication, incoming: ``X_ij = sum_k a_kj b_ki`` (``ops.py:674-680``)."""
 
     _outgoing = False
+
+
+class OuterProductMean(nn.Module):
+    """MSA -> pair update of the Evoformer block (``ops.py:683-785``): ``a, b`` = two
+    projections of LN(msa) times the mask, the outer product ``a[s,i] (x) b[s,j]`` summed over
+    the sequences, contracted with ``out_w`` [CH, CH, c_z] plus ``out_b``, divided by
+    ``1e-3 +`` the number of sequences holding both residues. Same parameter names as the
+    reference (``norm``, ``proj_a``, ``proj_b``, ``out_w``, ``out_b``)."""
+
+    def __init__(self, c_msa: int, c_z: int, c_hidden: int = 32, optim: OptimConfig | None = None):
+        super().__init__()
+        require_hip("OuterProductMean", optim)
+        self.norm = LayerNorm(c_msa)
+        self.proj_a = LinearNoBias(c_msa, c_hidden)
+        self.proj_b = LinearNoBias(c_msa, c_hidden)
+        self.out_w = nn.Parameter(torch.zeros(c_hidden, c_hidden, c_z))  # AF3 final init (zeros)
+        self.out_b = nn.Parameter(torch.zeros(c_z))
+        self._cache = WeightCache()
+        # Residual scale of this branch (the block's s_ros), folded into out_w and out_b.
+        self.branch_scale = 1.0
+
+    def _operands(self, cdt: torch.dtype) -> dict:
+        from .kernels import cast_weight
+
+        params = [self.norm.weight, self.norm.bias, self.proj_a.weight, self.proj_b.weight, self.out_w, self.out_b]
+
+        def build():
+            ch, _, cz = self.out_w.shape
+            w_out = self.out_w.detach().to(torch.float32).permute(2, 0, 1).reshape(cz, ch * ch) * self.branch_scale
+            return dict(
+                w_ab=cast_weight(torch.cat([self.proj_a.weight, self.proj_b.weight]).detach(), cdt),
+                w_out=cast_weight(w_out.contiguous(), cdt),
+                b_out=(self.out_b.detach().to(torch.float32) * self.branch_scale).contiguous(),
+                lnw=self.norm.weight.detach().to(torch.float32).contiguous(),
+                lnb=self.norm.bias.detach().to(torch.float32).contiguous(),
+            )
+
+        return self._cache.get(params, cdt, build, tag=self.branch_scale)
+
+    def _run(self, msa, mask, out, accumulate):
+        from .kernels import outer_product_mean_forward
+
+        kernel_census.record("OuterProductMean", "hip_outer_product_mean")
+        op = self._operands(gemm_dtype_for(msa))
+        return outer_product_mean_forward(
+            msa, mask, op["lnw"], op["lnb"], self.norm.eps, op["w_ab"], op["w_out"], op["b_out"], out=out,
+            accumulate=accumulate,
+        )  # fmt: skip
+
+    @inference_only("OuterProductMean")
+    def forward(self, msa: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """msa [B?, S, N, c_msa], mask [B?, S, N] -> [B?, N, N, c_z] (not added to the pair)."""
+        has_batch = msa.dim() == 4
+        if not has_batch:
+            msa, mask = msa.unsqueeze(0), mask.unsqueeze(0)
+        out = self._run(msa, mask, None, False)
+        return out if has_batch else out.squeeze(0)
+
+    @inference_only("OuterProductMean")
+    def forward_residual_(self, pair: torch.Tensor, msa: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """``pair += update`` in place; pair contiguous [B, N, N, c_z] in msa's dtype."""
+        if not pair.is_contiguous():
+            raise NotActive("OuterProductMean", "in-place residual needs a contiguous pair")
+        return self._run(msa, mask, pair, True)

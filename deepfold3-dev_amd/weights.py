@@ -126,6 +126,65 @@ def make_trunk_weights(seed: int, num_blocks: int, perturb_affine: bool = False)
     return [make_block_weights(seed * 1000 + b, perturb_affine) for b in range(num_blocks)]
 
 
+def evoformer_block_param_spec(
+    c_msa: int = 64, c_pair: int = C_PAIR, num_msa_heads: int = 8, num_pair_heads: int = NUM_PAIR_HEADS,
+    outer_product_hidden: int = 32,
+) -> list[tuple[str, tuple[int, ...], str]]:
+    """Ordered ``(key, shape, kind)`` for one EvoformerBlock (``evoformer.py:100-146``):
+    the MSA parts, then the pair half of the PairFormer block (same keys)."""
+    cm, cz, ch = c_msa, c_pair, outer_product_hidden
+    spec: list[tuple[str, tuple[int, ...], str]] = [
+        ("row_attn.norm.weight", (cm,), "ln_w"),
+        ("row_attn.norm.bias", (cm,), "ln_b"),
+        ("row_attn.pair_norm.weight", (cz,), "ln_w"),
+        ("row_attn.pair_norm.bias", (cz,), "ln_b"),
+        ("row_attn.pair_logits.weight", (num_msa_heads, cz), "linear"),
+        ("row_attn.to_v.weight", (cm, cm), "linear"),
+        ("row_attn.to_g.weight", (cm, cm), "linear"),
+        ("row_attn.out_proj.weight", (cm, cm), "linear"),
+        ("outer_product.norm.weight", (cm,), "ln_w"),
+        ("outer_product.norm.bias", (cm,), "ln_b"),
+        ("outer_product.proj_a.weight", (ch, cm), "linear"),
+        ("outer_product.proj_b.weight", (ch, cm), "linear"),
+        ("outer_product.out_w", (ch, ch, cz), "linear3"),
+        ("outer_product.out_b", (cz,), "bias"),
+    ]
+    pair_keys = ("tri_mul_out.", "tri_mul_in.", "pair_attn_row.", "pair_attn_col.", "pair_transition.")
+    spec += [e for e in block_param_spec(c_pair=cz, num_pair_heads=num_pair_heads) if e[0].startswith(pair_keys)]
+    spec += [
+        ("msa_transition.norm.weight", (cm,), "ln_w"),
+        ("msa_transition.norm.bias", (cm,), "ln_b"),
+        ("msa_transition.linear1.weight", (2 * TRANSITION_FACTOR * cm, cm), "linear"),
+        ("msa_transition.linear2.weight", (cm, TRANSITION_FACTOR * cm), "linear"),
+    ]
+    return spec
+
+
+def make_evoformer_block_weights(seed: int, perturb_affine: bool = False, **spec_kwargs) -> dict[str, torch.Tensor]:
+    """fp32 CPU state dict for one EvoformerBlock from ``seed``: LeCun truncated normal on every
+    weight (``out_w`` [CH, CH, c_z] with fan-in CH^2), LayerNorm 1 / 0 and ``out_b`` 0 unless
+    ``perturb_affine``."""
+    gen = torch.Generator().manual_seed(int(seed))
+    out: dict[str, torch.Tensor] = {}
+    for key, shape, kind in evoformer_block_param_spec(**spec_kwargs):
+        t = torch.empty(shape, dtype=torch.float32)
+        if kind == "linear":
+            lecun_trunc_normal_(t, gen)
+        elif kind == "linear3":
+            std = 1.0 / math.sqrt(shape[0] * shape[1])
+            torch.nn.init.trunc_normal_(t, 0.0, std, -2.0 * std, 2.0 * std, generator=gen)
+        elif kind == "ln_w":
+            t.fill_(1.0)
+            if perturb_affine:
+                t.add_(0.1 * torch.randn(shape, generator=gen))
+        else:
+            t.zero_()
+            if perturb_affine:
+                t.add_(0.1 * torch.randn(shape, generator=gen))
+        out[key] = t
+    return out
+
+
 def state_dict_sha256(sd: dict[str, torch.Tensor]) -> str:
     """sha256 over keys (sorted) and the little-endian fp32 bytes of each tensor."""
     h = hashlib.sha256()

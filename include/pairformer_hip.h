@@ -164,6 +164,28 @@ int pf_recycle_embed_fwd(const void* prev, const float* ln_w, const float* ln_b,
                          int C, int zdtype, int cdtype, void* out, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* ---- MSA stack (Evoformer block) ----------------------------------------- */
+/* OuterProductMean.forward (ops.py:683-785): msa [B,S,N,Cm] (mdtype), msa_mask [B,S,N] fp32;
+ * LN params fp32; w_ab [2 CH, Cm] cdtype (proj_a rows, then proj_b rows); w_out [Cz, CH*CH]
+ * cdtype (out_w[e][f][c] at row c, column e CH + f); b_out [Cz] fp32. The [B,N,N,Cz] result
+ * is written to `out` (zdtype == mdtype) or added into it (accumulate != 0). Cm a multiple
+ * of 32, CH of 8, Cz of 16. */
+size_t pf_outer_product_mean_workspace_bytes(int B, int S, int N, int Cm, int CH, int Cz, int cdtype);
+int pf_outer_product_mean_fwd(const void* msa, const float* msa_mask, const float* ln_w, const float* ln_b, float eps,
+                              const void* w_ab, const void* w_out, const float* b_out, int B, int S, int N, int Cm,
+                              int CH, int Cz, int mdtype, int zdtype, int cdtype, void* out, int accumulate,
+                              void* workspace, size_t workspace_bytes, void* stream);
+/* MSAAttention.forward (attention.py:272-341), AF3's pair-weighted averaging: msa [B,S,N,Cm]
+ * and pair [B,N,N,Cz] (both mdtype), msa_mask [B,S,N] fp32; LN params fp32 (norm, pair_norm);
+ * w_logits [16, Cz] cdtype (pair_logits rows, zero-padded to 16); w_vg [2 Cm, Cm] cdtype
+ * (to_v rows, then to_g rows); w_out [Cm, Cm]. H heads of Cm/H. The [B,S,N,Cm] update is
+ * written to `out` (mdtype) or added into it. Cm and Cz multiples of 32, 1 <= H <= 16. */
+size_t pf_msa_pair_avg_workspace_bytes(int B, int S, int N, int Cm, int Cz, int H, int cdtype);
+int pf_msa_pair_avg_fwd(const void* msa, const float* msa_mask, const void* pair, const float* ln_w, const float* ln_b,
+                        float eps, const float* pair_ln_w, const float* pair_ln_b, float pair_eps, const void* w_logits,
+                        const void* w_vg, const void* w_out, int B, int S, int N, int Cm, int Cz, int H, int mdtype,
+                        int cdtype, void* out, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- single attention with pair bias ----------------------------------- */
 /* SingleAttention.forward (attention.py:344-452), pair_bias_gate off: s [B,N,C] zdtype;
  * seq_mask [B,N] fp32; pair_logits [B,H,N,N] fp32; w_qkvg [4C, C] cdtype rows

@@ -27,6 +27,8 @@ Pinning (what checks this restatement, beyond retyping it):
     it); a zero transition gain equals a zeroed ``linear2``; s = 0 returns the inputs.
   * recycling embedding: zero previous outputs give ``init + b W^T`` (LN of a zero row
     is its bias b); LayerNorm's invariance to per-row shifts; linearity in W.
+  * outer product mean and MSA pair-weighted averaging: explicit loops at tiny sizes; the
+    Evoformer block: its pair half equals the template block's on the OPM-updated pair.
 """
 
 from __future__ import annotations
@@ -46,6 +48,9 @@ __all__ = [
     "pairformer_trunk",
     "recycle_embed",
     "recycled_trunk",
+    "outer_product_mean",
+    "msa_attention",
+    "evoformer_block",
 ]
 
 
@@ -347,3 +352,70 @@ def recycled_trunk(
         pair, single = pairformer_trunk(pair, single, pair_mask, seq_mask, blocks, row_chunk=row_chunk, scales=scales)
         prev_pair, prev_single = pair, single
     return pair, single
+
+
+def outer_product_mean(msa: torch.Tensor, mask: torch.Tensor, p: dict[str, torch.Tensor]) -> torch.Tensor:
+    """``OuterProductMean.forward`` (``ops.py:683-785``): a, b = proj(LN(msa)) * mask,
+    ``ab[i,j,e,f] = sum_s a[s,i,e] b[s,j,f]``, ``act = ab . out_w + out_b``, divided by
+    ``1e-3 + sum_s m[s,i] m[s,j]``. msa [B, S, N, c_msa], mask [B, S, N] -> [B, N, N, c_z]."""
+    m = mask.unsqueeze(-1)
+    x = layer_norm(msa, p["norm.weight"], p["norm.bias"])
+    a = F.linear(x, p["proj_a.weight"]) * m
+    b = F.linear(x, p["proj_b.weight"]) * m
+    ab = torch.einsum("bsie,bsjf->bijef", a, b)
+    act = torch.einsum("bijef,efc->bijc", ab, p["out_w"]) + p["out_b"]
+    mf = mask.float()
+    norm = torch.einsum("bsi,bsj->bij", mf, mf)
+    return act / (1e-3 + norm.unsqueeze(-1))
+
+
+def msa_attention(
+    msa: torch.Tensor, mask: torch.Tensor, pair: torch.Tensor, p: dict[str, torch.Tensor], num_heads: int = 8
+) -> torch.Tensor:
+    """``MSAAttention`` (``attention.py:272-341``): pair-weighted averaging. The weights
+    ``softmax_k(LN(pair) W_h + 1e9 (colmask_k - 1))`` (colmask = max over sequences of the
+    mask, softmax in fp32, cast to msa's dtype) are shared by every MSA row; each row averages
+    its values ``to_v(LN(msa))`` with them, gated by ``sigmoid(to_g(LN(msa)))``, then out_proj.
+    msa [B, S, N, c_msa], mask [B, S, N], pair [B, N, N, c_pair] -> [B, S, N, c_msa]."""
+    B, S, N, C = msa.shape
+    H = num_heads
+    D = C // H
+    logits = F.linear(layer_norm(pair, p["pair_norm.weight"], p["pair_norm.bias"]), p["pair_logits.weight"])
+    logits = logits.permute(0, 3, 1, 2)  # [B, H, q, k]
+    col_mask, _ = mask.max(dim=-2)
+    logits = logits + 1e9 * (col_mask.float() - 1.0).view(B, 1, 1, N)
+    w = F.softmax(logits.float(), dim=-1)
+    x = layer_norm(msa, p["norm.weight"], p["norm.bias"])
+    w = w.to(x.dtype)
+    v = F.linear(x, p["to_v.weight"]).view(B, S, N, H, D)
+    v_avg = torch.einsum("bhqk,bskhc->bsqhc", w, v).reshape(B, S, N, H * D)
+    g = torch.sigmoid(F.linear(x, p["to_g.weight"]))
+    return F.linear(v_avg * g, p["out_proj.weight"])
+
+
+def evoformer_block(
+    msa: torch.Tensor,
+    pair: torch.Tensor,
+    msa_mask: torch.Tensor,
+    pair_mask: torch.Tensor,
+    p: dict[str, torch.Tensor],
+    num_msa_heads: int = 8,
+    residual_out_scale: float = 1.0,
+    row_chunk: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``EvoformerBlock.forward`` in eval mode (``evoformer.py:148-175``): pair += OPM(msa),
+    msa += MSAAttention(msa, pair), msa += msa_transition(msa), then the pair half of the
+    PairFormer block (trimul out, in, attention rows, columns, pair transition); every
+    branch output-scaled by ``residual_out_scale``."""
+    s = float(residual_out_scale)
+    pair = pair + _scaled(outer_product_mean(msa, msa_mask, _sub(p, "outer_product.")), s)
+    msa = msa + _scaled(msa_attention(msa, msa_mask, pair, _sub(p, "row_attn."), num_msa_heads), s)
+    msa = msa + _scaled(transition(msa, _sub(p, "msa_transition.")), s)
+    pair = pair + _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True), s)
+    pair = pair + _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False), s)
+    row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
+    pair = pair + _scaled(row, s)
+    col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
+    pair = pair + _scaled(col, s)
+    pair = pair + _scaled(transition(pair, _sub(p, "pair_transition.")), s)
+    return msa, pair

@@ -416,3 +416,110 @@ def test_recycled_trunk_is_recycle_then_trunk():
         p, s = R.pairformer_trunk(*R.recycle_embed(x["pair"], x["single"], zp, zs, rp), *args, blocks)
         p, s = R.pairformer_trunk(*R.recycle_embed(x["pair"], x["single"], p, s, rp), *args, blocks)
     assert torch.equal(got[0], p) and torch.equal(got[1], s)
+
+
+def _tiny_evo_params(cm=8, cz=6, ch=3, H=2, seed=5):
+    gen = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=gen, dtype=torch.float64) * 0.4  # noqa: E731
+    return {
+        "outer_product.norm.weight": 1 + 0.1 * r(cm), "outer_product.norm.bias": 0.1 * r(cm),
+        "outer_product.proj_a.weight": r(ch, cm), "outer_product.proj_b.weight": r(ch, cm),
+        "outer_product.out_w": r(ch, ch, cz), "outer_product.out_b": r(cz),
+        "row_attn.norm.weight": 1 + 0.1 * r(cm), "row_attn.norm.bias": 0.1 * r(cm),
+        "row_attn.pair_norm.weight": 1 + 0.1 * r(cz), "row_attn.pair_norm.bias": 0.1 * r(cz),
+        "row_attn.pair_logits.weight": r(H, cz), "row_attn.to_v.weight": r(cm, cm),
+        "row_attn.to_g.weight": r(cm, cm), "row_attn.out_proj.weight": r(cm, cm),
+    }  # fmt: skip
+
+
+def test_outer_product_mean_against_loops():
+    """ops.py:683-785: mean over the sequences that have both residues, of the outer product
+    of the two projections, through out_w, plus out_b."""
+    S, N, cm, cz, ch = 4, 5, 8, 6, 3
+    p = _sub_keys(_tiny_evo_params(cm, cz, ch), "outer_product.")
+    gen = torch.Generator().manual_seed(6)
+    msa = torch.randn(1, S, N, cm, generator=gen, dtype=torch.float64)
+    mask = (torch.rand(1, S, N, generator=gen) > 0.3).double()
+    got = R.outer_product_mean(msa, mask, p)
+    x = F.layer_norm(msa[0], (cm,), p["norm.weight"], p["norm.bias"])
+    ref = torch.zeros(N, N, cz, dtype=torch.float64)
+    for i in range(N):
+        for j in range(N):
+            acc = torch.zeros(ch, ch, dtype=torch.float64)
+            cnt = 0.0
+            for s in range(S):
+                a = (x[s, i] @ p["proj_a.weight"].T) * mask[0, s, i]
+                b = (x[s, j] @ p["proj_b.weight"].T) * mask[0, s, j]
+                acc += torch.outer(a, b)
+                cnt += float(mask[0, s, i] * mask[0, s, j])
+            for c in range(cz):
+                ref[i, j, c] = ((acc * p["out_w"][:, :, c]).sum() + p["out_b"][c]) / (1e-3 + cnt)
+    assert (got[0] - ref).abs().max() <= 1e-6 * ref.abs().max()
+
+
+def _sub_keys(p, prefix):
+    return {k[len(prefix) :]: v for k, v in p.items() if k.startswith(prefix)}
+
+
+def test_msa_attention_against_loops():
+    """attention.py:272-341: every MSA row averages its values with the same pair-derived
+    weights (softmax over keys of LN(pair) W_h, keys masked when no sequence has them)."""
+    S, N, cm, cz, H = 3, 5, 8, 6, 2
+    D = cm // H
+    p = _sub_keys(_tiny_evo_params(cm, cz, 3, H), "row_attn.")
+    gen = torch.Generator().manual_seed(7)
+    msa = torch.randn(1, S, N, cm, generator=gen, dtype=torch.float64)
+    pair = torch.randn(1, N, N, cz, generator=gen, dtype=torch.float64)
+    mask = torch.ones(1, S, N, dtype=torch.float64)
+    mask[0, :, 2] = 0  # key 2 absent from every sequence: masked
+    mask[0, 1, 4] = 0  # key 4 present in some: kept
+    got = R.msa_attention(msa, mask, pair, p, H)
+    xp = F.layer_norm(pair[0], (cz,), p["pair_norm.weight"], p["pair_norm.bias"])
+    xm = F.layer_norm(msa[0], (cm,), p["norm.weight"], p["norm.bias"])
+    ref = torch.zeros(S, N, cm, dtype=torch.float64)
+    for s in range(S):
+        for q in range(N):
+            o = torch.zeros(cm, dtype=torch.float64)
+            for h in range(H):
+                lg = torch.stack([xp[q, k] @ p["pair_logits.weight"][h] + (0.0 if k != 2 else -1e9) for k in range(N)])
+                w = torch.softmax(lg.float(), 0).double()
+                sl = slice(h * D, (h + 1) * D)
+                o[sl] = sum(w[k] * (xm[s, k] @ p["to_v.weight"][sl].T) for k in range(N))
+            g = torch.sigmoid(xm[s, q] @ p["to_g.weight"].T)
+            ref[s, q] = (o * g) @ p["out_proj.weight"].T
+    assert (got[0] - ref).abs().max() <= 1e-6 * ref.abs().max()
+
+
+def test_evoformer_block_composition():
+    """evoformer.py:148-175: the pair output is the template block's pair half (factor-4
+    transition) applied to pair + OPM(msa); the MSA output is msa + attention(msa, that pair)
+    + transition of the sum; a residual scale s scales every branch."""
+    sd = W.make_block_weights(51, perturb_affine=True)
+    pair_keys = ("tri_mul_out.", "tri_mul_in.", "pair_attn_row.", "pair_attn_col.", "pair_transition.")
+    p = {k: v for k, v in sd.items() if k.startswith(pair_keys)}
+    gen = torch.Generator().manual_seed(8)
+    cm = 64
+    r = lambda *s: torch.randn(*s, generator=gen) * 0.1  # noqa: E731
+    p.update({
+        "outer_product.norm.weight": 1 + r(cm), "outer_product.norm.bias": r(cm),
+        "outer_product.proj_a.weight": r(32, cm), "outer_product.proj_b.weight": r(32, cm),
+        "outer_product.out_w": r(32, 32, 128), "outer_product.out_b": r(128),
+        "row_attn.norm.weight": 1 + r(cm), "row_attn.norm.bias": r(cm),
+        "row_attn.pair_norm.weight": 1 + r(128), "row_attn.pair_norm.bias": r(128),
+        "row_attn.pair_logits.weight": r(8, 128), "row_attn.to_v.weight": r(cm, cm),
+        "row_attn.to_g.weight": r(cm, cm), "row_attn.out_proj.weight": r(cm, cm),
+        "msa_transition.norm.weight": 1 + r(cm), "msa_transition.norm.bias": r(cm),
+        "msa_transition.linear1.weight": r(8 * cm, cm), "msa_transition.linear2.weight": r(cm, 4 * cm),
+    })  # fmt: skip
+    x = W.make_inputs(7, seed=9, pad_last=1)
+    msa = torch.randn(1, 3, 7, cm, generator=gen)
+    mmask = (torch.rand(1, 3, 7, generator=gen) > 0.2).float()
+    with torch.no_grad():
+        m1, z1 = R.evoformer_block(msa, x["pair"], mmask, x["pair_mask"], p)
+        z0 = x["pair"] + R.outer_product_mean(msa, mmask, _sub_keys(p, "outer_product."))
+        zw = R.template_pairformer_block(z0, x["pair_mask"], {k: v for k, v in p.items() if k.startswith(pair_keys)})
+        ma = msa + R.msa_attention(msa, mmask, z0, _sub_keys(p, "row_attn."))
+        mw = ma + R.transition(ma, _sub_keys(p, "msa_transition."))
+        m2, z2 = R.evoformer_block(msa, x["pair"], mmask, x["pair_mask"], p, residual_out_scale=0.0)
+    assert torch.equal(z1, zw) and torch.equal(m1, mw)
+    assert torch.equal(z2, x["pair"]) and torch.equal(m2, msa)
