@@ -10,7 +10,9 @@ the weights by state-dict key. This module does the same for the parts built her
   per-layer residual scales included);
 - its recycling embeddings, ``evoformer.prev_*`` (``evoformer.py:400-412``);
 - the confidence head's PairFormer layers, ``confidence_head.layers.{i}.*``, constructed
-  from ``ConfidenceConfig`` (``confidence.py:88-117``).
+  from ``ConfidenceConfig`` (``confidence.py:88-117``);
+- the MSA stack, ``evoformer.msa_stack.{i}.*``, constructed from ``EvoformerConfig``
+  (``evoformer.py:433-455``).
 
 Tensors are read one key at a time through safetensors' ``safe_open`` (nothing in the file
 is executed, and only the keys under the requested prefix are read). A configuration this
@@ -29,12 +31,13 @@ import os
 import torch
 
 from .config import OptimConfig
-from .evoformer import ConfidencePairFormer, PairFormerStack, TrunkRecycler
+from .evoformer import ConfidencePairFormer, EvoformerStack, PairFormerStack, TrunkRecycler
 
 MODEL_CFG_KEY = "model_cfg_json"  # config.py:1898
 TRUNK_PREFIX = "evoformer.trunk_pairformer."
 RECYCLE_PREFIX = "evoformer."
 CONFIDENCE_PREFIX = "confidence_head.layers."
+MSA_STACK_PREFIX = "evoformer."
 
 # PairFormerConfig defaults (config.py:122-269), the fields that shape a block.
 PAIRFORMER_DEFAULTS: dict = {
@@ -81,6 +84,26 @@ CONFIDENCE_DEFAULTS: dict = {
     "pair_transition_residual_gain": None,
     "pair_transition_residual_per_layer_extra": False,
     "branch_scaler": "identity",
+}
+
+
+# EvoformerConfig defaults (config.py:71-121), the fields that shape an MSA-stack block.
+EVOFORMER_DEFAULTS: dict = {
+    "num_layer": 4,
+    "msa_channel": 64,
+    "pair_channel": 128,
+    "msa_attention": {"num_head": 8},
+    "outer_product_num_channel": 32,
+    "pair_attention": {"num_head": 4},
+    "msa_dropout": 0.15,
+    "pair_dropout": 0.25,
+    "residual_output_scaling": False,
+    "uniform_residual_scale": False,
+    "use_triangle_attention": True,
+    "trimul_num_heads": 0,
+    "trimul_head_norm": "channel",
+    "trimul_router": False,
+    "trimul_router_kind": "softmax",
 }
 
 
@@ -161,6 +184,30 @@ def confidence_config(model_cfg: dict | None) -> dict:
     return _section(model_cfg, "confidence", CONFIDENCE_DEFAULTS)
 
 
+def evoformer_config(model_cfg: dict | None) -> dict:
+    """The MSA stack's ``EvoformerConfig`` fields."""
+    return _section(model_cfg, "evoformer", EVOFORMER_DEFAULTS)
+
+
+def msa_block_kwargs(ec: dict, layer_idx: int) -> dict:
+    """``EvoformerBlock`` arguments of MSA-stack layer ``layer_idx`` (``evoformer.py:433-455``)."""
+    return dict(
+        num_msa_heads=ec["msa_attention"]["num_head"],
+        num_pair_heads=ec["pair_attention"]["num_head"],
+        outer_product_hidden=ec["outer_product_num_channel"],
+        msa_dropout=ec["msa_dropout"],
+        pair_dropout=ec["pair_dropout"],
+        residual_out_scale=block_residual_scale(
+            layer_idx, ec["num_layer"], ec["residual_output_scaling"], ec["uniform_residual_scale"]
+        ),
+        use_triangle_attention=ec["use_triangle_attention"],
+        trimul_kwargs=dict(
+            num_heads=ec["trimul_num_heads"], head_norm=ec["trimul_head_norm"], router=ec["trimul_router"],
+            router_kind=ec["trimul_router_kind"],
+        ),  # fmt: skip
+    )
+
+
 def trunk_block_kwargs(pf: dict, layer_idx: int) -> dict:
     """``PairFormerBlock`` arguments of trunk layer ``layer_idx`` (``evoformer.py:459-489``)."""
     kw = dict(
@@ -220,6 +267,14 @@ def build_confidence_pairformer(model_cfg: dict | None, optim: OptimConfig | Non
         cc["num_layer"], cc["pair_channel"], cc["seq_channel"], num_pair_heads=cc["pair_attention_num_head"],
         num_single_heads=cc["single_attention_num_head"], optim=optim,
         layer_kwargs=lambda i: confidence_block_kwargs(cc, i),
+    )  # fmt: skip
+
+
+def build_msa_stack(model_cfg: dict | None, optim: OptimConfig | None = None) -> EvoformerStack:
+    ec = evoformer_config(model_cfg)
+    return EvoformerStack(
+        ec["num_layer"], ec["msa_channel"], ec["pair_channel"], optim=optim,
+        layer_kwargs=lambda i: msa_block_kwargs(ec, i),
     )  # fmt: skip
 
 
@@ -285,4 +340,14 @@ def load_confidence_pairformer(
     cfg = read_model_cfg(path)
     stack = build_confidence_pairformer(cfg, optim)
     load_prefixed(stack.layers, path, CONFIDENCE_PREFIX)
+    return _finish(stack, device, dtype)
+
+
+def load_msa_stack(
+    path: str | os.PathLike, device=None, dtype: torch.dtype | None = None, optim: OptimConfig | None = None
+) -> EvoformerStack:
+    """The MSA stack (``evoformer.msa_stack.*``) of a reference checkpoint."""
+    cfg = read_model_cfg(path)
+    stack = build_msa_stack(cfg, optim)
+    load_prefixed(stack, path, MSA_STACK_PREFIX, scope="msa_stack.")
     return _finish(stack, device, dtype)

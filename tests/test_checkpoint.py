@@ -37,8 +37,10 @@ def _recycle(seed: int) -> dict:
     }
 
 
-def write_checkpoint(path, model_cfg: dict | None, trunk_layers: int = 2, conf_layers: int = 2, seed: int = 40):
-    """A reference-layout checkpoint; returns the tensors written, by key."""
+def write_checkpoint(path, model_cfg: dict | None, trunk_layers: int = 2, conf_layers: int = 2, seed: int = 40,
+                     msa_layers: int = 0):  # fmt: skip
+    """A reference-layout checkpoint; returns the tensors written, by key. With ``msa_layers``
+    0 the MSA stack is a stray key the other loaders must leave alone."""
     from safetensors.torch import save_file
 
     sd = {}
@@ -49,7 +51,12 @@ def write_checkpoint(path, model_cfg: dict | None, trunk_layers: int = 2, conf_l
         sd.update({f"confidence_head.layers.{i}.{k}": v for k, v in blk.items()})
     # parts outside the hot path, which the loaders must leave alone
     sd["evoformer.position_activations.weight"] = torch.randn(128, 139)
-    sd["evoformer.msa_stack.0.msa_transition.linear1.weight"] = torch.randn(512, 64)
+    if msa_layers:
+        for i in range(msa_layers):
+            blk = W.make_evoformer_block_weights(seed + 3 + i, perturb_affine=True)
+            sd.update({f"evoformer.msa_stack.{i}.{k}": v for k, v in blk.items()})
+    else:
+        sd["evoformer.msa_stack.0.msa_transition.linear1.weight"] = torch.randn(512, 64)
     sd["confidence_head.pae_logits.weight"] = torch.randn(64, 128)
     sd["diffusion.conditioning.weight"] = torch.randn(8, 8)
     sd = {k: v.contiguous() for k, v in sd.items()}
@@ -69,7 +76,7 @@ CFG = {
         "a_field_from_a_later_revision": "ignored",
     },
     "confidence": {"num_layer": 2, "uniform_residual_scale": True},
-    "evoformer": {"num_layer": 4},
+    "evoformer": {"num_layer": 2, "residual_output_scaling": True, "msa_attention": {"num_head": 8}},
     "optim": {"use_fused_triangle_mul": True},
 }
 
@@ -176,3 +183,36 @@ def test_unbuilt_architectures_refuse_by_name(field, value, needle):
     cfg = {"pairformer": {"num_layer": 1, field: value}}
     with pytest.raises(guard.NotActive, match=needle):
         ck.build_trunk(cfg)
+
+
+def test_msa_block_kwargs_per_layer():
+    ec = ck.evoformer_config(CFG)
+    assert ec["num_layer"] == 2 and ec["msa_channel"] == 64 and ec["outer_product_num_channel"] == 32
+    for i in range(2):
+        kw = ck.msa_block_kwargs(ec, i)
+        assert kw["residual_out_scale"] == pytest.approx(1 / math.sqrt(i + 1))
+        assert kw["num_msa_heads"] == 8 and kw["num_pair_heads"] == 4 and kw["outer_product_hidden"] == 32
+    assert ck.evoformer_config(None)["num_layer"] == 4
+    assert ck.msa_block_kwargs(ck.evoformer_config(None), 3)["residual_out_scale"] == 1.0
+
+
+def test_load_msa_stack(tmp_path):
+    path = tmp_path / "m.safetensors"
+    sd = write_checkpoint(path, CFG, msa_layers=2)
+    stack = ck.load_msa_stack(path)
+    assert len(stack.msa_stack) == 2
+    for i, blk in enumerate(stack.msa_stack):
+        s = 1 / math.sqrt(i + 1)
+        assert blk.row_attn.branch_scale == pytest.approx(s)
+        assert blk.outer_product.branch_scale == pytest.approx(s)
+        assert blk.msa_transition.branch_scale == pytest.approx(s)
+        assert blk.tri_mul_out.branch_scale == pytest.approx(s)
+        for k, v in blk.state_dict().items():
+            assert torch.equal(v, sd[f"evoformer.msa_stack.{i}.{k}"]), (i, k)
+    # the trunk and the recycler load beside it
+    ck.load_trunk(path)
+    ck.load_recycler(path)
+    stray = tmp_path / "stray.safetensors"
+    write_checkpoint(stray, CFG)  # one stray MSA-stack key only
+    with pytest.raises(KeyError, match="msa_stack"):
+        ck.load_msa_stack(stray)

@@ -9,6 +9,8 @@ recycle loop, against the oracle.
   around the trunk (``model.py:385-470``, stages between the embedding and the trunk left
   out on both sides).
 - The template block with a residual scale (``template_embedding.py:220-240``).
+- The MSA stack with per-layer residual output scaling (``evoformer.py:433-455``), against the
+  oracle's Evoformer blocks in order.
 
 fp32 at relL2 <= 1e-5 and max-abs <= 1e-5 max|ref|; bf16 by the reference's rule
 relL2(HIP - fp32) <= 2 relL2(eager bf16 - fp32) (tests/triton/test_fused_trimul.py:66-83).
@@ -159,3 +161,27 @@ def test_template_block_residual_scale_fp32(dev):
         got = m(x["pair"].to(dev), x["pair_mask"].to(dev))
         ref = R.template_pairformer_block(x["pair"], x["pair_mask"], p, residual_out_scale=0.5)
     assert_fp32_close(got.cpu(), ref, what="template block s=0.5")
+
+
+def test_checkpoint_msa_stack_fp32(dev, tmp_path):
+    path = tmp_path / "m.safetensors"
+    sd = write_checkpoint(path, CFG, seed=90, msa_layers=2)
+    stack = ck.load_msa_stack(path, device=dev)
+    ec = ck.evoformer_config(CFG)
+    g = torch.Generator().manual_seed(16)
+    S, N = 9, 27
+    msa = torch.randn(1, S, N, 64, generator=g)
+    pair = torch.randn(1, N, N, 128, generator=g)
+    mask = (torch.rand(1, S, N, generator=g) > 0.15).float()
+    mask[:, :, N - 2 :] = 0.0
+    seq = (mask.max(dim=1).values > 0).float()
+    pm = seq[:, :, None] * seq[:, None, :]
+    print(f"[checkpoint MSA stack fp32] S={S} N={N}", flush=True)
+    with torch.no_grad():
+        m, p = stack(msa.to(dev), pair.to(dev), mask.to(dev), pm.to(dev))
+        rm, rp = msa, pair
+        for i in range(2):
+            s = ck.msa_block_kwargs(ec, i)["residual_out_scale"]
+            rm, rp = R.evoformer_block(rm, rp, mask, pm, sub(sd, f"evoformer.msa_stack.{i}."), residual_out_scale=s)
+    assert_fp32_close(m.cpu(), rm, what="checkpoint MSA stack msa")
+    assert_fp32_close(p.cpu(), rp, what="checkpoint MSA stack pair")
