@@ -11,8 +11,9 @@ reference, so call sites written against its Triton layer run unchanged:
 - ``FusedTransitionBlock`` (``fused_transition.py:34-83``)
 - ``dropout_add_rowwise`` / ``dropout_add_columnwise`` (``dropout_add.py:221-265``)
 
-All are forward-only (inference): under grad they raise ``InferenceOnlyKernelError``;
-anything the kernels cannot serve raises ``NotActive``. There is no PyTorch fallback.
+``_EvoformerAttention`` is differentiable (the HIP backward); the others are forward-only
+(inference) and raise ``InferenceOnlyKernelError`` under grad. Anything the kernels cannot
+serve raises ``NotActive``. There is no PyTorch fallback.
 """
 
 from __future__ import annotations
@@ -42,6 +43,74 @@ def _ws(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
+def _evo_fwd(Q, K, V, rm, pb, zero_rows: bool) -> torch.Tensor:
+    """Forward in the kernel layout: Q, K, V ``[B,S,H,N,D]`` contiguous, rm ``[B,S,N]`` and
+    pb ``[B,H,N,N]`` fp32. The flash kernel runs four heads per line; other head counts are
+    zero-padded to a multiple of four and regrouped as extra batch items."""
+    B, S, H, N, D = Q.shape
+    code = _lib.dtype_code(Q.dtype)
+    G = -(-H // 4)
+    if H != 4:
+        pad = 4 * G - H
+        if pad:
+            Q, K, V = (torch.cat([t, t.new_zeros(B, S, pad, N, D)], 2) for t in (Q, K, V))
+            pb = torch.cat([pb, pb.new_zeros(B, pad, N, N)], 1)
+        # (with B = 1 the reshape can return a strided view: the kernel needs dense operands)
+        Q, K, V = (t.view(B, S, G, 4, N, D).transpose(1, 2).reshape(B * G, S, 4, N, D).contiguous() for t in (Q, K, V))
+        rm = rm.repeat_interleave(G, dim=0)
+        pb = pb.reshape(B * G, 4, N, N)
+    Bk = Q.shape[0]
+    ws_bytes = _lib.lib().pf_evo_attn_workspace_bytes(Bk, S, 4, N, D, code)
+    if ws_bytes == 0:
+        raise NotActive("evo_attention", f"D={D}: built for D=32")
+    out = torch.empty(Q.shape, dtype=Q.dtype, device=Q.device)
+    ws = _ws(ws_bytes, Q.device)
+    _lib.call(
+        "pf_evo_attn_fwd", Q.data_ptr(), K.data_ptr(), V.data_ptr(), rm.data_ptr(), pb.data_ptr(), Bk, S, 4, N, D,
+        code, int(zero_rows), out.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(Q),
+    )  # fmt: skip
+    _lib.note_redo("pf_evo_attn_redo_flags", ws, Bk, S, 4, N, D, code)
+    if H != 4:
+        out = out.view(B, G, S, 4, N, D).transpose(1, 2).reshape(B, S, 4 * G, N, D)[:, :, :H].contiguous()
+    return out
+
+
+def _evo_bwd(Q, K, V, rm, pb, dO):
+    """Backward in the kernel layout (``pf_evo_attn_bwd``): returns dQ, dK, dV (Q's dtype) and
+    d_pair_bias ``[B,H,N,N]`` fp32."""
+    B, S, H, N, D = Q.shape
+    code = _lib.dtype_code(Q.dtype)
+    dO = dO.to(Q.dtype).contiguous()
+    ws_bytes = _lib.lib().pf_evo_attn_bwd_workspace_bytes(B, S, H, N, D, code)
+    if ws_bytes == 0:
+        raise NotActive("evo_attention.backward", f"H={H}, D={D}: built for D=32")
+    dQ, dK, dV = (torch.empty(Q.shape, dtype=Q.dtype, device=Q.device) for _ in range(3))
+    dpb = torch.empty((B, H, N, N), dtype=torch.float32, device=Q.device)
+    ws = _ws(ws_bytes, Q.device)
+    _lib.call(
+        "pf_evo_attn_bwd", Q.data_ptr(), K.data_ptr(), V.data_ptr(), rm.data_ptr(), pb.data_ptr(), dO.data_ptr(),
+        B, S, H, N, D, code, float(D) ** -0.5, dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(), dpb.data_ptr(),
+        ws.data_ptr(), ws_bytes, _lib.stream_of(Q),
+    )  # fmt: skip
+    return dQ, dK, dV, dpb
+
+
+class _EvoAttnFunction(torch.autograd.Function):
+    """Kernel-layout attention with the HIP backward; the forward saves its inputs only."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, rm, pb):
+        ctx.save_for_backward(Q, K, V, rm, pb)
+        return _evo_fwd(Q, K, V, rm, pb, True)
+
+    @staticmethod
+    def backward(ctx, dO):
+        Q, K, V, rm, pb = ctx.saved_tensors
+        kernel_census.record("evo_attention.backward", "hip_evo_attn_bwd")
+        dQ, dK, dV, dpb = _evo_bwd(Q, K, V, rm, pb, dO)
+        return dQ, dK, dV, None, dpb
+
+
 class _EvoformerAttention:
     """Flash attention with pair bias and per-line key mask (``evo_attention.py:1198-1292``).
 
@@ -51,35 +120,40 @@ class _EvoformerAttention:
     ``pair_bias [B, 1, H, N_res, N_res]`` fp32. Returns O in the layout of Q.
     ``masked_rows="zero"`` is the reference kernel's rule for a line whose keys are all
     masked (output 0, ``evo_attention.py:307-318``); ``"eager"`` gives the stock path's
-    uniform average (``attention.py:157-160``). Built for H = 4, D = 32.
+    uniform average (``attention.py:157-160``). D = 32, any H.
+
+    Differentiable in Q, K, V and pair_bias (``evo_attention.py:1295-1472``): under grad the
+    backward runs ``pf_evo_attn_bwd`` (centred softmax Jacobian, row statistics recomputed,
+    nothing saved but the inputs). The backward implements the reference kernel's
+    masked-row rule, so training calls take ``masked_rows="zero"``.
     """
 
     @staticmethod
-    @inference_only("evo_attention")
     def apply(Q, K, V, res_mask, pair_bias, pre_transposed: bool = False, masked_rows: str = "zero"):
         _lib.require_device("evo_attention", Q, K, V, res_mask, pair_bias)
         if masked_rows not in ("zero", "eager"):
             raise ValueError(f"masked_rows must be 'zero' or 'eager', got {masked_rows!r}")
+        grad = torch.is_grad_enabled() and any(t.requires_grad for t in (Q, K, V, pair_bias))
+        if grad and masked_rows != "zero":
+            raise NotActive("evo_attention", "the backward implements the reference kernel's masked-row rule; "
+                            "train with masked_rows='zero'")  # fmt: skip
         if not pre_transposed:
             Q, K, V = (t.transpose(-2, -3) for t in (Q, K, V))
         Q, K, V = (t.contiguous() for t in (Q, K, V))
         B, S, H, N, D = Q.shape
         if K.shape != Q.shape or V.shape != Q.shape or K.dtype != Q.dtype or V.dtype != Q.dtype:
             raise NotActive("evo_attention", "Q, K, V must share shape and dtype")
-        rm = res_mask.to(torch.float32).expand(B, S, 1, 1, N).reshape(B, S, N).contiguous()
+        if D != 32:
+            raise NotActive("evo_attention", f"D={D}: built for D=32")
+        rm = res_mask.detach().to(torch.float32).expand(B, S, 1, 1, N).reshape(B, S, N).contiguous()
         pb = pair_bias.to(torch.float32).expand(B, 1, H, N, N).reshape(B, H, N, N).contiguous()
-        out = torch.empty_like(Q)
-        code = _lib.dtype_code(Q.dtype)
-        ws_bytes = _lib.lib().pf_evo_attn_workspace_bytes(B, S, H, N, D, code)
-        if ws_bytes == 0:
-            raise NotActive("evo_attention", f"H={H}, D={D}: built for H=4, D=32")
-        ws = _ws(ws_bytes, Q.device)
-        kernel_census.record("evo_attention", "hip_evo_attn")
-        _lib.call(
-            "pf_evo_attn_fwd", Q.data_ptr(), K.data_ptr(), V.data_ptr(), rm.data_ptr(), pb.data_ptr(), B, S, H, N, D,
-            code, int(masked_rows == "zero"), out.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(Q),
-        )  # fmt: skip
-        _lib.note_redo("pf_evo_attn_redo_flags", ws, B, S, H, N, D, code)
+        if grad:
+            kernel_census.record("evo_attention", "hip_evo_attn_grad")
+            out = _EvoAttnFunction.apply(Q, K, V, rm, pb)
+        else:
+            kernel_census.record("evo_attention", "hip_evo_attn")
+            with torch.no_grad():
+                out = _evo_fwd(Q, K, V, rm, pb, masked_rows == "zero")
         if not pre_transposed:
             out = out.transpose(-2, -3).contiguous()
         return out

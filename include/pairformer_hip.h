@@ -230,6 +230,18 @@ int pf_evo_attn_fwd(const void* q, const void* k, const void* v, const float* re
  * on its stream, its workspace holds *count such flags starting at byte *offset. */
 int pf_grid_attn_redo_flags(int B, int N, int C, int H, int cdtype, size_t* offset, size_t* count);
 int pf_evo_attn_redo_flags(int B, int S, int H, int N, int D, int dtype, size_t* offset, size_t* count);
+/* _EvoformerAttention.backward (triton/evo_attention.py:1295-1472; kernels :335-1195):
+ * gradients of out = softmax(scale q k^T + pair_bias + res_mask) v for q, k, v, dout
+ * [B,S,H,N,D] (dtype) and res_mask [B,S,N], pair_bias [B,H,N,N] fp32, under the reference
+ * kernel's masked-row rule (a line whose keys are all masked has output 0 and gradient 0).
+ * The softmax Jacobian is formed centred on each row's argmax, dS = P (u - C) with
+ * u = dP - dP_imax (docs/optimizations.md:417-483). Writes dq, dk, dv (dtype) and
+ * dpair_bias [B,H,N,N] fp32 (summed over S). The row statistics are recomputed here: the
+ * forward saves nothing. Any H; D = 32. */
+size_t pf_evo_attn_bwd_workspace_bytes(int B, int S, int H, int N, int D, int dtype);
+int pf_evo_attn_bwd(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias,
+                    const void* dout, int B, int S, int H, int N, int D, int dtype, float softmax_scale, void* dq,
+                    void* dk, void* dv, float* dpair_bias, void* workspace, size_t workspace_bytes, void* stream);
 /* FusedPairBias(c, H)(z, ln_w, ln_b, proj_w, mask) (triton/fused_pair_bias.py:348-416):
  * z [B,N,N,C] -> out [B,H,N,N] in z's dtype; proj_w16 [16, C] fp32 (proj_w padded with zero
  * rows); mask [B,N] fp32 or NULL adds (1 - mask) * (-1e9) on the last axis. C = 128, H <= 16. */

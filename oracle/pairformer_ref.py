@@ -29,6 +29,9 @@ Pinning (what checks this restatement, beyond retyping it):
     is its bias b); LayerNorm's invariance to per-row shifts; linearity in W.
   * outer product mean and MSA pair-weighted averaging: explicit loops at tiny sizes; the
     Evoformer block: its pair half equals the template block's on the OPM-updated pair.
+  * kernel-level attention and its backward: a per-row loop for the forward; the centred
+    backward equals autograd of the forward in fp64 and finite differences
+    (``torch.autograd.gradcheck``); the centring constant sums to the uncentred D.
 """
 
 from __future__ import annotations
@@ -51,6 +54,8 @@ __all__ = [
     "outer_product_mean",
     "msa_attention",
     "evoformer_block",
+    "evo_attention",
+    "evo_attention_backward",
 ]
 
 
@@ -419,3 +424,50 @@ def evoformer_block(
     pair = pair + _scaled(col, s)
     pair = pair + _scaled(transition(pair, _sub(p, "pair_transition.")), s)
     return msa, pair
+
+
+def evo_attention(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    res_mask: torch.Tensor,
+    pair_bias: torch.Tensor,
+    zero_rows: bool = True,
+) -> torch.Tensor:
+    """The fused attention op in its kernel layout (``_attn_fwd``, ``triton/evo_attention.py:34-135``,
+    ``:179-333``): Q, K, V [B,S,H,N,D], res_mask [B,S,1,1,N] additive, pair_bias [B,1,H,N,N];
+    softmax(Q K^T D^-1/2 + pair_bias + res_mask) V, softmax over keys. A query row whose
+    logits all sit below -1e8 outputs 0 (``zero_rows``, the kernel's rule, ``:307-318``) or
+    the mean of V (the stock fp32 path, whose -1e9 logits round to one value)."""
+    D = Q.shape[-1]
+    logits = torch.matmul(Q, K.transpose(-1, -2).contiguous()) * D**-0.5 + pair_bias + res_mask
+    dead = logits.amax(dim=-1, keepdim=True) < -1e8
+    out = torch.matmul(torch.softmax(logits, dim=-1), V)
+    fill = torch.zeros_like(out) if zero_rows else V.mean(dim=-2, keepdim=True).expand_as(out)
+    return torch.where(dead, fill, out)
+
+
+def evo_attention_backward(
+    Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, res_mask: torch.Tensor, pair_bias: torch.Tensor,
+    dO: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients of ``evo_attention(zero_rows=True)`` in the centred form of the reference's
+    backward (``_attn_bwd_d`` / ``_dq`` / ``_dk_dv`` / ``_db``, ``triton/evo_attention.py:335-1195``;
+    ``docs/optimizations.md:417-483``): per row, imax = first argmax of the logits,
+    u_j = dP_j - dP_imax (0 at imax), C = sum_j P_j u_j, dS = P (u - C). Returns dQ, dK, dV
+    [B,S,H,N,D] and d_pair_bias [B,1,H,N,N] (dS summed over S)."""
+    D = Q.shape[-1]
+    scale = D**-0.5
+    t = torch.matmul(Q, K.transpose(-1, -2).contiguous()) * scale + pair_bias + res_mask
+    dead = t.amax(dim=-1, keepdim=True) < -1e8
+    P = torch.where(dead, torch.zeros_like(t), torch.softmax(t, dim=-1))
+    dP = torch.matmul(dO, V.transpose(-1, -2).contiguous())
+    imax = t.argmax(dim=-1, keepdim=True)
+    u = dP - dP.gather(-1, imax)
+    u = u.scatter(-1, imax, torch.zeros_like(imax, dtype=u.dtype))
+    C = (P * u).sum(dim=-1, keepdim=True)
+    dS = P * (u - C)
+    dQ = torch.matmul(dS, K) * scale
+    dK = torch.matmul(dS.transpose(-1, -2).contiguous(), Q) * scale
+    dV = torch.matmul(P.transpose(-1, -2).contiguous(), dO)
+    return dQ, dK, dV, dS.sum(dim=1, keepdim=True)

@@ -1,0 +1,157 @@
+"""GPU: the backward of the fused attention op (``_EvoformerAttention``, evo_attention.py:1295-1472).
+
+- Against the oracle's centred backward in fp64 (itself pinned to autograd and finite
+  differences in test_oracle.py): fp32 at relL2 <= 1e-5 and max-abs <= 1e-5 max|ref| for dQ,
+  dK, dV and d_pair_bias, with ragged N, random key masks, a fully masked line (zero
+  gradients) and head counts 2, 4 and 8.
+- The reference's own backward gate (tests/triton/test_evo_attn_robustness.py:340-389):
+  shapes (1,1,128,4,32) and (1,2,384,8,32), seeds 0/42/99, fp32 and bf16, per-element
+  tolerance atol_frac * max|ref| + rtol |ref| with at most 0.1 % of elements outside, the
+  reference's (atol_frac, rtol) policy, here against fp64.
+- Softmax collapse (tests/triton/test_evo_attn_softmax_collapse.py): winner-take-all pair
+  bias at margin ~14.5; dQ within 0.1 of the true peak and d_pair_bias rows summing to
+  <= 0.05 of their peak.
+- The module-layout wrapper, bitwise-reproducible gradients, and refusal of the stock
+  masked-row rule under grad.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import pairformer_ref as R
+from tests._helpers import assert_fp32_close, mod
+
+pytestmark = pytest.mark.gpu
+fused = mod("fused")
+NotActive = mod("inference_guard").NotActive
+BF = torch.bfloat16
+
+
+def _inputs(B, S, H, N, dtype, seed, mask_frac=0.85, dead_line=True, sigma=1.0, layout="kernel"):
+    g = torch.Generator().manual_seed(seed)
+    D = 32
+    qs = sigma / math.sqrt(D)
+    Q, K = (torch.randn(B, S, H, N, D, generator=g) * qs for _ in range(2))
+    V = torch.randn(B, S, H, N, D, generator=g) * sigma
+    pb = torch.randn(B, 1, H, N, N, generator=g)
+    keep = torch.rand(B, S, 1, 1, N, generator=g) < mask_frac
+    keep[..., 0] = True
+    if dead_line and S > 1:
+        keep[:, 1] = False
+    rm = torch.where(keep, 0.0, -1e9)
+    dO = torch.randn(B, S, H, N, D, generator=g) * 0.1
+    Q, K, V, dO = (t.to(dtype) for t in (Q, K, V, dO))
+    return Q, K, V, rm, pb, dO
+
+
+def _hip_grads(Q, K, V, rm, pb, dO, dev):
+    leaves = [t.to(dev).requires_grad_(True) for t in (Q, K, V, pb)]
+    out = fused._EvoformerAttention.apply(leaves[0], leaves[1], leaves[2], rm.to(dev), leaves[3], True)
+    grads = torch.autograd.grad(out, leaves, grad_outputs=dO.to(dev))
+    return [g.float().cpu() for g in grads], out.detach()
+
+
+def _oracle_grads(Q, K, V, rm, pb, dO):
+    return R.evo_attention_backward(*(t.double() for t in (Q, K, V, rm, pb, dO)))
+
+
+@pytest.mark.parametrize("B,S,H,N", [(2, 3, 4, 50), (1, 2, 8, 128), (1, 3, 2, 70), (1, 2, 4, 200)])
+def test_attn_backward_fp32(dev, B, S, H, N):
+    print(f"[attn bwd fp32] B={B} S={S} H={H} N={N}", flush=True)
+    Q, K, V, rm, pb, dO = _inputs(B, S, H, N, torch.float32, seed=N + H)
+    got, out = _hip_grads(Q, K, V, rm, pb, dO, dev)
+    want = _oracle_grads(Q, K, V, rm, pb, dO)
+    for a, b, name in zip(got, want, ("dQ", "dK", "dV", "d_pair_bias")):
+        assert a.shape == b.shape, name
+        assert_fp32_close(a, b.float(), what=f"{name} N={N} H={H}")
+    # the fully masked line: output and every gradient are 0
+    assert torch.count_nonzero(out[:, 1]) == 0
+    for a in got[:3]:
+        assert torch.count_nonzero(a[:, 1]) == 0
+
+
+def _metrics(kernel, ref, atol_frac, rtol):
+    kf, rf = kernel.double(), ref.double()
+    tol = atol_frac * rf.abs().max() + rtol * rf.abs()
+    return float(((kf - rf).abs() > tol).double().mean()), bool(torch.isfinite(kf).all())
+
+
+# (atol_frac, rtol) of the reference's BWD_QKV_POLICY / BWD_BIAS_POLICY (fp32 entries are its TF32 ones)
+POLICY = {torch.float32: ((5e-3, 1e-2), (5e-3, 1e-2)), BF: ((5e-3, 5e-2), (5e-3, 2e-2))}
+
+
+@pytest.mark.parametrize("B,S,N,H", [(1, 1, 128, 4), (1, 2, 384, 8)])
+@pytest.mark.parametrize("seed", [0, 42, 99])
+@pytest.mark.parametrize("dtype", [torch.float32, BF], ids=["fp32", "bf16"])
+def test_attn_backward_reference_gate(dev, dtype, seed, B, S, N, H):
+    print(f"[attn bwd gate] {dtype} seed={seed} S={S} N={N} H={H}", flush=True)
+    Q, K, V, rm, pb, dO = _inputs(B, S, H, N, dtype, seed, mask_frac=1.0, dead_line=False)
+    got, _ = _hip_grads(Q, K, V, rm, pb, dO, dev)
+    want = _oracle_grads(Q, K, V, rm, pb, dO)
+    qkv, bias = POLICY[dtype]
+    for a, b, name in zip(got, want, ("dQ", "dK", "dV", "d_pair_bias")):
+        frac, finite = _metrics(a, b, *(bias if name == "d_pair_bias" else qkv))
+        assert finite and frac <= 1e-3, f"{name}: fail_frac {frac:.3e}"
+
+
+def _wta(spike: float, dtype=BF, seed=42):
+    """Winner-take-all: +spike on one pair-bias column per head (B1 S2 N256 H8 D32)."""
+    B, S, N, H, D = 1, 2, 256, 8, 32
+    g = torch.Generator().manual_seed(seed)
+    qs = D**-0.5
+    Q, K = (torch.randn(B, S, H, N, D, generator=g) * qs for _ in range(2))
+    V = torch.randn(B, S, H, N, D, generator=g)
+    pb = torch.randn(B, 1, H, N, N, generator=g) * 0.1
+    for h in range(H):
+        pb[:, :, h, :, (h * 37) % N] += spike
+    dO = torch.randn(B, S, H, N, D, generator=g) * 0.1
+    rm = torch.zeros(B, S, 1, 1, N)
+    Q, K, V, dO = (t.to(dtype) for t in (Q, K, V, dO))
+    return Q, K, V, rm, pb, dO
+
+
+def test_attn_backward_softmax_collapse(dev):
+    Q, K, V, rm, pb, dO = _wta(20.0)
+    t = torch.matmul(Q.double(), K.double().transpose(-1, -2)) * 32**-0.5 + pb.double()
+    imax = t.argmax(-1, keepdim=True)
+    margin = (t.gather(-1, imax) - torch.logsumexp(t.scatter(-1, imax, -torch.inf), -1, keepdim=True)).mean()
+    assert 13.0 < float(margin) < 16.6
+    print(f"[attn bwd collapse] margin {float(margin):.2f}", flush=True)
+    got, _ = _hip_grads(Q, K, V, rm, pb, dO, dev)
+    want = _oracle_grads(Q, K, V, rm, pb, dO)
+    peak = want[0].abs().max()
+    assert 3e-8 < float(peak) < 1e-6  # the true dQ is small but not noise
+    err = (got[0].double() - want[0]).abs().max()
+    assert err <= 0.1 * peak, f"dQ error {float(err):.3e} vs true peak {float(peak):.3e}"
+    db = got[3]
+    assert want[3].sum(-1).abs().max() <= 1e-6 * want[3].abs().max()
+    assert db.sum(-1).abs().max() <= 0.05 * db.abs().max(), "d_pair_bias rows no longer sum to zero"
+
+
+def test_attn_backward_wrapper_and_determinism(dev):
+    B, S, N, H = 1, 4, 96, 4
+    Q, K, V, rm, pb, dO = _inputs(B, S, H, N, BF, seed=5, dead_line=False)
+    # module layout: q, k, v [B*S, N, H, D], pair_bias [B, H, N, N], mask [B*S, N] (1 keep)
+    mask = (rm.view(B * S, N) > -1).float().to(dev)
+    q, k, v = (t.transpose(-2, -3).reshape(B * S, N, H, 32).to(dev).requires_grad_(True) for t in (Q, K, V))
+    p = pb.view(B, H, N, N).to(dev).requires_grad_(True)
+    o = fused.fused_evo_attention(q, k, v, p, mask)
+    do = dO.transpose(-2, -3).reshape(B * S, N, H, 32).to(dev)
+    g1 = torch.autograd.grad(o, [q, k, v, p], grad_outputs=do)
+    got, _ = _hip_grads(Q, K, V, rm, pb, dO, dev)
+    assert torch.equal(g1[0].float().cpu().view(B, S, N, H, 32).transpose(-2, -3), got[0])
+    assert torch.equal(g1[3].float().cpu(), got[3].view(B, H, N, N))
+    again, _ = _hip_grads(Q, K, V, rm, pb, dO, dev)
+    for a, b in zip(got, again):
+        assert torch.equal(a, b)
+
+
+def test_attn_backward_refuses_stock_rule(dev):
+    Q, K, V, rm, pb, _ = _inputs(1, 2, 4, 32, torch.float32, seed=6)
+    q = Q.to(dev).requires_grad_(True)
+    with pytest.raises(NotActive, match="masked-row rule"):
+        fused._EvoformerAttention.apply(q, K.to(dev), V.to(dev), rm.to(dev), pb.to(dev), True, "eager")

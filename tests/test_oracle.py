@@ -523,3 +523,76 @@ def test_evoformer_block_composition():
         m2, z2 = R.evoformer_block(msa, x["pair"], mmask, x["pair_mask"], p, residual_out_scale=0.0)
     assert torch.equal(z1, zw) and torch.equal(m1, mw)
     assert torch.equal(z2, x["pair"]) and torch.equal(m2, msa)
+
+
+def _evo_case(B=1, S=3, H=2, N=6, D=4, seed=0, dead_line=True):
+    g = torch.Generator().manual_seed(seed)
+    Q, K, V = (torch.randn(B, S, H, N, D, generator=g, dtype=torch.float64) for _ in range(3))
+    pb = torch.randn(B, 1, H, N, N, generator=g, dtype=torch.float64)
+    keep = torch.rand(B, S, 1, 1, N, generator=g) > 0.3
+    keep[..., 0] = True
+    if dead_line:
+        keep[:, -1] = False
+    rm = torch.where(keep, 0.0, -1e9).double()
+    dO = torch.randn(B, S, H, N, D, generator=g, dtype=torch.float64)
+    return Q, K, V, rm, pb, dO
+
+
+def test_evo_attention_against_loops():
+    """evo_attention.py:179-333: per (line, head, query) softmax over keys of
+    q.k / sqrt(D) + bias + mask, weights times V; an all-masked line gives 0 (zero rule) or
+    the mean of V (stock rule)."""
+    import math
+
+    Q, K, V, rm, pb, _ = _evo_case(seed=1)
+    B, S, H, N, D = Q.shape
+    for zero in (True, False):
+        got = R.evo_attention(Q, K, V, rm, pb, zero_rows=zero)
+        for s in range(S):
+            for h in range(H):
+                for i in range(N):
+                    logit = [float(Q[0, s, h, i] @ K[0, s, h, j]) / math.sqrt(D) + float(pb[0, 0, h, i, j])
+                             + float(rm[0, s, 0, 0, j]) for j in range(N)]  # fmt: skip
+                    if max(logit) < -1e8:
+                        want = torch.zeros(D, dtype=torch.float64) if zero else V[0, s, h].mean(0)
+                    else:
+                        m = max(logit)
+                        e = [math.exp(x - m) for x in logit]
+                        want = sum(e[j] / sum(e) * V[0, s, h, j] for j in range(N))
+                    assert torch.allclose(got[0, s, h, i], want, rtol=1e-12, atol=1e-12), (zero, s, h, i)
+
+
+def test_evo_attention_backward_equals_autograd():
+    """The centred backward (evo_attention.py:335-1195) is the gradient of the zero-rule
+    forward: equal to autograd in fp64, including the dead line (all zeros)."""
+    Q, K, V, rm, pb, dO = _evo_case(B=2, S=3, H=2, N=9, D=4, seed=2)
+    leaves = [t.clone().requires_grad_(True) for t in (Q, K, V, pb)]
+    out = R.evo_attention(leaves[0], leaves[1], leaves[2], rm, leaves[3], zero_rows=True)
+    want = torch.autograd.grad(out, leaves, grad_outputs=dO)
+    got = R.evo_attention_backward(Q, K, V, rm, pb, dO)
+    for a, b, name in zip(got, want, ("dQ", "dK", "dV", "d_pair_bias")):
+        assert a.shape == b.shape, name
+        assert torch.allclose(a, b, rtol=1e-10, atol=1e-12), name
+    assert torch.count_nonzero(got[0][:, -1]) == 0 and torch.count_nonzero(got[2][:, -1]) == 0
+
+
+def test_evo_attention_gradcheck():
+    """Finite differences pin the forward's gradient (and so the restated backward)."""
+    Q, K, V, rm, pb, _ = _evo_case(B=1, S=2, H=1, N=5, D=3, seed=3, dead_line=False)
+    leaves = [t.clone().requires_grad_(True) for t in (Q, K, V, pb)]
+    assert torch.autograd.gradcheck(lambda q, k, v, b: R.evo_attention(q, k, v, rm, b), leaves, eps=1e-6,
+                                    atol=1e-7)  # fmt: skip
+
+
+def test_evo_attention_centring_identity():
+    """C = sum_j P_j (dP_j - dP_imax) equals D - dP_imax with D = rowsum(P dP) = rowsum(dO O):
+    the centred and uncentred dS agree where both are exact (fp64, moderate margins)."""
+    Q, K, V, rm, pb, dO = _evo_case(B=1, S=2, H=2, N=8, D=4, seed=4, dead_line=False)
+    t = torch.matmul(Q, K.transpose(-1, -2)) * 0.5 + pb + rm
+    P = torch.softmax(t, dim=-1)
+    dP = torch.matmul(dO, V.transpose(-1, -2))
+    out = R.evo_attention(Q, K, V, rm, pb)
+    Dv = (dO * out).sum(-1, keepdim=True)
+    dS_plain = P * (dP - Dv)
+    got = R.evo_attention_backward(Q, K, V, rm, pb, dO)
+    assert torch.allclose(got[3], dS_plain.sum(1, keepdim=True), rtol=1e-10, atol=1e-13)
