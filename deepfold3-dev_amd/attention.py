@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import kernel_census
 from .config import OptimConfig, require_hip
@@ -75,13 +76,42 @@ class GridSelfAttention(nn.Module):
             num_heads=self.num_heads, out=out, accumulate=accumulate,
         )  # fmt: skip
 
-    @inference_only("GridSelfAttention")
+    def _forward_grad(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """Training path, as the reference's fused-attention branch (``attention.py:211-257``):
+        LayerNorm, pair bias and q/k/v/g projections in autograd, the HIP flash attention with
+        its backward (``fused._EvoformerAttention``, the kernel's masked-row rule), gate and
+        output projection in autograd. Head dimension 32."""
+        from .fused import _EvoformerAttention
+
+        B, N, _, C = z.shape
+        H, D = self.num_heads, self.head_dim
+        if D != 32:
+            raise NotActive("GridSelfAttention", f"head dim {D}: the differentiable attention is built for 32")
+        zn = F.layer_norm(z.float(), (C,), self.norm.weight.float(), self.norm.bias.float(), self.norm.eps).to(z.dtype)
+        pb = F.linear(zn, self.pair_bias.weight).permute(0, 3, 1, 2)  # [B, H, N, N], un-transposed z
+        if self.transpose:
+            zn, mask = zn.transpose(1, 2), mask.transpose(1, 2)
+        qkv = [F.linear(zn, lin.weight).reshape(B, N, N, H, D).transpose(-2, -3).contiguous()
+               for lin in (self.to_q, self.to_k, self.to_v)]  # fmt: skip
+        res_mask = torch.where(mask > 0.5, 0.0, -1e9).view(B, N, 1, 1, N)
+        o = _EvoformerAttention.apply(*qkv, res_mask, pb.unsqueeze(1).float(), True)
+        o = o.transpose(-2, -3).reshape(B, N, N, H * D)
+        g = torch.sigmoid(F.linear(zn, self.to_g.weight))
+        w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
+        out = F.linear(o * g, w_out)
+        return out.transpose(1, 2) if self.transpose else out
+
     def forward(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
-        """The update for z [B?, N, N, C], mask [B?, N, N] (not added to z)."""
+        """The update for z [B?, N, N, C], mask [B?, N, N] (not added to z). Under grad it
+        runs the differentiable path, else the fused inference kernels."""
         has_batch = z.dim() == 4
         if not has_batch:
             z, mask = z.unsqueeze(0), mask.unsqueeze(0)
-        out = self._run(z, mask, None, False)
+        if torch.is_grad_enabled():
+            kernel_census.record("GridSelfAttention.attention", "hip_evo_attn_grad")
+            out = self._forward_grad(z, mask)
+        else:
+            out = self._run(z, mask, None, False)
         return out if has_batch else out.squeeze(0)
 
     @inference_only("GridSelfAttention")

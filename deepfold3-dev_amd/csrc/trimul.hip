@@ -27,7 +27,9 @@ constexpr int trimul_bm() { return sizeof(TC) == 2 ? 64 : 32; }
 // ------------------------------------------------------------------ K1
 // Packed weights w4 [4C][C]: for channel block j (16 channels), rows 64j + 16*kind + r,
 // kind 0 = a projection, 1 = a gate, 2 = b projection, 3 = b gate (channel 16j + r).
-template <class TZ, class TC, int C>
+// NORM = false takes z as already normalised (the training entry, whose input LayerNorm
+// runs outside).
+template <class TZ, class TC, int C, bool NORM = true>
 __global__ __launch_bounds__(256) void trimul_project_kernel(const TZ* __restrict__ z, const float* __restrict__ mask,
                                                              const float* __restrict__ lnw,
                                                              const float* __restrict__ lnb, float eps,
@@ -60,7 +62,10 @@ __global__ __launch_bounds__(256) void trimul_project_kernel(const TZ* __restric
     const long pos = pos_of(p);
     return pos < 0 ? nullptr : zb + pos * C;
   };
-  ln_tile_to_lds<TZ, TC, C, BM, NT>(rowptr, lnw, lnb, eps, A, LDA);
+  if constexpr (NORM)
+    ln_tile_to_lds<TZ, TC, C, BM, NT>(rowptr, lnw, lnb, eps, A, LDA);
+  else
+    copy_tile_to_lds<TZ, TC, C, BM, NT>(rowptr, A, LDA);
   if (tid < BM) {
     const long pos = pos_of(tid);
     mk[tid] = pos < 0 ? 0.f : mask[(size_t)b * N * N + pos];
@@ -492,7 +497,7 @@ struct OutputCfg {
   static constexpr int NQ = 256 / BM;  // threads per position in the LN_out pass
 };
 
-template <class TZ, class TC, int C>
+template <class TZ, class TC, int C, bool NORM = true>
 __global__ __launch_bounds__(256) void trimul_output_kernel(
     const TC* __restrict__ X, const TZ* __restrict__ z, TZ* __restrict__ out, const float* __restrict__ lniw,
     const float* __restrict__ lnib, float eps_in, const float* __restrict__ lnow, const float* __restrict__ lnob,
@@ -536,7 +541,10 @@ __global__ __launch_bounds__(256) void trimul_output_kernel(
     const int j = j0 + p;
     return j < N ? zb + ((size_t)i * N + j) * C : nullptr;
   };
-  ln_tile_to_lds<TZ, TC, C, BM, NT>(zrow, lniw, lnib, eps_in, A2, ALD);
+  if constexpr (NORM)
+    ln_tile_to_lds<TZ, TC, C, BM, NT>(zrow, lniw, lnib, eps_in, A2, ALD);
+  else
+    copy_tile_to_lds<TZ, TC, C, BM, NT>(zrow, A2, ALD);
   __syncthreads();
 
   // 2) LN_out over channels of X, transposing into A1[p][c]
@@ -1328,6 +1336,42 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
   return pf::ok();
 }
 
+// Training forward (FusedTriMulFunction.forward): the generic K1 and K3 without the input
+// LayerNorm, the planes P, Q and the contraction X left in `planes` for the backward.
+template <class TZ, class TC, int C>
+int trimul_train_launch(const void* x, const float* mask, const void* w4, const float* lnow, const float* lnob,
+                        float eps_out, const void* wo, const void* wog, int B, int N, int outgoing, void* planes_ws,
+                        void* out, hipStream_t s) {
+  const int Np = pf::pad128(N);
+  const size_t pe = (size_t)Np * Np;
+  TC* planes = reinterpret_cast<TC*>(planes_ws);
+  TC* P = planes;
+  TC* Q = planes + (size_t)B * C * pe;
+  TC* X = planes + (size_t)2 * B * C * pe;
+  constexpr int BM = trimul_bm<TC>();
+  trimul_project_kernel<TZ, TC, C, false><<<dim3(Np / BM, Np, B), 256, 0, s>>>(
+      (const TZ*)x, mask, nullptr, nullptr, 0.f, (const TC*)w4, planes, B, N, Np, outgoing);
+  if (int e = pf::check_launch("trimul_train_project")) return e;
+  const int G = B * C;
+  const int remap = (G % 8 == 0) ? 1 : 0;
+  int e = PF_OK;
+  if constexpr (sizeof(TC) == 2) {
+    if (Np % 768 == 0)
+      e = contract_persistent_launch<384>(P, Q, X, G, Np, remap, s);
+    else if (Np % 256 == 0)
+      e = contract_persistent_launch<256>(P, Q, X, G, Np, remap, s);
+    else
+      e = contract_generic_launch<TC>(P, Q, X, G, Np, remap, s);
+  } else {
+    e = contract_generic_launch<TC>(P, Q, X, G, Np, remap, s);
+  }
+  if (e) return e;
+  trimul_output_kernel<TZ, TC, C, false><<<dim3((N + BM - 1) / BM, N, B), 256, 0, s>>>(
+      X, (const TZ*)x, (TZ*)out, nullptr, nullptr, 0.f, lnow, lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
+      0);
+  return pf::check_launch("trimul_train_output");
+}
+
 }  // namespace
 
 extern "C" {
@@ -1390,6 +1434,61 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
                                             w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
     return trimul_launch<bf16, bf16, CC>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out,
                                          w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+  };
+  if (C == 64) return run(std::integral_constant<int, 64>{});
+  if (C == 256) return run(std::integral_constant<int, 256>{});
+  return run(std::integral_constant<int, 128>{});
+}
+
+int pf_trimul_train_pack_weights(const void* w_proj, const void* w_gate, int wdtype, void* packed, int C, int cdtype,
+                                 void* stream) {
+  PF_REQUIRE(w_proj && w_gate && packed, PF_ERR_INVALID_ARG, "pf_trimul_train_pack_weights: null pointer");
+  PF_REQUIRE(C == 64 || C == 128 || C == 256, PF_ERR_UNSUPPORTED,
+             "pf_trimul_train_pack_weights: C=%d (built: 64, 128, 256)", C);
+  PF_REQUIRE((wdtype == PF_F32 || wdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16), PF_ERR_UNSUPPORTED,
+             "pf_trimul_train_pack_weights: bad dtype");
+  hipStream_t s = pf::as_stream(stream);
+  dim3 grid((4 * C * C + 255) / 256);
+  if (wdtype == PF_F32 && cdtype == PF_F32)
+    trimul_pack_kernel<float, float><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (float*)packed, C, 16);
+  else if (wdtype == PF_F32)
+    trimul_pack_kernel<float, bf16><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (bf16*)packed, C, 16);
+  else if (cdtype == PF_F32)
+    trimul_pack_kernel<bf16, float><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (float*)packed, C, 16);
+  else
+    trimul_pack_kernel<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (bf16*)packed, C, 16);
+  return pf::check_launch("pf_trimul_train_pack_weights");
+}
+
+int pf_trimul_train_fwd(const void* x, const float* mask, const void* w_packed, const float* ln_out_w,
+                        const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate, int B, int N,
+                        int C, int outgoing, int xdtype, int cdtype, void* planes, size_t planes_bytes, void* out,
+                        void* stream) {
+  PF_REQUIRE(x && mask && w_packed && ln_out_w && ln_out_b && w_out && w_out_gate && planes && out,
+             PF_ERR_INVALID_ARG, "pf_trimul_train_fwd: null pointer");
+  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_trimul_train_fwd: B=%d N=%d", B, N);
+  PF_REQUIRE(C == 64 || C == 128 || C == 256, PF_ERR_UNSUPPORTED, "pf_trimul_train_fwd: C=%d (built: 64, 128, 256)",
+             C);
+  PF_REQUIRE((xdtype == PF_F32 || xdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16) &&
+                 !(xdtype == PF_BF16 && cdtype == PF_F32),
+             PF_ERR_UNSUPPORTED, "pf_trimul_train_fwd: xdtype %d cdtype %d", xdtype, cdtype);
+  PF_REQUIRE(pf::aligned16(x) && pf::aligned16(out) && pf::aligned16(planes) && pf::aligned16(w_packed) &&
+                 pf::aligned16(w_out) && pf::aligned16(w_out_gate),
+             PF_ERR_ALIGNMENT, "pf_trimul_train_fwd: pointers must be 16-byte aligned");
+  PF_REQUIRE(planes_bytes >= pf_trimul_workspace_bytes(B, N, C, cdtype), PF_ERR_WORKSPACE,
+             "pf_trimul_train_fwd: planes buffer %zu < %zu bytes", planes_bytes,
+             pf_trimul_workspace_bytes(B, N, C, cdtype));
+  hipStream_t s = pf::as_stream(stream);
+  auto run = [&](auto cc) {
+    constexpr int CC = decltype(cc)::value;
+    if (xdtype == PF_F32 && cdtype == PF_F32)
+      return trimul_train_launch<float, float, CC>(x, mask, w_packed, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate,
+                                                   B, N, outgoing, planes, out, s);
+    if (xdtype == PF_F32)
+      return trimul_train_launch<float, bf16, CC>(x, mask, w_packed, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate,
+                                                  B, N, outgoing, planes, out, s);
+    return trimul_train_launch<bf16, bf16, CC>(x, mask, w_packed, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate, B,
+                                               N, outgoing, planes, out, s);
   };
   if (C == 64) return run(std::integral_constant<int, 64>{});
   if (C == 256) return run(std::integral_constant<int, 256>{});

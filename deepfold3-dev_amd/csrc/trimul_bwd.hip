@@ -1,0 +1,527 @@
+// Backward of the triangle multiply after its input LayerNorm (FusedTriMulFunction.backward,
+// src/deepfold3/model/triton/fused_trimul.py:298-330, VJP kernels :153-262).
+//
+// Forward (x = LN_in(z) given): a | b = sigmoid(x Wg^T) * (x Wp^T) * mask on channel-major
+// planes P, Q; X = P Q^T per channel; out = sigmoid(x Wog^T) * (LN_out(X) Wo^T).
+//
+//   trimul_output_vjp:  per (line, 64 plane positions): recompute LN_out(X) and both output
+//                       GEMMs, gp = g s, gg = g p s (1 - s); d(xln) = gp Wo, pulled through
+//                       LN_out into dX (channel-major planes, zero at padding); the output
+//                       gate's x cotangent gg Wog (fp32); gp, gg and xln token-major for the
+//                       weight gradients; per-block partial sums of the LN_out affine
+//                       gradients, reduced in a fixed order by trimul_ln_grad_reduce.
+//   (host)              dP = dX Q, dQ = dX^T P, weight gradients: plain library GEMMs.
+//   trimul_project_vjp: per (line, plane positions) as the forward K1: recompute both gated
+//                       projections, G = (gp_a, gg_a, gp_b, gg_b) in the packed weight order,
+//                       dx = gx + G W4 (W4 the packed [4C][C] weights), G token-major.
+//
+// The LN_out pullback with xn the standardised X and u = d(xln) * ln_w is
+// rstd (u - mean_c(u) - xn mean_c(u xn)) (fused_trimul.py:166-171).
+#include <algorithm>
+#include <type_traits>
+
+#include "capi.h"
+#include "common.h"
+
+namespace {
+
+// Positions per block: 64 where LDS allows (C * sizeof(TC) <= 256 bytes), fewer above.
+template <class TC, int C>
+constexpr int vjp_bm() {
+  return std::min(64, 16384 / (C * (int)sizeof(TC)));
+}
+
+// ------------------------------------------------------------------ output VJP
+template <class TZ, class TC, int C>
+__global__ __launch_bounds__(256) void trimul_output_vjp_kernel(
+    const TZ* __restrict__ g, const TC* __restrict__ X, const TZ* __restrict__ x, const float* __restrict__ lnow,
+    const float* __restrict__ lnob, float eps, const TC* __restrict__ Wo, const TC* __restrict__ Wog,
+    const TC* __restrict__ WoT, const TC* __restrict__ WogT, int B, int N, int Np, TC* __restrict__ gp_out,
+    TC* __restrict__ gg_out, TC* __restrict__ xln_out, TC* __restrict__ dX, float* __restrict__ gx,
+    float* __restrict__ partial) {
+  constexpr int BM = vjp_bm<TC, C>();
+  constexpr int NT = 256;
+  constexpr int RB = BM / 16;
+  constexpr int CBW = C / 64;  // 16-channel blocks per wave
+  constexpr int XLD = BM + lds_pad<TC>();
+  constexpr int ALD = C + lds_pad<TC>();
+  constexpr int SLD = C + 4;
+  constexpr int NQ = NT / BM;  // threads per position in the per-position passes
+  constexpr int CPQ = C / NQ;
+  constexpr int VEC = 16 / sizeof(TC);
+  static_assert(CPQ % VEC == 0, "per-thread channel run must be whole 16-byte chunks");
+  constexpr int XS_BYTES = C * XLD * (int)sizeof(TC);
+  constexpr int A_BYTES = BM * ALD * (int)sizeof(TC);
+  constexpr int ST_BYTES = BM * SLD * 4;
+  constexpr int R_BYTES = 2 * A_BYTES > ST_BYTES ? 2 * A_BYTES : ST_BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[XS_BYTES + R_BYTES];
+  __shared__ float s_mean[BM], s_rstd[BM];
+  TC* Xs = reinterpret_cast<TC*>(smem);                       // X [c][p], later dX
+  TC* A1 = reinterpret_cast<TC*>(smem + XS_BYTES);            // xln, then gp
+  TC* A2 = reinterpret_cast<TC*>(smem + XS_BYTES + A_BYTES);  // x, then gg
+  float* stage = reinterpret_cast<float*>(smem + XS_BYTES);   // d(xln), fp32
+
+  const int j0 = blockIdx.x * BM;
+  const int i = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const size_t pe = (size_t)Np * Np;
+  auto tok = [&](int p) -> long {
+    const int j = j0 + p;
+    return (i < N && j < N) ? ((long)b * N + i) * N + j : -1;
+  };
+
+  // X tile, channel-major (rows of BM contiguous positions per channel)
+  {
+    constexpr int CPR = BM / VEC;
+    const TC* Xb = X + (size_t)b * C * pe + (size_t)i * Np + j0;
+    for (int idx = tid; idx < C * CPR; idx += NT) {
+      const int c = idx / CPR;
+      const int ch = idx % CPR;
+      *reinterpret_cast<u32x4*>(Xs + c * XLD + ch * VEC) =
+          *reinterpret_cast<const u32x4*>(Xb + (size_t)c * pe + ch * VEC);
+    }
+  }
+  copy_tile_to_lds<TZ, TC, C, BM, NT>(
+      [&](int p) -> const TZ* {
+        const long t = tok(p);
+        return t < 0 ? nullptr : x + t * C;
+      },
+      A2, ALD);
+  __syncthreads();
+
+  // LN_out statistics (fp32, two-pass) and xln = LN_out(X) into A1 [p][c] and to xln_out
+  const int pq = tid / NQ;
+  const int qq = tid % NQ;
+  {
+    float xv[CPQ];
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      xv[e] = to_f32(Xs[(qq * CPQ + e) * XLD + pq]);
+      s += xv[e];
+    }
+    const float mean = group_sum<NQ>(s) * (1.0f / C);
+    float v = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      const float d = xv[e] - mean;
+      v += d * d;
+    }
+    const float rstd = rsqrtf(group_sum<NQ>(v) * (1.0f / C) + eps);
+    if (qq == 0) {
+      s_mean[pq] = mean;
+      s_rstd[pq] = rstd;
+    }
+    float y[CPQ];
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      const int c = qq * CPQ + e;
+      y[e] = (xv[e] - mean) * rstd * lnow[c] + lnob[c];
+    }
+    const long t = tok(pq);
+#pragma unroll
+    for (int e = 0; e < CPQ; e += VEC) {
+      store_vec<TC, VEC>(A1 + pq * ALD + qq * CPQ + e, y + e);
+      if (t >= 0) store_vec<TC, VEC>(xln_out + t * C + qq * CPQ + e, y + e);
+    }
+  }
+  __syncthreads();
+
+  // p = xln Wo^T, s = sigmoid(x Wog^T)
+  const int w = wave_id();
+  const int l = lane_id();
+  int wrow0[CBW];
+#pragma unroll
+  for (int j = 0; j < CBW; ++j) wrow0[j] = (w * CBW + j) * 16;
+  f32x4 accp[RB][CBW], accg[RB][CBW];
+  zero_acc(accp);
+  zero_acc(accg);
+  gemm16_lds_x_w<TC, C, RB, CBW>(accp, A1, ALD, 0, Wo, C, wrow0);
+  gemm16_lds_x_w<TC, C, RB, CBW>(accg, A2, ALD, 0, Wog, C, wrow0);
+  __syncthreads();  // A1 / A2 are rewritten below
+
+  // gp = g s, gg = g p s (1 - s), rounded to TC as the next GEMMs' operands
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int jb = 0; jb < CBW; ++jb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p = rb * 16 + 4 * (l >> 4) + e;
+        const int c = (w * CBW + jb) * 16 + (l & 15);
+        const long t = tok(p);
+        const float gv = t < 0 ? 0.f : to_f32(g[t * C + c]);
+        const float sv = sigmoidf_(accg[rb][jb][e]);
+        A1[p * ALD + c] = from_f32<TC>(gv * sv);
+        A2[p * ALD + c] = from_f32<TC>(gv * accp[rb][jb][e] * sv * (1.f - sv));
+      }
+  __syncthreads();
+  {
+    constexpr int CPR = C / VEC;
+    for (int idx = tid; idx < BM * CPR; idx += NT) {
+      const int p = idx / CPR;
+      const int ch = (idx % CPR) * VEC;
+      const long t = tok(p);
+      if (t < 0) continue;
+      *reinterpret_cast<u32x4*>(gp_out + t * C + ch) = *reinterpret_cast<const u32x4*>(A1 + p * ALD + ch);
+      *reinterpret_cast<u32x4*>(gg_out + t * C + ch) = *reinterpret_cast<const u32x4*>(A2 + p * ALD + ch);
+    }
+  }
+
+  // d(xln) = gp Wo, the output gate's x cotangent gg Wog
+  f32x4 accd[RB][CBW], accx[RB][CBW];
+  zero_acc(accd);
+  zero_acc(accx);
+  gemm16_lds_x_w<TC, C, RB, CBW>(accd, A1, ALD, 0, WoT, C, wrow0);
+  gemm16_lds_x_w<TC, C, RB, CBW>(accx, A2, ALD, 0, WogT, C, wrow0);
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int jb = 0; jb < CBW; ++jb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p = rb * 16 + 4 * (l >> 4) + e;
+        const int c = (w * CBW + jb) * 16 + (l & 15);
+        const long t = tok(p);
+        if (t >= 0) gx[t * C + c] = accx[rb][jb][e];
+      }
+  __syncthreads();  // A1 / A2 dead: the fp32 stage takes their place
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int jb = 0; jb < CBW; ++jb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p = rb * 16 + 4 * (l >> 4) + e;
+        const int c = (w * CBW + jb) * 16 + (l & 15);
+        stage[p * SLD + c] = accd[rb][jb][e];
+      }
+  __syncthreads();
+
+  // Per-block partial sums of the LN_out affine gradients, one thread per channel.
+  {
+    const size_t blk = ((size_t)b * gridDim.y + i) * gridDim.x + blockIdx.x;
+    for (int c = tid; c < C; c += NT) {
+      float sw = 0.f, sb = 0.f;
+      for (int p = 0; p < BM; ++p) {
+        const float xn = (to_f32(Xs[c * XLD + p]) - s_mean[p]) * s_rstd[p];
+        const float d = stage[p * SLD + c];
+        sw += d * xn;
+        sb += d;
+      }
+      partial[blk * 2 * C + c] = sw;
+      partial[blk * 2 * C + C + c] = sb;
+    }
+  }
+  __syncthreads();  // Xs is overwritten with dX below
+
+  // LN_out pullback, in place over Xs: each thread owns (position pq, channels qq*CPQ..)
+  {
+    const float mean = s_mean[pq], rstd = s_rstd[pq];
+    float u[CPQ], xn[CPQ];
+    float su = 0.f, sux = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) {
+      const int c = qq * CPQ + e;
+      xn[e] = (to_f32(Xs[c * XLD + pq]) - mean) * rstd;
+      u[e] = stage[pq * SLD + c] * lnow[c];
+      su += u[e];
+      sux += u[e] * xn[e];
+    }
+    su = group_sum<NQ>(su) * (1.0f / C);
+    sux = group_sum<NQ>(sux) * (1.0f / C);
+#pragma unroll
+    for (int e = 0; e < CPQ; ++e) Xs[(qq * CPQ + e) * XLD + pq] = from_f32<TC>(rstd * (u[e] - su - xn[e] * sux));
+  }
+  __syncthreads();
+  {
+    constexpr int CPR = BM / VEC;
+    TC* Db = dX + (size_t)b * C * pe + (size_t)i * Np + j0;
+    for (int idx = tid; idx < C * CPR; idx += NT) {
+      const int c = idx / CPR;
+      const int ch = idx % CPR;
+      *reinterpret_cast<u32x4*>(Db + (size_t)c * pe + ch * VEC) =
+          *reinterpret_cast<const u32x4*>(Xs + c * XLD + ch * VEC);
+    }
+  }
+}
+
+// out[k] = sum over blocks of partial[blk][k], k < 2C (w then b), in a fixed order.
+__global__ __launch_bounds__(256) void trimul_ln_grad_reduce_kernel(const float* __restrict__ partial, long nblk,
+                                                                    int C2, float* __restrict__ dw,
+                                                                    float* __restrict__ db) {
+  __shared__ float red[256];
+  const int k = blockIdx.x;
+  float s = 0.f;
+  for (long blk = threadIdx.x; blk < nblk; blk += 256) s += partial[blk * C2 + k];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const int C = C2 / 2;
+    if (k < C)
+      dw[k] = red[0];
+    else
+      db[k - C] = red[0];
+  }
+}
+
+// ------------------------------------------------------------------ project VJP
+// Packed weights w4 [4C][C] as the forward K1 reads them (16-channel blocks, rows
+// 64 j + 16 kind + r: a proj, a gate, b proj, b gate); w4t = w4^T [C][4C].
+template <class TZ, class TC, int C>
+__global__ __launch_bounds__(256) void trimul_project_vjp_kernel(const TC* __restrict__ dplanes,
+                                                                 const TZ* __restrict__ x,
+                                                                 const float* __restrict__ mask,
+                                                                 const TC* __restrict__ w4,
+                                                                 const TC* __restrict__ w4t,
+                                                                 const float* __restrict__ gx_in, int B, int N,
+                                                                 int Np, int outgoing, TC* __restrict__ gpg,
+                                                                 TZ* __restrict__ dx) {
+  constexpr int BM = vjp_bm<TC, C>();
+  constexpr int NT = 256;
+  constexpr int RB = BM / 16;
+  constexpr int CBW = C / 64;
+  constexpr int LDA = C + lds_pad<TC>();
+  constexpr int SLD = BM + lds_pad<TC>();
+  constexpr int GLD = 4 * C + lds_pad<TC>();
+  constexpr int VEC = 16 / sizeof(TC);
+  constexpr int A_BYTES = BM * LDA * (int)sizeof(TC);
+  constexpr int S_BYTES = 2 * C * SLD * (int)sizeof(TC);
+  constexpr int G_BYTES = BM * GLD * (int)sizeof(TC);
+  constexpr int SMEM = (A_BYTES + S_BYTES) > G_BYTES ? (A_BYTES + S_BYTES) : G_BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[SMEM];
+  __shared__ float mk[BM];
+  TC* A = reinterpret_cast<TC*>(smem);
+  TC* S = reinterpret_cast<TC*>(smem + A_BYTES);
+  TC* G = reinterpret_cast<TC*>(smem);
+
+  const int t0 = blockIdx.x * BM;
+  const int line = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const size_t pe = (size_t)Np * Np;
+  auto pos_of = [&](int p) -> long {
+    const int t = t0 + p;
+    if (line >= N || t >= N) return -1;
+    return outgoing ? (long)line * N + t : (long)t * N + line;
+  };
+  auto tok = [&](int p) -> long {
+    const long pos = pos_of(p);
+    return pos < 0 ? -1 : (long)b * N * N + pos;
+  };
+  copy_tile_to_lds<TZ, TC, C, BM, NT>(
+      [&](int p) -> const TZ* {
+        const long t = tok(p);
+        return t < 0 ? nullptr : x + t * C;
+      },
+      A, LDA);
+  if (tid < BM) {
+    const long t = tok(tid);
+    mk[tid] = t < 0 ? 0.f : mask[t];
+  }
+  {
+    // cotangents of this block's plane entries: rows (plane, channel) of BM positions
+    constexpr int CPR = BM / VEC;
+    for (int idx = tid; idx < 2 * C * CPR; idx += NT) {
+      const int row = idx / CPR;
+      const int ch = idx % CPR;
+      const int plane = row / C;
+      const int c = row % C;
+      const TC* src = dplanes + ((size_t)plane * B * C + (size_t)b * C + c) * pe + (size_t)line * Np + t0 + ch * VEC;
+      *reinterpret_cast<u32x4*>(S + row * SLD + ch * VEC) = *reinterpret_cast<const u32x4*>(src);
+    }
+  }
+  __syncthreads();
+
+  const int w = wave_id();
+  const int l = lane_id();
+  f32x4 acc[RB][4 * CBW];
+  zero_acc(acc);
+  int wrow0[4 * CBW];
+#pragma unroll
+  for (int j = 0; j < 4 * CBW; ++j) wrow0[j] = (w * CBW + j / 4) * 64 + (j % 4) * 16;
+  gemm16_lds_x_w<TC, C, RB, 4 * CBW>(acc, A, LDA, 0, w4, C, wrow0);
+
+  // G = (gp_a, gg_a, gp_b, gg_b) in place of (proj_a, gate_a, proj_b, gate_b)
+#pragma unroll
+  for (int cbi = 0; cbi < CBW; ++cbi) {
+    const int ch = (w * CBW + cbi) * 16 + (l & 15);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p = rb * 16 + 4 * (l >> 4) + r;
+        const float m = mk[p];
+        const float ga = to_f32(S[ch * SLD + p]) * m;
+        const float gb = to_f32(S[(C + ch) * SLD + p]) * m;
+        const float pa = acc[rb][4 * cbi + 0][r], sa = sigmoidf_(acc[rb][4 * cbi + 1][r]);
+        const float pb = acc[rb][4 * cbi + 2][r], sb = sigmoidf_(acc[rb][4 * cbi + 3][r]);
+        acc[rb][4 * cbi + 0][r] = ga * sa;
+        acc[rb][4 * cbi + 1][r] = ga * pa * sa * (1.f - sa);
+        acc[rb][4 * cbi + 2][r] = gb * sb;
+        acc[rb][4 * cbi + 3][r] = gb * pb * sb * (1.f - sb);
+      }
+  }
+  __syncthreads();  // A and S dead: G takes their place
+#pragma unroll
+  for (int j = 0; j < 4 * CBW; ++j)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p = rb * 16 + 4 * (l >> 4) + r;
+        G[p * GLD + wrow0[j] + (l & 15)] = from_f32<TC>(acc[rb][j][r]);
+      }
+  __syncthreads();
+  {
+    constexpr int CPR = 4 * C / VEC;
+    for (int idx = tid; idx < BM * CPR; idx += NT) {
+      const int p = idx / CPR;
+      const int ch = (idx % CPR) * VEC;
+      const long t = tok(p);
+      if (t < 0) continue;
+      *reinterpret_cast<u32x4*>(gpg + t * 4 * C + ch) = *reinterpret_cast<const u32x4*>(G + p * GLD + ch);
+    }
+  }
+
+  // dx = gx + G W4 (k = 4C)
+  f32x4 acc2[RB][CBW];
+  zero_acc(acc2);
+  int wrow1[CBW];
+#pragma unroll
+  for (int j = 0; j < CBW; ++j) wrow1[j] = (w * CBW + j) * 16;
+  gemm16_lds_x_w<TC, 4 * C, RB, CBW>(acc2, G, GLD, 0, w4t, 4 * C, wrow1);
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int jb = 0; jb < CBW; ++jb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p = rb * 16 + 4 * (l >> 4) + e;
+        const int c = wrow1[jb] + (l & 15);
+        const long t = tok(p);
+        if (t >= 0) dx[t * C + c] = from_f32<TZ>(gx_in[t * C + c] + acc2[rb][jb][e]);
+      }
+}
+
+template <class TC, int C>
+size_t out_vjp_partials(int B, int N) {
+  const int Np = pf::pad128(N);
+  return (size_t)B * Np * (Np / vjp_bm<TC, C>()) * 2 * C * sizeof(float);
+}
+
+template <class TZ, class TC, int C>
+int output_vjp_launch(const void* g, const void* X, const void* x, const float* lnow, const float* lnob, float eps,
+                      const void* wo, const void* wog, const void* wot, const void* wogt, int B, int N, void* gp,
+                      void* gg, void* xln, void* dX, float* gx, float* dlnw, float* dlnb, void* ws, hipStream_t s) {
+  const int Np = pf::pad128(N);
+  constexpr int BM = vjp_bm<TC, C>();
+  const dim3 grid(Np / BM, Np, B);
+  float* partial = static_cast<float*>(ws);
+  trimul_output_vjp_kernel<TZ, TC, C><<<grid, 256, 0, s>>>(
+      (const TZ*)g, (const TC*)X, (const TZ*)x, lnow, lnob, eps, (const TC*)wo, (const TC*)wog, (const TC*)wot,
+      (const TC*)wogt, B, N, Np, (TC*)gp, (TC*)gg, (TC*)xln, (TC*)dX, gx, partial);
+  if (int e = pf::check_launch("trimul_output_vjp")) return e;
+  const long nblk = (long)B * Np * (Np / BM);
+  trimul_ln_grad_reduce_kernel<<<2 * C, 256, 0, s>>>(partial, nblk, 2 * C, dlnw, dlnb);
+  return pf::check_launch("trimul_ln_grad_reduce");
+}
+
+template <class TZ, class TC, int C>
+int project_vjp_launch(const void* dplanes, const void* x, const float* mask, const void* w4, const void* w4t,
+                       const float* gx_in, int B, int N, int outgoing, void* gpg, void* dx, hipStream_t s) {
+  const int Np = pf::pad128(N);
+  constexpr int BM = vjp_bm<TC, C>();
+  trimul_project_vjp_kernel<TZ, TC, C><<<dim3(Np / BM, Np, B), 256, 0, s>>>(
+      (const TC*)dplanes, (const TZ*)x, mask, (const TC*)w4, (const TC*)w4t, gx_in, B, N, Np, outgoing, (TC*)gpg,
+      (TZ*)dx);
+  return pf::check_launch("trimul_project_vjp");
+}
+
+// Calls f(TZ{}, TC{}, std::integral_constant<int, C>{}) for the built (xdtype, cdtype, C).
+template <class F>
+int dispatch_vjp(int xdtype, int cdtype, int C, F&& f) {
+  auto by_c = [&](auto tz, auto tc) {
+    if (C == 64) return f(tz, tc, std::integral_constant<int, 64>{});
+    if (C == 256) return f(tz, tc, std::integral_constant<int, 256>{});
+    return f(tz, tc, std::integral_constant<int, 128>{});
+  };
+  if (xdtype == PF_F32 && cdtype == PF_F32) return by_c(float{}, float{});
+  if (xdtype == PF_F32) return by_c(float{}, bf16{});
+  return by_c(bf16{}, bf16{});
+}
+
+bool vjp_args_ok(int B, int N, int C, int xdtype, int cdtype) {
+  return B > 0 && N > 0 && (C == 64 || C == 128 || C == 256) && (xdtype == PF_F32 || xdtype == PF_BF16) &&
+         (cdtype == PF_F32 || cdtype == PF_BF16) && !(xdtype == PF_BF16 && cdtype == PF_F32) &&
+         (long)pf::pad128(N) * B <= 65535;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t pf_trimul_output_vjp_workspace_bytes(int B, int N, int C, int cdtype) {
+  if (B <= 0 || N <= 0 || (cdtype != PF_F32 && cdtype != PF_BF16)) return 0;
+  auto pick = [&](auto tc) -> size_t {
+    using TC = decltype(tc);
+    if (C == 64) return out_vjp_partials<TC, 64>(B, N);
+    if (C == 128) return out_vjp_partials<TC, 128>(B, N);
+    if (C == 256) return out_vjp_partials<TC, 256>(B, N);
+    return 0;
+  };
+  return cdtype == PF_F32 ? pick(float{}) : pick(bf16{});
+}
+
+int pf_trimul_output_vjp(const void* g, const void* X, const void* x, const float* ln_out_w, const float* ln_out_b,
+                         float eps_out, const void* w_out, const void* w_out_gate, const void* w_out_t,
+                         const void* w_out_gate_t, int B, int N, int C, int xdtype, int cdtype, void* gp, void* gg,
+                         void* xln, void* dX, float* gx, float* d_ln_out_w, float* d_ln_out_b, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(g && X && x && ln_out_w && ln_out_b && w_out && w_out_gate && w_out_t && w_out_gate_t && gp && gg &&
+                 xln && dX && gx && d_ln_out_w && d_ln_out_b && workspace,
+             PF_ERR_INVALID_ARG, "pf_trimul_output_vjp: null pointer");
+  PF_REQUIRE(vjp_args_ok(B, N, C, xdtype, cdtype), PF_ERR_UNSUPPORTED,
+             "pf_trimul_output_vjp: B=%d N=%d C=%d xdtype=%d cdtype=%d", B, N, C, xdtype, cdtype);
+  PF_REQUIRE(pf::aligned16(g) && pf::aligned16(X) && pf::aligned16(x) && pf::aligned16(gp) && pf::aligned16(gg) &&
+                 pf::aligned16(xln) && pf::aligned16(dX) && pf::aligned16(gx) && pf::aligned16(workspace),
+             PF_ERR_ALIGNMENT, "pf_trimul_output_vjp: pointers must be 16-byte aligned");
+  const size_t need = pf_trimul_output_vjp_workspace_bytes(B, N, C, cdtype);
+  PF_REQUIRE(workspace_bytes >= need, PF_ERR_WORKSPACE, "pf_trimul_output_vjp: workspace %zu < %zu bytes",
+             workspace_bytes, need);
+  hipStream_t s = pf::as_stream(stream);
+  return dispatch_vjp(xdtype, cdtype, C, [&](auto tz, auto tc, auto cc) {
+    using TZ = decltype(tz);
+    using TC = decltype(tc);
+    constexpr int CC = decltype(cc)::value;
+    return output_vjp_launch<TZ, TC, CC>(g, X, x, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate, w_out_t,
+                                         w_out_gate_t, B, N, gp, gg, xln, dX, gx, d_ln_out_w, d_ln_out_b, workspace,
+                                         s);
+  });
+}
+
+int pf_trimul_project_vjp(const void* dplanes, const void* x, const float* mask, const void* w_packed,
+                          const void* w_packed_t, const float* gx_in, int B, int N, int C, int outgoing, int xdtype,
+                          int cdtype, void* gpg, void* dx, void* stream) {
+  PF_REQUIRE(dplanes && x && mask && w_packed && w_packed_t && gx_in && gpg && dx, PF_ERR_INVALID_ARG,
+             "pf_trimul_project_vjp: null pointer");
+  PF_REQUIRE(vjp_args_ok(B, N, C, xdtype, cdtype), PF_ERR_UNSUPPORTED,
+             "pf_trimul_project_vjp: B=%d N=%d C=%d xdtype=%d cdtype=%d", B, N, C, xdtype, cdtype);
+  PF_REQUIRE(pf::aligned16(dplanes) && pf::aligned16(x) && pf::aligned16(gpg) && pf::aligned16(dx) &&
+                 pf::aligned16(w_packed) && pf::aligned16(w_packed_t),
+             PF_ERR_ALIGNMENT, "pf_trimul_project_vjp: pointers must be 16-byte aligned");
+  hipStream_t s = pf::as_stream(stream);
+  return dispatch_vjp(xdtype, cdtype, C, [&](auto tz, auto tc, auto cc) {
+    using TZ = decltype(tz);
+    using TC = decltype(tc);
+    constexpr int CC = decltype(cc)::value;
+    return project_vjp_launch<TZ, TC, CC>(dplanes, x, mask, w_packed, w_packed_t, gx_in, B, N, outgoing, gpg, dx, s);
+  });
+}
+
+}  // extern "C"

@@ -13,7 +13,7 @@ import weakref
 
 import torch
 
-from . import _lib
+from . import _lib, kernel_census
 from .inference_guard import NotActive, inference_only
 
 __all__ = [
@@ -214,6 +214,106 @@ def fused_trimul(
         z, mask, norm_in.weight, norm_in.bias, norm_in.eps, packed, norm_out.weight, norm_out.bias, norm_out.eps,
         cast_weight(w_out, cdt), cast_weight(w_out_gate, cdt), outgoing,
     )  # fmt: skip
+
+
+class FusedTriMulFunction(torch.autograd.Function):
+    """Trainable triangle multiply after the input LayerNorm (``FusedTriMulFunction``,
+    ``triton/fused_trimul.py:285-330``); same ``apply`` arguments.
+
+    ``apply(x, mask, w_gate, w_proj, ln_out_w, ln_out_b, w_out, w_out_gate, eps, outgoing)``:
+    x [B, N, N, C] is ``norm_left(z)`` (its LayerNorm stays in autograd), ``w_gate`` /
+    ``w_proj`` [2C, C] in block order (rows [a; b]). The forward runs the generic K1 and K3
+    without the input LayerNorm and K2, and keeps the planes and the contraction; the
+    backward runs ``pf_trimul_output_vjp``, the contraction's cotangents ``dP = dX Q``,
+    ``dQ = dX^T P`` and the weight gradients as library GEMMs, then ``pf_trimul_project_vjp``.
+    GEMM operands are bf16 for bf16 x or under bf16 autocast (the reference's regime), fp32
+    otherwise. Returns gradients for x, w_gate, w_proj, ln_out_w, ln_out_b, w_out, w_out_gate.
+    """
+
+    @staticmethod
+    def forward(ctx, x, mask, w_gate, w_proj, ln_out_w, ln_out_b, w_out, w_out_gate, eps, outgoing):
+        _lib.require_device("FusedTriMulFunction", x, mask)
+        if x.dim() != 4 or x.shape[1] != x.shape[2]:
+            raise NotActive("FusedTriMulFunction", f"x must be [B, N, N, C], got {tuple(x.shape)}")
+        B, N, _, C = x.shape
+        if C not in TRIMUL_CHANNELS:
+            raise NotActive("FusedTriMulFunction", f"C={C}: built for C in {TRIMUL_CHANNELS}")
+        cdt = gemm_dtype_for(x)
+        xc = x.detach().contiguous()
+        if xc.dtype not in (torch.float32, torch.bfloat16) or (xc.dtype == torch.bfloat16 and cdt == torch.float32):
+            raise NotActive("FusedTriMulFunction", f"x dtype {xc.dtype}")
+        m = mask.detach().to(torch.float32).contiguous()
+        wp, wg = w_proj.detach().contiguous(), w_gate.detach().to(w_proj.dtype).contiguous()
+        w4 = torch.empty((4 * C, C), dtype=cdt, device=x.device)
+        _lib.call(
+            "pf_trimul_train_pack_weights", wp.data_ptr(), wg.data_ptr(), _lib.dtype_code(wp.dtype), w4.data_ptr(), C,
+            _lib.dtype_code(cdt), _lib.stream_of(xc),
+        )  # fmt: skip
+        wo, wog = cast_weight(w_out, cdt), cast_weight(w_out_gate, cdt)
+        lnow, lnob = _f32(ln_out_w), _f32(ln_out_b)
+        nbytes = _lib.lib().pf_trimul_workspace_bytes(B, N, C, _lib.dtype_code(cdt))
+        planes = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        out = torch.empty_like(xc)
+        kernel_census.record("TriangleMul", "hip_trimul_grad")
+        _lib.call(
+            "pf_trimul_train_fwd", xc.data_ptr(), m.data_ptr(), w4.data_ptr(), lnow.data_ptr(), lnob.data_ptr(),
+            float(eps), wo.data_ptr(), wog.data_ptr(), B, N, C, int(bool(outgoing)), _lib.dtype_code(xc.dtype),
+            _lib.dtype_code(cdt), planes.data_ptr(), nbytes, out.data_ptr(), _lib.stream_of(xc),
+        )  # fmt: skip
+        ctx.save_for_backward(xc, m, planes, w4, wo, wog, lnow, lnob)
+        ctx.eps, ctx.outgoing, ctx.cdt = float(eps), bool(outgoing), cdt
+        ctx.dtypes = (x.dtype, w_gate.dtype, w_proj.dtype, ln_out_w.dtype, ln_out_b.dtype, w_out.dtype, w_out_gate.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        xc, m, planes, w4, wo, wog, lnow, lnob = ctx.saved_tensors
+        cdt = ctx.cdt
+        B, N, _, C = xc.shape
+        Np = -(-N // 128) * 128
+        M = B * N * N
+        dev = xc.device
+        code_x, code_c = _lib.dtype_code(xc.dtype), _lib.dtype_code(cdt)
+        stream = _lib.stream_of(xc)
+        g = g.to(xc.dtype).contiguous()
+        kernel_census.record("TriangleMul.backward", "hip_trimul_vjp")
+        pl = planes.view(cdt).view(3, B * C, Np, Np)
+        gp, gg, xln = (torch.empty((M, C), dtype=cdt, device=dev) for _ in range(3))
+        dX = torch.empty((B * C, Np, Np), dtype=cdt, device=dev)
+        gx = torch.empty((M, C), dtype=torch.float32, device=dev)
+        dlnw, dlnb = (torch.empty(C, dtype=torch.float32, device=dev) for _ in range(2))
+        ws_bytes = _lib.lib().pf_trimul_output_vjp_workspace_bytes(B, N, C, code_c)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        wot, wogt = wo.t().contiguous(), wog.t().contiguous()
+        _lib.call(
+            "pf_trimul_output_vjp", g.data_ptr(), pl[2].data_ptr(), xc.data_ptr(), lnow.data_ptr(), lnob.data_ptr(),
+            ctx.eps, wo.data_ptr(), wog.data_ptr(), wot.data_ptr(), wogt.data_ptr(), B, N, C, code_x, code_c,
+            gp.data_ptr(), gg.data_ptr(), xln.data_ptr(), dX.data_ptr(), gx.data_ptr(), dlnw.data_ptr(),
+            dlnb.data_ptr(), ws.data_ptr(), ws_bytes, stream,
+        )  # fmt: skip
+        xb = xc.reshape(M, C).to(cdt)
+        d_out = torch.mm(gp.t(), xln).float()
+        d_out_gate = torch.mm(gg.t(), xb).float()
+        del gp, gg, xln
+        # X = P Q^T per channel plane: dP = dX Q, dQ = dX^T P (contiguous operands)
+        dpl = torch.empty((2, B * C, Np, Np), dtype=cdt, device=dev)
+        torch.bmm(dX, pl[1], out=dpl[0])
+        torch.bmm(dX.transpose(1, 2).contiguous(), pl[0], out=dpl[1])
+        del dX
+        gpg = torch.empty((M, 4 * C), dtype=cdt, device=dev)
+        dx = torch.empty_like(xc)
+        w4t = w4.t().contiguous()
+        _lib.call(
+            "pf_trimul_project_vjp", dpl.data_ptr(), xc.data_ptr(), m.data_ptr(), w4.data_ptr(), w4t.data_ptr(),
+            gx.data_ptr(), B, N, C, int(ctx.outgoing), code_x, code_c, gpg.data_ptr(), dx.data_ptr(), stream,
+        )  # fmt: skip
+        del dpl, gx
+        dw4 = torch.mm(gpg.t(), xb).float().view(C // 16, 4, 16, C)  # packed rows 64 j + 16 kind + r
+        d_proj = torch.cat([dw4[:, 0].reshape(C, C), dw4[:, 2].reshape(C, C)])
+        d_gate = torch.cat([dw4[:, 1].reshape(C, C), dw4[:, 3].reshape(C, C)])
+        dt = ctx.dtypes
+        return (dx.to(dt[0]), None, d_gate.to(dt[1]), d_proj.to(dt[2]), dlnw.to(dt[3]), dlnb.to(dt[4]),
+                d_out.to(dt[5]), d_out_gate.to(dt[6]), None, None)  # fmt: skip
 
 
 # ---------------------------------------------------------------- triangle attention

@@ -4,7 +4,8 @@
 parameters, state-dict keys and ``forward(z, mask)`` signature
 (``src/deepfold3/model/ops.py:179-231``, ``:645-680``); the forward is the
 three-launch HIP triangle multiply (K1 project, K2 per-channel MFMA GEMM, K3
-output), see ``csrc/trimul.hip``. Multi-head routed (MHR) variants are not built
+output), see ``csrc/trimul.hip``; under grad, ``FusedTriMulFunction`` with the VJP
+kernels of ``csrc/trimul_bwd.hip``. Multi-head routed (MHR) variants are not built
 and refuse at construction.
 """
 
@@ -12,11 +13,19 @@ from __future__ import annotations
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import kernel_census
 from .config import OptimConfig, require_hip
 from .inference_guard import NotActive, inference_only
-from .kernels import cast_weight, gemm_dtype_for, pack_trimul_weights, scaled_weight, trimul_forward
+from .kernels import (
+    FusedTriMulFunction,
+    cast_weight,
+    gemm_dtype_for,
+    pack_trimul_weights,
+    scaled_weight,
+    trimul_forward,
+)
 from .primitives import LayerNorm, LinearNoBias, WeightCache
 
 
@@ -78,13 +87,29 @@ class _TriangleMulBase(nn.Module):
             self.norm_center.eps, op["w_out"], op["w_out_gate"], self._outgoing, out=out, accumulate=accumulate,
         )  # fmt: skip
 
-    @inference_only("TriangleMul")
+    def _forward_grad(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """Training path (``ops.py:375-388``): ``norm_left`` in autograd (fp32 statistics, cast
+        back), then the HIP ``FusedTriMulFunction`` with its VJP kernels."""
+        C = z.shape[-1]
+        nl = self.norm_left
+        x = F.layer_norm(z.float(), (C,), nl.weight.float(), nl.bias.float(), nl.eps).to(z.dtype)
+        order = self._block_order.to(z.device)
+        w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
+        return FusedTriMulFunction.apply(
+            x.contiguous(), mask, self.gate.weight[order], self.proj.weight[order], self.norm_center.weight,
+            self.norm_center.bias, w_out, self.out_gate.weight, self.norm_center.eps, self._outgoing,
+        )  # fmt: skip
+
     def forward(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
-        """The update for z [B?, N, N, C] and mask [B?, N, N] (not added to z)."""
+        """The update for z [B?, N, N, C] and mask [B?, N, N] (not added to z). Under grad it
+        runs the differentiable path (``FusedTriMulFunction``), else the inference kernels."""
         has_batch = z.dim() == 4
         if not has_batch:
             z, mask = z.unsqueeze(0), mask.unsqueeze(0)
-        out = self._run(z, mask, None, False)
+        if torch.is_grad_enabled():
+            out = self._forward_grad(z, mask)
+        else:
+            out = self._run(z, mask, None, False)
         return out if has_batch else out.squeeze(0)
 
     @inference_only("TriangleMul")

@@ -99,6 +99,47 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
                   const void* w_out, const void* w_out_gate, int B, int N, int C, int outgoing, int zdtype, int cdtype,
                   void* out, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Training: FusedTriMulFunction (triton/fused_trimul.py:285-330), the triangle multiply
+ * after its input LayerNorm, with a backward.
+ *
+ * pf_trimul_train_pack_weights: as pf_trimul_pack_weights, in the layout the training
+ * kernels read (16-channel blocks, rows 64 j + 16 kind + r; kind 0 a proj, 1 a gate,
+ * 2 b proj, 3 b gate) for every C and cdtype.
+ *
+ * pf_trimul_train_fwd: x [B,N,N,C] (xdtype) is the input LayerNorm's output; writes the
+ * update to `out` (xdtype) and keeps the planes P, Q and the contraction X, channel-major
+ * [B*C][Np][Np] each (cdtype, Np = N rounded up to 128, zero at padding), in `planes`
+ * (pf_trimul_workspace_bytes(B, N, C, cdtype) bytes) for the backward.
+ *
+ * pf_trimul_output_vjp (_output_vjp_kernel, fused_trimul.py:153-212): with g the update's
+ * cotangent [B,N,N,C] (xdtype), X from `planes` and w_out_t, w_out_gate_t the transposed
+ * [C,C] weights, writes gp = g s, gg = g p s (1 - s) and xln = LN_out(X) token-major
+ * [B*N*N, C] (cdtype), dX the cotangent of X (channel-major like X, zero at padding),
+ * gx = gg Wog [B*N*N, C] fp32 and the LN_out affine gradients [C] fp32 (summed in a fixed
+ * order). The host then forms dP = dX Q, dQ = dX^T P and the weight gradients
+ * (w_out: gp^T xln, w_out_gate: gg^T x).
+ *
+ * pf_trimul_project_vjp (_project_vjp_kernel, fused_trimul.py:214-262): dplanes = [dP; dQ]
+ * (two [B*C][Np][Np] cdtype sets), w_packed from pf_trimul_train_pack_weights and
+ * w_packed_t its [C, 4C] transpose; writes G = (gp_a, gg_a, gp_b, gg_b) token-major
+ * [B*N*N, 4C] in the packed row order (the packed weights' gradient is G^T x) and
+ * dx = gx_in + G W4 [B*N*N, C] (xdtype). C = 64, 128 or 256. */
+int pf_trimul_train_pack_weights(const void* w_proj, const void* w_gate, int wdtype, void* packed, int C, int cdtype,
+                                 void* stream);
+int pf_trimul_train_fwd(const void* x, const float* mask, const void* w_packed, const float* ln_out_w,
+                        const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate, int B, int N,
+                        int C, int outgoing, int xdtype, int cdtype, void* planes, size_t planes_bytes, void* out,
+                        void* stream);
+size_t pf_trimul_output_vjp_workspace_bytes(int B, int N, int C, int cdtype);
+int pf_trimul_output_vjp(const void* g, const void* X, const void* x, const float* ln_out_w, const float* ln_out_b,
+                         float eps_out, const void* w_out, const void* w_out_gate, const void* w_out_t,
+                         const void* w_out_gate_t, int B, int N, int C, int xdtype, int cdtype, void* gp, void* gg,
+                         void* xln, void* dX, float* gx, float* d_ln_out_w, float* d_ln_out_b, void* workspace,
+                         size_t workspace_bytes, void* stream);
+int pf_trimul_project_vjp(const void* dplanes, const void* x, const float* mask, const void* w_packed,
+                          const void* w_packed_t, const float* gx_in, int B, int N, int C, int outgoing, int xdtype,
+                          int cdtype, void* gpg, void* dx, void* stream);
+
 
 /* ---- triangle attention (starting / ending node) ------------------------ */
 /* Whole-module GridSelfAttention forward: replaces GridSelfAttention.forward

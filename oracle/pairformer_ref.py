@@ -32,6 +32,9 @@ Pinning (what checks this restatement, beyond retyping it):
   * kernel-level attention and its backward: a per-row loop for the forward; the centred
     backward equals autograd of the forward in fp64 and finite differences
     (``torch.autograd.gradcheck``); the centring constant sums to the uncentred D.
+  * the triangle multiply after its input LayerNorm (``tri_mul_core``): composing it with
+    the LayerNorm and the block-order weights gives ``tri_mul`` (pinned by the golden
+    vectors); its gradient by finite differences.
 """
 
 from __future__ import annotations
@@ -56,6 +59,7 @@ __all__ = [
     "evoformer_block",
     "evo_attention",
     "evo_attention_backward",
+    "tri_mul_core",
 ]
 
 
@@ -471,3 +475,30 @@ def evo_attention_backward(
     dK = torch.matmul(dS.transpose(-1, -2).contiguous(), Q) * scale
     dV = torch.matmul(P.transpose(-1, -2).contiguous(), dO)
     return dQ, dK, dV, dS.sum(dim=1, keepdim=True)
+
+
+def tri_mul_core(
+    x: torch.Tensor,
+    mask: torch.Tensor,
+    w_gate: torch.Tensor,
+    w_proj: torch.Tensor,
+    ln_out_w: torch.Tensor,
+    ln_out_b: torch.Tensor,
+    w_out: torch.Tensor,
+    w_out_gate: torch.Tensor,
+    eps: float,
+    outgoing: bool,
+) -> torch.Tensor:
+    """``FusedTriMulFunction.forward`` (``triton/fused_trimul.py:285-296``, kernels ``:64-151``,
+    ``:264-281``): x = norm_left(z) given; ``w_gate``, ``w_proj`` [2C, C] in block order
+    (rows [a; b]); a | b = sigmoid(x Wg^T) (x Wp^T) mask; X_ij = sum_k a_ik b_jk (outgoing) or
+    sum_k a_ki b_kj (incoming); out = sigmoid(x Wog^T) (LN(X) Wo^T). Differentiable."""
+    C = x.shape[-1]
+    ab = torch.sigmoid(F.linear(x, w_gate)) * F.linear(x, w_proj) * mask.unsqueeze(-1)
+    a, b = ab[..., :C], ab[..., C:]
+    if outgoing:
+        X = torch.einsum("bikc,bjkc->bijc", a, b)
+    else:
+        X = torch.einsum("bkic,bkjc->bijc", a, b)
+    xln = F.layer_norm(X, (C,), ln_out_w, ln_out_b, eps)
+    return torch.sigmoid(F.linear(x, w_out_gate)) * F.linear(xln, w_out)

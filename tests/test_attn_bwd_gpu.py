@@ -155,3 +155,78 @@ def test_attn_backward_refuses_stock_rule(dev):
     q = Q.to(dev).requires_grad_(True)
     with pytest.raises(NotActive, match="masked-row rule"):
         fused._EvoformerAttention.apply(q, K.to(dev), V.to(dev), rm.to(dev), pb.to(dev), True, "eager")
+
+
+def _grid_module(transpose, c=128, heads=4, seed=7):
+    W = mod("weights")
+    attention = mod("attention")
+    prefix = "pair_attn_col." if transpose else "pair_attn_row."
+    p = {k[len(prefix):]: v for k, v in W.make_block_weights(seed, perturb_affine=True, c_pair=c,
+                                                            num_pair_heads=heads).items() if k.startswith(prefix)}  # fmt: skip
+    m = attention.GridSelfAttention(c, heads, transpose=transpose)
+    m.load_state_dict(p)
+    return m, p
+
+
+def _grid_oracle_grads(p, z, mask, weight, transpose, autocast, dtype=torch.float32):
+    leaves = {k: v.to(dtype).clone().requires_grad_(True) for k, v in p.items()}
+    zz = z.to(dtype).clone().requires_grad_(True)
+    with torch.autocast("cpu", dtype=BF, enabled=autocast):
+        out = R.grid_attention(zz, mask.to(dtype), leaves, transpose)
+    (out.to(dtype) * weight.to(dtype)).sum().backward()
+    return {"z": zz.grad.float(), **{k: t.grad.float() for k, t in leaves.items()}}
+
+
+def _pair_mask(B, N, seed):
+    g = torch.Generator().manual_seed(seed)
+    m = (torch.rand(B, N, N, generator=g) > 0.1).float()
+    m[:, :, 0] = 1.0  # no fully masked line (the training kernel's rule and the stock rule differ there)
+    m[:, 0, :] = 1.0
+    return m
+
+
+@pytest.mark.parametrize("transpose", [False, True], ids=["rows", "cols"])
+def test_grid_attention_module_backward_fp32(dev, transpose):
+    """GridSelfAttention under grad (attention.py:211-257 with the fused op) against the stock
+    module differentiated in fp64: every gradient at 1e-5."""
+    m, p = _grid_module(transpose)
+    N = 45
+    g = torch.Generator().manual_seed(8)
+    z = torch.randn(1, N, N, 128, generator=g)
+    mask = _pair_mask(1, N, 9)
+    weight = torch.randn(z.shape, generator=g)
+    want = _grid_oracle_grads(p, z, mask, weight, transpose, False, torch.float64)
+    m = m.to(dev)
+    x = z.to(dev).requires_grad_(True)
+    out = m(x, mask.to(dev))
+    (out * weight.to(dev)).sum().backward()
+    got = {"z": x.grad.cpu(), **{k: t.grad.cpu() for k, t in m.named_parameters()}}
+    for k, ref in want.items():
+        assert_fp32_close(got[k], ref, what=f"grid attention d{k}")
+
+
+@pytest.mark.parametrize("transpose", [False, True], ids=["rows", "cols"])
+def test_grid_attention_module_backward_bf16(dev, transpose):
+    """Under bf16 autocast (the reference's training regime): each gradient within 3x the
+    stock path's bf16 error (+1e-3), as tests/triton/test_fused_trimul.py:87-106 gates the
+    fused trimul; stock references on the CPU."""
+    m, p = _grid_module(transpose, seed=10)
+    B, N = 1, 96
+    g = torch.Generator().manual_seed(11)
+    z = torch.randn(B, N, N, 128, generator=g)
+    mask = _pair_mask(B, N, 12)
+    weight = torch.randn(z.shape, generator=g)
+    ref32 = _grid_oracle_grads(p, z, mask, weight, transpose, False)
+    ref16 = _grid_oracle_grads(p, z, mask, weight, transpose, True)
+    m = m.to(dev)
+    x = z.to(dev).requires_grad_(True)
+    with torch.autocast("cuda", dtype=BF):
+        out = m(x, mask.to(dev))
+    (out.float() * weight.to(dev)).sum().backward()
+    got = {"z": x.grad.float().cpu(), **{k: t.grad.float().cpu() for k, t in m.named_parameters()}}
+    from tests._helpers import rel_l2
+
+    for k, ref in ref32.items():
+        e_hip, e_stock = rel_l2(got[k], ref), rel_l2(ref16[k], ref)
+        print(f"  {k}: hip {e_hip:.2e} stock-bf16 {e_stock:.2e}", flush=True)
+        assert e_hip < 3 * e_stock + 1e-3, k

@@ -596,3 +596,43 @@ def test_evo_attention_centring_identity():
     dS_plain = P * (dP - Dv)
     got = R.evo_attention_backward(Q, K, V, rm, pb, dO)
     assert torch.allclose(got[3], dS_plain.sum(1, keepdim=True), rtol=1e-10, atol=1e-13)
+
+
+def _block_order(C: int, outgoing: bool) -> torch.Tensor:
+    even, odd = torch.arange(0, 2 * C, 2), torch.arange(1, 2 * C, 2)
+    return torch.cat((even, odd)) if outgoing else torch.cat((odd, even))
+
+
+@pytest.mark.parametrize("outgoing", [True, False], ids=["out", "in"])
+def test_tri_mul_core_composes_to_tri_mul(outgoing):
+    """fused_trimul.py:285-296 after ops.py:380-386: norm_left in front and the block-order
+    rows (ops.py:285-288) give the stock triangle multiply (pinned by the golden vectors)."""
+    prefix = "tri_mul_out." if outgoing else "tri_mul_in."
+    p = {k: v.double() for k, v in sub(W.make_block_weights(21, perturb_affine=True), prefix).items()}
+    x = W.make_inputs(11, seed=22, pad_last=2)
+    z, mask = x["pair"].double(), x["pair_mask"].double()
+    want = R.tri_mul(z, mask, p, outgoing)
+    order = _block_order(128, outgoing)
+    xn = F.layer_norm(z, (128,), p["norm_left.weight"], p["norm_left.bias"], 1e-5)
+    got = R.tri_mul_core(xn, mask, p["gate.weight"][order], p["proj.weight"][order], p["norm_center.weight"],
+                         p["norm_center.bias"], p["out_proj.weight"], p["out_gate.weight"], 1e-5, outgoing)  # fmt: skip
+    # tri_mul's LayerNorms run in fp32 (primitives.py:110-115): agreement to fp32 rounding
+    assert (got - want).abs().max() <= 1e-5 * want.abs().max()
+    swapped = R.tri_mul_core(xn, mask, p["gate.weight"][order], p["proj.weight"][order], p["norm_center.weight"],
+                             p["norm_center.bias"], p["out_proj.weight"], p["out_gate.weight"], 1e-5, not outgoing)
+    assert (swapped - want).abs().max() > 1e-2 * want.abs().max()  # the direction matters
+
+
+@pytest.mark.parametrize("outgoing", [True, False], ids=["out", "in"])
+def test_tri_mul_core_gradcheck(outgoing):
+    g = torch.Generator().manual_seed(23)
+    B, N, C = 1, 4, 4
+    r = lambda *s: torch.randn(*s, generator=g, dtype=torch.float64)  # noqa: E731
+    mask = (torch.rand(B, N, N, generator=g) > 0.2).double()
+    leaves = [r(B, N, N, C), r(2 * C, C), r(2 * C, C), 1 + 0.1 * r(C), 0.1 * r(C), r(C, C), r(C, C)]
+    leaves = [t.requires_grad_(True) for t in leaves]
+
+    def f(x, wg, wp, lw, lb, wo, wog):
+        return R.tri_mul_core(x, mask, wg, wp, lw, lb, wo, wog, 1e-5, outgoing)
+
+    assert torch.autograd.gradcheck(f, leaves, eps=1e-6, atol=1e-6)

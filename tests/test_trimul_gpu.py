@@ -112,7 +112,13 @@ def test_fused_trimul_functional_api(dev):
 
 
 def test_grad_enabled_is_refused(dev):
+    """The inference entries refuse grad (fused_trimul.py:332 is inference-only); the module's
+    forward under grad takes the differentiable path instead (tests/test_trimul_bwd_gpu.py)."""
     m = _module(True, sub(W.make_block_weights(1), "tri_mul_out."), dev)
     err = mod("inference_guard").InferenceOnlyKernelError
+    z, mask = torch.randn(1, 8, 8, 128, device=dev), torch.ones(1, 8, 8, device=dev)
     with pytest.raises(err):
-        m(torch.randn(1, 8, 8, 128, device=dev), torch.ones(1, 8, 8, device=dev))
+        m.forward_residual_(z, mask)
+    with pytest.raises(err):
+        kernels.fused_trimul(z, mask, True, m.norm_left, m.gate.weight, m.proj.weight, m.norm_center,
+                             m.out_proj.weight, m.out_gate.weight)  # fmt: skip
