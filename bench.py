@@ -163,6 +163,74 @@ def kernel_figures(_lib, W, ops, attention, kernels, dev) -> list[dict]:
     return out
 
 
+def training_figures(ops, fused, dev, iters: int = 5) -> list[dict]:
+    """Forward and backward of the two differentiable paths at the trunk's shape (N=768,
+    bf16): the fused attention op over 768 lines of 4 heads, and the triangle multiply
+    module (outgoing) under grad. Times from CUDA events on torch's stream, which the
+    library launches on; medians over ``iters``."""
+    import torch
+
+    out = []
+
+    def median_ms(fn) -> float:
+        ts = []
+        for _ in range(iters + 1):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return sorted(ts[1:])[len(ts[1:]) // 2]
+
+    n, S, H, D = 768, 768, 4, 32
+    g = torch.Generator().manual_seed(6)
+    q, k, v = ((torch.randn(1, S, H, n, D, generator=g) * D**-0.5).to(dev, torch.bfloat16).requires_grad_(True)
+               for _ in range(3))  # fmt: skip
+    pb = torch.randn(1, 1, H, n, n, generator=g).to(dev).requires_grad_(True)
+    rm = torch.zeros(1, S, 1, 1, n, device=dev)
+    do = torch.randn(1, S, H, n, D, generator=g).to(dev, torch.bfloat16)
+    state = {}
+
+    def attn_fwd():
+        state["o"] = fused._EvoformerAttention.apply(q, k, v, rm, pb, True)
+
+    def attn_bwd():
+        torch.autograd.grad(state["o"], [q, k, v, pb], grad_outputs=do, retain_graph=True)
+
+    fwd_ms = median_ms(attn_fwd)
+    bwd_ms = median_ms(attn_bwd)
+    flops = 5 * 2.0 * n * n * D * S * H  # recomputed QK^T, dV, dP, dQ, dK
+    rate = flops / (bwd_ms * 1e-3) / 1e12
+    out.append({"op": "evo_attention backward", "config": "B=1 S=768 H=4 N=768 D=32 bf16", "fwd_ms": round(fwd_ms, 3),
+                "bwd_ms": round(bwd_ms, 3), "flops": flops, "achieved": round(rate, 1), "unit": "TFLOP/s",
+                "peak": MFMA_BF16_PEAK_TFLOPS, "frac": round(rate / MFMA_BF16_PEAK_TFLOPS, 4)})  # fmt: skip
+    log(f"evo attention N={n}: fwd {fwd_ms:.3f} ms, bwd {bwd_ms:.3f} ms ({rate:.1f} TFLOP/s)")
+    del q, k, v, pb, do, state["o"]
+    torch.cuda.empty_cache()
+
+    m = ops.TriangleMulOutgoing(128).to(dev).to(torch.bfloat16)
+    for p in m.parameters():
+        with torch.no_grad():
+            p.copy_(torch.randn(p.shape, generator=g).to(p) / 128**0.5 if p.dim() == 2 else p)
+    z = torch.randn(1, n, n, 128, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
+    mask = torch.ones(1, n, n, device=dev)
+    gz = torch.randn(1, n, n, 128, generator=g).to(dev, torch.bfloat16)
+
+    def tm_fwd():
+        state["u"] = m(z, mask)
+
+    def tm_bwd():
+        torch.autograd.grad(state["u"], [z] + list(m.parameters()), grad_outputs=gz, retain_graph=True)
+
+    fwd_ms = median_ms(tm_fwd)
+    bwd_ms = median_ms(tm_bwd)
+    out.append({"op": "TriangleMulOutgoing backward", "config": "B=1 N=768 C=128 bf16", "fwd_ms": round(fwd_ms, 3),
+                "bwd_ms": round(bwd_ms, 3)})  # fmt: skip
+    log(f"triangle multiply N={n}: fwd {fwd_ms:.3f} ms, bwd {bwd_ms:.3f} ms")
+    return out
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -290,6 +358,10 @@ def main() -> int:
         "--kernels-only", action="store_true",
         help="run only the per-kernel figures (no trunk) and print them as one JSON line, for profiling",
     )  # fmt: skip
+    ap.add_argument(
+        "--training", action="store_true",
+        help="run only the training-path figures (forward and backward at N=768) as one JSON line",
+    )  # fmt: skip
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -328,6 +400,11 @@ def main() -> int:
         buf.clone()
         torch.cuda.synchronize()
         del buf
+
+    if args.training:
+        fused = import_module("deepfold3_dev_amd.fused")
+        print(json.dumps({"training": training_figures(ops, fused, dev)}), flush=True)
+        return 0
 
     if args.kernels_only:
         if args.calibration_copy:

@@ -7,13 +7,14 @@
 //   trimul_output_vjp:  per (line, 64 plane positions): recompute LN_out(X) and both output
 //                       GEMMs, gp = g s, gg = g p s (1 - s); d(xln) = gp Wo, pulled through
 //                       LN_out into dX (channel-major planes, zero at padding); the output
-//                       gate's x cotangent gg Wog (fp32); gp, gg and xln token-major for the
-//                       weight gradients; per-block partial sums of the LN_out affine
-//                       gradients, reduced in a fixed order by trimul_ln_grad_reduce.
+//                       gate's x cotangent gg Wog (fp32); gp, gg channel-major and xln
+//                       token-major for the weight gradients; per-block partial sums of the
+//                       LN_out affine gradients, reduced in a fixed order by
+//                       trimul_ln_grad_reduce.
 //   (host)              dP = dX Q, dQ = dX^T P, weight gradients: plain library GEMMs.
 //   trimul_project_vjp: per (line, plane positions) as the forward K1: recompute both gated
 //                       projections, G = (gp_a, gg_a, gp_b, gg_b) in the packed weight order,
-//                       dx = gx + G W4 (W4 the packed [4C][C] weights), G token-major.
+//                       dx = gx + G W4 (W4 the packed [4C][C] weights), G channel-major.
 //
 // The LN_out pullback with xn the standardised X and u = d(xln) * ln_w is
 // rstd (u - mean_c(u) - xn mean_c(u xn)) (fused_trimul.py:166-171).
@@ -39,6 +40,7 @@ __global__ __launch_bounds__(256) void trimul_output_vjp_kernel(
     const TC* __restrict__ WoT, const TC* __restrict__ WogT, int B, int N, int Np, TC* __restrict__ gp_out,
     TC* __restrict__ gg_out, TC* __restrict__ xln_out, TC* __restrict__ dX, float* __restrict__ gx,
     float* __restrict__ partial) {
+  const size_t M = (size_t)B * N * N;
   constexpr int BM = vjp_bm<TC, C>();
   constexpr int NT = 256;
   constexpr int RB = BM / 16;
@@ -157,16 +159,14 @@ __global__ __launch_bounds__(256) void trimul_output_vjp_kernel(
         A2[p * ALD + c] = from_f32<TC>(gv * accp[rb][jb][e] * sv * (1.f - sv));
       }
   __syncthreads();
-  {
-    constexpr int CPR = C / VEC;
-    for (int idx = tid; idx < BM * CPR; idx += NT) {
-      const int p = idx / CPR;
-      const int ch = (idx % CPR) * VEC;
-      const long t = tok(p);
-      if (t < 0) continue;
-      *reinterpret_cast<u32x4*>(gp_out + t * C + ch) = *reinterpret_cast<const u32x4*>(A1 + p * ALD + ch);
-      *reinterpret_cast<u32x4*>(gg_out + t * C + ch) = *reinterpret_cast<const u32x4*>(A2 + p * ALD + ch);
-    }
+  // gp, gg channel-major [C][M] (rows of contiguous tokens) for the weight-gradient GEMMs
+  for (int idx = tid; idx < BM * C; idx += NT) {
+    const int c = idx / BM;
+    const int p = idx % BM;
+    const long t = tok(p);
+    if (t < 0) continue;
+    gp_out[(size_t)c * M + t] = A1[p * ALD + c];
+    gg_out[(size_t)c * M + t] = A2[p * ALD + c];
   }
 
   // d(xln) = gp Wo, the output gate's x cotangent gg Wog
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256) void trimul_project_vjp_kernel(const TC* __res
                                                                  const TC* __restrict__ w4t,
                                                                  const float* __restrict__ gx_in, int B, int N,
                                                                  int Np, int outgoing, TC* __restrict__ gpg,
-                                                                 TZ* __restrict__ dx) {
+                                                                 TC* __restrict__ xw, TZ* __restrict__ dx) {
   constexpr int BM = vjp_bm<TC, C>();
   constexpr int NT = 256;
   constexpr int RB = BM / 16;
@@ -323,6 +323,17 @@ __global__ __launch_bounds__(256) void trimul_project_vjp_kernel(const TC* __res
   if (tid < BM) {
     const long t = tok(tid);
     mk[tid] = t < 0 ? 0.f : mask[t];
+  }
+  if (!outgoing) {
+    __syncthreads();
+    constexpr int CPR = C / VEC;
+    for (int idx = tid; idx < BM * CPR; idx += NT) {
+      const int p = idx / CPR;
+      const int ch = (idx % CPR) * VEC;
+      if (line >= N || t0 + p >= N) continue;
+      *reinterpret_cast<u32x4*>(xw + (((size_t)b * N + line) * N + t0 + p) * C + ch) =
+          *reinterpret_cast<const u32x4*>(A + p * LDA + ch);
+    }
   }
   {
     // cotangents of this block's plane entries: rows (plane, channel) of BM positions
@@ -378,14 +389,17 @@ __global__ __launch_bounds__(256) void trimul_project_vjp_kernel(const TC* __res
         G[p * GLD + wrow0[j] + (l & 15)] = from_f32<TC>(acc[rb][j][r]);
       }
   __syncthreads();
+  // G channel-major [4C][M] in this kernel's walk order (position (line, t) at
+  // b N^2 + line N + t): rows of contiguous positions. For the outgoing direction that is the
+  // token order; for the incoming one x is written in the same order (xw, before the tile is
+  // reused), so that the packed weights' gradient G xw needs no transposed copy.
   {
-    constexpr int CPR = 4 * C / VEC;
-    for (int idx = tid; idx < BM * CPR; idx += NT) {
-      const int p = idx / CPR;
-      const int ch = (idx % CPR) * VEC;
-      const long t = tok(p);
-      if (t < 0) continue;
-      *reinterpret_cast<u32x4*>(gpg + t * 4 * C + ch) = *reinterpret_cast<const u32x4*>(G + p * GLD + ch);
+    const size_t M = (size_t)B * N * N;
+    for (int idx = tid; idx < BM * 4 * C; idx += NT) {
+      const int k = idx / BM;
+      const int p = idx % BM;
+      if (line >= N || t0 + p >= N) continue;
+      gpg[(size_t)k * M + ((size_t)b * N + line) * N + t0 + p] = G[p * GLD + k];
     }
   }
 
@@ -407,6 +421,24 @@ __global__ __launch_bounds__(256) void trimul_project_vjp_kernel(const TC* __res
         const long t = tok(p);
         if (t >= 0) dx[t * C + c] = from_f32<TZ>(gx_in[t * C + c] + acc2[rb][jb][e]);
       }
+}
+
+// dst[g] = src[g]^T for G planes of [Np][Np] (64 x 64 tiles through LDS).
+template <class T>
+__global__ __launch_bounds__(256) void plane_transpose_kernel(const T* __restrict__ src, T* __restrict__ dst,
+                                                              int Np) {
+  __shared__ T t[64][65];
+  const size_t base = (size_t)blockIdx.z * Np * Np;
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int r = i / 64, c = i % 64;
+    t[r][c] = src[base + (size_t)(r0 + r) * Np + c0 + c];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int r = i / 64, c = i % 64;
+    dst[base + (size_t)(c0 + r) * Np + r0 + c] = t[c][r];
+  }
 }
 
 template <class TC, int C>
@@ -434,12 +466,12 @@ int output_vjp_launch(const void* g, const void* X, const void* x, const float* 
 
 template <class TZ, class TC, int C>
 int project_vjp_launch(const void* dplanes, const void* x, const float* mask, const void* w4, const void* w4t,
-                       const float* gx_in, int B, int N, int outgoing, void* gpg, void* dx, hipStream_t s) {
+                       const float* gx_in, int B, int N, int outgoing, void* gpg, void* xw, void* dx, hipStream_t s) {
   const int Np = pf::pad128(N);
   constexpr int BM = vjp_bm<TC, C>();
   trimul_project_vjp_kernel<TZ, TC, C><<<dim3(Np / BM, Np, B), 256, 0, s>>>(
       (const TC*)dplanes, (const TZ*)x, mask, (const TC*)w4, (const TC*)w4t, gx_in, B, N, Np, outgoing, (TC*)gpg,
-      (TZ*)dx);
+      (TC*)xw, (TZ*)dx);
   return pf::check_launch("trimul_project_vjp");
 }
 
@@ -507,9 +539,9 @@ int pf_trimul_output_vjp(const void* g, const void* X, const void* x, const floa
 
 int pf_trimul_project_vjp(const void* dplanes, const void* x, const float* mask, const void* w_packed,
                           const void* w_packed_t, const float* gx_in, int B, int N, int C, int outgoing, int xdtype,
-                          int cdtype, void* gpg, void* dx, void* stream) {
-  PF_REQUIRE(dplanes && x && mask && w_packed && w_packed_t && gx_in && gpg && dx, PF_ERR_INVALID_ARG,
-             "pf_trimul_project_vjp: null pointer");
+                          int cdtype, void* gpg, void* xw, void* dx, void* stream) {
+  PF_REQUIRE(dplanes && x && mask && w_packed && w_packed_t && gx_in && gpg && dx && (outgoing || xw),
+             PF_ERR_INVALID_ARG, "pf_trimul_project_vjp: null pointer");
   PF_REQUIRE(vjp_args_ok(B, N, C, xdtype, cdtype), PF_ERR_UNSUPPORTED,
              "pf_trimul_project_vjp: B=%d N=%d C=%d xdtype=%d cdtype=%d", B, N, C, xdtype, cdtype);
   PF_REQUIRE(pf::aligned16(dplanes) && pf::aligned16(x) && pf::aligned16(gpg) && pf::aligned16(dx) &&
@@ -520,8 +552,23 @@ int pf_trimul_project_vjp(const void* dplanes, const void* x, const float* mask,
     using TZ = decltype(tz);
     using TC = decltype(tc);
     constexpr int CC = decltype(cc)::value;
-    return project_vjp_launch<TZ, TC, CC>(dplanes, x, mask, w_packed, w_packed_t, gx_in, B, N, outgoing, gpg, dx, s);
+    return project_vjp_launch<TZ, TC, CC>(dplanes, x, mask, w_packed, w_packed_t, gx_in, B, N, outgoing, gpg, xw, dx,
+                                          s);
   });
+}
+
+int pf_planes_transpose(const void* src, void* dst, int G, int Np, int dtype, void* stream) {
+  PF_REQUIRE(src && dst && src != dst, PF_ERR_INVALID_ARG, "pf_planes_transpose: null or aliased pointers");
+  PF_REQUIRE(G > 0 && G <= 65535 && Np > 0 && Np % 64 == 0, PF_ERR_INVALID_ARG, "pf_planes_transpose: G=%d Np=%d", G,
+             Np);
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_planes_transpose: dtype %d", dtype);
+  hipStream_t s = pf::as_stream(stream);
+  const dim3 grid((unsigned)(Np / 64), (unsigned)(Np / 64), (unsigned)G);
+  if (dtype == PF_F32)
+    plane_transpose_kernel<float><<<grid, 256, 0, s>>>((const float*)src, (float*)dst, Np);
+  else
+    plane_transpose_kernel<bf16><<<grid, 256, 0, s>>>((const bf16*)src, (bf16*)dst, Np);
+  return pf::check_launch("pf_planes_transpose");
 }
 
 }  // extern "C"

@@ -216,6 +216,28 @@ def fused_trimul(
     )  # fmt: skip
 
 
+def _token_chunk(B: int, N: int, target: int = 4096) -> int:
+    """A divisor of M = B N^2 near ``target`` tokens: N times the largest divisor d of B N with
+    N d <= max(target, N)."""
+    best = 1
+    for d in range(1, B * N + 1):
+        if N * d > max(target, N):
+            break
+        if (B * N) % d == 0:
+            best = d
+    return N * best
+
+
+def _weight_grad(a_cm: torch.Tensor, b: torch.Tensor, chunk: int) -> torch.Tensor:
+    """``a b`` in fp32 for channel-major ``a_cm`` [Ca, M] and token-major ``b`` [M, Cb], M in the
+    hundreds of thousands: split over token chunks as one batched GEMM on strided views (one
+    [Ca, Cb] output tile alone would leave the GPU idle), then summed over the chunks."""
+    Ca, M = a_cm.shape
+    S = M // chunk
+    a3 = a_cm.view(Ca, S, chunk).permute(1, 0, 2)  # [S, Ca, chunk], rows of stride M
+    return torch.bmm(a3, b.view(S, chunk, b.shape[1])).float().sum(0)
+
+
 class FusedTriMulFunction(torch.autograd.Function):
     """Trainable triangle multiply after the input LayerNorm (``FusedTriMulFunction``,
     ``triton/fused_trimul.py:285-330``); same ``apply`` arguments.
@@ -278,7 +300,8 @@ class FusedTriMulFunction(torch.autograd.Function):
         g = g.to(xc.dtype).contiguous()
         kernel_census.record("TriangleMul.backward", "hip_trimul_vjp")
         pl = planes.view(cdt).view(3, B * C, Np, Np)
-        gp, gg, xln = (torch.empty((M, C), dtype=cdt, device=dev) for _ in range(3))
+        gp, gg = (torch.empty((C, M), dtype=cdt, device=dev) for _ in range(2))  # channel-major
+        xln = torch.empty((M, C), dtype=cdt, device=dev)
         dX = torch.empty((B * C, Np, Np), dtype=cdt, device=dev)
         gx = torch.empty((M, C), dtype=torch.float32, device=dev)
         dlnw, dlnb = (torch.empty(C, dtype=torch.float32, device=dev) for _ in range(2))
@@ -292,23 +315,29 @@ class FusedTriMulFunction(torch.autograd.Function):
             dlnb.data_ptr(), ws.data_ptr(), ws_bytes, stream,
         )  # fmt: skip
         xb = xc.reshape(M, C).to(cdt)
-        d_out = torch.mm(gp.t(), xln).float()
-        d_out_gate = torch.mm(gg.t(), xb).float()
+        chunk = _token_chunk(B, N)
+        d_out = _weight_grad(gp, xln, chunk)
+        d_out_gate = _weight_grad(gg, xb, chunk)
         del gp, gg, xln
         # X = P Q^T per channel plane: dP = dX Q, dQ = dX^T P (contiguous operands)
         dpl = torch.empty((2, B * C, Np, Np), dtype=cdt, device=dev)
         torch.bmm(dX, pl[1], out=dpl[0])
-        torch.bmm(dX.transpose(1, 2).contiguous(), pl[0], out=dpl[1])
+        dXt = torch.empty_like(dX)
+        _lib.call("pf_planes_transpose", dX.data_ptr(), dXt.data_ptr(), B * C, Np, code_c, stream)
         del dX
-        gpg = torch.empty((M, 4 * C), dtype=cdt, device=dev)
+        torch.bmm(dXt, pl[0], out=dpl[1])
+        del dXt
+        gpg = torch.empty((4 * C, M), dtype=cdt, device=dev)  # channel-major, the kernel's walk order
+        xw = None if ctx.outgoing else torch.empty((M, C), dtype=cdt, device=dev)  # x in that order
         dx = torch.empty_like(xc)
         w4t = w4.t().contiguous()
         _lib.call(
             "pf_trimul_project_vjp", dpl.data_ptr(), xc.data_ptr(), m.data_ptr(), w4.data_ptr(), w4t.data_ptr(),
-            gx.data_ptr(), B, N, C, int(ctx.outgoing), code_x, code_c, gpg.data_ptr(), dx.data_ptr(), stream,
+            gx.data_ptr(), B, N, C, int(ctx.outgoing), code_x, code_c, gpg.data_ptr(), _lib.ptr(xw), dx.data_ptr(),
+            stream,
         )  # fmt: skip
         del dpl, gx
-        dw4 = torch.mm(gpg.t(), xb).float().view(C // 16, 4, 16, C)  # packed rows 64 j + 16 kind + r
+        dw4 = _weight_grad(gpg, xb if xw is None else xw, chunk).view(C // 16, 4, 16, C)  # rows 64 j + 16 kind + r
         d_proj = torch.cat([dw4[:, 0].reshape(C, C), dw4[:, 2].reshape(C, C)])
         d_gate = torch.cat([dw4[:, 1].reshape(C, C), dw4[:, 3].reshape(C, C)])
         dt = ctx.dtypes

@@ -113,17 +113,23 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
  *
  * pf_trimul_output_vjp (_output_vjp_kernel, fused_trimul.py:153-212): with g the update's
  * cotangent [B,N,N,C] (xdtype), X from `planes` and w_out_t, w_out_gate_t the transposed
- * [C,C] weights, writes gp = g s, gg = g p s (1 - s) and xln = LN_out(X) token-major
- * [B*N*N, C] (cdtype), dX the cotangent of X (channel-major like X, zero at padding),
+ * [C,C] weights, writes gp = g s, gg = g p s (1 - s) channel-major [C, B*N*N] and
+ * xln = LN_out(X) token-major [B*N*N, C] (cdtype), dX the cotangent of X (channel-major like X, zero at padding),
  * gx = gg Wog [B*N*N, C] fp32 and the LN_out affine gradients [C] fp32 (summed in a fixed
  * order). The host then forms dP = dX Q, dQ = dX^T P and the weight gradients
  * (w_out: gp^T xln, w_out_gate: gg^T x).
  *
  * pf_trimul_project_vjp (_project_vjp_kernel, fused_trimul.py:214-262): dplanes = [dP; dQ]
  * (two [B*C][Np][Np] cdtype sets), w_packed from pf_trimul_train_pack_weights and
- * w_packed_t its [C, 4C] transpose; writes G = (gp_a, gg_a, gp_b, gg_b) token-major
- * [B*N*N, 4C] in the packed row order (the packed weights' gradient is G^T x) and
- * dx = gx_in + G W4 [B*N*N, C] (xdtype). C = 64, 128 or 256. */
+ * w_packed_t its [C, 4C] transpose; writes G = (gp_a, gg_a, gp_b, gg_b) channel-major
+ * [4C, B*N*N] in the packed row order and dx = gx_in + G^T W4 [B*N*N, C] (xdtype). G's
+ * columns follow the kernel's walk over plane positions (line, t) at b N^2 + line N + t:
+ * token order when outgoing; when incoming (line = column of z) x is also written in that
+ * order to xw [B*N*N, C] (cdtype), so the packed weights' gradient is G x (outgoing) or
+ * G xw (incoming). C = 64, 128 or 256.
+ *
+ * pf_planes_transpose: dst[g] = src[g]^T for G planes [Np][Np] (Np a multiple of 64), the
+ * dX^T operand of dQ = dX^T P. */
 int pf_trimul_train_pack_weights(const void* w_proj, const void* w_gate, int wdtype, void* packed, int C, int cdtype,
                                  void* stream);
 int pf_trimul_train_fwd(const void* x, const float* mask, const void* w_packed, const float* ln_out_w,
@@ -138,7 +144,8 @@ int pf_trimul_output_vjp(const void* g, const void* X, const void* x, const floa
                          size_t workspace_bytes, void* stream);
 int pf_trimul_project_vjp(const void* dplanes, const void* x, const float* mask, const void* w_packed,
                           const void* w_packed_t, const float* gx_in, int B, int N, int C, int outgoing, int xdtype,
-                          int cdtype, void* gpg, void* dx, void* stream);
+                          int cdtype, void* gpg, void* xw, void* dx, void* stream);
+int pf_planes_transpose(const void* src, void* dst, int G, int Np, int dtype, void* stream);
 
 
 /* ---- triangle attention (starting / ending node) ------------------------ */
