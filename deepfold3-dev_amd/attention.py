@@ -87,7 +87,9 @@ class GridSelfAttention(nn.Module):
         H, D = self.num_heads, self.head_dim
         if D != 32:
             raise NotActive("GridSelfAttention", f"head dim {D}: the differentiable attention is built for 32")
-        zn = F.layer_norm(z.float(), (C,), self.norm.weight.float(), self.norm.bias.float(), self.norm.eps).to(z.dtype)
+        from .kernels import LayerNormFunction
+
+        zn = LayerNormFunction.apply(z, self.norm.weight, self.norm.bias, self.norm.eps)
         pb = F.linear(zn, self.pair_bias.weight).permute(0, 3, 1, 2)  # [B, H, N, N], un-transposed z
         if self.transpose:
             zn, mask = zn.transpose(1, 2), mask.transpose(1, 2)

@@ -8,8 +8,11 @@
 // C = 128 (the pair representation): 16 lanes per row, 16 rows per wave (layernorm128_kernel).
 // Other C: one wave per row; each lane owns C/128 chunks of two channels, so every load
 // instruction of a wave reads one 256-byte (bf16) or 512-byte (fp32) contiguous run.
+#include <type_traits>
+
 #include "capi.h"
 #include "common.h"
+#include "rowops.h"
 
 namespace {
 
@@ -140,6 +143,115 @@ __global__ __launch_bounds__(256) void layernorm128_kernel(const T* __restrict__
   }
 }
 
+// ------------------------------------------------------------------ backward
+// One wave per row, kLnbRows rows per block; each lane owns C / 64 consecutive channels.
+// dx = rstd (g - mean(g) - xn mean(g xn)) with g = dy * w and xn the standardised x
+// (statistics recomputed, fp32 two-pass as the forward); per-block partial sums of
+// dy * xn (weight) and dy (bias), added in block order by ln_param_grad_reduce.
+constexpr int kLnbRows = 64;
+
+template <class T, int C>
+__global__ __launch_bounds__(256) void layernorm_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                            const float* __restrict__ w, float eps, long M,
+                                                            T* __restrict__ dx, float* __restrict__ partial) {
+  constexpr int CPL = C / 64;  // channels per lane
+  __shared__ float red[4][2 * C];
+  const int wv = wave_id();
+  const int l = lane_id();
+  float wl[CPL], sw[CPL], sb[CPL];
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) {
+    wl[e] = w[l * CPL + e];
+    sw[e] = sb[e] = 0.f;
+  }
+  for (int rr = wv; rr < kLnbRows; rr += 4) {
+    const long r = (long)blockIdx.x * kLnbRows + rr;
+    if (r >= M) break;
+    float xv[CPL], gv[CPL], dv[CPL];
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      xv[e] = to_f32(x[r * C + l * CPL + e]);
+      dv[e] = to_f32(dy[r * C + l * CPL + e]);
+      s += xv[e];
+    }
+    const float mean = group_sum<64>(s) * (1.0f / C);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      const float d = xv[e] - mean;
+      q += d * d;
+    }
+    const float rstd = rsqrtf(group_sum<64>(q) * (1.0f / C) + eps);
+    float sg = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      xv[e] = (xv[e] - mean) * rstd;  // xn
+      gv[e] = dv[e] * wl[e];
+      sg += gv[e];
+      sgx += gv[e] * xv[e];
+      sw[e] += dv[e] * xv[e];
+      sb[e] += dv[e];
+    }
+    sg = group_sum<64>(sg) * (1.0f / C);
+    sgx = group_sum<64>(sgx) * (1.0f / C);
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) dx[r * C + l * CPL + e] = from_f32<T>(rstd * (gv[e] - sg - xv[e] * sgx));
+  }
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) {
+    red[wv][l * CPL + e] = sw[e];
+    red[wv][C + l * CPL + e] = sb[e];
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < 2 * C; k += 256)
+    partial[(size_t)blockIdx.x * 2 * C + k] = red[0][k] + red[1][k] + red[2][k] + red[3][k];
+}
+
+// out[k] = sum over blocks of partial[blk][k] (k < 2C: weight then bias), in block order.
+__global__ __launch_bounds__(256) void ln_param_grad_reduce_kernel(const float* __restrict__ partial, long nblk,
+                                                                   int C, float* __restrict__ dw,
+                                                                   float* __restrict__ db) {
+  __shared__ float red[256];
+  const int k = blockIdx.x;
+  float s = 0.f;
+  for (long blk = threadIdx.x; blk < nblk; blk += 256) s += partial[blk * 2 * C + k];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (k < C)
+      dw[k] = red[0];
+    else
+      db[k - C] = red[0];
+  }
+}
+
+template <class T>
+int ln_bwd_launch(const void* x, const void* dy, const float* w, float eps, long M, int C, void* dx, float* dw,
+                  float* db, void* ws, hipStream_t s) {
+  const long nblk = (M + kLnbRows - 1) / kLnbRows;
+  float* partial = static_cast<float*>(ws);
+  auto run = [&](auto cc) {
+    constexpr int CC = decltype(cc)::value;
+    layernorm_bwd_kernel<T, CC><<<(unsigned)nblk, 256, 0, s>>>((const T*)x, (const T*)dy, w, eps, M, (T*)dx,
+                                                                partial);
+  };
+  switch (C) {
+    case 64: run(std::integral_constant<int, 64>{}); break;
+    case 128: run(std::integral_constant<int, 128>{}); break;
+    case 256: run(std::integral_constant<int, 256>{}); break;
+    case 384: run(std::integral_constant<int, 384>{}); break;
+    default: run(std::integral_constant<int, 512>{}); break;
+  }
+  if (int e = pf::check_launch("layernorm_bwd")) return e;
+  ln_param_grad_reduce_kernel<<<2 * C, 256, 0, s>>>(partial, nblk, C, dw, db);
+  return pf::check_launch("ln_param_grad_reduce");
+}
+
 template <class T>
 int ln_dispatch(const void* x, const float* w, const float* b, float eps, void* out, long M, int C, int N1, int N2,
                 int transpose, hipStream_t s) {
@@ -160,7 +272,8 @@ int ln_dispatch(const void* x, const float* w, const float* b, float eps, void* 
       layernorm_rows_kernel<T, 512><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
       break;
     default:
-      pf::set_error(PF_ERR_UNSUPPORTED, "layernorm: C=%d (built: 128, 256, 384, 512)", C);
+      if (!transpose && C > 0) return ln_launch<T, T>(x, w, b, eps, out, M, C, s);  // any other width: wave per row
+      pf::set_error(PF_ERR_UNSUPPORTED, "layernorm + transpose: C=%d (built: 128, 256, 384, 512)", C);
       return PF_ERR_UNSUPPORTED;
   }
   timer.stop();
@@ -193,6 +306,25 @@ int pf_ln_transpose_fwd(const void* x, int dtype, const float* w, const float* b
   hipStream_t s = pf::as_stream(stream);
   if (dtype == PF_F32) return ln_dispatch<float>(x, w, b, eps, out, M, C, N1, N2, do_transpose, s);
   return ln_dispatch<bf16>(x, w, b, eps, out, M, C, N1, N2, do_transpose, s);
+}
+
+size_t pf_layernorm_bwd_workspace_bytes(long M, int C) {
+  if (M <= 0 || C <= 0) return 0;
+  return (size_t)((M + kLnbRows - 1) / kLnbRows) * 2 * C * sizeof(float);
+}
+
+int pf_layernorm_bwd(const void* x, const void* dy, int dtype, const float* w, float eps, void* dx, float* dw,
+                     float* db, long M, int C, void* workspace, size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(x && dy && w && dx && dw && db, PF_ERR_INVALID_ARG, "pf_layernorm_bwd: null pointer");
+  PF_REQUIRE(M > 0, PF_ERR_INVALID_ARG, "pf_layernorm_bwd: M=%ld", M);
+  PF_REQUIRE(C == 64 || C == 128 || C == 256 || C == 384 || C == 512, PF_ERR_UNSUPPORTED,
+             "pf_layernorm_bwd: C=%d (built: 64, 128, 256, 384, 512)", C);
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_layernorm_bwd: dtype %d", dtype);
+  PF_REQUIRE(workspace && workspace_bytes >= pf_layernorm_bwd_workspace_bytes(M, C), PF_ERR_WORKSPACE,
+             "pf_layernorm_bwd: workspace %zu < %zu bytes", workspace_bytes, pf_layernorm_bwd_workspace_bytes(M, C));
+  hipStream_t s = pf::as_stream(stream);
+  if (dtype == PF_F32) return ln_bwd_launch<float>(x, dy, w, eps, M, C, dx, dw, db, workspace, s);
+  return ln_bwd_launch<bf16>(x, dy, w, eps, M, C, dx, dw, db, workspace, s);
 }
 
 }  // extern "C"

@@ -104,6 +104,38 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: f
     return out
 
 
+class LayerNormFunction(torch.autograd.Function):
+    """Differentiable LayerNorm on the HIP kernels (``primitives.py:90-115`` semantics: fp32
+    statistics, output in x's dtype): ``pf_layernorm_fwd`` and ``pf_layernorm_bwd``, the
+    affine gradients summed over rows in a fixed order. ``apply(x, weight, bias, eps)``."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps):
+        xc = x.detach().contiguous()
+        out = layer_norm(xc, weight, bias, eps)
+        ctx.save_for_backward(xc, weight)
+        ctx.eps = float(eps)
+        ctx.dtypes = (weight.dtype, bias.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        xc, weight = ctx.saved_tensors
+        C = xc.shape[-1]
+        M = xc.numel() // C
+        dyc = dy.to(xc.dtype).contiguous()
+        dx = torch.empty_like(xc)
+        dw, db = (torch.empty(C, dtype=torch.float32, device=xc.device) for _ in range(2))
+        ws_bytes = _lib.lib().pf_layernorm_bwd_workspace_bytes(M, C)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=xc.device)
+        kernel_census.record("LayerNorm.backward", "hip_layernorm_bwd")
+        _lib.call(
+            "pf_layernorm_bwd", xc.data_ptr(), dyc.data_ptr(), _lib.dtype_code(xc.dtype), _f32(weight).data_ptr(),
+            ctx.eps, dx.data_ptr(), dw.data_ptr(), db.data_ptr(), M, C, ws.data_ptr(), ws_bytes, _lib.stream_of(xc),
+        )  # fmt: skip
+        return dx, dw.to(ctx.dtypes[0]), db.to(ctx.dtypes[1]), None
+
+
 def ln_transpose(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float, do_transpose: bool):
     """``LN(x).permute(0, 2, 1, 3)`` for x [B,N1,N2,C] (``triton/layernorm_transpose.py:269-316``)."""
     _lib.require_device("ln_transpose", x)

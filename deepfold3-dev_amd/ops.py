@@ -13,13 +13,13 @@ from __future__ import annotations
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import kernel_census
 from .config import OptimConfig, require_hip
 from .inference_guard import NotActive, inference_only
 from .kernels import (
     FusedTriMulFunction,
+    LayerNormFunction,
     cast_weight,
     gemm_dtype_for,
     pack_trimul_weights,
@@ -88,11 +88,10 @@ class _TriangleMulBase(nn.Module):
         )  # fmt: skip
 
     def _forward_grad(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
-        """Training path (``ops.py:375-388``): ``norm_left`` in autograd (fp32 statistics, cast
-        back), then the HIP ``FusedTriMulFunction`` with its VJP kernels."""
-        C = z.shape[-1]
+        """Training path (``ops.py:375-388``): ``norm_left`` (the HIP LayerNorm and its backward),
+        then the HIP ``FusedTriMulFunction`` with its VJP kernels."""
         nl = self.norm_left
-        x = F.layer_norm(z.float(), (C,), nl.weight.float(), nl.bias.float(), nl.eps).to(z.dtype)
+        x = LayerNormFunction.apply(z, nl.weight, nl.bias, nl.eps)
         order = self._block_order.to(z.device)
         w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
         return FusedTriMulFunction.apply(

@@ -67,9 +67,17 @@ int pf_add(const void* res, int res_dtype, const void* x, int x_dtype, void* out
 
 /* ---- LayerNorm -------------------------------------------------------- */
 /* out[r, :] = LN(x[r, :]) over C channels, fp32 statistics, output in x's dtype.
- * Replaces layer_norm / LayerNorm.forward (primitives.py:90-155). C in {128, 256, 384, 512}. */
+ * Replaces layer_norm / LayerNorm.forward (primitives.py:90-155). Tuned for C in
+ * {128, 256, 384, 512}; other widths run a wave-per-row kernel. */
 int pf_layernorm_fwd(const void* x, int dtype, const float* w, const float* b, float eps, void* out, long M, int C,
                      void* stream);
+/* Backward of pf_layernorm_fwd (LayerNorm under autograd, primitives.py:90-115): for
+ * dy = dL/dout [M, C] (x's dtype) writes dx (x's dtype) and the affine gradients dw, db [C]
+ * fp32 (summed over rows in a fixed order). Statistics are recomputed from x.
+ * C in {64, 128, 256, 384, 512}. */
+size_t pf_layernorm_bwd_workspace_bytes(long M, int C);
+int pf_layernorm_bwd(const void* x, const void* dy, int dtype, const float* w, float eps, void* dx, float* dw,
+                     float* db, long M, int C, void* workspace, size_t workspace_bytes, void* stream);
 /* x [B,N1,N2,C] -> out [B,N2,N1,C] (do_transpose) or [B,N1,N2,C]: LN then permute(0,2,1,3).
  * Replaces FusedLayerNormTranspose(C, do_transpose)(x, w, b) (triton/layernorm_transpose.py:269-316). */
 int pf_ln_transpose_fwd(const void* x, int dtype, const float* w, const float* b, float eps, void* out, int B, int N1,
