@@ -89,6 +89,7 @@ SIGNATURES: dict[str, tuple] = {
     "pf_layernorm_linear_workspace_bytes": (_sz, [_l, _i, _i]),
     "pf_layernorm_linear_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, _vp, _l, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "pf_swiglu_fwd": (_i, [_vp, _i, _vp, _l, _i, _vp]),
+    "pf_swiglu_bwd": (_i, [_vp, _vp, _i, _vp, ctypes.c_long, _i, _vp]),
     "pf_single_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "pf_single_attn_fwd": (
         _i,

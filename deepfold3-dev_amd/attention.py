@@ -255,13 +255,47 @@ class SingleAttention(nn.Module):
             self.num_heads, out=out, accumulate=accumulate,
         )  # fmt: skip
 
-    @inference_only("SingleAttention")
+    def _forward_grad(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
+        """Training path: LayerNorm (HIP, with its backward), the q/k/v/g projections and the output
+        projection in autograd, and the attention core on the HIP flash attention with its
+        backward (``fused._EvoformerAttention``; one line per batch item, the heads' key and value
+        dimensions zero-padded to 32 and q scaled so that the kernel's 32^-1/2 gives d^-1/2,
+        ``attention.py:415-433``)."""
+        from .fused import _EvoformerAttention
+        from .kernels import LayerNormFunction
+
+        B, N, _ = x.shape
+        H, Dk, Dv = self.num_heads, self.key_dim_per_head, self.val_dim_per_head
+        if Dk > 32 or Dv > 32:
+            raise NotActive("SingleAttention", f"head dims {Dk}/{Dv}: the differentiable attention takes up to 32")
+        xn = LayerNormFunction.apply(x, self.norm.weight, self.norm.bias, self.norm.eps)
+        q = F.linear(xn, self.to_q.weight, self.to_q.bias) * (Dk**-0.5 * 32**0.5)
+
+        def heads(t: torch.Tensor, d: int) -> torch.Tensor:  # [B, N, H d] -> [B, 1, H, N, 32]
+            t = t.reshape(B, N, H, d).transpose(1, 2)
+            if d < 32:
+                t = F.pad(t, (0, 32 - d))
+            return t.unsqueeze(1).contiguous()
+
+        Q, K, V = heads(q, Dk), heads(F.linear(xn, self.to_k.weight), Dk), heads(F.linear(xn, self.to_v.weight), Dv)
+        res_mask = (1e9 * (mask.float() - 1.0)).view(B, 1, 1, 1, N)
+        o = _EvoformerAttention.apply(Q, K, V, res_mask, pair_logits.float().unsqueeze(1), True)
+        o = o[:, 0, :, :, :Dv].transpose(1, 2).reshape(B, N, H * Dv)
+        g = torch.sigmoid(F.linear(xn, self.to_g.weight))
+        w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
+        return F.linear(o * g, w_out)
+
     def forward(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
-        """x [B?, N, c], mask [B?, N], pair_logits [B?, H, N, N] -> update [B?, N, c]."""
+        """x [B?, N, c], mask [B?, N], pair_logits [B?, H, N, N] -> update [B?, N, c]. Under grad
+        the differentiable path."""
         has_batch = x.dim() == 3
         if not has_batch:
             x, mask, pair_logits = x.unsqueeze(0), mask.unsqueeze(0), pair_logits.unsqueeze(0)
-        out = self._run(x, mask, pair_logits, None, False)
+        if torch.is_grad_enabled():
+            kernel_census.record("SingleAttention", "hip_evo_attn_grad")
+            out = self._forward_grad(x, mask, pair_logits)
+        else:
+            out = self._run(x, mask, pair_logits, None, False)
         return out if has_batch else out.squeeze(0)
 
     @inference_only("SingleAttention")

@@ -225,6 +225,24 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ x, T*
   }
 }
 
+// Backward of swiglu_kernel: for y = silu(a) b, da = dy b silu'(a) with
+// silu'(a) = s (1 + a (1 - s)), s = sigmoid(a), and db = dy silu(a); dx = [da | db].
+template <class T>
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                         T* __restrict__ dx, long M, int D) {
+  const long n = M * D;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    const long r = i / D;
+    const int c = (int)(i % D);
+    const float a = to_f32(x[r * 2 * D + c]);
+    const float bb = to_f32(x[r * 2 * D + D + c]);
+    const float g = to_f32(dy[i]);
+    const float sg = sigmoidf_(a);
+    dx[r * 2 * D + c] = from_f32<T>(g * bb * sg * (1.f + a * (1.f - sg)));
+    dx[r * 2 * D + D + c] = from_f32<T>(g * a * sg);
+  }
+}
+
 size_t es_of(int dt) { return dt == PF_F32 ? 4 : 2; }
 
 template <class TZ, class TC>
@@ -408,6 +426,21 @@ int pf_swiglu_fwd(const void* x, int dtype, void* y, long M, int D, void* stream
   else
     swiglu_kernel<bf16><<<g, 256, 0, s>>>((const bf16*)x, (bf16*)y, M, D);
   return pf::check_launch("swiglu");
+}
+
+int pf_swiglu_bwd(const void* x, const void* dy, int dtype, void* dx, long M, int D, void* stream) {
+  PF_REQUIRE(x && dy && dx, PF_ERR_INVALID_ARG, "pf_swiglu_bwd: null pointer");
+  PF_REQUIRE(M >= 0 && D > 0, PF_ERR_INVALID_ARG, "pf_swiglu_bwd: M=%ld D=%d", M, D);
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_swiglu_bwd: dtype %d", dtype);
+  if (M == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  const long n = M * D;
+  const unsigned g = (unsigned)((n + 255) / 256 > 65536 ? 65536 : (n + 255) / 256);
+  if (dtype == PF_F32)
+    swiglu_bwd_kernel<float><<<g, 256, 0, s>>>((const float*)x, (const float*)dy, (float*)dx, M, D);
+  else
+    swiglu_bwd_kernel<bf16><<<g, 256, 0, s>>>((const bf16*)x, (const bf16*)dy, (bf16*)dx, M, D);
+  return pf::check_launch("swiglu_bwd");
 }
 
 size_t pf_layernorm_linear_workspace_bytes(long M, int K, int cdtype) {

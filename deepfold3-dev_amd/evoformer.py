@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import kernel_census
 from .attention import GridSelfAttention, SingleAttention
@@ -143,16 +144,40 @@ class PairFormerBlock(nn.Module):
         self.single_transition.forward_residual_(single)
         return single
 
-    @inference_only("PairFormerBlock")
+    def forward_grad(
+        self, pair: torch.Tensor, single: torch.Tensor, pair_mask: torch.Tensor, seq_mask: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """The block out of place and differentiable (``evoformer.py:270-355``, eval dropout):
+        each branch's training path (triangle multiplications and attention, transitions and
+        single attention on the HIP kernels with their backward), residual adds in autograd,
+        every residual scale folded into its branch's output projection."""
+        from .kernels import LayerNormFunction
+
+        kernel_census.record("PairFormerBlock", "hip_block_grad")
+        p = pair + self.tri_mul_out(pair, pair_mask)
+        p = p + self.tri_mul_in(p, pair_mask)
+        p = p + self.pair_attn_row(p, pair_mask)
+        p = p + self.pair_attn_col(p, pair_mask)
+        p = p + self.pair_transition(p)
+        n = self.single_to_pair_norm
+        logits = F.linear(LayerNormFunction.apply(p, n.weight, n.bias, n.eps), self.single_to_pair.weight)
+        s = single + self.single_attn(single, seq_mask, logits.movedim(-1, -3))
+        s = s + self.single_transition(s)
+        return p, s
+
     def forward(
         self, pair: torch.Tensor, single: torch.Tensor, pair_mask: torch.Tensor, seq_mask: torch.Tensor
     ) -> tuple[torch.Tensor, torch.Tensor]:
-        """Reference signature (``evoformer.py:270-355``): returns new ``(pair, single)``."""
+        """Reference signature (``evoformer.py:270-355``): returns new ``(pair, single)``; under
+        grad the differentiable path (``forward_grad``), else the in-place inference kernels."""
         has_batch = pair.dim() == 4
         if not has_batch:
             pair, single = pair.unsqueeze(0), single.unsqueeze(0)
             pair_mask, seq_mask = pair_mask.unsqueeze(0), seq_mask.unsqueeze(0)
-        p, s = self.forward_(pair.contiguous().clone(), single.contiguous().clone(), pair_mask, seq_mask)
+        if torch.is_grad_enabled():
+            p, s = self.forward_grad(pair, single, pair_mask.to(torch.float32), seq_mask)
+        else:
+            p, s = self.forward_(pair.contiguous().clone(), single.contiguous().clone(), pair_mask, seq_mask)
         return (p, s) if has_batch else (p.squeeze(0), s.squeeze(0))
 
     def pair_logits(self, pair: torch.Tensor) -> torch.Tensor:
@@ -186,7 +211,6 @@ class PairFormerStack(nn.Module):
     def blocks(self) -> nn.ModuleList:
         return self._modules[self._layer_attr]
 
-    @inference_only("PairFormerStack")
     def forward(
         self, pair: torch.Tensor, single: torch.Tensor, pair_mask: torch.Tensor, seq_mask: torch.Tensor
     ) -> tuple[torch.Tensor, torch.Tensor]:
@@ -194,7 +218,13 @@ class PairFormerStack(nn.Module):
         runs on a second stream, beside the pair half of block i + 1: the pair update never
         reads the single representation, and the single half of block i needs only block i's
         pair logits (an event orders it after them) and block i - 1's single half (same
-        stream). The streams join before returning."""
+        stream). The streams join before returning. Under grad the blocks' differentiable
+        path runs in order on one stream."""
+        if torch.is_grad_enabled():
+            pair_mask = pair_mask.to(torch.float32)
+            for blk in self.blocks:
+                pair, single = blk.forward_grad(pair, single, pair_mask, seq_mask)
+            return pair, single
         pair = pair.contiguous().clone()
         single = single.contiguous().clone()
         # One fp32 mask object for every block: the attention kernels' outer-product check

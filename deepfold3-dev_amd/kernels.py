@@ -136,6 +136,33 @@ class LayerNormFunction(torch.autograd.Function):
         return dx, dw.to(ctx.dtypes[0]), db.to(ctx.dtypes[1]), None
 
 
+class SwiGLUFunction(torch.autograd.Function):
+    """Differentiable ``silu(x[..., :D]) * x[..., D:]`` on the HIP kernels (``pf_swiglu_fwd``,
+    ``pf_swiglu_bwd``; the reference's ``FusedSwiGLU``, ``triton/swiglu.py:60-95``, ``:192-200``)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        _lib.require_device("swiglu", x)
+        xc = x.detach().contiguous()
+        D = xc.shape[-1] // 2
+        y = torch.empty(xc.shape[:-1] + (D,), dtype=xc.dtype, device=xc.device)
+        _lib.call("pf_swiglu_fwd", xc.data_ptr(), _lib.dtype_code(xc.dtype), y.data_ptr(), xc.numel() // (2 * D), D,
+                  _lib.stream_of(xc))  # fmt: skip
+        ctx.save_for_backward(xc)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (xc,) = ctx.saved_tensors
+        D = xc.shape[-1] // 2
+        dyc = dy.to(xc.dtype).contiguous()
+        dx = torch.empty_like(xc)
+        kernel_census.record("SwiGLU.backward", "hip_swiglu_bwd")
+        _lib.call("pf_swiglu_bwd", xc.data_ptr(), dyc.data_ptr(), _lib.dtype_code(xc.dtype), dx.data_ptr(),
+                  xc.numel() // (2 * D), D, _lib.stream_of(xc))  # fmt: skip
+        return dx
+
+
 def ln_transpose(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float, do_transpose: bool):
     """``LN(x).permute(0, 2, 1, 3)`` for x [B,N1,N2,C] (``triton/layernorm_transpose.py:269-316``)."""
     _lib.require_device("ln_transpose", x)

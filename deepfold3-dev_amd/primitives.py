@@ -143,10 +143,25 @@ class TransitionBlock(nn.Module):
         kernel_census.record("TransitionBlock", "hip_transition")
         return transition_forward(x, op["lnw"], op["lnb"], self.norm.eps, op["w1"], op["w2"], out, accumulate), None
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        from .inference_guard import require_no_grad
+    def _forward_grad(self, x: torch.Tensor) -> torch.Tensor:
+        """Training path, the reference's fused transition's structure (``fused_transition.py:34-83``:
+        LN + linear1, SwiGLU, linear2): the HIP LayerNorm and SwiGLU with their backward, the
+        two linears as library GEMMs in autograd, the branch scale on linear2."""
+        import torch.nn.functional as F
 
-        require_no_grad("TransitionBlock")
+        from .kernels import LayerNormFunction, SwiGLUFunction
+
+        xn = LayerNormFunction.apply(x, self.norm.weight, self.norm.bias, self.norm.eps)
+        w2 = self.linear2.weight if self.branch_scale == 1.0 else self.linear2.weight * self.branch_scale
+        return F.linear(SwiGLUFunction.apply(F.linear(xn, self.linear1.weight)), w2)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """``transition(x)`` (not added to x); under grad the differentiable path."""
+        if torch.is_grad_enabled():
+            from . import kernel_census
+
+            kernel_census.record("TransitionBlock", "hip_transition_grad")
+            return self._forward_grad(x)
         return self.run(x)[0]
 
     def forward_residual_(self, x: torch.Tensor, s2p=None):

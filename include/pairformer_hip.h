@@ -313,6 +313,9 @@ int pf_layernorm_linear_fwd(const void* x, int xdtype, const float* ln_w, const 
                             void* workspace, size_t workspace_bytes, void* stream);
 /* FusedSwiGLU()(x) (triton/swiglu.py:192-200): y [M, D] = silu(x[:, :D]) * x[:, D:], x [M, 2D]. */
 int pf_swiglu_fwd(const void* x, int dtype, void* y, long M, int D, void* stream);
+/* Backward of pf_swiglu_fwd (FusedSwiGLU's VJP, triton/swiglu.py:60-95): dx [M, 2D] from
+ * x [M, 2D] and dy [M, D], all in dtype. */
+int pf_swiglu_bwd(const void* x, const void* dy, int dtype, void* dx, long M, int D, void* stream);
 
 #ifdef __cplusplus
 }
