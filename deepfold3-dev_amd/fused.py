@@ -11,19 +11,21 @@ reference, so call sites written against its Triton layer run unchanged:
 - ``FusedTransitionBlock`` (``fused_transition.py:34-83``)
 - ``dropout_add_rowwise`` / ``dropout_add_columnwise`` (``dropout_add.py:221-265``)
 
-``_EvoformerAttention`` is differentiable (the HIP backward); the others are forward-only
-(inference) and raise ``InferenceOnlyKernelError`` under grad. Anything the kernels cannot
-serve raises ``NotActive``. There is no PyTorch fallback.
+``_EvoformerAttention`` is differentiable (the HIP backward), and so are the others: under
+grad the LayerNorm runs ``kernels.LayerNormFunction`` and SwiGLU ``kernels.SwiGLUFunction``
+(HIP forward and backward), the small projections autograd's library GEMMs. Anything the
+kernels cannot serve raises ``NotActive``. There is no PyTorch fallback for the kernels.
 """
 
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import _lib, kernel_census
-from .inference_guard import NotActive, inference_only
-from .kernels import cast_weight, gemm_dtype_for, ln_transpose, residual_add
+from .inference_guard import NotActive
+from .kernels import LayerNormFunction, SwiGLUFunction, cast_weight, gemm_dtype_for, ln_transpose, residual_add
 from .primitives import TransitionBlock, f32
 
 __all__ = [
@@ -181,9 +183,15 @@ class FusedPairBias(nn.Module):
         super().__init__()
         self.c, self.num_heads, self.eps = c, num_heads, eps
 
-    @inference_only("FusedPairBias")
     def forward(self, z, ln_weight, ln_bias, proj_weight, mask=None):
+        """Under grad: the HIP LayerNorm with its backward and the projection in autograd."""
         _lib.require_device("FusedPairBias", z)
+        if torch.is_grad_enabled():
+            kernel_census.record("GridSelfAttention.norm", "hip_pair_bias_grad")
+            out = F.linear(LayerNormFunction.apply(z, ln_weight, ln_bias, self.eps), proj_weight).permute(0, 3, 1, 2)
+            if mask is not None:
+                out = out + (1.0 - mask.to(out.dtype))[:, None, None, :] * (-1e9)
+            return out
         B, N, _, C = z.shape
         H = proj_weight.shape[0]
         if C != self.c or H > 16:
@@ -209,8 +217,12 @@ class FusedLayerNormTranspose(nn.Module):
         super().__init__()
         self.c, self.do_transpose, self.eps = c, do_transpose, eps
 
-    @inference_only("FusedLayerNormTranspose")
     def forward(self, x, weight, bias):
+        """Under grad: the HIP LayerNorm with its backward, then the permute in autograd."""
+        if torch.is_grad_enabled():
+            kernel_census.record("GridSelfAttention.norm", "hip_ln_transpose_grad")
+            y = LayerNormFunction.apply(x, weight, bias, self.eps)
+            return y.permute(0, 2, 1, 3) if self.do_transpose else y
         kernel_census.record("GridSelfAttention.norm", "hip_ln_transpose")
         return ln_transpose(x, weight, bias, self.eps, self.do_transpose)
 
@@ -231,14 +243,18 @@ class FusedLayerNormLinear(nn.Module):
             self._wkey = key
         return self._wval
 
-    @inference_only("FusedLayerNormLinear")
     def forward(self, X, ln_weight, ln_bias, linear_weight, linear_bias=None):
+        """Under grad: the HIP LayerNorm with its backward, then ``LN(X) W + b`` in autograd."""
         if linear_bias is not None and not self.has_linear_bias:
             raise ValueError("linear_bias provided but module configured with has_linear_bias=False")
         _lib.require_device("FusedLayerNormLinear", X)
         K, N = self.in_features, self.out_features
         if tuple(linear_weight.shape) != (K, N):
             raise NotActive("FusedLayerNormLinear", f"weight must be [K, N] = [{K}, {N}]")
+        if torch.is_grad_enabled():
+            kernel_census.record("FusedLayerNormLinear", "hip_layernorm_grad")
+            y = torch.matmul(LayerNormFunction.apply(X, ln_weight, ln_bias, 1e-5), linear_weight.contiguous())
+            return y if linear_bias is None else y + linear_bias
         cdt = gemm_dtype_for(X)
         Xc = X.contiguous()
         M = Xc.numel() // K
@@ -258,9 +274,11 @@ class FusedLayerNormLinear(nn.Module):
 class FusedSwiGLU(nn.Module):
     """``silu(a) * b`` with ``[a, b] = split(x, 2, dim=-1)`` (``swiglu.py:192-200``)."""
 
-    @inference_only("FusedSwiGLU")
     def forward(self, x):
+        """Differentiable: the HIP backward under grad."""
         _lib.require_device("FusedSwiGLU", x)
+        if torch.is_grad_enabled():
+            return SwiGLUFunction.apply(x)
         xc = x.contiguous()
         D = xc.shape[-1] // 2
         y = torch.empty(xc.shape[:-1] + (D,), dtype=x.dtype, device=x.device)
@@ -280,6 +298,9 @@ class FusedTransitionBlock(TransitionBlock):
 def _dropout_add(residual, x, p_drop: float, training: bool, site: str):
     if training and p_drop > 0.0:
         raise NotActive(site, "training-mode dropout is not built (eval only)")
+    if torch.is_grad_enabled() and (residual.requires_grad or x.requires_grad):
+        kernel_census.record(site, "add_grad")
+        return residual + x  # eval dropout-add under autograd (dropout_add.py:236-237)
     kernel_census.record(site, "hip_add")
     return residual_add(residual, x)
 

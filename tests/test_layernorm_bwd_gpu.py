@@ -2,7 +2,8 @@
 pf_layernorm_bwd), against torch's LayerNorm differentiated in fp64 (a library routine), at
 the widths the training paths use; fp32 at relL2 <= 1e-5 and max-abs <= 1e-5 max|ref|; bf16
 within 2x the error of torch's own bf16 LayerNorm gradient (computed on the CPU). The affine
-gradients are summed in a fixed order: bitwise-reproducible."""
+gradients are summed in a fixed order: bitwise-reproducible. The kernel-level fused ops under
+grad (built on it and on the HIP SwiGLU backward) against torch's formulas in fp64."""
 
 from __future__ import annotations
 
@@ -58,3 +59,53 @@ def test_layernorm_backward_bf16(dev):
     assert rel_l2(got[0].double().cpu(), want[0]) <= 2 * rel_l2(eager_dx, want[0]) + 1e-6
     for a, r in zip(got[1:], want[1:]):
         assert rel_l2(a.double().cpu(), r) < 1e-3
+
+
+def _grads(fn, leaves, cot):
+    out = fn(*leaves)
+    return out, torch.autograd.grad(out, leaves, grad_outputs=cot)
+
+
+def test_fused_ops_are_differentiable_fp32(dev):
+    """FusedSwiGLU, FusedLayerNormLinear, FusedPairBias and FusedLayerNormTranspose under grad
+    (swiglu.py:60-95, layernorm_linear.py:164-322, fused_pair_bias.py, layernorm_transpose.py:95-161)
+    against torch's formulas differentiated in fp64."""
+    fused = mod("fused")
+    g = torch.Generator().manual_seed(7)
+    # SwiGLU
+    x = torch.randn(300, 2 * 96, generator=g)
+    cot = torch.randn(300, 96, generator=g)
+    _, got = _grads(fused.FusedSwiGLU(), [x.to(dev).requires_grad_(True)], cot.to(dev))
+    _, want = _grads(lambda t: F.silu(t[:, :96]) * t[:, 96:], [x.double().requires_grad_(True)], cot.double())
+    assert_fp32_close(got[0].cpu(), want[0].float(), what="FusedSwiGLU dx")
+    # LayerNorm + linear with bias, W as [K, N]
+    K, N = 128, 64
+    X = torch.randn(4, 50, K, generator=g)
+    lw, lb = 1 + 0.1 * torch.randn(K, generator=g), 0.1 * torch.randn(K, generator=g)
+    Wt, bias = torch.randn(K, N, generator=g) / K**0.5, torch.randn(N, generator=g)
+    cot = torch.randn(4, 50, N, generator=g)
+    op = fused.FusedLayerNormLinear(K, N, has_linear_bias=True)
+    _, got = _grads(op, [t.to(dev).requires_grad_(True) for t in (X, lw, lb, Wt, bias)], cot.to(dev))
+    _, want = _grads(lambda a, w, b, W_, bb: F.layer_norm(a, (K,), w, b, 1e-5) @ W_ + bb,
+                     [t.double().requires_grad_(True) for t in (X, lw, lb, Wt, bias)], cot.double())  # fmt: skip
+    for a, r, name in zip(got, want, ("X", "ln_w", "ln_b", "W", "b")):
+        assert_fp32_close(a.cpu(), r.float(), what=f"FusedLayerNormLinear d{name}")
+    # pair bias with a mask, and LayerNorm + transpose
+    B, Nr, C, H = 1, 20, 128, 4
+    z = torch.randn(B, Nr, Nr, C, generator=g)
+    pw = torch.randn(H, C, generator=g) / C**0.5
+    mask = (torch.rand(B, Nr, generator=g) > 0.2).float()
+    cot = torch.randn(B, H, Nr, Nr, generator=g)
+    _, got = _grads(lambda a, w, b, p: fused.FusedPairBias(C, H)(a, w, b, p, mask.to(dev)),
+                    [t.to(dev).requires_grad_(True) for t in (z, lw, lb, pw)], cot.to(dev))  # fmt: skip
+    _, want = _grads(lambda a, w, b, p: F.linear(F.layer_norm(a, (C,), w, b, 1e-5), p).permute(0, 3, 1, 2),
+                     [t.double().requires_grad_(True) for t in (z, lw, lb, pw)], cot.double())  # fmt: skip
+    for a, r, name in zip(got, want, ("z", "ln_w", "ln_b", "proj_w")):
+        assert_fp32_close(a.cpu(), r.float(), what=f"FusedPairBias d{name}")
+    cot = torch.randn(B, Nr, Nr, C, generator=g)
+    _, got = _grads(fused.FusedLayerNormTranspose(C, True), [t.to(dev).requires_grad_(True) for t in (z, lw, lb)],
+                    cot.to(dev))  # fmt: skip
+    _, want = _grads(lambda a, w, b: F.layer_norm(a, (C,), w, b, 1e-5).permute(0, 2, 1, 3),
+                     [t.double().requires_grad_(True) for t in (z, lw, lb)], cot.double())  # fmt: skip
+    for a, r, name in zip(got, want, ("x", "w", "b")):
+        assert_fp32_close(a.cpu(), r.float(), what=f"FusedLayerNormTranspose d{name}")
