@@ -12,12 +12,14 @@
 // gradient of its rows is 0: the reference kernel's masked-row rule (its forward writes 0).
 //
 // Kernels, all on 32x32 MFMA tiles with D = 32:
-//   attn_bwd_transpose: K, Q, dO transposed to [d][row] once, so that the products that
-//                  contract over rows (dQ over keys, dK and dV over queries) load their
-//                  fragments straight from memory.
-//   attn_bwd_dq:   query-major. Pass 1 over the keys builds (LSE, dP_imax, imax, C) per row
-//                  online (running max with rescaling and re-centring); pass 2 forms dS and
-//                  dQ. The row statistics go to the workspace for the other kernels.
+//   attn_bwd_relayout: K, Q, dO, V copied once into MFMA fragment order, as themselves and
+//                  (K, Q, dO) transposed for the products that contract over rows (dQ over
+//                  keys, dK and dV over queries): every fragment load of a wave is then one
+//                  contiguous 1 KB piece.
+//   attn_bwd_dq:   query-major. Pass 1 over the keys finds each row's maximum logit and first
+//                  argmax; pass 2 forms P, dP and the centred sums and the two products whose
+//                  difference is dQ, and leaves (LSE, dP_imax, imax, C) per row in the
+//                  workspace for the other kernels.
 //   attn_bwd_dkdv: key-major, loops over query tiles: dV^T += dO^T P, dK^T += Q^T dS.
 //   attn_bwd_db:   one (query tile, key tile) of one (b, h), loops over a group of lines and
 //                  sums dS in registers; the groups' partial sums are added in a fixed order,
@@ -41,26 +43,19 @@ constexpr int kSubKv = 1;          // 32-key sub-tiles per wave in the dK / dV k
 // Zero masked-row rule threshold in log2 units (the reference tests t < -1e8).
 constexpr float kDeadLog2 = -1.0e8f * kLog2e;
 
-// An A fragment whose k order matches bfrag_from_acc (the accumulator's row order):
-// bf16 step t of 2: element e is k = 16t + 8(e>>2) + 4h + (e&3); fp32 step t of 4:
-// element e is k = 8t + 4h + e. `row` points at the A row in LDS, k contiguous.
+// Tile row that element e of step t of lane half h's A fragment reads, for a product that
+// contracts over the 32 rows of a tile with the other operand from bfrag_from_acc (the
+// accumulator's row order): bf16 step t of 2 reads rows 16t + 8(e>>2) + 4h + (e&3), fp32
+// step t of 4 reads rows 8t + 4h + e.
 template <class TC>
-PF_DEVICE typename Mfma<TC>::Frag afrag_perm(const TC* row, int t, int h);
+PF_DEVICE int frag_row(int t, int h, int e);
 template <>
-PF_DEVICE bf16x8 afrag_perm<bf16>(const bf16* row, int t, int h) {
-  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 16 * t + 4 * h);
-  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 16 * t + 8 + 4 * h);
-  bf16x8 f;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    f[e] = lo[e];
-    f[4 + e] = hi[e];
-  }
-  return f;
+PF_DEVICE int frag_row<bf16>(int t, int h, int e) {
+  return 16 * t + 8 * (e >> 2) + 4 * h + (e & 3);
 }
 template <>
-PF_DEVICE f32x4 afrag_perm<float>(const float* row, int t, int h) {
-  return *reinterpret_cast<const f32x4*>(row + 8 * t + 4 * h);
+PF_DEVICE int frag_row<float>(int t, int h, int e) {
+  return 8 * t + 4 * h + e;
 }
 
 // A 32x32 accumulator (lane: column l&31, rows 8(r>>2) + 4h + (r&3)) as the B operand of a
@@ -82,43 +77,66 @@ PF_DEVICE f32x4 bfrag_from_acc<float>(const f32x16& acc, int t) {
 // Accumulator row r of lane half h.
 PF_DEVICE int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-// XT [line][d][Np] = X [line][n][d] for n < N, 0 for N <= n < Np, for the three operands a
-// contraction over rows needs with rows along the lanes' k slices (blockIdx.z: K, Q, dO).
+// One 32-row tile of an operand in MFMA fragment order, [tile][step][lane][16 bytes], so that
+// every fragment load of a wave is one contiguous 1 KB piece (a row-major tile spreads each
+// step over all 16 of its cache lines). Two orders, written from the same LDS stage:
+//   XR: the fragments of X itself, lane (h, c) of step t holding row c, elements
+//       t K32 + h KPL ..: the operands of Q K^T, dO V^T (K, Q, dO, V);
+//   XT: the A fragments of X^T, lane (h, c) holding element d = c of the rows frag_row(t, h, .):
+//       the operands of the products that contract over rows, dQ over keys and dK, dV over
+//       queries (K, Q, dO).
+// Rows past N are zero. blockIdx.z: 0 K, 1 Q, 2 dO, 3 V (no XT).
 template <class TC>
-__global__ __launch_bounds__(256) void attn_bwd_transpose_kernel(const TC* __restrict__ K, const TC* __restrict__ Q,
-                                                                 const TC* __restrict__ dO, TC* __restrict__ KT,
-                                                                 TC* __restrict__ QT, TC* __restrict__ OT, int N,
-                                                                 int Np) {
-  constexpr int VEC = 16 / sizeof(TC);
-  constexpr int R = 64;  // rows per block
-  constexpr int LD = R + VEC;
-  __shared__ __attribute__((aligned(16))) TC t[kBD * LD];  // [d][row]
-  const TC* X = blockIdx.z == 0 ? K : (blockIdx.z == 1 ? Q : dO);
-  TC* XT = blockIdx.z == 0 ? KT : (blockIdx.z == 1 ? QT : OT);
+PF_DEVICE size_t frag_offset(size_t line, int Np, int tile, int step, int lane) {
+  constexpr int STEPS = kBD / Mfma<TC>::K32;
+  return (((line * (size_t)(Np / 32) + tile) * STEPS + step) * 64 + lane) * Mfma<TC>::KPL;
+}
+
+template <class TC>
+__global__ __launch_bounds__(256) void attn_bwd_relayout_kernel(const TC* __restrict__ K, const TC* __restrict__ Q,
+                                                                const TC* __restrict__ dO, const TC* __restrict__ V,
+                                                                TC* __restrict__ KR, TC* __restrict__ QR,
+                                                                TC* __restrict__ OR, TC* __restrict__ VR,
+                                                                TC* __restrict__ KT, TC* __restrict__ QT,
+                                                                TC* __restrict__ OT, int N, int Np) {
+  using M = Mfma<TC>;
+  constexpr int VEC = M::KPL;  // elements per 16-byte piece
+  constexpr int STEPS = kBD / M::K32;
+  constexpr int R = 64;          // rows per block: two tiles
+  constexpr int LD = kBD + VEC;  // [row][d] with a 16-byte pad
+  __shared__ __attribute__((aligned(16))) TC t[R * LD];
+  const int z = blockIdx.z;
+  const TC* X = z == 0 ? K : (z == 1 ? Q : (z == 2 ? dO : V));
+  TC* XR = z == 0 ? KR : (z == 1 ? QR : (z == 2 ? OR : VR));
+  TC* XT = z == 0 ? KT : (z == 1 ? QT : OT);
   const size_t line = blockIdx.y;
   const int n0 = blockIdx.x * R;
   const TC* Xl = X + line * N * kBD;
   for (int i = threadIdx.x; i < R * (kBD / VEC); i += 256) {
     const int r = i / (kBD / VEC);
     const int d0 = (i % (kBD / VEC)) * VEC;
-    const int n = n0 + r;
-    TC e[VEC];
-    if (n < N) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(Xl + (size_t)n * kBD + d0);
-      __builtin_memcpy(e, &v, 16);
-    } else {
-#pragma unroll
-      for (int u = 0; u < VEC; ++u) e[u] = from_f32<TC>(0.f);
-    }
-#pragma unroll
-    for (int u = 0; u < VEC; ++u) t[(d0 + u) * LD + r] = e[u];
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (n0 + r < N) v = *reinterpret_cast<const u32x4*>(Xl + (size_t)(n0 + r) * kBD + d0);
+    *reinterpret_cast<u32x4*>(t + r * LD + d0) = v;
   }
   __syncthreads();
-  TC* XTl = XT + line * kBD * Np;
-  for (int i = threadIdx.x; i < kBD * (R / VEC); i += 256) {
-    const int d = i / (R / VEC);
-    const int r0 = (i % (R / VEC)) * VEC;
-    *reinterpret_cast<u32x4*>(XTl + (size_t)d * Np + n0 + r0) = *reinterpret_cast<const u32x4*>(t + d * LD + r0);
+  // piece i = (tile jj, step st, lane): consecutive threads write consecutive 16 bytes
+  const size_t base = frag_offset<TC>(line, Np, n0 / 32, 0, 0);
+  for (int i = threadIdx.x; i < 2 * STEPS * 64; i += 256) {
+    const int jj = i / (STEPS * 64);
+    const int st = (i / 64) % STEPS;
+    const int h = (i >> 5) & 1;
+    const int c = i & 31;
+    *reinterpret_cast<u32x4*>(XR + base + (size_t)i * VEC) =
+        *reinterpret_cast<const u32x4*>(t + (32 * jj + c) * LD + st * M::K32 + h * VEC);
+    if (z < 3) {
+      TC e[VEC];
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) e[u] = t[(32 * jj + frag_row<TC>(st, h, u)) * LD + c];
+      u32x4 v;
+      __builtin_memcpy(&v, e, 16);
+      *reinterpret_cast<u32x4*>(XT + base + (size_t)i * VEC) = v;
+    }
   }
 }
 
@@ -156,27 +174,50 @@ PF_DEVICE f32x4 stats_pack(float lse2, float ref, float cen, int imax) {
 }
 
 // ------------------------------------------------------------------ dQ (+ row statistics)
-// Block: four lines of one (b, h) sharing a double-buffered pair-bias tile in LDS; each wave
-// owns one line and kRows queries (kSub sub-tiles of 32, the columns of S^T = K Q^T). The
-// next key tile's K / V / K^T fragments and mask are fetched while the current one computes.
+// Block: four lines of one (b, h) sharing a double-buffered pair-bias tile in LDS, which
+// also holds the four lines' key masks; each wave owns one line and kRows queries (kSub
+// sub-tiles of 32, the columns of S^T = K Q^T). The next key tile's fragments, bias and
+// masks are fetched while the current one computes.
+//
+// Pass 1 forms the logits only and keeps each row's maximum m and first argmax. The
+// reference value dP_imax = dO_i . v_imax is then one gathered dot product, and pass 2 needs
+// no rescaling: with p_j = exp2(x_j - m) and W = sum_j p_j it accumulates W, C W = sum_j p_j
+// u_j and the two products A = sum_j p_j u_j k_j and B = sum_j p_j k_j, so that
+// dQ = scale (A - C B) / W. Each term of A and of C B is O(1 - P_imax): nothing of order one
+// is cancelled, as in the per-element form P (u - C).
 template <class TC>
 struct DqOps {
   typename Mfma<TC>::Frag k[kBD / Mfma<TC>::K32], v[kBD / Mfma<TC>::K32], kt[kBD / Mfma<TC>::K32];
-  f32x4 m[4];
 };
 
+// Dot product of two fragments (the same k slice of two rows), in fp32.
+PF_DEVICE float frag_dot(const bf16x8& a, const bf16x8& b) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s = fmaf((float)a[e], (float)b[e], s);
+  return s;
+}
+PF_DEVICE float frag_dot(const f32x4& a, const f32x4& b) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s = fmaf(a[e], b[e], s);
+  return s;
+}
+
 template <class TC, int kSub>
-__global__ __launch_bounds__(kNT) void attn_bwd_dq_kernel(const TC* __restrict__ Q, const TC* __restrict__ K,
-                                                          const TC* __restrict__ V, const TC* __restrict__ dO,
-                                                          const TC* __restrict__ KT, const float* __restrict__ mask2,
-                                                          const float* __restrict__ bias2, int S, int H, int N,
-                                                          int Np, float scale, TC* __restrict__ dQ,
-                                                          f32x4* __restrict__ st4) {
+__global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kernel(const TC* __restrict__ QR, const TC* __restrict__ KR,
+                                                             const TC* __restrict__ VR, const TC* __restrict__ OR,
+                                                             const TC* __restrict__ V, const TC* __restrict__ KT,
+                                                             const float* __restrict__ mask2,
+                                                             const float* __restrict__ bias2, int S, int H, int N,
+                                                             int Np, float scale, TC* __restrict__ dQ,
+                                                             f32x4* __restrict__ st4) {
   using M = Mfma<TC>;
   constexpr int STEPS = kBD / M::K32;
   constexpr int kRows = 32 * kSub;
   constexpr int BLD = 36;  // bias stage [query][32 keys + 4]
   __shared__ __attribute__((aligned(16))) float bstage[2][kRows * BLD];
+  __shared__ __attribute__((aligned(16))) float mstage[2][kLines * 32];  // [line][key]
 
   const int bh = blockIdx.z;
   const int b = bh / H;
@@ -189,10 +230,9 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dq_kernel(const TC* __restrict__
   const bool active = s < S;  // inactive waves mirror the group's first line and skip the math
   const long bs = (long)b * S + (active ? s : (int)blockIdx.y * kLines);
   const size_t line = (size_t)bs * H + hd;
-  const size_t lo = line * N * kBD;
-  const TC *Kl = K + lo, *Vl = V + lo;
-  const TC* KTl = KT + line * kBD * Np;
-  const float* m2l = mask2 + bs * Np;
+  const TC* Vl = V + line * N * kBD;
+  // line whose key mask thread t < 128 stages (the four lines of the group, clamped)
+  const float* m2s = mask2 + ((long)b * S + min((int)blockIdx.y * kLines + (int)(threadIdx.x >> 5), S - 1)) * Np;
   const float* b2l = bias2 + (size_t)bh * Np * Np;
   const int q0 = blockIdx.x * kRows;
   const float sl2 = scale * kLog2e;
@@ -201,15 +241,15 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dq_kernel(const TC* __restrict__
   typename M::Frag qf[kSub][STEPS], of[kSub][STEPS];
 #pragma unroll
   for (int sub = 0; sub < kSub; ++sub) {
-    const int qc = min(q0 + 32 * sub + c, N - 1);
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
-      qf[sub][t] = M::load(Q + lo + (size_t)qc * kBD + t * M::K32 + hh * M::KPL);
-      of[sub][t] = M::load(dO + lo + (size_t)qc * kBD + t * M::K32 + hh * M::KPL);
+      qf[sub][t] = M::load(QR + frag_offset<TC>(line, Np, q0 / 32 + sub, t, l));
+      of[sub][t] = M::load(OR + frag_offset<TC>(line, Np, q0 / 32 + sub, t, l));
     }
   }
 
   f32x4 pf[2];
+  float pm = 0.f;
   constexpr int BU = kRows * 8 / kNT;  // 16-byte bias loads per thread per step
   auto bias_load = [&](int k0) {
 #pragma unroll
@@ -217,6 +257,7 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dq_kernel(const TC* __restrict__
       const int i = threadIdx.x + u * kNT;
       pf[u] = *reinterpret_cast<const f32x4*>(b2l + (size_t)(q0 + (i >> 3)) * Np + k0 + (i & 7) * 4);
     }
+    if (threadIdx.x < kLines * 32) pm = m2s[k0 + (threadIdx.x & 31)];
   };
   auto bias_store = [&](int st) {
 #pragma unroll
@@ -224,47 +265,39 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dq_kernel(const TC* __restrict__
       const int i = threadIdx.x + u * kNT;
       *reinterpret_cast<f32x4*>(&bstage[st][(i >> 3) * BLD + (i & 7) * 4]) = pf[u];
     }
+    if (threadIdx.x < kLines * 32) mstage[st][threadIdx.x] = pm;
   };
-  auto fetch = [&](int k0, DqOps<TC>& o, bool with_kt) {
-    const int kc = min(k0 + c, N - 1);
+  // K (pass 1); V and K^T as well (pass 2)
+  auto fetch = [&](int k0, DqOps<TC>& o, bool full) {
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
-      o.k[t] = M::load(Kl + (size_t)kc * kBD + t * M::K32 + hh * M::KPL);
-      o.v[t] = M::load(Vl + (size_t)kc * kBD + t * M::K32 + hh * M::KPL);
-      if (with_kt) o.kt[t] = afrag_perm<TC>(KTl + (size_t)c * Np + k0, t, hh);
+      o.k[t] = M::load(KR + frag_offset<TC>(line, Np, k0 / 32, t, l));
+      if (full) {
+        o.v[t] = M::load(VR + frag_offset<TC>(line, Np, k0 / 32, t, l));
+        o.kt[t] = M::load(KT + frag_offset<TC>(line, Np, k0 / 32, t, l));
+      }
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o.m[j] = *reinterpret_cast<const f32x4*>(m2l + k0 + 8 * j + 4 * hh);
   };
-  // log2 logits x and dP^T for keys k0..k0+31 (rows) and this wave's queries (columns)
-  auto tile = [&](const DqOps<TC>& o, int st, f32x16 (&x)[kSub], f32x16 (&dp)[kSub]) {
+  // log2 logits from the raw scores for keys k0..k0+31 (rows) and sub-tile `sub` (columns)
+  auto logits = [&](const f32x16& sa, int st, int sub, f32x16& x) {
+    const float* brow = &bstage[st][(32 * sub + c) * BLD];
+    const float* mrow2 = &mstage[st][w * 32];
 #pragma unroll
-    for (int sub = 0; sub < kSub; ++sub) {
-      f32x16 sa = {};
-      dp[sub] = f32x16{};
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 b4 = *reinterpret_cast<const f32x4*>(brow + 8 * j + 4 * hh);
+      const f32x4 m4 = *reinterpret_cast<const f32x4*>(mrow2 + 8 * j + 4 * hh);
 #pragma unroll
-      for (int t = 0; t < STEPS; ++t) {
-        M::mma32(sa, o.k[t], qf[sub][t]);
-        M::mma32(dp[sub], o.v[t], of[sub][t]);
-      }
-      const float* brow = &bstage[st][(32 * sub + c) * BLD];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 b4 = *reinterpret_cast<const f32x4*>(brow + 8 * j + 4 * hh);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[sub][4 * j + e] = logit2(sa[4 * j + e], sl2, b4[e], o.m[j][e]);
-      }
+      for (int e = 0; e < 4; ++e) x[4 * j + e] = logit2(sa[4 * j + e], sl2, b4[e], m4[e]);
     }
   };
 
-  // Pass 1: running max m, first argmax, dP there, and per-lane partial sums
-  // W = sum exp2(x - m), Cp = sum exp2(x - m) (dP - ref) over this lane's keys.
-  float run_max[kSub], refv[kSub], Wp[kSub], Cp[kSub];
+  // Pass 1: maximum and first argmax over this lane's half of the keys (its accumulator
+  // rows ascend in key order, tiles ascend, so a strict > keeps the first).
+  float run_max[kSub];
   int imx[kSub];
 #pragma unroll
   for (int sub = 0; sub < kSub; ++sub) {
     run_max[sub] = -INFINITY;
-    refv[sub] = Wp[sub] = Cp[sub] = 0.f;
     imx[sub] = 0;
   }
   {
@@ -275,77 +308,74 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dq_kernel(const TC* __restrict__
     __syncthreads();
     for (int kt = 0; kt < nkt; ++kt) {
       const int k0 = kt * 32;
-      if (kt + 1 < nkt) {
+      const bool more = kt + 1 < nkt;
+      if (more) {
         bias_load(k0 + 32);
         fetch(k0 + 32, nxt, false);
       }
       if (active) {
-        f32x16 x[kSub], dp[kSub];
-        tile(cur, kt & 1, x, dp);
+        f32x16 sa[kSub];
 #pragma unroll
         for (int sub = 0; sub < kSub; ++sub) {
-          float tmax = x[sub][0];
+          sa[sub] = f32x16{};
 #pragma unroll
-          for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, x[sub][r]);
-          tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-          int targ = INT_MAX;
+          for (int t = 0; t < STEPS; ++t) M::mma32(sa[sub], cur.k[t], qf[sub][t]);
+        }
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (x[sub][r] == tmax) targ = min(targ, k0 + acc_row(r, hh));
-          targ = min(targ, __shfl_xor(targ, 32, 64));
-          float tref = 0.f;
+        for (int sub = 0; sub < kSub; ++sub) {
+          f32x16 x;
+          logits(sa[sub], kt & 1, sub, x);
+          // tile maximum, then its first row (rows ascend in key order: scan downwards)
+          float tmax = x[0];
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (k0 + acc_row(r, hh) == targ) tref = dp[sub][r];
-          tref += __shfl_xor(tref, 32, 64);  // exactly one lane of the pair holds it
-          const bool better = tmax > run_max[sub];
-          const float m_new = better ? tmax : run_max[sub];
-          if (m_new != -INFINITY) {
-            const float alpha = __builtin_amdgcn_exp2f(run_max[sub] - m_new);
-            Wp[sub] *= alpha;
-            Cp[sub] *= alpha;
-            if (better) {
-              Cp[sub] += (refv[sub] - tref) * Wp[sub];  // re-centre the mass seen so far
-              refv[sub] = tref;
-              imx[sub] = targ;
-            }
-            float ws = 0.f, cs = 0.f;
+          for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, x[r]);
+          int trow = 0;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const float p = x[sub][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x[sub][r] - m_new);
-              ws += p;
-              cs += p * (dp[sub][r] - refv[sub]);
-            }
-            Wp[sub] += ws;
-            Cp[sub] += cs;
-            run_max[sub] = m_new;
+          for (int r = 15; r >= 0; --r) trow = x[r] == tmax ? acc_row(r, hh) : trow;
+          if (tmax > run_max[sub]) {
+            run_max[sub] = tmax;
+            imx[sub] = k0 + trow;
           }
         }
       }
-      if (kt + 1 < nkt) bias_store((kt + 1) & 1);
+      if (more) bias_store((kt + 1) & 1);
       __syncthreads();
       cur = nxt;
     }
   }
-  float lse2[kSub], cen[kSub], ref[kSub];
+  // Merge the two halves (larger maximum; the smaller index on a tie), then dP at the argmax.
+  float mrow[kSub], ref[kSub];
   int imax[kSub];
+  bool dead[kSub];
 #pragma unroll
   for (int sub = 0; sub < kSub; ++sub) {
-    const float Wt = Wp[sub] + __shfl_xor(Wp[sub], 32, 64);
-    const float Ct = Cp[sub] + __shfl_xor(Cp[sub], 32, 64);
-    const int q = q0 + 32 * sub + c;
-    const bool dead = !(run_max[sub] >= kDeadLog2) || q >= N;
-    lse2[sub] = dead ? INFINITY : run_max[sub] + __builtin_amdgcn_logf(Wt);
-    cen[sub] = dead ? 0.f : Ct / Wt;
-    ref[sub] = dead ? 0.f : refv[sub];
-    imax[sub] = dead ? -1 : imx[sub];
-    if (active && hh == 0) st4[line * Np + q] = stats_pack(lse2[sub], ref[sub], cen[sub], imax[sub]);
+    const float om = __shfl_xor(run_max[sub], 32, 64);
+    const int oi = __shfl_xor(imx[sub], 32, 64);
+    if (om > run_max[sub] || (om == run_max[sub] && oi < imx[sub])) {
+      run_max[sub] = om;
+      imx[sub] = oi;
+    }
+    const bool live = run_max[sub] >= kDeadLog2;
+    dead[sub] = !live || q0 + 32 * sub + c >= N;
+    mrow[sub] = live ? run_max[sub] : 0.f;
+    imax[sub] = dead[sub] ? -1 : imx[sub];
+    const int iv = live ? imx[sub] : 0;  // < N: keys past N have logit -inf
+    float part = 0.f;
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t)
+      part += frag_dot(of[sub][t], M::load(Vl + (size_t)iv * kBD + t * M::K32 + hh * M::KPL));
+    part += __shfl_xor(part, 32, 64);
+    ref[sub] = dead[sub] ? 0.f : part;
   }
 
-  // Pass 2: dS^T, then dQ^T [d x q] += K^T [d x keys] dS^T [keys x q].
-  f32x16 dq[kSub];
+  // Pass 2: A^T [d x q] += K^T [d x keys] (p u)^T, B^T += K^T p^T, with W and C W per lane.
+  f32x16 da[kSub], db[kSub];
+  float Wp[kSub], Cp[kSub];
 #pragma unroll
-  for (int sub = 0; sub < kSub; ++sub) dq[sub] = f32x16{};
+  for (int sub = 0; sub < kSub; ++sub) {
+    da[sub] = db[sub] = f32x16{};
+    Wp[sub] = Cp[sub] = 0.f;
+  }
   {
     DqOps<TC> cur, nxt;
     fetch(0, cur, true);
@@ -354,42 +384,64 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dq_kernel(const TC* __restrict__
     __syncthreads();
     for (int kt = 0; kt < nkt; ++kt) {
       const int k0 = kt * 32;
-      if (kt + 1 < nkt) {
+      const bool more = kt + 1 < nkt;
+      if (more) {
         bias_load(k0 + 32);
         fetch(k0 + 32, nxt, true);
       }
       if (active) {
-        f32x16 x[kSub], dp[kSub];
-        tile(cur, kt & 1, x, dp);
+        f32x16 sa[kSub], dp[kSub];
 #pragma unroll
         for (int sub = 0; sub < kSub; ++sub) {
-          f32x16 ds;
+          sa[sub] = dp[sub] = f32x16{};
+#pragma unroll
+          for (int t = 0; t < STEPS; ++t) {
+            M::mma32(sa[sub], cur.k[t], qf[sub][t]);
+            M::mma32(dp[sub], cur.v[t], of[sub][t]);
+          }
+        }
+#pragma unroll
+        for (int sub = 0; sub < kSub; ++sub) {
+          f32x16 x;
+          logits(sa[sub], kt & 1, sub, x);
+          f32x16 p, pu;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const float p = __builtin_amdgcn_exp2f(x[sub][r] - lse2[sub]);
+            const float pv = __builtin_amdgcn_exp2f(x[r] - mrow[sub]);
             const float u = (k0 + acc_row(r, hh) == imax[sub]) ? 0.f : dp[sub][r] - ref[sub];
-            ds[r] = p * (u - cen[sub]);
+            p[r] = pv;
+            pu[r] = pv * u;
+            Wp[sub] += pv;
+            Cp[sub] += pu[r];
           }
 #pragma unroll
-          for (int t = 0; t < STEPS; ++t) M::mma32(dq[sub], cur.kt[t], bfrag_from_acc<TC>(ds, t));
+          for (int t = 0; t < STEPS; ++t) {
+            M::mma32(da[sub], cur.kt[t], bfrag_from_acc<TC>(pu, t));
+            M::mma32(db[sub], cur.kt[t], bfrag_from_acc<TC>(p, t));
+          }
         }
       }
-      if (kt + 1 < nkt) bias_store((kt + 1) & 1);
+      if (more) bias_store((kt + 1) & 1);
       __syncthreads();
       cur = nxt;
     }
   }
-  if (!active) return;
 #pragma unroll
   for (int sub = 0; sub < kSub; ++sub) {
+    const float Wt = Wp[sub] + __shfl_xor(Wp[sub], 32, 64);
+    const float Ct = Cp[sub] + __shfl_xor(Cp[sub], 32, 64);
     const int q = q0 + 32 * sub + c;
-    if (q >= N) continue;
-    TC* dst = dQ + lo + (size_t)q * kBD;
+    const float lse2 = dead[sub] ? INFINITY : mrow[sub] + __builtin_amdgcn_logf(Wt);
+    const float cen = dead[sub] ? 0.f : Ct / Wt;
+    if (active && hh == 0) st4[line * Np + q] = stats_pack(lse2, ref[sub], cen, imax[sub]);
+    if (!active || q >= N) continue;
+    const float f = dead[sub] ? 0.f : scale / Wt;
+    TC* dst = dQ + (line * N + q) * kBD;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = dq[sub][4 * j + e] * scale;
+      for (int e = 0; e < 4; ++e) v[e] = (da[sub][4 * j + e] - cen * db[sub][4 * j + e]) * f;
       store_vec<TC, 4>(dst + 8 * j + 4 * hh, v);
     }
   }
@@ -399,22 +451,19 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dq_kernel(const TC* __restrict__
 // Block: four lines of one (b, h); each wave owns one line and kRows keys (the columns of
 // S = Q K^T) and loops over 32-query tiles. A double-buffered LDS step holds the bias tile
 // (transposed, [key][query], so a lane reads its key's rows as 16-byte vectors) and the four
-// lines' row statistics; the next tile's Q / dO / Q^T / dO^T fragments are fetched while the
-// current one computes.
-template <class TC>
-struct DkvOps {
-  typename Mfma<TC>::Frag q[kBD / Mfma<TC>::K32], o[kBD / Mfma<TC>::K32], qt[kBD / Mfma<TC>::K32],
-      ot[kBD / Mfma<TC>::K32];
-};
-
+// lines' row statistics. The Q / dO fragments of the next tile are loaded into the registers
+// of the current ones as soon as S and dP are issued, and the Q^T / dO^T fragments of the
+// current tile at the same point: both loads are covered by the tile's softmax work, and no
+// register copies between tiles are needed.
 template <class TC, int kSub>
-__global__ __launch_bounds__(kNT) void attn_bwd_dkdv_kernel(
-    const TC* __restrict__ Q, const TC* __restrict__ K, const TC* __restrict__ V, const TC* __restrict__ dO,
+__global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dkdv_kernel(
+    const TC* __restrict__ QR, const TC* __restrict__ KR, const TC* __restrict__ VR, const TC* __restrict__ OR,
     const TC* __restrict__ QT, const TC* __restrict__ OT, const float* __restrict__ mask2,
     const float* __restrict__ bias2, int S, int H, int N, int Np, float scale, const f32x4* __restrict__ st4,
     TC* __restrict__ dK, TC* __restrict__ dV) {
   using M = Mfma<TC>;
   constexpr int STEPS = kBD / M::K32;
+  constexpr int EPS = 16 / STEPS;  // accumulator elements per B fragment step
   constexpr int kRows = 32 * kSub;
   constexpr int BLD = 36;  // bias stage [kRows keys][32 queries + 4]
   __shared__ __attribute__((aligned(16))) float bstage[2][kRows * BLD];
@@ -432,9 +481,6 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dkdv_kernel(
   const long bs = (long)b * S + (active ? s : (int)blockIdx.y * kLines);
   const size_t line = (size_t)bs * H + hd;
   const size_t lo = line * N * kBD;
-  const TC *Ql = Q + lo, *Ol = dO + lo;
-  const TC* QTl = QT + line * kBD * Np;
-  const TC* OTl = OT + line * kBD * Np;
   const float* b2l = bias2 + (size_t)bh * Np * Np;
   const int kb0 = blockIdx.x * kRows;
   const float sl2 = scale * kLog2e;
@@ -449,11 +495,10 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dkdv_kernel(
 #pragma unroll
   for (int sub = 0; sub < kSub; ++sub) {
     key[sub] = kb0 + 32 * sub + c;
-    const int kc = min(key[sub], N - 1);
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
-      kf[sub][t] = M::load(K + lo + (size_t)kc * kBD + t * M::K32 + hh * M::KPL);
-      vf[sub][t] = M::load(V + lo + (size_t)kc * kBD + t * M::K32 + hh * M::KPL);
+      kf[sub][t] = M::load(KR + frag_offset<TC>(line, Np, kb0 / 32 + sub, t, l));
+      vf[sub][t] = M::load(VR + frag_offset<TC>(line, Np, kb0 / 32 + sub, t, l));
     }
     mk2[sub] = mask2[bs * Np + key[sub]];
   }
@@ -480,66 +525,72 @@ __global__ __launch_bounds__(kNT) void attn_bwd_dkdv_kernel(
     }
     if (threadIdx.x < kLines * 32) sstage[st][threadIdx.x] = ps;
   };
-  auto fetch = [&](int q0, DkvOps<TC>& o) {
-    const int qc = min(q0 + c, N - 1);
+  typename M::Frag qa[STEPS], oa[STEPS];
+  auto fetch_qo = [&](int q0) {
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
-      o.q[t] = M::load(Ql + (size_t)qc * kBD + t * M::K32 + hh * M::KPL);
-      o.o[t] = M::load(Ol + (size_t)qc * kBD + t * M::K32 + hh * M::KPL);
-      o.qt[t] = afrag_perm<TC>(QTl + (size_t)c * Np + q0, t, hh);
-      o.ot[t] = afrag_perm<TC>(OTl + (size_t)c * Np + q0, t, hh);
+      qa[t] = M::load(QR + frag_offset<TC>(line, Np, q0 / 32, t, l));
+      oa[t] = M::load(OR + frag_offset<TC>(line, Np, q0 / 32, t, l));
     }
   };
 
   f32x16 dk[kSub], dv[kSub];
 #pragma unroll
   for (int sub = 0; sub < kSub; ++sub) dk[sub] = dv[sub] = f32x16{};
-  DkvOps<TC> cur, nxt;
-  fetch(0, cur);
+  if (active) fetch_qo(0);
   stage_load(0);
   stage_store(0);
   __syncthreads();
   for (int qt = 0; qt < nqt; ++qt) {
     const int q0 = qt * 32;
-    if (qt + 1 < nqt) {
-      stage_load(q0 + 32);
-      fetch(q0 + 32, nxt);
-    }
+    const bool more = qt + 1 < nqt;
+    if (more) stage_load(q0 + 32);
     if (active) {
+      f32x16 sa[kSub], dp[kSub];
+#pragma unroll
+      for (int sub = 0; sub < kSub; ++sub) {
+        sa[sub] = dp[sub] = f32x16{};
+#pragma unroll
+        for (int t = 0; t < STEPS; ++t) {
+          M::mma32(sa[sub], qa[t], kf[sub][t]);
+          M::mma32(dp[sub], oa[t], vf[sub][t]);
+        }
+      }
+      typename M::Frag qtf[STEPS], otf[STEPS];
+#pragma unroll
+      for (int t = 0; t < STEPS; ++t) {
+        qtf[t] = M::load(QT + frag_offset<TC>(line, Np, q0 / 32, t, l));
+        otf[t] = M::load(OT + frag_offset<TC>(line, Np, q0 / 32, t, l));
+      }
+      if (more) fetch_qo(q0 + 32);
       const float* bst = bstage[qt & 1];
       const f32x4* sst = &sstage[qt & 1][w * 32];
 #pragma unroll
       for (int sub = 0; sub < kSub; ++sub) {
-        f32x16 sa = {}, dp = {};
 #pragma unroll
         for (int t = 0; t < STEPS; ++t) {
-          M::mma32(sa, cur.q[t], kf[sub][t]);
-          M::mma32(dp, cur.o[t], vf[sub][t]);
-        }
-        f32x16 p, ds;
+          f32x16 p, ds;  // elements EPS t .. EPS t + EPS - 1 are formed and used here
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4 b4 = *reinterpret_cast<const f32x4*>(bst + (32 * sub + c) * BLD + 8 * j + 4 * hh);
+          for (int jj = 0; jj < EPS / 4; ++jj) {
+            const int j = t * (EPS / 4) + jj;
+            const f32x4 b4 = *reinterpret_cast<const f32x4*>(bst + (32 * sub + c) * BLD + 8 * j + 4 * hh);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * j + e;
-            const f32x4 st = sst[8 * j + 4 * hh + e];  // {lse2, ref, cen, imax}
-            const float pv = __builtin_amdgcn_exp2f(logit2(sa[r], sl2, b4[e], mk2[sub]) - st[0]);
-            const float u = (key[sub] == __float_as_int(st[3])) ? 0.f : dp[r] - st[1];
-            p[r] = pv;
-            ds[r] = pv * (u - st[2]);
+            for (int e = 0; e < 4; ++e) {
+              const int r = 4 * j + e;
+              const f32x4 st = sst[8 * j + 4 * hh + e];  // {lse2, ref, cen, imax}
+              const float pv = __builtin_amdgcn_exp2f(logit2(sa[sub][r], sl2, b4[e], mk2[sub]) - st[0]);
+              const float u = (key[sub] == __float_as_int(st[3])) ? 0.f : dp[sub][r] - st[1];
+              p[r] = pv;
+              ds[r] = pv * (u - st[2]);
+            }
           }
-        }
-#pragma unroll
-        for (int t = 0; t < STEPS; ++t) {
-          M::mma32(dv[sub], cur.ot[t], bfrag_from_acc<TC>(p, t));
-          M::mma32(dk[sub], cur.qt[t], bfrag_from_acc<TC>(ds, t));
+          M::mma32(dv[sub], otf[t], bfrag_from_acc<TC>(p, t));
+          M::mma32(dk[sub], qtf[t], bfrag_from_acc<TC>(ds, t));
         }
       }
     }
-    if (qt + 1 < nqt) stage_store((qt + 1) & 1);
+    if (more) stage_store((qt + 1) & 1);
     __syncthreads();
-    cur = nxt;
   }
   if (!active) return;
 #pragma unroll
@@ -573,8 +624,8 @@ struct DbOps {
 };
 
 template <class TC>
-__global__ __launch_bounds__(kNT) void attn_bwd_db_kernel(const TC* __restrict__ Q, const TC* __restrict__ K,
-                                                          const TC* __restrict__ V, const TC* __restrict__ dO,
+__global__ __launch_bounds__(kNT, 3) void attn_bwd_db_kernel(const TC* __restrict__ QR, const TC* __restrict__ KR,
+                                                          const TC* __restrict__ VR, const TC* __restrict__ OR,
                                                           const float* __restrict__ mask2,
                                                           const float* __restrict__ bias2, int S, int H, int N,
                                                           int Np, float scale, int groups,
@@ -590,9 +641,7 @@ __global__ __launch_bounds__(kNT) void attn_bwd_db_kernel(const TC* __restrict__
   const int hh = l >> 5;
   const int c = l & 31;
   const int q = blockIdx.x * 64 + (w & 1) * 32 + c;
-  const int qc = min(q, N - 1);
   const int k0 = blockIdx.y * 64 + (w >> 1) * 32;
-  const int kc = min(k0 + c, N - 1);
   const float sl2 = scale * kLog2e;
   const int s_begin = (int)((long)S * grp / groups);
   const int s_end = (int)((long)S * (grp + 1) / groups);
@@ -603,14 +652,12 @@ __global__ __launch_bounds__(kNT) void attn_bwd_db_kernel(const TC* __restrict__
   auto fetch = [&](int s, DbOps<TC>& op) {
     const long bs = (long)b * S + s;
     const size_t line = (size_t)bs * H + hd;
-    const size_t lo = line * N * kBD;
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
-      const int dofs = t * M::K32 + hh * M::KPL;
-      op.k[t] = M::load(K + lo + (size_t)kc * kBD + dofs);
-      op.q[t] = M::load(Q + lo + (size_t)qc * kBD + dofs);
-      op.v[t] = M::load(V + lo + (size_t)kc * kBD + dofs);
-      op.o[t] = M::load(dO + lo + (size_t)qc * kBD + dofs);
+      op.k[t] = M::load(KR + frag_offset<TC>(line, Np, k0 / 32, t, l));
+      op.q[t] = M::load(QR + frag_offset<TC>(line, Np, q / 32, t, l));
+      op.v[t] = M::load(VR + frag_offset<TC>(line, Np, k0 / 32, t, l));
+      op.o[t] = M::load(OR + frag_offset<TC>(line, Np, q / 32, t, l));
     }
     op.st = st4[line * Np + q];
 #pragma unroll
@@ -671,7 +718,7 @@ int db_groups(int B, int H, int N, int S) {
 }
 
 struct BwdWs {
-  size_t st, bias2, mask2, kt, qt, ot, part, total;
+  size_t st, bias2, mask2, kr, qr, orr, vr, kt, qt, ot, part, total;
   int groups;
 };
 
@@ -689,6 +736,10 @@ BwdWs bwd_ws_layout(int B, int S, int H, int N, int es) {
   w.st = take(lines * Np * 16);
   w.bias2 = take((size_t)B * H * Np * Np * 4);
   w.mask2 = take((size_t)B * S * Np * 4);
+  w.kr = take(lines * kBD * Np * es);
+  w.qr = take(lines * kBD * Np * es);
+  w.orr = take(lines * kBD * Np * es);
+  w.vr = take(lines * kBD * Np * es);
   w.kt = take(lines * kBD * Np * es);
   w.qt = take(lines * kBD * Np * es);
   w.ot = take(lines * kBD * Np * es);
@@ -706,6 +757,10 @@ int attn_bwd_launch(const void* q, const void* k, const void* v, const float* re
   f32x4* st4 = reinterpret_cast<f32x4*>(base + lay.st);
   float* bias2 = reinterpret_cast<float*>(base + lay.bias2);
   float* mask2 = reinterpret_cast<float*>(base + lay.mask2);
+  TC* KR = reinterpret_cast<TC*>(base + lay.kr);
+  TC* QR = reinterpret_cast<TC*>(base + lay.qr);
+  TC* OR = reinterpret_cast<TC*>(base + lay.orr);
+  TC* VR = reinterpret_cast<TC*>(base + lay.vr);
   TC* KT = reinterpret_cast<TC*>(base + lay.kt);
   TC* QT = reinterpret_cast<TC*>(base + lay.qt);
   TC* OT = reinterpret_cast<TC*>(base + lay.ot);
@@ -719,20 +774,21 @@ int attn_bwd_launch(const void* q, const void* k, const void* v, const float* re
         pair_bias, res_mask, bias2, mask2, B * H, B * S, N, Np);
     if (int e = pf::check_launch("attn_bwd_prep")) return e;
   }
-  attn_bwd_transpose_kernel<TC><<<dim3((unsigned)(Np / 64), lines, 3), 256, 0, s>>>(K, Q, dO, KT, QT, OT, N, Np);
-  if (int e = pf::check_launch("attn_bwd_transpose")) return e;
+  attn_bwd_relayout_kernel<TC><<<dim3((unsigned)(Np / 64), lines, 4), 256, 0, s>>>(K, Q, dO, V, KR, QR, OR, VR, KT,
+                                                                                   QT, OT, N, Np);
+  if (int e = pf::check_launch("attn_bwd_relayout")) return e;
   const unsigned lg = (unsigned)((S + kLines - 1) / kLines);
-  attn_bwd_dq_kernel<TC, kSubDq><<<dim3((unsigned)(Np / (32 * kSubDq)), lg, (unsigned)(B * H)), kNT, 0, s>>>(Q, K, V, dO, KT, mask2, bias2, S, H, N, Np, scale, static_cast<TC*>(dq),
-                                            st4);
+  attn_bwd_dq_kernel<TC, kSubDq><<<dim3((unsigned)(Np / (32 * kSubDq)), lg, (unsigned)(B * H)), kNT, 0, s>>>(
+      QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N, Np, scale, static_cast<TC*>(dq), st4);
   if (int e = pf::check_launch("attn_bwd_dq")) return e;
-  attn_bwd_dkdv_kernel<TC, kSubKv><<<dim3((unsigned)(Np / (32 * kSubKv)), lg, (unsigned)(B * H)), kNT, 0, s>>>(Q, K, V, dO, QT, OT, mask2, bias2, S, H, N, Np, scale, st4,
-                                              static_cast<TC*>(dk), static_cast<TC*>(dv));
+  attn_bwd_dkdv_kernel<TC, kSubKv><<<dim3((unsigned)(Np / (32 * kSubKv)), lg, (unsigned)(B * H)), kNT, 0, s>>>(
+      QR, KR, VR, OR, QT, OT, mask2, bias2, S, H, N, Np, scale, st4, static_cast<TC*>(dk), static_cast<TC*>(dv));
   if (int e = pf::check_launch("attn_bwd_dkdv")) return e;
   const unsigned nb = (unsigned)((N + 63) / 64);
   const int G = lay.groups;
   float* part = G > 1 ? reinterpret_cast<float*>(base + lay.part) : dbias;
-  attn_bwd_db_kernel<TC><<<dim3(nb, nb, (unsigned)(B * H * G)), kNT, 0, s>>>(Q, K, V, dO, mask2, bias2, S, H, N, Np,
-                                                                             scale, G, st4, part);
+  attn_bwd_db_kernel<TC><<<dim3(nb, nb, (unsigned)(B * H * G)), kNT, 0, s>>>(QR, KR, VR, OR, mask2, bias2, S, H, N,
+                                                                             Np, scale, G, st4, part);
   if (int e = pf::check_launch("attn_bwd_db")) return e;
   if (G > 1) {
     const size_t n = (size_t)B * H * N * N;
