@@ -87,21 +87,25 @@ class GridSelfAttention(nn.Module):
         H, D = self.num_heads, self.head_dim
         if D != 32:
             raise NotActive("GridSelfAttention", f"head dim {D}: the differentiable attention is built for 32")
-        from .kernels import LayerNormFunction
+        from .kernels import LayerNormFunction, token_linear
 
         zn = LayerNormFunction.apply(z, self.norm.weight, self.norm.bias, self.norm.eps)
-        pb = F.linear(zn, self.pair_bias.weight).permute(0, 3, 1, 2)  # [B, H, N, N], un-transposed z
+        pb = token_linear(zn, self.pair_bias.weight).permute(0, 3, 1, 2)  # [B, H, N, N], un-transposed z
+        # q, k, v, g in one product over the un-transposed tokens; the column mode's lines are
+        # the second token axis, taken by the permutation into the attention frame.
+        w_qkvg = torch.cat([self.to_q.weight, self.to_k.weight, self.to_v.weight, self.to_g.weight])
+        y = token_linear(zn, w_qkvg).view(B, N, N, 4, H, D).unbind(3)  # backward: one stack
+        frame = (0, 2, 3, 1, 4) if self.transpose else (0, 1, 3, 2, 4)  # [B, line, H, key, D]
+        qkv = [t.permute(*frame).contiguous() for t in y[:3]]
         if self.transpose:
-            zn, mask = zn.transpose(1, 2), mask.transpose(1, 2)
-        qkv = [F.linear(zn, lin.weight).reshape(B, N, N, H, D).transpose(-2, -3).contiguous()
-               for lin in (self.to_q, self.to_k, self.to_v)]  # fmt: skip
+            mask = mask.transpose(1, 2)
         res_mask = torch.where(mask > 0.5, 0.0, -1e9).view(B, N, 1, 1, N)
         o = _EvoformerAttention.apply(*qkv, res_mask, pb.unsqueeze(1).float(), True)
-        o = o.transpose(-2, -3).reshape(B, N, N, H * D)
-        g = torch.sigmoid(F.linear(zn, self.to_g.weight))
+        back = (0, 3, 1, 2, 4) if self.transpose else (0, 1, 3, 2, 4)  # to [B, N, N, H, D]
+        o = o.permute(*back).reshape(B, N, N, H * D)
+        g = torch.sigmoid(y[3].reshape(B, N, N, H * D))
         w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
-        out = F.linear(o * g, w_out)
-        return out.transpose(1, 2) if self.transpose else out
+        return token_linear(o * g, w_out)
 
     def forward(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
         """The update for z [B?, N, N, C], mask [B?, N, N] (not added to z). Under grad it

@@ -723,7 +723,9 @@ __global__ __launch_bounds__(256) void trimul_project32_kernel(const TZ* __restr
 // the other half of a double-buffered LDS tile. The two waves that share a SIMD (w, w + 4)
 // work out of phase: waves 4-7 LayerNorm first and then run their GEMMs, waves 0-3 run their
 // GEMMs first and LayerNorm after, so each wave's MFMAs overlap the other's LayerNorm and
-// gating VALU work. One barrier per tile publishes the next tile's LayerNorm.
+// gating VALU work. One barrier per tile publishes the next tile's LayerNorm. NORM = false
+// (the training forward, whose input is already LayerNormed in autograd) only rounds the rows
+// to bf16 in that step.
 struct ProjectWs {
   static constexpr int C = 128;
   static constexpr int BP = 64;   // positions per tile
@@ -733,7 +735,7 @@ struct ProjectWs {
   static constexpr int SLD = BP + 8;  // stage rows (bf16)
 };
 
-template <class TZ>
+template <class TZ, bool NORM = true>
 __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
     const TZ* __restrict__ z, const float* __restrict__ mask, const float* __restrict__ lnw,
     const float* __restrict__ lnb, float eps, const bf16* __restrict__ w4, bf16* __restrict__ planes, int B, int N,
@@ -775,8 +777,8 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
   float lw[VEC], lb[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) {
-    lw[e] = lnw[chunk * VEC + e];
-    lb[e] = lnb[chunk * VEC + e];
+    lw[e] = NORM ? lnw[chunk * VEC + e] : 1.f;
+    lb[e] = NORM ? lnb[chunk * VEC + e] : 0.f;
   }
 
   auto tile_coords = [&](int tile, int& b, int& line, int& t0) {
@@ -815,19 +817,21 @@ __global__ __launch_bounds__(ProjectWs::NT) void trimul_project_ws_kernel(
     for (int q = 0; q < NLD; ++q) {
       float v[VEC];
       unpack16<TZ>(zr[set][q], v);
-      float sum = 0.f;
+      if constexpr (NORM) {
+        float sum = 0.f;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) sum += v[e];
-      const float mean = row_group_sum<LPR>(sum) * (1.0f / C);
-      float sq = 0.f;
+        for (int e = 0; e < VEC; ++e) sum += v[e];
+        const float mean = row_group_sum<LPR>(sum) * (1.0f / C);
+        float sq = 0.f;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float d = v[e] - mean;
-        sq += d * d;
+        for (int e = 0; e < VEC; ++e) {
+          const float d = v[e] - mean;
+          sq += d * d;
+        }
+        const float rstd = rsqrtf(row_group_sum<LPR>(sq) * (1.0f / C) + eps);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = (v[e] - mean) * rstd * lw[e] + lb[e];
       }
-      const float rstd = rsqrtf(row_group_sum<LPR>(sq) * (1.0f / C) + eps);
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) v[e] = (v[e] - mean) * rstd * lw[e] + lb[e];
       const int row = w * RPW + q * RPI + l / LPR;
       store_vec<bf16, VEC>(xs[buf] + row * XLD + chunk * VEC, v);
       if (chunk == 0) mks[buf][row] = (okb[set] >> q) & 1u ? mkn[set][q] : 0.f;
@@ -1349,8 +1353,19 @@ int trimul_train_launch(const void* x, const float* mask, const void* w4, const 
   TC* Q = planes + (size_t)B * C * pe;
   TC* X = planes + (size_t)2 * B * C * pe;
   constexpr int BM = trimul_bm<TC>();
-  trimul_project_kernel<TZ, TC, C, false><<<dim3(Np / BM, Np, B), 256, 0, s>>>(
-      (const TZ*)x, mask, nullptr, nullptr, 0.f, (const TC*)w4, planes, B, N, Np, outgoing);
+  if constexpr (sizeof(TC) == 2 && C == 128) {
+    // the persistent K1 without its LayerNorm; weights packed in 32-channel blocks
+    const long ntiles = (long)B * Np * (Np / ProjectWs::BP);
+    PF_REQUIRE(ntiles < (1L << 31), PF_ERR_UNSUPPORTED, "trimul_train_project: B=%d N=%d (B Np Np/64 must stay below 2^31)",
+               B, N);
+    const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+    trimul_project_ws_kernel<TZ, false><<<nblk, ProjectWs::NT, 0, s>>>((const TZ*)x, mask, nullptr, nullptr, 0.f,
+                                                                       (const bf16*)w4, (bf16*)planes, B, N, Np,
+                                                                       outgoing);
+  } else {
+    trimul_project_kernel<TZ, TC, C, false><<<dim3(Np / BM, Np, B), 256, 0, s>>>(
+        (const TZ*)x, mask, nullptr, nullptr, 0.f, (const TC*)w4, planes, B, N, Np, outgoing);
+  }
   if (int e = pf::check_launch("trimul_train_project")) return e;
   const int G = B * C;
   const int remap = (G % 8 == 0) ? 1 : 0;
@@ -1447,16 +1462,19 @@ int pf_trimul_train_pack_weights(const void* w_proj, const void* w_gate, int wdt
              "pf_trimul_train_pack_weights: C=%d (built: 64, 128, 256)", C);
   PF_REQUIRE((wdtype == PF_F32 || wdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16), PF_ERR_UNSUPPORTED,
              "pf_trimul_train_pack_weights: bad dtype");
+  // the K1 and project VJP that read them: 32-channel blocks for bf16 C = 128 (persistent
+  // kernels), 16 otherwise
+  const int cb = (cdtype == PF_BF16 && C == 128) ? 32 : 16;
   hipStream_t s = pf::as_stream(stream);
   dim3 grid((4 * C * C + 255) / 256);
   if (wdtype == PF_F32 && cdtype == PF_F32)
-    trimul_pack_kernel<float, float><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (float*)packed, C, 16);
+    trimul_pack_kernel<float, float><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (float*)packed, C, cb);
   else if (wdtype == PF_F32)
-    trimul_pack_kernel<float, bf16><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (bf16*)packed, C, 16);
+    trimul_pack_kernel<float, bf16><<<grid, 256, 0, s>>>((const float*)w_proj, (const float*)w_gate, (bf16*)packed, C, cb);
   else if (cdtype == PF_F32)
-    trimul_pack_kernel<bf16, float><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (float*)packed, C, 16);
+    trimul_pack_kernel<bf16, float><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (float*)packed, C, cb);
   else
-    trimul_pack_kernel<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (bf16*)packed, C, 16);
+    trimul_pack_kernel<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)w_proj, (const bf16*)w_gate, (bf16*)packed, C, cb);
   return pf::check_launch("pf_trimul_train_pack_weights");
 }
 

@@ -389,17 +389,18 @@ __global__ __launch_bounds__(256) void trimul_project_vjp_kernel(const TC* __res
         G[p * GLD + wrow0[j] + (l & 15)] = from_f32<TC>(acc[rb][j][r]);
       }
   __syncthreads();
-  // G channel-major [4C][M] in this kernel's walk order (position (line, t) at
-  // b N^2 + line N + t): rows of contiguous positions. For the outgoing direction that is the
+  // G token-major [M][4C] in this kernel's walk order (position (line, t) at row
+  // b N^2 + line N + t): the tile's rows are contiguous. For the outgoing direction that is the
   // token order; for the incoming one x is written in the same order (xw, before the tile is
-  // reused), so that the packed weights' gradient G xw needs no transposed copy.
+  // reused), so that the packed weights' gradient G^T xw needs no transposed copy.
   {
-    const size_t M = (size_t)B * N * N;
-    for (int idx = tid; idx < BM * 4 * C; idx += NT) {
-      const int k = idx / BM;
-      const int p = idx % BM;
+    constexpr int CPR = 4 * C / VEC;  // 16-byte pieces per G row
+    for (int idx = tid; idx < BM * CPR; idx += NT) {
+      const int p = idx / CPR;
+      const int ch = (idx % CPR) * VEC;
       if (line >= N || t0 + p >= N) continue;
-      gpg[(size_t)k * M + ((size_t)b * N + line) * N + t0 + p] = G[p * GLD + k];
+      *reinterpret_cast<u32x4*>(gpg + (((size_t)b * N + line) * N + t0 + p) * 4 * C + ch) =
+          *reinterpret_cast<const u32x4*>(G + p * GLD + ch);
     }
   }
 
@@ -421,6 +422,207 @@ __global__ __launch_bounds__(256) void trimul_project_vjp_kernel(const TC* __res
         const long t = tok(p);
         if (t >= 0) dx[t * C + c] = from_f32<TZ>(gx_in[t * C + c] + acc2[rb][jb][e]);
       }
+}
+
+// Project VJP, persistent and weight-stationary (bf16 GEMMs, C = 128; weights packed in
+// 32-channel blocks, rows 128 j + 32 kind + r, as the persistent K1 reads them). One 512-thread
+// block per CU walks 64-position tiles along the lines. Wave w holds in MFMA operand registers,
+// for the whole kernel, the proj and gate rows of plane w >> 2 (a | b), channels 32 (w & 3) ..
+// +32, as the A operand of acc^T [row][position] = W4 x^T (lane: row l & 31, 8 k per step), so
+// these weights are read once per CU, not once per tile. For dx [position][c] = G W4, wave w
+// takes the columns c = 16 w .. +16; their B fragments (16x16x32 steps, lane: column l & 15,
+// rows 32 s + 8 (l >> 4) ..) are 16-byte pieces of the rows of W4^T, read from L2 four steps
+// at a time (registers for all sixteen would cost the occupancy). Per tile: x rows -> LDS (bf16), each
+// wave's cotangent rows (32 channels x 64 positions of dP or dQ) -> its private LDS stage,
+// both loaded a tile ahead into registers; acc^T, G in registers, G rows -> the LDS G tile;
+// then G leaves token-major (1 KB rows) and dx = gx_in + G W4 is formed from the G tile.
+struct ProjectVjpWs {
+  static constexpr int C = 128;
+  static constexpr int BP = 64;         // positions per tile
+  static constexpr int NW = 8;          // waves per block
+  static constexpr int NT = 64 * NW;
+  static constexpr int XLD = C + 8;     // x tile rows (bf16): 272 bytes, conflict-free 16-byte reads
+  static constexpr int GLD = 4 * C + 8; // G tile rows (bf16): 1040 bytes
+  static constexpr int SLD = BP + 8;    // cotangent stage rows (bf16): [32 channels][64 positions]
+};
+
+template <class TZ>
+__global__ __launch_bounds__(ProjectVjpWs::NT) void trimul_project_vjp_ws_kernel(
+    const bf16* __restrict__ dplanes, const TZ* __restrict__ x, const float* __restrict__ mask,
+    const bf16* __restrict__ w4, const bf16* __restrict__ w4t, const float* __restrict__ gx_in, int B, int N,
+    int Np, int outgoing, bf16* __restrict__ gpg, bf16* __restrict__ xw, TZ* __restrict__ dx) {
+  using Cfg = ProjectVjpWs;
+  constexpr int C = Cfg::C, BP = Cfg::BP, NT = Cfg::NT, XLD = Cfg::XLD, GLD = Cfg::GLD, SLD = Cfg::SLD;
+  constexpr int XV = 16 / sizeof(TZ);       // x elements per 16-byte load
+  constexpr int XL = BP * C / XV / NT;      // x loads per thread per tile
+  __shared__ __attribute__((aligned(16))) bf16 xs[BP * XLD];
+  __shared__ __attribute__((aligned(16))) float mks[BP];
+  __shared__ __attribute__((aligned(16))) bf16 gs[BP * GLD];
+  __shared__ __attribute__((aligned(16))) bf16 cst_all[Cfg::NW][32 * SLD];
+
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const int hh = l >> 5;
+  const int pl = w >> 2;  // plane: 0 a (dP), 1 b (dQ)
+  const int cj = w & 3;   // 32-channel chunk
+  bf16* cst = cst_all[w];
+  const size_t pe = (size_t)Np * Np;
+  const int tpl = (N + BP - 1) / BP;
+  const int ntiles = B * N * tpl;  // < 2^31 (checked at launch)
+  const int G = gridDim.x;
+
+  // Weights, once. G operand: rows 128 cj + 32 (2 pl + kind) + (l & 31), k = 16 ks + 8 hh + e.
+  bf16x8 wa[2][C / 16];
+#pragma unroll
+  for (int kind = 0; kind < 2; ++kind) {
+    const bf16* r = w4 + (size_t)(128 * cj + 32 * (2 * pl + kind) + (l & 31)) * C + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < C / 16; ++ks) wa[kind][ks] = *reinterpret_cast<const bf16x8*>(r + 16 * ks);
+  }
+  // dx operand: row 16 w + (l & 15) of W4^T, k = 32 s + 8 (l >> 4) + e.
+  const bf16* wbrow = w4t + (size_t)(16 * w + (l & 15)) * 4 * C + 8 * (l >> 4);
+
+  auto tile_coords = [&](int tile, int& b, int& line, int& t0) {
+    b = tile / (N * tpl);
+    const int rem = tile - b * (N * tpl);
+    line = rem / tpl;
+    t0 = (rem - line * tpl) * BP;
+  };
+  auto tok = [&](int b, int line, int t) -> long {
+    return (long)b * N * N + (outgoing ? (long)line * N + t : (long)t * N + line);
+  };
+  // Next tile's x rows (thread: XL 16-byte pieces), mask value (threads < BP) and this wave's
+  // cotangent rows (lane: row 8 it + (l >> 3), 8 positions), in registers. Positions past N
+  // read a clamped real row; their mask and G are zero and nothing is stored for them.
+  u32x4 xr[XL], cr[4];
+  float mr = 0.f;
+  auto issue = [&](int tile) __attribute__((always_inline)) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
+#pragma unroll
+    for (int q = 0; q < XL; ++q) {
+      const int idx = tid + q * NT;
+      const int p = idx / (C / XV);
+      const int ch = (idx % (C / XV)) * XV;
+      xr[q] = *reinterpret_cast<const u32x4*>(x + tok(b, line, min(t0 + p, N - 1)) * C + ch);
+    }
+    if (tid < BP) mr = t0 + tid < N ? mask[tok(b, line, t0 + tid)] : 0.f;
+    const bf16* cb = dplanes + ((size_t)(pl * B + b) * C + 32 * cj) * pe + (size_t)line * Np + t0 + 8 * (l & 7);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) cr[it] = *reinterpret_cast<const u32x4*>(cb + (size_t)(8 * it + (l >> 3)) * pe);
+  };
+  auto stage = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < XL; ++q) {
+      const int idx = tid + q * NT;
+      const int p = idx / (C / XV);
+      const int ch = (idx % (C / XV)) * XV;
+      float v[XV];
+      unpack16<TZ>(xr[q], v);
+      store_vec<bf16, XV>(xs + p * XLD + ch, v);
+    }
+    if (tid < BP) mks[tid] = mr;
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+      *reinterpret_cast<u32x4*>(cst + (8 * it + (l >> 3)) * SLD + 8 * (l & 7)) = cr[it];
+  };
+
+  int tile = blockIdx.x;
+  if (tile < ntiles) issue(tile);
+  for (; tile < ntiles; tile += G) {
+    int b, line, t0;
+    tile_coords(tile, b, line, t0);
+    stage();
+    if (tile + G < ntiles) issue(tile + G);
+    __syncthreads();  // x tile, masks and stages of this tile
+
+    // acc^T [row][position] per 32-position half, then G = (g s, g p s (1 - s)) into gs.
+#pragma unroll 1
+    for (int pt = 0; pt < 2; ++pt) {
+      f32x16 acc[2] = {};
+      const bf16* xrow = xs + (32 * pt + (l & 31)) * XLD + 8 * hh;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xrow + 16 * ks);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[0][ks], xf, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[1][ks], xf, acc[1], 0, 0, 0);
+      }
+      const int p = 32 * pt + (l & 31);
+      const float m = mks[p];
+      bf16* grow = gs + p * GLD + 128 * cj + 64 * pl;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float gp[4], gg[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * j + e;
+          const float g = to_f32(cst[(8 * j + 4 * hh + e) * SLD + p]) * m;
+          const float sg = sigmoidf_(acc[1][r]);
+          gp[e] = g * sg;
+          gg[e] = g * acc[0][r] * sg * (1.f - sg);
+        }
+        store_vec<bf16, 4>(grow + 8 * j + 4 * hh, gp);
+        store_vec<bf16, 4>(grow + 32 + 8 * j + 4 * hh, gg);
+      }
+    }
+    __syncthreads();  // G tile
+
+    // G rows token-major (walk order), 1 KB each; x rows in walk order for the incoming
+    // direction.
+    const int nvalid = min(BP, N - t0);
+    bf16* gdst = gpg + (((size_t)b * N + line) * N + t0) * 4 * C;
+#pragma unroll
+    for (int it = 0; it < BP * 4 * C / 8 / NT; ++it) {
+      const int idx = tid + it * NT;
+      const int p = idx / (4 * C / 8);
+      const int ch = (idx % (4 * C / 8)) * 8;
+      if (p < nvalid)
+        *reinterpret_cast<u32x4*>(gdst + (size_t)p * 4 * C + ch) = *reinterpret_cast<const u32x4*>(gs + p * GLD + ch);
+    }
+    if (!outgoing) {
+      bf16* xdst = xw + (((size_t)b * N + line) * N + t0) * C;
+#pragma unroll
+      for (int it = 0; it < BP * C / 8 / NT; ++it) {
+        const int idx = tid + it * NT;
+        const int p = idx / (C / 8);
+        const int ch = (idx % (C / 8)) * 8;
+        if (p < nvalid)
+          *reinterpret_cast<u32x4*>(xdst + (size_t)p * C + ch) = *reinterpret_cast<const u32x4*>(xs + p * XLD + ch);
+      }
+    }
+
+    // dx [position][16 w + (l & 15)] = gx_in + G W4 (k = 4C in 32-row steps)
+    const int c = 16 * w + (l & 15);
+    f32x4 acc2[BP / 16] = {};
+#pragma unroll 1
+    for (int s4 = 0; s4 < 4 * C / 32; s4 += 4) {
+      bf16x8 wb[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) wb[u] = *reinterpret_cast<const bf16x8*>(wbrow + 32 * (s4 + u));
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int rb = 0; rb < BP / 16; ++rb) {
+          const bf16x8 gf =
+              *reinterpret_cast<const bf16x8*>(gs + (16 * rb + (l & 15)) * GLD + 32 * (s4 + u) + 8 * (l >> 4));
+          acc2[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gf, wb[u], acc2[rb], 0, 0, 0);
+        }
+    }
+    // position p of the tile is token tbase + p tstr
+    const long tbase = tok(b, line, t0);
+    const long tstr = outgoing ? 1 : N;
+    const float* gxt = gx_in + tbase * C + c;
+    TZ* dxt = dx + tbase * C + c;
+#pragma unroll
+    for (int rb = 0; rb < BP / 16; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p = 16 * rb + 4 * (l >> 4) + r;
+        if (p < nvalid) dxt[p * tstr * C] = from_f32<TZ>(gxt[p * tstr * C] + acc2[rb][r]);
+      }
+    __syncthreads();  // x tile, stages and G tile free for the next tile
+  }
 }
 
 // dst[g] = src[g]^T for G planes of [Np][Np] (64 x 64 tiles through LDS).
@@ -468,6 +670,15 @@ template <class TZ, class TC, int C>
 int project_vjp_launch(const void* dplanes, const void* x, const float* mask, const void* w4, const void* w4t,
                        const float* gx_in, int B, int N, int outgoing, void* gpg, void* xw, void* dx, hipStream_t s) {
   const int Np = pf::pad128(N);
+  if constexpr (sizeof(TC) == 2 && C == 128) {
+    const long ntiles = (long)B * N * ((N + ProjectVjpWs::BP - 1) / ProjectVjpWs::BP);
+    PF_REQUIRE(ntiles < (1L << 31), PF_ERR_UNSUPPORTED, "trimul_project_vjp: B=%d N=%d too large", B, N);
+    const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+    trimul_project_vjp_ws_kernel<TZ><<<nblk, ProjectVjpWs::NT, 0, s>>>(
+        (const bf16*)dplanes, (const TZ*)x, mask, (const bf16*)w4, (const bf16*)w4t, gx_in, B, N, Np, outgoing,
+        (bf16*)gpg, (bf16*)xw, (TZ*)dx);
+    return pf::check_launch("trimul_project_vjp");
+  }
   constexpr int BM = vjp_bm<TC, C>();
   trimul_project_vjp_kernel<TZ, TC, C><<<dim3(Np / BM, Np, B), 256, 0, s>>>(
       (const TC*)dplanes, (const TZ*)x, mask, (const TC*)w4, (const TC*)w4t, gx_in, B, N, Np, outgoing, (TC*)gpg,

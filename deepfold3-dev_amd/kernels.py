@@ -297,6 +297,75 @@ def _weight_grad(a_cm: torch.Tensor, b: torch.Tensor, chunk: int) -> torch.Tenso
     return torch.bmm(a3, b.view(S, chunk, b.shape[1])).float().sum(0)
 
 
+def _split_chunk(M: int, target: int = 4096) -> int:
+    """Token chunk for a split-K weight gradient over M tokens: the divisor of M in
+    [target / 2, 2 target] closest to ``target``, else ``target`` (the rows past the last
+    whole chunk are then added by one more product)."""
+    best = 0
+    for d in range(target // 2, 2 * target + 1):
+        if M % d == 0 and (best == 0 or abs(d - target) < abs(best - target)):
+            best = d
+    return best or target
+
+
+def _weight_grad_tm(gy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """``gy^T x`` (fp32, or fp64 for fp64 operands) for token-major gy [M, Co] and x [M, Ci]
+    with M in the hundreds of thousands: the tokens split into chunks of a batched GEMM (one
+    [Co, Ci] tile alone leaves the GPU idle; left operand a strided view, right operand
+    contiguous), summed over chunks."""
+    acc = torch.promote_types(gy.dtype, torch.float32)
+    M = gy.shape[0]
+    chunk = _split_chunk(M)
+    S = M // chunk
+    m0 = S * chunk
+    g3 = gy[:m0].view(S, chunk, gy.shape[1]).transpose(1, 2)  # [S, Co, chunk]
+    out = torch.bmm(g3, x[:m0].view(S, chunk, x.shape[1])).to(acc).sum(0)
+    if m0 < M:
+        out += (gy[m0:].t() @ x[m0:]).to(acc)
+    return out
+
+
+class _TokenLinear(torch.autograd.Function):
+    """``x W^T`` over many tokens; the weight gradient runs split over token chunks."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        return torch.nn.functional.linear(x, w)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, w = ctx.saved_tensors
+        gy = gy.to(x.dtype).contiguous()
+        gx = gw = None
+        if ctx.needs_input_grad[0]:
+            gx = gy @ w
+        if ctx.needs_input_grad[1]:
+            Ci = x.shape[-1]
+            gw = _weight_grad_tm(gy.view(-1, gy.shape[-1]), x.view(-1, Ci)).to(w.dtype)
+        return gx, gw
+
+
+# Below this many tokens a linear's weight gradient is one library GEMM.
+SPLIT_K_TOKENS = 32768
+
+
+def token_linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``F.linear(x, weight)`` (no bias) for the training path. Over a pair's tokens
+    (``B N^2`` of them) the weight gradient is a GEMM with a reduction dimension in the
+    hundreds of thousands and an output of a few hundred rows, which a single library call
+    runs on a handful of workgroups; here it runs split over token chunks. Under autocast the
+    operands are cast as autocast would cast them, so the numerics are the stock linear's."""
+    M = x.numel() // x.shape[-1]
+    if not torch.is_grad_enabled() or M < SPLIT_K_TOKENS or not (x.requires_grad or weight.requires_grad):
+        return torch.nn.functional.linear(x, weight)
+    if torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+        x, weight = x.to(dt), weight.to(dt)
+    with torch.autocast("cuda", enabled=False):
+        return _TokenLinear.apply(x.contiguous(), weight)
+
+
 class FusedTriMulFunction(torch.autograd.Function):
     """Trainable triangle multiply after the input LayerNorm (``FusedTriMulFunction``,
     ``triton/fused_trimul.py:285-330``); same ``apply`` arguments.
@@ -386,7 +455,7 @@ class FusedTriMulFunction(torch.autograd.Function):
         del dX
         torch.bmm(dXt, pl[0], out=dpl[1])
         del dXt
-        gpg = torch.empty((4 * C, M), dtype=cdt, device=dev)  # channel-major, the kernel's walk order
+        gpg = torch.empty((M, 4 * C), dtype=cdt, device=dev)  # token-major, the kernel's walk order
         xw = None if ctx.outgoing else torch.empty((M, C), dtype=cdt, device=dev)  # x in that order
         dx = torch.empty_like(xc)
         w4t = w4.t().contiguous()
@@ -396,7 +465,8 @@ class FusedTriMulFunction(torch.autograd.Function):
             stream,
         )  # fmt: skip
         del dpl, gx
-        dw4 = _weight_grad(gpg, xb if xw is None else xw, chunk).view(C // 16, 4, 16, C)  # rows 64 j + 16 kind + r
+        cb = 32 if (cdt == torch.bfloat16 and C == 128) else 16  # channel blocks of the packed rows
+        dw4 = _weight_grad_tm(gpg, xb if xw is None else xw).view(C // cb, 4, cb, C)  # rows 4 cb j + cb kind + r
         d_proj = torch.cat([dw4[:, 0].reshape(C, C), dw4[:, 2].reshape(C, C)])
         d_gate = torch.cat([dw4[:, 1].reshape(C, C), dw4[:, 3].reshape(C, C)])
         dt = ctx.dtypes

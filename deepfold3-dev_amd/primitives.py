@@ -146,14 +146,15 @@ class TransitionBlock(nn.Module):
     def _forward_grad(self, x: torch.Tensor) -> torch.Tensor:
         """Training path, the reference's fused transition's structure (``fused_transition.py:34-83``:
         LN + linear1, SwiGLU, linear2): the HIP LayerNorm and SwiGLU with their backward, the
-        two linears as library GEMMs in autograd, the branch scale on linear2."""
+        two linears as library GEMMs in autograd (``token_linear``: split-K weight gradients
+        over a pair's tokens), the branch scale on linear2."""
         import torch.nn.functional as F
 
-        from .kernels import LayerNormFunction, SwiGLUFunction
+        from .kernels import LayerNormFunction, SwiGLUFunction, token_linear
 
         xn = LayerNormFunction.apply(x, self.norm.weight, self.norm.bias, self.norm.eps)
         w2 = self.linear2.weight if self.branch_scale == 1.0 else self.linear2.weight * self.branch_scale
-        return F.linear(SwiGLUFunction.apply(F.linear(xn, self.linear1.weight)), w2)
+        return token_linear(SwiGLUFunction.apply(token_linear(xn, self.linear1.weight)), w2)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """``transition(x)`` (not added to x); under grad the differentiable path."""

@@ -111,8 +111,8 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
  * after its input LayerNorm, with a backward.
  *
  * pf_trimul_train_pack_weights: as pf_trimul_pack_weights, in the layout the training
- * kernels read (16-channel blocks, rows 64 j + 16 kind + r; kind 0 a proj, 1 a gate,
- * 2 b proj, 3 b gate) for every C and cdtype.
+ * kernels read: rows cb (4 j + kind) + r, kind 0 a proj, 1 a gate, 2 b proj, 3 b gate, in
+ * blocks of cb = 32 channels for bf16 at C = 128 (the persistent kernels), 16 otherwise.
  *
  * pf_trimul_train_fwd: x [B,N,N,C] (xdtype) is the input LayerNorm's output; writes the
  * update to `out` (xdtype) and keeps the planes P, Q and the contraction X, channel-major
@@ -129,12 +129,12 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
  *
  * pf_trimul_project_vjp (_project_vjp_kernel, fused_trimul.py:214-262): dplanes = [dP; dQ]
  * (two [B*C][Np][Np] cdtype sets), w_packed from pf_trimul_train_pack_weights and
- * w_packed_t its [C, 4C] transpose; writes G = (gp_a, gg_a, gp_b, gg_b) channel-major
- * [4C, B*N*N] in the packed row order and dx = gx_in + G^T W4 [B*N*N, C] (xdtype). G's
- * columns follow the kernel's walk over plane positions (line, t) at b N^2 + line N + t:
+ * w_packed_t its [C, 4C] transpose; writes G = (gp_a, gg_a, gp_b, gg_b) token-major
+ * [B*N*N, 4C] in the packed row order and dx = gx_in + G W4 [B*N*N, C] (xdtype). G's
+ * rows follow the kernel's walk over plane positions (line, t) at b N^2 + line N + t:
  * token order when outgoing; when incoming (line = column of z) x is also written in that
- * order to xw [B*N*N, C] (cdtype), so the packed weights' gradient is G x (outgoing) or
- * G xw (incoming). C = 64, 128 or 256.
+ * order to xw [B*N*N, C] (cdtype), so the packed weights' gradient is G^T x (outgoing) or
+ * G^T xw (incoming). C = 64, 128 or 256.
  *
  * pf_planes_transpose: dst[g] = src[g]^T for G planes [Np][Np] (Np a multiple of 64), the
  * dX^T operand of dQ = dX^T P. */

@@ -1,5 +1,6 @@
 """CPU: host-side logic -- the kernel census, the refusal contract, the out-buffer check,
-and the default initialisation of the transition block."""
+the default initialisation of the transition block, and the split-K token linear of the
+training path."""
 
 from __future__ import annotations
 
@@ -14,6 +15,7 @@ census = mod("kernel_census")
 guard = mod("inference_guard")
 primitives = mod("primitives")
 _lib = mod("_lib")
+kernels = mod("kernels")
 
 
 @pytest.fixture(autouse=True)
@@ -156,3 +158,33 @@ def test_confidence_layers_keys():
     keys = list(evoformer.ConfidencePairFormer().state_dict())
     assert keys[0].startswith("layers.0.") and any(k.startswith("layers.3.") for k in keys)
     assert not any(k.startswith("layers.4.") for k in keys)
+
+
+@pytest.mark.parametrize("n", [190, 181])  # M = 36100 = 10 chunks of 3610; 32761 + 1 past a threshold
+def test_token_linear_gradients_match_linear(n):
+    """The split-K weight gradient (chunks of a batched product, rows past the last whole
+    chunk in one more product) against autograd's linear, fp64."""
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(1, n, n, 24, generator=g, dtype=torch.float64)
+    w = torch.randn(40, 24, generator=g, dtype=torch.float64)
+    gy = torch.randn(1, n, n, 40, generator=g, dtype=torch.float64)
+    old = kernels.SPLIT_K_TOKENS
+    kernels.SPLIT_K_TOKENS = 1000
+    try:
+        x1, w1 = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+        y1 = kernels.token_linear(x1, w1)
+        (y1 * gy).sum().backward()
+    finally:
+        kernels.SPLIT_K_TOKENS = old
+    x2, w2 = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    y2 = torch.nn.functional.linear(x2, w2)
+    (y2 * gy).sum().backward()
+    assert torch.equal(y1, y2)
+    torch.testing.assert_close(x1.grad, x2.grad, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(w1.grad, w2.grad, rtol=1e-10, atol=1e-10)
+
+
+def test_split_chunk():
+    assert kernels._split_chunk(768 * 768) == 4096
+    assert kernels._split_chunk(190 * 190) == 3610
+    assert kernels._split_chunk(32761) == 4096  # 181^2 = 32761: no divisor in range
