@@ -40,7 +40,6 @@ __global__ __launch_bounds__(256) void trimul_output_vjp_kernel(
     const TC* __restrict__ WoT, const TC* __restrict__ WogT, int B, int N, int Np, TC* __restrict__ gp_out,
     TC* __restrict__ gg_out, TC* __restrict__ xln_out, TC* __restrict__ dX, float* __restrict__ gx,
     float* __restrict__ partial) {
-  const size_t M = (size_t)B * N * N;
   constexpr int BM = vjp_bm<TC, C>();
   constexpr int NT = 256;
   constexpr int RB = BM / 16;
@@ -159,14 +158,17 @@ __global__ __launch_bounds__(256) void trimul_output_vjp_kernel(
         A2[p * ALD + c] = from_f32<TC>(gv * accp[rb][jb][e] * sv * (1.f - sv));
       }
   __syncthreads();
-  // gp, gg channel-major [C][M] (rows of contiguous tokens) for the weight-gradient GEMMs
-  for (int idx = tid; idx < BM * C; idx += NT) {
-    const int c = idx / BM;
-    const int p = idx % BM;
-    const long t = tok(p);
-    if (t < 0) continue;
-    gp_out[(size_t)c * M + t] = A1[p * ALD + c];
-    gg_out[(size_t)c * M + t] = A2[p * ALD + c];
+  // gp, gg token-major [M][C] for the weight-gradient GEMMs: the tile's rows are contiguous
+  {
+    constexpr int CPR = C / VEC;
+    for (int idx = tid; idx < BM * CPR; idx += NT) {
+      const int p = idx / CPR;
+      const int ch = (idx % CPR) * VEC;
+      const long t = tok(p);
+      if (t < 0) continue;
+      *reinterpret_cast<u32x4*>(gp_out + t * C + ch) = *reinterpret_cast<const u32x4*>(A1 + p * ALD + ch);
+      *reinterpret_cast<u32x4*>(gg_out + t * C + ch) = *reinterpret_cast<const u32x4*>(A2 + p * ALD + ch);
+    }
   }
 
   // d(xln) = gp Wo, the output gate's x cotangent gg Wog
@@ -244,6 +246,261 @@ __global__ __launch_bounds__(256) void trimul_output_vjp_kernel(
       *reinterpret_cast<u32x4*>(Db + (size_t)c * pe + ch * VEC) =
           *reinterpret_cast<const u32x4*>(Xs + c * XLD + ch * VEC);
     }
+  }
+}
+
+// Output VJP, persistent and weight-stationary (bf16 GEMMs, C = 128): the same steps as
+// trimul_output_vjp_kernel, with one 512-thread block per CU walking 64-position tiles. Wave w
+// takes the output columns 16 w .. +16 of all four GEMMs (xln Wo^T, x Wog^T, gp Wo, gg Wog);
+// their B fragments (16x16x32 steps, lane: column l & 15, k = 32 s + 8 (l >> 4) ..) are rows of
+// Wo, Wog, Wo^T, Wog^T and stay in registers for the whole kernel. The LN_out affine gradients
+// accumulate per thread (channel tid & 127, positions 16 (tid >> 7) .. +16 of every tile) and
+// leave as one partial sum per block.
+struct OutputVjpWs {
+  static constexpr int C = 128;
+  static constexpr int BM = 64;
+  static constexpr int NT = 512;
+  static constexpr int XLD = BM + 8;  // X tile [c][p] (bf16)
+  static constexpr int ALD = C + 8;   // xln / x, then gp / gg, [p][c] (bf16)
+  static constexpr int SLD = C + 4;   // d(xln) [p][c] (fp32)
+  static constexpr int NQ = NT / BM;  // threads per position in the per-position passes
+  static constexpr int CPQ = C / NQ;
+};
+
+// acc[rb] (rows 16 rb .., columns of this wave) += A [64][C] (LDS, k contiguous) W, W's B
+// fragments in registers.
+PF_DEVICE void gemm_a_lds_w_regs(f32x4 (&acc)[4], const bf16* A, int lda, const bf16x8 (&wf)[4]) {
+  const int l = lane_id();
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const bf16x8 af = *reinterpret_cast<const bf16x8*>(A + (16 * rb + (l & 15)) * lda + 32 * st + 8 * (l >> 4));
+      acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[st], acc[rb], 0, 0, 0);
+    }
+}
+
+template <class TZ>
+__global__ __launch_bounds__(OutputVjpWs::NT) void trimul_output_vjp_ws_kernel(
+    const TZ* __restrict__ g, const bf16* __restrict__ X, const TZ* __restrict__ x, const float* __restrict__ lnow,
+    const float* __restrict__ lnob, float eps, const bf16* __restrict__ Wo, const bf16* __restrict__ Wog,
+    const bf16* __restrict__ WoT, const bf16* __restrict__ WogT, int B, int N, int Np, bf16* __restrict__ gp_out,
+    bf16* __restrict__ gg_out, bf16* __restrict__ xln_out, bf16* __restrict__ dX, float* __restrict__ gx,
+    float* __restrict__ partial) {
+  using Cfg = OutputVjpWs;
+  constexpr int C = Cfg::C, BM = Cfg::BM, NT = Cfg::NT, XLD = Cfg::XLD, ALD = Cfg::ALD, SLD = Cfg::SLD;
+  constexpr int NQ = Cfg::NQ, CPQ = Cfg::CPQ;
+  constexpr int A_BYTES = BM * ALD * 2;
+  constexpr int ST_BYTES = BM * SLD * 4;
+  constexpr int R_BYTES = 2 * A_BYTES > ST_BYTES ? 2 * A_BYTES : ST_BYTES;
+  __shared__ __attribute__((aligned(16))) bf16 Xs[C * XLD];  // X [c][p], later dX
+  __shared__ __attribute__((aligned(16))) char rsm[R_BYTES];
+  __shared__ float s_mean[BM], s_rstd[BM];
+  __shared__ float s_lnw[C], s_lnb[C];
+  __shared__ float red[2][NT];
+  bf16* A1 = reinterpret_cast<bf16*>(rsm);            // xln, then gp
+  bf16* A2 = reinterpret_cast<bf16*>(rsm + A_BYTES);  // x, then gg
+  float* stage = reinterpret_cast<float*>(rsm);       // d(xln), fp32
+
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const size_t pe = (size_t)Np * Np;
+  const int tpl = Np / BM;
+  const int ntiles = B * Np * tpl;  // every tile of the planes, padding included (< 2^31)
+  const int G = gridDim.x;
+  const int col = 16 * w + (l & 15);  // this lane's output column in all four GEMMs
+
+  bf16x8 wo[4], wog[4], wot[4], wogt[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const int k = 32 * st + 8 * (l >> 4);
+    wo[st] = *reinterpret_cast<const bf16x8*>(Wo + (size_t)col * C + k);
+    wog[st] = *reinterpret_cast<const bf16x8*>(Wog + (size_t)col * C + k);
+    wot[st] = *reinterpret_cast<const bf16x8*>(WoT + (size_t)col * C + k);
+    wogt[st] = *reinterpret_cast<const bf16x8*>(WogT + (size_t)col * C + k);
+  }
+  const int pq = tid / NQ;
+  const int qq = tid % NQ;
+  if (tid < C) {
+    s_lnw[tid] = lnow[tid];
+    s_lnb[tid] = lnob[tid];
+  }
+  float pw = 0.f, pb = 0.f;  // LN_out affine partials of channel tid & 127
+
+  for (int tile = blockIdx.x; tile < ntiles; tile += G) {
+    const int b = tile / (Np * tpl);
+    const int rem = tile - b * (Np * tpl);
+    const int i = rem / tpl;
+    const int j0 = (rem - i * tpl) * BM;
+    const int nvalid = i < N ? max(0, min(BM, N - j0)) : 0;
+    const long tok0 = ((long)b * N + i) * N + j0;  // position p is token tok0 + p (p < nvalid)
+    if (nvalid == 0) {
+      // padding only: dX is zero there (the contraction's cotangent GEMMs read it)
+      bf16* Db = dX + (size_t)b * C * pe + (size_t)i * Np + j0;
+#pragma unroll
+      for (int it = 0; it < C * BM / 8 / NT; ++it) {
+        const int idx = tid + it * NT;
+        *reinterpret_cast<u32x4*>(Db + (size_t)(idx / (BM / 8)) * pe + (idx % (BM / 8)) * 8) = u32x4{0u, 0u, 0u, 0u};
+      }
+      continue;  // block-uniform
+    }
+
+    // X tile, channel-major (rows of 64 contiguous positions per channel); x rows
+    {
+      const bf16* Xb = X + (size_t)b * C * pe + (size_t)i * Np + j0;
+#pragma unroll
+      for (int it = 0; it < C * BM / 8 / NT; ++it) {
+        const int idx = tid + it * NT;
+        const int c = idx / (BM / 8);
+        const int ch = (idx % (BM / 8)) * 8;
+        *reinterpret_cast<u32x4*>(Xs + c * XLD + ch) = *reinterpret_cast<const u32x4*>(Xb + (size_t)c * pe + ch);
+      }
+    }
+    copy_tile_to_lds<TZ, bf16, C, BM, NT>(
+        [&](int p) -> const TZ* { return p < nvalid ? x + (tok0 + p) * C : nullptr; }, A2, ALD);
+    __syncthreads();
+
+    // LN_out statistics (fp32, two-pass) and xln = LN_out(X) into A1 and xln_out
+    {
+      float xv[CPQ];
+      float sm = 0.f;
+#pragma unroll
+      for (int e = 0; e < CPQ; ++e) {
+        xv[e] = to_f32(Xs[(qq * CPQ + e) * XLD + pq]);
+        sm += xv[e];
+      }
+      const float mean = group_sum<NQ>(sm) * (1.0f / C);
+      float v = 0.f;
+#pragma unroll
+      for (int e = 0; e < CPQ; ++e) {
+        const float d = xv[e] - mean;
+        v += d * d;
+      }
+      const float rstd = rsqrtf(group_sum<NQ>(v) * (1.0f / C) + eps);
+      if (qq == 0) {
+        s_mean[pq] = mean;
+        s_rstd[pq] = rstd;
+      }
+      float y[CPQ];
+#pragma unroll
+      for (int e = 0; e < CPQ; ++e) y[e] = (xv[e] - mean) * rstd * s_lnw[qq * CPQ + e] + s_lnb[qq * CPQ + e];
+#pragma unroll
+      for (int e = 0; e < CPQ; e += 8) {
+        store_vec<bf16, 8>(A1 + pq * ALD + qq * CPQ + e, y + e);
+        if (pq < nvalid) store_vec<bf16, 8>(xln_out + (tok0 + pq) * C + qq * CPQ + e, y + e);
+      }
+    }
+    __syncthreads();
+
+    // p = xln Wo^T, s = sigmoid(x Wog^T)
+    f32x4 accp[4] = {}, accg[4] = {};
+    gemm_a_lds_w_regs(accp, A1, ALD, wo);
+    gemm_a_lds_w_regs(accg, A2, ALD, wog);
+    __syncthreads();  // A1 / A2 are rewritten below
+
+    // gp = g s, gg = g p s (1 - s), rounded to bf16 as the next GEMMs' operands
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p = 16 * rb + 4 * (l >> 4) + e;
+        const float gv = p < nvalid ? to_f32(g[(tok0 + p) * C + col]) : 0.f;
+        const float sv = sigmoidf_(accg[rb][e]);
+        A1[p * ALD + col] = from_f32<bf16>(gv * sv);
+        A2[p * ALD + col] = from_f32<bf16>(gv * accp[rb][e] * sv * (1.f - sv));
+      }
+    __syncthreads();
+    // gp, gg token-major for the weight-gradient GEMMs
+#pragma unroll
+    for (int it = 0; it < BM * C / 8 / NT; ++it) {
+      const int idx = tid + it * NT;
+      const int p = idx / (C / 8);
+      const int ch = (idx % (C / 8)) * 8;
+      if (p < nvalid) {
+        *reinterpret_cast<u32x4*>(gp_out + (tok0 + p) * C + ch) = *reinterpret_cast<const u32x4*>(A1 + p * ALD + ch);
+        *reinterpret_cast<u32x4*>(gg_out + (tok0 + p) * C + ch) = *reinterpret_cast<const u32x4*>(A2 + p * ALD + ch);
+      }
+    }
+
+    // d(xln) = gp Wo, the output gate's x cotangent gg Wog
+    f32x4 accd[4] = {}, accx[4] = {};
+    gemm_a_lds_w_regs(accd, A1, ALD, wot);
+    gemm_a_lds_w_regs(accx, A2, ALD, wogt);
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p = 16 * rb + 4 * (l >> 4) + e;
+        if (p < nvalid) gx[(tok0 + p) * C + col] = accx[rb][e];
+      }
+    __syncthreads();  // A1 / A2 dead: the fp32 stage takes their place
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) stage[(16 * rb + 4 * (l >> 4) + e) * SLD + col] = accd[rb][e];
+    __syncthreads();
+
+    // LN_out affine partials: channel tid & 127 over positions 16 (tid >> 7) .. +16 (positions
+    // past N have d = 0)
+    {
+      const int c = tid & (C - 1);
+      const int p0 = 16 * (tid >> 7);
+#pragma unroll 4
+      for (int p = p0; p < p0 + 16; ++p) {
+        const float xn = (to_f32(Xs[c * XLD + p]) - s_mean[p]) * s_rstd[p];
+        const float d = stage[p * SLD + c];
+        pw += d * xn;
+        pb += d;
+      }
+    }
+    __syncthreads();  // Xs is overwritten with dX below
+
+    // LN_out pullback, in place over Xs: each thread owns (position pq, channels qq*CPQ..)
+    {
+      const float mean = s_mean[pq], rstd = s_rstd[pq];
+      float u[CPQ], xn[CPQ];
+      float su = 0.f, sux = 0.f;
+#pragma unroll
+      for (int e = 0; e < CPQ; ++e) {
+        const int c = qq * CPQ + e;
+        xn[e] = (to_f32(Xs[c * XLD + pq]) - mean) * rstd;
+        u[e] = stage[pq * SLD + c] * s_lnw[c];
+        su += u[e];
+        sux += u[e] * xn[e];
+      }
+      su = group_sum<NQ>(su) * (1.0f / C);
+      sux = group_sum<NQ>(sux) * (1.0f / C);
+#pragma unroll
+      for (int e = 0; e < CPQ; ++e)
+        Xs[(qq * CPQ + e) * XLD + pq] = from_f32<bf16>(rstd * (u[e] - su - xn[e] * sux));
+    }
+    __syncthreads();
+    {
+      bf16* Db = dX + (size_t)b * C * pe + (size_t)i * Np + j0;
+#pragma unroll
+      for (int it = 0; it < C * BM / 8 / NT; ++it) {
+        const int idx = tid + it * NT;
+        const int c = idx / (BM / 8);
+        const int ch = (idx % (BM / 8)) * 8;
+        *reinterpret_cast<u32x4*>(Db + (size_t)c * pe + ch) = *reinterpret_cast<const u32x4*>(Xs + c * XLD + ch);
+      }
+    }
+    __syncthreads();  // Xs, A1 / A2 and the stage free for the next tile
+  }
+  // this block's partials: the four position quarters added in order
+  red[0][tid] = pw;
+  red[1][tid] = pb;
+  __syncthreads();
+  if (tid < C) {
+    float sw = 0.f, sb = 0.f;
+#pragma unroll
+    for (int q = 0; q < NT / C; ++q) {
+      sw += red[0][q * C + tid];
+      sb += red[1][q * C + tid];
+    }
+    partial[(size_t)blockIdx.x * 2 * C + tid] = sw;
+    partial[(size_t)blockIdx.x * 2 * C + C + tid] = sb;
   }
 }
 
@@ -654,9 +911,20 @@ int output_vjp_launch(const void* g, const void* X, const void* x, const float* 
                       const void* wo, const void* wog, const void* wot, const void* wogt, int B, int N, void* gp,
                       void* gg, void* xln, void* dX, float* gx, float* dlnw, float* dlnb, void* ws, hipStream_t s) {
   const int Np = pf::pad128(N);
+  float* partial = static_cast<float*>(ws);
+  if constexpr (sizeof(TC) == 2 && C == 128) {
+    const long ntiles = (long)B * Np * (Np / OutputVjpWs::BM);
+    PF_REQUIRE(ntiles < (1L << 31), PF_ERR_UNSUPPORTED, "trimul_output_vjp: B=%d N=%d too large", B, N);
+    const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+    trimul_output_vjp_ws_kernel<TZ><<<nblk, OutputVjpWs::NT, 0, s>>>(
+        (const TZ*)g, (const bf16*)X, (const TZ*)x, lnow, lnob, eps, (const bf16*)wo, (const bf16*)wog,
+        (const bf16*)wot, (const bf16*)wogt, B, N, Np, (bf16*)gp, (bf16*)gg, (bf16*)xln, (bf16*)dX, gx, partial);
+    if (int e = pf::check_launch("trimul_output_vjp")) return e;
+    trimul_ln_grad_reduce_kernel<<<2 * C, 256, 0, s>>>(partial, nblk, 2 * C, dlnw, dlnb);
+    return pf::check_launch("trimul_ln_grad_reduce");
+  }
   constexpr int BM = vjp_bm<TC, C>();
   const dim3 grid(Np / BM, Np, B);
-  float* partial = static_cast<float*>(ws);
   trimul_output_vjp_kernel<TZ, TC, C><<<grid, 256, 0, s>>>(
       (const TZ*)g, (const TC*)X, (const TZ*)x, lnow, lnob, eps, (const TC*)wo, (const TC*)wog, (const TC*)wot,
       (const TC*)wogt, B, N, Np, (TC*)gp, (TC*)gg, (TC*)xln, (TC*)dX, gx, partial);

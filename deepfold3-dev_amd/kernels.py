@@ -275,28 +275,6 @@ def fused_trimul(
     )  # fmt: skip
 
 
-def _token_chunk(B: int, N: int, target: int = 4096) -> int:
-    """A divisor of M = B N^2 near ``target`` tokens: N times the largest divisor d of B N with
-    N d <= max(target, N)."""
-    best = 1
-    for d in range(1, B * N + 1):
-        if N * d > max(target, N):
-            break
-        if (B * N) % d == 0:
-            best = d
-    return N * best
-
-
-def _weight_grad(a_cm: torch.Tensor, b: torch.Tensor, chunk: int) -> torch.Tensor:
-    """``a b`` in fp32 for channel-major ``a_cm`` [Ca, M] and token-major ``b`` [M, Cb], M in the
-    hundreds of thousands: split over token chunks as one batched GEMM on strided views (one
-    [Ca, Cb] output tile alone would leave the GPU idle), then summed over the chunks."""
-    Ca, M = a_cm.shape
-    S = M // chunk
-    a3 = a_cm.view(Ca, S, chunk).permute(1, 0, 2)  # [S, Ca, chunk], rows of stride M
-    return torch.bmm(a3, b.view(S, chunk, b.shape[1])).float().sum(0)
-
-
 def _split_chunk(M: int, target: int = 4096) -> int:
     """Token chunk for a split-K weight gradient over M tokens: the divisor of M in
     [target / 2, 2 target] closest to ``target``, else ``target`` (the rows past the last
@@ -428,7 +406,7 @@ class FusedTriMulFunction(torch.autograd.Function):
         g = g.to(xc.dtype).contiguous()
         kernel_census.record("TriangleMul.backward", "hip_trimul_vjp")
         pl = planes.view(cdt).view(3, B * C, Np, Np)
-        gp, gg = (torch.empty((C, M), dtype=cdt, device=dev) for _ in range(2))  # channel-major
+        gp, gg = (torch.empty((M, C), dtype=cdt, device=dev) for _ in range(2))  # token-major
         xln = torch.empty((M, C), dtype=cdt, device=dev)
         dX = torch.empty((B * C, Np, Np), dtype=cdt, device=dev)
         gx = torch.empty((M, C), dtype=torch.float32, device=dev)
@@ -443,9 +421,8 @@ class FusedTriMulFunction(torch.autograd.Function):
             dlnb.data_ptr(), ws.data_ptr(), ws_bytes, stream,
         )  # fmt: skip
         xb = xc.reshape(M, C).to(cdt)
-        chunk = _token_chunk(B, N)
-        d_out = _weight_grad(gp, xln, chunk)
-        d_out_gate = _weight_grad(gg, xb, chunk)
+        d_out = _weight_grad_tm(gp, xln)
+        d_out_gate = _weight_grad_tm(gg, xb)
         del gp, gg, xln
         # X = P Q^T per channel plane: dP = dX Q, dQ = dX^T P (contiguous operands)
         dpl = torch.empty((2, B * C, Np, Np), dtype=cdt, device=dev)

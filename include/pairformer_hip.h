@@ -121,11 +121,11 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
  *
  * pf_trimul_output_vjp (_output_vjp_kernel, fused_trimul.py:153-212): with g the update's
  * cotangent [B,N,N,C] (xdtype), X from `planes` and w_out_t, w_out_gate_t the transposed
- * [C,C] weights, writes gp = g s, gg = g p s (1 - s) channel-major [C, B*N*N] and
- * xln = LN_out(X) token-major [B*N*N, C] (cdtype), dX the cotangent of X (channel-major like X, zero at padding),
+ * [C,C] weights, writes gp = g s, gg = g p s (1 - s) and xln = LN_out(X), token-major
+ * [B*N*N, C] (cdtype), dX the cotangent of X (channel-major like X, zero at padding),
  * gx = gg Wog [B*N*N, C] fp32 and the LN_out affine gradients [C] fp32 (summed in a fixed
  * order). The host then forms dP = dX Q, dQ = dX^T P and the weight gradients
- * (w_out: gp^T xln, w_out_gate: gg^T x).
+ * (w_out: gp^T xln, w_out_gate: gg^T x). `workspace` holds per-block partial sums.
  *
  * pf_trimul_project_vjp (_project_vjp_kernel, fused_trimul.py:214-262): dplanes = [dP; dQ]
  * (two [B*C][Np][Np] cdtype sets), w_packed from pf_trimul_train_pack_weights and
