@@ -163,11 +163,13 @@ def kernel_figures(_lib, W, ops, attention, kernels, dev) -> list[dict]:
     return out
 
 
-def training_figures(ops, fused, dev, iters: int = 5) -> list[dict]:
-    """Forward and backward of the two differentiable paths at the trunk's shape (N=768,
-    bf16): the fused attention op over 768 lines of 4 heads, and the triangle multiply
-    module (outgoing) under grad. Times from CUDA events on torch's stream, which the
-    library launches on; medians over ``iters``."""
+def training_figures(ops, fused, evoformer, dev, iters: int = 5) -> list[dict]:
+    """Forward and backward at the trunk's shape (N=768): the fused attention op over 768
+    lines of 4 heads and the triangle multiply module (outgoing) under grad, in bf16; and one
+    training step (forward and backward) of a whole PairFormerBlock under bf16 autocast with
+    an fp32 pair stream, the reference's training regime (random weights, synthetic inputs).
+    Times from CUDA events on torch's stream, which the library launches on; medians over
+    ``iters``."""
     import torch
 
     out = []
@@ -228,6 +230,27 @@ def training_figures(ops, fused, dev, iters: int = 5) -> list[dict]:
     out.append({"op": "TriangleMulOutgoing backward", "config": "B=1 N=768 C=128 bf16", "fwd_ms": round(fwd_ms, 3),
                 "bwd_ms": round(bwd_ms, 3)})  # fmt: skip
     log(f"triangle multiply N={n}: fwd {fwd_ms:.3f} ms, bwd {bwd_ms:.3f} ms")
+    del m, z, gz, state["u"]
+    torch.cuda.empty_cache()
+
+    blk = evoformer.PairFormerBlock(128, 384).to(dev)
+    pair = torch.randn(1, n, n, 128, generator=g).to(dev).requires_grad_(True)
+    single = torch.randn(1, n, 384, generator=g).to(dev).requires_grad_(True)
+    pm, sm = torch.ones(1, n, n, device=dev), torch.ones(1, n, device=dev)
+    gp = torch.randn(1, n, n, 128, generator=g).to(dev)
+    gs = torch.randn(1, n, 384, generator=g).to(dev)
+
+    def block_step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            p, s = blk(pair, single, pm, sm)
+        torch.autograd.backward([p, s], [gp, gs])
+        blk.zero_grad(set_to_none=True)
+        pair.grad = single.grad = None
+
+    step_ms = median_ms(block_step)
+    out.append({"op": "PairFormerBlock training step", "config": "B=1 N=768 C=128, bf16 autocast, fp32 pair",
+                "step_ms": round(step_ms, 3), "peak_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2)})  # fmt: skip
+    log(f"PairFormerBlock training step N={n}: {step_ms:.3f} ms")
     return out
 
 
@@ -403,7 +426,7 @@ def main() -> int:
 
     if args.training:
         fused = import_module("deepfold3_dev_amd.fused")
-        print(json.dumps({"training": training_figures(ops, fused, dev)}), flush=True)
+        print(json.dumps({"training": training_figures(ops, fused, evoformer, dev)}), flush=True)
         return 0
 
     if args.kernels_only:
