@@ -37,6 +37,8 @@ SIGNATURES: dict[str, tuple] = {
     "pf_layernorm_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, ctypes.c_long, _i, _vp]),
     "pf_layernorm_bwd_workspace_bytes": (_sz, [ctypes.c_long, _i]),
     "pf_layernorm_bwd": (_i, [_vp, _vp, _i, _vp, _f, _vp, _vp, _vp, ctypes.c_long, _i, _vp, _sz, _vp]),
+    "pf_layernorm_fwd_mixed": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, ctypes.c_long, _i, _vp]),
+    "pf_layernorm_bwd_mixed": (_i, [_vp, _i, _vp, _i, _vp, _f, _vp, _vp, _vp, ctypes.c_long, _i, _vp, _sz, _vp]),
     "pf_ln_transpose_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, _i, _i, _i, _i, _vp]),
     "pf_trimul_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "pf_trimul_pack_weights": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp]),

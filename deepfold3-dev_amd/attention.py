@@ -87,9 +87,9 @@ class GridSelfAttention(nn.Module):
         H, D = self.num_heads, self.head_dim
         if D != 32:
             raise NotActive("GridSelfAttention", f"head dim {D}: the differentiable attention is built for 32")
-        from .kernels import LayerNormFunction, token_linear
+        from .kernels import layer_norm_for_gemm, token_linear
 
-        zn = LayerNormFunction.apply(z, self.norm.weight, self.norm.bias, self.norm.eps)
+        zn = layer_norm_for_gemm(z, self.norm.weight, self.norm.bias, self.norm.eps)
         pb = token_linear(zn, self.pair_bias.weight).permute(0, 3, 1, 2)  # [B, H, N, N], un-transposed z
         # q, k, v, g in one product over the un-transposed tokens; the column mode's lines are
         # the second token axis, taken by the permutation into the attention frame.

@@ -4,6 +4,9 @@
 //                        x's dtype (reference layer_norm, src/deepfold3/model/primitives.py:90-115).
 //   pf_ln_transpose_fwd: x [B,N1,N2,C] -> out [B,N2,N1,C] = LN(x).permute(0,2,1,3)
 //                        (reference FusedLayerNormTranspose, triton/layernorm_transpose.py:269-316).
+//   pf_layernorm_fwd_mixed / pf_layernorm_bwd_mixed: the same with the output (forward) or
+//                        the cotangent dy (backward) in a dtype of its own: the autocast training
+//                        path's LayerNorm of an fp32 stream feeding bf16 GEMMs, without the casts.
 //
 // C = 128 (the pair representation): 16 lanes per row, 16 rows per wave (layernorm128_kernel).
 // Other C: one wave per row; each lane owns C/128 chunks of two channels, so every load
@@ -28,12 +31,13 @@ struct Pair<bf16> {
 };
 
 // rows_per_wave rows per wave, each row C channels (C % 128 == 0).
-template <class T, int C>
+template <class T, int C, class TY = T>
 __global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                              const float* __restrict__ b, float eps,
-                                                             T* __restrict__ out, long M, int N1, int N2,
+                                                             TY* __restrict__ out, long M, int N1, int N2,
                                                              int transpose) {
   using V2 = typename Pair<T>::V;
+  using VY = typename Pair<TY>::V;
   constexpr int CH = C / 128;  // two-channel chunks per lane
   const int l = lane_id();
   const long row = (long)blockIdx.x * 4 + wave_id();
@@ -65,14 +69,14 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* __restrict
     const long bb = t / N1;
     orow = (bb * N2 + j) * N1 + i;
   }
-  T* dst = out + orow * C;
+  TY* dst = out + orow * C;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int ch = c * 128 + 2 * l;
-    V2 o;
-    o[0] = from_f32<T>((v[c][0] - mean) * rstd * w[ch] + b[ch]);
-    o[1] = from_f32<T>((v[c][1] - mean) * rstd * w[ch + 1] + b[ch + 1]);
-    *reinterpret_cast<V2*>(dst + ch) = o;
+    VY o;
+    o[0] = from_f32<TY>((v[c][0] - mean) * rstd * w[ch] + b[ch]);
+    o[1] = from_f32<TY>((v[c][1] - mean) * rstd * w[ch + 1] + b[ch + 1]);
+    *reinterpret_cast<VY*>(dst + ch) = o;
   }
 }
 
@@ -82,16 +86,17 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* __restrict
 // where the one-wave-per-row kernel has 4). Row statistics are two-pass fp32 sums over the
 // 16 lanes (DPP within the row of 16 lanes). Each output row is one contiguous 256- or
 // 512-byte store, whether or not it is transposed.
-template <class T>
+template <class T, class TY = T>
 __global__ __launch_bounds__(256) void layernorm128_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ b, float eps,
-                                                           T* __restrict__ out, long M, int N1, int N2,
+                                                           TY* __restrict__ out, long M, int N1, int N2,
                                                            int transpose) {
   constexpr int C = 128;
   constexpr int R = 4;                     // rows per lane group
   constexpr int LPR = 16;                  // lanes per row
   constexpr int VL = 16 / sizeof(T);       // channels per 16-byte load
   constexpr int NL = 8 / VL;               // loads per lane per row
+  constexpr int VY = 16 / sizeof(TY);      // channels per 16-byte store
   const int l = lane_id();
   const int grp = l / LPR, q = l % LPR;
   const long row0 = ((long)blockIdx.x * 4 + wave_id()) * (R * 64 / LPR);
@@ -139,7 +144,7 @@ __global__ __launch_bounds__(256) void layernorm128_kernel(const T* __restrict__
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = (v[r][e] - mean) * rstd * wv[e] + bv[e];
 #pragma unroll
-    for (int h = 0; h < NL; ++h) store_vec<T, VL>(out + orow * C + 8 * q + VL * h, o + VL * h);
+    for (int h = 0; h < 8 / VY; ++h) store_vec<TY, VY>(out + orow * C + 8 * q + VY * h, o + VY * h);
   }
 }
 
@@ -150,8 +155,8 @@ __global__ __launch_bounds__(256) void layernorm128_kernel(const T* __restrict__
 // dy * xn (weight) and dy (bias), added in block order by ln_param_grad_reduce.
 constexpr int kLnbRows = 64;
 
-template <class T, int C>
-__global__ __launch_bounds__(256) void layernorm_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+template <class T, int C, class TD = T>
+__global__ __launch_bounds__(256) void layernorm_bwd_kernel(const T* __restrict__ x, const TD* __restrict__ dy,
                                                             const float* __restrict__ w, float eps, long M,
                                                             T* __restrict__ dx, float* __restrict__ partial) {
   constexpr int CPL = C / 64;  // channels per lane
@@ -230,15 +235,15 @@ __global__ __launch_bounds__(256) void ln_param_grad_reduce_kernel(const float* 
   }
 }
 
-template <class T>
+template <class T, class TD = T>
 int ln_bwd_launch(const void* x, const void* dy, const float* w, float eps, long M, int C, void* dx, float* dw,
                   float* db, void* ws, hipStream_t s) {
   const long nblk = (M + kLnbRows - 1) / kLnbRows;
   float* partial = static_cast<float*>(ws);
   auto run = [&](auto cc) {
     constexpr int CC = decltype(cc)::value;
-    layernorm_bwd_kernel<T, CC><<<(unsigned)nblk, 256, 0, s>>>((const T*)x, (const T*)dy, w, eps, M, (T*)dx,
-                                                                partial);
+    layernorm_bwd_kernel<T, CC, TD><<<(unsigned)nblk, 256, 0, s>>>((const T*)x, (const TD*)dy, w, eps, M, (T*)dx,
+                                                                    partial);
   };
   switch (C) {
     case 64: run(std::integral_constant<int, 64>{}); break;
@@ -252,27 +257,27 @@ int ln_bwd_launch(const void* x, const void* dy, const float* w, float eps, long
   return pf::check_launch("ln_param_grad_reduce");
 }
 
-template <class T>
+template <class T, class TY = T>
 int ln_dispatch(const void* x, const float* w, const float* b, float eps, void* out, long M, int C, int N1, int N2,
                 int transpose, hipStream_t s) {
   dim3 grid((unsigned)((M + 3) / 4));
   pf::KernelTimer timer(transpose ? "ln_transpose" : "layernorm", s);
   switch (C) {
     case 128:
-      layernorm128_kernel<T><<<dim3((unsigned)((M + 63) / 64)), 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1,
-                                                                            N2, transpose);
+      layernorm128_kernel<T, TY><<<dim3((unsigned)((M + 63) / 64)), 256, 0, s>>>((const T*)x, w, b, eps, (TY*)out, M,
+                                                                                N1, N2, transpose);
       break;
     case 256:
-      layernorm_rows_kernel<T, 256><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
+      layernorm_rows_kernel<T, 256, TY><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (TY*)out, M, N1, N2, transpose);
       break;
     case 384:
-      layernorm_rows_kernel<T, 384><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
+      layernorm_rows_kernel<T, 384, TY><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (TY*)out, M, N1, N2, transpose);
       break;
     case 512:
-      layernorm_rows_kernel<T, 512><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (T*)out, M, N1, N2, transpose);
+      layernorm_rows_kernel<T, 512, TY><<<grid, 256, 0, s>>>((const T*)x, w, b, eps, (TY*)out, M, N1, N2, transpose);
       break;
     default:
-      if (!transpose && C > 0) return ln_launch<T, T>(x, w, b, eps, out, M, C, s);  // any other width: wave per row
+      if (!transpose && C > 0) return ln_launch<T, TY>(x, w, b, eps, out, M, C, s);  // any other width: wave per row
       pf::set_error(PF_ERR_UNSUPPORTED, "layernorm + transpose: C=%d (built: 128, 256, 384, 512)", C);
       return PF_ERR_UNSUPPORTED;
   }
@@ -325,6 +330,41 @@ int pf_layernorm_bwd(const void* x, const void* dy, int dtype, const float* w, f
   hipStream_t s = pf::as_stream(stream);
   if (dtype == PF_F32) return ln_bwd_launch<float>(x, dy, w, eps, M, C, dx, dw, db, workspace, s);
   return ln_bwd_launch<bf16>(x, dy, w, eps, M, C, dx, dw, db, workspace, s);
+}
+
+int pf_layernorm_fwd_mixed(const void* x, int xdtype, const float* w, const float* b, float eps, void* out,
+                           int odtype, long M, int C, void* stream) {
+  PF_REQUIRE(x && w && b && out, PF_ERR_INVALID_ARG, "pf_layernorm_fwd_mixed: null pointer");
+  PF_REQUIRE(M >= 0, PF_ERR_INVALID_ARG, "pf_layernorm_fwd_mixed: M=%ld", M);
+  PF_REQUIRE((xdtype == PF_F32 || xdtype == PF_BF16) && (odtype == PF_F32 || odtype == PF_BF16), PF_ERR_UNSUPPORTED,
+             "pf_layernorm_fwd_mixed: dtypes %d -> %d", xdtype, odtype);
+  if (M == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  if (xdtype == PF_F32)
+    return odtype == PF_F32 ? ln_dispatch<float, float>(x, w, b, eps, out, M, C, 1, 1, 0, s)
+                            : ln_dispatch<float, bf16>(x, w, b, eps, out, M, C, 1, 1, 0, s);
+  return odtype == PF_F32 ? ln_dispatch<bf16, float>(x, w, b, eps, out, M, C, 1, 1, 0, s)
+                          : ln_dispatch<bf16, bf16>(x, w, b, eps, out, M, C, 1, 1, 0, s);
+}
+
+int pf_layernorm_bwd_mixed(const void* x, int xdtype, const void* dy, int dydtype, const float* w, float eps,
+                           void* dx, float* dw, float* db, long M, int C, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  PF_REQUIRE(x && dy && w && dx && dw && db, PF_ERR_INVALID_ARG, "pf_layernorm_bwd_mixed: null pointer");
+  PF_REQUIRE(M > 0, PF_ERR_INVALID_ARG, "pf_layernorm_bwd_mixed: M=%ld", M);
+  PF_REQUIRE(C == 64 || C == 128 || C == 256 || C == 384 || C == 512, PF_ERR_UNSUPPORTED,
+             "pf_layernorm_bwd_mixed: C=%d (built: 64, 128, 256, 384, 512)", C);
+  PF_REQUIRE((xdtype == PF_F32 || xdtype == PF_BF16) && (dydtype == PF_F32 || dydtype == PF_BF16), PF_ERR_UNSUPPORTED,
+             "pf_layernorm_bwd_mixed: dtypes x %d dy %d", xdtype, dydtype);
+  PF_REQUIRE(workspace && workspace_bytes >= pf_layernorm_bwd_workspace_bytes(M, C), PF_ERR_WORKSPACE,
+             "pf_layernorm_bwd_mixed: workspace %zu < %zu bytes", workspace_bytes,
+             pf_layernorm_bwd_workspace_bytes(M, C));
+  hipStream_t s = pf::as_stream(stream);
+  if (xdtype == PF_F32)
+    return dydtype == PF_F32 ? ln_bwd_launch<float, float>(x, dy, w, eps, M, C, dx, dw, db, workspace, s)
+                             : ln_bwd_launch<float, bf16>(x, dy, w, eps, M, C, dx, dw, db, workspace, s);
+  return dydtype == PF_F32 ? ln_bwd_launch<bf16, float>(x, dy, w, eps, M, C, dx, dw, db, workspace, s)
+                           : ln_bwd_launch<bf16, bf16>(x, dy, w, eps, M, C, dx, dw, db, workspace, s);
 }
 
 }  // extern "C"

@@ -150,7 +150,7 @@ class PairFormerBlock(nn.Module):
         each branch's training path (triangle multiplications and attention, transitions and
         single attention on the HIP kernels with their backward), residual adds in autograd,
         every residual scale folded into its branch's output projection."""
-        from .kernels import LayerNormFunction, token_linear
+        from .kernels import layer_norm_for_gemm, token_linear
 
         kernel_census.record("PairFormerBlock", "hip_block_grad")
         p = pair + self.tri_mul_out(pair, pair_mask)
@@ -159,7 +159,7 @@ class PairFormerBlock(nn.Module):
         p = p + self.pair_attn_col(p, pair_mask)
         p = p + self.pair_transition(p)
         n = self.single_to_pair_norm
-        logits = token_linear(LayerNormFunction.apply(p, n.weight, n.bias, n.eps), self.single_to_pair.weight)
+        logits = token_linear(layer_norm_for_gemm(p, n.weight, n.bias, n.eps), self.single_to_pair.weight)
         s = single + self.single_attn(single, seq_mask, logits.movedim(-1, -3))
         s = s + self.single_transition(s)
         return p, s

@@ -29,6 +29,7 @@ from .kernels import (
     SwiGLUFunction,
     cast_weight,
     gemm_dtype_for,
+    layer_norm_for_gemm,
     ln_transpose,
     residual_add,
     token_linear,
@@ -195,7 +196,7 @@ class FusedPairBias(nn.Module):
         _lib.require_device("FusedPairBias", z)
         if torch.is_grad_enabled():
             kernel_census.record("GridSelfAttention.norm", "hip_pair_bias_grad")
-            out = token_linear(LayerNormFunction.apply(z, ln_weight, ln_bias, self.eps), proj_weight).permute(0, 3, 1, 2)
+            out = token_linear(layer_norm_for_gemm(z, ln_weight, ln_bias, self.eps), proj_weight).permute(0, 3, 1, 2)
             if mask is not None:
                 out = out + (1.0 - mask.to(out.dtype))[:, None, None, :] * (-1e9)
             return out
@@ -260,7 +261,7 @@ class FusedLayerNormLinear(nn.Module):
             raise NotActive("FusedLayerNormLinear", f"weight must be [K, N] = [{K}, {N}]")
         if torch.is_grad_enabled():
             kernel_census.record("FusedLayerNormLinear", "hip_layernorm_grad")
-            y = token_linear(LayerNormFunction.apply(X, ln_weight, ln_bias, 1e-5), linear_weight.t())
+            y = token_linear(layer_norm_for_gemm(X, ln_weight, ln_bias, 1e-5), linear_weight.t())
             return y if linear_bias is None else y + linear_bias
         cdt = gemm_dtype_for(X)
         Xc = X.contiguous()

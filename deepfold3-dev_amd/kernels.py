@@ -107,15 +107,30 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: f
 class LayerNormFunction(torch.autograd.Function):
     """Differentiable LayerNorm on the HIP kernels (``primitives.py:90-115`` semantics: fp32
     statistics, output in x's dtype): ``pf_layernorm_fwd`` and ``pf_layernorm_bwd``, the
-    affine gradients summed over rows in a fixed order. ``apply(x, weight, bias, eps)``."""
+    affine gradients summed over rows in a fixed order. ``apply(x, weight, bias, eps)``;
+    ``apply(x, weight, bias, eps, out_dtype)`` writes the output in ``out_dtype`` instead
+    (``pf_layernorm_fwd_mixed``). The backward takes the cotangent in its own dtype
+    (``pf_layernorm_bwd_mixed``) and returns dx in x's dtype."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, eps):
+    def forward(ctx, x, weight, bias, eps, *out_dtype):
         xc = x.detach().contiguous()
-        out = layer_norm(xc, weight, bias, eps)
+        odt = out_dtype[0] if out_dtype and out_dtype[0] is not None else xc.dtype
+        if odt == xc.dtype:
+            out = layer_norm(xc, weight, bias, eps)
+        else:
+            _lib.require_device("layer_norm", xc)
+            C = xc.shape[-1]
+            out = torch.empty(xc.shape, dtype=odt, device=xc.device)
+            _lib.call(
+                "pf_layernorm_fwd_mixed", xc.data_ptr(), _lib.dtype_code(xc.dtype), _f32(weight).data_ptr(),
+                _f32(bias).data_ptr(), float(eps), out.data_ptr(), _lib.dtype_code(odt), xc.numel() // C, C,
+                _lib.stream_of(xc),
+            )  # fmt: skip
         ctx.save_for_backward(xc, weight)
         ctx.eps = float(eps)
         ctx.dtypes = (weight.dtype, bias.dtype)
+        ctx.nextra = len(out_dtype)
         return out
 
     @staticmethod
@@ -123,17 +138,28 @@ class LayerNormFunction(torch.autograd.Function):
         xc, weight = ctx.saved_tensors
         C = xc.shape[-1]
         M = xc.numel() // C
-        dyc = dy.to(xc.dtype).contiguous()
+        dyc = dy.contiguous() if dy.dtype in (torch.float32, torch.bfloat16) else dy.to(xc.dtype).contiguous()
         dx = torch.empty_like(xc)
         dw, db = (torch.empty(C, dtype=torch.float32, device=xc.device) for _ in range(2))
         ws_bytes = _lib.lib().pf_layernorm_bwd_workspace_bytes(M, C)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=xc.device)
         kernel_census.record("LayerNorm.backward", "hip_layernorm_bwd")
         _lib.call(
-            "pf_layernorm_bwd", xc.data_ptr(), dyc.data_ptr(), _lib.dtype_code(xc.dtype), _f32(weight).data_ptr(),
-            ctx.eps, dx.data_ptr(), dw.data_ptr(), db.data_ptr(), M, C, ws.data_ptr(), ws_bytes, _lib.stream_of(xc),
+            "pf_layernorm_bwd_mixed", xc.data_ptr(), _lib.dtype_code(xc.dtype), dyc.data_ptr(),
+            _lib.dtype_code(dyc.dtype), _f32(weight).data_ptr(), ctx.eps, dx.data_ptr(), dw.data_ptr(), db.data_ptr(),
+            M, C, ws.data_ptr(), ws_bytes, _lib.stream_of(xc),
         )  # fmt: skip
-        return dx, dw.to(ctx.dtypes[0]), db.to(ctx.dtypes[1]), None
+        return (dx, dw.to(ctx.dtypes[0]), db.to(ctx.dtypes[1]), None) + (None,) * ctx.nextra
+
+
+def layer_norm_for_gemm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float) -> torch.Tensor:
+    """Differentiable LayerNorm whose output feeds GEMMs. Under bf16 autocast an fp32 x gives
+    the bf16 output the next GEMM would cast it to, in the same pass (the reference's
+    autocast path: fp32 LayerNorm, then the cast), and the cotangent comes back in bf16."""
+    dev = x.device.type
+    if x.dtype == torch.float32 and torch.is_autocast_enabled(dev) and torch.get_autocast_dtype(dev) == torch.bfloat16:
+        return LayerNormFunction.apply(x, weight, bias, eps, torch.bfloat16)
+    return LayerNormFunction.apply(x, weight, bias, eps)
 
 
 class SwiGLUFunction(torch.autograd.Function):

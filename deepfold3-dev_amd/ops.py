@@ -19,9 +19,9 @@ from .config import OptimConfig, require_hip
 from .inference_guard import NotActive, inference_only
 from .kernels import (
     FusedTriMulFunction,
-    LayerNormFunction,
     cast_weight,
     gemm_dtype_for,
+    layer_norm_for_gemm,
     pack_trimul_weights,
     scaled_weight,
     trimul_forward,
@@ -91,7 +91,7 @@ class _TriangleMulBase(nn.Module):
         """Training path (``ops.py:375-388``): ``norm_left`` (the HIP LayerNorm and its backward),
         then the HIP ``FusedTriMulFunction`` with its VJP kernels."""
         nl = self.norm_left
-        x = LayerNormFunction.apply(z, nl.weight, nl.bias, nl.eps)
+        x = layer_norm_for_gemm(z, nl.weight, nl.bias, nl.eps)
         order = self._block_order.to(z.device)
         w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
         return FusedTriMulFunction.apply(

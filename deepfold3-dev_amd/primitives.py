@@ -150,9 +150,9 @@ class TransitionBlock(nn.Module):
         over a pair's tokens), the branch scale on linear2."""
         import torch.nn.functional as F
 
-        from .kernels import LayerNormFunction, SwiGLUFunction, token_linear
+        from .kernels import SwiGLUFunction, layer_norm_for_gemm, token_linear
 
-        xn = LayerNormFunction.apply(x, self.norm.weight, self.norm.bias, self.norm.eps)
+        xn = layer_norm_for_gemm(x, self.norm.weight, self.norm.bias, self.norm.eps)
         w2 = self.linear2.weight if self.branch_scale == 1.0 else self.linear2.weight * self.branch_scale
         return token_linear(SwiGLUFunction.apply(token_linear(xn, self.linear1.weight)), w2)
 

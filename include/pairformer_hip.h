@@ -78,6 +78,16 @@ int pf_layernorm_fwd(const void* x, int dtype, const float* w, const float* b, f
 size_t pf_layernorm_bwd_workspace_bytes(long M, int C);
 int pf_layernorm_bwd(const void* x, const void* dy, int dtype, const float* w, float eps, void* dx, float* dw,
                      float* db, long M, int C, void* workspace, size_t workspace_bytes, void* stream);
+/* Mixed-dtype LayerNorm (no counterpart in the reference, whose autocast path runs the
+ * fp32 LayerNorm and then casts its output to bf16 for the next GEMM, and the cotangent back):
+ * pf_layernorm_fwd_mixed writes LN(x) in odtype; pf_layernorm_bwd_mixed takes dy in dydtype
+ * and writes dx in x's dtype. Same kernels, arithmetic and C range as the single-dtype entry
+ * points; the autocast training path's input LayerNorms use them. */
+int pf_layernorm_fwd_mixed(const void* x, int xdtype, const float* w, const float* b, float eps, void* out,
+                           int odtype, long M, int C, void* stream);
+int pf_layernorm_bwd_mixed(const void* x, int xdtype, const void* dy, int dydtype, const float* w, float eps,
+                           void* dx, float* dw, float* db, long M, int C, void* workspace, size_t workspace_bytes,
+                           void* stream);
 /* x [B,N1,N2,C] -> out [B,N2,N1,C] (do_transpose) or [B,N1,N2,C]: LN then permute(0,2,1,3).
  * Replaces FusedLayerNormTranspose(C, do_transpose)(x, w, b) (triton/layernorm_transpose.py:269-316). */
 int pf_ln_transpose_fwd(const void* x, int dtype, const float* w, const float* b, float eps, void* out, int B, int N1,
