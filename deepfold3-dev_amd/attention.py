@@ -79,9 +79,11 @@ class GridSelfAttention(nn.Module):
     def _forward_grad(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
         """Training path, as the reference's fused-attention branch (``attention.py:211-257``):
         LayerNorm, pair bias and q/k/v/g projections in autograd, the HIP flash attention with
-        its backward (``fused._EvoformerAttention``, the kernel's masked-row rule), gate and
-        output projection in autograd. Head dimension 32."""
-        from .fused import _EvoformerAttention
+        its backward (the kernel's masked-row rule), gate and output projection in autograd.
+        With 4 heads the attention (``fused._GridAttnCore``) reads the token-major projection
+        and writes O and the gradients in that order through strides; other head counts go
+        through the kernel-layout ``fused._EvoformerAttention``. Head dimension 32."""
+        from .fused import _EvoformerAttention, _GridAttnCore
 
         B, N, _, C = z.shape
         H, D = self.num_heads, self.head_dim
@@ -91,20 +93,26 @@ class GridSelfAttention(nn.Module):
 
         zn = layer_norm_for_gemm(z, self.norm.weight, self.norm.bias, self.norm.eps)
         pb = token_linear(zn, self.pair_bias.weight).permute(0, 3, 1, 2)  # [B, H, N, N], un-transposed z
-        # q, k, v, g in one product over the un-transposed tokens; the column mode's lines are
-        # the second token axis, taken by the permutation into the attention frame.
-        w_qkvg = torch.cat([self.to_q.weight, self.to_k.weight, self.to_v.weight, self.to_g.weight])
-        y = token_linear(zn, w_qkvg).view(B, N, N, 4, H, D).unbind(3)  # backward: one stack
+        pb = pb.to(torch.float32, memory_format=torch.contiguous_format)
+        line_mask = mask.transpose(1, 2) if self.transpose else mask  # [B, lines, keys]
+        res_mask = torch.where(line_mask > 0.5, 0.0, -1e9).contiguous()
+        w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
+        g = torch.sigmoid(token_linear(zn, self.to_g.weight))
+        if H == 4:
+            # q, k, v in one product over the un-transposed tokens; the attention reads them and
+            # writes O (and, backward, the gradients) in that token order through strides
+            w_qkv = torch.cat([self.to_q.weight, self.to_k.weight, self.to_v.weight])
+            qkv = token_linear(zn, w_qkv).view(B, N, N, 3, H, D)
+            o = _GridAttnCore.apply(qkv, res_mask, pb, self.transpose)
+            return token_linear(o.view(B, N, N, H * D) * g, w_out)
+        # other head counts: the kernel-layout op with its head groups
+        w_qkv = torch.cat([self.to_q.weight, self.to_k.weight, self.to_v.weight])
+        y = token_linear(zn, w_qkv).view(B, N, N, 3, H, D).unbind(3)  # backward: one stack
         frame = (0, 2, 3, 1, 4) if self.transpose else (0, 1, 3, 2, 4)  # [B, line, H, key, D]
-        qkv = [t.permute(*frame).contiguous() for t in y[:3]]
-        if self.transpose:
-            mask = mask.transpose(1, 2)
-        res_mask = torch.where(mask > 0.5, 0.0, -1e9).view(B, N, 1, 1, N)
-        o = _EvoformerAttention.apply(*qkv, res_mask, pb.unsqueeze(1).float(), True)
+        qkv = [t.permute(*frame).contiguous() for t in y]
+        o = _EvoformerAttention.apply(*qkv, res_mask.view(B, N, 1, 1, N), pb.unsqueeze(1), True)
         back = (0, 3, 1, 2, 4) if self.transpose else (0, 1, 3, 2, 4)  # to [B, N, N, H, D]
         o = o.permute(*back).reshape(B, N, N, H * D)
-        g = torch.sigmoid(y[3].reshape(B, N, N, H * D))
-        w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
         return token_linear(o * g, w_out)
 
     def forward(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:

@@ -515,6 +515,12 @@ constexpr float kRaise = 32.0f;
 constexpr float kLower = 64.0f;
 constexpr int kBiasStages = 3;  // LDS ring of pair-bias tiles, filled two key blocks ahead
 
+// Element strides of one [B][S][H][N][D] operand view of the kernel-level attention op (D
+// contiguous): batch item, line, head, key. Zero strides mean the dense [b][line][h][q][d].
+struct Strides4 {
+  long b, s, h, n;
+};
+
 // XOR swizzle of the 16-byte chunks of a 128-byte bias row: the 16 lanes of a ds_read_b128
 // (rows R..R+15, one logical chunk) land on 16 distinct bank groups.
 PF_DEVICE int bias_swz(int row) { return (row >> 1) & 7; }
@@ -595,7 +601,7 @@ template <class TC, int QS, bool O_HEAD_MAJOR, bool FAST, bool POST_SCALE = fals
 __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2)) void tri_attn_kernel(
     const TC* __restrict__ Q, const TC* __restrict__ K, const TC* __restrict__ Vt, const float* __restrict__ PB,
     const float* __restrict__ MA, TC* __restrict__ O, int B, int N, int Np, int L, int Lp, int zero_masked_lines,
-    int xcd_remap, int* __restrict__ redo, float post_scale = 1.f) {
+    int xcd_remap, int* __restrict__ redo, float post_scale = 1.f, Strides4 ost = {}) {
   constexpr int QB = 32 * QS;
   constexpr int NT = 64 * kLinesPerBlock;
   constexpr int QLD = kHeadDim + (sizeof(TC) == 2 ? 0 : lds_pad<TC>());
@@ -989,8 +995,12 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
     const float inv = write_zero ? 0.f : 1.0f / lt;
     const int q = q0 + 32 * s + lq;
     if (q >= N) continue;
-    TC* dst = O_HEAD_MAJOR ? O + ((lineq * kHeads + h) * (size_t)N + q) * kHeadDim
-                           : O + (lineq * (size_t)Np + q) * kC + h * kHeadDim;
+    TC* dst;
+    if constexpr (O_HEAD_MAJOR)
+      dst = ost.n ? O + b * ost.b + line * ost.s + h * ost.h + q * ost.n
+                  : O + ((lineq * kHeads + h) * (size_t)N + q) * kHeadDim;
+    else
+      dst = O + (lineq * (size_t)Np + q) * kC + h * kHeadDim;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v[4];
@@ -1523,8 +1533,8 @@ __global__ __launch_bounds__(256) void mask_outer_check_kernel(const float* __re
 // -inf mask entries become -1e9.
 template <class TC>
 __global__ __launch_bounds__(256) void evo_pack_qk_kernel(const TC* __restrict__ q, const TC* __restrict__ k,
-                                                          TC* __restrict__ Qw, TC* __restrict__ Kw, int N, int Np,
-                                                          float qscale) {
+                                                          TC* __restrict__ Qw, TC* __restrict__ Kw, int S, int N,
+                                                          int Np, float qscale, Strides4 sx) {
   constexpr int VEC = 16 / sizeof(TC);
   constexpr int CPT = kHeadDim / VEC;  // chunks per token
   const size_t bsh = blockIdx.y;       // (b, s, h) flattened
@@ -1534,8 +1544,10 @@ __global__ __launch_bounds__(256) void evo_pack_qk_kernel(const TC* __restrict__
   const int d0 = (idx % CPT) * VEC;
   float vq[VEC], vk[VEC];
   if (t < N) {
-    load16<TC>(q + (bsh * N + t) * kHeadDim + d0, vq);
-    load16<TC>(k + (bsh * N + t) * kHeadDim + d0, vk);
+    const long off = (long)(bsh / ((size_t)S * kHeads)) * sx.b + (long)((bsh / kHeads) % S) * sx.s +
+                     (long)(bsh % kHeads) * sx.h + (long)t * sx.n + d0;
+    load16<TC>(q + off, vq);
+    load16<TC>(k + off, vk);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) vq[e] *= qscale;
   } else {
@@ -1551,14 +1563,16 @@ __global__ __launch_bounds__(256) void evo_pack_qk_kernel(const TC* __restrict__
 
 // One block per (32-key block, b s h): V[t][d] -> Vt[d][slot] (bf16: the key-block tile).
 template <class TC>
-__global__ __launch_bounds__(256) void evo_pack_v_kernel(const TC* __restrict__ v, TC* __restrict__ Vt, int N,
-                                                         int Np) {
+__global__ __launch_bounds__(256) void evo_pack_v_kernel(const TC* __restrict__ v, TC* __restrict__ Vt, int S,
+                                                         int N, int Np, Strides4 sx) {
   __shared__ float tile[32][kHeadDim + 1];
   const size_t bsh = blockIdx.y;
   const int k0 = blockIdx.x * 32;
+  const TC* vl = v + (long)(bsh / ((size_t)S * kHeads)) * sx.b + (long)((bsh / kHeads) % S) * sx.s +
+                 (long)(bsh % kHeads) * sx.h;
   for (int i = threadIdx.x; i < 32 * kHeadDim; i += 256) {
     const int t = i / kHeadDim, d = i % kHeadDim;
-    tile[t][d] = (k0 + t < N) ? to_f32(v[(bsh * N + k0 + t) * kHeadDim + d]) : 0.f;
+    tile[t][d] = (k0 + t < N) ? to_f32(vl[(long)(k0 + t) * sx.n + d]) : 0.f;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < 32 * kHeadDim; i += 256) {
@@ -1623,7 +1637,12 @@ EvoWs evo_ws_layout(int B, int S, int N, int cdtype) {
 template <class TC>
 int evo_attn_launch(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias, int B,
                     int S, int N, int zero_rule, void* out, void* ws, hipStream_t s,
-                    float softmax_scale = 1.0f / sqrtf((float)kHeadDim)) {
+                    float softmax_scale = 1.0f / sqrtf((float)kHeadDim), const Strides4* sx_in = nullptr,
+                    const Strides4* so_in = nullptr) {
+  const Strides4 sx = sx_in ? *sx_in
+                            : Strides4{(long)S * kHeads * N * kHeadDim, (long)kHeads * N * kHeadDim,
+                                       (long)N * kHeadDim, kHeadDim};
+  const Strides4 so = so_in ? *so_in : Strides4{};
   const int Np = (int)pf::round_up((size_t)N, kPad);
   const EvoWs L = evo_ws_layout(B, S, N, sizeof(TC) == 4 ? PF_F32 : PF_BF16);
   char* base = reinterpret_cast<char*>(ws);
@@ -1642,8 +1661,8 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   const unsigned bsh = (unsigned)(B * S * kHeads);
   constexpr int VEC = 16 / sizeof(TC);
   evo_pack_qk_kernel<TC><<<dim3((Np * (kHeadDim / VEC) + 255) / 256, bsh), 256, 0, s>>>(
-      (const TC*)q, (const TC*)k, Qw, Kw, N, Np, qscale);
-  evo_pack_v_kernel<TC><<<dim3(Np / 32, bsh), 256, 0, s>>>((const TC*)v, Vw, N, Np);
+      (const TC*)q, (const TC*)k, Qw, Kw, S, N, Np, qscale, sx);
+  evo_pack_v_kernel<TC><<<dim3(Np / 32, bsh), 256, 0, s>>>((const TC*)v, Vw, S, N, Np, sx);
   evo_pack_bias_kernel<<<dim3((unsigned)(((long)Np * Np + 255) / 256), B * kHeads), 256, 0, s>>>(pair_bias, PBw,
                                                                                                    N, Np, bscale);
   evo_pack_mask_kernel<<<dim3((Np + 255) / 256, B * S), 256, 0, s>>>(res_mask, MAw, N, Np, bscale);
@@ -1656,10 +1675,10 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   const int remap = (total % 8 == 0) ? 1 : 0;
   pf::KernelTimer timer("evo_attn", s);
   tri_attn_kernel<TC, QS, true, true, kPost><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
-      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post);
+      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post, so);
   if (int e = pf::check_launch("evo_attn")) return e;
   tri_attn_kernel<TC, QS, true, false, kPost><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
-      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post);
+      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post, so);
   timer.stop();
   return pf::check_launch("evo_attn redo");
 }
@@ -1914,6 +1933,37 @@ int pf_evo_attn_fwd(const void* q, const void* k, const void* v, const float* re
   if (dtype == PF_F32)
     return evo_attn_launch<float>(q, k, v, res_mask, pair_bias, B, S, N, masked_rows_zero, out, workspace, s);
   return evo_attn_launch<bf16>(q, k, v, res_mask, pair_bias, B, S, N, masked_rows_zero, out, workspace, s);
+}
+
+int pf_evo_attn_fwd_strided(const void* q, const void* k, const void* v, const long* qkv_strides,
+                            const float* res_mask, const float* pair_bias, int B, int S, int H, int N, int D,
+                            int dtype, int masked_rows_zero, void* out, const long* out_strides, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(q && k && v && qkv_strides && res_mask && pair_bias && out && out_strides && workspace,
+             PF_ERR_INVALID_ARG, "pf_evo_attn_fwd_strided: null pointer");
+  PF_REQUIRE(B > 0 && S > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_evo_attn_fwd_strided: B=%d S=%d N=%d", B, S, N);
+  PF_REQUIRE(H == kHeads && D == kHeadDim, PF_ERR_UNSUPPORTED,
+             "pf_evo_attn_fwd_strided: H=%d D=%d (built: H=4, D=32)", H, D);
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_evo_attn_fwd_strided: dtype %d", dtype);
+  const Strides4 sx{qkv_strides[0], qkv_strides[1], qkv_strides[2], qkv_strides[3]};
+  const Strides4 so{out_strides[0], out_strides[1], out_strides[2], out_strides[3]};
+  const long vec = dtype == PF_F32 ? 4 : 8;  // elements per 16 bytes
+  for (const Strides4* st : {&sx, &so})
+    PF_REQUIRE(st->b % vec == 0 && st->s % vec == 0 && st->h % vec == 0 && st->n % vec == 0 && st->n >= kHeadDim,
+               PF_ERR_ALIGNMENT, "pf_evo_attn_fwd_strided: strides must keep 16-byte aligned rows of D elements");
+  PF_REQUIRE(pf::aligned16(q) && pf::aligned16(k) && pf::aligned16(v) && pf::aligned16(out) &&
+                 pf::aligned16(workspace),
+             PF_ERR_ALIGNMENT, "pf_evo_attn_fwd_strided: pointers must be 16-byte aligned");
+  PF_REQUIRE(workspace_bytes >= evo_ws_layout(B, S, N, dtype).total, PF_ERR_WORKSPACE,
+             "pf_evo_attn_fwd_strided: workspace %zu < %zu bytes", workspace_bytes,
+             evo_ws_layout(B, S, N, dtype).total);
+  hipStream_t s = pf::as_stream(stream);
+  const float sc = 1.0f / sqrtf((float)kHeadDim);
+  if (dtype == PF_F32)
+    return evo_attn_launch<float>(q, k, v, res_mask, pair_bias, B, S, N, masked_rows_zero, out, workspace, s, sc, &sx,
+                                  &so);
+  return evo_attn_launch<bf16>(q, k, v, res_mask, pair_bias, B, S, N, masked_rows_zero, out, workspace, s, sc, &sx,
+                               &so);
 }
 
 }  // extern "C"

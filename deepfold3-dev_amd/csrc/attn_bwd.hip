@@ -43,6 +43,13 @@ constexpr int kSubKv = 1;          // 32-key sub-tiles per wave in the dK / dV k
 // Zero masked-row rule threshold in log2 units (the reference tests t < -1e8).
 constexpr float kDeadLog2 = -1.0e8f * kLog2e;
 
+// Element strides of one [B][S][H][N][D] operand view (D contiguous): batch item, line, head
+// and key (row); a dense operand has {S H N D, H N D, N D, D}.
+struct Strides4 {
+  long b, s, h, n;
+};
+PF_DEVICE long line_offset(const Strides4& st, long b, long s, long h) { return b * st.b + s * st.s + h * st.h; }
+
 // Tile row that element e of step t of lane half h's A fragment reads, for a product that
 // contracts over the 32 rows of a tile with the other operand from bfrag_from_acc (the
 // accumulator's row order): bf16 step t of 2 reads rows 16t + 8(e>>2) + 4h + (e&3), fp32
@@ -98,7 +105,8 @@ __global__ __launch_bounds__(256) void attn_bwd_relayout_kernel(const TC* __rest
                                                                 TC* __restrict__ KR, TC* __restrict__ QR,
                                                                 TC* __restrict__ OR, TC* __restrict__ VR,
                                                                 TC* __restrict__ KT, TC* __restrict__ QT,
-                                                                TC* __restrict__ OT, int N, int Np) {
+                                                                TC* __restrict__ OT, int S, int H, int N, int Np,
+                                                                Strides4 sx, Strides4 sdo) {
   using M = Mfma<TC>;
   constexpr int VEC = M::KPL;  // elements per 16-byte piece
   constexpr int STEPS = kBD / M::K32;
@@ -111,12 +119,14 @@ __global__ __launch_bounds__(256) void attn_bwd_relayout_kernel(const TC* __rest
   TC* XT = z == 0 ? KT : (z == 1 ? QT : OT);
   const size_t line = blockIdx.y;
   const int n0 = blockIdx.x * R;
-  const TC* Xl = X + line * N * kBD;
+  const Strides4& st = z == 2 ? sdo : sx;
+  const long lb = (long)(line / ((size_t)S * H)), ls = (long)((line / H) % S), lh = (long)(line % H);
+  const TC* Xl = X + line_offset(st, lb, ls, lh);
   for (int i = threadIdx.x; i < R * (kBD / VEC); i += 256) {
     const int r = i / (kBD / VEC);
     const int d0 = (i % (kBD / VEC)) * VEC;
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (n0 + r < N) v = *reinterpret_cast<const u32x4*>(Xl + (size_t)(n0 + r) * kBD + d0);
+    if (n0 + r < N) v = *reinterpret_cast<const u32x4*>(Xl + (long)(n0 + r) * st.n + d0);
     *reinterpret_cast<u32x4*>(t + r * LD + d0) = v;
   }
   __syncthreads();
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
                                                              const float* __restrict__ mask2,
                                                              const float* __restrict__ bias2, int S, int H, int N,
                                                              int Np, float scale, TC* __restrict__ dQ,
-                                                             f32x4* __restrict__ st4) {
+                                                             f32x4* __restrict__ st4, Strides4 sx, Strides4 sg) {
   using M = Mfma<TC>;
   constexpr int STEPS = kBD / M::K32;
   constexpr int kRows = 32 * kSub;
@@ -228,9 +238,10 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
   const int c = l & 31;
   const int s = blockIdx.y * kLines + w;
   const bool active = s < S;  // inactive waves mirror the group's first line and skip the math
-  const long bs = (long)b * S + (active ? s : (int)blockIdx.y * kLines);
+  const long sl = active ? s : (int)blockIdx.y * kLines;  // this wave's line (or the mirrored one)
+  const long bs = (long)b * S + sl;
   const size_t line = (size_t)bs * H + hd;
-  const TC* Vl = V + line * N * kBD;
+  const TC* Vl = V + line_offset(sx, b, sl, hd);
   // line whose key mask thread t < 128 stages (the four lines of the group, clamped)
   const float* m2s = mask2 + ((long)b * S + min((int)blockIdx.y * kLines + (int)(threadIdx.x >> 5), S - 1)) * Np;
   const float* b2l = bias2 + (size_t)bh * Np * Np;
@@ -363,7 +374,7 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
     float part = 0.f;
 #pragma unroll
     for (int t = 0; t < STEPS; ++t)
-      part += frag_dot(of[sub][t], M::load(Vl + (size_t)iv * kBD + t * M::K32 + hh * M::KPL));
+      part += frag_dot(of[sub][t], M::load(Vl + (long)iv * sx.n + t * M::K32 + hh * M::KPL));
     part += __shfl_xor(part, 32, 64);
     ref[sub] = dead[sub] ? 0.f : part;
   }
@@ -436,7 +447,7 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
     if (active && hh == 0) st4[line * Np + q] = stats_pack(lse2, ref[sub], cen, imax[sub]);
     if (!active || q >= N) continue;
     const float f = dead[sub] ? 0.f : scale / Wt;
-    TC* dst = dQ + (line * N + q) * kBD;
+    TC* dst = dQ + line_offset(sg, b, sl, hd) + (long)q * sg.n;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v[4];
@@ -460,7 +471,7 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dkdv_ke
     const TC* __restrict__ QR, const TC* __restrict__ KR, const TC* __restrict__ VR, const TC* __restrict__ OR,
     const TC* __restrict__ QT, const TC* __restrict__ OT, const float* __restrict__ mask2,
     const float* __restrict__ bias2, int S, int H, int N, int Np, float scale, const f32x4* __restrict__ st4,
-    TC* __restrict__ dK, TC* __restrict__ dV) {
+    TC* __restrict__ dK, TC* __restrict__ dV, Strides4 sg) {
   using M = Mfma<TC>;
   constexpr int STEPS = kBD / M::K32;
   constexpr int EPS = 16 / STEPS;  // accumulator elements per B fragment step
@@ -478,9 +489,10 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dkdv_ke
   const int c = l & 31;
   const int s = blockIdx.y * kLines + w;
   const bool active = s < S;
-  const long bs = (long)b * S + (active ? s : (int)blockIdx.y * kLines);
+  const long sl = active ? s : (int)blockIdx.y * kLines;
+  const long bs = (long)b * S + sl;
   const size_t line = (size_t)bs * H + hd;
-  const size_t lo = line * N * kBD;
+  const long lo = line_offset(sg, b, sl, hd);  // this line's dK / dV rows
   const float* b2l = bias2 + (size_t)bh * Np * Np;
   const int kb0 = blockIdx.x * kRows;
   const float sl2 = scale * kLog2e;
@@ -604,8 +616,8 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dkdv_ke
         vk[e] = dk[sub][4 * j + e] * scale;
         vv[e] = dv[sub][4 * j + e];
       }
-      store_vec<TC, 4>(dK + lo + (size_t)key[sub] * kBD + 8 * j + 4 * hh, vk);
-      store_vec<TC, 4>(dV + lo + (size_t)key[sub] * kBD + 8 * j + 4 * hh, vv);
+      store_vec<TC, 4>(dK + lo + (long)key[sub] * sg.n + 8 * j + 4 * hh, vk);
+      store_vec<TC, 4>(dV + lo + (long)key[sub] * sg.n + 8 * j + 4 * hh, vv);
     }
   }
 }
@@ -751,7 +763,8 @@ BwdWs bwd_ws_layout(int B, int S, int H, int N, int es) {
 template <class TC>
 int attn_bwd_launch(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias,
                     const void* dout, int B, int S, int H, int N, float scale, void* dq, void* dk, void* dv,
-                    float* dbias, void* ws, hipStream_t s) {
+                    float* dbias, void* ws, hipStream_t s, const Strides4& sx, const Strides4& sdo,
+                    const Strides4& sg) {
   const BwdWs lay = bwd_ws_layout(B, S, H, N, (int)sizeof(TC));
   char* base = static_cast<char*>(ws);
   f32x4* st4 = reinterpret_cast<f32x4*>(base + lay.st);
@@ -775,14 +788,14 @@ int attn_bwd_launch(const void* q, const void* k, const void* v, const float* re
     if (int e = pf::check_launch("attn_bwd_prep")) return e;
   }
   attn_bwd_relayout_kernel<TC><<<dim3((unsigned)(Np / 64), lines, 4), 256, 0, s>>>(K, Q, dO, V, KR, QR, OR, VR, KT,
-                                                                                   QT, OT, N, Np);
+                                                                                   QT, OT, S, H, N, Np, sx, sdo);
   if (int e = pf::check_launch("attn_bwd_relayout")) return e;
   const unsigned lg = (unsigned)((S + kLines - 1) / kLines);
   attn_bwd_dq_kernel<TC, kSubDq><<<dim3((unsigned)(Np / (32 * kSubDq)), lg, (unsigned)(B * H)), kNT, 0, s>>>(
-      QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N, Np, scale, static_cast<TC*>(dq), st4);
+      QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N, Np, scale, static_cast<TC*>(dq), st4, sx, sg);
   if (int e = pf::check_launch("attn_bwd_dq")) return e;
   attn_bwd_dkdv_kernel<TC, kSubKv><<<dim3((unsigned)(Np / (32 * kSubKv)), lg, (unsigned)(B * H)), kNT, 0, s>>>(
-      QR, KR, VR, OR, QT, OT, mask2, bias2, S, H, N, Np, scale, st4, static_cast<TC*>(dk), static_cast<TC*>(dv));
+      QR, KR, VR, OR, QT, OT, mask2, bias2, S, H, N, Np, scale, st4, static_cast<TC*>(dk), static_cast<TC*>(dv), sg);
   if (int e = pf::check_launch("attn_bwd_dkdv")) return e;
   const unsigned nb = (unsigned)((N + 63) / 64);
   const int G = lay.groups;
@@ -798,6 +811,36 @@ int attn_bwd_launch(const void* q, const void* k, const void* v, const float* re
   return PF_OK;
 }
 
+// Shared checks and dispatch of the dense and strided entry points.
+int evo_attn_bwd_any(const char* fn, const void* q, const void* k, const void* v, const float* res_mask,
+                     const float* pair_bias, const void* dout, int B, int S, int H, int N, int D, int dtype,
+                     float softmax_scale, void* dq, void* dk, void* dv, float* dpair_bias, void* workspace,
+                     size_t workspace_bytes, void* stream, const Strides4& sx, const Strides4& sdo,
+                     const Strides4& sg) {
+  PF_REQUIRE(q && k && v && res_mask && pair_bias && dout && dq && dk && dv && dpair_bias && workspace,
+             PF_ERR_INVALID_ARG, "%s: null pointer", fn);
+  PF_REQUIRE(B > 0 && S > 0 && H > 0 && N > 0, PF_ERR_INVALID_ARG, "%s: B=%d S=%d H=%d N=%d", fn, B, S, H, N);
+  PF_REQUIRE((long)B * S * H <= 65535 && (long)B * H <= 65535 && (long)N * N < (1L << 31), PF_ERR_INVALID_ARG,
+             "%s: B*S*H=%ld N=%d too large (grid rows are the B*S*H lines)", fn, (long)B * S * H, N);
+  PF_REQUIRE(D == kBD, PF_ERR_UNSUPPORTED, "%s: D=%d (built: D=32)", fn, D);
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "%s: dtype %d", fn, dtype);
+  const long vec = dtype == PF_F32 ? 4 : 8;  // elements per 16 bytes
+  for (const Strides4* st : {&sx, &sdo, &sg})
+    PF_REQUIRE(st->b % vec == 0 && st->s % vec == 0 && st->h % vec == 0 && st->n % vec == 0 && st->n >= kBD,
+               PF_ERR_ALIGNMENT, "%s: strides must keep 16-byte aligned rows of D elements", fn);
+  PF_REQUIRE(pf::aligned16(q) && pf::aligned16(k) && pf::aligned16(v) && pf::aligned16(dout) && pf::aligned16(dq) &&
+                 pf::aligned16(dk) && pf::aligned16(dv) && pf::aligned16(workspace),
+             PF_ERR_ALIGNMENT, "%s: operand pointers must be 16-byte aligned", fn);
+  const size_t need = bwd_ws_layout(B, S, H, N, dtype == PF_F32 ? 4 : 2).total;
+  PF_REQUIRE(workspace_bytes >= need, PF_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes, need);
+  hipStream_t s = pf::as_stream(stream);
+  if (dtype == PF_F32)
+    return attn_bwd_launch<float>(q, k, v, res_mask, pair_bias, dout, B, S, H, N, softmax_scale, dq, dk, dv,
+                                  dpair_bias, workspace, s, sx, sdo, sg);
+  return attn_bwd_launch<bf16>(q, k, v, res_mask, pair_bias, dout, B, S, H, N, softmax_scale, dq, dk, dv, dpair_bias,
+                               workspace, s, sx, sdo, sg);
+}
+
 }  // namespace
 
 extern "C" {
@@ -810,26 +853,22 @@ size_t pf_evo_attn_bwd_workspace_bytes(int B, int S, int H, int N, int D, int dt
 int pf_evo_attn_bwd(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias,
                     const void* dout, int B, int S, int H, int N, int D, int dtype, float softmax_scale, void* dq,
                     void* dk, void* dv, float* dpair_bias, void* workspace, size_t workspace_bytes, void* stream) {
-  PF_REQUIRE(q && k && v && res_mask && pair_bias && dout && dq && dk && dv && dpair_bias && workspace,
-             PF_ERR_INVALID_ARG, "pf_evo_attn_bwd: null pointer");
-  PF_REQUIRE(B > 0 && S > 0 && H > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_evo_attn_bwd: B=%d S=%d H=%d N=%d", B, S, H,
-             N);
-  PF_REQUIRE((long)B * S * H <= 65535 && (long)B * H <= 65535 && (long)N * N < (1L << 31), PF_ERR_INVALID_ARG,
-             "pf_evo_attn_bwd: B*S*H=%ld N=%d too large (grid rows are the B*S*H lines)", (long)B * S * H, N);
-  PF_REQUIRE(D == kBD, PF_ERR_UNSUPPORTED, "pf_evo_attn_bwd: D=%d (built: D=32)", D);
-  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_evo_attn_bwd: dtype %d", dtype);
-  PF_REQUIRE(pf::aligned16(q) && pf::aligned16(k) && pf::aligned16(v) && pf::aligned16(dout) && pf::aligned16(dq) &&
-                 pf::aligned16(dk) && pf::aligned16(dv) && pf::aligned16(workspace),
-             PF_ERR_ALIGNMENT, "pf_evo_attn_bwd: operand pointers must be 16-byte aligned");
-  const size_t need = bwd_ws_layout(B, S, H, N, dtype == PF_F32 ? 4 : 2).total;
-  PF_REQUIRE(workspace_bytes >= need, PF_ERR_WORKSPACE, "pf_evo_attn_bwd: workspace %zu < %zu bytes",
-             workspace_bytes, need);
-  hipStream_t s = pf::as_stream(stream);
-  if (dtype == PF_F32)
-    return attn_bwd_launch<float>(q, k, v, res_mask, pair_bias, dout, B, S, H, N, softmax_scale, dq, dk, dv,
-                                  dpair_bias, workspace, s);
-  return attn_bwd_launch<bf16>(q, k, v, res_mask, pair_bias, dout, B, S, H, N, softmax_scale, dq, dk, dv, dpair_bias,
-                               workspace, s);
+  const Strides4 dense{(long)S * H * N * D, (long)H * N * D, (long)N * D, D};
+  return evo_attn_bwd_any("pf_evo_attn_bwd", q, k, v, res_mask, pair_bias, dout, B, S, H, N, D, dtype, softmax_scale,
+                          dq, dk, dv, dpair_bias, workspace, workspace_bytes, stream, dense, dense, dense);
+}
+
+int pf_evo_attn_bwd_strided(const void* q, const void* k, const void* v, const long* qkv_strides,
+                            const float* res_mask, const float* pair_bias, const void* dout, const long* dout_strides,
+                            int B, int S, int H, int N, int D, int dtype, float softmax_scale, void* dq, void* dk,
+                            void* dv, const long* grad_strides, float* dpair_bias, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(qkv_strides && dout_strides && grad_strides, PF_ERR_INVALID_ARG, "pf_evo_attn_bwd_strided: null strides");
+  const Strides4 sx{qkv_strides[0], qkv_strides[1], qkv_strides[2], qkv_strides[3]};
+  const Strides4 sdo{dout_strides[0], dout_strides[1], dout_strides[2], dout_strides[3]};
+  const Strides4 sg{grad_strides[0], grad_strides[1], grad_strides[2], grad_strides[3]};
+  return evo_attn_bwd_any("pf_evo_attn_bwd_strided", q, k, v, res_mask, pair_bias, dout, B, S, H, N, D, dtype,
+                          softmax_scale, dq, dk, dv, dpair_bias, workspace, workspace_bytes, stream, sx, sdo, sg);
 }
 
 }  // extern "C"

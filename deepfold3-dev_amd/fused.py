@@ -19,6 +19,8 @@ kernels cannot serve raises ``NotActive``. There is no PyTorch fallback for the 
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 import torch.nn as nn
 
@@ -119,6 +121,82 @@ class _EvoAttnFunction(torch.autograd.Function):
         kernel_census.record("evo_attention.backward", "hip_evo_attn_bwd")
         dQ, dK, dV, dpb = _evo_bwd(Q, K, V, rm, pb, dO)
         return dQ, dK, dV, None, dpb
+
+
+def _strides(*st: int) -> tuple:
+    """A long[4] of element strides {batch, line, head, key} and the address to pass."""
+    arr = (ctypes.c_long * 4)(*st)
+    return arr, ctypes.addressof(arr)
+
+
+class _GridAttnCore(torch.autograd.Function):
+    """The flash attention of ``GridSelfAttention``'s training path on the token-major
+    projection (``attention.py:211-257``, the fused branch): ``apply(qkv, res_mask,
+    pair_bias, transpose)`` with qkv ``[B, N, N, 3, H, D]`` (q | k | v of every pair position
+    (i, j)), res_mask ``[B, lines, N]`` additive fp32, pair_bias ``[B, H, N, N]`` fp32; lines are
+    the rows i (transpose False) or the columns j (True). Returns O ``[B, N, N, H, D]`` in the
+    same token order. The kernels read q, k, v and dO and write O and dq, dk, dv (into the
+    gradient of qkv) through strides (``pf_evo_attn_fwd_strided`` / ``pf_evo_attn_bwd_strided``),
+    so nothing is permuted or copied around them. The kernel's masked-line rule (a line whose
+    keys are all masked outputs 0). H = 4, D = 32."""
+
+    @staticmethod
+    def _layout(qkv, transpose):
+        B, N1, N2, _, H, D = qkv.shape
+        tok = 3 * H * D
+        if transpose:  # lines j, keys i
+            sx = (N1 * N2 * tok, tok, D, N2 * tok)
+            so = (N1 * N2 * H * D, H * D, D, N2 * H * D)
+        else:
+            sx = (N1 * N2 * tok, N2 * tok, D, tok)
+            so = (N1 * N2 * H * D, N2 * H * D, D, H * D)
+        S = N2 if transpose else N1
+        return B, S, H, N1, D, sx, so
+
+    @staticmethod
+    def forward(ctx, qkv, rm, pb, transpose):
+        qkv = qkv.contiguous()
+        B, S, H, N, D, sx, so = _GridAttnCore._layout(qkv, transpose)
+        code = _lib.dtype_code(qkv.dtype)
+        ws_bytes = _lib.lib().pf_evo_attn_workspace_bytes(B, S, H, N, D, code)
+        if ws_bytes == 0:
+            raise NotActive("GridSelfAttention", f"H={H}, D={D}: the strided attention is built for H=4, D=32")
+        out = torch.empty(qkv.shape[:3] + (H, D), dtype=qkv.dtype, device=qkv.device)
+        ws = _ws(ws_bytes, qkv.device)
+        es = qkv.element_size()
+        base = qkv.data_ptr()
+        ax, px = _strides(*sx)
+        ao, po = _strides(*so)
+        _lib.call(
+            "pf_evo_attn_fwd_strided", base, base + H * D * es, base + 2 * H * D * es, px, rm.data_ptr(),
+            pb.data_ptr(), B, S, H, N, D, code, 1, out.data_ptr(), po, ws.data_ptr(), ws_bytes, _lib.stream_of(qkv),
+        )  # fmt: skip
+        _lib.note_redo("pf_evo_attn_redo_flags", ws, B, S, H, N, D, code)
+        ctx.save_for_backward(qkv, rm, pb)
+        ctx.transpose = bool(transpose)
+        return out
+
+    @staticmethod
+    def backward(ctx, dO):
+        qkv, rm, pb = ctx.saved_tensors
+        B, S, H, N, D, sx, so = _GridAttnCore._layout(qkv, ctx.transpose)
+        code = _lib.dtype_code(qkv.dtype)
+        dO = dO.to(qkv.dtype).contiguous()
+        ws_bytes = _lib.lib().pf_evo_attn_bwd_workspace_bytes(B, S, H, N, D, code)
+        dqkv = torch.empty_like(qkv)
+        dpb = torch.empty((B, H, N, N), dtype=torch.float32, device=qkv.device)
+        ws = _ws(ws_bytes, qkv.device)
+        es = qkv.element_size()
+        base, gbase = qkv.data_ptr(), dqkv.data_ptr()
+        ax, px = _strides(*sx)
+        ao, po = _strides(*so)
+        kernel_census.record("GridSelfAttention.backward", "hip_evo_attn_bwd_strided")
+        _lib.call(
+            "pf_evo_attn_bwd_strided", base, base + H * D * es, base + 2 * H * D * es, px, rm.data_ptr(),
+            pb.data_ptr(), dO.data_ptr(), po, B, S, H, N, D, code, float(D) ** -0.5, gbase, gbase + H * D * es,
+            gbase + 2 * H * D * es, px, dpb.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(qkv),
+        )  # fmt: skip
+        return dqkv, None, dpb, None
 
 
 class _EvoformerAttention:

@@ -93,7 +93,7 @@ def residual_add(res: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = 
 
 def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
     """LayerNorm over the last dim with fp32 statistics, in x's dtype (``primitives.py:90-115``)."""
-    _lib.require_device("layer_norm", x)
+    _lib.require_device("layer_norm", x, weight, bias)
     C = x.shape[-1]
     xc = x.contiguous()
     out = torch.empty_like(xc)
@@ -119,7 +119,7 @@ class LayerNormFunction(torch.autograd.Function):
         if odt == xc.dtype:
             out = layer_norm(xc, weight, bias, eps)
         else:
-            _lib.require_device("layer_norm", xc)
+            _lib.require_device("layer_norm", xc, weight, bias)
             C = xc.shape[-1]
             out = torch.empty(xc.shape, dtype=odt, device=xc.device)
             _lib.call(

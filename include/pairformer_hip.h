@@ -308,6 +308,24 @@ size_t pf_evo_attn_bwd_workspace_bytes(int B, int S, int H, int N, int D, int dt
 int pf_evo_attn_bwd(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias,
                     const void* dout, int B, int S, int H, int N, int D, int dtype, float softmax_scale, void* dq,
                     void* dk, void* dv, float* dpair_bias, void* workspace, size_t workspace_bytes, void* stream);
+/* Strided forms of pf_evo_attn_fwd / pf_evo_attn_bwd (no counterpart in the reference, whose
+ * module path makes the [B, S, H, N, D] operands contiguous before the kernel): q, k, v, out,
+ * dout, dq, dk, dv are views given by element strides {batch, line, head, key} (long[4]; D
+ * contiguous; every stride a multiple of 16 bytes, the key stride >= D). q, k, v share
+ * qkv_strides and dq, dk, dv share grad_strides. GridSelfAttention's training path passes
+ * views of its token-major [B, N, N, 3, H, D] projection (rows: line stride N 3HD, key stride
+ * 3HD; columns the two swapped) and takes O and the gradients in the same token order, so no
+ * operand is permuted or copied around the kernels. Same arithmetic as the dense entry points;
+ * res_mask [B, S, N] and pair_bias [B, H, N, N] stay dense. */
+int pf_evo_attn_fwd_strided(const void* q, const void* k, const void* v, const long* qkv_strides,
+                            const float* res_mask, const float* pair_bias, int B, int S, int H, int N, int D,
+                            int dtype, int masked_rows_zero, void* out, const long* out_strides, void* workspace,
+                            size_t workspace_bytes, void* stream);
+int pf_evo_attn_bwd_strided(const void* q, const void* k, const void* v, const long* qkv_strides,
+                            const float* res_mask, const float* pair_bias, const void* dout, const long* dout_strides,
+                            int B, int S, int H, int N, int D, int dtype, float softmax_scale, void* dq, void* dk,
+                            void* dv, const long* grad_strides, float* dpair_bias, void* workspace,
+                            size_t workspace_bytes, void* stream);
 /* FusedPairBias(c, H)(z, ln_w, ln_b, proj_w, mask) (triton/fused_pair_bias.py:348-416):
  * z [B,N,N,C] -> out [B,H,N,N] in z's dtype; proj_w16 [16, C] fp32 (proj_w padded with zero
  * rows); mask [B,N] fp32 or NULL adds (1 - mask) * (-1e9) on the last axis. C = 128, H <= 16. */

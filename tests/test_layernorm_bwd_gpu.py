@@ -2,8 +2,10 @@
 pf_layernorm_bwd), against torch's LayerNorm differentiated in fp64 (a library routine), at
 the widths the training paths use; fp32 at relL2 <= 1e-5 and max-abs <= 1e-5 max|ref|; bf16
 within 2x the error of torch's own bf16 LayerNorm gradient (computed on the CPU). The affine
-gradients are summed in a fixed order: bitwise-reproducible. The kernel-level fused ops under
-grad (built on it and on the HIP SwiGLU backward) against torch's formulas in fp64."""
+gradients are summed in a fixed order: bitwise-reproducible. The mixed-dtype entry points
+(fp32 input, bf16 output and cotangent: the autocast training path) against the fp32 kernels
+with the cast done by torch, bit for bit. The kernel-level fused ops under grad (built on it
+and on the HIP SwiGLU backward) against torch's formulas in fp64."""
 
 from __future__ import annotations
 
@@ -64,6 +66,33 @@ def test_layernorm_backward_bf16(dev):
 def _grads(fn, leaves, cot):
     out = fn(*leaves)
     return out, torch.autograd.grad(out, leaves, grad_outputs=cot)
+
+
+@pytest.mark.parametrize("C", [128, 384, 96])
+def test_layernorm_mixed_dtypes_are_the_casts(dev, C):
+    """bf16 output from fp32 x = the fp32 LayerNorm rounded by torch; the backward with a bf16
+    cotangent = the fp32 backward with that cotangent upcast (the same arithmetic, bit for
+    bit). C=96 runs the generic row kernel forward (the backward is built for 64..512)."""
+    M = 777
+    x, w, b, dy = _case(M, C, 11 + C)
+    x32 = x.to(dev).requires_grad_(True)
+    w1, b1 = w.to(dev).requires_grad_(True), b.to(dev).requires_grad_(True)
+    out16 = kernels.LayerNormFunction.apply(x32, w1, b1, 1e-5, torch.bfloat16)
+    assert out16.dtype == torch.bfloat16
+    with torch.no_grad():
+        ref32 = kernels.LayerNormFunction.apply(x32.detach(), w1.detach(), b1.detach(), 1e-5)
+    assert torch.equal(out16, ref32.to(torch.bfloat16))
+    if C == 96:
+        return
+    dy16 = dy.to(dev, torch.bfloat16)
+    got = torch.autograd.grad(out16, [x32, w1, b1], grad_outputs=dy16)
+    x2 = x.to(dev).requires_grad_(True)
+    w2, b2 = w.to(dev).requires_grad_(True), b.to(dev).requires_grad_(True)
+    out32 = kernels.LayerNormFunction.apply(x2, w2, b2, 1e-5)
+    want = torch.autograd.grad(out32, [x2, w2, b2], grad_outputs=dy16.float())
+    print(f"[layernorm mixed] C={C}", flush=True)
+    for g_, r_ in zip(got, want):
+        assert g_.dtype == r_.dtype and torch.equal(g_, r_)
 
 
 def test_fused_ops_are_differentiable_fp32(dev):
