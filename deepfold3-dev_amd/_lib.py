@@ -84,8 +84,8 @@ SIGNATURES: dict[str, tuple] = {
     "pf_evo_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "pf_evo_attn_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "pf_evo_attn_bwd": (_i, [_vp] * 6 + [_i] * 6 + [_f] + [_vp] * 5 + [_sz, _vp]),
-    "pf_evo_attn_fwd_strided": (_i, [_vp] * 6 + [_i] * 7 + [_vp] * 3 + [_sz, _vp]),
-    "pf_evo_attn_bwd_strided": (_i, [_vp] * 8 + [_i] * 6 + [_f] + [_vp] * 6 + [_sz, _vp]),
+    "pf_evo_attn_fwd_strided": (_i, [_vp] * 6 + [_i] * 7 + [_vp] * 4 + [_sz, _vp]),
+    "pf_evo_attn_bwd_strided": (_i, [_vp] * 9 + [_i] * 6 + [_f] + [_vp] * 6 + [_sz, _vp]),
     "pf_pair_mask_outer": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "pf_grid_attn_redo_flags": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "pf_evo_attn_redo_flags": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),

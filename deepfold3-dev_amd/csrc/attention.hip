@@ -601,7 +601,8 @@ template <class TC, int QS, bool O_HEAD_MAJOR, bool FAST, bool POST_SCALE = fals
 __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2)) void tri_attn_kernel(
     const TC* __restrict__ Q, const TC* __restrict__ K, const TC* __restrict__ Vt, const float* __restrict__ PB,
     const float* __restrict__ MA, TC* __restrict__ O, int B, int N, int Np, int L, int Lp, int zero_masked_lines,
-    int xcd_remap, int* __restrict__ redo, float post_scale = 1.f, Strides4 ost = {}) {
+    int xcd_remap, int* __restrict__ redo, float post_scale = 1.f, Strides4 ost = {},
+    float* __restrict__ lse_out = nullptr) {
   constexpr int QB = 32 * QS;
   constexpr int NT = 64 * kLinesPerBlock;
   constexpr int QLD = kHeadDim + (sizeof(TC) == 2 ? 0 : lds_pad<TC>());
@@ -995,6 +996,13 @@ __global__ __launch_bounds__(64 * kLinesPerBlock, QS == 1 ? 4 : (QS == 2 ? 4 : 2
     const float inv = write_zero ? 0.f : 1.0f / lt;
     const int q = q0 + 32 * s + lq;
     if (q >= N) continue;
+    if (lse_out != nullptr && hf == 0) {
+      // log2-unit LSE of the row (the softmax reference plus log2 of the row sum); +inf for a
+      // line whose keys are all masked or a row whose logits are all below -1e8 log2 e.
+      float lse2 = mref[s] + __builtin_amdgcn_logf(lt);
+      if (all_masked || !(lse2 >= -1.0e8f * kLog2e)) lse2 = INFINITY;
+      lse_out[(((size_t)b * L + line) * kHeads + h) * Np + q] = lse2;
+    }
     TC* dst;
     if constexpr (O_HEAD_MAJOR)
       dst = ost.n ? O + b * ost.b + line * ost.s + h * ost.h + q * ost.n
@@ -1638,7 +1646,7 @@ template <class TC>
 int evo_attn_launch(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias, int B,
                     int S, int N, int zero_rule, void* out, void* ws, hipStream_t s,
                     float softmax_scale = 1.0f / sqrtf((float)kHeadDim), const Strides4* sx_in = nullptr,
-                    const Strides4* so_in = nullptr) {
+                    const Strides4* so_in = nullptr, float* lse_out = nullptr) {
   const Strides4 sx = sx_in ? *sx_in
                             : Strides4{(long)S * kHeads * N * kHeadDim, (long)kHeads * N * kHeadDim,
                                        (long)N * kHeadDim, kHeadDim};
@@ -1675,10 +1683,10 @@ int evo_attn_launch(const void* q, const void* k, const void* v, const float* re
   const int remap = (total % 8 == 0) ? 1 : 0;
   pf::KernelTimer timer("evo_attn", s);
   tri_attn_kernel<TC, QS, true, true, kPost><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
-      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post, so);
+      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post, so, lse_out);
   if (int e = pf::check_launch("evo_attn")) return e;
   tri_attn_kernel<TC, QS, true, false, kPost><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<TC>(), s>>>(
-      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post, so);
+      Qw, Kw, Vw, PBw, MAw, (TC*)out, B, N, Np, S, S, zero_rule, remap, redo, post, so, lse_out);
   timer.stop();
   return pf::check_launch("evo_attn redo");
 }
@@ -1937,8 +1945,8 @@ int pf_evo_attn_fwd(const void* q, const void* k, const void* v, const float* re
 
 int pf_evo_attn_fwd_strided(const void* q, const void* k, const void* v, const long* qkv_strides,
                             const float* res_mask, const float* pair_bias, int B, int S, int H, int N, int D,
-                            int dtype, int masked_rows_zero, void* out, const long* out_strides, void* workspace,
-                            size_t workspace_bytes, void* stream) {
+                            int dtype, int masked_rows_zero, void* out, const long* out_strides, float* lse_out,
+                            void* workspace, size_t workspace_bytes, void* stream) {
   PF_REQUIRE(q && k && v && qkv_strides && res_mask && pair_bias && out && out_strides && workspace,
              PF_ERR_INVALID_ARG, "pf_evo_attn_fwd_strided: null pointer");
   PF_REQUIRE(B > 0 && S > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_evo_attn_fwd_strided: B=%d S=%d N=%d", B, S, N);
@@ -1961,9 +1969,9 @@ int pf_evo_attn_fwd_strided(const void* q, const void* k, const void* v, const l
   const float sc = 1.0f / sqrtf((float)kHeadDim);
   if (dtype == PF_F32)
     return evo_attn_launch<float>(q, k, v, res_mask, pair_bias, B, S, N, masked_rows_zero, out, workspace, s, sc, &sx,
-                                  &so);
+                                  &so, lse_out);
   return evo_attn_launch<bf16>(q, k, v, res_mask, pair_bias, B, S, N, masked_rows_zero, out, workspace, s, sc, &sx,
-                               &so);
+                               &so, lse_out);
 }
 
 }  // extern "C"

@@ -19,7 +19,12 @@
 //   attn_bwd_dq:   query-major. Pass 1 over the keys finds each row's maximum logit and first
 //                  argmax; pass 2 forms P, dP and the centred sums and the two products whose
 //                  difference is dQ, and leaves (LSE, dP_imax, imax, C) per row in the
-//                  workspace for the other kernels.
+//                  workspace for the other kernels. Given the forward's row LSE, pass 1 is
+//                  skipped: p = 2^(x - LSE) <= ~1 needs no maximum, and the centring key is
+//                  the row's dominant one (p > 1/2, the first in key order; none if no key
+//                  dominates, then the sums stay centred on 0), found in pass 2 itself; the
+//                  sums taken before it are moved onto it once (A += (ref - dP_k) B,
+//                  C W += (ref - dP_k) W).
 //   attn_bwd_dkdv: key-major, loops over query tiles: dV^T += dO^T P, dK^T += Q^T dS.
 //   attn_bwd_db:   one (query tile, key tile) of one (b, h), loops over a group of lines and
 //                  sums dS in registers; the groups' partial sums are added in a fixed order,
@@ -214,14 +219,15 @@ PF_DEVICE float frag_dot(const f32x4& a, const f32x4& b) {
   return s;
 }
 
-template <class TC, int kSub>
+template <class TC, int kSub, bool kLse>
 __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kernel(const TC* __restrict__ QR, const TC* __restrict__ KR,
                                                              const TC* __restrict__ VR, const TC* __restrict__ OR,
                                                              const TC* __restrict__ V, const TC* __restrict__ KT,
                                                              const float* __restrict__ mask2,
                                                              const float* __restrict__ bias2, int S, int H, int N,
                                                              int Np, float scale, TC* __restrict__ dQ,
-                                                             f32x4* __restrict__ st4, Strides4 sx, Strides4 sg) {
+                                                             f32x4* __restrict__ st4, Strides4 sx, Strides4 sg,
+                                                             const float* __restrict__ lse_in) {
   using M = Mfma<TC>;
   constexpr int STEPS = kBD / M::K32;
   constexpr int kRows = 32 * kSub;
@@ -302,81 +308,96 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
     }
   };
 
-  // Pass 1: maximum and first argmax over this lane's half of the keys (its accumulator
-  // rows ascend in key order, tiles ascend, so a strict > keeps the first).
-  float run_max[kSub];
-  int imx[kSub];
-#pragma unroll
-  for (int sub = 0; sub < kSub; ++sub) {
-    run_max[sub] = -INFINITY;
-    imx[sub] = 0;
-  }
-  {
-    DqOps<TC> cur, nxt;
-    fetch(0, cur, false);
-    bias_load(0);
-    bias_store(0);
-    __syncthreads();
-    for (int kt = 0; kt < nkt; ++kt) {
-      const int k0 = kt * 32;
-      const bool more = kt + 1 < nkt;
-      if (more) {
-        bias_load(k0 + 32);
-        fetch(k0 + 32, nxt, false);
-      }
-      if (active) {
-        f32x16 sa[kSub];
-#pragma unroll
-        for (int sub = 0; sub < kSub; ++sub) {
-          sa[sub] = f32x16{};
-#pragma unroll
-          for (int t = 0; t < STEPS; ++t) M::mma32(sa[sub], cur.k[t], qf[sub][t]);
-        }
-#pragma unroll
-        for (int sub = 0; sub < kSub; ++sub) {
-          f32x16 x;
-          logits(sa[sub], kt & 1, sub, x);
-          // tile maximum, then its first row (rows ascend in key order: scan downwards)
-          float tmax = x[0];
-#pragma unroll
-          for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, x[r]);
-          int trow = 0;
-#pragma unroll
-          for (int r = 15; r >= 0; --r) trow = x[r] == tmax ? acc_row(r, hh) : trow;
-          if (tmax > run_max[sub]) {
-            run_max[sub] = tmax;
-            imx[sub] = k0 + trow;
-          }
-        }
-      }
-      if (more) bias_store((kt + 1) & 1);
-      __syncthreads();
-      cur = nxt;
-    }
-  }
-  // Merge the two halves (larger maximum; the smaller index on a tie), then dP at the argmax.
   float mrow[kSub], ref[kSub];
   int imax[kSub];
-  bool dead[kSub];
+  bool dead[kSub], found[kSub];
+  if constexpr (kLse) {
+    // The forward's LSE (log2 units, +inf for a dead row) as the exponent offset: p <= ~1.
 #pragma unroll
-  for (int sub = 0; sub < kSub; ++sub) {
-    const float om = __shfl_xor(run_max[sub], 32, 64);
-    const int oi = __shfl_xor(imx[sub], 32, 64);
-    if (om > run_max[sub] || (om == run_max[sub] && oi < imx[sub])) {
-      run_max[sub] = om;
-      imx[sub] = oi;
+    for (int sub = 0; sub < kSub; ++sub) {
+      const int q = q0 + 32 * sub + c;
+      const float lf = q < N ? lse_in[line * Np + q] : INFINITY;
+      dead[sub] = !(lf >= kDeadLog2 && lf < INFINITY);
+      mrow[sub] = dead[sub] ? INFINITY : lf;
+      ref[sub] = 0.f;
+      imax[sub] = -1;
+      found[sub] = false;
     }
-    const bool live = run_max[sub] >= kDeadLog2;
-    dead[sub] = !live || q0 + 32 * sub + c >= N;
-    mrow[sub] = live ? run_max[sub] : 0.f;
-    imax[sub] = dead[sub] ? -1 : imx[sub];
-    const int iv = live ? imx[sub] : 0;  // < N: keys past N have logit -inf
-    float part = 0.f;
+  } else {
+    // Pass 1: maximum and first argmax over this lane's half of the keys (its accumulator
+    // rows ascend in key order, tiles ascend, so a strict > keeps the first).
+    float run_max[kSub];
+    int imx[kSub];
+  #pragma unroll
+    for (int sub = 0; sub < kSub; ++sub) {
+      run_max[sub] = -INFINITY;
+      imx[sub] = 0;
+    }
+    {
+      DqOps<TC> cur, nxt;
+      fetch(0, cur, false);
+      bias_load(0);
+      bias_store(0);
+      __syncthreads();
+      for (int kt = 0; kt < nkt; ++kt) {
+        const int k0 = kt * 32;
+        const bool more = kt + 1 < nkt;
+        if (more) {
+          bias_load(k0 + 32);
+          fetch(k0 + 32, nxt, false);
+        }
+        if (active) {
+          f32x16 sa[kSub];
+  #pragma unroll
+          for (int sub = 0; sub < kSub; ++sub) {
+            sa[sub] = f32x16{};
+  #pragma unroll
+            for (int t = 0; t < STEPS; ++t) M::mma32(sa[sub], cur.k[t], qf[sub][t]);
+          }
+  #pragma unroll
+          for (int sub = 0; sub < kSub; ++sub) {
+            f32x16 x;
+            logits(sa[sub], kt & 1, sub, x);
+            // tile maximum, then its first row (rows ascend in key order: scan downwards)
+            float tmax = x[0];
+  #pragma unroll
+            for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, x[r]);
+            int trow = 0;
+  #pragma unroll
+            for (int r = 15; r >= 0; --r) trow = x[r] == tmax ? acc_row(r, hh) : trow;
+            if (tmax > run_max[sub]) {
+              run_max[sub] = tmax;
+              imx[sub] = k0 + trow;
+            }
+          }
+        }
+        if (more) bias_store((kt + 1) & 1);
+        __syncthreads();
+        cur = nxt;
+      }
+    }
+    // Merge the two halves (larger maximum; the smaller index on a tie), then dP at the argmax.
 #pragma unroll
-    for (int t = 0; t < STEPS; ++t)
-      part += frag_dot(of[sub][t], M::load(Vl + (long)iv * sx.n + t * M::K32 + hh * M::KPL));
-    part += __shfl_xor(part, 32, 64);
-    ref[sub] = dead[sub] ? 0.f : part;
+    for (int sub = 0; sub < kSub; ++sub) {
+      const float om = __shfl_xor(run_max[sub], 32, 64);
+      const int oi = __shfl_xor(imx[sub], 32, 64);
+      if (om > run_max[sub] || (om == run_max[sub] && oi < imx[sub])) {
+        run_max[sub] = om;
+        imx[sub] = oi;
+      }
+      const bool live = run_max[sub] >= kDeadLog2;
+      dead[sub] = !live || q0 + 32 * sub + c >= N;
+      mrow[sub] = live ? run_max[sub] : 0.f;
+      imax[sub] = dead[sub] ? -1 : imx[sub];
+      const int iv = live ? imx[sub] : 0;  // < N: keys past N have logit -inf
+      float part = 0.f;
+  #pragma unroll
+      for (int t = 0; t < STEPS; ++t)
+        part += frag_dot(of[sub][t], M::load(Vl + (long)iv * sx.n + t * M::K32 + hh * M::KPL));
+      part += __shfl_xor(part, 32, 64);
+      ref[sub] = dead[sub] ? 0.f : part;
+    }
+
   }
 
   // Pass 2: A^T [d x q] += K^T [d x keys] (p u)^T, B^T += K^T p^T, with W and C W per lane.
@@ -417,12 +438,47 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
           logits(sa[sub], kt & 1, sub, x);
           f32x16 p, pu;
 #pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(x[r] - mrow[sub]);
+          if constexpr (kLse) {
+            // The dominant key (p > 1/2: at most one per row up to rounding; the first in key
+            // order) becomes the reference when it appears: the sums so far, taken about 0,
+            // are re-centred once. A row without one keeps 0 (no term dominates D).
+            float tmax = p[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, p[r]);
+            if (__any(!found[sub] && tmax > 0.5f)) {
+              int kk = INT_MAX;
+              float dv = 0.f;
+#pragma unroll
+              for (int r = 15; r >= 0; --r)
+                if (p[r] > 0.5f) {
+                  kk = k0 + acc_row(r, hh);
+                  dv = dp[sub][r];
+                }
+              const int ok = __shfl_xor(kk, 32, 64);
+              const float odv = __shfl_xor(dv, 32, 64);
+              if (ok < kk) {
+                kk = ok;
+                dv = odv;
+              }
+              if (!found[sub] && kk != INT_MAX) {
+                const float d = ref[sub] - dv;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) da[sub][r] += d * db[sub][r];
+                Cp[sub] += d * Wp[sub];
+                ref[sub] = dv;
+                imax[sub] = kk;
+                found[sub] = true;
+              }
+            }
+          }
+#pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(x[r] - mrow[sub]);
-            const float u = (k0 + acc_row(r, hh) == imax[sub]) ? 0.f : dp[sub][r] - ref[sub];
-            p[r] = pv;
-            pu[r] = pv * u;
-            Wp[sub] += pv;
+            // with the forward's LSE the reference is this pass's own dP at imax: u = 0 there
+            const float u = kLse ? dp[sub][r] - ref[sub]
+                                 : ((k0 + acc_row(r, hh) == imax[sub]) ? 0.f : dp[sub][r] - ref[sub]);
+            pu[r] = p[r] * u;
+            Wp[sub] += p[r];
             Cp[sub] += pu[r];
           }
 #pragma unroll
@@ -764,7 +820,7 @@ template <class TC>
 int attn_bwd_launch(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias,
                     const void* dout, int B, int S, int H, int N, float scale, void* dq, void* dk, void* dv,
                     float* dbias, void* ws, hipStream_t s, const Strides4& sx, const Strides4& sdo,
-                    const Strides4& sg) {
+                    const Strides4& sg, const float* lse_in) {
   const BwdWs lay = bwd_ws_layout(B, S, H, N, (int)sizeof(TC));
   char* base = static_cast<char*>(ws);
   f32x4* st4 = reinterpret_cast<f32x4*>(base + lay.st);
@@ -791,8 +847,13 @@ int attn_bwd_launch(const void* q, const void* k, const void* v, const float* re
                                                                                    QT, OT, S, H, N, Np, sx, sdo);
   if (int e = pf::check_launch("attn_bwd_relayout")) return e;
   const unsigned lg = (unsigned)((S + kLines - 1) / kLines);
-  attn_bwd_dq_kernel<TC, kSubDq><<<dim3((unsigned)(Np / (32 * kSubDq)), lg, (unsigned)(B * H)), kNT, 0, s>>>(
-      QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N, Np, scale, static_cast<TC*>(dq), st4, sx, sg);
+  const dim3 gdq((unsigned)(Np / (32 * kSubDq)), lg, (unsigned)(B * H));
+  if (lse_in)
+    attn_bwd_dq_kernel<TC, kSubDq, true><<<gdq, kNT, 0, s>>>(QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N, Np, scale,
+                                                            static_cast<TC*>(dq), st4, sx, sg, lse_in);
+  else
+    attn_bwd_dq_kernel<TC, kSubDq, false><<<gdq, kNT, 0, s>>>(QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N, Np, scale,
+                                                             static_cast<TC*>(dq), st4, sx, sg, nullptr);
   if (int e = pf::check_launch("attn_bwd_dq")) return e;
   attn_bwd_dkdv_kernel<TC, kSubKv><<<dim3((unsigned)(Np / (32 * kSubKv)), lg, (unsigned)(B * H)), kNT, 0, s>>>(
       QR, KR, VR, OR, QT, OT, mask2, bias2, S, H, N, Np, scale, st4, static_cast<TC*>(dk), static_cast<TC*>(dv), sg);
@@ -816,7 +877,7 @@ int evo_attn_bwd_any(const char* fn, const void* q, const void* k, const void* v
                      const float* pair_bias, const void* dout, int B, int S, int H, int N, int D, int dtype,
                      float softmax_scale, void* dq, void* dk, void* dv, float* dpair_bias, void* workspace,
                      size_t workspace_bytes, void* stream, const Strides4& sx, const Strides4& sdo,
-                     const Strides4& sg) {
+                     const Strides4& sg, const float* lse_in) {
   PF_REQUIRE(q && k && v && res_mask && pair_bias && dout && dq && dk && dv && dpair_bias && workspace,
              PF_ERR_INVALID_ARG, "%s: null pointer", fn);
   PF_REQUIRE(B > 0 && S > 0 && H > 0 && N > 0, PF_ERR_INVALID_ARG, "%s: B=%d S=%d H=%d N=%d", fn, B, S, H, N);
@@ -836,9 +897,9 @@ int evo_attn_bwd_any(const char* fn, const void* q, const void* k, const void* v
   hipStream_t s = pf::as_stream(stream);
   if (dtype == PF_F32)
     return attn_bwd_launch<float>(q, k, v, res_mask, pair_bias, dout, B, S, H, N, softmax_scale, dq, dk, dv,
-                                  dpair_bias, workspace, s, sx, sdo, sg);
+                                  dpair_bias, workspace, s, sx, sdo, sg, lse_in);
   return attn_bwd_launch<bf16>(q, k, v, res_mask, pair_bias, dout, B, S, H, N, softmax_scale, dq, dk, dv, dpair_bias,
-                               workspace, s, sx, sdo, sg);
+                               workspace, s, sx, sdo, sg, lse_in);
 }
 
 }  // namespace
@@ -855,12 +916,13 @@ int pf_evo_attn_bwd(const void* q, const void* k, const void* v, const float* re
                     void* dk, void* dv, float* dpair_bias, void* workspace, size_t workspace_bytes, void* stream) {
   const Strides4 dense{(long)S * H * N * D, (long)H * N * D, (long)N * D, D};
   return evo_attn_bwd_any("pf_evo_attn_bwd", q, k, v, res_mask, pair_bias, dout, B, S, H, N, D, dtype, softmax_scale,
-                          dq, dk, dv, dpair_bias, workspace, workspace_bytes, stream, dense, dense, dense);
+                          dq, dk, dv, dpair_bias, workspace, workspace_bytes, stream, dense, dense, dense, nullptr);
 }
 
 int pf_evo_attn_bwd_strided(const void* q, const void* k, const void* v, const long* qkv_strides,
                             const float* res_mask, const float* pair_bias, const void* dout, const long* dout_strides,
-                            int B, int S, int H, int N, int D, int dtype, float softmax_scale, void* dq, void* dk,
+                            const float* lse, int B, int S, int H, int N, int D, int dtype, float softmax_scale,
+                            void* dq, void* dk,
                             void* dv, const long* grad_strides, float* dpair_bias, void* workspace,
                             size_t workspace_bytes, void* stream) {
   PF_REQUIRE(qkv_strides && dout_strides && grad_strides, PF_ERR_INVALID_ARG, "pf_evo_attn_bwd_strided: null strides");
@@ -868,7 +930,8 @@ int pf_evo_attn_bwd_strided(const void* q, const void* k, const void* v, const l
   const Strides4 sdo{dout_strides[0], dout_strides[1], dout_strides[2], dout_strides[3]};
   const Strides4 sg{grad_strides[0], grad_strides[1], grad_strides[2], grad_strides[3]};
   return evo_attn_bwd_any("pf_evo_attn_bwd_strided", q, k, v, res_mask, pair_bias, dout, B, S, H, N, D, dtype,
-                          softmax_scale, dq, dk, dv, dpair_bias, workspace, workspace_bytes, stream, sx, sdo, sg);
+                          softmax_scale, dq, dk, dv, dpair_bias, workspace, workspace_bytes, stream, sx, sdo, sg,
+                          lse);
 }
 
 }  // extern "C"

@@ -138,7 +138,14 @@ class _GridAttnCore(torch.autograd.Function):
     same token order. The kernels read q, k, v and dO and write O and dq, dk, dv (into the
     gradient of qkv) through strides (``pf_evo_attn_fwd_strided`` / ``pf_evo_attn_bwd_strided``),
     so nothing is permuted or copied around them. The kernel's masked-line rule (a line whose
-    keys are all masked outputs 0). H = 4, D = 32."""
+    keys are all masked outputs 0). H = 4, D = 32.
+
+    With ``use_lse`` (the default) the forward also writes each row's log-sum-exp and the
+    backward's dQ kernel takes it in place of its own pass over the keys for the row maximum
+    (``pf_evo_attn_bwd_strided``'s ``lse``; the reference saves softmax_lse the same way,
+    ``evo_attention.py:1279-1290``)."""
+
+    use_lse = True
 
     @staticmethod
     def _layout(qkv, transpose):
@@ -162,6 +169,9 @@ class _GridAttnCore(torch.autograd.Function):
         if ws_bytes == 0:
             raise NotActive("GridSelfAttention", f"H={H}, D={D}: the strided attention is built for H=4, D=32")
         out = torch.empty(qkv.shape[:3] + (H, D), dtype=qkv.dtype, device=qkv.device)
+        # row log-sum-exp (log2 units) for the backward's single dQ pass; rows padded to 128
+        use_lse = _GridAttnCore.use_lse
+        lse = torch.empty((B, S, H, -(-N // 128) * 128) if use_lse else (0,), dtype=torch.float32, device=qkv.device)
         ws = _ws(ws_bytes, qkv.device)
         es = qkv.element_size()
         base = qkv.data_ptr()
@@ -169,16 +179,17 @@ class _GridAttnCore(torch.autograd.Function):
         ao, po = _strides(*so)
         _lib.call(
             "pf_evo_attn_fwd_strided", base, base + H * D * es, base + 2 * H * D * es, px, rm.data_ptr(),
-            pb.data_ptr(), B, S, H, N, D, code, 1, out.data_ptr(), po, ws.data_ptr(), ws_bytes, _lib.stream_of(qkv),
+            pb.data_ptr(), B, S, H, N, D, code, 1, out.data_ptr(), po, lse.data_ptr() if use_lse else None,
+            ws.data_ptr(), ws_bytes, _lib.stream_of(qkv),
         )  # fmt: skip
         _lib.note_redo("pf_evo_attn_redo_flags", ws, B, S, H, N, D, code)
-        ctx.save_for_backward(qkv, rm, pb)
+        ctx.save_for_backward(qkv, rm, pb, lse)
         ctx.transpose = bool(transpose)
         return out
 
     @staticmethod
     def backward(ctx, dO):
-        qkv, rm, pb = ctx.saved_tensors
+        qkv, rm, pb, lse = ctx.saved_tensors
         B, S, H, N, D, sx, so = _GridAttnCore._layout(qkv, ctx.transpose)
         code = _lib.dtype_code(qkv.dtype)
         dO = dO.to(qkv.dtype).contiguous()
@@ -193,8 +204,9 @@ class _GridAttnCore(torch.autograd.Function):
         kernel_census.record("GridSelfAttention.backward", "hip_evo_attn_bwd_strided")
         _lib.call(
             "pf_evo_attn_bwd_strided", base, base + H * D * es, base + 2 * H * D * es, px, rm.data_ptr(),
-            pb.data_ptr(), dO.data_ptr(), po, B, S, H, N, D, code, float(D) ** -0.5, gbase, gbase + H * D * es,
-            gbase + 2 * H * D * es, px, dpb.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(qkv),
+            pb.data_ptr(), dO.data_ptr(), po, lse.data_ptr() if lse.numel() else None, B, S, H, N, D, code,
+            float(D) ** -0.5, gbase, gbase + H * D * es, gbase + 2 * H * D * es, px, dpb.data_ptr(), ws.data_ptr(),
+            ws_bytes, _lib.stream_of(qkv),
         )  # fmt: skip
         return dqkv, None, dpb, None
 

@@ -316,16 +316,25 @@ int pf_evo_attn_bwd(const void* q, const void* k, const void* v, const float* re
  * views of its token-major [B, N, N, 3, H, D] projection (rows: line stride N 3HD, key stride
  * 3HD; columns the two swapped) and takes O and the gradients in the same token order, so no
  * operand is permuted or copied around the kernels. Same arithmetic as the dense entry points;
- * res_mask [B, S, N] and pair_bias [B, H, N, N] stay dense. */
+ * res_mask [B, S, N] and pair_bias [B, H, N, N] stay dense.
+ * lse (optional, NULL to skip): the forward writes each row's log-sum-exp of the logits in
+ * log2 units, fp32 [B, S, H, Np] with Np = N rounded up to 128 (rows q < N written; +inf for a
+ * line whose keys are all masked), the reference kernel's saved softmax_lse
+ * (evo_attention.py:1279-1290). Given to the backward, it replaces the backward's first pass
+ * over the keys (the row maximum): dQ's single pass takes p = 2^(x - lse) and re-centres its
+ * sums on the row's dominant key (p > 1/2) when that key is reached. The backward recomputes
+ * the row sum itself, so its results do not depend on the forward's rounding of lse; it must
+ * come from the forward on the same q, k, res_mask, pair_bias and the backward's scale must
+ * be 32^-1/2. NULL keeps the two-pass backward. */
 int pf_evo_attn_fwd_strided(const void* q, const void* k, const void* v, const long* qkv_strides,
                             const float* res_mask, const float* pair_bias, int B, int S, int H, int N, int D,
-                            int dtype, int masked_rows_zero, void* out, const long* out_strides, void* workspace,
-                            size_t workspace_bytes, void* stream);
+                            int dtype, int masked_rows_zero, void* out, const long* out_strides, float* lse,
+                            void* workspace, size_t workspace_bytes, void* stream);
 int pf_evo_attn_bwd_strided(const void* q, const void* k, const void* v, const long* qkv_strides,
                             const float* res_mask, const float* pair_bias, const void* dout, const long* dout_strides,
-                            int B, int S, int H, int N, int D, int dtype, float softmax_scale, void* dq, void* dk,
-                            void* dv, const long* grad_strides, float* dpair_bias, void* workspace,
-                            size_t workspace_bytes, void* stream);
+                            const float* lse, int B, int S, int H, int N, int D, int dtype, float softmax_scale,
+                            void* dq, void* dk, void* dv, const long* grad_strides, float* dpair_bias,
+                            void* workspace, size_t workspace_bytes, void* stream);
 /* FusedPairBias(c, H)(z, ln_w, ln_b, proj_w, mask) (triton/fused_pair_bias.py:348-416):
  * z [B,N,N,C] -> out [B,H,N,N] in z's dtype; proj_w16 [16, C] fp32 (proj_w padded with zero
  * rows); mask [B,N] fp32 or NULL adds (1 - mask) * (-1e9) on the last axis. C = 128, H <= 16. */

@@ -15,7 +15,8 @@
   masked-row rule under grad.
 - The strided entry points (GridSelfAttention's training path on its token-major
   projection, rows and columns) against the dense ones on the same values: O, dQ, dK, dV
-  and d_pair_bias bit for bit.
+  and d_pair_bias bit for bit; with the forward's saved row LSE (single dQ pass) against
+  the two-pass backward, flat and peaked softmax.
 """
 
 from __future__ import annotations
@@ -235,11 +236,7 @@ def test_grid_attention_module_backward_bf16(dev, transpose):
         assert e_hip < 3 * e_stock + 1e-3, k
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, BF], ids=["fp32", "bf16"])
-@pytest.mark.parametrize("transpose", [False, True], ids=["rows", "cols"])
-def test_strided_attention_equals_dense(dev, transpose, dtype):
-    """fused._GridAttnCore (strides) against _EvoAttnFunction on the permuted, contiguous
-    operands: the same packed operands reach the same kernels, so every output is equal."""
+def _strided_case(dev, transpose, dtype, bias_sigma):
     B, N, H, D = 2, 45, 4, 32
     g = torch.Generator().manual_seed(17 + int(transpose))
     qkv = (torch.randn(B, N, N, 3, H, D, generator=g) * 0.4).to(dev, dtype)
@@ -247,22 +244,78 @@ def test_strided_attention_equals_dense(dev, transpose, dtype):
     keep[:, :, 0] = True
     keep[:, 5] = False  # a fully masked line
     rm = torch.where(keep, 0.0, -1e9).to(dev)  # [B, lines, keys]
-    pb = torch.randn(B, H, N, N, generator=g).to(dev)
+    pb = (torch.randn(B, H, N, N, generator=g) * bias_sigma).to(dev)
     dO = torch.randn(B, N, N, H, D, generator=g).to(dev, dtype)
-    print(f"[strided attention] transpose={transpose} dtype={dtype}", flush=True)
+    return qkv, rm, pb, dO
 
-    x1 = qkv.clone().requires_grad_(True)
-    p1 = pb.clone().requires_grad_(True)
-    o1 = fused._GridAttnCore.apply(x1, rm, p1, transpose)
-    o1.backward(dO)
 
+def _run_strided(qkv, rm, pb, dO, transpose, use_lse):
+    x = qkv.clone().requires_grad_(True)
+    p = pb.clone().requires_grad_(True)
+    saved = fused._GridAttnCore.use_lse
+    fused._GridAttnCore.use_lse = use_lse
+    try:
+        o = fused._GridAttnCore.apply(x, rm, p, transpose)
+        o.backward(dO)
+    finally:
+        fused._GridAttnCore.use_lse = saved
+    return o, x.grad, p.grad
+
+
+def _run_dense(qkv, rm, pb, dO, transpose):
     frame = (0, 2, 3, 1, 4) if transpose else (0, 1, 3, 2, 4)  # [B, line, H, key, D]
     back = (0, 3, 1, 2, 4) if transpose else (0, 1, 3, 2, 4)
-    x2 = qkv.clone().requires_grad_(True)
-    p2 = pb.clone().requires_grad_(True)
-    q, k, v = (x2[:, :, :, i].permute(*frame).contiguous() for i in range(3))
-    o2 = fused._EvoAttnFunction.apply(q, k, v, rm, p2).permute(*back)
-    o2.backward(dO)
+    x = qkv.clone().requires_grad_(True)
+    p = pb.clone().requires_grad_(True)
+    q, k, v = (x[:, :, :, i].permute(*frame).contiguous() for i in range(3))
+    o = fused._EvoAttnFunction.apply(q, k, v, rm, p).permute(*back)
+    o.backward(dO)
+    return o, x.grad, p.grad
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, BF], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("transpose", [False, True], ids=["rows", "cols"])
+def test_strided_attention_equals_dense(dev, transpose, dtype):
+    """fused._GridAttnCore (strides, two-pass backward) against _EvoAttnFunction on the
+    permuted, contiguous operands: the same packed operands reach the same kernels, so every
+    output is equal."""
+    qkv, rm, pb, dO = _strided_case(dev, transpose, dtype, 1.0)
+    print(f"[strided attention] transpose={transpose} dtype={dtype}", flush=True)
+    o1, gx1, gp1 = _run_strided(qkv, rm, pb, dO, transpose, use_lse=False)
+    o2, gx2, gp2 = _run_dense(qkv, rm, pb, dO, transpose)
     assert torch.equal(o1, o2)
-    assert torch.equal(x1.grad, x2.grad)
-    assert torch.equal(p1.grad, p2.grad)
+    assert torch.equal(gx1, gx2)
+    assert torch.equal(gp1, gp2)
+
+
+@pytest.mark.parametrize("bias_sigma", [1.0, 6.0], ids=["flat", "peaked"])
+@pytest.mark.parametrize("dtype", [torch.float32, BF], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("transpose", [False, True], ids=["rows", "cols"])
+def test_strided_attention_saved_lse(dev, transpose, dtype, bias_sigma):
+    """The backward on the forward's saved row LSE (one dQ pass, re-centred on the dominant
+    key when it is reached) against the two-pass backward: the same O; gradients within
+    relL2 1e-5 of the two-pass fp32 ones in fp32, and in bf16 no further from the fp32
+    two-pass gradients than the bf16 two-pass ones (x 1.25 + 1e-4). The peaked case (pair
+    bias sigma 6) puts most rows' mass on one key, some of them in the second key tile."""
+    qkv, rm, pb, dO = _strided_case(dev, transpose, dtype, bias_sigma)
+    print(f"[strided attention lse] transpose={transpose} dtype={dtype} sigma={bias_sigma}", flush=True)
+    o1, gx1, gp1 = _run_strided(qkv, rm, pb, dO, transpose, use_lse=True)
+    o2, gx2, gp2 = _run_strided(qkv, rm, pb, dO, transpose, use_lse=False)
+    assert torch.equal(o1, o2)
+    assert torch.isfinite(gx1).all() and torch.isfinite(gp1).all()
+    from tests._helpers import rel_l2
+
+    if dtype == torch.float32:
+        for a, b, what in ((gx1, gx2, "dqkv"), (gp1, gp2, "dpair_bias")):
+            e = rel_l2(a.cpu(), b.cpu())
+            print(f"  {what}: relL2 {e:.2e}", flush=True)
+            assert e <= 1e-5, what
+    else:
+        _, rx, rp = _run_strided(qkv.float(), rm, pb, dO.float(), transpose, use_lse=False)
+        for a, b, r, what in ((gx1, gx2, rx, "dqkv"), (gp1, gp2, rp, "dpair_bias")):
+            e1, e2 = rel_l2(a.float().cpu(), r.cpu()), rel_l2(b.float().cpu(), r.cpu())
+            print(f"  {what}: lse {e1:.2e} two-pass {e2:.2e}", flush=True)
+            assert e1 <= 1.25 * e2 + 1e-4, what
+    # the fully masked line has zero gradients either way
+    line = (slice(None), slice(None), 5) if transpose else (slice(None), 5)
+    assert not gx1[line].any()
