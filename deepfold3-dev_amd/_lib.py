@@ -34,6 +34,9 @@ SIGNATURES: dict[str, tuple] = {
     "pf_kernel_timer_stop": (_i, []),
     "pf_cast": (_i, [_vp, _i, _vp, _i, _sz, _vp]),
     "pf_add": (_i, [_vp, _i, _vp, _i, _vp, _sz, _vp]),
+    "pf_dropout_mask": (_i, [_vp, _l, _f, ctypes.c_ulonglong, _vp]),
+    "pf_dropout_add_fwd": (_i, [_vp, _i, _vp, _i, _vp, _l, _l, _l, _l, _i, _f, ctypes.c_ulonglong, _vp]),
+    "pf_dropout_bwd": (_i, [_vp, _i, _vp, _i, _l, _l, _l, _l, _i, _f, ctypes.c_ulonglong, _vp]),
     "pf_layernorm_fwd": (_i, [_vp, _i, _vp, _vp, _f, _vp, ctypes.c_long, _i, _vp]),
     "pf_layernorm_bwd_workspace_bytes": (_sz, [ctypes.c_long, _i]),
     "pf_layernorm_bwd": (_i, [_vp, _vp, _i, _vp, _f, _vp, _vp, _vp, ctypes.c_long, _i, _vp, _sz, _vp]),
@@ -83,7 +86,7 @@ SIGNATURES: dict[str, tuple] = {
     "pf_evo_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "pf_evo_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "pf_evo_attn_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
-    "pf_evo_attn_bwd": (_i, [_vp] * 6 + [_i] * 6 + [_f] + [_vp] * 5 + [_sz, _vp]),
+    "pf_evo_attn_bwd": (_i, [_vp] * 6 + [_i] * 6 + [_f, _i] + [_vp] * 5 + [_sz, _vp]),
     "pf_evo_attn_fwd_strided": (_i, [_vp] * 6 + [_i] * 7 + [_vp] * 4 + [_sz, _vp]),
     "pf_evo_attn_bwd_strided": (_i, [_vp] * 9 + [_i] * 6 + [_f] + [_vp] * 6 + [_sz, _vp]),
     "pf_pair_mask_outer": (_i, [_vp, _i, _i, _vp, _vp, _vp]),

@@ -48,10 +48,11 @@ class GridSelfAttention(nn.Module):
         self.to_g = LinearNoBias(c, num_heads * self.head_dim, initializer="zeros")
         self.out_proj = LinearNoBias(num_heads * self.head_dim, c, initializer="zeros")
         self._cache = WeightCache()
-        # Residual scale of this branch (the block's ``s_ros``), folded into out_proj.
+        # Residual scale of this branch inside its block (the block's ``s_ros``), folded into
+        # out_proj by ``branch`` and ``forward_residual_``; ``forward`` is unscaled.
         self.branch_scale = 1.0
 
-    def _operands(self, cdt: torch.dtype) -> dict:
+    def _operands(self, cdt: torch.dtype, scale: float = 1.0) -> dict:
         params = [
             self.norm.weight, self.norm.bias, self.pair_bias.weight, self.to_q.weight, self.to_k.weight,
             self.to_v.weight, self.to_g.weight, self.out_proj.weight,
@@ -62,27 +63,28 @@ class GridSelfAttention(nn.Module):
                 w5=pack_grid_attn_weights(
                     self.to_q.weight, self.to_k.weight, self.to_v.weight, self.to_g.weight, self.pair_bias.weight, cdt
                 ),
-                w_out=scaled_weight(self.out_proj.weight, self.branch_scale, cdt),
+                w_out=scaled_weight(self.out_proj.weight, scale, cdt),
                 lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
             )  # fmt: skip
 
-        return self._cache.get(params, cdt, build, tag=self.branch_scale)
+        return self._cache.get(params, cdt, build, tag=float(scale))
 
-    def _run(self, z, mask, out, accumulate):
+    def _run(self, z, mask, out, accumulate, scale: float = 1.0):
         kernel_census.record("GridSelfAttention.attention", "hip_tri_attn_col" if self.transpose else "hip_tri_attn_row")
-        op = self._operands(gemm_dtype_for(z))
+        op = self._operands(gemm_dtype_for(z), scale)
         return grid_attention_forward(
             z, mask, op["lnw"], op["lnb"], self.norm.eps, op["w5"], op["w_out"], self.transpose,
             num_heads=self.num_heads, out=out, accumulate=accumulate,
         )  # fmt: skip
 
-    def _forward_grad(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    def _forward_grad(self, z: torch.Tensor, mask: torch.Tensor, scale: float) -> torch.Tensor:
         """Training path, as the reference's fused-attention branch (``attention.py:211-257``):
         LayerNorm, pair bias and q/k/v/g projections in autograd, the HIP flash attention with
         its backward (the kernel's masked-row rule), gate and output projection in autograd.
         With 4 heads the attention (``fused._GridAttnCore``) reads the token-major projection
         and writes O and the gradients in that order through strides; other head counts go
-        through the kernel-layout ``fused._EvoformerAttention``. Head dimension 32."""
+        through the kernel-layout ``fused._EvoformerAttention``. Head dimension 32; ``scale`` on
+        out_proj."""
         from .fused import _EvoformerAttention, _GridAttnCore
 
         B, N, _, C = z.shape
@@ -96,7 +98,7 @@ class GridSelfAttention(nn.Module):
         pb = pb.to(torch.float32, memory_format=torch.contiguous_format)
         line_mask = mask.transpose(1, 2) if self.transpose else mask  # [B, lines, keys]
         res_mask = torch.where(line_mask > 0.5, 0.0, -1e9).contiguous()
-        w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
+        w_out = self.out_proj.weight if scale == 1.0 else self.out_proj.weight * scale
         g = torch.sigmoid(token_linear(zn, self.to_g.weight))
         if H == 4:
             # q, k, v in one product over the un-transposed tokens; the attention reads them and
@@ -115,25 +117,32 @@ class GridSelfAttention(nn.Module):
         o = o.permute(*back).reshape(B, N, N, H * D)
         return token_linear(o * g, w_out)
 
-    def forward(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
-        """The update for z [B?, N, N, C], mask [B?, N, N] (not added to z). Under grad it
-        runs the differentiable path, else the fused inference kernels."""
+    def _update(self, z: torch.Tensor, mask: torch.Tensor, scale: float) -> torch.Tensor:
         has_batch = z.dim() == 4
         if not has_batch:
             z, mask = z.unsqueeze(0), mask.unsqueeze(0)
         if torch.is_grad_enabled():
             kernel_census.record("GridSelfAttention.attention", "hip_evo_attn_grad")
-            out = self._forward_grad(z, mask)
+            out = self._forward_grad(z, mask, scale)
         else:
-            out = self._run(z, mask, None, False)
+            out = self._run(z, mask, None, False, scale)
         return out if has_batch else out.squeeze(0)
+
+    def forward(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """The update for z [B?, N, N, C], mask [B?, N, N] (not added to z). Under grad it
+        runs the differentiable path, else the fused inference kernels."""
+        return self._update(z, mask, 1.0)
+
+    def branch(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """``branch_scale * forward(z, mask)``: the update as its block adds it (out of place)."""
+        return self._update(z, mask, self.branch_scale)
 
     @inference_only("GridSelfAttention")
     def forward_residual_(self, z: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
-        """``z += update`` in place (fused into the output projection)."""
+        """``z += branch_scale * update`` in place (fused into the output projection)."""
         if not z.is_contiguous():
             raise NotActive("GridSelfAttention", "in-place residual needs a contiguous z")
-        return self._run(z, mask, z, True)
+        return self._run(z, mask, z, True, self.branch_scale)
 
 
 class MSAAttention(nn.Module):
@@ -157,10 +166,11 @@ class MSAAttention(nn.Module):
         self.to_g = LinearNoBias(c_msa, num_heads * self.head_dim, initializer="zeros")
         self.out_proj = LinearNoBias(num_heads * self.head_dim, c_msa, initializer="zeros")
         self._cache = WeightCache()
-        # Residual scale of this branch (the block's s_ros), folded into out_proj.
+        # Residual scale of this branch inside its block (the block's s_ros), folded into
+        # out_proj by ``branch`` and ``forward_residual_``; ``forward`` is unscaled.
         self.branch_scale = 1.0
 
-    def _operands(self, cdt: torch.dtype) -> dict:
+    def _operands(self, cdt: torch.dtype, scale: float = 1.0) -> dict:
         params = [
             self.norm.weight, self.norm.bias, self.pair_norm.weight, self.pair_norm.bias, self.pair_logits.weight,
             self.to_v.weight, self.to_g.weight, self.out_proj.weight,
@@ -172,18 +182,18 @@ class MSAAttention(nn.Module):
             return dict(
                 w_lg=cast_weight(torch.cat([w_lg, pad]), cdt),
                 w_vg=cast_weight(torch.cat([self.to_v.weight, self.to_g.weight]).detach(), cdt),
-                w_out=scaled_weight(self.out_proj.weight, self.branch_scale, cdt),
+                w_out=scaled_weight(self.out_proj.weight, scale, cdt),
                 lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
                 plnw=f32(self.pair_norm.weight), plnb=f32(self.pair_norm.bias),
             )  # fmt: skip
 
-        return self._cache.get(params, cdt, build, tag=self.branch_scale)
+        return self._cache.get(params, cdt, build, tag=float(scale))
 
-    def _run(self, msa, mask, pair, out, accumulate):
+    def _run(self, msa, mask, pair, out, accumulate, scale: float = 1.0):
         from .kernels import msa_pair_avg_forward
 
         kernel_census.record("MSAAttention", "hip_msa_pair_avg")
-        op = self._operands(gemm_dtype_for(msa))
+        op = self._operands(gemm_dtype_for(msa), scale)
         return msa_pair_avg_forward(
             msa, mask, pair, op["lnw"], op["lnb"], self.norm.eps, op["plnw"], op["plnb"], self.pair_norm.eps,
             op["w_lg"], op["w_vg"], op["w_out"], self.num_heads, out=out, accumulate=accumulate,
@@ -192,18 +202,26 @@ class MSAAttention(nn.Module):
     @inference_only("MSAAttention")
     def forward(self, msa: torch.Tensor, mask: torch.Tensor, pair: torch.Tensor) -> torch.Tensor:
         """msa [B?, S, N, c_msa], mask [B?, S, N], pair [B?, N, N, c_pair] -> the msa update."""
+        return self._update(msa, mask, pair, 1.0)
+
+    @inference_only("MSAAttention")
+    def branch(self, msa: torch.Tensor, mask: torch.Tensor, pair: torch.Tensor) -> torch.Tensor:
+        """``branch_scale * forward(msa, mask, pair)``: the update as its block adds it."""
+        return self._update(msa, mask, pair, self.branch_scale)
+
+    def _update(self, msa, mask, pair, scale):
         has_batch = msa.dim() == 4
         if not has_batch:
             msa, mask, pair = msa.unsqueeze(0), mask.unsqueeze(0), pair.unsqueeze(0)
-        out = self._run(msa, mask, pair, None, False)
+        out = self._run(msa, mask, pair, None, False, scale)
         return out if has_batch else out.squeeze(0)
 
     @inference_only("MSAAttention")
     def forward_residual_(self, msa: torch.Tensor, mask: torch.Tensor, pair: torch.Tensor) -> torch.Tensor:
-        """``msa += update`` in place; msa contiguous [B, S, N, c_msa]."""
+        """``msa += branch_scale * update`` in place; msa contiguous [B, S, N, c_msa]."""
         if not msa.is_contiguous():
             raise NotActive("MSAAttention", "in-place residual needs a contiguous msa")
-        return self._run(msa, mask, pair, msa, True)
+        return self._run(msa, mask, pair, msa, True, self.branch_scale)
 
 
 class SingleAttention(nn.Module):
@@ -241,10 +259,11 @@ class SingleAttention(nn.Module):
         self.to_g = LinearNoBias(c, value_dim, initializer="zeros")
         self.out_proj = LinearNoBias(value_dim, c, initializer="zeros")
         self._cache = WeightCache()
-        # Residual scale of this branch (the block's ``s_ros``), folded into out_proj.
+        # Residual scale of this branch inside its block (the block's ``s_ros``), folded into
+        # out_proj by ``branch`` and ``forward_residual_``; ``forward`` is unscaled.
         self.branch_scale = 1.0
 
-    def _operands(self, cdt: torch.dtype) -> dict:
+    def _operands(self, cdt: torch.dtype, scale: float = 1.0) -> dict:
         params = [
             self.norm.weight, self.norm.bias, self.to_q.weight, self.to_q.bias, self.to_k.weight, self.to_v.weight,
             self.to_g.weight, self.out_proj.weight,
@@ -253,26 +272,27 @@ class SingleAttention(nn.Module):
         def build():
             w = torch.cat([self.to_q.weight, self.to_k.weight, self.to_v.weight, self.to_g.weight]).detach()
             return dict(
-                wqkvg=cast_weight(w, cdt), w_out=scaled_weight(self.out_proj.weight, self.branch_scale, cdt),
+                wqkvg=cast_weight(w, cdt), w_out=scaled_weight(self.out_proj.weight, scale, cdt),
                 qb=f32(self.to_q.bias), lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
             )  # fmt: skip
 
-        return self._cache.get(params, cdt, build, tag=self.branch_scale)
+        return self._cache.get(params, cdt, build, tag=float(scale))
 
-    def _run(self, x, mask, pair_logits, out, accumulate):
+    def _run(self, x, mask, pair_logits, out, accumulate, scale: float = 1.0):
         kernel_census.record("SingleAttention", "hip_single_attn")
-        op = self._operands(gemm_dtype_for(x))
+        op = self._operands(gemm_dtype_for(x), scale)
         return single_attention_forward(
             x, mask, pair_logits, op["lnw"], op["lnb"], self.norm.eps, op["wqkvg"], op["qb"], op["w_out"],
             self.num_heads, out=out, accumulate=accumulate,
         )  # fmt: skip
 
-    def _forward_grad(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
+    def _forward_grad(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor, scale: float) -> torch.Tensor:
         """Training path: LayerNorm (HIP, with its backward), the q/k/v/g projections and the output
         projection in autograd, and the attention core on the HIP flash attention with its
         backward (``fused._EvoformerAttention``; one line per batch item, the heads' key and value
         dimensions zero-padded to 32 and q scaled so that the kernel's 32^-1/2 gives d^-1/2,
-        ``attention.py:415-433``)."""
+        ``attention.py:415-433``), under the eager masked-row rule in both passes, as the stock
+        softmax: a batch item whose keys are all masked attends uniformly."""
         from .fused import _EvoformerAttention
         from .kernels import LayerNormFunction
 
@@ -291,27 +311,36 @@ class SingleAttention(nn.Module):
 
         Q, K, V = heads(q, Dk), heads(F.linear(xn, self.to_k.weight), Dk), heads(F.linear(xn, self.to_v.weight), Dv)
         res_mask = (1e9 * (mask.float() - 1.0)).view(B, 1, 1, 1, N)
-        o = _EvoformerAttention.apply(Q, K, V, res_mask, pair_logits.float().unsqueeze(1), True)
+        # the stock path's rule for a batch item whose keys are all masked: uniform weights
+        o = _EvoformerAttention.apply(Q, K, V, res_mask, pair_logits.float().unsqueeze(1), True, "eager")
         o = o[:, 0, :, :, :Dv].transpose(1, 2).reshape(B, N, H * Dv)
         g = torch.sigmoid(F.linear(xn, self.to_g.weight))
-        w_out = self.out_proj.weight if self.branch_scale == 1.0 else self.out_proj.weight * self.branch_scale
+        w_out = self.out_proj.weight if scale == 1.0 else self.out_proj.weight * scale
         return F.linear(o * g, w_out)
 
-    def forward(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
-        """x [B?, N, c], mask [B?, N], pair_logits [B?, H, N, N] -> update [B?, N, c]. Under grad
-        the differentiable path."""
+    def _update(self, x, mask, pair_logits, scale: float) -> torch.Tensor:
         has_batch = x.dim() == 3
         if not has_batch:
             x, mask, pair_logits = x.unsqueeze(0), mask.unsqueeze(0), pair_logits.unsqueeze(0)
         if torch.is_grad_enabled():
             kernel_census.record("SingleAttention", "hip_evo_attn_grad")
-            out = self._forward_grad(x, mask, pair_logits)
+            out = self._forward_grad(x, mask, pair_logits, scale)
         else:
-            out = self._run(x, mask, pair_logits, None, False)
+            out = self._run(x, mask, pair_logits, None, False, scale)
         return out if has_batch else out.squeeze(0)
+
+    def forward(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
+        """x [B?, N, c], mask [B?, N], pair_logits [B?, H, N, N] -> update [B?, N, c]. Under grad
+        the differentiable path."""
+        return self._update(x, mask, pair_logits, 1.0)
+
+    def branch(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
+        """``branch_scale * forward(x, mask, pair_logits)``: the update as its block adds it."""
+        return self._update(x, mask, pair_logits, self.branch_scale)
 
     @inference_only("SingleAttention")
     def forward_residual_(self, x: torch.Tensor, mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
+        """``x += branch_scale * update`` in place."""
         if not x.is_contiguous():
             raise NotActive("SingleAttention", "in-place residual needs a contiguous x")
-        return self._run(x, mask, pair_logits, x, True)
+        return self._run(x, mask, pair_logits, x, True, self.branch_scale)

@@ -17,9 +17,10 @@ the weights by state-dict key. This module does the same for the parts built her
 Tensors are read one key at a time through safetensors' ``safe_open`` (nothing in the file
 is executed, and only the keys under the requested prefix are read). A configuration this
 build cannot serve (pair channels other than 64, 128 or 256, pair heads wider than 32, MHR
-trimul, the pair-bias gate, an RMSNorm branch scaler, a stack without triangle attention or
-the single track) refuses by name when the stack is constructed or first run. Loading is strict within the prefix: a missing or unexpected
-key raises.
+trimul, the pair-bias gate, an RMSNorm branch scaler) refuses by name when the stack is
+constructed or first run. Stacks without triangle attention or without the single track (the
+reference's current ``configs/stage0.yaml`` shape) are built without those branches. Loading
+is strict within the prefix: a missing or unexpected key raises.
 """
 
 from __future__ import annotations
@@ -141,7 +142,8 @@ def block_residual_scale(layer_idx: int, num_layer: int, per_layer: bool, unifor
     """Residual output scale of layer ``layer_idx`` (``primitives.py:20-44``): 1/sqrt(i+1)
     per layer, 1/sqrt(L) uniform, 1 otherwise; both set is an error."""
     if per_layer and uniform:
-        raise ValueError("residual_output_scaling and uniform_residual_scale are mutually exclusive on the same stack")
+        raise ValueError("a stack takes either per-layer (residual_output_scaling) or uniform "
+                         "(uniform_residual_scale) residual scales, not both")  # fmt: skip
     if per_layer:
         return 1.0 / math.sqrt(float(layer_idx + 1))
     if uniform:

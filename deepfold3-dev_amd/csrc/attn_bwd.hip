@@ -8,8 +8,16 @@
 //   C_i = sum_j P_ij u_ij,
 // which equals P (dP - rowsum(P dP)) but never subtracts two O(1) numbers at the softmax
 // argmax. Outputs: dQ = scale dS K, dK = scale dS^T Q, dV = P^T dO, d_bias = sum_s dS.
-// A line whose keys are all masked (max logit < -1e8) gets LSE = +inf, so P = 0 and every
-// gradient of its rows is 0: the reference kernel's masked-row rule (its forward writes 0).
+// Masked rows: under the reference kernel's rule a line whose keys are all masked (max logit
+// < -1e8) gets LSE = +inf, so P = 0 and every gradient of its rows is 0 (its forward writes 0).
+// Under the stock eager rule (the dense entry point with zero_masked_rows = 0) such a row is
+// an ordinary row: its -1e9-shifted logits round to one value, P is uniform, and the
+// gradients are the softmax Jacobian's at that point, as autograd of the eager path gives;
+// only a row with no finite logit is dead there. Such a row's logits sit near -1.44e9 (log2
+// units), where fp32 values are 128 apart, so its log-sum-exp cannot be stored there: under
+// the eager rule every logit is formed at full magnitude (so it rounds exactly as the eager
+// path's does) and then shifted by its line's offset, the line's largest key mask when that
+// is below the dead threshold (0 otherwise), which keeps every statistic small.
 //
 // Kernels, all on 32x32 MFMA tiles with D = 32:
 //   attn_bwd_relayout: K, Q, dO, V copied once into MFMA fragment order, as themselves and
@@ -45,8 +53,10 @@ constexpr int kNT = 256;           // four waves
 constexpr int kLines = 4;          // lines of one (b, h) per block: they share the bias tile
 constexpr int kSubDq = 1;          // 32-query sub-tiles per wave in the dQ kernel
 constexpr int kSubKv = 1;          // 32-key sub-tiles per wave in the dK / dV kernel
-// Zero masked-row rule threshold in log2 units (the reference tests t < -1e8).
+// Dead-row threshold in log2 units: the zero masked-row rule (the reference tests t < -1e8),
+// and the eager rule (only rows without a finite logit).
 constexpr float kDeadLog2 = -1.0e8f * kLog2e;
+constexpr float kDeadEager = -3.402823466e38f;
 
 // Element strides of one [B][S][H][N][D] operand view (D contiguous): batch item, line, head
 // and key (row); a dense operand has {S H N D, H N D, N D, D}.
@@ -179,6 +189,18 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restr
   }
 }
 
+// Per-line logit offset of the eager masked-row rule: the line's largest key mask (log2
+// units) when it is below the dead threshold, else 0. One 64-lane block per line.
+__global__ __launch_bounds__(64) void attn_bwd_lineoff_kernel(const float* __restrict__ mask2, float* __restrict__ off,
+                                                             int N, int Np, float dead_below) {
+  const float* m = mask2 + (size_t)blockIdx.x * Np;
+  float mx = -INFINITY;
+  for (int k = threadIdx.x; k < N; k += 64) mx = fmaxf(mx, m[k]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (threadIdx.x == 0) off[blockIdx.x] = (mx < dead_below && mx > -INFINITY) ? mx : 0.f;
+}
+
 // Logit in log2 units from the raw product s (times scale log2 e), the bias and the mask
 // (both already times log2 e); every kernel forms it the same way.
 PF_DEVICE float logit2(float s, float sl2, float b2, float m2) { return fmaf(s, sl2, b2 + m2); }
@@ -219,7 +241,7 @@ PF_DEVICE float frag_dot(const f32x4& a, const f32x4& b) {
   return s;
 }
 
-template <class TC, int kSub, bool kLse>
+template <class TC, int kSub, bool kLse, bool kOff>
 __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kernel(const TC* __restrict__ QR, const TC* __restrict__ KR,
                                                              const TC* __restrict__ VR, const TC* __restrict__ OR,
                                                              const TC* __restrict__ V, const TC* __restrict__ KT,
@@ -227,7 +249,8 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
                                                              const float* __restrict__ bias2, int S, int H, int N,
                                                              int Np, float scale, TC* __restrict__ dQ,
                                                              f32x4* __restrict__ st4, Strides4 sx, Strides4 sg,
-                                                             const float* __restrict__ lse_in) {
+                                                             const float* __restrict__ lse_in, float dead_below,
+                                                             const float* __restrict__ lineoff) {
   using M = Mfma<TC>;
   constexpr int STEPS = kBD / M::K32;
   constexpr int kRows = 32 * kSub;
@@ -248,6 +271,7 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
   const long bs = (long)b * S + sl;
   const size_t line = (size_t)bs * H + hd;
   const TC* Vl = V + line_offset(sx, b, sl, hd);
+  const float off = kOff ? lineoff[bs] : 0.f;  // eager rule: this line's logit offset
   // line whose key mask thread t < 128 stages (the four lines of the group, clamped)
   const float* m2s = mask2 + ((long)b * S + min((int)blockIdx.y * kLines + (int)(threadIdx.x >> 5), S - 1)) * Np;
   const float* b2l = bias2 + (size_t)bh * Np * Np;
@@ -304,7 +328,10 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
       const f32x4 b4 = *reinterpret_cast<const f32x4*>(brow + 8 * j + 4 * hh);
       const f32x4 m4 = *reinterpret_cast<const f32x4*>(mrow2 + 8 * j + 4 * hh);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[4 * j + e] = logit2(sa[4 * j + e], sl2, b4[e], m4[e]);
+      for (int e = 0; e < 4; ++e) {
+        x[4 * j + e] = logit2(sa[4 * j + e], sl2, b4[e], m4[e]);
+        if constexpr (kOff) x[4 * j + e] -= off;
+      }
     }
   };
 
@@ -317,7 +344,7 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
     for (int sub = 0; sub < kSub; ++sub) {
       const int q = q0 + 32 * sub + c;
       const float lf = q < N ? lse_in[line * Np + q] : INFINITY;
-      dead[sub] = !(lf >= kDeadLog2 && lf < INFINITY);
+      dead[sub] = !(lf >= dead_below && lf < INFINITY);
       mrow[sub] = dead[sub] ? INFINITY : lf;
       ref[sub] = 0.f;
       imax[sub] = -1;
@@ -385,7 +412,7 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
         run_max[sub] = om;
         imx[sub] = oi;
       }
-      const bool live = run_max[sub] >= kDeadLog2;
+      const bool live = run_max[sub] >= dead_below;
       dead[sub] = !live || q0 + 32 * sub + c >= N;
       mrow[sub] = live ? run_max[sub] : 0.f;
       imax[sub] = dead[sub] ? -1 : imx[sub];
@@ -522,12 +549,12 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dq_kern
 // of the current ones as soon as S and dP are issued, and the Q^T / dO^T fragments of the
 // current tile at the same point: both loads are covered by the tile's softmax work, and no
 // register copies between tiles are needed.
-template <class TC, int kSub>
+template <class TC, int kSub, bool kOff>
 __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dkdv_kernel(
     const TC* __restrict__ QR, const TC* __restrict__ KR, const TC* __restrict__ VR, const TC* __restrict__ OR,
     const TC* __restrict__ QT, const TC* __restrict__ OT, const float* __restrict__ mask2,
     const float* __restrict__ bias2, int S, int H, int N, int Np, float scale, const f32x4* __restrict__ st4,
-    TC* __restrict__ dK, TC* __restrict__ dV, Strides4 sg) {
+    TC* __restrict__ dK, TC* __restrict__ dV, Strides4 sg, const float* __restrict__ lineoff) {
   using M = Mfma<TC>;
   constexpr int STEPS = kBD / M::K32;
   constexpr int EPS = 16 / STEPS;  // accumulator elements per B fragment step
@@ -549,6 +576,7 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dkdv_ke
   const long bs = (long)b * S + sl;
   const size_t line = (size_t)bs * H + hd;
   const long lo = line_offset(sg, b, sl, hd);  // this line's dK / dV rows
+  const float off = kOff ? lineoff[bs] : 0.f;  // eager rule: this line's logit offset
   const float* b2l = bias2 + (size_t)bh * Np * Np;
   const int kb0 = blockIdx.x * kRows;
   const float sl2 = scale * kLog2e;
@@ -646,7 +674,9 @@ __global__ __launch_bounds__(kNT, sizeof(TC) == 2 ? 3 : 2) void attn_bwd_dkdv_ke
             for (int e = 0; e < 4; ++e) {
               const int r = 4 * j + e;
               const f32x4 st = sst[8 * j + 4 * hh + e];  // {lse2, ref, cen, imax}
-              const float pv = __builtin_amdgcn_exp2f(logit2(sa[sub][r], sl2, b4[e], mk2[sub]) - st[0]);
+              float x = logit2(sa[sub][r], sl2, b4[e], mk2[sub]);
+              if constexpr (kOff) x -= off;
+              const float pv = __builtin_amdgcn_exp2f(x - st[0]);
               const float u = (key[sub] == __float_as_int(st[3])) ? 0.f : dp[sub][r] - st[1];
               p[r] = pv;
               ds[r] = pv * (u - st[2]);
@@ -689,15 +719,17 @@ struct DbOps {
       o[kBD / Mfma<TC>::K32];
   f32x4 st;
   f32x4 m[4];
+  float off;
 };
 
-template <class TC>
+template <class TC, bool kOff>
 __global__ __launch_bounds__(kNT, 3) void attn_bwd_db_kernel(const TC* __restrict__ QR, const TC* __restrict__ KR,
                                                           const TC* __restrict__ VR, const TC* __restrict__ OR,
                                                           const float* __restrict__ mask2,
                                                           const float* __restrict__ bias2, int S, int H, int N,
                                                           int Np, float scale, int groups,
-                                                          const f32x4* __restrict__ st4, float* __restrict__ dbias) {
+                                                          const f32x4* __restrict__ st4, float* __restrict__ dbias,
+                                                          const float* __restrict__ lineoff) {
   using M = Mfma<TC>;
   constexpr int STEPS = kBD / M::K32;
   const int bh = blockIdx.z / groups;
@@ -728,6 +760,7 @@ __global__ __launch_bounds__(kNT, 3) void attn_bwd_db_kernel(const TC* __restric
       op.o[t] = M::load(OR + frag_offset<TC>(line, Np, q / 32, t, l));
     }
     op.st = st4[line * Np + q];
+    op.off = kOff ? lineoff[bs] : 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) op.m[j] = *reinterpret_cast<const f32x4*>(mask2 + bs * Np + k0 + 8 * j + 4 * hh);
   };
@@ -750,7 +783,9 @@ __global__ __launch_bounds__(kNT, 3) void attn_bwd_db_kernel(const TC* __restric
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * j + e;
           const int key = k0 + 8 * j + 4 * hh + e;
-          const float pv = __builtin_amdgcn_exp2f(logit2(sa[r], sl2, b4[j][e], cur.m[j][e]) - cur.st[0]);
+          float x = logit2(sa[r], sl2, b4[j][e], cur.m[j][e]);
+          if constexpr (kOff) x -= cur.off;
+          const float pv = __builtin_amdgcn_exp2f(x - cur.st[0]);
           const float u = key == im ? 0.f : dp[r] - cur.st[1];
           acc[r] += pv * (u - cur.st[2]);
         }
@@ -786,7 +821,7 @@ int db_groups(int B, int H, int N, int S) {
 }
 
 struct BwdWs {
-  size_t st, bias2, mask2, kr, qr, orr, vr, kt, qt, ot, part, total;
+  size_t st, bias2, mask2, off, kr, qr, orr, vr, kt, qt, ot, part, total;
   int groups;
 };
 
@@ -804,6 +839,7 @@ BwdWs bwd_ws_layout(int B, int S, int H, int N, int es) {
   w.st = take(lines * Np * 16);
   w.bias2 = take((size_t)B * H * Np * Np * 4);
   w.mask2 = take((size_t)B * S * Np * 4);
+  w.off = take((size_t)B * S * 4);
   w.kr = take(lines * kBD * Np * es);
   w.qr = take(lines * kBD * Np * es);
   w.orr = take(lines * kBD * Np * es);
@@ -820,12 +856,13 @@ template <class TC>
 int attn_bwd_launch(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias,
                     const void* dout, int B, int S, int H, int N, float scale, void* dq, void* dk, void* dv,
                     float* dbias, void* ws, hipStream_t s, const Strides4& sx, const Strides4& sdo,
-                    const Strides4& sg, const float* lse_in) {
+                    const Strides4& sg, const float* lse_in, bool zero_rows) {
   const BwdWs lay = bwd_ws_layout(B, S, H, N, (int)sizeof(TC));
   char* base = static_cast<char*>(ws);
   f32x4* st4 = reinterpret_cast<f32x4*>(base + lay.st);
   float* bias2 = reinterpret_cast<float*>(base + lay.bias2);
   float* mask2 = reinterpret_cast<float*>(base + lay.mask2);
+  float* lineoff = reinterpret_cast<float*>(base + lay.off);
   TC* KR = reinterpret_cast<TC*>(base + lay.kr);
   TC* QR = reinterpret_cast<TC*>(base + lay.qr);
   TC* OR = reinterpret_cast<TC*>(base + lay.orr);
@@ -848,21 +885,46 @@ int attn_bwd_launch(const void* q, const void* k, const void* v, const float* re
   if (int e = pf::check_launch("attn_bwd_relayout")) return e;
   const unsigned lg = (unsigned)((S + kLines - 1) / kLines);
   const dim3 gdq((unsigned)(Np / (32 * kSubDq)), lg, (unsigned)(B * H));
+  // The eager rule shifts each line's logits by its offset (the saved-LSE path is zero-rule only).
+  const bool eager = !zero_rows;
+  if (eager) {
+    attn_bwd_lineoff_kernel<<<(unsigned)(B * S), 64, 0, s>>>(mask2, lineoff, N, Np, kDeadLog2);
+    if (int e = pf::check_launch("attn_bwd_lineoff")) return e;
+  }
+  const float dead_below = zero_rows ? kDeadLog2 : kDeadEager;
   if (lse_in)
-    attn_bwd_dq_kernel<TC, kSubDq, true><<<gdq, kNT, 0, s>>>(QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N, Np, scale,
-                                                            static_cast<TC*>(dq), st4, sx, sg, lse_in);
+    attn_bwd_dq_kernel<TC, kSubDq, true, false><<<gdq, kNT, 0, s>>>(QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N,
+                                                                    Np, scale, static_cast<TC*>(dq), st4, sx, sg,
+                                                                    lse_in, dead_below, nullptr);
+  else if (eager)
+    attn_bwd_dq_kernel<TC, kSubDq, false, true><<<gdq, kNT, 0, s>>>(QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N,
+                                                                    Np, scale, static_cast<TC*>(dq), st4, sx, sg,
+                                                                    nullptr, dead_below, lineoff);
   else
-    attn_bwd_dq_kernel<TC, kSubDq, false><<<gdq, kNT, 0, s>>>(QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N, Np, scale,
-                                                             static_cast<TC*>(dq), st4, sx, sg, nullptr);
+    attn_bwd_dq_kernel<TC, kSubDq, false, false><<<gdq, kNT, 0, s>>>(QR, KR, VR, OR, V, KT, mask2, bias2, S, H, N,
+                                                                     Np, scale, static_cast<TC*>(dq), st4, sx, sg,
+                                                                     nullptr, dead_below, nullptr);
   if (int e = pf::check_launch("attn_bwd_dq")) return e;
-  attn_bwd_dkdv_kernel<TC, kSubKv><<<dim3((unsigned)(Np / (32 * kSubKv)), lg, (unsigned)(B * H)), kNT, 0, s>>>(
-      QR, KR, VR, OR, QT, OT, mask2, bias2, S, H, N, Np, scale, st4, static_cast<TC*>(dk), static_cast<TC*>(dv), sg);
+  const dim3 gkv((unsigned)(Np / (32 * kSubKv)), lg, (unsigned)(B * H));
+  if (eager)
+    attn_bwd_dkdv_kernel<TC, kSubKv, true><<<gkv, kNT, 0, s>>>(QR, KR, VR, OR, QT, OT, mask2, bias2, S, H, N, Np,
+                                                               scale, st4, static_cast<TC*>(dk),
+                                                               static_cast<TC*>(dv), sg, lineoff);
+  else
+    attn_bwd_dkdv_kernel<TC, kSubKv, false><<<gkv, kNT, 0, s>>>(QR, KR, VR, OR, QT, OT, mask2, bias2, S, H, N, Np,
+                                                                scale, st4, static_cast<TC*>(dk),
+                                                                static_cast<TC*>(dv), sg, nullptr);
   if (int e = pf::check_launch("attn_bwd_dkdv")) return e;
   const unsigned nb = (unsigned)((N + 63) / 64);
   const int G = lay.groups;
   float* part = G > 1 ? reinterpret_cast<float*>(base + lay.part) : dbias;
-  attn_bwd_db_kernel<TC><<<dim3(nb, nb, (unsigned)(B * H * G)), kNT, 0, s>>>(QR, KR, VR, OR, mask2, bias2, S, H, N,
-                                                                             Np, scale, G, st4, part);
+  const dim3 gdb(nb, nb, (unsigned)(B * H * G));
+  if (eager)
+    attn_bwd_db_kernel<TC, true><<<gdb, kNT, 0, s>>>(QR, KR, VR, OR, mask2, bias2, S, H, N, Np, scale, G, st4, part,
+                                                     lineoff);
+  else
+    attn_bwd_db_kernel<TC, false><<<gdb, kNT, 0, s>>>(QR, KR, VR, OR, mask2, bias2, S, H, N, Np, scale, G, st4, part,
+                                                      nullptr);
   if (int e = pf::check_launch("attn_bwd_db")) return e;
   if (G > 1) {
     const size_t n = (size_t)B * H * N * N;
@@ -877,7 +939,7 @@ int evo_attn_bwd_any(const char* fn, const void* q, const void* k, const void* v
                      const float* pair_bias, const void* dout, int B, int S, int H, int N, int D, int dtype,
                      float softmax_scale, void* dq, void* dk, void* dv, float* dpair_bias, void* workspace,
                      size_t workspace_bytes, void* stream, const Strides4& sx, const Strides4& sdo,
-                     const Strides4& sg, const float* lse_in) {
+                     const Strides4& sg, const float* lse_in, bool zero_rows) {
   PF_REQUIRE(q && k && v && res_mask && pair_bias && dout && dq && dk && dv && dpair_bias && workspace,
              PF_ERR_INVALID_ARG, "%s: null pointer", fn);
   PF_REQUIRE(B > 0 && S > 0 && H > 0 && N > 0, PF_ERR_INVALID_ARG, "%s: B=%d S=%d H=%d N=%d", fn, B, S, H, N);
@@ -885,6 +947,8 @@ int evo_attn_bwd_any(const char* fn, const void* q, const void* k, const void* v
              "%s: B*S*H=%ld N=%d too large (grid rows are the B*S*H lines)", fn, (long)B * S * H, N);
   PF_REQUIRE(D == kBD, PF_ERR_UNSUPPORTED, "%s: D=%d (built: D=32)", fn, D);
   PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "%s: dtype %d", fn, dtype);
+  PF_REQUIRE(zero_rows || !lse_in, PF_ERR_UNSUPPORTED, "%s: the saved-LSE backward follows the zero masked-row rule",
+             fn);
   const long vec = dtype == PF_F32 ? 4 : 8;  // elements per 16 bytes
   for (const Strides4* st : {&sx, &sdo, &sg})
     PF_REQUIRE(st->b % vec == 0 && st->s % vec == 0 && st->h % vec == 0 && st->n % vec == 0 && st->n >= kBD,
@@ -897,9 +961,9 @@ int evo_attn_bwd_any(const char* fn, const void* q, const void* k, const void* v
   hipStream_t s = pf::as_stream(stream);
   if (dtype == PF_F32)
     return attn_bwd_launch<float>(q, k, v, res_mask, pair_bias, dout, B, S, H, N, softmax_scale, dq, dk, dv,
-                                  dpair_bias, workspace, s, sx, sdo, sg, lse_in);
+                                  dpair_bias, workspace, s, sx, sdo, sg, lse_in, zero_rows);
   return attn_bwd_launch<bf16>(q, k, v, res_mask, pair_bias, dout, B, S, H, N, softmax_scale, dq, dk, dv, dpair_bias,
-                               workspace, s, sx, sdo, sg, lse_in);
+                               workspace, s, sx, sdo, sg, lse_in, zero_rows);
 }
 
 }  // namespace
@@ -912,11 +976,13 @@ size_t pf_evo_attn_bwd_workspace_bytes(int B, int S, int H, int N, int D, int dt
 }
 
 int pf_evo_attn_bwd(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias,
-                    const void* dout, int B, int S, int H, int N, int D, int dtype, float softmax_scale, void* dq,
-                    void* dk, void* dv, float* dpair_bias, void* workspace, size_t workspace_bytes, void* stream) {
+                    const void* dout, int B, int S, int H, int N, int D, int dtype, float softmax_scale,
+                    int zero_masked_rows, void* dq, void* dk, void* dv, float* dpair_bias, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   const Strides4 dense{(long)S * H * N * D, (long)H * N * D, (long)N * D, D};
   return evo_attn_bwd_any("pf_evo_attn_bwd", q, k, v, res_mask, pair_bias, dout, B, S, H, N, D, dtype, softmax_scale,
-                          dq, dk, dv, dpair_bias, workspace, workspace_bytes, stream, dense, dense, dense, nullptr);
+                          dq, dk, dv, dpair_bias, workspace, workspace_bytes, stream, dense, dense, dense, nullptr,
+                          zero_masked_rows != 0);
 }
 
 int pf_evo_attn_bwd_strided(const void* q, const void* k, const void* v, const long* qkv_strides,
@@ -931,7 +997,7 @@ int pf_evo_attn_bwd_strided(const void* q, const void* k, const void* v, const l
   const Strides4 sg{grad_strides[0], grad_strides[1], grad_strides[2], grad_strides[3]};
   return evo_attn_bwd_any("pf_evo_attn_bwd_strided", q, k, v, res_mask, pair_bias, dout, B, S, H, N, D, dtype,
                           softmax_scale, dq, dk, dv, dpair_bias, workspace, workspace_bytes, stream, sx, sdo, sg,
-                          lse);
+                          lse, true);
 }
 
 }  // extern "C"

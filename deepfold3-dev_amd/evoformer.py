@@ -2,12 +2,14 @@
 
 ``PairFormerBlock`` keeps the reference's constructor arguments, submodule names
 (so state dicts load unchanged) and ``forward(pair, single, pair_mask, seq_mask)``
-signature (``src/deepfold3/model/evoformer.py:178-355``). Eval-mode semantics: the
-branch scaler is the identity, ``residual_out_scale`` and the transitions' residual gains
-are folded into each branch's output projection, and dropout-add is a plain add
-(``triton/dropout_add.py:236-237``), so every residual add is fused into the epilogue of
-the kernel that produces the branch. ``single_to_pair`` is fused into the
-pair transition's epilogue (it normalises the updated pair rows).
+signature (``src/deepfold3/model/evoformer.py:178-355``). The branch scaler is the identity;
+``residual_out_scale`` and the transitions' residual gains are folded into each branch's
+output projection. In eval mode dropout-add is a plain add (``triton/dropout_add.py:236-237``),
+so every residual add is fused into the epilogue of the kernel that produces the branch; in
+training mode the four dropped pair branches (triangle multiplications and attention) add
+through the HIP shared-mask dropout-add (``csrc/dropout.hip``), with grad or without.
+``single_to_pair`` is fused into the pair transition's epilogue (it normalises the updated
+pair rows).
 
 ``PairFormerStack`` is the trunk loop (``evoformer.py:593-601``): it copies the inputs
 once and then updates them in place, block after block.
@@ -15,20 +17,44 @@ once and then updates them in place, block after block.
 
 from __future__ import annotations
 
+from functools import partial
+
 import torch
 import torch.nn as nn
+from torch.utils.checkpoint import checkpoint as _torch_checkpoint
 
 from . import kernel_census
 from .attention import GridSelfAttention, SingleAttention
 from .config import OptimConfig, require_hip
 from .inference_guard import NotActive, inference_only
-from .kernels import gemm_dtype_for, single_to_pair
+from .kernels import (
+    DropoutAddFunction,
+    dropout_add,
+    gemm_dtype_for,
+    next_dropout_seed,
+    single_to_pair,
+)
 from .ops import TriangleMulIncoming, TriangleMulOutgoing
 from .primitives import LayerNorm, LinearNoBias, WeightCache, f32, make_transition_block
 
+# Per-block activation checkpointing as the reference's trunk loop (``evoformer.py:58``).
+_checkpoint = partial(_torch_checkpoint, use_reentrant=False, determinism_check="none")
+
+
+def _dropout_residual_(module, pair: torch.Tensor, mask: torch.Tensor, p: float, rowwise: bool) -> None:
+    """``pair += dropout(module.branch(pair, mask))`` in place: the eval-mode fused residual
+    epilogue when ``p == 0``, else the branch out of place and the HIP shared-mask dropout-add
+    (``dropout_add.py:221-265``) writing back into ``pair``."""
+    if p > 0.0:
+        dropout_add(pair, module.branch(pair, mask), p, rowwise, next_dropout_seed(), out=pair)
+    else:
+        module.forward_residual_(pair, mask)
+
 
 class PairFormerBlock(nn.Module):
-    """One PairFormer layer with the single track (AF3 ``PairFormerIteration``)."""
+    """One PairFormer layer (AF3 ``PairFormerIteration``), with the single track unless
+    ``use_single_track=False`` and with triangle attention unless ``use_triangle_attention=False``
+    (the reference's deletable branches, ``evoformer.py:226-236``, ``:302-321``, ``:353``)."""
 
     def __init__(
         self,
@@ -55,29 +81,32 @@ class PairFormerBlock(nn.Module):
         require_hip("PairFormerBlock", optim)
         if branch_scaler != "identity":
             raise NotActive("PairFormerBlock", f"branch_scaler={branch_scaler!r}: only the identity scaler is built")
-        if not use_triangle_attention or not use_single_track:
-            raise NotActive("PairFormerBlock", "the triangle-attention and single-track branches are always built")
         tk = trimul_kwargs or {}
         self.tri_mul_out = TriangleMulOutgoing(c_pair, optim=optim, **tk)
         self.tri_mul_in = TriangleMulIncoming(c_pair, optim=optim, **tk)
-        self.use_triangle_attention = True
-        self.pair_attn_row = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=False, optim=optim)
-        self.pair_attn_col = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=True, optim=optim)
+        self.use_triangle_attention = bool(use_triangle_attention)
+        if self.use_triangle_attention:
+            self.pair_attn_row = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=False, optim=optim)
+            self.pair_attn_col = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=True, optim=optim)
         self.pair_transition = make_transition_block(c_pair, config=optim)
-        self.use_single_track = True
-        self.single_to_pair_norm = LayerNorm(c_pair)
-        self.single_to_pair = LinearNoBias(c_pair, num_single_heads)
-        self.single_attn = SingleAttention(
-            c_single, num_heads=num_single_heads, key_dim=single_key_dim, value_dim=single_value_dim, optim=optim,
-            pair_bias_gate=pair_bias_gate, pair_bias_gate_init_tau=pair_bias_gate_init_tau,
-        )  # fmt: skip
-        self.single_transition = make_transition_block(
-            c_single, config=optim, linear_out_init_gain=single_transition_linear_out_init_gain
-        )
+        # The single track reads the pair representation through the pair logits and never
+        # writes back, so deleting it leaves the pair update unchanged.
+        self.use_single_track = bool(use_single_track)
+        if self.use_single_track:
+            self.single_to_pair_norm = LayerNorm(c_pair)
+            self.single_to_pair = LinearNoBias(c_pair, num_single_heads)
+            self.single_attn = SingleAttention(
+                c_single, num_heads=num_single_heads, key_dim=single_key_dim, value_dim=single_value_dim,
+                optim=optim, pair_bias_gate=pair_bias_gate, pair_bias_gate_init_tau=pair_bias_gate_init_tau,
+            )  # fmt: skip
+            self.single_transition = make_transition_block(
+                c_single, config=optim, linear_out_init_gain=single_transition_linear_out_init_gain
+            )
         # Residual scales (evoformer.py:207-217, applied at :282-353): every branch's output
         # is multiplied by s_ros, the two transitions' also by their residual gain (None = 1).
-        # Each branch ends in a bias-free output projection, so the scale is folded into
-        # that weight when its operands are prepared.
+        # Each branch ends in a bias-free output projection, so inside the block the scale is
+        # folded into that weight (each branch module's ``branch`` / ``forward_residual_``);
+        # the modules' own ``forward`` stays unscaled, as in the reference.
         self.residual_out_scale = float(residual_out_scale)
         self.single_transition_residual_gain = (
             1.0 if single_transition_residual_gain is None else float(single_transition_residual_gain)
@@ -87,12 +116,31 @@ class PairFormerBlock(nn.Module):
         )
         self.branch_scaler_kind = "identity"
         s_ros = self.residual_out_scale
-        for m in (self.tri_mul_out, self.tri_mul_in, self.pair_attn_row, self.pair_attn_col, self.single_attn):
+        for m in self._pair_branches() + ([self.single_attn] if self.use_single_track else []):
             m.branch_scale = s_ros
         self.pair_transition.branch_scale = s_ros * self.pair_transition_residual_gain
-        self.single_transition.branch_scale = s_ros * self.single_transition_residual_gain
+        if self.use_single_track:
+            self.single_transition.branch_scale = s_ros * self.single_transition_residual_gain
         self.pair_dropout = pair_dropout
         self._s2p_cache = WeightCache()
+
+    def _pair_branches(self) -> list:
+        """The pair branches that take dropout, in block order."""
+        mods = [self.tri_mul_out, self.tri_mul_in]
+        if self.use_triangle_attention:
+            mods += [self.pair_attn_row, self.pair_attn_col]
+        return mods
+
+    def _dropout_sites(self) -> list:
+        """(module, rowwise) of every dropout-add, in the reference's order (``evoformer.py:289-310``)."""
+        sites = [(self.tri_mul_out, True), (self.tri_mul_in, True)]
+        if self.use_triangle_attention:
+            sites += [(self.pair_attn_row, True), (self.pair_attn_col, False)]
+        return sites
+
+    def dropout_p(self) -> float:
+        """The pair dropout rate in effect: ``pair_dropout`` in training mode, else 0."""
+        return float(self.pair_dropout) if self.training else 0.0
 
     def _s2p_operands(self, cdt: torch.dtype):
         from .kernels import cast_weight
@@ -111,24 +159,28 @@ class PairFormerBlock(nn.Module):
     def forward_(
         self, pair: torch.Tensor, single: torch.Tensor, pair_mask: torch.Tensor, seq_mask: torch.Tensor
     ) -> tuple[torch.Tensor, torch.Tensor]:
-        """In-place block update of contiguous ``pair`` [B, N, N, C] and ``single`` [B, N, Cs]."""
-        if self.training:
-            raise NotActive("PairFormerBlock", "training-mode dropout is not built (eval only)")
-        kernel_census.record("PairFormerBlock", "hip_block")
+        """In-place block update of contiguous ``pair`` [B, N, N, C] and ``single`` [B, N, Cs]
+        (training mode: the shared-mask dropout on the four dropped pair branches)."""
+        kernel_census.record("PairFormerBlock", "hip_block_train" if self.dropout_p() > 0 else "hip_block")
         pair_logits = self.pair_forward_(pair, pair_mask)
-        self.single_forward_(single, seq_mask, pair_logits)
+        if self.use_single_track:
+            self.single_forward_(single, seq_mask, pair_logits)
         return pair, single
 
-    def pair_forward_(self, pair: torch.Tensor, pair_mask: torch.Tensor) -> torch.Tensor:
-        """The pair half of the block, in place; returns the single track's pair logits.
+    def pair_forward_(self, pair: torch.Tensor, pair_mask: torch.Tensor) -> torch.Tensor | None:
+        """The pair half of the block, in place; returns the single track's pair logits (None
+        without the single track).
 
         The pair update reads only the pair representation (``evoformer.py:289-321``), so it
-        does not depend on the single half of the block.
-        """
-        self.tri_mul_out.forward_residual_(pair, pair_mask)
-        self.tri_mul_in.forward_residual_(pair, pair_mask)
-        self.pair_attn_row.forward_residual_(pair, pair_mask)
-        self.pair_attn_col.forward_residual_(pair, pair_mask)
+        does not depend on the single half of the block. In training mode the four dropped
+        branches run out of place and their shared-mask dropout-add writes into ``pair``; the
+        masks' seeds are drawn in branch order (``kernels.next_dropout_seed``)."""
+        p = self.dropout_p()
+        for m, rowwise in self._dropout_sites():
+            _dropout_residual_(m, pair, pair_mask, p, rowwise)
+        if not self.use_single_track:
+            self.pair_transition.forward_residual_(pair)
+            return None
         if self.pair_transition.fused_pair:
             s2p = self._s2p_operands(gemm_dtype_for(pair))
             _, pair_logits = self.pair_transition.forward_residual_(pair, s2p=s2p)
@@ -146,29 +198,34 @@ class PairFormerBlock(nn.Module):
     def forward_grad(
         self, pair: torch.Tensor, single: torch.Tensor, pair_mask: torch.Tensor, seq_mask: torch.Tensor
     ) -> tuple[torch.Tensor, torch.Tensor]:
-        """The block out of place and differentiable (``evoformer.py:270-355``, eval dropout):
-        each branch's training path (triangle multiplications and attention, transitions and
-        single attention on the HIP kernels with their backward), residual adds in autograd,
-        every residual scale folded into its branch's output projection."""
+        """The block out of place and differentiable (``evoformer.py:270-355``): each branch's
+        training path (triangle multiplications and attention, transitions and single attention
+        on the HIP kernels with their backward), every residual scale folded into its branch's
+        output projection, the residual adds in autograd; in training mode the four dropped pair
+        branches add through the HIP shared-mask dropout-add (``DropoutAddFunction``; seeds drawn
+        in branch order, so ``torch.utils.checkpoint``'s recompute regenerates the same masks)."""
         from .kernels import layer_norm_for_gemm, token_linear
 
         kernel_census.record("PairFormerBlock", "hip_block_grad")
-        p = pair + self.tri_mul_out(pair, pair_mask)
-        p = p + self.tri_mul_in(p, pair_mask)
-        p = p + self.pair_attn_row(p, pair_mask)
-        p = p + self.pair_attn_col(p, pair_mask)
-        p = p + self.pair_transition(p)
+        p_drop = self.dropout_p()
+        p = pair
+        for m, rowwise in self._dropout_sites():
+            upd = m.branch(p, pair_mask)
+            p = DropoutAddFunction.apply(p, upd, p_drop, rowwise, next_dropout_seed()) if p_drop > 0 else p + upd
+        p = p + self.pair_transition.branch(p)
+        if not self.use_single_track:
+            return p, single
         n = self.single_to_pair_norm
         logits = token_linear(layer_norm_for_gemm(p, n.weight, n.bias, n.eps), self.single_to_pair.weight)
-        s = single + self.single_attn(single, seq_mask, logits.movedim(-1, -3))
-        s = s + self.single_transition(s)
+        s = single + self.single_attn.branch(single, seq_mask, logits.movedim(-1, -3))
+        s = s + self.single_transition.branch(s)
         return p, s
 
     def forward(
         self, pair: torch.Tensor, single: torch.Tensor, pair_mask: torch.Tensor, seq_mask: torch.Tensor
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """Reference signature (``evoformer.py:270-355``): returns new ``(pair, single)``; under
-        grad the differentiable path (``forward_grad``), else the in-place inference kernels."""
+        grad the differentiable path (``forward_grad``), else the in-place kernels on copies."""
         has_batch = pair.dim() == 4
         if not has_batch:
             pair, single = pair.unsqueeze(0), single.unsqueeze(0)
@@ -191,12 +248,15 @@ class PairFormerStack(nn.Module):
     ``layer_attr`` names the ModuleList in the state dict (``blocks`` here; the confidence
     head's stack uses the reference's ``layers``). ``layer_kwargs(i)``, when given, returns
     the constructor arguments that differ per layer (the reference's per-layer residual
-    scales, ``evoformer.py:459-489``); they override ``block_kwargs``."""
+    scales, ``evoformer.py:459-489``); they override ``block_kwargs``. With
+    ``optim.use_gradient_checkpointing`` each block runs under ``torch.utils.checkpoint``
+    (non-reentrant) when autograd is recording, as at ``evoformer.py:58``, ``:593-596``."""
 
     def __init__(self, num_blocks: int, c_pair: int = 128, c_single: int = 384, optim: OptimConfig | None = None,
                  layer_attr: str = "blocks", layer_kwargs=None, **block_kwargs):  # fmt: skip
         super().__init__()
         self._layer_attr = layer_attr
+        self.use_gradient_checkpointing = bool(optim is not None and optim.use_gradient_checkpointing)
 
         def block(i: int) -> PairFormerBlock:
             kw = dict(block_kwargs)
@@ -218,11 +278,14 @@ class PairFormerStack(nn.Module):
         reads the single representation, and the single half of block i needs only block i's
         pair logits (an event orders it after them) and block i - 1's single half (same
         stream). The streams join before returning. Under grad the blocks' differentiable
-        path runs in order on one stream."""
+        path runs in order on one stream, each block checkpointed when the optim config asks."""
         if torch.is_grad_enabled():
             pair_mask = pair_mask.to(torch.float32)
             for blk in self.blocks:
-                pair, single = blk.forward_grad(pair, single, pair_mask, seq_mask)
+                if self.use_gradient_checkpointing:
+                    pair, single = _checkpoint(blk.forward_grad, pair, single, pair_mask, seq_mask)
+                else:
+                    pair, single = blk.forward_grad(pair, single, pair_mask, seq_mask)
             return pair, single
         pair = pair.contiguous().clone()
         single = single.contiguous().clone()
@@ -237,8 +300,10 @@ class PairFormerStack(nn.Module):
         side = self._side_stream(pair.device)
         side.wait_stream(main)  # single, masks and the clones above
         for blk in self.blocks:
-            kernel_census.record("PairFormerBlock", "hip_block")
+            kernel_census.record("PairFormerBlock", "hip_block_train" if blk.dropout_p() > 0 else "hip_block")
             pair_logits = blk.pair_forward_(pair, pair_mask)
+            if not blk.use_single_track:
+                continue
             done = torch.cuda.Event()
             done.record(main)
             side.wait_event(done)
@@ -307,14 +372,14 @@ class TemplatePairFormerBlock(nn.Module):
             m.branch_scale = self.residual_out_scale
 
     def forward_(self, pair: torch.Tensor, pair_mask: torch.Tensor) -> torch.Tensor:
-        """In place: ``pair`` [B, N, N, C] contiguous (``template_embedding.py:230-240``, eval)."""
-        if self.training and self.pair_dropout > 0.0:
-            raise NotActive("TemplatePairFormerBlock", "training-mode dropout is not built (eval only)")
-        kernel_census.record("TemplatePairFormerBlock", "hip_block")
-        self.tri_mul_out.forward_residual_(pair, pair_mask)
-        self.tri_mul_in.forward_residual_(pair, pair_mask)
-        self.pair_attn_row.forward_residual_(pair, pair_mask)
-        self.pair_attn_col.forward_residual_(pair, pair_mask)
+        """In place: ``pair`` [B, N, N, C] contiguous (``template_embedding.py:230-240``); in
+        training mode the shared-mask dropout-add on the four dropped branches."""
+        p = float(self.pair_dropout) if self.training else 0.0
+        kernel_census.record("TemplatePairFormerBlock", "hip_block_train" if p > 0 else "hip_block")
+        _dropout_residual_(self.tri_mul_out, pair, pair_mask, p, True)
+        _dropout_residual_(self.tri_mul_in, pair, pair_mask, p, True)
+        _dropout_residual_(self.pair_attn_row, pair, pair_mask, p, True)
+        _dropout_residual_(self.pair_attn_col, pair, pair_mask, p, False)
         self.pair_transition.forward_residual_(pair)
         return pair
 
@@ -446,40 +511,51 @@ class EvoformerBlock(nn.Module):
         from .ops import OuterProductMean
 
         require_hip("EvoformerBlock", optim)
-        if not use_triangle_attention:
-            raise NotActive("EvoformerBlock", "the triangle-attention branches are always built")
         tk = trimul_kwargs or {}
         self.row_attn = MSAAttention(c_msa, c_pair, num_heads=num_msa_heads, optim=optim)
         self.outer_product = OuterProductMean(c_msa, c_pair, c_hidden=outer_product_hidden, optim=optim)
         self.tri_mul_out = TriangleMulOutgoing(c_pair, optim=optim, **tk)
         self.tri_mul_in = TriangleMulIncoming(c_pair, optim=optim, **tk)
-        self.use_triangle_attention = True
-        self.pair_attn_row = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=False, optim=optim)
-        self.pair_attn_col = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=True, optim=optim)
+        self.use_triangle_attention = bool(use_triangle_attention)
+        if self.use_triangle_attention:
+            self.pair_attn_row = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=False, optim=optim)
+            self.pair_attn_col = GridSelfAttention(c_pair, num_heads=num_pair_heads, transpose=True, optim=optim)
         self.pair_transition = make_transition_block(c_pair, config=optim)
         self.msa_transition = make_transition_block(c_msa, config=optim)
         self.msa_dropout = msa_dropout
         self.pair_dropout = pair_dropout
         self.residual_out_scale = float(residual_out_scale)
-        for m in (self.row_attn, self.outer_product, self.tri_mul_out, self.tri_mul_in, self.pair_attn_row,
-                  self.pair_attn_col, self.pair_transition, self.msa_transition):  # fmt: skip
+        mods = [self.row_attn, self.outer_product, self.tri_mul_out, self.tri_mul_in, self.pair_transition,
+                self.msa_transition]  # fmt: skip
+        if self.use_triangle_attention:
+            mods += [self.pair_attn_row, self.pair_attn_col]
+        for m in mods:
             m.branch_scale = self.residual_out_scale
 
     @inference_only("EvoformerBlock")
     def forward_(
         self, msa: torch.Tensor, pair: torch.Tensor, msa_mask: torch.Tensor, pair_mask: torch.Tensor
     ) -> tuple[torch.Tensor, torch.Tensor]:
-        """In place on contiguous ``msa`` [B, S, N, c_msa] and ``pair`` [B, N, N, c_pair]."""
-        if self.training:
-            raise NotActive("EvoformerBlock", "training-mode dropout is not built (eval only)")
-        kernel_census.record("EvoformerBlock", "hip_block")
+        """In place on contiguous ``msa`` [B, S, N, c_msa] and ``pair`` [B, N, N, c_pair]; in
+        training mode the MSA update of ``row_attn`` takes the row-shared ``msa_dropout`` and the
+        pair branches the shared-mask ``pair_dropout`` (``evoformer.py:162-174``; seeds drawn in
+        that order)."""
+        train = self.training
+        p_msa = float(self.msa_dropout) if train else 0.0
+        p_pair = float(self.pair_dropout) if train else 0.0
+        kernel_census.record("EvoformerBlock", "hip_block_train" if max(p_msa, p_pair) > 0 else "hip_block")
         self.outer_product.forward_residual_(pair, msa, msa_mask)
-        self.row_attn.forward_residual_(msa, msa_mask, pair)
+        if p_msa > 0.0:
+            upd = self.row_attn.branch(msa, msa_mask, pair)
+            dropout_add(msa, upd, p_msa, True, next_dropout_seed(), out=msa)
+        else:
+            self.row_attn.forward_residual_(msa, msa_mask, pair)
         self.msa_transition.forward_residual_(msa)
-        self.tri_mul_out.forward_residual_(pair, pair_mask)
-        self.tri_mul_in.forward_residual_(pair, pair_mask)
-        self.pair_attn_row.forward_residual_(pair, pair_mask)
-        self.pair_attn_col.forward_residual_(pair, pair_mask)
+        _dropout_residual_(self.tri_mul_out, pair, pair_mask, p_pair, True)
+        _dropout_residual_(self.tri_mul_in, pair, pair_mask, p_pair, True)
+        if self.use_triangle_attention:
+            _dropout_residual_(self.pair_attn_row, pair, pair_mask, p_pair, True)
+            _dropout_residual_(self.pair_attn_col, pair, pair_mask, p_pair, False)
         self.pair_transition.forward_residual_(pair)
         return msa, pair
 

@@ -27,12 +27,15 @@ import torch.nn as nn
 from . import _lib, kernel_census
 from .inference_guard import NotActive
 from .kernels import (
+    DropoutAddFunction,
     LayerNormFunction,
     SwiGLUFunction,
     cast_weight,
+    dropout_add,
     gemm_dtype_for,
     layer_norm_for_gemm,
     ln_transpose,
+    next_dropout_seed,
     residual_add,
     token_linear,
 )
@@ -87,9 +90,10 @@ def _evo_fwd(Q, K, V, rm, pb, zero_rows: bool) -> torch.Tensor:
     return out
 
 
-def _evo_bwd(Q, K, V, rm, pb, dO):
+def _evo_bwd(Q, K, V, rm, pb, dO, zero_rows: bool = True):
     """Backward in the kernel layout (``pf_evo_attn_bwd``): returns dQ, dK, dV (Q's dtype) and
-    d_pair_bias ``[B,H,N,N]`` fp32."""
+    d_pair_bias ``[B,H,N,N]`` fp32. ``zero_rows`` selects the masked-row rule (True: the
+    reference kernel's, zero gradients; False: the eager path's uniform softmax)."""
     B, S, H, N, D = Q.shape
     code = _lib.dtype_code(Q.dtype)
     dO = dO.to(Q.dtype).contiguous()
@@ -101,26 +105,28 @@ def _evo_bwd(Q, K, V, rm, pb, dO):
     ws = _ws(ws_bytes, Q.device)
     _lib.call(
         "pf_evo_attn_bwd", Q.data_ptr(), K.data_ptr(), V.data_ptr(), rm.data_ptr(), pb.data_ptr(), dO.data_ptr(),
-        B, S, H, N, D, code, float(D) ** -0.5, dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(), dpb.data_ptr(),
-        ws.data_ptr(), ws_bytes, _lib.stream_of(Q),
+        B, S, H, N, D, code, float(D) ** -0.5, int(zero_rows), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(),
+        dpb.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(Q),
     )  # fmt: skip
     return dQ, dK, dV, dpb
 
 
 class _EvoAttnFunction(torch.autograd.Function):
-    """Kernel-layout attention with the HIP backward; the forward saves its inputs only."""
+    """Kernel-layout attention with the HIP backward; the forward saves its inputs only.
+    ``apply(Q, K, V, rm, pb, zero_rows)``: both passes follow the same masked-row rule."""
 
     @staticmethod
-    def forward(ctx, Q, K, V, rm, pb):
+    def forward(ctx, Q, K, V, rm, pb, zero_rows=True):
         ctx.save_for_backward(Q, K, V, rm, pb)
-        return _evo_fwd(Q, K, V, rm, pb, True)
+        ctx.zero_rows = bool(zero_rows)
+        return _evo_fwd(Q, K, V, rm, pb, ctx.zero_rows)
 
     @staticmethod
     def backward(ctx, dO):
         Q, K, V, rm, pb = ctx.saved_tensors
         kernel_census.record("evo_attention.backward", "hip_evo_attn_bwd")
-        dQ, dK, dV, dpb = _evo_bwd(Q, K, V, rm, pb, dO)
-        return dQ, dK, dV, None, dpb
+        dQ, dK, dV, dpb = _evo_bwd(Q, K, V, rm, pb, dO, ctx.zero_rows)
+        return dQ, dK, dV, None, dpb, None
 
 
 def _strides(*st: int) -> tuple:
@@ -224,8 +230,9 @@ class _EvoformerAttention:
 
     Differentiable in Q, K, V and pair_bias (``evo_attention.py:1295-1472``): under grad the
     backward runs ``pf_evo_attn_bwd`` (centred softmax Jacobian, row statistics recomputed,
-    nothing saved but the inputs). The backward implements the reference kernel's
-    masked-row rule, so training calls take ``masked_rows="zero"``.
+    nothing saved but the inputs) under the same masked-row rule as the forward: zero
+    gradients for a fully masked line (``"zero"``) or the uniform softmax's Jacobian
+    (``"eager"``, what autograd of the stock path gives).
     """
 
     @staticmethod
@@ -234,9 +241,6 @@ class _EvoformerAttention:
         if masked_rows not in ("zero", "eager"):
             raise ValueError(f"masked_rows must be 'zero' or 'eager', got {masked_rows!r}")
         grad = torch.is_grad_enabled() and any(t.requires_grad for t in (Q, K, V, pair_bias))
-        if grad and masked_rows != "zero":
-            raise NotActive("evo_attention", "the backward implements the reference kernel's masked-row rule; "
-                            "train with masked_rows='zero'")  # fmt: skip
         if not pre_transposed:
             Q, K, V = (t.transpose(-2, -3) for t in (Q, K, V))
         Q, K, V = (t.contiguous() for t in (Q, K, V))
@@ -249,7 +253,7 @@ class _EvoformerAttention:
         pb = pair_bias.to(torch.float32).expand(B, 1, H, N, N).reshape(B, H, N, N).contiguous()
         if grad:
             kernel_census.record("evo_attention", "hip_evo_attn_grad")
-            out = _EvoAttnFunction.apply(Q, K, V, rm, pb)
+            out = _EvoAttnFunction.apply(Q, K, V, rm, pb, masked_rows == "zero")
         else:
             kernel_census.record("evo_attention", "hip_evo_attn")
             with torch.no_grad():
@@ -393,9 +397,15 @@ class FusedTransitionBlock(TransitionBlock):
         self.channels = channels
 
 
-def _dropout_add(residual, x, p_drop: float, training: bool, site: str):
+def _dropout_add(residual, x, p_drop: float, training: bool, site: str, rowwise: bool):
     if training and p_drop > 0.0:
-        raise NotActive(site, "training-mode dropout is not built (eval only)")
+        _lib.require_device(site, residual, x)
+        seed = next_dropout_seed()
+        if torch.is_grad_enabled() and (residual.requires_grad or x.requires_grad):
+            kernel_census.record(site, "hip_dropout_add_grad")
+            return DropoutAddFunction.apply(residual, x, p_drop, rowwise, seed)
+        kernel_census.record(site, "hip_dropout_add")
+        return dropout_add(residual, x, p_drop, rowwise, seed)
     if torch.is_grad_enabled() and (residual.requires_grad or x.requires_grad):
         kernel_census.record(site, "add_grad")
         return residual + x  # eval dropout-add under autograd (dropout_add.py:236-237)
@@ -404,10 +414,13 @@ def _dropout_add(residual, x, p_drop: float, training: bool, site: str):
 
 
 def dropout_add_rowwise(residual, x, p_drop: float, training: bool, use_fused: bool = True):
-    """Eval: ``residual + x`` (``dropout_add.py:221-242``); training dropout refuses."""
-    return _dropout_add(residual, x, p_drop, training, "dropout_add_rowwise")
+    """``residual + dropout(x)`` with the mask shared along dim -3 (``dropout_add.py:221-242``):
+    eval is ``residual + x``; training runs the HIP shared-mask dropout-add (differentiable
+    under grad; the seed comes from ``kernels.next_dropout_seed``). ``use_fused`` is accepted
+    for the reference's signature; there is one implementation."""
+    return _dropout_add(residual, x, p_drop, training, "dropout_add_rowwise", True)
 
 
 def dropout_add_columnwise(residual, x, p_drop: float, training: bool, use_fused: bool = True):
-    """Eval: ``residual + x`` (``dropout_add.py:245-265``); training dropout refuses."""
-    return _dropout_add(residual, x, p_drop, training, "dropout_add_columnwise")
+    """``residual + dropout(x)`` with the mask shared along dim -2 (``dropout_add.py:245-265``)."""
+    return _dropout_add(residual, x, p_drop, training, "dropout_add_columnwise", False)

@@ -25,6 +25,10 @@ __all__ = [
     "trimul_forward",
     "fused_trimul",
     "residual_add",
+    "next_dropout_seed",
+    "dropout_mask",
+    "dropout_add",
+    "DropoutAddFunction",
     "pack_grid_attn_weights",
     "grid_attention_forward",
     "pair_transition_forward",
@@ -89,6 +93,89 @@ def residual_add(res: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = 
         out.data_ptr(), res_c.numel(), _lib.stream_of(res_c),
     )  # fmt: skip
     return out
+
+
+def next_dropout_seed() -> int:
+    """A 63-bit seed for one dropout-add, drawn from torch's default CPU generator.
+
+    The reference draws each call's seed from a private generator (``dropout_add.py:33-48``).
+    Drawing from the default generator instead makes the masks reproducible under
+    ``torch.manual_seed`` and under activation checkpointing: ``torch.utils.checkpoint``
+    restores the CPU RNG state before it recomputes a block, so the recomputed forward
+    regenerates the masks of the original one."""
+    return int(torch.randint(0, 2**63 - 1, (1,), dtype=torch.int64).item())
+
+
+def _dropout_dims(x: torch.Tensor) -> tuple[int, int, int, int]:
+    """[..., R, Cc, D] as (B, R, Cc, D) with the leading dims folded into B."""
+    if x.dim() < 3:
+        raise NotActive("dropout_add", f"needs [..., R, Cc, D], got shape {tuple(x.shape)}")
+    *lead, R, Cc, D = x.shape
+    B = 1
+    for d in lead:
+        B *= d
+    if D % 4:
+        raise NotActive("dropout_add", f"last dim {D} must be a multiple of 4")
+    return B, R, Cc, D
+
+
+def dropout_mask(shape, rowwise: bool, p: float, seed: int, device) -> torch.Tensor:
+    """The shared mask a dropout-add of an activation of ``shape`` [..., R, Cc, D] applies,
+    broadcastable to it ([..., 1, Cc, D] row-shared or [..., R, 1, D] column-shared), fp32 entries
+    0 or 1/(1-p) (``pf_dropout_mask``)."""
+    *lead, R, Cc, D = shape
+    mshape = (*lead, 1, Cc, D) if rowwise else (*lead, R, 1, D)
+    out = torch.empty(mshape, dtype=torch.float32, device=device)
+    _lib.require_device("dropout_mask", out)
+    _lib.call("pf_dropout_mask", out.data_ptr(), out.numel(), float(p), int(seed), _lib.stream_of(out))
+    return out
+
+
+def dropout_add(res: torch.Tensor, x: torch.Tensor, p: float, rowwise: bool, seed: int,
+                out: torch.Tensor | None = None) -> torch.Tensor:  # fmt: skip
+    """Training-mode ``res + dropout(x)`` with the mask shared along dim -3 (``rowwise``) or -2
+    (``dropout_add.py:57-99``, ``:221-265``), in ``res``'s dtype; ``out`` may be ``res`` (in place).
+    Not differentiable: ``DropoutAddFunction`` is the autograd form."""
+    _lib.require_device("dropout_add", res, x)
+    if res.shape != x.shape:
+        raise NotActive("dropout_add", f"shape mismatch {tuple(res.shape)} vs {tuple(x.shape)}")
+    B, R, Cc, D = _dropout_dims(x)
+    res_c, x_c = res.contiguous(), x.contiguous()
+    if out is None:
+        out = torch.empty_like(res_c)
+    elif out is not res or not res.is_contiguous():
+        _lib.check_out("dropout_add", out, res_c)
+    _lib.call(
+        "pf_dropout_add_fwd", res_c.data_ptr(), _lib.dtype_code(res_c.dtype), x_c.data_ptr(),
+        _lib.dtype_code(x_c.dtype), out.data_ptr(), B, R, Cc, D, int(rowwise), float(p), int(seed),
+        _lib.stream_of(res_c),
+    )  # fmt: skip
+    return out
+
+
+class DropoutAddFunction(torch.autograd.Function):
+    """``apply(res, x, p, rowwise, seed)``: differentiable shared-mask dropout-add on the HIP
+    kernels (``dropout_add.py:137-201``): the forward ``pf_dropout_add_fwd``, the backward passes
+    the cotangent to ``res`` and regenerates the mask from the seed for ``x``
+    (``pf_dropout_bwd``); nothing but the seed is saved."""
+
+    @staticmethod
+    def forward(ctx, res, x, p, rowwise, seed):
+        ctx.meta = (float(p), bool(rowwise), int(seed), x.dtype, res.dtype)
+        return dropout_add(res.detach(), x.detach(), p, rowwise, seed)
+
+    @staticmethod
+    def backward(ctx, g):
+        p, rowwise, seed, x_dtype, res_dtype = ctx.meta
+        g = g.contiguous()
+        B, R, Cc, D = _dropout_dims(g)
+        gx = torch.empty(g.shape, dtype=x_dtype, device=g.device)
+        _lib.call(
+            "pf_dropout_bwd", g.data_ptr(), _lib.dtype_code(g.dtype), gx.data_ptr(), _lib.dtype_code(x_dtype), B, R,
+            Cc, D, int(rowwise), p, seed, _lib.stream_of(g),
+        )  # fmt: skip
+        gres = g if g.dtype == res_dtype else g.to(res_dtype)
+        return gres, gx, None, None, None
 
 
 def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:

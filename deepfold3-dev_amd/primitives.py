@@ -41,21 +41,28 @@ class LinearNoBias(nn.Linear):
 class WeightCache:
     """Prepared (cast / packed) weight operands, rebuilt when a parameter changes.
 
-    The key is every parameter's storage pointer and in-place version counter plus
-    the operand dtype and a caller tag (a folded residual scale), so an optimizer step,
-    ``load_state_dict`` or a new scale invalidates it.
+    One entry per (operand dtype, caller tag); the tag is a folded residual scale, so a
+    module called both unscaled (its own ``forward``) and scaled (inside its block) keeps
+    both. An entry is valid while every parameter's storage pointer and in-place version
+    counter are unchanged, so an optimizer step or ``load_state_dict`` invalidates it.
     """
 
+    _MAX_ENTRIES = 4
+
     def __init__(self):
-        self._key = None
-        self._val = None
+        self._entries: dict = {}
 
     def get(self, params: list[torch.Tensor], dtype: torch.dtype, build, tag=None):
-        key = (dtype, tag, tuple((p.data_ptr(), p._version) for p in params))
-        if key != self._key:
-            self._val = build()
-            self._key = key
-        return self._val
+        slot = (dtype, tag)
+        key = tuple((p.data_ptr(), p._version) for p in params)
+        hit = self._entries.get(slot)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        if slot not in self._entries and len(self._entries) >= self._MAX_ENTRIES:
+            self._entries.clear()
+        val = build()
+        self._entries[slot] = (key, val)
+        return val
 
 
 def f32(t: torch.Tensor) -> torch.Tensor:
@@ -106,15 +113,15 @@ class TransitionBlock(nn.Module):
         if linear_out_init_gain is not None:
             nn.init.orthogonal_(self.linear2.weight, gain=float(linear_out_init_gain))
         self._cache = WeightCache()
-        # Residual scale of this branch (s_ros times the transition's residual gain),
-        # folded into linear2.
+        # Residual scale of this branch inside its block (s_ros times the transition's residual
+        # gain), folded into linear2 by ``branch`` and ``forward_residual_``.
         self.branch_scale = 1.0
 
     @property
     def fused_pair(self) -> bool:
         return self.c == 128 and self.n == 4
 
-    def operands(self, cdt: torch.dtype) -> dict:
+    def operands(self, cdt: torch.dtype, scale: float = 1.0) -> dict:
         from .kernels import cast_weight, scaled_weight
 
         params = [self.norm.weight, self.norm.bias, self.linear1.weight, self.linear2.weight]
@@ -122,17 +129,18 @@ class TransitionBlock(nn.Module):
         def build():
             return dict(
                 w1=cast_weight(self.linear1.weight, cdt),
-                w2=scaled_weight(self.linear2.weight, self.branch_scale, cdt),
+                w2=scaled_weight(self.linear2.weight, scale, cdt),
                 lnw=f32(self.norm.weight), lnb=f32(self.norm.bias),
             )  # fmt: skip
 
-        return self._cache.get(params, cdt, build, tag=self.branch_scale)
+        return self._cache.get(params, cdt, build, tag=float(scale))
 
-    def run(self, x: torch.Tensor, out=None, accumulate: bool = False, s2p=None):
+    def run(self, x: torch.Tensor, out=None, accumulate: bool = False, s2p=None, scale: float = 1.0):
+        """The kernels: ``scale * transition(x)``, into ``out`` (added to it with ``accumulate``)."""
         from . import kernel_census
         from .kernels import gemm_dtype_for, pair_transition_forward, transition_forward
 
-        op = self.operands(gemm_dtype_for(x))
+        op = self.operands(gemm_dtype_for(x), scale)
         if self.fused_pair:
             kernel_census.record("TransitionBlock", "hip_pair_transition")
             return pair_transition_forward(
@@ -143,31 +151,36 @@ class TransitionBlock(nn.Module):
         kernel_census.record("TransitionBlock", "hip_transition")
         return transition_forward(x, op["lnw"], op["lnb"], self.norm.eps, op["w1"], op["w2"], out, accumulate), None
 
-    def _forward_grad(self, x: torch.Tensor) -> torch.Tensor:
+    def _forward_grad(self, x: torch.Tensor, scale: float) -> torch.Tensor:
         """Training path, the reference's fused transition's structure (``fused_transition.py:34-83``:
         LN + linear1, SwiGLU, linear2): the HIP LayerNorm and SwiGLU with their backward, the
         two linears as library GEMMs in autograd (``token_linear``: split-K weight gradients
-        over a pair's tokens), the branch scale on linear2."""
-        import torch.nn.functional as F
-
+        over a pair's tokens), ``scale`` on linear2."""
         from .kernels import SwiGLUFunction, layer_norm_for_gemm, token_linear
 
         xn = layer_norm_for_gemm(x, self.norm.weight, self.norm.bias, self.norm.eps)
-        w2 = self.linear2.weight if self.branch_scale == 1.0 else self.linear2.weight * self.branch_scale
+        w2 = self.linear2.weight if scale == 1.0 else self.linear2.weight * scale
         return token_linear(SwiGLUFunction.apply(token_linear(xn, self.linear1.weight)), w2)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        """``transition(x)`` (not added to x); under grad the differentiable path."""
+    def _update(self, x: torch.Tensor, scale: float) -> torch.Tensor:
         if torch.is_grad_enabled():
             from . import kernel_census
 
             kernel_census.record("TransitionBlock", "hip_transition_grad")
-            return self._forward_grad(x)
-        return self.run(x)[0]
+            return self._forward_grad(x, scale)
+        return self.run(x, scale=scale)[0]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """``transition(x)`` (not added to x); under grad the differentiable path."""
+        return self._update(x, 1.0)
+
+    def branch(self, x: torch.Tensor) -> torch.Tensor:
+        """``branch_scale * transition(x)``, the update a block adds (out of place)."""
+        return self._update(x, self.branch_scale)
 
     def forward_residual_(self, x: torch.Tensor, s2p=None):
-        """``x += transition(x)`` in place; returns ``(x, pair_logits or None)``."""
-        return self.run(x, out=x, accumulate=True, s2p=s2p)
+        """``x += branch_scale * transition(x)`` in place; returns ``(x, pair_logits or None)``."""
+        return self.run(x, out=x, accumulate=True, s2p=s2p, scale=self.branch_scale)
 
 
 def make_transition_block(

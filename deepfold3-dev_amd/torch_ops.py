@@ -18,9 +18,12 @@ Operators (argument meaning as in the function they wrap):
   w_out_gate, outgoing)``: ``kernels.trimul_forward`` on K1-packed weights
   (``triton/fused_trimul.py:332-366``).
 - ``evo_attention(q, k, v, res_mask, pair_bias, zero_masked_rows)``: the flash kernel in the
-  reference kernel's layout, q/k/v ``[B, S, H, N, D]``, res_mask ``[B, S, N]`` and pair_bias
+  reference kernel's layout, q/k/v ``[B, S, H, N, 32]``, res_mask ``[B, S, N]`` and pair_bias
   ``[B, H, N, N]`` fp32 (``triton/evo_attention.py:1198-1292``); differentiable through
-  ``evo_attention_backward`` (the HIP backward) registered as its autograd formula.
+  ``evo_attention_backward`` (the HIP backward, same masked-row rule) registered as its
+  autograd formula. Shapes, dtypes and devices are checked before any launch (and shapes and
+  dtypes in the fake implementations too): the kernels read these buffers with the sizes q
+  implies, so a broadcast mask or a bf16 bias would be read out of bounds.
 """
 
 from __future__ import annotations
@@ -40,7 +43,7 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: f
 
 @layer_norm.register_fake
 def _(x, weight, bias, eps):
-    return torch.empty_like(x)
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
 
 
 @torch.library.custom_op(f"{NS}::ln_transpose", mutates_args=())
@@ -90,31 +93,76 @@ def _(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out, 
     return torch.empty_like(z, memory_format=torch.contiguous_format)
 
 
+_ATTN_DTYPES = (torch.float32, torch.bfloat16)
+
+
+def _check_evo(q, k, v, res_mask, pair_bias, grad_out=None) -> None:
+    """Refuse (``NotActive``) operands the kernels would misread, before anything touches a
+    device: q, k, v ``[B, S, H, N, 32]`` of one dtype (fp32 or bf16) and shape, res_mask
+    ``[B, S, N]`` and pair_bias ``[B, H, N, N]`` fp32 (the kernel layout; the reference's
+    ``[B, S, 1, 1, N]`` mask and ``[B, 1, H, N, N]`` bias go through ``fused._EvoformerAttention``),
+    grad_out shaped like q."""
+    site = "evo_attention"
+    if q.dim() != 5:
+        raise NotActive(site, f"q must be [B, S, H, N, D], got shape {tuple(q.shape)}")
+    B, S, H, N, D = q.shape
+    if q.dtype not in _ATTN_DTYPES:
+        raise NotActive(site, f"q dtype {q.dtype}: fp32 or bf16 only")
+    for name, t in (("k", k), ("v", v)) + ((("grad_out", grad_out),) if grad_out is not None else ()):
+        if tuple(t.shape) != tuple(q.shape):
+            raise NotActive(site, f"{name} shape {tuple(t.shape)} != q shape {tuple(q.shape)}")
+        if name != "grad_out" and t.dtype != q.dtype:
+            raise NotActive(site, f"{name} dtype {t.dtype} != q dtype {q.dtype}")
+    if D != 32:
+        raise NotActive(site, f"D={D}: built for D=32")
+    if res_mask.dtype != torch.float32 or tuple(res_mask.shape) != (B, S, N):
+        raise NotActive(site, f"res_mask must be fp32 [B, S, N] = {[B, S, N]}, got {res_mask.dtype} "
+                        f"{tuple(res_mask.shape)}")  # fmt: skip
+    if pair_bias.dtype != torch.float32 or tuple(pair_bias.shape) != (B, H, N, N):
+        raise NotActive(site, f"pair_bias must be fp32 [B, H, N, N] = {[B, H, N, N]}, got {pair_bias.dtype} "
+                        f"{tuple(pair_bias.shape)}")  # fmt: skip
+
+
+def _check_evo_device(*ts) -> None:
+    from . import _lib
+
+    _lib.require_device("evo_attention", *ts)
+    dev = ts[0].device
+    if any(t.device != dev for t in ts):
+        raise NotActive("evo_attention", "all operands must be on one device")
+
+
 @torch.library.custom_op(f"{NS}::evo_attention", mutates_args=())
 def evo_attention(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, res_mask: torch.Tensor, pair_bias: torch.Tensor,
     zero_masked_rows: bool,
 ) -> torch.Tensor:  # fmt: skip
+    _check_evo(q, k, v, res_mask, pair_bias)
+    _check_evo_device(q, k, v, res_mask, pair_bias)
     return fused._evo_fwd(q.contiguous(), k.contiguous(), v.contiguous(), res_mask.contiguous(),
                           pair_bias.contiguous(), zero_masked_rows)  # fmt: skip
 
 
 @evo_attention.register_fake
 def _(q, k, v, res_mask, pair_bias, zero_masked_rows):
+    _check_evo(q, k, v, res_mask, pair_bias)
     return torch.empty_like(q, memory_format=torch.contiguous_format)
 
 
 @torch.library.custom_op(f"{NS}::evo_attention_backward", mutates_args=())
 def evo_attention_backward(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, res_mask: torch.Tensor, pair_bias: torch.Tensor,
-    grad_out: torch.Tensor,
+    grad_out: torch.Tensor, zero_masked_rows: bool,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:  # fmt: skip
+    _check_evo(q, k, v, res_mask, pair_bias, grad_out)
+    _check_evo_device(q, k, v, res_mask, pair_bias, grad_out)
     return fused._evo_bwd(q.contiguous(), k.contiguous(), v.contiguous(), res_mask.contiguous(),
-                          pair_bias.contiguous(), grad_out)  # fmt: skip
+                          pair_bias.contiguous(), grad_out, zero_masked_rows)  # fmt: skip
 
 
 @evo_attention_backward.register_fake
-def _(q, k, v, res_mask, pair_bias, grad_out):
+def _(q, k, v, res_mask, pair_bias, grad_out, zero_masked_rows):
+    _check_evo(q, k, v, res_mask, pair_bias, grad_out)
     like = lambda t: torch.empty_like(t, memory_format=torch.contiguous_format)  # noqa: E731
     B, S, H, N, D = q.shape
     return like(q), like(k), like(v), q.new_empty((B, H, N, N), dtype=torch.float32)
@@ -127,11 +175,8 @@ def _evo_setup(ctx, inputs, output):
 
 
 def _evo_backward(ctx, grad_out):
-    if not ctx.zero_masked_rows:
-        raise NotActive("evo_attention.backward", "the HIP backward follows the reference kernel's rule "
-                        "(zero_masked_rows=True)")  # fmt: skip
     q, k, v, res_mask, pair_bias = ctx.saved_tensors
-    dq, dk, dv, dpb = evo_attention_backward(q, k, v, res_mask, pair_bias, grad_out)
+    dq, dk, dv, dpb = evo_attention_backward(q, k, v, res_mask, pair_bias, grad_out, ctx.zero_masked_rows)
     return dq, dk, dv, None, dpb, None
 
 

@@ -44,8 +44,12 @@ def block_param_spec(
     single_key_dim: int = C_SINGLE,
     single_value_dim: int = C_SINGLE,
     factor: int = TRANSITION_FACTOR,
+    use_triangle_attention: bool = True,
+    use_single_track: bool = True,
 ) -> list[tuple[str, tuple[int, ...], str]]:
-    """Ordered ``(key, shape, kind)`` for one PairFormerBlock; kind is ln_w, ln_b, linear or bias."""
+    """Ordered ``(key, shape, kind)`` for one PairFormerBlock; kind is ln_w, ln_b, linear or bias.
+    A block without triangle attention has no ``pair_attn_*`` keys, one without the single
+    track no ``single_*`` keys (``evoformer.py:226-249``)."""
     c, cs = c_pair, c_single
     spec: list[tuple[str, tuple[int, ...], str]] = []
     for p in ("tri_mul_out.", "tri_mul_in."):
@@ -92,6 +96,10 @@ def block_param_spec(
         ("single_transition.linear1.weight", (2 * factor * cs, cs), "linear"),
         ("single_transition.linear2.weight", (cs, factor * cs), "linear"),
     ]
+    if not use_triangle_attention:
+        spec = [e for e in spec if not e[0].startswith("pair_attn_")]
+    if not use_single_track:
+        spec = [e for e in spec if not e[0].startswith("single_")]
     return spec
 
 
@@ -121,17 +129,19 @@ def make_block_weights(seed: int, perturb_affine: bool = False, **spec_kwargs) -
     return out
 
 
-def make_trunk_weights(seed: int, num_blocks: int, perturb_affine: bool = False) -> list[dict[str, torch.Tensor]]:
+def make_trunk_weights(seed: int, num_blocks: int, perturb_affine: bool = False,
+                       **spec_kwargs) -> list[dict[str, torch.Tensor]]:  # fmt: skip
     """Per-block state dicts; block ``b`` is drawn from ``seed * 1000 + b``."""
-    return [make_block_weights(seed * 1000 + b, perturb_affine) for b in range(num_blocks)]
+    return [make_block_weights(seed * 1000 + b, perturb_affine, **spec_kwargs) for b in range(num_blocks)]
 
 
 def evoformer_block_param_spec(
     c_msa: int = 64, c_pair: int = C_PAIR, num_msa_heads: int = 8, num_pair_heads: int = NUM_PAIR_HEADS,
-    outer_product_hidden: int = 32,
+    outer_product_hidden: int = 32, use_triangle_attention: bool = True,
 ) -> list[tuple[str, tuple[int, ...], str]]:
     """Ordered ``(key, shape, kind)`` for one EvoformerBlock (``evoformer.py:100-146``):
-    the MSA parts, then the pair half of the PairFormer block (same keys)."""
+    the MSA parts, then the pair half of the PairFormer block (same keys; no ``pair_attn_*``
+    without triangle attention)."""
     cm, cz, ch = c_msa, c_pair, outer_product_hidden
     spec: list[tuple[str, tuple[int, ...], str]] = [
         ("row_attn.norm.weight", (cm,), "ln_w"),
@@ -150,7 +160,11 @@ def evoformer_block_param_spec(
         ("outer_product.out_b", (cz,), "bias"),
     ]
     pair_keys = ("tri_mul_out.", "tri_mul_in.", "pair_attn_row.", "pair_attn_col.", "pair_transition.")
-    spec += [e for e in block_param_spec(c_pair=cz, num_pair_heads=num_pair_heads) if e[0].startswith(pair_keys)]
+    spec += [
+        e
+        for e in block_param_spec(c_pair=cz, num_pair_heads=num_pair_heads, use_triangle_attention=use_triangle_attention)
+        if e[0].startswith(pair_keys)
+    ]
     spec += [
         ("msa_transition.norm.weight", (cm,), "ln_w"),
         ("msa_transition.norm.bias", (cm,), "ln_b"),

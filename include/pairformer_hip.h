@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PF_ABI_VERSION 1
+#define PF_ABI_VERSION 2
 
 #define PF_F32 0
 #define PF_BF16 1
@@ -64,6 +64,25 @@ int pf_cast(const void* src, int src_dtype, void* dst, int dst_dtype, size_t n, 
  * Replaces the eval branch of dropout_add_rowwise / dropout_add_columnwise
  * (triton/dropout_add.py:221-265, which return `residual + x` when not training). */
 int pf_add(const void* res, int res_dtype, const void* x, int x_dtype, void* out, size_t n, void* stream);
+
+/* ---- training-mode dropout-add (mask shared along one axis) ------------
+ * Replaces the training branch of dropout_add_rowwise / dropout_add_columnwise
+ * (triton/dropout_add.py:57-135 kernels, :137-201 autograd function, :221-265 wrappers).
+ * The activation is [B, R, Cc, D] (D contiguous, D % 4 == 0). rowwise != 0 shares the mask
+ * along R (one entry per (b, c, d), index b*Cc*D + c*D + d); rowwise == 0 shares it along Cc
+ * (one entry per (b, r, d), index b*R*D + r*D + d). Mask entry i is 1/(1-p) when u_i >= p and
+ * 0 otherwise, u_i = (word i%4 of Philox4x32-10(counter = i/4, key = seed) >> 8) * 2^-24; the
+ * mask is never stored (the backward regenerates it from the seed). 0 <= p < 1.
+ * pf_dropout_add_fwd: out = res + x * m in res's dtype (fp32 arithmetic, x*m and the add
+ * rounded separately; out may alias res). pf_dropout_bwd: grad_x = grad_out * m in x's dtype
+ * (the residual's gradient is grad_out itself). pf_dropout_mask writes the n mask entries
+ * (0 or 1/(1-p), fp32) of a seed, for checking and for callers that want the mask. Pointers:
+ * fp32 16-byte aligned, bf16 8-byte aligned. */
+int pf_dropout_mask(float* mask, long n, float p, unsigned long long seed, void* stream);
+int pf_dropout_add_fwd(const void* res, int res_dtype, const void* x, int x_dtype, void* out, long B, long R,
+                       long Cc, long D, int rowwise, float p, unsigned long long seed, void* stream);
+int pf_dropout_bwd(const void* grad_out, int grad_dtype, void* grad_x, int x_dtype, long B, long R, long Cc, long D,
+                   int rowwise, float p, unsigned long long seed, void* stream);
 
 /* ---- LayerNorm -------------------------------------------------------- */
 /* out[r, :] = LN(x[r, :]) over C channels, fp32 statistics, output in x's dtype.
@@ -298,16 +317,20 @@ int pf_grid_attn_redo_flags(int B, int N, int C, int H, int cdtype, size_t* offs
 int pf_evo_attn_redo_flags(int B, int S, int H, int N, int D, int dtype, size_t* offset, size_t* count);
 /* _EvoformerAttention.backward (triton/evo_attention.py:1295-1472; kernels :335-1195):
  * gradients of out = softmax(scale q k^T + pair_bias + res_mask) v for q, k, v, dout
- * [B,S,H,N,D] (dtype) and res_mask [B,S,N], pair_bias [B,H,N,N] fp32, under the reference
- * kernel's masked-row rule (a line whose keys are all masked has output 0 and gradient 0).
+ * [B,S,H,N,D] (dtype) and res_mask [B,S,N], pair_bias [B,H,N,N] fp32. zero_masked_rows != 0
+ * is the reference kernel's masked-row rule (a line whose keys are all masked, max logit
+ * < -1e8, has output 0 and gradient 0); 0 is the stock eager rule (attention.py:415-433 under
+ * autograd: the -1e9-shifted logits of such a row round to one value, its softmax is uniform
+ * and its gradients are that softmax's Jacobian; only a row with no finite logit gets 0).
  * The softmax Jacobian is formed centred on each row's argmax, dS = P (u - C) with
  * u = dP - dP_imax (docs/optimizations.md:417-483). Writes dq, dk, dv (dtype) and
  * dpair_bias [B,H,N,N] fp32 (summed over S). The row statistics are recomputed here: the
  * forward saves nothing. Any H; D = 32. */
 size_t pf_evo_attn_bwd_workspace_bytes(int B, int S, int H, int N, int D, int dtype);
 int pf_evo_attn_bwd(const void* q, const void* k, const void* v, const float* res_mask, const float* pair_bias,
-                    const void* dout, int B, int S, int H, int N, int D, int dtype, float softmax_scale, void* dq,
-                    void* dk, void* dv, float* dpair_bias, void* workspace, size_t workspace_bytes, void* stream);
+                    const void* dout, int B, int S, int H, int N, int D, int dtype, float softmax_scale,
+                    int zero_masked_rows, void* dq, void* dk, void* dv, float* dpair_bias, void* workspace,
+                    size_t workspace_bytes, void* stream);
 /* Strided forms of pf_evo_attn_fwd / pf_evo_attn_bwd (no counterpart in the reference, whose
  * module path makes the [B, S, H, N, D] operands contiguous before the kernel): q, k, v, out,
  * dout, dq, dk, dv are views given by element strides {batch, line, head, key} (long[4]; D

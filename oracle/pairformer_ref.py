@@ -39,6 +39,7 @@ Pinning (what checks this restatement, beyond retyping it):
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -60,6 +61,10 @@ __all__ = [
     "evo_attention",
     "evo_attention_backward",
     "tri_mul_core",
+    "philox4x32_10",
+    "dropout_mask",
+    "shared_dropout_mask",
+    "dropout_add",
 ]
 
 
@@ -231,11 +236,19 @@ def pairformer_block(
     row_chunk: int = 0,
     branches: dict[str, torch.Tensor] | None = None,
     scales: dict | None = None,
+    use_triangle_attention: bool = True,
+    use_single_track: bool = True,
+    dropout: dict[str, torch.Tensor] | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """``PairFormerBlock.forward`` in eval mode (``evoformer.py:270-355``).
+    """``PairFormerBlock.forward`` (``evoformer.py:270-355``).
 
-    Identity branch scaler, eval dropout-add is a plain add (``dropout_add.py:236-237``).
-    ``scales`` may hold ``residual_out_scale`` (s_ros, every branch) and
+    Identity branch scaler. Eval dropout-add is a plain add (``dropout_add.py:236-237``);
+    ``dropout`` (training mode) maps the four dropped sites ``tri_mul_out``, ``tri_mul_in``,
+    ``pair_attn_row`` (row-shared masks) and ``pair_attn_col`` (column-shared) to their masks
+    (see ``dropout_add``), applied as at ``evoformer.py:289-310``; the transitions and the single
+    track take no dropout. ``use_triangle_attention=False`` deletes the two attention branches
+    (``:302-310``), ``use_single_track=False`` the single update (``:321-353``; single is returned
+    unchanged). ``scales`` may hold ``residual_out_scale`` (s_ros, every branch) and
     ``pair_transition_residual_gain`` / ``single_transition_residual_gain`` (None = 1, the
     transitions' extra factor), applied to each branch output as at ``evoformer.py:282-353``.
     If ``branches`` is a dict, each unscaled branch output is stored in it under the
@@ -247,32 +260,32 @@ def pairformer_block(
     g_sf = sc.get("single_transition_residual_gain")
     s_pf = s_ros * (1.0 if g_pf is None else float(g_pf))
     s_sf = s_ros * (1.0 if g_sf is None else float(g_sf))
-    tmo = tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True)
-    pair = pair + _scaled(tmo, s_ros)
-    tmi = tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False)
-    pair = pair + _scaled(tmi, s_ros)
-    row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
-    pair = pair + _scaled(row, s_ros)
-    col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
-    pair = pair + _scaled(col, s_ros)
-    pt = transition(pair, _sub(p, "pair_transition."))
-    pair = pair + _scaled(pt, s_pf)
-    logits = single_to_pair(pair, p)
-    sa = single_attention(single, seq_mask, logits, _sub(p, "single_attn."))
-    single = single + _scaled(sa, s_ros)
-    st = transition(single, _sub(p, "single_transition."))
-    single = single + _scaled(st, s_sf)
+    drop = dropout or {}
+
+    def add(res: torch.Tensor, upd: torch.Tensor, site: str) -> torch.Tensor:
+        return dropout_add(res, upd, drop[site]) if site in drop else res + upd
+
+    out: dict[str, torch.Tensor] = {}
+    out["tri_mul_out"] = tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True)
+    pair = add(pair, _scaled(out["tri_mul_out"], s_ros), "tri_mul_out")
+    out["tri_mul_in"] = tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False)
+    pair = add(pair, _scaled(out["tri_mul_in"], s_ros), "tri_mul_in")
+    if use_triangle_attention:
+        row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
+        pair = add(pair, _scaled(row, s_ros), "pair_attn_row")
+        col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
+        pair = add(pair, _scaled(col, s_ros), "pair_attn_col")
+        out.update(pair_attn_row=row, pair_attn_col=col)
+    out["pair_transition"] = transition(pair, _sub(p, "pair_transition."))
+    pair = pair + _scaled(out["pair_transition"], s_pf)
+    if use_single_track:
+        out["pair_logits"] = single_to_pair(pair, p)
+        out["single_attn"] = single_attention(single, seq_mask, out["pair_logits"], _sub(p, "single_attn."))
+        single = single + _scaled(out["single_attn"], s_ros)
+        out["single_transition"] = transition(single, _sub(p, "single_transition."))
+        single = single + _scaled(out["single_transition"], s_sf)
     if branches is not None:
-        branches.update(
-            tri_mul_out=tmo,
-            tri_mul_in=tmi,
-            pair_attn_row=row,
-            pair_attn_col=col,
-            pair_transition=pt,
-            pair_logits=logits,
-            single_attn=sa,
-            single_transition=st,
-        )
+        branches.update(out)
     return pair, single
 
 
@@ -282,18 +295,24 @@ def template_pairformer_block(
     p: dict[str, torch.Tensor],
     row_chunk: int = 0,
     residual_out_scale: float = 1.0,
+    dropout: dict[str, torch.Tensor] | None = None,
 ) -> torch.Tensor:
-    """``TemplatePairFormerBlock.forward`` in eval mode (``template_embedding.py:220-240``):
+    """``TemplatePairFormerBlock.forward`` (``template_embedding.py:220-240``):
     the five pair branches of the PairFormer block in the same order, the transition with
     its own intermediate factor (read from the weights), every branch output-scaled by
-    ``residual_out_scale``."""
+    ``residual_out_scale``; ``dropout`` as in ``pairformer_block`` (eval when None)."""
     s = float(residual_out_scale)
-    pair = pair + _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True), s)
-    pair = pair + _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False), s)
+    drop = dropout or {}
+
+    def add(res: torch.Tensor, upd: torch.Tensor, site: str) -> torch.Tensor:
+        return dropout_add(res, upd, drop[site]) if site in drop else res + upd
+
+    pair = add(pair, _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True), s), "tri_mul_out")
+    pair = add(pair, _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False), s), "tri_mul_in")
     row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
-    pair = pair + _scaled(row, s)
+    pair = add(pair, _scaled(row, s), "pair_attn_row")
     col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
-    pair = pair + _scaled(col, s)
+    pair = add(pair, _scaled(col, s), "pair_attn_col")
     return pair + _scaled(transition(pair, _sub(p, "pair_transition.")), s)
 
 
@@ -305,12 +324,18 @@ def pairformer_trunk(
     blocks: list[dict[str, torch.Tensor]],
     row_chunk: int = 0,
     scales: list[dict] | None = None,
+    dropout: list[dict] | None = None,
+    **block_flags,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """The trunk loop (``evoformer.py:593-601``) without checkpointing or meters;
-    ``scales[i]`` are block i's residual scales (see ``pairformer_block``)."""
+    ``scales[i]`` are block i's residual scales and ``dropout[i]`` its masks (see
+    ``pairformer_block``, which also takes ``block_flags``)."""
     for i, p in enumerate(blocks):
         sc = None if scales is None else scales[i]
-        pair, single = pairformer_block(pair, single, pair_mask, seq_mask, p, row_chunk=row_chunk, scales=sc)
+        dr = None if dropout is None else dropout[i]
+        pair, single = pairformer_block(
+            pair, single, pair_mask, seq_mask, p, row_chunk=row_chunk, scales=sc, dropout=dr, **block_flags
+        )
     return pair, single
 
 
@@ -411,21 +436,31 @@ def evoformer_block(
     num_msa_heads: int = 8,
     residual_out_scale: float = 1.0,
     row_chunk: int = 0,
+    use_triangle_attention: bool = True,
+    dropout: dict[str, torch.Tensor] | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """``EvoformerBlock.forward`` in eval mode (``evoformer.py:148-175``): pair += OPM(msa),
+    """``EvoformerBlock.forward`` (``evoformer.py:148-175``): pair += OPM(msa),
     msa += MSAAttention(msa, pair), msa += msa_transition(msa), then the pair half of the
-    PairFormer block (trimul out, in, attention rows, columns, pair transition); every
-    branch output-scaled by ``residual_out_scale``."""
+    PairFormer block (trimul out, in, attention rows, columns unless
+    ``use_triangle_attention=False``, pair transition); every branch output-scaled by
+    ``residual_out_scale``. ``dropout`` (training) maps ``row_attn`` (msa, row-shared) and the
+    four pair sites of ``pairformer_block`` to their masks; None is eval."""
     s = float(residual_out_scale)
+    drop = dropout or {}
+
+    def add(res: torch.Tensor, upd: torch.Tensor, site: str) -> torch.Tensor:
+        return dropout_add(res, upd, drop[site]) if site in drop else res + upd
+
     pair = pair + _scaled(outer_product_mean(msa, msa_mask, _sub(p, "outer_product.")), s)
-    msa = msa + _scaled(msa_attention(msa, msa_mask, pair, _sub(p, "row_attn."), num_msa_heads), s)
+    msa = add(msa, _scaled(msa_attention(msa, msa_mask, pair, _sub(p, "row_attn."), num_msa_heads), s), "row_attn")
     msa = msa + _scaled(transition(msa, _sub(p, "msa_transition.")), s)
-    pair = pair + _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True), s)
-    pair = pair + _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False), s)
-    row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
-    pair = pair + _scaled(row, s)
-    col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
-    pair = pair + _scaled(col, s)
+    pair = add(pair, _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True), s), "tri_mul_out")
+    pair = add(pair, _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False), s), "tri_mul_in")
+    if use_triangle_attention:
+        row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
+        pair = add(pair, _scaled(row, s), "pair_attn_row")
+        col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
+        pair = add(pair, _scaled(col, s), "pair_attn_col")
     pair = pair + _scaled(transition(pair, _sub(p, "pair_transition.")), s)
     return msa, pair
 
@@ -502,3 +537,60 @@ def tri_mul_core(
         X = torch.einsum("bkic,bkjc->bijc", a, b)
     xln = F.layer_norm(X, (C,), ln_out_w, ln_out_b, eps)
     return torch.sigmoid(F.linear(x, w_out_gate)) * F.linear(xln, w_out)
+
+
+# ---------------------------------------------------------------- training-mode dropout
+# Philox4x32 constants (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as
+# 1, 2, 3", SC 2011): round multipliers and Weyl key increments.
+_PHILOX_M = (0xD2511F53, 0xCD9E8D57)
+_PHILOX_W = (0x9E3779B9, 0xBB67AE85)
+
+
+def philox4x32_10(counter: np.ndarray, key: tuple[int, int]) -> np.ndarray:
+    """Philox4x32 with 10 rounds on ``counter`` [n, 4] uint32 words under ``key`` (two uint32
+    words); returns [n, 4] uint32. Each round: (hi0, lo0) = M0 * c0, (hi1, lo1) = M1 * c2
+    (64-bit products), c = (hi1 ^ c1 ^ k0, lo1, hi0 ^ c3 ^ k1, lo0); the key gains
+    (W0, W1) after every round. Pinned by the published known-answer vectors."""
+    c = [counter[:, i].astype(np.uint64) for i in range(4)]
+    k0, k1 = np.uint64(key[0] & 0xFFFFFFFF), np.uint64(key[1] & 0xFFFFFFFF)
+    m0, m1 = np.uint64(_PHILOX_M[0]), np.uint64(_PHILOX_M[1])
+    lo32 = np.uint64(0xFFFFFFFF)
+    for _ in range(10):
+        p0, p1 = m0 * c[0], m1 * c[2]  # < 2^64: no overflow
+        hi0, lo0 = p0 >> np.uint64(32), p0 & lo32
+        hi1, lo1 = p1 >> np.uint64(32), p1 & lo32
+        c = [hi1 ^ c[1] ^ k0, lo1, hi0 ^ c[3] ^ k1, lo0]
+        k0 = (k0 + np.uint64(_PHILOX_W[0])) & lo32
+        k1 = (k1 + np.uint64(_PHILOX_W[1])) & lo32
+    return np.stack(c, axis=1).astype(np.uint32)
+
+
+def dropout_mask(n: int, p: float, seed: int) -> torch.Tensor:
+    """The n mask entries of a seed (fp32, 0 or 1/(1-p)): entry i keeps when
+    u_i = (word i % 4 of Philox4x32-10(counter = i // 4 as a 64-bit word in the first two
+    lanes, key = seed) >> 8) * 2^-24 is >= p, the keep rule of ``dropout_add.py:91-94``."""
+    q = np.arange((n + 3) // 4, dtype=np.uint64)
+    ctr = np.zeros((q.size, 4), dtype=np.uint32)
+    ctr[:, 0] = (q & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+    ctr[:, 1] = (q >> np.uint64(32)).astype(np.uint32)
+    words = philox4x32_10(ctr, (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF)).reshape(-1)[:n]
+    u = (words >> np.uint32(8)).astype(np.float32) * np.float32(2.0**-24)
+    p32 = np.float32(p)
+    scale = np.float32(1.0) / (np.float32(1.0) - p32)
+    return torch.from_numpy(np.where(u >= p32, scale, np.float32(0.0)).astype(np.float32))
+
+
+def shared_dropout_mask(shape: tuple[int, ...], rowwise: bool, p: float, seed: int) -> torch.Tensor:
+    """The broadcastable mask of a [B, R, Cc, D] activation: [B, 1, Cc, D] shared along R
+    (``dropout_add_rowwise``, share dim -3) or [B, R, 1, D] shared along Cc (columnwise, share
+    dim -2), entries in the index order of ``dropout_add.py:81-88``."""
+    B, R, Cc, D = shape
+    mshape = (B, 1, Cc, D) if rowwise else (B, R, 1, D)
+    n = B * (Cc if rowwise else R) * D
+    return dropout_mask(n, p, seed).view(mshape)
+
+
+def dropout_add(residual: torch.Tensor, x: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """Training-mode dropout-add with a given shared mask (``dropout_add.py:57-99``, the fused
+    kernel): ``residual + x * mask`` in fp32, rounded once to the residual's dtype."""
+    return (residual.float() + x.float() * mask.float()).to(residual.dtype)

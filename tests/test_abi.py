@@ -30,7 +30,7 @@ def test_every_header_symbol_is_exported_and_bound():
 
 def test_version_and_error_reporting_without_gpu():
     lib = _lib.lib()
-    assert lib.pf_version() == 1
+    assert lib.pf_version() == 2
     # Argument validation runs before any device work, so it is testable on CPU.
     nul = None
     status = lib.pf_trimul_fwd(
@@ -72,3 +72,17 @@ def test_noalloc_single_attention_refuses_oversize_without_gpu():
     assert b"static" in lib.pf_last_error()
     with open(_lib.HEADER_PATH) as f:
         assert f"#define PF_NOALLOC_SCRATCH_BYTES (32u << 20)" in f.read()
+
+
+def test_dropout_entry_points_validate_before_launch():
+    """Bad rates, channel counts and null pointers are refused on the host (no GPU here)."""
+    lib = _lib.lib()
+    d = 256  # a non-null, aligned address the call must never dereference
+    assert lib.pf_dropout_add_fwd(d, 0, d, 0, d, 1, 4, 4, 6, 1, 0.25, 1, None) == 2  # D % 4
+    assert b"multiple of 4" in lib.pf_last_error()
+    assert lib.pf_dropout_add_fwd(d, 0, d, 0, d, 1, 4, 4, 8, 1, 1.0, 1, None) == 1  # p = 1
+    assert lib.pf_dropout_bwd(None, 0, d, 0, 1, 4, 4, 8, 0, 0.1, 1, None) == 1  # null
+    assert lib.pf_dropout_mask(None, 8, 0.1, 1, None) == 1
+    assert lib.pf_dropout_add_fwd(d + 4, 0, d, 0, d, 1, 4, 4, 8, 1, 0.25, 1, None) == 4  # fp32 not 16-aligned
+    # nothing to do: status OK without a launch
+    assert lib.pf_dropout_add_fwd(d, 1, d, 1, d, 0, 4, 4, 8, 0, 0.25, 1, None) == 0

@@ -11,8 +11,9 @@
 - Softmax collapse (tests/triton/test_evo_attn_softmax_collapse.py): winner-take-all pair
   bias at margin ~14.5; dQ within 0.1 of the true peak and d_pair_bias rows summing to
   <= 0.05 of their peak.
-- The module-layout wrapper, bitwise-reproducible gradients, and refusal of the stock
-  masked-row rule under grad.
+- The module-layout wrapper, bitwise-reproducible gradients, and the stock masked-row rule
+  under grad (``masked_rows="eager"``) against autograd of the stock formula, a fully masked
+  line included.
 - The strided entry points (GridSelfAttention's training path on its token-major
   projection, rows and columns) against the dense ones on the same values: O, dQ, dK, dV
   and d_pair_bias bit for bit; with the forward's saved row LSE (single dQ pass) against
@@ -154,11 +155,35 @@ def test_attn_backward_wrapper_and_determinism(dev):
         assert torch.equal(a, b)
 
 
-def test_attn_backward_refuses_stock_rule(dev):
-    Q, K, V, rm, pb, _ = _inputs(1, 2, 4, 32, torch.float32, seed=6)
-    q = Q.to(dev).requires_grad_(True)
-    with pytest.raises(NotActive, match="masked-row rule"):
-        fused._EvoformerAttention.apply(q, K.to(dev), V.to(dev), rm.to(dev), pb.to(dev), True, "eager")
+def _stock_grads(Q, K, V, rm, pb, dO):
+    """Autograd of the stock eager path (``attention.py:151-160``): fp64 products, the softmax on
+    the logits cast to fp32 (``softmax(logits.float())``), where a fully masked line's -1e9-shifted
+    logits round to one value and its weights are uniform."""
+    leaves = [t.double().clone().requires_grad_(True) for t in (Q, K, V, pb)]
+    q, k, v, b = leaves
+    logits = torch.matmul(q, k.transpose(-1, -2)) * 32**-0.5 + b + rm.double()
+    out = torch.matmul(torch.softmax(logits.float(), dim=-1).double(), v)
+    return [g.float() for g in torch.autograd.grad(out, leaves, grad_outputs=dO.double())], out.float()
+
+
+@pytest.mark.parametrize("B,S,H,N", [(1, 3, 4, 50), (2, 2, 4, 128)])
+def test_attn_backward_eager_rule(dev, B, S, H, N):
+    """``masked_rows="eager"`` under grad: the forward and every gradient follow the stock path,
+    a fully masked line included (uniform weights; nonzero gradients there), fp32 at 1e-5."""
+    print(f"[attn bwd eager rule] B={B} S={S} H={H} N={N}", flush=True)
+    Q, K, V, rm, pb, dO = _inputs(B, S, H, N, torch.float32, seed=N + 3)
+    assert bool((rm[:, 1] < 0).all())  # line 1 is fully masked
+    leaves = [t.to(dev).requires_grad_(True) for t in (Q, K, V, pb)]
+    out = fused._EvoformerAttention.apply(leaves[0], leaves[1], leaves[2], rm.to(dev), leaves[3], True, "eager")
+    got = [g.float().cpu() for g in torch.autograd.grad(out, leaves, grad_outputs=dO.to(dev))]
+    want, ref_out = _stock_grads(Q, K, V, rm, pb, dO)
+    assert_fp32_close(out.detach().cpu(), ref_out, what="O")
+    for name, a, b in zip(("dQ", "dK", "dV", "d_pair_bias"), got, want):
+        assert_fp32_close(a, b, what=name)
+    assert float(got[0][:, 1].abs().max()) > 0 and float(got[2][:, 1].abs().max()) > 0
+    # the reference kernel's rule zeroes that line's gradients instead
+    zero, _ = _hip_grads(Q, K, V, rm, pb, dO, dev)
+    assert float(zero[0][:, 1].abs().max()) == 0.0 and float(zero[2][:, 1].abs().max()) == 0.0
 
 
 def _grid_module(transpose, c=128, heads=4, seed=7):

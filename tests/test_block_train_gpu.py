@@ -75,7 +75,7 @@ def test_block_backward_fp32(dev, scaled):
     kw = dict(residual_out_scale=0.7, pair_transition_residual_gain=0.5) if scaled else {}
     blk = evoformer.PairFormerBlock(128, 384, **kw)
     blk.load_state_dict(sd)
-    blk = blk.to(dev)
+    blk = blk.to(dev).eval()  # eval mode: no dropout (training mode: tests/test_train_mode_gpu.py)
     args = _inputs(30, 62)
     print(f"[block backward fp32] N=30 scaled={scaled}", flush=True)
     scales = {"residual_out_scale": 0.7, "pair_transition_residual_gain": 0.5} if scaled else None
@@ -94,7 +94,7 @@ def test_block_backward_bf16_autocast(dev):
     sd = W.make_block_weights(63, perturb_affine=True)
     blk = evoformer.PairFormerBlock(128, 384)
     blk.load_state_dict(sd)
-    blk = blk.to(dev)
+    blk = blk.to(dev).eval()
     args = _inputs(64, 64)
     print("[block backward bf16 autocast] N=64", flush=True)
     ref32 = _oracle_grads(sd, *args, torch.float32)
@@ -118,7 +118,7 @@ def test_stack_backward_is_blocks_in_order(dev):
     stack = evoformer.PairFormerStack(2, 128, 384)
     for blk, sd in zip(stack.blocks, sds):
         blk.load_state_dict(sd)
-    stack = stack.to(dev)
+    stack = stack.to(dev).eval()
     pair, single, pm, sm, gp, gs = _inputs(24, 66)
     p0, s0 = pair.to(dev).requires_grad_(True), single.to(dev).requires_grad_(True)
     p, s = stack(p0, s0, pm.to(dev), sm.to(dev))

@@ -90,7 +90,7 @@ def test_residual_scale_rules_match_reference_closed_forms():
         assert ck.branch_residual_gain(i, 0.25, False) == 0.25
         assert ck.branch_residual_gain(i, None, True) == pytest.approx(1 / math.sqrt(i + 1))
         assert ck.branch_residual_gain(i, 0.25, True) == pytest.approx(0.25 / math.sqrt(i + 1))
-    with pytest.raises(ValueError, match="mutually exclusive"):
+    with pytest.raises(ValueError, match="not both"):
         ck.block_residual_scale(0, 4, True, True)
 
 
@@ -175,14 +175,66 @@ def test_loading_is_strict(tmp_path):
         ("pair_bias_gate", True, "pair-bias gate"),
         ("branch_scaler", "rmsnorm", "branch_scaler"),
         ("trimul_num_heads", 2, "multi-head"),
-        ("use_triangle_attention", False, "triangle-attention"),
-        ("use_single_track", False, "single-track"),
     ],
 )
 def test_unbuilt_architectures_refuse_by_name(field, value, needle):
     cfg = {"pairformer": {"num_layer": 1, field: value}}
     with pytest.raises(guard.NotActive, match=needle):
         ck.build_trunk(cfg)
+
+
+# The reference's current stage-0 model shape (configs/stage0.yaml:50-75): 256 pair channels in 8
+# heads, no triangle attention in the trunk or the MSA stack, no single track in the trunk.
+STAGE0 = {
+    "evoformer": {"num_layer": 2, "msa_channel": 128, "pair_channel": 256, "pair_attention": {"num_head": 8},
+                  "msa_attention": {"num_head": 16}, "use_triangle_attention": False, "trimul_num_heads": 0},
+    "pairformer": {"num_layer": 2, "pair_channel": 256, "pair_attention": {"num_head": 8},
+                   "use_triangle_attention": False, "trimul_num_heads": 0, "use_single_track": False},
+    "confidence": {"num_layer": 1, "pair_channel": 256, "pair_attention_num_head": 8},
+}  # fmt: skip
+
+
+def write_stage0_checkpoint(path, seed: int = 60) -> dict:
+    """A reference-layout checkpoint of the STAGE0 shape (trunk, recycler without the single
+    embedding, MSA stack); returns the tensors by key."""
+    from safetensors.torch import save_file
+
+    sd = {}
+    for i, blk in enumerate(W.make_trunk_weights(seed, 2, perturb_affine=True, c_pair=256, num_pair_heads=8,
+                                                 use_triangle_attention=False, use_single_track=False)):  # fmt: skip
+        sd.update({f"evoformer.trunk_pairformer.{i}.{k}": v for k, v in blk.items()})
+    g = torch.Generator().manual_seed(seed + 1)
+    sd["evoformer.prev_embedding_layer_norm.weight"] = 1.0 + 0.2 * torch.randn(256, generator=g)
+    sd["evoformer.prev_embedding_layer_norm.bias"] = 0.3 * torch.randn(256, generator=g)
+    sd["evoformer.prev_embedding.weight"] = torch.randn(256, 256, generator=g) / 16.0
+    for i in range(2):
+        blk = W.make_evoformer_block_weights(seed + 2 + i, perturb_affine=True, c_msa=128, c_pair=256,
+                                             num_msa_heads=16, num_pair_heads=8, use_triangle_attention=False)  # fmt: skip
+        sd.update({f"evoformer.msa_stack.{i}.{k}": v for k, v in blk.items()})
+    sd = {k: v.contiguous() for k, v in sd.items()}
+    save_file(sd, str(path), metadata={ck.MODEL_CFG_KEY: json.dumps(STAGE0)})
+    return sd
+
+
+def test_stage0_shape_builds_without_deleted_branches_and_loads(tmp_path):
+    """Blocks of a config without triangle attention and without the single track have
+    exactly the reference's keys for that shape (no ``pair_attn_*``, no ``single_*``) and load
+    strictly; the recycler has no single embedding."""
+    path = tmp_path / "stage0.safetensors"
+    sd = write_stage0_checkpoint(path)
+    trunk, cfg = ck.load_trunk(path)
+    assert cfg == STAGE0 and len(trunk.blocks) == 2
+    for i, blk in enumerate(trunk.blocks):
+        assert not blk.use_triangle_attention and not blk.use_single_track
+        keys = set(blk.state_dict())
+        assert not any(k.startswith(("pair_attn_", "single_")) for k in keys)
+        assert keys == {k[len(f"evoformer.trunk_pairformer.{i}."):] for k in sd if k.startswith(f"evoformer.trunk_pairformer.{i}.")}
+    rec = ck.load_recycler(path)
+    assert not rec.use_single_track and rec.prev_embedding.weight.shape == (256, 256)
+    msa = ck.load_msa_stack(path)
+    for blk in msa.msa_stack:
+        assert not blk.use_triangle_attention
+        assert not any(k.startswith("pair_attn_") for k in blk.state_dict())
 
 
 def test_msa_block_kwargs_per_layer():

@@ -142,8 +142,17 @@ def test_ln_transpose_module_and_dropout_add(dev):
     ref = F.layer_norm(x.double(), (128,), w.double(), b.double()).permute(0, 2, 1, 3)
     assert_fp32_close(got.cpu(), ref.float(), what="LN transpose")
     assert torch.equal(added, res + upd) and torch.equal(added_c, res + upd)
-    with pytest.raises(NotActive):
-        fused.dropout_add_rowwise(res, upd, 0.25, True)
+    # training: the HIP shared-mask dropout-add, the mask of the seed drawn after manual_seed
+    from oracle import pairformer_ref as R
+
+    kernels = mod("kernels")
+    for rowwise, fn in ((True, fused.dropout_add_rowwise), (False, fused.dropout_add_columnwise)):
+        torch.manual_seed(11)
+        with torch.no_grad():
+            got = fn(res, upd, 0.25, True)
+        torch.manual_seed(11)
+        m = R.shared_dropout_mask(tuple(res.shape), rowwise, 0.25, kernels.next_dropout_seed())
+        assert torch.equal(got.cpu(), R.dropout_add(res.cpu(), upd.cpu(), m))
 
 
 def test_fused_transition_block_keys(dev):

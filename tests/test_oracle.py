@@ -636,3 +636,141 @@ def test_tri_mul_core_gradcheck(outgoing):
         return R.tri_mul_core(x, mask, wg, wp, lw, lb, wo, wog, 1e-5, outgoing)
 
     assert torch.autograd.gradcheck(f, leaves, eps=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------- training-mode dropout
+# Known-answer vectors of Philox4x32-10 published with the Random123 library (kat_vectors:
+# counter words, key words, output words).
+PHILOX_KAT = [
+    ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF,) * 4, (0xFFFFFFFF, 0xFFFFFFFF), (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    (
+        (0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344),
+        (0xA4093822, 0x299F31D0),
+        (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1),
+    ),
+]
+
+
+def test_philox_known_answer_vectors():
+    for ctr, key, want in PHILOX_KAT:
+        got = R.philox4x32_10(np.array([ctr], dtype=np.uint32), key)[0]
+        assert tuple(int(x) for x in got) == want
+
+
+def test_dropout_mask_values_rate_and_index_order():
+    """Entries are 0 or 1/(1-p) (fp32), keep with probability 1 - p, and entry i is word i % 4 of
+    the Philox call on counter i // 4 (two calls of the generator, by hand)."""
+    p, seed = 0.25, (7 << 40) + 12345
+    m = R.dropout_mask(200_003, p, seed)
+    scale = np.float32(1.0) / (np.float32(1.0) - np.float32(p))
+    vals = set(np.unique(m.numpy()).tolist())
+    assert vals == {0.0, float(scale)}
+    keep = (m > 0).double().mean().item()
+    assert abs(keep - 0.75) < 0.005  # 200k Bernoulli(0.75): sd 0.001
+    for i in (0, 1, 2, 3, 4, 7, 99_999, 200_002):
+        w = R.philox4x32_10(np.array([[i // 4, 0, 0, 0]], dtype=np.uint32), (seed & 0xFFFFFFFF, seed >> 32))[0, i % 4]
+        u = np.float32(int(w) >> 8) * np.float32(2.0**-24)
+        assert float(m[i]) == (float(scale) if u >= np.float32(p) else 0.0), i
+    assert torch.equal(R.dropout_mask(5, 0.0, 3), torch.ones(5))  # p = 0 keeps all at scale 1
+    other = R.dropout_mask(1000, p, seed + 1)
+    assert not torch.equal(other, m[:1000])  # another seed, another mask
+
+
+def test_shared_dropout_mask_axes():
+    """Row-shared masks are [B, 1, Cc, D] with entry (b, c, d) at b Cc D + c D + d; column-shared
+    [B, R, 1, D] with (b, r, d) at b R D + r D + d (dropout_add.py:81-88)."""
+    B, Rr, Cc, D = 2, 3, 5, 4
+    flat_r = R.dropout_mask(B * Cc * D, 0.5, 9)
+    flat_c = R.dropout_mask(B * Rr * D, 0.5, 9)
+    mr = R.shared_dropout_mask((B, Rr, Cc, D), True, 0.5, 9)
+    mc = R.shared_dropout_mask((B, Rr, Cc, D), False, 0.5, 9)
+    assert mr.shape == (B, 1, Cc, D) and mc.shape == (B, Rr, 1, D)
+    for b in range(B):
+        for c in range(Cc):
+            for d in range(D):
+                assert mr[b, 0, c, d] == flat_r[b * Cc * D + c * D + d]
+        for r in range(Rr):
+            for d in range(D):
+                assert mc[b, r, 0, d] == flat_c[b * Rr * D + r * D + d]
+
+
+def test_dropout_add_closed_forms():
+    g = torch.Generator().manual_seed(3)
+    res, x = torch.randn(2, 4, 5, 8, generator=g), torch.randn(2, 4, 5, 8, generator=g)
+    ones = torch.ones(2, 1, 5, 8)
+    assert torch.equal(R.dropout_add(res, x, ones), res + x)
+    assert torch.equal(R.dropout_add(res, x, torch.zeros(2, 4, 1, 8)), res)
+    m = R.shared_dropout_mask((2, 4, 5, 8), True, 0.25, 11)
+    out = R.dropout_add(res, x, m)
+    kept = (m > 0).expand_as(x)
+    assert torch.equal(out[~kept], res[~kept])
+    assert torch.allclose(out[kept], (res + x * (4.0 / 3.0))[kept], rtol=0, atol=1e-6)
+    # bf16 residual: fp32 arithmetic rounded once
+    rb, xb = res.bfloat16(), x.bfloat16()
+    assert torch.equal(R.dropout_add(rb, xb, m), (rb.float() + xb.float() * m).bfloat16())
+
+
+_DROP_SITES = (("tri_mul_out", True), ("tri_mul_in", True), ("pair_attn_row", True), ("pair_attn_col", False))
+
+
+def test_block_dropout_composition():
+    """Unit masks give the eval block; a zero mask at one site equals the block with that
+    branch's output projection zeroed (the branch adds nothing there); a mask that drops some
+    entries lands between."""
+    sd = W.make_block_weights(31, perturb_affine=True)
+    x = W.make_inputs(9, seed=5, pad_last=1)
+    args = (x["pair"], x["single"], x["pair_mask"], x["seq_mask"])
+    shape = tuple(x["pair"].shape)
+    unit = {s: torch.ones((1, 1, 9, 128) if rw else (1, 9, 1, 128)) for s, rw in _DROP_SITES}
+    with torch.no_grad():
+        p0, s0 = R.pairformer_block(*args, sd)
+        p1, s1 = R.pairformer_block(*args, sd, dropout=unit)
+        assert torch.equal(p0, p1) and torch.equal(s0, s1)
+        for site, rw in _DROP_SITES:
+            zero = dict(unit, **{site: torch.zeros_like(unit[site])})
+            pz, sz = R.pairformer_block(*args, sd, dropout=zero)
+            pw, sw = R.pairformer_block(*args, {**sd, f"{site}.out_proj.weight": torch.zeros(128, 128)})
+            assert torch.equal(pz, pw) and torch.equal(sz, sw), site
+        masks = {s: R.shared_dropout_mask(shape, rw, 0.25, 100 + i) for i, (s, rw) in enumerate(_DROP_SITES)}
+        pd, _ = R.pairformer_block(*args, sd, dropout=masks)
+    assert rel_l2(pd, p0) > 1e-3
+
+
+def test_block_without_deleted_branches():
+    """use_triangle_attention=False equals the full block with both attention output
+    projections zeroed (evoformer.py:302-310); use_single_track=False leaves single unchanged
+    and the pair update that of the full block (the single track never writes to pair)."""
+    sd = W.make_block_weights(32, perturb_affine=True)
+    x = W.make_inputs(10, seed=6, pad_last=2)
+    args = (x["pair"], x["single"], x["pair_mask"], x["seq_mask"])
+    no_attn = {k: v for k, v in sd.items() if not k.startswith("pair_attn_")}
+    zeroed = {**sd, "pair_attn_row.out_proj.weight": torch.zeros(128, 128),
+              "pair_attn_col.out_proj.weight": torch.zeros(128, 128)}  # fmt: skip
+    no_single = {k: v for k, v in sd.items() if not k.startswith("single_")}
+    with torch.no_grad():
+        pa, sa = R.pairformer_block(*args, no_attn, use_triangle_attention=False)
+        pz, sz = R.pairformer_block(*args, zeroed)
+        ps, ss = R.pairformer_block(*args, no_single, use_single_track=False)
+        pf, _ = R.pairformer_block(*args, sd)
+    assert torch.equal(pa, pz) and torch.equal(sa, sz)
+    assert torch.equal(ps, pf) and ss is x["single"]
+
+
+def test_evoformer_block_without_triangle_attention():
+    sd = W.make_evoformer_block_weights(33, perturb_affine=True)
+    no_attn = {k: v for k, v in sd.items() if not k.startswith("pair_attn_")}
+    zeroed = {**sd, "pair_attn_row.out_proj.weight": torch.zeros(128, 128),
+              "pair_attn_col.out_proj.weight": torch.zeros(128, 128)}  # fmt: skip
+    x = W.make_inputs(7, seed=7, pad_last=1)
+    gen = torch.Generator().manual_seed(2)
+    msa = torch.randn(1, 3, 7, 64, generator=gen)
+    mmask = (torch.rand(1, 3, 7, generator=gen) > 0.2).float()
+    with torch.no_grad():
+        m1, z1 = R.evoformer_block(msa, x["pair"], mmask, x["pair_mask"], no_attn, use_triangle_attention=False)
+        m2, z2 = R.evoformer_block(msa, x["pair"], mmask, x["pair_mask"], zeroed)
+        # MSA dropout: a zero mask on row_attn equals a zeroed row_attn.out_proj
+        m3, z3 = R.evoformer_block(msa, x["pair"], mmask, x["pair_mask"], sd, dropout={"row_attn": torch.zeros(1, 1, 7, 64)})
+        m4, z4 = R.evoformer_block(msa, x["pair"], mmask, x["pair_mask"], {**sd, "row_attn.out_proj.weight": torch.zeros(64, 64)})
+    assert torch.equal(m1, m2) and torch.equal(z1, z2)
+    assert torch.equal(m3, m4) and torch.equal(z3, z4)

@@ -39,5 +39,50 @@ def test_fake_shapes():
         rm, pb = torch.empty(1, 3, 10), torch.empty(1, 4, 10, 10)
         o = T.evo_attention(q, q, q, rm, pb, True)
         assert o.shape == q.shape and o.dtype == q.dtype
-        dq, dk, dv, dpb = T.evo_attention_backward(q, q, q, rm, pb, o)
+        dq, dk, dv, dpb = T.evo_attention_backward(q, q, q, rm, pb, o, True)
         assert dq.shape == q.shape and dpb.shape == (1, 4, 10, 10) and dpb.dtype == torch.float32
+        # the real op returns a contiguous tensor; the fake must report the same strides
+        xp = torch.empty(2, 7, 5, 128).permute(0, 2, 1, 3)
+        assert T.layer_norm(xp, w, b, 1e-5).is_contiguous()
+
+
+def test_attention_ops_refuse_bad_operands_before_any_device_call():
+    """Wrong dtypes or shapes (a bf16 pair bias, the reference's broadcast [B, S, 1, 1, N] mask,
+    K/V unlike Q) raise NotActive from the checks themselves: these are CPU tensors, so a device
+    call would have refused differently ("no CPU path")."""
+    NotActive = mod("inference_guard").NotActive
+    q = torch.zeros(1, 3, 4, 10, 32, dtype=torch.bfloat16)
+    rm, pb = torch.zeros(1, 3, 10), torch.zeros(1, 4, 10, 10)
+    cases = [
+        ((q, q, q, rm, pb.bfloat16()), "pair_bias"),
+        ((q, q, q, rm.view(1, 3, 1, 1, 10), pb), "res_mask"),
+        ((q, q, q, rm, pb.unsqueeze(1)), "pair_bias"),
+        ((q, q.float(), q, rm, pb), "dtype"),
+        ((q, q[:, :, :, :9], q, rm, pb), "shape"),
+        ((q[..., :16], q[..., :16], q[..., :16], rm, pb), "D=16"),
+        ((q.to(torch.float16), q.to(torch.float16), q.to(torch.float16), rm, pb), "dtype"),
+    ]
+    for args, needle in cases:
+        for fn in (lambda *a: T.evo_attention(*a, True), lambda *a: T.evo_attention_backward(*a, a[0], True)):
+            try:
+                fn(*args)
+            except NotActive as e:
+                assert needle in str(e), (needle, str(e))
+                assert "CPU path" not in str(e)
+            else:
+                raise AssertionError(f"accepted {needle}")
+        with FakeTensorMode():  # the fake implementation refuses the same operands at trace time
+            fa = [torch.empty(t.shape, dtype=t.dtype) for t in args]
+            try:
+                T.evo_attention(*fa, True)
+            except NotActive:
+                pass
+            else:
+                raise AssertionError(f"fake accepted {needle}")
+    # well-formed CPU operands pass the checks and are refused only for the device
+    try:
+        T.evo_attention(q, q, q, rm, pb, True)
+    except NotActive as e:
+        assert "CPU path" in str(e)
+    else:
+        raise AssertionError("CPU operands accepted")
