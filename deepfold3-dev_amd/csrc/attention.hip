@@ -1733,9 +1733,12 @@ GridGenWs grid_gen_layout(int B, int N, int C, int H, int cdtype) {
   return w;
 }
 
-// One thread per (position, head) with the head count padded to a multiple of four (the
-// padding heads are zero). Position (b, x, y) of z: row mode line x, token y; column mode
-// line y, token x. The pair bias is that of position (x, y) in both modes (attention.py:204-209).
+// One thread per (position, head, 8-wide chunk of the 32-wide padded head dimension): the
+// chunk runs fastest, then the head (count padded to a multiple of four; padding heads and
+// dimensions are zero), then the position, so the reads of a position's q / k / v columns
+// and the 16-byte stores of a head row are contiguous across the wave. Position (b, x, y)
+// of z: row mode line x, token y; column mode line y, token x. The pair bias is that of
+// position (x, y) in both modes (attention.py:204-209).
 template <class TC>
 __global__ __launch_bounds__(256) void grid_gen_pack_kernel(const TC* __restrict__ proj, const float* __restrict__ mask,
                                                             TC* __restrict__ Q, TC* __restrict__ K, TC* __restrict__ V,
@@ -1743,43 +1746,56 @@ __global__ __launch_bounds__(256) void grid_gen_pack_kernel(const TC* __restrict
                                                             int H, int H4, int d, int PW, int transpose) {
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   const long M = (long)B * N * N;
-  if (idx >= M * H4) return;
-  const int h = (int)(idx % H4);
-  const long pos = idx / H4;
+  if (idx >= M * H4 * 4) return;
+  const int c = (int)(idx & 3);
+  const int h = (int)((idx >> 2) % H4);
+  const long pos = (idx >> 2) / H4;
   const int b = (int)(pos / ((long)N * N));
   const int x = (int)((pos / N) % N), y = (int)(pos % N);
   const int line = transpose ? y : x, tok = transpose ? x : y;
   const int g = h / 4, hh = h % 4;
-  const size_t head = (((((size_t)g * B + b) * N + line) * 4 + hh) * N + tok) * kHeadDim;
+  const size_t head = (((((size_t)g * B + b) * N + line) * 4 + hh) * N + tok) * kHeadDim + 8 * c;
   const TC* row = proj + pos * PW;
   const int HD = H * d;
-  for (int e = 0; e < kHeadDim; ++e) {
-    const bool real = h < H && e < d;
-    Q[head + e] = real ? row[h * d + e] : from_f32<TC>(0.f);
-    K[head + e] = real ? row[HD + h * d + e] : from_f32<TC>(0.f);
-    V[head + e] = real ? row[2 * HD + h * d + e] : from_f32<TC>(0.f);
+  float q[8], k[8], v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int dd = 8 * c + e;
+    const bool real = h < H && dd < d;
+    q[e] = real ? to_f32(row[h * d + dd]) : 0.f;
+    k[e] = real ? to_f32(row[HD + h * d + dd]) : 0.f;
+    v[e] = real ? to_f32(row[2 * HD + h * d + dd]) : 0.f;
   }
-  PB[(((size_t)g * B + b) * 4 + hh) * N * N + (size_t)x * N + y] = h < H ? to_f32(row[4 * HD + h]) : 0.f;
-  if (h == 0) MA[((size_t)b * N + line) * N + tok] = (mask[pos] - 1.0f) * 1e9f;
+  store_vec<TC, 8>(Q + head, q);
+  store_vec<TC, 8>(K + head, k);
+  store_vec<TC, 8>(V + head, v);
+  if (c == 0) PB[(((size_t)g * B + b) * 4 + hh) * N * N + (size_t)x * N + y] = h < H ? to_f32(row[4 * HD + h]) : 0.f;
+  if (c == 0 && h == 0) MA[((size_t)b * N + line) * N + tok] = (mask[pos] - 1.0f) * 1e9f;
 }
 
 // og[pos][h d + e] = o * sigmoid(g) for the real heads and dimensions, in z position order.
-template <class TC>
+// VEC = 8 (head dimension a multiple of 8): one thread per 8-wide chunk, chunk fastest, with
+// 16-byte stores; VEC = 1: one thread per element.
+template <class TC, int VEC>
 __global__ __launch_bounds__(256) void grid_gen_gate_kernel(const TC* __restrict__ O, const TC* __restrict__ proj,
                                                             TC* __restrict__ og, int B, int N, int H, int d, int PW,
                                                             int transpose) {
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   const int HD = H * d;
-  if (idx >= (long)B * N * N * HD) return;
-  const int e = (int)(idx % d);
-  const int h = (int)((idx / d) % H);
-  const long pos = idx / HD;
+  const int nc = d / VEC;
+  if (idx >= (long)B * N * N * H * nc) return;
+  const int e0 = (int)(idx % nc) * VEC;
+  const int h = (int)((idx / nc) % H);
+  const long pos = idx / ((long)nc * H);
   const int b = (int)(pos / ((long)N * N));
   const int x = (int)((pos / N) % N), y = (int)(pos % N);
   const int line = transpose ? y : x, tok = transpose ? x : y;
-  const size_t head = (((((size_t)(h / 4) * B + b) * N + line) * 4 + h % 4) * N + tok) * kHeadDim;
-  const float gate = sigmoidf_(to_f32(proj[pos * PW + 3 * HD + h * d + e]));
-  og[pos * HD + h * d + e] = from_f32<TC>(to_f32(O[head + e]) * gate);
+  const size_t head = (((((size_t)(h / 4) * B + b) * N + line) * 4 + h % 4) * N + tok) * kHeadDim + e0;
+  const TC* gr = proj + pos * PW + 3 * HD + h * d + e0;
+  float r[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) r[e] = to_f32(O[head + e]) * sigmoidf_(to_f32(gr[e]));
+  store_vec<TC, VEC>(og + pos * HD + h * d + e0, r);
 }
 
 template <class TZ, class TC>
@@ -1804,8 +1820,8 @@ int grid_attn_generic_launch(const void* z, const float* mask, const float* lnw,
   TC* og = reinterpret_cast<TC*>(base + L.og);
   if (int e = ln_launch<TZ, TC>(z, lnw, lnb, eps, xn, M, C, s)) return e;
   if (int e = rowgemm_launch<TC, TC, EPI_STORE>(xn, w5, nullptr, 0, proj, M, PW, C, s)) return e;
-  grid_gen_pack_kernel<TC><<<(unsigned)((M * H4 + 255) / 256), 256, 0, s>>>(proj, mask, Q, K, V, PB, MA, B, N, H, H4, d,
-                                                                            PW, transpose);
+  grid_gen_pack_kernel<TC><<<(unsigned)((M * H4 * 4 + 255) / 256), 256, 0, s>>>(proj, mask, Q, K, V, PB, MA, B, N, H,
+                                                                                H4, d, PW, transpose);
   if (int e = pf::check_launch("grid_gen_pack")) return e;
   const size_t group = (size_t)B * N * 4 * N * kHeadDim;  // elements of one four-head group
   for (int g = 0; g < H4 / 4; ++g) {
@@ -1813,7 +1829,12 @@ int grid_attn_generic_launch(const void* z, const float* mask, const float* lnw,
                                     B, N, N, 0, O + g * group, base + L.evo, s, 1.0f / sqrtf((float)d)))
       return e;
   }
-  grid_gen_gate_kernel<TC><<<(unsigned)((M * H * d + 255) / 256), 256, 0, s>>>(O, proj, og, B, N, H, d, PW, transpose);
+  if (d % 8 == 0)
+    grid_gen_gate_kernel<TC, 8><<<(unsigned)((M * H * (d / 8) + 255) / 256), 256, 0, s>>>(O, proj, og, B, N, H, d, PW,
+                                                                                        transpose);
+  else
+    grid_gen_gate_kernel<TC, 1><<<(unsigned)((M * H * d + 255) / 256), 256, 0, s>>>(O, proj, og, B, N, H, d, PW,
+                                                                                  transpose);
   if (int e = pf::check_launch("grid_gen_gate")) return e;
   if (accumulate) return rowgemm_launch<TC, TZ, EPI_RESIDUAL>(og, wo, nullptr, 0, out, M, C, H * d, s);
   return rowgemm_launch<TC, TZ, EPI_STORE>(og, wo, nullptr, 0, out, M, C, H * d, s);

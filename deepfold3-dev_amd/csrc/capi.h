@@ -29,9 +29,15 @@ inline int pad128(int n) { return (int)round_up((size_t)n, 128); }
 // Compute units of the current device (cached per device), for persistent grids.
 int cu_count();
 
-// Opt-in per-kernel timing with HIP events on the launch stream (pf_kernel_timer_*).
-// Construct before a launch site and call stop() after it; both are no-ops unless the
-// site's name is the one selected with pf_kernel_timer_start.
+// Opt-in per-kernel timing (pf_kernel_timer_*). Construct before a launch site and call
+// stop() after it: both record a HIP event on the launch stream (without the system-scope
+// fence, so no cache flush), and the site's time is the difference of the two events' end
+// timestamps, each read against one reference event recorded when timing starts. Measured on
+// gfx950: an event's start timestamp can come before the work queued ahead of it has ended
+// (back-to-back 52 us kernels read 100-110 us from start to end), its end timestamp cannot;
+// end to end, the figures exceed the rocprofv3 kernel trace of the same launches by the
+// ~5 us of the two events. Both are no-ops unless the site's name is the one selected with
+// pf_kernel_timer_start.
 class KernelTimer {
  public:
   KernelTimer(const char* name, hipStream_t stream);

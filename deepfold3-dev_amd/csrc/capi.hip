@@ -60,6 +60,7 @@ std::mutex g_timer_mu;
 std::string g_timer_name;  // empty: timing off
 std::vector<hipEvent_t> g_free_events;
 std::vector<std::pair<hipEvent_t, hipEvent_t>> g_pending;
+hipEvent_t g_ref = nullptr;  // recorded when timing starts; intervals are end(stop) - end(start)
 double g_timer_total_ms = 0.0;
 long g_timer_count = 0;
 
@@ -69,18 +70,23 @@ hipEvent_t take_event() {
     g_free_events.pop_back();
     return e;
   }
-  // Timing-only events: without the system-scope fence a recorded event would write back
-  // and invalidate the caches, and that cost lands inside the interval of the timed kernel
-  // (tens of microseconds after a kernel that leaves much dirty data in L2).
   hipEvent_t e = nullptr;
   if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
   return e;
+}
+
+void recycle_locked() {
+  for (auto& pr : g_pending) {
+    g_free_events.push_back(pr.first);
+    g_free_events.push_back(pr.second);
+  }
+  g_pending.clear();
 }
 }  // namespace
 
 KernelTimer::KernelTimer(const char* name, hipStream_t stream) : stream_(stream) {
   std::lock_guard<std::mutex> lk(g_timer_mu);
-  if (g_timer_name.empty() || g_timer_name != name) return;
+  if (g_timer_name.empty() || g_timer_name != name || !g_ref) return;
   hipEvent_t e = take_event();
   if (e && hipEventRecord(e, stream_) == hipSuccess) start_ = e;
 }
@@ -119,15 +125,18 @@ const char* pf_last_error(void) { return pf::g_err; }
 
 int pf_kernel_timer_start(const char* kernel) {
   PF_REQUIRE(kernel != nullptr, PF_ERR_INVALID_ARG, "pf_kernel_timer_start: null name");
+  PF_REQUIRE(hipDeviceSynchronize() == hipSuccess, PF_ERR_LAUNCH, "pf_kernel_timer_start: device error");
   std::lock_guard<std::mutex> lk(pf::g_timer_mu);
   pf::g_timer_name = kernel;
   pf::g_timer_total_ms = 0.0;
   pf::g_timer_count = 0;
-  for (auto& pr : pf::g_pending) {
-    pf::g_free_events.push_back(pr.first);
-    pf::g_free_events.push_back(pr.second);
+  pf::recycle_locked();
+  if (!pf::g_ref) {
+    PF_REQUIRE(hipEventCreate(&pf::g_ref) == hipSuccess, PF_ERR_LAUNCH, "pf_kernel_timer_start: event");
   }
-  pf::g_pending.clear();
+  hipError_t e = hipEventRecord(pf::g_ref, nullptr);
+  if (e == hipSuccess) e = hipEventSynchronize(pf::g_ref);
+  PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "pf_kernel_timer_start: %s", hipGetErrorString(e));
   return pf::ok();
 }
 
@@ -135,16 +144,16 @@ int pf_kernel_timer_read(double* total_ms, long* count) {
   PF_REQUIRE(total_ms && count, PF_ERR_INVALID_ARG, "pf_kernel_timer_read: null pointer");
   std::lock_guard<std::mutex> lk(pf::g_timer_mu);
   for (auto& pr : pf::g_pending) {
-    float ms = 0.f;
+    // elapsed(ref, x) = end(x) - start(ref): the difference is end(stop) - end(start).
+    float t0 = 0.f, t1 = 0.f;
     hipError_t e = hipEventSynchronize(pr.second);
-    if (e == hipSuccess) e = hipEventElapsedTime(&ms, pr.first, pr.second);
+    if (e == hipSuccess) e = hipEventElapsedTime(&t0, pf::g_ref, pr.first);
+    if (e == hipSuccess) e = hipEventElapsedTime(&t1, pf::g_ref, pr.second);
     PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "pf_kernel_timer_read: %s", hipGetErrorString(e));
-    pf::g_timer_total_ms += ms;
+    pf::g_timer_total_ms += (double)t1 - (double)t0;
     pf::g_timer_count += 1;
-    pf::g_free_events.push_back(pr.first);
-    pf::g_free_events.push_back(pr.second);
   }
-  pf::g_pending.clear();
+  pf::recycle_locked();
   *total_ms = pf::g_timer_total_ms;
   *count = pf::g_timer_count;
   return pf::ok();

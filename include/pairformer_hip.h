@@ -49,9 +49,12 @@ int pf_last_error_code(void);
  * events in benchmarks/utils.py:58-120). pf_kernel_timer_start(name) selects one launch
  * site ("trimul_project", "trimul_contract", "trimul_output", "attn_project", "pb_transpose",
  * "tri_attn", "tri_attn_redo", "attn_out", "evo_attn", "pair_transition", "single_attn_core",
- * "layernorm", "ln_transpose") and resets the totals; every later launch of that site
- * is bracketed by HIP events recorded on its own stream. pf_kernel_timer_read waits for
- * the recorded events and returns the summed duration and launch count so far;
+ * "layernorm", "ln_transpose"), waits for the device to finish what it has queued, records
+ * a reference event, and resets the totals; every later call of that site is bracketed by
+ * HIP events on its own stream (without the system-scope fence) and timed from the first
+ * event's end timestamp to the second's, both read against the reference event (an event's
+ * start timestamp can precede the end of work queued ahead of it). pf_kernel_timer_read waits
+ * for the events and returns the summed duration and the number of site calls so far;
  * pf_kernel_timer_stop switches timing off. Host-side state, guarded by a mutex. */
 int pf_kernel_timer_start(const char* kernel);
 int pf_kernel_timer_read(double* total_ms, long* count);
