@@ -127,7 +127,157 @@ int bgemm_launch(const void* A, const void* B, void* C, int M, int N, int K, lon
   return pf::check_launch("bgemm");
 }
 
+// Row GEMM over many rows: out[m][n] = epi(sum_k A[m][k] W[n][k]) on the bgemm tiling
+// (128 rows x 128 weight rows per block, 2 x 2 waves of 64 x 64, k-tiles through LDS), with
+// the row GEMM's epilogues: EPI 0 store, 1 add into out (residual), 2 SwiGLU (W has 2 Nout
+// rows; out column j = silu(h_j) h_{Nout + j}). SwiGLU tiles cover 64 output columns: the
+// B tile's rows are, per wave column, 32 "a" rows then the 32 matching "b" rows, so a lane
+// holds both factors of each output (accumulator blocks j and j + 2). A [M][K], W [*][K],
+// out [M][Nout], all row-major with k or n contiguous. Blocks walk the weight tiles of one
+// row tile consecutively (the A tile stays in L2).
+template <class TC, class TO, int EPI>
+__global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restrict__ A, const TC* __restrict__ W,
+                                                             TO* __restrict__ out, long M, int Nout, int K) {
+  using Cfg = BgemmCfg<TC>;
+  using MF = Mfma<TC>;
+  constexpr int BMN = Cfg::BMN, KT = Cfg::KT, LDK = Cfg::LDK;
+  constexpr int OCT = EPI == 2 ? 64 : 128;  // output columns per tile
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  TC* lds = reinterpret_cast<TC*>(smem);
+
+  const int tn = (Nout + OCT - 1) / OCT;
+  const long i0 = (long)(blockIdx.x / tn) * BMN;
+  const int oc0 = (int)(blockIdx.x % tn) * OCT;
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const int wr = (w >> 1) * 64;
+  const int wc = (w & 1) * 64;
+
+  // Weight row of B-tile row rr.
+  auto wrow = [&](int rr) -> int {
+    if constexpr (EPI == 2) {
+      const int col = min(oc0 + (rr >> 6) * 32 + (rr & 31), Nout - 1);
+      return (rr & 32) ? Nout + col : col;
+    } else {
+      return min(oc0 + rr, Nout - 1);
+    }
+  };
+
+  constexpr int VEC = 16 / sizeof(TC);
+  constexpr int CPR = KT / VEC;
+  constexpr int LOADS = 2 * BMN * CPR / 256;
+  static_assert((2 * BMN * CPR) % 256 == 0, "stage must split evenly");
+  const TC* src_row[LOADS];
+  int dst_off[LOADS];
+#pragma unroll
+  for (int q = 0; q < LOADS; ++q) {
+    const int idx = tid + q * 256;
+    const int row = idx / CPR;
+    const int chunk = idx % CPR;
+    src_row[q] = (row < BMN ? A + (size_t)min(i0 + row, M - 1) * K : W + (size_t)wrow(row - BMN) * K) + chunk * VEC;
+    dst_off[q] = row * LDK + chunk * VEC;
+  }
+  u32x4 reg[LOADS];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < LOADS; ++q) reg[q] = *reinterpret_cast<const u32x4*>(src_row[q] + k0);
+  };
+  auto lstore = [&](int buf) {
+    TC* base = lds + buf * 2 * Cfg::TILE_ELEMS;
+#pragma unroll
+    for (int q = 0; q < LOADS; ++q) *reinterpret_cast<u32x4*>(base + dst_off[q]) = reg[q];
+  };
+
+  f32x4 acc[4][4];
+  zero_acc(acc);
+  const int nk = K / KT;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int r = l & 15;
+  const int kq = (l >> 4) * MF::KPL;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * KT);
+    const TC* As = lds + buf * 2 * Cfg::TILE_ELEMS;
+    const TC* Bs = As + Cfg::TILE_ELEMS;
+#pragma unroll
+    for (int kk = 0; kk < KT; kk += MF::K16) {
+      typename MF::Frag af[4], bfr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = MF::load(As + (wr + i * 16 + r) * LDK + kk + kq);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfr[j] = MF::load(Bs + (wc + j * 16 + r) * LDK + kk + kq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) MF::mma16(acc[i][j], af[i], bfr[j]);
+    }
+    if (kt + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+  // acc[i][j][e]: row wr + 16 i + 4 (l >> 4) + e, B-tile row wc + 16 j + (l & 15)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const long m = i0 + wr + i * 16 + 4 * (l >> 4) + e;
+      if (m >= M) continue;
+      TO* orow = out + m * Nout;
+      if constexpr (EPI == 2) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = oc0 + (wc >> 6) * 32 + j * 16 + r;
+          if (n < Nout) orow[n] = from_f32<TO>(siluf_(acc[i][j][e]) * acc[i][j + 2][e]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int n = oc0 + wc + j * 16 + r;
+          if (n >= Nout) continue;
+          if constexpr (EPI == 1)
+            orow[n] = from_f32<TO>(to_f32(orow[n]) + acc[i][j][e]);
+          else
+            orow[n] = from_f32<TO>(acc[i][j][e]);
+        }
+      }
+    }
+}
+
+template <class TC, class TO, int EPI>
+int tile_gemm_rows_launch(const void* A, const void* W, void* out, long M, int Nout, int K, hipStream_t s) {
+  using Cfg = BgemmCfg<TC>;
+  const void* fn = (const void*)tile_gemm_rows_kernel<TC, TO, EPI>;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::SMEM);
+  PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "row gemm: cannot reserve %d bytes of LDS: %s", Cfg::SMEM,
+             hipGetErrorString(e));
+  const long tn = (Nout + (EPI == 2 ? 64 : 128) - 1) / (EPI == 2 ? 64 : 128);
+  const long blocks = (M + Cfg::BMN - 1) / Cfg::BMN * tn;
+  PF_REQUIRE(blocks < (1L << 31), PF_ERR_UNSUPPORTED, "row gemm: M=%ld Nout=%d", M, Nout);
+  tile_gemm_rows_kernel<TC, TO, EPI><<<dim3((unsigned)blocks), 256, Cfg::SMEM, s>>>((const TC*)A, (const TC*)W,
+                                                                                   (TO*)out, M, Nout, K);
+  return pf::check_launch("row gemm");
+}
+
+template <class TC, class TO>
+int tile_gemm_rows_epi(const void* A, const void* W, void* out, long M, int Nout, int K, int epi, hipStream_t s) {
+  if (epi == 1) return tile_gemm_rows_launch<TC, TO, 1>(A, W, out, M, Nout, K, s);
+  if (epi == 2) return tile_gemm_rows_launch<TC, TO, 2>(A, W, out, M, Nout, K, s);
+  return tile_gemm_rows_launch<TC, TO, 0>(A, W, out, M, Nout, K, s);
+}
+
 }  // namespace
+
+int tile_gemm_rows(const void* A, const void* W, void* out, long M, int Nout, int K, int epi, int tc_dtype,
+                   int out_dtype, hipStream_t s) {
+  const int kt = tc_dtype == PF_F32 ? BgemmCfg<float>::KT : BgemmCfg<bf16>::KT;
+  PF_REQUIRE(M > 0 && Nout > 0 && K > 0 && K % kt == 0 && epi >= 0 && epi <= 2, PF_ERR_INVALID_ARG,
+             "row gemm: M=%ld Nout=%d K=%d (a multiple of %d) epi=%d", M, Nout, K, kt, epi);
+  if (tc_dtype == PF_F32) return tile_gemm_rows_epi<float, float>(A, W, out, M, Nout, K, epi, s);
+  if (out_dtype == PF_F32) return tile_gemm_rows_epi<bf16, float>(A, W, out, M, Nout, K, epi, s);
+  return tile_gemm_rows_epi<bf16, bf16>(A, W, out, M, Nout, K, epi, s);
+}
 
 int bgemm_nt(const void* A, const void* B, void* C, int M, int N, int K, long lda, long ldb, long ldc, long sA,
              long sB, long sC, int batch, int tc_dtype, int out_dtype, hipStream_t s) {

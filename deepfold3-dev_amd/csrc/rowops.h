@@ -6,6 +6,7 @@
 
 #include "capi.h"
 #include "common.h"
+#include "gemm.h"
 
 namespace {
 
@@ -113,6 +114,12 @@ int ln_launch(const void* x, const float* w, const float* b, float eps, void* ou
 template <class TC, class TO, int EPI>
 int rowgemm_launch(const void* A, const void* W, const float* bias, int nbias, void* out, long M, int Nout, int K,
                    hipStream_t s) {
+  // Many rows (the pair paths at generic widths): the LDS-tiled GEMM with the same epilogue.
+  constexpr int kt = sizeof(TC) == 2 ? 64 : 32;
+  if (M >= kTileGemmMinRows && K % kt == 0 && (bias == nullptr || nbias == 0) && pf::aligned16(A) &&
+      pf::aligned16(W))
+    return tile_gemm_rows(A, W, out, M, Nout, K, EPI, sizeof(TC) == 2 ? PF_BF16 : PF_F32,
+                          sizeof(TO) == 2 ? PF_BF16 : PF_F32, s);
   const long nb64 = ((M + 63) / 64) * ((Nout + 63) / 64);
   if (nb64 < 2L * pf::cu_count()) {  // few row blocks: 32-row tiles, twice the blocks
     dim3 grid((unsigned)((M + 31) / 32), (unsigned)((Nout + 63) / 64));
