@@ -1798,6 +1798,45 @@ __global__ __launch_bounds__(256) void grid_gen_gate_kernel(const TC* __restrict
   store_vec<TC, VEC>(og + pos * HD + h * d + e0, r);
 }
 
+// The pair bias and the line mask of the strided path: one thread per (position, head of the
+// four-head groups), PB [g][b][hh][x][y] fp32 (zero for padding heads) and MA [b][line][tok].
+template <class TC>
+__global__ __launch_bounds__(256) void grid_gen_bias_kernel(const TC* __restrict__ proj, const float* __restrict__ mask,
+                                                            float* __restrict__ PB, float* __restrict__ MA, int B, int N,
+                                                            int H, int H4, int d, int PW, int transpose) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const long M = (long)B * N * N;
+  if (idx >= M * H4) return;
+  const int h = (int)(idx % H4);
+  const long pos = idx / H4;
+  const int b = (int)(pos / ((long)N * N));
+  const int x = (int)((pos / N) % N), y = (int)(pos % N);
+  PB[(((size_t)(h / 4) * B + b) * 4 + h % 4) * N * N + (size_t)x * N + y] =
+      h < H ? to_f32(proj[pos * PW + 4 * H * d + h]) : 0.f;
+  if (h == 0) {
+    const int line = transpose ? y : x, tok = transpose ? x : y;
+    MA[((size_t)b * N + line) * N + tok] = (mask[pos] - 1.0f) * 1e9f;
+  }
+}
+
+// og[pos][j] *= sigmoid(g[pos][j]) in place, g the gate columns of the projection; 8 columns
+// per thread (H d a multiple of 8).
+template <class TC>
+__global__ __launch_bounds__(256) void grid_gen_gate_inplace_kernel(TC* __restrict__ og, const TC* __restrict__ proj,
+                                                                    long M, int HD, int PW) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const int nc = HD / 8;
+  if (idx >= M * nc) return;
+  const long pos = idx / nc;
+  const int j = (int)(idx % nc) * 8;
+  TC* o = og + pos * HD + j;
+  const TC* g = proj + pos * PW + 3 * HD + j;
+  float r[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = to_f32(o[e]) * sigmoidf_(to_f32(g[e]));
+  store_vec<TC, 8>(o, r);
+}
+
 template <class TZ, class TC>
 int grid_attn_generic_launch(const void* z, const float* mask, const float* lnw, const float* lnb, float eps,
                              const void* w5, const void* wo, int B, int N, int C, int H, int transpose, void* out,
@@ -1820,6 +1859,33 @@ int grid_attn_generic_launch(const void* z, const float* mask, const float* lnw,
   TC* og = reinterpret_cast<TC*>(base + L.og);
   if (int e = ln_launch<TZ, TC>(z, lnw, lnb, eps, xn, M, C, s)) return e;
   if (int e = rowgemm_launch<TC, TC, EPI_STORE>(xn, w5, nullptr, 0, proj, M, PW, C, s)) return e;
+  if (d == kHeadDim && H % 4 == 0) {
+    // Heads of the flash kernel's width in whole groups of four: the attention reads q, k, v
+    // straight from the projection rows and writes o into og's rows (strided), so nothing
+    // is repacked into a head-major layout and back. Element (b, line, head, token, e) of
+    // q sits at proj[pos (b, x, y)][head d + e] with (x, y) = (line, token) for rows and
+    // (token, line) for columns; o goes to og[pos][head d + e].
+    grid_gen_bias_kernel<TC><<<(unsigned)((M * H4 + 255) / 256), 256, 0, s>>>(proj, mask, PB, MA, B, N, H, H4, d, PW,
+                                                                               transpose);
+    if (int e = pf::check_launch("grid_gen_bias")) return e;
+    const int HD = H * d;
+    const long NN = (long)N * N;
+    const Strides4 sx = transpose ? Strides4{NN * PW, (long)PW, (long)d, (long)N * PW}
+                                  : Strides4{NN * PW, (long)N * PW, (long)d, (long)PW};
+    const Strides4 so = transpose ? Strides4{NN * HD, (long)HD, (long)d, (long)N * HD}
+                                  : Strides4{NN * HD, (long)N * HD, (long)d, (long)HD};
+    for (int g = 0; g < H / 4; ++g) {
+      const size_t hoff = (size_t)g * 4 * d;
+      if (int e = evo_attn_launch<TC>(proj + hoff, proj + HD + hoff, proj + 2 * HD + hoff, MA,
+                                      PB + (size_t)g * B * 4 * N * N, B, N, N, 0, og + hoff, base + L.evo, s,
+                                      1.0f / sqrtf((float)d), &sx, &so))
+        return e;
+    }
+    grid_gen_gate_inplace_kernel<TC><<<(unsigned)((M * (HD / 8) + 255) / 256), 256, 0, s>>>(og, proj, M, HD, PW);
+    if (int e = pf::check_launch("grid_gen_gate")) return e;
+    if (accumulate) return rowgemm_launch<TC, TZ, EPI_RESIDUAL>(og, wo, nullptr, 0, out, M, C, HD, s);
+    return rowgemm_launch<TC, TZ, EPI_STORE>(og, wo, nullptr, 0, out, M, C, HD, s);
+  }
   grid_gen_pack_kernel<TC><<<(unsigned)((M * H4 * 4 + 255) / 256), 256, 0, s>>>(proj, mask, Q, K, V, PB, MA, B, N, H,
                                                                                 H4, d, PW, transpose);
   if (int e = pf::check_launch("grid_gen_pack")) return e;

@@ -32,6 +32,53 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const TI* __restrict__ x, 
   for (int c = l; c < C; c += 64) dst[c] = from_f32<TO>((to_f32(src[c]) - mean) * rstd * w[c] + b[c]);
 }
 
+// LayerNorm rows with 8 elements per lane (16-byte bf16 loads): C / 8 lanes per row, 64 / (C / 8)
+// rows per wave, statistics by shuffles within the row's lanes. C in {64, 128, 256, 512}.
+template <class TI, class TO, int C>
+__global__ __launch_bounds__(256) void ln_rows_vec_kernel(const TI* __restrict__ x, const float* __restrict__ w,
+                                                          const float* __restrict__ b, float eps, TO* __restrict__ out,
+                                                          long M) {
+  constexpr int LPR = C / 8;
+  constexpr int RPW = 64 / LPR;
+  static_assert(LPR >= 8 && LPR <= 64 && 64 % LPR == 0, "8 to 64 lanes per row");
+  const int l = lane_id();
+  const long row = ((long)blockIdx.x * 4 + wave_id()) * RPW + l / LPR;
+  if (row >= M) return;  // whole row groups leave together: the shuffles stay within a group
+  const int c0 = (l % LPR) * 8;
+  const TI* src = x + row * C + c0;
+  float v[8];
+  if constexpr (sizeof(TI) == 2) {
+    load16<TI>(src, v);
+  } else {
+    float a[4], bb[4];
+    load16<TI>(src, a);
+    load16<TI>(src + 4, bb);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = a[e], v[e + 4] = bb[e];
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s += v[e];
+  const float mean = group_sum<LPR>(s) / C;
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float d = v[e] - mean;
+    q += d * d;
+  }
+  const float rstd = rsqrtf(group_sum<LPR>(q) / C + eps);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = (v[e] - mean) * rstd * w[c0 + e] + b[c0 + e];
+  TO* dst = out + row * C + c0;
+  if constexpr (sizeof(TO) == 2) {
+    store_vec<TO, 8>(dst, y);
+  } else {
+    store_vec<TO, 4>(dst, y);
+    store_vec<TO, 4>(dst + 4, y + 4);
+  }
+}
+
 // ------------------------------------------------------------------ row GEMM
 enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2 };
 
@@ -107,6 +154,17 @@ __global__ __launch_bounds__(256) void rowgemm_kernel(const TC* __restrict__ A, 
 
 template <class TI, class TO>
 int ln_launch(const void* x, const float* w, const float* b, float eps, void* out, long M, int C, hipStream_t s) {
+  if (pf::aligned16(x) && pf::aligned16(out) && (C == 64 || C == 128 || C == 256 || C == 512)) {
+    const long rows_per_block = 4L * (64 / (C / 8));
+    const unsigned grid = (unsigned)((M + rows_per_block - 1) / rows_per_block);
+    switch (C) {
+      case 64: ln_rows_vec_kernel<TI, TO, 64><<<grid, 256, 0, s>>>((const TI*)x, w, b, eps, (TO*)out, M); break;
+      case 128: ln_rows_vec_kernel<TI, TO, 128><<<grid, 256, 0, s>>>((const TI*)x, w, b, eps, (TO*)out, M); break;
+      case 256: ln_rows_vec_kernel<TI, TO, 256><<<grid, 256, 0, s>>>((const TI*)x, w, b, eps, (TO*)out, M); break;
+      default: ln_rows_vec_kernel<TI, TO, 512><<<grid, 256, 0, s>>>((const TI*)x, w, b, eps, (TO*)out, M); break;
+    }
+    return pf::check_launch("ln_rows");
+  }
   ln_rows_kernel<TI, TO><<<(unsigned)((M + 3) / 4), 256, 0, s>>>((const TI*)x, w, b, eps, (TO*)out, M, C);
   return pf::check_launch("ln_rows");
 }
