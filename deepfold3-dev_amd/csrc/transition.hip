@@ -777,9 +777,93 @@ __global__ __launch_bounds__(256) void single_to_pair_generic_kernel(const TZ* _
   if (l < kS2pHeads) logits[((row / NN) * kS2pHeads + l) * NN + row % NN] = mine;
 }
 
+// bf16 operands, C in {64, 256}: 16 positions per wave. The wave LayerNorms its rows with
+// C / 8 lanes per row (16-byte loads), stores the normalised rows rounded to bf16 in its LDS
+// tile, and one 16x16 MFMA block per 32 channels gives the 16 positions x 16 heads logits
+// (W [16][C] fragments from L1).
+template <class TZ, int C>
+__global__ __launch_bounds__(256) void single_to_pair_mfma_kernel(const TZ* __restrict__ z,
+                                                                  const float* __restrict__ lnw,
+                                                                  const float* __restrict__ lnb, float eps,
+                                                                  const bf16* __restrict__ w, float* __restrict__ logits,
+                                                                  long M, long NN) {
+  constexpr int LPR = C / 8;
+  constexpr int RPP = 64 / LPR;  // rows per pass
+  constexpr int LDC = C + 8;
+  static_assert(C % 64 == 0 && C <= 256, "64 to 256 channels");
+  __shared__ __attribute__((aligned(16))) bf16 tile[4][16 * LDC];
+  const int wv = wave_id();
+  const int l = lane_id();
+  bf16* t = tile[wv];
+  const long r0 = ((long)blockIdx.x * 4 + wv) * 16;
+  const int c0 = (l % LPR) * 8;
+#pragma unroll
+  for (int pass = 0; pass < 16 / RPP; ++pass) {
+    const int rr = pass * RPP + l / LPR;
+    const long row = min(r0 + rr, M - 1);
+    const TZ* src = z + row * C + c0;
+    float v[8];
+    if constexpr (sizeof(TZ) == 2) {
+      load16<TZ>(src, v);
+    } else {
+      float a[4], b[4];
+      load16<TZ>(src, a);
+      load16<TZ>(src + 4, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = a[e], v[e + 4] = b[e];
+    }
+    float sm = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm += v[e];
+    const float mean = group_sum<LPR>(sm) / C;
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = v[e] - mean;
+      q += d * d;
+    }
+    const float rstd = rsqrtf(group_sum<LPR>(q) / C + eps);
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (v[e] - mean) * rstd * lnw[c0 + e] + lnb[c0 + e];
+    store_vec<bf16, 8>(t + rr * LDC + c0, y);
+  }
+  __syncthreads();  // the tile's rows are in LDS
+  using MF = Mfma<bf16>;
+  const int r = l & 15;
+  const int kq = (l >> 4) * MF::KPL;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k0 = 0; k0 < C; k0 += MF::K16) {
+    const MF::Frag af = MF::load(t + r * LDC + k0 + kq);
+    const MF::Frag bf = MF::load(w + (size_t)r * C + k0 + kq);
+    MF::mma16(acc, af, bf);
+  }
+  // acc[e]: position r0 + 4 (l >> 4) + e, head l & 15
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const long row = r0 + 4 * (l >> 4) + e;
+    if (row < M) logits[((row / NN) * kS2pHeads + r) * NN + row % NN] = acc[e];
+  }
+}
+
 template <class TZ, class TC>
 int s2p_generic_launch(const void* z, const float* lnw, const float* lnb, float eps, const void* w, float* logits,
                        long M, long NN, int C, hipStream_t s) {
+  if constexpr (sizeof(TC) == 2) {
+    const bool al = pf::aligned16(z) && pf::aligned16(w);
+    const unsigned grid = (unsigned)((M + 63) / 64);
+    if (al && C == 256) {
+      single_to_pair_mfma_kernel<TZ, 256><<<grid, 256, 0, s>>>((const TZ*)z, lnw, lnb, eps, (const bf16*)w, logits,
+                                                               M, NN);
+      return pf::check_launch("single_to_pair");
+    }
+    if (al && C == 64) {
+      single_to_pair_mfma_kernel<TZ, 64><<<grid, 256, 0, s>>>((const TZ*)z, lnw, lnb, eps, (const bf16*)w, logits, M,
+                                                              NN);
+      return pf::check_launch("single_to_pair");
+    }
+  }
   single_to_pair_generic_kernel<TZ, TC><<<(unsigned)((M + 3) / 4), 256, 0, s>>>((const TZ*)z, lnw, lnb, eps,
                                                                                  (const TC*)w, logits, M, NN, C);
   return pf::check_launch("single_to_pair");

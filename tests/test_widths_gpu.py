@@ -28,6 +28,7 @@ W = mod("weights")
 ops = mod("ops")
 attention = mod("attention")
 evoformer = mod("evoformer")
+kernels = mod("kernels")
 BF = torch.bfloat16
 
 
@@ -173,3 +174,23 @@ def test_pairformer_block_c256_bf16_rule(dev):
         rp, rs = R.pairformer_block(z.float(), single.float(), pm, sm, to(sd, dev))
     print("[PairFormer block C=256 bf16]", assert_bf16_rule(p.cpu(), ep.cpu(), rp.cpu(), "pair"),
           assert_bf16_rule(s.cpu(), es.cpu(), rs.cpu(), "single"), flush=True)  # fmt: skip
+
+
+@pytest.mark.parametrize("stream_dtype", [torch.float32, BF], ids=["fp32-stream", "bf16-stream"])
+@pytest.mark.parametrize("c", [64, 256])
+def test_single_to_pair_widths_bf16_rule(dev, c, stream_dtype):
+    """The standalone single_to_pair at 64 and 256 channels with bf16 GEMM operands (16
+    positions per wave on MFMAs), 70 tokens (a ragged last group of positions)."""
+    n = 70
+    sd = W.make_block_weights(47, perturb_affine=True, c_pair=c)
+    p = {k: v for k, v in sd.items() if k.startswith("single_to_pair")}
+    z = _z(n, c, 11)
+    with torch.no_grad():
+        got = kernels.single_to_pair(z.to(dev, stream_dtype), p["single_to_pair_norm.weight"].to(dev),
+                                     p["single_to_pair_norm.bias"].to(dev), 1e-5,
+                                     p["single_to_pair.weight"].to(dev, BF))  # fmt: skip
+        with torch.autocast("cuda", dtype=BF):
+            eager = R.single_to_pair(z.to(dev, stream_dtype), to(p, dev, stream_dtype))
+        ref = R.single_to_pair(z, p)
+    print(f"[single_to_pair width] C={c} stream={stream_dtype}",
+          assert_bf16_rule(got.cpu(), eager.float().cpu(), ref, f"single_to_pair C={c}"), flush=True)  # fmt: skip
