@@ -1513,4 +1513,21 @@ int pf_trimul_train_fwd(const void* x, const float* mask, const void* w_packed, 
   return run(std::integral_constant<int, 128>{});
 }
 
+int pf_planes_contract(const void* A, const void* Bm, void* X, int G, int Np, int dtype, void* stream) {
+  PF_REQUIRE(A && Bm && X && X != A && X != Bm, PF_ERR_INVALID_ARG, "pf_planes_contract: null or aliased pointers");
+  PF_REQUIRE(G > 0 && Np > 0 && Np % 128 == 0, PF_ERR_INVALID_ARG, "pf_planes_contract: G=%d Np=%d (a multiple of 128)",
+             G, Np);
+  PF_REQUIRE(dtype == PF_F32 || dtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_planes_contract: dtype %d", dtype);
+  PF_REQUIRE(pf::aligned16(A) && pf::aligned16(Bm) && pf::aligned16(X), PF_ERR_ALIGNMENT,
+             "pf_planes_contract: pointers must be 16-byte aligned");
+  hipStream_t s = pf::as_stream(stream);
+  const int remap = (G % 8 == 0) ? 1 : 0;
+  if (dtype == PF_BF16) {
+    if (Np % 768 == 0) return contract_persistent_launch<384>(A, Bm, X, G, Np, remap, s);
+    if (Np % 256 == 0) return contract_persistent_launch<256>(A, Bm, X, G, Np, remap, s);
+    return contract_generic_launch<bf16>(A, Bm, X, G, Np, remap, s);
+  }
+  return contract_generic_launch<float>(A, Bm, X, G, Np, remap, s);
+}
+
 }  // extern "C"

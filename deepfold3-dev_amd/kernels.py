@@ -537,14 +537,19 @@ class FusedTriMulFunction(torch.autograd.Function):
         d_out = _weight_grad_tm(gp, xln)
         d_out_gate = _weight_grad_tm(gg, xb)
         del gp, gg, xln
-        # X = P Q^T per channel plane: dP = dX Q, dQ = dX^T P (contiguous operands)
-        dpl = torch.empty((2, B * C, Np, Np), dtype=cdt, device=dev)
-        torch.bmm(dX, pl[1], out=dpl[0])
+        # X = P Q^T per channel plane: dP = dX Q = contract(dX, Q^T), dQ = dX^T P =
+        # contract(dX^T, P^T), on the forward's contraction kernels.
+        G = B * C
+        dpl = torch.empty((2, G, Np, Np), dtype=cdt, device=dev)
+        tp = torch.empty((G, Np, Np), dtype=cdt, device=dev)
+        _lib.call("pf_planes_transpose", pl[1].data_ptr(), tp.data_ptr(), G, Np, code_c, stream)
+        _lib.call("pf_planes_contract", dX.data_ptr(), tp.data_ptr(), dpl[0].data_ptr(), G, Np, code_c, stream)
+        _lib.call("pf_planes_transpose", pl[0].data_ptr(), tp.data_ptr(), G, Np, code_c, stream)
         dXt = torch.empty_like(dX)
-        _lib.call("pf_planes_transpose", dX.data_ptr(), dXt.data_ptr(), B * C, Np, code_c, stream)
+        _lib.call("pf_planes_transpose", dX.data_ptr(), dXt.data_ptr(), G, Np, code_c, stream)
         del dX
-        torch.bmm(dXt, pl[0], out=dpl[1])
-        del dXt
+        _lib.call("pf_planes_contract", dXt.data_ptr(), tp.data_ptr(), dpl[1].data_ptr(), G, Np, code_c, stream)
+        del dXt, tp
         gpg = torch.empty((M, 4 * C), dtype=cdt, device=dev)  # token-major, the kernel's walk order
         xw = None if ctx.outgoing else torch.empty((M, C), dtype=cdt, device=dev)  # x in that order
         dx = torch.empty_like(xc)

@@ -169,7 +169,12 @@ int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const 
  * G^T xw (incoming). C = 64, 128 or 256.
  *
  * pf_planes_transpose: dst[g] = src[g]^T for G planes [Np][Np] (Np a multiple of 64), the
- * dX^T operand of dQ = dX^T P. */
+ * dX^T operand of dQ = dX^T P.
+ *
+ * pf_planes_contract: X[g] = A[g] B[g]^T for G planes [Np][Np] (k contiguous, Np a multiple of
+ * 128), on the forward's contraction kernels (K2). The VJP of X = P Q^T takes its cotangents
+ * from it with transposed planes: dP = contract(dX, Q^T), dQ = contract(dX^T, P^T) (the
+ * reference's backward forms both inside triton/fused_trimul.py:262-330). */
 int pf_trimul_train_pack_weights(const void* w_proj, const void* w_gate, int wdtype, void* packed, int C, int cdtype,
                                  void* stream);
 int pf_trimul_train_fwd(const void* x, const float* mask, const void* w_packed, const float* ln_out_w,
@@ -186,6 +191,7 @@ int pf_trimul_project_vjp(const void* dplanes, const void* x, const float* mask,
                           const void* w_packed_t, const float* gx_in, int B, int N, int C, int outgoing, int xdtype,
                           int cdtype, void* gpg, void* xw, void* dx, void* stream);
 int pf_planes_transpose(const void* src, void* dst, int G, int Np, int dtype, void* stream);
+int pf_planes_contract(const void* A, const void* B, void* X, int G, int Np, int dtype, void* stream);
 
 
 /* ---- triangle attention (starting / ending node) ------------------------ */

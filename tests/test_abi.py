@@ -86,3 +86,14 @@ def test_dropout_entry_points_validate_before_launch():
     assert lib.pf_dropout_add_fwd(d + 4, 0, d, 0, d, 1, 4, 4, 8, 1, 0.25, 1, None) == 4  # fp32 not 16-aligned
     # nothing to do: status OK without a launch
     assert lib.pf_dropout_add_fwd(d, 1, d, 1, d, 0, 4, 4, 8, 0, 0.25, 1, None) == 0
+
+
+def test_planes_contract_validates_before_launch():
+    """Null, aliased, misaligned and badly sized plane contractions are refused on the host."""
+    lib = _lib.lib()
+    d = 256
+    assert lib.pf_planes_contract(None, d, d + 4096, 2, 128, 1, None) == 1  # null
+    assert lib.pf_planes_contract(d, d, d, 2, 128, 1, None) == 1  # X aliases A
+    assert lib.pf_planes_contract(d, d + 4096, d + 8192, 2, 96, 1, None) == 1  # Np % 128
+    assert b"multiple of 128" in lib.pf_last_error()
+    assert lib.pf_planes_contract(d + 2, d + 4096, d + 8192, 2, 128, 1, None) == 4  # misaligned
