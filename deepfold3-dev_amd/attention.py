@@ -11,6 +11,8 @@ single-track kernels (``csrc/single.hip``).
 
 from __future__ import annotations
 
+import math
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -239,8 +241,6 @@ class SingleAttention(nn.Module):
     ):
         super().__init__()
         require_hip("SingleAttention", optim)
-        if pair_bias_gate:
-            raise NotActive("SingleAttention", "the per-head pair-bias gate is not built")
         if key_dim != value_dim or key_dim != c or key_dim // num_heads != 24:
             raise NotActive("SingleAttention", "built for key_dim = value_dim = c with head dim 24")
         self.num_heads = num_heads
@@ -248,7 +248,14 @@ class SingleAttention(nn.Module):
         self.val_dim_per_head = value_dim // num_heads
         self.scale = self.key_dim_per_head**-0.5
         self.norm = LayerNorm(c)
-        self.register_parameter("pair_bias_gate_a", None)
+        # Per-head pair-bias gate (attention.py:392-398): tau_h = exp(a_h) scales head h's pair
+        # logits, a_h starting at log(tau_0).
+        if pair_bias_gate:
+            if not pair_bias_gate_init_tau > 0.0:
+                raise ValueError(f"pair_bias_gate_init_tau={pair_bias_gate_init_tau}: tau_0 must be positive")
+            self.pair_bias_gate_a = nn.Parameter(torch.full((num_heads,), math.log(float(pair_bias_gate_init_tau))))
+        else:
+            self.register_parameter("pair_bias_gate_a", None)
         self.to_q = nn.Linear(c, key_dim)
         from .primitives import af3_linear_init_
 
@@ -318,7 +325,17 @@ class SingleAttention(nn.Module):
         w_out = self.out_proj.weight if scale == 1.0 else self.out_proj.weight * scale
         return F.linear(o * g, w_out)
 
+    def _gated(self, pair_logits: torch.Tensor) -> torch.Tensor:
+        """Head h's pair logits times tau_h = exp(a_h) in their dtype (``attention.py:422-424``);
+        differentiable in a under grad. Without the gate, the logits themselves."""
+        if self.pair_bias_gate_a is None:
+            return pair_logits
+        H = self.num_heads
+        tau = torch.exp(self.pair_bias_gate_a).to(pair_logits.dtype)
+        return pair_logits * tau.view(*([1] * (pair_logits.dim() - 3)), H, 1, 1)
+
     def _update(self, x, mask, pair_logits, scale: float) -> torch.Tensor:
+        pair_logits = self._gated(pair_logits)
         has_batch = x.dim() == 3
         if not has_batch:
             x, mask, pair_logits = x.unsqueeze(0), mask.unsqueeze(0), pair_logits.unsqueeze(0)
@@ -343,4 +360,4 @@ class SingleAttention(nn.Module):
         """``x += branch_scale * update`` in place."""
         if not x.is_contiguous():
             raise NotActive("SingleAttention", "in-place residual needs a contiguous x")
-        return self._run(x, mask, pair_logits, x, True, self.branch_scale)
+        return self._run(x, mask, self._gated(pair_logits), x, True, self.branch_scale)

@@ -46,10 +46,12 @@ def block_param_spec(
     factor: int = TRANSITION_FACTOR,
     use_triangle_attention: bool = True,
     use_single_track: bool = True,
+    pair_bias_gate: bool = False,
 ) -> list[tuple[str, tuple[int, ...], str]]:
-    """Ordered ``(key, shape, kind)`` for one PairFormerBlock; kind is ln_w, ln_b, linear or bias.
-    A block without triangle attention has no ``pair_attn_*`` keys, one without the single
-    track no ``single_*`` keys (``evoformer.py:226-249``)."""
+    """Ordered ``(key, shape, kind)`` for one PairFormerBlock; kind is ln_w, ln_b, linear, bias
+    or log_tau (the single attention's per-head pair-bias gate, ``attention.py:392-398``,
+    initialised to log 0.25). A block without triangle attention has no ``pair_attn_*`` keys,
+    one without the single track no ``single_*`` keys (``evoformer.py:226-249``)."""
     c, cs = c_pair, c_single
     spec: list[tuple[str, tuple[int, ...], str]] = []
     for p in ("tri_mul_out.", "tri_mul_in."):
@@ -91,6 +93,7 @@ def block_param_spec(
         ("single_attn.to_v.weight", (single_value_dim, cs), "linear"),
         ("single_attn.to_g.weight", (single_value_dim, cs), "linear"),
         ("single_attn.out_proj.weight", (cs, single_value_dim), "linear"),
+        *([("single_attn.pair_bias_gate_a", (num_single_heads,), "log_tau")] if pair_bias_gate else []),
         ("single_transition.norm.weight", (cs,), "ln_w"),
         ("single_transition.norm.bias", (cs,), "ln_b"),
         ("single_transition.linear1.weight", (2 * factor * cs, cs), "linear"),
@@ -121,6 +124,10 @@ def make_block_weights(seed: int, perturb_affine: bool = False, **spec_kwargs) -
             t.fill_(1.0)
             if perturb_affine:
                 t.add_(0.1 * torch.randn(shape, generator=gen))
+        elif kind == "log_tau":
+            t.fill_(math.log(0.25))
+            if perturb_affine:
+                t.add_(0.5 * torch.randn(shape, generator=gen))
         else:  # ln_b, bias
             t.zero_()
             if perturb_affine:

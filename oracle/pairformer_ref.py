@@ -204,7 +204,10 @@ def single_to_pair(z: torch.Tensor, p: dict[str, torch.Tensor]) -> torch.Tensor:
 def single_attention(
     s: torch.Tensor, seq_mask: torch.Tensor, pair_logits: torch.Tensor, p: dict[str, torch.Tensor], num_heads: int = 16
 ) -> torch.Tensor:
-    """``SingleAttention.forward`` (``attention.py:415-452``), no pair-bias gate."""
+    """``SingleAttention.forward`` (``attention.py:415-452``). With ``pair_bias_gate_a`` in ``p``
+    (the per-head pair-bias gate, ``attention.py:392-398``) the pair logits of head h are
+    multiplied by tau_h = exp(a_h), cast to their dtype, before they join q k^T
+    (``attention.py:422-424``)."""
     B, N, C = s.shape
     H = num_heads
     Dk = p["to_q.weight"].shape[0] // H
@@ -214,6 +217,8 @@ def single_attention(
     k = F.linear(xn, p["to_k.weight"]).view(B, N, H, Dk).permute(0, 2, 1, 3)
     v = F.linear(xn, p["to_v.weight"]).view(B, N, H, Dv).permute(0, 2, 1, 3).contiguous()
     logits = torch.matmul(q * Dk**-0.5, k.transpose(-2, -1).contiguous())
+    if "pair_bias_gate_a" in p:
+        pair_logits = pair_logits * torch.exp(p["pair_bias_gate_a"]).to(pair_logits.dtype).view(1, H, 1, 1)
     logits = logits + pair_logits
     logits = logits + (1e9 * (seq_mask.float() - 1.0)).view(B, 1, 1, N)
     w = F.softmax(logits.float(), dim=-1).to(xn.dtype)

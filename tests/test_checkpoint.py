@@ -172,7 +172,6 @@ def test_loading_is_strict(tmp_path):
 @pytest.mark.parametrize(
     "field,value,needle",
     [
-        ("pair_bias_gate", True, "pair-bias gate"),
         ("branch_scaler", "rmsnorm", "branch_scaler"),
         ("trimul_num_heads", 2, "multi-head"),
     ],
@@ -181,6 +180,18 @@ def test_unbuilt_architectures_refuse_by_name(field, value, needle):
     cfg = {"pairformer": {"num_layer": 1, field: value}}
     with pytest.raises(guard.NotActive, match=needle):
         ck.build_trunk(cfg)
+
+
+def test_pair_bias_gate_builds_with_its_key_and_init():
+    """pair_bias_gate (attention.py:392-398): a [16] parameter single_attn.pair_bias_gate_a per
+    block, initialised to log(pair_bias_gate_init_tau); a non-positive tau_0 is refused."""
+    trunk = ck.build_trunk({"pairformer": {"num_layer": 2, "pair_bias_gate": True, "pair_bias_gate_init_tau": 0.5}})
+    keys = [k for k in trunk.state_dict() if k.endswith("pair_bias_gate_a")]
+    assert keys == ["blocks.0.single_attn.pair_bias_gate_a", "blocks.1.single_attn.pair_bias_gate_a"]
+    a = trunk.state_dict()[keys[0]]
+    assert a.shape == (16,) and torch.allclose(a, torch.full((16,), math.log(0.5)))
+    with pytest.raises(ValueError, match="tau_0 must be positive"):
+        ck.build_trunk({"pairformer": {"num_layer": 1, "pair_bias_gate": True, "pair_bias_gate_init_tau": 0.0}})
 
 
 # The reference's current stage-0 model shape (configs/stage0.yaml:50-75): 256 pair channels in 8

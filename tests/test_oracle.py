@@ -774,3 +774,24 @@ def test_evoformer_block_without_triangle_attention():
         m4, z4 = R.evoformer_block(msa, x["pair"], mmask, x["pair_mask"], {**sd, "row_attn.out_proj.weight": torch.zeros(64, 64)})
     assert torch.equal(m1, m2) and torch.equal(z1, z2)
     assert torch.equal(m3, m4) and torch.equal(z3, z4)
+
+
+def test_pair_bias_gate_pins():
+    """The per-head pair-bias gate (attention.py:392-398, :422-424): a = 0 (tau = 1) is the
+    ungated attention exactly; a gated block equals the ungated block whose single_to_pair
+    weight rows are scaled by tau_h (the logits are linear in that weight); a head with a
+    large tau lets its pair logits dominate that head's weights."""
+    sd = W.make_block_weights(33, perturb_affine=True, pair_bias_gate=True)
+    x = W.make_inputs(11, seed=7, pad_last=2)
+    args = (x["pair"], x["single"], x["pair_mask"], x["seq_mask"])
+    ungated = {k: v for k, v in sd.items() if k != "single_attn.pair_bias_gate_a"}
+    tau = torch.exp(sd["single_attn.pair_bias_gate_a"])
+    with torch.no_grad():
+        p0, s0 = R.pairformer_block(*args, ungated)
+        p1, s1 = R.pairformer_block(*args, {**ungated, "single_attn.pair_bias_gate_a": torch.zeros(16)})
+        assert torch.equal(p0, p1) and torch.equal(s0, s1)
+        pg, sg = R.pairformer_block(*args, sd)
+        folded = {**ungated, "single_to_pair.weight": ungated["single_to_pair.weight"] * tau[:, None]}
+        pf, sf = R.pairformer_block(*args, folded)
+        assert torch.equal(pg, p0)  # the gate touches only the single track
+        assert rel_l2(sg, sf) < 1e-6 and rel_l2(sg, s0) > 1e-4
