@@ -23,6 +23,10 @@ namespace {
 
 template <class TC>
 constexpr int trimul_bm() { return sizeof(TC) == 2 ? 64 : 32; }
+// Threads of the generic K1 / K3 blocks: 8 waves from 256 channels (each wave's accumulators
+// and LN_out columns halve; 4 waves hold 512 VGPRs per lane at C=256, one wave per SIMD).
+template <int C>
+constexpr int trimul_nt() { return C >= 256 ? 512 : 256; }
 
 // ------------------------------------------------------------------ K1
 // Packed weights w4 [4C][C]: for channel block j (16 channels), rows 64j + 16*kind + r,
@@ -30,17 +34,17 @@ constexpr int trimul_bm() { return sizeof(TC) == 2 ? 64 : 32; }
 // NORM = false takes z as already normalised (the training entry, whose input LayerNorm
 // runs outside).
 template <class TZ, class TC, int C, bool NORM = true>
-__global__ __launch_bounds__(256) void trimul_project_kernel(const TZ* __restrict__ z, const float* __restrict__ mask,
+__global__ __launch_bounds__(trimul_nt<C>()) void trimul_project_kernel(const TZ* __restrict__ z, const float* __restrict__ mask,
                                                              const float* __restrict__ lnw,
                                                              const float* __restrict__ lnb, float eps,
                                                              const TC* __restrict__ w4, TC* __restrict__ planes,
                                                              int B, int N, int Np, int outgoing) {
   constexpr int BM = trimul_bm<TC>();
-  constexpr int NT = 256;
+  constexpr int NT = trimul_nt<C>();
   constexpr int LDA = C + lds_pad<TC>();
   constexpr int SLD = BM + lds_pad<TC>();
   constexpr int RB = BM / 16;
-  constexpr int CBW = C / 16 / 4;  // channel blocks per wave
+  constexpr int CBW = C / 16 / (NT / 64);  // channel blocks per wave
   constexpr int A_BYTES = BM * LDA * (int)sizeof(TC);
   constexpr int S_BYTES = 2 * C * SLD * (int)sizeof(TC);
   __shared__ __attribute__((aligned(16))) char smem[(A_BYTES > S_BYTES ? A_BYTES : S_BYTES)];
@@ -494,19 +498,19 @@ struct OutputCfg {
   static constexpr int XS_BYTES = C * XLD * (int)sizeof(TC);
   static constexpr int A_BYTES = BM * ALD * (int)sizeof(TC);
   static constexpr int STAGE_BYTES = BM * SLD * 4;
-  static constexpr int NQ = 256 / BM;  // threads per position in the LN_out pass
+  static constexpr int NQ = trimul_nt<C>() / BM;  // threads per position in the LN_out pass
 };
 
 template <class TZ, class TC, int C, bool NORM = true>
-__global__ __launch_bounds__(256) void trimul_output_kernel(
+__global__ __launch_bounds__(trimul_nt<C>()) void trimul_output_kernel(
     const TC* __restrict__ X, const TZ* __restrict__ z, TZ* __restrict__ out, const float* __restrict__ lniw,
     const float* __restrict__ lnib, float eps_in, const float* __restrict__ lnow, const float* __restrict__ lnob,
     float eps_out, const TC* __restrict__ Wo, const TC* __restrict__ Wog, int B, int N, int Np, int accumulate) {
   using Cfg = OutputCfg<TZ, TC, C>;
   constexpr int BM = Cfg::BM, XLD = Cfg::XLD, ALD = Cfg::ALD, SLD = Cfg::SLD, NQ = Cfg::NQ;
-  constexpr int NT = 256;
+  constexpr int NT = trimul_nt<C>();
   constexpr int RB = BM / 16;
-  constexpr int CBW = C / 16 / 4;
+  constexpr int CBW = C / 16 / (NT / 64);
   constexpr int SMEM1 = Cfg::XS_BYTES + 2 * Cfg::A_BYTES;
   constexpr int SMEM = SMEM1 > Cfg::STAGE_BYTES ? SMEM1 : Cfg::STAGE_BYTES;
   __shared__ __attribute__((aligned(16))) char smem[SMEM];
@@ -1296,7 +1300,7 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
       (void)grid;
     }
     else
-      trimul_project_kernel<TZ, TC, C><<<grid, 256, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const TC*)w4,
+      trimul_project_kernel<TZ, TC, C><<<grid, trimul_nt<C>(), 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const TC*)w4,
                                                             planes, B, N, Np, outgoing);
     timer_trimul_project.stop();
     if (int e = pf::check_launch("trimul_project")) return e;
@@ -1331,7 +1335,7 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
                                                                 (const bf16*)wog, B, N, Np, accumulate);
       (void)grid;
     } else
-      trimul_output_kernel<TZ, TC, C><<<grid, 256, 0, s>>>(X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow,
+      trimul_output_kernel<TZ, TC, C><<<grid, trimul_nt<C>(), 0, s>>>(X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow,
                                                            lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
                                                            accumulate);
     timer_trimul_output.stop();
@@ -1363,7 +1367,7 @@ int trimul_train_launch(const void* x, const float* mask, const void* w4, const 
                                                                        (const bf16*)w4, (bf16*)planes, B, N, Np,
                                                                        outgoing);
   } else {
-    trimul_project_kernel<TZ, TC, C, false><<<dim3(Np / BM, Np, B), 256, 0, s>>>(
+    trimul_project_kernel<TZ, TC, C, false><<<dim3(Np / BM, Np, B), trimul_nt<C>(), 0, s>>>(
         (const TZ*)x, mask, nullptr, nullptr, 0.f, (const TC*)w4, planes, B, N, Np, outgoing);
   }
   if (int e = pf::check_launch("trimul_train_project")) return e;
@@ -1381,7 +1385,7 @@ int trimul_train_launch(const void* x, const float* mask, const void* w4, const 
     e = contract_generic_launch<TC>(P, Q, X, G, Np, remap, s);
   }
   if (e) return e;
-  trimul_output_kernel<TZ, TC, C, false><<<dim3((N + BM - 1) / BM, N, B), 256, 0, s>>>(
+  trimul_output_kernel<TZ, TC, C, false><<<dim3((N + BM - 1) / BM, N, B), trimul_nt<C>(), 0, s>>>(
       X, (const TZ*)x, (TZ*)out, nullptr, nullptr, 0.f, lnow, lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
       0);
   return pf::check_launch("trimul_train_output");
