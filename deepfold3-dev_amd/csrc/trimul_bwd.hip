@@ -31,19 +31,23 @@ template <class TC, int C>
 constexpr int vjp_bm() {
   return std::min(64, 16384 / (C * (int)sizeof(TC)));
 }
+// Threads of the generic VJP blocks: 8 waves from 256 channels, so each wave's accumulators
+// halve (with 4 waves the project VJP held 320 VGPRs per lane at C=256, one wave per SIMD).
+template <int C>
+constexpr int vjp_nt() { return C >= 256 ? 512 : 256; }
 
 // ------------------------------------------------------------------ output VJP
 template <class TZ, class TC, int C>
-__global__ __launch_bounds__(256) void trimul_output_vjp_kernel(
+__global__ __launch_bounds__(vjp_nt<C>()) void trimul_output_vjp_kernel(
     const TZ* __restrict__ g, const TC* __restrict__ X, const TZ* __restrict__ x, const float* __restrict__ lnow,
     const float* __restrict__ lnob, float eps, const TC* __restrict__ Wo, const TC* __restrict__ Wog,
     const TC* __restrict__ WoT, const TC* __restrict__ WogT, int B, int N, int Np, TC* __restrict__ gp_out,
     TC* __restrict__ gg_out, TC* __restrict__ xln_out, TC* __restrict__ dX, float* __restrict__ gx,
     float* __restrict__ partial) {
   constexpr int BM = vjp_bm<TC, C>();
-  constexpr int NT = 256;
+  constexpr int NT = vjp_nt<C>();
   constexpr int RB = BM / 16;
-  constexpr int CBW = C / 64;  // 16-channel blocks per wave
+  constexpr int CBW = C / 16 / (NT / 64);  // 16-channel blocks per wave
   constexpr int XLD = BM + lds_pad<TC>();
   constexpr int ALD = C + lds_pad<TC>();
   constexpr int SLD = C + 4;
@@ -531,7 +535,7 @@ __global__ __launch_bounds__(256) void trimul_ln_grad_reduce_kernel(const float*
 // Packed weights w4 [4C][C] as the forward K1 reads them (16-channel blocks, rows
 // 64 j + 16 kind + r: a proj, a gate, b proj, b gate); w4t = w4^T [C][4C].
 template <class TZ, class TC, int C>
-__global__ __launch_bounds__(256) void trimul_project_vjp_kernel(const TC* __restrict__ dplanes,
+__global__ __launch_bounds__(vjp_nt<C>()) void trimul_project_vjp_kernel(const TC* __restrict__ dplanes,
                                                                  const TZ* __restrict__ x,
                                                                  const float* __restrict__ mask,
                                                                  const TC* __restrict__ w4,
@@ -540,9 +544,9 @@ __global__ __launch_bounds__(256) void trimul_project_vjp_kernel(const TC* __res
                                                                  int Np, int outgoing, TC* __restrict__ gpg,
                                                                  TC* __restrict__ xw, TZ* __restrict__ dx) {
   constexpr int BM = vjp_bm<TC, C>();
-  constexpr int NT = 256;
+  constexpr int NT = vjp_nt<C>();
   constexpr int RB = BM / 16;
-  constexpr int CBW = C / 64;
+  constexpr int CBW = C / 16 / (NT / 64);
   constexpr int LDA = C + lds_pad<TC>();
   constexpr int SLD = BM + lds_pad<TC>();
   constexpr int GLD = 4 * C + lds_pad<TC>();
@@ -925,7 +929,7 @@ int output_vjp_launch(const void* g, const void* X, const void* x, const float* 
   }
   constexpr int BM = vjp_bm<TC, C>();
   const dim3 grid(Np / BM, Np, B);
-  trimul_output_vjp_kernel<TZ, TC, C><<<grid, 256, 0, s>>>(
+  trimul_output_vjp_kernel<TZ, TC, C><<<grid, vjp_nt<C>(), 0, s>>>(
       (const TZ*)g, (const TC*)X, (const TZ*)x, lnow, lnob, eps, (const TC*)wo, (const TC*)wog, (const TC*)wot,
       (const TC*)wogt, B, N, Np, (TC*)gp, (TC*)gg, (TC*)xln, (TC*)dX, gx, partial);
   if (int e = pf::check_launch("trimul_output_vjp")) return e;
@@ -948,7 +952,7 @@ int project_vjp_launch(const void* dplanes, const void* x, const float* mask, co
     return pf::check_launch("trimul_project_vjp");
   }
   constexpr int BM = vjp_bm<TC, C>();
-  trimul_project_vjp_kernel<TZ, TC, C><<<dim3(Np / BM, Np, B), 256, 0, s>>>(
+  trimul_project_vjp_kernel<TZ, TC, C><<<dim3(Np / BM, Np, B), vjp_nt<C>(), 0, s>>>(
       (const TC*)dplanes, (const TZ*)x, mask, (const TC*)w4, (const TC*)w4t, gx_in, B, N, Np, outgoing, (TC*)gpg,
       (TC*)xw, (TZ*)dx);
   return pf::check_launch("trimul_project_vjp");
