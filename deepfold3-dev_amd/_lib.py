@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple] = {
     "pf_trimul_project_vjp": (_i, [_vp] * 6 + [_i] * 6 + [_vp] * 4),
     "pf_planes_transpose": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "pf_planes_contract": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "pf_rms_residual_add": (_i, [_vp, _i, _vp, _i, _vp, _l, _i, _f, _f, _vp]),
     "pf_trimul_fwd": (
         _i,
         [_vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],

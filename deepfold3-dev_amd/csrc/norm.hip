@@ -287,7 +287,57 @@ int ln_dispatch(const void* x, const float* w, const float* b, float eps, void* 
 
 }  // namespace
 
+// out[m] = res[m] + scale * x[m] / sqrt(mean_c x[m][c]^2 + eps): the RMSNorm branch scaler
+// (non-learnable unit-RMS rows) and the residual add in one pass; one wave per row, fp32
+// arithmetic, one rounding to the residual's dtype. out may alias res or x (each element is read
+// and written by the same lane).
+template <class TR, class TX>
+__global__ __launch_bounds__(256) void rms_residual_add_kernel(const TR* res, const TX* x, TR* out,
+                                                               long M, int C, float scale, float eps) {
+  const long row = (long)blockIdx.x * 4 + wave_id();
+  if (row >= M) return;
+  const int l = lane_id();
+  const TX* xr = x + row * C;
+  float q = 0.f;
+  for (int c = l; c < C; c += 64) {
+    const float v = to_f32(xr[c]);
+    q += v * v;
+  }
+  const float r = scale * rsqrtf(group_sum<64>(q) / C + eps);
+  TR* o = out + row * C;
+  if (res == nullptr) {
+    for (int c = l; c < C; c += 64) o[c] = from_f32<TR>(to_f32(xr[c]) * r);
+    return;
+  }
+  const TR* rr = res + row * C;
+  for (int c = l; c < C; c += 64) o[c] = from_f32<TR>(to_f32(rr[c]) + to_f32(xr[c]) * r);
+}
+
 extern "C" {
+
+int pf_rms_residual_add(const void* res, int res_dtype, const void* x, int x_dtype, void* out, long M, int C,
+                        float scale, float eps, void* stream) {
+  PF_REQUIRE(x && out, PF_ERR_INVALID_ARG, "pf_rms_residual_add: null pointer");
+  PF_REQUIRE(M >= 0 && C > 0, PF_ERR_INVALID_ARG, "pf_rms_residual_add: M=%ld C=%d", M, C);
+  PF_REQUIRE((res_dtype == PF_F32 || res_dtype == PF_BF16) && (x_dtype == PF_F32 || x_dtype == PF_BF16),
+             PF_ERR_UNSUPPORTED, "pf_rms_residual_add: dtypes (%d, %d)", res_dtype, x_dtype);
+  if (M == 0) return pf::ok();
+  hipStream_t s = pf::as_stream(stream);
+  const unsigned grid = (unsigned)((M + 3) / 4);
+  if (res_dtype == PF_F32 && x_dtype == PF_F32)
+    rms_residual_add_kernel<float, float><<<grid, 256, 0, s>>>((const float*)res, (const float*)x, (float*)out, M, C,
+                                                               scale, eps);
+  else if (res_dtype == PF_F32)
+    rms_residual_add_kernel<float, bf16><<<grid, 256, 0, s>>>((const float*)res, (const bf16*)x, (float*)out, M, C,
+                                                              scale, eps);
+  else if (x_dtype == PF_F32)
+    rms_residual_add_kernel<bf16, float><<<grid, 256, 0, s>>>((const bf16*)res, (const float*)x, (bf16*)out, M, C,
+                                                              scale, eps);
+  else
+    rms_residual_add_kernel<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)res, (const bf16*)x, (bf16*)out, M, C,
+                                                             scale, eps);
+  return pf::check_launch("pf_rms_residual_add");
+}
 
 int pf_layernorm_fwd(const void* x, int dtype, const float* w, const float* b, float eps, void* out, long M, int C,
                      void* stream) {

@@ -32,6 +32,7 @@ from .kernels import (
     dropout_add,
     gemm_dtype_for,
     next_dropout_seed,
+    rms_residual_add,
     single_to_pair,
 )
 from .ops import TriangleMulIncoming, TriangleMulOutgoing
@@ -79,8 +80,13 @@ class PairFormerBlock(nn.Module):
     ):
         super().__init__()
         require_hip("PairFormerBlock", optim)
-        if branch_scaler != "identity":
-            raise NotActive("PairFormerBlock", f"branch_scaler={branch_scaler!r}: only the identity scaler is built")
+        if branch_scaler not in ("identity", "rmsnorm"):
+            raise NotActive("PairFormerBlock", f"branch_scaler={branch_scaler!r}: identity and rmsnorm are built")
+        if branch_scaler != "identity" and (
+            single_transition_residual_gain is not None or pair_transition_residual_gain is not None
+        ):
+            # config.py:252-269: unit-RMS branches make branch-specific gains a rescaled block gamma
+            raise ValueError(f"branch_scaler={branch_scaler!r} takes no per-transition residual gains")
         tk = trimul_kwargs or {}
         self.tri_mul_out = TriangleMulOutgoing(c_pair, optim=optim, **tk)
         self.tri_mul_in = TriangleMulIncoming(c_pair, optim=optim, **tk)
@@ -114,8 +120,13 @@ class PairFormerBlock(nn.Module):
         self.pair_transition_residual_gain = (
             1.0 if pair_transition_residual_gain is None else float(pair_transition_residual_gain)
         )
-        self.branch_scaler_kind = "identity"
-        s_ros = self.residual_out_scale
+        # Branch scaler (evoformer.py:289-335, branch_scaler.py): "rmsnorm" makes each branch's
+        # output unit-RMS per token before s_ros multiplies it, so the scale cannot be folded
+        # into the output projections there; the branches return unscaled updates and
+        # ``_rms_add`` applies normalisation, scale and residual add in one pass.
+        self.branch_scaler_kind = str(branch_scaler)
+        self._rms = self.branch_scaler_kind == "rmsnorm"
+        s_ros = 1.0 if self._rms else self.residual_out_scale
         for m in self._pair_branches() + ([self.single_attn] if self.use_single_track else []):
             m.branch_scale = s_ros
         self.pair_transition.branch_scale = s_ros * self.pair_transition_residual_gain
@@ -141,6 +152,21 @@ class PairFormerBlock(nn.Module):
     def dropout_p(self) -> float:
         """The pair dropout rate in effect: ``pair_dropout`` in training mode, else 0."""
         return float(self.pair_dropout) if self.training else 0.0
+
+    def _rms_add_(self, res: torch.Tensor, upd: torch.Tensor) -> torch.Tensor:
+        """``res += s_ros * rms_normalize(upd)`` in place (the "rmsnorm" branch scaler)."""
+        return rms_residual_add(res, upd, self.residual_out_scale, out=res)
+
+    def _pair_site_(self, m, pair: torch.Tensor, mask: torch.Tensor, p: float, rowwise: bool) -> None:
+        """One dropped pair branch in place: the fused residual epilogue (identity scaler, eval),
+        or the branch out of place through the scaler and the shared-mask dropout-add."""
+        if not self._rms:
+            _dropout_residual_(m, pair, mask, p, rowwise)
+        elif p > 0.0:
+            b = rms_residual_add(None, m.branch(pair, mask), self.residual_out_scale)
+            dropout_add(pair, b, p, rowwise, next_dropout_seed(), out=pair)
+        else:
+            self._rms_add_(pair, m.branch(pair, mask))
 
     def _s2p_operands(self, cdt: torch.dtype):
         from .kernels import cast_weight
@@ -177,7 +203,10 @@ class PairFormerBlock(nn.Module):
         masks' seeds are drawn in branch order (``kernels.next_dropout_seed``)."""
         p = self.dropout_p()
         for m, rowwise in self._dropout_sites():
-            _dropout_residual_(m, pair, pair_mask, p, rowwise)
+            self._pair_site_(m, pair, pair_mask, p, rowwise)
+        if self._rms:
+            self._rms_add_(pair, self.pair_transition.branch(pair))
+            return self.pair_logits(pair) if self.use_single_track else None
         if not self.use_single_track:
             self.pair_transition.forward_residual_(pair)
             return None
@@ -191,6 +220,10 @@ class PairFormerBlock(nn.Module):
 
     def single_forward_(self, single: torch.Tensor, seq_mask: torch.Tensor, pair_logits: torch.Tensor) -> torch.Tensor:
         """The single half of the block, in place (``evoformer.py:322-353``)."""
+        if self._rms:
+            self._rms_add_(single, self.single_attn.branch(single, seq_mask, pair_logits))
+            self._rms_add_(single, self.single_transition.branch(single))
+            return single
         self.single_attn.forward_residual_(single, seq_mask, pair_logits)
         self.single_transition.forward_residual_(single)
         return single
@@ -208,17 +241,28 @@ class PairFormerBlock(nn.Module):
 
         kernel_census.record("PairFormerBlock", "hip_block_grad")
         p_drop = self.dropout_p()
+        if self._rms:
+            # unit-RMS rows (F.rms_norm, eps 1e-6 as primitives.py:79-87) times s_ros, in autograd
+            s_ros = self.residual_out_scale
+
+            def sc(u: torch.Tensor) -> torch.Tensor:
+                return s_ros * torch.nn.functional.rms_norm(u, (u.shape[-1],), eps=1e-6)
+        else:
+
+            def sc(u: torch.Tensor) -> torch.Tensor:
+                return u
+
         p = pair
         for m, rowwise in self._dropout_sites():
-            upd = m.branch(p, pair_mask)
+            upd = sc(m.branch(p, pair_mask))
             p = DropoutAddFunction.apply(p, upd, p_drop, rowwise, next_dropout_seed()) if p_drop > 0 else p + upd
-        p = p + self.pair_transition.branch(p)
+        p = p + sc(self.pair_transition.branch(p))
         if not self.use_single_track:
             return p, single
         n = self.single_to_pair_norm
         logits = token_linear(layer_norm_for_gemm(p, n.weight, n.bias, n.eps), self.single_to_pair.weight)
-        s = single + self.single_attn.branch(single, seq_mask, logits.movedim(-1, -3))
-        s = s + self.single_transition.branch(s)
+        s = single + sc(self.single_attn.branch(single, seq_mask, logits.movedim(-1, -3)))
+        s = s + sc(self.single_transition.branch(s))
         return p, s
 
     def forward(

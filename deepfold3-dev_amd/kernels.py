@@ -95,6 +95,28 @@ def residual_add(res: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = 
     return out
 
 
+def rms_residual_add(res: torch.Tensor | None, x: torch.Tensor, scale: float, out: torch.Tensor | None = None,
+                     eps: float = 1e-6) -> torch.Tensor:
+    """``res + scale * x / sqrt(mean x^2 + eps)`` over the last axis (the RMSNorm branch scaler,
+    ``branch_scaler.py:38-50``, then the residual add), or the scaled branch alone when ``res``
+    is None; ``out`` may be ``res`` (in place). One HIP pass (pf_rms_residual_add)."""
+    _lib.require_device("rms_residual_add", x)
+    xc = x.contiguous()
+    C = xc.shape[-1]
+    ref = xc if res is None else res
+    if res is not None and (res.shape != xc.shape or not res.is_contiguous()):
+        raise NotActive("rms_residual_add", "res must be contiguous and shaped like x")
+    if out is None:
+        out = torch.empty_like(ref)
+    else:
+        _lib.check_out("rms_residual_add", out, ref)
+    _lib.call(
+        "pf_rms_residual_add", _lib.ptr(res), _lib.dtype_code(ref.dtype), xc.data_ptr(), _lib.dtype_code(xc.dtype),
+        out.data_ptr(), xc.numel() // C, C, float(scale), float(eps), _lib.stream_of(xc),
+    )  # fmt: skip
+    return out
+
+
 def next_dropout_seed() -> int:
     """A 63-bit seed for one dropout-add, drawn from torch's default CPU generator.
 

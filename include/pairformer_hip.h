@@ -87,6 +87,13 @@ int pf_dropout_add_fwd(const void* res, int res_dtype, const void* x, int x_dtyp
 int pf_dropout_bwd(const void* grad_out, int grad_dtype, void* grad_x, int x_dtype, long B, long R, long Cc, long D,
                    int rowwise, float p, unsigned long long seed, void* stream);
 
+/* RMSNormScaler + residual add (branch_scaler.py:38-50 with primitives.py:79-87, applied at
+ * evoformer.py:298-335): out [M, C] = res + scale * x / sqrt(mean_c x^2 + eps) per row (eps
+ * 1e-6 in the reference), fp32 arithmetic rounded once to res_dtype; out may alias res or x.
+ * res NULL: out = scale * x / sqrt(mean_c x^2 + eps) (the scaled branch alone, in res_dtype). */
+int pf_rms_residual_add(const void* res, int res_dtype, const void* x, int x_dtype, void* out, long M, int C,
+                        float scale, float eps, void* stream);
+
 /* ---- LayerNorm -------------------------------------------------------- */
 /* out[r, :] = LN(x[r, :]) over C channels, fp32 statistics, output in x's dtype.
  * Replaces layer_norm / LayerNorm.forward (primitives.py:90-155). Tuned for C in

@@ -227,6 +227,12 @@ def single_attention(
     return F.linear(out * g, p["out_proj.weight"])
 
 
+def rms_normalize(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Non-learnable RMSNorm over the last axis (``primitives.py:79-87``): ``x / sqrt(mean x^2 +
+    eps)``, the reference's ``F.rms_norm`` with no weight."""
+    return F.rms_norm(x, (x.shape[-1],), eps=eps)
+
+
 def _scaled(x: torch.Tensor, s: float) -> torch.Tensor:
     """``s * x``; a unit scale returns ``x`` itself (the same values, one pass fewer)."""
     return x if s == 1.0 else s * x
@@ -244,10 +250,12 @@ def pairformer_block(
     use_triangle_attention: bool = True,
     use_single_track: bool = True,
     dropout: dict[str, torch.Tensor] | None = None,
+    branch_scaler: str = "identity",
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``PairFormerBlock.forward`` (``evoformer.py:270-355``).
 
-    Identity branch scaler. Eval dropout-add is a plain add (``dropout_add.py:236-237``);
+    ``branch_scaler`` "identity" (AF3) or "rmsnorm" (each branch output made unit-RMS per
+    token before its scale, ``branch_scaler.py:38-50``). Eval dropout-add is a plain add (``dropout_add.py:236-237``);
     ``dropout`` (training mode) maps the four dropped sites ``tri_mul_out``, ``tri_mul_in``,
     ``pair_attn_row`` (row-shared masks) and ``pair_attn_col`` (column-shared) to their masks
     (see ``dropout_add``), applied as at ``evoformer.py:289-310``; the transitions and the single
@@ -266,29 +274,34 @@ def pairformer_block(
     s_pf = s_ros * (1.0 if g_pf is None else float(g_pf))
     s_sf = s_ros * (1.0 if g_sf is None else float(g_sf))
     drop = dropout or {}
+    if branch_scaler not in ("identity", "rmsnorm"):
+        raise ValueError(f"branch_scaler {branch_scaler!r}")
+    # The branch scaler before each branch's scale (evoformer.py:289-335): identity, or the
+    # non-learnable unit-RMS rows of branch_scaler.py:38-50 (primitives.py:79-87, eps 1e-6).
+    sc_fn = (lambda x: x) if branch_scaler == "identity" else rms_normalize
 
     def add(res: torch.Tensor, upd: torch.Tensor, site: str) -> torch.Tensor:
         return dropout_add(res, upd, drop[site]) if site in drop else res + upd
 
     out: dict[str, torch.Tensor] = {}
     out["tri_mul_out"] = tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True)
-    pair = add(pair, _scaled(out["tri_mul_out"], s_ros), "tri_mul_out")
+    pair = add(pair, _scaled(sc_fn(out["tri_mul_out"]), s_ros), "tri_mul_out")
     out["tri_mul_in"] = tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False)
-    pair = add(pair, _scaled(out["tri_mul_in"], s_ros), "tri_mul_in")
+    pair = add(pair, _scaled(sc_fn(out["tri_mul_in"]), s_ros), "tri_mul_in")
     if use_triangle_attention:
         row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
-        pair = add(pair, _scaled(row, s_ros), "pair_attn_row")
+        pair = add(pair, _scaled(sc_fn(row), s_ros), "pair_attn_row")
         col = grid_attention(pair, pair_mask, _sub(p, "pair_attn_col."), transpose=True, row_chunk=row_chunk)
-        pair = add(pair, _scaled(col, s_ros), "pair_attn_col")
+        pair = add(pair, _scaled(sc_fn(col), s_ros), "pair_attn_col")
         out.update(pair_attn_row=row, pair_attn_col=col)
     out["pair_transition"] = transition(pair, _sub(p, "pair_transition."))
-    pair = pair + _scaled(out["pair_transition"], s_pf)
+    pair = pair + _scaled(sc_fn(out["pair_transition"]), s_pf)
     if use_single_track:
         out["pair_logits"] = single_to_pair(pair, p)
         out["single_attn"] = single_attention(single, seq_mask, out["pair_logits"], _sub(p, "single_attn."))
-        single = single + _scaled(out["single_attn"], s_ros)
+        single = single + _scaled(sc_fn(out["single_attn"]), s_ros)
         out["single_transition"] = transition(single, _sub(p, "single_transition."))
-        single = single + _scaled(out["single_transition"], s_sf)
+        single = single + _scaled(sc_fn(out["single_transition"]), s_sf)
     if branches is not None:
         branches.update(out)
     return pair, single

@@ -97,3 +97,13 @@ def test_planes_contract_validates_before_launch():
     assert lib.pf_planes_contract(d, d + 4096, d + 8192, 2, 96, 1, None) == 1  # Np % 128
     assert b"multiple of 128" in lib.pf_last_error()
     assert lib.pf_planes_contract(d + 2, d + 4096, d + 8192, 2, 128, 1, None) == 4  # misaligned
+
+
+def test_rms_residual_add_validates_before_launch():
+    """Null operands, bad sizes and dtype codes are refused on the host; M = 0 is a no-op."""
+    lib = _lib.lib()
+    d = 256
+    assert lib.pf_rms_residual_add(d, 1, None, 1, d, 4, 128, 1.0, 1e-6, None) == 1
+    assert lib.pf_rms_residual_add(d, 1, d, 1, d, 4, 0, 1.0, 1e-6, None) == 1
+    assert lib.pf_rms_residual_add(d, 3, d, 1, d, 4, 128, 1.0, 1e-6, None) == 2
+    assert lib.pf_rms_residual_add(None, 1, d, 1, d, 0, 128, 1.0, 1e-6, None) == 0

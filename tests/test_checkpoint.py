@@ -172,7 +172,6 @@ def test_loading_is_strict(tmp_path):
 @pytest.mark.parametrize(
     "field,value,needle",
     [
-        ("branch_scaler", "rmsnorm", "branch_scaler"),
         ("trimul_num_heads", 2, "multi-head"),
     ],
 )
@@ -180,6 +179,15 @@ def test_unbuilt_architectures_refuse_by_name(field, value, needle):
     cfg = {"pairformer": {"num_layer": 1, field: value}}
     with pytest.raises(guard.NotActive, match=needle):
         ck.build_trunk(cfg)
+
+
+def test_rmsnorm_branch_scaler_builds_and_refuses_transition_gains():
+    """branch_scaler="rmsnorm" builds (config.py:185); with a transition residual gain set it is
+    refused as the reference's PairFormerConfig.__post_init__ refuses it (config.py:252-269)."""
+    trunk = ck.build_trunk({"pairformer": {"num_layer": 1, "branch_scaler": "rmsnorm"}})
+    assert trunk.blocks[0].branch_scaler_kind == "rmsnorm"
+    with pytest.raises(ValueError, match="residual gains"):
+        ck.build_trunk({"pairformer": {"num_layer": 1, "branch_scaler": "rmsnorm", "pair_transition_residual_gain": 0.5}})
 
 
 def test_pair_bias_gate_builds_with_its_key_and_init():

@@ -795,3 +795,44 @@ def test_pair_bias_gate_pins():
         pf, sf = R.pairformer_block(*args, folded)
         assert torch.equal(pg, p0)  # the gate touches only the single track
         assert rel_l2(sg, sf) < 1e-6 and rel_l2(sg, s0) > 1e-4
+
+
+def test_rms_normalize_closed_forms():
+    """primitives.py:79-87: unit RMS per row (up to eps = 1e-6), invariant to a positive row
+    scale, zero rows stay zero."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(50, 128, generator=g) * (0.5 + 10 * torch.rand(50, 1, generator=g))
+    y = R.rms_normalize(x)
+    rms = y.pow(2).mean(-1).sqrt()
+    assert (rms - 1).abs().max() < 1e-5
+    assert rel_l2(R.rms_normalize(3.5 * x), y) < 1e-6
+    assert torch.equal(R.rms_normalize(torch.zeros(2, 128)), torch.zeros(2, 128))
+
+
+def test_rmsnorm_branch_scaler_block_invariance():
+    """With branch_scaler="rmsnorm" every branch enters the residual stream at unit RMS times
+    its scale, so multiplying a branch's output projection by a positive constant changes
+    nothing up to eps (and changes the identity-scaler block); the residual scale s then sets the
+    size of the first increment: RMS(pair1 - pair0) = s per token, up to eps."""
+    sd = W.make_block_weights(34, perturb_affine=True)
+    x = W.make_inputs(10, seed=8, pad_last=2)
+    args = (x["pair"], x["single"], x["pair_mask"], x["seq_mask"])
+    scaled = dict(sd)
+    for k, c in (("tri_mul_out.out_proj.weight", 3.0), ("pair_attn_col.out_proj.weight", 0.25),
+                 ("pair_transition.linear2.weight", 2.0), ("single_attn.out_proj.weight", 5.0),
+                 ("single_transition.linear2.weight", 0.5)):  # fmt: skip
+        scaled[k] = sd[k] * c
+    with torch.no_grad():
+        p0, s0 = R.pairformer_block(*args, sd, branch_scaler="rmsnorm")
+        p1, s1 = R.pairformer_block(*args, scaled, branch_scaler="rmsnorm")
+        q0, _ = R.pairformer_block(*args, sd)
+        q1, _ = R.pairformer_block(*args, scaled)
+        # eps = 1e-6 against branch rows of mean square down to ~1e-3: invariance to ~1e-4
+        assert rel_l2(p1, p0) < 1e-3 and rel_l2(s1, s0) < 1e-3
+        assert rel_l2(q1, q0) > 0.1
+        # only tri_mul_out active: the increment is s times a unit-RMS row
+        only = {k: (torch.zeros_like(v) if k.endswith(("out_proj.weight", "linear2.weight")) and
+                    not k.startswith("tri_mul_out.") else v) for k, v in sd.items()}  # fmt: skip
+        p2, _ = R.pairformer_block(*args, only, branch_scaler="rmsnorm", scales={"residual_out_scale": 0.3})
+    inc = (p2 - x["pair"]).pow(2).mean(-1).sqrt()
+    assert (inc - 0.3).abs().max() < 5e-4  # eps = 1e-6 against rows of mean square >= ~1e-3
