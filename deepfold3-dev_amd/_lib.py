@@ -53,6 +53,18 @@ SIGNATURES: dict[str, tuple] = {
     "pf_planes_transpose": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "pf_planes_contract": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "pf_rms_residual_add": (_i, [_vp, _i, _vp, _i, _vp, _l, _i, _f, _f, _vp]),
+    "pf_trimul_mhr_fwd": (
+        _i,
+        [_vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _f, _vp, _vp] + [_i] * 6 + [_vp, _i, _vp, _sz] + [_i, _i, _vp, _i, _vp],
+    ),
+    "pf_trimul_mhr_train_fwd": (
+        _i, [_vp] * 3 + [_vp, _vp, _f, _vp, _vp] + [_i] * 6 + [_vp, _sz, _vp] + [_i, _i, _vp, _i, _vp],
+    ),
+    "pf_trimul_mhr_router_wgrad_workspace_bytes": (_sz, [_l, _i, _i]),
+    "pf_trimul_mhr_router_wgrad": (_i, [_vp, _vp, _i, _l, _i, _i, _vp, _vp, _sz, _vp]),
+    "pf_trimul_mhr_output_vjp": (
+        _i, [_vp] * 5 + [_f] + [_vp] * 4 + [_i] * 5 + [_vp] * 8 + [_sz] + [_i, _i, _vp, _i, _vp, _vp],
+    ),
     "pf_trimul_fwd": (
         _i,
         [_vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _sz, _vp],

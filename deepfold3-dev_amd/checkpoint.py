@@ -16,9 +16,9 @@ the weights by state-dict key. This module does the same for the parts built her
 
 Tensors are read one key at a time through safetensors' ``safe_open`` (nothing in the file
 is executed, and only the keys under the requested prefix are read). A configuration this
-build cannot serve (pair channels other than 64, 128 or 256, pair heads wider than 32, MHR
-trimul, the pair-bias gate, an RMSNorm branch scaler) refuses by name when the stack is
-constructed or first run. Stacks without triangle attention or without the single track (the
+build cannot serve (pair channels other than 64, 128 or 256, pair heads wider than 32)
+refuses by name when the stack is constructed or first run; the off-by-default variants (MHR
+triangle multiplication, the pair-bias gate, the RMSNorm branch scaler) are built. Stacks without triangle attention or without the single track (the
 reference's current ``configs/stage0.yaml`` shape) are built without those branches. Loading
 is strict within the prefix: a missing or unexpected key raises.
 """

@@ -18,6 +18,7 @@
 
 #include "capi.h"
 #include "common.h"
+#include "mhr.h"
 
 namespace {
 
@@ -501,11 +502,14 @@ struct OutputCfg {
   static constexpr int NQ = trimul_nt<C>() / BM;  // threads per position in the LN_out pass
 };
 
-template <class TZ, class TC, int C, bool NORM = true>
+// MHR = true replaces LN_out by the multi-head routed mix `mx` (mhr.h) of at most HM heads
+// (the LDS its per-head values take); ln_out_b may then be null (head_rms).
+template <class TZ, class TC, int C, bool NORM = true, bool MHR = false, int HM = kMhrMaxHeads>
 __global__ __launch_bounds__(trimul_nt<C>()) void trimul_output_kernel(
     const TC* __restrict__ X, const TZ* __restrict__ z, TZ* __restrict__ out, const float* __restrict__ lniw,
     const float* __restrict__ lnib, float eps_in, const float* __restrict__ lnow, const float* __restrict__ lnob,
-    float eps_out, const TC* __restrict__ Wo, const TC* __restrict__ Wog, int B, int N, int Np, int accumulate) {
+    float eps_out, const TC* __restrict__ Wo, const TC* __restrict__ Wog, int B, int N, int Np, int accumulate,
+    MixSpec mx) {
   using Cfg = OutputCfg<TZ, TC, C>;
   constexpr int BM = Cfg::BM, XLD = Cfg::XLD, ALD = Cfg::ALD, SLD = Cfg::SLD, NQ = Cfg::NQ;
   constexpr int NT = trimul_nt<C>();
@@ -513,9 +517,12 @@ __global__ __launch_bounds__(trimul_nt<C>()) void trimul_output_kernel(
   constexpr int CBW = C / 16 / (NT / 64);
   constexpr int SMEM1 = Cfg::XS_BYTES + 2 * Cfg::A_BYTES;
   constexpr int SMEM = SMEM1 > Cfg::STAGE_BYTES ? SMEM1 : Cfg::STAGE_BYTES;
+  constexpr int MXN = MHR ? BM * HM : 1;
   __shared__ __attribute__((aligned(16))) char smem[SMEM];
   __shared__ float red[NQ][BM];
   __shared__ float stat_mean[BM];
+  __shared__ float mx_gate[MXN], mx_sa[MXN], mx_sb[MXN], mx_part[MXN];
+  __shared__ float mx_w[MHR ? C : 1], mx_b[MHR ? C : 1];  // norm_center's affine, staged once
   TC* Xs = reinterpret_cast<TC*>(smem);
   TC* A1 = reinterpret_cast<TC*>(smem + Cfg::XS_BYTES);
   TC* A2 = reinterpret_cast<TC*>(smem + Cfg::XS_BYTES + Cfg::A_BYTES);
@@ -526,6 +533,14 @@ __global__ __launch_bounds__(trimul_nt<C>()) void trimul_output_kernel(
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
   const size_t pe = (size_t)Np * Np;
+  RouterFrags<TC, C> rf;
+  if constexpr (MHR) {
+    if (mx.wr != nullptr && wave_id() < RB) rf.load(mx, 0);
+    for (int c = tid; c < C; c += NT) {
+      mx_w[c] = lnow[c];
+      mx_b[c] = lnob != nullptr ? lnob[c] : 0.f;
+    }
+  }
 
   // 1) raw X tile, channel-major: Xs[c][p] = X[b*C + c][i][j0 + p]
   {
@@ -551,8 +566,12 @@ __global__ __launch_bounds__(trimul_nt<C>()) void trimul_output_kernel(
     copy_tile_to_lds<TZ, TC, C, BM, NT>(zrow, A2, ALD);
   __syncthreads();
 
-  // 2) LN_out over channels of X, transposing into A1[p][c]
-  {
+  // 2) LN_out (or the MHR mix) over channels of X, transposing into A1[p][c]
+  if constexpr (MHR) {
+    mhr_gates<TC, C, BM, NT>(A2, ALD, mx, mx_gate, rf);
+    mhr_stats<TC, C, BM, NT>(Xs, XLD, mx_gate, mx, eps_out, mx_sa, mx_sb, mx_part);
+    mhr_mix_write<TC, C, BM, NT>(Xs, XLD, mx_gate, mx_sa, mx_sb, mx, mx_w, mx_b, A1, ALD);
+  } else {
     constexpr int CPQ = C / NQ;
     const int p = tid % BM;
     const int q = tid / BM;
@@ -1273,11 +1292,12 @@ __global__ void trimul_pack_kernel(const TS* __restrict__ wp, const TS* __restri
 
 // C = 128 in bf16 runs the persistent weight-stationary K1/K3; fp32 and the other channel
 // counts (the template stack's 64, the 256-channel trunk) run the generic tile kernels.
+// mx.heads > 0 runs the MHR mix in K3 (always the generic K3).
 template <class TZ, class TC, int C>
 int trimul_launch(const void* z, const float* mask, const float* lniw, const float* lnib, float eps_in,
                   const void* w4, const float* lnow, const float* lnob, float eps_out, const void* wo,
                   const void* wog, int B, int N, int outgoing, void* out, int accumulate, void* ws,
-                  hipStream_t s) {
+                  hipStream_t s, const MixSpec& mx) {
   constexpr bool kWs = sizeof(TC) == 2 && C == 128;
   const int Np = pf::pad128(N);
   const size_t pe = (size_t)Np * Np;
@@ -1321,7 +1341,21 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     }
     if (e) return e;
   }
-  {
+  if (mx.heads > 0) {
+    constexpr int BM = trimul_bm<TC>();
+    const dim3 grid((N + BM - 1) / BM, N, B);
+    pf::KernelTimer timer_trimul_output("trimul_output", s);
+    if (mx.heads <= kMhrHeadsSmall)
+      trimul_output_kernel<TZ, TC, C, true, true, kMhrHeadsSmall><<<grid, trimul_nt<C>(), 0, s>>>(
+          X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow, lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N,
+          Np, accumulate, mx);
+    else
+      trimul_output_kernel<TZ, TC, C, true, true><<<grid, trimul_nt<C>(), 0, s>>>(
+          X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow, lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N,
+          Np, accumulate, mx);
+    timer_trimul_output.stop();
+    if (int e = pf::check_launch("trimul_output")) return e;
+  } else {
     constexpr int BM = kWs ? 64 : trimul_bm<TC>();
     dim3 grid((N + BM - 1) / BM, N, B);
     pf::KernelTimer timer_trimul_output("trimul_output", s);
@@ -1337,7 +1371,7 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
     } else
       trimul_output_kernel<TZ, TC, C><<<grid, trimul_nt<C>(), 0, s>>>(X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow,
                                                            lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
-                                                           accumulate);
+                                                           accumulate, mx);
     timer_trimul_output.stop();
     if (int e = pf::check_launch("trimul_output")) return e;
   }
@@ -1349,7 +1383,7 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
 template <class TZ, class TC, int C>
 int trimul_train_launch(const void* x, const float* mask, const void* w4, const float* lnow, const float* lnob,
                         float eps_out, const void* wo, const void* wog, int B, int N, int outgoing, void* planes_ws,
-                        void* out, hipStream_t s) {
+                        void* out, hipStream_t s, const MixSpec& mx) {
   const int Np = pf::pad128(N);
   const size_t pe = (size_t)Np * Np;
   TC* planes = reinterpret_cast<TC*>(planes_ws);
@@ -1385,9 +1419,19 @@ int trimul_train_launch(const void* x, const float* mask, const void* w4, const 
     e = contract_generic_launch<TC>(P, Q, X, G, Np, remap, s);
   }
   if (e) return e;
-  trimul_output_kernel<TZ, TC, C, false><<<dim3((N + BM - 1) / BM, N, B), trimul_nt<C>(), 0, s>>>(
-      X, (const TZ*)x, (TZ*)out, nullptr, nullptr, 0.f, lnow, lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N, Np,
-      0);
+  if (mx.heads > kMhrHeadsSmall)
+    trimul_output_kernel<TZ, TC, C, false, true><<<dim3((N + BM - 1) / BM, N, B), trimul_nt<C>(), 0, s>>>(
+        X, (const TZ*)x, (TZ*)out, nullptr, nullptr, 0.f, lnow, lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N,
+        Np, 0, mx);
+  else if (mx.heads > 0)
+    trimul_output_kernel<TZ, TC, C, false, true, kMhrHeadsSmall><<<dim3((N + BM - 1) / BM, N, B), trimul_nt<C>(), 0,
+                                                                  s>>>(
+        X, (const TZ*)x, (TZ*)out, nullptr, nullptr, 0.f, lnow, lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N,
+        Np, 0, mx);
+  else
+    trimul_output_kernel<TZ, TC, C, false><<<dim3((N + BM - 1) / BM, N, B), trimul_nt<C>(), 0, s>>>(
+        X, (const TZ*)x, (TZ*)out, nullptr, nullptr, 0.f, lnow, lnob, eps_out, (const TC*)wo, (const TC*)wog, B, N,
+        Np, 0, mx);
   return pf::check_launch("trimul_train_output");
 }
 
@@ -1424,39 +1468,64 @@ int pf_trimul_pack_weights(const void* w_proj, const void* w_gate, int wdtype, v
   return pf::check_launch("pf_trimul_pack_weights");
 }
 
-int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const float* ln_in_b, float eps_in,
-                  const void* w_packed, const float* ln_out_w, const float* ln_out_b, float eps_out,
-                  const void* w_out, const void* w_out_gate, int B, int N, int C, int outgoing, int zdtype, int cdtype,
-                  void* out, int accumulate, void* workspace, size_t workspace_bytes, void* stream) {
-  PF_REQUIRE(z && mask && ln_in_w && ln_in_b && w_packed && ln_out_w && ln_out_b && w_out && w_out_gate && out &&
+static int trimul_fwd_impl(const char* fn, const void* z, const float* mask, const float* ln_in_w,
+                           const float* ln_in_b, float eps_in, const void* w_packed, const float* ln_out_w,
+                           const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate, int B,
+                           int N, int C, int outgoing, int zdtype, int cdtype, void* out, int accumulate,
+                           void* workspace, size_t workspace_bytes, void* stream,
+                           const MixSpec& mx) {
+  PF_REQUIRE(z && mask && ln_in_w && ln_in_b && w_packed && ln_out_w && w_out && w_out_gate && out &&
                  workspace,
-             PF_ERR_INVALID_ARG, "pf_trimul_fwd: null pointer");
-  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_trimul_fwd: B=%d N=%d", B, N);
-  PF_REQUIRE(C == 64 || C == 128 || C == 256, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: C=%d (built: 64, 128, 256)", C);
-  PF_REQUIRE(zdtype == PF_F32 || zdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: zdtype %d", zdtype);
-  PF_REQUIRE(cdtype == PF_F32 || cdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_trimul_fwd: cdtype %d", cdtype);
+             PF_ERR_INVALID_ARG, "%s: null pointer", fn);
+  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "%s: B=%d N=%d", fn, B, N);
+  PF_REQUIRE(C == 64 || C == 128 || C == 256, PF_ERR_UNSUPPORTED, "%s: C=%d (built: 64, 128, 256)", fn, C);
+  PF_REQUIRE(zdtype == PF_F32 || zdtype == PF_BF16, PF_ERR_UNSUPPORTED, "%s: zdtype %d", fn, zdtype);
+  PF_REQUIRE(cdtype == PF_F32 || cdtype == PF_BF16, PF_ERR_UNSUPPORTED, "%s: cdtype %d", fn, cdtype);
   PF_REQUIRE(!(zdtype == PF_BF16 && cdtype == PF_F32), PF_ERR_UNSUPPORTED,
-             "pf_trimul_fwd: bf16 activations with fp32 GEMMs is not a supported regime");
+             "%s: bf16 activations with fp32 GEMMs is not a supported regime", fn);
   PF_REQUIRE(pf::aligned16(z) && pf::aligned16(out) && pf::aligned16(workspace) && pf::aligned16(w_packed) &&
                  pf::aligned16(w_out) && pf::aligned16(w_out_gate),
-             PF_ERR_ALIGNMENT, "pf_trimul_fwd: pointers must be 16-byte aligned");
+             PF_ERR_ALIGNMENT, "%s: pointers must be 16-byte aligned", fn);
   PF_REQUIRE(workspace_bytes >= pf_trimul_workspace_bytes(B, N, C, cdtype), PF_ERR_WORKSPACE,
-             "pf_trimul_fwd: workspace %zu < %zu bytes", workspace_bytes, pf_trimul_workspace_bytes(B, N, C, cdtype));
+             "%s: workspace %zu < %zu bytes", fn, workspace_bytes, pf_trimul_workspace_bytes(B, N, C, cdtype));
   hipStream_t s = pf::as_stream(stream);
   auto run = [&](auto cc) {
     constexpr int CC = decltype(cc)::value;
     if (zdtype == PF_F32 && cdtype == PF_F32)
       return trimul_launch<float, float, CC>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out,
-                                             w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+                                             w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s, mx);
     if (zdtype == PF_F32)
       return trimul_launch<float, bf16, CC>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out,
-                                            w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+                                            w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s, mx);
     return trimul_launch<bf16, bf16, CC>(z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out,
-                                         w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s);
+                                         w_out, w_out_gate, B, N, outgoing, out, accumulate, workspace, s, mx);
   };
   if (C == 64) return run(std::integral_constant<int, 64>{});
   if (C == 256) return run(std::integral_constant<int, 256>{});
   return run(std::integral_constant<int, 128>{});
+}
+
+
+int pf_trimul_fwd(const void* z, const float* mask, const float* ln_in_w, const float* ln_in_b, float eps_in,
+                  const void* w_packed, const float* ln_out_w, const float* ln_out_b, float eps_out,
+                  const void* w_out, const void* w_out_gate, int B, int N, int C, int outgoing, int zdtype, int cdtype,
+                  void* out, int accumulate, void* workspace, size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(ln_out_b, PF_ERR_INVALID_ARG, "pf_trimul_fwd: null pointer");
+  return trimul_fwd_impl("pf_trimul_fwd", z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b, eps_out,
+                         w_out, w_out_gate, B, N, C, outgoing, zdtype, cdtype, out, accumulate, workspace,
+                         workspace_bytes, stream, MixSpec{0, 0, 0, nullptr});
+}
+
+int pf_trimul_mhr_fwd(const void* z, const float* mask, const float* ln_in_w, const float* ln_in_b, float eps_in,
+                      const void* w_packed, const float* ln_out_w, const float* ln_out_b, float eps_out,
+                      const void* w_out, const void* w_out_gate, int B, int N, int C, int outgoing, int zdtype,
+                      int cdtype, void* out, int accumulate, void* workspace, size_t workspace_bytes, int num_heads,
+                      int head_norm, const float* w_router, int router_kind, void* stream) {
+  MixSpec mx;
+  if (int e = mix_spec("pf_trimul_mhr_fwd", C, num_heads, head_norm, w_router, router_kind, ln_out_b, mx)) return e;
+  return trimul_fwd_impl("pf_trimul_mhr_fwd", z, mask, ln_in_w, ln_in_b, eps_in, w_packed, ln_out_w, ln_out_b,
+                         eps_out, w_out, w_out_gate, B, N, C, outgoing, zdtype, cdtype, out, accumulate, workspace,
+                         workspace_bytes, stream, mx);
 }
 
 int pf_trimul_train_pack_weights(const void* w_proj, const void* w_gate, int wdtype, void* packed, int C, int cdtype,
@@ -1482,39 +1551,60 @@ int pf_trimul_train_pack_weights(const void* w_proj, const void* w_gate, int wdt
   return pf::check_launch("pf_trimul_train_pack_weights");
 }
 
-int pf_trimul_train_fwd(const void* x, const float* mask, const void* w_packed, const float* ln_out_w,
-                        const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate, int B, int N,
-                        int C, int outgoing, int xdtype, int cdtype, void* planes, size_t planes_bytes, void* out,
-                        void* stream) {
-  PF_REQUIRE(x && mask && w_packed && ln_out_w && ln_out_b && w_out && w_out_gate && planes && out,
-             PF_ERR_INVALID_ARG, "pf_trimul_train_fwd: null pointer");
-  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "pf_trimul_train_fwd: B=%d N=%d", B, N);
-  PF_REQUIRE(C == 64 || C == 128 || C == 256, PF_ERR_UNSUPPORTED, "pf_trimul_train_fwd: C=%d (built: 64, 128, 256)",
-             C);
+static int trimul_train_fwd_impl(const char* fn, const void* x, const float* mask, const void* w_packed,
+                                 const float* ln_out_w, const float* ln_out_b, float eps_out, const void* w_out,
+                                 const void* w_out_gate, int B, int N, int C, int outgoing, int xdtype, int cdtype,
+                                 void* planes, size_t planes_bytes, void* out, void* stream, const MixSpec& mx) {
+  PF_REQUIRE(x && mask && w_packed && ln_out_w && w_out && w_out_gate && planes && out,
+             PF_ERR_INVALID_ARG, "%s: null pointer", fn);
+  PF_REQUIRE(B > 0 && N > 0, PF_ERR_INVALID_ARG, "%s: B=%d N=%d", fn, B, N);
+  PF_REQUIRE(C == 64 || C == 128 || C == 256, PF_ERR_UNSUPPORTED, "%s: C=%d (built: 64, 128, 256)", fn, C);
   PF_REQUIRE((xdtype == PF_F32 || xdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16) &&
                  !(xdtype == PF_BF16 && cdtype == PF_F32),
-             PF_ERR_UNSUPPORTED, "pf_trimul_train_fwd: xdtype %d cdtype %d", xdtype, cdtype);
+             PF_ERR_UNSUPPORTED, "%s: xdtype %d cdtype %d", fn, xdtype, cdtype);
   PF_REQUIRE(pf::aligned16(x) && pf::aligned16(out) && pf::aligned16(planes) && pf::aligned16(w_packed) &&
                  pf::aligned16(w_out) && pf::aligned16(w_out_gate),
-             PF_ERR_ALIGNMENT, "pf_trimul_train_fwd: pointers must be 16-byte aligned");
+             PF_ERR_ALIGNMENT, "%s: pointers must be 16-byte aligned", fn);
   PF_REQUIRE(planes_bytes >= pf_trimul_workspace_bytes(B, N, C, cdtype), PF_ERR_WORKSPACE,
-             "pf_trimul_train_fwd: planes buffer %zu < %zu bytes", planes_bytes,
+             "%s: planes buffer %zu < %zu bytes", fn, planes_bytes,
              pf_trimul_workspace_bytes(B, N, C, cdtype));
   hipStream_t s = pf::as_stream(stream);
   auto run = [&](auto cc) {
     constexpr int CC = decltype(cc)::value;
     if (xdtype == PF_F32 && cdtype == PF_F32)
       return trimul_train_launch<float, float, CC>(x, mask, w_packed, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate,
-                                                   B, N, outgoing, planes, out, s);
+                                                   B, N, outgoing, planes, out, s, mx);
     if (xdtype == PF_F32)
       return trimul_train_launch<float, bf16, CC>(x, mask, w_packed, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate,
-                                                  B, N, outgoing, planes, out, s);
+                                                  B, N, outgoing, planes, out, s, mx);
     return trimul_train_launch<bf16, bf16, CC>(x, mask, w_packed, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate, B,
-                                               N, outgoing, planes, out, s);
+                                               N, outgoing, planes, out, s, mx);
   };
   if (C == 64) return run(std::integral_constant<int, 64>{});
   if (C == 256) return run(std::integral_constant<int, 256>{});
   return run(std::integral_constant<int, 128>{});
+}
+
+int pf_trimul_train_fwd(const void* x, const float* mask, const void* w_packed, const float* ln_out_w,
+                        const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate, int B, int N,
+                        int C, int outgoing, int xdtype, int cdtype, void* planes, size_t planes_bytes, void* out,
+                        void* stream) {
+  PF_REQUIRE(ln_out_b, PF_ERR_INVALID_ARG, "pf_trimul_train_fwd: null pointer");
+  return trimul_train_fwd_impl("pf_trimul_train_fwd", x, mask, w_packed, ln_out_w, ln_out_b, eps_out, w_out,
+                               w_out_gate, B, N, C, outgoing, xdtype, cdtype, planes, planes_bytes, out, stream,
+                               MixSpec{0, 0, 0, nullptr});
+}
+
+int pf_trimul_mhr_train_fwd(const void* x, const float* mask, const void* w_packed, const float* ln_out_w,
+                            const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate, int B,
+                            int N, int C, int outgoing, int xdtype, int cdtype, void* planes, size_t planes_bytes,
+                            void* out, int num_heads, int head_norm, const float* w_router, int router_kind,
+                            void* stream) {
+  MixSpec mx;
+  if (int e = mix_spec("pf_trimul_mhr_train_fwd", C, num_heads, head_norm, w_router, router_kind, ln_out_b, mx))
+    return e;
+  return trimul_train_fwd_impl("pf_trimul_mhr_train_fwd", x, mask, w_packed, ln_out_w, ln_out_b, eps_out, w_out,
+                               w_out_gate, B, N, C, outgoing, xdtype, cdtype, planes, planes_bytes, out, stream, mx);
 }
 
 int pf_planes_contract(const void* A, const void* Bm, void* X, int G, int Np, int dtype, void* stream) {

@@ -23,6 +23,7 @@
 
 #include "capi.h"
 #include "common.h"
+#include "mhr.h"
 
 namespace {
 
@@ -37,13 +38,16 @@ template <int C>
 constexpr int vjp_nt() { return C >= 256 ? 512 : 256; }
 
 // ------------------------------------------------------------------ output VJP
-template <class TZ, class TC, int C>
+// MHR = true: the multi-head routed mix `mx` (mhr.h) in place of LN_out; xln_out is then its
+// output Y, the affine gradients are those of the mix's norm and dr [M][H] (fp32) receives the
+// router logits' cotangent when mx has a router.
+template <class TZ, class TC, int C, bool MHR = false, int HM = kMhrMaxHeads>
 __global__ __launch_bounds__(vjp_nt<C>()) void trimul_output_vjp_kernel(
     const TZ* __restrict__ g, const TC* __restrict__ X, const TZ* __restrict__ x, const float* __restrict__ lnow,
     const float* __restrict__ lnob, float eps, const TC* __restrict__ Wo, const TC* __restrict__ Wog,
     const TC* __restrict__ WoT, const TC* __restrict__ WogT, int B, int N, int Np, TC* __restrict__ gp_out,
     TC* __restrict__ gg_out, TC* __restrict__ xln_out, TC* __restrict__ dX, float* __restrict__ gx,
-    float* __restrict__ partial) {
+    float* __restrict__ partial, MixSpec mx, float* __restrict__ dr) {
   constexpr int BM = vjp_bm<TC, C>();
   constexpr int NT = vjp_nt<C>();
   constexpr int RB = BM / 16;
@@ -61,6 +65,9 @@ __global__ __launch_bounds__(vjp_nt<C>()) void trimul_output_vjp_kernel(
   constexpr int R_BYTES = 2 * A_BYTES > ST_BYTES ? 2 * A_BYTES : ST_BYTES;
   __shared__ __attribute__((aligned(16))) char smem[XS_BYTES + R_BYTES];
   __shared__ float s_mean[BM], s_rstd[BM];
+  constexpr int MXN = MHR ? BM * HM : 1;
+  __shared__ float mx_gate[MXN], mx_sa[MXN], mx_sb[MXN], mx_pa[MXN], mx_pb[MXN], mx_dg[MXN];
+  __shared__ float mx_w[MHR ? C : 1], mx_b[MHR ? C : 1];  // norm_center's affine, staged once
   TC* Xs = reinterpret_cast<TC*>(smem);                       // X [c][p], later dX
   TC* A1 = reinterpret_cast<TC*>(smem + XS_BYTES);            // xln, then gp
   TC* A2 = reinterpret_cast<TC*>(smem + XS_BYTES + A_BYTES);  // x, then gg
@@ -71,6 +78,14 @@ __global__ __launch_bounds__(vjp_nt<C>()) void trimul_output_vjp_kernel(
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
   const size_t pe = (size_t)Np * Np;
+  RouterFrags<TC, C> rf;
+  if constexpr (MHR) {
+    if (mx.wr != nullptr && wave_id() < RB) rf.load(mx, 0);
+    for (int c = tid; c < C; c += NT) {
+      mx_w[c] = lnow[c];
+      mx_b[c] = lnob != nullptr ? lnob[c] : 0.f;
+    }
+  }
   auto tok = [&](int p) -> long {
     const int j = j0 + p;
     return (i < N && j < N) ? ((long)b * N + i) * N + j : -1;
@@ -98,7 +113,19 @@ __global__ __launch_bounds__(vjp_nt<C>()) void trimul_output_vjp_kernel(
   // LN_out statistics (fp32, two-pass) and xln = LN_out(X) into A1 [p][c] and to xln_out
   const int pq = tid / NQ;
   const int qq = tid % NQ;
-  {
+  if constexpr (MHR) {
+    mhr_gates<TC, C, BM, NT>(A2, ALD, mx, mx_gate, rf);
+    mhr_stats<TC, C, BM, NT>(Xs, XLD, mx_gate, mx, eps, mx_sa, mx_sb, mx_pa);
+    mhr_mix_write<TC, C, BM, NT>(Xs, XLD, mx_gate, mx_sa, mx_sb, mx, mx_w, mx_b, A1, ALD);
+    __syncthreads();
+    constexpr int CPR = C / VEC;
+    for (int idx = tid; idx < BM * CPR; idx += NT) {
+      const int p = idx / CPR;
+      const int ch = (idx % CPR) * VEC;
+      const long t = tok(p);
+      if (t >= 0) *reinterpret_cast<u32x4*>(xln_out + t * C + ch) = *reinterpret_cast<const u32x4*>(A1 + p * ALD + ch);
+    }
+  } else {
     float xv[CPQ];
     float s = 0.f;
 #pragma unroll
@@ -181,17 +208,19 @@ __global__ __launch_bounds__(vjp_nt<C>()) void trimul_output_vjp_kernel(
   zero_acc(accx);
   gemm16_lds_x_w<TC, C, RB, CBW>(accd, A1, ALD, 0, WoT, C, wrow0);
   gemm16_lds_x_w<TC, C, RB, CBW>(accx, A2, ALD, 0, WogT, C, wrow0);
+  if constexpr (!MHR) {  // with the mix, gx also takes the router's share and leaves last
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int jb = 0; jb < CBW; ++jb)
+      for (int jb = 0; jb < CBW; ++jb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int p = rb * 16 + 4 * (l >> 4) + e;
-        const int c = (w * CBW + jb) * 16 + (l & 15);
-        const long t = tok(p);
-        if (t >= 0) gx[t * C + c] = accx[rb][jb][e];
-      }
+        for (int e = 0; e < 4; ++e) {
+          const int p = rb * 16 + 4 * (l >> 4) + e;
+          const int c = (w * CBW + jb) * 16 + (l & 15);
+          const long t = tok(p);
+          if (t >= 0) gx[t * C + c] = accx[rb][jb][e];
+        }
+  }
   __syncthreads();  // A1 / A2 dead: the fp32 stage takes their place
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
@@ -205,6 +234,48 @@ __global__ __launch_bounds__(vjp_nt<C>()) void trimul_output_vjp_kernel(
       }
   __syncthreads();
 
+  if constexpr (MHR) {
+    // the mix's pullback; between its passes, the per-block partial sums of the affine
+    // gradients (one thread per channel) while Xs still holds X
+    const size_t blk = ((size_t)b * gridDim.y + i) * gridDim.x + blockIdx.x;
+    mhr_mix_pullback<TC, C, BM, NT>(Xs, XLD, mx_gate, mx_sa, mx_sb, mx, mx_w, mx_b, stage, SLD, mx_dg, mx_pa, mx_pb,
+                                    [&]() {
+                                      mhr_affine_partials<TC, C, BM, NT>(Xs, XLD, mx_gate, mx_sa, mx_sb, mx, stage,
+                                                                         SLD, partial + blk * 2 * C,
+                                                                         partial + blk * 2 * C + C);
+                                    });
+    // the router logits' cotangent dr, and gx = gg Wog + dr Wr (x's share through the router)
+    const int H = mx.heads;
+    if (mx.wr != nullptr) {
+      for (int pr = tid; pr < BM * H; pr += NT) {
+        const int p = pr % BM, h = pr / BM;
+        const float v = mhr_router_grad<BM>(mx_gate, mx_dg, mx, p, h);
+        mx_pa[h * BM + p] = v;
+        const long t = tok(p);
+        if (t >= 0) dr[t * H + h] = v;
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int jb = 0; jb < CBW; ++jb) {
+      const int c = (w * CBW + jb) * 16 + (l & 15);
+      float wc[HM];
+#pragma unroll
+      for (int h = 0; h < HM; ++h) wc[h] = (mx.wr != nullptr && h < H) ? mx.wr[(size_t)h * C + c] : 0.f;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int p = rb * 16 + 4 * (l >> 4) + e;
+          float v = accx[rb][jb][e];
+#pragma unroll
+          for (int h = 0; h < HM; ++h)
+            if (h < H) v += mx_pa[h * BM + p] * wc[h];
+          const long t = tok(p);
+          if (t >= 0) gx[t * C + c] = mx.wr != nullptr ? v : accx[rb][jb][e];
+        }
+    }
+  } else {
   // Per-block partial sums of the LN_out affine gradients, one thread per channel.
   {
     const size_t blk = ((size_t)b * gridDim.y + i) * gridDim.x + blockIdx.x;
@@ -239,6 +310,7 @@ __global__ __launch_bounds__(vjp_nt<C>()) void trimul_output_vjp_kernel(
     sux = group_sum<NQ>(sux) * (1.0f / C);
 #pragma unroll
     for (int e = 0; e < CPQ; ++e) Xs[(qq * CPQ + e) * XLD + pq] = from_f32<TC>(rstd * (u[e] - su - xn[e] * sux));
+  }
   }
   __syncthreads();
   {
@@ -528,6 +600,51 @@ __global__ __launch_bounds__(256) void trimul_ln_grad_reduce_kernel(const float*
       dw[k] = red[0];
     else
       db[k - C] = red[0];
+  }
+}
+
+// MHR router weight gradient dWr = dr^T x: block b takes tokens [b tpb, (b + 1) tpb); thread
+// (phase ph, channel c), NT = C x phases, accumulates sum_t dr[t][h] x[t][c] over its phase's
+// tokens for every head; the phases are summed through LDS and the block leaves its [H][C]
+// partial, reduced over blocks by trimul_ln_grad_reduce_kernel.
+template <class TX, int H>
+__global__ __launch_bounds__(256) void mhr_router_wgrad_kernel(const float* __restrict__ dr, const TX* __restrict__ x,
+                                                               long M, int C, long tpb, float* __restrict__ partial) {
+  constexpr int CH = 64;  // tokens per staged chunk of dr
+  __shared__ float drs[CH * H];
+  __shared__ float red[256];
+  const int tid = threadIdx.x;
+  const int nph = 256 / C;  // C in {64, 128, 256}
+  const int c = tid % C, ph = tid / C;
+  const long t0 = (long)blockIdx.x * tpb;
+  const long t1 = t0 + tpb < M ? t0 + tpb : M;
+  float acc[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) acc[h] = 0.f;
+  for (long tc = t0; tc < t1; tc += CH) {
+    const int n = (int)(t1 - tc < CH ? t1 - tc : CH);
+    __syncthreads();
+    for (int i = tid; i < n * H; i += 256) drs[i] = dr[tc * H + i];
+    __syncthreads();
+#pragma unroll 4
+    for (int tt = ph; tt < n; tt += nph) {
+      const float xv = to_f32(x[(tc + tt) * C + c]);
+#pragma unroll
+      for (int h = 0; h < H; ++h) acc[h] += drs[tt * H + h] * xv;  // one address per wave: a broadcast
+    }
+  }
+  // sum the phases (at most 4) through LDS, one head at a time
+  float* out = partial + (size_t)blockIdx.x * H * C;
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    __syncthreads();
+    red[tid] = acc[h];
+    __syncthreads();
+    if (ph == 0) {
+      float v = 0.f;
+      for (int q = 0; q < nph; ++q) v += red[q * C + c];
+      out[h * C + c] = v;
+    }
   }
 }
 
@@ -910,12 +1027,29 @@ size_t out_vjp_partials(int B, int N) {
   return (size_t)B * Np * (Np / vjp_bm<TC, C>()) * 2 * C * sizeof(float);
 }
 
+// mx.heads > 0 runs the MHR pullback (always the generic kernel); dr its router cotangent.
 template <class TZ, class TC, int C>
 int output_vjp_launch(const void* g, const void* X, const void* x, const float* lnow, const float* lnob, float eps,
                       const void* wo, const void* wog, const void* wot, const void* wogt, int B, int N, void* gp,
-                      void* gg, void* xln, void* dX, float* gx, float* dlnw, float* dlnb, void* ws, hipStream_t s) {
+                      void* gg, void* xln, void* dX, float* gx, float* dlnw, float* dlnb, void* ws, hipStream_t s,
+                      const MixSpec& mx, float* dr) {
   const int Np = pf::pad128(N);
   float* partial = static_cast<float*>(ws);
+  if (mx.heads > 0) {
+    constexpr int BM = vjp_bm<TC, C>();
+    if (mx.heads <= kMhrHeadsSmall)
+      trimul_output_vjp_kernel<TZ, TC, C, true, kMhrHeadsSmall><<<dim3(Np / BM, Np, B), vjp_nt<C>(), 0, s>>>(
+          (const TZ*)g, (const TC*)X, (const TZ*)x, lnow, lnob, eps, (const TC*)wo, (const TC*)wog, (const TC*)wot,
+          (const TC*)wogt, B, N, Np, (TC*)gp, (TC*)gg, (TC*)xln, (TC*)dX, gx, partial, mx, dr);
+    else
+      trimul_output_vjp_kernel<TZ, TC, C, true><<<dim3(Np / BM, Np, B), vjp_nt<C>(), 0, s>>>(
+          (const TZ*)g, (const TC*)X, (const TZ*)x, lnow, lnob, eps, (const TC*)wo, (const TC*)wog, (const TC*)wot,
+          (const TC*)wogt, B, N, Np, (TC*)gp, (TC*)gg, (TC*)xln, (TC*)dX, gx, partial, mx, dr);
+    if (int e = pf::check_launch("trimul_output_vjp")) return e;
+    const long nblk = (long)B * Np * (Np / BM);
+    trimul_ln_grad_reduce_kernel<<<2 * C, 256, 0, s>>>(partial, nblk, 2 * C, dlnw, dlnb);
+    return pf::check_launch("trimul_ln_grad_reduce");
+  }
   if constexpr (sizeof(TC) == 2 && C == 128) {
     const long ntiles = (long)B * Np * (Np / OutputVjpWs::BM);
     PF_REQUIRE(ntiles < (1L << 31), PF_ERR_UNSUPPORTED, "trimul_output_vjp: B=%d N=%d too large", B, N);
@@ -931,7 +1065,7 @@ int output_vjp_launch(const void* g, const void* X, const void* x, const float* 
   const dim3 grid(Np / BM, Np, B);
   trimul_output_vjp_kernel<TZ, TC, C><<<grid, vjp_nt<C>(), 0, s>>>(
       (const TZ*)g, (const TC*)X, (const TZ*)x, lnow, lnob, eps, (const TC*)wo, (const TC*)wog, (const TC*)wot,
-      (const TC*)wogt, B, N, Np, (TC*)gp, (TC*)gg, (TC*)xln, (TC*)dX, gx, partial);
+      (const TC*)wogt, B, N, Np, (TC*)gp, (TC*)gg, (TC*)xln, (TC*)dX, gx, partial, mx, dr);
   if (int e = pf::check_launch("trimul_output_vjp")) return e;
   const long nblk = (long)B * Np * (Np / BM);
   trimul_ln_grad_reduce_kernel<<<2 * C, 256, 0, s>>>(partial, nblk, 2 * C, dlnw, dlnb);
@@ -993,22 +1127,22 @@ size_t pf_trimul_output_vjp_workspace_bytes(int B, int N, int C, int cdtype) {
   return cdtype == PF_F32 ? pick(float{}) : pick(bf16{});
 }
 
-int pf_trimul_output_vjp(const void* g, const void* X, const void* x, const float* ln_out_w, const float* ln_out_b,
-                         float eps_out, const void* w_out, const void* w_out_gate, const void* w_out_t,
-                         const void* w_out_gate_t, int B, int N, int C, int xdtype, int cdtype, void* gp, void* gg,
-                         void* xln, void* dX, float* gx, float* d_ln_out_w, float* d_ln_out_b, void* workspace,
-                         size_t workspace_bytes, void* stream) {
-  PF_REQUIRE(g && X && x && ln_out_w && ln_out_b && w_out && w_out_gate && w_out_t && w_out_gate_t && gp && gg &&
+static int output_vjp_impl(const char* fn, const void* g, const void* X, const void* x, const float* ln_out_w,
+                           const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate,
+                           const void* w_out_t, const void* w_out_gate_t, int B, int N, int C, int xdtype, int cdtype,
+                           void* gp, void* gg, void* xln, void* dX, float* gx, float* d_ln_out_w, float* d_ln_out_b,
+                           void* workspace, size_t workspace_bytes, void* stream, const MixSpec& mx, float* dr) {
+  PF_REQUIRE(g && X && x && ln_out_w && w_out && w_out_gate && w_out_t && w_out_gate_t && gp && gg &&
                  xln && dX && gx && d_ln_out_w && d_ln_out_b && workspace,
-             PF_ERR_INVALID_ARG, "pf_trimul_output_vjp: null pointer");
+             PF_ERR_INVALID_ARG, "%s: null pointer", fn);
   PF_REQUIRE(vjp_args_ok(B, N, C, xdtype, cdtype), PF_ERR_UNSUPPORTED,
-             "pf_trimul_output_vjp: B=%d N=%d C=%d xdtype=%d cdtype=%d", B, N, C, xdtype, cdtype);
+             "%s: B=%d N=%d C=%d xdtype=%d cdtype=%d", fn, B, N, C, xdtype, cdtype);
   PF_REQUIRE(pf::aligned16(g) && pf::aligned16(X) && pf::aligned16(x) && pf::aligned16(gp) && pf::aligned16(gg) &&
                  pf::aligned16(xln) && pf::aligned16(dX) && pf::aligned16(gx) && pf::aligned16(workspace),
-             PF_ERR_ALIGNMENT, "pf_trimul_output_vjp: pointers must be 16-byte aligned");
+             PF_ERR_ALIGNMENT, "%s: pointers must be 16-byte aligned", fn);
   const size_t need = pf_trimul_output_vjp_workspace_bytes(B, N, C, cdtype);
-  PF_REQUIRE(workspace_bytes >= need, PF_ERR_WORKSPACE, "pf_trimul_output_vjp: workspace %zu < %zu bytes",
-             workspace_bytes, need);
+  PF_REQUIRE(workspace_bytes >= need, PF_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes,
+             need);
   hipStream_t s = pf::as_stream(stream);
   return dispatch_vjp(xdtype, cdtype, C, [&](auto tz, auto tc, auto cc) {
     using TZ = decltype(tz);
@@ -1016,8 +1150,35 @@ int pf_trimul_output_vjp(const void* g, const void* X, const void* x, const floa
     constexpr int CC = decltype(cc)::value;
     return output_vjp_launch<TZ, TC, CC>(g, X, x, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate, w_out_t,
                                          w_out_gate_t, B, N, gp, gg, xln, dX, gx, d_ln_out_w, d_ln_out_b, workspace,
-                                         s);
+                                         s, mx, dr);
   });
+}
+
+int pf_trimul_output_vjp(const void* g, const void* X, const void* x, const float* ln_out_w, const float* ln_out_b,
+                         float eps_out, const void* w_out, const void* w_out_gate, const void* w_out_t,
+                         const void* w_out_gate_t, int B, int N, int C, int xdtype, int cdtype, void* gp, void* gg,
+                         void* xln, void* dX, float* gx, float* d_ln_out_w, float* d_ln_out_b, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(ln_out_b, PF_ERR_INVALID_ARG, "pf_trimul_output_vjp: null pointer");
+  return output_vjp_impl("pf_trimul_output_vjp", g, X, x, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate, w_out_t,
+                         w_out_gate_t, B, N, C, xdtype, cdtype, gp, gg, xln, dX, gx, d_ln_out_w, d_ln_out_b,
+                         workspace, workspace_bytes, stream, MixSpec{0, 0, 0, nullptr}, nullptr);
+}
+
+int pf_trimul_mhr_output_vjp(const void* g, const void* X, const void* x, const float* ln_out_w,
+                             const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate,
+                             const void* w_out_t, const void* w_out_gate_t, int B, int N, int C, int xdtype,
+                             int cdtype, void* gp, void* gg, void* xln, void* dX, float* gx, float* d_ln_out_w,
+                             float* d_ln_out_b, void* workspace, size_t workspace_bytes, int num_heads, int head_norm,
+                             const float* w_router, int router_kind, float* d_router_logits, void* stream) {
+  MixSpec mx;
+  if (int e = mix_spec("pf_trimul_mhr_output_vjp", C, num_heads, head_norm, w_router, router_kind, ln_out_b, mx))
+    return e;
+  PF_REQUIRE(w_router == nullptr || d_router_logits != nullptr, PF_ERR_INVALID_ARG,
+             "pf_trimul_mhr_output_vjp: a router needs d_router_logits");
+  return output_vjp_impl("pf_trimul_mhr_output_vjp", g, X, x, ln_out_w, ln_out_b, eps_out, w_out, w_out_gate,
+                         w_out_t, w_out_gate_t, B, N, C, xdtype, cdtype, gp, gg, xln, dX, gx, d_ln_out_w, d_ln_out_b,
+                         workspace, workspace_bytes, stream, mx, d_router_logits);
 }
 
 int pf_trimul_project_vjp(const void* dplanes, const void* x, const float* mask, const void* w_packed,
@@ -1038,6 +1199,51 @@ int pf_trimul_project_vjp(const void* dplanes, const void* x, const float* mask,
     return project_vjp_launch<TZ, TC, CC>(dplanes, x, mask, w_packed, w_packed_t, gx_in, B, N, outgoing, gpg, xw, dx,
                                           s);
   });
+}
+
+size_t pf_trimul_mhr_router_wgrad_workspace_bytes(long M, int C, int H) {
+  if (M <= 0 || C <= 0 || H <= 0) return 0;
+  const long nblk = std::min<long>(1024, (M + 255) / 256);
+  return (size_t)nblk * H * C * sizeof(float);
+}
+
+int pf_trimul_mhr_router_wgrad(const float* d_router_logits, const void* x, int xdtype, long M, int C, int H,
+                               float* d_router, void* workspace, size_t workspace_bytes, void* stream) {
+  PF_REQUIRE(d_router_logits && x && d_router && workspace, PF_ERR_INVALID_ARG,
+             "pf_trimul_mhr_router_wgrad: null pointer");
+  PF_REQUIRE(M > 0 && (C == 64 || C == 128 || C == 256) && H >= 1 && H <= kMhrMaxHeads && C % H == 0,
+             PF_ERR_INVALID_ARG, "pf_trimul_mhr_router_wgrad: M=%ld C=%d H=%d", M, C, H);
+  PF_REQUIRE(xdtype == PF_F32 || xdtype == PF_BF16, PF_ERR_UNSUPPORTED, "pf_trimul_mhr_router_wgrad: xdtype %d",
+             xdtype);
+  const size_t need = pf_trimul_mhr_router_wgrad_workspace_bytes(M, C, H);
+  PF_REQUIRE(workspace_bytes >= need, PF_ERR_WORKSPACE, "pf_trimul_mhr_router_wgrad: workspace %zu < %zu bytes",
+             workspace_bytes, need);
+  hipStream_t s = pf::as_stream(stream);
+  const long nblk = std::min<long>(1024, (M + 255) / 256);
+  const long tpb = (M + nblk - 1) / nblk;
+  float* partial = static_cast<float*>(workspace);
+  auto launch = [&](auto hc) {
+    constexpr int HH = decltype(hc)::value;
+    if (xdtype == PF_F32)
+      mhr_router_wgrad_kernel<float, HH><<<(unsigned)nblk, 256, 0, s>>>(d_router_logits, (const float*)x, M, C, tpb,
+                                                                        partial);
+    else
+      mhr_router_wgrad_kernel<bf16, HH><<<(unsigned)nblk, 256, 0, s>>>(d_router_logits, (const bf16*)x, M, C, tpb,
+                                                                       partial);
+  };
+  // C is a power of two, so the heads dividing it are too
+  switch (H) {
+    case 1: launch(std::integral_constant<int, 1>{}); break;
+    case 2: launch(std::integral_constant<int, 2>{}); break;
+    case 4: launch(std::integral_constant<int, 4>{}); break;
+    case 8: launch(std::integral_constant<int, 8>{}); break;
+    case 16: launch(std::integral_constant<int, 16>{}); break;
+    default: launch(std::integral_constant<int, 32>{}); break;
+  }
+  if (int e = pf::check_launch("mhr_router_wgrad")) return e;
+  const int HC = H * C;  // even: the reduce writes columns [0, HC/2) and [HC/2, HC) through two pointers
+  trimul_ln_grad_reduce_kernel<<<HC, 256, 0, s>>>(partial, nblk, HC, d_router, d_router + HC / 2);
+  return pf::check_launch("mhr_router_wgrad_reduce");
 }
 
 int pf_planes_transpose(const void* src, void* dst, int G, int Np, int dtype, void* stream) {

@@ -350,8 +350,14 @@ def trimul_forward(
     outgoing: bool,
     out: torch.Tensor | None = None,
     accumulate: bool = False,
+    mix: tuple | None = None,
 ) -> torch.Tensor:
-    """Launch K1, K2, K3 on prepared operands; returns ``out`` (the update, or z + update if accumulating)."""
+    """Launch K1, K2, K3 on prepared operands; returns ``out`` (the update, or z + update if accumulating).
+
+    ``mix = (num_heads, head_norm, w_router, router_kind)`` runs the multi-head routed head mix
+    in K3 (``pf_trimul_mhr_fwd``): head_norm and router_kind as ``MHR_HEAD_NORMS`` /
+    ``MHR_ROUTER_KINDS`` codes, w_router [H, C] fp32 or None; ``ln_out_b`` may then be None
+    (head_rms)."""
     _lib.require_device("fused_trimul", z, mask)
     if z.dim() != 4 or z.shape[1] != z.shape[2]:
         raise NotActive("fused_trimul", f"z must be [B, N, N, C], got {tuple(z.shape)}")
@@ -374,13 +380,25 @@ def trimul_forward(
     code_c = _lib.dtype_code(cdt)
     ws_bytes = _lib.lib().pf_trimul_workspace_bytes(B, N, C, code_c)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=z.device)
-    _lib.call(
-        "pf_trimul_fwd", zc.data_ptr(), m.data_ptr(), _f32(ln_in_w).data_ptr(), _f32(ln_in_b).data_ptr(),
-        float(eps_in), w_packed.data_ptr(), _f32(ln_out_w).data_ptr(), _f32(ln_out_b).data_ptr(), float(eps_out),
-        w_out.data_ptr(), w_out_gate.data_ptr(), B, N, C, int(outgoing), _lib.dtype_code(z.dtype), code_c,
-        out.data_ptr(), int(accumulate), ws.data_ptr(), ws_bytes, _lib.stream_of(zc),
+    args = (
+        zc.data_ptr(), m.data_ptr(), _f32(ln_in_w).data_ptr(), _f32(ln_in_b).data_ptr(), float(eps_in),
+        w_packed.data_ptr(), _f32(ln_out_w).data_ptr(), _lib.ptr(_f32(ln_out_b) if ln_out_b is not None else None),
+        float(eps_out), w_out.data_ptr(), w_out_gate.data_ptr(), B, N, C, int(outgoing), _lib.dtype_code(z.dtype),
+        code_c, out.data_ptr(), int(accumulate), ws.data_ptr(), ws_bytes,
     )  # fmt: skip
+    if mix is None:
+        _lib.call("pf_trimul_fwd", *args, _lib.stream_of(zc))
+    else:
+        heads, head_norm, w_router, router_kind = mix
+        wr = _f32(w_router) if w_router is not None else None
+        _lib.call("pf_trimul_mhr_fwd", *args, int(heads), int(head_norm), _lib.ptr(wr), int(router_kind),
+                  _lib.stream_of(zc))  # fmt: skip
     return out
+
+
+# MHR codes of the C-ABI (pf_trimul_mhr_*): head_norm and router kind.
+MHR_HEAD_NORMS = {"channel": 0, "head_rms": 1, "head_ln": 2, "post_channel": 3}
+MHR_ROUTER_KINDS = {"softmax": 0, "sigmoid": 1}
 
 
 @inference_only("fused_trimul")
@@ -491,10 +509,18 @@ class FusedTriMulFunction(torch.autograd.Function):
     ``dQ = dX^T P`` and the weight gradients as library GEMMs, then ``pf_trimul_project_vjp``.
     GEMM operands are bf16 for bf16 x or under bf16 autocast (the reference's regime), fp32
     otherwise. Returns gradients for x, w_gate, w_proj, ln_out_w, ln_out_b, w_out, w_out_gate.
+
+    Two trailing arguments run the multi-head routed variant (``ops.py:476-545``):
+    ``w_router`` [H, C] (or None) and ``mix = (num_heads, head_norm, router_kind)`` as
+    ``MHR_HEAD_NORMS`` / ``MHR_ROUTER_KINDS`` codes; ``ln_out_b`` may then be None (head_rms).
+    The forward and the output VJP run ``pf_trimul_mhr_train_fwd`` / ``pf_trimul_mhr_output_vjp``
+    (which also adds the router's share ``d_r Wr`` of x's cotangent, d_r the router logits'
+    cotangent); ``pf_trimul_mhr_router_wgrad`` forms Wr's gradient ``d_r^T x``.
     """
 
     @staticmethod
-    def forward(ctx, x, mask, w_gate, w_proj, ln_out_w, ln_out_b, w_out, w_out_gate, eps, outgoing):
+    def forward(ctx, x, mask, w_gate, w_proj, ln_out_w, ln_out_b, w_out, w_out_gate, eps, outgoing, w_router=None,
+                mix=None):  # fmt: skip
         _lib.require_device("FusedTriMulFunction", x, mask)
         if x.dim() != 4 or x.shape[1] != x.shape[2]:
             raise NotActive("FusedTriMulFunction", f"x must be [B, N, N, C], got {tuple(x.shape)}")
@@ -513,25 +539,35 @@ class FusedTriMulFunction(torch.autograd.Function):
             _lib.dtype_code(cdt), _lib.stream_of(xc),
         )  # fmt: skip
         wo, wog = cast_weight(w_out, cdt), cast_weight(w_out_gate, cdt)
-        lnow, lnob = _f32(ln_out_w), _f32(ln_out_b)
+        lnow = _f32(ln_out_w)
+        lnob = _f32(ln_out_b) if ln_out_b is not None else None
+        wr = _f32(w_router) if w_router is not None else None
         nbytes = _lib.lib().pf_trimul_workspace_bytes(B, N, C, _lib.dtype_code(cdt))
         planes = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
         out = torch.empty_like(xc)
         kernel_census.record("TriangleMul", "hip_trimul_grad")
-        _lib.call(
-            "pf_trimul_train_fwd", xc.data_ptr(), m.data_ptr(), w4.data_ptr(), lnow.data_ptr(), lnob.data_ptr(),
-            float(eps), wo.data_ptr(), wog.data_ptr(), B, N, C, int(bool(outgoing)), _lib.dtype_code(xc.dtype),
-            _lib.dtype_code(cdt), planes.data_ptr(), nbytes, out.data_ptr(), _lib.stream_of(xc),
+        args = (
+            xc.data_ptr(), m.data_ptr(), w4.data_ptr(), lnow.data_ptr(), _lib.ptr(lnob), float(eps), wo.data_ptr(),
+            wog.data_ptr(), B, N, C, int(bool(outgoing)), _lib.dtype_code(xc.dtype), _lib.dtype_code(cdt),
+            planes.data_ptr(), nbytes, out.data_ptr(),
         )  # fmt: skip
-        ctx.save_for_backward(xc, m, planes, w4, wo, wog, lnow, lnob)
-        ctx.eps, ctx.outgoing, ctx.cdt = float(eps), bool(outgoing), cdt
-        ctx.dtypes = (x.dtype, w_gate.dtype, w_proj.dtype, ln_out_w.dtype, ln_out_b.dtype, w_out.dtype, w_out_gate.dtype)
+        if mix is None:
+            _lib.call("pf_trimul_train_fwd", *args, _lib.stream_of(xc))
+        else:
+            _lib.call("pf_trimul_mhr_train_fwd", *args, int(mix[0]), int(mix[1]), _lib.ptr(wr), int(mix[2]),
+                      _lib.stream_of(xc))  # fmt: skip
+        ctx.save_for_backward(xc, m, planes, w4, wo, wog, lnow, lnob, wr)
+        ctx.eps, ctx.outgoing, ctx.cdt, ctx.mix = float(eps), bool(outgoing), cdt, mix
+        ctx.dtypes = (
+            x.dtype, w_gate.dtype, w_proj.dtype, ln_out_w.dtype, None if ln_out_b is None else ln_out_b.dtype,
+            w_out.dtype, w_out_gate.dtype, None if w_router is None else w_router.dtype,
+        )  # fmt: skip
         return out
 
     @staticmethod
     def backward(ctx, g):
-        xc, m, planes, w4, wo, wog, lnow, lnob = ctx.saved_tensors
-        cdt = ctx.cdt
+        xc, m, planes, w4, wo, wog, lnow, lnob, wr = ctx.saved_tensors
+        cdt, mix = ctx.cdt, ctx.mix
         B, N, _, C = xc.shape
         Np = -(-N // 128) * 128
         M = B * N * N
@@ -549,12 +585,25 @@ class FusedTriMulFunction(torch.autograd.Function):
         ws_bytes = _lib.lib().pf_trimul_output_vjp_workspace_bytes(B, N, C, code_c)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         wot, wogt = wo.t().contiguous(), wog.t().contiguous()
-        _lib.call(
-            "pf_trimul_output_vjp", g.data_ptr(), pl[2].data_ptr(), xc.data_ptr(), lnow.data_ptr(), lnob.data_ptr(),
-            ctx.eps, wo.data_ptr(), wog.data_ptr(), wot.data_ptr(), wogt.data_ptr(), B, N, C, code_x, code_c,
-            gp.data_ptr(), gg.data_ptr(), xln.data_ptr(), dX.data_ptr(), gx.data_ptr(), dlnw.data_ptr(),
-            dlnb.data_ptr(), ws.data_ptr(), ws_bytes, stream,
+        args = (
+            g.data_ptr(), pl[2].data_ptr(), xc.data_ptr(), lnow.data_ptr(), _lib.ptr(lnob), ctx.eps, wo.data_ptr(),
+            wog.data_ptr(), wot.data_ptr(), wogt.data_ptr(), B, N, C, code_x, code_c, gp.data_ptr(), gg.data_ptr(),
+            xln.data_ptr(), dX.data_ptr(), gx.data_ptr(), dlnw.data_ptr(), dlnb.data_ptr(), ws.data_ptr(), ws_bytes,
         )  # fmt: skip
+        d_router = None
+        if mix is None:
+            _lib.call("pf_trimul_output_vjp", *args, stream)
+        else:
+            dr = None if wr is None else torch.empty((M, int(mix[0])), dtype=torch.float32, device=dev)
+            _lib.call("pf_trimul_mhr_output_vjp", *args, int(mix[0]), int(mix[1]), _lib.ptr(wr), int(mix[2]),
+                      _lib.ptr(dr), stream)  # fmt: skip
+            if dr is not None:  # gx holds the router's share already; Wr's gradient dr^T x
+                H = int(mix[0])
+                d_router = torch.empty((H, C), dtype=torch.float32, device=dev)
+                wb = _lib.lib().pf_trimul_mhr_router_wgrad_workspace_bytes(M, C, H)
+                wws = torch.empty(wb, dtype=torch.uint8, device=dev)
+                _lib.call("pf_trimul_mhr_router_wgrad", dr.data_ptr(), xc.data_ptr(), code_x, M, C, H,
+                          d_router.data_ptr(), wws.data_ptr(), wb, stream)  # fmt: skip
         xb = xc.reshape(M, C).to(cdt)
         d_out = _weight_grad_tm(gp, xln)
         d_out_gate = _weight_grad_tm(gg, xb)
@@ -587,8 +636,9 @@ class FusedTriMulFunction(torch.autograd.Function):
         d_proj = torch.cat([dw4[:, 0].reshape(C, C), dw4[:, 2].reshape(C, C)])
         d_gate = torch.cat([dw4[:, 1].reshape(C, C), dw4[:, 3].reshape(C, C)])
         dt = ctx.dtypes
-        return (dx.to(dt[0]), None, d_gate.to(dt[1]), d_proj.to(dt[2]), dlnw.to(dt[3]), dlnb.to(dt[4]),
-                d_out.to(dt[5]), d_out_gate.to(dt[6]), None, None)  # fmt: skip
+        return (dx.to(dt[0]), None, d_gate.to(dt[1]), d_proj.to(dt[2]), dlnw.to(dt[3]),
+                None if dt[4] is None else dlnb.to(dt[4]), d_out.to(dt[5]), d_out_gate.to(dt[6]), None, None,
+                None if d_router is None else d_router.to(dt[7]), None)  # fmt: skip
 
 
 # ---------------------------------------------------------------- triangle attention

@@ -52,9 +52,9 @@ class WeightCache:
     def __init__(self):
         self._entries: dict = {}
 
-    def get(self, params: list[torch.Tensor], dtype: torch.dtype, build, tag=None):
+    def get(self, params: list[torch.Tensor | None], dtype: torch.dtype, build, tag=None):
         slot = (dtype, tag)
-        key = tuple((p.data_ptr(), p._version) for p in params)
+        key = tuple(None if p is None else (p.data_ptr(), p._version) for p in params)
         hit = self._entries.get(slot)
         if hit is not None and hit[0] == key:
             return hit[1]

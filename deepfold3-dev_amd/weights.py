@@ -47,11 +47,16 @@ def block_param_spec(
     use_triangle_attention: bool = True,
     use_single_track: bool = True,
     pair_bias_gate: bool = False,
+    trimul_num_heads: int = 0,
+    trimul_head_norm: str = "channel",
+    trimul_router: bool = False,
 ) -> list[tuple[str, tuple[int, ...], str]]:
     """Ordered ``(key, shape, kind)`` for one PairFormerBlock; kind is ln_w, ln_b, linear, bias
     or log_tau (the single attention's per-head pair-bias gate, ``attention.py:392-398``,
     initialised to log 0.25). A block without triangle attention has no ``pair_attn_*`` keys,
-    one without the single track no ``single_*`` keys (``evoformer.py:226-249``)."""
+    one without the single track no ``single_*`` keys (``evoformer.py:226-249``). The MHR
+    triangle multiply (``ops.py:219-255``) adds ``router.weight`` [H, C] with the router (drawn
+    as a linear here, so routing is not uniform) and has no ``norm_center.bias`` for head_rms."""
     c, cs = c_pair, c_single
     spec: list[tuple[str, tuple[int, ...], str]] = []
     for p in ("tri_mul_out.", "tri_mul_in."):
@@ -61,9 +66,10 @@ def block_param_spec(
             (p + "proj.weight", (2 * c, c), "linear"),
             (p + "gate.weight", (2 * c, c), "linear"),
             (p + "norm_center.weight", (c,), "ln_w"),
-            (p + "norm_center.bias", (c,), "ln_b"),
+            *([(p + "norm_center.bias", (c,), "ln_b")] if trimul_head_norm != "head_rms" else []),
             (p + "out_proj.weight", (c, c), "linear"),
             (p + "out_gate.weight", (c, c), "linear"),
+            *([(p + "router.weight", (trimul_num_heads, c), "linear")] if trimul_router else []),
         ]
     hd = max(c // num_pair_heads, 16)  # attention.py:67
     for p in ("pair_attn_row.", "pair_attn_col."):

@@ -200,6 +200,47 @@ int pf_trimul_project_vjp(const void* dplanes, const void* x, const float* mask,
 int pf_planes_transpose(const void* src, void* dst, int G, int Np, int dtype, void* stream);
 int pf_planes_contract(const void* A, const void* B, void* X, int G, int Np, int dtype, void* stream);
 
+/* Multi-head routed (MHR) triangle multiplication: _TriangleMulBase with num_heads > 0
+ * (ops.py:179-345) and its _mhr_head_mix (ops.py:476-545), between the contraction X and
+ * out_proj. The C channels are H = num_heads heads of d = C / H (1 <= H <= 32); head_norm
+ * 0 "channel" (LayerNorm over C), 1 "head_rms" (RMSNorm over each head, no shift: ln_out_b
+ * may be NULL), 2 "head_ln" (LayerNorm over each head), 3 "post_channel" (gates, then
+ * LayerNorm over C; needs the router); ln_out_w / ln_out_b are norm_center's [C] affine
+ * (viewed [H, d] by the head modes), eps_out its eps. w_router [H, C] fp32 is the router
+ * (r = LN_in(z) Wr^T per position; gates g = H softmax_h(r) for router_kind 0, 2 sigmoid(r)
+ * for 1), or NULL for g = 1. The other arguments are those of the entry point each
+ * extends:
+ *
+ * pf_trimul_mhr_fwd:        pf_trimul_fwd with the mix in K3 (the generic K3 at every C).
+ * pf_trimul_mhr_train_fwd:  pf_trimul_train_fwd with the mix.
+ * pf_trimul_mhr_output_vjp: pf_trimul_output_vjp through the mix: xln is the mix's output
+ *                           (out_proj's input), the affine gradients are norm_center's, and
+ *                           with a router d_router_logits [B*N*N, H] fp32 receives the
+ *                           logits' cotangent dr, and gx also takes the router's share dr Wr.
+ * pf_trimul_mhr_router_wgrad: the router weight's gradient d_router [H, C] fp32 = dr^T x over
+ *                           the M = B*N*N tokens of x [M, C] (xdtype, the input LayerNorm's
+ *                           output), summed in a fixed order; workspace >=
+ *                           pf_trimul_mhr_router_wgrad_workspace_bytes(M, C, H). */
+int pf_trimul_mhr_fwd(const void* z, const float* mask, const float* ln_in_w, const float* ln_in_b, float eps_in,
+                      const void* w_packed, const float* ln_out_w, const float* ln_out_b, float eps_out,
+                      const void* w_out, const void* w_out_gate, int B, int N, int C, int outgoing, int zdtype,
+                      int cdtype, void* out, int accumulate, void* workspace, size_t workspace_bytes, int num_heads,
+                      int head_norm, const float* w_router, int router_kind, void* stream);
+int pf_trimul_mhr_train_fwd(const void* x, const float* mask, const void* w_packed, const float* ln_out_w,
+                            const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate, int B,
+                            int N, int C, int outgoing, int xdtype, int cdtype, void* planes, size_t planes_bytes,
+                            void* out, int num_heads, int head_norm, const float* w_router, int router_kind,
+                            void* stream);
+int pf_trimul_mhr_output_vjp(const void* g, const void* X, const void* x, const float* ln_out_w,
+                             const float* ln_out_b, float eps_out, const void* w_out, const void* w_out_gate,
+                             const void* w_out_t, const void* w_out_gate_t, int B, int N, int C, int xdtype,
+                             int cdtype, void* gp, void* gg, void* xln, void* dX, float* gx, float* d_ln_out_w,
+                             float* d_ln_out_b, void* workspace, size_t workspace_bytes, int num_heads, int head_norm,
+                             const float* w_router, int router_kind, float* d_router_logits, void* stream);
+size_t pf_trimul_mhr_router_wgrad_workspace_bytes(long M, int C, int H);
+int pf_trimul_mhr_router_wgrad(const float* d_router_logits, const void* x, int xdtype, long M, int C, int H,
+                               float* d_router, void* workspace, size_t workspace_bytes, void* stream);
+
 
 /* ---- triangle attention (starting / ending node) ------------------------ */
 /* Whole-module GridSelfAttention forward: replaces GridSelfAttention.forward

@@ -35,6 +35,13 @@ Pinning (what checks this restatement, beyond retyping it):
   * the triangle multiply after its input LayerNorm (``tri_mul_core``): composing it with
     the LayerNorm and the block-order weights gives ``tri_mul`` (pinned by the golden
     vectors); its gradient by finite differences.
+  * multi-head routed triangle multiplication (``mhr_head_mix``): a zero router with
+    "channel" is exactly the plain ``tri_mul``; head_rms / head_ln give every head unit RMS /
+    zero mean before the affine (closed forms, against a per-head loop); the softmax gates
+    sum to H, the sigmoid gates equal 2 sigmoid(r); post_channel with uniform gates equals
+    channel; a one-hot-scaled head equals scaling out_proj's column block (the gate is a
+    per-head factor before out_proj); scaling one head's contraction leaves head_rms /
+    head_ln unchanged.
 """
 
 from __future__ import annotations
@@ -46,6 +53,7 @@ import torch.nn.functional as F
 __all__ = [
     "layer_norm",
     "tri_mul",
+    "mhr_head_mix",
     "grid_attention",
     "transition",
     "single_to_pair",
@@ -86,12 +94,24 @@ def _triangle_matmul(a: torch.Tensor, b: torch.Tensor, outgoing: bool) -> torch.
     return torch.matmul(a.permute(0, 3, 2, 1).contiguous(), b.permute(0, 3, 1, 2).contiguous()).permute(0, 3, 2, 1)
 
 
-def tri_mul(z: torch.Tensor, mask: torch.Tensor, p: dict[str, torch.Tensor], outgoing: bool) -> torch.Tensor:
-    """Stock ``_TriangleMulBase._compute`` with plain heads (``ops.py:412-473``).
+def tri_mul(
+    z: torch.Tensor,
+    mask: torch.Tensor,
+    p: dict[str, torch.Tensor],
+    outgoing: bool,
+    num_heads: int = 0,
+    head_norm: str = "channel",
+    router: bool = False,
+    router_kind: str = "softmax",
+) -> torch.Tensor:
+    """Stock ``_TriangleMulBase._compute`` (``ops.py:412-473``), plain heads (AF3) by default,
+    or multi-head routed (``num_heads`` > 0 with a per-head norm and / or the router,
+    ``ops.py:179-345``, ``:476-545``).
 
     Args:
         z: [B, N, N, C]; mask: [B, N, N]; p: keys ``norm_left.*``, ``proj.weight``,
-        ``gate.weight``, ``norm_center.*``, ``out_proj.weight``, ``out_gate.weight``.
+        ``gate.weight``, ``norm_center.weight`` (and ``.bias`` except for ``head_rms``),
+        ``out_proj.weight``, ``out_gate.weight``, ``router.weight`` [H, C] with the router.
     Returns:
         The update [B, N, N, C] (not added to z).
     """
@@ -99,6 +119,7 @@ def tri_mul(z: torch.Tensor, mask: torch.Tensor, p: dict[str, torch.Tensor], out
     proj = F.linear(z0, p["proj.weight"])
     gate = torch.sigmoid(F.linear(z0, p["gate.weight"]))
     out_gate = torch.sigmoid(F.linear(z0, p["out_gate.weight"]))
+    router_logits = F.linear(z0, p["router.weight"]) if router else None
     del z0
     proj = proj * gate
     a = proj[..., 0::2]
@@ -108,9 +129,49 @@ def tri_mul(z: torch.Tensor, mask: torch.Tensor, p: dict[str, torch.Tensor], out
     b = (b * m).contiguous()
     act = _triangle_matmul(a, b, outgoing)
     del a, b
-    act = layer_norm(act, p["norm_center.weight"], p["norm_center.bias"])
+    if head_norm != "channel" or router:
+        act = mhr_head_mix(act, router_logits, p, num_heads, head_norm, router_kind)
+    else:
+        act = layer_norm(act, p["norm_center.weight"], p["norm_center.bias"])
     act = F.linear(act, p["out_proj.weight"])
     return act * out_gate
+
+
+def mhr_head_mix(
+    act: torch.Tensor, router_logits: torch.Tensor | None, p: dict[str, torch.Tensor], h: int, head_norm: str,
+    router_kind: str, eps: float = 1e-5,
+) -> torch.Tensor:
+    """``_TriangleMulBase._mhr_head_mix`` (``ops.py:476-545``): the contraction [.., C] as H heads
+    of d = C / H; "channel" LayerNorms all C, "head_rms" / "head_ln" normalise each head (fp32,
+    rounded to act's dtype before the affine of ``norm_center`` viewed [H, d]); the router's
+    gates g = H softmax_h(R) or 2 sigmoid(R) (fp32, cast to the heads' dtype) scale each head;
+    "post_channel" gates first and LayerNorms all C after."""
+    d = act.shape[-1] // h
+    w = p["norm_center.weight"]
+    bias = p.get("norm_center.bias")
+
+    def gates() -> torch.Tensor:
+        r = router_logits.float()
+        return float(h) * torch.softmax(r, dim=-1) if router_kind == "softmax" else 2.0 * torch.sigmoid(r)
+
+    if head_norm == "post_channel":
+        t = act.unflatten(-1, (h, d))
+        if router_logits is not None:
+            t = t * gates().to(t.dtype).unsqueeze(-1)
+        return layer_norm(t.flatten(-2), w, bias, eps)
+    if head_norm == "channel":
+        t = layer_norm(act, w, bias, eps).unflatten(-1, (h, d))
+    else:
+        t32 = act.unflatten(-1, (h, d)).float()
+        if head_norm == "head_rms":
+            t = (t32 * torch.rsqrt(t32.pow(2).mean(-1, keepdim=True) + eps)).to(act.dtype) * w.view(h, d)
+        else:  # head_ln
+            mu = t32.mean(-1, keepdim=True)
+            t32 = (t32 - mu) * torch.rsqrt(t32.var(-1, keepdim=True, unbiased=False) + eps)
+            t = t32.to(act.dtype) * w.view(h, d) + bias.view(h, d)
+    if router_logits is not None:
+        t = t * gates().to(t.dtype).unsqueeze(-1)
+    return t.flatten(-2)
 
 
 def _grid_attention_rows(
@@ -251,8 +312,12 @@ def pairformer_block(
     use_single_track: bool = True,
     dropout: dict[str, torch.Tensor] | None = None,
     branch_scaler: str = "identity",
+    trimul_kwargs: dict | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``PairFormerBlock.forward`` (``evoformer.py:270-355``).
+
+    ``trimul_kwargs`` (num_heads, head_norm, router, router_kind) go to both triangle
+    multiplies (``evoformer.py:85-92``, the MHR variants of ``tri_mul``).
 
     ``branch_scaler`` "identity" (AF3) or "rmsnorm" (each branch output made unit-RMS per
     token before its scale, ``branch_scaler.py:38-50``). Eval dropout-add is a plain add (``dropout_add.py:236-237``);
@@ -284,9 +349,10 @@ def pairformer_block(
         return dropout_add(res, upd, drop[site]) if site in drop else res + upd
 
     out: dict[str, torch.Tensor] = {}
-    out["tri_mul_out"] = tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True)
+    tk = trimul_kwargs or {}
+    out["tri_mul_out"] = tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True, **tk)
     pair = add(pair, _scaled(sc_fn(out["tri_mul_out"]), s_ros), "tri_mul_out")
-    out["tri_mul_in"] = tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False)
+    out["tri_mul_in"] = tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False, **tk)
     pair = add(pair, _scaled(sc_fn(out["tri_mul_in"]), s_ros), "tri_mul_in")
     if use_triangle_attention:
         row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
@@ -456,6 +522,7 @@ def evoformer_block(
     row_chunk: int = 0,
     use_triangle_attention: bool = True,
     dropout: dict[str, torch.Tensor] | None = None,
+    trimul_kwargs: dict | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``EvoformerBlock.forward`` (``evoformer.py:148-175``): pair += OPM(msa),
     msa += MSAAttention(msa, pair), msa += msa_transition(msa), then the pair half of the
@@ -472,8 +539,9 @@ def evoformer_block(
     pair = pair + _scaled(outer_product_mean(msa, msa_mask, _sub(p, "outer_product.")), s)
     msa = add(msa, _scaled(msa_attention(msa, msa_mask, pair, _sub(p, "row_attn."), num_msa_heads), s), "row_attn")
     msa = msa + _scaled(transition(msa, _sub(p, "msa_transition.")), s)
-    pair = add(pair, _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True), s), "tri_mul_out")
-    pair = add(pair, _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False), s), "tri_mul_in")
+    tk = trimul_kwargs or {}
+    pair = add(pair, _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_out."), outgoing=True, **tk), s), "tri_mul_out")
+    pair = add(pair, _scaled(tri_mul(pair, pair_mask, _sub(p, "tri_mul_in."), outgoing=False, **tk), s), "tri_mul_in")
     if use_triangle_attention:
         row = grid_attention(pair, pair_mask, _sub(p, "pair_attn_row."), transpose=False, row_chunk=row_chunk)
         pair = add(pair, _scaled(row, s), "pair_attn_row")
@@ -541,11 +609,17 @@ def tri_mul_core(
     w_out_gate: torch.Tensor,
     eps: float,
     outgoing: bool,
+    w_router: torch.Tensor | None = None,
+    num_heads: int = 0,
+    head_norm: str = "channel",
+    router_kind: str = "softmax",
 ) -> torch.Tensor:
     """``FusedTriMulFunction.forward`` (``triton/fused_trimul.py:285-296``, kernels ``:64-151``,
     ``:264-281``): x = norm_left(z) given; ``w_gate``, ``w_proj`` [2C, C] in block order
     (rows [a; b]); a | b = sigmoid(x Wg^T) (x Wp^T) mask; X_ij = sum_k a_ik b_jk (outgoing) or
-    sum_k a_ki b_kj (incoming); out = sigmoid(x Wog^T) (LN(X) Wo^T). Differentiable."""
+    sum_k a_ki b_kj (incoming); out = sigmoid(x Wog^T) (LN(X) Wo^T). Differentiable. With
+    ``num_heads`` and a per-head norm or ``w_router`` [H, C], LN(X) is the MHR head mix
+    (``mhr_head_mix``) with router logits x Wr^T (``ops.py:412-473``)."""
     C = x.shape[-1]
     ab = torch.sigmoid(F.linear(x, w_gate)) * F.linear(x, w_proj) * mask.unsqueeze(-1)
     a, b = ab[..., :C], ab[..., C:]
@@ -553,7 +627,14 @@ def tri_mul_core(
         X = torch.einsum("bikc,bjkc->bijc", a, b)
     else:
         X = torch.einsum("bkic,bkjc->bijc", a, b)
-    xln = F.layer_norm(X, (C,), ln_out_w, ln_out_b, eps)
+    if head_norm != "channel" or w_router is not None:
+        affine = {"norm_center.weight": ln_out_w}
+        if ln_out_b is not None:
+            affine["norm_center.bias"] = ln_out_b
+        r = None if w_router is None else F.linear(x, w_router)
+        xln = mhr_head_mix(X, r, affine, num_heads, head_norm, router_kind, eps)
+    else:
+        xln = F.layer_norm(X, (C,), ln_out_w, ln_out_b, eps)
     return torch.sigmoid(F.linear(x, w_out_gate)) * F.linear(xln, w_out)
 
 

@@ -107,3 +107,33 @@ def test_rms_residual_add_validates_before_launch():
     assert lib.pf_rms_residual_add(d, 1, d, 1, d, 4, 0, 1.0, 1e-6, None) == 1
     assert lib.pf_rms_residual_add(d, 3, d, 1, d, 4, 128, 1.0, 1e-6, None) == 2
     assert lib.pf_rms_residual_add(None, 1, d, 1, d, 0, 128, 1.0, 1e-6, None) == 0
+
+
+def test_mhr_trimul_validates_before_launch():
+    """The multi-head routed entry points refuse bad head counts, modes, router kinds, a
+    post_channel mix without its router and a missing norm shift (outside head_rms) on the
+    host; head_rms takes a null shift (then the workspace check is what refuses here)."""
+    lib = _lib.lib()
+    d = 1 << 20
+
+    def fwd(heads, head_norm, wr, kind, lnb=d):
+        # z, mask, ln_in w/b, eps, packed, ln_out w/b, eps, w_out, w_out_gate, B, N, C, outgoing,
+        # zdtype, cdtype, out, accumulate, workspace, workspace_bytes (too small), MHR args, stream
+        return lib.pf_trimul_mhr_fwd(d, d, d, d, 1e-5, d, d, lnb, 1e-5, d, d, 1, 8, 64, 1, 1, 1, d, 0, d, 16, heads,
+                                     head_norm, wr, kind, None)  # fmt: skip
+
+    assert fwd(0, 2, None, 0) == 1
+    assert fwd(7, 2, None, 0) == 1 and b"dividing C=64" in lib.pf_last_error()
+    assert fwd(64, 2, None, 0) == 1  # beyond 32 heads
+    assert fwd(8, 4, None, 0) == 1
+    assert fwd(8, 2, d, 2) == 1
+    assert fwd(8, 3, None, 0) == 1 and b"post_channel needs the router" in lib.pf_last_error()
+    assert fwd(8, 2, None, 0, lnb=None) == 1
+    assert fwd(8, 1, None, 0, lnb=None) == 3  # head_rms: no shift needed; refused for the workspace
+    assert fwd(8, 3, d, 1) == 3
+    # the training forward and the output VJP share the checks
+    assert lib.pf_trimul_mhr_train_fwd(d, d, d, d, d, 1e-5, d, d, 1, 8, 64, 1, 1, 1, d, 16, d, 8, 3, None, 0,
+                                       None) == 1  # fmt: skip
+    assert lib.pf_trimul_mhr_output_vjp(d, d, d, d, d, 1e-5, d, d, d, d, 1, 8, 64, 1, 1, d, d, d, d, d, d, d, d, 16,
+                                        8, 2, d, 0, None, None) == 1  # router without d_router_logits  # fmt: skip
+    assert b"d_router_logits" in lib.pf_last_error()

@@ -169,16 +169,31 @@ def test_loading_is_strict(tmp_path):
         ck.load_recycler(tmp_path / "prev.safetensors")
 
 
-@pytest.mark.parametrize(
-    "field,value,needle",
-    [
-        ("trimul_num_heads", 2, "multi-head"),
-    ],
-)
-def test_unbuilt_architectures_refuse_by_name(field, value, needle):
-    cfg = {"pairformer": {"num_layer": 1, field: value}}
-    with pytest.raises(guard.NotActive, match=needle):
-        ck.build_trunk(cfg)
+def test_mhr_trimul_builds_with_the_reference_keys():
+    """MHR triangle multiplication (config.py:104-119, ops.py:179-260): the reference's r17
+    arm (8 heads, head_ln, softmax router) adds ``router.weight`` [8, C] (zeros) to each
+    triangle multiply; head_rms drops ``norm_center.bias``; bad combinations are refused with
+    the reference's messages."""
+    trunk = ck.build_trunk({"pairformer": {"num_layer": 1, "pair_channel": 256, "pair_attention": {"num_head": 8},
+                                           "trimul_num_heads": 8, "trimul_head_norm": "head_ln",
+                                           "trimul_router": True}})  # fmt: skip
+    sd = trunk.state_dict()
+    for site in ("tri_mul_out", "tri_mul_in"):
+        r = sd[f"blocks.0.{site}.router.weight"]
+        assert r.shape == (8, 256) and not r.any()
+        assert f"blocks.0.{site}.norm_center.bias" in sd
+        assert trunk.blocks[0].tri_mul_out.is_mhr
+    rms = ck.build_trunk({"pairformer": {"num_layer": 1, "trimul_num_heads": 4, "trimul_head_norm": "head_rms"}})
+    keys = set(rms.state_dict())
+    assert "blocks.0.tri_mul_in.norm_center.bias" not in keys and "blocks.0.tri_mul_in.router.weight" not in keys
+    with pytest.raises(ValueError, match="divisible"):
+        ck.build_trunk({"pairformer": {"num_layer": 1, "trimul_num_heads": 7, "trimul_head_norm": "head_rms"}})
+    with pytest.raises(ValueError, match="num_heads > 0"):
+        ck.build_trunk({"pairformer": {"num_layer": 1, "trimul_router": True}})
+    with pytest.raises(ValueError, match="meaningless without router"):
+        ck.build_trunk({"pairformer": {"num_layer": 1, "trimul_num_heads": 4, "trimul_head_norm": "post_channel"}})
+    with pytest.raises(ValueError, match="head_norm"):
+        ck.build_trunk({"pairformer": {"num_layer": 1, "trimul_num_heads": 4, "trimul_head_norm": "groupnorm"}})
 
 
 def test_rmsnorm_branch_scaler_builds_and_refuses_transition_gains():
