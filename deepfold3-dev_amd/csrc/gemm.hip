@@ -137,7 +137,8 @@ int bgemm_launch(const void* A, const void* B, void* C, int M, int N, int K, lon
 // row tile consecutively (the A tile stays in L2).
 template <class TC, class TO, int EPI>
 __global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restrict__ A, const TC* __restrict__ W,
-                                                             TO* __restrict__ out, long M, int Nout, int K) {
+                                                             TO* __restrict__ out, long M, int Nout, int K,
+                                                             int vec_out) {
   using Cfg = BgemmCfg<TC>;
   using MF = Mfma<TC>;
   constexpr int BMN = Cfg::BMN, KT = Cfg::KT, LDK = Cfg::LDK;
@@ -217,32 +218,56 @@ __global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restric
     if (kt + 1 < nk) lstore(buf ^ 1);
     __syncthreads();
   }
-  // acc[i][j][e]: row wr + 16 i + 4 (l >> 4) + e, B-tile row wc + 16 j + (l & 15)
+  // acc[i][j][e]: row wr + 16 i + 4 (l >> 4) + e, B-tile row wc + 16 j + (l & 15). The tile
+  // (after the SwiGLU pairing) is staged in fp32 through the LDS the k loop used, then leaves
+  // as 16-byte row pieces (with the residual read the same way); rounding as a direct store.
+  constexpr int SLD = OCT + 4;
+  static_assert(BMN * SLD * 4 <= Cfg::SMEM, "the output stage must fit the operand LDS");
+  float* st = reinterpret_cast<float*>(smem);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const long m = i0 + wr + i * 16 + 4 * (l >> 4) + e;
-      if (m >= M) continue;
-      TO* orow = out + m * Nout;
+      const int row = wr + i * 16 + 4 * (l >> 4) + e;
       if constexpr (EPI == 2) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int n = oc0 + (wc >> 6) * 32 + j * 16 + r;
-          if (n < Nout) orow[n] = from_f32<TO>(siluf_(acc[i][j][e]) * acc[i][j + 2][e]);
-        }
+        for (int j = 0; j < 2; ++j)
+          st[row * SLD + (wc >> 6) * 32 + j * 16 + r] = siluf_(acc[i][j][e]) * acc[i][j + 2][e];
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int n = oc0 + wc + j * 16 + r;
-          if (n >= Nout) continue;
-          if constexpr (EPI == 1)
-            orow[n] = from_f32<TO>(to_f32(orow[n]) + acc[i][j][e]);
-          else
-            orow[n] = from_f32<TO>(acc[i][j][e]);
-        }
+        for (int j = 0; j < 4; ++j) st[row * SLD + wc + j * 16 + r] = acc[i][j][e];
       }
     }
+  __syncthreads();
+  constexpr int OV = 16 / sizeof(TO);  // outputs per 16-byte piece
+  constexpr int PPR = OCT / OV;        // pieces per tile row
+  for (int idx = tid; idx < BMN * PPR; idx += 256) {
+    const int row = idx / PPR;
+    const int c0 = (idx % PPR) * OV;
+    const long m = i0 + row;
+    const int n0 = oc0 + c0;
+    if (m >= M || n0 >= Nout) continue;
+    TO* dst = out + m * Nout + n0;
+    float v[OV];
+#pragma unroll
+    for (int e = 0; e < OV; ++e) v[e] = st[row * SLD + c0 + e];
+    if (vec_out && n0 + OV <= Nout) {
+      if constexpr (EPI == 1) {
+        float rv[OV];
+        load16<TO>(dst, rv);
+#pragma unroll
+        for (int e = 0; e < OV; ++e) v[e] += rv[e];
+      }
+      store_vec<TO, OV>(dst, v);
+    } else {
+      for (int e = 0; e < OV && n0 + e < Nout; ++e) {
+        if constexpr (EPI == 1)
+          dst[e] = from_f32<TO>(to_f32(dst[e]) + v[e]);
+        else
+          dst[e] = from_f32<TO>(v[e]);
+      }
+    }
+  }
 }
 
 template <class TC, class TO, int EPI>
@@ -255,8 +280,9 @@ int tile_gemm_rows_launch(const void* A, const void* W, void* out, long M, int N
   const long tn = (Nout + (EPI == 2 ? 64 : 128) - 1) / (EPI == 2 ? 64 : 128);
   const long blocks = (M + Cfg::BMN - 1) / Cfg::BMN * tn;
   PF_REQUIRE(blocks < (1L << 31), PF_ERR_UNSUPPORTED, "row gemm: M=%ld Nout=%d", M, Nout);
+  const int vec_out = pf::aligned16(out) && Nout % (16 / (int)sizeof(TO)) == 0;
   tile_gemm_rows_kernel<TC, TO, EPI><<<dim3((unsigned)blocks), 256, Cfg::SMEM, s>>>((const TC*)A, (const TC*)W,
-                                                                                   (TO*)out, M, Nout, K);
+                                                                                   (TO*)out, M, Nout, K, vec_out);
   return pf::check_launch("row gemm");
 }
 
