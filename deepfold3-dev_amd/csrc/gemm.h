@@ -13,8 +13,8 @@ int bgemm_nt(const void* A, const void* B, void* C, int M, int N, int K, long ld
 
 // Row GEMM over many rows with the row kernels' epilogues: out[m][n] = epi(A W^T), A [M][K],
 // W [Nout or 2 Nout][K], out [M][Nout], row-major. epi 0 stores, 1 adds into out, 2 is
-// SwiGLU (out column j = silu(h_j) h_{Nout + j}). K must be a multiple of the k-tile (64 for
-// bf16 operands, 32 for fp32). Operands bf16 with bf16 or fp32 output, or fp32 throughout.
+// SwiGLU (out column j = silu(h_j) h_{Nout + j}). K must be a multiple of the k-tile (32 for
+// bf16 operands, 16 for fp32). Operands bf16 with bf16 or fp32 output, or fp32 throughout.
 int tile_gemm_rows(const void* A, const void* W, void* out, long M, int Nout, int K, int epi, int tc_dtype,
                    int out_dtype, hipStream_t s);
 // Rows from which the row GEMM hands over to tile_gemm_rows.

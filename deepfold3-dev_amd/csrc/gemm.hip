@@ -135,11 +135,24 @@ int bgemm_launch(const void* A, const void* B, void* C, int M, int N, int K, lon
 // holds both factors of each output (accumulator blocks j and j + 2). A [M][K], W [*][K],
 // out [M][Nout], all row-major with k or n contiguous. Blocks walk the weight tiles of one
 // row tile consecutively (the A tile stays in L2).
+// The many-row GEMM's tiles: k-tiles half the batched GEMM's (41 KB of LDS per block, three
+// blocks per CU), so more blocks keep loads in flight over the short k loops (K = 128-1024).
+template <class TC>
+struct TileRowsCfg {
+  static constexpr int BMN = 128;
+  static constexpr int KT = sizeof(TC) == 2 ? 32 : 16;
+  static constexpr int LDK = KT + lds_pad<TC>();
+  static constexpr int TILE_ELEMS = BMN * LDK;
+  static constexpr int SMEM = 2 * 2 * TILE_ELEMS * (int)sizeof(TC);
+  static constexpr int OSMEM = BMN / 2 * (128 + 4) * 4;  // the fp32 output stage, half a tile
+  static constexpr int LDS = SMEM > OSMEM ? SMEM : OSMEM;
+};
+
 template <class TC, class TO, int EPI>
 __global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restrict__ A, const TC* __restrict__ W,
                                                              TO* __restrict__ out, long M, int Nout, int K,
                                                              int vec_out) {
-  using Cfg = BgemmCfg<TC>;
+  using Cfg = TileRowsCfg<TC>;
   using MF = Mfma<TC>;
   constexpr int BMN = Cfg::BMN, KT = Cfg::KT, LDK = Cfg::LDK;
   constexpr int OCT = EPI == 2 ? 64 : 128;  // output columns per tile
@@ -219,69 +232,77 @@ __global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restric
     __syncthreads();
   }
   // acc[i][j][e]: row wr + 16 i + 4 (l >> 4) + e, B-tile row wc + 16 j + (l & 15). The tile
-  // (after the SwiGLU pairing) is staged in fp32 through the LDS the k loop used, then leaves
-  // as 16-byte row pieces (with the residual read the same way); rounding as a direct store.
+  // (after the SwiGLU pairing) is staged in fp32 through the LDS the k loop used, half a
+  // tile (64 rows: waves 0-1, then 2-3) at a time, and leaves as 16-byte row pieces (with the
+  // residual read the same way); rounding as a direct store.
   constexpr int SLD = OCT + 4;
-  static_assert(BMN * SLD * 4 <= Cfg::SMEM, "the output stage must fit the operand LDS");
+  constexpr int HR = BMN / 2;
+  static_assert(HR * SLD * 4 <= Cfg::LDS, "the output stage must fit the block's LDS");
   float* st = reinterpret_cast<float*>(smem);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = wr + i * 16 + 4 * (l >> 4) + e;
-      if constexpr (EPI == 2) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          st[row * SLD + (wc >> 6) * 32 + j * 16 + r] = siluf_(acc[i][j][e]) * acc[i][j + 2][e];
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) st[row * SLD + wc + j * 16 + r] = acc[i][j][e];
-      }
-    }
-  __syncthreads();
   constexpr int OV = 16 / sizeof(TO);  // outputs per 16-byte piece
   constexpr int PPR = OCT / OV;        // pieces per tile row
-  for (int idx = tid; idx < BMN * PPR; idx += 256) {
-    const int row = idx / PPR;
-    const int c0 = (idx % PPR) * OV;
-    const long m = i0 + row;
-    const int n0 = oc0 + c0;
-    if (m >= M || n0 >= Nout) continue;
-    TO* dst = out + m * Nout + n0;
-    float v[OV];
 #pragma unroll
-    for (int e = 0; e < OV; ++e) v[e] = st[row * SLD + c0 + e];
-    if (vec_out && n0 + OV <= Nout) {
-      if constexpr (EPI == 1) {
-        float rv[OV];
-        load16<TO>(dst, rv);
+  for (int half = 0; half < 2; ++half) {
+    if ((wr >> 6) == half) {
 #pragma unroll
-        for (int e = 0; e < OV; ++e) v[e] += rv[e];
-      }
-      store_vec<TO, OV>(dst, v);
-    } else {
-      for (int e = 0; e < OV && n0 + e < Nout; ++e) {
-        if constexpr (EPI == 1)
-          dst[e] = from_f32<TO>(to_f32(dst[e]) + v[e]);
-        else
-          dst[e] = from_f32<TO>(v[e]);
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = i * 16 + 4 * (l >> 4) + e;  // within the half
+          if constexpr (EPI == 2) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+              st[row * SLD + (wc >> 6) * 32 + j * 16 + r] = siluf_(acc[i][j][e]) * acc[i][j + 2][e];
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) st[row * SLD + wc + j * 16 + r] = acc[i][j][e];
+          }
+        }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < HR * PPR; idx += 256) {
+      const int row = idx / PPR;
+      const int c0 = (idx % PPR) * OV;
+      const long m = i0 + half * HR + row;
+      const int n0 = oc0 + c0;
+      if (m >= M || n0 >= Nout) continue;
+      TO* dst = out + m * Nout + n0;
+      float v[OV];
+#pragma unroll
+      for (int e = 0; e < OV; ++e) v[e] = st[row * SLD + c0 + e];
+      if (vec_out && n0 + OV <= Nout) {
+        if constexpr (EPI == 1) {
+          float rv[OV];
+          load16<TO>(dst, rv);
+#pragma unroll
+          for (int e = 0; e < OV; ++e) v[e] += rv[e];
+        }
+        store_vec<TO, OV>(dst, v);
+      } else {
+        for (int e = 0; e < OV && n0 + e < Nout; ++e) {
+          if constexpr (EPI == 1)
+            dst[e] = from_f32<TO>(to_f32(dst[e]) + v[e]);
+          else
+            dst[e] = from_f32<TO>(v[e]);
+        }
       }
     }
+    if (half == 0) __syncthreads();
   }
 }
 
 template <class TC, class TO, int EPI>
 int tile_gemm_rows_launch(const void* A, const void* W, void* out, long M, int Nout, int K, hipStream_t s) {
-  using Cfg = BgemmCfg<TC>;
+  using Cfg = TileRowsCfg<TC>;
   const void* fn = (const void*)tile_gemm_rows_kernel<TC, TO, EPI>;
-  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::SMEM);
-  PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "row gemm: cannot reserve %d bytes of LDS: %s", Cfg::SMEM,
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS);
+  PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "row gemm: cannot reserve %d bytes of LDS: %s", Cfg::LDS,
              hipGetErrorString(e));
   const long tn = (Nout + (EPI == 2 ? 64 : 128) - 1) / (EPI == 2 ? 64 : 128);
   const long blocks = (M + Cfg::BMN - 1) / Cfg::BMN * tn;
   PF_REQUIRE(blocks < (1L << 31), PF_ERR_UNSUPPORTED, "row gemm: M=%ld Nout=%d", M, Nout);
   const int vec_out = pf::aligned16(out) && Nout % (16 / (int)sizeof(TO)) == 0;
-  tile_gemm_rows_kernel<TC, TO, EPI><<<dim3((unsigned)blocks), 256, Cfg::SMEM, s>>>((const TC*)A, (const TC*)W,
+  tile_gemm_rows_kernel<TC, TO, EPI><<<dim3((unsigned)blocks), 256, Cfg::LDS, s>>>((const TC*)A, (const TC*)W,
                                                                                    (TO*)out, M, Nout, K, vec_out);
   return pf::check_launch("row gemm");
 }
@@ -297,7 +318,7 @@ int tile_gemm_rows_epi(const void* A, const void* W, void* out, long M, int Nout
 
 int tile_gemm_rows(const void* A, const void* W, void* out, long M, int Nout, int K, int epi, int tc_dtype,
                    int out_dtype, hipStream_t s) {
-  const int kt = tc_dtype == PF_F32 ? BgemmCfg<float>::KT : BgemmCfg<bf16>::KT;
+  const int kt = tc_dtype == PF_F32 ? TileRowsCfg<float>::KT : TileRowsCfg<bf16>::KT;
   PF_REQUIRE(M > 0 && Nout > 0 && K > 0 && K % kt == 0 && epi >= 0 && epi <= 2, PF_ERR_INVALID_ARG,
              "row gemm: M=%ld Nout=%d K=%d (a multiple of %d) epi=%d", M, Nout, K, kt, epi);
   if (tc_dtype == PF_F32) return tile_gemm_rows_epi<float, float>(A, W, out, M, Nout, K, epi, s);

@@ -173,7 +173,7 @@ template <class TC, class TO, int EPI>
 int rowgemm_launch(const void* A, const void* W, const float* bias, int nbias, void* out, long M, int Nout, int K,
                    hipStream_t s) {
   // Many rows (the pair paths at generic widths): the LDS-tiled GEMM with the same epilogue.
-  constexpr int kt = sizeof(TC) == 2 ? 64 : 32;
+  constexpr int kt = sizeof(TC) == 2 ? 32 : 16;  // tile_gemm_rows' k-tile
   if (M >= kTileGemmMinRows && K % kt == 0 && (bias == nullptr || nbias == 0) && pf::aligned16(A) &&
       pf::aligned16(W))
     return tile_gemm_rows(A, W, out, M, Nout, K, EPI, sizeof(TC) == 2 ? PF_BF16 : PF_F32,
