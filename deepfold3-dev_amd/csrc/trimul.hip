@@ -749,6 +749,235 @@ __global__ __launch_bounds__(256) void trimul_project32_kernel(const TZ* __restr
 // gating VALU work. One barrier per tile publishes the next tile's LayerNorm. NORM = false
 // (the training forward, whose input is already LayerNormed in autograd) only rounds the rows
 // to bf16 in that step.
+// K1 at 256 channels (bf16 GEMMs), persistent and weight-streaming: one 8-wave block per CU
+// walks tiles of 128 plane positions (one line, 128 consecutive t). The packed weights
+// (1024 rows x 256 k, 512 KB: too large to stay in registers as at 128 channels) stream
+// through a double-buffered LDS ring in 64-row chunks (16 channels: a proj, a gate, b proj,
+// b gate; 32 KB) by direct buffer->LDS loads one chunk ahead, 16-byte pieces XOR-swizzled by
+// row so fragment reads are conflict-free. Wave w owns rows 32 (w & 1) .. of every chunk
+// (the a or b pair of projection and gate) and positions 32 (w >> 1) ..: its 32 positions
+// are LayerNormed straight into registers as the B operands for the whole tile (a
+// position's 256 channels live in lanes l and l ^ 32), and the next tile's rows are loaded
+// while this tile's chunks run. Per chunk a wave issues 16 32x32x16 MFMAs; the projection
+// and gate rows of one channel land in one lane (accumulator rows r and r + 16), so the
+// gating is in registers; the gated values go through a double-buffered LDS stage
+// [a | b][16 channels][128 positions] and leave as 256-byte plane-row pieces one chunk later.
+// One barrier per chunk. (Three stages, weights two chunks ahead with each wait counting the
+// vector-memory operations issued after them, measured slower: 533 -> 600-609 us at N=768;
+// so did 64 positions per wave, whose operands spill.)
+struct Project256 {
+  static constexpr int C = 256;
+  static constexpr int BP = 128;                  // positions per tile
+  static constexpr int NW = 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int CR = 64;                   // weight rows per chunk
+  static constexpr int NCH = 4 * C / CR;          // 16 chunks per tile
+  static constexpr int ROWB = C * 2;              // 512-byte weight rows
+  static constexpr int CHUNK = CR * ROWB;         // 32 KB
+  static constexpr int NSTAGE = 2;                // weight chunks issued one ahead
+  static constexpr int DMA = CHUNK / 1024 / NW;   // direct loads per wave per chunk
+  static constexpr int SLD = BP + 8;              // stage rows (bf16)
+};
+
+// Byte offset of logical 16-byte piece c (0..31) of 512-byte weight row r: the piece index's
+// low four bits XOR the row's, so 16 consecutive rows at one logical piece spread over the
+// 16 bank groups.
+PF_DEVICE int p256_off(int r, int c) { return r * Project256::ROWB + 16 * (c ^ (r & 15)); }
+
+template <class TZ, bool NORM = true>
+__global__ __launch_bounds__(Project256::NT, 1) void trimul_project256_kernel(
+    const TZ* __restrict__ z, const float* __restrict__ mask, const float* __restrict__ lnw,
+    const float* __restrict__ lnb, float eps, const bf16* __restrict__ w4, bf16* __restrict__ planes, int B, int N,
+    int Np, int outgoing) {
+  using Cfg = Project256;
+  constexpr int C = Cfg::C, BP = Cfg::BP, NCH = Cfg::NCH, SLD = Cfg::SLD, NS = Cfg::NSTAGE;
+  // bf16 rows: the next tile's rows load during this tile's chunks (a second register set
+  // would not fit fp32 rows)
+  constexpr bool PREFETCH = sizeof(TZ) == 2;
+  constexpr int NPIECE = C / 16 * (int)sizeof(TZ) / 2;  // 16-byte loads of a lane's half row
+  __shared__ __attribute__((aligned(16))) char ring[NS * Cfg::CHUNK];
+  __shared__ __attribute__((aligned(16))) bf16 stage[2][2][16][SLD];
+  __shared__ float lnp[2 * C];
+
+  const int w = wave_id();
+  const int l = lane_id();
+  const int lq = l & 31, hf = l >> 5;
+  const int rb = w & 1;   // a (0) or b (1) rows of each chunk
+  const int pb = w >> 1;  // positions 32 pb ..
+  const int NT1 = Np / BP;
+  const long ntiles = (long)B * Np * NT1;
+  const size_t pe = (size_t)Np * Np;
+  // chunks this block consumes: its tiles x NCH
+  const long total = blockIdx.x < ntiles ? ((ntiles - 1 - blockIdx.x) / gridDim.x + 1) * NCH : 0;
+
+  if (NORM)
+    for (int i = threadIdx.x; i < C; i += Cfg::NT) {
+      lnp[i] = lnw[i];
+      lnp[C + i] = lnb[i];
+    }
+
+  const auto rw = buf_rsrc(w4, 4 * C * C * 2);
+  auto issue_chunk = [&](long gg) {
+    const int c = (int)(gg % NCH);
+    char* st = ring + (gg % NS) * Cfg::CHUNK;
+#pragma unroll
+    for (int t = 0; t < Cfg::DMA; ++t) {
+      const int ins = w * Cfg::DMA + t;  // two 512-byte rows per instruction
+      const int row = 2 * ins + (l >> 5);
+      const int lc = (l & 31) ^ (row & 15);
+      buf_load_lds16(rw, st + ins * 1024, ((c * Cfg::CR + row) * C + 8 * lc) * 2, 0);
+    }
+  };
+  auto tile_pos = [&](long tl, int& b, int& line, int& t0) {
+    b = (int)(tl / ((long)Np * NT1));
+    const long r = tl - (long)b * Np * NT1;
+    line = (int)(r / NT1);
+    t0 = (int)(r - (long)line * NT1) * BP;
+  };
+  // this lane's half row of tile tl: channels 16 ks + 8 hf .. +7, ks = 0..15 (zeros past N)
+  u32x4 zr[NPIECE];
+  auto load_half = [&](long tl) {
+    int b, line, t0;
+    tile_pos(tl, b, line, t0);
+    const int t = t0 + 32 * pb + lq;
+    const TZ* src = nullptr;
+    if (line < N && t < N)
+      src = z + ((size_t)b * N * N + (outgoing ? (long)line * N + t : (long)t * N + line)) * C + 8 * hf;
+#pragma unroll
+    for (int ks = 0; ks < C / 16; ++ks) {
+      if constexpr (sizeof(TZ) == 2) {
+        zr[ks] = src ? *reinterpret_cast<const u32x4*>(src + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+      } else {
+        zr[2 * ks] = src ? *reinterpret_cast<const u32x4*>(src + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+        zr[2 * ks + 1] = src ? *reinterpret_cast<const u32x4*>(src + 16 * ks + 4) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto get = [&](int ks, float (&v)[8]) {
+    if constexpr (sizeof(TZ) == 2) {
+      const bf16x8 t = __builtin_bit_cast(bf16x8, zr[ks]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (float)t[e];
+    } else {
+      const f32x4 a = __builtin_bit_cast(f32x4, zr[2 * ks]), c4 = __builtin_bit_cast(f32x4, zr[2 * ks + 1]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = a[e];
+        v[4 + e] = c4[e];
+      }
+    }
+  };
+  // chunk gg's gated values (stage gg & 1, plane-row pieces) -> planes of tile (b, line, t0)
+  auto store_chunk = [&](long gg, int b, int line, int t0) {
+    const int idx = threadIdx.x;  // 2 planes x 16 channels x 16 pieces = 512 threads
+    const int p2 = idx >> 8, ch = (idx >> 4) & 15, pc = idx & 15;
+    const int c = (int)(gg % NCH);
+    bf16* dst = planes + ((size_t)p2 * B * C + (size_t)b * C + 16 * c + ch) * pe + (size_t)line * Np + t0 + 8 * pc;
+    *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(&stage[gg & 1][p2][ch][8 * pc]);
+  };
+
+  long g = 0;
+  long tile = blockIdx.x;
+  int sb = 0, sline = 0, st0 = 0;  // tile of the chunk waiting in the stage
+  if (total > 0) {
+    load_half(tile);
+    for (int i = 0; i < NS - 1 && i < total; ++i) issue_chunk(i);
+  }
+  __syncthreads();  // LN parameters
+
+  for (; tile < ntiles; tile += gridDim.x) {
+    int b, line, t0;
+    tile_pos(tile, b, line, t0);
+    const int tpos = t0 + 32 * pb + lq;
+    const bool live = line < N && tpos < N;
+    const float mk =
+        live ? mask[(size_t)b * N * N + (outgoing ? (long)line * N + tpos : (long)tpos * N + line)] : 0.f;
+    if (!PREFETCH && tile != (long)blockIdx.x) load_half(tile);
+
+    // ---- LN (or the given x) -> B operands xf[ks]: channels 16 ks + 8 hf .. +7
+    bf16x8 xf[C / 16];
+    if constexpr (NORM) {
+      float s = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        get(ks, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += v[e];
+      }
+      s += __shfl_xor(s, 32, 64);
+      const float mean = s * (1.0f / C);
+      float q = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        get(ks, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[e] - mean;
+          q += d * d;
+        }
+      }
+      q += __shfl_xor(q, 32, 64);
+      const float rstd = rsqrtf(q * (1.0f / C) + eps);
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        get(ks, v);
+        const float* pw = lnp + 16 * ks + 8 * hf;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[ks][e] = (bf16)((v[e] - mean) * rstd * pw[e] + pw[C + e]);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        get(ks, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[ks][e] = (bf16)v[e];
+      }
+    }
+    const bool more = tile + gridDim.x < ntiles;
+
+#pragma unroll 1
+    for (int c = 0; c < NCH; ++c, ++g) {
+      // Chunk g's weights landed in every wave. Past the barrier, ring slot (g + 1) % NS (read
+      // by chunk g - 1's MFMAs) takes chunk g + 1, and stage (g - 1) & 1 leaves for the
+      // planes before chunk g + 1's barrier lets it be rewritten.
+      __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+      lds_barrier();
+      if (g > 0) store_chunk(g - 1, sb, sline, st0);
+      if (PREFETCH && c == 1 && more) load_half(tile + gridDim.x);  // zr is free after LN
+      if (g + NS - 1 < total) issue_chunk(g + NS - 1);
+      const char* st = ring + (g % NS) * Cfg::CHUNK;
+      f32x16 acc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const bf16x8 wf = *reinterpret_cast<const bf16x8*>(st + p256_off(32 * rb + lq, 2 * ks + hf));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xf[ks], acc, 0, 0, 0);
+      }
+      // acc[e]: chunk row 32 rb + 8 (e >> 2) + 4 hf + (e & 3), position 32 pb + lq; rows
+      // 0..15 of the pair are the projection of channel 16 c + row, rows 16..31 its gate
+      bf16(*sg)[SLD] = stage[g & 1][rb];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int ch = 8 * (e >> 2) + 4 * hf + (e & 3);
+        sg[ch][32 * pb + lq] = (bf16)(sigmoidf_(acc[e + 8]) * acc[e] * mk);
+      }
+      sb = b;
+      sline = line;
+      st0 = t0;
+    }
+  }
+  if (total > 0) {
+    lds_barrier();
+    store_chunk(g - 1, sb, sline, st0);
+  }
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // no direct load outlives the block
+}
+
 struct ProjectWs {
   static constexpr int C = 128;
   static constexpr int BP = 64;   // positions per tile
@@ -1290,8 +1519,9 @@ __global__ void trimul_pack_kernel(const TS* __restrict__ wp, const TS* __restri
   }
 }
 
-// C = 128 in bf16 runs the persistent weight-stationary K1/K3; fp32 and the other channel
-// counts (the template stack's 64, the 256-channel trunk) run the generic tile kernels.
+// C = 128 in bf16 runs the persistent weight-stationary K1/K3 and C = 256 with bf16 z the
+// persistent weight-streaming K1; fp32 and the other channel counts (the template stack's 64)
+// run the generic tile kernels, as does K3 at 256 channels.
 // mx.heads > 0 runs the MHR mix in K3 (always the generic K3).
 template <class TZ, class TC, int C>
 int trimul_launch(const void* z, const float* mask, const float* lniw, const float* lnib, float eps_in,
@@ -1319,7 +1549,14 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
                                                                   outgoing);
       (void)grid;
     }
-    else
+    else if constexpr (sizeof(TC) == 2 && C == 256 && sizeof(TZ) == 2) {  // (fp32 rows would spill)
+      const long ntiles = (long)B * Np * (Np / Project256::BP);
+      const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+      trimul_project256_kernel<TZ><<<nblk, Project256::NT, 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in,
+                                                                   (const bf16*)w4, (bf16*)planes, B, N, Np,
+                                                                   outgoing);
+      (void)grid;
+    } else
       trimul_project_kernel<TZ, TC, C><<<grid, trimul_nt<C>(), 0, s>>>((const TZ*)z, mask, lniw, lnib, eps_in, (const TC*)w4,
                                                             planes, B, N, Np, outgoing);
     timer_trimul_project.stop();
@@ -1400,6 +1637,12 @@ int trimul_train_launch(const void* x, const float* mask, const void* w4, const 
     trimul_project_ws_kernel<TZ, false><<<nblk, ProjectWs::NT, 0, s>>>((const TZ*)x, mask, nullptr, nullptr, 0.f,
                                                                        (const bf16*)w4, (bf16*)planes, B, N, Np,
                                                                        outgoing);
+  } else if constexpr (sizeof(TC) == 2 && C == 256) {
+    const long ntiles = (long)B * Np * (Np / Project256::BP);
+    const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+    trimul_project256_kernel<TZ, false><<<nblk, Project256::NT, 0, s>>>((const TZ*)x, mask, nullptr, nullptr, 0.f,
+                                                                        (const bf16*)w4, (bf16*)planes, B, N, Np,
+                                                                        outgoing);
   } else {
     trimul_project_kernel<TZ, TC, C, false><<<dim3(Np / BM, Np, B), trimul_nt<C>(), 0, s>>>(
         (const TZ*)x, mask, nullptr, nullptr, 0.f, (const TC*)w4, planes, B, N, Np, outgoing);
