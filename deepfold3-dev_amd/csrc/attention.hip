@@ -1819,22 +1819,434 @@ __global__ __launch_bounds__(256) void grid_gen_bias_kernel(const TC* __restrict
   }
 }
 
-// og[pos][j] *= sigmoid(g[pos][j]) in place, g the gate columns of the projection; 8 columns
-// per thread (H d a multiple of 8).
+// og[pos][j] *= sigmoid(g[pos][j]) in place, g the columns from `goff` of rows of PW
+// elements (the gate columns of the projection); 8 columns per thread (H d a multiple of 8).
 template <class TC>
 __global__ __launch_bounds__(256) void grid_gen_gate_inplace_kernel(TC* __restrict__ og, const TC* __restrict__ proj,
-                                                                    long M, int HD, int PW) {
+                                                                    long M, int HD, int PW, int goff) {
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   const int nc = HD / 8;
   if (idx >= M * nc) return;
   const long pos = idx / nc;
   const int j = (int)(idx % nc) * 8;
   TC* o = og + pos * HD + j;
-  const TC* g = proj + pos * PW + 3 * HD + j;
+  const TC* g = proj + pos * PW + goff + j;
   float r[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) r[e] = to_f32(o[e]) * sigmoidf_(to_f32(g[e]));
   store_vec<TC, 8>(o, r);
+}
+
+// ------------------------------------------------------------------ 256 channels, 8 heads
+// GridSelfAttention at 256 channels in 8 heads of 32 with bf16 GEMMs (the reference's
+// production width, configs/stage0.yaml:54-56): one persistent projection kernel writes the
+// flash kernel's frame for both four-head groups -- Q (pre-scaled by d^-1/2 log2 e), the K
+// and Vt key-block tiles, the pair bias (log2 units; query-major in key-slot order for rows,
+// key-major for columns, turned by pb_transpose) and the line mask -- plus the gate rows
+// G [pos][256] in z order; then per group the flash kernel (o into og's rows, strided), the
+// gate og *= sigmoid(G) and the output GEMM. No LayerNorm round trip, no projection rows,
+// no repacking.
+//
+// The projection: one 8-wave block per CU walks tiles of 128 tokens of one line (the z
+// positions (line, t) for rows, (t, line) for columns). A position's LayerNormed 256
+// channels are held in registers as the B operand for the whole tile (lanes l and l ^ 32);
+// the packed rows of w_qkvgb (q | k | v | g, 256 each, then the 8 bias rows) stream through
+// a two-stage LDS ring in 64-row chunks (32 KB, XOR-swizzled 16-byte pieces) by direct
+// buffer->LDS loads one chunk ahead, 16 q/k/v/g chunks (two heads each) and one bias chunk.
+// Wave w computes rows 32 (w & 1) .. of each chunk for tokens 32 (w >> 1) ..; the values
+// go through a double-buffered LDS stage in the layout their destination needs (token-major
+// for Q, K and G, d-major in key-slot order for Vt, head-major for the bias) and leave as
+// 16-byte pieces one chunk later, while the next tile's z rows load under this tile's chunks.
+struct GridProj256 {
+  static constexpr int C = 256;
+  static constexpr int H = 8;
+  static constexpr int HD = 256;                  // H x 32
+  static constexpr int WROWS = 4 * HD + 16;       // rows of w_qkvgb (8 bias rows, 8 zero rows)
+  static constexpr int BP = 128;                  // tokens per tile
+  static constexpr int NW = 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int CR = 64;                   // weight rows per chunk
+  static constexpr int NCH = 4 * HD / CR + 1;     // 16 head chunks + the bias chunk
+  static constexpr int ROWB = C * 2;              // 512-byte weight rows
+  static constexpr int CHUNK = CR * ROWB;         // 32 KB
+  static constexpr int NS = 2;                    // ring stages (one chunk ahead)
+  static constexpr int DMA = CHUNK / 1024 / NW;   // direct loads per wave per chunk
+  static constexpr int TLD = 40;                  // token-major stage rows: 32 d + pad (bf16)
+  static constexpr int VLD = BP + 8;              // d-major stage rows (bf16)
+  static constexpr int STAGE = 2 * BP * TLD * 2;  // bytes per stage buffer (largest layout)
+  static_assert(2 * 32 * VLD * 2 <= STAGE && 8 * BP * 4 <= STAGE, "stage layouts");
+};
+
+// Byte offset of logical 16-byte piece c (0..31) of 512-byte weight row r: the piece index's
+// low four bits XOR the row's, so 16 consecutive rows at one logical piece spread over the
+// 16 bank groups.
+PF_DEVICE int gp256_off(int r, int c) { return r * GridProj256::ROWB + 16 * (c ^ (r & 15)); }
+
+// Frame of the 256-channel path inside the workspace: per group of four heads, Q, K and Vt
+// [B][N lines][4][Np][32] bf16 and the pair bias [B][4][Np][Np] fp32; one line mask
+// [B][N][Np]; the gate rows and og [B N N][256] bf16; the redo flags of both groups.
+struct Grid256Ws {
+  size_t q, k, v, pb, ma, g, og, redo, total;
+  size_t gq, gpb, gredo;  // per-group strides (elements of Q / K / Vt, floats of PB, ints)
+};
+
+Grid256Ws grid256_layout(int B, int N) {
+  const size_t Np = pf::round_up((size_t)N, kPad);
+  const size_t M = (size_t)B * N * N;
+  Grid256Ws w;
+  w.gq = (size_t)B * N * 4 * Np * kHeadDim;
+  w.gpb = (size_t)B * 4 * Np * Np;
+  w.gredo = redo_flag_bytes(B, N, (int)Np) / sizeof(int);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += pf::round_up(bytes, 256);
+    return at;
+  };
+  w.q = take(2 * w.gq * 2);
+  w.k = take(2 * w.gq * 2);
+  w.v = take(2 * w.gq * 2);
+  w.pb = take(2 * w.gpb * 4);
+  w.ma = take((size_t)B * N * Np * 4);
+  w.g = take(M * GridProj256::HD * 2);
+  w.og = take(M * GridProj256::HD * 2);
+  w.redo = take(2 * w.gredo * sizeof(int));
+  w.total = off;
+  return w;
+}
+
+bool grid256_applies(int C, int H, int cdtype) { return C == GridProj256::C && H == GridProj256::H && cdtype == PF_BF16; }
+
+template <class TZ>
+__global__ __launch_bounds__(GridProj256::NT, 1) void grid_project256_kernel(
+    const TZ* __restrict__ z, const float* __restrict__ mask, const float* __restrict__ lnw,
+    const float* __restrict__ lnb, float eps, const bf16* __restrict__ w5, bf16* __restrict__ Q,
+    bf16* __restrict__ K, bf16* __restrict__ Vt, float* __restrict__ PB, float* __restrict__ MA,
+    bf16* __restrict__ G, int B, int N, int Np, int transpose, float qscale, size_t gq, size_t gpb) {
+  using Cfg = GridProj256;
+  constexpr int C = Cfg::C, BP = Cfg::BP, NCH = Cfg::NCH, NS = Cfg::NS, TLD = Cfg::TLD, VLD = Cfg::VLD;
+  // bf16 rows: the next tile's rows load during this tile's chunks (a second register set
+  // would not fit fp32 rows)
+  constexpr bool PREFETCH = sizeof(TZ) == 2;
+  constexpr int NPIECE = C / 16 * (int)sizeof(TZ) / 2;  // 16-byte loads of a lane's half row
+  __shared__ __attribute__((aligned(16))) char ring[NS * Cfg::CHUNK];
+  __shared__ __attribute__((aligned(16))) char stage[2][Cfg::STAGE];
+  __shared__ float lnp[2 * C];
+
+  const int w = wave_id();
+  const int l = lane_id();
+  const int lq = l & 31, hf = l >> 5;
+  const int rb = w & 1;   // rows 32 rb .. of each chunk
+  const int pb = w >> 1;  // tokens 32 pb ..
+  const int NT1 = Np / BP;
+  const long ntiles = (long)B * N * NT1;
+  const size_t NN = (size_t)N * N;
+  const long total = blockIdx.x < ntiles ? ((ntiles - 1 - blockIdx.x) / gridDim.x + 1) * NCH : 0;
+
+  for (int i = threadIdx.x; i < C; i += Cfg::NT) {
+    lnp[i] = lnw[i];
+    lnp[C + i] = lnb[i];
+  }
+
+  const auto rw = buf_rsrc(w5, Cfg::WROWS * C * 2);
+  auto issue_chunk = [&](long gg) {
+    const int c = (int)(gg % NCH);
+    char* st = ring + (gg % NS) * Cfg::CHUNK;
+#pragma unroll
+    for (int t = 0; t < Cfg::DMA; ++t) {
+      const int ins = w * Cfg::DMA + t;  // two 512-byte rows per instruction
+      const int row = 2 * ins + (l >> 5);
+      const int lc = (l & 31) ^ (row & 15);
+      // the bias chunk's rows past the packed weights repeat its last row (never used)
+      const int src = min(c * Cfg::CR + row, Cfg::WROWS - 1);
+      buf_load_lds16(rw, st + ins * 1024, (src * C + 8 * lc) * 2, 0);
+    }
+  };
+  auto tile_pos = [&](long tl, int& b, int& line, int& t0) {
+    b = (int)(tl / ((long)N * NT1));
+    const long r = tl - (long)b * N * NT1;
+    line = (int)(r / NT1);
+    t0 = (int)(r - (long)line * NT1) * BP;
+  };
+  auto zpos = [&](int line, int t) { return transpose ? (size_t)t * N + line : (size_t)line * N + t; };
+  // this lane's half row of tile tl: channels 16 ks + 8 hf .. +7, ks = 0..15 (zeros past N)
+  u32x4 zr[NPIECE];
+  auto load_half = [&](long tl) {
+    int b, line, t0;
+    tile_pos(tl, b, line, t0);
+    const int t = t0 + 32 * pb + lq;
+    const TZ* src = t < N ? z + ((size_t)b * NN + zpos(line, t)) * C + 8 * hf : nullptr;
+#pragma unroll
+    for (int ks = 0; ks < C / 16; ++ks) {
+      if constexpr (sizeof(TZ) == 2) {
+        zr[ks] = src ? *reinterpret_cast<const u32x4*>(src + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+      } else {
+        zr[2 * ks] = src ? *reinterpret_cast<const u32x4*>(src + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+        zr[2 * ks + 1] = src ? *reinterpret_cast<const u32x4*>(src + 16 * ks + 4) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto get = [&](int ks, float (&v)[8]) {
+    if constexpr (sizeof(TZ) == 2) {
+      const bf16x8 t = __builtin_bit_cast(bf16x8, zr[ks]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (float)t[e];
+    } else {
+      const f32x4 a = __builtin_bit_cast(f32x4, zr[2 * ks]), c4 = __builtin_bit_cast(f32x4, zr[2 * ks + 1]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = a[e];
+        v[4 + e] = c4[e];
+      }
+    }
+  };
+  // Chunk gg's staged values -> their destination (tile b, line, t0). Chunk c < 16 holds
+  // part c / 4 (q, k, v, g) of heads 2 (c % 4) + rb; chunk 16 the bias of the 8 heads.
+  auto store_chunk = [&](long gg, int b, int line, int t0) {
+    const int c = (int)(gg % NCH);
+    const char* sb = stage[gg & 1];
+    const int idx = threadIdx.x;
+    if (c == NCH - 1) {
+      // bias: 8 heads x 32 pieces of 4 floats; row `line` of [b][head][Np][Np] in both modes
+      if (idx < 256) {
+        const int h8 = idx >> 5, p4 = idx & 31;
+        float* dst = PB + (h8 >> 2) * gpb + (((size_t)b * 4 + (h8 & 3)) * Np + line) * Np + t0 + 4 * p4;
+        *reinterpret_cast<f32x4*>(dst) = *reinterpret_cast<const f32x4*>(sb + (h8 * BP + 4 * p4) * 4);
+      }
+      return;
+    }
+    const int part = c >> 2, hp = c & 3;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const int pc = idx + 512 * k2;
+      const int r2 = pc >> 9;  // rb of the staged rows
+      const int head = 2 * hp + r2;
+      const size_t bsh = ((size_t)b * N + line) * 4 + (head & 3);
+      const size_t grp = (size_t)(head >> 2) * gq;
+      if (part == 0 || part == 3) {
+        const int tok = (pc >> 2) & (BP - 1), c4 = pc & 3;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(sb + ((r2 * BP + tok) * TLD + 8 * c4) * 2);
+        if (part == 0) {
+          *reinterpret_cast<u32x4*>(Q + grp + (bsh * Np + t0 + tok) * kHeadDim + 8 * c4) = v;
+        } else if (t0 + tok < N) {
+          *reinterpret_cast<u32x4*>(G + ((size_t)b * NN + zpos(line, t0 + tok)) * Cfg::HD + head * kHeadDim +
+                                    8 * c4) = v;
+        }
+      } else {
+        // key-block tiles: piece pi = 32 cc + row of block kb, cc = 2 (c8 & 1) + (c8 >> 1)
+        const int kb = (pc >> 7) & 3, pi = pc & 127;
+        const int row = pi & 31, cc = pi >> 5;
+        const int c8 = ((cc & 1) << 1) | (cc >> 1);
+        const size_t dst = grp + (bsh * Np + t0 + 32 * kb) * kHeadDim + 8 * pi;
+        if (part == 1)  // K: 8 dims of token 32 kb + row
+          *reinterpret_cast<u32x4*>(K + dst) =
+              *reinterpret_cast<const u32x4*>(sb + ((r2 * BP + 32 * kb + row) * TLD + 8 * c8) * 2);
+        else  // Vt: dim `row`, slots 8 c8 .. of block kb
+          *reinterpret_cast<u32x4*>(Vt + dst) =
+              *reinterpret_cast<const u32x4*>(sb + ((r2 * 32 + row) * VLD + 32 * kb + 8 * c8) * 2);
+      }
+    }
+  };
+
+  long g = 0;
+  long tile = blockIdx.x;
+  int sbb = 0, sline = 0, st0 = 0;  // tile of the chunk waiting in the stage
+  if (total > 0) {
+    if (PREFETCH) load_half(tile);
+    issue_chunk(0);
+  }
+  __syncthreads();  // LN parameters
+
+  for (; tile < ntiles; tile += gridDim.x) {
+    int b, line, t0;
+    tile_pos(tile, b, line, t0);
+    const int tpos = t0 + 32 * pb + lq;
+    const bool live = tpos < N;
+    const float mk = live ? mask[(size_t)b * NN + zpos(line, tpos)] : 0.f;
+    if (!PREFETCH) load_half(tile);  // fp32 rows: loaded per tile, dead after the LayerNorm
+    // the line mask of this tile's keys (log2 units; -inf past N)
+    if (rb == 0 && hf == 0)
+      MA[((size_t)b * N + line) * Np + t0 + 32 * pb + key_slot(lq)] =
+          live ? (mk - 1.0f) * 1e9f * kLog2e : -INFINITY;
+
+    // ---- LN -> B operands xf[ks]: channels 16 ks + 8 hf .. +7
+    bf16x8 xf[C / 16];
+    {
+      float s = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        get(ks, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += v[e];
+      }
+      s += __shfl_xor(s, 32, 64);
+      const float mean = s * (1.0f / C);
+      float q = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        get(ks, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[e] - mean;
+          q += d * d;
+        }
+      }
+      q += __shfl_xor(q, 32, 64);
+      const float rstd = rsqrtf(q * (1.0f / C) + eps);
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        float v[8];
+        get(ks, v);
+        const float* pw = lnp + 16 * ks + 8 * hf;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[ks][e] = (bf16)((v[e] - mean) * rstd * pw[e] + pw[C + e]);
+      }
+    }
+    const bool more = tile + gridDim.x < ntiles;
+
+#pragma unroll 1
+    for (int c = 0; c < NCH; ++c, ++g) {
+      // Chunk g's weights landed in every wave. Past the barrier, ring slot (g + 1) % NS (read
+      // by chunk g - 1's MFMAs) takes chunk g + 1, and stage (g - 1) & 1 leaves for its
+      // destination before chunk g + 1's barrier lets it be rewritten.
+      __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+      lds_barrier();
+      if (g > 0) store_chunk(g - 1, sbb, sline, st0);
+      if (PREFETCH && c == 1 && more) load_half(tile + gridDim.x);  // zr is free after LN
+      if (g + NS - 1 < total) issue_chunk(g + NS - 1);
+      if (c < NCH - 1 || rb == 0) {  // the bias chunk's rows 32 .. are empty
+        const char* st = ring + (g % NS) * Cfg::CHUNK;
+        f32x16 acc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < C / 16; ++ks) {
+          const bf16x8 wf = *reinterpret_cast<const bf16x8*>(st + gp256_off(32 * rb + lq, 2 * ks + hf));
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xf[ks], acc, 0, 0, 0);
+        }
+        // acc[e]: chunk row 32 rb + 8 (e >> 2) + 4 hf + (e & 3), token 32 pb + lq
+        char* sb = stage[g & 1];
+        const int tok = 32 * pb + lq;
+        const int part = c >> 2;
+        if (c == NCH - 1) {
+          // bias rows 0..7 (heads 4 hf + e): head-major, key-slot order for rows
+          const int col = transpose ? tok : 32 * pb + key_slot(lq);
+          float* bs = reinterpret_cast<float*>(sb);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bs[(4 * hf + e) * BP + col] = live ? acc[e] * kLog2e : 0.f;
+        } else if (part == 2) {
+          // Vt: [rb][d][slot] (zero past N)
+          bf16* vs = reinterpret_cast<bf16*>(sb) + rb * 32 * VLD;
+          const int slot = 32 * pb + key_slot(lq);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) vs[(8 * (e >> 2) + 4 * hf + (e & 3)) * VLD + slot] = (bf16)(live ? acc[e] : 0.f);
+        } else {
+          // Q (scaled), K, G: [rb][token][d] (Q and K zero past N)
+          const float sc = part == 0 ? qscale : 1.0f;
+          const float keep = (part == 3 || live) ? sc : 0.f;
+          bf16* ts = reinterpret_cast<bf16*>(sb) + (rb * BP + tok) * TLD;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            bf16x4 v4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = (bf16)(acc[4 * j + e] * keep);
+            *reinterpret_cast<bf16x4*>(ts + 8 * j + 4 * hf) = v4;
+          }
+        }
+      }
+      sbb = b;
+      sline = line;
+      st0 = t0;
+    }
+  }
+  if (total > 0) {
+    lds_barrier();
+    store_chunk(g - 1, sbb, sline, st0);
+  }
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // no direct load outlives the block
+}
+
+// Rows N .. Np - 1 of each pair-bias matrix (keys past N once column mode has transposed
+// it; padding queries in row mode) get no tile: zero them so every bias value is finite.
+__global__ __launch_bounds__(256) void pb_zero_pad_rows_kernel(float* __restrict__ PB, int N, int Np) {
+  float* m = PB + (size_t)blockIdx.y * Np * Np + (size_t)N * Np;
+  const long n4 = (long)(Np - N) * Np / 4;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long)gridDim.x * 256)
+    reinterpret_cast<f32x4*>(m)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+template <class TZ>
+int grid_attn256_launch(const void* z, const float* mask, const float* lnw, const float* lnb, float eps,
+                        const void* w5, const void* wo, int B, int N, int transpose, void* out, int accumulate,
+                        void* ws, hipStream_t s) {
+  using Cfg = GridProj256;
+  const int Np = (int)pf::round_up((size_t)N, kPad);
+  const Grid256Ws L = grid256_layout(B, N);
+  char* base = reinterpret_cast<char*>(ws);
+  bf16* Q = reinterpret_cast<bf16*>(base + L.q);
+  bf16* K = reinterpret_cast<bf16*>(base + L.k);
+  bf16* V = reinterpret_cast<bf16*>(base + L.v);
+  float* PB = reinterpret_cast<float*>(base + L.pb);
+  float* MA = reinterpret_cast<float*>(base + L.ma);
+  bf16* G = reinterpret_cast<bf16*>(base + L.g);
+  bf16* og = reinterpret_cast<bf16*>(base + L.og);
+  int* redo = reinterpret_cast<int*>(base + L.redo);
+  const long M = (long)B * N * N;
+  const float qscale = (1.0f / sqrtf((float)kHeadDim)) * kLog2e;
+  {
+    const long ntiles = (long)B * N * (Np / Cfg::BP);
+    const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+    pf::KernelTimer timer("grid_project256", s);
+    grid_project256_kernel<TZ><<<nblk, Cfg::NT, 0, s>>>((const TZ*)z, mask, lnw, lnb, eps, (const bf16*)w5, Q, K,
+                                                        V, PB, MA, G, B, N, Np, transpose, qscale, L.gq, L.gpb);
+    timer.stop();
+    if (int e = pf::check_launch("grid_project256")) return e;
+  }
+  const int HD = Cfg::HD;
+  const long NN = (long)N * N;
+  // o of (b, line, head, token) at og[pos][head d + e]: pos = (line, token) for rows,
+  // (token, line) for columns
+  const Strides4 so = transpose ? Strides4{NN * HD, (long)HD, (long)kHeadDim, (long)N * HD}
+                                : Strides4{NN * HD, (long)N * HD, (long)kHeadDim, (long)HD};
+  constexpr int QS = attn_qsub<bf16>();
+  constexpr int NT = 64 * kLinesPerBlock;
+  const int nqb = Np / (32 * QS);
+  const int nlg = (N + kLinesPerBlock - 1) / kLinesPerBlock;
+  const long total = (long)B * nlg * kHeads * nqb;
+  const int remap = (total % 8 == 0) ? 1 : 0;
+  if (Np > N) {
+    const long n4 = (long)(Np - N) * Np / 4;
+    pb_zero_pad_rows_kernel<<<dim3((unsigned)std::min<long>((n4 + 255) / 256, 64), 2 * B * kHeads), 256, 0, s>>>(
+        PB, N, Np);
+    if (int e = pf::check_launch("pb_zero_pad_rows")) return e;
+  }
+  for (int gi = 0; gi < 2; ++gi) {
+    bf16* Qg = Q + gi * L.gq;
+    bf16* Kg = K + gi * L.gq;
+    bf16* Vg = V + gi * L.gq;
+    float* PBg = PB + gi * L.gpb;
+    int* rg = redo + gi * L.gredo;
+    bf16* Og = og + gi * 4 * kHeadDim;
+    if (transpose) {
+      const int nt = Np / 32;
+      pb_transpose_kernel<<<dim3(nt * (nt + 1) / 2, B * kHeads), 256, 0, s>>>(PBg, Np, nullptr, N);
+      if (int e = pf::check_launch("pb_transpose")) return e;
+    }
+    pf::KernelTimer timer("tri_attn", s);
+    tri_attn_kernel<bf16, QS, true, true, false, true><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<bf16>(), s>>>(
+        Qg, Kg, Vg, PBg, MA, Og, B, N, Np, N, N, 0, remap, rg, 1.f, so);
+    timer.stop();
+    if (int e = pf::check_launch("tri_attn")) return e;
+    tri_attn_kernel<bf16, QS, true, false, false, true><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<bf16>(), s>>>(
+        Qg, Kg, Vg, PBg, MA, Og, B, N, Np, N, N, 0, remap, rg, 1.f, so);
+    if (int e = pf::check_launch("tri_attn_redo")) return e;
+  }
+  grid_gen_gate_inplace_kernel<bf16><<<(unsigned)((M * (HD / 8) + 255) / 256), 256, 0, s>>>(og, G, M, HD, HD, 0);
+  if (int e = pf::check_launch("grid_gen_gate")) return e;
+  if (accumulate) return rowgemm_launch<bf16, TZ, EPI_RESIDUAL>(og, wo, nullptr, 0, out, M, Cfg::C, HD, s);
+  return rowgemm_launch<bf16, TZ, EPI_STORE>(og, wo, nullptr, 0, out, M, Cfg::C, HD, s);
 }
 
 template <class TZ, class TC>
@@ -1842,6 +2254,9 @@ int grid_attn_generic_launch(const void* z, const float* mask, const float* lnw,
                              const void* w5, const void* wo, int B, int N, int C, int H, int transpose, void* out,
                              int accumulate, void* ws, hipStream_t s) {
   const int cd = sizeof(TC) == 4 ? PF_F32 : PF_BF16;
+  if constexpr (sizeof(TC) == 2)
+    if (grid256_applies(C, H, cd))
+      return grid_attn256_launch<TZ>(z, mask, lnw, lnb, eps, w5, wo, B, N, transpose, out, accumulate, ws, s);
   const GridGenWs L = grid_gen_layout(B, N, C, H, cd);
   const int d = grid_gen_head_dim(C, H);
   const int H4 = (H + 3) / 4 * 4;
@@ -1881,7 +2296,8 @@ int grid_attn_generic_launch(const void* z, const float* mask, const float* lnw,
                                       1.0f / sqrtf((float)d), &sx, &so))
         return e;
     }
-    grid_gen_gate_inplace_kernel<TC><<<(unsigned)((M * (HD / 8) + 255) / 256), 256, 0, s>>>(og, proj, M, HD, PW);
+    grid_gen_gate_inplace_kernel<TC><<<(unsigned)((M * (HD / 8) + 255) / 256), 256, 0, s>>>(og, proj, M, HD, PW,
+                                                                                          3 * HD);
     if (int e = pf::check_launch("grid_gen_gate")) return e;
     if (accumulate) return rowgemm_launch<TC, TZ, EPI_RESIDUAL>(og, wo, nullptr, 0, out, M, C, HD, s);
     return rowgemm_launch<TC, TZ, EPI_STORE>(og, wo, nullptr, 0, out, M, C, HD, s);
@@ -1919,6 +2335,7 @@ extern "C" {
 size_t pf_grid_attn_workspace_bytes(int B, int N, int C, int H, int cdtype) {
   if (B <= 0 || N <= 0) return 0;
   if (C == kC && H == kHeads) return attn_ws_layout(B, N, cdtype).total;
+  if (grid256_applies(C, H, cdtype)) return grid256_layout(B, N).total;
   return grid_gen_supported(C, H) ? grid_gen_layout(B, N, C, H, cdtype).total : 0;
 }
 
@@ -1989,10 +2406,15 @@ int pf_grid_attn_redo_flags(int B, int N, int C, int H, int cdtype, size_t* offs
   const bool fused = C == kC && H == kHeads;
   PF_REQUIRE(B > 0 && N > 0 && (fused || grid_gen_supported(C, H)) && (cdtype == PF_F32 || cdtype == PF_BF16),
              PF_ERR_UNSUPPORTED, "pf_grid_attn_redo_flags: B=%d N=%d C=%d H=%d cdtype=%d", B, N, C, H, cdtype);
-  // generic channels: the flags of the last group of four heads
+  // generic channels: the flags of the last group of four heads (256 channels: both groups)
+  *count = redo_flag_count(B, N, pf::pad128(N), cdtype);
+  if (!fused && grid256_applies(C, H, cdtype)) {
+    const Grid256Ws L = grid256_layout(B, N);
+    *offset = L.redo + L.gredo * sizeof(int);
+    return pf::ok();
+  }
   *offset = fused ? attn_ws_layout(B, N, cdtype).redo
                   : grid_gen_layout(B, N, C, H, cdtype).evo + evo_ws_layout(B, N, N, cdtype).redo;
-  *count = redo_flag_count(B, N, pf::pad128(N), cdtype);
   return pf::ok();
 }
 
