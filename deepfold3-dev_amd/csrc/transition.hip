@@ -789,6 +789,8 @@ __global__ __launch_bounds__(256) void single_to_pair_mfma_kernel(const TZ* __re
                                                                   long M, long NN) {
   constexpr int LPR = C / 8;
   constexpr int RPP = 64 / LPR;  // rows per pass
+  constexpr int NPASS = 16 / RPP;
+  constexpr int NV = sizeof(TZ) == 2 ? 1 : 2;  // 16-byte loads per lane per pass
   constexpr int LDC = C + 8;
   static_assert(C % 64 == 0 && C <= 256, "64 to 256 channels");
   __shared__ __attribute__((aligned(16))) bf16 tile[4][16 * LDC];
@@ -797,35 +799,49 @@ __global__ __launch_bounds__(256) void single_to_pair_mfma_kernel(const TZ* __re
   bf16* t = tile[wv];
   const long r0 = ((long)blockIdx.x * 4 + wv) * 16;
   const int c0 = (l % LPR) * 8;
+  // Every pass's row piece is requested before any is used (one memory round trip per
+  // wave, not one per pass); the lane's LayerNorm parameters are read once.
+  u32x4 raw[NPASS][NV];
 #pragma unroll
-  for (int pass = 0; pass < 16 / RPP; ++pass) {
-    const int rr = pass * RPP + l / LPR;
-    const long row = min(r0 + rr, M - 1);
+  for (int pass = 0; pass < NPASS; ++pass) {
+    const long row = min(r0 + pass * RPP + l / LPR, M - 1);
     const TZ* src = z + row * C + c0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) raw[pass][j] = *reinterpret_cast<const u32x4*>(src + 4 * j);
+  }
+  float lw[8], lbv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    lw[e] = lnw[c0 + e];
+    lbv[e] = lnb[c0 + e];
+  }
+#pragma unroll
+  for (int pass = 0; pass < NPASS; ++pass) {
+    const int rr = pass * RPP + l / LPR;
     float v[8];
     if constexpr (sizeof(TZ) == 2) {
-      load16<TZ>(src, v);
+      const bf16x8 b8 = __builtin_bit_cast(bf16x8, raw[pass][0]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (float)b8[e];
     } else {
-      float a[4], b[4];
-      load16<TZ>(src, a);
-      load16<TZ>(src + 4, b);
+      const f32x4 a = __builtin_bit_cast(f32x4, raw[pass][0]), b = __builtin_bit_cast(f32x4, raw[pass][NV - 1]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = a[e], v[e + 4] = b[e];
     }
     float sm = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) sm += v[e];
-    const float mean = group_sum<LPR>(sm) / C;
+    const float mean = (LPR >= 16 ? row_group_sum<(LPR >= 32 ? 32 : 16)>(sm) : group_sum<LPR>(sm)) / C;
     float q = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float d = v[e] - mean;
       q += d * d;
     }
-    const float rstd = rsqrtf(group_sum<LPR>(q) / C + eps);
+    const float rstd = rsqrtf((LPR >= 16 ? row_group_sum<(LPR >= 32 ? 32 : 16)>(q) : group_sum<LPR>(q)) / C + eps);
     float y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = (v[e] - mean) * rstd * lnw[c0 + e] + lnb[c0 + e];
+    for (int e = 0; e < 8; ++e) y[e] = (v[e] - mean) * rstd * lw[e] + lbv[e];
     store_vec<bf16, 8>(t + rr * LDC + c0, y);
   }
   __syncthreads();  // the tile's rows are in LDS
@@ -839,11 +855,26 @@ __global__ __launch_bounds__(256) void single_to_pair_mfma_kernel(const TZ* __re
     const MF::Frag bf = MF::load(w + (size_t)r * C + k0 + kq);
     MF::mma16(acc, af, bf);
   }
-  // acc[e]: position r0 + 4 (l >> 4) + e, head l & 15
+  // acc[e]: position r0 + 4 (l >> 4) + e, head l & 15. The block's 64 positions go through
+  // LDS so each head's run leaves as 16-byte stores (256 contiguous bytes per head) instead of
+  // 4-byte stores scattered over the 16 head planes.
+  __shared__ __attribute__((aligned(16))) float ot[kS2pHeads][64 + 4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const long row = r0 + 4 * (l >> 4) + e;
-    if (row < M) logits[((row / NN) * kS2pHeads + r) * NN + row % NN] = acc[e];
+  for (int e = 0; e < 4; ++e) ot[r][16 * wv + 4 * (l >> 4) + e] = acc[e];
+  __syncthreads();
+  const long p0 = (long)blockIdx.x * 64;
+  if (NN % 64 == 0 && p0 + 64 <= M) {
+    // one batch item, 16-byte aligned runs
+    const int h = threadIdx.x >> 4, pc = threadIdx.x & 15;
+    *reinterpret_cast<f32x4*>(logits + ((p0 / NN) * kS2pHeads + h) * NN + p0 % NN + 4 * pc) =
+        *reinterpret_cast<const f32x4*>(&ot[h][4 * pc]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = threadIdx.x + 256 * i;  // (head, position) = (k >> 6, k & 63)
+      const long row = p0 + (k & 63);
+      if (row < M) logits[((row / NN) * kS2pHeads + (k >> 6)) * NN + row % NN] = ot[k >> 6][k & 63];
+    }
   }
 }
 
