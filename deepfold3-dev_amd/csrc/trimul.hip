@@ -1365,6 +1365,211 @@ __global__ __launch_bounds__(OutputWs::NT) void trimul_output_ws_kernel(
   }
 }
 
+// K3 at 256 channels, persistent and weight-stationary (bf16 GEMMs, bf16 z). One 512-thread
+// block per CU walks tiles of 64 positions (i, j0 .. j0+63) of one row. Wave w owns output
+// channels 32 w .. +32 for both position halves: its rows of out_proj and out_gate stay in
+// registers for the whole launch as 32x32x16 MFMA A operands (128 VGPRs), so no weight
+// bytes move per tile. Per tile: the X tile (channel-major, 256 x 64, loaded into registers
+// one tile ahead) goes to LDS and is normalised (LN_out) by a pass whose reads run along
+// positions; the z rows (also one tile ahead) are normalised (LN_in) from registers that
+// keep them for the residual; each 32-position half then runs 32 MFMAs per wave, stages its
+// fp32 update block-wide and adds it to the z rows of that half.
+struct Output256 {
+  static constexpr int C = 256;
+  static constexpr int BP = 64;
+  static constexpr int NW = 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int XLD = C + 8;   // bf16 operand rows [pos][ch]
+  static constexpr int TLD = BP + 8;  // bf16 X tile rows [ch][pos]
+  static constexpr int SLD = C + 4;   // fp32 update stage rows [pos][ch], one half tile
+};
+
+__global__ __launch_bounds__(Output256::NT, 1) void trimul_output256_kernel(
+    const bf16* __restrict__ X, const bf16* __restrict__ z, bf16* __restrict__ out, const float* __restrict__ lniw,
+    const float* __restrict__ lnib, float eps_in, const float* __restrict__ lnow, const float* __restrict__ lnob,
+    float eps_out, const bf16* __restrict__ Wo, const bf16* __restrict__ Wog, int B, int N, int Np, int accumulate) {
+  using Cfg = Output256;
+  constexpr int C = Cfg::C, BP = Cfg::BP, NW = Cfg::NW, NT = Cfg::NT, XLD = Cfg::XLD, TLD = Cfg::TLD,
+                SLD = Cfg::SLD;
+  constexpr int VEC = 8;                 // z elements per 16-byte load
+  constexpr int LPR = C / VEC;           // lanes per z row (32)
+  constexpr int RPI = 64 / LPR;          // z rows per wave-wide load (2)
+  constexpr int RPW = BP / NW;           // z rows per wave per tile (8)
+  constexpr int NLD = RPW / RPI;         // z loads per lane per tile (4)
+  constexpr int XLDS = C * BP / 8 / NT;  // 16-byte X loads per lane per tile (4)
+  __shared__ __attribute__((aligned(16))) bf16 xt[C * TLD];   // X tile [ch][pos]
+  __shared__ __attribute__((aligned(16))) bf16 xa[BP * XLD];  // LN_out(X) [pos][ch]
+  __shared__ __attribute__((aligned(16))) bf16 xb[BP * XLD];  // LN_in(z) [pos][ch]
+  __shared__ __attribute__((aligned(16))) float upd[32 * SLD];
+  __shared__ float lno[2 * C];  // LN_out weight | bias
+  __shared__ float lni[2 * C];  // LN_in weight | bias
+
+  const int tid = threadIdx.x;
+  const int w = wave_id();
+  const int l = lane_id();
+  const int lq = l & 31, hf = l >> 5;
+  const int pe = Np * Np;  // plane size (elements); checked below 2^31 / C at launch
+  const int tpr = (N + BP - 1) / BP;
+  const int ntiles = B * N * tpr;
+
+  // Weights: lane holds row 32 w + lq, k = 16 ks + 8 hf + e.
+  bf16x8 wo[C / 16], wg[C / 16];
+#pragma unroll
+  for (int ks = 0; ks < C / 16; ++ks) {
+    const size_t r = (size_t)(32 * w + lq) * C + 16 * ks + 8 * hf;
+    wo[ks] = *reinterpret_cast<const bf16x8*>(Wo + r);
+    wg[ks] = *reinterpret_cast<const bf16x8*>(Wog + r);
+  }
+  for (int i = tid; i < C; i += NT) {
+    lno[i] = lnow[i];
+    lno[C + i] = lnob[i];
+    lni[i] = lniw[i];
+    lni[C + i] = lnib[i];
+  }
+  const int chunk = l % LPR;
+  // LN_out: thread (position op = tid / 8, part os = tid % 8) normalises the channel pairs
+  // 16 k + 2 os + {0, 1}, k = 0..15: the 64 lanes of one read touch 32 distinct dwords in
+  // 32 distinct banks (rows 2 os + 16 k, positions op).
+  const int op = tid >> 3, os = tid & 7;
+  auto och = [&](int c) { return 16 * (c >> 1) + 2 * os + (c & 1); };
+  const int zoff0 = (w * RPW + l / LPR) * C + chunk * VEC;  // + q RPI C for load q
+  const int xoff = (tid >> 3) * pe + 8 * (tid & 7);
+
+  auto tile_coords = [&](int tile, int& b, int& i, int& j0) {
+    b = tile / (N * tpr);
+    const int rem = tile - b * (N * tpr);
+    i = rem / tpr;
+    j0 = (rem - i * tpr) * BP;
+  };
+  u32x4 zr[NLD], xr[XLDS];
+  auto issue = [&](int tile) {
+    int b, i, j0;
+    tile_coords(tile, b, i, j0);
+    const bf16* zb = z + (((size_t)b * N + i) * N + j0) * C;
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      const int j = j0 + w * RPW + q * RPI + l / LPR;
+      zr[q] = j < N ? *reinterpret_cast<const u32x4*>(zb + zoff0 + q * RPI * C) : u32x4{0u, 0u, 0u, 0u};
+    }
+    const bf16* Xb = X + (size_t)b * C * pe + (size_t)i * Np + j0;
+#pragma unroll
+    for (int q = 0; q < XLDS; ++q)
+      xr[q] = *reinterpret_cast<const u32x4*>(Xb + (size_t)q * (NT / 8) * pe + xoff);
+  };
+
+  // After the LN_out pass the X tile's LDS holds the raw z rows [pos][ch] for the residual.
+  bf16* zs = xt;
+  int tile = blockIdx.x;
+  if (tile < ntiles) issue(tile);
+  __syncthreads();  // LN parameters
+  for (; tile < ntiles; tile += gridDim.x) {
+    int b, i, j0;
+    tile_coords(tile, b, i, j0);
+    if (tile != (int)blockIdx.x) __syncthreads();  // the last residual pass is done with zs
+    // X tile -> LDS [ch][pos]; LN_in(z rows) -> xb
+#pragma unroll
+    for (int q = 0; q < XLDS; ++q) {
+      const int c = (tid >> 3) + q * (NT / 8);
+      *reinterpret_cast<u32x4*>(xt + c * TLD + 8 * (tid & 7)) = xr[q];
+    }
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      float zv[VEC];
+      unpack16<bf16>(zr[q], zv);
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum += zv[e];
+      const float mean = row_group_sum<LPR>(sum) * (1.0f / C);
+      float sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = zv[e] - mean;
+        sq += d * d;
+      }
+      const float rstd = rsqrtf(row_group_sum<LPR>(sq) * (1.0f / C) + eps_in);
+      float y[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) y[e] = (zv[e] - mean) * rstd * lni[chunk * VEC + e] + lni[C + chunk * VEC + e];
+      store_vec<bf16, VEC>(xb + (w * RPW + q * RPI + l / LPR) * XLD + chunk * VEC, y);
+    }
+    __syncthreads();  // xt complete
+    {
+      float v[32];
+      float sum = 0.f;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) {
+        v[c] = (float)xt[och(c) * TLD + op];
+        sum += v[c];
+      }
+      const float mean = dpp_sum8(sum) * (1.0f / C);
+      float sq = 0.f;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) {
+        const float d = v[c] - mean;
+        sq += d * d;
+      }
+      const float rstd = rsqrtf(dpp_sum8(sq) * (1.0f / C) + eps_out);
+#pragma unroll
+      for (int c = 0; c < 32; ++c) v[c] = (v[c] - mean) * rstd * lno[och(c)] + lno[C + och(c)];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) store_vec<bf16, 2>(xa + op * XLD + och(2 * k), v + 2 * k);
+    }
+    __syncthreads();  // xa, xb complete; every wave is done with the X tile
+    // raw z rows -> zs (each lane reads back only what it wrote), then the next tile's loads
+#pragma unroll
+    for (int q = 0; q < NLD; ++q)
+      *reinterpret_cast<u32x4*>(zs + (w * RPW + q * RPI + l / LPR) * C + chunk * VEC) = zr[q];
+    const int next = tile + gridDim.x;
+    if (next < ntiles) issue(next);
+
+    bf16* ob = out + ((size_t)b * N + i) * N * C;
+#pragma unroll 1
+    for (int pt = 0; pt < 2; ++pt) {
+      f32x16 ao, ag;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ao[r] = ag[r] = 0.f;
+      const int brow = (32 * pt + lq) * XLD + 8 * hf;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const bf16x8 fa = *reinterpret_cast<const bf16x8*>(xa + brow + 16 * ks);
+        const bf16x8 fb = *reinterpret_cast<const bf16x8*>(xb + brow + 16 * ks);
+        ao = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wo[ks], fa, ao, 0, 0, 0);
+        ag = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wg[ks], fb, ag, 0, 0, 0);
+      }
+      if (pt == 1) __syncthreads();  // the first half's residual pass is done with upd
+      // update = sigmoid(gate) * out: lane holds channels 32 w + acc32_row(r) of position
+      // 32 pt + lq.
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        f32x4 u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) u[e] = sigmoidf_(ag[4 * g4 + e]) * ao[4 * g4 + e];
+        *reinterpret_cast<f32x4*>(upd + lq * SLD + 32 * w + acc32_row(4 * g4)) = u;
+      }
+      __syncthreads();  // this half's update complete
+      // waves 4 pt .. 4 pt + 3 hold the z rows of positions 32 pt ..
+      if ((w >> 2) == pt) {
+#pragma unroll
+        for (int q = 0; q < NLD; ++q) {
+          const int p = w * RPW + q * RPI + l / LPR;
+          const int j = j0 + p;
+          if (j >= N) continue;
+          float zv[VEC], y[VEC];
+          unpack16<bf16>(*reinterpret_cast<const u32x4*>(zs + p * C + chunk * VEC), zv);
+#pragma unroll
+          for (int e = 0; e < VEC; e += 4) {
+            const f32x4 u = *reinterpret_cast<const f32x4*>(upd + (p - 32 * pt) * SLD + chunk * VEC + e);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) y[e + k] = accumulate ? zv[e + k] + u[k] : u[k];
+          }
+          store_vec<bf16, VEC>(ob + (size_t)j * C + chunk * VEC, y);
+        }
+      }
+    }
+  }
+}
+
+
 // K3 on 64 positions of one row i: X tile (channel-major) -> LN_out -> A1 [pos][ch];
 // LN_in(z) -> A2; acc^T for g = Wog A2^T and p = Wo A1^T (wave w: channels 32 w, all 64
 // positions), update = sigmoid(g) p through an fp32 stage, stored or added.
@@ -1604,6 +1809,15 @@ int trimul_launch(const void* z, const float* mask, const float* lniw, const flo
       trimul_output_ws_kernel<TZ><<<nblk, OutputWs::NT, 0, s>>>((const bf16*)X, (const TZ*)z, (TZ*)out, lniw, lnib,
                                                                 eps_in, lnow, lnob, eps_out, (const bf16*)wo,
                                                                 (const bf16*)wog, B, N, Np, accumulate);
+      (void)grid;
+    } else if constexpr (sizeof(TC) == 2 && C == 256 && sizeof(TZ) == 2) {
+      const long ntiles = (long)B * N * ((N + Output256::BP - 1) / Output256::BP);
+      PF_REQUIRE(ntiles < (1L << 31) && (long)Np * Np * Output256::C < (1L << 31), PF_ERR_UNSUPPORTED,
+                 "trimul_output: N=%d B=%d (B N ceil(N/64) and 256 Np^2 must stay below 2^31)", N, B);
+      const int nblk = (int)std::min<long>(ntiles, pf::cu_count());
+      trimul_output256_kernel<<<nblk, Output256::NT, 0, s>>>((const bf16*)X, (const bf16*)z, (bf16*)out, lniw, lnib,
+                                                             eps_in, lnow, lnob, eps_out, (const bf16*)wo,
+                                                             (const bf16*)wog, B, N, Np, accumulate);
       (void)grid;
     } else
       trimul_output_kernel<TZ, TC, C><<<grid, trimul_nt<C>(), 0, s>>>(X, (const TZ*)z, (TZ*)out, lniw, lnib, eps_in, lnow,
