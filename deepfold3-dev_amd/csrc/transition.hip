@@ -533,9 +533,10 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
       __builtin_amdgcn_wave_barrier();  // u reads issued before the next chunk's writes
     }
 
-    // ---- next tile's rows (their latency overlaps this epilogue), then the residual
-    // operands, all issued before any of them is used.
-    if (tile + gridDim.x < ntiles) zr.load(x, (tile + gridDim.x) * BP + w * PW + lq, M, hf);
+    // ---- the residual operands, then the next tile's rows (their latency overlaps this
+    // epilogue and the next tile's first chunk), all issued before any of them is used.
+    // Loads complete in issue order: the rows issued first would hold up every wait on
+    // the residual.
     // Lane (position lq, half hf) holds channels 32 o + 8 gq + 4 hf + e of y[o][4 gq + e].
     // Swapping the (gq = 2 p, gq = 2 p + 1) registers between lanes l and l + 32 leaves lane
     // hf with channels 32 o + 16 p + 8 hf + e, e = 0..7, in v[o][8 p + e]: 16-byte row
@@ -552,41 +553,57 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
           v[o][8 * pp + e] = a;
           v[o][8 * pp + 4 + e] = b;
         }
-    float res[4][16];
-    if (accumulate && m < M) {
-      const TZ* row = out + m * C;
+    // Raw 16-byte pieces of the residual row, unpacked after the next tile's loads are
+    // issued. Both groups of loads are unconditional (a position past M reads row M - 1,
+    // never stored), so the compiler counts them exactly on every path.
+    constexpr int RN = sizeof(TZ) == 2 ? 8 : 16;
+    u32x4 rr[RN];
+    {
+      const TZ* row = out + min(m, M - 1) * C;
 #pragma unroll
       for (int o = 0; o < 4; ++o)
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
           const TZ* src = row + 32 * o + 16 * pp + 8 * hf;
           if constexpr (sizeof(TZ) == 2) {
-            load16<bf16>(src, *reinterpret_cast<float(*)[8]>(&res[o][8 * pp]));
+            rr[2 * o + pp] = *reinterpret_cast<const u32x4*>(src);
           } else {
-            load16<float>(src, *reinterpret_cast<float(*)[4]>(&res[o][8 * pp]));
-            load16<float>(src + 4, *reinterpret_cast<float(*)[4]>(&res[o][8 * pp + 4]));
+            rr[2 * (2 * o + pp)] = *reinterpret_cast<const u32x4*>(src);
+            rr[2 * (2 * o + pp) + 1] = *reinterpret_cast<const u32x4*>(src + 4);
           }
         }
-    } else {
-#pragma unroll
-      for (int o = 0; o < 4; ++o)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) res[o][e] = 0.f;
     }
-    if (m < M) {
+    zr.load(x, min((tile + gridDim.x) * BP + w * PW + lq, M - 1), M, hf);
+    __builtin_amdgcn_sched_barrier(0);  // keep the row loads ahead of the residual's waits
+    // the residual add runs for every lane (its loads are used outside the store's branch,
+    // so the compiler keeps them where they are), only the stores are conditional
+    {
       TZ* row = out + m * C;
 #pragma unroll
       for (int o = 0; o < 4; ++o)
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
+          float r8[8];
+          if constexpr (sizeof(TZ) == 2) {
+            const bf16x8 t = __builtin_bit_cast(bf16x8, rr[2 * o + pp]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) r8[e] = (float)t[e];
+          } else {
+            const f32x4 ra = __builtin_bit_cast(f32x4, rr[2 * (2 * o + pp)]);
+            const f32x4 rb = __builtin_bit_cast(f32x4, rr[2 * (2 * o + pp) + 1]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r8[e] = ra[e], r8[4 + e] = rb[e];
+          }
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            v[o][8 * pp + e] = to_f32(from_f32<TZ>(res[o][8 * pp + e] + v[o][8 * pp + e]));  // as stored
-          if constexpr (sizeof(TZ) == 2) {
-            store_vec<bf16, 8>(row + 32 * o + 16 * pp + 8 * hf, &v[o][8 * pp]);
-          } else {
-            store_vec<float, 4>(row + 32 * o + 16 * pp + 8 * hf, &v[o][8 * pp]);
-            store_vec<float, 4>(row + 32 * o + 16 * pp + 8 * hf + 4, &v[o][8 * pp + 4]);
+            v[o][8 * pp + e] = to_f32(from_f32<TZ>((accumulate ? r8[e] : 0.f) + v[o][8 * pp + e]));  // as stored
+          if (m < M) {
+            if constexpr (sizeof(TZ) == 2) {
+              store_vec<bf16, 8>(row + 32 * o + 16 * pp + 8 * hf, &v[o][8 * pp]);
+            } else {
+              store_vec<float, 4>(row + 32 * o + 16 * pp + 8 * hf, &v[o][8 * pp]);
+              store_vec<float, 4>(row + 32 * o + 16 * pp + 8 * hf + 4, &v[o][8 * pp + 4]);
+            }
           }
         }
     }
