@@ -2177,10 +2177,13 @@ __global__ __launch_bounds__(256) void pb_zero_pad_rows_kernel(float* __restrict
     reinterpret_cast<f32x4*>(m)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
+// key_mask (optional): the folded key mask [B][N] of a pair mask that is the outer product of
+// its diagonal; it is then added to the pair bias (rows: a pass over the bias; columns: inside
+// the transpose) and the flash kernel runs without its per-line key-mask MFMA.
 template <class TZ>
 int grid_attn256_launch(const void* z, const float* mask, const float* lnw, const float* lnb, float eps,
                         const void* w5, const void* wo, int B, int N, int transpose, void* out, int accumulate,
-                        void* ws, hipStream_t s) {
+                        const float* key_mask, void* ws, hipStream_t s) {
   using Cfg = GridProj256;
   const int Np = (int)pf::round_up((size_t)N, kPad);
   const Grid256Ws L = grid256_layout(B, N);
@@ -2231,18 +2234,35 @@ int grid_attn256_launch(const void* z, const float* mask, const float* lnw, cons
     bf16* Og = og + gi * 4 * kHeadDim;
     if (transpose) {
       const int nt = Np / 32;
-      pb_transpose_kernel<<<dim3(nt * (nt + 1) / 2, B * kHeads), 256, 0, s>>>(PBg, Np, nullptr, N);
+      pb_transpose_kernel<<<dim3(nt * (nt + 1) / 2, B * kHeads), 256, 0, s>>>(PBg, Np, key_mask, N);
       if (int e = pf::check_launch("pb_transpose")) return e;
+    } else if (key_mask != nullptr) {
+      const long n4 = (long)Np * Np / 4;
+      const int gx = (int)std::min<long>((n4 + 255) / 256, (4L * pf::cu_count() + B * kHeads - 1) / (B * kHeads));
+      pb_fold_kernel<<<dim3(std::max(gx, 1), B * kHeads), 256, 0, s>>>(PBg, key_mask, N, Np);
+      if (int e = pf::check_launch("pb_fold")) return e;
     }
     pf::KernelTimer timer("tri_attn", s);
-    tri_attn_kernel<bf16, QS, true, true, false, true><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<bf16>(), s>>>(
-        Qg, Kg, Vg, PBg, MA, Og, B, N, Np, N, N, 0, remap, rg, 1.f, so);
+    const dim3 grid((unsigned)total);
+    constexpr size_t lds = attn_bias_lds_bytes<bf16>();
+    if (key_mask != nullptr)
+      tri_attn_kernel<bf16, QS, true, true, false, false><<<grid, NT, lds, s>>>(
+          Qg, Kg, Vg, PBg, MA, Og, B, N, Np, N, N, 0, remap, rg, 1.f, so);
+    else
+      tri_attn_kernel<bf16, QS, true, true, false, true><<<grid, NT, lds, s>>>(
+          Qg, Kg, Vg, PBg, MA, Og, B, N, Np, N, N, 0, remap, rg, 1.f, so);
     timer.stop();
     if (int e = pf::check_launch("tri_attn")) return e;
-    tri_attn_kernel<bf16, QS, true, false, false, true><<<dim3((unsigned)total), NT, attn_bias_lds_bytes<bf16>(), s>>>(
-        Qg, Kg, Vg, PBg, MA, Og, B, N, Np, N, N, 0, remap, rg, 1.f, so);
+    if (key_mask != nullptr)
+      tri_attn_kernel<bf16, QS, true, false, false, false><<<grid, NT, lds, s>>>(
+          Qg, Kg, Vg, PBg, MA, Og, B, N, Np, N, N, 0, remap, rg, 1.f, so);
+    else
+      tri_attn_kernel<bf16, QS, true, false, false, true><<<grid, NT, lds, s>>>(
+          Qg, Kg, Vg, PBg, MA, Og, B, N, Np, N, N, 0, remap, rg, 1.f, so);
     if (int e = pf::check_launch("tri_attn_redo")) return e;
   }
+  // (o * sigmoid(g) in the flash kernel's epilogue instead: its gate loads at the end of
+  // every wave cost that kernel 67 us per launch, more than this pass's 136 us per two)
   grid_gen_gate_inplace_kernel<bf16><<<(unsigned)((M * (HD / 8) + 255) / 256), 256, 0, s>>>(og, G, M, HD, HD, 0);
   if (int e = pf::check_launch("grid_gen_gate")) return e;
   if (accumulate) return rowgemm_launch<bf16, TZ, EPI_RESIDUAL>(og, wo, nullptr, 0, out, M, Cfg::C, HD, s);
@@ -2252,11 +2272,12 @@ int grid_attn256_launch(const void* z, const float* mask, const float* lnw, cons
 template <class TZ, class TC>
 int grid_attn_generic_launch(const void* z, const float* mask, const float* lnw, const float* lnb, float eps,
                              const void* w5, const void* wo, int B, int N, int C, int H, int transpose, void* out,
-                             int accumulate, void* ws, hipStream_t s) {
+                             int accumulate, const float* key_mask, void* ws, hipStream_t s) {
   const int cd = sizeof(TC) == 4 ? PF_F32 : PF_BF16;
   if constexpr (sizeof(TC) == 2)
     if (grid256_applies(C, H, cd))
-      return grid_attn256_launch<TZ>(z, mask, lnw, lnb, eps, w5, wo, B, N, transpose, out, accumulate, ws, s);
+      return grid_attn256_launch<TZ>(z, mask, lnw, lnb, eps, w5, wo, B, N, transpose, out, accumulate, key_mask, ws,
+                                     s);
   const GridGenWs L = grid_gen_layout(B, N, C, H, cd);
   const int d = grid_gen_head_dim(C, H);
   const int H4 = (H + 3) / 4 * 4;
@@ -2362,15 +2383,16 @@ int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const 
              "pf_grid_attn_fwd: workspace %zu < %zu bytes", workspace_bytes,
              pf_grid_attn_workspace_bytes(B, N, C, H, cdtype));
   hipStream_t s = pf::as_stream(stream);
-  if (!fused) {  // the generic path takes the per-line mask (key_mask is not used)
+  if (!fused) {  // key_mask: used by the 256-channel bf16 path only (the others take the per-line mask)
+    const float* km = grid256_applies(C, H, cdtype) ? key_mask : nullptr;
     if (zdtype == PF_F32 && cdtype == PF_F32)
       return grid_attn_generic_launch<float, float>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, C, H, transpose,
-                                                    out, accumulate, workspace, s);
+                                                    out, accumulate, km, workspace, s);
     if (zdtype == PF_F32)
       return grid_attn_generic_launch<float, bf16>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, C, H, transpose,
-                                                   out, accumulate, workspace, s);
+                                                   out, accumulate, km, workspace, s);
     return grid_attn_generic_launch<bf16, bf16>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, C, H, transpose, out,
-                                                accumulate, workspace, s);
+                                                accumulate, km, workspace, s);
   }
   if (zdtype == PF_F32 && cdtype == PF_F32)
     return grid_attn_launch<float, float>(z, mask, ln_w, ln_b, eps, w_qkvgb, w_out, B, N, transpose, out, accumulate,

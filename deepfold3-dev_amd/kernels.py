@@ -731,8 +731,10 @@ def grid_attention_forward(
         out = torch.empty_like(zc)
     else:
         _lib.check_out("GridSelfAttention", out, zc)
-    # the outer-product path belongs to the fused 128-channel kernels
-    km = outer_key_mask(m) if fused and (mask_outer is None or mask_outer) else None
+    # the outer-product path belongs to the fused 128-channel kernels and the 256-channel,
+    # 8-head bf16 path
+    folds = fused or (C == 256 and num_heads == 8 and cdt == torch.bfloat16)
+    km = outer_key_mask(m) if folds and (mask_outer is None or mask_outer) else None
     if mask_outer and km is None:
         raise NotActive("GridSelfAttention", "mask_outer=True needs a mask that is the outer product of its diagonal")
     ws_bytes = _lib.lib().pf_grid_attn_workspace_bytes(B, N, C, num_heads, code_c)

@@ -255,13 +255,16 @@ int pf_trimul_mhr_router_wgrad(const float* d_router_logits, const void* x, int 
  * Writes the update to `out`, or adds it into `out` when accumulate != 0 (out == z is the
  * fused residual). Masking follows the reference's eager path: keys with mask 0 get
  * -1e9 added in fp32, so a fully masked line attends uniformly (mean of V); the Triton
- * kernel's zero-output rule for such lines is not used. Built: C=128, H=4 (head dim 32).
+ * kernel's zero-output rule for such lines is not used. Built: C=128, H=4 (head dim 32);
+ * C=256, H=8 with bf16 GEMMs (a persistent projection kernel writes both four-head frames);
+ * other C a multiple of 32 with 1-16 heads of dimension max(C/H, 16) <= 32 (composed).
  * key_mask: NULL, or the caller's assertion that every mask[b] is the outer product of its
  * binary diagonal (m[i][k] = m[i][i] m[k][k], m in {0, 1}: the trunk's seq_mask x seq_mask),
  * given as that diagonal's additive key mask key_mask [B,N] fp32 = 1e9 (m[k][k] - 1) (both
  * from pf_pair_mask_outer). The key mask is then added to the pair bias once and the flash
  * kernel runs without per-line key masks; the result is the same. A mask that is not of that
- * form gives wrong results with key_mask set. */
+ * form gives wrong results with key_mask set. Read by the C=128 and the C=256 bf16 paths;
+ * the composed paths for other widths take the per-line masks and ignore it. */
 size_t pf_grid_attn_workspace_bytes(int B, int N, int C, int H, int cdtype);
 int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const float* ln_b, float eps,
                      const void* w_qkvgb, const void* w_out, int B, int N, int C, int H, int transpose, int zdtype,

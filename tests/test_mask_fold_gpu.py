@@ -78,3 +78,32 @@ def test_folded_mask_is_bit_identical(dev, dtype, transpose, n, pad):
     assert torch.isfinite(folded.float()).all()
     assert torch.equal(folded, general)
     assert torch.equal(auto, folded)
+
+
+def _module256(dev, transpose, seed):
+    sd = W.make_block_weights(seed, c_pair=256, num_pair_heads=8)
+    prefix = "pair_attn_col." if transpose else "pair_attn_row."
+    m = attention.GridSelfAttention(256, 8, transpose=transpose).to(dev)
+    m.load_state_dict({k[len(prefix) :]: v for k, v in sd.items() if k.startswith(prefix)})
+    return m.to(BF).eval()
+
+
+@pytest.mark.parametrize("transpose", [False, True], ids=["rows", "cols"])
+@pytest.mark.parametrize("n,pad", [(70, [1, 40, 69]), (200, list(range(190, 200)))])
+def test_folded_mask_is_bit_identical_c256(dev, transpose, n, pad):
+    """The 256-channel, 8-head bf16 path: both four-head groups fold the key mask the same
+    way (rows: a pass over the bias; columns: inside the transpose)."""
+    m = _module256(dev, transpose, 6)
+    g = torch.Generator().manual_seed(n + 1)
+    z = torch.randn(1, n, n, 256, generator=g).to(dev, BF)
+    mask = _seq_outer(n, pad, dev=dev)
+    op = m._operands(kernels.gemm_dtype_for(z))
+    args = (z, mask, op["lnw"], op["lnb"], m.norm.eps, op["w5"], op["w_out"], transpose)
+    print(f"[mask fold C=256] n={n} transpose={transpose}", flush=True)
+    with torch.no_grad():
+        folded = kernels.grid_attention_forward(*args, num_heads=8, mask_outer=True)
+        general = kernels.grid_attention_forward(*args, num_heads=8, mask_outer=False)
+        auto = kernels.grid_attention_forward(*args, num_heads=8)
+    assert torch.isfinite(folded.float()).all()
+    assert torch.equal(folded, general)
+    assert torch.equal(auto, folded)
