@@ -439,6 +439,28 @@ PF_DEVICE void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int
 #endif
 }
 
+// The same load issued through inline assembly, which the compiler does not see as a write
+// to LDS: it then inserts no wait for it before later LDS accesses (its conservative
+// aliasing would otherwise wait for every direct load in flight before any LDS read, which
+// makes a chunk wait for the next chunk's loads before its own fragment reads). The caller
+// orders every LDS access to the destination with explicit s_waitcnt vmcnt and barriers.
+// `r_words` is the buffer resource as four dwords (buf_rsrc_words).
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+PF_DEVICE i32x4_t buf_rsrc_words(const void* p, unsigned bytes) {
+  const unsigned long long a = (unsigned long long)p;
+  return i32x4_t{(int)(unsigned)a, (int)(unsigned)(a >> 32) & 0xffff, (int)bytes, 0x00020000};
+}
+PF_DEVICE void buf_load_lds16_async(const i32x4_t& r_words, void* lds, int voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const unsigned m0 =
+      __builtin_amdgcn_readfirstlane((unsigned)(unsigned long long)(__attribute__((address_space(3))) char*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(r_words), "s"(soff)
+               : "memory", "m0");
+#endif
+}
+
 // Workgroup barrier after this wave's LDS operations (s_waitcnt lgkmcnt(0); s_barrier),
 // without waiting for outstanding global or buffer-to-LDS loads (vmcnt), which
 // __syncthreads() would. Only for LDS data written by ds_* instructions.

@@ -660,6 +660,214 @@ __global__ __launch_bounds__(TransWs::NT, 1) void pair_transition_ws_kernel(
   __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // no direct load outlives the block
 }
 
+// Pair transition at 256 channels (factor 4: W1 [2048][256], W2 [256][1024]) with bf16 GEMMs
+// and a bf16 stream, persistent and weight-streaming: the hidden activations never leave the
+// chip (the composed path wrote and re-read 2 KB of them per position). One 8-wave block per
+// CU walks tiles of 128 positions; the hidden dim is walked in 32 chunks of 32 units. A
+// chunk's W1 rows (a 0-15, b 0-15, a 16-31, b 16-31 of its units: 32 KB) and W2 columns
+// (256 x 32: 16 KB) stream into a two-stage LDS ring by direct buffer->LDS loads one chunk
+// ahead, swizzled so fragment reads are conflict-free. GEMM1: wave (rb = w & 1, pb = w >> 1)
+// computes the 32 rows 32 rb .. (a and b of 16 units) for positions 32 pb .. from its
+// LayerNormed rows held in registers; a unit's a and b land in one lane (accumulator rows r and
+// r + 16), so u = silu(a) b is formed in registers and written to an LDS tile [128][32].
+// GEMM2: wave w accumulates y^T rows 32 w .. (its 32 output channels) for all 128 positions
+// in registers over the whole tile. Epilogue: lane-pair swaps give 16-byte row pieces for
+// the residual add and the stores.
+struct Trans256 {
+  static constexpr int C = 256;
+  static constexpr int HID = 4 * C;                 // 1024 hidden units
+  static constexpr int HC = 32;                     // units per chunk
+  static constexpr int NCH = HID / HC;              // 32 chunks per tile
+  static constexpr int BP = 128;                    // positions per tile
+  static constexpr int NW = 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int W1_BYTES = 2 * HC * C * 2;   // 64 rows x 512 B
+  static constexpr int W2_BYTES = C * HC * 2;       // 256 rows x 64 B
+  static constexpr int STAGE = W1_BYTES + W2_BYTES; // 48 KB
+  static constexpr int DMA1 = W1_BYTES / 1024 / NW; // 4
+  static constexpr int DMA2 = W2_BYTES / 1024 / NW; // 2
+};
+
+// Byte offsets in the chunk stage: W1 rows of 512 B (16-byte piece c XOR row & 15), W2 and
+// the u tile rows of 64 B (piece c XOR (row >> 2) & 3: 16 consecutive rows at one logical
+// piece cover the 16 bank groups).
+PF_DEVICE int t256_w1(int r, int c) { return r * 512 + 16 * (c ^ (r & 15)); }
+PF_DEVICE int t256_r64(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+__global__ __launch_bounds__(Trans256::NT, 1) void pair_transition256_kernel(
+    const bf16* __restrict__ x, bf16* __restrict__ out, const float* __restrict__ lnw, const float* __restrict__ lnb,
+    float eps, const bf16* __restrict__ W1, const bf16* __restrict__ W2, long M, int accumulate) {
+  using Cfg = Trans256;
+  constexpr int C = Cfg::C, HC = Cfg::HC, NCH = Cfg::NCH, BP = Cfg::BP;
+  __shared__ __attribute__((aligned(16))) char ring[2 * Cfg::STAGE];
+  __shared__ __attribute__((aligned(16))) char ut[BP * HC * 2];  // u [pos][unit], 64-byte rows
+  __shared__ float lnp[2 * C];
+
+  const int w = wave_id();
+  const int l = lane_id();
+  const int lq = l & 31, hf = l >> 5;
+  const int rb = w & 1, pb = w >> 1;
+  const long ntiles = (M + BP - 1) / BP;
+  const long total = blockIdx.x < ntiles ? ((ntiles - 1 - blockIdx.x) / gridDim.x + 1) * NCH : 0;
+
+  for (int i = threadIdx.x; i < C; i += Cfg::NT) {
+    lnp[i] = lnw[i];
+    lnp[C + i] = lnb[i];
+  }
+  const i32x4_t r1 = buf_rsrc_words(W1, 2 * Cfg::HID * C * 2);
+  const i32x4_t r2 = buf_rsrc_words(W2, C * Cfg::HID * 2);
+  auto issue_chunk = [&](long gg) {
+    const int c = (int)(gg % NCH);
+    char* st = ring + (gg & 1) * Cfg::STAGE;
+#pragma unroll
+    for (int t = 0; t < Cfg::DMA1; ++t) {
+      const int ins = w * Cfg::DMA1 + t;  // two 512-byte rows per instruction
+      const int row = 2 * ins + (l >> 5);
+      const int lc = (l & 31) ^ (row & 15);
+      const int blk = row >> 4;  // a (even) or b (odd) rows of units 16 (blk >> 1) ..
+      const int src = (blk & 1) * Cfg::HID + HC * c + 16 * (blk >> 1) + (row & 15);
+      buf_load_lds16_async(r1, st + ins * 1024, (src * C + 8 * lc) * 2, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < Cfg::DMA2; ++t) {
+      const int ins = w * Cfg::DMA2 + t;  // sixteen 64-byte rows per instruction
+      const int o = 16 * ins + (l >> 2);
+      const int lc = (l & 3) ^ ((o >> 2) & 3);
+      buf_load_lds16_async(r2, st + Cfg::W1_BYTES + ins * 1024, (o * Cfg::HID + HC * c + 8 * lc) * 2, 0);
+    }
+  };
+  // this lane's half row for GEMM1: channels 16 ks + 8 hf .. +7 of position 32 pb + lq
+  u32x4 zr[C / 16];
+  auto load_half = [&](long tl) {
+    const long m = min(tl * BP + 32 * pb + lq, M - 1);  // past M: row M - 1, never stored
+    const bf16* src = x + m * C + 8 * hf;
+#pragma unroll
+    for (int ks = 0; ks < C / 16; ++ks) zr[ks] = *reinterpret_cast<const u32x4*>(src + 16 * ks);
+  };
+
+  long g = 0;
+  long tile = blockIdx.x;
+  if (total > 0) issue_chunk(0);
+  __syncthreads();  // LN parameters
+
+  for (; tile < ntiles; tile += gridDim.x) {
+    load_half(tile);  // rows dead after the LayerNorm (no register set held across the chunks)
+    // ---- LN -> B operands xf[ks]
+    bf16x8 xf[C / 16];
+    {
+      float s = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const bf16x8 t = __builtin_bit_cast(bf16x8, zr[ks]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += (float)t[e];
+      }
+      s += __shfl_xor(s, 32, 64);
+      const float mean = s * (1.0f / C);
+      float q = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const bf16x8 t = __builtin_bit_cast(bf16x8, zr[ks]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = (float)t[e] - mean;
+          q += d * d;
+        }
+      }
+      q += __shfl_xor(q, 32, 64);
+      const float rstd = rsqrtf(q * (1.0f / C) + eps);
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const bf16x8 t = __builtin_bit_cast(bf16x8, zr[ks]);
+        const float* pw = lnp + 16 * ks + 8 * hf;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[ks][e] = (bf16)(((float)t[e] - mean) * rstd * pw[e] + pw[C + e]);
+      }
+    }
+    f32x16 y[4];  // y^T [out rows 32 w ..][positions 32 p ..]
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) y[p][e] = 0.f;
+
+#pragma unroll 1
+    for (int c = 0; c < NCH; ++c, ++g) {
+      // Chunk g landed in every wave; the previous chunk's GEMM2 (reads of ring slot
+      // (g + 1) & 1 and of ut) is done in every wave.
+      __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+      lds_barrier();
+      if (g + 1 < total) issue_chunk(g + 1);
+      const char* st = ring + (g & 1) * Cfg::STAGE;
+      f32x16 acc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        const bf16x8 wf = *reinterpret_cast<const bf16x8*>(st + t256_w1(32 * rb + lq, 2 * ks + hf));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xf[ks], acc, 0, 0, 0);
+      }
+      // acc[e] (e < 8): a of unit 16 rb + 8 (e >> 2) + 4 hf + (e & 3); acc[e + 8]: its b
+      {
+        const int pos = 32 * pb + lq;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const int u0 = 16 * rb + 8 * (e >> 2) + 4 * hf + (e & 3);
+          bf16x2 v2;
+          v2[0] = (bf16)(siluf_(acc[e]) * acc[e + 8]);
+          v2[1] = (bf16)(siluf_(acc[e + 1]) * acc[e + 9]);
+          *reinterpret_cast<bf16x2*>(ut + t256_r64(pos, u0 >> 3) + 2 * (u0 & 7)) = v2;
+        }
+      }
+      lds_barrier();  // ut complete
+      const char* w2s = st + Cfg::W1_BYTES;
+#pragma unroll
+      for (int ks = 0; ks < HC / 16; ++ks) {
+        const bf16x8 af = *reinterpret_cast<const bf16x8*>(w2s + t256_r64(32 * w + lq, 2 * ks + hf));
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const bf16x8 uf = *reinterpret_cast<const bf16x8*>(ut + t256_r64(32 * p + lq, 2 * ks + hf));
+          y[p] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, uf, y[p], 0, 0, 0);
+        }
+      }
+    }
+
+    // ---- epilogue: lane (position 32 p + lq, half hf) holds channels 32 w + 8 gq + 4 hf + e
+    // of y[p][4 gq + e]; swapping (gq = 2 q, 2 q + 1) between lanes l and l + 32 leaves lane hf
+    // with channels 32 w + 16 q + 8 hf + e in v[8 q + e]: 16-byte row pieces.
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      float v[16];
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float a = y[p][8 * qq + e], b = y[p][8 * qq + 4 + e];
+          permlane32_swap(a, b);
+          v[8 * qq + e] = a;
+          v[8 * qq + 4 + e] = b;
+        }
+      const long m = tile * BP + 32 * p + lq;
+      const long mr = min(m, M - 1);
+      u32x4 rr[2];
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq)
+        rr[qq] = *reinterpret_cast<const u32x4*>(out + mr * C + 32 * w + 16 * qq + 8 * hf);
+      if (m < M) {
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          const bf16x8 t = __builtin_bit_cast(bf16x8, rr[qq]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[8 * qq + e] += accumulate ? (float)t[e] : 0.f;
+          store_vec<bf16, 8>(out + m * C + 32 * w + 16 * qq + 8 * hf, &v[8 * qq]);
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // no direct load outlives the block
+}
+
 // Standalone single_to_pair: LN'(z) Ws2p^T -> logits [B][16][N][N].
 template <class TZ, class TC>
 __global__ __launch_bounds__(256) void single_to_pair_kernel(const TZ* __restrict__ z, const float* __restrict__ lnw,
@@ -931,8 +1139,11 @@ int pf_pair_transition_fwd(const void* x, const float* ln_w, const float* ln_b, 
                            const float* s2p_ln_w, const float* s2p_ln_b, float s2p_eps, const void* w_s2p,
                            float* pair_logits, long NN, void* stream) {
   PF_REQUIRE(x && ln_w && ln_b && w1 && w2 && out, PF_ERR_INVALID_ARG, "pf_pair_transition_fwd: null pointer");
-  PF_REQUIRE(C == kC && factor == 4, PF_ERR_UNSUPPORTED,
-             "pf_pair_transition_fwd: C=%d factor=%d (built: C=128, factor 4)", C, factor);
+  const bool c256 = C == Trans256::C && factor == 4 && zdtype == PF_BF16 && cdtype == PF_BF16 && !pair_logits;
+  PF_REQUIRE((C == kC && factor == 4) || c256, PF_ERR_UNSUPPORTED,
+             "pf_pair_transition_fwd: C=%d factor=%d (built: C=128, factor 4; C=256, factor 4 with bf16 z and GEMMs "
+             "and no fused single_to_pair)",
+             C, factor);
   PF_REQUIRE(M >= 0, PF_ERR_INVALID_ARG, "pf_pair_transition_fwd: M=%ld", M);
   PF_REQUIRE((zdtype == PF_F32 || zdtype == PF_BF16) && (cdtype == PF_F32 || cdtype == PF_BF16) &&
                  !(zdtype == PF_BF16 && cdtype == PF_F32),
@@ -943,6 +1154,15 @@ int pf_pair_transition_fwd(const void* x, const float* ln_w, const float* ln_b, 
              "pf_pair_transition_fwd: pointers must be 16-byte aligned");
   if (M == 0) return pf::ok();
   hipStream_t s = pf::as_stream(stream);
+  if (c256) {
+    const long ntiles = (M + Trans256::BP - 1) / Trans256::BP;
+    const unsigned nblk = (unsigned)std::min<long>(ntiles, pf::cu_count());
+    pf::KernelTimer timer("pair_transition", s);
+    pair_transition256_kernel<<<nblk, Trans256::NT, 0, s>>>((const bf16*)x, (bf16*)out, ln_w, ln_b, eps,
+                                                            (const bf16*)w1, (const bf16*)w2, M, accumulate);
+    timer.stop();
+    return pf::check_launch("pair_transition256");
+  }
   return PF_DISPATCH_ZC(zdtype, cdtype, transition_launch, x, ln_w, ln_b, eps, w1, w2, M, out, accumulate, s2p_ln_w,
                         s2p_ln_b, s2p_eps, w_s2p, pair_logits, NN, s);
 }

@@ -763,7 +763,8 @@ def pair_transition_forward(
     accumulate: bool = False,
     s2p: tuple | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
-    """Fused pair transition (C=128, factor 4); optionally also the single_to_pair logits.
+    """Fused pair transition (C=128, factor 4; or C=256, factor 4 with bf16 z and GEMM
+    operands, without the single_to_pair epilogue); optionally also the single_to_pair logits.
 
     ``s2p = (ln_w, ln_b, eps, w_s2p)`` computes ``pair_logits [B, 16, N, N]`` (fp32) from the
     updated rows (``evoformer.py:322-328``). Returns ``(out, pair_logits or None)``.

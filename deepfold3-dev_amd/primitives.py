@@ -140,11 +140,18 @@ class TransitionBlock(nn.Module):
         from . import kernel_census
         from .kernels import gemm_dtype_for, pair_transition_forward, transition_forward
 
-        op = self.operands(gemm_dtype_for(x), scale)
+        cdt = gemm_dtype_for(x)
+        op = self.operands(cdt, scale)
         if self.fused_pair:
             kernel_census.record("TransitionBlock", "hip_pair_transition")
             return pair_transition_forward(
                 x, op["lnw"], op["lnb"], self.norm.eps, op["w1"], op["w2"], out=out, accumulate=accumulate, s2p=s2p
+            )
+        if self.c == 256 and self.n == 4 and x.dtype == torch.bfloat16 and cdt == torch.bfloat16 and s2p is None:
+            # the fused 256-channel kernel (hidden activations kept on chip)
+            kernel_census.record("TransitionBlock", "hip_pair_transition")
+            return pair_transition_forward(
+                x, op["lnw"], op["lnb"], self.norm.eps, op["w1"], op["w2"], out=out, accumulate=accumulate
             )
         if s2p is not None:
             raise ValueError("the single_to_pair epilogue is fused only into the C=128 pair transition")

@@ -278,12 +278,14 @@ int pf_grid_attn_fwd(const void* z, const float* mask, const float* ln_w, const 
 int pf_pair_mask_outer(const float* mask, int B, int N, int* flag, float* key_mask, void* stream);
 
 /* ---- transitions ------------------------------------------------------- */
-/* Pair transition, C=128, factor 4: replaces FusedTransitionBlock / TransitionBlock.forward
+/* Pair transition, factor 4: replaces FusedTransitionBlock / TransitionBlock.forward
  * (triton/fused_transition.py:34-83, primitives.py:193-251; FusedLayerNormLinear
  * triton/layernorm_linear.py:537-592 and FusedSwiGLU triton/swiglu.py:192-200 inside it).
+ * Built: C=128 (any supported dtype pair), and C=256 with bf16 x and bf16 weights (the
+ * hidden activations stay on chip; no fused single_to_pair at this width).
  * x [M, C] zdtype; w1 [2*factor*C, C], w2 [C, factor*C] cdtype. out = y or out += y.
- * Optional fused single_to_pair (evoformer.py:322-328): when pair_logits != NULL, the
- * updated rows are normalised with (s2p_ln_w, s2p_ln_b) and projected by w_s2p [16, C]
+ * Optional fused single_to_pair at C=128 (evoformer.py:322-328): when pair_logits != NULL,
+ * the updated rows are normalised with (s2p_ln_w, s2p_ln_b) and projected by w_s2p [16, C]
  * into pair_logits [M/NN, 16, NN] fp32 (NN = N*N positions per batch item). */
 int pf_pair_transition_fwd(const void* x, const float* ln_w, const float* ln_b, float eps, const void* w1,
                            const void* w2, long M, int C, int factor, int zdtype, int cdtype, void* out, int accumulate,
