@@ -1925,9 +1925,9 @@ __global__ __launch_bounds__(GridProj256::NT, 1) void grid_project256_kernel(
     bf16* __restrict__ G, int B, int N, int Np, int transpose, float qscale, size_t gq, size_t gpb) {
   using Cfg = GridProj256;
   constexpr int C = Cfg::C, BP = Cfg::BP, NCH = Cfg::NCH, NS = Cfg::NS, TLD = Cfg::TLD, VLD = Cfg::VLD;
-  // bf16 rows: the next tile's rows load during this tile's chunks (a second register set
-  // would not fit fp32 rows)
-  constexpr bool PREFETCH = sizeof(TZ) == 2;
+  // The rows are loaded at the start of their tile: holding the next tile's rows through the
+  // chunks (64 VGPRs) spills, and each spill reload waits for every load in flight.
+  constexpr bool PREFETCH = false;
   constexpr int NPIECE = C / 16 * (int)sizeof(TZ) / 2;  // 16-byte loads of a lane's half row
   __shared__ __attribute__((aligned(16))) char ring[NS * Cfg::CHUNK];
   __shared__ __attribute__((aligned(16))) char stage[2][Cfg::STAGE];
@@ -1948,7 +1948,7 @@ __global__ __launch_bounds__(GridProj256::NT, 1) void grid_project256_kernel(
     lnp[C + i] = lnb[i];
   }
 
-  const auto rw = buf_rsrc(w5, Cfg::WROWS * C * 2);
+  const i32x4_t rw = buf_rsrc_words(w5, Cfg::WROWS * C * 2);
   auto issue_chunk = [&](long gg) {
     const int c = (int)(gg % NCH);
     char* st = ring + (gg % NS) * Cfg::CHUNK;
@@ -1959,7 +1959,7 @@ __global__ __launch_bounds__(GridProj256::NT, 1) void grid_project256_kernel(
       const int lc = (l & 31) ^ (row & 15);
       // the bias chunk's rows past the packed weights repeat its last row (never used)
       const int src = min(c * Cfg::CR + row, Cfg::WROWS - 1);
-      buf_load_lds16(rw, st + ins * 1024, (src * C + 8 * lc) * 2, 0);
+      buf_load_lds16_async(rw, st + ins * 1024, (src * C + 8 * lc) * 2, 0);
     }
   };
   auto tile_pos = [&](long tl, int& b, int& line, int& t0) {
