@@ -1843,9 +1843,9 @@ __global__ __launch_bounds__(256) void grid_gen_gate_inplace_kernel(TC* __restri
 // flash kernel's frame for both four-head groups -- Q (pre-scaled by d^-1/2 log2 e), the K
 // and Vt key-block tiles, the pair bias (log2 units; query-major in key-slot order for rows,
 // key-major for columns, turned by pb_transpose) and the line mask -- plus the gate rows
-// G [pos][256] in z order; then per group the flash kernel (o into og's rows, strided), the
-// gate og *= sigmoid(G) and the output GEMM. No LayerNorm round trip, no projection rows,
-// no repacking.
+// sigmoid(g) as G [pos][256] in z order; then per group the flash kernel (o into og's rows,
+// strided), and the output GEMM on og * G (the gate applied as its operand tile loads). No
+// LayerNorm round trip, no projection rows, no repacking.
 //
 // The projection: one 8-wave block per CU walks tiles of 128 tokens of one line (the z
 // positions (line, t) for rows, (t, line) for columns). A position's LayerNormed 256
@@ -2143,15 +2143,20 @@ __global__ __launch_bounds__(GridProj256::NT, 1) void grid_project256_kernel(
 #pragma unroll
           for (int e = 0; e < 16; ++e) vs[(8 * (e >> 2) + 4 * hf + (e & 3)) * VLD + slot] = (bf16)(live ? acc[e] : 0.f);
         } else {
-          // Q (scaled), K, G: [rb][token][d] (Q and K zero past N)
+          // Q (scaled), K, sigmoid(G): [rb][token][d] (Q and K zero past N)
           const float sc = part == 0 ? qscale : 1.0f;
-          const float keep = (part == 3 || live) ? sc : 0.f;
+          const float keep = live ? sc : 0.f;
           bf16* ts = reinterpret_cast<bf16*>(sb) + (rb * BP + tok) * TLD;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             bf16x4 v4;
+            if (part == 3) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v4[e] = (bf16)(acc[4 * j + e] * keep);
+              for (int e = 0; e < 4; ++e) v4[e] = (bf16)sigmoidf_(acc[4 * j + e]);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v4[e] = (bf16)(acc[4 * j + e] * keep);
+            }
             *reinterpret_cast<bf16x4*>(ts + 8 * j + 4 * hf) = v4;
           }
         }
@@ -2261,12 +2266,10 @@ int grid_attn256_launch(const void* z, const float* mask, const float* lnw, cons
           Qg, Kg, Vg, PBg, MA, Og, B, N, Np, N, N, 0, remap, rg, 1.f, so);
     if (int e = pf::check_launch("tri_attn_redo")) return e;
   }
-  // (o * sigmoid(g) in the flash kernel's epilogue instead: its gate loads at the end of
-  // every wave cost that kernel 67 us per launch, more than this pass's 136 us per two)
-  grid_gen_gate_inplace_kernel<bf16><<<(unsigned)((M * (HD / 8) + 255) / 256), 256, 0, s>>>(og, G, M, HD, HD, 0);
-  if (int e = pf::check_launch("grid_gen_gate")) return e;
-  if (accumulate) return rowgemm_launch<bf16, TZ, EPI_RESIDUAL>(og, wo, nullptr, 0, out, M, Cfg::C, HD, s);
-  return rowgemm_launch<bf16, TZ, EPI_STORE>(og, wo, nullptr, 0, out, M, Cfg::C, HD, s);
+  // The gate (G holds sigmoid(g)) is applied as the output GEMM loads og, so og is not
+  // rewritten (a gate pass over og and G cost 136 us per call; o * sigmoid(g) in the flash
+  // kernel's epilogue cost that kernel 67 us per launch).
+  return tile_gemm_rows_gated(og, G, wo, out, M, Cfg::C, HD, accumulate, sizeof(TZ) == 2 ? PF_BF16 : PF_F32, s);
 }
 
 template <class TZ, class TC>

@@ -444,7 +444,10 @@ PF_DEVICE void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int
 // aliasing would otherwise wait for every direct load in flight before any LDS read, which
 // makes a chunk wait for the next chunk's loads before its own fragment reads). The caller
 // orders every LDS access to the destination with explicit s_waitcnt vmcnt and barriers.
-// `r_words` is the buffer resource as four dwords (buf_rsrc_words).
+// `r_words` is the buffer resource as four dwords (buf_rsrc_words). m0 is reserved to the
+// compiler, which does not honour the clobber (hence its warning): use this only in kernels
+// in which the compiler itself keeps nothing in m0 (no buf_load_lds16 beside it); in the
+// assembly of the kernels that use it, m0 is written by these statements only.
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 PF_DEVICE i32x4_t buf_rsrc_words(const void* p, unsigned bytes) {
   const unsigned long long a = (unsigned long long)p;

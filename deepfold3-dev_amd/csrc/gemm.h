@@ -17,5 +17,9 @@ int bgemm_nt(const void* A, const void* B, void* C, int M, int N, int K, long ld
 // bf16 operands, 16 for fp32). Operands bf16 with bf16 or fp32 output, or fp32 throughout.
 int tile_gemm_rows(const void* A, const void* W, void* out, long M, int Nout, int K, int epi, int tc_dtype,
                    int out_dtype, hipStream_t s);
+// The same GEMM (bf16 operands, epi 0 or 1) on the gated operand: out = epi((A * gate) W^T),
+// gate [M][K] like A, each product rounded to bf16 before the GEMM.
+int tile_gemm_rows_gated(const void* A, const void* gate, const void* W, void* out, long M, int Nout, int K,
+                         int accumulate, int out_dtype, hipStream_t s);
 // Rows from which the row GEMM hands over to tile_gemm_rows.
 constexpr long kTileGemmMinRows = 16384;

@@ -148,10 +148,12 @@ struct TileRowsCfg {
   static constexpr int LDS = SMEM > OSMEM ? SMEM : OSMEM;
 };
 
-template <class TC, class TO, int EPI>
+// GATE: the A operand is A * gate elementwise (gate [M][K] like A, bf16 operands), each
+// product rounded to the operand dtype as it enters the LDS tile.
+template <class TC, class TO, int EPI, bool GATE = false>
 __global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restrict__ A, const TC* __restrict__ W,
                                                              TO* __restrict__ out, long M, int Nout, int K,
-                                                             int vec_out) {
+                                                             int vec_out, const TC* __restrict__ gate = nullptr) {
   using Cfg = TileRowsCfg<TC>;
   using MF = Mfma<TC>;
   constexpr int BMN = Cfg::BMN, KT = Cfg::KT, LDK = Cfg::LDK;
@@ -182,6 +184,9 @@ __global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restric
   constexpr int CPR = KT / VEC;
   constexpr int LOADS = 2 * BMN * CPR / 256;
   static_assert((2 * BMN * CPR) % 256 == 0, "stage must split evenly");
+  constexpr int ALOADS = BMN * CPR / 256;  // loads q < ALOADS are A rows, the rest W rows
+  static_assert((BMN * CPR) % 256 == 0, "A rows must fill whole loads");
+  static_assert(!GATE || sizeof(TC) == 2, "the gated operand is bf16");
   const TC* src_row[LOADS];
   int dst_off[LOADS];
 #pragma unroll
@@ -193,12 +198,29 @@ __global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restric
     dst_off[q] = row * LDK + chunk * VEC;
   }
   u32x4 reg[LOADS];
+  u32x4 greg[GATE ? ALOADS : 1];
   auto gload = [&](int k0) {
 #pragma unroll
     for (int q = 0; q < LOADS; ++q) reg[q] = *reinterpret_cast<const u32x4*>(src_row[q] + k0);
+    if constexpr (GATE) {
+#pragma unroll
+      for (int q = 0; q < ALOADS; ++q)
+        greg[q] = *reinterpret_cast<const u32x4*>(src_row[q] - A + gate + k0);
+    }
   };
   auto lstore = [&](int buf) {
     TC* base = lds + buf * 2 * Cfg::TILE_ELEMS;
+    if constexpr (GATE) {
+#pragma unroll
+      for (int q = 0; q < ALOADS; ++q) {
+        const bf16x8 a = __builtin_bit_cast(bf16x8, reg[q]);
+        const bf16x8 g = __builtin_bit_cast(bf16x8, greg[q]);
+        bf16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (bf16)((float)a[e] * (float)g[e]);
+        reg[q] = __builtin_bit_cast(u32x4, v);
+      }
+    }
 #pragma unroll
     for (int q = 0; q < LOADS; ++q) *reinterpret_cast<u32x4*>(base + dst_off[q]) = reg[q];
   };
@@ -291,10 +313,11 @@ __global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restric
   }
 }
 
-template <class TC, class TO, int EPI>
-int tile_gemm_rows_launch(const void* A, const void* W, void* out, long M, int Nout, int K, hipStream_t s) {
+template <class TC, class TO, int EPI, bool GATE = false>
+int tile_gemm_rows_launch(const void* A, const void* W, void* out, long M, int Nout, int K, hipStream_t s,
+                          const void* gate = nullptr) {
   using Cfg = TileRowsCfg<TC>;
-  const void* fn = (const void*)tile_gemm_rows_kernel<TC, TO, EPI>;
+  const void* fn = (const void*)tile_gemm_rows_kernel<TC, TO, EPI, GATE>;
   const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS);
   PF_REQUIRE(e == hipSuccess, PF_ERR_LAUNCH, "row gemm: cannot reserve %d bytes of LDS: %s", Cfg::LDS,
              hipGetErrorString(e));
@@ -302,8 +325,8 @@ int tile_gemm_rows_launch(const void* A, const void* W, void* out, long M, int N
   const long blocks = (M + Cfg::BMN - 1) / Cfg::BMN * tn;
   PF_REQUIRE(blocks < (1L << 31), PF_ERR_UNSUPPORTED, "row gemm: M=%ld Nout=%d", M, Nout);
   const int vec_out = pf::aligned16(out) && Nout % (16 / (int)sizeof(TO)) == 0;
-  tile_gemm_rows_kernel<TC, TO, EPI><<<dim3((unsigned)blocks), 256, Cfg::LDS, s>>>((const TC*)A, (const TC*)W,
-                                                                                   (TO*)out, M, Nout, K, vec_out);
+  tile_gemm_rows_kernel<TC, TO, EPI, GATE><<<dim3((unsigned)blocks), 256, Cfg::LDS, s>>>(
+      (const TC*)A, (const TC*)W, (TO*)out, M, Nout, K, vec_out, (const TC*)gate);
   return pf::check_launch("row gemm");
 }
 
@@ -324,6 +347,20 @@ int tile_gemm_rows(const void* A, const void* W, void* out, long M, int Nout, in
   if (tc_dtype == PF_F32) return tile_gemm_rows_epi<float, float>(A, W, out, M, Nout, K, epi, s);
   if (out_dtype == PF_F32) return tile_gemm_rows_epi<bf16, float>(A, W, out, M, Nout, K, epi, s);
   return tile_gemm_rows_epi<bf16, bf16>(A, W, out, M, Nout, K, epi, s);
+}
+
+int tile_gemm_rows_gated(const void* A, const void* gate, const void* W, void* out, long M, int Nout, int K,
+                         int accumulate, int out_dtype, hipStream_t s) {
+  constexpr int kt = TileRowsCfg<bf16>::KT;
+  PF_REQUIRE(M > 0 && Nout > 0 && K > 0 && K % kt == 0, PF_ERR_INVALID_ARG,
+             "gated row gemm: M=%ld Nout=%d K=%d (a multiple of %d)", M, Nout, K, kt);
+  PF_REQUIRE(pf::aligned16(A) && pf::aligned16(gate) && pf::aligned16(W), PF_ERR_INVALID_ARG,
+             "gated row gemm: operands must be 16-byte aligned");
+  if (out_dtype == PF_F32)
+    return accumulate ? tile_gemm_rows_launch<bf16, float, 1, true>(A, W, out, M, Nout, K, s, gate)
+                      : tile_gemm_rows_launch<bf16, float, 0, true>(A, W, out, M, Nout, K, s, gate);
+  return accumulate ? tile_gemm_rows_launch<bf16, bf16, 1, true>(A, W, out, M, Nout, K, s, gate)
+                    : tile_gemm_rows_launch<bf16, bf16, 0, true>(A, W, out, M, Nout, K, s, gate);
 }
 
 int bgemm_nt(const void* A, const void* B, void* C, int M, int N, int K, long lda, long ldb, long ldc, long sA,
