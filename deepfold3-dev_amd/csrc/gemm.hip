@@ -162,8 +162,13 @@ __global__ __launch_bounds__(256) void tile_gemm_rows_kernel(const TC* __restric
   TC* lds = reinterpret_cast<TC*>(smem);
 
   const int tn = (Nout + OCT - 1) / OCT;
-  const long i0 = (long)(blockIdx.x / tn) * BMN;
-  const int oc0 = (int)(blockIdx.x % tn) * OCT;
+  // Blocks are dispatched round-robin over the 8 XCDs; when the grid splits evenly, XCD x
+  // takes the x-th eighth of the tiles in order, so the column tiles of one row tile run on
+  // one XCD one after another and the second reads A from that XCD's L2.
+  const unsigned nb = gridDim.x;
+  const unsigned bid = nb % 8 == 0 ? (blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const long i0 = (long)(bid / tn) * BMN;
+  const int oc0 = (int)(bid % tn) * OCT;
   const int tid = threadIdx.x;
   const int w = wave_id();
   const int l = lane_id();
