@@ -1441,20 +1441,25 @@ __global__ __launch_bounds__(Output256::NT, 1) void trimul_output256_kernel(
     i = rem / tpr;
     j0 = (rem - i * tpr) * BP;
   };
+  // The tile's loads and residual stores are buffer operations on a per-tile base with
+  // 32-bit lane offsets: 64-bit per-lane addresses held across the tile spilled, and each
+  // spill reload waited for the next tile's loads in flight. The z rows' buffer ends at
+  // position N of the row, so rows past N load zeros and their stores are dropped.
   u32x4 zr[NLD], xr[XLDS];
   auto issue = [&](int tile) {
     int b, i, j0;
     tile_coords(tile, b, i, j0);
-    const bf16* zb = z + (((size_t)b * N + i) * N + j0) * C;
+    const __amdgpu_buffer_rsrc_t zrs =
+        buf_rsrc(z + (((size_t)b * N + i) * N + j0) * C, (unsigned)((N - j0) * C * 2));
 #pragma unroll
-    for (int q = 0; q < NLD; ++q) {
-      const int j = j0 + w * RPW + q * RPI + l / LPR;
-      zr[q] = j < N ? *reinterpret_cast<const u32x4*>(zb + zoff0 + q * RPI * C) : u32x4{0u, 0u, 0u, 0u};
-    }
-    const bf16* Xb = X + (size_t)b * C * pe + (size_t)i * Np + j0;
+    for (int q = 0; q < NLD; ++q)
+      zr[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(zrs, (zoff0 + q * RPI * C) * 2, 0, 0));
+    const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(X + (size_t)b * C * pe, (unsigned)((size_t)C * pe * 2));
 #pragma unroll
     for (int q = 0; q < XLDS; ++q)
-      xr[q] = *reinterpret_cast<const u32x4*>(Xb + (size_t)q * (NT / 8) * pe + xoff);
+      xr[q] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     xrs, (int)((unsigned)(i * Np + j0 + q * (NT / 8) * pe + xoff) * 2u), 0, 0));
   };
 
   // After the LN_out pass the X tile's LDS holds the raw z rows [pos][ch] for the residual.
@@ -1522,7 +1527,8 @@ __global__ __launch_bounds__(Output256::NT, 1) void trimul_output256_kernel(
     const int next = tile + gridDim.x;
     if (next < ntiles) issue(next);
 
-    bf16* ob = out + ((size_t)b * N + i) * N * C;
+    const __amdgpu_buffer_rsrc_t ors =
+        buf_rsrc(out + (((size_t)b * N + i) * N + j0) * C, (unsigned)((N - j0) * C * 2));
 #pragma unroll 1
     for (int pt = 0; pt < 2; ++pt) {
       f32x16 ao, ag;
@@ -1552,8 +1558,6 @@ __global__ __launch_bounds__(Output256::NT, 1) void trimul_output256_kernel(
 #pragma unroll
         for (int q = 0; q < NLD; ++q) {
           const int p = w * RPW + q * RPI + l / LPR;
-          const int j = j0 + p;
-          if (j >= N) continue;
           float zv[VEC], y[VEC];
           unpack16<bf16>(*reinterpret_cast<const u32x4*>(zs + p * C + chunk * VEC), zv);
 #pragma unroll
@@ -1562,7 +1566,10 @@ __global__ __launch_bounds__(Output256::NT, 1) void trimul_output256_kernel(
 #pragma unroll
             for (int k = 0; k < 4; ++k) y[e + k] = accumulate ? zv[e + k] + u[k] : u[k];
           }
-          store_vec<bf16, VEC>(ob + (size_t)j * C + chunk * VEC, y);
+          bf16x8 o8;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o8[e] = (bf16)y[e];
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o8), ors, (p * C + chunk * VEC) * 2, 0, 0);
         }
       }
     }
